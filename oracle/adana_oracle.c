@@ -1,0 +1,215 @@
+/*
+ * adana_oracle.c -- CPU restatement of the ADana-family optimizer step.
+ *
+ * TEST INFRASTRUCTURE ONLY.  Nothing in the product (adana_amd/) links, loads
+ * or calls this file; only tests/, __graft_entry__.smoke() and bench.py's
+ * cpu_baseline leg do, and only as the checker / the timed CPU baseline.
+ *
+ * What it restates (reference = mlexpos/adana):
+ *   adana_oracle_adana_step  <- ADana._update_param_compiled
+ *                               src/optim/adana.py:100-151
+ *   adana_oracle_star_step   <- DANA_STAR_MK4._update_param_compiled
+ *                               src/optim/dana_star_mk4.py:136-203
+ *
+ * Arithmetic contract (the oracle of record):
+ *   - every tensor op of the reference is one IEEE-754 binary32 operation,
+ *     correctly rounded, in the reference's op order; no contraction
+ *     (built with -ffp-contract=off);
+ *   - the two composite ATen ops the reference uses are single-rounded FMAs,
+ *     as torch 2.10's CPU kernels compute them (probed bitwise):
+ *       lerp(a, b, w)          = |w| < 0.5 ? fma(w, b-a, a) : fma(w-1, b-a, b)
+ *       addcmul(s, t, t, val)  = fma(val*t, t, s)
+ *   - Dana-Star's per-element pow(et, 1-kappa) takes the exponent rounded to
+ *     binary32 (the vectorised ATen path does) and is evaluated in binary64,
+ *     then rounded once to binary32;
+ *   - sign(x) is 0 for x == +-0 and NaN; clamp / relu propagate NaN.
+ *
+ * Per-tensor diagnostics (reference :146-151 / :198-203) are accumulated in
+ * binary64: sum(alpha_factor), sum(g^2), sum(mfac), sum(m^2).
+ *
+ * Parity pins for this file (see tests/test_oracle.py):
+ *   - golden vectors written by the reference's own step() in this container
+ *     (tests/golden/make_golden.py): m, v bit-exact; tau and p within a few
+ *     ulp (the reference's CPU sqrt/pow are Sleef approximations);
+ *   - closed forms for a constant gradient (m_t = g(1-Pi_t), v_t = g^2(1-Pi_t));
+ *   - invariants (state independent of p, clipsnr=inf == no clip, kappa=1 =>
+ *     pow == 1, weight_decay=0 => opw == 1) and a binary64 brute-force loop.
+ */
+#include <math.h>
+#include <stdint.h>
+#include <string.h>
+
+typedef struct {
+    float a;        /* alpha = fp32(delta / (delta + t)), double divide      */
+    float oma;      /* fp32(1 - a)                                           */
+    float s;        /* fp32(t)                                               */
+    float eps;      /* fp32(epsilon)                                         */
+    float pw;       /* ADana: fp32((1 + s) ** (1 - kappa)), binary64 pow     */
+    float min_p;    /* Star: fp32(1 / (1 + s))                               */
+    float clip;     /* fp32(clipsnr)                                         */
+    int32_t has_clip;
+    float c3;       /* fp32(-lr) * fp32(gamma_3_factor)                      */
+    float cg2;      /* fp32(-lr)                                             */
+    float opw;      /* fp32(1 + wd_factor)                                   */
+    float star_exp; /* fp32(1 - kappa): exponent of the per-element pow      */
+    int32_t pow_mode; /* ATen's pow(Tensor, Scalar) specialisation, below     */
+} adana_oracle_scalars;
+
+/* pow(Tensor, Scalar) specialisations in ATen, chosen on the binary64
+ * exponent: 0 -> ones, 0.5 -> sqrt, -0.5 -> 1/sqrt, -1 -> 1/x, 2 -> x*x,
+ * 3 -> x*x*x, -2 -> 1/(x*x); anything else is a general pow. */
+enum { POW_GENERAL = 0, POW_ONE, POW_SQRT, POW_RSQRT, POW_RECIP, POW_SQUARE, POW_CUBE, POW_INVSQ };
+
+static inline float o_pow(float x, const adana_oracle_scalars *sc) {
+    switch (sc->pow_mode) {
+    case POW_ONE: return 1.0f;
+    case POW_SQRT: return sqrtf(x);
+    case POW_RSQRT: return 1.0f / sqrtf(x);
+    case POW_RECIP: return 1.0f / x;
+    case POW_SQUARE: return x * x;
+    case POW_CUBE: return (x * x) * x;
+    case POW_INVSQ: return 1.0f / (x * x);
+    default: return (float)pow((double)x, (double)sc->star_exp);
+    }
+}
+
+static inline float o_lerp(float self, float end, float w) {
+    float d = end - self;
+    return (fabsf(w) < 0.5f) ? fmaf(w, d, self) : fmaf(w - 1.0f, d, end);
+}
+static inline float o_sign(float x) { return x > 0.0f ? 1.0f : (x < 0.0f ? -1.0f : 0.0f); }
+static inline float o_clamp_max(float x, float c) { return x > c ? c : x; }
+static inline float o_clamp_min(float x, float c) { return x < c ? c : x; }
+static inline float o_relu(float x) { return x < 0.0f ? 0.0f : x; }
+
+static inline float bf16_to_f32(uint16_t h) {
+    uint32_t u = ((uint32_t)h) << 16;
+    float f;
+    memcpy(&f, &u, 4);
+    return f;
+}
+/* Round-to-nearest-even binary32 -> bfloat16 (NaN kept quiet). */
+static inline uint16_t f32_to_bf16(float f) {
+    uint32_t u;
+    memcpy(&u, &f, 4);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return (uint16_t)(u >> 16);
+}
+
+/* One ADana / Dana-MK4 element (src/optim/adana.py:101-143). */
+static inline float adana_elem(float p, float g, float *mp, float *vp,
+                               const adana_oracle_scalars *sc, double acc[4]) {
+    float m = o_lerp(*mp, g, sc->a);                         /* :101 */
+    float v = *vp * sc->oma;                                 /* :104 mul_ */
+    v = fmaf(sc->a * g, g, v);                               /* :104 addcmul_ */
+    float se = sqrtf(v) + sc->eps;                           /* :107 */
+    float nt = 1.0f / se;                                    /* :110 */
+    float mn = fabsf(m) * nt;                                /* :111, :115 */
+    float af = sc->pw * mn;                                  /* :119/:123 */
+    if (sc->has_clip) af = o_clamp_max(af, sc->clip);        /* :118-121 */
+    float inner = o_sign(m) * af + m * nt;                   /* :126 */
+    float g3t = sc->c3 * inner;
+    float g2t = (sc->cg2 * g) * nt;                          /* :129 */
+    float u = g2t + g3t;                                     /* :132 */
+    p = p + u;                                               /* :135 */
+    p = p * sc->opw;                                         /* :143 */
+    *mp = m;
+    *vp = v;
+    acc[0] += (double)af;
+    acc[1] += (double)g * (double)g;
+    acc[2] += (double)mn;
+    acc[3] += (double)m * (double)m;
+    return p;
+}
+
+/* One Dana-Star / Dana-Star-MK4 element (src/optim/dana_star_mk4.py:137-195). */
+static inline float star_elem(float p, float g, float *mp, float *vp, float *tp,
+                              const adana_oracle_scalars *sc, double acc[4]) {
+    float m = o_lerp(*mp, g, sc->a);                         /* :137 */
+    float v = *vp * sc->oma;                                 /* :140 */
+    v = fmaf(sc->a * g, g, v);
+    float se = sqrtf(v) + sc->eps;                           /* :143 */
+    float ag = fabsf(g);                                     /* :147 */
+    float tu = ag / (ag + se);                               /* :148 */
+    float tau = o_lerp(*tp, tu, sc->a);                      /* :149 */
+    float ct = o_clamp_max(tau, 0.5f);                       /* :152 */
+    float pe = ct / (1.0f - ct);                             /* :153 */
+    float tr = sc->min_p + o_relu(pe - sc->min_p);           /* :154-156 */
+    float et = o_clamp_min(tau * sc->s, 1.0f);               /* :159 */
+    float nt = sqrtf(tr) / se;                               /* :163-164 */
+    float mnt = fabsf(m) * nt;                               /* :165 */
+    float mf = mnt / tr;                                     /* :167 */
+    float pw = o_pow(et, sc);                                /* :170 / :174 */
+    float af = pw * mf;
+    if (sc->has_clip) af = o_clamp_max(af, sc->clip);        /* :169-172 */
+    float inner = o_sign(m) * (tr * af + mnt);               /* :177 */
+    float g3t = sc->c3 * inner;
+    float g2t = (sc->cg2 * g) * nt;                          /* :180 */
+    float u = g2t + g3t;                                     /* :183 */
+    p = p + u;                                               /* :186 */
+    p = p * sc->opw;                                         /* :195 */
+    *mp = m;
+    *vp = v;
+    *tp = tau;
+    acc[0] += (double)af;
+    acc[1] += (double)g * (double)g;
+    acc[2] += (double)mf;
+    acc[3] += (double)m * (double)m;
+    return p;
+}
+
+/* Parallel element loops.  Element results do not depend on the thread
+ * count; the binary64 diagnostic sums may differ in the last bits. */
+#define DIAG_LOOP(BODY)                                                        \
+    double s0 = 0.0, s1 = 0.0, s2 = 0.0, s3 = 0.0;                             \
+    _Pragma("omp parallel for schedule(static) reduction(+:s0,s1,s2,s3) if(n > 65536)") \
+    for (int64_t i = 0; i < n; ++i) {                                          \
+        double acc[4] = {0.0, 0.0, 0.0, 0.0};                                  \
+        BODY;                                                                  \
+        s0 += acc[0]; s1 += acc[1]; s2 += acc[2]; s3 += acc[3];                \
+    }                                                                          \
+    diag[0] = s0; diag[1] = s1; diag[2] = s2; diag[3] = s3;
+
+void adana_oracle_adana_step(int64_t n, float *p, const float *g, float *m, float *v,
+                             const adana_oracle_scalars *sc, double diag[4]) {
+    DIAG_LOOP(p[i] = adana_elem(p[i], g[i], &m[i], &v[i], sc, acc))
+}
+
+void adana_oracle_star_step(int64_t n, float *p, const float *g, float *m, float *v,
+                            float *tau, const adana_oracle_scalars *sc, double diag[4]) {
+    DIAG_LOOP(p[i] = star_elem(p[i], g[i], &m[i], &v[i], &tau[i], sc, acc))
+}
+
+/* bf16-parameter mode (an extension; the reference has no master weights):
+ * the fp32 master copy is the parameter of the fp32 math, the gradient is
+ * bf16 widened exactly, and the bf16 parameter is RNE(master). tau may be
+ * NULL for the ADana variants. */
+void adana_oracle_master_step(int64_t n, int32_t star, float *master, uint16_t *p16,
+                              const uint16_t *g16, float *m, float *v, float *tau,
+                              const adana_oracle_scalars *sc, double diag[4]) {
+    if (star) {
+        DIAG_LOOP(master[i] = star_elem(master[i], bf16_to_f32(g16[i]), &m[i], &v[i], &tau[i], sc, acc);
+                  p16[i] = f32_to_bf16(master[i]))
+    } else {
+        DIAG_LOOP(master[i] = adana_elem(master[i], bf16_to_f32(g16[i]), &m[i], &v[i], sc, acc);
+                  p16[i] = f32_to_bf16(master[i]))
+    }
+}
+
+/* fp32 parameters with bf16 gradients (extension, same math). */
+void adana_oracle_step_g16(int64_t n, int32_t star, float *p, const uint16_t *g16, float *m,
+                           float *v, float *tau, const adana_oracle_scalars *sc,
+                           double diag[4]) {
+    if (star) {
+        DIAG_LOOP(p[i] = star_elem(p[i], bf16_to_f32(g16[i]), &m[i], &v[i], &tau[i], sc, acc))
+    } else {
+        DIAG_LOOP(p[i] = adana_elem(p[i], bf16_to_f32(g16[i]), &m[i], &v[i], sc, acc))
+    }
+}
+
+void adana_oracle_f32_to_bf16(int64_t n, const float *x, uint16_t *y) {
+    for (int64_t i = 0; i < n; ++i) y[i] = f32_to_bf16(x[i]);
+}
+
+int adana_oracle_abi_version(void) { return 1; }

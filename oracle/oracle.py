@@ -1,0 +1,301 @@
+"""CPU oracle for the ADana-family optimizer step.
+
+TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and the
+cpu_baseline leg of bench.py, always as the checker (or the timed CPU
+baseline), never by the product package ``adana_amd``.
+
+This module restates, independently of the product:
+
+* the host-side scalar schedule of ``ADana.step`` (src/optim/adana.py:162-208)
+  and ``DANA_STAR_MK4.step`` (src/optim/dana_star_mk4.py:215-272), including
+  the 0-d tensor arithmetic the compiled update performs on those scalars
+  (``1 - alpha``, ``1.0 + step``, ``(-g3) * gamma_3_factor``, the weight-decay
+  factor, ``1.0 / (1.0 + step)``), each as one binary32 operation in numpy;
+* the per-tensor step loop (grad-None skip, lazy state init, per-tensor step
+  counter, diagnostics), src/optim/adana.py:184-225 and
+  src/optim/dana_star_mk4.py:243-294;
+* the element math itself lives in ``adana_oracle.c`` (same directory).
+"""
+from __future__ import annotations
+
+import ctypes
+import math
+import os
+from dataclasses import dataclass, field
+from typing import Dict, List, Optional, Sequence
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "liboracle.so")
+
+f32 = np.float32
+
+
+class OracleScalars(ctypes.Structure):
+    """Mirror of ``adana_oracle_scalars`` in adana_oracle.c."""
+
+    _fields_ = [
+        ("a", ctypes.c_float),
+        ("oma", ctypes.c_float),
+        ("s", ctypes.c_float),
+        ("eps", ctypes.c_float),
+        ("pw", ctypes.c_float),
+        ("min_p", ctypes.c_float),
+        ("clip", ctypes.c_float),
+        ("has_clip", ctypes.c_int32),
+        ("c3", ctypes.c_float),
+        ("cg2", ctypes.c_float),
+        ("opw", ctypes.c_float),
+        ("star_exp", ctypes.c_float),
+        ("pow_mode", ctypes.c_int32),
+    ]
+
+
+_lib = None
+
+
+def lib():
+    """Load (building first if needed) the oracle's shared library."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            build()
+        L = ctypes.CDLL(LIB_PATH)
+        P = ctypes.c_void_p
+        i64 = ctypes.c_int64
+        i32 = ctypes.c_int32
+        SP = ctypes.POINTER(OracleScalars)
+        L.adana_oracle_adana_step.argtypes = [i64, P, P, P, P, SP, P]
+        L.adana_oracle_star_step.argtypes = [i64, P, P, P, P, P, SP, P]
+        L.adana_oracle_master_step.argtypes = [i64, i32, P, P, P, P, P, P, SP, P]
+        L.adana_oracle_step_g16.argtypes = [i64, i32, P, P, P, P, P, SP, P]
+        L.adana_oracle_f32_to_bf16.argtypes = [i64, P, P]
+        for fn in (L.adana_oracle_adana_step, L.adana_oracle_star_step,
+                   L.adana_oracle_master_step, L.adana_oracle_step_g16,
+                   L.adana_oracle_f32_to_bf16):
+            fn.restype = None
+        _lib = L
+    return _lib
+
+
+def build() -> None:
+    """Compile adana_oracle.c with the oracle's Makefile."""
+    import subprocess
+
+    subprocess.run(["make", "-s", "-C", _HERE], check=True)
+
+
+# --------------------------------------------------------------------------
+# Host scalars
+# --------------------------------------------------------------------------
+
+def _pow0d(x: np.float32, e: float) -> np.float32:
+    """``x ** e`` for a 0-d binary32 tensor and a Python-float exponent.
+
+    ATen's pow(Tensor, Scalar) special-cases a few exponents (0 fills ones;
+    0.5 sqrt; -0.5 rsqrt; -1 reciprocal; 2, 3, -2 by multiplication) and
+    otherwise evaluates std::pow(float, double) in binary64 for a 0-d tensor
+    (probed bitwise against torch 2.10; reference call site
+    src/optim/adana.py:119,123).
+    """
+    x = f32(x)
+    if e == 0.0:
+        return f32(1.0)
+    if e == 0.5:
+        return f32(np.sqrt(x))
+    if e == -0.5:
+        return f32(1.0) / f32(np.sqrt(x))
+    if e == -1.0:
+        return f32(1.0) / x
+    if e == 2.0:
+        return x * x
+    if e == 3.0:
+        return (x * x) * x
+    if e == -2.0:
+        return f32(1.0) / (x * x)
+    return f32(math.pow(float(x), e))
+
+
+POW_GENERAL, POW_ONE, POW_SQRT, POW_RSQRT, POW_RECIP, POW_SQUARE, POW_CUBE, POW_INVSQ = range(8)
+
+
+def pow_mode(e: float) -> int:
+    """Which ATen pow specialisation an exponent selects (see _pow0d)."""
+    return {0.0: POW_ONE, 0.5: POW_SQRT, -0.5: POW_RSQRT, -1.0: POW_RECIP,
+            2.0: POW_SQUARE, 3.0: POW_CUBE, -2.0: POW_INVSQ}.get(e, POW_GENERAL)
+
+
+def step_scalars(*, lr: float, peak_lr: float, delta: float, kappa: float, epsilon: float,
+                 weight_decay: float, clipsnr: Optional[float], wd_decaying: bool,
+                 wd_ts: float, gamma_3_factor: float, t: int) -> OracleScalars:
+    """Scalars of one tensor's update at per-tensor step ``t`` (already incremented).
+
+    Follows src/optim/adana.py:163-208 (host) and :104-143 (0-d tensor ops
+    inside the compiled update); Dana-Star uses the same host code
+    (src/optim/dana_star_mk4.py:217-272) plus min_p (:154).
+    """
+    sf = f32(lr / peak_lr)                       # :165 double divide, :207 fp32
+    g2 = f32(lr)                                 # :205
+    g3 = f32(lr)                                 # :206
+    wd = f32(weight_decay)                       # :208
+    a = f32(delta / (delta + t))                 # :200 double, :204 fp32
+    s = f32(t)                                   # :203
+    one_p_s = f32(1.0) + s                       # :114 ``1.0 + step``
+    sc = OracleScalars()
+    sc.a = a
+    sc.oma = f32(1.0) - a                        # :104 ``1 - alpha``
+    sc.s = s
+    sc.eps = f32(epsilon)                        # :107 add_(epsilon)
+    sc.pw = _pow0d(one_p_s, 1.0 - kappa)         # :119 / :123
+    sc.min_p = f32(1.0) / one_p_s                # dana_star_mk4.py:154
+    sc.has_clip = 0 if clipsnr is None else 1
+    sc.clip = f32(clipsnr) if clipsnr is not None else f32(np.inf)
+    sc.c3 = (-g3) * f32(gamma_3_factor)          # :126 ``(-g3) * gamma_3_factor``
+    sc.cg2 = -g2                                 # :129 ``(-g2)``
+    if wd_decaying:                              # :139-142
+        wdf = ((-wd) / (f32(1.0) + s / f32(wd_ts))) * sf
+    else:
+        wdf = (-wd) * sf
+    sc.opw = f32(1.0) + wdf                      # :143 ``1 + wd_factor``
+    sc.star_exp = f32(1.0 - kappa)               # dana_star_mk4.py:170 (vectorised pow)
+    sc.pow_mode = pow_mode(1.0 - kappa)
+    return sc
+
+
+# --------------------------------------------------------------------------
+# Element kernels
+# --------------------------------------------------------------------------
+
+def _ptr(a: np.ndarray) -> ctypes.c_void_p:
+    assert a.flags["C_CONTIGUOUS"], "oracle arrays must be C-contiguous"
+    return ctypes.c_void_p(a.ctypes.data)
+
+
+def element_step(star: bool, p: np.ndarray, g: np.ndarray, m: np.ndarray, v: np.ndarray,
+                 tau: Optional[np.ndarray], sc: OracleScalars) -> np.ndarray:
+    """Apply one element-wise update in place; return binary64 sums
+    [sum(alpha_factor), sum(g^2), sum(mfac), sum(m^2)]."""
+    L = lib()
+    diag = np.zeros(4, dtype=np.float64)
+    n = p.size
+    if g.dtype == np.float32 and p.dtype == np.float32:
+        if star:
+            L.adana_oracle_star_step(n, _ptr(p), _ptr(g), _ptr(m), _ptr(v), _ptr(tau),
+                                     ctypes.byref(sc), _ptr(diag))
+        else:
+            L.adana_oracle_adana_step(n, _ptr(p), _ptr(g), _ptr(m), _ptr(v),
+                                      ctypes.byref(sc), _ptr(diag))
+    elif g.dtype == np.uint16 and p.dtype == np.float32:
+        L.adana_oracle_step_g16(n, int(star), _ptr(p), _ptr(g), _ptr(m), _ptr(v),
+                                _ptr(tau) if star else None, ctypes.byref(sc), _ptr(diag))
+    else:
+        raise TypeError(f"oracle: unsupported dtypes p={p.dtype} g={g.dtype}")
+    return diag
+
+
+def master_step(star: bool, master: np.ndarray, p16: np.ndarray, g16: np.ndarray,
+                m: np.ndarray, v: np.ndarray, tau: Optional[np.ndarray],
+                sc: OracleScalars) -> np.ndarray:
+    """bf16-parameter mode: fp32 math on ``master``; ``p16`` = RNE(master)."""
+    L = lib()
+    diag = np.zeros(4, dtype=np.float64)
+    L.adana_oracle_master_step(master.size, int(star), _ptr(master), _ptr(p16), _ptr(g16),
+                               _ptr(m), _ptr(v), _ptr(tau) if star else None,
+                               ctypes.byref(sc), _ptr(diag))
+    return diag
+
+
+def f32_to_bf16(x: np.ndarray) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    y = np.empty(x.shape, dtype=np.uint16)
+    lib().adana_oracle_f32_to_bf16(x.size, _ptr(x), _ptr(y))
+    return y
+
+
+def bf16_to_f32(h: np.ndarray) -> np.ndarray:
+    return (np.ascontiguousarray(h, dtype=np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+# --------------------------------------------------------------------------
+# Step loop (restates the reference optimizers' step() bookkeeping)
+# --------------------------------------------------------------------------
+
+DIAG_KEYS = ("current_alpha", "gradient_norm", "auto_factor_mean",
+             "current_kappa_factor", "m_norm")
+
+
+def finalize_diag(sums: np.ndarray, n: int) -> Dict[str, float]:
+    """Per-tensor diagnostics from binary64 sums (src/optim/adana.py:146-151,221-225)."""
+    with np.errstate(invalid="ignore", divide="ignore"):
+        ca = sums[0] / n if n else float("nan")
+        afm = sums[2] / n if n else float("nan")
+        kf = np.float64(ca) / np.float64(afm)
+    return {"current_alpha": float(ca), "gradient_norm": math.sqrt(sums[1]),
+            "auto_factor_mean": float(afm), "current_kappa_factor": float(kf),
+            "m_norm": math.sqrt(sums[3])}
+
+
+@dataclass
+class OracleGroup:
+    params: List[np.ndarray]
+    lr: float
+    delta: float = 8.0
+    epsilon: float = 1e-8
+    weight_decay: float = 0.0
+    weighted_step_count: float = 0.0
+
+
+@dataclass
+class OracleOptimizer:
+    """Restatement of ADana / DANA_STAR_MK4 over numpy arrays.
+
+    ``star`` selects Dana-Star(-MK4); ``clipsnr=None`` disables SNR clipping.
+    ``peak_lr`` plays the part of the constructor's ``lr`` (``self.lr``).
+    Params are float32 arrays (or, with ``master=True``, uint16 bf16 arrays
+    with an fp32 master copy kept in the state).
+    """
+
+    groups: List[OracleGroup]
+    star: bool
+    peak_lr: float
+    kappa: float = 1.0
+    clipsnr: Optional[float] = None
+    wd_decaying: bool = False
+    wd_ts: float = 1.0
+    gamma_3_factor: float = 1.0
+    master: bool = False
+    state: Dict[int, dict] = field(default_factory=dict)
+
+    def step(self, grads: Sequence[Sequence[Optional[np.ndarray]]]) -> None:
+        """``grads[gi][pi]`` is the gradient of group gi's param pi, or None."""
+        for gi, group in enumerate(self.groups):
+            sf = group.lr / self.peak_lr                       # adana.py:165
+            group.weighted_step_count += sf                    # adana.py:167
+            for pi, p in enumerate(group.params):
+                g = grads[gi][pi]
+                if g is None:                                  # adana.py:186
+                    continue
+                key = id(p)
+                st = self.state.get(key)
+                if st is None:                                 # adana.py:191-195
+                    st = {"step": 0,
+                          "m": np.zeros(p.shape, np.float32),
+                          "v": np.zeros(p.shape, np.float32)}
+                    if self.star:
+                        st["tau"] = np.zeros(p.shape, np.float32)
+                    if self.master:
+                        st["master"] = bf16_to_f32(p).reshape(p.shape).copy()
+                    self.state[key] = st
+                st["step"] += 1                                # adana.py:197
+                sc = step_scalars(lr=group.lr, peak_lr=self.peak_lr, delta=group.delta,
+                                  kappa=self.kappa, epsilon=group.epsilon,
+                                  weight_decay=group.weight_decay, clipsnr=self.clipsnr,
+                                  wd_decaying=self.wd_decaying, wd_ts=self.wd_ts,
+                                  gamma_3_factor=self.gamma_3_factor, t=st["step"])
+                if self.master:
+                    sums = master_step(self.star, st["master"], p, g, st["m"], st["v"],
+                                       st.get("tau"), sc)
+                else:
+                    sums = element_step(self.star, p, g, st["m"], st["v"], st.get("tau"), sc)
+                st.update(finalize_diag(sums, p.size))

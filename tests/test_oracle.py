@@ -1,0 +1,317 @@
+"""Pins the CPU oracle (oracle/) before it is trusted as the parity checker.
+
+1. Golden vectors written by the reference's own step() (tests/golden/):
+   m and v bit-exact along the whole trajectory; tau within 2 ulp; p within
+   2 ulp (ADana) / 4 ulp (Dana-Star) per step from identical state, in ulps
+   of max(|p_before|, |p_after|, |update|) (the reference's CPU sqrt and pow are Sleef
+   approximations, the oracle's are correctly rounded).
+2. Closed forms for a constant gradient from zero state (float64 maths).
+3. Invariants and special cases the reference's formulas imply.
+"""
+import math
+
+import numpy as np
+import pytest
+
+from helpers import golden_cases, load_golden_case, load_golden_inputs, ulp_diff
+
+pytestmark = pytest.mark.filterwarnings("ignore::RuntimeWarning")
+
+
+def _make_oracle(O, meta, case, params):
+    kw = meta["cases"][case]["kwargs"]
+    star = meta["cases"][case]["class"] == "DANA_STAR_MK4"
+    groups = []
+    for gi in range(2):
+        groups.append(O.OracleGroup(
+            params=[params[i] for i in range(len(params)) if meta["group_of"][i] == gi],
+            lr=kw["lr"], delta=kw["delta"], epsilon=1e-8,
+            weight_decay=kw["weight_decay"] * meta["group_wd_scale"][gi]))
+    opt = O.OracleOptimizer(groups=groups, star=star, peak_lr=kw["lr"], kappa=kw["kappa"],
+                            clipsnr=kw["clipsnr"], wd_decaying=kw["wd_decaying"],
+                            wd_ts=kw["wd_ts"], gamma_3_factor=kw["gamma_3_factor"])
+    return opt, kw, star
+
+
+def _grads_for_step(meta, grads, has_grad, k):
+    out = []
+    for gi in range(2):
+        idx = [i for i in range(len(meta["shapes"])) if meta["group_of"][i] == gi]
+        out.append([grads[k - 1][i] if has_grad[k - 1, i] else None for i in idx])
+    return out
+
+
+def _scaled_err(x, ref, scale):
+    """|x - ref| in units of ulp(scale) (elementwise)."""
+    scale = np.maximum(np.abs(scale), np.float32(1e-30)).astype(np.float32)
+    ulp = np.spacing(scale).astype(np.float64)
+    return np.abs(x.astype(np.float64) - ref.astype(np.float64)) / ulp
+
+
+@pytest.mark.parametrize("case", golden_cases("eager"))
+def test_golden_trajectory(oracle_mod, case):
+    O = oracle_mod
+    meta, p0, grads, has_grad = load_golden_inputs()
+    gold = load_golden_case(case, "eager")
+    params = [x.copy() for x in p0]
+    opt, kw, star = _make_oracle(O, meta, case, params)
+    diag_keys = O.DIAG_KEYS
+    for k in range(1, meta["n_steps"] + 1):
+        for g in opt.groups:
+            g.lr = kw["lr"] * meta["lr_multiplier"][k - 1]
+        opt.step(_grads_for_step(meta, grads, has_grad, k))
+        for i, p in enumerate(params):
+            st = opt.state.get(id(p))
+            if st is None:
+                continue
+            ref = gold["diag"][k - 1, i]
+            got = np.array([st[key] for key in diag_keys])
+            np.testing.assert_allclose(got, ref, rtol=2e-5, atol=1e-12, equal_nan=True,
+                                       err_msg=f"{case} diag t={k} tensor {i}")
+        if k not in meta["checkpoints"]:
+            continue
+        for i, p in enumerate(params):
+            st = opt.state.get(id(p), {})
+            assert st.get("step", 0) == int(gold[f"step{i}_t{k}"])
+            if "m" not in st:
+                np.testing.assert_array_equal(p, gold[f"p{i}_t{k}"])
+                continue
+            # m, v: bit-exact (no sqrt/pow on their path)
+            assert ulp_diff(st["m"], gold[f"m{i}_t{k}"]).max() == 0, f"{case} m t={k} i={i}"
+            assert ulp_diff(st["v"], gold[f"v{i}_t{k}"]).max() == 0, f"{case} v t={k} i={i}"
+            if star:
+                assert ulp_diff(st["tau"], gold[f"tau{i}_t{k}"]).max() <= 2
+            # p along the trajectory: differences start as <=1-ulp per step and
+            # accumulate additively; bound them by ulp(max |p| of the tensor) * k.
+            scale = np.full(p.shape, np.abs(gold[f"p{i}_t{k}"]).max(), np.float32)
+            assert _scaled_err(p, gold[f"p{i}_t{k}"], scale).max() <= 2 * k
+
+
+@pytest.mark.parametrize("case", golden_cases("eager"))
+@pytest.mark.parametrize("t0", [0, 7, 8])
+def test_golden_single_step(oracle_mod, case, t0):
+    """From the reference's own state at step t0, one oracle step lands within
+    2 ulp of the reference's state at t0 + 1 (bit-exact for m and v)."""
+    O = oracle_mod
+    meta, p0, grads, has_grad = load_golden_inputs()
+    gold = load_golden_case(case, "eager")
+    k = t0 + 1
+    params = [(p0[i] if t0 == 0 else gold[f"p{i}_t{t0}"]).copy() for i in range(len(p0))]
+    opt, kw, star = _make_oracle(O, meta, case, params)
+    if t0 > 0:
+        for i, p in enumerate(params):
+            if f"m{i}_t{t0}" not in gold:
+                continue
+            st = {"step": int(gold[f"step{i}_t{t0}"]), "m": gold[f"m{i}_t{t0}"].copy(),
+                  "v": gold[f"v{i}_t{t0}"].copy()}
+            if star:
+                st["tau"] = gold[f"tau{i}_t{t0}"].copy()
+            opt.state[id(p)] = st
+    prev = [p.copy() for p in params]
+    for g in opt.groups:
+        g.lr = kw["lr"] * meta["lr_multiplier"][k - 1]
+    opt.step(_grads_for_step(meta, grads, has_grad, k))
+    for i, p in enumerate(params):
+        st = opt.state.get(id(p))
+        if st is None:
+            continue
+        assert st["step"] == int(gold[f"step{i}_t{k}"])
+        assert ulp_diff(st["m"], gold[f"m{i}_t{k}"]).max() == 0
+        assert ulp_diff(st["v"], gold[f"v{i}_t{k}"]).max() == 0
+        if star:
+            assert ulp_diff(st["tau"], gold[f"tau{i}_t{k}"]).max() <= 2
+        ref = gold[f"p{i}_t{k}"]
+        scale = np.maximum(np.maximum(np.abs(prev[i]), np.abs(ref)), np.abs(ref - prev[i]))
+        err = _scaled_err(p, ref, scale)
+        # Dana-Star's update passes through three of the reference's Sleef
+        # approximations (sqrt(v), sqrt(tau_reg), pow), each <=1 ulp off the
+        # correctly rounded value the oracle takes, so its bound is 4 ulp.
+        bound = 4 if star else 2
+        assert err.max() <= bound, f"{case} t0={t0} tensor {i}: {err.max()} ulp"
+
+
+@pytest.mark.parametrize("case", golden_cases("compiled"))
+def test_golden_compiled_close(oracle_mod, case):
+    """The reference's default torch.compile path (Inductor-CPU) agrees with the
+    oracle to a few ulp of the tensors' scale after 20 steps."""
+    O = oracle_mod
+    meta, p0, grads, has_grad = load_golden_inputs()
+    gold = load_golden_case(case, "compiled")
+    params = [x.copy() for x in p0]
+    opt, kw, star = _make_oracle(O, meta, case, params)
+    for k in range(1, meta["n_steps"] + 1):
+        for g in opt.groups:
+            g.lr = kw["lr"] * meta["lr_multiplier"][k - 1]
+        opt.step(_grads_for_step(meta, grads, has_grad, k))
+    k = meta["n_steps"]
+    for i, p in enumerate(params):
+        st = opt.state[id(p)]
+        for name, arr in (("m", st["m"]), ("v", st["v"])) + ((("tau", st["tau"]),) if star else ()):
+            ref = gold[f"{name}{i}_t{k}"]
+            scale = np.full(arr.shape, np.abs(ref).max(), np.float32)
+            assert _scaled_err(arr, ref, scale).max() <= 4, f"{case} {name}{i}"
+        ref = gold[f"p{i}_t{k}"]
+        scale = np.full(p.shape, np.abs(ref).max(), np.float32)
+        assert _scaled_err(p, ref, scale).max() <= 2 * k, f"{case} p{i}"
+
+
+# --------------------------------------------------------------------------
+# Closed forms (float64 mathematics) for a constant gradient from zero state
+# --------------------------------------------------------------------------
+
+def _pi(delta, t):
+    """prod_{k<=t} (1 - delta/(delta+k)) = prod k/(delta+k)."""
+    return math.exp(math.lgamma(t + 1) + math.lgamma(delta + 1) - math.lgamma(delta + t + 1))
+
+
+@pytest.mark.parametrize("star", [False, True])
+@pytest.mark.parametrize("clipsnr", [None, 0.9])
+def test_closed_form_constant_gradient(oracle_mod, star, clipsnr):
+    O = oracle_mod
+    rng = np.random.default_rng(5)
+    n = 257
+    g = (rng.normal(0, 1e-3, n)).astype(np.float32)
+    g[::17] = 0.0
+    p = rng.normal(0, 0.02, n).astype(np.float32)
+    lr, delta, kappa, eps, wd, wd_ts, g3f = 2e-3, 8.0, 0.8, 1e-8, 0.3, 10.0, 0.75
+    opt = O.OracleOptimizer(groups=[O.OracleGroup(params=[p], lr=lr, delta=delta, epsilon=eps,
+                                                  weight_decay=wd)],
+                            star=star, peak_lr=lr, kappa=kappa, clipsnr=clipsnr,
+                            wd_decaying=True, wd_ts=wd_ts, gamma_3_factor=g3f)
+    gd = g.astype(np.float64)
+    pd = p.astype(np.float64)
+    taud = np.zeros(n)
+    for t in range(1, 31):
+        opt.step([[g]])
+        st = opt.state[id(p)]
+        pi = _pi(delta, t)
+        m_cf = gd * (1 - pi)
+        v_cf = gd * gd * (1 - pi)
+        np.testing.assert_allclose(st["m"], m_cf, rtol=4e-6 * t, atol=1e-30)
+        np.testing.assert_allclose(st["v"], v_cf, rtol=4e-6 * t, atol=1e-30)
+        a = delta / (delta + t)
+        se = np.sqrt(v_cf) + np.float64(np.float32(eps))
+        if star:
+            tu = np.abs(gd) / (np.abs(gd) + se)
+            taud = (1 - a) * taud + a * tu
+            np.testing.assert_allclose(st["tau"], taud, rtol=1e-5, atol=1e-12)
+            ct = np.minimum(taud, 0.5)
+            tr = np.maximum(ct / (1 - ct), 1.0 / (1 + t))
+            et = np.maximum(taud * t, 1.0)
+            nt = np.sqrt(tr) / se
+            mnt = np.abs(m_cf) * nt
+            af = et ** (1 - kappa) * mnt / tr
+            if clipsnr is not None:
+                af = np.minimum(af, clipsnr)
+            u = -lr * gd * nt - lr * g3f * np.sign(m_cf) * (tr * af + mnt)
+        else:
+            nt = 1.0 / se
+            af = (1 + t) ** (1 - kappa) * np.abs(m_cf) * nt
+            if clipsnr is not None:
+                af = np.minimum(af, clipsnr)
+            u = -lr * gd * nt - lr * g3f * (np.sign(m_cf) * af + m_cf * nt)
+        pd = (pd + u) * (1 - wd / (1 + t / wd_ts))
+        np.testing.assert_allclose(p, pd, rtol=1e-5, atol=2e-9 * t)
+        np.testing.assert_allclose(st["current_alpha"], af.mean(), rtol=1e-5)
+        np.testing.assert_allclose(st["gradient_norm"], np.linalg.norm(gd), rtol=1e-6)
+        np.testing.assert_allclose(st["m_norm"], np.linalg.norm(m_cf), rtol=1e-5)
+
+
+# --------------------------------------------------------------------------
+# Scalars and invariants
+# --------------------------------------------------------------------------
+
+def test_scalars_alpha_half_at_t_equals_delta(oracle_mod):
+    sc = oracle_mod.step_scalars(lr=1e-3, peak_lr=1e-3, delta=8.0, kappa=0.85, epsilon=1e-8,
+                                 weight_decay=0.0, clipsnr=None, wd_decaying=False,
+                                 wd_ts=1.0, gamma_3_factor=1.0, t=8)
+    assert sc.a == 0.5 and sc.oma == 0.5
+    assert sc.opw == 1.0                      # weight_decay 0 leaves p*1 exact
+    assert sc.min_p == np.float32(1.0) / np.float32(9.0)
+
+
+def test_scalars_weight_decay_factor(oracle_mod):
+    for t in (1, 7, 100, 12345):
+        sc = oracle_mod.step_scalars(lr=3e-3, peak_lr=6e-3, delta=8.0, kappa=0.85,
+                                     epsilon=1e-8, weight_decay=0.4, clipsnr=None,
+                                     wd_decaying=True, wd_ts=20.0, gamma_3_factor=1.0, t=t)
+        exact = 1.0 - 0.4 / (1.0 + t / 20.0) * 0.5
+        assert abs(float(sc.opw) - exact) <= 2 * np.spacing(np.float32(exact))
+        assert abs(float(sc.pw) - (1.0 + t) ** 0.15) <= np.spacing(np.float32((1.0 + t) ** 0.15))
+
+
+def _run(O, star, clipsnr, kappa, p, grads, wd=0.2):
+    opt = O.OracleOptimizer(groups=[O.OracleGroup(params=[p], lr=1e-3, weight_decay=wd)],
+                            star=star, peak_lr=1e-3, kappa=kappa, clipsnr=clipsnr,
+                            wd_decaying=True, wd_ts=5.0)
+    for g in grads:
+        opt.step([[g]])
+    return opt.state[id(p)]
+
+
+@pytest.mark.parametrize("star", [False, True])
+def test_invariants(oracle_mod, star):
+    O = oracle_mod
+    rng = np.random.default_rng(9)
+    n = 1000
+    grads = [rng.normal(0, 1e-3, n).astype(np.float32) for _ in range(12)]
+    p_a = rng.normal(0, 0.02, n).astype(np.float32)
+    p_b = rng.normal(0, 1.0, n).astype(np.float32)
+    sa = _run(O, star, None, 0.85, p_a, grads)
+    sb = _run(O, star, None, 0.85, p_b, grads)
+    # state never reads p
+    for key in ("m", "v") + (("tau",) if star else ()):
+        np.testing.assert_array_equal(sa[key], sb[key])
+    # clipsnr = +inf is the unclipped variant, bit for bit
+    p_c = p_a.copy()
+    p_a2 = rng.normal(0, 0.02, n).astype(np.float32)
+    p_c = p_a2.copy()
+    s1 = _run(O, star, None, 0.85, p_a2, grads)
+    s2 = _run(O, star, float("inf"), 0.85, p_c, grads)
+    np.testing.assert_array_equal(p_a2, p_c)
+    assert s1["current_alpha"] == s2["current_alpha"]
+    # a tight clip really clips: mean alpha factor never exceeds it
+    p_d = rng.normal(0, 0.02, n).astype(np.float32)
+    s3 = _run(O, star, 0.05, 0.85, p_d, grads)
+    assert s3["current_alpha"] <= 0.05 + 1e-9
+    if star:
+        assert np.all(sa["tau"] >= 0) and np.all(sa["tau"] < 1)
+    assert np.all(sa["v"] >= 0)
+
+
+def test_zero_gradient_tensor(oracle_mod):
+    """All-zero grads: m = v = tau = 0, sign(0) = 0, kappa factor 0/0 = NaN
+    (src/optim/adana.py:224), p only decays."""
+    O = oracle_mod
+    for star in (False, True):
+        p = np.linspace(-1, 1, 64).astype(np.float32)
+        p0 = p.copy()
+        st = _run(O, star, 2.0, 0.85, p, [np.zeros(64, np.float32)] * 3, wd=0.0)
+        assert np.all(st["m"] == 0) and np.all(st["v"] == 0)
+        assert math.isnan(st["current_kappa_factor"])
+        assert st["current_alpha"] == 0.0 and st["gradient_norm"] == 0.0
+        np.testing.assert_array_equal(p, p0)     # wd = 0 and zero update
+
+
+def test_kappa_one_pow_is_one(oracle_mod):
+    """kappa = 1 gives (1+t)^0 = 1 and Dana-Star's et^0 = 1."""
+    sc = oracle_mod.step_scalars(lr=1.0, peak_lr=1.0, delta=8.0, kappa=1.0, epsilon=1e-8,
+                                 weight_decay=0.0, clipsnr=None, wd_decaying=False, wd_ts=1.0,
+                                 gamma_3_factor=1.0, t=77)
+    assert sc.pw == 1.0 and sc.pow_mode == oracle_mod.POW_ONE
+
+
+def test_gamma3_zero_is_rmsprop_like(oracle_mod):
+    """gamma_3_factor = 0 removes the momentum term: p -= lr * g / (sqrt(v)+eps)."""
+    O = oracle_mod
+    rng = np.random.default_rng(3)
+    n = 300
+    p = rng.normal(0, 0.02, n).astype(np.float32)
+    g = rng.normal(0, 1e-3, n).astype(np.float32)
+    pd = p.astype(np.float64)
+    opt = O.OracleOptimizer(groups=[O.OracleGroup(params=[p], lr=1e-2)], star=False,
+                            peak_lr=1e-2, kappa=0.85, gamma_3_factor=0.0)
+    opt.step([[g]])
+    v = (8.0 / 9.0) * g.astype(np.float64) ** 2
+    pd = pd - 1e-2 * g / (np.sqrt(v) + 1e-8)
+    np.testing.assert_allclose(p, pd, rtol=1e-6, atol=3e-9)
