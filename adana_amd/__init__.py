@@ -1,0 +1,11 @@
+"""adana_amd: MI355X-native ADana-family optimizer step.
+
+``ADana`` (ADana / Dana-MK4) and ``DANA_STAR_MK4`` (Dana-Star / Dana-Star-MK4)
+are drop-ins for mlexpos/adana's src/optim/adana.py and
+src/optim/dana_star_mk4.py whose step() runs one hand-written gfx950 HIP
+multi-tensor kernel (adana_amd/csrc/adana_mta.hip) through the C ABI in
+include/adana_mta.h.
+"""
+from .optim import ADana, DANA_STAR_MK4, DIAG_KEYS
+
+__all__ = ["ADana", "DANA_STAR_MK4", "DIAG_KEYS"]

@@ -1,0 +1,369 @@
+"""Drop-in ``ADana`` and ``DANA_STAR_MK4`` whose ``step()`` runs one HIP kernel.
+
+Reference: mlexpos/adana ``src/optim/adana.py`` (ADana: ``clipsnr=None`` is
+ADana, a float is Dana-MK4) and ``src/optim/dana_star_mk4.py`` (Dana-Star /
+Dana-Star-MK4).  Constructor arguments, defaults, ``param_groups`` keys,
+instance attributes and per-parameter state keys are the reference's:
+
+    state[p] = {'step': int, 'm': T, 'v': T, ['tau': T,]
+                'current_alpha', 'gradient_norm', 'auto_factor_mean',
+                'current_kappa_factor', 'm_norm'}            (0-d fp32 tensors)
+
+What differs is how a step executes.  The reference loops over tensors in
+Python, makes six 0-d device tensors per tensor and calls a torch.compile'd
+update per tensor (src/optim/adana.py:184-225).  Here the host computes the
+per-step scalars once per (group, step) class in C, and a single
+multi-tensor HIP kernel (adana_amd/csrc/adana_mta.hip) updates every tensor
+and writes all diagnostics into one device buffer.  The diagnostic entries of
+the state are 0-d views of that buffer: they hold the latest step's values
+(the reference rebinds new tensors each step; here the same tensors are
+refreshed in place).
+
+Extension (no reference counterpart): ``master_weights=True`` lets bfloat16
+parameters keep a float32 master copy (state key ``'master'``) with float32
+m/v[/tau]; the update runs in float32 on the master and the bf16 parameter is
+written as RNE(master) in the same pass.
+"""
+from __future__ import annotations
+
+import ctypes
+from typing import Iterable, List, Optional
+
+import numpy as np
+import torch
+from torch.optim import Optimizer
+
+from . import _lib
+
+DIAG_KEYS = ("current_alpha", "gradient_norm", "auto_factor_mean",
+             "current_kappa_factor", "m_norm")
+
+
+class _LaunchSet:
+    """Tensors sharing one kernel instantiation, one device and <= MAX_CLASSES
+    scalar classes: one adana_mta_step call per step."""
+
+    def __init__(self, device, flags, class_base):
+        self.device = device
+        self.flags = flags
+        self.class_base = class_base
+        self.index: List[int] = []       # positions in the step's (param, grad) list
+        self.params: List[torch.Tensor] = []
+        self.grads: List[torch.Tensor] = []
+        self.states: List[dict] = []
+        self.sclass: List[int] = []
+        self.host_desc = None
+        self.vstart = None
+        self.n_chunks = 0
+        self.dev_table = None
+        self.chunk_first = None
+        self.partials = None
+        self.diag = None
+        self.ptr_key = None
+
+
+class _DanaFamily(Optimizer):
+    """Shared engine of ADana and DANA_STAR_MK4 (one code path for both)."""
+
+    _STAR = False
+
+    def _engine_init(self, master_weights: bool) -> None:
+        self.master_weights = bool(master_weights)
+        self._sets: Optional[List[_LaunchSet]] = None
+        self._structure = None
+        _lib.lib()  # fail at construction, not at the first step, without the kernel library
+
+    # -- state ------------------------------------------------------------
+    def _init_state(self, p: torch.Tensor, state: dict) -> None:
+        state["step"] = 0
+        if p.dtype == torch.bfloat16 and self.master_weights:
+            state["m"] = torch.zeros_like(p, dtype=torch.float32)
+            state["v"] = torch.zeros_like(p, dtype=torch.float32)
+            if self._STAR:
+                state["tau"] = torch.zeros_like(p, dtype=torch.float32)
+            state["master"] = p.detach().to(torch.float32)
+        else:
+            state["m"] = torch.zeros_like(p)            # src/optim/adana.py:193-194
+            state["v"] = torch.zeros_like(p)
+            if self._STAR:
+                state["tau"] = torch.zeros_like(p)      # src/optim/dana_star_mk4.py:255
+
+    def invalidate_plan(self) -> None:
+        """Forget cached device tables (call after swapping state tensors or
+        parameter storage by hand)."""
+        self._sets = None
+        self._structure = None
+
+    def load_state_dict(self, state_dict) -> None:
+        super().load_state_dict(state_dict)
+        if self.master_weights:
+            # torch casts floating state to the parameter dtype on load; the
+            # master copy and the moments of bf16 parameters stay float32.
+            saved = state_dict["state"]
+            order = [p for g in self.param_groups for p in g["params"]]
+            saved_ids = [i for g in state_dict["param_groups"] for i in g["params"]]
+            for pid, p in zip(saved_ids, order):
+                if pid in saved and p.dtype == torch.bfloat16:
+                    st = self.state[p]
+                    for k in ("master", "m", "v", "tau"):
+                        if k in saved[pid]:
+                            st[k] = saved[pid][k].to(device=p.device, dtype=torch.float32)
+        self.invalidate_plan()
+
+    # -- plan -------------------------------------------------------------
+    def _validate(self, p: torch.Tensor, g: torch.Tensor) -> int:
+        """Return the kernel variant flags of one (param, grad) pair or raise."""
+        if p.device.type != "cuda":
+            raise RuntimeError(f"{type(self).__name__}: parameters must live on a ROCm GPU "
+                               f"(got {p.device}); the step has no CPU path")
+        if g.is_sparse:
+            raise RuntimeError(f"{type(self).__name__} does not support sparse gradients")
+        if g.device != p.device or g.shape != p.shape:
+            raise RuntimeError(f"{type(self).__name__}: grad must match its parameter's "
+                               f"device and shape ({g.device}/{tuple(g.shape)} vs "
+                               f"{p.device}/{tuple(p.shape)})")
+        if not (p.is_contiguous() and g.is_contiguous()):
+            raise NotImplementedError(f"{type(self).__name__}: non-contiguous parameters or "
+                                      "gradients are not supported")
+        flags = _lib.VARIANT_STAR if self._STAR else 0
+        if p.dtype == torch.float32:
+            if g.dtype != torch.float32:
+                raise RuntimeError(f"{type(self).__name__}: float32 parameter with {g.dtype} "
+                                   "gradient (expected float32)")
+        elif p.dtype == torch.bfloat16:
+            if not self.master_weights:
+                raise NotImplementedError(
+                    f"{type(self).__name__}: bfloat16 parameters need master_weights=True "
+                    "(float32 master copy and moments)")
+            if g.dtype != torch.bfloat16:
+                raise RuntimeError(f"{type(self).__name__}: bfloat16 parameter with {g.dtype} "
+                                   "gradient (expected bfloat16)")
+            flags |= _lib.PARAM_BF16 | _lib.GRAD_BF16
+        else:
+            raise NotImplementedError(f"{type(self).__name__}: parameter dtype {p.dtype}")
+        return flags
+
+    def _desc_rows(self, ls: _LaunchSet) -> np.ndarray:
+        n = len(ls.params)
+        d = np.zeros(n, dtype=_lib.DESC_DTYPE)
+        for j, (p, g, st) in enumerate(zip(ls.params, ls.grads, ls.states)):
+            master = st.get("master")
+            param_ptr = master.data_ptr() if master is not None else p.data_ptr()
+            lp_ptr = p.data_ptr() if master is not None else 0
+            tau_ptr = st["tau"].data_ptr() if self._STAR else 0
+            gp = g.data_ptr()
+            m_ptr, v_ptr = st["m"].data_ptr(), st["v"].data_ptr()
+            ok = (param_ptr % 16 == 0 and m_ptr % 16 == 0 and v_ptr % 16 == 0
+                  and tau_ptr % 16 == 0 and gp % (8 if g.dtype == torch.bfloat16 else 16) == 0
+                  and lp_ptr % 8 == 0)
+            d[j] = (param_ptr, gp, m_ptr, v_ptr, tau_ptr, lp_ptr, p.numel(), ls.sclass[j],
+                    _lib.DESC_VEC_OK if ok else 0)
+        return d
+
+    def _upload(self, ls: _LaunchSet) -> None:
+        table = np.concatenate([ls.host_desc.view(np.uint8), ls.vstart.view(np.uint8)])
+        host = torch.from_numpy(table).pin_memory()
+        if ls.dev_table is None or ls.dev_table.numel() != host.numel():
+            ls.dev_table = torch.empty(host.numel(), dtype=torch.uint8, device=ls.device)
+        ls.dev_table.copy_(host, non_blocking=True)
+
+    def _build(self, params, grads, states, sclass, flags_list) -> List[_LaunchSet]:
+        sets = {}
+        for i, (p, g, st, c, fl) in enumerate(zip(params, grads, states, sclass, flags_list)):
+            key = (p.device, fl, c // _lib.MAX_CLASSES)
+            ls = sets.get(key)
+            if ls is None:
+                ls = sets[key] = _LaunchSet(p.device, fl, (c // _lib.MAX_CLASSES) * _lib.MAX_CLASSES)
+            ls.index.append(i)
+            ls.params.append(p)
+            ls.grads.append(g)
+            ls.states.append(st)
+            ls.sclass.append(c - ls.class_base)
+        out = list(sets.values())
+        for ls in out:
+            numels = np.fromiter((p.numel() for p in ls.params), dtype=np.int64, count=len(ls.params))
+            ls.vstart, ls.n_chunks = _lib.plan_layout(numels)
+            ls.host_desc = self._desc_rows(ls)
+            ls.ptr_key = ls.host_desc["grad"].copy()
+            with torch.cuda.device(ls.device):
+                self._upload(ls)
+                n = len(ls.params)
+                ls.chunk_first = torch.empty(max(ls.n_chunks, 1), dtype=torch.int32, device=ls.device)
+                stream = torch.cuda.current_stream(ls.device).cuda_stream
+                _lib.check(_lib.lib().adana_plan_index(
+                    ctypes.c_void_p(ls.dev_table.data_ptr() + 64 * n), n, ls.n_chunks,
+                    ctypes.c_void_p(ls.chunk_first.data_ptr()), ctypes.c_void_p(stream)),
+                    "adana_plan_index")
+                ls.partials = torch.empty(_lib.partials_floats(len(ls.params), ls.n_chunks),
+                                          dtype=torch.float32, device=ls.device)
+                ls.diag = torch.full((len(ls.params), 5), float("nan"), dtype=torch.float32,
+                                     device=ls.device)
+            for j, st in enumerate(ls.states):
+                row = ls.diag[j]
+                for k, key in enumerate(DIAG_KEYS):
+                    st[key] = row[k]
+        return out
+
+    # -- step -------------------------------------------------------------
+    def _hparams(self, group) -> "_lib.HParams":
+        hp = _lib.HParams()
+        hp.peak_lr = self.lr
+        hp.delta = group["delta"]
+        hp.kappa = self.kappa
+        hp.epsilon = group["epsilon"]
+        hp.weight_decay = group["weight_decay"]
+        hp.has_clip = 0 if self.clipsnr is None else 1
+        hp.clipsnr = 0.0 if self.clipsnr is None else float(self.clipsnr)
+        hp.wd_ts = self.wd_ts
+        hp.gamma_3_factor = self.gamma_3_factor
+        hp.wd_decaying = 1 if self.wd_decaying else 0
+        return hp
+
+    @torch.no_grad()
+    def step(self, closure=None):
+        loss = None
+        if closure is not None:
+            with torch.enable_grad():
+                loss = closure()
+
+        params, grads, states, keys = [], [], [], []
+        for gi, group in enumerate(self.param_groups):
+            # src/optim/adana.py:163-167: g2 = g3 = lr, sf = lr / self.lr
+            group["weighted_step_count"] += group["lr"] / self.lr
+            for p in group["params"]:
+                g = p.grad
+                if g is None:                          # adana.py:186
+                    continue
+                st = self.state[p]
+                if len(st) == 0:                       # adana.py:191-195
+                    self._init_state(p, st)
+                st["step"] += 1                        # adana.py:197
+                params.append(p)
+                grads.append(g)
+                states.append(st)
+                keys.append((gi, st["step"]))
+        if not params:
+            return loss
+
+        # (group, step) scalar classes
+        cls_index = {}
+        sclass = []
+        for k in keys:
+            c = cls_index.get(k)
+            if c is None:
+                c = cls_index[k] = len(cls_index)
+            sclass.append(c)
+        classes = list(cls_index)
+        scalars = []
+        hps = {}
+        for gi, t in classes:
+            hp = hps.get(gi)
+            if hp is None:
+                hp = hps[gi] = self._hparams(self.param_groups[gi])
+            scalars.append(_lib.step_scalars(hp, self.param_groups[gi]["lr"], t))
+
+        structure = (tuple(map(id, params)), tuple(sclass))
+        if self._sets is None or structure != self._structure:
+            flags = [self._validate(p, g) for p, g in zip(params, grads)]
+            self._sets = self._build(params, grads, states, sclass, flags)
+            self._structure = structure
+        else:
+            # same tensors and classes: refresh gradient pointers if they moved
+            for ls in self._sets:
+                ls.grads = grads if len(self._sets) == 1 else [grads[i] for i in ls.index]
+                gptr = np.fromiter((g.data_ptr() for g in ls.grads), dtype=np.uint64,
+                                   count=len(ls.grads))
+                if not np.array_equal(gptr, ls.ptr_key):
+                    for p, g in zip(ls.params, ls.grads):
+                        if self._validate(p, g) != ls.flags:
+                            raise RuntimeError(f"{type(self).__name__}: gradient dtype changed")
+                    ls.host_desc = self._desc_rows(ls)
+                    ls.ptr_key = ls.host_desc["grad"].copy()
+                    with torch.cuda.device(ls.device):
+                        self._upload(ls)
+
+        L = _lib.lib()
+        for ls in self._sets:
+            n_cls = min(_lib.MAX_CLASSES, len(classes) - ls.class_base)
+            sc_arr = (_lib.StepScalars * n_cls)(*scalars[ls.class_base:ls.class_base + n_cls])
+            base = ls.dev_table.data_ptr()
+            n = len(ls.params)
+            with torch.cuda.device(ls.device):
+                stream = torch.cuda.current_stream(ls.device).cuda_stream
+                _lib.check(L.adana_mta_step(
+                    ctypes.c_void_p(base), ctypes.c_void_p(base + 64 * n),
+                    ctypes.c_void_p(ls.chunk_first.data_ptr()), n, ls.n_chunks,
+                    ctypes.cast(sc_arr, ctypes.c_void_p), n_cls, ls.flags,
+                    ctypes.c_void_p(ls.partials.data_ptr()), ctypes.c_void_p(ls.diag.data_ptr()),
+                    ctypes.c_void_p(stream)), "adana_mta_step")
+        torch._C._increment_version(params)
+        return loss
+
+
+class ADana(_DanaFamily):
+    """ADana (``clipsnr=None``) and Dana-MK4 (``clipsnr=float``).
+
+    Same constructor, defaults, group keys and state keys as
+    src/optim/adana.py:32-70; ``use_foreach`` is accepted and has no effect
+    (there is one code path).  ``master_weights`` is an extension for
+    bfloat16 parameters (keyword-only).
+    """
+
+    _STAR = False
+
+    def __init__(self, params: Iterable[torch.Tensor], lr: float = 1.0, delta: float = 8.0,
+                 kappa: float = 1.0, epsilon: float = 1e-8, weight_decay: float = 0.0,
+                 clipsnr: float = None, wd_decaying: bool = False, wd_ts: float = 1.0,
+                 gamma_3_factor: float = 1.0, use_foreach: bool = False, *,
+                 master_weights: bool = False):
+        defaults = dict(lr=lr, delta=delta, epsilon=epsilon, weight_decay=weight_decay,
+                        weighted_step_count=0)
+        self.lr = lr
+        self.delta = delta
+        self.kappa = kappa
+        self.epsilon = epsilon
+        self.weight_decay = weight_decay
+        self.clipsnr = clipsnr
+        self.wd_decaying = wd_decaying
+        self.wd_ts = wd_ts
+        self.gamma_3_factor = gamma_3_factor
+        self.use_foreach = use_foreach
+        super().__init__(params, defaults)
+        self._engine_init(master_weights)
+
+
+class DANA_STAR_MK4(_DanaFamily):
+    """Dana-Star (``clipsnr=None``) and Dana-Star-MK4 (``clipsnr=float``).
+
+    Same constructor (including the mk4A / mk4B / weight_time assertions),
+    defaults, group keys and state keys as src/optim/dana_star_mk4.py:10-86.
+    """
+
+    _STAR = True
+
+    def __init__(self, params: Iterable[torch.Tensor], lr: float = 1.0, delta: float = 8.0,
+                 kappa: float = 1.0, mk4A: float = 0.0, mk4B: float = 0.0,
+                 epsilon: float = 1e-8, weight_decay: float = 0.0, clipsnr: float = 1.0,
+                 weight_time: bool = False, wd_decaying: bool = False, wd_ts: float = 1.0,
+                 gamma_3_factor: float = 1.0, use_foreach: bool = False, *,
+                 master_weights: bool = False):
+        assert mk4A == 0.0, f"mk4A must be 0.0, got {mk4A}"
+        assert mk4B == 0.0, f"mk4B must be 0.0, got {mk4B}"
+        assert weight_time == False, f"weight_time must be False, got {weight_time}"  # noqa: E712
+        defaults = dict(lr=lr, delta=delta, epsilon=epsilon, weight_decay=weight_decay,
+                        weighted_step_count=0)
+        self.lr = lr
+        self.delta = delta
+        self.kappa = kappa
+        self.mk4A = 0.0
+        self.mk4B = 0.0
+        self.clipsnr = clipsnr
+        self.epsilon = epsilon
+        self.weight_decay = weight_decay
+        self.weight_time = False
+        self.wd_decaying = wd_decaying
+        self.wd_ts = wd_ts
+        self.gamma_3_factor = gamma_3_factor
+        self.use_foreach = use_foreach
+        super().__init__(params, defaults)
+        self._engine_init(master_weights)

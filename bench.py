@@ -1,0 +1,272 @@
+#!/usr/bin/env python3
+"""Benchmark of the ADana-family optimizer step on one MI355X.
+
+A "step" is one ``optimizer.step()`` over the workload's whole parameter list
+with parameters, gradients and state already resident in HBM.  The default
+workload is the north-star: Dana-Star-MK4, fp32 params and state, on the
+2,645,527,040-parameter list of BASELINE config 4's geometry (d_model 2560,
+32 layers, MLP 4x, vocab 50304, tied embedding).  Other workloads (c1..c5)
+are the remaining BASELINE configs.
+
+Prints ONE JSON line.  ``value`` is the whole-step throughput in algorithmic
+HBM GB/s (bytes the update must move per element x elements / wall-clock ms
+per step, host work included).  ``roofline.achieved`` uses the device time of
+the step's kernels, measured with HIP events recorded on the stream they are
+launched on.  ``cpu_baseline`` times the CPU oracle (a C restatement of the
+reference step, OpenMP over the host cores) on a bounded sample of the same
+workload.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+METRIC = "optimizer step ms + achieved HBM GB/s (% of peak) at 2.62B params, 1 GPU"
+HBM_PEAK_GBS = 8000.0
+
+# Launcher conventions (reference scripts/launch.sh:36-40,188-223,309-312):
+# kappa 0.85, delta 8, omega 4, clipsnr 2.0, weight_decay = omega / wd_ts,
+# wd_ts = iterations / 10, wd_decaying.
+def _hp(iterations, clipsnr=2.0, peak_lr=1e-3):
+    wd_ts = iterations / 10.0
+    return dict(lr=peak_lr, delta=8.0, kappa=0.85, epsilon=1e-8, weight_decay=4.0 / wd_ts,
+                clipsnr=clipsnr, wd_decaying=True, wd_ts=wd_ts)
+
+
+def gpt_shapes(vocab, d, layers, mlp=4, ln_bias=False):
+    """(decay, no_decay) parameter shapes of a tied-embedding GPT, grouped the
+    way src/models/base.py:503-561 groups them (Linear weights decay; the
+    embedding and LayerNorm vectors do not)."""
+    decay, nodecay = [], [(vocab, d)]
+    for _ in range(layers):
+        decay += [(3 * d, d), (d, d), (mlp * d, d), (d, mlp * d)]
+        nodecay += [(d,), (d,)] * (2 if ln_bias else 1)
+    nodecay += [(d,)] * (2 if ln_bias else 1)
+    return decay, nodecay
+
+
+def workload(name):
+    """Return a dict describing one BASELINE workload."""
+    if name == "c1":
+        return dict(name=name, optimizer="ADana", star=False, groups=[[(1024, 4096)]],
+                    group_wd=[1.0], hp=_hp(100, clipsnr=None), master=False, schedule=None,
+                    grad_note="dense N(0,1e-3)")
+    if name == "c2":
+        decay, nodecay = gpt_shapes(50304, 512, 8, ln_bias=True)
+        return dict(name=name, optimizer="Dana-MK4", star=False, groups=[decay, nodecay],
+                    group_wd=[1.0, 0.0], hp=_hp(200, peak_lr=3e-3), master=False,
+                    schedule="cos_inf", grad_note="N(0,1e-3); 1-D grads x0.1")
+    if name == "c3":
+        decay, nodecay = gpt_shapes(50304, 2048, 24)
+        return dict(name=name, optimizer="Dana-Star-MK4", star=True, groups=[decay, nodecay],
+                    group_wd=[1.0, 0.0], hp=_hp(500), master=False, schedule=None,
+                    grad_note="N(0,1e-3); embedding rows nonzero w.p. 0.1")
+    if name in ("c4", "north_star"):
+        decay, nodecay = gpt_shapes(50304, 2560, 32)
+        if name == "c4":
+            return dict(name=name, optimizer="ADana", star=False, groups=[decay, nodecay],
+                        group_wd=[1.0, 0.0], hp=_hp(100, clipsnr=None), master=True,
+                        schedule=None, grad_note="bf16 N(0,1e-3)")
+        return dict(name=name, optimizer="Dana-Star-MK4", star=True, groups=[decay, nodecay],
+                    group_wd=[1.0, 0.0], hp=_hp(100), master=False, schedule=None,
+                    grad_note="N(0,1e-3); embedding rows nonzero w.p. 0.1")
+    if name == "c5":
+        rng = np.random.default_rng(5)
+        sizes = np.floor(np.exp(rng.uniform(math.log(64), math.log(65536), 10000))).astype(int)
+        return dict(name=name, optimizer="Dana-Star-MK4", star=True,
+                    groups=[[(int(n),) for n in sizes]], group_wd=[1.0], hp=_hp(200),
+                    master=False, schedule=None, grad_note="N(0,1e-3); 5% of tensors all-zero")
+    raise SystemExit(f"unknown workload {name}")
+
+
+def bytes_per_elem(w):
+    if w["master"]:
+        return 28 + (8 if w["star"] else 0)   # master 4+4, g 2, m/v 16, p_bf16 2 (+tau 8)
+    return 36 if w["star"] else 28
+
+
+def cos_inf(k, n=200, warmup=4, final_div=0.1):
+    if k < warmup:
+        return (k + 1) / warmup
+    return final_div + (1 - final_div) * 0.5 * (1 + math.cos(math.pi * min(k - warmup, n - warmup) / (n - warmup)))
+
+
+def build_gpu(w, seed=0):
+    import torch
+    import adana_amd
+
+    dev = torch.device("cuda:0")
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(seed)
+    pdtype = torch.bfloat16 if w["master"] else torch.float32
+    groups, params = [], []
+    zero_rng = np.random.default_rng(seed + 1)
+    for gi, shapes in enumerate(w["groups"]):
+        ps = []
+        for ti, s in enumerate(shapes):
+            p = torch.empty(s, dtype=torch.float32, device=dev).normal_(0.0, 0.02, generator=gen)
+            g = torch.empty(s, dtype=torch.float32, device=dev).normal_(0.0, 1e-3, generator=gen)
+            if w["name"] == "c2" and len(s) == 1:
+                g.mul_(0.1)
+            if w["name"] in ("c3", "north_star") and gi == 1 and ti == 0:
+                rows = torch.rand(s[0], device=dev, generator=gen) < 0.1     # row-sparse embedding grad
+                g.mul_(rows[:, None].to(g.dtype))
+            if w["name"] == "c5" and zero_rng.random() < 0.05:
+                g.zero_()
+            p = torch.nn.Parameter(p.to(pdtype))
+            p.grad = g.to(pdtype)
+            ps.append(p)
+        params += ps
+        groups.append(dict(params=ps, weight_decay=w["hp"]["weight_decay"] * w["group_wd"][gi]))
+    cls = adana_amd.DANA_STAR_MK4 if w["star"] else adana_amd.ADana
+    opt = cls(groups, master_weights=w["master"], **w["hp"])
+    return opt, params
+
+
+def cpu_baseline(w, target_s=10.0, max_elems=1 << 26):
+    """Time the CPU oracle on the first tensors of the workload (up to
+    max_elems elements), one step per repetition, for about target_s seconds."""
+    from oracle import oracle as O
+
+    cores = len(os.sched_getaffinity(0))
+    cores = min(cores, int(os.environ.get("OMP_NUM_THREADS", cores)), 16)
+    threads = O.set_threads(cores)
+    rng = np.random.default_rng(3)
+    shapes = [s for shapes in w["groups"] for s in shapes]
+    arrays, total = [], 0
+    for s in shapes:
+        n = int(np.prod(s))
+        if total + n > max_elems:
+            n = max_elems - total
+        if n <= 0:
+            break
+        arrays.append(n)
+        total += n
+    ps = [rng.normal(0, 0.02, n).astype(np.float32) for n in arrays]
+    gs = [rng.normal(0, 1e-3, n).astype(np.float32) for n in arrays]
+    if w["master"]:
+        ps = [O.f32_to_bf16(x) for x in ps]
+        gs = [O.f32_to_bf16(x) for x in gs]
+    hp = w["hp"]
+    opt = O.OracleOptimizer(groups=[O.OracleGroup(params=ps, lr=hp["lr"], delta=hp["delta"],
+                                                  epsilon=hp["epsilon"],
+                                                  weight_decay=hp["weight_decay"])],
+                            star=w["star"], peak_lr=hp["lr"], kappa=hp["kappa"],
+                            clipsnr=hp["clipsnr"], wd_decaying=hp["wd_decaying"],
+                            wd_ts=hp["wd_ts"], master=w["master"])
+    opt.step([gs])                       # warm-up: first touch of the state
+    reps, t0 = 0, time.perf_counter()
+    while True:
+        opt.step([gs])
+        reps += 1
+        el = time.perf_counter() - t0
+        if el >= target_s or reps >= 50:
+            break
+    per_step = el / reps
+    gbs = total * bytes_per_elem(w) / per_step / 1e9
+    return {"value": round(gbs, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+            "sample": f"{total} elements (first {len(arrays)} tensors of the list), "
+                      f"{reps} timed steps after 1 warm-up, {per_step * 1e3:.1f} ms/step, "
+                      f"oracle/adana_oracle.c with {threads} OpenMP threads",
+            "ms_per_step_sample": round(per_step * 1e3, 3)}
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--workload", default="north_star",
+                    choices=["north_star", "c1", "c2", "c3", "c4", "c5"])
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: this build's step is single-GPU "
+              f"(--gpus {args.gpus} requested); see DESIGN.md for how it shards", file=sys.stderr)
+        return 2
+
+    import torch
+
+    w = workload(args.workload)
+    print(f"[bench] workload {w['name']} ({w['optimizer']}): building on cuda:0", file=sys.stderr,
+          flush=True)
+    opt, params = build_gpu(w)
+    n_elems = sum(p.numel() for p in params)
+    bpe = bytes_per_elem(w)
+    algo_bytes = n_elems * bpe
+    peak = w["hp"]["lr"]
+
+    def one_step(k):
+        if w["schedule"] == "cos_inf":
+            for g in opt.param_groups:
+                g["lr"] = peak * cos_inf(k)
+        opt.step()
+
+    torch.cuda.synchronize()
+    for k in range(args.warmup):
+        one_step(k)
+    torch.cuda.synchronize()
+    print(f"[bench] warm-up done ({args.warmup} steps); timing {args.steps}", file=sys.stderr,
+          flush=True)
+    stream = torch.cuda.current_stream()
+    events = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps + 1)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for k in range(args.steps):
+        events[k].record(stream)
+        one_step(args.warmup + k)
+    events[-1].record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    dev_ms = [events[k].elapsed_time(events[k + 1]) for k in range(args.steps)]
+    ms_per_step = wall * 1e3 / args.steps
+    kern_ms = float(np.mean(dev_ms))
+    achieved = algo_bytes / (kern_ms * 1e-3) / 1e9
+    value = algo_bytes / (ms_per_step * 1e-3) / 1e9
+
+    traffic = None
+    tpath = os.path.join(ROOT, "profiles", f"traffic_{w['name']}.json")
+    if os.path.exists(tpath):
+        with open(tpath) as f:
+            traffic = json.load(f).get("hbm_bytes_per_launch")
+
+    result = {
+        "metric": METRIC, "value": round(value, 2), "unit": "GB/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "bf16+f32" if w["master"] else "f32", "data": "synthetic",
+        "config": {"workload": w["name"], "optimizer": w["optimizer"], "params": n_elems,
+                   "tensors": len(params), "bytes_per_elem": bpe,
+                   "algorithmic_bytes_per_step": algo_bytes, "grads": w["grad_note"],
+                   "hyperparams": w["hp"], "master_weights": w["master"],
+                   "parallelism": "single GPU"},
+        "kernel_ms_per_step": round(kern_ms, 4),
+        "kernel_ms_p90": round(float(np.percentile(dev_ms, 90)), 4),
+        "params_per_s": round(n_elems / (ms_per_step * 1e-3), 1),
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": traffic,
+                     "kernel": "mta_step_kernel + finalize_kernel (events bracket one step)"},
+    }
+    del opt, params
+    torch.cuda.empty_cache()
+    if not args.no_cpu_baseline:
+        print("[bench] timing the CPU oracle baseline", file=sys.stderr, flush=True)
+        result["cpu_baseline"] = cpu_baseline(w, target_s=args.cpu_seconds)
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,174 @@
+/*
+ * adana_mta.h -- C ABI of the MI355X (gfx950) ADana-family optimizer step.
+ *
+ * One multi-tensor kernel updates every (param, grad, m, v[, tau]) of a
+ * parameter list in a single pass over HBM and produces the per-tensor
+ * diagnostics the reference stores in the optimizer state.
+ *
+ * What each entry point replaces in the reference (mlexpos/adana):
+ *
+ *   adana_step_scalars_init  <- the host scalar code of ADana.step
+ *        (src/optim/adana.py:163-208: g2, g3, schedule_factor, alpha, the six
+ *        0-d device tensors) and the 0-d tensor arithmetic inside the compiled
+ *        update (:104 ``1 - alpha``, :114 ``1.0 + step``, :119 pow, :126
+ *        ``(-g3) * gamma_3_factor``, :139-143 weight-decay factor) and
+ *        DANA_STAR_MK4.step (src/optim/dana_star_mk4.py:217-272, :154 min_p).
+ *   adana_plan_layout        <- the per-tensor Python loop itself
+ *        (src/optim/adana.py:184-216; src/optim/dana_star_mk4.py:243-282):
+ *        instead of one compiled call per tensor, tensors are laid end to end
+ *        in a virtual index space cut into fixed-size work chunks.
+ *   adana_plan_index         <- (same loop) the chunk -> first-tensor index the
+ *        kernel uses to find its tensors without a search.
+ *   adana_mta_step           <- ADana._update_param_compiled
+ *        (src/optim/adana.py:81-153) and DANA_STAR_MK4._update_param_compiled
+ *        (src/optim/dana_star_mk4.py:105-205) for ALL tensors of the list,
+ *        plus the diagnostics stored at src/optim/adana.py:221-225 /
+ *        src/optim/dana_star_mk4.py:290-294.
+ *   adana_last_error, adana_abi_version, adana_partials_floats: plumbing
+ *        (no reference counterpart).
+ *
+ * Ownership: the library allocates nothing; every device buffer is owned by
+ * the caller (PyTorch's caching allocator in the Python binding) and only
+ * borrowed for the call.  Launches are asynchronous on the caller's HIP
+ * stream; nothing synchronises the host.  Errors: functions return 0 on
+ * success or a negative code; adana_last_error() returns the message of the
+ * calling thread's last failure.
+ */
+#ifndef ADANA_MTA_H
+#define ADANA_MTA_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define ADANA_ABI_VERSION 1
+
+/* Elements per work chunk (one 256-thread workgroup, one 16-byte vector per
+ * thread per array).  Tensors start at multiples of ADANA_ALIGN_ELEMS in the
+ * virtual index space, so every vector belongs to exactly one tensor. */
+#define ADANA_CHUNK_ELEMS 1024
+#define ADANA_ALIGN_ELEMS 4
+/* Scalar classes (distinct (group, step) pairs) one launch can carry. */
+#define ADANA_MAX_CLASSES 8
+
+/* variant_flags of adana_mta_step */
+#define ADANA_VARIANT_STAR 0x1u  /* Dana-Star(-MK4): tau state and estimator   */
+#define ADANA_GRAD_BF16    0x2u  /* gradients are bfloat16 (else float32)      */
+#define ADANA_PARAM_BF16   0x4u  /* param = fp32 master; param_lp = bf16 copy  */
+
+/* adana_tensor_desc.flags */
+#define ADANA_DESC_VEC_OK  0x1u  /* all pointers aligned for 16-byte access   */
+
+/* Error codes */
+#define ADANA_OK              0
+#define ADANA_E_INVALID     (-1)
+#define ADANA_E_HIP         (-2)
+#define ADANA_E_UNSUPPORTED (-3)
+
+/* One tensor of the list.  64 bytes; the array lives in device memory. */
+typedef struct adana_tensor_desc {
+    void       *param;     /* float32 param, or the float32 master copy      */
+    const void *grad;      /* float32 or bfloat16 gradient (same numel)      */
+    float      *m;         /* first moment, float32                          */
+    float      *v;         /* second moment, float32                         */
+    float      *tau;       /* Dana-Star tau, float32 (NULL otherwise)        */
+    void       *param_lp;  /* bfloat16 param written as RNE(master), or NULL */
+    int64_t     numel;
+    int32_t     sclass;    /* index into the launch's scalar classes         */
+    uint32_t    flags;     /* ADANA_DESC_* bits                              */
+} adana_tensor_desc;
+
+/* Hyper-parameters of one parameter group (reference ctor arguments and
+ * group keys, src/optim/adana.py:32-57). */
+typedef struct adana_hparams {
+    double  peak_lr;        /* the constructor's lr (self.lr)                */
+    double  delta;          /* group['delta']                                */
+    double  kappa;          /* self.kappa                                    */
+    double  epsilon;        /* group['epsilon']                              */
+    double  weight_decay;   /* group['weight_decay']                         */
+    double  clipsnr;        /* self.clipsnr (ignored unless has_clip)        */
+    double  wd_ts;          /* self.wd_ts                                    */
+    double  gamma_3_factor; /* self.gamma_3_factor                           */
+    int32_t has_clip;       /* self.clipsnr is not None                      */
+    int32_t wd_decaying;    /* self.wd_decaying                              */
+} adana_hparams;
+
+/* Per-step binary32 scalars of one (group, step) class, each computed on the
+ * host exactly as the reference's 0-d tensor ops round it.  64 bytes. */
+typedef struct adana_step_scalars {
+    float   a;          /* alpha = fp32(delta / (delta + t))                 */
+    float   oma;        /* 1 - alpha                                         */
+    float   lerp_coef;  /* alpha if |alpha| < 0.5 else alpha - 1 (ATen lerp) */
+    float   s;          /* fp32(t)                                           */
+    float   eps;        /* fp32(epsilon)                                     */
+    float   pw;         /* ADana: (1 + s) ** (1 - kappa)                     */
+    float   min_p;      /* Dana-Star: 1 / (1 + s)                            */
+    float   clip;       /* fp32(clipsnr)                                     */
+    float   c3;         /* (-lr) * gamma_3_factor                            */
+    float   cg2;        /* -lr                                               */
+    float   opw;        /* 1 + weight-decay factor                           */
+    float   star_exp;   /* fp32(1 - kappa), exponent of Dana-Star's pow      */
+    int32_t pow_mode;   /* ATen pow specialisation (ADANA_POW_*)             */
+    int32_t has_clip;
+    int32_t lerp_small; /* |alpha| < 0.5                                     */
+    int32_t reserved;
+} adana_step_scalars;
+
+/* pow(Tensor, Scalar) specialisations ATen selects on the binary64 exponent */
+enum {
+    ADANA_POW_GENERAL = 0, ADANA_POW_ONE, ADANA_POW_SQRT, ADANA_POW_RSQRT,
+    ADANA_POW_RECIP, ADANA_POW_SQUARE, ADANA_POW_CUBE, ADANA_POW_INVSQ
+};
+
+int adana_abi_version(void);
+
+/* Copies the calling thread's last error message (NUL-terminated). */
+size_t adana_last_error(char *buf, size_t len);
+
+/* Host only.  Scalars of one tensor update at learning rate ``lr``
+ * (group['lr']) and per-tensor step ``step`` (state['step'] after += 1). */
+int adana_step_scalars_init(adana_step_scalars *out, const adana_hparams *hp,
+                            double lr, int64_t step);
+
+/* Host only.  Writes vstart[0..n] (virtual start of each tensor; vstart[n] is
+ * the padded total) and returns the number of work chunks (>= 0), or a
+ * negative error code. */
+int64_t adana_plan_layout(const int64_t *numel, int32_t n, int64_t *vstart);
+
+/* Device.  Fills d_chunk_first[c] (c < n_chunks) with the index of the first
+ * tensor whose virtual range reaches chunk c, from the device copy of vstart.
+ * Asynchronous on ``stream``; run once per layout. */
+int adana_plan_index(const int64_t *d_vstart, int32_t n_tensors, int64_t n_chunks,
+                     int32_t *d_chunk_first, void *stream);
+
+/* Floats of the d_partials workspace a launch over n tensors / n_chunks
+ * chunks needs. */
+int64_t adana_partials_floats(int32_t n_tensors, int64_t n_chunks);
+
+/* Device step over one tensor list.
+ *   d_desc      device array of n_tensors descriptors
+ *   d_vstart    device copy of adana_plan_layout's vstart (n_tensors + 1)
+ *   d_chunk_first  adana_plan_index's output (n_chunks entries)
+ *   n_chunks    adana_plan_layout's return value
+ *   h_scalars   host array of n_classes scalar classes (passed by value to
+ *               the kernel; no host-to-device copy)
+ *   d_partials  device workspace, adana_partials_floats(...) floats
+ *   d_diag      device float[5 * n_tensors]: per tensor current_alpha,
+ *               gradient_norm, auto_factor_mean, current_kappa_factor,
+ *               m_norm (src/optim/adana.py:221-225)
+ *   stream      hipStream_t (NULL = default stream)
+ * All tensors of one call share variant_flags. */
+int adana_mta_step(const adana_tensor_desc *d_desc, const int64_t *d_vstart,
+                   const int32_t *d_chunk_first, int32_t n_tensors, int64_t n_chunks,
+                   const adana_step_scalars *h_scalars, int32_t n_classes,
+                   uint32_t variant_flags, float *d_partials, float *d_diag,
+                   void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* ADANA_MTA_H */

@@ -213,3 +213,8 @@ void adana_oracle_f32_to_bf16(int64_t n, const float *x, uint16_t *y) {
 }
 
 int adana_oracle_abi_version(void) { return 1; }
+
+/* Thread count of the parallel loops (the CPU baseline reports it). */
+#include <omp.h>
+void adana_oracle_set_threads(int n) { if (n > 0) omp_set_num_threads(n); }
+int adana_oracle_get_threads(void) { return omp_get_max_threads(); }

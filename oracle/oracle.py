@@ -71,6 +71,10 @@ def lib():
         L.adana_oracle_master_step.argtypes = [i64, i32, P, P, P, P, P, P, SP, P]
         L.adana_oracle_step_g16.argtypes = [i64, i32, P, P, P, P, P, SP, P]
         L.adana_oracle_f32_to_bf16.argtypes = [i64, P, P]
+        L.adana_oracle_set_threads.argtypes = [ctypes.c_int]
+        L.adana_oracle_set_threads.restype = None
+        L.adana_oracle_get_threads.argtypes = []
+        L.adana_oracle_get_threads.restype = ctypes.c_int
         for fn in (L.adana_oracle_adana_step, L.adana_oracle_star_step,
                    L.adana_oracle_master_step, L.adana_oracle_step_g16,
                    L.adana_oracle_f32_to_bf16):
@@ -79,11 +83,18 @@ def lib():
     return _lib
 
 
-def build() -> None:
+def build(force: bool = False) -> None:
     """Compile adana_oracle.c with the oracle's Makefile."""
     import subprocess
 
-    subprocess.run(["make", "-s", "-C", _HERE], check=True)
+    subprocess.run(["make", "-s"] + (["-B"] if force else []) + ["-C", _HERE], check=True)
+
+
+def set_threads(n: int) -> int:
+    """Set the OpenMP thread count of the element loops; return the count in use."""
+    L = lib()
+    L.adana_oracle_set_threads(int(n))
+    return int(L.adana_oracle_get_threads())
 
 
 # --------------------------------------------------------------------------

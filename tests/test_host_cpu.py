@@ -1,0 +1,217 @@
+"""CPU tests of the product's host side: the C ABI library loads and exports
+every symbol include/adana_mta.h declares, its host scalar code agrees bit for
+bit with the oracle's independent restatement, the layout is sound, and the
+Python classes keep the reference's interface.  No GPU compute is called."""
+import ctypes
+import inspect
+import math
+import os
+import re
+
+import numpy as np
+import pytest
+import torch
+
+from helpers import ROOT
+
+
+def _header_functions():
+    text = open(os.path.join(ROOT, "include", "adana_mta.h")).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(adana_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol():
+    from adana_amd import _lib
+
+    L = _lib.lib()
+    declared = _header_functions()
+    assert declared, "no functions parsed from the header"
+    for name in declared:
+        assert hasattr(L, name), f"{name} declared in include/adana_mta.h but not exported"
+    assert sorted(_lib.EXPORTS) == declared
+    assert L.adana_abi_version() == _lib.ABI_VERSION
+
+
+def test_single_hip_runtime_mapped():
+    from adana_amd import _lib
+
+    _lib.lib()
+    assert len(_lib._hip_runtimes_mapped()) <= 1
+
+
+def _hp(_lib, **kw):
+    hp = _lib.HParams()
+    hp.peak_lr = kw["peak_lr"]
+    hp.delta = kw["delta"]
+    hp.kappa = kw["kappa"]
+    hp.epsilon = kw["epsilon"]
+    hp.weight_decay = kw["weight_decay"]
+    hp.has_clip = 0 if kw["clipsnr"] is None else 1
+    hp.clipsnr = 0.0 if kw["clipsnr"] is None else kw["clipsnr"]
+    hp.wd_ts = kw["wd_ts"]
+    hp.gamma_3_factor = kw["gamma_3_factor"]
+    hp.wd_decaying = int(kw["wd_decaying"])
+    return hp
+
+
+def _f32bits(x):
+    return np.float32(x).view(np.int32)
+
+
+@pytest.mark.parametrize("kappa", [0.85, 1.0, 0.5, 0.75, 1.5, -1.0, 0.0])
+def test_host_scalars_match_oracle_bitwise(oracle_mod, kappa):
+    from adana_amd import _lib
+
+    rng = np.random.default_rng(int(abs(kappa) * 100) + 7)
+    for trial in range(60):
+        kw = dict(peak_lr=float(10 ** rng.uniform(-4, -1)), delta=float(rng.choice([8.0, 6.0, 16.0, 3.5])),
+                  kappa=kappa, epsilon=float(rng.choice([1e-8, 1e-6, 1e-10])),
+                  weight_decay=float(rng.choice([0.0, 0.4, 0.1, 1.3])),
+                  clipsnr=[None, 1.0, 2.0, 0.37][trial % 4],
+                  wd_decaying=bool(trial % 2), wd_ts=float(rng.choice([1.0, 10.0, 20.0, 37.5])),
+                  gamma_3_factor=float(rng.choice([1.0, 0.5, 0.0, 1.7])))
+        lr = kw["peak_lr"] * float(rng.uniform(0.01, 1.0))
+        t = int(rng.choice([1, 2, 7, 8, 9, 100, 12345, 2 ** 20 + 3]))
+        sc = _lib.step_scalars(_hp(_lib, **kw), lr, t)
+        ref = oracle_mod.step_scalars(lr=lr, t=t, **kw)
+        for name in ("a", "oma", "s", "eps", "pw", "min_p", "c3", "cg2", "opw", "star_exp"):
+            assert _f32bits(getattr(sc, name)) == _f32bits(getattr(ref, name)), (name, kw, lr, t)
+        assert sc.pow_mode == ref.pow_mode
+        assert sc.has_clip == ref.has_clip
+        if ref.has_clip:
+            assert _f32bits(sc.clip) == _f32bits(ref.clip)
+        # lerp helper fields: ATen's |w| < 0.5 branch and its coefficient
+        assert sc.lerp_small == int(abs(float(ref.a)) < 0.5)
+        coef = ref.a if sc.lerp_small else np.float32(ref.a) - np.float32(1.0)
+        assert _f32bits(sc.lerp_coef) == _f32bits(coef)
+
+
+def test_host_scalars_reject_bad_input():
+    from adana_amd import _lib
+
+    hp = _lib.HParams(peak_lr=1e-3, delta=8.0, kappa=0.85, epsilon=1e-8)
+    with pytest.raises(_lib.AdanaLibraryError, match="step"):
+        _lib.step_scalars(hp, 1e-3, 0)
+    hp.peak_lr = 0.0
+    with pytest.raises(_lib.AdanaLibraryError, match="peak lr"):
+        _lib.step_scalars(hp, 1e-3, 1)
+
+
+def test_plan_layout_properties():
+    from adana_amd import _lib
+
+    rng = np.random.default_rng(0)
+    numels = np.concatenate([rng.integers(0, 70000, 300), [0, 1, 3, 4, 5, 16384, 16385]])
+    vstart, chunks = _lib.plan_layout(numels)
+    assert vstart[0] == 0
+    assert np.all(vstart % _lib.ALIGN_ELEMS == 0)
+    pad = vstart[1:] - vstart[:-1]
+    assert np.all(pad >= numels) and np.all(pad - numels < _lib.ALIGN_ELEMS)
+    assert chunks == math.ceil(vstart[-1] / _lib.CHUNK_ELEMS)
+    # (chunk, tensor) segment slots chunk + tensor are distinct
+    slots = set()
+    for i, (vs, n) in enumerate(zip(vstart[:-1], numels)):
+        if n == 0:
+            continue
+        for b in range(vs // _lib.CHUNK_ELEMS, (vs + n - 1) // _lib.CHUNK_ELEMS + 1):
+            assert b + i not in slots
+            slots.add(b + i)
+    assert max(slots) < _lib.partials_floats(len(numels), chunks) // 4
+    assert _lib.plan_layout(np.zeros(0, np.int64))[1] == 0
+    # the chunk -> first tensor rule the device index kernel applies
+    first = np.searchsorted(vstart[:-1], np.arange(chunks) * _lib.CHUNK_ELEMS, side="right") - 1
+    for c in range(chunks):
+        i = first[c]
+        lo = c * _lib.CHUNK_ELEMS
+        assert vstart[i] <= lo
+        # no earlier tensor has elements at or after lo
+        assert all(vstart[k] + numels[k] <= lo for k in range(i))
+
+
+def test_mta_step_rejects_bad_arguments():
+    from adana_amd import _lib
+
+    L = _lib.lib()
+    sc = (_lib.StepScalars * 1)()
+    rc = L.adana_mta_step(None, None, None, -1, 0, ctypes.cast(sc, ctypes.c_void_p), 1, 0, None,
+                          None, None)
+    assert rc == -1 and "bad sizes" in _lib.last_error()
+    rc = L.adana_mta_step(None, None, None, 3, 1, ctypes.cast(sc, ctypes.c_void_p), 1, 0, None,
+                          None, None)
+    assert rc == -1 and "null pointer" in _lib.last_error()
+    rc = L.adana_mta_step(None, None, None, 0, 0, None, 0, 0x80, None, None, None)
+    assert rc == -1 and "variant flags" in _lib.last_error()
+    assert L.adana_mta_step(None, None, None, 0, 0, None, 0, 0, None, None, None) == 0
+    assert L.adana_plan_index(None, 0, 0, None, None) == 0
+    assert L.adana_plan_index(None, 3, 5, None, None) == -1
+
+
+# --------------------------------------------------------------------------
+# Python interface parity with the reference classes
+# --------------------------------------------------------------------------
+
+REF_ADANA_SIG = ["params", "lr", "delta", "kappa", "epsilon", "weight_decay", "clipsnr",
+                 "wd_decaying", "wd_ts", "gamma_3_factor", "use_foreach"]     # adana.py:32-45
+REF_ADANA_DEFAULTS = dict(lr=1.0, delta=8.0, kappa=1.0, epsilon=1e-8, weight_decay=0.0,
+                          clipsnr=None, wd_decaying=False, wd_ts=1.0, gamma_3_factor=1.0,
+                          use_foreach=False)
+REF_STAR_SIG = ["params", "lr", "delta", "kappa", "mk4A", "mk4B", "epsilon", "weight_decay",
+                "clipsnr", "weight_time", "wd_decaying", "wd_ts", "gamma_3_factor",
+                "use_foreach"]                                                 # dana_star_mk4.py:10-26
+REF_STAR_DEFAULTS = dict(lr=1.0, delta=8.0, kappa=1.0, mk4A=0.0, mk4B=0.0, epsilon=1e-8,
+                         weight_decay=0.0, clipsnr=1.0, weight_time=False, wd_decaying=False,
+                         wd_ts=1.0, gamma_3_factor=1.0, use_foreach=False)
+
+
+@pytest.mark.parametrize("which", ["ADana", "DANA_STAR_MK4"])
+def test_constructor_matches_reference(which):
+    import adana_amd
+
+    cls = getattr(adana_amd, which)
+    sig = inspect.signature(cls.__init__)
+    positional = [n for n, p in sig.parameters.items()
+                  if n != "self" and p.kind == p.POSITIONAL_OR_KEYWORD]
+    ref_sig, ref_def = ((REF_ADANA_SIG, REF_ADANA_DEFAULTS) if which == "ADana"
+                        else (REF_STAR_SIG, REF_STAR_DEFAULTS))
+    assert positional == ref_sig
+    for k, v in ref_def.items():
+        assert sig.parameters[k].default == v, k
+    p = torch.nn.Parameter(torch.zeros(3))
+    opt = cls([p], lr=0.01, delta=6.0, epsilon=1e-7, weight_decay=0.2)
+    assert set(opt.param_groups[0]) == {"params", "lr", "delta", "epsilon", "weight_decay",
+                                        "weighted_step_count"}
+    assert opt.param_groups[0]["weighted_step_count"] == 0
+    for attr in ("lr", "delta", "kappa", "epsilon", "weight_decay", "clipsnr", "wd_decaying",
+                 "wd_ts", "gamma_3_factor", "use_foreach"):
+        assert hasattr(opt, attr)
+
+
+def test_star_asserts_like_reference():
+    import adana_amd
+
+    p = torch.nn.Parameter(torch.zeros(3))
+    for kw in (dict(mk4A=0.1), dict(mk4B=1.0), dict(weight_time=True)):
+        with pytest.raises(AssertionError):
+            adana_amd.DANA_STAR_MK4([p], **kw)
+
+
+def test_cpu_parameters_fail_loudly():
+    """No silent CPU fallback: a step on CPU tensors raises."""
+    import adana_amd
+
+    p = torch.nn.Parameter(torch.ones(8))
+    p.grad = torch.ones(8)
+    opt = adana_amd.ADana([p], lr=1e-3)
+    with pytest.raises(RuntimeError, match="ROCm GPU"):
+        opt.step()
+
+
+def test_grad_none_is_skipped_without_state():
+    import adana_amd
+
+    p = torch.nn.Parameter(torch.ones(8))
+    opt = adana_amd.DANA_STAR_MK4([p], lr=1e-3)
+    opt.step()
+    assert len(opt.state[p]) == 0
+    assert opt.param_groups[0]["weighted_step_count"] == 1.0
