@@ -20,6 +20,7 @@ ABI_VERSION = 1
 CHUNK_ELEMS = 1024
 ALIGN_ELEMS = 4
 MAX_CLASSES = 8
+FOLD_CHUNKS = 2048
 
 VARIANT_STAR = 0x1
 GRAD_BF16 = 0x2
@@ -62,10 +63,20 @@ class StepScalars(ctypes.Structure):
 
 assert ctypes.sizeof(StepScalars) == 64
 
+
+class Plan(ctypes.Structure):
+    """adana_plan: host struct of device pointers."""
+
+    _fields_ = [
+        ("desc", ctypes.c_void_p), ("vstart", ctypes.c_void_p), ("chunk_first", ctypes.c_void_p),
+        ("fold_first", ctypes.c_void_p), ("n_tensors", ctypes.c_int32),
+        ("reserved", ctypes.c_int32), ("n_chunks", ctypes.c_int64), ("n_folds", ctypes.c_int64),
+    ]
+
 # Every symbol include/adana_mta.h declares (checked by the CPU test suite).
 EXPORTS = (
     "adana_abi_version", "adana_last_error", "adana_step_scalars_init",
-    "adana_plan_layout", "adana_plan_index", "adana_partials_floats", "adana_mta_step",
+    "adana_plan_layout", "adana_plan_index", "adana_workspace_bytes", "adana_mta_step",
 )
 
 _lib = None
@@ -85,13 +96,13 @@ def _declare(L) -> None:
     L.adana_step_scalars_init.argtypes = [ctypes.POINTER(StepScalars), ctypes.POINTER(HParams),
                                           ctypes.c_double, i64]
     L.adana_step_scalars_init.restype = ctypes.c_int
-    L.adana_plan_layout.argtypes = [P, i32, P]
+    L.adana_plan_layout.argtypes = [P, i32, P, P, ctypes.POINTER(i64)]
     L.adana_plan_layout.restype = i64
     L.adana_plan_index.argtypes = [P, i32, i64, P, P]
     L.adana_plan_index.restype = ctypes.c_int
-    L.adana_partials_floats.argtypes = [i32, i64]
-    L.adana_partials_floats.restype = i64
-    L.adana_mta_step.argtypes = [P, P, P, i32, i64, P, i32, u32, P, P, P]
+    L.adana_workspace_bytes.argtypes = [ctypes.POINTER(Plan)]
+    L.adana_workspace_bytes.restype = ctypes.c_size_t
+    L.adana_mta_step.argtypes = [ctypes.POINTER(Plan), P, i32, u32, P, ctypes.c_size_t, P, P]
     L.adana_mta_step.restype = ctypes.c_int
 
 
@@ -147,16 +158,19 @@ def step_scalars(hp: HParams, lr: float, step: int) -> StepScalars:
 
 
 def plan_layout(numels: np.ndarray):
-    """Return (vstart[int64 n+1], n_chunks)."""
+    """Return (vstart[int64 n+1], fold_first[int32 n+1], n_chunks, n_folds)."""
     numels = np.ascontiguousarray(numels, dtype=np.int64)
     n = numels.size
     vstart = np.zeros(n + 1, dtype=np.int64)
+    fold_first = np.zeros(n + 1, dtype=np.int32)
+    n_folds = ctypes.c_int64(0)
     chunks = lib().adana_plan_layout(ctypes.c_void_p(numels.ctypes.data), n,
-                                     ctypes.c_void_p(vstart.ctypes.data))
+                                     ctypes.c_void_p(vstart.ctypes.data),
+                                     ctypes.c_void_p(fold_first.ctypes.data), ctypes.byref(n_folds))
     if chunks < 0:
         check(int(chunks), "adana_plan_layout")
-    return vstart, int(chunks)
+    return vstart, fold_first, int(chunks), int(n_folds.value)
 
 
-def partials_floats(n_tensors: int, n_chunks: int) -> int:
-    return int(lib().adana_partials_floats(n_tensors, n_chunks))
+def workspace_bytes(plan: Plan) -> int:
+    return int(lib().adana_workspace_bytes(ctypes.byref(plan)))

@@ -45,8 +45,8 @@ int set_err(int code, const char *fmt, ...) {
 constexpr int kBlock = 256;
 constexpr int kWaves = kBlock / 64;
 constexpr int kChunk = ADANA_CHUNK_ELEMS;
-static_assert(kChunk == 4 * kBlock, "one 4-element vector per thread per chunk");
-static_assert(ADANA_ALIGN_ELEMS == 4, "tensors start on vector boundaries");
+static_assert(kChunk == 4 * kBlock, "auxiliary kernels use 256-thread workgroups");
+static_assert(ADANA_ALIGN_ELEMS % 4 == 0, "tensors start on vector boundaries");
 static_assert(sizeof(adana_tensor_desc) == 64, "descriptor layout");
 static_assert(sizeof(adana_step_scalars) == 64, "scalar layout");
 
@@ -76,67 +76,146 @@ __device__ __forceinline__ unsigned short f32_to_bf16(float f) {
     return static_cast<unsigned short>(u >> 16);
 }
 
-// x ** e with ATen's exponent specialisations (pow(Tensor, Scalar)); the
-// general case is evaluated in binary64 and rounded once (adana_pow.h).
+// x ** e with ATen's exponent specialisations (pow(Tensor, Scalar)).  POWK
+// selects the code at compile time: POW_GENERAL (0 < e < 1, i.e. 0 < kappa
+// < 1) evaluates in binary64 and rounds once (adana_pow.h); POW_ONE (kappa
+// == 1) is exactly 1; POW_SPECIAL dispatches on the remaining ATen
+// specialisations, with any other exponent through the slow-path-guarded pow.
+enum PowKind { POW_GENERAL = 0, POW_ONE = 1, POW_SPECIAL = 2 };
+
+template <int POWK>
 __device__ __forceinline__ float pow_aten(float x, const adana_step_scalars &sc) {
-    if (sc.pow_mode == ADANA_POW_GENERAL) return adana::pow_f32_via_f64(x, sc.star_exp);
-    switch (sc.pow_mode) {
-    case ADANA_POW_ONE: return 1.0f;
-    case ADANA_POW_SQRT: return sqrtf(x);
-    case ADANA_POW_RSQRT: return 1.0f / sqrtf(x);
-    case ADANA_POW_RECIP: return 1.0f / x;
-    case ADANA_POW_SQUARE: return x * x;
-    case ADANA_POW_CUBE: return (x * x) * x;
-    case ADANA_POW_INVSQ: return 1.0f / (x * x);
-    default: return adana::pow_f32_via_f64(x, sc.star_exp);
+    if constexpr (POWK == POW_GENERAL) {
+        return adana::pow_f32_unit_exp(x, sc.star_exp);
+    } else if constexpr (POWK == POW_ONE) {
+        return 1.0f;
+    } else {
+        switch (sc.pow_mode) {
+        case ADANA_POW_ONE: return 1.0f;
+        case ADANA_POW_SQRT: return sqrtf(x);
+        case ADANA_POW_RSQRT: return 1.0f / sqrtf(x);
+        case ADANA_POW_RECIP: return 1.0f / x;
+        case ADANA_POW_SQUARE: return x * x;
+        case ADANA_POW_CUBE: return (x * x) * x;
+        case ADANA_POW_INVSQ: return 1.0f / (x * x);
+        default: return adana::pow_f32_via_f64(x, sc.star_exp);
+        }
     }
 }
 
-// One element.  ADana / Dana-MK4: src/optim/adana.py:101-143.
-// Dana-Star / Dana-Star-MK4: src/optim/dana_star_mk4.py:137-195.
-template <bool STAR>
-__device__ __forceinline__ float update_elem(float p, float g, float &m, float &v, float &tau,
-                                             const adana_step_scalars &sc, float (&acc)[4]) {
-    // m.lerp_(grad, alpha): ATen computes fma(w, end - self, self) for |w| < 0.5
-    // and fma(w - 1, end - self, end) otherwise.
-    const float mn_ = __builtin_fmaf(sc.lerp_coef, g - m, sc.lerp_small ? m : g);
-    // v.mul_(1 - alpha).addcmul_(grad, grad, value=alpha) = fma(alpha*g, g, v*(1-alpha))
-    const float vn = __builtin_fmaf(sc.a * g, g, v * sc.oma);
-    const float se = sqrtf(vn) + sc.eps;
-    float nt, mfac, af, inner;
-    if constexpr (!STAR) {
-        nt = 1.0f / se;                                   // adana.py:110
-        mfac = fabsf(mn_) * nt;                           // :111, :115
-        af = sc.pw * mfac;                                // :119 / :123
-        if (sc.has_clip) af = clamp_max(af, sc.clip);
-        inner = sign_f(mn_) * af + mn_ * nt;              // :126
-    } else {
-        const float ag = fabsf(g);                        // dana_star_mk4.py:147
-        const float tu = ag / (ag + se);                  // :148
-        const float tn = __builtin_fmaf(sc.lerp_coef, tu - tau, sc.lerp_small ? tau : tu);
-        const float ct = clamp_max(tn, 0.5f);             // :152
-        const float pe = ct / (1.0f - ct);                // :153
-        const float tr = sc.min_p + relu_f(pe - sc.min_p);  // :154-156
-        const float et = clamp_min(tn * sc.s, 1.0f);      // :159
-        nt = sqrtf(tr) / se;                              // :163-164
-        const float mnt = fabsf(mn_) * nt;                // :165
-        mfac = mnt / tr;                                  // :167
-        af = pow_aten(et, sc) * mfac;                     // :170 / :174
-        if (sc.has_clip) af = clamp_max(af, sc.clip);
-        inner = sign_f(mn_) * (tr * af + mnt);            // :177
-        tau = tn;
-    }
-    const float g3t = sc.c3 * inner;                      // (-g3) * gamma_3_factor * (...)
-    const float g2t = (sc.cg2 * g) * nt;                  // (-g2) * grad * norm_term
-    float pn = p + (g2t + g3t);                           // p.add_(update)
-    pn = pn * sc.opw;                                     // p.mul_(1 + wd_factor)
-    m = mn_;
-    v = vn;
+// m.lerp_(grad, alpha): ATen computes fma(w, end - self, self) for |w| < 0.5
+// and fma(w - 1, end - self, end) otherwise (w - 1 is precomputed, exact).
+__device__ __forceinline__ float lerp_aten(float self, float end, const adana_step_scalars &sc) {
+    return __builtin_fmaf(sc.lerp_coef, end - self, sc.lerp_small ? self : end);
+}
+
+__device__ __forceinline__ void accumulate(float (&acc)[4], float af, float g, float mfac, float m) {
     acc[0] += af;
     acc[1] += g * g;
     acc[2] += mfac;
-    acc[3] += mn_ * mn_;
+    acc[3] += m * m;
+}
+
+// ADana / Dana-MK4, one element: src/optim/adana.py:101-143.
+__device__ __forceinline__ float adana_elem(float p, float g, float &m, float &v,
+                                            const adana_step_scalars &sc, float (&acc)[4]) {
+    const float mn = lerp_aten(m, g, sc);                        // :101
+    const float vn = __builtin_fmaf(sc.a * g, g, v * sc.oma);    // :104 mul_, addcmul_
+    const float se = sqrtf(vn) + sc.eps;                         // :107
+    const float nt = 1.0f / se;                                  // :110
+    const float mfac = fabsf(mn) * nt;                           // :111, :115
+    float af = sc.pw * mfac;                                     // :119 / :123
+    if (sc.has_clip) af = clamp_max(af, sc.clip);
+    const float inner = sign_f(mn) * af + mn * nt;               // :126
+    const float g3t = sc.c3 * inner;
+    const float g2t = (sc.cg2 * g) * nt;                         // :129
+    float pn = p + (g2t + g3t);                                  // :132-135
+    pn = pn * sc.opw;                                            // :143
+    m = mn;
+    v = vn;
+    accumulate(acc, af, g, mfac, mn);
     return pn;
+}
+
+// Dana-Star / Dana-Star-MK4, split around the per-element pow so that the
+// kernel can evaluate four pows together and share their rare slow path.
+struct StarMid {
+    float m, v, se, tau, tr, et;
+};
+
+// src/optim/dana_star_mk4.py:137-159
+__device__ __forceinline__ StarMid star_phase_a(float g, float m, float v, float tau,
+                                                const adana_step_scalars &sc) {
+    StarMid o;
+    o.m = lerp_aten(m, g, sc);                                   // :137
+    o.v = __builtin_fmaf(sc.a * g, g, v * sc.oma);               // :140
+    o.se = sqrtf(o.v) + sc.eps;                                  // :143
+    const float ag = fabsf(g);                                   // :147
+    const float tu = ag / (ag + o.se);                           // :148
+    o.tau = lerp_aten(tau, tu, sc);                              // :149
+    const float ct = clamp_max(o.tau, 0.5f);                     // :152
+    const float pe = ct / (1.0f - ct);                           // :153
+    o.tr = sc.min_p + relu_f(pe - sc.min_p);                     // :154-156
+    o.et = clamp_min(o.tau * sc.s, 1.0f);                        // :159
+    return o;
+}
+
+// src/optim/dana_star_mk4.py:163-195, given pw = effective_time ** (1 - kappa)
+__device__ __forceinline__ float star_phase_b(float p, float g, const StarMid &a, float pw,
+                                              const adana_step_scalars &sc, float (&acc)[4]) {
+    const float nt = sqrtf(a.tr) / a.se;                         // :163-164
+    const float mnt = fabsf(a.m) * nt;                           // :165
+    const float mfac = mnt / a.tr;                               // :167
+    float af = pw * mfac;                                        // :170 / :174
+    if (sc.has_clip) af = clamp_max(af, sc.clip);
+    const float inner = sign_f(a.m) * (a.tr * af + mnt);         // :177
+    const float g3t = sc.c3 * inner;
+    const float g2t = (sc.cg2 * g) * nt;                         // :180
+    float pn = p + (g2t + g3t);                                  // :183-186
+    pn = pn * sc.opw;                                            // :195
+    accumulate(acc, af, g, mfac, a.m);
+    return pn;
+}
+
+// One element of either variant (the element-wise tail path).
+template <bool STAR, int POWK>
+__device__ __forceinline__ float update_elem(float p, float g, float &m, float &v, float &tau,
+                                             const adana_step_scalars &sc, float (&acc)[4]) {
+    if constexpr (!STAR) {
+        return adana_elem(p, g, m, v, sc, acc);
+    } else {
+        const StarMid a = star_phase_a(g, m, v, tau, sc);
+        const float pn = star_phase_b(p, g, a, pow_aten<POWK>(a.et, sc), sc, acc);
+        m = a.m;
+        v = a.v;
+        tau = a.tau;
+        return pn;
+    }
+}
+
+// N consecutive elements of one thread (the vector path).  Dana-Star runs
+// phase A for all N, then the N pows, then phase B.
+template <bool STAR, int POWK, int N>
+__device__ __forceinline__ void update_n(float (&P)[N], const float (&G)[N], float (&M)[N], float (&V)[N],
+                                         float (&T)[N], const adana_step_scalars &sc, float (&acc)[4]) {
+    if constexpr (!STAR) {
+#pragma unroll
+        for (int k = 0; k < N; ++k) P[k] = adana_elem(P[k], G[k], M[k], V[k], sc, acc);
+    } else {
+        StarMid a[N];
+#pragma unroll
+        for (int k = 0; k < N; ++k) a[k] = star_phase_a(G[k], M[k], V[k], T[k], sc);
+        float pw[N];
+#pragma unroll
+        for (int k = 0; k < N; ++k) pw[k] = pow_aten<POWK>(a[k].et, sc);
+#pragma unroll
+        for (int k = 0; k < N; ++k) {
+            P[k] = star_phase_b(P[k], G[k], a[k], pw[k], sc, acc);
+            M[k] = a[k].m;
+            V[k] = a[k].v;
+            T[k] = a[k].tau;
+        }
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -145,35 +224,65 @@ __device__ __forceinline__ float update_elem(float p, float g, float &m, float &
 // ---------------------------------------------------------------------------
 
 #define GLOBAL_AS __attribute__((address_space(1)))
-typedef float v4f __attribute__((ext_vector_type(4)));
-typedef unsigned int v2u __attribute__((ext_vector_type(2)));
+template <int N>
+struct VecT;
+template <>
+struct VecT<4> {
+    typedef float F __attribute__((ext_vector_type(4)));
+    typedef unsigned int H __attribute__((ext_vector_type(2)));  // 4 bf16
+};
+template <>
+struct VecT<2> {
+    typedef float F __attribute__((ext_vector_type(2)));
+    typedef unsigned int H;                                       // 2 bf16
+};
 
-__device__ __forceinline__ v4f ld4(const float *p) {
-    return __builtin_nontemporal_load((const GLOBAL_AS v4f *)(p));
+template <int N>
+__device__ __forceinline__ void ld_n(const float *p, float (&o)[N]) {
+    const typename VecT<N>::F v = __builtin_nontemporal_load((const GLOBAL_AS typename VecT<N>::F *)(p));
+#pragma unroll
+    for (int k = 0; k < N; ++k) o[k] = v[k];
 }
-__device__ __forceinline__ void st4(float *p, v4f x) {
-    __builtin_nontemporal_store(x, (GLOBAL_AS v4f *)(p));
+template <int N>
+__device__ __forceinline__ void st_n(float *p, const float (&x)[N]) {
+    typename VecT<N>::F v;
+#pragma unroll
+    for (int k = 0; k < N; ++k) v[k] = x[k];
+    __builtin_nontemporal_store(v, (GLOBAL_AS typename VecT<N>::F *)(p));
 }
-__device__ __forceinline__ v2u ld2u(const void *p) {
-    return __builtin_nontemporal_load((const GLOBAL_AS v2u *)(p));
-}
-__device__ __forceinline__ void st2u(void *p, v2u x) {
-    __builtin_nontemporal_store(x, (GLOBAL_AS v2u *)(p));
-}
-
-template <bool GBF16>
-__device__ __forceinline__ v4f load_grad4(const void *g, int64_t off) {
-    if constexpr (GBF16) {
-        const v2u r = ld2u(static_cast<const unsigned short *>(g) + off);
-        v4f o;
-        o.x = __uint_as_float(r.x << 16);
-        o.y = __uint_as_float(r.x & 0xffff0000u);
-        o.z = __uint_as_float(r.y << 16);
-        o.w = __uint_as_float(r.y & 0xffff0000u);
-        return o;
+// N bfloat16 values <-> their bits packed two per 32-bit word
+template <int N>
+__device__ __forceinline__ void ld_bf16_n(const void *p, float (&o)[N]) {
+    const typename VecT<N>::H h = __builtin_nontemporal_load((const GLOBAL_AS typename VecT<N>::H *)(p));
+    if constexpr (N == 2) {
+        o[0] = __uint_as_float(h << 16);
+        o[1] = __uint_as_float(h & 0xffff0000u);
     } else {
-        return ld4(static_cast<const float *>(g) + off);
+#pragma unroll
+        for (int k = 0; k < N / 2; ++k) {
+            o[2 * k] = __uint_as_float(h[k] << 16);
+            o[2 * k + 1] = __uint_as_float(h[k] & 0xffff0000u);
+        }
     }
+}
+template <int N>
+__device__ __forceinline__ void st_bf16_n(void *p, const float (&x)[N]) {
+    typename VecT<N>::H h;
+    if constexpr (N == 2) {
+        h = static_cast<unsigned int>(f32_to_bf16(x[0])) | (static_cast<unsigned int>(f32_to_bf16(x[1])) << 16);
+    } else {
+#pragma unroll
+        for (int k = 0; k < N / 2; ++k)
+            h[k] = static_cast<unsigned int>(f32_to_bf16(x[2 * k])) |
+                   (static_cast<unsigned int>(f32_to_bf16(x[2 * k + 1])) << 16);
+    }
+    __builtin_nontemporal_store(h, (GLOBAL_AS typename VecT<N>::H *)(p));
+}
+
+template <bool GBF16, int N>
+__device__ __forceinline__ void load_grad_n(const void *g, int64_t off, float (&o)[N]) {
+    if constexpr (GBF16) ld_bf16_n<N>(static_cast<const unsigned short *>(g) + off, o);
+    else ld_n<N>(static_cast<const float *>(g) + off, o);
 }
 template <bool GBF16>
 __device__ __forceinline__ float load_grad1(const void *g, int64_t off) {
@@ -182,26 +291,30 @@ __device__ __forceinline__ float load_grad1(const void *g, int64_t off) {
 }
 
 // ---------------------------------------------------------------------------
-// Main multi-tensor kernel: one 1024-element chunk per 256-thread workgroup,
-// one 16-byte vector per thread per array, a single load -> update -> store
-// pass (waves exit right after their stores; looping waves would wait on
-// their own stores, which the gfx9 vmcnt counter orders with later loads).
+// Main multi-tensor kernel: one 1024-element chunk per workgroup, VEC
+// consecutive elements (one 4*VEC-byte vector per array) per thread, a single
+// load -> update -> store pass (waves exit right after their stores; looping
+// waves would wait on their own stores, which the gfx9 vmcnt counter orders
+// with later loads).  All variants run VEC = 4 (256 threads); VEC = 2 (512
+// threads) is kept compilable for tuning.
 // ---------------------------------------------------------------------------
 
-template <bool STAR, bool GBF16, bool PBF16>
-__global__ __launch_bounds__(kBlock) void mta_step_kernel(const adana_tensor_desc *__restrict__ desc,
-                                                          const int64_t *__restrict__ vstart,
-                                                          const int32_t *__restrict__ chunk_first,
-                                                          int32_t n, ScalarPack pack,
-                                                          float *__restrict__ partials) {
-    __shared__ float red[kWaves][4];
+template <bool STAR, bool GBF16, bool PBF16, int POWK, int VEC>
+__global__ __launch_bounds__(kChunk / VEC) void mta_step_kernel(const adana_tensor_desc *__restrict__ desc,
+                                                                const int64_t *__restrict__ vstart,
+                                                                const int32_t *__restrict__ chunk_first,
+                                                                int32_t n, ScalarPack pack,
+                                                                float *__restrict__ partials) {
+    constexpr int kThreads = kChunk / VEC;
+    constexpr int kW = kThreads / 64;
+    __shared__ float red[kW][4];
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
     const int64_t chunk = blockIdx.x;
     const int64_t lo = chunk * kChunk;
     const int64_t hi = lo + kChunk;
-    const int64_t mine = lo + 4 * tid;   // virtual index of this thread's 4 elements
+    const int64_t mine = lo + VEC * tid;   // virtual index of this thread's VEC elements
 
     for (int i = chunk_first[chunk]; i < n; ++i) {
         const int64_t vs = vstart[i];
@@ -212,50 +325,36 @@ __global__ __launch_bounds__(kBlock) void mta_step_kernel(const adana_tensor_des
         const adana_step_scalars &sc = pack.c[d.sclass];
         float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
         if (mine >= vs && mine < ve) {
-            const int64_t off = mine - vs;                         // multiple of 4
+            const int64_t off = mine - vs;                         // multiple of VEC
             float *pp = static_cast<float *>(d.param) + off;
             float *mp = d.m + off;
             float *vp = d.v + off;
             float *tp = STAR ? d.tau + off : nullptr;
-            const int cnt = (ve - mine) < 4 ? static_cast<int>(ve - mine) : 4;
-            if (cnt == 4 && (d.flags & ADANA_DESC_VEC_OK)) {
-                const v4f P = ld4(pp);
-                const v4f G = load_grad4<GBF16>(d.grad, off);
-                v4f M = ld4(mp);
-                v4f V = ld4(vp);
-                v4f T = {0.0f, 0.0f, 0.0f, 0.0f};
-                if constexpr (STAR) T = ld4(tp);
-                v4f O;
-                float t0 = T.x, t1 = T.y, t2 = T.z, t3 = T.w;
-                float m0 = M.x, m1 = M.y, m2 = M.z, m3 = M.w;
-                float v0 = V.x, v1 = V.y, v2 = V.z, v3 = V.w;
-                O.x = update_elem<STAR>(P.x, G.x, m0, v0, t0, sc, acc);
-                O.y = update_elem<STAR>(P.y, G.y, m1, v1, t1, sc, acc);
-                O.z = update_elem<STAR>(P.z, G.z, m2, v2, t2, sc, acc);
-                O.w = update_elem<STAR>(P.w, G.w, m3, v3, t3, sc, acc);
-                M.x = m0; M.y = m1; M.z = m2; M.w = m3;
-                V.x = v0; V.y = v1; V.z = v2; V.w = v3;
-                st4(pp, O);
-                st4(mp, M);
-                st4(vp, V);
+            const int cnt = (ve - mine) < VEC ? static_cast<int>(ve - mine) : VEC;
+            if (cnt == VEC && (d.flags & ADANA_DESC_VEC_OK)) {
+                float P[VEC], G[VEC], M[VEC], V[VEC], T[VEC];
+                ld_n<VEC>(pp, P);
+                load_grad_n<GBF16, VEC>(d.grad, off, G);
+                ld_n<VEC>(mp, M);
+                ld_n<VEC>(vp, V);
                 if constexpr (STAR) {
-                    T.x = t0; T.y = t1; T.z = t2; T.w = t3;
-                    st4(tp, T);
+                    ld_n<VEC>(tp, T);
+                } else {
+#pragma unroll
+                    for (int k = 0; k < VEC; ++k) T[k] = 0.0f;
                 }
-                if constexpr (PBF16) {
-                    v2u b;
-                    b.x = static_cast<unsigned int>(f32_to_bf16(O.x)) |
-                          (static_cast<unsigned int>(f32_to_bf16(O.y)) << 16);
-                    b.y = static_cast<unsigned int>(f32_to_bf16(O.z)) |
-                          (static_cast<unsigned int>(f32_to_bf16(O.w)) << 16);
-                    st2u(static_cast<unsigned short *>(d.param_lp) + off, b);
-                }
+                update_n<STAR, POWK, VEC>(P, G, M, V, T, sc, acc);
+                st_n<VEC>(pp, P);
+                st_n<VEC>(mp, M);
+                st_n<VEC>(vp, V);
+                if constexpr (STAR) st_n<VEC>(tp, T);
+                if constexpr (PBF16) st_bf16_n<VEC>(static_cast<unsigned short *>(d.param_lp) + off, P);
             } else {
-                // unaligned tensor, or the last (<4) elements of a tensor
+                // unaligned tensor, or the last (< VEC) elements of a tensor
                 for (int e = 0; e < cnt; ++e) {
                     float mm = mp[e], vv = vp[e], tt = STAR ? tp[e] : 0.0f;
-                    const float o = update_elem<STAR>(pp[e], load_grad1<GBF16>(d.grad, off + e), mm, vv,
-                                                      tt, sc, acc);
+                    const float o = update_elem<STAR, POWK>(pp[e], load_grad1<GBF16>(d.grad, off + e), mm, vv,
+                                                            tt, sc, acc);
                     pp[e] = o;
                     mp[e] = mm;
                     vp[e] = vv;
@@ -274,11 +373,14 @@ __global__ __launch_bounds__(kBlock) void mta_step_kernel(const adana_tensor_des
         }
         __syncthreads();
         if (tid == 0) {
-            float4 q;
-            q.x = ((red[0][0] + red[1][0]) + red[2][0]) + red[3][0];
-            q.y = ((red[0][1] + red[1][1]) + red[2][1]) + red[3][1];
-            q.z = ((red[0][2] + red[1][2]) + red[2][2]) + red[3][2];
-            q.w = ((red[0][3] + red[1][3]) + red[2][3]) + red[3][3];
+            float4 q = make_float4(red[0][0], red[0][1], red[0][2], red[0][3]);
+#pragma unroll
+            for (int w = 1; w < kW; ++w) {
+                q.x += red[w][0];
+                q.y += red[w][1];
+                q.z += red[w][2];
+                q.w += red[w][3];
+            }
             reinterpret_cast<float4 *>(partials)[chunk + i] = q;
         }
         __syncthreads();
@@ -301,27 +403,17 @@ __global__ __launch_bounds__(kBlock) void chunk_index_kernel(const int64_t *__re
     chunk_first[c] = l;
 }
 
-// One workgroup per tensor: binary64 sum of the tensor's (chunk, tensor)
-// partials in a fixed order, then the five diagnostics
-// (src/optim/adana.py:146-151, :221-225).
-__global__ __launch_bounds__(kBlock) void finalize_kernel(const adana_tensor_desc *__restrict__ desc,
-                                                          const int64_t *__restrict__ vstart,
-                                                          int32_t n, const float *__restrict__ partials,
-                                                          float *__restrict__ diag) {
-    __shared__ double red[kWaves][4];
-    const int i = blockIdx.x;
+// Diagnostics combine, stage 1: fold workgroup j reduces up to
+// ADANA_FOLD_CHUNKS consecutive (chunk, tensor) partials of one tensor in
+// binary64, in a fixed order, to folds[j].  fold_first[i] is tensor i's first
+// fold workgroup.
+constexpr int kFold = ADANA_FOLD_CHUNKS;
+constexpr int kFoldPerThread = kFold / kBlock;
+static_assert(kFold % kBlock == 0, "fold workgroups cover whole thread rows");
+
+__device__ __forceinline__ void block_sum4(double &s0, double &s1, double &s2, double &s3,
+                                           double (*red)[4]) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int64_t numel = desc[i].numel;
-    const int64_t vs = vstart[i];
-    double s0 = 0.0, s1 = 0.0, s2 = 0.0, s3 = 0.0;
-    if (numel > 0) {
-        const int64_t b0 = vs / kChunk, b1 = (vs + numel - 1) / kChunk;
-        const float4 *p4 = reinterpret_cast<const float4 *>(partials);
-        for (int64_t b = b0 + tid; b <= b1; b += kBlock) {
-            const float4 q = p4[b + i];
-            s0 += q.x; s1 += q.y; s2 += q.z; s3 += q.w;
-        }
-    }
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) {
         s0 += __shfl_xor(s0, o, 64);
@@ -331,12 +423,68 @@ __global__ __launch_bounds__(kBlock) void finalize_kernel(const adana_tensor_des
     }
     if (lane == 0) { red[wave][0] = s0; red[wave][1] = s1; red[wave][2] = s2; red[wave][3] = s3; }
     __syncthreads();
-    if (tid == 0) {
-        s0 = ((red[0][0] + red[1][0]) + red[2][0]) + red[3][0];
-        s1 = ((red[0][1] + red[1][1]) + red[2][1]) + red[3][1];
-        s2 = ((red[0][2] + red[1][2]) + red[2][2]) + red[3][2];
-        s3 = ((red[0][3] + red[1][3]) + red[2][3]) + red[3][3];
-        const double nd = static_cast<double>(numel);
+    s0 = ((red[0][0] + red[1][0]) + red[2][0]) + red[3][0];
+    s1 = ((red[0][1] + red[1][1]) + red[2][1]) + red[3][1];
+    s2 = ((red[0][2] + red[1][2]) + red[2][2]) + red[3][2];
+    s3 = ((red[0][3] + red[1][3]) + red[2][3]) + red[3][3];
+}
+
+__global__ __launch_bounds__(kBlock) void fold_kernel(const adana_tensor_desc *__restrict__ desc,
+                                                      const int64_t *__restrict__ vstart,
+                                                      const int32_t *__restrict__ fold_first, int32_t n,
+                                                      const float *__restrict__ partials,
+                                                      double4 *__restrict__ folds) {
+    __shared__ double red[kWaves][4];
+    const int64_t j = blockIdx.x;
+    int l = 0, r = n - 1;                       // last tensor with fold_first[i] <= j
+    while (l < r) {
+        const int mid = (l + r + 1) >> 1;
+        if (fold_first[mid] <= j) l = mid; else r = mid - 1;
+    }
+    const int i = l;
+    const int64_t vs = vstart[i], numel = desc[i].numel;
+    const int64_t b0 = vs / kChunk, b1 = (vs + numel - 1) / kChunk;
+    const int64_t lo = b0 + (j - fold_first[i]) * kFold;
+    const int64_t hi = (lo + kFold - 1 < b1) ? lo + kFold - 1 : b1;
+    const float4 *p4 = reinterpret_cast<const float4 *>(partials);
+    float4 q[kFoldPerThread];
+#pragma unroll
+    for (int u = 0; u < kFoldPerThread; ++u) {
+        const int64_t b = lo + u * kBlock + threadIdx.x;
+        q[u] = (b <= hi) ? p4[b + i] : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+    double s0 = 0.0, s1 = 0.0, s2 = 0.0, s3 = 0.0;
+#pragma unroll
+    for (int u = 0; u < kFoldPerThread; ++u) {
+        s0 += q[u].x; s1 += q[u].y; s2 += q[u].z; s3 += q[u].w;
+    }
+    block_sum4(s0, s1, s2, s3, red);
+    if (threadIdx.x == 0) folds[j] = make_double4(s0, s1, s2, s3);
+}
+
+// Stage 2: one wave per tensor sums its folds and writes the five
+// diagnostics (src/optim/adana.py:146-151, :221-225).
+__global__ __launch_bounds__(kBlock) void finalize_kernel(const adana_tensor_desc *__restrict__ desc,
+                                                          const int32_t *__restrict__ fold_first,
+                                                          int32_t n, const double4 *__restrict__ folds,
+                                                          float *__restrict__ diag) {
+    const int lane = threadIdx.x & 63;
+    const int i = blockIdx.x * kWaves + (threadIdx.x >> 6);
+    if (i >= n) return;                                   // whole wave
+    double s0 = 0.0, s1 = 0.0, s2 = 0.0, s3 = 0.0;
+    for (int f = fold_first[i] + lane; f < fold_first[i + 1]; f += 64) {
+        const double4 q = folds[f];
+        s0 += q.x; s1 += q.y; s2 += q.z; s3 += q.w;
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        s0 += __shfl_xor(s0, o, 64);
+        s1 += __shfl_xor(s1, o, 64);
+        s2 += __shfl_xor(s2, o, 64);
+        s3 += __shfl_xor(s3, o, 64);
+    }
+    if (lane == 0) {
+        const double nd = static_cast<double>(desc[i].numel);
         const float ca = static_cast<float>(s0 / nd);     // alpha_factor.mean()
         const float afm = static_cast<float>(s2 / nd);    // mfac.mean()
         float *o = diag + 5 * static_cast<int64_t>(i);
@@ -348,11 +496,38 @@ __global__ __launch_bounds__(kBlock) void finalize_kernel(const adana_tensor_des
     }
 }
 
-template <bool STAR, bool GBF16, bool PBF16>
+// Workspace layout: chunk partials (float4 per (chunk, tensor) slot), then the
+// folds (double4 each), 256-byte aligned.
+size_t partials_bytes(const adana_plan &pl) {
+    return static_cast<size_t>(pl.n_chunks + pl.n_tensors) * 16;
+}
+size_t folds_offset(const adana_plan &pl) { return (partials_bytes(pl) + 255) / 256 * 256; }
+size_t workspace_bytes(const adana_plan &pl) {
+    return folds_offset(pl) + static_cast<size_t>(pl.n_folds) * 32;
+}
+
+template <bool STAR, bool GBF16, bool PBF16, int POWK>
 void launch_main(int64_t n_chunks, hipStream_t st, const adana_tensor_desc *d, const int64_t *vs,
                  const int32_t *cf, int32_t n, const ScalarPack &pack, float *partials) {
-    hipLaunchKernelGGL((mta_step_kernel<STAR, GBF16, PBF16>), dim3(static_cast<unsigned>(n_chunks)),
-                       dim3(kBlock), 0, st, d, vs, cf, n, pack, partials);
+    constexpr int kVec = 4;
+    hipLaunchKernelGGL((mta_step_kernel<STAR, GBF16, PBF16, POWK, kVec>), dim3(static_cast<unsigned>(n_chunks)),
+                       dim3(kChunk / kVec), 0, st, d, vs, cf, n, pack, partials);
+}
+
+template <bool STAR, bool GBF16, bool PBF16>
+void launch_pow(int powk, int64_t n_chunks, hipStream_t st, const adana_tensor_desc *d,
+                const int64_t *vs, const int32_t *cf, int32_t n, const ScalarPack &pack,
+                float *partials) {
+    if constexpr (!STAR) {
+        // ADana's (1 + t) ** (1 - kappa) is a host scalar: no per-element pow
+        launch_main<false, GBF16, PBF16, POW_ONE>(n_chunks, st, d, vs, cf, n, pack, partials);
+    } else if (powk == POW_GENERAL) {
+        launch_main<true, GBF16, PBF16, POW_GENERAL>(n_chunks, st, d, vs, cf, n, pack, partials);
+    } else if (powk == POW_ONE) {
+        launch_main<true, GBF16, PBF16, POW_ONE>(n_chunks, st, d, vs, cf, n, pack, partials);
+    } else {
+        launch_main<true, GBF16, PBF16, POW_SPECIAL>(n_chunks, st, d, vs, cf, n, pack, partials);
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -442,16 +617,25 @@ int adana_step_scalars_init(adana_step_scalars *out, const adana_hparams *hp, do
     return ADANA_OK;
 }
 
-int64_t adana_plan_layout(const int64_t *numel, int32_t n, int64_t *vstart) {
-    if (n < 0 || (n > 0 && (!numel || !vstart)))
+int64_t adana_plan_layout(const int64_t *numel, int32_t n, int64_t *vstart,
+                          int32_t *fold_first, int64_t *n_folds) {
+    if (n < 0 || !vstart || !fold_first || !n_folds || (n > 0 && !numel))
         return set_err(ADANA_E_INVALID, "adana_plan_layout: bad arguments");
-    int64_t off = 0;
+    int64_t off = 0, folds = 0;
     for (int32_t i = 0; i < n; ++i) {
         if (numel[i] < 0) return set_err(ADANA_E_INVALID, "adana_plan_layout: numel[%d] < 0", i);
         vstart[i] = off;
+        fold_first[i] = static_cast<int32_t>(folds);
+        if (numel[i] > 0) {
+            const int64_t chunks_i = (off + numel[i] - 1) / kChunk - off / kChunk + 1;
+            folds += (chunks_i + kFold - 1) / kFold;
+        }
         off += (numel[i] + ADANA_ALIGN_ELEMS - 1) / ADANA_ALIGN_ELEMS * ADANA_ALIGN_ELEMS;
+        if (folds > 0x7fffffffLL) return set_err(ADANA_E_UNSUPPORTED, "adana_plan_layout: list too large");
     }
-    if (vstart) vstart[n] = off;
+    vstart[n] = off;
+    fold_first[n] = static_cast<int32_t>(folds);
+    *n_folds = folds;
     const int64_t chunks = (off + kChunk - 1) / kChunk;
     if (chunks > 0x7fffffffLL) return set_err(ADANA_E_UNSUPPORTED, "adana_plan_layout: list too large");
     return chunks;
@@ -473,51 +657,73 @@ int adana_plan_index(const int64_t *d_vstart, int32_t n_tensors, int64_t n_chunk
     return ADANA_OK;
 }
 
-int64_t adana_partials_floats(int32_t n_tensors, int64_t n_chunks) {
-    return 4 * (static_cast<int64_t>(n_tensors) + n_chunks);
+size_t adana_workspace_bytes(const adana_plan *plan) {
+    return plan ? workspace_bytes(*plan) : 0;
 }
 
-int adana_mta_step(const adana_tensor_desc *d_desc, const int64_t *d_vstart,
-                   const int32_t *d_chunk_first, int32_t n_tensors, int64_t n_chunks,
-                   const adana_step_scalars *h_scalars, int32_t n_classes, uint32_t variant_flags,
-                   float *d_partials, float *d_diag, void *stream) {
-    if (n_tensors < 0 || n_chunks < 0 || n_chunks > 0x7fffffffLL)
+int adana_mta_step(const adana_plan *plan, const adana_step_scalars *h_scalars, int32_t n_classes,
+                   uint32_t variant_flags, void *d_workspace, size_t ws_bytes, float *d_diag,
+                   void *stream) {
+    if (!plan) return set_err(ADANA_E_INVALID, "adana_mta_step: null plan");
+    const adana_plan &pl = *plan;
+    if (pl.n_tensors < 0 || pl.n_chunks < 0 || pl.n_chunks > 0x7fffffffLL || pl.n_folds < 0 ||
+        pl.n_folds > 0x7fffffffLL)
         return set_err(ADANA_E_INVALID, "adana_mta_step: bad sizes (n_tensors=%d, n_chunks=%lld)",
-                       n_tensors, static_cast<long long>(n_chunks));
+                       pl.n_tensors, static_cast<long long>(pl.n_chunks));
     if (variant_flags & ~(ADANA_VARIANT_STAR | ADANA_GRAD_BF16 | ADANA_PARAM_BF16))
         return set_err(ADANA_E_INVALID, "adana_mta_step: unknown variant flags 0x%x", variant_flags);
-    if (n_tensors == 0) return ADANA_OK;
-    if (!d_desc || !d_vstart || !d_partials || !d_diag || !h_scalars ||
-        (n_chunks > 0 && !d_chunk_first))
+    if (pl.n_tensors == 0) return ADANA_OK;
+    if (!pl.desc || !pl.vstart || !pl.fold_first || !d_workspace || !d_diag || !h_scalars ||
+        (pl.n_chunks > 0 && !pl.chunk_first))
         return set_err(ADANA_E_INVALID, "adana_mta_step: null pointer argument");
     if (n_classes < 1 || n_classes > ADANA_MAX_CLASSES)
         return set_err(ADANA_E_INVALID, "adana_mta_step: n_classes=%d outside [1, %d]", n_classes,
                        ADANA_MAX_CLASSES);
+    if (ws_bytes < workspace_bytes(pl))
+        return set_err(ADANA_E_INVALID, "adana_mta_step: workspace of %zu bytes < %zu needed", ws_bytes,
+                       workspace_bytes(pl));
     ScalarPack pack;
     memset(&pack, 0, sizeof pack);
     memcpy(pack.c, h_scalars, sizeof(adana_step_scalars) * static_cast<size_t>(n_classes));
     hipStream_t st = static_cast<hipStream_t>(stream);
+    float *partials = static_cast<float *>(d_workspace);
+    double4 *folds = reinterpret_cast<double4 *>(static_cast<char *>(d_workspace) + folds_offset(pl));
     const bool star = variant_flags & ADANA_VARIANT_STAR;
     const bool gb = variant_flags & ADANA_GRAD_BF16;
     const bool pb = variant_flags & ADANA_PARAM_BF16;
-    if (n_chunks > 0) {
-        if (star) {
-            if (gb) { if (pb) launch_main<true, true, true>(n_chunks, st, d_desc, d_vstart, d_chunk_first, n_tensors, pack, d_partials);
-                      else launch_main<true, true, false>(n_chunks, st, d_desc, d_vstart, d_chunk_first, n_tensors, pack, d_partials); }
-            else    { if (pb) launch_main<true, false, true>(n_chunks, st, d_desc, d_vstart, d_chunk_first, n_tensors, pack, d_partials);
-                      else launch_main<true, false, false>(n_chunks, st, d_desc, d_vstart, d_chunk_first, n_tensors, pack, d_partials); }
-        } else {
-            if (gb) { if (pb) launch_main<false, true, true>(n_chunks, st, d_desc, d_vstart, d_chunk_first, n_tensors, pack, d_partials);
-                      else launch_main<false, true, false>(n_chunks, st, d_desc, d_vstart, d_chunk_first, n_tensors, pack, d_partials); }
-            else    { if (pb) launch_main<false, false, true>(n_chunks, st, d_desc, d_vstart, d_chunk_first, n_tensors, pack, d_partials);
-                      else launch_main<false, false, false>(n_chunks, st, d_desc, d_vstart, d_chunk_first, n_tensors, pack, d_partials); }
+    const int32_t n = pl.n_tensors;
+    if (pl.n_chunks > 0) {
+        // one pow code path per launch: all classes must agree on it
+        bool all_one = true, all_general = true;
+        for (int c = 0; c < n_classes; ++c) {
+            all_one = all_one && h_scalars[c].pow_mode == ADANA_POW_ONE;
+            all_general = all_general && h_scalars[c].pow_mode == ADANA_POW_GENERAL &&
+                          h_scalars[c].star_exp > 0.0f && h_scalars[c].star_exp < 1.0f;
         }
+        const int powk = all_general ? POW_GENERAL : (all_one ? POW_ONE : POW_SPECIAL);
+#define ADANA_LAUNCH(S, G, P) \
+        launch_pow<S, G, P>(powk, pl.n_chunks, st, pl.desc, pl.vstart, pl.chunk_first, n, pack, partials)
+        if (star) {
+            if (gb) { if (pb) ADANA_LAUNCH(true, true, true); else ADANA_LAUNCH(true, true, false); }
+            else    { if (pb) ADANA_LAUNCH(true, false, true); else ADANA_LAUNCH(true, false, false); }
+        } else {
+            if (gb) { if (pb) ADANA_LAUNCH(false, true, true); else ADANA_LAUNCH(false, true, false); }
+            else    { if (pb) ADANA_LAUNCH(false, false, true); else ADANA_LAUNCH(false, false, false); }
+        }
+#undef ADANA_LAUNCH
         hipError_t err = hipGetLastError();
         if (err != hipSuccess)
             return set_err(ADANA_E_HIP, "adana_mta_step: main launch failed: %s", hipGetErrorString(err));
     }
-    hipLaunchKernelGGL(finalize_kernel, dim3(static_cast<unsigned>(n_tensors)), dim3(kBlock), 0, st, d_desc, d_vstart,
-                       n_tensors, d_partials, d_diag);
+    if (pl.n_folds > 0) {
+        hipLaunchKernelGGL(fold_kernel, dim3(static_cast<unsigned>(pl.n_folds)), dim3(kBlock), 0, st,
+                           pl.desc, pl.vstart, pl.fold_first, n, partials, folds);
+        hipError_t err = hipGetLastError();
+        if (err != hipSuccess)
+            return set_err(ADANA_E_HIP, "adana_mta_step: fold launch failed: %s", hipGetErrorString(err));
+    }
+    hipLaunchKernelGGL(finalize_kernel, dim3(static_cast<unsigned>((n + kWaves - 1) / kWaves)), dim3(kBlock),
+                       0, st, pl.desc, pl.fold_first, n, folds, d_diag);
     hipError_t err = hipGetLastError();
     if (err != hipSuccess)
         return set_err(ADANA_E_HIP, "adana_mta_step: finalize launch failed: %s", hipGetErrorString(err));

@@ -5,102 +5,125 @@
 // tensor effective_time = clamp(tau * step, min=1) (src/optim/dana_star_mk4.py
 // :159, :170/:174).  The exponent is the binary32 rounding of 1 - kappa.
 //
-// Method (standard argument reduction, all in binary64):
-//   x = 2^k * m, m in [sqrt(1/2), sqrt(2))
-//   ln m = 2u (1 + u^2/3 + u^4/5 + ... + u^22/23),  u = (m-1)/(m+1), |u| < 0.1716
-//   ln x = k*ln2_hi + (k*ln2_lo + ln m)
-//   t = y * ln x;  n = rint(t / ln2);  r = t - n*ln2 (two-step, |r| <= 0.347)
-//   e^r = sum_{j<=13} r^j / j!;  x^y = 2^n * e^r
-// Truncation errors are below 2^-56 relative for both series; the result
-// before the final rounding is within a few binary64 ulps of x^y, so the
-// binary32 result equals the correctly rounded one except when x^y lies
-// within ~2^-50 (relative) of a binary32 rounding boundary.
+// Method (table-driven argument reduction, all arithmetic in binary64):
+//   x = 2^e * m, m in [1, 2);  j = top 7 bits of m's fraction
+//   r = m * invc[j] - 1 (exact: invc has 12 significant bits), |r| < 0.0043
+//   ln x = e*ln2 + (-ln invc[j]) + log1p(r),  log1p by its degree-7 series
+//   t = y * ln x;  k = rint(t * 128 / ln2);  r' = t - k * ln2/128 (|r'| < 0.0028)
+//   x^y = 2^(k >> 7) * 2^((k & 127) / 128) * (1 + expm1(r')), degree-5 series
+// Series truncation is below 2^-60; table entries are correctly rounded
+// binary64 values (gen_pow_tables.py).  The binary64 result is within about
+// (|t| + 4) binary64 ulps of x^y, so its binary32 rounding is the correctly
+// rounded binary32 x^y unless the result lies next to a binary32 rounding
+// boundary.
 //
-// Domain of the fast path: 1 <= x < 3e38 (finite).  Anything else (NaN,
-// +inf), and results next to a binary32 rounding boundary, go to the
-// platform's binary64 pow.  Usable from host code (the CPU
-// test suite checks it against the C library's pow).
+// Two entry points: pow_f32_unit_exp (0 < y < 1, the kernel's hot path; see
+// there why it needs no slow path) and pow_f32_via_f64 (any y: results next
+// to a rounding boundary -- about 1e-7 of inputs, and every input whose x^y
+// is exactly a boundary -- and inputs outside 1 <= x < 3e38 are re-evaluated
+// with the platform's binary64 pow).  Usable from host code: the CPU test
+// suite checks both against the C library's pow.
 #ifndef ADANA_POW_H
 #define ADANA_POW_H
 
 #include <cmath>
+#include <cstdint>
+#include <cstring>
 
 #if defined(__HIPCC__) || defined(__HIP__)
 #define ADANA_HD __host__ __device__
+#define ADANA_TABLE_ATTR __device__ __constant__
 #else
 #define ADANA_HD
+#define ADANA_TABLE_ATTR static
 #endif
+
+#include "adana_pow_tables.h"
 
 namespace adana {
 
-ADANA_HD inline double pow_core_f64(double x, double y) {
-    // x = m * 2^k with m in [0.5, 1)
-    int k;
-    double m = std::frexp(x, &k);
-    if (m < 0.70710678118654752440) {   // move m to [sqrt(1/2), sqrt(2))
-        m = m + m;
-        k -= 1;
-    }
-    const double u = (m - 1.0) / (m + 1.0);
-    const double w = u * u;
-    // Q(w) = 1/3 + w/5 + ... + w^10/23
-    double q = 1.0 / 23.0;
-    q = std::fma(q, w, 1.0 / 21.0);
-    q = std::fma(q, w, 1.0 / 19.0);
-    q = std::fma(q, w, 1.0 / 17.0);
-    q = std::fma(q, w, 1.0 / 15.0);
-    q = std::fma(q, w, 1.0 / 13.0);
-    q = std::fma(q, w, 1.0 / 11.0);
-    q = std::fma(q, w, 1.0 / 9.0);
-    q = std::fma(q, w, 1.0 / 7.0);
-    q = std::fma(q, w, 1.0 / 5.0);
-    q = std::fma(q, w, 1.0 / 3.0);
-    const double s = u + u;
-    const double lnm = std::fma(s * w, q, s);
-    // ln 2 split so that k * LN2_HI is exact for |k| < 2^11
-    const double LN2_HI = 6.93147180369123816490e-01;
-    const double LN2_LO = 1.90821492927058770002e-10;
-    const double kd = static_cast<double>(k);
-    const double lnx = kd * LN2_HI + (kd * LN2_LO + lnm);
-    const double t = y * lnx;
-    // e^t = 2^n e^r
-    const double n = std::rint(t * 1.44269504088896338700);
-    double r = std::fma(-n, LN2_HI, t);
-    r = std::fma(-n, LN2_LO, r);
-    double e = 1.0 / 6227020800.0;               // 1/13!
-    e = std::fma(e, r, 1.0 / 479001600.0);       // 1/12!
-    e = std::fma(e, r, 1.0 / 39916800.0);
-    e = std::fma(e, r, 1.0 / 3628800.0);
-    e = std::fma(e, r, 1.0 / 362880.0);
-    e = std::fma(e, r, 1.0 / 40320.0);
-    e = std::fma(e, r, 1.0 / 5040.0);
-    e = std::fma(e, r, 1.0 / 720.0);
-    e = std::fma(e, r, 1.0 / 120.0);
-    e = std::fma(e, r, 1.0 / 24.0);
-    e = std::fma(e, r, 1.0 / 6.0);
-    e = std::fma(e, r, 0.5);
-    e = std::fma(e, r, 1.0);
-    e = std::fma(e, r, 1.0);
-    return std::ldexp(e, static_cast<int>(n));
+template <typename To, typename From>
+ADANA_HD inline To bits_as(From v) {
+    static_assert(sizeof(To) == sizeof(From), "size");
+    To o;
+    std::memcpy(&o, &v, sizeof o);
+    return o;
 }
 
-// binary32 x ** y as fp32(x ** y evaluated in binary64).  When the core's
-// result lies within 2^-46 (relative) of a binary32 rounding boundary -- about
-// 2e-7 of inputs, and every case where x ** y is exactly a boundary -- the
-// rounding is decided by the platform's binary64 pow instead.
+// binary64 x ** y for 1 <= x < 3e38 (finite).  Writes t = y * ln x.
+ADANA_HD inline double pow_core_f64(float x, float y, double &t_out) {
+    const uint32_t xb = bits_as<uint32_t>(x);
+    const int e = static_cast<int>(xb >> 23) - 127;
+    const int j = static_cast<int>((xb >> 16) & 127u);
+    const double m = static_cast<double>(bits_as<float>((xb & 0x007fffffu) | 0x3f800000u));
+    const double r = std::fma(m, kLogInvC[j], -1.0);
+    // log1p(r) = r + r^2 * (-1/2 + r/3 - r^2/4 + r^3/5 - r^4/6 + r^5/7)
+    double q = 1.0 / 7.0;
+    q = std::fma(q, r, -1.0 / 6.0);
+    q = std::fma(q, r, 1.0 / 5.0);
+    q = std::fma(q, r, -1.0 / 4.0);
+    q = std::fma(q, r, 1.0 / 3.0);
+    q = std::fma(q, r, -0.5);
+    const double lp = std::fma(r * r, q, r);
+    // ln 2 split so that e * LN2_HI and k * LN2_HI / 128 are exact
+    const double LN2_HI = 6.93147180369123816490e-01;
+    const double LN2_LO = 1.90821492927058770002e-10;
+    const double ed = static_cast<double>(e);
+    const double lnx = std::fma(ed, LN2_HI, kLogNegLnC[j]) + std::fma(ed, LN2_LO, lp);
+    const double t = static_cast<double>(y) * lnx;
+    // e^t = 2^(k/128) e^r'
+    const double kd = std::rint(t * 184.66496523378731);        // 128 / ln 2
+    double rr = std::fma(-kd, LN2_HI / 128.0, t);
+    rr = std::fma(-kd, LN2_LO / 128.0, rr);
+    double p = 1.0 / 120.0;
+    p = std::fma(p, rr, 1.0 / 24.0);
+    p = std::fma(p, rr, 1.0 / 6.0);
+    p = std::fma(p, rr, 0.5);
+    p = std::fma(rr * rr, p, rr);                                // expm1(r')
+    const int k = static_cast<int>(kd);
+    const double tj = kExp2J[k & 127];
+    t_out = t;
+    return std::ldexp(std::fma(tj, p, tj), k >> 7);
+}
+
+// True when fp32(res) may differ from the correctly rounded binary32 x ** y:
+// binary32 rounding drops the low 29 of the 52 fraction bits, and res is
+// within 8 * (|t| + 4) binary64 ulps of the half-way pattern (or outside
+// binary32's normal range).
+ADANA_HD inline bool near_boundary(double res, double t) {
+    const uint32_t dropped = static_cast<uint32_t>(bits_as<uint64_t>(res)) & 0x1fffffffu;
+    const int32_t dist = static_cast<int32_t>(dropped) - 0x10000000;
+    const int32_t w = 32 + 8 * static_cast<int32_t>(std::fabs(t));
+    return (dist <= w && dist >= -w) || !(res >= 1.1754943508222875e-38);
+}
+
+// The platform's binary64 pow, rounded once: the slow path.
+ADANA_HD inline float pow_f32_slow(float x, float y) {
+    return static_cast<float>(std::pow(static_cast<double>(x), static_cast<double>(y)));
+}
+
+// x ** y for an exponent 0 < y < 1 and x >= 1 (NaN and +inf pass through,
+// as pow gives them for such y).  No slow path: for 0 < y < 1, x ** y is
+// never exactly a binary32 half-way point (x^p = M^q would need a 25-bit odd
+// M with M^q, q > p, fitting x's 24 bits), so fp32(core) differs from the
+// correctly rounded result only when x ** y lies within the core's error
+// (~2^-51 relative) of a half-way point -- measured 1 in 2e8 inputs against
+// the C library's pow (tests/pow_harness.cpp).
+ADANA_HD inline float pow_f32_unit_exp(float x, float y) {
+    if (!(x < 3.0e38f)) return x;
+    double t;
+    return static_cast<float>(pow_core_f64(x, y, t));
+}
+
+// Any exponent: the core, and the slow path next to rounding boundaries and
+// outside the core's domain.
 ADANA_HD inline float pow_f32_via_f64(float x, float y) {
     if (x >= 1.0f && x < 3.0e38f) {
-        const double d = pow_core_f64(static_cast<double>(x), static_cast<double>(y));
-        const float f = static_cast<float>(d);
-        const double fd = static_cast<double>(f);
-        const double err = std::fabs(d - fd);
-        // half the binary32 spacing above fd, and below it (a power of two has
-        // a spacing below that is half the spacing above)
-        const double half_up = std::ldexp(1.0, std::ilogb(fd) - 24);
-        const double tol = d * 1.4210854715202004e-14;    // 2^-46
-        if (std::fabs(err - half_up) > tol && std::fabs(err - 0.5 * half_up) > tol) return f;
+        double t;
+        const double res = pow_core_f64(x, y, t);
+        if (!near_boundary(res, t)) return static_cast<float>(res);
     }
-    return static_cast<float>(std::pow(static_cast<double>(x), static_cast<double>(y)));
+    return pow_f32_slow(x, y);
 }
 
 }  // namespace adana

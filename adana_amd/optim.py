@@ -54,10 +54,13 @@ class _LaunchSet:
         self.sclass: List[int] = []
         self.host_desc = None
         self.vstart = None
+        self.fold_first = None
         self.n_chunks = 0
+        self.n_folds = 0
         self.dev_table = None
         self.chunk_first = None
-        self.partials = None
+        self.workspace = None
+        self.plan = None
         self.diag = None
         self.ptr_key = None
 
@@ -161,11 +164,23 @@ class _DanaFamily(Optimizer):
         return d
 
     def _upload(self, ls: _LaunchSet) -> None:
-        table = np.concatenate([ls.host_desc.view(np.uint8), ls.vstart.view(np.uint8)])
+        """Copy [descriptors | vstart | fold_first] to the device (async, pinned)."""
+        table = np.concatenate([ls.host_desc.view(np.uint8), ls.vstart.view(np.uint8),
+                                ls.fold_first.view(np.uint8)])
         host = torch.from_numpy(table).pin_memory()
         if ls.dev_table is None or ls.dev_table.numel() != host.numel():
             ls.dev_table = torch.empty(host.numel(), dtype=torch.uint8, device=ls.device)
         ls.dev_table.copy_(host, non_blocking=True)
+        n = len(ls.params)
+        base = ls.dev_table.data_ptr()
+        if ls.plan is None:
+            ls.plan = _lib.Plan()
+        ls.plan.desc = base
+        ls.plan.vstart = base + 64 * n
+        ls.plan.fold_first = base + 64 * n + 8 * (n + 1)
+        ls.plan.n_tensors = n
+        ls.plan.n_chunks = ls.n_chunks
+        ls.plan.n_folds = ls.n_folds
 
     def _build(self, params, grads, states, sclass, flags_list) -> List[_LaunchSet]:
         sets = {}
@@ -182,7 +197,7 @@ class _DanaFamily(Optimizer):
         out = list(sets.values())
         for ls in out:
             numels = np.fromiter((p.numel() for p in ls.params), dtype=np.int64, count=len(ls.params))
-            ls.vstart, ls.n_chunks = _lib.plan_layout(numels)
+            ls.vstart, ls.fold_first, ls.n_chunks, ls.n_folds = _lib.plan_layout(numels)
             ls.host_desc = self._desc_rows(ls)
             ls.ptr_key = ls.host_desc["grad"].copy()
             with torch.cuda.device(ls.device):
@@ -191,11 +206,12 @@ class _DanaFamily(Optimizer):
                 ls.chunk_first = torch.empty(max(ls.n_chunks, 1), dtype=torch.int32, device=ls.device)
                 stream = torch.cuda.current_stream(ls.device).cuda_stream
                 _lib.check(_lib.lib().adana_plan_index(
-                    ctypes.c_void_p(ls.dev_table.data_ptr() + 64 * n), n, ls.n_chunks,
+                    ctypes.c_void_p(ls.plan.vstart), n, ls.n_chunks,
                     ctypes.c_void_p(ls.chunk_first.data_ptr()), ctypes.c_void_p(stream)),
                     "adana_plan_index")
-                ls.partials = torch.empty(_lib.partials_floats(len(ls.params), ls.n_chunks),
-                                          dtype=torch.float32, device=ls.device)
+                ls.plan.chunk_first = ls.chunk_first.data_ptr()
+                ls.workspace = torch.empty(max(_lib.workspace_bytes(ls.plan), 1), dtype=torch.uint8,
+                                           device=ls.device)
                 ls.diag = torch.full((len(ls.params), 5), float("nan"), dtype=torch.float32,
                                      device=ls.device)
             for j, st in enumerate(ls.states):
@@ -286,16 +302,12 @@ class _DanaFamily(Optimizer):
         for ls in self._sets:
             n_cls = min(_lib.MAX_CLASSES, len(classes) - ls.class_base)
             sc_arr = (_lib.StepScalars * n_cls)(*scalars[ls.class_base:ls.class_base + n_cls])
-            base = ls.dev_table.data_ptr()
-            n = len(ls.params)
             with torch.cuda.device(ls.device):
                 stream = torch.cuda.current_stream(ls.device).cuda_stream
                 _lib.check(L.adana_mta_step(
-                    ctypes.c_void_p(base), ctypes.c_void_p(base + 64 * n),
-                    ctypes.c_void_p(ls.chunk_first.data_ptr()), n, ls.n_chunks,
-                    ctypes.cast(sc_arr, ctypes.c_void_p), n_cls, ls.flags,
-                    ctypes.c_void_p(ls.partials.data_ptr()), ctypes.c_void_p(ls.diag.data_ptr()),
-                    ctypes.c_void_p(stream)), "adana_mta_step")
+                    ctypes.byref(ls.plan), ctypes.cast(sc_arr, ctypes.c_void_p), n_cls, ls.flags,
+                    ctypes.c_void_p(ls.workspace.data_ptr()), ls.workspace.numel(),
+                    ctypes.c_void_p(ls.diag.data_ptr()), ctypes.c_void_p(stream)), "adana_mta_step")
         torch._C._increment_version(params)
         return loss
 

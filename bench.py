@@ -181,13 +181,36 @@ def cpu_baseline(w, target_s=10.0, max_elems=1 << 26):
             "ms_per_step_sample": round(per_step * 1e3, 3)}
 
 
+def copy_probe(steps):
+    """Plain device-to-device copy of a known size (1 GiB read + 1 GiB written
+    per launch): the calibration for the HBM FETCH_SIZE / WRITE_SIZE counters."""
+    import torch
+
+    n = (1 << 30) // 4
+    a = torch.ones(n, device="cuda:0")
+    b = torch.empty_like(a)
+    for _ in range(2):
+        b.copy_(a)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(steps):
+        b.copy_(a)
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / steps
+    print(json.dumps({"copy_probe_bytes_read": 1 << 30, "copy_probe_bytes_written": 1 << 30,
+                      "ms_per_copy": round(ms, 4), "GBps": round(2 * (1 << 30) / ms / 1e6, 1)}))
+    return 0
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--workload", default="north_star",
-                    choices=["north_star", "c1", "c2", "c3", "c4", "c5"])
+                    choices=["north_star", "c1", "c2", "c3", "c4", "c5", "copy_probe"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     args = ap.parse_args()
@@ -198,6 +221,8 @@ def main():
 
     import torch
 
+    if args.workload == "copy_probe":
+        return copy_probe(args.steps)
     w = workload(args.workload)
     print(f"[bench] workload {w['name']} ({w['optimizer']}): building on cuda:0", file=sys.stderr,
           flush=True)

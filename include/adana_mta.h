@@ -24,7 +24,7 @@
  *        (src/optim/dana_star_mk4.py:105-205) for ALL tensors of the list,
  *        plus the diagnostics stored at src/optim/adana.py:221-225 /
  *        src/optim/dana_star_mk4.py:290-294.
- *   adana_last_error, adana_abi_version, adana_partials_floats: plumbing
+ *   adana_last_error, adana_abi_version, adana_workspace_bytes: plumbing
  *        (no reference counterpart).
  *
  * Ownership: the library allocates nothing; every device buffer is owned by
@@ -53,6 +53,8 @@ extern "C" {
 #define ADANA_ALIGN_ELEMS 4
 /* Scalar classes (distinct (group, step) pairs) one launch can carry. */
 #define ADANA_MAX_CLASSES 8
+/* Chunk partials one fold workgroup of the diagnostics combine reduces. */
+#define ADANA_FOLD_CHUNKS 2048
 
 /* variant_flags of adana_mta_step */
 #define ADANA_VARIANT_STAR 0x1u  /* Dana-Star(-MK4): tau state and estimator   */
@@ -80,6 +82,20 @@ typedef struct adana_tensor_desc {
     int32_t     sclass;    /* index into the launch's scalar classes         */
     uint32_t    flags;     /* ADANA_DESC_* bits                              */
 } adana_tensor_desc;
+
+/* A laid-out tensor list: host struct holding device pointers (all device
+ * arrays are owned by the caller).  Built with adana_plan_layout (host part)
+ * and adana_plan_index (chunk_first). */
+typedef struct adana_plan {
+    const adana_tensor_desc *desc;   /* device, n_tensors entries              */
+    const int64_t *vstart;           /* device, n_tensors + 1 (layout output)  */
+    const int32_t *chunk_first;      /* device, n_chunks (adana_plan_index)    */
+    const int32_t *fold_first;       /* device, n_tensors + 1 (layout output)  */
+    int32_t n_tensors;
+    int32_t reserved;
+    int64_t n_chunks;
+    int64_t n_folds;
+} adana_plan;
 
 /* Hyper-parameters of one parameter group (reference ctor arguments and
  * group keys, src/optim/adana.py:32-57). */
@@ -133,10 +149,13 @@ size_t adana_last_error(char *buf, size_t len);
 int adana_step_scalars_init(adana_step_scalars *out, const adana_hparams *hp,
                             double lr, int64_t step);
 
-/* Host only.  Writes vstart[0..n] (virtual start of each tensor; vstart[n] is
- * the padded total) and returns the number of work chunks (>= 0), or a
- * negative error code. */
-int64_t adana_plan_layout(const int64_t *numel, int32_t n, int64_t *vstart);
+/* Host only.  Lays n tensors end to end: writes vstart[0..n] (virtual start
+ * of each tensor, multiples of ADANA_ALIGN_ELEMS; vstart[n] is the padded
+ * total) and fold_first[0..n] (first fold workgroup of each tensor's
+ * diagnostics combine; fold_first[n] = *n_folds), and returns the number of
+ * work chunks (>= 0), or a negative error code. */
+int64_t adana_plan_layout(const int64_t *numel, int32_t n, int64_t *vstart,
+                          int32_t *fold_first, int64_t *n_folds);
 
 /* Device.  Fills d_chunk_first[c] (c < n_chunks) with the index of the first
  * tensor whose virtual range reaches chunk c, from the device copy of vstart.
@@ -144,28 +163,24 @@ int64_t adana_plan_layout(const int64_t *numel, int32_t n, int64_t *vstart);
 int adana_plan_index(const int64_t *d_vstart, int32_t n_tensors, int64_t n_chunks,
                      int32_t *d_chunk_first, void *stream);
 
-/* Floats of the d_partials workspace a launch over n tensors / n_chunks
- * chunks needs. */
-int64_t adana_partials_floats(int32_t n_tensors, int64_t n_chunks);
+/* Bytes of device workspace adana_mta_step needs for ``plan``. */
+size_t adana_workspace_bytes(const adana_plan *plan);
 
 /* Device step over one tensor list.
- *   d_desc      device array of n_tensors descriptors
- *   d_vstart    device copy of adana_plan_layout's vstart (n_tensors + 1)
- *   d_chunk_first  adana_plan_index's output (n_chunks entries)
- *   n_chunks    adana_plan_layout's return value
+ *   plan        the laid-out list (host struct, device arrays)
  *   h_scalars   host array of n_classes scalar classes (passed by value to
  *               the kernel; no host-to-device copy)
- *   d_partials  device workspace, adana_partials_floats(...) floats
+ *   d_workspace device scratch of at least adana_workspace_bytes(plan) bytes
+ *               (per-chunk partial sums and their folds; contents on entry
+ *               are ignored)
  *   d_diag      device float[5 * n_tensors]: per tensor current_alpha,
  *               gradient_norm, auto_factor_mean, current_kappa_factor,
  *               m_norm (src/optim/adana.py:221-225)
  *   stream      hipStream_t (NULL = default stream)
  * All tensors of one call share variant_flags. */
-int adana_mta_step(const adana_tensor_desc *d_desc, const int64_t *d_vstart,
-                   const int32_t *d_chunk_first, int32_t n_tensors, int64_t n_chunks,
-                   const adana_step_scalars *h_scalars, int32_t n_classes,
-                   uint32_t variant_flags, float *d_partials, float *d_diag,
-                   void *stream);
+int adana_mta_step(const adana_plan *plan, const adana_step_scalars *h_scalars,
+                   int32_t n_classes, uint32_t variant_flags, void *d_workspace,
+                   size_t workspace_bytes, float *d_diag, void *stream);
 
 #ifdef __cplusplus
 }

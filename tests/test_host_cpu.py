@@ -102,31 +102,44 @@ def test_plan_layout_properties():
     from adana_amd import _lib
 
     rng = np.random.default_rng(0)
-    numels = np.concatenate([rng.integers(0, 70000, 300), [0, 1, 3, 4, 5, 16384, 16385]])
-    vstart, chunks = _lib.plan_layout(numels)
+    numels = np.concatenate([rng.integers(0, 70000, 300), [0, 1, 3, 4, 5, 16384, 16385],
+                             [5_000_000, 0, 7]])
+    vstart, fold_first, chunks, n_folds = _lib.plan_layout(numels)
+    C = _lib.CHUNK_ELEMS
     assert vstart[0] == 0
     assert np.all(vstart % _lib.ALIGN_ELEMS == 0)
     pad = vstart[1:] - vstart[:-1]
     assert np.all(pad >= numels) and np.all(pad - numels < _lib.ALIGN_ELEMS)
-    assert chunks == math.ceil(vstart[-1] / _lib.CHUNK_ELEMS)
+    assert chunks == math.ceil(vstart[-1] / C)
     # (chunk, tensor) segment slots chunk + tensor are distinct
     slots = set()
     for i, (vs, n) in enumerate(zip(vstart[:-1], numels)):
         if n == 0:
             continue
-        for b in range(vs // _lib.CHUNK_ELEMS, (vs + n - 1) // _lib.CHUNK_ELEMS + 1):
+        for b in range(vs // C, (vs + n - 1) // C + 1):
             assert b + i not in slots
             slots.add(b + i)
-    assert max(slots) < _lib.partials_floats(len(numels), chunks) // 4
-    assert _lib.plan_layout(np.zeros(0, np.int64))[1] == 0
+    assert max(slots) < chunks + len(numels)
+    # fold workgroups: ceil(chunks of tensor / FOLD_CHUNKS) per non-empty tensor
+    for i, (vs, n) in enumerate(zip(vstart[:-1], numels)):
+        nch = 0 if n == 0 else (vs + n - 1) // C - vs // C + 1
+        assert fold_first[i + 1] - fold_first[i] == math.ceil(nch / _lib.FOLD_CHUNKS)
+    assert fold_first[-1] == n_folds
+    assert _lib.plan_layout(np.zeros(0, np.int64))[2] == 0
     # the chunk -> first tensor rule the device index kernel applies
-    first = np.searchsorted(vstart[:-1], np.arange(chunks) * _lib.CHUNK_ELEMS, side="right") - 1
-    for c in range(chunks):
+    first = np.searchsorted(vstart[:-1], np.arange(chunks) * C, side="right") - 1
+    for c in range(0, chunks, 7):
         i = first[c]
-        lo = c * _lib.CHUNK_ELEMS
+        lo = c * C
         assert vstart[i] <= lo
-        # no earlier tensor has elements at or after lo
-        assert all(vstart[k] + numels[k] <= lo for k in range(i))
+        assert all(vstart[k] + numels[k] <= lo for k in range(max(0, i - 50), i))
+
+
+def test_workspace_bytes():
+    from adana_amd import _lib
+
+    pl = _lib.Plan(n_tensors=10, n_chunks=100, n_folds=12)
+    assert _lib.workspace_bytes(pl) == (110 * 16 + 255) // 256 * 256 + 12 * 32
 
 
 def test_mta_step_rejects_bad_arguments():
@@ -134,15 +147,25 @@ def test_mta_step_rejects_bad_arguments():
 
     L = _lib.lib()
     sc = (_lib.StepScalars * 1)()
-    rc = L.adana_mta_step(None, None, None, -1, 0, ctypes.cast(sc, ctypes.c_void_p), 1, 0, None,
-                          None, None)
-    assert rc == -1 and "bad sizes" in _lib.last_error()
-    rc = L.adana_mta_step(None, None, None, 3, 1, ctypes.cast(sc, ctypes.c_void_p), 1, 0, None,
-                          None, None)
-    assert rc == -1 and "null pointer" in _lib.last_error()
-    rc = L.adana_mta_step(None, None, None, 0, 0, None, 0, 0x80, None, None, None)
-    assert rc == -1 and "variant flags" in _lib.last_error()
-    assert L.adana_mta_step(None, None, None, 0, 0, None, 0, 0, None, None, None) == 0
+    scp = ctypes.cast(sc, ctypes.c_void_p)
+    assert L.adana_mta_step(None, scp, 1, 0, None, 0, None, None) == -1
+    assert "null plan" in _lib.last_error()
+    pl = _lib.Plan(n_tensors=-1)
+    assert L.adana_mta_step(ctypes.byref(pl), scp, 1, 0, None, 0, None, None) == -1
+    assert "bad sizes" in _lib.last_error()
+    pl = _lib.Plan(n_tensors=3, n_chunks=1, n_folds=3)
+    assert L.adana_mta_step(ctypes.byref(pl), scp, 1, 0, None, 0, None, None) == -1
+    assert "null pointer" in _lib.last_error()
+    assert L.adana_mta_step(ctypes.byref(pl), scp, 1, 0x80, None, 0, None, None) == -1
+    assert "variant flags" in _lib.last_error()
+    fake = ctypes.c_void_p(0x1000)
+    pl = _lib.Plan(desc=0x1000, vstart=0x1000, chunk_first=0x1000, fold_first=0x1000,
+                   n_tensors=3, n_chunks=1, n_folds=3)
+    assert L.adana_mta_step(ctypes.byref(pl), scp, 0, 0, fake, 1 << 20, fake, None) == -1
+    assert "n_classes" in _lib.last_error()
+    assert L.adana_mta_step(ctypes.byref(pl), scp, 1, 0, fake, 16, fake, None) == -1
+    assert "workspace" in _lib.last_error()
+    assert L.adana_mta_step(ctypes.byref(_lib.Plan()), None, 0, 0, None, 0, None, None) == 0
     assert L.adana_plan_index(None, 0, 0, None, None) == 0
     assert L.adana_plan_index(None, 3, 5, None, None) == -1
 
