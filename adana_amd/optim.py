@@ -27,6 +27,8 @@ written as RNE(master) in the same pass.
 from __future__ import annotations
 
 import ctypes
+import itertools
+import operator
 from typing import Iterable, List, Optional
 
 import numpy as np
@@ -37,6 +39,8 @@ from . import _lib
 
 DIAG_KEYS = ("current_alpha", "gradient_norm", "auto_factor_mean",
              "current_kappa_factor", "m_norm")
+_GRAD = operator.attrgetter("grad")
+_DATA_PTR = torch.Tensor.data_ptr
 
 
 class _LaunchSet:
@@ -74,6 +78,8 @@ class _DanaFamily(Optimizer):
         self.master_weights = bool(master_weights)
         self._sets: Optional[List[_LaunchSet]] = None
         self._structure = None
+        self._flat = None
+        self._active = None
         _lib.lib()  # fail at construction, not at the first step, without the kernel library
 
     # -- state ------------------------------------------------------------
@@ -92,10 +98,13 @@ class _DanaFamily(Optimizer):
                 state["tau"] = torch.zeros_like(p)      # src/optim/dana_star_mk4.py:255
 
     def invalidate_plan(self) -> None:
-        """Forget cached device tables (call after swapping state tensors or
-        parameter storage by hand)."""
+        """Forget cached device tables and tensor lists (call after swapping
+        state tensors or parameter storage, or editing a group's parameter
+        list in place)."""
         self._sets = None
         self._structure = None
+        self._flat = None
+        self._active = None
 
     def load_state_dict(self, state_dict) -> None:
         super().load_state_dict(state_dict)
@@ -235,6 +244,27 @@ class _DanaFamily(Optimizer):
         hp.wd_decaying = 1 if self.wd_decaying else 0
         return hp
 
+    def _flat_params(self):
+        """All parameters in group order, with their group index (cached)."""
+        sig = tuple((id(g["params"]), len(g["params"])) for g in self.param_groups)
+        if self._flat is None or self._flat[0] != sig:
+            params, gidx = [], []
+            for gi, group in enumerate(self.param_groups):
+                params.extend(group["params"])
+                gidx.extend([gi] * len(group["params"]))
+            self._flat = (sig, params, gidx)
+            self._active = None
+        return self._flat[1], self._flat[2]
+
+    def _scalars(self, classes):
+        hps, out = {}, []
+        for gi, t in classes:
+            hp = hps.get(gi)
+            if hp is None:
+                hp = hps[gi] = self._hparams(self.param_groups[gi])
+            out.append(_lib.step_scalars(hp, self.param_groups[gi]["lr"], t))
+        return out
+
     @torch.no_grad()
     def step(self, closure=None):
         loss = None
@@ -242,62 +272,67 @@ class _DanaFamily(Optimizer):
             with torch.enable_grad():
                 loss = closure()
 
-        params, grads, states, keys = [], [], [], []
-        for gi, group in enumerate(self.param_groups):
+        for group in self.param_groups:
             # src/optim/adana.py:163-167: g2 = g3 = lr, sf = lr / self.lr
             group["weighted_step_count"] += group["lr"] / self.lr
-            for p in group["params"]:
-                g = p.grad
-                if g is None:                          # adana.py:186
+        all_params, gidx = self._flat_params()
+        all_grads = list(map(_GRAD, all_params))
+        absent = tuple(map(operator.is_, all_grads, itertools.repeat(None)))   # adana.py:186
+
+        act = self._active
+        if self._sets is not None and act is not None and act["absent"] == absent:
+            # Steady state: the same tensors have gradients as at the last step, so
+            # every active tensor advances by one and the scalar classes carry over.
+            grads = all_grads if act["all"] else [all_grads[i] for i in act["index"]]
+            for st in act["states"]:
+                st["step"] += 1                                              # adana.py:197
+            classes = act["classes"] = [(gi, t + 1) for gi, t in act["classes"]]
+            params = act["params"]
+            for ls in self._sets:
+                new = grads if len(self._sets) == 1 else [grads[i] for i in ls.index]
+                if not all(map(operator.is_, new, ls.grads)):
+                    ls.grads = new
+                    self._refresh_grads(ls)
+        else:
+            params, grads, states, keys, index = [], [], [], [], []
+            for i, (p, g) in enumerate(zip(all_params, all_grads)):
+                if g is None:                                                # adana.py:186
                     continue
                 st = self.state[p]
-                if len(st) == 0:                       # adana.py:191-195
+                if len(st) == 0:                                             # adana.py:191-195
                     self._init_state(p, st)
-                st["step"] += 1                        # adana.py:197
+                st["step"] += 1                                              # adana.py:197
                 params.append(p)
                 grads.append(g)
                 states.append(st)
-                keys.append((gi, st["step"]))
-        if not params:
-            return loss
+                keys.append((gidx[i], st["step"]))
+                index.append(i)
+            if not params:
+                self._active = None
+                return loss
+            # (group, step) scalar classes
+            cls_index = {}
+            sclass = []
+            for k in keys:
+                c = cls_index.get(k)
+                if c is None:
+                    c = cls_index[k] = len(cls_index)
+                sclass.append(c)
+            classes = list(cls_index)
+            structure = (tuple(map(id, params)), tuple(sclass))
+            if self._sets is None or structure != self._structure:
+                flags = [self._validate(p, g) for p, g in zip(params, grads)]
+                self._sets = self._build(params, grads, states, sclass, flags)
+                self._structure = structure
+            else:
+                for ls in self._sets:
+                    ls.grads = grads if len(self._sets) == 1 else [grads[i] for i in ls.index]
+                    self._refresh_grads(ls)
+            self._active = {"absent": absent, "all": len(index) == len(all_params),
+                            "index": index, "states": states, "params": params,
+                            "classes": classes}
 
-        # (group, step) scalar classes
-        cls_index = {}
-        sclass = []
-        for k in keys:
-            c = cls_index.get(k)
-            if c is None:
-                c = cls_index[k] = len(cls_index)
-            sclass.append(c)
-        classes = list(cls_index)
-        scalars = []
-        hps = {}
-        for gi, t in classes:
-            hp = hps.get(gi)
-            if hp is None:
-                hp = hps[gi] = self._hparams(self.param_groups[gi])
-            scalars.append(_lib.step_scalars(hp, self.param_groups[gi]["lr"], t))
-
-        structure = (tuple(map(id, params)), tuple(sclass))
-        if self._sets is None or structure != self._structure:
-            flags = [self._validate(p, g) for p, g in zip(params, grads)]
-            self._sets = self._build(params, grads, states, sclass, flags)
-            self._structure = structure
-        else:
-            # same tensors and classes: refresh gradient pointers if they moved
-            for ls in self._sets:
-                ls.grads = grads if len(self._sets) == 1 else [grads[i] for i in ls.index]
-                gptr = np.fromiter((g.data_ptr() for g in ls.grads), dtype=np.uint64,
-                                   count=len(ls.grads))
-                if not np.array_equal(gptr, ls.ptr_key):
-                    for p, g in zip(ls.params, ls.grads):
-                        if self._validate(p, g) != ls.flags:
-                            raise RuntimeError(f"{type(self).__name__}: gradient dtype changed")
-                    ls.host_desc = self._desc_rows(ls)
-                    ls.ptr_key = ls.host_desc["grad"].copy()
-                    with torch.cuda.device(ls.device):
-                        self._upload(ls)
-
+        scalars = self._scalars(classes)
         L = _lib.lib()
         for ls in self._sets:
             n_cls = min(_lib.MAX_CLASSES, len(classes) - ls.class_base)
@@ -310,6 +345,20 @@ class _DanaFamily(Optimizer):
                     ctypes.c_void_p(ls.diag.data_ptr()), ctypes.c_void_p(stream)), "adana_mta_step")
         torch._C._increment_version(params)
         return loss
+
+    def _refresh_grads(self, ls: _LaunchSet) -> None:
+        """Re-point the launch set's descriptors at this step's gradients (only
+        re-uploaded when an address moved)."""
+        gptr = np.fromiter(map(_DATA_PTR, ls.grads), dtype=np.uint64, count=len(ls.grads))
+        if np.array_equal(gptr, ls.ptr_key):
+            return
+        for p, g in zip(ls.params, ls.grads):
+            if self._validate(p, g) != ls.flags:
+                raise RuntimeError(f"{type(self).__name__}: gradient dtype changed")
+        ls.host_desc = self._desc_rows(ls)
+        ls.ptr_key = ls.host_desc["grad"].copy()
+        with torch.cuda.device(ls.device):
+            self._upload(ls)
 
 
 class ADana(_DanaFamily):
