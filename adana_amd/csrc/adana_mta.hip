@@ -28,6 +28,7 @@
 #include <cstring>
 
 #include "adana_mta.h"
+#include "adana_fastmath.h"
 #include "adana_pow.h"
 
 namespace {
@@ -154,7 +155,8 @@ __device__ __forceinline__ StarMid star_phase_a(float g, float m, float v, float
     const float tu = ag / (ag + o.se);                           // :148
     o.tau = lerp_aten(tau, tu, sc);                              // :149
     const float ct = clamp_max(o.tau, 0.5f);                     // :152
-    const float pe = ct / (1.0f - ct);                           // :153
+    // ct in [0, 0.5]: 1 - ct is in [0.5, 1], and exactly 1 when ct < 2^-25
+    const float pe = adana::div_core(ct, 1.0f - ct);                    // :153
     o.tr = sc.min_p + relu_f(pe - sc.min_p);                     // :154-156
     o.et = clamp_min(o.tau * sc.s, 1.0f);                        // :159
     return o;
@@ -163,7 +165,8 @@ __device__ __forceinline__ StarMid star_phase_a(float g, float m, float v, float
 // src/optim/dana_star_mk4.py:163-195, given pw = effective_time ** (1 - kappa)
 __device__ __forceinline__ float star_phase_b(float p, float g, const StarMid &a, float pw,
                                               const adana_step_scalars &sc, float (&acc)[4]) {
-    const float nt = sqrtf(a.tr) / a.se;                         // :163-164
+    // tau_reg >= 1/(1+t) >= 2^-24 (t < 2^24): far above sqrt's scaling range
+    const float nt = adana::sqrt_normal(a.tr) / a.se;                   // :163-164
     const float mnt = fabsf(a.m) * nt;                           // :165
     const float mfac = mnt / a.tr;                               // :167
     float af = pw * mfac;                                        // :170 / :174

@@ -50,6 +50,20 @@ ADANA_HD inline To bits_as(From v) {
     return o;
 }
 
+// fma(a, b, c) with c a wave-uniform constant: on the GPU, v_fma_f64 reading
+// c from an SGPR pair.  (Left to itself the compiler copies each 64-bit
+// polynomial coefficient into a VGPR pair for the accumulator form -- two VALU
+// moves per Horner step.)  The same IEEE fused multiply-add either way.
+#if defined(__HIP_DEVICE_COMPILE__)
+__device__ __forceinline__ double fma_uc(double a, double b, double c) {
+    double d;
+    asm("v_fma_f64 %0, %1, %2, %3" : "=v"(d) : "v"(a), "v"(b), "s"(c));
+    return d;
+}
+#else
+inline double fma_uc(double a, double b, double c) { return std::fma(a, b, c); }
+#endif
+
 // binary64 x ** y for 1 <= x < 3e38 (finite).  Writes t = y * ln x.
 ADANA_HD inline double pow_core_f64(float x, float y, double &t_out) {
     const uint32_t xb = bits_as<uint32_t>(x);
@@ -59,11 +73,11 @@ ADANA_HD inline double pow_core_f64(float x, float y, double &t_out) {
     const double r = std::fma(m, kLogInvC[j], -1.0);
     // log1p(r) = r + r^2 * (-1/2 + r/3 - r^2/4 + r^3/5 - r^4/6 + r^5/7)
     double q = 1.0 / 7.0;
-    q = std::fma(q, r, -1.0 / 6.0);
-    q = std::fma(q, r, 1.0 / 5.0);
-    q = std::fma(q, r, -1.0 / 4.0);
-    q = std::fma(q, r, 1.0 / 3.0);
-    q = std::fma(q, r, -0.5);
+    q = fma_uc(q, r, -1.0 / 6.0);
+    q = fma_uc(q, r, 1.0 / 5.0);
+    q = fma_uc(q, r, -1.0 / 4.0);
+    q = fma_uc(q, r, 1.0 / 3.0);
+    q = fma_uc(q, r, -0.5);
     const double lp = std::fma(r * r, q, r);
     // ln 2 split so that e * LN2_HI and k * LN2_HI / 128 are exact
     const double LN2_HI = 6.93147180369123816490e-01;
@@ -76,9 +90,9 @@ ADANA_HD inline double pow_core_f64(float x, float y, double &t_out) {
     double rr = std::fma(-kd, LN2_HI / 128.0, t);
     rr = std::fma(-kd, LN2_LO / 128.0, rr);
     double p = 1.0 / 120.0;
-    p = std::fma(p, rr, 1.0 / 24.0);
-    p = std::fma(p, rr, 1.0 / 6.0);
-    p = std::fma(p, rr, 0.5);
+    p = fma_uc(p, rr, 1.0 / 24.0);
+    p = fma_uc(p, rr, 1.0 / 6.0);
+    p = fma_uc(p, rr, 0.5);
     p = std::fma(rr * rr, p, rr);                                // expm1(r')
     const int k = static_cast<int>(kd);
     const double tj = kExp2J[k & 127];
