@@ -8,6 +8,7 @@
 // Method (table-driven argument reduction, all arithmetic in binary64):
 //   x = 2^e * m, m in [1, 2);  j = top 7 bits of m's fraction
 //   r = m * invc[j] - 1 (exact: invc has 12 significant bits), |r| < 0.0043
+//   (invc[j] and -ln invc[j] sit side by side: one 16-byte table load)
 //   ln x = e*ln2 + (-ln invc[j]) + log1p(r),  log1p by its degree-7 series
 //   t = y * ln x;  k = rint(t * 128 / ln2);  r' = t - k * ln2/128 (|r'| < 0.0028)
 //   x^y = 2^(k >> 7) * 2^((k & 127) / 128) * (1 + expm1(r')), degree-5 series
@@ -70,7 +71,8 @@ ADANA_HD inline double pow_core_f64(float x, float y, double &t_out) {
     const int e = static_cast<int>(xb >> 23) - 127;
     const int j = static_cast<int>((xb >> 16) & 127u);
     const double m = static_cast<double>(bits_as<float>((xb & 0x007fffffu) | 0x3f800000u));
-    const double r = std::fma(m, kLogInvC[j], -1.0);
+    const LogPair c = kLog[j];
+    const double r = std::fma(m, c.inv_c, -1.0);
     // log1p(r) = r + r^2 * (-1/2 + r/3 - r^2/4 + r^3/5 - r^4/6 + r^5/7)
     double q = 1.0 / 7.0;
     q = fma_uc(q, r, -1.0 / 6.0);
@@ -83,7 +85,7 @@ ADANA_HD inline double pow_core_f64(float x, float y, double &t_out) {
     const double LN2_HI = 6.93147180369123816490e-01;
     const double LN2_LO = 1.90821492927058770002e-10;
     const double ed = static_cast<double>(e);
-    const double lnx = std::fma(ed, LN2_HI, kLogNegLnC[j]) + std::fma(ed, LN2_LO, lp);
+    const double lnx = std::fma(ed, LN2_HI, c.neg_log) + std::fma(ed, LN2_LO, lp);
     const double t = static_cast<double>(y) * lnx;
     // e^t = 2^(k/128) e^r'
     const double kd = std::rint(t * 184.66496523378731);        // 128 / ln 2
@@ -117,16 +119,19 @@ ADANA_HD inline float pow_f32_slow(float x, float y) {
 }
 
 // x ** y for an exponent 0 < y < 1 and x >= 1 (NaN and +inf pass through,
-// as pow gives them for such y).  No slow path: for 0 < y < 1, x ** y is
+// as pow gives them for such y).  Branch-free: the core runs on every x (its
+// table indices are 7-bit fields of x's bits, in range for any x) and the
+// result is selected afterwards, so a thread's pows can overlap their table
+// loads.  No slow path: for 0 < y < 1, x ** y is
 // never exactly a binary32 half-way point (x^p = M^q would need a 25-bit odd
 // M with M^q, q > p, fitting x's 24 bits), so fp32(core) differs from the
 // correctly rounded result only when x ** y lies within the core's error
 // (~2^-51 relative) of a half-way point -- measured 1 in 2e8 inputs against
 // the C library's pow (tests/pow_harness.cpp).
 ADANA_HD inline float pow_f32_unit_exp(float x, float y) {
-    if (!(x < 3.0e38f)) return x;
     double t;
-    return static_cast<float>(pow_core_f64(x, y, t));
+    const float r = static_cast<float>(pow_core_f64(x, y, t));
+    return (x < 3.0e38f) ? r : x;
 }
 
 // Any exponent: the core, and the slow path next to rounding boundaries and
