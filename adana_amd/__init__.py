@@ -6,6 +6,7 @@ src/optim/dana_star_mk4.py whose step() runs one hand-written gfx950 HIP
 multi-tensor kernel (adana_amd/csrc/adana_mta.hip) through the C ABI in
 include/adana_mta.h.
 """
+from .clip import clip_grad_norm_
 from .optim import ADana, DANA_STAR_MK4, DIAG_KEYS
 
-__all__ = ["ADana", "DANA_STAR_MK4", "DIAG_KEYS"]
+__all__ = ["ADana", "DANA_STAR_MK4", "DIAG_KEYS", "clip_grad_norm_"]

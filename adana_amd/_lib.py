@@ -16,7 +16,7 @@ import numpy as np
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libadana_mta.so")
 
-ABI_VERSION = 1
+ABI_VERSION = 2
 CHUNK_ELEMS = 1024
 ALIGN_ELEMS = 4
 MAX_CLASSES = 8
@@ -25,6 +25,7 @@ FOLD_CHUNKS = 2048
 VARIANT_STAR = 0x1
 GRAD_BF16 = 0x2
 PARAM_BF16 = 0x4
+WRITE_GRAD = 0x8
 DESC_VEC_OK = 0x1
 
 # adana_tensor_desc as a numpy record (64 bytes, same field order).
@@ -77,6 +78,7 @@ class Plan(ctypes.Structure):
 EXPORTS = (
     "adana_abi_version", "adana_last_error", "adana_step_scalars_init",
     "adana_plan_layout", "adana_plan_index", "adana_workspace_bytes", "adana_mta_step",
+    "adana_mta_step_scaled", "adana_grad_clip_norm", "adana_grad_scale",
 )
 
 _lib = None
@@ -104,6 +106,13 @@ def _declare(L) -> None:
     L.adana_workspace_bytes.restype = ctypes.c_size_t
     L.adana_mta_step.argtypes = [ctypes.POINTER(Plan), P, i32, u32, P, ctypes.c_size_t, P, P]
     L.adana_mta_step.restype = ctypes.c_int
+    L.adana_mta_step_scaled.argtypes = [ctypes.POINTER(Plan), P, i32, u32, P, P, ctypes.c_size_t, P, P]
+    L.adana_mta_step_scaled.restype = ctypes.c_int
+    L.adana_grad_clip_norm.argtypes = [ctypes.POINTER(Plan), u32, ctypes.c_double, P, ctypes.c_size_t,
+                                       P, P, P]
+    L.adana_grad_clip_norm.restype = ctypes.c_int
+    L.adana_grad_scale.argtypes = [ctypes.POINTER(Plan), u32, P, P]
+    L.adana_grad_scale.restype = ctypes.c_int
 
 
 def _hip_runtimes_mapped():

@@ -53,6 +53,9 @@ static_assert(sizeof(adana_step_scalars) == 64, "scalar layout");
 
 struct ScalarPack {
     adana_step_scalars c[ADANA_MAX_CLASSES];
+    const float *gscale;  // device pointer to the clip coefficient, or NULL
+    int32_t write_grad;   // store the scaled gradient back (ADANA_WRITE_GRAD)
+    int32_t reserved;
 };
 
 // ---------------------------------------------------------------------------
@@ -75,6 +78,16 @@ __device__ __forceinline__ unsigned short f32_to_bf16(float f) {
     if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<unsigned short>((u >> 16) | 0x40u);
     u += 0x7fffu + ((u >> 16) & 1u);
     return static_cast<unsigned short>(u >> 16);
+}
+__device__ __forceinline__ float bf16_round(float f) { return bf16_to_f32(f32_to_bf16(f)); }
+
+// clip_grad_norm_'s in-place product (torch/nn/utils/clip_grad.py,
+// _clip_grads_with_norm_: torch._foreach_mul_(grads, clip_coef_clamped)):
+// g * coef in binary32, rounded to bfloat16 for bfloat16 gradients.
+template <bool GBF16>
+__device__ __forceinline__ float scale_grad(float g, float s) {
+    const float x = g * s;
+    return GBF16 ? bf16_round(x) : x;
 }
 
 // x ** e with ATen's exponent specialisations (pow(Tensor, Scalar)).  POWK
@@ -292,6 +305,18 @@ __device__ __forceinline__ float load_grad1(const void *g, int64_t off) {
     if constexpr (GBF16) return bf16_to_f32(static_cast<const unsigned short *>(g)[off]);
     else return static_cast<const float *>(g)[off];
 }
+// Gradient write-back (only with ADANA_WRITE_GRAD: the caller's gradient
+// buffers are writable then).
+template <bool GBF16, int N>
+__device__ __forceinline__ void store_grad_n(const void *g, int64_t off, const float (&x)[N]) {
+    if constexpr (GBF16) st_bf16_n<N>(const_cast<unsigned short *>(static_cast<const unsigned short *>(g)) + off, x);
+    else st_n<N>(const_cast<float *>(static_cast<const float *>(g)) + off, x);
+}
+template <bool GBF16>
+__device__ __forceinline__ void store_grad1(const void *g, int64_t off, float x) {
+    if constexpr (GBF16) const_cast<unsigned short *>(static_cast<const unsigned short *>(g))[off] = f32_to_bf16(x);
+    else const_cast<float *>(static_cast<const float *>(g))[off] = x;
+}
 
 // ---------------------------------------------------------------------------
 // Main multi-tensor kernel: one 1024-element chunk per workgroup, VEC
@@ -318,6 +343,8 @@ __global__ __launch_bounds__(kChunk / VEC) void mta_step_kernel(const adana_tens
     const int64_t lo = chunk * kChunk;
     const int64_t hi = lo + kChunk;
     const int64_t mine = lo + VEC * tid;   // virtual index of this thread's VEC elements
+    const bool scaled = pack.gscale != nullptr;                    // uniform
+    const float gs = scaled ? *pack.gscale : 1.0f;
 
     for (int i = chunk_first[chunk]; i < n; ++i) {
         const int64_t vs = vstart[i];
@@ -346,6 +373,11 @@ __global__ __launch_bounds__(kChunk / VEC) void mta_step_kernel(const adana_tens
 #pragma unroll
                     for (int k = 0; k < VEC; ++k) T[k] = 0.0f;
                 }
+                if (scaled) {
+#pragma unroll
+                    for (int k = 0; k < VEC; ++k) G[k] = scale_grad<GBF16>(G[k], gs);
+                    if (pack.write_grad) store_grad_n<GBF16, VEC>(d.grad, off, G);
+                }
                 update_n<STAR, POWK, VEC>(P, G, M, V, T, sc, acc);
                 st_n<VEC>(pp, P);
                 st_n<VEC>(mp, M);
@@ -356,8 +388,12 @@ __global__ __launch_bounds__(kChunk / VEC) void mta_step_kernel(const adana_tens
                 // unaligned tensor, or the last (< VEC) elements of a tensor
                 for (int e = 0; e < cnt; ++e) {
                     float mm = mp[e], vv = vp[e], tt = STAR ? tp[e] : 0.0f;
-                    const float o = update_elem<STAR, POWK>(pp[e], load_grad1<GBF16>(d.grad, off + e), mm, vv,
-                                                            tt, sc, acc);
+                    float g = load_grad1<GBF16>(d.grad, off + e);
+                    if (scaled) {
+                        g = scale_grad<GBF16>(g, gs);
+                        if (pack.write_grad) store_grad1<GBF16>(d.grad, off + e, g);
+                    }
+                    const float o = update_elem<STAR, POWK>(pp[e], g, mm, vv, tt, sc, acc);
                     pp[e] = o;
                     mp[e] = mm;
                     vp[e] = vv;
@@ -496,6 +532,219 @@ __global__ __launch_bounds__(kBlock) void finalize_kernel(const adana_tensor_des
         o[2] = afm;
         o[3] = ca / afm;                                  // current_alpha / auto_factor_mean
         o[4] = static_cast<float>(sqrt(s3));              // m.norm()
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Gradient-norm clipping: torch.nn.utils.clip_grad_norm_(params, max_norm)
+// as the reference's training loop calls it before every step
+// (src/optim/base.py:250-257, src/distributed/backend.py:33-35).  Torch runs
+// a per-tensor norm pass, a norm of the norms, and a read-modify-write pass
+// over every gradient.  Here: one read-only pass for the sums of squares, the
+// same two-stage combine as the diagnostics, and a one-workgroup finalize
+// that writes the total norm and the clip coefficient to device memory; the
+// optimizer kernel then multiplies by the coefficient as it loads the
+// gradient (or grad_scale_kernel does it in place for a caller without one).
+// ---------------------------------------------------------------------------
+
+// Sum of squares per (chunk, tensor) segment in binary64 (each square of a
+// binary32 value is exact in binary64), written to partials[chunk + tensor].x.
+// One workgroup covers kSumsqChunks consecutive chunks.  When they all lie in
+// one tensor with aligned vectors (every chunk of a large tensor but its
+// ends), each thread issues its kSumsqChunks 16-byte loads at once and the
+// per-chunk sums are reduced together; otherwise the chunks are walked one by
+// one, segment by segment.  Either way each chunk's partial is the same
+// fixed-order sum of its own elements.
+constexpr int kSumsqChunks = 4;
+
+template <bool GBF16>
+__device__ __forceinline__ void sumsq_chunk(const adana_tensor_desc *__restrict__ desc,
+                                              const int64_t *__restrict__ vstart, int first, int32_t n,
+                                              int64_t chunk, double2 *__restrict__ partials, double (*red)[kWaves]) {
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int64_t lo = chunk * kChunk, hi = lo + kChunk;
+    const int64_t mine = lo + 4 * tid;
+    for (int i = first; i < n; ++i) {
+        const int64_t vs = vstart[i];
+        if (vs >= hi) break;
+        const adana_tensor_desc d = desc[i];
+        const int64_t ve = vs + d.numel;
+        if (ve <= lo) continue;
+        double acc = 0.0;
+        if (mine >= vs && mine < ve) {
+            const int64_t off = mine - vs;
+            const int cnt = (ve - mine) < 4 ? static_cast<int>(ve - mine) : 4;
+            if (cnt == 4 && (d.flags & ADANA_DESC_VEC_OK)) {
+                float G[4];
+                load_grad_n<GBF16, 4>(d.grad, off, G);
+#pragma unroll
+                for (int k = 0; k < 4; ++k) acc += static_cast<double>(G[k]) * static_cast<double>(G[k]);
+            } else {
+                for (int e = 0; e < cnt; ++e) {
+                    const double g = load_grad1<GBF16>(d.grad, off + e);
+                    acc += g * g;
+                }
+            }
+        }
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) acc += __shfl_xor(acc, o, 64);
+        if (lane == 0) red[0][wave] = acc;
+        __syncthreads();
+        if (tid == 0) partials[chunk + i] = make_double2(((red[0][0] + red[0][1]) + red[0][2]) + red[0][3], 0.0);
+        __syncthreads();
+    }
+}
+
+template <bool GBF16>
+__global__ __launch_bounds__(kBlock) void grad_sumsq_kernel(const adana_tensor_desc *__restrict__ desc,
+                                                            const int64_t *__restrict__ vstart,
+                                                            const int32_t *__restrict__ chunk_first,
+                                                            int32_t n, int64_t n_chunks,
+                                                            double2 *__restrict__ partials) {
+    constexpr int K = kSumsqChunks;
+    __shared__ double red[K][kWaves];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int64_t c0 = static_cast<int64_t>(blockIdx.x) * K;
+    const int64_t nc = (n_chunks - c0) < K ? n_chunks - c0 : K;
+    const int i0 = chunk_first[c0];
+    const int64_t vs = vstart[i0];
+    const adana_tensor_desc d = desc[i0];
+    if (nc == K && vs <= c0 * kChunk && vs + d.numel >= (c0 + K) * kChunk && (d.flags & ADANA_DESC_VEC_OK)) {
+        const int64_t off0 = c0 * kChunk + 4 * tid - vs;
+        float G[K][4];
+#pragma unroll
+        for (int c = 0; c < K; ++c) load_grad_n<GBF16, 4>(d.grad, off0 + c * kChunk, G[c]);
+        double acc[K];
+#pragma unroll
+        for (int c = 0; c < K; ++c) {
+            acc[c] = 0.0;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) acc[c] += static_cast<double>(G[c][k]) * static_cast<double>(G[c][k]);
+        }
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) {
+#pragma unroll
+            for (int c = 0; c < K; ++c) acc[c] += __shfl_xor(acc[c], o, 64);
+        }
+        if (lane == 0) {
+#pragma unroll
+            for (int c = 0; c < K; ++c) red[c][wave] = acc[c];
+        }
+        __syncthreads();
+        if (tid < K)
+            partials[c0 + tid + i0] = make_double2(((red[tid][0] + red[tid][1]) + red[tid][2]) + red[tid][3], 0.0);
+        return;
+    }
+    for (int c = 0; c < nc; ++c) sumsq_chunk<GBF16>(desc, vstart, chunk_first[c0 + c], n, c0 + c, partials, red);
+}
+
+// Stage 1 of the norm combine: like fold_kernel, for one binary64 sum.
+__global__ __launch_bounds__(kBlock) void sumsq_fold_kernel(const adana_tensor_desc *__restrict__ desc,
+                                                            const int64_t *__restrict__ vstart,
+                                                            const int32_t *__restrict__ fold_first, int32_t n,
+                                                            const double2 *__restrict__ partials,
+                                                            double *__restrict__ folds) {
+    __shared__ double red[kWaves];
+    const int64_t j = blockIdx.x;
+    int l = 0, r = n - 1;
+    while (l < r) {
+        const int mid = (l + r + 1) >> 1;
+        if (fold_first[mid] <= j) l = mid; else r = mid - 1;
+    }
+    const int i = l;
+    const int64_t vs = vstart[i], numel = desc[i].numel;
+    const int64_t b0 = vs / kChunk, b1 = (vs + numel - 1) / kChunk;
+    const int64_t lo = b0 + (j - fold_first[i]) * kFold;
+    const int64_t hi = (lo + kFold - 1 < b1) ? lo + kFold - 1 : b1;
+    double s = 0.0;
+#pragma unroll
+    for (int u = 0; u < kFoldPerThread; ++u) {
+        const int64_t b = lo + u * kBlock + threadIdx.x;
+        if (b <= hi) s += partials[b + i].x;
+    }
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o, 64);
+    if (lane == 0) red[wave] = s;
+    __syncthreads();
+    if (threadIdx.x == 0) folds[j] = ((red[0] + red[1]) + red[2]) + red[3];
+}
+
+// Stage 2, one workgroup: per-tensor norms (torch._foreach_norm, in the
+// gradient's dtype), the norm of the norms (torch.linalg.vector_norm of their
+// stack) and the clip coefficient, in torch's order and dtype:
+//   clip_coef = reciprocal(total + 1e-6) * max_norm   (float / Tensor is
+//               Tensor.__rtruediv__ = reciprocal() * other)
+//   clip_coef_clamped = clamp(clip_coef, max=1.0)     (NaN stays NaN)
+// Each op rounds to the gradient dtype (bfloat16 gradients give bfloat16
+// norms and coefficient).  clip[0] = total norm, clip[1] = coefficient.
+constexpr int kClipThreads = 1024;
+template <bool GBF16>
+__global__ __launch_bounds__(kClipThreads) void clip_finalize_kernel(const int32_t *__restrict__ fold_first,
+                                                                     int32_t n, const double *__restrict__ folds,
+                                                                     float max_norm, float *__restrict__ norms,
+                                                                     float *__restrict__ clip) {
+    __shared__ double red[kClipThreads / 64];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    double tot = 0.0;
+    for (int i = tid; i < n; i += kClipThreads) {
+        double s = 0.0;
+        for (int f = fold_first[i]; f < fold_first[i + 1]; ++f) s += folds[f];
+        float nrm = static_cast<float>(sqrt(s));
+        if (GBF16) nrm = bf16_round(nrm);
+        if (norms) norms[i] = nrm;
+        tot += static_cast<double>(nrm) * static_cast<double>(nrm);
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) tot += __shfl_xor(tot, o, 64);
+    if (lane == 0) red[wave] = tot;
+    __syncthreads();
+    if (tid == 0) {
+        double t = 0.0;
+        for (int w = 0; w < kClipThreads / 64; ++w) t += red[w];
+        float total = static_cast<float>(sqrt(t));
+        if (GBF16) total = bf16_round(total);
+        float den = total + 1e-6f;
+        if (GBF16) den = bf16_round(den);
+        float rc = 1.0f / den;
+        if (GBF16) rc = bf16_round(rc);
+        float coef = rc * max_norm;
+        if (GBF16) coef = bf16_round(coef);
+        coef = coef > 1.0f ? 1.0f : coef;
+        clip[0] = total;
+        clip[1] = coef;
+    }
+}
+
+// In-place g *= coef over a gradient list (clip_grad_norm_ without a fused
+// optimizer step).
+template <bool GBF16>
+__global__ __launch_bounds__(kBlock) void grad_scale_kernel(const adana_tensor_desc *__restrict__ desc,
+                                                            const int64_t *__restrict__ vstart,
+                                                            const int32_t *__restrict__ chunk_first,
+                                                            int32_t n, const float *__restrict__ scale) {
+    const int64_t chunk = blockIdx.x;
+    const int64_t lo = chunk * kChunk, hi = lo + kChunk;
+    const int64_t mine = lo + 4 * threadIdx.x;
+    const float s = *scale;
+    for (int i = chunk_first[chunk]; i < n; ++i) {
+        const int64_t vs = vstart[i];
+        if (vs >= hi) break;
+        const adana_tensor_desc d = desc[i];
+        const int64_t ve = vs + d.numel;
+        if (ve <= lo || mine < vs || mine >= ve) continue;
+        const int64_t off = mine - vs;
+        const int cnt = (ve - mine) < 4 ? static_cast<int>(ve - mine) : 4;
+        if (cnt == 4 && (d.flags & ADANA_DESC_VEC_OK)) {
+            float G[4];
+            load_grad_n<GBF16, 4>(d.grad, off, G);
+#pragma unroll
+            for (int k = 0; k < 4; ++k) G[k] = scale_grad<GBF16>(G[k], s);
+            store_grad_n<GBF16, 4>(d.grad, off, G);
+        } else {
+            for (int e = 0; e < cnt; ++e)
+                store_grad1<GBF16>(d.grad, off + e, scale_grad<GBF16>(load_grad1<GBF16>(d.grad, off + e), s));
+        }
     }
 }
 
@@ -664,30 +913,56 @@ size_t adana_workspace_bytes(const adana_plan *plan) {
     return plan ? workspace_bytes(*plan) : 0;
 }
 
-int adana_mta_step(const adana_plan *plan, const adana_step_scalars *h_scalars, int32_t n_classes,
-                   uint32_t variant_flags, void *d_workspace, size_t ws_bytes, float *d_diag,
-                   void *stream) {
-    if (!plan) return set_err(ADANA_E_INVALID, "adana_mta_step: null plan");
+}  // extern "C"
+
+namespace {
+
+// Plan checks shared by the entry points; return ADANA_OK or an error code.
+int check_plan(const adana_plan *plan, const char *fn) {
+    if (!plan) return set_err(ADANA_E_INVALID, "%s: null plan", fn);
     const adana_plan &pl = *plan;
     if (pl.n_tensors < 0 || pl.n_chunks < 0 || pl.n_chunks > 0x7fffffffLL || pl.n_folds < 0 ||
         pl.n_folds > 0x7fffffffLL)
-        return set_err(ADANA_E_INVALID, "adana_mta_step: bad sizes (n_tensors=%d, n_chunks=%lld)",
-                       pl.n_tensors, static_cast<long long>(pl.n_chunks));
-    if (variant_flags & ~(ADANA_VARIANT_STAR | ADANA_GRAD_BF16 | ADANA_PARAM_BF16))
-        return set_err(ADANA_E_INVALID, "adana_mta_step: unknown variant flags 0x%x", variant_flags);
+        return set_err(ADANA_E_INVALID, "%s: bad sizes (n_tensors=%d, n_chunks=%lld)", fn, pl.n_tensors,
+                       static_cast<long long>(pl.n_chunks));
+    return ADANA_OK;
+}
+int check_plan_arrays(const adana_plan &pl, const char *fn) {
+    if (pl.n_tensors > 0 && (!pl.desc || !pl.vstart || !pl.fold_first || (pl.n_chunks > 0 && !pl.chunk_first)))
+        return set_err(ADANA_E_INVALID, "%s: null pointer in the plan arrays", fn);
+    return ADANA_OK;
+}
+
+int launch_status(const char *fn, const char *what) {
+    hipError_t err = hipGetLastError();
+    if (err != hipSuccess)
+        return set_err(ADANA_E_HIP, "%s: %s launch failed: %s", fn, what, hipGetErrorString(err));
+    return ADANA_OK;
+}
+
+int step_impl(const char *fn, const adana_plan *plan, const adana_step_scalars *h_scalars, int32_t n_classes,
+              uint32_t variant_flags, const float *d_grad_scale, void *d_workspace, size_t ws_bytes,
+              float *d_diag, void *stream) {
+    if (int rc = check_plan(plan, fn)) return rc;
+    const adana_plan &pl = *plan;
+    const uint32_t allowed = ADANA_VARIANT_STAR | ADANA_GRAD_BF16 | ADANA_PARAM_BF16 |
+                             (d_grad_scale ? ADANA_WRITE_GRAD : 0u);
+    if (variant_flags & ~allowed)
+        return set_err(ADANA_E_INVALID, "%s: unknown variant flags 0x%x", fn, variant_flags);
+    if (int rc = check_plan_arrays(pl, fn)) return rc;
     if (pl.n_tensors == 0) return ADANA_OK;
-    if (!pl.desc || !pl.vstart || !pl.fold_first || !d_workspace || !d_diag || !h_scalars ||
-        (pl.n_chunks > 0 && !pl.chunk_first))
-        return set_err(ADANA_E_INVALID, "adana_mta_step: null pointer argument");
+    if (!d_workspace || !d_diag || !h_scalars)
+        return set_err(ADANA_E_INVALID, "%s: null pointer argument", fn);
     if (n_classes < 1 || n_classes > ADANA_MAX_CLASSES)
-        return set_err(ADANA_E_INVALID, "adana_mta_step: n_classes=%d outside [1, %d]", n_classes,
-                       ADANA_MAX_CLASSES);
+        return set_err(ADANA_E_INVALID, "%s: n_classes=%d outside [1, %d]", fn, n_classes, ADANA_MAX_CLASSES);
     if (ws_bytes < workspace_bytes(pl))
-        return set_err(ADANA_E_INVALID, "adana_mta_step: workspace of %zu bytes < %zu needed", ws_bytes,
+        return set_err(ADANA_E_INVALID, "%s: workspace of %zu bytes < %zu needed", fn, ws_bytes,
                        workspace_bytes(pl));
     ScalarPack pack;
     memset(&pack, 0, sizeof pack);
     memcpy(pack.c, h_scalars, sizeof(adana_step_scalars) * static_cast<size_t>(n_classes));
+    pack.gscale = d_grad_scale;
+    pack.write_grad = (variant_flags & ADANA_WRITE_GRAD) ? 1 : 0;
     hipStream_t st = static_cast<hipStream_t>(stream);
     float *partials = static_cast<float *>(d_workspace);
     double4 *folds = reinterpret_cast<double4 *>(static_cast<char *>(d_workspace) + folds_offset(pl));
@@ -714,23 +989,93 @@ int adana_mta_step(const adana_plan *plan, const adana_step_scalars *h_scalars, 
             else    { if (pb) ADANA_LAUNCH(false, false, true); else ADANA_LAUNCH(false, false, false); }
         }
 #undef ADANA_LAUNCH
-        hipError_t err = hipGetLastError();
-        if (err != hipSuccess)
-            return set_err(ADANA_E_HIP, "adana_mta_step: main launch failed: %s", hipGetErrorString(err));
+        if (int rc = launch_status(fn, "main")) return rc;
     }
     if (pl.n_folds > 0) {
         hipLaunchKernelGGL(fold_kernel, dim3(static_cast<unsigned>(pl.n_folds)), dim3(kBlock), 0, st,
                            pl.desc, pl.vstart, pl.fold_first, n, partials, folds);
-        hipError_t err = hipGetLastError();
-        if (err != hipSuccess)
-            return set_err(ADANA_E_HIP, "adana_mta_step: fold launch failed: %s", hipGetErrorString(err));
+        if (int rc = launch_status(fn, "fold")) return rc;
     }
     hipLaunchKernelGGL(finalize_kernel, dim3(static_cast<unsigned>((n + kWaves - 1) / kWaves)), dim3(kBlock),
                        0, st, pl.desc, pl.fold_first, n, folds, d_diag);
-    hipError_t err = hipGetLastError();
-    if (err != hipSuccess)
-        return set_err(ADANA_E_HIP, "adana_mta_step: finalize launch failed: %s", hipGetErrorString(err));
-    return ADANA_OK;
+    return launch_status(fn, "finalize");
+}
+
+}  // namespace
+
+extern "C" {
+
+int adana_mta_step(const adana_plan *plan, const adana_step_scalars *h_scalars, int32_t n_classes,
+                   uint32_t variant_flags, void *d_workspace, size_t ws_bytes, float *d_diag,
+                   void *stream) {
+    return step_impl("adana_mta_step", plan, h_scalars, n_classes, variant_flags, nullptr, d_workspace,
+                     ws_bytes, d_diag, stream);
+}
+
+int adana_mta_step_scaled(const adana_plan *plan, const adana_step_scalars *h_scalars, int32_t n_classes,
+                          uint32_t variant_flags, const float *d_grad_scale, void *d_workspace,
+                          size_t ws_bytes, float *d_diag, void *stream) {
+    if (!d_grad_scale) return set_err(ADANA_E_INVALID, "adana_mta_step_scaled: null gradient scale");
+    return step_impl("adana_mta_step_scaled", plan, h_scalars, n_classes, variant_flags, d_grad_scale,
+                     d_workspace, ws_bytes, d_diag, stream);
+}
+
+int adana_grad_clip_norm(const adana_plan *plan, uint32_t grad_flags, double max_norm, void *d_workspace,
+                         size_t ws_bytes, float *d_norms, float *d_clip, void *stream) {
+    const char *fn = "adana_grad_clip_norm";
+    if (int rc = check_plan(plan, fn)) return rc;
+    const adana_plan &pl = *plan;
+    if (grad_flags & ~ADANA_GRAD_BF16) return set_err(ADANA_E_INVALID, "%s: unknown flags 0x%x", fn, grad_flags);
+    if (int rc = check_plan_arrays(pl, fn)) return rc;
+    if (!d_clip) return set_err(ADANA_E_INVALID, "%s: null clip output", fn);
+    if (pl.n_tensors > 0 && !d_workspace) return set_err(ADANA_E_INVALID, "%s: null workspace", fn);
+    if (ws_bytes < workspace_bytes(pl))
+        return set_err(ADANA_E_INVALID, "%s: workspace of %zu bytes < %zu needed", fn, ws_bytes,
+                       workspace_bytes(pl));
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    const bool gb = grad_flags & ADANA_GRAD_BF16;
+    double2 *partials = static_cast<double2 *>(d_workspace);
+    double *folds = reinterpret_cast<double *>(static_cast<char *>(d_workspace) + folds_offset(pl));
+    const int32_t n = pl.n_tensors;
+    if (pl.n_chunks > 0) {
+        const dim3 grid(static_cast<unsigned>((pl.n_chunks + kSumsqChunks - 1) / kSumsqChunks));
+        if (gb) hipLaunchKernelGGL(grad_sumsq_kernel<true>, grid, dim3(kBlock), 0, st, pl.desc, pl.vstart,
+                                   pl.chunk_first, n, pl.n_chunks, partials);
+        else hipLaunchKernelGGL(grad_sumsq_kernel<false>, grid, dim3(kBlock), 0, st, pl.desc, pl.vstart,
+                                pl.chunk_first, n, pl.n_chunks, partials);
+        if (int rc = launch_status(fn, "sum of squares")) return rc;
+    }
+    if (pl.n_folds > 0) {
+        hipLaunchKernelGGL(sumsq_fold_kernel, dim3(static_cast<unsigned>(pl.n_folds)), dim3(kBlock), 0, st,
+                           pl.desc, pl.vstart, pl.fold_first, n, partials, folds);
+        if (int rc = launch_status(fn, "fold")) return rc;
+    }
+    // torch casts the Python float max_norm to the coefficient's binary32 opmath
+    const float mn = static_cast<float>(max_norm);
+    if (gb) hipLaunchKernelGGL(clip_finalize_kernel<true>, dim3(1), dim3(kClipThreads), 0, st, pl.fold_first, n,
+                               folds, mn, d_norms, d_clip);
+    else hipLaunchKernelGGL(clip_finalize_kernel<false>, dim3(1), dim3(kClipThreads), 0, st, pl.fold_first, n,
+                            folds, mn, d_norms, d_clip);
+    return launch_status(fn, "finalize");
+}
+
+int adana_grad_scale(const adana_plan *plan, uint32_t grad_flags, const float *d_scale, void *stream) {
+    const char *fn = "adana_grad_scale";
+    if (int rc = check_plan(plan, fn)) return rc;
+    const adana_plan &pl = *plan;
+    if (grad_flags & ~ADANA_GRAD_BF16) return set_err(ADANA_E_INVALID, "%s: unknown flags 0x%x", fn, grad_flags);
+    if (int rc = check_plan_arrays(pl, fn)) return rc;
+    if (!d_scale) return set_err(ADANA_E_INVALID, "%s: null scale", fn);
+    if (pl.n_tensors == 0 || pl.n_chunks == 0) return ADANA_OK;
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    const dim3 grid(static_cast<unsigned>(pl.n_chunks));
+    if (grad_flags & ADANA_GRAD_BF16)
+        hipLaunchKernelGGL(grad_scale_kernel<true>, grid, dim3(kBlock), 0, st, pl.desc, pl.vstart, pl.chunk_first,
+                           pl.n_tensors, d_scale);
+    else
+        hipLaunchKernelGGL(grad_scale_kernel<false>, grid, dim3(kBlock), 0, st, pl.desc, pl.vstart, pl.chunk_first,
+                           pl.n_tensors, d_scale);
+    return launch_status(fn, "scale");
 }
 
 }  // extern "C"

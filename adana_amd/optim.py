@@ -19,6 +19,11 @@ the state are 0-d views of that buffer: they hold the latest step's values
 (the reference rebinds new tensors each step; here the same tensors are
 refreshed in place).
 
+Gradient clipping (src/optim/base.py:250-257): ``opt.clip_grad_norm_(max_norm)``
+(or ``adana_amd.clip_grad_norm_(params, max_norm, optimizer=opt)``) returns
+torch.nn.utils.clip_grad_norm_'s total norm and folds the in-place scaling
+into the next ``step()`` (adana_amd/clip.py).
+
 Extension (no reference counterpart): ``master_weights=True`` lets bfloat16
 parameters keep a float32 master copy (state key ``'master'``) with float32
 m/v[/tau]; the update runs in float32 on the master and the bf16 parameter is
@@ -36,6 +41,7 @@ import torch
 from torch.optim import Optimizer
 
 from . import _lib
+from .clip import GradPlan, clip_grad_norm_ as _clip_grad_norm
 
 DIAG_KEYS = ("current_alpha", "gradient_norm", "auto_factor_mean",
              "current_kappa_factor", "m_norm")
@@ -80,6 +86,8 @@ class _DanaFamily(Optimizer):
         self._structure = None
         self._flat = None
         self._active = None
+        self._pending_clip = None
+        self._clip_plan_obj = None
         _lib.lib()  # fail at construction, not at the first step, without the kernel library
 
     # -- state ------------------------------------------------------------
@@ -121,6 +129,46 @@ class _DanaFamily(Optimizer):
                         if k in saved[pid]:
                             st[k] = saved[pid][k].to(device=p.device, dtype=torch.float32)
         self.invalidate_plan()
+
+    # -- gradient clipping -------------------------------------------------
+    def clip_grad_norm_(self, max_norm: float, norm_type: float = 2.0,
+                        error_if_nonfinite: bool = False, foreach: Optional[bool] = None, *,
+                        write_back: bool = True) -> torch.Tensor:
+        """torch.nn.utils.clip_grad_norm_ over this optimizer's parameters, with
+        the scaling fused into the next step() (adana_amd/clip.py)."""
+        params, _ = self._flat_params()
+        return _clip_grad_norm(params, max_norm, norm_type, error_if_nonfinite, foreach,
+                               optimizer=self, write_back=write_back)
+
+    def flush_clip(self) -> None:
+        """Apply a pending clip scaling to the gradients now (in place)."""
+        pend = self._pending_clip
+        if pend is not None:
+            self._pending_clip = None
+            pend[1].scale(pend[2])
+
+    def zero_grad(self, set_to_none: bool = True) -> None:
+        self._pending_clip = None          # the clipped gradients are being discarded
+        super().zero_grad(set_to_none=set_to_none)
+
+    def _clip_plan(self, device, bf16: bool) -> GradPlan:
+        plan = self._clip_plan_obj
+        if plan is None or plan.device != device or plan.bf16 != bf16:
+            plan = self._clip_plan_obj = GradPlan(device, bf16)
+        return plan
+
+    def _arm_clip(self, grads, plan, clip, write_back: bool) -> bool:
+        """Defer clip scaling to the next step() if ``grads`` are exactly the
+        gradients that step will consume; False leaves the scaling to the caller."""
+        params, _ = self._flat_params()
+        own = [g for g in map(_GRAD, params) if g is not None]
+        if len(own) != len(grads):
+            return False
+        ids = set(map(id, grads))
+        if not all(id(g) in ids for g in own):
+            return False
+        self._pending_clip = (own, plan, clip, bool(write_back))
+        return True
 
     # -- plan -------------------------------------------------------------
     def _validate(self, p: torch.Tensor, g: torch.Tensor) -> int:
@@ -332,6 +380,20 @@ class _DanaFamily(Optimizer):
                             "index": index, "states": states, "params": params,
                             "classes": classes}
 
+        # a clip armed by clip_grad_norm_(..., optimizer=self) on exactly these
+        # gradients is applied inside the kernel; otherwise it is applied now
+        gscale, wflag = None, 0
+        pend = self._pending_clip
+        if pend is not None:
+            own, _, clip, write_back = pend
+            if (len(own) == len(grads) and all(map(operator.is_, grads, own))
+                    and all(ls.device == clip.device for ls in self._sets)):
+                self._pending_clip = None
+                gscale = clip.data_ptr() + 4
+                wflag = _lib.WRITE_GRAD if write_back else 0
+            else:
+                self.flush_clip()
+
         scalars = self._scalars(classes)
         L = _lib.lib()
         for ls in self._sets:
@@ -339,11 +401,21 @@ class _DanaFamily(Optimizer):
             sc_arr = (_lib.StepScalars * n_cls)(*scalars[ls.class_base:ls.class_base + n_cls])
             with torch.cuda.device(ls.device):
                 stream = torch.cuda.current_stream(ls.device).cuda_stream
-                _lib.check(L.adana_mta_step(
-                    ctypes.byref(ls.plan), ctypes.cast(sc_arr, ctypes.c_void_p), n_cls, ls.flags,
-                    ctypes.c_void_p(ls.workspace.data_ptr()), ls.workspace.numel(),
-                    ctypes.c_void_p(ls.diag.data_ptr()), ctypes.c_void_p(stream)), "adana_mta_step")
+                if gscale is None:
+                    _lib.check(L.adana_mta_step(
+                        ctypes.byref(ls.plan), ctypes.cast(sc_arr, ctypes.c_void_p), n_cls, ls.flags,
+                        ctypes.c_void_p(ls.workspace.data_ptr()), ls.workspace.numel(),
+                        ctypes.c_void_p(ls.diag.data_ptr()), ctypes.c_void_p(stream)), "adana_mta_step")
+                else:
+                    _lib.check(L.adana_mta_step_scaled(
+                        ctypes.byref(ls.plan), ctypes.cast(sc_arr, ctypes.c_void_p), n_cls,
+                        ls.flags | wflag, ctypes.c_void_p(gscale),
+                        ctypes.c_void_p(ls.workspace.data_ptr()), ls.workspace.numel(),
+                        ctypes.c_void_p(ls.diag.data_ptr()), ctypes.c_void_p(stream)),
+                        "adana_mta_step_scaled")
         torch._C._increment_version(params)
+        if wflag:
+            torch._C._increment_version(grads)
         return loss
 
     def _refresh_grads(self, ls: _LaunchSet) -> None:

@@ -6,7 +6,10 @@ with parameters, gradients and state already resident in HBM.  The default
 workload is the north-star: Dana-Star-MK4, fp32 params and state, on the
 2,645,527,040-parameter list of BASELINE config 4's geometry (d_model 2560,
 32 layers, MLP 4x, vocab 50304, tied embedding).  Other workloads (c1..c5)
-are the remaining BASELINE configs.
+are the remaining BASELINE configs; north_star_clip adds the training loop's
+gradient-norm clipping before every step (src/optim/base.py:250-257, max_norm
+0.5 as scripts/launch.sh:47) through the optimizer's fused clip, including the
+loop's ``grad_norm.item()``.
 
 Prints ONE JSON line.  ``value`` is the whole-step throughput in algorithmic
 HBM GB/s (bytes the update must move per element x elements / wall-clock ms
@@ -71,6 +74,10 @@ def workload(name):
         return dict(name=name, optimizer="Dana-Star-MK4", star=True, groups=[decay, nodecay],
                     group_wd=[1.0, 0.0], hp=_hp(500), master=False, schedule=None,
                     grad_note="N(0,1e-3); embedding rows nonzero w.p. 0.1")
+    if name == "north_star_clip":
+        w = workload("north_star")
+        w.update(name=name, clip=0.5, grad_note=w["grad_note"] + "; clip_grad_norm_(0.5) each step")
+        return w
     if name in ("c4", "north_star"):
         decay, nodecay = gpt_shapes(50304, 2560, 32)
         if name == "c4":
@@ -91,8 +98,12 @@ def workload(name):
 
 def bytes_per_elem(w):
     if w["master"]:
-        return 28 + (8 if w["star"] else 0)   # master 4+4, g 2, m/v 16, p_bf16 2 (+tau 8)
-    return 36 if w["star"] else 28
+        b = 28 + (8 if w["star"] else 0)      # master 4+4, g 2, m/v 16, p_bf16 2 (+tau 8)
+    else:
+        b = 36 if w["star"] else 28
+    if w.get("clip"):
+        b += 2 * (2 if w["master"] else 4)    # norm pass reads g, the step writes clipped g back
+    return b
 
 
 def cos_inf(k, n=200, warmup=4, final_div=0.1):
@@ -118,7 +129,7 @@ def build_gpu(w, seed=0):
             g = torch.empty(s, dtype=torch.float32, device=dev).normal_(0.0, 1e-3, generator=gen)
             if w["name"] == "c2" and len(s) == 1:
                 g.mul_(0.1)
-            if w["name"] in ("c3", "north_star") and gi == 1 and ti == 0:
+            if w["name"] in ("c3", "north_star", "north_star_clip") and gi == 1 and ti == 0:
                 rows = torch.rand(s[0], device=dev, generator=gen) < 0.1     # row-sparse embedding grad
                 g.mul_(rows[:, None].to(g.dtype))
             if w["name"] == "c5" and zero_rng.random() < 0.05:
@@ -210,7 +221,8 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--workload", default="north_star",
-                    choices=["north_star", "c1", "c2", "c3", "c4", "c5", "copy_probe"])
+                    choices=["north_star", "north_star_clip", "c1", "c2", "c3", "c4", "c5",
+                             "copy_probe"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     args = ap.parse_args()
@@ -231,11 +243,14 @@ def main():
     bpe = bytes_per_elem(w)
     algo_bytes = n_elems * bpe
     peak = w["hp"]["lr"]
+    grad_norms = []
 
     def one_step(k):
         if w["schedule"] == "cos_inf":
             for g in opt.param_groups:
                 g["lr"] = peak * cos_inf(k)
+        if w.get("clip"):
+            grad_norms.append(opt.clip_grad_norm_(w["clip"]).item())   # src/optim/base.py:250-257
         opt.step()
 
     torch.cuda.synchronize()
@@ -275,14 +290,17 @@ def main():
                    "tensors": len(params), "bytes_per_elem": bpe,
                    "algorithmic_bytes_per_step": algo_bytes, "grads": w["grad_note"],
                    "hyperparams": w["hp"], "master_weights": w["master"],
-                   "parallelism": "single GPU"},
+                   "parallelism": "single GPU",
+                   **({"grad_clip": w["clip"], "first_grad_norm": grad_norms[0]} if w.get("clip") else {})},
         "kernel_ms_per_step": round(kern_ms, 4),
         "kernel_ms_p90": round(float(np.percentile(dev_ms, 90)), 4),
         "params_per_s": round(n_elems / (ms_per_step * 1e-3), 1),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": traffic,
-                     "kernel": "mta_step_kernel + finalize_kernel (events bracket one step)"},
+                     "kernel": ("grad_sumsq_kernel + clip finalize + mta_step_kernel + finalize_kernel "
+                                "(events bracket one step)" if w.get("clip") else
+                                "mta_step_kernel + finalize_kernel (events bracket one step)")},
     }
     del opt, params
     torch.cuda.empty_cache()

@@ -24,6 +24,14 @@
  *        (src/optim/dana_star_mk4.py:105-205) for ALL tensors of the list,
  *        plus the diagnostics stored at src/optim/adana.py:221-225 /
  *        src/optim/dana_star_mk4.py:290-294.
+ *   adana_grad_clip_norm     <- the gradient-norm clipping the training loop
+ *        runs before every step (src/optim/base.py:250-257 ->
+ *        src/distributed/backend.py:33-35 -> torch.nn.utils.clip_grad_norm_):
+ *        total norm and clip coefficient on the device.
+ *   adana_mta_step_scaled    <- clip_grad_norm_'s in-place gradient scaling
+ *        fused into adana_mta_step's gradient load.
+ *   adana_grad_scale         <- the same scaling as a separate in-place pass
+ *        (for a gradient list no fused step consumes).
  *   adana_last_error, adana_abi_version, adana_workspace_bytes: plumbing
  *        (no reference counterpart).
  *
@@ -44,7 +52,7 @@
 extern "C" {
 #endif
 
-#define ADANA_ABI_VERSION 1
+#define ADANA_ABI_VERSION 2
 
 /* Elements per work chunk (one 256-thread workgroup, one 16-byte vector per
  * thread per array).  Tensors start at multiples of ADANA_ALIGN_ELEMS in the
@@ -60,6 +68,8 @@ extern "C" {
 #define ADANA_VARIANT_STAR 0x1u  /* Dana-Star(-MK4): tau state and estimator   */
 #define ADANA_GRAD_BF16    0x2u  /* gradients are bfloat16 (else float32)      */
 #define ADANA_PARAM_BF16   0x4u  /* param = fp32 master; param_lp = bf16 copy  */
+#define ADANA_WRITE_GRAD   0x8u  /* adana_mta_step_scaled: store the scaled
+                                    gradient back into grad                   */
 
 /* adana_tensor_desc.flags */
 #define ADANA_DESC_VEC_OK  0x1u  /* all pointers aligned for 16-byte access   */
@@ -181,6 +191,42 @@ size_t adana_workspace_bytes(const adana_plan *plan);
 int adana_mta_step(const adana_plan *plan, const adana_step_scalars *h_scalars,
                    int32_t n_classes, uint32_t variant_flags, void *d_workspace,
                    size_t workspace_bytes, float *d_diag, void *stream);
+
+/* Device.  adana_mta_step on clipped gradients: each gradient element is
+ * replaced by g * (*d_grad_scale) as it is loaded (rounded to bfloat16 for
+ * bfloat16 gradients), which is what torch.nn.utils.clip_grad_norm_'s
+ * ``torch._foreach_mul_(grads, clip_coef_clamped)`` leaves in the gradient
+ * (torch/nn/utils/clip_grad.py, _clip_grads_with_norm_), so the update and
+ * the diagnostics see exactly the clipped gradient.  With ADANA_WRITE_GRAD in
+ * variant_flags the scaled gradient is also stored back, leaving grad as the
+ * reference's in-place clipping does; without it grad is not modified.
+ * d_grad_scale: device float, typically d_clip + 1 of adana_grad_clip_norm. */
+int adana_mta_step_scaled(const adana_plan *plan, const adana_step_scalars *h_scalars,
+                          int32_t n_classes, uint32_t variant_flags,
+                          const float *d_grad_scale, void *d_workspace,
+                          size_t workspace_bytes, float *d_diag, void *stream);
+
+/* Device.  The norm half of torch.nn.utils.clip_grad_norm_(params, max_norm)
+ * with norm_type 2 (src/optim/base.py:250-257, src/distributed/backend.py:
+ * 33-35), over the gradients of ``plan`` (only desc[i].grad, numel and flags
+ * are read; grad_flags: 0 for float32 or ADANA_GRAD_BF16 for bfloat16
+ * gradients, shared by the whole list).  Writes, in torch's order and dtype
+ * (each value rounded to the gradient dtype):
+ *   d_norms[i]  ||grad_i||_2 (torch._foreach_norm), or d_norms == NULL
+ *   d_clip[0]   total norm = ||(norm_0, ..., norm_{n-1})||_2
+ *   d_clip[1]   min(reciprocal(total + 1e-6) * max_norm, 1)  (NaN propagates)
+ * Sums of squares are accumulated in binary64.  d_workspace: at least
+ * adana_workspace_bytes(plan) bytes (its own, or one not in use by a step
+ * running concurrently).  Asynchronous on ``stream``. */
+int adana_grad_clip_norm(const adana_plan *plan, uint32_t grad_flags, double max_norm,
+                         void *d_workspace, size_t workspace_bytes, float *d_norms,
+                         float *d_clip, void *stream);
+
+/* Device.  In place grad_i *= *d_scale for every gradient of ``plan``
+ * (clip_grad_norm_'s torch._foreach_mul_; bfloat16 products rounded to
+ * bfloat16).  Asynchronous on ``stream``. */
+int adana_grad_scale(const adana_plan *plan, uint32_t grad_flags, const float *d_scale,
+                     void *stream);
 
 #ifdef __cplusplus
 }

@@ -229,6 +229,49 @@ def bf16_to_f32(h: np.ndarray) -> np.ndarray:
 
 
 # --------------------------------------------------------------------------
+# Gradient-norm clipping (src/optim/base.py:250-257 -> torch.nn.utils.
+# clip_grad_norm_ with norm_type 2, torch/nn/utils/clip_grad.py)
+# --------------------------------------------------------------------------
+
+def _round_to(x, bf16: bool) -> np.float32:
+    x = np.float32(x)
+    return bf16_to_f32(f32_to_bf16(np.array([x])))[0] if bf16 else x
+
+
+def clip_norms(grads: Sequence[np.ndarray], bf16: bool = False):
+    """(per-tensor norms, total norm) as torch._foreach_norm and
+    torch.linalg.vector_norm(torch.stack(norms)) produce them: each norm in
+    the gradient dtype (binary32, or bfloat16 for bfloat16 gradients), from
+    binary64 sums of squares (torch accumulates in binary32; both are within
+    a few binary32 ulps of the exact value)."""
+    norms = [_round_to(math.sqrt(float(np.sum(np.square(np.asarray(g, dtype=np.float64)))))
+                       , bf16) for g in grads]
+    total = _round_to(math.sqrt(math.fsum(float(n) * float(n) for n in norms)), bf16)
+    return norms, total
+
+
+def clip_coef(total, max_norm: float, bf16: bool = False) -> np.float32:
+    """torch's coefficient from the total norm (_clip_grads_with_norm_):
+    ``clamp(max_norm / (total + 1e-6), max=1.0)`` where ``float / Tensor`` is
+    ``Tensor.reciprocal() * float``; every op is one binary32 operation on
+    binary32 operands (the Python floats 1e-6 and max_norm cast to binary32),
+    rounded to bfloat16 after each op for bfloat16 norms.  NaN propagates."""
+    den = _round_to(np.float32(total) + np.float32(1e-6), bf16)
+    with np.errstate(divide="ignore", over="ignore", invalid="ignore"):
+        rc = _round_to(np.float32(1.0) / den, bf16)
+        coef = _round_to(rc * np.float32(max_norm), bf16)
+    return np.float32(1.0) if coef > np.float32(1.0) else coef
+
+
+def clip_scale(g: np.ndarray, coef, bf16: bool = False) -> np.ndarray:
+    """torch._foreach_mul_(grads, coef): g * coef in binary32, rounded to
+    bfloat16 for bfloat16 gradients (returned as float32 values)."""
+    with np.errstate(over="ignore", invalid="ignore"):
+        y = np.asarray(g, dtype=np.float32) * np.float32(coef)
+    return bf16_to_f32(f32_to_bf16(y)).reshape(y.shape) if bf16 else y
+
+
+# --------------------------------------------------------------------------
 # Step loop (restates the reference optimizers' step() bookkeeping)
 # --------------------------------------------------------------------------
 
