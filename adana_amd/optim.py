@@ -115,6 +115,11 @@ class _DanaFamily(Optimizer):
         self._active = None
 
     def load_state_dict(self, state_dict) -> None:
+        """torch's load_state_dict (checkpoints of the reference optimizers load
+        as they are: src/optim/utils.py:283-361 saves ``opt.state_dict()``).  In
+        master-weights mode the moments of bf16 parameters are kept float32, and
+        a checkpoint without a ``'master'`` entry (the reference keeps none)
+        starts the master copy from the bf16 parameter."""
         super().load_state_dict(state_dict)
         if self.master_weights:
             # torch casts floating state to the parameter dtype on load; the
@@ -128,6 +133,8 @@ class _DanaFamily(Optimizer):
                     for k in ("master", "m", "v", "tau"):
                         if k in saved[pid]:
                             st[k] = saved[pid][k].to(device=p.device, dtype=torch.float32)
+                    if "m" in st and "master" not in st:
+                        st["master"] = p.detach().to(torch.float32)
         self.invalidate_plan()
 
     # -- gradient clipping -------------------------------------------------

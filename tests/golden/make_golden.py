@@ -17,7 +17,13 @@ Two modes of the reference are recorded:
   compiled  -- the reference's default ``torch.compile`` path (Inductor-CPU),
                recorded when the container can compile it (--compiled).
 
-Usage:  python tests/golden/make_golden.py [--ref /root/reference] [--compiled]
+A third output is the reference optimizer's own ``state_dict()`` at step
+STATE_AT of the eager run (``<case>.state8.npz``: every tensor, plus a JSON
+schema of keys, Python types, dtypes and shapes): the checkpoint interchange
+tests load it into this build's optimizers and compare schemas
+(src/optim/utils.py:283-310 saves exactly this dict).
+
+Usage:  python tests/golden/make_golden.py [--ref /root/reference] [--compiled] [--state-only]
 """
 from __future__ import annotations
 
@@ -40,6 +46,7 @@ ROW_SPARSE = 4
 NONE_ON_ODD = 5
 N_STEPS = 20
 CHECKPOINTS = (1, 7, 8, 9, 20)       # t = delta = 8 puts alpha exactly at 0.5
+STATE_AT = 8
 
 CASES = {
     # name: (module, class, ctor kwargs, group weight decays)
@@ -104,7 +111,28 @@ def load_module(ref: str, name: str):
     return mod
 
 
-def run_case(ref: str, case: str, compiled: bool, p0, grads, has_grad):
+def state_dict_fixture(sd) -> dict:
+    """Flatten an optimizer state_dict into npz entries + a JSON schema."""
+    import torch
+
+    out, schema = {}, {"state": {}, "param_groups": []}
+    for idx, st in sd["state"].items():
+        ent = {}
+        for k, v in st.items():
+            if isinstance(v, torch.Tensor):
+                out[f"state.{idx}.{k}"] = v.detach().cpu().numpy().copy()
+                ent[k] = {"type": "Tensor", "dtype": str(v.dtype), "shape": list(v.shape)}
+            else:
+                ent[k] = {"type": type(v).__name__, "value": v}
+        schema["state"][str(idx)] = ent
+    for g in sd["param_groups"]:
+        schema["param_groups"].append({k: (v if not isinstance(v, float) else float(v))
+                                       for k, v in g.items()})
+    out["schema"] = np.array(json.dumps(schema))
+    return out
+
+
+def run_case(ref: str, case: str, compiled: bool, p0, grads, has_grad, state_out=None):
     import torch
 
     modname, clsname, kw = CASES[case]
@@ -132,6 +160,8 @@ def run_case(ref: str, case: str, compiled: bool, p0, grads, has_grad):
             st = opt.state[p]
             if st:
                 diags[k - 1, i] = [float(st[x]) for x in keys]
+        if state_out is not None and k == STATE_AT:
+            state_out.update(state_dict_fixture(opt.state_dict()))
         if k in CHECKPOINTS:
             for i, p in enumerate(params):
                 st = opt.state[p]
@@ -149,6 +179,8 @@ def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--ref", default="/root/reference")
     ap.add_argument("--compiled", action="store_true")
+    ap.add_argument("--state-only", action="store_true",
+                    help="only (re)write the <case>.state8.npz checkpoint fixtures")
     args = ap.parse_args()
     import torch
 
@@ -166,13 +198,23 @@ def main():
                       for c, (m, cl, kw) in CASES.items()},
             "torch": torch.__version__, "cpu_capability": torch.backends.cpu.get_cpu_capability()}
     inputs["meta"] = np.array(json.dumps(meta))
+    if args.state_only:
+        for case in CASES:
+            st = {}
+            run_case(args.ref, case, False, p0, grads, has_grad, state_out=st)
+            np.savez_compressed(os.path.join(HERE, f"{case}.state{STATE_AT}.npz"), **st)
+            print(f"wrote {case}.state{STATE_AT}.npz", flush=True)
+        return 0
     np.savez_compressed(os.path.join(HERE, "inputs.npz"), **inputs)
     modes = ["eager"] + (["compiled"] if args.compiled else [])
     for mode in modes:
         for case in CASES:
-            out = run_case(args.ref, case, mode == "compiled", p0, grads, has_grad)
+            st = {} if mode == "eager" else None
+            out = run_case(args.ref, case, mode == "compiled", p0, grads, has_grad, state_out=st)
             np.savez_compressed(os.path.join(HERE, f"{case}.{mode}.npz"), **out)
             print(f"wrote {case}.{mode}.npz", flush=True)
+            if st:
+                np.savez_compressed(os.path.join(HERE, f"{case}.state{STATE_AT}.npz"), **st)
 
 
 if __name__ == "__main__":

@@ -63,3 +63,42 @@ def golden_cases(mode: str = "eager") -> List[str]:
 
 def is_star_class(cls_name: str) -> bool:
     return cls_name == "DANA_STAR_MK4"
+
+
+def load_reference_state_dict(case: str, device: str = "cpu"):
+    """The reference optimizer's own ``state_dict()`` at step 8 of the golden
+    run (tests/golden/<case>.state8.npz), rebuilt as torch objects."""
+    import torch
+
+    z = np.load(os.path.join(GOLDEN, f"{case}.state8.npz"))
+    schema = json.loads(str(z["schema"]))
+    state = {}
+    for idx, ent in schema["state"].items():
+        st = {}
+        for k, spec in ent.items():
+            if spec["type"] == "Tensor":
+                st[k] = torch.from_numpy(z[f"state.{idx}.{k}"].copy()).to(device)
+            else:
+                st[k] = spec["value"]
+        state[int(idx)] = st
+    groups = [dict(g) for g in schema["param_groups"]]
+    return {"state": state, "param_groups": groups}, schema
+
+
+def state_dict_schema(sd) -> dict:
+    """Keys, Python types, dtypes and shapes of an optimizer state_dict (the
+    form of the fixture schema) and its group entries."""
+    import torch
+
+    out = {"state": {}, "param_groups": []}
+    for idx, st in sd["state"].items():
+        ent = {}
+        for k, v in st.items():
+            if isinstance(v, torch.Tensor):
+                ent[k] = {"type": "Tensor", "dtype": str(v.dtype), "shape": list(v.shape)}
+            else:
+                ent[k] = {"type": type(v).__name__}
+        out["state"][str(idx)] = ent
+    for g in sd["param_groups"]:
+        out["param_groups"].append(sorted(g.keys()))
+    return out

@@ -1,0 +1,141 @@
+"""Checkpoint interchange without a GPU: the reference optimizer's own
+state_dict (tests/golden/<case>.state8.npz, written by its step() in
+tests/golden/make_golden.py; saved by the reference at
+src/optim/utils.py:283-310) loads into ADana / DANA_STAR_MK4 unchanged and
+comes back out with the same schema and values."""
+import io
+
+import numpy as np
+import pytest
+import torch
+
+from helpers import golden_cases, load_golden_inputs, load_reference_state_dict, state_dict_schema
+
+
+def _make(case, device="cpu"):
+    import adana_amd
+
+    meta, p0, _, _ = load_golden_inputs()
+    c = meta["cases"][case]
+    kw = dict(c["kwargs"])
+    cls = adana_amd.DANA_STAR_MK4 if c["class"] == "DANA_STAR_MK4" else adana_amd.ADana
+    params = [torch.nn.Parameter(torch.from_numpy(x.copy()).to(device)) for x in p0]
+    groups = []
+    for gi in range(2):
+        groups.append({"params": [p for i, p in enumerate(params) if meta["group_of"][i] == gi],
+                       "weight_decay": kw["weight_decay"] * meta["group_wd_scale"][gi]})
+    return cls(groups, **kw), params
+
+
+@pytest.mark.parametrize("case", golden_cases("eager"))
+def test_reference_state_dict_round_trips(case):
+    """load_state_dict(reference) then state_dict(): same keys, Python types
+    (``step`` stays an int), dtypes, shapes, group entries and values --
+    also through torch.save / torch.load(weights_only=True)."""
+    opt, _ = _make(case)
+    ref, schema = load_reference_state_dict(case)
+    buf = io.BytesIO()
+    torch.save(ref, buf)
+    buf.seek(0)
+    opt.load_state_dict(torch.load(buf, weights_only=True))
+    out = opt.state_dict()
+    got = state_dict_schema(out)
+    want = state_dict_schema(ref)
+    assert got == want
+    for idx, st in ref["state"].items():
+        for k, v in st.items():
+            o = out["state"][idx][k]
+            if isinstance(v, torch.Tensor):
+                assert torch.equal(o.cpu().view(torch.int32) if v.dtype == torch.float32 else o.cpu(),
+                                   v.view(torch.int32) if v.dtype == torch.float32 else v), (idx, k)
+            else:
+                assert type(o) is type(v) and o == v, (idx, k)
+    for g_out, g_ref in zip(out["param_groups"], schema["param_groups"]):
+        for k, v in g_ref.items():
+            assert g_out[k] == v, k
+
+
+def test_reference_schema_is_what_the_build_writes():
+    """The fixture's schema is the one this build's state holds: per-tensor
+    'step' (int), m, v[, tau] shaped like p, and the five 0-d float32
+    diagnostics; groups carry lr, delta, epsilon, weight_decay,
+    weighted_step_count."""
+    from adana_amd import DIAG_KEYS
+
+    for case in golden_cases("eager"):
+        _, schema = load_reference_state_dict(case)
+        star = "star" in case
+        for idx, ent in schema["state"].items():
+            keys = {"step", "m", "v"} | ({"tau"} if star else set()) | set(DIAG_KEYS)
+            assert set(ent) == keys, (case, idx)
+            assert ent["step"]["type"] == "int"
+            for k in DIAG_KEYS:
+                assert ent[k]["dtype"] == "torch.float32" and ent[k]["shape"] == []
+        for g in schema["param_groups"]:
+            assert set(g) == {"lr", "delta", "epsilon", "weight_decay", "weighted_step_count", "params"}
+
+
+def _scaled_err(x, ref, scale):
+    scale = np.maximum(np.abs(scale), np.float32(1e-30)).astype(np.float32)
+    return np.abs(x.astype(np.float64) - ref.astype(np.float64)) / np.spacing(scale).astype(np.float64)
+
+
+def resume_bars(case, k, got, gold, star):
+    """Bars of a run resumed from the reference's step-8 checkpoint against the
+    reference's own trajectory at step k (shared with the GPU test):
+    m, v bit-exact; tau within 2 ulp; p within 2 ulp per step since the resume
+    in ulps of the tensor's largest |p| (the oracle's golden-trajectory bar)."""
+    from helpers import ulp_diff
+
+    for i, st in enumerate(got):
+        tag = f"{case} t={k} tensor {i}"
+        assert st["step"] == int(gold[f"step{i}_t{k}"]), tag
+        assert ulp_diff(st["m"], gold[f"m{i}_t{k}"]).max() == 0, tag + " m"
+        assert ulp_diff(st["v"], gold[f"v{i}_t{k}"]).max() == 0, tag + " v"
+        if star:
+            assert ulp_diff(st["tau"], gold[f"tau{i}_t{k}"]).max() <= 2, tag + " tau"
+        ref = gold[f"p{i}_t{k}"]
+        scale = np.full(ref.shape, np.abs(ref).max(), np.float32)
+        assert _scaled_err(st["p"], ref, scale).max() <= 2 * (k - 8), tag + " p"
+
+
+@pytest.mark.parametrize("case", golden_cases("eager"))
+def test_oracle_resumes_reference_checkpoint(oracle_mod, case):
+    """The oracle restarted from the reference's step-8 state_dict follows
+    the reference's own trajectory to step 20 (calibrates resume_bars)."""
+    from helpers import load_golden_case
+
+    O = oracle_mod
+    meta, p0, grads, has_grad = load_golden_inputs()
+    gold = load_golden_case(case, "eager")
+    ref, schema = load_reference_state_dict(case)
+    c = meta["cases"][case]
+    kw = c["kwargs"]
+    star = c["class"] == "DANA_STAR_MK4"
+    params = [gold[f"p{i}_t8"].copy() for i in range(len(p0))]
+    groups = []
+    for gi in range(2):
+        groups.append(O.OracleGroup(params=[params[i] for i in range(len(params)) if meta["group_of"][i] == gi],
+                                    lr=kw["lr"], delta=kw["delta"], epsilon=1e-8,
+                                    weight_decay=kw["weight_decay"] * meta["group_wd_scale"][gi],
+                                    weighted_step_count=schema["param_groups"][gi]["weighted_step_count"]))
+    opt = O.OracleOptimizer(groups=groups, star=star, peak_lr=kw["lr"], kappa=kw["kappa"],
+                            clipsnr=kw["clipsnr"], wd_decaying=kw["wd_decaying"], wd_ts=kw["wd_ts"],
+                            gamma_3_factor=kw["gamma_3_factor"])
+    for i, p in enumerate(params):
+        st = ref["state"][i]
+        opt.state[id(p)] = {"step": st["step"], "m": st["m"].numpy().copy(), "v": st["v"].numpy().copy(),
+                            **({"tau": st["tau"].numpy().copy()} if star else {})}
+    for k in range(9, meta["n_steps"] + 1):
+        for g in opt.groups:
+            g.lr = kw["lr"] * meta["lr_multiplier"][k - 1]
+        gl = []
+        for gi in range(2):
+            idx = [i for i in range(len(p0)) if meta["group_of"][i] == gi]
+            gl.append([grads[k - 1][i] if has_grad[k - 1, i] else None for i in idx])
+        opt.step(gl)
+        if k in (9, 20):
+            got = [dict(opt.state[id(p)], p=p) for p in params]
+            resume_bars(case, k, got, gold, star)
+    for g, wsc in zip(opt.groups, gold["weighted_step_count"]):
+        assert g.weighted_step_count == wsc

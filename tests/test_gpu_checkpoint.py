@@ -1,0 +1,187 @@
+"""Checkpoint interchange on the GPU (src/optim/utils.py:260-361 saves and
+restores ``opt.state_dict()``):
+
+  * a checkpoint the reference optimizer wrote at step 8
+    (tests/golden/<case>.state8.npz) resumes in this build and follows the
+    reference's own trajectory to step 20 (bars: resume_bars, shared with the
+    oracle's CPU run of the same resume in tests/test_checkpoint_cpu.py);
+  * this build's state_dict after 8 steps has the reference's schema (keys,
+    Python types, dtypes, shapes, group entries) and its values (m, v
+    bit-exact; tau within 2 ulp; diagnostics rtol 2e-5);
+  * a torch.save / torch.load(weights_only=True) round trip mid-run resumes
+    bit-identically;
+  * a reference checkpoint (fp32 moments, no master copy) loads into the bf16
+    master-weights extension and continues as the oracle does from the same
+    state.
+"""
+import io
+
+import numpy as np
+import pytest
+import torch
+
+from helpers import (golden_cases, load_golden_case, load_golden_inputs, load_reference_state_dict,
+                     state_dict_schema, ulp_diff)
+from test_checkpoint_cpu import resume_bars
+
+pytestmark = [pytest.mark.gpu,
+              pytest.mark.skipif(not torch.cuda.is_available(), reason="needs a ROCm GPU")]
+
+DEV = "cuda:0"
+
+
+def _build(case, p_init, dtype=torch.float32, **extra):
+    import adana_amd
+
+    meta, *_ = load_golden_inputs()
+    c = meta["cases"][case]
+    kw = dict(c["kwargs"])
+    cls = adana_amd.DANA_STAR_MK4 if c["class"] == "DANA_STAR_MK4" else adana_amd.ADana
+    params = [torch.nn.Parameter(torch.from_numpy(x.copy()).to(DEV, dtype)) for x in p_init]
+    groups = []
+    for gi in range(2):
+        groups.append({"params": [p for i, p in enumerate(params) if meta["group_of"][i] == gi],
+                       "weight_decay": kw["weight_decay"] * meta["group_wd_scale"][gi]})
+    return cls(groups, **kw, **extra), params, meta, kw, c["class"] == "DANA_STAR_MK4"
+
+
+def _run(opt, params, meta, kw, grads, has_grad, k0, k1, dtype=torch.float32, on_step=None):
+    for k in range(k0, k1 + 1):
+        for g in opt.param_groups:
+            g["lr"] = kw["lr"] * meta["lr_multiplier"][k - 1]
+        for i, p in enumerate(params):
+            p.grad = torch.from_numpy(grads[k - 1][i].copy()).to(DEV, dtype) if has_grad[k - 1, i] else None
+        opt.step()
+        if on_step:
+            on_step(k)
+
+
+@pytest.mark.parametrize("case", golden_cases("eager"))
+def test_resume_from_reference_checkpoint(case):
+    print("case: resume reference checkpoint", case, flush=True)
+    meta, p0, grads, has_grad = load_golden_inputs()
+    gold = load_golden_case(case, "eager")
+    opt, params, meta, kw, star = _build(case, [gold[f"p{i}_t8"] for i in range(len(p0))])
+    ref, _ = load_reference_state_dict(case, device=DEV)
+    opt.load_state_dict(ref)
+
+    def check(k):
+        if k in (9, 20):
+            torch.cuda.synchronize()
+            got = []
+            for p in params:
+                st = opt.state[p]
+                got.append({"step": st["step"], "m": st["m"].cpu().numpy(), "v": st["v"].cpu().numpy(),
+                            "p": p.detach().cpu().numpy(),
+                            **({"tau": st["tau"].cpu().numpy()} if star else {})})
+            resume_bars(case, k, got, gold, star)
+
+    _run(opt, params, meta, kw, grads, has_grad, 9, meta["n_steps"], on_step=check)
+    for g, wsc in zip(opt.param_groups, gold["weighted_step_count"]):
+        assert g["weighted_step_count"] == wsc
+    for i, p in enumerate(params):                  # diagnostics of the last step
+        st = opt.state[p]
+        got = np.array([float(st[k]) for k in ("current_alpha", "gradient_norm", "auto_factor_mean",
+                                                "current_kappa_factor", "m_norm")])
+        np.testing.assert_allclose(got, gold["diag"][-1, i], rtol=2e-5, atol=1e-12, equal_nan=True)
+
+
+@pytest.mark.parametrize("case", golden_cases("eager"))
+def test_state_dict_matches_reference_schema(case):
+    print("case: state_dict schema", case, flush=True)
+    meta, p0, grads, has_grad = load_golden_inputs()
+    opt, params, meta, kw, star = _build(case, p0)
+    _run(opt, params, meta, kw, grads, has_grad, 1, 8)
+    torch.cuda.synchronize()
+    ours = opt.state_dict()
+    ref, schema = load_reference_state_dict(case)
+    assert state_dict_schema(ours) == state_dict_schema(ref)
+    for gi, (g_ours, g_ref) in enumerate(zip(ours["param_groups"], schema["param_groups"])):
+        for k, v in g_ref.items():
+            assert g_ours[k] == v, (gi, k)
+    for idx, st in ref["state"].items():
+        o = ours["state"][idx]
+        assert o["step"] == st["step"]
+        assert ulp_diff(o["m"].cpu().numpy(), st["m"].numpy()).max() == 0
+        assert ulp_diff(o["v"].cpu().numpy(), st["v"].numpy()).max() == 0
+        if star:
+            assert ulp_diff(o["tau"].cpu().numpy(), st["tau"].numpy()).max() <= 2
+        for k in ("current_alpha", "gradient_norm", "auto_factor_mean", "current_kappa_factor", "m_norm"):
+            np.testing.assert_allclose(float(o[k]), float(st[k]), rtol=2e-5, atol=1e-12, equal_nan=True)
+
+
+@pytest.mark.parametrize("case", ["dana_mk4", "dana_star_mk4"])
+def test_torch_save_round_trip_resumes_bit_identically(case):
+    print("case: torch.save round trip", case, flush=True)
+    meta, p0, grads, has_grad = load_golden_inputs()
+    a, pa, meta, kw, star = _build(case, p0)
+    _run(a, pa, meta, kw, grads, has_grad, 1, 8)
+    buf = io.BytesIO()
+    torch.save({"optimizer": a.state_dict(), "params": [p.detach().cpu() for p in pa]}, buf)
+    buf.seek(0)
+    ck = torch.load(buf, weights_only=True)
+    b, pb, *_ = _build(case, [t.numpy() for t in ck["params"]])
+    b.load_state_dict(ck["optimizer"])
+    _run(a, pa, meta, kw, grads, has_grad, 9, meta["n_steps"])
+    _run(b, pb, meta, kw, grads, has_grad, 9, meta["n_steps"])
+    torch.cuda.synchronize()
+    for x, y in zip(pa, pb):
+        assert torch.equal(x.detach().view(torch.int32), y.detach().view(torch.int32))
+        for k in ("m", "v") + (("tau",) if star else ()):
+            assert torch.equal(a.state[x][k].view(torch.int32), b.state[y][k].view(torch.int32))
+        assert a.state[x]["step"] == b.state[y]["step"]
+
+
+def test_reference_checkpoint_into_bf16_master_mode(oracle_mod):
+    """fp32-moment checkpoint without 'master' into master_weights=True bf16
+    parameters: the master starts as float(p_bf16) and the run continues as
+    the oracle's master-mode run from that state (ADana: bit-exact)."""
+    print("case: reference checkpoint into bf16 master mode", flush=True)
+    O = oracle_mod
+    case = "dana_mk4"
+    meta, p0, grads, has_grad = load_golden_inputs()
+    gold = load_golden_case(case, "eager")
+    p16 = [O.f32_to_bf16(gold[f"p{i}_t8"]).reshape(gold[f"p{i}_t8"].shape) for i in range(len(p0))]
+    p_bf = [O.bf16_to_f32(x).reshape(x.shape) for x in p16]
+    opt, params, meta, kw, star = _build(case, p_bf, dtype=torch.bfloat16, master_weights=True)
+    ref, schema = load_reference_state_dict(case, device=DEV)
+    opt.load_state_dict(ref)
+    for p in params:
+        st = opt.state[p]
+        assert st["m"].dtype == torch.float32 and st["master"].dtype == torch.float32
+        assert torch.equal(st["master"], p.detach().float())
+    groups = []
+    for gi in range(2):
+        groups.append(O.OracleGroup(params=[p16[i] for i in range(len(p16)) if meta["group_of"][i] == gi],
+                                    lr=kw["lr"], delta=kw["delta"], epsilon=1e-8,
+                                    weight_decay=kw["weight_decay"] * meta["group_wd_scale"][gi],
+                                    weighted_step_count=schema["param_groups"][gi]["weighted_step_count"]))
+    orc = O.OracleOptimizer(groups=groups, star=False, peak_lr=kw["lr"], kappa=kw["kappa"],
+                            clipsnr=kw["clipsnr"], wd_decaying=kw["wd_decaying"], wd_ts=kw["wd_ts"],
+                            gamma_3_factor=kw["gamma_3_factor"], master=True)
+    for i, p in enumerate(p16):
+        st = ref["state"][i]
+        orc.state[id(p)] = {"step": st["step"], "m": st["m"].cpu().numpy().copy(),
+                            "v": st["v"].cpu().numpy().copy(), "master": p_bf[i].copy()}
+    g16 = [[O.f32_to_bf16(g).reshape(g.shape) for g in gs] for gs in grads]
+    for k in range(9, 13):
+        lr = kw["lr"] * meta["lr_multiplier"][k - 1]
+        for g in opt.param_groups:
+            g["lr"] = lr
+        for g in orc.groups:
+            g.lr = lr
+        for i, p in enumerate(params):
+            p.grad = (torch.from_numpy(g16[k - 1][i].view(np.int16).copy()).view(torch.bfloat16).to(DEV)
+                      if has_grad[k - 1, i] else None)
+        opt.step()
+        gl = []
+        for gi in range(2):
+            idx = [i for i in range(len(p16)) if meta["group_of"][i] == gi]
+            gl.append([g16[k - 1][i] if has_grad[k - 1, i] else None for i in idx])
+        orc.step(gl)
+    torch.cuda.synchronize()
+    for i, p in enumerate(params):
+        st, ost = opt.state[p], orc.state[id(p16[i])]
+        assert ulp_diff(st["master"].cpu().numpy(), ost["master"]).max() == 0, i
+        assert ulp_diff(st["m"].cpu().numpy(), ost["m"]).max() == 0, i
+        assert np.array_equal(p.detach().cpu().view(torch.int16).numpy().view(np.uint16), p16[i]), i
