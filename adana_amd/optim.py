@@ -88,6 +88,7 @@ class _DanaFamily(Optimizer):
         self._active = None
         self._pending_clip = None
         self._clip_plan_obj = None
+        self._diag_loc = {}        # param -> (diagnostics buffer, row) of its latest plan
         _lib.lib()  # fail at construction, not at the first step, without the kernel library
 
     # -- state ------------------------------------------------------------
@@ -278,11 +279,47 @@ class _DanaFamily(Optimizer):
                                            device=ls.device)
                 ls.diag = torch.full((len(ls.params), 5), float("nan"), dtype=torch.float32,
                                      device=ls.device)
-            for j, st in enumerate(ls.states):
+            for j, (p, st) in enumerate(zip(ls.params, ls.states)):
                 row = ls.diag[j]
                 for k, key in enumerate(DIAG_KEYS):
                     st[key] = row[k]
+                self._diag_loc[p] = (ls.diag, j)
         return out
+
+    # -- diagnostics read-out ---------------------------------------------
+    def diagnostics_host(self):
+        """Every parameter's five diagnostics (DIAG_KEYS order) as float32 rows
+        of a numpy array, in param_groups order, skipping parameters without
+        them: one asynchronous device-to-host copy per diagnostics buffer and
+        one synchronisation, instead of one ``.item()`` per value.  Returns
+        (params, values[n, 5])."""
+        params, locs = [], []
+        for group in self.param_groups:
+            for p in group["params"]:
+                st = self.state.get(p) if p in self.state else None
+                if not st or "current_alpha" not in st:
+                    continue
+                loc = self._diag_loc.get(p)
+                if loc is not None and st["current_alpha"].data_ptr() != loc[0].data_ptr() + 20 * loc[1]:
+                    loc = None                     # state tensors replaced (e.g. load_state_dict)
+                params.append(p)
+                locs.append(loc if loc is not None else st)
+        host = {}
+        for loc in locs:
+            if isinstance(loc, tuple) and id(loc[0]) not in host:
+                h = torch.empty(loc[0].shape, dtype=loc[0].dtype, pin_memory=True)
+                h.copy_(loc[0], non_blocking=True)
+                host[id(loc[0])] = (loc[0].device, h)
+        for dev in {d for d, _ in host.values()}:
+            torch.cuda.current_stream(dev).synchronize()
+        out = np.empty((len(locs), 5), dtype=np.float32)
+        arrays = {k: h.numpy() for k, (_, h) in host.items()}
+        for r, loc in enumerate(locs):
+            if isinstance(loc, tuple):
+                out[r] = arrays[id(loc[0])][loc[1]]
+            else:                                  # loaded, not yet stepped: read one by one
+                out[r] = [float(loc[k]) for k in DIAG_KEYS]
+        return params, out
 
     # -- step -------------------------------------------------------------
     def _hparams(self, group) -> "_lib.HParams":
