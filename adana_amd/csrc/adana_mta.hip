@@ -13,9 +13,10 @@
 //   * each workgroup streams p, g, m, v (and tau) once with 16-byte loads,
 //     applies the update element by element and writes p, m, v (tau) once;
 //   * the four per-tensor sums behind the diagnostics are reduced per
-//     (chunk, tensor) segment with wave shuffles and an LDS combine, written to
-//     partials[chunk + tensor], and combined per tensor in binary64 by a
-//     one-workgroup-per-tensor finalize kernel (deterministic, no atomics).
+//     (chunk, tensor) segment with DPP wave reductions and an LDS combine,
+//     written to partials[chunk + tensor], and combined per tensor in binary64
+//     by a fold kernel and a one-wave-per-tensor finalize kernel
+//     (deterministic, no atomics).
 //
 // Element arithmetic follows the reference's op order with every op one
 // correctly rounded binary32 operation (built with -ffp-contract=off); the
@@ -235,6 +236,33 @@ __device__ __forceinline__ void update_n(float (&P)[N], const float (&G)[N], flo
 }
 
 // ---------------------------------------------------------------------------
+// Wave reduction: the sum over a wave's 64 lanes, left in lane 63.  GFX9 DPP
+// lane moves fused into the adds (no LDS round trips): quad_perm xor 1 and
+// xor 2, row_half_mirror and row_mirror (swap the halves of 8- and 16-lane
+// groups whose lanes already agree), then row_bcast:15 and row_bcast:31
+// fold rows 0-2 into row 3.  Fixed order: deterministic.
+// ---------------------------------------------------------------------------
+template <int CTRL, int ROWS>
+__device__ __forceinline__ float dpp_add(float v) {
+    const int t = __builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, ROWS, 0xF, false);
+    return v + __int_as_float(t);
+}
+__device__ __forceinline__ void wave_sum4_to_lane63(float (&a)[4]) {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) a[k] = dpp_add<0xB1, 0xF>(a[k]);   // quad_perm(1,0,3,2)
+#pragma unroll
+    for (int k = 0; k < 4; ++k) a[k] = dpp_add<0x4E, 0xF>(a[k]);   // quad_perm(2,3,0,1)
+#pragma unroll
+    for (int k = 0; k < 4; ++k) a[k] = dpp_add<0x141, 0xF>(a[k]);  // row_half_mirror
+#pragma unroll
+    for (int k = 0; k < 4; ++k) a[k] = dpp_add<0x140, 0xF>(a[k]);  // row_mirror
+#pragma unroll
+    for (int k = 0; k < 4; ++k) a[k] = dpp_add<0x142, 0xA>(a[k]);  // row_bcast:15 into rows 1, 3
+#pragma unroll
+    for (int k = 0; k < 4; ++k) a[k] = dpp_add<0x143, 0xC>(a[k]);  // row_bcast:31 into rows 2, 3
+}
+
+// ---------------------------------------------------------------------------
 // Memory access: global (not flat) 16-byte vectors, non-temporal for the
 // streamed arrays (each byte is touched once per step).
 // ---------------------------------------------------------------------------
@@ -335,7 +363,8 @@ __global__ __launch_bounds__(kChunk / VEC) void mta_step_kernel(const adana_tens
                                                                 float *__restrict__ partials) {
     constexpr int kThreads = kChunk / VEC;
     constexpr int kW = kThreads / 64;
-    __shared__ float red[kW][4];
+    __shared__ float red[2][kW][4];
+    int par = 0;
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
@@ -402,27 +431,27 @@ __global__ __launch_bounds__(kChunk / VEC) void mta_step_kernel(const adana_tens
                 }
             }
         }
-        // (chunk, tensor) segment sums: wave butterfly, fixed-order wave combine.
+        // (chunk, tensor) segment sums: wave reduction, then a fixed-order
+        // combine of the waves in LDS.  The LDS slot alternates between
+        // segments, so no barrier is needed after thread 0 has read it.
+        wave_sum4_to_lane63(acc);
+        if (lane == 63) {
 #pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            float x = acc[k];
-#pragma unroll
-            for (int o = 32; o > 0; o >>= 1) x += __shfl_xor(x, o, 64);
-            if (lane == 0) red[wave][k] = x;
+            for (int k = 0; k < 4; ++k) red[par][wave][k] = acc[k];
         }
         __syncthreads();
         if (tid == 0) {
-            float4 q = make_float4(red[0][0], red[0][1], red[0][2], red[0][3]);
+            float4 q = make_float4(red[par][0][0], red[par][0][1], red[par][0][2], red[par][0][3]);
 #pragma unroll
             for (int w = 1; w < kW; ++w) {
-                q.x += red[w][0];
-                q.y += red[w][1];
-                q.z += red[w][2];
-                q.w += red[w][3];
+                q.x += red[par][w][0];
+                q.y += red[par][w][1];
+                q.z += red[par][w][2];
+                q.w += red[par][w][3];
             }
             reinterpret_cast<float4 *>(partials)[chunk + i] = q;
         }
-        __syncthreads();
+        par ^= 1;
     }
 }
 
@@ -758,12 +787,55 @@ size_t workspace_bytes(const adana_plan &pl) {
     return folds_offset(pl) + static_cast<size_t>(pl.n_folds) * 32;
 }
 
+// Residency cap.  The streaming instances (no per-element pow) reach the
+// highest HBM throughput with 4 (fp32 params) or 5 (bf16 params with fp32
+// master) workgroups per CU rather than the 8 their registers allow: fewer
+// concurrent streams contend less in the memory system (measured on MI355X:
+// ADana fp32 13.1 -> 12.1 ms, Dana-Star kappa=1 17.1 -> 16.1 ms, bf16 master
+// 13.0 -> 12.1 ms at 2.65B params).  Dana-Star with the binary64 pow is
+// compute-heavy and runs best at its register-limited 5, uncapped.  The cap
+// is imposed with dynamic LDS the kernel does not touch.
+template <bool STAR, bool PBF16, int POWK>
+constexpr int residency_cap() {
+    return (STAR && POWK == POW_GENERAL) ? 0 : (PBF16 ? 5 : 4);
+}
+
+// Dynamic LDS bytes that leave room for exactly `wgs` workgroups per CU on
+// the current device (0: no cap, or the device's LDS size is unavailable).
+// Grids of fewer than 64 chunks per CU stay uncapped: there the cap only adds
+// dispatch rounds.
+size_t lds_for_cap(int wgs, int64_t n_chunks) {
+    if (wgs <= 0) return 0;
+    static int lds_per_cu[64];
+    static int lds_per_block[64];
+    static int cus[64];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+    if (lds_per_cu[dev] <= 0) {
+        int cu = 0, blk = 0, n_cu = 0;
+        if (hipDeviceGetAttribute(&cu, hipDeviceAttributeMaxSharedMemoryPerMultiprocessor, dev) != hipSuccess ||
+            hipDeviceGetAttribute(&blk, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess ||
+            hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+            return 0;
+        lds_per_block[dev] = blk;
+        cus[dev] = n_cu;
+        lds_per_cu[dev] = cu;
+    }
+    if (n_chunks < 64 * static_cast<int64_t>(cus[dev])) return 0;
+    // wgs * L <= lds < (wgs + 1) * L, with 1 KB left for the kernel's static LDS
+    const size_t per_cu = static_cast<size_t>(lds_per_cu[dev]);
+    if (per_cu < 20 * 1024) return 0;
+    const size_t l = per_cu / static_cast<size_t>(wgs) - 1024;
+    return l <= static_cast<size_t>(lds_per_block[dev]) ? l : 0;
+}
+
 template <bool STAR, bool GBF16, bool PBF16, int POWK>
 void launch_main(int64_t n_chunks, hipStream_t st, const adana_tensor_desc *d, const int64_t *vs,
                  const int32_t *cf, int32_t n, const ScalarPack &pack, float *partials) {
     constexpr int kVec = 4;
+    const size_t lds = lds_for_cap(residency_cap<STAR, PBF16, POWK>(), n_chunks);
     hipLaunchKernelGGL((mta_step_kernel<STAR, GBF16, PBF16, POWK, kVec>), dim3(static_cast<unsigned>(n_chunks)),
-                       dim3(kChunk / kVec), 0, st, d, vs, cf, n, pack, partials);
+                       dim3(kChunk / kVec), static_cast<unsigned>(lds), st, d, vs, cf, n, pack, partials);
 }
 
 template <bool STAR, bool GBF16, bool PBF16>

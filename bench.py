@@ -122,10 +122,17 @@ def build_gpu(w, seed=0):
     pdtype = torch.bfloat16 if w["master"] else torch.float32
     groups, params = [], []
     zero_rng = np.random.default_rng(seed + 1)
+    # Every parameter first, then every gradient: the order in which a model's
+    # constructor and then its backward pass allocate them.
     for gi, shapes in enumerate(w["groups"]):
         ps = []
-        for ti, s in enumerate(shapes):
+        for s in shapes:
             p = torch.empty(s, dtype=torch.float32, device=dev).normal_(0.0, 0.02, generator=gen)
+            ps.append(torch.nn.Parameter(p.to(pdtype)))
+        params += ps
+        groups.append(dict(params=ps, weight_decay=w["hp"]["weight_decay"] * w["group_wd"][gi]))
+    for gi, shapes in enumerate(w["groups"]):
+        for ti, (s, p) in enumerate(zip(shapes, groups[gi]["params"])):
             g = torch.empty(s, dtype=torch.float32, device=dev).normal_(0.0, 1e-3, generator=gen)
             if w["name"] == "c2" and len(s) == 1:
                 g.mul_(0.1)
@@ -134,11 +141,7 @@ def build_gpu(w, seed=0):
                 g.mul_(rows[:, None].to(g.dtype))
             if w["name"] == "c5" and zero_rng.random() < 0.05:
                 g.zero_()
-            p = torch.nn.Parameter(p.to(pdtype))
             p.grad = g.to(pdtype)
-            ps.append(p)
-        params += ps
-        groups.append(dict(params=ps, weight_decay=w["hp"]["weight_decay"] * w["group_wd"][gi]))
     cls = adana_amd.DANA_STAR_MK4 if w["star"] else adana_amd.ADana
     opt = cls(groups, master_weights=w["master"], **w["hp"])
     return opt, params

@@ -185,3 +185,36 @@ def test_reference_checkpoint_into_bf16_master_mode(oracle_mod):
         assert ulp_diff(st["master"].cpu().numpy(), ost["master"]).max() == 0, i
         assert ulp_diff(st["m"].cpu().numpy(), ost["m"]).max() == 0, i
         assert np.array_equal(p.detach().cpu().view(torch.int16).numpy().view(np.uint16), p16[i]), i
+
+
+def test_state_tensors_have_own_storages_in_family_slabs():
+    """State tensors are laid out family by family (all m end to end, then
+    all v, all tau; 4 KB aligned) but each has a storage of its own, so a
+    per-parameter deepcopy (DynamicsLogger, src/logger/logger.py:93) and
+    torch.save copy only that tensor's bytes."""
+    import copy
+    import adana_amd
+
+    print("case: state slab layout", flush=True)
+    shapes = [(300, 7), (5,), (4096,), (1, 1), (70000,)]
+    params = [torch.nn.Parameter(torch.randn(s, device=DEV)) for s in shapes]
+    opt = adana_amd.DANA_STAR_MK4(params, lr=1e-3, kappa=0.85)
+    for p in params:
+        p.grad = torch.randn_like(p) * 1e-3
+    opt.step()
+    torch.cuda.synchronize()
+    for fam in ("m", "v", "tau"):
+        ptrs = [opt.state[p][fam].data_ptr() for p in params]
+        assert all(x % 4096 == 0 for x in ptrs), fam
+        for a, b, p in zip(ptrs, ptrs[1:], params):
+            assert b - a == (p.numel() + 1023) // 1024 * 4096, fam     # end to end in one slab
+        for p in params:
+            t = opt.state[p][fam]
+            assert t._base is None and t.untyped_storage().nbytes() == 4 * p.numel()
+            assert t.shape == p.shape and t.dtype == p.dtype and t.is_contiguous()
+    snap = copy.deepcopy(opt.state[params[2]])
+    assert snap["m"].untyped_storage().nbytes() == 4 * 4096
+    assert torch.equal(snap["m"], opt.state[params[2]]["m"])
+    buf = io.BytesIO()
+    torch.save(opt.state_dict(), buf)
+    assert len(buf.getvalue()) < 3 * 4 * sum(p.numel() for p in params) + 200_000
