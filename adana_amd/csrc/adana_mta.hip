@@ -323,6 +323,24 @@ __device__ __forceinline__ void st_bf16_n(void *p, const float (&x)[N]) {
     __builtin_nontemporal_store(h, (GLOBAL_AS typename VecT<N>::H *)(p));
 }
 
+// The vector path's fp32 stores of p, m, v, tau go out as buffer stores
+// with the system-scope + non-temporal policy (sc1 nt): the data is not
+// re-read by this step, and on MI355X this lets the write stream through the
+// caches 1-2% faster than a non-temporal global store (same-process A/B on
+// 2.65B params).  The resource's base is the segment's first element, so a
+// lane's byte offset is below 4 KB.
+typedef unsigned int U32x4 __attribute__((ext_vector_type(4)));
+constexpr int kStorePolicy = 16 | 2;   // sc1 | nt
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const float *base) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(base), 0, 0x7fffffff, 0x00020000);
+}
+__device__ __forceinline__ void st4_stream(const float *seg_base, int byte_off, const float (&x)[4]) {
+    U32x4 u;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) u[k] = __float_as_uint(x[k]);
+    __builtin_amdgcn_raw_buffer_store_b128(u, buffer_rsrc(seg_base), byte_off, 0, kStorePolicy);
+}
+
 template <bool GBF16, int N>
 __device__ __forceinline__ void load_grad_n(const void *g, int64_t off, float (&o)[N]) {
     if constexpr (GBF16) ld_bf16_n<N>(static_cast<const unsigned short *>(g) + off, o);
@@ -408,10 +426,19 @@ __global__ __launch_bounds__(kChunk / VEC) void mta_step_kernel(const adana_tens
                     if (pack.write_grad) store_grad_n<GBF16, VEC>(d.grad, off, G);
                 }
                 update_n<STAR, POWK, VEC>(P, G, M, V, T, sc, acc);
-                st_n<VEC>(pp, P);
-                st_n<VEC>(mp, M);
-                st_n<VEC>(vp, V);
-                if constexpr (STAR) st_n<VEC>(tp, T);
+                if constexpr (VEC == 4) {
+                    const int64_t seg0 = (lo > vs ? lo : vs) - vs;      // uniform
+                    const int byte_off = static_cast<int>((off - seg0) * 4);
+                    st4_stream(static_cast<float *>(d.param) + seg0, byte_off, P);
+                    st4_stream(d.m + seg0, byte_off, M);
+                    st4_stream(d.v + seg0, byte_off, V);
+                    if constexpr (STAR) st4_stream(d.tau + seg0, byte_off, T);
+                } else {
+                    st_n<VEC>(pp, P);
+                    st_n<VEC>(mp, M);
+                    st_n<VEC>(vp, V);
+                    if constexpr (STAR) st_n<VEC>(tp, T);
+                }
                 if constexpr (PBF16) st_bf16_n<VEC>(static_cast<unsigned short *>(d.param_lp) + off, P);
             } else {
                 // unaligned tensor, or the last (< VEC) elements of a tensor
