@@ -9,5 +9,7 @@ include/adana_mta.h.
 from .clip import clip_grad_norm_
 from .optim import ADana, DANA_STAR_MK4, DIAG_KEYS
 from .schedules import log_optimizer_schedules
+from .tau_stats import compute_tau_order_statistics, extract_tau_statistics
 
-__all__ = ["ADana", "DANA_STAR_MK4", "DIAG_KEYS", "clip_grad_norm_", "log_optimizer_schedules"]
+__all__ = ["ADana", "DANA_STAR_MK4", "DIAG_KEYS", "clip_grad_norm_", "log_optimizer_schedules",
+           "compute_tau_order_statistics", "extract_tau_statistics"]

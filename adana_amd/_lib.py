@@ -79,6 +79,7 @@ EXPORTS = (
     "adana_abi_version", "adana_last_error", "adana_step_scalars_init",
     "adana_plan_layout", "adana_plan_index", "adana_workspace_bytes", "adana_mta_step",
     "adana_mta_step_scaled", "adana_grad_clip_norm", "adana_grad_scale",
+    "adana_order_stats_workspace", "adana_order_stats",
 )
 
 _lib = None
@@ -113,6 +114,10 @@ def _declare(L) -> None:
     L.adana_grad_clip_norm.restype = ctypes.c_int
     L.adana_grad_scale.argtypes = [ctypes.POINTER(Plan), u32, P, P]
     L.adana_grad_scale.restype = ctypes.c_int
+    L.adana_order_stats_workspace.argtypes = [i32, i64]
+    L.adana_order_stats_workspace.restype = ctypes.c_size_t
+    L.adana_order_stats.argtypes = [P, P, i32, P, P, P, P, ctypes.c_size_t, P]
+    L.adana_order_stats.restype = ctypes.c_int
 
 
 def _hip_runtimes_mapped():

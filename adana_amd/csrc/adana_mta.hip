@@ -29,20 +29,23 @@
 #include <cstring>
 
 #include "adana_mta.h"
+#include "adana_internal.h"
 #include "adana_fastmath.h"
 #include "adana_pow.h"
 
 namespace {
-
 thread_local char g_err[512] = "";
+}  // namespace
 
-int set_err(int code, const char *fmt, ...) {
+int adana_set_error(int code, const char *fmt, ...) {
     va_list ap;
     va_start(ap, fmt);
     vsnprintf(g_err, sizeof g_err, fmt, ap);
     va_end(ap);
     return code;
 }
+
+namespace {
 
 constexpr int kBlock = 256;
 constexpr int kWaves = kBlock / 64;
@@ -929,11 +932,11 @@ size_t adana_last_error(char *buf, size_t len) {
 
 int adana_step_scalars_init(adana_step_scalars *out, const adana_hparams *hp, double lr,
                             int64_t step) {
-    if (!out || !hp) return set_err(ADANA_E_INVALID, "adana_step_scalars_init: null pointer");
-    if (step < 1) return set_err(ADANA_E_INVALID, "adana_step_scalars_init: step %lld < 1",
+    if (!out || !hp) return adana_set_error(ADANA_E_INVALID, "adana_step_scalars_init: null pointer");
+    if (step < 1) return adana_set_error(ADANA_E_INVALID, "adana_step_scalars_init: step %lld < 1",
                                  static_cast<long long>(step));
     if (!(hp->peak_lr != 0.0))
-        return set_err(ADANA_E_INVALID, "adana_step_scalars_init: peak lr must be nonzero");
+        return adana_set_error(ADANA_E_INVALID, "adana_step_scalars_init: peak lr must be nonzero");
     // Host doubles (src/optim/adana.py:163-165, :200), rounded to binary32 the
     // way torch.tensor(x, dtype=float32) does (:203-208).
     const float sf = static_cast<float>(lr / hp->peak_lr);
@@ -971,10 +974,10 @@ int adana_step_scalars_init(adana_step_scalars *out, const adana_hparams *hp, do
 int64_t adana_plan_layout(const int64_t *numel, int32_t n, int64_t *vstart,
                           int32_t *fold_first, int64_t *n_folds) {
     if (n < 0 || !vstart || !fold_first || !n_folds || (n > 0 && !numel))
-        return set_err(ADANA_E_INVALID, "adana_plan_layout: bad arguments");
+        return adana_set_error(ADANA_E_INVALID, "adana_plan_layout: bad arguments");
     int64_t off = 0, folds = 0;
     for (int32_t i = 0; i < n; ++i) {
-        if (numel[i] < 0) return set_err(ADANA_E_INVALID, "adana_plan_layout: numel[%d] < 0", i);
+        if (numel[i] < 0) return adana_set_error(ADANA_E_INVALID, "adana_plan_layout: numel[%d] < 0", i);
         vstart[i] = off;
         fold_first[i] = static_cast<int32_t>(folds);
         if (numel[i] > 0) {
@@ -982,29 +985,29 @@ int64_t adana_plan_layout(const int64_t *numel, int32_t n, int64_t *vstart,
             folds += (chunks_i + kFold - 1) / kFold;
         }
         off += (numel[i] + ADANA_ALIGN_ELEMS - 1) / ADANA_ALIGN_ELEMS * ADANA_ALIGN_ELEMS;
-        if (folds > 0x7fffffffLL) return set_err(ADANA_E_UNSUPPORTED, "adana_plan_layout: list too large");
+        if (folds > 0x7fffffffLL) return adana_set_error(ADANA_E_UNSUPPORTED, "adana_plan_layout: list too large");
     }
     vstart[n] = off;
     fold_first[n] = static_cast<int32_t>(folds);
     *n_folds = folds;
     const int64_t chunks = (off + kChunk - 1) / kChunk;
-    if (chunks > 0x7fffffffLL) return set_err(ADANA_E_UNSUPPORTED, "adana_plan_layout: list too large");
+    if (chunks > 0x7fffffffLL) return adana_set_error(ADANA_E_UNSUPPORTED, "adana_plan_layout: list too large");
     return chunks;
 }
 
 int adana_plan_index(const int64_t *d_vstart, int32_t n_tensors, int64_t n_chunks,
                      int32_t *d_chunk_first, void *stream) {
     if (n_tensors < 0 || n_chunks < 0 || n_chunks > 0x7fffffffLL)
-        return set_err(ADANA_E_INVALID, "adana_plan_index: bad sizes");
+        return adana_set_error(ADANA_E_INVALID, "adana_plan_index: bad sizes");
     if (n_chunks == 0) return ADANA_OK;
     if (n_tensors == 0 || !d_vstart || !d_chunk_first)
-        return set_err(ADANA_E_INVALID, "adana_plan_index: null pointer or no tensors");
+        return adana_set_error(ADANA_E_INVALID, "adana_plan_index: null pointer or no tensors");
     const unsigned blocks = static_cast<unsigned>((n_chunks + kBlock - 1) / kBlock);
     hipLaunchKernelGGL(chunk_index_kernel, dim3(blocks), dim3(kBlock), 0,
                        static_cast<hipStream_t>(stream), d_vstart, n_tensors, n_chunks, d_chunk_first);
     hipError_t err = hipGetLastError();
     if (err != hipSuccess)
-        return set_err(ADANA_E_HIP, "adana_plan_index: launch failed: %s", hipGetErrorString(err));
+        return adana_set_error(ADANA_E_HIP, "adana_plan_index: launch failed: %s", hipGetErrorString(err));
     return ADANA_OK;
 }
 
@@ -1018,24 +1021,24 @@ namespace {
 
 // Plan checks shared by the entry points; return ADANA_OK or an error code.
 int check_plan(const adana_plan *plan, const char *fn) {
-    if (!plan) return set_err(ADANA_E_INVALID, "%s: null plan", fn);
+    if (!plan) return adana_set_error(ADANA_E_INVALID, "%s: null plan", fn);
     const adana_plan &pl = *plan;
     if (pl.n_tensors < 0 || pl.n_chunks < 0 || pl.n_chunks > 0x7fffffffLL || pl.n_folds < 0 ||
         pl.n_folds > 0x7fffffffLL)
-        return set_err(ADANA_E_INVALID, "%s: bad sizes (n_tensors=%d, n_chunks=%lld)", fn, pl.n_tensors,
+        return adana_set_error(ADANA_E_INVALID, "%s: bad sizes (n_tensors=%d, n_chunks=%lld)", fn, pl.n_tensors,
                        static_cast<long long>(pl.n_chunks));
     return ADANA_OK;
 }
 int check_plan_arrays(const adana_plan &pl, const char *fn) {
     if (pl.n_tensors > 0 && (!pl.desc || !pl.vstart || !pl.fold_first || (pl.n_chunks > 0 && !pl.chunk_first)))
-        return set_err(ADANA_E_INVALID, "%s: null pointer in the plan arrays", fn);
+        return adana_set_error(ADANA_E_INVALID, "%s: null pointer in the plan arrays", fn);
     return ADANA_OK;
 }
 
 int launch_status(const char *fn, const char *what) {
     hipError_t err = hipGetLastError();
     if (err != hipSuccess)
-        return set_err(ADANA_E_HIP, "%s: %s launch failed: %s", fn, what, hipGetErrorString(err));
+        return adana_set_error(ADANA_E_HIP, "%s: %s launch failed: %s", fn, what, hipGetErrorString(err));
     return ADANA_OK;
 }
 
@@ -1047,15 +1050,15 @@ int step_impl(const char *fn, const adana_plan *plan, const adana_step_scalars *
     const uint32_t allowed = ADANA_VARIANT_STAR | ADANA_GRAD_BF16 | ADANA_PARAM_BF16 |
                              (d_grad_scale ? ADANA_WRITE_GRAD : 0u);
     if (variant_flags & ~allowed)
-        return set_err(ADANA_E_INVALID, "%s: unknown variant flags 0x%x", fn, variant_flags);
+        return adana_set_error(ADANA_E_INVALID, "%s: unknown variant flags 0x%x", fn, variant_flags);
     if (int rc = check_plan_arrays(pl, fn)) return rc;
     if (pl.n_tensors == 0) return ADANA_OK;
     if (!d_workspace || !d_diag || !h_scalars)
-        return set_err(ADANA_E_INVALID, "%s: null pointer argument", fn);
+        return adana_set_error(ADANA_E_INVALID, "%s: null pointer argument", fn);
     if (n_classes < 1 || n_classes > ADANA_MAX_CLASSES)
-        return set_err(ADANA_E_INVALID, "%s: n_classes=%d outside [1, %d]", fn, n_classes, ADANA_MAX_CLASSES);
+        return adana_set_error(ADANA_E_INVALID, "%s: n_classes=%d outside [1, %d]", fn, n_classes, ADANA_MAX_CLASSES);
     if (ws_bytes < workspace_bytes(pl))
-        return set_err(ADANA_E_INVALID, "%s: workspace of %zu bytes < %zu needed", fn, ws_bytes,
+        return adana_set_error(ADANA_E_INVALID, "%s: workspace of %zu bytes < %zu needed", fn, ws_bytes,
                        workspace_bytes(pl));
     ScalarPack pack;
     memset(&pack, 0, sizeof pack);
@@ -1114,7 +1117,7 @@ int adana_mta_step(const adana_plan *plan, const adana_step_scalars *h_scalars, 
 int adana_mta_step_scaled(const adana_plan *plan, const adana_step_scalars *h_scalars, int32_t n_classes,
                           uint32_t variant_flags, const float *d_grad_scale, void *d_workspace,
                           size_t ws_bytes, float *d_diag, void *stream) {
-    if (!d_grad_scale) return set_err(ADANA_E_INVALID, "adana_mta_step_scaled: null gradient scale");
+    if (!d_grad_scale) return adana_set_error(ADANA_E_INVALID, "adana_mta_step_scaled: null gradient scale");
     return step_impl("adana_mta_step_scaled", plan, h_scalars, n_classes, variant_flags, d_grad_scale,
                      d_workspace, ws_bytes, d_diag, stream);
 }
@@ -1124,12 +1127,12 @@ int adana_grad_clip_norm(const adana_plan *plan, uint32_t grad_flags, double max
     const char *fn = "adana_grad_clip_norm";
     if (int rc = check_plan(plan, fn)) return rc;
     const adana_plan &pl = *plan;
-    if (grad_flags & ~ADANA_GRAD_BF16) return set_err(ADANA_E_INVALID, "%s: unknown flags 0x%x", fn, grad_flags);
+    if (grad_flags & ~ADANA_GRAD_BF16) return adana_set_error(ADANA_E_INVALID, "%s: unknown flags 0x%x", fn, grad_flags);
     if (int rc = check_plan_arrays(pl, fn)) return rc;
-    if (!d_clip) return set_err(ADANA_E_INVALID, "%s: null clip output", fn);
-    if (pl.n_tensors > 0 && !d_workspace) return set_err(ADANA_E_INVALID, "%s: null workspace", fn);
+    if (!d_clip) return adana_set_error(ADANA_E_INVALID, "%s: null clip output", fn);
+    if (pl.n_tensors > 0 && !d_workspace) return adana_set_error(ADANA_E_INVALID, "%s: null workspace", fn);
     if (ws_bytes < workspace_bytes(pl))
-        return set_err(ADANA_E_INVALID, "%s: workspace of %zu bytes < %zu needed", fn, ws_bytes,
+        return adana_set_error(ADANA_E_INVALID, "%s: workspace of %zu bytes < %zu needed", fn, ws_bytes,
                        workspace_bytes(pl));
     hipStream_t st = static_cast<hipStream_t>(stream);
     const bool gb = grad_flags & ADANA_GRAD_BF16;
@@ -1162,9 +1165,9 @@ int adana_grad_scale(const adana_plan *plan, uint32_t grad_flags, const float *d
     const char *fn = "adana_grad_scale";
     if (int rc = check_plan(plan, fn)) return rc;
     const adana_plan &pl = *plan;
-    if (grad_flags & ~ADANA_GRAD_BF16) return set_err(ADANA_E_INVALID, "%s: unknown flags 0x%x", fn, grad_flags);
+    if (grad_flags & ~ADANA_GRAD_BF16) return adana_set_error(ADANA_E_INVALID, "%s: unknown flags 0x%x", fn, grad_flags);
     if (int rc = check_plan_arrays(pl, fn)) return rc;
-    if (!d_scale) return set_err(ADANA_E_INVALID, "%s: null scale", fn);
+    if (!d_scale) return adana_set_error(ADANA_E_INVALID, "%s: null scale", fn);
     if (pl.n_tensors == 0 || pl.n_chunks == 0) return ADANA_OK;
     hipStream_t st = static_cast<hipStream_t>(stream);
     const dim3 grid(static_cast<unsigned>(pl.n_chunks));

@@ -1,0 +1,278 @@
+// adana_order_stats.hip -- exact order statistics of float32 tensors on the
+// GPU: for each tensor, the values at requested ranks of its ascending order.
+//
+// Reference: TauStatsCollector._extract_tau_statistics
+// (src/optim/tau_stats_collector.py:131-160) copies every Dana-Star tau tensor
+// to the host and calls compute_tau_order_statistics (:336-376), which runs
+// np.sort and reads the sorted array at ranks floor(1.1^k) - 1 from both
+// ends.  Only those few hundred ranks per tensor are needed, so instead of a
+// sort this is a multi-rank radix select over the tensor in HBM:
+//
+//   * each value is mapped to a 32-bit key whose unsigned order is np.sort's
+//     order (NaN last; -0 and +0 adjacent, equal as values);
+//   * a pass resolves the next w key bits (w <= 8) of every wanted rank: one
+//     read of the tensors, a histogram per (tensor, active prefix) of the next
+//     digit, kept in LDS by each workgroup and flushed with global atomics;
+//   * the host walks each histogram to the wanted rank's digit and residual
+//     rank, and the next pass narrows to the new prefixes.  w is 8 while few
+//     prefixes are active and smaller when many are, so that the histograms
+//     always fit in LDS.
+// Exact (integer counting), deterministic results; no sort scratch.  Traffic:
+// 4 bytes per element per pass, 4 to 8 passes.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdint>
+#include <cstdio>
+#include <cstring>
+#include <vector>
+
+#include "adana_mta.h"
+#include "adana_internal.h"
+
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kTileElems = 16384;                 // elements per workgroup (16 loads of 4 per thread)
+constexpr int kLdsBudget = 40 * 1024;             // histogram + prefix table bytes per workgroup
+
+typedef float F4 __attribute__((ext_vector_type(4)));
+#define GLOBAL_AS __attribute__((address_space(1)))
+
+// Order-preserving key: unsigned order of keys == np.sort order of values.
+__device__ __forceinline__ uint32_t order_key(float x) {
+    const uint32_t b = __float_as_uint(x);
+    if ((b & 0x7fffffffu) > 0x7f800000u) return 0xffffffffu;   // NaN sorts last
+    return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+}
+
+struct PassArgs {
+    const float *const *tensor;   // device array of tensor base pointers
+    const int64_t *numel;         // device, per tensor
+    const int64_t *tile_first;    // device, n + 1: first workgroup of each tensor
+    const int32_t *slot_first;    // device, n + 1: first prefix slot of each tensor
+    const uint32_t *prefix;       // device, sorted prefixes of each tensor's slots
+    uint32_t *hist;               // device, [slot][bin] counts
+    int32_t n;
+    int32_t known_bits;           // key bits already resolved (prefix width)
+    int32_t width;                // bits resolved by this pass
+};
+
+__global__ __launch_bounds__(kThreads) void select_hist_kernel(PassArgs a) {
+    extern __shared__ uint32_t lds[];
+    const int64_t wg = blockIdx.x;
+    int l = 0, r = a.n - 1;                             // last tensor with tile_first <= wg
+    while (l < r) {
+        const int mid = (l + r + 1) >> 1;
+        if (a.tile_first[mid] <= wg) l = mid; else r = mid - 1;
+    }
+    const int t = l;
+    const int s0 = a.slot_first[t];
+    const int ns = a.slot_first[t + 1] - s0;
+    if (ns == 0) return;                                 // nothing wanted from this tensor (uniform)
+    const int bins = 1 << a.width;
+    uint32_t *h = lds;                                   // [ns][bins]
+    uint32_t *pre = lds + ns * bins;                     // [ns]
+    for (int i = threadIdx.x; i < ns * bins; i += kThreads) h[i] = 0;
+    for (int i = threadIdx.x; i < ns; i += kThreads) pre[i] = a.prefix[s0 + i];
+    __syncthreads();
+
+    const float *x = a.tensor[t];
+    const int64_t n = a.numel[t];
+    const int64_t base = (wg - a.tile_first[t]) * kTileElems;
+    const int shift = 32 - a.known_bits - a.width;
+    const uint32_t mask = static_cast<uint32_t>(bins - 1);
+    const bool aligned = (reinterpret_cast<uintptr_t>(x) & 15u) == 0;
+    for (int it = 0; it < kTileElems / (4 * kThreads); ++it) {
+        const int64_t e0 = base + (static_cast<int64_t>(it) * kThreads + threadIdx.x) * 4;
+        if (e0 >= n) break;
+        float v[4];
+        int cnt = 4;
+        if (aligned && e0 + 4 <= n) {
+            const F4 q = __builtin_nontemporal_load((const GLOBAL_AS F4 *)(x + e0));
+            v[0] = q[0]; v[1] = q[1]; v[2] = q[2]; v[3] = q[3];
+        } else {
+            cnt = static_cast<int>((n - e0) < 4 ? n - e0 : 4);
+            for (int k = 0; k < cnt; ++k) v[k] = x[e0 + k];
+        }
+        for (int k = 0; k < cnt; ++k) {
+            const uint32_t key = order_key(v[k]);
+            int s = 0;
+            if (a.known_bits > 0) {                      // the slot whose prefix matches, if any
+                const uint32_t p = key >> (32 - a.known_bits);
+                int lo = 0, hi = ns - 1;
+                while (lo < hi) {
+                    const int mid = (lo + hi + 1) >> 1;
+                    if (pre[mid] <= p) lo = mid; else hi = mid - 1;
+                }
+                if (pre[lo] != p) continue;
+                s = lo;
+            }
+            atomicAdd(&h[s * bins + ((key >> shift) & mask)], 1u);
+        }
+    }
+    __syncthreads();
+    uint32_t *g = a.hist + static_cast<int64_t>(s0) * bins;
+    for (int i = threadIdx.x; i < ns * bins; i += kThreads)
+        if (h[i]) atomicAdd(&g[i], h[i]);
+}
+
+inline uint32_t key_to_bits(uint32_t key) {
+    return (key & 0x80000000u) ? (key & 0x7fffffffu) : ~key;
+}
+
+int check(hipError_t e, const char *what) {
+    if (e != hipSuccess) return adana_set_error(ADANA_E_HIP, "adana_order_stats: %s: %s", what, hipGetErrorString(e));
+    return ADANA_OK;
+}
+
+struct Layout {                 // device workspace carving
+    size_t ptrs, numel, tile_first, slot_first, prefix, hist, total;
+};
+
+Layout layout(int32_t n, int64_t total_ranks) {
+    auto up = [](size_t b) { return (b + 255) / 256 * 256; };
+    Layout L{};
+    size_t off = 0;
+    L.ptrs = off; off += up(sizeof(void *) * static_cast<size_t>(n));
+    L.numel = off; off += up(8 * static_cast<size_t>(n));
+    L.tile_first = off; off += up(8 * static_cast<size_t>(n + 1));
+    L.slot_first = off; off += up(4 * static_cast<size_t>(n + 1));
+    L.prefix = off; off += up(4 * static_cast<size_t>(total_ranks > 0 ? total_ranks : 1));
+    L.hist = off; off += up(4 * 256 * static_cast<size_t>(total_ranks > 0 ? total_ranks : 1));
+    L.total = off;
+    return L;
+}
+
+}  // namespace
+
+extern "C" {
+
+size_t adana_order_stats_workspace(int32_t n_tensors, int64_t total_ranks) {
+    if (n_tensors < 0 || total_ranks < 0) return 0;
+    return layout(n_tensors, total_ranks).total;
+}
+
+int adana_order_stats(const float *const *h_tensor, const int64_t *h_numel, int32_t n,
+                      const int64_t *h_ranks, const int64_t *h_rank_first, float *h_values,
+                      void *d_workspace, size_t ws_bytes, void *stream) {
+    if (n < 0 || (n > 0 && (!h_tensor || !h_numel || !h_rank_first)))
+        return adana_set_error(ADANA_E_INVALID, "adana_order_stats: bad arguments");
+    if (n == 0) return ADANA_OK;
+    const int64_t total = h_rank_first[n];
+    if (total < 0 || (total > 0 && (!h_ranks || !h_values)))
+        return adana_set_error(ADANA_E_INVALID, "adana_order_stats: bad rank arrays");
+    for (int32_t i = 0; i < n; ++i) {
+        if (h_numel[i] < 0 || h_rank_first[i] > h_rank_first[i + 1] || h_rank_first[i] < 0)
+            return adana_set_error(ADANA_E_INVALID, "adana_order_stats: bad sizes at tensor %d", i);
+        if (h_rank_first[i + 1] > h_rank_first[i] && !h_tensor[i])
+            return adana_set_error(ADANA_E_INVALID, "adana_order_stats: null tensor %d", i);
+        for (int64_t j = h_rank_first[i]; j < h_rank_first[i + 1]; ++j)
+            if (h_ranks[j] < 0 || h_ranks[j] >= h_numel[i])
+                return adana_set_error(ADANA_E_INVALID, "adana_order_stats: rank %lld outside tensor %d of %lld elements",
+                            static_cast<long long>(h_ranks[j]), i, static_cast<long long>(h_numel[i]));
+    }
+    if (total == 0) return ADANA_OK;
+    const Layout L = layout(n, total);
+    if (!d_workspace || ws_bytes < L.total)
+        return adana_set_error(ADANA_E_INVALID, "adana_order_stats: workspace of %zu bytes < %zu needed", ws_bytes, L.total);
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    char *ws = static_cast<char *>(d_workspace);
+
+    // per-rank search state: the rank's slot prefix and residual rank in it
+    std::vector<uint32_t> rank_prefix(static_cast<size_t>(total), 0u);
+    std::vector<int64_t> residual(h_ranks, h_ranks + total);
+    std::vector<int64_t> tile_first(static_cast<size_t>(n) + 1, 0);
+    for (int32_t i = 0; i < n; ++i) {
+        const bool wanted = h_rank_first[i + 1] > h_rank_first[i];
+        const int64_t tiles = wanted ? (h_numel[i] + kTileElems - 1) / kTileElems : 0;
+        tile_first[i + 1] = tile_first[i] + tiles;
+    }
+    const int64_t n_tiles = tile_first[n];
+    if (n_tiles > 0x7fffffffLL) return adana_set_error(ADANA_E_UNSUPPORTED, "adana_order_stats: too many elements");
+    int rc;
+    if ((rc = check(hipMemcpyAsync(ws + L.ptrs, h_tensor, sizeof(void *) * n, hipMemcpyHostToDevice, st), "copy")) ||
+        (rc = check(hipMemcpyAsync(ws + L.numel, h_numel, 8 * static_cast<size_t>(n), hipMemcpyHostToDevice, st), "copy")) ||
+        (rc = check(hipMemcpyAsync(ws + L.tile_first, tile_first.data(), 8 * static_cast<size_t>(n + 1),
+                                   hipMemcpyHostToDevice, st), "copy")))
+        return rc;
+
+    std::vector<int32_t> slot_first(static_cast<size_t>(n) + 1);
+    std::vector<uint32_t> prefix;
+    std::vector<int32_t> rank_slot(static_cast<size_t>(total));
+    std::vector<uint32_t> hist;
+    int known = 0;
+    while (known < 32) {
+        // slots: each tensor's distinct prefixes among its wanted ranks, sorted
+        prefix.clear();
+        int max_slots = 0;
+        for (int32_t i = 0; i < n; ++i) {
+            slot_first[i] = static_cast<int32_t>(prefix.size());
+            const int64_t a = h_rank_first[i], b = h_rank_first[i + 1];
+            std::vector<uint32_t> p(rank_prefix.begin() + a, rank_prefix.begin() + b);
+            std::sort(p.begin(), p.end());
+            p.erase(std::unique(p.begin(), p.end()), p.end());
+            for (int64_t j = a; j < b; ++j)
+                rank_slot[j] = static_cast<int32_t>(std::lower_bound(p.begin(), p.end(), rank_prefix[j]) - p.begin());
+            prefix.insert(prefix.end(), p.begin(), p.end());
+            max_slots = std::max(max_slots, static_cast<int>(p.size()));
+        }
+        slot_first[n] = static_cast<int32_t>(prefix.size());
+        // digit width: the widest whose histograms (and prefix table) fit the LDS budget
+        int width = 8;
+        while (width > 1 && static_cast<size_t>(max_slots) * ((1u << width) + 1) * 4 > kLdsBudget) --width;
+        if (static_cast<size_t>(max_slots) * ((1u << width) + 1) * 4 > kLdsBudget)
+            return adana_set_error(ADANA_E_UNSUPPORTED, "adana_order_stats: %d ranks in one tensor is too many", max_slots);
+        width = std::min(width, 32 - known);
+        const int bins = 1 << width;
+        const size_t hist_n = prefix.size() * static_cast<size_t>(bins);
+        if ((rc = check(hipMemcpyAsync(ws + L.slot_first, slot_first.data(), 4 * static_cast<size_t>(n + 1),
+                                       hipMemcpyHostToDevice, st), "copy")) ||
+            (rc = check(hipMemcpyAsync(ws + L.prefix, prefix.data(), 4 * prefix.size(), hipMemcpyHostToDevice, st),
+                        "copy")) ||
+            (rc = check(hipMemsetAsync(ws + L.hist, 0, 4 * hist_n, st), "clear")))
+            return rc;
+        PassArgs pa;
+        pa.tensor = reinterpret_cast<const float *const *>(ws + L.ptrs);
+        pa.numel = reinterpret_cast<const int64_t *>(ws + L.numel);
+        pa.tile_first = reinterpret_cast<const int64_t *>(ws + L.tile_first);
+        pa.slot_first = reinterpret_cast<const int32_t *>(ws + L.slot_first);
+        pa.prefix = reinterpret_cast<const uint32_t *>(ws + L.prefix);
+        pa.hist = reinterpret_cast<uint32_t *>(ws + L.hist);
+        pa.n = n;
+        pa.known_bits = known;
+        pa.width = width;
+        const size_t lds = static_cast<size_t>(max_slots) * (bins + 1) * 4;
+        hipLaunchKernelGGL(select_hist_kernel, dim3(static_cast<unsigned>(n_tiles)), dim3(kThreads),
+                           static_cast<unsigned>(lds), st, pa);
+        if ((rc = check(hipGetLastError(), "histogram launch"))) return rc;
+        hist.resize(hist_n);
+        if ((rc = check(hipMemcpyAsync(hist.data(), ws + L.hist, 4 * hist_n, hipMemcpyDeviceToHost, st), "copy")) ||
+            (rc = check(hipStreamSynchronize(st), "synchronize")))
+            return rc;
+        // each rank: the digit whose cumulative count passes its residual rank
+        for (int32_t i = 0; i < n; ++i) {
+            for (int64_t j = h_rank_first[i]; j < h_rank_first[i + 1]; ++j) {
+                const uint32_t *hs = hist.data() + (static_cast<size_t>(slot_first[i]) + rank_slot[j]) * bins;
+                int64_t rr = residual[j];
+                int d = 0;
+                for (; d < bins; ++d) {
+                    if (rr < static_cast<int64_t>(hs[d])) break;
+                    rr -= hs[d];
+                }
+                if (d == bins)
+                    return adana_set_error(ADANA_E_HIP, "adana_order_stats: histogram of tensor %d does not cover rank", i);
+                residual[j] = rr;
+                rank_prefix[j] = (width == 32 ? 0u : (rank_prefix[j] << width)) | static_cast<uint32_t>(d);
+            }
+        }
+        known += width;
+    }
+    for (int64_t j = 0; j < total; ++j) {
+        const uint32_t b = key_to_bits(rank_prefix[j]);
+        memcpy(&h_values[j], &b, 4);
+    }
+    return ADANA_OK;
+}
+
+}  // extern "C"

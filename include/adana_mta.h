@@ -32,8 +32,14 @@
  *        fused into adana_mta_step's gradient load.
  *   adana_grad_scale         <- the same scaling as a separate in-place pass
  *        (for a gradient list no fused step consumes).
- *   adana_last_error, adana_abi_version, adana_workspace_bytes: plumbing
- *        (no reference counterpart).
+ *   adana_order_stats        <- the tau order statistics of the Dana-Star
+ *        state (TauStatsCollector._extract_tau_statistics,
+ *        src/optim/tau_stats_collector.py:131-160, which copies every tau
+ *        tensor to the host and calls compute_tau_order_statistics, :336-376:
+ *        np.sort, then the sorted values at ranks floor(1.1^k) - 1 from both
+ *        ends): exact values at given ranks, selected on the GPU.
+ *   adana_last_error, adana_abi_version, adana_workspace_bytes,
+ *        adana_order_stats_workspace: plumbing (no reference counterpart).
  *
  * Ownership: the library allocates nothing; every device buffer is owned by
  * the caller (PyTorch's caching allocator in the Python binding) and only
@@ -227,6 +233,23 @@ int adana_grad_clip_norm(const adana_plan *plan, uint32_t grad_flags, double max
  * bfloat16).  Asynchronous on ``stream``. */
 int adana_grad_scale(const adana_plan *plan, uint32_t grad_flags, const float *d_scale,
                      void *stream);
+
+/* Bytes of device workspace adana_order_stats needs. */
+size_t adana_order_stats_workspace(int32_t n_tensors, int64_t total_ranks);
+
+/* Host-driven, synchronous.  Exact order statistics of float32 tensors: for
+ * each tensor i (h_tensors[i]: device pointer, h_numel[i] elements, any
+ * alignment), the values at ranks h_ranks[h_rank_first[i] ..
+ * h_rank_first[i+1]) (0 <= rank < h_numel[i]) of its ascending order as
+ * np.sort orders it (NaN last; -0 and +0 equal as values), written to the
+ * host array h_values at the same positions.  A multi-rank radix select: 4
+ * to 8 passes that each read the tensors once and histogram the next key
+ * digit per wanted prefix in LDS; between passes the host narrows every rank
+ * to its next digit.  Synchronises ``stream``.  d_workspace: at least
+ * adana_order_stats_workspace(n_tensors, h_rank_first[n_tensors]) bytes. */
+int adana_order_stats(const float *const *h_tensors, const int64_t *h_numel, int32_t n_tensors,
+                      const int64_t *h_ranks, const int64_t *h_rank_first, float *h_values,
+                      void *d_workspace, size_t workspace_bytes, void *stream);
 
 #ifdef __cplusplus
 }

@@ -353,3 +353,21 @@ class OracleOptimizer:
                 else:
                     sums = element_step(self.star, p, g, st["m"], st["v"], st.get("tau"), sc)
                 st.update(finalize_diag(sums, p.size))
+
+
+# --------------------------------------------------------------------------
+# Tau order statistics (src/optim/tau_stats_collector.py:336-376)
+# --------------------------------------------------------------------------
+
+def tau_order_statistics(tau: np.ndarray):
+    """(largest, smallest): np.sort of the flattened values, read at indices
+    unique(int32(1.1**k) - 1) for k = 0..ceil(log n / log 1.1), clamped to
+    n - 1, from the small end and from the large end (NaN sorts last)."""
+    x = np.asarray(tau).reshape(-1)
+    n = x.size
+    if n == 0:
+        return np.array([]), np.array([])
+    s = np.sort(x)
+    max_k = int(np.ceil(np.log(n) / np.log(1.1)))
+    idx = np.minimum(np.unique(np.int32(1.1 ** np.arange(max_k + 1)) - 1), n - 1)
+    return s[(n - 1) - idx], s[idx]

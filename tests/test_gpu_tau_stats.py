@@ -1,0 +1,120 @@
+"""GPU parity of the tau order statistics (adana_order_stats through
+adana_amd.tau_stats) against the oracle's np.sort-based restatement of
+compute_tau_order_statistics (src/optim/tau_stats_collector.py:336-376):
+bit-identical float32 values (NaN equal to NaN; -0 and +0 equal as values,
+as np.sort ranks them), for value distributions and sizes that exercise every
+pass width, and for a real DANA_STAR_MK4 state through
+extract_tau_statistics (:131-160)."""
+import time
+
+import numpy as np
+import pytest
+import torch
+
+pytestmark = [pytest.mark.gpu,
+              pytest.mark.skipif(not torch.cuda.is_available(), reason="needs a ROCm GPU")]
+
+DEV = "cuda:0"
+
+
+def _same(a, b):
+    a = np.asarray(a, np.float64)
+    b = np.asarray(b, np.float64)
+    return a.shape == b.shape and bool(np.all((a == b) | (np.isnan(a) & np.isnan(b))))
+
+
+def _cases(rng):
+    out = []
+    for n in (1, 2, 3, 17, 1000, 16384, 16385, 100_003):
+        out.append((f"uniform{n}", rng.random(n).astype(np.float32)))
+    out.append(("tau_like", np.clip(rng.beta(2, 5, 300_000), 0, 1).astype(np.float32)))
+    out.append(("dups", (rng.integers(0, 7, 200_000) / 8).astype(np.float32)))
+    out.append(("constant", np.full(50_000, 0.25, np.float32)))
+    x = rng.normal(0, 1, 123_457).astype(np.float32)
+    x[::97] = np.nan
+    x[1::101] = 0.0
+    x[2::103] = -0.0
+    x[3::107] = np.inf
+    x[4::109] = -np.inf
+    x[5::113] = 1e-42                                   # denormals
+    out.append(("special", x))
+    out.append(("wide", (10.0 ** rng.uniform(-30, 30, 200_000)).astype(np.float32)))
+    return out
+
+
+def test_order_statistics_match_oracle(oracle_mod):
+    from adana_amd.tau_stats import _stats_for
+
+    rng = np.random.default_rng(3)
+    cases = _cases(rng)
+    print("case: order statistics,", len(cases), "tensors in one batch", flush=True)
+    tensors = [torch.from_numpy(x).to(DEV) for _, x in cases]
+    got = _stats_for(tensors)
+    for (name, x), (gl, gs) in zip(cases, got):
+        wl, ws = oracle_mod.tau_order_statistics(x)
+        assert _same(gl, wl) and _same(gs, ws), name
+        assert gl.dtype == np.float32
+
+
+def test_unaligned_and_empty_tensors(oracle_mod):
+    import adana_amd
+
+    print("case: order statistics unaligned/empty", flush=True)
+    base = torch.rand(10_001, device=DEV)
+    view = base[1:]                                     # 4-byte offset: element-wise loads
+    wl, ws = oracle_mod.tau_order_statistics(view.cpu().numpy())
+    gl, gs = adana_amd.compute_tau_order_statistics(view)
+    assert _same(gl, wl) and _same(gs, ws)
+    e = adana_amd.compute_tau_order_statistics(torch.zeros(0, device=DEV))
+    assert e[0].size == 0 and e[1].size == 0
+
+
+def test_extract_tau_statistics_from_optimizer(oracle_mod):
+    import adana_amd
+
+    print("case: extract_tau_statistics", flush=True)
+    torch.manual_seed(0)
+    shapes = [(256, 64), (64,), (1000, 33), (5,)]
+    for named in (True, False):
+        params = [torch.nn.Parameter(torch.randn(s, device=DEV) * 0.02) for s in shapes]
+        if named:     # src/main.py:367 adds param_names to every group
+            groups = [{"params": params[:2], "param_names": ["w0", "b0"]},
+                      {"params": params[2:], "param_names": ["w1", "b1"]}]
+        else:
+            groups = [{"params": params[:2]}, {"params": params[2:]}]
+        opt = adana_amd.DANA_STAR_MK4(groups, lr=1e-3, kappa=0.85)
+        for _ in range(5):
+            for p in params:
+                p.grad = torch.randn_like(p) * 1e-3
+            opt.step()
+        stats = adana_amd.extract_tau_statistics(opt)
+        g0, g1 = opt.param_groups
+        names = (["w0", "b0", "w1", "b1"] if named else
+                 [f"param_group_{id(g)}_idx_{i}" for g in (g0, g1) for i in range(2)])
+        assert list(stats) == names
+        for name, p in zip(names, params):
+            tau = opt.state[p]["tau"]
+            wl, ws = oracle_mod.tau_order_statistics(tau.cpu().numpy())
+            e = stats[name]
+            assert e["shape"] == tuple(tau.shape) and e["num_elements"] == tau.numel()
+            assert _same(e["largest_order_stats"], wl) and _same(e["smallest_order_stats"], ws), name
+
+
+def test_large_tensor_timing(oracle_mod):
+    """A 64M-element tau-like tensor: equal to the oracle; prints the GPU
+    selection time and the host path's (copy + np.sort) time."""
+    import adana_amd
+
+    print("case: order statistics 64M", flush=True)
+    n = 1 << 26
+    t = torch.rand(n, device=DEV).pow_(2)
+    adana_amd.compute_tau_order_statistics(t[:100_000])    # warm-up
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    gl, gs = adana_amd.compute_tau_order_statistics(t)
+    t1 = time.perf_counter()
+    x = t.cpu().numpy()
+    wl, ws = oracle_mod.tau_order_statistics(x)
+    t2 = time.perf_counter()
+    assert _same(gl, wl) and _same(gs, ws)
+    print(f"64M elements: GPU select {1e3 * (t1 - t0):.1f} ms, copy + np.sort {1e3 * (t2 - t1):.1f} ms", flush=True)

@@ -1,0 +1,77 @@
+"""Tau order statistics: the oracle's restatement of
+compute_tau_order_statistics (src/optim/tau_stats_collector.py:336-376)
+pinned by brute force (pure-Python sort and index formula on small inputs)
+and by invariants; the product's host-side index computation and argument
+checks without a GPU."""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+
+def _brute(values):
+    """Pure Python: sort with NaN last; indices floor(1.1**k) - 1 for
+    k = 0..ceil(log n / log 1.1), deduplicated, clamped to n - 1."""
+    n = len(values)
+    s = sorted(values, key=lambda v: (math.isnan(v), v if not math.isnan(v) else 0.0))
+    max_k = math.ceil(math.log(n) / math.log(1.1))
+    idx = sorted({int(1.1 ** k) - 1 for k in range(max_k + 1)})
+    idx = [min(i, n - 1) for i in idx]
+    return [s[n - 1 - i] for i in idx], [s[i] for i in idx]
+
+
+def _same(a, b):
+    a = np.asarray(a, np.float64)
+    b = np.asarray(b, np.float64)
+    return a.shape == b.shape and bool(np.all((a == b) | (np.isnan(a) & np.isnan(b))))
+
+
+@pytest.mark.parametrize("n", [1, 2, 3, 10, 11, 37, 100, 1000, 4097])
+def test_oracle_matches_brute_force(oracle_mod, n):
+    rng = np.random.default_rng(n)
+    for dist in ("uniform", "dups", "special"):
+        if dist == "uniform":
+            x = rng.random(n).astype(np.float32)
+        elif dist == "dups":
+            x = rng.integers(0, 5, n).astype(np.float32) / 4
+        else:
+            x = rng.normal(0, 1, n).astype(np.float32)
+            x[::7] = np.nan
+            x[1::11] = 0.0
+            x[2::13] = -0.0
+            x[3::17] = np.inf
+        largest, smallest = oracle_mod.tau_order_statistics(x)
+        bl, bs = _brute([float(v) for v in x])
+        assert _same(largest, bl) and _same(smallest, bs), (n, dist)
+
+
+def test_oracle_invariants(oracle_mod):
+    rng = np.random.default_rng(0)
+    x = rng.random(50000).astype(np.float32)
+    largest, smallest = oracle_mod.tau_order_statistics(x)
+    assert smallest[0] == x.min() and largest[0] == x.max()
+    assert np.all(np.diff(smallest) >= 0) and np.all(np.diff(largest) <= 0)
+    assert smallest.dtype == np.float32 and largest.size == smallest.size
+    assert smallest[-1] == largest[-1] == np.sort(x)[-1] or smallest.size > 0
+    e = oracle_mod.tau_order_statistics(np.zeros(0, np.float32))
+    assert e[0].size == 0 and e[1].size == 0
+
+
+@pytest.mark.parametrize("n", [1, 2, 5, 64, 1000, 65536, 10 ** 8])
+def test_product_indices_match_oracle_formula(n):
+    from adana_amd.tau_stats import order_stat_indices
+
+    idx = order_stat_indices(n)
+    max_k = math.ceil(math.log(n) / math.log(1.1))
+    want = sorted({min(int(1.1 ** k) - 1, n - 1) for k in range(max_k + 1)})
+    assert sorted(set(idx.tolist())) == want
+    assert idx.dtype.kind == "i" and idx.max() <= n - 1 and idx.min() >= 0
+
+
+def test_order_values_rejects_cpu_tensors():
+    from adana_amd.tau_stats import order_values
+
+    with pytest.raises(RuntimeError, match="ROCm"):
+        order_values([torch.zeros(4)], [np.array([0])])
+    assert order_values([], []) == []
