@@ -21,6 +21,7 @@ CHUNK_ELEMS = 1024
 ALIGN_ELEMS = 4
 MAX_CLASSES = 8
 FOLD_CHUNKS = 2048
+DIRECT_CHUNKS = 512
 
 VARIANT_STAR = 0x1
 GRAD_BF16 = 0x2

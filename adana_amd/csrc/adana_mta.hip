@@ -560,19 +560,34 @@ __global__ __launch_bounds__(kBlock) void fold_kernel(const adana_tensor_desc *_
     if (threadIdx.x == 0) folds[j] = make_double4(s0, s1, s2, s3);
 }
 
-// Stage 2: one wave per tensor sums its folds and writes the five
-// diagnostics (src/optim/adana.py:146-151, :221-225).
+// Stage 2: one wave per tensor sums its folds -- or, for a tensor of at most
+// ADANA_DIRECT_CHUNKS chunks (no folds), its chunk partials directly, in
+// binary64 -- and writes the five diagnostics (src/optim/adana.py:146-151,
+// :221-225).
 __global__ __launch_bounds__(kBlock) void finalize_kernel(const adana_tensor_desc *__restrict__ desc,
+                                                          const int64_t *__restrict__ vstart,
                                                           const int32_t *__restrict__ fold_first,
-                                                          int32_t n, const double4 *__restrict__ folds,
+                                                          int32_t n, const float *__restrict__ partials,
+                                                          const double4 *__restrict__ folds,
                                                           float *__restrict__ diag) {
     const int lane = threadIdx.x & 63;
     const int i = blockIdx.x * kWaves + (threadIdx.x >> 6);
     if (i >= n) return;                                   // whole wave
     double s0 = 0.0, s1 = 0.0, s2 = 0.0, s3 = 0.0;
-    for (int f = fold_first[i] + lane; f < fold_first[i + 1]; f += 64) {
-        const double4 q = folds[f];
-        s0 += q.x; s1 += q.y; s2 += q.z; s3 += q.w;
+    const int64_t numel = desc[i].numel;
+    if (fold_first[i + 1] > fold_first[i]) {
+        for (int f = fold_first[i] + lane; f < fold_first[i + 1]; f += 64) {
+            const double4 q = folds[f];
+            s0 += q.x; s1 += q.y; s2 += q.z; s3 += q.w;
+        }
+    } else if (numel > 0) {
+        const float4 *p4 = reinterpret_cast<const float4 *>(partials);
+        const int64_t b0 = vstart[i] / kChunk, b1 = (vstart[i] + numel - 1) / kChunk;
+#pragma unroll 8
+        for (int64_t b = b0 + lane; b <= b1; b += 64) {
+            const float4 q = p4[b + i];
+            s0 += q.x; s1 += q.y; s2 += q.z; s3 += q.w;
+        }
     }
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) {
@@ -738,29 +753,44 @@ __global__ __launch_bounds__(kBlock) void sumsq_fold_kernel(const adana_tensor_d
 // Each op rounds to the gradient dtype (bfloat16 gradients give bfloat16
 // norms and coefficient).  clip[0] = total norm, clip[1] = coefficient.
 constexpr int kClipThreads = 1024;
+// One wave per tensor (tensors w, w + 16, ... for wave w) sums the tensor's
+// folds, or its chunk partials directly when it has no folds.
 template <bool GBF16>
-__global__ __launch_bounds__(kClipThreads) void clip_finalize_kernel(const int32_t *__restrict__ fold_first,
-                                                                     int32_t n, const double *__restrict__ folds,
+__global__ __launch_bounds__(kClipThreads) void clip_finalize_kernel(const adana_tensor_desc *__restrict__ desc,
+                                                                     const int64_t *__restrict__ vstart,
+                                                                     const int32_t *__restrict__ fold_first,
+                                                                     int32_t n, const double2 *__restrict__ partials,
+                                                                     const double *__restrict__ folds,
                                                                      float max_norm, float *__restrict__ norms,
                                                                      float *__restrict__ clip) {
-    __shared__ double red[kClipThreads / 64];
+    constexpr int kClipWaves = kClipThreads / 64;
+    __shared__ double red[kClipWaves];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    double tot = 0.0;
-    for (int i = tid; i < n; i += kClipThreads) {
+    double tot = 0.0;                                    // lane 0: this wave's tensors, in order
+    for (int i = wave; i < n; i += kClipWaves) {
         double s = 0.0;
-        for (int f = fold_first[i]; f < fold_first[i + 1]; ++f) s += folds[f];
+        const int64_t numel = desc[i].numel;
+        if (fold_first[i + 1] > fold_first[i]) {
+            for (int f = fold_first[i] + lane; f < fold_first[i + 1]; f += 64) s += folds[f];
+        } else if (numel > 0) {
+            const int64_t b0 = vstart[i] / kChunk, b1 = (vstart[i] + numel - 1) / kChunk;
+#pragma unroll 8
+            for (int64_t b = b0 + lane; b <= b1; b += 64) s += partials[b + i].x;
+        }
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o, 64);
         float nrm = static_cast<float>(sqrt(s));
         if (GBF16) nrm = bf16_round(nrm);
-        if (norms) norms[i] = nrm;
-        tot += static_cast<double>(nrm) * static_cast<double>(nrm);
+        if (lane == 0) {
+            if (norms) norms[i] = nrm;
+            tot += static_cast<double>(nrm) * static_cast<double>(nrm);
+        }
     }
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) tot += __shfl_xor(tot, o, 64);
     if (lane == 0) red[wave] = tot;
     __syncthreads();
     if (tid == 0) {
         double t = 0.0;
-        for (int w = 0; w < kClipThreads / 64; ++w) t += red[w];
+        for (int w = 0; w < kClipWaves; ++w) t += red[w];
         float total = static_cast<float>(sqrt(t));
         if (GBF16) total = bf16_round(total);
         float den = total + 1e-6f;
@@ -982,7 +1012,7 @@ int64_t adana_plan_layout(const int64_t *numel, int32_t n, int64_t *vstart,
         fold_first[i] = static_cast<int32_t>(folds);
         if (numel[i] > 0) {
             const int64_t chunks_i = (off + numel[i] - 1) / kChunk - off / kChunk + 1;
-            folds += (chunks_i + kFold - 1) / kFold;
+            if (chunks_i > ADANA_DIRECT_CHUNKS) folds += (chunks_i + kFold - 1) / kFold;
         }
         off += (numel[i] + ADANA_ALIGN_ELEMS - 1) / ADANA_ALIGN_ELEMS * ADANA_ALIGN_ELEMS;
         if (folds > 0x7fffffffLL) return adana_set_error(ADANA_E_UNSUPPORTED, "adana_plan_layout: list too large");
@@ -1099,7 +1129,7 @@ int step_impl(const char *fn, const adana_plan *plan, const adana_step_scalars *
         if (int rc = launch_status(fn, "fold")) return rc;
     }
     hipLaunchKernelGGL(finalize_kernel, dim3(static_cast<unsigned>((n + kWaves - 1) / kWaves)), dim3(kBlock),
-                       0, st, pl.desc, pl.fold_first, n, folds, d_diag);
+                       0, st, pl.desc, pl.vstart, pl.fold_first, n, partials, folds, d_diag);
     return launch_status(fn, "finalize");
 }
 
@@ -1154,10 +1184,10 @@ int adana_grad_clip_norm(const adana_plan *plan, uint32_t grad_flags, double max
     }
     // torch casts the Python float max_norm to the coefficient's binary32 opmath
     const float mn = static_cast<float>(max_norm);
-    if (gb) hipLaunchKernelGGL(clip_finalize_kernel<true>, dim3(1), dim3(kClipThreads), 0, st, pl.fold_first, n,
-                               folds, mn, d_norms, d_clip);
-    else hipLaunchKernelGGL(clip_finalize_kernel<false>, dim3(1), dim3(kClipThreads), 0, st, pl.fold_first, n,
-                            folds, mn, d_norms, d_clip);
+    if (gb) hipLaunchKernelGGL(clip_finalize_kernel<true>, dim3(1), dim3(kClipThreads), 0, st, pl.desc, pl.vstart,
+                               pl.fold_first, n, partials, folds, mn, d_norms, d_clip);
+    else hipLaunchKernelGGL(clip_finalize_kernel<false>, dim3(1), dim3(kClipThreads), 0, st, pl.desc, pl.vstart,
+                            pl.fold_first, n, partials, folds, mn, d_norms, d_clip);
     return launch_status(fn, "finalize");
 }
 

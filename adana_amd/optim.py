@@ -40,7 +40,7 @@ import numpy as np
 import torch
 from torch.optim import Optimizer
 
-from . import _lib
+from . import _hoststep, _lib
 from .clip import GradPlan, clip_grad_norm_ as _clip_grad_norm
 
 DIAG_KEYS = ("current_alpha", "gradient_norm", "auto_factor_mean",
@@ -434,10 +434,20 @@ class _DanaFamily(Optimizer):
             # src/optim/adana.py:163-167: g2 = g3 = lr, sf = lr / self.lr
             group["weighted_step_count"] += group["lr"] / self.lr
         all_params, gidx = self._flat_params()
+        act = self._active
+        if (self._sets is not None and act is not None
+                and _hoststep.advance_if_same(all_params, act["all_grads"], act["states"])):
+            # Persistent gradients: every p.grad is the same tensor object as at
+            # the last step (grad None where it was None), so the active set,
+            # device tables and scalar classes carry over; advance_if_same has
+            # already done the per-tensor ``state['step'] += 1`` (adana.py:197).
+            grads = act["grads"]
+            classes = act["classes"] = [(gi, t + 1) for gi, t in act["classes"]]
+            params = act["params"]
+            return self._launch(params, grads, classes, loss)
         all_grads = list(map(_GRAD, all_params))
         absent = tuple(map(operator.is_, all_grads, itertools.repeat(None)))   # adana.py:186
 
-        act = self._active
         if self._sets is not None and act is not None and act["absent"] == absent:
             # Steady state: the same tensors have gradients as at the last step, so
             # every active tensor advances by one and the scalar classes carry over.
@@ -451,6 +461,8 @@ class _DanaFamily(Optimizer):
                 if not all(map(operator.is_, new, ls.grads)):
                     ls.grads = new
                     self._refresh_grads(ls)
+            act["all_grads"] = all_grads
+            act["grads"] = grads
         else:
             params, grads, states, keys, index, fresh = [], [], [], [], [], []
             for i, (p, g) in enumerate(zip(all_params, all_grads)):
@@ -491,8 +503,11 @@ class _DanaFamily(Optimizer):
                     self._refresh_grads(ls)
             self._active = {"absent": absent, "all": len(index) == len(all_params),
                             "index": index, "states": states, "params": params,
-                            "classes": classes}
+                            "classes": classes, "all_grads": all_grads, "grads": grads}
+        return self._launch(params, grads, classes, loss)
 
+    def _launch(self, params, grads, classes, loss):
+        """One adana_mta_step (or adana_mta_step_scaled) per launch set."""
         # a clip armed by clip_grad_norm_(..., optimizer=self) on exactly these
         # gradients is applied inside the kernel; otherwise it is applied now
         gscale, wflag = None, 0

@@ -67,8 +67,11 @@ extern "C" {
 #define ADANA_ALIGN_ELEMS 4
 /* Scalar classes (distinct (group, step) pairs) one launch can carry. */
 #define ADANA_MAX_CLASSES 8
-/* Chunk partials one fold workgroup of the diagnostics combine reduces. */
+/* Chunk partials one fold workgroup of the diagnostics combine reduces.
+ * Tensors of at most ADANA_DIRECT_CHUNKS chunks get no fold workgroups: the
+ * finalize step sums their chunk partials directly. */
 #define ADANA_FOLD_CHUNKS 2048
+#define ADANA_DIRECT_CHUNKS 512
 
 /* variant_flags of adana_mta_step */
 #define ADANA_VARIANT_STAR 0x1u  /* Dana-Star(-MK4): tau state and estimator   */
@@ -168,7 +171,9 @@ int adana_step_scalars_init(adana_step_scalars *out, const adana_hparams *hp,
 /* Host only.  Lays n tensors end to end: writes vstart[0..n] (virtual start
  * of each tensor, multiples of ADANA_ALIGN_ELEMS; vstart[n] is the padded
  * total) and fold_first[0..n] (first fold workgroup of each tensor's
- * diagnostics combine; fold_first[n] = *n_folds), and returns the number of
+ * diagnostics combine: ceil(chunks / ADANA_FOLD_CHUNKS) for a tensor of more
+ * than ADANA_DIRECT_CHUNKS chunks, none otherwise; fold_first[n] = *n_folds),
+ * and returns the number of
  * work chunks (>= 0), or a negative error code. */
 int64_t adana_plan_layout(const int64_t *numel, int32_t n, int64_t *vstart,
                           int32_t *fold_first, int64_t *n_folds);

@@ -444,3 +444,26 @@ def test_drift_over_1000_steps(oracle_mod, star):
                 assert n_diff <= 8, (t, n_diff)
     print(f"max drift of p over 1000 steps: {worst:.2f} ulp of max|p|", flush=True)
     assert worst <= 4
+
+
+@pytest.mark.parametrize("star", [False, True])
+def test_large_tensor_fold_path(oracle_mod, star):
+    """Tensors of more than ADANA_DIRECT_CHUNKS chunks go through the fold
+    workgroups; smaller ones are summed directly by the finalize step: both
+    in one list, diagnostics against the oracle (and the clip norm path)."""
+    import adana_amd
+
+    print("case: large tensor fold path star", star, flush=True)
+    rng = np.random.default_rng(9)
+    sizes = [9_000_000, 5, 512 * 1024, 512 * 1024 + 1, 70_000]
+    params = [_normal(rng, (n,), 0.02) for n in sizes]
+    pair = Pair(oracle_mod, star, [(params, {})], lr=1e-3, delta=8.0, kappa=0.85, clipsnr=2.0,
+                weight_decay=0.1, wd_decaying=True, wd_ts=10.0)
+    for k in range(3):
+        gl = [[_normal(rng, x.shape, 1e-3) for x in params]]
+        pair.step(gl)
+        pair.compare(where=f"k={k}")
+    grads = [p.grad for p in pair.gpu_params[0]]
+    total = adana_amd.clip_grad_norm_(pair.gpu_params[0], 1e9)
+    want = float(np.sqrt(sum(float(np.sum(np.square(g.cpu().numpy().astype(np.float64)))) for g in grads)))
+    assert abs(float(total) - want) <= 2e-6 * want

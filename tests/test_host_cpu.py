@@ -103,7 +103,7 @@ def test_plan_layout_properties():
 
     rng = np.random.default_rng(0)
     numels = np.concatenate([rng.integers(0, 70000, 300), [0, 1, 3, 4, 5, 16384, 16385],
-                             [5_000_000, 0, 7]])
+                             [5_000_000, 0, 7, 512 * 1024, 512 * 1024 + 1]])
     vstart, fold_first, chunks, n_folds = _lib.plan_layout(numels)
     C = _lib.CHUNK_ELEMS
     assert vstart[0] == 0
@@ -120,10 +120,12 @@ def test_plan_layout_properties():
             assert b + i not in slots
             slots.add(b + i)
     assert max(slots) < chunks + len(numels)
-    # fold workgroups: ceil(chunks of tensor / FOLD_CHUNKS) per non-empty tensor
+    # fold workgroups: ceil(chunks of tensor / FOLD_CHUNKS) for a tensor of more
+    # than DIRECT_CHUNKS chunks; none for smaller ones (summed directly)
     for i, (vs, n) in enumerate(zip(vstart[:-1], numels)):
         nch = 0 if n == 0 else (vs + n - 1) // C - vs // C + 1
-        assert fold_first[i + 1] - fold_first[i] == math.ceil(nch / _lib.FOLD_CHUNKS)
+        want = math.ceil(nch / _lib.FOLD_CHUNKS) if nch > _lib.DIRECT_CHUNKS else 0
+        assert fold_first[i + 1] - fold_first[i] == want
     assert fold_first[-1] == n_folds
     assert _lib.plan_layout(np.zeros(0, np.int64))[2] == 0
     # the chunk -> first tensor rule the device index kernel applies
@@ -238,3 +240,28 @@ def test_grad_none_is_skipped_without_state():
     opt.step()
     assert len(opt.state[p]) == 0
     assert opt.param_groups[0]["weighted_step_count"] == 1.0
+
+
+def test_hoststep_advance_if_same():
+    """The C steady-state walk: advances every state's step only when every
+    p.grad is the very object recorded at the last step (None included)."""
+    from adana_amd import _hoststep
+
+    class P:
+        def __init__(self, g):
+            self.grad = g
+
+    g1, g2 = object(), object()
+    params = [P(g1), P(None), P(g2)]
+    states = [{"step": 3}, {"step": 7}]
+    assert _hoststep.advance_if_same(params, [g1, None, g2], states) is True
+    assert [s["step"] for s in states] == [4, 8]
+    params[2].grad = object()                                  # a new gradient object
+    assert _hoststep.advance_if_same(params, [g1, None, g2], states) is False
+    assert [s["step"] for s in states] == [4, 8]               # untouched
+    params[2].grad = g2
+    params[1].grad = g1                                        # None -> tensor
+    assert _hoststep.advance_if_same(params, [g1, None, g2], states) is False
+    assert _hoststep.advance_if_same(params, [g1, g1], states) is False   # length mismatch
+    with pytest.raises(KeyError):
+        _hoststep.advance_if_same([], [], [{"m": 1}])
