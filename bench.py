@@ -301,9 +301,10 @@ def main():
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": traffic,
-                     "kernel": ("grad_sumsq_kernel + clip finalize + mta_step_kernel + finalize_kernel "
-                                "(events bracket one step)" if w.get("clip") else
-                                "mta_step_kernel + finalize_kernel (events bracket one step)")},
+                     "kernel": ("grad_sumsq_kernel + sumsq_fold_kernel + clip_finalize_kernel + "
+                                "mta_step_kernel + fold_kernel + finalize_kernel (events bracket one step)"
+                                if w.get("clip") else
+                                "mta_step_kernel + fold_kernel + finalize_kernel (events bracket one step)")},
     }
     del opt, params
     torch.cuda.empty_cache()

@@ -1,0 +1,77 @@
+"""The C ABI driven directly, as a non-Python caller (or INTEGRATION.md's
+ctypes example) would: plan layout, device table, chunk index, workspace,
+one adana_mta_step per step -- against the oracle, bit-exact for m, v and
+tau and under the Dana-Star pow bar for p; diagnostics rtol 1e-5."""
+import ctypes
+
+import numpy as np
+import pytest
+import torch
+
+from helpers import ulp_diff
+from test_gpu_parity import STAR_HARD_CASES
+
+pytestmark = [pytest.mark.gpu,
+              pytest.mark.skipif(not torch.cuda.is_available(), reason="needs a ROCm GPU")]
+
+
+def test_integration_example_through_the_c_abi(oracle_mod):
+    from adana_amd import _lib
+
+    print("case: raw C ABI, Dana-Star-MK4, 1M + 3 + 70000 elements", flush=True)
+    O = oracle_mod
+    L = _lib.lib()
+    rng = np.random.default_rng(4)
+    sizes = [1 << 20, 3, 70_000]
+    p_np = [rng.normal(0, 0.02, n).astype(np.float32) for n in sizes]
+    p = [torch.from_numpy(x.copy()).cuda() for x in p_np]
+    m = [torch.zeros_like(x) for x in p]
+    v = [torch.zeros_like(x) for x in p]
+    tau = [torch.zeros_like(x) for x in p]
+    g = [torch.empty_like(x) for x in p]
+
+    numel = np.array(sizes, dtype=np.int64)
+    vstart, fold_first, n_chunks, n_folds = _lib.plan_layout(numel)
+    desc = np.zeros(len(sizes), _lib.DESC_DTYPE)
+    for i in range(len(sizes)):
+        desc[i] = (p[i].data_ptr(), g[i].data_ptr(), m[i].data_ptr(), v[i].data_ptr(), tau[i].data_ptr(), 0,
+                   sizes[i], 0, _lib.DESC_VEC_OK)
+    table = torch.from_numpy(np.concatenate([desc.view(np.uint8), vstart.view(np.uint8),
+                                             fold_first.view(np.uint8)])).cuda()
+    n = len(sizes)
+    plan = _lib.Plan(desc=table.data_ptr(), vstart=table.data_ptr() + 64 * n,
+                     fold_first=table.data_ptr() + 64 * n + 8 * (n + 1), n_tensors=n,
+                     n_chunks=n_chunks, n_folds=n_folds)
+    chunk_first = torch.empty(n_chunks, dtype=torch.int32, device="cuda")
+    stream = torch.cuda.current_stream().cuda_stream
+    _lib.check(L.adana_plan_index(ctypes.c_void_p(plan.vstart), n, n_chunks,
+                                  ctypes.c_void_p(chunk_first.data_ptr()), ctypes.c_void_p(stream)), "plan_index")
+    plan.chunk_first = chunk_first.data_ptr()
+    ws = torch.empty(_lib.workspace_bytes(plan), dtype=torch.uint8, device="cuda")
+    diag = torch.empty(5 * n, device="cuda")
+    hp = _lib.HParams(peak_lr=1e-3, delta=8.0, kappa=0.85, epsilon=1e-8, weight_decay=0.4, clipsnr=2.0,
+                      wd_ts=10.0, gamma_3_factor=1.0, has_clip=1, wd_decaying=1)
+
+    cpu = {k: [x.copy() if k == "p" else np.zeros_like(x) for x in p_np] for k in ("p", "m", "v", "tau")}
+    for t in range(1, 6):
+        g_np = [rng.normal(0, 1e-3, nn).astype(np.float32) for nn in sizes]
+        for gi, x in zip(g, g_np):
+            gi.copy_(torch.from_numpy(x))
+        sc = (_lib.StepScalars * 1)(_lib.step_scalars(hp, 1e-3, t))
+        _lib.check(L.adana_mta_step(ctypes.byref(plan), ctypes.cast(sc, ctypes.c_void_p), 1, _lib.VARIANT_STAR,
+                                    ctypes.c_void_p(ws.data_ptr()), ws.numel(), ctypes.c_void_p(diag.data_ptr()),
+                                    ctypes.c_void_p(stream)), "mta_step")
+        osc = O.step_scalars(lr=1e-3, peak_lr=1e-3, delta=8.0, kappa=0.85, epsilon=1e-8, weight_decay=0.4,
+                             clipsnr=2.0, wd_decaying=True, wd_ts=10.0, gamma_3_factor=1.0, t=t)
+        sums = [O.element_step(True, cpu["p"][i], g_np[i], cpu["m"][i], cpu["v"][i], cpu["tau"][i], osc)
+                for i in range(n)]
+        torch.cuda.synchronize()
+        d = diag.cpu().numpy().reshape(n, 5)
+        for i in range(n):
+            for key, arr in (("m", m), ("v", v), ("tau", tau)):
+                assert ulp_diff(arr[i].cpu().numpy(), cpu[key][i]).max() == 0, (t, i, key)
+            bad = int(np.count_nonzero(ulp_diff(p[i].cpu().numpy(), cpu["p"][i])))
+            assert bad <= STAR_HARD_CASES, (t, i, bad)
+            cpu["p"][i][...] = p[i].cpu().numpy()
+            ref = O.finalize_diag(sums[i], sizes[i])
+            np.testing.assert_allclose(d[i], [ref[k] for k in O.DIAG_KEYS], rtol=1e-5, atol=1e-30, equal_nan=True)
