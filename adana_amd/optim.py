@@ -110,6 +110,8 @@ class _DanaFamily(Optimizer):
         self._pending_clip = None
         self._clip_plan_obj = None
         self._diag_loc = {}        # param -> (diagnostics buffer, row) of its latest plan
+        self._diag_epoch = 0       # bumped whenever a plan or the state tensors change
+        self._diag_cache = None
         _lib.lib()  # fail at construction, not at the first step, without the kernel library
 
     # -- state ------------------------------------------------------------
@@ -171,6 +173,7 @@ class _DanaFamily(Optimizer):
         self._structure = None
         self._flat = None
         self._active = None
+        self._diag_epoch += 1
 
     def load_state_dict(self, state_dict) -> None:
         """torch's load_state_dict (checkpoints of the reference optimizers load
@@ -350,6 +353,7 @@ class _DanaFamily(Optimizer):
                 for k, key in enumerate(DIAG_KEYS):
                     st[key] = row[k]
                 self._diag_loc[p] = (ls.diag, j)
+        self._diag_epoch += 1
         return out
 
     # -- diagnostics read-out ---------------------------------------------
@@ -358,33 +362,44 @@ class _DanaFamily(Optimizer):
         of a numpy array, in param_groups order, skipping parameters without
         them: one asynchronous device-to-host copy per diagnostics buffer and
         one synchronisation, instead of one ``.item()`` per value.  Returns
-        (params, values[n, 5])."""
-        params, locs = [], []
-        for group in self.param_groups:
-            for p in group["params"]:
+        (params, values[n, 5]).  Where each parameter's row lives is cached
+        until a plan or the state tensors change (call ``invalidate_plan()``
+        after replacing state tensors by hand)."""
+        all_params, _ = self._flat_params()
+        key = (self._diag_epoch, self._flat[0])
+        cache = self._diag_cache
+        if cache is None or cache[0] != key:
+            params, by_buf, loose = [], {}, []
+            for p in all_params:
                 st = self.state.get(p) if p in self.state else None
                 if not st or "current_alpha" not in st:
                     continue
                 loc = self._diag_loc.get(p)
                 if loc is not None and st["current_alpha"].data_ptr() != loc[0].data_ptr() + 20 * loc[1]:
                     loc = None                     # state tensors replaced (e.g. load_state_dict)
+                if loc is None:
+                    loose.append((len(params), st))
+                else:
+                    ent = by_buf.setdefault(id(loc[0]), (loc[0], [], []))
+                    ent[1].append(loc[1])
+                    ent[2].append(len(params))
                 params.append(p)
-                locs.append(loc if loc is not None else st)
-        host = {}
-        for loc in locs:
-            if isinstance(loc, tuple) and id(loc[0]) not in host:
-                h = torch.empty(loc[0].shape, dtype=loc[0].dtype, pin_memory=True)
-                h.copy_(loc[0], non_blocking=True)
-                host[id(loc[0])] = (loc[0].device, h)
-        for dev in {d for d, _ in host.values()}:
+            bufs = [(buf, np.asarray(rows, np.int64), np.asarray(pos, np.int64))
+                    for buf, rows, pos in by_buf.values()]
+            cache = self._diag_cache = (key, params, bufs, loose)
+        _, params, bufs, loose = cache
+        host = []
+        for buf, _, _ in bufs:
+            h = torch.empty(buf.shape, dtype=buf.dtype, pin_memory=True)
+            h.copy_(buf, non_blocking=True)
+            host.append(h)
+        for dev in {buf.device for buf, _, _ in bufs}:
             torch.cuda.current_stream(dev).synchronize()
-        out = np.empty((len(locs), 5), dtype=np.float32)
-        arrays = {k: h.numpy() for k, (_, h) in host.items()}
-        for r, loc in enumerate(locs):
-            if isinstance(loc, tuple):
-                out[r] = arrays[id(loc[0])][loc[1]]
-            else:                                  # loaded, not yet stepped: read one by one
-                out[r] = [float(loc[k]) for k in DIAG_KEYS]
+        out = np.empty((len(params), 5), dtype=np.float32)
+        for (buf, rows, pos), h in zip(bufs, host):
+            out[pos] = h.numpy()[rows]
+        for pos, st in loose:                      # loaded, not yet stepped: read one by one
+            out[pos] = [float(st[k]) for k in DIAG_KEYS]
         return params, out
 
     # -- step -------------------------------------------------------------

@@ -41,9 +41,9 @@ def _dana_values(optimizer):
     parameter order."""
     if hasattr(optimizer, "diagnostics_host"):
         _, vals = optimizer.diagnostics_host()
-        rows = vals.tolist()                 # binary32 values as Python floats, as .item() gives
-        return ([r[0] for r in rows], [r[3] for r in rows], [r[2] for r in rows], [],
-                [r[4] for r in rows])
+        # columns as Python floats (binary32 values, as .item() gives them)
+        col = lambda c: vals[:, c].tolist()                          # noqa: E731
+        return col(0), col(3), col(2), [], col(4)
     alpha, kappa, auto, g2, mnorm = [], [], [], [], []
     for group in optimizer.param_groups:
         for param in group["params"]:

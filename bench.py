@@ -9,7 +9,10 @@ workload is the north-star: Dana-Star-MK4, fp32 params and state, on the
 are the remaining BASELINE configs; north_star_clip adds the training loop's
 gradient-norm clipping before every step (src/optim/base.py:250-257, max_norm
 0.5 as scripts/launch.sh:47) through the optimizer's fused clip, including the
-loop's ``grad_norm.item()``.
+loop's ``grad_norm.item()``.  Two workloads time the step's consumers instead
+of the step: tau_stats (TauStatsCollector's tau order statistics over the
+north-star state, src/optim/tau_stats_collector.py:131-160) and diag_readout
+(log_optimizer_schedules over C5's 10,000 tensors, src/optim/utils.py:532).
 
 Prints ONE JSON line.  ``value`` is the whole-step throughput in algorithmic
 HBM GB/s (bytes the update must move per element x elements / wall-clock ms
@@ -218,6 +221,78 @@ def copy_probe(steps):
     return 0
 
 
+def consumer_bench(args):
+    """Time a consumer of the optimizer state on the GPU against the
+    reference's host path on a bounded sample."""
+    import torch
+    import adana_amd
+    from adana_amd.tau_stats import order_stat_indices
+
+    w = workload("north_star" if args.workload == "tau_stats" else "c5")
+    print(f"[bench] {args.workload}: building {w['name']} state on cuda:0", file=sys.stderr, flush=True)
+    opt, params = build_gpu(w)
+    for _ in range(3):
+        opt.step()
+    torch.cuda.synchronize()
+    if args.workload == "tau_stats":
+        taus = [opt.state[p]["tau"] for p in params]
+        n_elems = sum(t.numel() for t in taus)
+        run = lambda: adana_amd.extract_tau_statistics(opt)       # noqa: E731
+        unit_bytes = 4 * n_elems                                  # tau scanned once per pass
+    else:
+        name = "dana-star-mk4"
+        run = lambda: adana_amd.log_optimizer_schedules(opt, name)  # noqa: E731
+        n_elems = len(params)
+        unit_bytes = 20 * n_elems                                 # five fp32 diagnostics each
+    for _ in range(args.warmup):
+        run()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        run()
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) * 1e3 / args.steps
+    # the reference's host path, timed on a bounded sample
+    if args.workload == "tau_stats":
+        sample = [t for t in taus][:4]                            # first four tensors of the list
+        ns = sum(t.numel() for t in sample)
+        c0 = time.perf_counter()
+        for t in sample:
+            x = t.detach().cpu().flatten().numpy()                # tau_stats_collector.py:151
+            srt = np.sort(x)                                      # :355
+            idx = order_stat_indices(x.size)
+            _ = srt[idx], srt[(x.size - 1) - idx]
+        cpu_ms = (time.perf_counter() - c0) * 1e3
+        cpu = {"value": round(ns / (cpu_ms * 1e-3) / 1e9, 4), "unit": "Gelem/s", "cores": 1,
+               "kind": "port", "sample": f"first 4 tau tensors ({ns} elements): tau.cpu(), np.sort, "
+                                         f"order-statistic picks as src/optim/tau_stats_collector.py:131-160, "
+                                         f"{cpu_ms:.0f} ms"}
+        value = n_elems / (ms * 1e-3) / 1e9
+        metric, unit = "tau order statistics over the north-star state (elements/s)", "Gelem/s"
+    else:
+        c0 = time.perf_counter()
+        vals = []
+        for group in opt.param_groups:                            # src/optim/utils.py:572-596
+            for p in group["params"]:
+                st = opt.state[p]
+                for k in ("current_alpha", "current_kappa_factor", "auto_factor_mean", "m_norm"):
+                    vals.append(st[k].item())
+        cpu_ms = (time.perf_counter() - c0) * 1e3
+        cpu = {"value": round(n_elems / (cpu_ms * 1e-3), 1), "unit": "tensors/s", "cores": 1,
+               "kind": "port", "sample": f"all {n_elems} tensors, value by value (.item() per "
+                                         f"diagnostic) as src/optim/utils.py:572-596, {cpu_ms:.1f} ms"}
+        value = n_elems / (ms * 1e-3)
+        metric, unit = "log_optimizer_schedules over 10,000 tensors (tensors/s)", "tensors/s"
+    print(json.dumps({"metric": metric, "value": round(value, 4), "unit": unit, "n_gpus": 1,
+                      "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 4),
+                      "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+                      "data": "synthetic",
+                      "config": {"workload": args.workload, "state_of": w["name"], "elements": n_elems,
+                                 "bytes_read_once": unit_bytes},
+                      "cpu_baseline": cpu}), flush=True)
+    return 0
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -225,7 +300,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--workload", default="north_star",
                     choices=["north_star", "north_star_clip", "c1", "c2", "c3", "c4", "c5",
-                             "copy_probe"])
+                             "copy_probe", "tau_stats", "diag_readout"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     args = ap.parse_args()
@@ -238,6 +313,8 @@ def main():
 
     if args.workload == "copy_probe":
         return copy_probe(args.steps)
+    if args.workload in ("tau_stats", "diag_readout"):
+        return consumer_bench(args)
     w = workload(args.workload)
     print(f"[bench] workload {w['name']} ({w['optimizer']}): building on cuda:0", file=sys.stderr,
           flush=True)
