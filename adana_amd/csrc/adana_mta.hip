@@ -101,10 +101,19 @@ __device__ __forceinline__ float scale_grad(float g, float s) {
 // specialisations, with any other exponent through the slow-path-guarded pow.
 enum PowKind { POW_GENERAL = 0, POW_ONE = 1, POW_SPECIAL = 2 };
 
+// The pow's tables as the kernel reads them: POW_GENERAL instances copy them
+// into LDS at the start of each workgroup (3 KB), so the per-lane table reads
+// are LDS reads rather than gathers on the vector-memory path that carries
+// the step's streaming loads and stores.
+struct PowTab {
+    const adana::LogPair *log;
+    const double *exp2j;
+};
+
 template <int POWK>
-__device__ __forceinline__ float pow_aten(float x, const adana_step_scalars &sc) {
+__device__ __forceinline__ float pow_aten(float x, const adana_step_scalars &sc, const PowTab &tab) {
     if constexpr (POWK == POW_GENERAL) {
-        return adana::pow_f32_unit_exp(x, sc.star_exp);
+        return adana::pow_f32_unit_exp_tab(x, sc.star_exp, tab.log, tab.exp2j);
     } else if constexpr (POWK == POW_ONE) {
         return 1.0f;
     } else {
@@ -200,12 +209,12 @@ __device__ __forceinline__ float star_phase_b(float p, float g, const StarMid &a
 // One element of either variant (the element-wise tail path).
 template <bool STAR, int POWK>
 __device__ __forceinline__ float update_elem(float p, float g, float &m, float &v, float &tau,
-                                             const adana_step_scalars &sc, float (&acc)[4]) {
+                                             const adana_step_scalars &sc, const PowTab &tab, float (&acc)[4]) {
     if constexpr (!STAR) {
         return adana_elem(p, g, m, v, sc, acc);
     } else {
         const StarMid a = star_phase_a(g, m, v, tau, sc);
-        const float pn = star_phase_b(p, g, a, pow_aten<POWK>(a.et, sc), sc, acc);
+        const float pn = star_phase_b(p, g, a, pow_aten<POWK>(a.et, sc, tab), sc, acc);
         m = a.m;
         v = a.v;
         tau = a.tau;
@@ -217,7 +226,8 @@ __device__ __forceinline__ float update_elem(float p, float g, float &m, float &
 // phase A for all N, then the N pows, then phase B.
 template <bool STAR, int POWK, int N>
 __device__ __forceinline__ void update_n(float (&P)[N], const float (&G)[N], float (&M)[N], float (&V)[N],
-                                         float (&T)[N], const adana_step_scalars &sc, float (&acc)[4]) {
+                                         float (&T)[N], const adana_step_scalars &sc, const PowTab &tab,
+                                         float (&acc)[4]) {
     if constexpr (!STAR) {
 #pragma unroll
         for (int k = 0; k < N; ++k) P[k] = adana_elem(P[k], G[k], M[k], V[k], sc, acc);
@@ -227,7 +237,7 @@ __device__ __forceinline__ void update_n(float (&P)[N], const float (&G)[N], flo
         for (int k = 0; k < N; ++k) a[k] = star_phase_a(G[k], M[k], V[k], T[k], sc);
         float pw[N];
 #pragma unroll
-        for (int k = 0; k < N; ++k) pw[k] = pow_aten<POWK>(a[k].et, sc);
+        for (int k = 0; k < N; ++k) pw[k] = pow_aten<POWK>(a[k].et, sc, tab);
 #pragma unroll
         for (int k = 0; k < N; ++k) {
             P[k] = star_phase_b(P[k], G[k], a[k], pw[k], sc, acc);
@@ -395,6 +405,19 @@ __global__ __launch_bounds__(kChunk / VEC) void mta_step_kernel(const adana_tens
     const int64_t mine = lo + VEC * tid;   // virtual index of this thread's VEC elements
     const bool scaled = pack.gscale != nullptr;                    // uniform
     const float gs = scaled ? *pack.gscale : 1.0f;
+    PowTab tab{adana::kLog, adana::kExp2J};
+    if constexpr (STAR && POWK == POW_GENERAL) {
+        static_assert(kThreads >= 256, "one thread per table entry");
+        __shared__ adana::LogPair s_log[128];
+        __shared__ double s_exp2j[128];
+        if (tid < 128) {
+            s_log[tid] = adana::kLog[tid];
+        } else if (tid < 256) {
+            s_exp2j[tid - 128] = adana::kExp2J[tid - 128];
+        }
+        __syncthreads();
+        tab = PowTab{s_log, s_exp2j};
+    }
 
     for (int i = chunk_first[chunk]; i < n; ++i) {
         const int64_t vs = vstart[i];
@@ -428,7 +451,7 @@ __global__ __launch_bounds__(kChunk / VEC) void mta_step_kernel(const adana_tens
                     for (int k = 0; k < VEC; ++k) G[k] = scale_grad<GBF16>(G[k], gs);
                     if (pack.write_grad) store_grad_n<GBF16, VEC>(d.grad, off, G);
                 }
-                update_n<STAR, POWK, VEC>(P, G, M, V, T, sc, acc);
+                update_n<STAR, POWK, VEC>(P, G, M, V, T, sc, tab, acc);
                 if constexpr (VEC == 4) {
                     const int64_t seg0 = (lo > vs ? lo : vs) - vs;      // uniform
                     const int byte_off = static_cast<int>((off - seg0) * 4);
@@ -452,7 +475,7 @@ __global__ __launch_bounds__(kChunk / VEC) void mta_step_kernel(const adana_tens
                         g = scale_grad<GBF16>(g, gs);
                         if (pack.write_grad) store_grad1<GBF16>(d.grad, off + e, g);
                     }
-                    const float o = update_elem<STAR, POWK>(pp[e], g, mm, vv, tt, sc, acc);
+                    const float o = update_elem<STAR, POWK>(pp[e], g, mm, vv, tt, sc, tab, acc);
                     pp[e] = o;
                     mp[e] = mm;
                     vp[e] = vv;
@@ -847,18 +870,27 @@ size_t workspace_bytes(const adana_plan &pl) {
     return folds_offset(pl) + static_cast<size_t>(pl.n_folds) * 32;
 }
 
-// Residency cap.  The streaming instances (no per-element pow) reach the
-// highest HBM throughput with 4 (fp32 params) or 5 (bf16 params with fp32
-// master) workgroups per CU rather than the 8 their registers allow: fewer
-// concurrent streams contend less in the memory system (measured on MI355X:
-// ADana fp32 13.1 -> 12.1 ms, Dana-Star kappa=1 17.1 -> 16.1 ms, bf16 master
-// 13.0 -> 12.1 ms at 2.65B params).  Dana-Star with the binary64 pow is
-// compute-heavy and runs best at its register-limited 5, uncapped.  The cap
-// is imposed with dynamic LDS the kernel does not touch.
+// Residency cap.  The step reaches the highest HBM throughput with 4 (fp32
+// params) or 5 (bf16 params with fp32 master) workgroups per CU rather than
+// the 7-8 its registers allow: fewer concurrent streams contend less in the
+// memory system (measured on MI355X: ADana fp32 13.1 -> 12.1 ms, Dana-Star
+// kappa=1 17.1 -> 16.1 ms, bf16 master 13.0 -> 12.1 ms at 2.65B params;
+// Dana-Star with the pow, tables in LDS, 16.6 -> 16.3 ms).  The exception is
+// the pow instance on lists of small tensors (`small_tensors`: fewer than 64
+// chunks per tensor on average), whose workgroups spend a larger share of
+// their time in per-segment work (tensor lookup, reductions, partial stores)
+// and in the pow: it runs best at its register limit (Dana-Star over 10,000
+// tensors of 64-65536 elements: 0.715 ms capped, 0.666 ms uncapped; the same
+// list at kappa = 1 prefers the cap, 0.658 against 0.748 ms).  The cap is
+// imposed with dynamic LDS the kernel does not touch.
 template <bool STAR, bool PBF16, int POWK>
-constexpr int residency_cap() {
-    return (STAR && POWK == POW_GENERAL) ? 0 : (PBF16 ? 5 : 4);
+constexpr int residency_cap(bool small_tensors) {
+    return (STAR && POWK == POW_GENERAL && small_tensors) ? 0 : (PBF16 ? 5 : 4);
 }
+
+// Upper bound on the kernel's static LDS (the reduction slots and, for the
+// pow instances, the 3 KB table copy), reserved beside the cap's dynamic LDS.
+constexpr size_t kStaticLdsReserve = 4096;
 
 // Dynamic LDS bytes that leave room for exactly `wgs` workgroups per CU on
 // the current device (0: no cap, or the device's LDS size is unavailable).
@@ -882,10 +914,10 @@ size_t lds_for_cap(int wgs, int64_t n_chunks) {
         lds_per_cu[dev] = cu;
     }
     if (n_chunks < 64 * static_cast<int64_t>(cus[dev])) return 0;
-    // wgs * L <= lds < (wgs + 1) * L, with 1 KB left for the kernel's static LDS
+    // wgs * L <= lds < (wgs + 1) * L, with room left for the kernel's static LDS
     const size_t per_cu = static_cast<size_t>(lds_per_cu[dev]);
-    if (per_cu < 20 * 1024) return 0;
-    const size_t l = per_cu / static_cast<size_t>(wgs) - 1024;
+    if (per_cu < 32 * 1024) return 0;
+    const size_t l = per_cu / static_cast<size_t>(wgs) - kStaticLdsReserve;
     return l <= static_cast<size_t>(lds_per_block[dev]) ? l : 0;
 }
 
@@ -893,7 +925,8 @@ template <bool STAR, bool GBF16, bool PBF16, int POWK>
 void launch_main(int64_t n_chunks, hipStream_t st, const adana_tensor_desc *d, const int64_t *vs,
                  const int32_t *cf, int32_t n, const ScalarPack &pack, float *partials) {
     constexpr int kVec = 4;
-    const size_t lds = lds_for_cap(residency_cap<STAR, PBF16, POWK>(), n_chunks);
+    const bool small_tensors = n_chunks < 64 * static_cast<int64_t>(n);
+    const size_t lds = lds_for_cap(residency_cap<STAR, PBF16, POWK>(small_tensors), n_chunks);
     hipLaunchKernelGGL((mta_step_kernel<STAR, GBF16, PBF16, POWK, kVec>), dim3(static_cast<unsigned>(n_chunks)),
                        dim3(kChunk / kVec), static_cast<unsigned>(lds), st, d, vs, cf, n, pack, partials);
 }

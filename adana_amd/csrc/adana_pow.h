@@ -65,13 +65,17 @@ __device__ __forceinline__ double fma_uc(double a, double b, double c) {
 inline double fma_uc(double a, double b, double c) { return std::fma(a, b, c); }
 #endif
 
-// binary64 x ** y for 1 <= x < 3e38 (finite).  Writes t = y * ln x.
-ADANA_HD inline double pow_core_f64(float x, float y, double &t_out) {
+// binary64 x ** y for 1 <= x < 3e38 (finite).  Writes t = y * ln x.  The
+// tables are passed in so that a kernel can read them from a copy in LDS (the
+// per-lane gathers then stay off the vector-memory path that the streaming
+// loads use); pow_core_f64 reads the global tables.
+ADANA_HD inline double pow_core_tab(float x, float y, double &t_out, const LogPair *log_tab,
+                                    const double *exp_tab) {
     const uint32_t xb = bits_as<uint32_t>(x);
     const int e = static_cast<int>(xb >> 23) - 127;
     const int j = static_cast<int>((xb >> 16) & 127u);
     const double m = static_cast<double>(bits_as<float>((xb & 0x007fffffu) | 0x3f800000u));
-    const LogPair c = kLog[j];
+    const LogPair c = log_tab[j];
     const double r = std::fma(m, c.inv_c, -1.0);
     // log1p(r) = r + r^2 * (-1/2 + r/3 - r^2/4 + r^3/5 - r^4/6 + r^5/7)
     double q = 1.0 / 7.0;
@@ -97,9 +101,13 @@ ADANA_HD inline double pow_core_f64(float x, float y, double &t_out) {
     p = fma_uc(p, rr, 0.5);
     p = std::fma(rr * rr, p, rr);                                // expm1(r')
     const int k = static_cast<int>(kd);
-    const double tj = kExp2J[k & 127];
+    const double tj = exp_tab[k & 127];
     t_out = t;
     return std::ldexp(std::fma(tj, p, tj), k >> 7);
+}
+
+ADANA_HD inline double pow_core_f64(float x, float y, double &t_out) {
+    return pow_core_tab(x, y, t_out, kLog, kExp2J);
 }
 
 // True when fp32(res) may differ from the correctly rounded binary32 x ** y:
@@ -128,11 +136,13 @@ ADANA_HD inline float pow_f32_slow(float x, float y) {
 // correctly rounded result only when x ** y lies within the core's error
 // (~2^-51 relative) of a half-way point -- measured 1 in 2e8 inputs against
 // the C library's pow (tests/pow_harness.cpp).
-ADANA_HD inline float pow_f32_unit_exp(float x, float y) {
+ADANA_HD inline float pow_f32_unit_exp_tab(float x, float y, const LogPair *log_tab, const double *exp_tab) {
     double t;
-    const float r = static_cast<float>(pow_core_f64(x, y, t));
+    const float r = static_cast<float>(pow_core_tab(x, y, t, log_tab, exp_tab));
     return (x < 3.0e38f) ? r : x;
 }
+
+ADANA_HD inline float pow_f32_unit_exp(float x, float y) { return pow_f32_unit_exp_tab(x, y, kLog, kExp2J); }
 
 // Any exponent: the core, and the slow path next to rounding boundaries and
 // outside the core's domain.
