@@ -221,6 +221,50 @@ def copy_probe(steps):
     return 0
 
 
+def stream_ceiling(n_elems, reps=5):
+    """The HBM rate of the Dana-Star step's access pattern without its
+    arithmetic: 5 fp32 arrays read and 4 written back in place, with the step
+    kernel's tiles, load/store policies and residency cap
+    (adana_amd/csrc/stream_probe.hip), at the workload's element count.  The
+    better of 3 and 4 resident workgroups per CU is reported."""
+    import ctypes
+
+    import torch
+
+    lib = ctypes.CDLL(os.path.join(ROOT, "adana_amd", "libadana_probe.so"))
+    fn = lib.adana_probe_stream_5r4w
+    fn.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_void_p]
+    fn.restype = ctypes.c_int
+    n = n_elems // 1024 * 1024
+    arrays = [torch.zeros(n, device="cuda:0") for _ in range(5)]
+    ptrs = (ctypes.c_void_p * 5)(*[a.data_ptr() for a in arrays])
+    stream = torch.cuda.current_stream()
+    best = None
+    for cap in (3, 4):
+        def run():
+            rc = fn(ptrs, n, cap, ctypes.c_void_p(stream.cuda_stream))
+            if rc != 0:
+                raise RuntimeError(f"adana_probe_stream_5r4w failed ({rc})")
+        run()
+        torch.cuda.synchronize()
+        ev = [torch.cuda.Event(enable_timing=True) for _ in range(reps + 1)]
+        for k in range(reps):
+            ev[k].record(stream)
+            run()
+        ev[-1].record(stream)
+        torch.cuda.synchronize()
+        ms = float(np.median([ev[k].elapsed_time(ev[k + 1]) for k in range(reps)]))
+        gbs = 36 * n / (ms * 1e-3) / 1e9
+        if best is None or gbs > best[0]:
+            best = (gbs, cap, ms)
+    del arrays
+    torch.cuda.empty_cache()
+    return {"achieved": round(best[0], 2), "frac": round(best[0] / HBM_PEAK_GBS, 4), "wgs_per_cu": best[1],
+            "ms": round(best[2], 4),
+            "probe": f"5 fp32 arrays of {n} elements read, 4 written back in place, step-kernel access "
+                     f"pattern without arithmetic (stream_probe.hip), median of {reps} launches"}
+
+
 def consumer_bench(args):
     """Time a consumer of the optimizer state on the GPU against the
     reference's host path on a bounded sample."""
@@ -302,6 +346,8 @@ def main():
                     choices=["north_star", "north_star_clip", "c1", "c2", "c3", "c4", "c5",
                              "copy_probe", "tau_stats", "diag_readout"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-ceiling-probe", action="store_true",
+                    help="skip the 5-read/4-write stream probe reported as roofline.mix_ceiling")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     args = ap.parse_args()
     if args.gpus != 1:
@@ -385,6 +431,12 @@ def main():
     }
     del opt, params
     torch.cuda.empty_cache()
+    if bpe == 36 and not w["master"] and not args.no_ceiling_probe:
+        # the same access pattern without the arithmetic: what the memory system allows this mix
+        print("[bench] timing the 5-read/4-write stream probe", file=sys.stderr, flush=True)
+        ceiling = stream_ceiling(n_elems)
+        result["roofline"]["mix_ceiling"] = ceiling
+        result["roofline"]["frac_of_mix_ceiling"] = round(achieved / ceiling["achieved"], 4)
     if not args.no_cpu_baseline:
         print("[bench] timing the CPU oracle baseline", file=sys.stderr, flush=True)
         result["cpu_baseline"] = cpu_baseline(w, target_s=args.cpu_seconds)

@@ -265,3 +265,26 @@ def test_hoststep_advance_if_same():
     assert _hoststep.advance_if_same(params, [g1, g1], states) is False   # length mismatch
     with pytest.raises(KeyError):
         _hoststep.advance_if_same([], [], [{"m": 1}])
+
+
+def test_stream_probe_library_rejects_bad_arguments():
+    """bench.py's stream-rate probe (adana_amd/libadana_probe.so) loads and
+    refuses malformed launches before touching a device."""
+    import ctypes
+    import os
+
+    path = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "adana_amd",
+                        "libadana_probe.so")
+    lib = ctypes.CDLL(path)
+    fn = lib.adana_probe_stream_5r4w
+    fn.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_void_p]
+    fn.restype = ctypes.c_int
+    five = (ctypes.c_void_p * 5)(*([0x1000] * 5))
+    assert fn(None, 1024, 4, None) == -1                  # no array table
+    assert fn(five, 1000, 4, None) == -1                  # not a multiple of 1024
+    assert fn(five, 0, 4, None) == -1                     # empty
+    assert fn(five, 1024, -1, None) == -1                 # negative cap
+    holes = (ctypes.c_void_p * 5)(0x1000, 0x1000, 0, 0x1000, 0x1000)
+    assert fn(holes, 1024, 4, None) == -1                 # null array
+    odd = (ctypes.c_void_p * 5)(0x1000, 0x1004, 0x1000, 0x1000, 0x1000)
+    assert fn(odd, 1024, 4, None) == -1                   # misaligned array
