@@ -2,12 +2,16 @@
 // pattern with the arithmetic taken out, for bench.py's roofline report.
 //
 // The Dana-Star step streams 5 fp32 arrays in (p, g, m, v, tau) and 4 back
-// out in place (p, m, v, tau).  This kernel moves exactly those bytes in
-// exactly the step kernel's way -- one 256-thread workgroup per 1024-element
-// chunk, one 16-byte non-temporal global load per array per thread, 16-byte
-// sc1|nt buffer stores, a residency cap imposed with unused dynamic LDS --
-// and computes only a sum.  Its rate is the ceiling that memory-system
-// effects (stream count, read/write mix) leave for the step itself.
+// out in place (p, m, v, tau), and ends each 1024-element chunk with a
+// workgroup reduction and one 16-byte partial-sum store.  This kernel moves
+// exactly those bytes in exactly the step kernel's way -- one 256-thread
+// workgroup per chunk, one 16-byte non-temporal global load per array per
+// thread, 16-byte sc1|nt buffer stores, the end-of-chunk barrier and partial
+// store, a residency cap imposed with unused dynamic LDS -- and computes only
+// a sum.  Its rate is the ceiling that memory-system effects (stream count,
+// read/write mix) leave for the step itself.  (The end-of-chunk barrier and
+// store are part of the pattern: without them the same stream measured about
+// 5% slower on MI355X.)
 //
 // Not part of the optimizer's interface: built as a separate library
 // (libadana_probe.so) and loaded only by bench.py.
@@ -34,9 +38,35 @@ __device__ __forceinline__ void store_stream(float *chunk_base, int byte_off, F4
         u, __builtin_amdgcn_make_buffer_rsrc(chunk_base, 0, 0x7fffffff, 0x00020000), byte_off, 0, 16 | 2);
 }
 
+// The chunk's sum of s over the workgroup, stored by thread 0 as one float4.
+__device__ __forceinline__ void chunk_partial(F4 s, float4 *partials) {
+    __shared__ float red[kThreads / 64][4];
+    float t[4] = {s.x, s.y, s.z, s.w};
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+#pragma unroll
+        for (int k = 0; k < 4; ++k) t[k] += __shfl_xor(t[k], o, 64);
+    }
+    if ((threadIdx.x & 63) == 0) {
+#pragma unroll
+        for (int k = 0; k < 4; ++k) red[threadIdx.x >> 6][k] = t[k];
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        float4 q = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        for (int w = 0; w < kThreads / 64; ++w) {
+            q.x += red[w][0];
+            q.y += red[w][1];
+            q.z += red[w][2];
+            q.w += red[w][3];
+        }
+        partials[blockIdx.x] = q;
+    }
+}
+
 // arrays a[0..4] are read; a[0..3] are written back (in place)
 __global__ __launch_bounds__(kThreads) void stream_5r4w_kernel(float *a0, float *a1, float *a2, float *a3,
-                                                              float *a4) {
+                                                              float *a4, float4 *partials) {
     float *const a[5] = {a0, a1, a2, a3, a4};
     const int64_t lo = static_cast<int64_t>(blockIdx.x) * kChunk;
     const int64_t i = lo + 4 * threadIdx.x;
@@ -49,30 +79,60 @@ __global__ __launch_bounds__(kThreads) void stream_5r4w_kernel(float *a0, float 
         o.x += static_cast<float>(k);
         store_stream(a[k] + lo, 16 * threadIdx.x, o);
     }
+    chunk_partial(s, partials);
+}
+
+// STREAM copy in the same style: dst[i] = src[i], with the same end of chunk
+__global__ __launch_bounds__(kThreads) void stream_copy_kernel(float *dst, const float *src, float4 *partials) {
+    const int64_t lo = static_cast<int64_t>(blockIdx.x) * kChunk;
+    const F4 x = __builtin_nontemporal_load((const GF4 *)(src + lo + 4 * threadIdx.x));
+    store_stream(dst + lo, 16 * threadIdx.x, x);
+    chunk_partial(x, partials);
+}
+
+// Dynamic LDS bytes for a cap of `wgs` resident workgroups per CU (0: none);
+// -1 when the device cannot be queried or the cap is not expressible.
+int64_t cap_lds(int wgs) {
+    if (wgs == 0) return 0;
+    int dev = 0, per_cu = 0, per_block = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&per_cu, hipDeviceAttributeMaxSharedMemoryPerMultiprocessor, dev) != hipSuccess ||
+        hipDeviceGetAttribute(&per_block, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess)
+        return -1;
+    const int64_t l = static_cast<int64_t>(per_cu) / wgs - 1024;
+    return (l > 0 && l <= per_block) ? l : -1;
 }
 
 }  // namespace
 
 // One launch over n elements of each array (n a positive multiple of 1024;
-// the arrays 16-byte aligned, n elements each, distinct), capped at
-// `wgs_per_cu` resident workgroups per CU (0: no cap).  Returns 0 or a HIP
-// error code; -1 for bad arguments.
-extern "C" int adana_probe_stream_5r4w(float *const *arrays, int64_t n, int wgs_per_cu, hipStream_t stream) {
-    if (!arrays || n <= 0 || n % kChunk != 0 || n / kChunk > 0x7fffffff || wgs_per_cu < 0) return -1;
+// the arrays 16-byte aligned, n elements each, distinct; `partials` room for
+// n / 1024 float4), capped at `wgs_per_cu` resident workgroups per CU (0: no
+// cap).  Returns 0 or a HIP error code; -1 for bad arguments.
+extern "C" int adana_probe_stream_5r4w(float *const *arrays, int64_t n, float4 *partials, int wgs_per_cu,
+                                       hipStream_t stream) {
+    if (!arrays || !partials || n <= 0 || n % kChunk != 0 || n / kChunk > 0x7fffffff || wgs_per_cu < 0)
+        return -1;
     for (int k = 0; k < 5; ++k)
         if (!arrays[k] || reinterpret_cast<uintptr_t>(arrays[k]) % 16 != 0) return -1;
-    size_t lds = 0;
-    if (wgs_per_cu > 0) {
-        int dev = 0, per_cu = 0, per_block = 0;
-        if (hipGetDevice(&dev) != hipSuccess ||
-            hipDeviceGetAttribute(&per_cu, hipDeviceAttributeMaxSharedMemoryPerMultiprocessor, dev) != hipSuccess ||
-            hipDeviceGetAttribute(&per_block, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess)
-            return -1;
-        const size_t l = static_cast<size_t>(per_cu) / static_cast<size_t>(wgs_per_cu) - 1024;
-        if (l > static_cast<size_t>(per_block)) return -1;
-        lds = l;
-    }
+    const int64_t lds = cap_lds(wgs_per_cu);
+    if (lds < 0) return -1;
     hipLaunchKernelGGL(stream_5r4w_kernel, dim3(static_cast<unsigned>(n / kChunk)), dim3(kThreads),
-                       static_cast<unsigned>(lds), stream, arrays[0], arrays[1], arrays[2], arrays[3], arrays[4]);
+                       static_cast<unsigned>(lds), stream, arrays[0], arrays[1], arrays[2], arrays[3], arrays[4],
+                       partials);
+    return static_cast<int>(hipGetLastError());
+}
+
+// STREAM copy of n elements (same conditions as above; dst and src distinct).
+extern "C" int adana_probe_copy(float *dst, const float *src, int64_t n, float4 *partials, int wgs_per_cu,
+                                hipStream_t stream) {
+    if (!dst || !src || !partials || dst == src || n <= 0 || n % kChunk != 0 || n / kChunk > 0x7fffffff ||
+        wgs_per_cu < 0 ||
+        reinterpret_cast<uintptr_t>(dst) % 16 != 0 || reinterpret_cast<uintptr_t>(src) % 16 != 0)
+        return -1;
+    const int64_t lds = cap_lds(wgs_per_cu);
+    if (lds < 0) return -1;
+    hipLaunchKernelGGL(stream_copy_kernel, dim3(static_cast<unsigned>(n / kChunk)), dim3(kThreads),
+                       static_cast<unsigned>(lds), stream, dst, src, partials);
     return static_cast<int>(hipGetLastError());
 }

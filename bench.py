@@ -39,6 +39,7 @@ if ROOT not in sys.path:
 
 METRIC = "optimizer step ms + achieved HBM GB/s (% of peak) at 2.62B params, 1 GPU"
 HBM_PEAK_GBS = 8000.0
+MALL_BYTES = 256 << 20          # MI355X Infinity Cache (memory-side last-level cache)
 
 # Launcher conventions (reference scripts/launch.sh:36-40,188-223,309-312):
 # kappa 0.85, delta 8, omega 4, clipsnr 2.0, weight_decay = omega / wd_ts,
@@ -225,24 +226,26 @@ def stream_ceiling(n_elems, reps=5):
     """The HBM rate of the Dana-Star step's access pattern without its
     arithmetic: 5 fp32 arrays read and 4 written back in place, with the step
     kernel's tiles, load/store policies and residency cap
-    (adana_amd/csrc/stream_probe.hip), at the workload's element count.  The
-    better of 3 and 4 resident workgroups per CU is reported."""
+    (adana_amd/csrc/stream_probe.hip), at the workload's element count; the
+    better of 3 and 4 resident workgroups per CU.  Also a STREAM copy of the
+    same element count in the same style (the better of uncapped and 6)."""
     import ctypes
 
     import torch
 
     lib = ctypes.CDLL(os.path.join(ROOT, "adana_amd", "libadana_probe.so"))
     fn = lib.adana_probe_stream_5r4w
-    fn.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_void_p]
+    fn.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p]
     fn.restype = ctypes.c_int
     n = n_elems // 1024 * 1024
     arrays = [torch.zeros(n, device="cuda:0") for _ in range(5)]
+    partials = torch.empty(n // 1024 * 4, device="cuda:0")
     ptrs = (ctypes.c_void_p * 5)(*[a.data_ptr() for a in arrays])
     stream = torch.cuda.current_stream()
     best = None
     for cap in (3, 4):
         def run():
-            rc = fn(ptrs, n, cap, ctypes.c_void_p(stream.cuda_stream))
+            rc = fn(ptrs, n, ctypes.c_void_p(partials.data_ptr()), cap, ctypes.c_void_p(stream.cuda_stream))
             if rc != 0:
                 raise RuntimeError(f"adana_probe_stream_5r4w failed ({rc})")
         run()
@@ -257,12 +260,40 @@ def stream_ceiling(n_elems, reps=5):
         gbs = 36 * n / (ms * 1e-3) / 1e9
         if best is None or gbs > best[0]:
             best = (gbs, cap, ms)
-    del arrays
+    mix = {"achieved": round(best[0], 2), "frac": round(best[0] / HBM_PEAK_GBS, 4), "wgs_per_cu": best[1],
+           "ms": round(best[2], 4),
+           "probe": f"5 fp32 arrays of {n} elements read, 4 written back in place, one 16-byte partial "
+                    f"per 1024-element chunk: the step kernel's access pattern without its arithmetic "
+                    f"(stream_probe.hip), median of {reps} launches"}
+    # STREAM copy (arrays[1] -> arrays[0]) in the same style, the better of uncapped and 6 per CU
+    cp = lib.adana_probe_copy
+    cp.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p, ctypes.c_int,
+                   ctypes.c_void_p]
+    cp.restype = ctypes.c_int
+    best_copy = None
+    for cap in (0, 6):
+        def run_copy():
+            rc = cp(ctypes.c_void_p(arrays[0].data_ptr()), ctypes.c_void_p(arrays[1].data_ptr()), n,
+                    ctypes.c_void_p(partials.data_ptr()), cap, ctypes.c_void_p(stream.cuda_stream))
+            if rc != 0:
+                raise RuntimeError(f"adana_probe_copy failed ({rc})")
+        run_copy()
+        torch.cuda.synchronize()
+        ev = [torch.cuda.Event(enable_timing=True) for _ in range(reps + 1)]
+        for k in range(reps):
+            ev[k].record(stream)
+            run_copy()
+        ev[-1].record(stream)
+        torch.cuda.synchronize()
+        ms = float(np.median([ev[k].elapsed_time(ev[k + 1]) for k in range(reps)]))
+        gbs = 8 * n / (ms * 1e-3) / 1e9
+        if best_copy is None or gbs > best_copy[0]:
+            best_copy = (gbs, cap)
+    del arrays, partials
     torch.cuda.empty_cache()
-    return {"achieved": round(best[0], 2), "frac": round(best[0] / HBM_PEAK_GBS, 4), "wgs_per_cu": best[1],
-            "ms": round(best[2], 4),
-            "probe": f"5 fp32 arrays of {n} elements read, 4 written back in place, step-kernel access "
-                     f"pattern without arithmetic (stream_probe.hip), median of {reps} launches"}
+    copy = {"achieved": round(best_copy[0], 2), "frac": round(best_copy[0] / HBM_PEAK_GBS, 4),
+            "wgs_per_cu": best_copy[1], "probe": f"STREAM copy of {n} fp32 elements, same access style"}
+    return mix, copy
 
 
 def consumer_bench(args):
@@ -401,6 +432,26 @@ def main():
     achieved = algo_bytes / (kern_ms * 1e-3) / 1e9
     value = algo_bytes / (ms_per_step * 1e-3) / 1e9
 
+    cold = None
+    if algo_bytes < MALL_BYTES:
+        # the step's working set fits in the 256 MB MALL (Infinity Cache) and stays there between
+        # back-to-back steps: also time each step after evicting it with a 1 GiB write
+        flush = torch.empty(1 << 28, device="cuda:0")
+        cold_ms = []
+        for k in range(args.steps):
+            flush.fill_(float(k))
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(stream)
+            one_step(args.warmup + args.steps + k)
+            e1.record(stream)
+            torch.cuda.synchronize()
+            cold_ms.append(e0.elapsed_time(e1))
+        del flush
+        cms = float(np.mean(cold_ms))
+        cold = {"kernel_ms_per_step": round(cms, 4), "achieved": round(algo_bytes / (cms * 1e-3) / 1e9, 2),
+                "frac": round(algo_bytes / (cms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                "note": "MALL evicted before each step by writing a 1 GiB buffer; events bracket the step only"}
+
     traffic = None
     tpath = os.path.join(ROOT, "profiles", f"traffic_{w['name']}.json")
     if os.path.exists(tpath):
@@ -419,6 +470,7 @@ def main():
                    "parallelism": "single GPU",
                    **({"grad_clip": w["clip"], "first_grad_norm": grad_norms[0]} if w.get("clip") else {})},
         "kernel_ms_per_step": round(kern_ms, 4),
+        **({"mall_cold": cold} if cold else {}),
         "kernel_ms_p90": round(float(np.percentile(dev_ms, 90)), 4),
         "params_per_s": round(n_elems / (ms_per_step * 1e-3), 1),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS,
@@ -434,9 +486,11 @@ def main():
     if bpe == 36 and not w["master"] and not args.no_ceiling_probe:
         # the same access pattern without the arithmetic: what the memory system allows this mix
         print("[bench] timing the 5-read/4-write stream probe", file=sys.stderr, flush=True)
-        ceiling = stream_ceiling(n_elems)
+        ceiling, copy = stream_ceiling(n_elems)
         result["roofline"]["mix_ceiling"] = ceiling
         result["roofline"]["frac_of_mix_ceiling"] = round(achieved / ceiling["achieved"], 4)
+        result["roofline"]["stream_copy"] = copy
+        result["roofline"]["frac_of_stream_copy"] = round(achieved / copy["achieved"], 4)
     if not args.no_cpu_baseline:
         print("[bench] timing the CPU oracle baseline", file=sys.stderr, flush=True)
         result["cpu_baseline"] = cpu_baseline(w, target_s=args.cpu_seconds)

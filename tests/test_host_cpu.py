@@ -277,14 +277,24 @@ def test_stream_probe_library_rejects_bad_arguments():
                         "libadana_probe.so")
     lib = ctypes.CDLL(path)
     fn = lib.adana_probe_stream_5r4w
-    fn.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_void_p]
+    fn.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p]
     fn.restype = ctypes.c_int
     five = (ctypes.c_void_p * 5)(*([0x1000] * 5))
-    assert fn(None, 1024, 4, None) == -1                  # no array table
-    assert fn(five, 1000, 4, None) == -1                  # not a multiple of 1024
-    assert fn(five, 0, 4, None) == -1                     # empty
-    assert fn(five, 1024, -1, None) == -1                 # negative cap
+    part = 0x9000
+    assert fn(None, 1024, part, 4, None) == -1            # no array table
+    assert fn(five, 1024, None, 4, None) == -1            # no partials
+    assert fn(five, 1000, part, 4, None) == -1            # not a multiple of 1024
+    assert fn(five, 0, part, 4, None) == -1               # empty
+    assert fn(five, 1024, part, -1, None) == -1           # negative cap
     holes = (ctypes.c_void_p * 5)(0x1000, 0x1000, 0, 0x1000, 0x1000)
-    assert fn(holes, 1024, 4, None) == -1                 # null array
+    assert fn(holes, 1024, part, 4, None) == -1           # null array
     odd = (ctypes.c_void_p * 5)(0x1000, 0x1004, 0x1000, 0x1000, 0x1000)
-    assert fn(odd, 1024, 4, None) == -1                   # misaligned array
+    assert fn(odd, 1024, part, 4, None) == -1             # misaligned array
+    cp = lib.adana_probe_copy
+    cp.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p, ctypes.c_int,
+                   ctypes.c_void_p]
+    cp.restype = ctypes.c_int
+    assert cp(0x1000, 0x1000, 1024, part, 0, None) == -1  # same array
+    assert cp(0x1000, 0x2000, 1000, part, 0, None) == -1  # not a multiple of 1024
+    assert cp(0, 0x2000, 1024, part, 0, None) == -1       # null
+    assert cp(0x1000, 0x2000, 1024, None, 0, None) == -1  # no partials
