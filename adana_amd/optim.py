@@ -349,9 +349,12 @@ class _DanaFamily(Optimizer):
                 ls.diag = torch.full((len(ls.params), 5), float("nan"), dtype=torch.float32,
                                      device=ls.device)
             for j, (p, st) in enumerate(zip(ls.params, ls.states)):
-                row = ls.diag[j]
+                # 0-d tensors over the kernel's output rows, each with a storage
+                # of its own: a deepcopy of one parameter's state (DynamicsLogger,
+                # src/logger/logger.py:93) then copies 4 bytes per diagnostic,
+                # not the whole list's buffer
                 for k, key in enumerate(DIAG_KEYS):
-                    st[key] = row[k]
+                    st[key] = _carve(ls.diag, 5 * j + k, ())
                 self._diag_loc[p] = (ls.diag, j)
         self._diag_epoch += 1
         return out

@@ -15,6 +15,7 @@ restores ``opt.state_dict()``):
     state.
 """
 import io
+import math
 
 import numpy as np
 import pytest
@@ -218,3 +219,88 @@ def test_state_tensors_have_own_storages_in_family_slabs():
     buf = io.BytesIO()
     torch.save(opt.state_dict(), buf)
     assert len(buf.getvalue()) < 3 * 4 * sum(p.numel() for p in params) + 200_000
+
+
+def test_diagnostics_have_own_storages_and_stay_live():
+    """Each 0-d diagnostic is a tensor with a 4-byte storage of its own (a
+    per-parameter deepcopy copies 4 bytes, not the list's buffer) that the
+    kernel still writes every step; the packed read-out agrees with it."""
+    import copy
+    import adana_amd
+
+    print("case: diagnostics storages", flush=True)
+    shapes = [(300, 7), (5,), (4096,), (1, 1)]
+    params = [torch.nn.Parameter(torch.randn(s, device=DEV)) for s in shapes]
+    opt = adana_amd.DANA_STAR_MK4(params, lr=1e-3, kappa=0.85)
+    seen = []
+    for k in range(2):
+        for p in params:
+            p.grad = torch.randn_like(p) * 10.0 ** (-3 - k)
+        opt.step()
+        torch.cuda.synchronize()
+        seen.append([[float(opt.state[p][key]) for key in adana_amd.DIAG_KEYS] for p in params])
+    assert seen[0] != seen[1]                                # rewritten in place by the second step
+    _, packed = opt.diagnostics_host()
+    np.testing.assert_array_equal(packed, np.array(seen[1], np.float32))
+    for p in params:
+        st = opt.state[p]
+        for key in adana_amd.DIAG_KEYS:
+            t = st[key]
+            assert t.dim() == 0 and t.dtype == torch.float32 and t.untyped_storage().nbytes() == 4
+        snap = copy.deepcopy(st)
+        for key in adana_amd.DIAG_KEYS:
+            assert snap[key].untyped_storage().nbytes() == 4
+            assert float(snap[key]) == float(st[key]) or (math.isnan(float(snap[key])) and math.isnan(float(st[key])))
+
+
+def test_distributed_checkpoint_round_trip(tmp_path):
+    """The reference's FSDP checkpoint path (src/optim/utils.py:276-290 save,
+    :316-337 load): get_model/optimizer_state_dict and dcp.save, then, into a
+    fresh model and optimizer (whose state torch first initialises with a
+    zero-gradient, lr=0 step), dcp.load and set_model/optimizer_state_dict.
+    Both runs then continue bit-identically."""
+    import torch.distributed.checkpoint as dcp
+    from torch.distributed.checkpoint.state_dict import (get_model_state_dict, get_optimizer_state_dict,
+                                                         set_model_state_dict, set_optimizer_state_dict)
+    import adana_amd
+
+    print("case: torch.distributed.checkpoint round trip", flush=True)
+
+    def make(seed):
+        torch.manual_seed(seed)
+        model = torch.nn.Sequential(torch.nn.Linear(64, 256), torch.nn.GELU(), torch.nn.Linear(256, 64),
+                                    torch.nn.LayerNorm(64)).to(DEV)
+        opt = adana_amd.DANA_STAR_MK4(model.parameters(), lr=1e-3, kappa=0.85, clipsnr=2.0, weight_decay=0.1,
+                                      wd_decaying=True, wd_ts=10.0)
+        return model, opt
+
+    def train(model, opt, k0, k1):
+        for k in range(k0, k1):
+            gen = torch.Generator(device=DEV)
+            gen.manual_seed(1000 + k)
+            for p in model.parameters():
+                p.grad = torch.randn(p.shape, device=DEV, generator=gen) * 1e-3
+            opt.step()
+
+    a_model, a_opt = make(0)
+    train(a_model, a_opt, 0, 5)
+    sd = {"model": get_model_state_dict(a_model), "optimizer": get_optimizer_state_dict(a_model, a_opt)}
+    dcp.save(sd, checkpoint_id=str(tmp_path / "sharded"))
+
+    b_model, b_opt = make(1)
+    sd_b = {"model": get_model_state_dict(b_model), "optimizer": get_optimizer_state_dict(b_model, b_opt)}
+    dcp.load(sd_b, checkpoint_id=str(tmp_path / "sharded"))
+    set_model_state_dict(b_model, sd_b["model"])
+    set_optimizer_state_dict(b_model, b_opt, sd_b["optimizer"])
+    for ga, gb in zip(a_opt.param_groups, b_opt.param_groups):
+        assert ga["weighted_step_count"] == gb["weighted_step_count"]
+
+    train(a_model, a_opt, 5, 10)
+    train(b_model, b_opt, 5, 10)
+    torch.cuda.synchronize()
+    for pa, pb in zip(a_model.parameters(), b_model.parameters()):
+        assert torch.equal(pa.detach().view(torch.int32), pb.detach().view(torch.int32))
+        sa, sb = a_opt.state[pa], b_opt.state[pb]
+        assert sa["step"] == sb["step"] == 10
+        for key in ("m", "v", "tau"):
+            assert torch.equal(sa[key].view(torch.int32), sb[key].view(torch.int32)), key
