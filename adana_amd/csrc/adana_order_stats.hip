@@ -88,38 +88,79 @@ __global__ __launch_bounds__(kThreads) void select_hist_kernel(PassArgs a) {
     // atomic (same counts; far fewer conflicting atomics).
     int run_bin = -1;
     uint32_t run_len = 0;
-    for (int it = 0; it < kTileElems / (4 * kThreads); ++it) {
-        const int64_t e0 = base + (static_cast<int64_t>(it) * kThreads + threadIdx.x) * 4;
-        if (e0 >= n) break;
-        float v[4];
-        int cnt = 4;
-        if (aligned && e0 + 4 <= n) {
-            const F4 q = __builtin_nontemporal_load((const GLOBAL_AS F4 *)(x + e0));
-            v[0] = q[0]; v[1] = q[1]; v[2] = q[2]; v[3] = q[3];
+    auto add = [&](int b) {
+        if (b == run_bin) {
+            ++run_len;
         } else {
-            cnt = static_cast<int>((n - e0) < 4 ? n - e0 : 4);
-            for (int k = 0; k < cnt; ++k) v[k] = x[e0 + k];
+            if (run_len) atomicAdd(&h[run_bin], run_len);
+            run_bin = b;
+            run_len = 1;
         }
-        for (int k = 0; k < cnt; ++k) {
-            const uint32_t key = order_key(v[k]);
-            int s = 0;
-            if (a.known_bits > 0) {                      // the slot whose prefix matches, if any
-                const uint32_t p = key >> (32 - a.known_bits);
-                int lo = 0, hi = ns - 1;
-                while (lo < hi) {
-                    const int mid = (lo + hi + 1) >> 1;
-                    if (pre[mid] <= p) lo = mid; else hi = mid - 1;
-                }
-                if (pre[lo] != p) continue;
-                s = lo;
+    };
+    // Slot search: the last slot whose prefix is <= p (power-of-two steps
+    // from the largest below ns), run for a batch of values in lock-step so
+    // that their LDS reads overlap; a value counts if that slot's prefix is p.
+    int top = 1;
+    while (top * 2 < ns) top *= 2;
+    constexpr int kIters = kTileElems / (4 * kThreads);
+    // Whole aligned tiles: kBatch 16-byte loads in flight per thread (the LDS
+    // histograms cap residency at a few workgroups per CU, so each thread must
+    // keep several loads outstanding); 8 measured slower (registers).
+    constexpr int kBatch = 4;
+    constexpr int kVals = 4 * kBatch;
+    if (aligned && base + kTileElems <= n) {
+        for (int it = 0; it < kIters; it += kBatch) {
+            F4 q[kBatch];
+#pragma unroll
+            for (int u = 0; u < kBatch; ++u)
+                q[u] = __builtin_nontemporal_load(
+                    (const GLOBAL_AS F4 *)(x + base + (static_cast<int64_t>(it + u) * kThreads + threadIdx.x) * 4));
+            uint32_t key[kVals];
+#pragma unroll
+            for (int u = 0; u < kBatch; ++u) {
+#pragma unroll
+                for (int k = 0; k < 4; ++k) key[4 * u + k] = order_key(q[u][k]);
             }
-            const int b = s * bins + static_cast<int>((key >> shift) & mask);
-            if (b == run_bin) {
-                ++run_len;
+            if (a.known_bits == 0) {
+#pragma unroll
+                for (int e = 0; e < kVals; ++e) add(static_cast<int>((key[e] >> shift) & mask));
             } else {
-                if (run_len) atomicAdd(&h[run_bin], run_len);
-                run_bin = b;
-                run_len = 1;
+                uint32_t p[kVals];
+                int lo[kVals];
+#pragma unroll
+                for (int e = 0; e < kVals; ++e) {
+                    p[e] = key[e] >> (32 - a.known_bits);
+                    lo[e] = 0;
+                }
+                for (int step = top; step > 0; step >>= 1) {
+#pragma unroll
+                    for (int e = 0; e < kVals; ++e) {
+                        const int c = lo[e] + step;
+                        if (c < ns && pre[c] <= p[e]) lo[e] = c;
+                    }
+                }
+#pragma unroll
+                for (int e = 0; e < kVals; ++e)
+                    if (pre[lo[e]] == p[e]) add(lo[e] * bins + static_cast<int>((key[e] >> shift) & mask));
+            }
+        }
+    } else {
+        for (int it = 0; it < kIters; ++it) {
+            const int64_t e0 = base + (static_cast<int64_t>(it) * kThreads + threadIdx.x) * 4;
+            if (e0 >= n) break;
+            const int cnt = static_cast<int>((n - e0) < 4 ? n - e0 : 4);
+            for (int k = 0; k < cnt; ++k) {
+                const uint32_t key = order_key(x[e0 + k]);
+                int sl = 0;
+                if (a.known_bits > 0) {
+                    const uint32_t pk = key >> (32 - a.known_bits);
+                    for (int step = top; step > 0; step >>= 1) {
+                        const int c = sl + step;
+                        if (c < ns && pre[c] <= pk) sl = c;
+                    }
+                    if (pre[sl] != pk) continue;
+                }
+                add(sl * bins + static_cast<int>((key >> shift) & mask));
             }
         }
     }
@@ -214,6 +255,7 @@ int adana_order_stats(const float *const *h_tensor, const int64_t *h_numel, int3
     std::vector<uint32_t> prefix;
     std::vector<int32_t> rank_slot(static_cast<size_t>(total));
     std::vector<uint32_t> hist;
+    std::vector<int64_t> cum;
     int known = 0;
     while (known < 32) {
         // slots: each tensor's distinct prefixes among its wanted ranks, sorted
@@ -263,19 +305,24 @@ int adana_order_stats(const float *const *h_tensor, const int64_t *h_numel, int3
         if ((rc = check(hipMemcpyAsync(hist.data(), ws + L.hist, 4 * hist_n, hipMemcpyDeviceToHost, st), "copy")) ||
             (rc = check(hipStreamSynchronize(st), "synchronize")))
             return rc;
-        // each rank: the digit whose cumulative count passes its residual rank
+        // each slot's cumulative counts, then each rank: the first digit whose
+        // cumulative count exceeds its residual rank (binary search)
+        cum.resize(hist_n);
+        for (size_t sl = 0; sl < prefix.size(); ++sl) {
+            int64_t c = 0;
+            for (int d = 0; d < bins; ++d) {
+                c += hist[sl * bins + d];
+                cum[sl * bins + d] = c;
+            }
+        }
         for (int32_t i = 0; i < n; ++i) {
             for (int64_t j = h_rank_first[i]; j < h_rank_first[i + 1]; ++j) {
-                const uint32_t *hs = hist.data() + (static_cast<size_t>(slot_first[i]) + rank_slot[j]) * bins;
-                int64_t rr = residual[j];
-                int d = 0;
-                for (; d < bins; ++d) {
-                    if (rr < static_cast<int64_t>(hs[d])) break;
-                    rr -= hs[d];
-                }
+                const int64_t *cs = cum.data() + (static_cast<size_t>(slot_first[i]) + rank_slot[j]) * bins;
+                const int64_t rr = residual[j];
+                const int d = static_cast<int>(std::upper_bound(cs, cs + bins, rr) - cs);
                 if (d == bins)
                     return adana_set_error(ADANA_E_HIP, "adana_order_stats: histogram of tensor %d does not cover rank", i);
-                residual[j] = rr;
+                residual[j] = rr - (d > 0 ? cs[d - 1] : 0);
                 rank_prefix[j] = (width == 32 ? 0u : (rank_prefix[j] << width)) | static_cast<uint32_t>(d);
             }
         }
