@@ -16,7 +16,7 @@ import numpy as np
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libadana_mta.so")
 
-ABI_VERSION = 2
+ABI_VERSION = 3
 CHUNK_ELEMS = 1024
 ALIGN_ELEMS = 4
 MAX_CLASSES = 8
@@ -27,6 +27,7 @@ VARIANT_STAR = 0x1
 GRAD_BF16 = 0x2
 PARAM_BF16 = 0x4
 WRITE_GRAD = 0x8
+VARIANT_MANAU = 0x10
 DESC_VEC_OK = 0x1
 
 # adana_tensor_desc as a numpy record (64 bytes, same field order).
@@ -66,6 +67,31 @@ class StepScalars(ctypes.Structure):
 assert ctypes.sizeof(StepScalars) == 64
 
 
+class ManauHParams(ctypes.Structure):
+    """adana_manau_hparams."""
+
+    _fields_ = [
+        ("delta", ctypes.c_double), ("kappa", ctypes.c_double), ("mk4A", ctypes.c_double),
+        ("mk4B", ctypes.c_double), ("clipsnr", ctypes.c_double), ("epsilon", ctypes.c_double),
+        ("weight_decay", ctypes.c_double), ("wd_ts", ctypes.c_double),
+        ("wd_decaying", ctypes.c_int32), ("reserved", ctypes.c_int32),
+    ]
+
+
+class ManauScalars(ctypes.Structure):
+    """adana_manau_scalars (64 bytes; fills an adana_step_scalars slot)."""
+
+    _fields_ = [
+        ("a", ctypes.c_float), ("oma", ctypes.c_float), ("s", ctypes.c_float), ("eps", ctypes.c_float),
+        ("min_p", ctypes.c_float), ("clip", ctypes.c_float), ("lr", ctypes.c_float), ("wdf", ctypes.c_float),
+        ("e", ctypes.c_float * 3), ("mode", ctypes.c_int32 * 3), ("has_wd", ctypes.c_int32),
+        ("reserved", ctypes.c_int32),
+    ]
+
+
+assert ctypes.sizeof(ManauScalars) == 64
+
+
 class Plan(ctypes.Structure):
     """adana_plan: host struct of device pointers."""
 
@@ -77,7 +103,7 @@ class Plan(ctypes.Structure):
 
 # Every symbol include/adana_mta.h declares (checked by the CPU test suite).
 EXPORTS = (
-    "adana_abi_version", "adana_last_error", "adana_step_scalars_init",
+    "adana_abi_version", "adana_last_error", "adana_step_scalars_init", "adana_manau_scalars_init",
     "adana_plan_layout", "adana_plan_index", "adana_workspace_bytes", "adana_mta_step",
     "adana_mta_step_scaled", "adana_grad_clip_norm", "adana_grad_scale",
     "adana_order_stats_workspace", "adana_order_stats",
@@ -100,6 +126,9 @@ def _declare(L) -> None:
     L.adana_step_scalars_init.argtypes = [ctypes.POINTER(StepScalars), ctypes.POINTER(HParams),
                                           ctypes.c_double, i64]
     L.adana_step_scalars_init.restype = ctypes.c_int
+    L.adana_manau_scalars_init.argtypes = [ctypes.POINTER(ManauScalars), ctypes.POINTER(ManauHParams),
+                                           ctypes.c_double, ctypes.c_double, ctypes.c_double]
+    L.adana_manau_scalars_init.restype = ctypes.c_int
     L.adana_plan_layout.argtypes = [P, i32, P, P, ctypes.POINTER(i64)]
     L.adana_plan_layout.restype = i64
     L.adana_plan_index.argtypes = [P, i32, i64, P, P]
@@ -169,6 +198,13 @@ def step_scalars(hp: HParams, lr: float, step: int) -> StepScalars:
     sc = StepScalars()
     check(lib().adana_step_scalars_init(ctypes.byref(sc), ctypes.byref(hp), float(lr), int(step)),
           "adana_step_scalars_init")
+    return sc
+
+
+def manau_scalars(hp: ManauHParams, lr: float, step: float, alpha: float) -> ManauScalars:
+    sc = ManauScalars()
+    check(lib().adana_manau_scalars_init(ctypes.byref(sc), ctypes.byref(hp), float(lr), float(step),
+                                         float(alpha)), "adana_manau_scalars_init")
     return sc
 
 

@@ -54,6 +54,7 @@ static_assert(kChunk == 4 * kBlock, "auxiliary kernels use 256-thread workgroups
 static_assert(ADANA_ALIGN_ELEMS % 4 == 0, "tensors start on vector boundaries");
 static_assert(sizeof(adana_tensor_desc) == 64, "descriptor layout");
 static_assert(sizeof(adana_step_scalars) == 64, "scalar layout");
+static_assert(sizeof(adana_manau_scalars) == sizeof(adana_step_scalars), "Manau scalars share the slot");
 
 struct ScalarPack {
     adana_step_scalars c[ADANA_MAX_CLASSES];
@@ -99,7 +100,13 @@ __device__ __forceinline__ float scale_grad(float g, float s) {
 // < 1) evaluates in binary64 and rounds once (adana_pow.h); POW_ONE (kappa
 // == 1) is exactly 1; POW_SPECIAL dispatches on the remaining ATen
 // specialisations, with any other exponent through the slow-path-guarded pow.
-enum PowKind { POW_GENERAL = 0, POW_ONE = 1, POW_SPECIAL = 2 };
+enum PowKind { POW_GENERAL = 0, POW_ONE = 1, POW_SPECIAL = 2,
+               // Manau's Dana-Star-MK4 branch with mk4A = mk4B = 0 (its other two
+               // powers are then a copy and a one), by the kind of its 1 - kappa
+               // exponent; POW_MANAU_MK4: any exponents, chosen per class at run time
+               POW_MANAU_GENERAL = 3, POW_MANAU_ONE = 4, POW_MANAU_SPECIAL = 5, POW_MANAU_MK4 = 6 };
+constexpr bool is_manau(int powk) { return powk >= POW_MANAU_GENERAL; }
+constexpr bool pow_tables(int powk) { return powk == POW_GENERAL || powk == POW_MANAU_GENERAL; }
 
 // The pow's tables as the kernel reads them: POW_GENERAL instances copy them
 // into LDS at the start of each workgroup (3 KB), so the per-lane table reads
@@ -119,6 +126,7 @@ __device__ __forceinline__ float pow_aten(float x, const adana_step_scalars &sc,
     } else {
         switch (sc.pow_mode) {
         case ADANA_POW_ONE: return 1.0f;
+        case ADANA_POW_IDENTITY: return x;
         case ADANA_POW_SQRT: return sqrtf(x);
         case ADANA_POW_RSQRT: return 1.0f / sqrtf(x);
         case ADANA_POW_RECIP: return 1.0f / x;
@@ -206,11 +214,95 @@ __device__ __forceinline__ float star_phase_b(float p, float g, const StarMid &a
     return pn;
 }
 
+// ---------------------------------------------------------------------------
+// Manau's eager Dana-Star-MK4 branch (src/optim/manau.py:556-613).  Same state
+// as Dana-Star, different op order: multiply-then-add moments (ATen's
+// add_(x, alpha=a) is one fused multiply-add), (|g| + sqrt v) + eps in the
+// tau update, torch.maximum for tau_reg and the effective time, weight decay
+// applied to p before the update, and two more per-element powers for
+// general mk4A / mk4B.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ adana_manau_scalars as_manau(const adana_step_scalars &sc) {
+    adana_manau_scalars m;
+    __builtin_memcpy(&m, &sc, sizeof m);
+    return m;
+}
+
+// torch.maximum: NaN if either operand is NaN, else the larger (the first of equals)
+__device__ __forceinline__ float maximum_f(float a, float b) {
+    if (a != a) return a;
+    if (b != b) return b;
+    return a < b ? b : a;
+}
+
+// x ** e with ATen's pow(Tensor, Scalar) specialisations (mode chosen on the
+// binary64 exponent; e is its binary32 rounding), any other exponent through
+// the slow-path-guarded binary64 pow.
+__device__ __forceinline__ float pow_by_mode(float x, float e, int mode) {
+    switch (mode) {
+    case ADANA_POW_ONE: return 1.0f;
+    case ADANA_POW_IDENTITY: return x;
+    case ADANA_POW_SQRT: return sqrtf(x);
+    case ADANA_POW_RSQRT: return 1.0f / sqrtf(x);
+    case ADANA_POW_RECIP: return 1.0f / x;
+    case ADANA_POW_SQUARE: return x * x;
+    case ADANA_POW_CUBE: return (x * x) * x;
+    case ADANA_POW_INVSQ: return 1.0f / (x * x);
+    default: return adana::pow_f32_via_f64(x, e);
+    }
+}
+
+template <int POWK>
+__device__ __forceinline__ float manau_elem(float p, float g, float &m, float &v, float &tau,
+                                            const adana_manau_scalars &sc, const PowTab &tab, float (&acc)[4]) {
+    const float mn = __builtin_fmaf(g, sc.a, m * sc.oma);            // :567 mul_(1-a).add_(g, alpha=a)
+    const float vn = __builtin_fmaf(sc.a * g, g, v * sc.oma);        // :569 mul_(1-a).addcmul_(g, g, value=a)
+    const float ag = fabsf(g);
+    const float sv = sqrtf(vn);
+    const float tu = ag / ((ag + sv) + sc.eps);                      // :572, _tau_updater :292-299
+    const float tn = __builtin_fmaf(tu, sc.a, tau * sc.oma);         // :573
+    const float ct = clamp_max(tn, 0.5f);                            // _tau_reg :277-282
+    const float pe = ct / (1.0f - ct);
+    const float tr = maximum_f(pe, sc.min_p);
+    const float et = maximum_f(tn * sc.s, 1.0f);                     // _effective_time :288-290
+    const float nt = sqrtf(tr) / (sv + sc.eps);                      // _norm_term :301-310
+    const float mfac = (nt * fabsf(mn)) / tr;                        // :583
+    float af;                                                        // :584-589
+    if constexpr (POWK == POW_MANAU_MK4) {
+        af = (pow_by_mode(et, sc.e[0], sc.mode[0]) * pow_by_mode(mfac, sc.e[1], sc.mode[1])) *
+             pow_by_mode(nt, sc.e[2], sc.mode[2]);
+    } else {                                  // mfac ** 1 is mfac; nt ** 0 is 1, and x * 1 == x
+        float p0;
+        if constexpr (POWK == POW_MANAU_GENERAL) {
+            p0 = adana::pow_f32_unit_exp_tab(et, sc.e[0], tab.log, tab.exp2j);
+        } else if constexpr (POWK == POW_MANAU_ONE) {
+            p0 = 1.0f;
+        } else {
+            p0 = pow_by_mode(et, sc.e[0], sc.mode[0]);
+        }
+        af = p0 * mfac;
+    }
+    af = clamp_max(af, sc.clip);
+    const float i1 = (tr * sign_f(mn)) * af;                         // :590-593 (1.0 * m is m)
+    const float g3t = sc.lr * (i1 + mn * nt);
+    const float g2t = (sc.lr * g) * nt;                              // :600
+    const float u = -(g2t + g3t);                                    // :603
+    float pn = sc.has_wd ? p * sc.wdf : p;                           // :606-610
+    pn = pn + u;                                                     // :613
+    m = mn;
+    v = vn;
+    tau = tn;
+    accumulate(acc, af, g, mfac, mn);                                // :595-598
+    return pn;
+}
+
 // One element of either variant (the element-wise tail path).
 template <bool STAR, int POWK>
 __device__ __forceinline__ float update_elem(float p, float g, float &m, float &v, float &tau,
                                              const adana_step_scalars &sc, const PowTab &tab, float (&acc)[4]) {
-    if constexpr (!STAR) {
+    if constexpr (is_manau(POWK)) {
+        return manau_elem<POWK>(p, g, m, v, tau, as_manau(sc), tab, acc);
+    } else if constexpr (!STAR) {
         return adana_elem(p, g, m, v, sc, acc);
     } else {
         const StarMid a = star_phase_a(g, m, v, tau, sc);
@@ -228,7 +320,11 @@ template <bool STAR, int POWK, int N>
 __device__ __forceinline__ void update_n(float (&P)[N], const float (&G)[N], float (&M)[N], float (&V)[N],
                                          float (&T)[N], const adana_step_scalars &sc, const PowTab &tab,
                                          float (&acc)[4]) {
-    if constexpr (!STAR) {
+    if constexpr (is_manau(POWK)) {
+        const adana_manau_scalars ms = as_manau(sc);
+#pragma unroll
+        for (int k = 0; k < N; ++k) P[k] = manau_elem<POWK>(P[k], G[k], M[k], V[k], T[k], ms, tab, acc);
+    } else if constexpr (!STAR) {
 #pragma unroll
         for (int k = 0; k < N; ++k) P[k] = adana_elem(P[k], G[k], M[k], V[k], sc, acc);
     } else {
@@ -406,7 +502,7 @@ __global__ __launch_bounds__(kChunk / VEC) void mta_step_kernel(const adana_tens
     const bool scaled = pack.gscale != nullptr;                    // uniform
     const float gs = scaled ? *pack.gscale : 1.0f;
     PowTab tab{adana::kLog, adana::kExp2J};
-    if constexpr (STAR && POWK == POW_GENERAL) {
+    if constexpr (STAR && pow_tables(POWK)) {
         static_assert(kThreads >= 256, "one thread per table entry");
         __shared__ adana::LogPair s_log[128];
         __shared__ double s_exp2j[128];
@@ -885,7 +981,7 @@ size_t workspace_bytes(const adana_plan &pl) {
 // imposed with dynamic LDS the kernel does not touch.
 template <bool STAR, bool PBF16, int POWK>
 constexpr int residency_cap(bool small_tensors) {
-    return (STAR && POWK == POW_GENERAL && small_tensors) ? 0 : (PBF16 ? 5 : 4);
+    return (STAR && pow_tables(POWK) && small_tensors) ? 0 : (PBF16 ? 5 : 4);
 }
 
 // Upper bound on the kernel's static LDS (the reduction slots and, for the
@@ -942,8 +1038,18 @@ void launch_pow(int powk, int64_t n_chunks, hipStream_t st, const adana_tensor_d
         launch_main<true, GBF16, PBF16, POW_GENERAL>(n_chunks, st, d, vs, cf, n, pack, partials);
     } else if (powk == POW_ONE) {
         launch_main<true, GBF16, PBF16, POW_ONE>(n_chunks, st, d, vs, cf, n, pack, partials);
-    } else {
+    } else if (powk == POW_SPECIAL) {
         launch_main<true, GBF16, PBF16, POW_SPECIAL>(n_chunks, st, d, vs, cf, n, pack, partials);
+    } else if constexpr (!GBF16 && !PBF16) {        // Manau's branch: float32 only
+        if (powk == POW_MANAU_GENERAL) {
+            launch_main<true, false, false, POW_MANAU_GENERAL>(n_chunks, st, d, vs, cf, n, pack, partials);
+        } else if (powk == POW_MANAU_ONE) {
+            launch_main<true, false, false, POW_MANAU_ONE>(n_chunks, st, d, vs, cf, n, pack, partials);
+        } else if (powk == POW_MANAU_SPECIAL) {
+            launch_main<true, false, false, POW_MANAU_SPECIAL>(n_chunks, st, d, vs, cf, n, pack, partials);
+        } else {
+            launch_main<true, false, false, POW_MANAU_MK4>(n_chunks, st, d, vs, cf, n, pack, partials);
+        }
     }
 }
 
@@ -953,6 +1059,7 @@ void launch_pow(int powk, int64_t n_chunks, hipStream_t st, const adana_tensor_d
 
 int pow_mode_of(double e) {
     if (e == 0.0) return ADANA_POW_ONE;
+    if (e == 1.0) return ADANA_POW_IDENTITY;
     if (e == 0.5) return ADANA_POW_SQRT;
     if (e == -0.5) return ADANA_POW_RSQRT;
     if (e == -1.0) return ADANA_POW_RECIP;
@@ -967,6 +1074,7 @@ int pow_mode_of(double e) {
 float pow0d(float x, double e) {
     switch (pow_mode_of(e)) {
     case ADANA_POW_ONE: return 1.0f;
+    case ADANA_POW_IDENTITY: return x;
     case ADANA_POW_SQRT: return std::sqrt(x);
     case ADANA_POW_RSQRT: return 1.0f / std::sqrt(x);
     case ADANA_POW_RECIP: return 1.0f / x;
@@ -1031,6 +1139,33 @@ int adana_step_scalars_init(adana_step_scalars *out, const adana_hparams *hp, do
     out->opw = 1.0f + wdf;
     out->star_exp = static_cast<float>(1.0 - hp->kappa);
     out->pow_mode = pow_mode_of(1.0 - hp->kappa);
+    return ADANA_OK;
+}
+
+int adana_manau_scalars_init(adana_manau_scalars *out, const adana_manau_hparams *hp, double lr, double step,
+                             double alpha) {
+    if (!out || !hp) return adana_set_error(ADANA_E_INVALID, "adana_manau_scalars_init: null pointer");
+    if (!(step >= 0.0)) return adana_set_error(ADANA_E_INVALID, "adana_manau_scalars_init: step %g < 0", step);
+    // Python floats (src/optim/manau.py:539-555) rounded to binary32 where
+    // they meet float32 tensors: as tensor-scalar operands (mul_, add_,
+    // addcmul_, clamp, lr * tensor, tau * step) and full_like (min_p).
+    memset(out, 0, sizeof *out);
+    out->a = static_cast<float>(alpha);
+    out->oma = static_cast<float>(1.0 - alpha);                  // :567 mul_(1 - alpha)
+    out->s = static_cast<float>(step);                           // :289 tau * step
+    out->eps = static_cast<float>(hp->epsilon);
+    out->min_p = static_cast<float>(1.0 / (1.0 + step));        // :281 full_like(tau, 1/(1+step))
+    out->clip = static_cast<float>(hp->clipsnr);
+    out->lr = static_cast<float>(lr);
+    const double wdf = hp->wd_decaying ? 1.0 - hp->weight_decay / (1.0 + step / hp->wd_ts) * lr
+                                       : 1.0 - hp->weight_decay * lr;            // :606-610
+    out->wdf = static_cast<float>(wdf);
+    out->has_wd = hp->weight_decay != 0.0 ? 1 : 0;
+    const double ex[3] = {1.0 - hp->kappa, 2.0 * hp->mk4B + 1.0, 2.0 * (-hp->mk4A - hp->mk4B)};   // :585-587
+    for (int k = 0; k < 3; ++k) {
+        out->e[k] = static_cast<float>(ex[k]);
+        out->mode[k] = pow_mode_of(ex[k]);
+    }
     return ADANA_OK;
 }
 
@@ -1110,10 +1245,13 @@ int step_impl(const char *fn, const adana_plan *plan, const adana_step_scalars *
               float *d_diag, void *stream) {
     if (int rc = check_plan(plan, fn)) return rc;
     const adana_plan &pl = *plan;
-    const uint32_t allowed = ADANA_VARIANT_STAR | ADANA_GRAD_BF16 | ADANA_PARAM_BF16 |
+    const uint32_t allowed = ADANA_VARIANT_STAR | ADANA_GRAD_BF16 | ADANA_PARAM_BF16 | ADANA_VARIANT_MANAU |
                              (d_grad_scale ? ADANA_WRITE_GRAD : 0u);
     if (variant_flags & ~allowed)
         return adana_set_error(ADANA_E_INVALID, "%s: unknown variant flags 0x%x", fn, variant_flags);
+    const bool manau = variant_flags & ADANA_VARIANT_MANAU;
+    if (manau && (variant_flags & (ADANA_GRAD_BF16 | ADANA_PARAM_BF16)))
+        return adana_set_error(ADANA_E_INVALID, "%s: ADANA_VARIANT_MANAU is float32 only", fn);
     if (int rc = check_plan_arrays(pl, fn)) return rc;
     if (pl.n_tensors == 0) return ADANA_OK;
     if (!d_workspace || !d_diag || !h_scalars)
@@ -1137,16 +1275,28 @@ int step_impl(const char *fn, const adana_plan *plan, const adana_step_scalars *
     const int32_t n = pl.n_tensors;
     if (pl.n_chunks > 0) {
         // one pow code path per launch: all classes must agree on it
-        bool all_one = true, all_general = true;
+        bool all_one = true, all_general = true, mk4_trivial = true;
         for (int c = 0; c < n_classes; ++c) {
-            all_one = all_one && h_scalars[c].pow_mode == ADANA_POW_ONE;
-            all_general = all_general && h_scalars[c].pow_mode == ADANA_POW_GENERAL &&
-                          h_scalars[c].star_exp > 0.0f && h_scalars[c].star_exp < 1.0f;
+            int mode;
+            float e;
+            if (manau) {
+                adana_manau_scalars ms;
+                memcpy(&ms, &h_scalars[c], sizeof ms);
+                mode = ms.mode[0];
+                e = ms.e[0];
+                mk4_trivial = mk4_trivial && ms.mode[1] == ADANA_POW_IDENTITY && ms.mode[2] == ADANA_POW_ONE;
+            } else {
+                mode = h_scalars[c].pow_mode;
+                e = h_scalars[c].star_exp;
+            }
+            all_one = all_one && mode == ADANA_POW_ONE;
+            all_general = all_general && mode == ADANA_POW_GENERAL && e > 0.0f && e < 1.0f;
         }
-        const int powk = all_general ? POW_GENERAL : (all_one ? POW_ONE : POW_SPECIAL);
+        int powk = all_general ? POW_GENERAL : (all_one ? POW_ONE : POW_SPECIAL);
+        if (manau) powk = mk4_trivial ? powk + POW_MANAU_GENERAL : POW_MANAU_MK4;
 #define ADANA_LAUNCH(S, G, P) \
         launch_pow<S, G, P>(powk, pl.n_chunks, st, pl.desc, pl.vstart, pl.chunk_first, n, pack, partials)
-        if (star) {
+        if (star || manau) {
             if (gb) { if (pb) ADANA_LAUNCH(true, true, true); else ADANA_LAUNCH(true, true, false); }
             else    { if (pb) ADANA_LAUNCH(true, false, true); else ADANA_LAUNCH(true, false, false); }
         } else {

@@ -100,6 +100,9 @@ class _DanaFamily(Optimizer):
     """Shared engine of ADana and DANA_STAR_MK4 (one code path for both)."""
 
     _STAR = False
+    _VARIANT = 0                                   # adana_mta_step variant flags
+    _KEYS = ("m", "v", "tau")                      # state keys of the moments and tau
+    _DIAG_COLUMNS = tuple(enumerate(DIAG_KEYS))    # (kernel output column, state key)
 
     def _engine_init(self, master_weights: bool) -> None:
         self.master_weights = bool(master_weights)
@@ -116,7 +119,7 @@ class _DanaFamily(Optimizer):
 
     # -- state ------------------------------------------------------------
     def _state_families(self, p: torch.Tensor):
-        fams = ["m", "v"] + (["tau"] if self._STAR else [])
+        fams = list(self._KEYS[:3 if self._STAR else 2])
         if p.dtype == torch.bfloat16 and self.master_weights:
             fams.append("master")
         return fams
@@ -262,7 +265,7 @@ class _DanaFamily(Optimizer):
         if not (p.is_contiguous() and g.is_contiguous()):
             raise NotImplementedError(f"{type(self).__name__}: non-contiguous parameters or "
                                       "gradients are not supported")
-        flags = _lib.VARIANT_STAR if self._STAR else 0
+        flags = self._VARIANT
         if p.dtype == torch.float32:
             if g.dtype != torch.float32:
                 raise RuntimeError(f"{type(self).__name__}: float32 parameter with {g.dtype} "
@@ -287,9 +290,10 @@ class _DanaFamily(Optimizer):
             master = st.get("master")
             param_ptr = master.data_ptr() if master is not None else p.data_ptr()
             lp_ptr = p.data_ptr() if master is not None else 0
-            tau_ptr = st["tau"].data_ptr() if self._STAR else 0
+            km, kv, kt = self._KEYS
+            tau_ptr = st[kt].data_ptr() if self._STAR else 0
             gp = g.data_ptr()
-            m_ptr, v_ptr = st["m"].data_ptr(), st["v"].data_ptr()
+            m_ptr, v_ptr = st[km].data_ptr(), st[kv].data_ptr()
             ok = (param_ptr % 16 == 0 and m_ptr % 16 == 0 and v_ptr % 16 == 0
                   and tau_ptr % 16 == 0 and gp % (8 if g.dtype == torch.bfloat16 else 16) == 0
                   and lp_ptr % 8 == 0)
@@ -353,8 +357,8 @@ class _DanaFamily(Optimizer):
                 # of its own: a deepcopy of one parameter's state (DynamicsLogger,
                 # src/logger/logger.py:93) then copies 4 bytes per diagnostic,
                 # not the whole list's buffer
-                for k, key in enumerate(DIAG_KEYS):
-                    st[key] = _carve(ls.diag, 5 * j + k, ())
+                for col, key in self._DIAG_COLUMNS:
+                    st[key] = _carve(ls.diag, 5 * j + col, ())
                 self._diag_loc[p] = (ls.diag, j)
         self._diag_epoch += 1
         return out
@@ -371,14 +375,15 @@ class _DanaFamily(Optimizer):
         all_params, _ = self._flat_params()
         key = (self._diag_epoch, self._flat[0])
         cache = self._diag_cache
+        col0, mark = self._DIAG_COLUMNS[0]
         if cache is None or cache[0] != key:
             params, by_buf, loose = [], {}, []
             for p in all_params:
                 st = self.state.get(p) if p in self.state else None
-                if not st or "current_alpha" not in st:
+                if not st or mark not in st:
                     continue
                 loc = self._diag_loc.get(p)
-                if loc is not None and st["current_alpha"].data_ptr() != loc[0].data_ptr() + 20 * loc[1]:
+                if loc is not None and st[mark].data_ptr() != loc[0].data_ptr() + 4 * (5 * loc[1] + col0):
                     loc = None                     # state tensors replaced (e.g. load_state_dict)
                 if loc is None:
                     loose.append((len(params), st))
@@ -402,7 +407,9 @@ class _DanaFamily(Optimizer):
         for (buf, rows, pos), h in zip(bufs, host):
             out[pos] = h.numpy()[rows]
         for pos, st in loose:                      # loaded, not yet stepped: read one by one
-            out[pos] = [float(st[k]) for k in DIAG_KEYS]
+            out[pos] = np.nan
+            for col, k in self._DIAG_COLUMNS:
+                out[pos, col] = float(st[k])
         return params, out
 
     # -- step -------------------------------------------------------------
@@ -544,7 +551,7 @@ class _DanaFamily(Optimizer):
         L = _lib.lib()
         for ls in self._sets:
             n_cls = min(_lib.MAX_CLASSES, len(classes) - ls.class_base)
-            sc_arr = (_lib.StepScalars * n_cls)(*scalars[ls.class_base:ls.class_base + n_cls])
+            sc_arr = (type(scalars[0]) * n_cls)(*scalars[ls.class_base:ls.class_base + n_cls])
             with torch.cuda.device(ls.device):
                 stream = torch.cuda.current_stream(ls.device).cuda_stream
                 if gscale is None:
@@ -619,6 +626,7 @@ class DANA_STAR_MK4(_DanaFamily):
     """
 
     _STAR = True
+    _VARIANT = _lib.VARIANT_STAR
 
     def __init__(self, params: Iterable[torch.Tensor], lr: float = 1.0, delta: float = 8.0,
                  kappa: float = 1.0, mk4A: float = 0.0, mk4B: float = 0.0,

@@ -13,6 +13,8 @@ loop's ``grad_norm.item()``.  Two workloads time the step's consumers instead
 of the step: tau_stats (TauStatsCollector's tau order statistics over the
 north-star state, src/optim/tau_stats_collector.py:131-160) and diag_readout
 (log_optimizer_schedules over C5's 10,000 tensors, src/optim/utils.py:532).
+manau runs Manau (src/optim/manau.py) on the north-star model and reports its
+Dana-Star-MK4 branch (the HIP kernel) beside the whole step.
 
 Prints ONE JSON line.  ``value`` is the whole-step throughput in algorithmic
 HBM GB/s (bytes the update must move per element x elements / wall-clock ms
@@ -368,6 +370,104 @@ def consumer_bench(args):
     return 0
 
 
+def manau_bench(args):
+    """Manau (src/optim/manau.py) on the north-star model: Muon for the 2-D
+    Linear weights, the HIP Dana-Star-MK4 branch for the tied embedding and
+    the 1-D LayerNorm weights.  ``value`` is the Dana branch's algorithmic
+    GB/s (36 B per element, HIP events around its launches); the whole Manau
+    step, bfloat16 Newton-Schulz included, is reported beside it."""
+    import contextlib
+    import io
+
+    import torch
+
+    import adana_amd
+
+    d, layers, vocab = 2560, 32, 50304
+    dev = torch.device("cuda:0")
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(0)
+    decay, nodecay = [], [("transformer.wte.weight", (vocab, d))]
+    for l in range(layers):
+        decay += [(f"transformer.h.{l}.attn.c_attn.weight", (3 * d, d)), (f"transformer.h.{l}.attn.c_proj.weight", (d, d)),
+                  (f"transformer.h.{l}.mlp.c_fc.weight", (4 * d, d)), (f"transformer.h.{l}.mlp.c_proj.weight", (d, 4 * d))]
+        nodecay += [(f"transformer.h.{l}.ln_1.weight", (d,)), (f"transformer.h.{l}.ln_2.weight", (d,))]
+    nodecay += [("transformer.ln_f.weight", (d,))]
+    groups, params = [], []
+    for named, wd in ((decay, 0.1), (nodecay, 0.0)):
+        ps = [torch.nn.Parameter(torch.empty(s, device=dev).normal_(0, 0.02, generator=gen)) for _, s in named]
+        groups.append({"params": ps, "param_names": [n for n, _ in named], "weight_decay": wd})
+        params += ps
+    for p in params:
+        p.grad = torch.empty_like(p).normal_(0, 1e-3, generator=gen)
+    rows = (torch.rand((vocab, 1), device=dev, generator=gen) < 0.1).float()
+    groups[1]["params"][0].grad.mul_(rows)                      # row-sparse embedding gradient
+    hp = dict(lr=2e-2, kappa=0.85, clipsnr=2.0, delta=8.0, wd_decaying=True, wd_ts=10.0)
+    with contextlib.redirect_stdout(io.StringIO()):
+        opt = adana_amd.Manau(groups, **hp)
+    dana = [p for p in params if not opt.state[p]["use_muon"]]
+    n_dana = sum(p.numel() for p in dana)
+    n_muon = sum(p.numel() for p in params) - n_dana
+    print(f"[bench] manau: {n_muon} Muon + {n_dana} Dana params", file=sys.stderr, flush=True)
+    for _ in range(args.warmup):
+        opt.step()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+
+    def timed(fn, k):
+        ev = [torch.cuda.Event(enable_timing=True) for _ in range(k + 1)]
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for i in range(k):
+            ev[i].record(stream)
+            fn()
+        ev[-1].record(stream)
+        torch.cuda.synchronize()
+        return (time.perf_counter() - t0) * 1e3 / k, float(np.mean([ev[i].elapsed_time(ev[i + 1]) for i in range(k)]))
+
+    full_wall, full_dev = timed(opt.step, args.steps)
+    dana_wall, dana_dev = timed(opt._dana_step, args.steps)    # the branch alone, as step() runs it last
+    algo = 36 * n_dana
+    achieved = algo / (dana_dev * 1e-3) / 1e9
+    result = {
+        "metric": "Manau Dana-Star-MK4 branch step, achieved HBM GB/s (north-star model's embedding + 1-D params)",
+        "value": round(algo / (dana_wall * 1e-3) / 1e9, 2), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(dana_wall, 4), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "f32", "data": "synthetic",
+        "config": {"workload": "manau", "optimizer": "Manau", "dana_params": n_dana, "muon_params": n_muon,
+                   "bytes_per_elem": 36, "hyperparams": hp, "grads": "N(0,1e-3); embedding rows nonzero w.p. 0.1"},
+        "kernel_ms_per_step": round(dana_dev, 4),
+        "full_manau_step_ms": round(full_wall, 3),
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "mta_step_kernel (Manau variant) + fold_kernel + finalize_kernel"},
+    }
+    del opt, params, groups
+    torch.cuda.empty_cache()
+    if not args.no_cpu_baseline:
+        from oracle import oracle as O
+
+        threads = O.set_threads(min(len(os.sched_getaffinity(0)), int(os.environ.get("OMP_NUM_THREADS", 16)), 16))
+        rng = np.random.default_rng(3)
+        n = 1 << 25
+        arrs = [rng.normal(0, 0.02, n).astype(np.float32), rng.normal(0, 1e-3, n).astype(np.float32)]
+        m, v, tau = (np.zeros(n, np.float32) for _ in range(3))
+        sc = O.manau_scalars(lr=2e-2, step=5, alpha=8 / 13, kappa=0.85, mk4A=0.0, mk4B=0.0, clipsnr=2.0,
+                             epsilon=1e-8, weight_decay=0.0, wd_decaying=True, wd_ts=10.0)
+        O.manau_element_step(arrs[0], arrs[1], m, v, tau, sc)
+        reps, t0 = 0, time.perf_counter()
+        while time.perf_counter() - t0 < args.cpu_seconds:
+            O.manau_element_step(arrs[0], arrs[1], m, v, tau, sc)
+            reps += 1
+        per = (time.perf_counter() - t0) / reps
+        result["cpu_baseline"] = {"value": round(36 * n / per / 1e9, 3), "unit": "GB/s", "cores": threads,
+                                  "kind": "port",
+                                  "sample": f"{n} elements, {reps} steps of oracle/adana_oracle.c's Manau branch "
+                                            f"with {threads} OpenMP threads, {per * 1e3:.1f} ms/step"}
+    print(json.dumps(result), flush=True)
+    return 0
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -375,7 +475,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--workload", default="north_star",
                     choices=["north_star", "north_star_clip", "c1", "c2", "c3", "c4", "c5",
-                             "copy_probe", "tau_stats", "diag_readout"])
+                             "copy_probe", "tau_stats", "diag_readout", "manau"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-ceiling-probe", action="store_true",
                     help="skip the 5-read/4-write stream probe reported as roofline.mix_ceiling")
@@ -392,6 +492,8 @@ def main():
         return copy_probe(args.steps)
     if args.workload in ("tau_stats", "diag_readout"):
         return consumer_bench(args)
+    if args.workload == "manau":
+        return manau_bench(args)
     w = workload(args.workload)
     print(f"[bench] workload {w['name']} ({w['optimizer']}): building on cuda:0", file=sys.stderr,
           flush=True)

@@ -23,7 +23,11 @@
  *        (src/optim/adana.py:81-153) and DANA_STAR_MK4._update_param_compiled
  *        (src/optim/dana_star_mk4.py:105-205) for ALL tensors of the list,
  *        plus the diagnostics stored at src/optim/adana.py:221-225 /
- *        src/optim/dana_star_mk4.py:290-294.
+ *        src/optim/dana_star_mk4.py:290-294; with ADANA_VARIANT_MANAU, the
+ *        eager Dana-Star-MK4 branch of Manau.step (src/optim/manau.py:504-613)
+ *        for the parameters Manau does not give to Muon.
+ *   adana_manau_scalars_init <- that branch's host scalars (manau.py:539-555,
+ *        :606-610 and the Python-float operands of its tensor ops).
  *   adana_grad_clip_norm     <- the gradient-norm clipping the training loop
  *        runs before every step (src/optim/base.py:250-257 ->
  *        src/distributed/backend.py:33-35 -> torch.nn.utils.clip_grad_norm_):
@@ -58,7 +62,7 @@
 extern "C" {
 #endif
 
-#define ADANA_ABI_VERSION 2
+#define ADANA_ABI_VERSION 3
 
 /* Elements per work chunk (one 256-thread workgroup, one 16-byte vector per
  * thread per array).  Tensors start at multiples of ADANA_ALIGN_ELEMS in the
@@ -79,6 +83,9 @@ extern "C" {
 #define ADANA_PARAM_BF16   0x4u  /* param = fp32 master; param_lp = bf16 copy  */
 #define ADANA_WRITE_GRAD   0x8u  /* adana_mta_step_scaled: store the scaled
                                     gradient back into grad                   */
+#define ADANA_VARIANT_MANAU 0x10u /* Manau's Dana-Star-MK4 branch: tau state,
+                                    Manau's op order; float32 only; scalars
+                                    from adana_manau_scalars_init            */
 
 /* adana_tensor_desc.flags */
 #define ADANA_DESC_VEC_OK  0x1u  /* all pointers aligned for 16-byte access   */
@@ -152,11 +159,48 @@ typedef struct adana_step_scalars {
     int32_t reserved;
 } adana_step_scalars;
 
-/* pow(Tensor, Scalar) specialisations ATen selects on the binary64 exponent */
+/* pow(Tensor, Scalar) specialisations ATen selects on the binary64 exponent
+ * (ONE: exponent 0, the result is 1; IDENTITY: exponent 1, a copy) */
 enum {
     ADANA_POW_GENERAL = 0, ADANA_POW_ONE, ADANA_POW_SQRT, ADANA_POW_RSQRT,
-    ADANA_POW_RECIP, ADANA_POW_SQUARE, ADANA_POW_CUBE, ADANA_POW_INVSQ
+    ADANA_POW_RECIP, ADANA_POW_SQUARE, ADANA_POW_CUBE, ADANA_POW_INVSQ,
+    ADANA_POW_IDENTITY
 };
+
+/* Hyper-parameters of one Manau parameter group that its Dana-Star-MK4
+ * branch reads (group keys, src/optim/manau.py:121-173, :509-519). */
+typedef struct adana_manau_hparams {
+    double  delta;
+    double  kappa;
+    double  mk4A;
+    double  mk4B;
+    double  clipsnr;
+    double  epsilon;
+    double  weight_decay;
+    double  wd_ts;
+    int32_t wd_decaying;
+    int32_t reserved;
+} adana_manau_hparams;
+
+/* Per-step binary32 scalars of one class of Manau's branch.  Same size as
+ * adana_step_scalars: launches with ADANA_VARIANT_MANAU pass an array of
+ * these where adana_mta_step takes h_scalars. */
+typedef struct adana_manau_scalars {
+    float   a;          /* fp32(alpha), alpha the branch's binary64 value    */
+    float   oma;        /* fp32(1 - alpha), difference in binary64           */
+    float   s;          /* fp32(step) (a weighted step count with weight_time)*/
+    float   eps;        /* fp32(epsilon)                                     */
+    float   min_p;      /* fp32(1 / (1 + step)), binary64 quotient           */
+    float   clip;       /* fp32(clipsnr)                                     */
+    float   lr;         /* fp32(lr)                                          */
+    float   wdf;        /* fp32(1 - wd / (1 + step / wd_ts) * lr) or
+                           fp32(1 - wd * lr), binary64 arithmetic            */
+    float   e[3];       /* exponents 1 - kappa, 2 mk4B + 1, 2 (-mk4A - mk4B),
+                           rounded to binary32                               */
+    int32_t mode[3];    /* ADANA_POW_* of each exponent (binary64 value)     */
+    int32_t has_wd;     /* weight_decay != 0                                 */
+    int32_t reserved;
+} adana_manau_scalars;
 
 int adana_abi_version(void);
 
@@ -167,6 +211,12 @@ size_t adana_last_error(char *buf, size_t len);
  * (group['lr']) and per-tensor step ``step`` (state['step'] after += 1). */
 int adana_step_scalars_init(adana_step_scalars *out, const adana_hparams *hp,
                             double lr, int64_t step);
+
+/* Host only.  Scalars of one tensor update of Manau's branch at learning
+ * rate ``lr`` with the branch's ``step`` (state['step'], or the group's
+ * weighted step count when weight_time) and ``alpha`` (manau.py:548-555). */
+int adana_manau_scalars_init(adana_manau_scalars *out, const adana_manau_hparams *hp,
+                             double lr, double step, double alpha);
 
 /* Host only.  Lays n tensors end to end: writes vstart[0..n] (virtual start
  * of each tensor, multiples of ADANA_ALIGN_ELEMS; vstart[n] is the padded

@@ -10,6 +10,8 @@
  *                               src/optim/adana.py:100-151
  *   adana_oracle_star_step   <- DANA_STAR_MK4._update_param_compiled
  *                               src/optim/dana_star_mk4.py:136-203
+ *   adana_oracle_manau_step  <- Manau.step's Dana-Star-MK4 branch
+ *                               src/optim/manau.py:556-613
  *
  * Arithmetic contract (the oracle of record):
  *   - every tensor op of the reference is one IEEE-754 binary32 operation,
@@ -55,14 +57,49 @@ typedef struct {
     int32_t pow_mode; /* ATen's pow(Tensor, Scalar) specialisation, below     */
 } adana_oracle_scalars;
 
+/* Manau's Dana-Star-MK4 branch (src/optim/manau.py:556-613): its scalars
+ * are the branch's Python floats rounded to binary32 where they meet float32
+ * tensors (tensor-scalar operands, full_like). */
+typedef struct {
+    float a;        /* fp32(alpha)                                        */
+    float oma;      /* fp32(1 - alpha), binary64 difference               */
+    float s;        /* fp32(step)                                         */
+    float eps;      /* fp32(epsilon)                                      */
+    float min_p;    /* fp32(1 / (1 + step)), binary64 quotient            */
+    float clip;     /* fp32(clipsnr)                                      */
+    float lr;       /* fp32(lr)                                           */
+    float wdf;      /* fp32(1 - wd/(1+step/wd_ts)*lr) or fp32(1 - wd*lr)  */
+    float e[3];     /* fp32 exponents: 1-kappa, 2 mk4B + 1, 2 (-mk4A - mk4B) */
+    int32_t mode[3];/* their ATen specialisations                         */
+    int32_t has_wd; /* weight_decay != 0                                  */
+    int32_t reserved;
+} adana_oracle_manau_scalars;
+
 /* pow(Tensor, Scalar) specialisations in ATen, chosen on the binary64
  * exponent: 0 -> ones, 0.5 -> sqrt, -0.5 -> 1/sqrt, -1 -> 1/x, 2 -> x*x,
  * 3 -> x*x*x, -2 -> 1/(x*x); anything else is a general pow. */
-enum { POW_GENERAL = 0, POW_ONE, POW_SQRT, POW_RSQRT, POW_RECIP, POW_SQUARE, POW_CUBE, POW_INVSQ };
+enum { POW_GENERAL = 0, POW_ONE, POW_SQRT, POW_RSQRT, POW_RECIP, POW_SQUARE, POW_CUBE, POW_INVSQ, POW_IDENTITY };
+
+/* x ** e by ATen's specialisation `mode` (chosen on the binary64 exponent);
+ * any other exponent: binary64 pow of the binary32 exponent, rounded once. */
+static inline float o_pow_mode(float x, float e, int32_t mode) {
+    switch (mode) {
+    case POW_ONE: return 1.0f;
+    case POW_IDENTITY: return x;
+    case POW_SQRT: return sqrtf(x);
+    case POW_RSQRT: return 1.0f / sqrtf(x);
+    case POW_RECIP: return 1.0f / x;
+    case POW_SQUARE: return x * x;
+    case POW_CUBE: return (x * x) * x;
+    case POW_INVSQ: return 1.0f / (x * x);
+    default: return (float)pow((double)x, (double)e);
+    }
+}
 
 static inline float o_pow(float x, const adana_oracle_scalars *sc) {
     switch (sc->pow_mode) {
     case POW_ONE: return 1.0f;
+    case POW_IDENTITY: return x;
     case POW_SQRT: return sqrtf(x);
     case POW_RSQRT: return 1.0f / sqrtf(x);
     case POW_RECIP: return 1.0f / x;
@@ -159,6 +196,49 @@ static inline float star_elem(float p, float g, float *mp, float *vp, float *tp,
     return p;
 }
 
+static inline float o_maximum(float a, float b) {   /* torch.maximum: NaN propagates */
+    if (a != a) return a;
+    if (b != b) return b;
+    return a < b ? b : a;
+}
+
+/* One element of Manau's Dana-Star-MK4 branch (src/optim/manau.py:566-613).
+ * ATen's add_(x, alpha=a) and addcmul_(g, g, value=a) are single-rounded
+ * FMAs (probed bitwise against torch 2.10's CPU kernels). */
+static inline float manau_elem(float p, float g, float *mp, float *vp, float *tp,
+                               const adana_oracle_manau_scalars *sc, double acc[4]) {
+    float m = fmaf(g, sc->a, *mp * sc->oma);                 /* :567 */
+    float v = fmaf(sc->a * g, g, *vp * sc->oma);             /* :569 */
+    float ag = fabsf(g);
+    float sv = sqrtf(v);
+    float tu = ag / ((ag + sv) + sc->eps);                   /* :572, _tau_updater :292-299 */
+    float tau = fmaf(tu, sc->a, *tp * sc->oma);              /* :573 */
+    float ct = o_clamp_max(tau, 0.5f);                       /* _tau_reg :277-282 */
+    float pe = ct / (1.0f - ct);
+    float tr = o_maximum(pe, sc->min_p);
+    float et = o_maximum(tau * sc->s, 1.0f);                 /* _effective_time :288-290 */
+    float nt = sqrtf(tr) / (sv + sc->eps);                   /* _norm_term :301-310 */
+    float mfac = (nt * fabsf(m)) / tr;                       /* :583 */
+    float af = (o_pow_mode(et, sc->e[0], sc->mode[0]) *      /* :584-589 */
+                o_pow_mode(mfac, sc->e[1], sc->mode[1])) * o_pow_mode(nt, sc->e[2], sc->mode[2]);
+    af = o_clamp_max(af, sc->clip);
+    float i1 = (tr * o_sign(m)) * af;                        /* :590-593 */
+    float i2 = (1.0f * m) * nt;
+    float g3 = sc->lr * (i1 + i2);
+    float g2 = (sc->lr * g) * nt;                            /* :600 */
+    float u = -(g2 + g3);                                    /* :603 */
+    if (sc->has_wd) p = p * sc->wdf;                         /* :606-610 */
+    p = p + u;                                               /* :613 */
+    *mp = m;
+    *vp = v;
+    *tp = tau;
+    acc[0] += (double)af;                                    /* :595-598 */
+    acc[1] += (double)g * (double)g;
+    acc[2] += (double)mfac;
+    acc[3] += (double)m * (double)m;
+    return p;
+}
+
 /* Parallel element loops.  Element results do not depend on the thread
  * count; the binary64 diagnostic sums may differ in the last bits. */
 #define DIAG_LOOP(BODY)                                                        \
@@ -179,6 +259,11 @@ void adana_oracle_adana_step(int64_t n, float *p, const float *g, float *m, floa
 void adana_oracle_star_step(int64_t n, float *p, const float *g, float *m, float *v,
                             float *tau, const adana_oracle_scalars *sc, double diag[4]) {
     DIAG_LOOP(p[i] = star_elem(p[i], g[i], &m[i], &v[i], &tau[i], sc, acc))
+}
+
+void adana_oracle_manau_step(int64_t n, float *p, const float *g, float *m, float *v, float *tau,
+                             const adana_oracle_manau_scalars *sc, double diag[4]) {
+    DIAG_LOOP(p[i] = manau_elem(p[i], g[i], &m[i], &v[i], &tau[i], sc, acc))
 }
 
 /* bf16-parameter mode (an extension; the reference has no master weights):

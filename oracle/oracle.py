@@ -52,6 +52,17 @@ class OracleScalars(ctypes.Structure):
     ]
 
 
+class OracleManauScalars(ctypes.Structure):
+    """Mirror of ``adana_oracle_manau_scalars`` in adana_oracle.c."""
+
+    _fields_ = [
+        ("a", ctypes.c_float), ("oma", ctypes.c_float), ("s", ctypes.c_float), ("eps", ctypes.c_float),
+        ("min_p", ctypes.c_float), ("clip", ctypes.c_float), ("lr", ctypes.c_float), ("wdf", ctypes.c_float),
+        ("e", ctypes.c_float * 3), ("mode", ctypes.c_int32 * 3), ("has_wd", ctypes.c_int32),
+        ("reserved", ctypes.c_int32),
+    ]
+
+
 _lib = None
 
 
@@ -68,6 +79,7 @@ def lib():
         SP = ctypes.POINTER(OracleScalars)
         L.adana_oracle_adana_step.argtypes = [i64, P, P, P, P, SP, P]
         L.adana_oracle_star_step.argtypes = [i64, P, P, P, P, P, SP, P]
+        L.adana_oracle_manau_step.argtypes = [i64, P, P, P, P, P, ctypes.POINTER(OracleManauScalars), P]
         L.adana_oracle_master_step.argtypes = [i64, i32, P, P, P, P, P, P, SP, P]
         L.adana_oracle_step_g16.argtypes = [i64, i32, P, P, P, P, P, SP, P]
         L.adana_oracle_f32_to_bf16.argtypes = [i64, P, P]
@@ -105,7 +117,7 @@ def _pow0d(x: np.float32, e: float) -> np.float32:
     """``x ** e`` for a 0-d binary32 tensor and a Python-float exponent.
 
     ATen's pow(Tensor, Scalar) special-cases a few exponents (0 fills ones;
-    0.5 sqrt; -0.5 rsqrt; -1 reciprocal; 2, 3, -2 by multiplication) and
+    1 copies; 0.5 sqrt; -0.5 rsqrt; -1 reciprocal; 2, 3, -2 by multiplication) and
     otherwise evaluates std::pow(float, double) in binary64 for a 0-d tensor
     (probed bitwise against torch 2.10; reference call site
     src/optim/adana.py:119,123).
@@ -113,6 +125,8 @@ def _pow0d(x: np.float32, e: float) -> np.float32:
     x = f32(x)
     if e == 0.0:
         return f32(1.0)
+    if e == 1.0:
+        return x
     if e == 0.5:
         return f32(np.sqrt(x))
     if e == -0.5:
@@ -128,12 +142,14 @@ def _pow0d(x: np.float32, e: float) -> np.float32:
     return f32(math.pow(float(x), e))
 
 
-POW_GENERAL, POW_ONE, POW_SQRT, POW_RSQRT, POW_RECIP, POW_SQUARE, POW_CUBE, POW_INVSQ = range(8)
+POW_GENERAL, POW_ONE, POW_SQRT, POW_RSQRT, POW_RECIP, POW_SQUARE, POW_CUBE, POW_INVSQ, POW_IDENTITY = range(9)
 
 
 def pow_mode(e: float) -> int:
-    """Which ATen pow specialisation an exponent selects (see _pow0d)."""
-    return {0.0: POW_ONE, 0.5: POW_SQRT, -0.5: POW_RSQRT, -1.0: POW_RECIP,
+    """Which ATen pow specialisation an exponent selects (see _pow0d): torch's
+    pow(Tensor, Scalar) returns ones for exponent 0 and a copy for exponent 1
+    before its kernel's sqrt / rsqrt / reciprocal / square / cube cases."""
+    return {0.0: POW_ONE, 1.0: POW_IDENTITY, 0.5: POW_SQRT, -0.5: POW_RSQRT, -1.0: POW_RECIP,
             2.0: POW_SQUARE, 3.0: POW_CUBE, -2.0: POW_INVSQ}.get(e, POW_GENERAL)
 
 
@@ -353,6 +369,111 @@ class OracleOptimizer:
                 else:
                     sums = element_step(self.star, p, g, st["m"], st["v"], st.get("tau"), sc)
                 st.update(finalize_diag(sums, p.size))
+
+
+# --------------------------------------------------------------------------
+# Manau's eager Dana-Star-MK4 branch (src/optim/manau.py:504-613)
+# --------------------------------------------------------------------------
+
+def manau_scalars(*, lr: float, step: float, alpha: float, kappa: float, mk4A: float, mk4B: float,
+                  clipsnr: float, epsilon: float, weight_decay: float, wd_decaying: bool,
+                  wd_ts: float) -> OracleManauScalars:
+    """The branch's Python floats (manau.py:539-555, :606-610) rounded to
+    binary32 where they meet float32 tensors."""
+    sc = OracleManauScalars()
+    sc.a = f32(alpha)                                     # add_(g, alpha=alpha)
+    sc.oma = f32(1 - alpha)                               # mul_(1 - alpha)
+    sc.s = f32(step)                                      # tau * step (:289)
+    sc.eps = f32(epsilon)
+    sc.min_p = f32(1.0 / (1.0 + step))                    # full_like(tau, 1.0 / (1.0 + step)) (:281)
+    sc.clip = f32(clipsnr)                                # clamp(max=clipsnr) (:589)
+    sc.lr = f32(lr)                                       # lr * tensor (:591, :600)
+    if wd_decaying:                                       # :607-610 (binary64, then mul_)
+        sc.wdf = f32(1 - weight_decay / (1 + step / wd_ts) * lr)
+    else:
+        sc.wdf = f32(1 - weight_decay * lr)
+    sc.has_wd = 1 if weight_decay != 0 else 0
+    for k, e in enumerate((1 - kappa, 2 * mk4B + 1, 2 * (-mk4A - mk4B))):
+        sc.e[k] = f32(e)
+        sc.mode[k] = pow_mode(e)
+    return sc
+
+
+def manau_element_step(p: np.ndarray, g: np.ndarray, m: np.ndarray, v: np.ndarray, tau: np.ndarray,
+                       sc: OracleManauScalars) -> np.ndarray:
+    """One Manau Dana-branch update in place; binary64 sums [sum(alpha_factor),
+    sum(g^2), sum(mfac), sum(m^2)]."""
+    diag = np.zeros(4, dtype=np.float64)
+    lib().adana_oracle_manau_step(p.size, _ptr(p), _ptr(g), _ptr(m), _ptr(v), _ptr(tau), ctypes.byref(sc),
+                                  _ptr(diag))
+    return diag
+
+
+@dataclass
+class OracleManauGroup:
+    params: List[np.ndarray]
+    use_muon: List[bool]
+    lr: float
+    weight_decay: float = 0.1
+    delta: float = 8.0
+    kappa: float = 1.0
+    mk4A: float = 0.0
+    mk4B: float = 0.0
+    clipsnr: float = 1.0
+    epsilon: float = 1e-8
+    weight_time: bool = False
+    wd_decaying: bool = False
+    wd_ts: float = 1.0
+    dana_momentum: bool = False
+    weighted_step_count: float = 0.0
+
+
+@dataclass
+class OracleManau:
+    """Manau.step's Dana-Star-MK4 branch over numpy arrays (manau.py:504-613),
+    with the weighted step count the Muon loop advances before it (:348-353
+    when dana_momentum).  ``peak_lr`` is the constructor's lr (self.lr)."""
+
+    groups: List[OracleManauGroup]
+    peak_lr: float
+    state: Dict[int, dict] = field(default_factory=dict)
+
+    def step(self, grads: Sequence[Sequence[np.ndarray]]) -> None:
+        for group in self.groups:                         # Muon loop (:329-353): counter only
+            if group.dana_momentum:
+                for use in group.use_muon:
+                    if use:
+                        group.weighted_step_count += group.lr / self.peak_lr if group.weight_time else 1.0
+        for gi, group in enumerate(self.groups):          # :507-613
+            for pi, p in enumerate(group.params):
+                if group.use_muon[pi]:
+                    continue
+                g = grads[gi][pi]
+                st = self.state.get(id(p))
+                if st is None:                            # :533-537
+                    st = self.state[id(p)] = {"dana_m": np.zeros(p.shape, np.float32),
+                                              "dana_v": np.zeros(p.shape, np.float32),
+                                              "dana_tau": np.zeros(p.shape, np.float32), "step": 0}
+                st["step"] += 1                           # :542
+                time_factor = group.lr / self.peak_lr if group.weight_time else 1.0
+                group.weighted_step_count += time_factor  # :546
+                if group.weight_time:                     # :548-554
+                    step = group.weighted_step_count
+                    alpha = group.delta / (group.delta + step) * time_factor
+                else:
+                    step = st["step"]
+                    alpha = group.delta / (group.delta + step)
+                sc = manau_scalars(lr=group.lr, step=step, alpha=alpha, kappa=group.kappa, mk4A=group.mk4A,
+                                   mk4B=group.mk4B, clipsnr=group.clipsnr, epsilon=group.epsilon,
+                                   weight_decay=group.weight_decay, wd_decaying=group.wd_decaying,
+                                   wd_ts=group.wd_ts)
+                sums = manau_element_step(p, g, st["dana_m"], st["dana_v"], st["dana_tau"], sc)
+                n = p.size
+                st["current_alpha"] = alpha                # :578
+                st["current_alpha_factor"] = sums[0] / n if n else float("nan")
+                st["gradient_norm"] = math.sqrt(sums[1])
+                st["auto_factor_mean"] = sums[2] / n if n else float("nan")
+                st["m_norm"] = math.sqrt(sums[3])
 
 
 # --------------------------------------------------------------------------
