@@ -162,3 +162,52 @@ def test_manau_state_dict_schema_and_round_trip():
         for key in ("dana_m", "dana_v", "dana_tau", "muon_buffer"):
             if key in a.state[x]:
                 assert torch.equal(a.state[x][key].view(torch.int32), b.state[y][key].view(torch.int32)), key
+
+
+def test_manau_weight_time_many_classes(oracle_mod):
+    """weight_time gives every Dana parameter its own step and alpha (the
+    group's counter advances once per parameter): 12 parameters make 12
+    scalar classes, more than one launch carries, so the branch runs as two
+    launch sets.  Against the oracle as above."""
+    import contextlib
+
+    import adana_amd
+
+    O = oracle_mod
+    print("case: Manau weight_time, 12 classes", flush=True)
+    rng = np.random.default_rng(21)
+    shapes = [(57,), (300,), (4,), (1000,), (33,), (64, 9), (5,), (17, 3), (2048,), (1,), (99,), (7, 7)]
+    names = [f"block.{i}.norm.weight" if len(s) == 1 else f"wte.weight.{i}" for i, s in enumerate(shapes)]
+    p0 = [rng.normal(0, 0.02, s).astype(np.float32) for s in shapes]
+    params = [torch.nn.Parameter(torch.from_numpy(x.copy()).to(DEV)) for x in p0]
+    kw = dict(lr=1e-2, weight_decay=0.05, kappa=0.7, clipsnr=1.5, delta=8.0, weight_time=True, wd_decaying=True,
+              wd_ts=4.0)
+    with contextlib.redirect_stdout(io.StringIO()):
+        opt = adana_amd.Manau([{"params": params, "param_names": names}], **kw)
+    assert not any(opt.state[p]["use_muon"] for p in params)
+    host = [x.copy() for x in p0]
+    orc = O.OracleManau(groups=[O.OracleManauGroup(
+        params=host, use_muon=[False] * len(host), lr=kw["lr"], weight_decay=kw["weight_decay"], delta=8.0,
+        kappa=0.7, clipsnr=1.5, weight_time=True, wd_decaying=True, wd_ts=4.0)], peak_lr=kw["lr"])
+    for k in range(1, 7):
+        lr = kw["lr"] * (0.5 + 0.1 * k)
+        opt.param_groups[0]["lr"] = lr
+        orc.groups[0].lr = lr
+        gs = [rng.normal(0, 1e-3, s).astype(np.float32) for s in shapes]
+        for p, g in zip(params, gs):
+            p.grad = torch.from_numpy(g.copy()).to(DEV)
+        prev = [x.copy() for x in host]
+        opt.step()
+        orc.step([gs])
+        torch.cuda.synchronize()
+        assert opt.param_groups[0]["weighted_step_count"] == orc.groups[0].weighted_step_count
+        assert len(opt._sets) == 2
+        for i, p in enumerate(params):
+            st, ost = opt.state[p], orc.state[id(host[i])]
+            tag = f"t={k} tensor {i}"
+            for key in ("dana_m", "dana_v", "dana_tau"):
+                assert ulp_diff(st[key].cpu().numpy(), ost[key]).max() == 0, f"{tag} {key}"
+            gp = p.detach().cpu().numpy()
+            _check_star_p(gp, host[i], prev[i], tag)
+            host[i][...] = gp
+            assert st["current_alpha"] == ost["current_alpha"], tag
