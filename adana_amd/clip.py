@@ -34,7 +34,7 @@ from typing import Iterable, List, Optional, Union
 import numpy as np
 import torch
 
-from . import _lib
+from . import _hoststep, _lib
 
 __all__ = ["clip_grad_norm_", "GradPlan"]
 
@@ -119,7 +119,7 @@ class GradPlan:
             _lib.check(_lib.lib().adana_grad_scale(
                 ctypes.byref(self.plan), self.flags, ctypes.c_void_p(clip.data_ptr() + 4),
                 ctypes.c_void_p(stream)), "adana_grad_scale")
-        torch._C._increment_version(self.grads)
+        _hoststep.bump_versions(self.grads)                # g was scaled in place
 
 
 _PLANS: "OrderedDict[tuple, GradPlan]" = OrderedDict()

@@ -1,0 +1,156 @@
+/* hoststep.cpp -- the optimizer step's per-tensor host bookkeeping in C++.
+ *
+ * The reference's step() walks every parameter in Python: skip grad None,
+ * ``state['step'] += 1`` (src/optim/adana.py:184-197;
+ * src/optim/dana_star_mk4.py:243-262), and the in-place update bumps each
+ * parameter's autograd version counter.  In the steady state of a run whose
+ * gradient tensors persist between steps (the same ``p.grad`` tensors, updated
+ * in place), the optimizer's cached launch plan, scalar classes and device
+ * tables all carry over, and what is left per tensor is that walk.  With
+ * thousands of small tensors it dominates the step.
+ *
+ * This module does the walk on torch's C++ tensors: a parameter's gradient is
+ * read from its TensorImpl (no Python attribute lookup, no wrapper object) and
+ * version counters are bumped directly.  Objects that are not exactly a
+ * torch.Tensor or torch.nn.Parameter (subclasses may override attribute access)
+ * take the generic Python path.
+ */
+#include <torch/csrc/autograd/python_variable.h>
+#include <torch/csrc/autograd/variable.h>
+
+#include <Python.h>
+
+#include <exception>
+
+namespace {
+
+PyObject *g_grad_name = nullptr;
+PyObject *g_step_name = nullptr;
+PyObject *g_one = nullptr;
+
+// True when params[i].grad is the gradient cached[i] (None: no gradient).
+// Exact tensors compare TensorImpls, which is the identity of the Python
+// objects: a live TensorImpl has at most one Python object, and the caller's
+// list keeps the cached ones alive.
+int same_grad(PyObject *p, PyObject *cached) {
+    if (THPVariable_CheckExact(p)) {
+        const at::Tensor &g = THPVariable_Unpack(p).unsafeGetTensorImpl()->grad();
+        if (cached == Py_None) return !g.defined();
+        if (!g.defined() || !THPVariable_Check(cached)) return 0;
+        return g.unsafeGetTensorImpl() == THPVariable_Unpack(cached).unsafeGetTensorImpl();
+    }
+    PyObject *g = PyObject_GetAttr(p, g_grad_name);
+    if (!g) return -1;
+    const int same = g == cached;
+    Py_DECREF(g);
+    return same;
+}
+
+/* advance_if_same(params, grads, states) -> bool
+ *
+ * True when params[i].grad is grads[i] for every i (None included); then every
+ * dict in ``states`` has its "step" entry incremented by one.  False (and
+ * nothing modified) as soon as one gradient differs. */
+PyObject *advance_if_same(PyObject *, PyObject *args) {
+    PyObject *params, *grads, *states;
+    if (!PyArg_ParseTuple(args, "O!O!O!", &PyList_Type, &params, &PyList_Type, &grads, &PyList_Type, &states))
+        return nullptr;
+    const Py_ssize_t n = PyList_GET_SIZE(params);
+    if (PyList_GET_SIZE(grads) != n) Py_RETURN_FALSE;
+    try {
+        for (Py_ssize_t i = 0; i < n; ++i) {
+            const int same = same_grad(PyList_GET_ITEM(params, i), PyList_GET_ITEM(grads, i));
+            if (same < 0) return nullptr;
+            if (!same) Py_RETURN_FALSE;
+        }
+    } catch (const std::exception &e) {
+        PyErr_SetString(PyExc_RuntimeError, e.what());
+        return nullptr;
+    }
+    // Tensors stepped together hold equal counts: the new int of the previous
+    // entry is reused (ints are immutable) when this entry's old int is equal.
+    const Py_ssize_t m = PyList_GET_SIZE(states);
+    PyObject *prev_v = nullptr, *prev_w = nullptr;
+    int rc = 0;
+    for (Py_ssize_t i = 0; i < m && !rc; ++i) {
+        PyObject *st = PyList_GET_ITEM(states, i);
+        if (!PyDict_Check(st)) {
+            PyErr_SetString(PyExc_TypeError, "advance_if_same: state entries must be dicts");
+            rc = -1;
+            break;
+        }
+        PyObject *v = PyDict_GetItemWithError(st, g_step_name); /* borrowed */
+        if (!v) {
+            if (!PyErr_Occurred()) PyErr_SetString(PyExc_KeyError, "step");
+            rc = -1;
+            break;
+        }
+        const bool reuse = prev_v && (v == prev_v || (PyLong_CheckExact(v) && PyLong_CheckExact(prev_v) &&
+                                                      PyObject_RichCompareBool(v, prev_v, Py_EQ) == 1));
+        if (!reuse) {
+            PyObject *w = PyNumber_Add(v, g_one);
+            if (!w) {
+                rc = -1;
+                break;
+            }
+            Py_XDECREF(prev_v);
+            Py_XDECREF(prev_w);
+            Py_INCREF(v);
+            prev_v = v;
+            prev_w = w;
+        }
+        rc = PyDict_SetItem(st, g_step_name, prev_w);
+    }
+    Py_XDECREF(prev_v);
+    Py_XDECREF(prev_w);
+    if (rc) return nullptr;
+    Py_RETURN_TRUE;
+}
+
+/* bump_versions(tensors) -> None
+ *
+ * The autograd version counter of every tensor in the list goes up by one,
+ * as torch._C._increment_version(tensors) does (the in-place update of
+ * each parameter). */
+PyObject *bump_versions(PyObject *, PyObject *args) {
+    PyObject *tensors;
+    if (!PyArg_ParseTuple(args, "O!", &PyList_Type, &tensors)) return nullptr;
+    const Py_ssize_t n = PyList_GET_SIZE(tensors);
+    for (Py_ssize_t i = 0; i < n; ++i)
+        if (!THPVariable_Check(PyList_GET_ITEM(tensors, i))) {
+            PyErr_Format(PyExc_TypeError, "bump_versions: entry %zd is not a tensor", i);
+            return nullptr;
+        }
+    try {
+        for (Py_ssize_t i = 0; i < n; ++i)
+            torch::autograd::impl::bump_version(THPVariable_Unpack(PyList_GET_ITEM(tensors, i)));
+    } catch (const std::exception &e) {
+        PyErr_SetString(PyExc_RuntimeError, e.what());
+        return nullptr;
+    }
+    Py_RETURN_NONE;
+}
+
+PyMethodDef methods[] = {
+    {"advance_if_same", advance_if_same, METH_VARARGS,
+     "advance_if_same(params, grads, states) -> bool: if params[i].grad is grads[i] for all i, "
+     "increment every states[j]['step'] and return True; otherwise change nothing and return False."},
+    {"bump_versions", bump_versions, METH_VARARGS,
+     "bump_versions(tensors) -> None: increment each tensor's autograd version counter."},
+    {nullptr, nullptr, 0, nullptr},
+};
+
+PyModuleDef module = {PyModuleDef_HEAD_INIT, "_hoststep", nullptr, -1, methods, nullptr, nullptr, nullptr, nullptr};
+
+}  // namespace
+
+PyMODINIT_FUNC PyInit__hoststep(void) {
+    if (!THPVariableClass) {
+        PyErr_SetString(PyExc_ImportError, "adana_amd._hoststep: import torch first");
+        return nullptr;
+    }
+    if (!(g_grad_name = PyUnicode_InternFromString("grad"))) return nullptr;
+    if (!(g_step_name = PyUnicode_InternFromString("step"))) return nullptr;
+    if (!(g_one = PyLong_FromLong(1))) return nullptr;
+    return PyModule_Create(&module);
+}

@@ -566,9 +566,9 @@ class _DanaFamily(Optimizer):
                         ctypes.c_void_p(ls.workspace.data_ptr()), ls.workspace.numel(),
                         ctypes.c_void_p(ls.diag.data_ptr()), ctypes.c_void_p(stream)),
                         "adana_mta_step_scaled")
-        torch._C._increment_version(params)
+        _hoststep.bump_versions(params)                    # p was updated in place
         if wflag:
-            torch._C._increment_version(grads)
+            _hoststep.bump_versions(grads)
         return loss
 
     def _refresh_grads(self, ls: _LaunchSet) -> None:

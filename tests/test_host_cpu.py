@@ -267,6 +267,55 @@ def test_hoststep_advance_if_same():
         _hoststep.advance_if_same([], [], [{"m": 1}])
 
 
+def test_hoststep_on_torch_tensors():
+    """The same walk on real parameters (read through torch's C++ tensors):
+    identity of the gradient tensor, not equality of its values or address;
+    tensor subclasses take the generic attribute path.  Step counts stay
+    exact and keep their type; bump_versions moves each autograd version
+    counter by one, as torch._C._increment_version does."""
+    from adana_amd import _hoststep
+
+    class Sub(torch.Tensor):
+        pass
+
+    ps = [torch.nn.Parameter(torch.zeros(3)), torch.zeros(4, requires_grad=True), torch.nn.Parameter(torch.zeros(2)),
+          torch.zeros(5).as_subclass(Sub).requires_grad_()]
+    for p in ps[:2] + ps[3:]:
+        p.grad = torch.ones_like(p)
+    gs = [p.grad for p in ps]
+    assert gs[2] is None and type(gs[3]) is Sub
+    states = [{"step": 10 ** 30}, {"step": int("1000")}, {"step": int("1000")}, {"step": 2.5}]
+    assert _hoststep.advance_if_same(ps, gs, states) is True
+    assert [s["step"] for s in states] == [10 ** 30 + 1, 1001, 1001, 3.5]
+    assert type(states[3]["step"]) is float and states[1]["step"] is states[2]["step"]
+    ps[0].grad = ps[0].grad.detach()                           # same storage, new tensor
+    assert _hoststep.advance_if_same(ps, gs, states) is False
+    assert [s["step"] for s in states] == [10 ** 30 + 1, 1001, 1001, 3.5]
+    ps[0].grad = gs[0]
+    gs[1].add_(1.0)                                            # in place: still the same tensor
+    assert _hoststep.advance_if_same(ps, gs, states) is True
+    ps[2].grad = torch.zeros(2)                                # None -> tensor
+    assert _hoststep.advance_if_same(ps, gs, states) is False
+    ps[2].grad = None
+    ps[3].grad = torch.ones(5).as_subclass(Sub)               # subclass: generic path sees it
+    assert _hoststep.advance_if_same(ps, gs, states) is False
+    ps[3].grad = gs[3]
+    assert _hoststep.advance_if_same(ps, gs, states) is True
+    with pytest.raises(TypeError):
+        _hoststep.advance_if_same(ps[:1], gs[:1], [[1]])
+
+    before = [p._version for p in ps]
+    _hoststep.bump_versions(ps)
+    assert [p._version for p in ps] == [v + 1 for v in before]
+    with pytest.raises(TypeError):
+        _hoststep.bump_versions([ps[0], 3])
+    assert [p._version for p in ps] == [v + 1 for v in before]   # checked before any bump
+    with torch.inference_mode():
+        t = torch.zeros(2)
+    with pytest.raises(RuntimeError, match="inference"):
+        _hoststep.bump_versions([t])
+
+
 def test_stream_probe_library_rejects_bad_arguments():
     """bench.py's stream-rate probe (adana_amd/libadana_probe.so) loads and
     refuses malformed launches before touching a device."""
