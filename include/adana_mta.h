@@ -66,7 +66,9 @@ extern "C" {
 
 /* Elements per work chunk (one 256-thread workgroup, one 16-byte vector per
  * thread per array).  Tensors start at multiples of ADANA_ALIGN_ELEMS in the
- * virtual index space, so every vector belongs to exactly one tensor. */
+ * virtual index space, so every vector belongs to exactly one tensor, and a
+ * tensor that would cross a chunk boundary from inside a chunk starts at the
+ * next boundary (adana_plan_layout). */
 #define ADANA_CHUNK_ELEMS 1024
 #define ADANA_ALIGN_ELEMS 4
 /* Scalar classes (distinct (group, step) pairs) one launch can carry. */
@@ -219,8 +221,10 @@ int adana_manau_scalars_init(adana_manau_scalars *out, const adana_manau_hparams
                              double lr, double step, double alpha);
 
 /* Host only.  Lays n tensors end to end: writes vstart[0..n] (virtual start
- * of each tensor, multiples of ADANA_ALIGN_ELEMS; vstart[n] is the padded
- * total) and fold_first[0..n] (first fold workgroup of each tensor's
+ * of each tensor: the end of the previous one rounded up to a multiple of
+ * ADANA_ALIGN_ELEMS, or further up to the next multiple of ADANA_CHUNK_ELEMS
+ * when the tensor would otherwise cross that chunk boundary; vstart[n] is the
+ * padded total) and fold_first[0..n] (first fold workgroup of each tensor's
  * diagnostics combine: ceil(chunks / ADANA_FOLD_CHUNKS) for a tensor of more
  * than ADANA_DIRECT_CHUNKS chunks, none otherwise; fold_first[n] = *n_folds),
  * and returns the number of

@@ -106,10 +106,19 @@ def test_plan_layout_properties():
                              [5_000_000, 0, 7, 512 * 1024, 512 * 1024 + 1]])
     vstart, fold_first, chunks, n_folds = _lib.plan_layout(numels)
     C = _lib.CHUNK_ELEMS
+    A = _lib.ALIGN_ELEMS
     assert vstart[0] == 0
-    assert np.all(vstart % _lib.ALIGN_ELEMS == 0)
-    pad = vstart[1:] - vstart[:-1]
-    assert np.all(pad >= numels) and np.all(pad - numels < _lib.ALIGN_ELEMS)
+    assert np.all(vstart % A == 0)
+    # each tensor starts at the previous end rounded up to A, moved to the next
+    # chunk boundary only when it would otherwise cross that boundary
+    end = 0
+    for vs, n in zip(vstart[:-1].tolist(), numels.tolist()):
+        r = end % C
+        want = end + (C - r) if (r and r + n > C) else end
+        assert vs == want
+        assert vs % C == 0 or vs % C + n <= C                 # no chunk boundary crossed from inside
+        end = vs + -(-n // A) * A
+    assert vstart[-1] == end
     assert chunks == math.ceil(vstart[-1] / C)
     # (chunk, tensor) segment slots chunk + tensor are distinct
     slots = set()
