@@ -171,6 +171,54 @@ __global__ __launch_bounds__(kThreads) void select_hist_kernel(PassArgs a) {
         if (h[i]) atomicAdd(&g[i], h[i]);
 }
 
+// One wavefront per wanted rank: the first digit of the rank's slot
+// histogram whose cumulative count exceeds the rank's residual rank becomes
+// the rank's next prefix digit, and the residual drops by the counts below
+// it.  A rank that no digit covers sets *err (the histograms disagree with
+// the tensor sizes).
+constexpr int kWalkWaves = kThreads / 64;
+
+__global__ __launch_bounds__(kThreads) void select_walk_kernel(const uint32_t *__restrict__ hist,
+                                                                const int32_t *__restrict__ rank_slot,
+                                                                int64_t *__restrict__ residual,
+                                                                uint32_t *__restrict__ rank_prefix, int64_t total,
+                                                                int width, int32_t *__restrict__ err) {
+    const int lane = threadIdx.x & 63;
+    const int64_t j = static_cast<int64_t>(blockIdx.x) * kWalkWaves + (threadIdx.x >> 6);
+    if (j >= total) return;                                         // uniform across the wave
+    const int bins = 1 << width;
+    const int per = bins > 64 ? bins / 64 : 1;                      // bins held by one lane (<= 4)
+    const uint32_t *h = hist + (static_cast<int64_t>(rank_slot[j]) << width);
+    uint64_t c[4] = {0, 0, 0, 0};
+    uint64_t mine = 0;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const int b = lane * per + k;
+        if (k < per && b < bins) c[k] = h[b];
+        mine += c[k];
+    }
+    uint64_t incl = mine;                                           // inclusive scan over the lanes
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const uint64_t u = __shfl_up(incl, o, 64);
+        if (lane >= o) incl += u;
+    }
+    const uint64_t rr = static_cast<uint64_t>(residual[j]);
+    const unsigned long long over = __ballot(incl > rr);
+    if (over == 0) {
+        if (lane == 0) *err = 1;
+        return;
+    }
+    const int first = __ffsll(over) - 1;
+    if (lane == first) {
+        uint64_t below = incl - mine;
+        int d = 0;
+        while (d < per - 1 && below + c[d] <= rr) below += c[d++];
+        residual[j] = static_cast<int64_t>(rr - below);
+        rank_prefix[j] = (rank_prefix[j] << width) | static_cast<uint32_t>(lane * per + d);
+    }
+}
+
 inline uint32_t key_to_bits(uint32_t key) {
     return (key & 0x80000000u) ? (key & 0x7fffffffu) : ~key;
 }
@@ -181,7 +229,7 @@ int check(hipError_t e, const char *what) {
 }
 
 struct Layout {                 // device workspace carving
-    size_t ptrs, numel, tile_first, slot_first, prefix, hist, total;
+    size_t ptrs, numel, tile_first, slot_first, prefix, hist, rank_slot, residual, rank_prefix, err, total;
 };
 
 Layout layout(int32_t n, int64_t total_ranks) {
@@ -194,6 +242,11 @@ Layout layout(int32_t n, int64_t total_ranks) {
     L.slot_first = off; off += up(4 * static_cast<size_t>(n + 1));
     L.prefix = off; off += up(4 * static_cast<size_t>(total_ranks > 0 ? total_ranks : 1));
     L.hist = off; off += up(4 * 256 * static_cast<size_t>(total_ranks > 0 ? total_ranks : 1));
+    const size_t nr = static_cast<size_t>(total_ranks > 0 ? total_ranks : 1);
+    L.rank_slot = off; off += up(4 * nr);
+    L.residual = off; off += up(8 * nr);
+    L.rank_prefix = off; off += up(4 * nr);
+    L.err = off; off += up(4);
     L.total = off;
     return L;
 }
@@ -219,6 +272,9 @@ int adana_order_stats(const float *const *h_tensor, const int64_t *h_numel, int3
     for (int32_t i = 0; i < n; ++i) {
         if (h_numel[i] < 0 || h_rank_first[i] > h_rank_first[i + 1] || h_rank_first[i] < 0)
             return adana_set_error(ADANA_E_INVALID, "adana_order_stats: bad sizes at tensor %d", i);
+        if (h_numel[i] > 0xffffffffLL)          // histogram bins are 32-bit counters
+            return adana_set_error(ADANA_E_UNSUPPORTED, "adana_order_stats: tensor %d has %lld elements (at most 2^32 - 1)",
+                                   i, static_cast<long long>(h_numel[i]));
         if (h_rank_first[i + 1] > h_rank_first[i] && !h_tensor[i])
             return adana_set_error(ADANA_E_INVALID, "adana_order_stats: null tensor %d", i);
         for (int64_t j = h_rank_first[i]; j < h_rank_first[i + 1]; ++j)
@@ -233,9 +289,9 @@ int adana_order_stats(const float *const *h_tensor, const int64_t *h_numel, int3
     hipStream_t st = static_cast<hipStream_t>(stream);
     char *ws = static_cast<char *>(d_workspace);
 
-    // per-rank search state: the rank's slot prefix and residual rank in it
+    // per-rank search state: the rank's prefix (host copy, read back after
+    // each pass) and, on the device, its residual rank within that prefix
     std::vector<uint32_t> rank_prefix(static_cast<size_t>(total), 0u);
-    std::vector<int64_t> residual(h_ranks, h_ranks + total);
     std::vector<int64_t> tile_first(static_cast<size_t>(n) + 1, 0);
     for (int32_t i = 0; i < n; ++i) {
         const bool wanted = h_rank_first[i + 1] > h_rank_first[i];
@@ -244,31 +300,37 @@ int adana_order_stats(const float *const *h_tensor, const int64_t *h_numel, int3
     }
     const int64_t n_tiles = tile_first[n];
     if (n_tiles > 0x7fffffffLL) return adana_set_error(ADANA_E_UNSUPPORTED, "adana_order_stats: too many elements");
+    int32_t *d_err = reinterpret_cast<int32_t *>(ws + L.err);
     int rc;
     if ((rc = check(hipMemcpyAsync(ws + L.ptrs, h_tensor, sizeof(void *) * n, hipMemcpyHostToDevice, st), "copy")) ||
         (rc = check(hipMemcpyAsync(ws + L.numel, h_numel, 8 * static_cast<size_t>(n), hipMemcpyHostToDevice, st), "copy")) ||
         (rc = check(hipMemcpyAsync(ws + L.tile_first, tile_first.data(), 8 * static_cast<size_t>(n + 1),
-                                   hipMemcpyHostToDevice, st), "copy")))
+                                   hipMemcpyHostToDevice, st), "copy")) ||
+        (rc = check(hipMemcpyAsync(ws + L.residual, h_ranks, 8 * static_cast<size_t>(total), hipMemcpyHostToDevice,
+                                   st), "copy")) ||
+        (rc = check(hipMemsetAsync(ws + L.rank_prefix, 0, 4 * static_cast<size_t>(total), st), "clear")) ||
+        (rc = check(hipMemsetAsync(d_err, 0, 4, st), "clear")))
         return rc;
 
     std::vector<int32_t> slot_first(static_cast<size_t>(n) + 1);
     std::vector<uint32_t> prefix;
     std::vector<int32_t> rank_slot(static_cast<size_t>(total));
-    std::vector<uint32_t> hist;
-    std::vector<int64_t> cum;
+    std::vector<uint32_t> p;
     int known = 0;
     while (known < 32) {
-        // slots: each tensor's distinct prefixes among its wanted ranks, sorted
+        // slots: each tensor's distinct prefixes among its wanted ranks, sorted;
+        // rank_slot: each rank's slot (absolute index)
         prefix.clear();
         int max_slots = 0;
         for (int32_t i = 0; i < n; ++i) {
             slot_first[i] = static_cast<int32_t>(prefix.size());
             const int64_t a = h_rank_first[i], b = h_rank_first[i + 1];
-            std::vector<uint32_t> p(rank_prefix.begin() + a, rank_prefix.begin() + b);
+            p.assign(rank_prefix.begin() + a, rank_prefix.begin() + b);
             std::sort(p.begin(), p.end());
             p.erase(std::unique(p.begin(), p.end()), p.end());
             for (int64_t j = a; j < b; ++j)
-                rank_slot[j] = static_cast<int32_t>(std::lower_bound(p.begin(), p.end(), rank_prefix[j]) - p.begin());
+                rank_slot[j] = slot_first[i] +
+                               static_cast<int32_t>(std::lower_bound(p.begin(), p.end(), rank_prefix[j]) - p.begin());
             prefix.insert(prefix.end(), p.begin(), p.end());
             max_slots = std::max(max_slots, static_cast<int>(p.size()));
         }
@@ -285,6 +347,8 @@ int adana_order_stats(const float *const *h_tensor, const int64_t *h_numel, int3
                                        hipMemcpyHostToDevice, st), "copy")) ||
             (rc = check(hipMemcpyAsync(ws + L.prefix, prefix.data(), 4 * prefix.size(), hipMemcpyHostToDevice, st),
                         "copy")) ||
+            (rc = check(hipMemcpyAsync(ws + L.rank_slot, rank_slot.data(), 4 * static_cast<size_t>(total),
+                                       hipMemcpyHostToDevice, st), "copy")) ||
             (rc = check(hipMemsetAsync(ws + L.hist, 0, 4 * hist_n, st), "clear")))
             return rc;
         PassArgs pa;
@@ -301,31 +365,19 @@ int adana_order_stats(const float *const *h_tensor, const int64_t *h_numel, int3
         hipLaunchKernelGGL(select_hist_kernel, dim3(static_cast<unsigned>(n_tiles)), dim3(kThreads),
                            static_cast<unsigned>(lds), st, pa);
         if ((rc = check(hipGetLastError(), "histogram launch"))) return rc;
-        hist.resize(hist_n);
-        if ((rc = check(hipMemcpyAsync(hist.data(), ws + L.hist, 4 * hist_n, hipMemcpyDeviceToHost, st), "copy")) ||
+        const int64_t walk_blocks = (total + kWalkWaves - 1) / kWalkWaves;
+        hipLaunchKernelGGL(select_walk_kernel, dim3(static_cast<unsigned>(walk_blocks)), dim3(kThreads), 0, st,
+                           pa.hist, reinterpret_cast<const int32_t *>(ws + L.rank_slot),
+                           reinterpret_cast<int64_t *>(ws + L.residual), reinterpret_cast<uint32_t *>(ws + L.rank_prefix),
+                           total, width, d_err);
+        if ((rc = check(hipGetLastError(), "walk launch"))) return rc;
+        int32_t err = 0;
+        if ((rc = check(hipMemcpyAsync(rank_prefix.data(), ws + L.rank_prefix, 4 * static_cast<size_t>(total),
+                                       hipMemcpyDeviceToHost, st), "copy")) ||
+            (rc = check(hipMemcpyAsync(&err, d_err, 4, hipMemcpyDeviceToHost, st), "copy")) ||
             (rc = check(hipStreamSynchronize(st), "synchronize")))
             return rc;
-        // each slot's cumulative counts, then each rank: the first digit whose
-        // cumulative count exceeds its residual rank (binary search)
-        cum.resize(hist_n);
-        for (size_t sl = 0; sl < prefix.size(); ++sl) {
-            int64_t c = 0;
-            for (int d = 0; d < bins; ++d) {
-                c += hist[sl * bins + d];
-                cum[sl * bins + d] = c;
-            }
-        }
-        for (int32_t i = 0; i < n; ++i) {
-            for (int64_t j = h_rank_first[i]; j < h_rank_first[i + 1]; ++j) {
-                const int64_t *cs = cum.data() + (static_cast<size_t>(slot_first[i]) + rank_slot[j]) * bins;
-                const int64_t rr = residual[j];
-                const int d = static_cast<int>(std::upper_bound(cs, cs + bins, rr) - cs);
-                if (d == bins)
-                    return adana_set_error(ADANA_E_HIP, "adana_order_stats: histogram of tensor %d does not cover rank", i);
-                residual[j] = rr - (d > 0 ? cs[d - 1] : 0);
-                rank_prefix[j] = (width == 32 ? 0u : (rank_prefix[j] << width)) | static_cast<uint32_t>(d);
-            }
-        }
+        if (err) return adana_set_error(ADANA_E_HIP, "adana_order_stats: a histogram does not cover its rank");
         known += width;
     }
     for (int64_t j = 0; j < total; ++j) {

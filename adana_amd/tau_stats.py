@@ -17,6 +17,7 @@ np.sort).
 from __future__ import annotations
 
 import ctypes
+import functools
 from typing import Dict, List, Sequence, Tuple
 
 import numpy as np
@@ -79,6 +80,21 @@ def order_values(tensors: Sequence[torch.Tensor], ranks: Sequence[np.ndarray]) -
     return [values[a:b].copy() for a, b in zip(rank_first[:-1], rank_first[1:])]
 
 
+@functools.lru_cache(maxsize=1024)
+def _rank_plan(n: int) -> Tuple[np.ndarray, np.ndarray, np.ndarray]:
+    """For n >= 1 elements: the distinct ranks to select (both ends'
+    positions, ascending) and where the smallest / largest order statistics
+    sit among them.  Depends on n only, so it is cached (a model's tensors
+    repeat a few shapes); the arrays are read-only."""
+    idx = order_stat_indices(n)
+    wanted = np.unique(np.concatenate([idx, (n - 1) - idx])).astype(np.int64)
+    pos_small = np.searchsorted(wanted, idx)
+    pos_large = np.searchsorted(wanted, (n - 1) - idx)
+    for a in (wanted, pos_small, pos_large):
+        a.flags.writeable = False
+    return wanted, pos_small, pos_large
+
+
 def _stats_for(tensors: Sequence[torch.Tensor]) -> List[Tuple[np.ndarray, np.ndarray]]:
     plans, ranks = [], []
     for t in tensors:
@@ -87,21 +103,17 @@ def _stats_for(tensors: Sequence[torch.Tensor]) -> List[Tuple[np.ndarray, np.nda
             plans.append(None)
             ranks.append(np.zeros(0, np.int64))
             continue
-        idx = order_stat_indices(n)
-        wanted = np.unique(np.concatenate([idx, (n - 1) - idx])).astype(np.int64)
-        plans.append((idx, wanted))
-        ranks.append(wanted)
+        plan = _rank_plan(n)
+        plans.append(plan)
+        ranks.append(plan[0])
     vals = order_values(tensors, ranks)
     out = []
-    for t, plan, v in zip(tensors, plans, vals):
+    for plan, v in zip(plans, vals):
         if plan is None:
             out.append((np.array([]), np.array([])))          # the reference's empty result
             continue
-        idx, wanted = plan
-        n = t.numel()
-        smallest = v[np.searchsorted(wanted, idx)]
-        largest = v[np.searchsorted(wanted, (n - 1) - idx)]
-        out.append((largest, smallest))
+        _, pos_small, pos_large = plan
+        out.append((v[pos_large], v[pos_small]))
     return out
 
 

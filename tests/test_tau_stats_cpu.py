@@ -75,3 +75,29 @@ def test_order_values_rejects_cpu_tensors():
     with pytest.raises(RuntimeError, match="ROCm"):
         order_values([torch.zeros(4)], [np.array([0])])
     assert order_values([], []) == []
+
+
+def test_order_stats_library_validates_before_device_work():
+    """adana_order_stats checks every size and rank before it touches the
+    device (fake device pointers here): ranks outside a tensor, negative
+    sizes, and tensors of 2^32 or more elements (its histogram bins are
+    32-bit counters) are refused."""
+    import ctypes
+
+    from adana_amd import _lib
+
+    L = _lib.lib()
+    fake = (ctypes.c_void_p * 1)(0x1000)
+    vals = (ctypes.c_float * 2)()
+
+    def call(numel, ranks):
+        nm = (ctypes.c_int64 * 1)(numel)
+        rk = (ctypes.c_int64 * len(ranks))(*ranks)
+        rf = (ctypes.c_int64 * 2)(0, len(ranks))
+        return L.adana_order_stats(fake, nm, 1, rk, rf, vals, None, 0, None)
+
+    assert call(10, [10]) == -1 and "outside tensor" in _lib.last_error()
+    assert call(-1, []) == -1 and "bad sizes" in _lib.last_error()
+    assert call(1 << 32, [0]) == -3 and "2^32" in _lib.last_error()          # ADANA_E_UNSUPPORTED
+    assert call(10, [3]) == -1 and "workspace" in _lib.last_error()
+    assert L.adana_order_stats_workspace(1, 2) > L.adana_order_stats_workspace(1, 1) > 0
