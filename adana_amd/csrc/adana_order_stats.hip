@@ -13,8 +13,9 @@
 //   * a pass resolves the next w key bits (w <= 8) of every wanted rank: one
 //     read of the tensors, a histogram per (tensor, active prefix) of the next
 //     digit, kept in LDS by each workgroup and flushed with global atomics;
-//   * the host walks each histogram to the wanted rank's digit and residual
-//     rank, and the next pass narrows to the new prefixes.  w is 8 while few
+//   * a walk kernel (one wavefront per rank) takes each rank's histogram to
+//     its next digit and residual rank on the device; the host reads back the
+//     new prefixes and the next pass narrows to them.  w is 8 while few
 //     prefixes are active and smaller when many are, so that the histograms
 //     always fit in LDS.
 // Exact (integer counting), deterministic results; no sort scratch.  Traffic:

@@ -303,8 +303,9 @@ size_t adana_order_stats_workspace(int32_t n_tensors, int64_t total_ranks);
  * np.sort orders it (NaN last; -0 and +0 equal as values), written to the
  * host array h_values at the same positions.  A multi-rank radix select: 4
  * to 8 passes that each read the tensors once and histogram the next key
- * digit per wanted prefix in LDS; between passes the host narrows every rank
- * to its next digit.  Synchronises ``stream``.  d_workspace: at least
+ * digit per wanted prefix in LDS; after each pass every rank is narrowed to
+ * its next digit on the device, and the host reads back the new prefixes to
+ * set up the next pass.  Synchronises ``stream``.  d_workspace: at least
  * adana_order_stats_workspace(n_tensors, h_rank_first[n_tensors]) bytes. */
 int adana_order_stats(const float *const *h_tensors, const int64_t *h_numel, int32_t n_tensors,
                       const int64_t *h_ranks, const int64_t *h_rank_first, float *h_values,
