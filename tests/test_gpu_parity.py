@@ -237,6 +237,28 @@ def test_gpt_list_two_groups(oracle_mod, star):
         pair.compare(where=f"k={k}")
 
 
+@pytest.mark.parametrize("kappa", [1.0, 0.0, 1.5, 2.0, -1.0, -2.0, 3.0, 0.3])
+def test_star_pow_modes(oracle_mod, kappa):
+    """Every kind of the per-element pow eff_time ** (1 - kappa)
+    (src/optim/dana_star_mk4.py:168-170) through the kernel: exponent 0
+    (kappa 1: no pow), 1 (kappa 0: identity), ATen's special exponents
+    -0.5, -1, 2, 3, -2, and a general one (0.5 and 0.15 run in the golden
+    cases).  No SNR clip, so the pow reaches p unclamped; 12 steps, so that
+    tau * t passes 1 and the pow sees arguments above 1."""
+    print("case: Dana-Star pow mode kappa", kappa, flush=True)
+    rng = np.random.default_rng(int(100 + 10 * kappa))
+    shapes = [(37, 19), (1024,), (5,), (4096 + 3,)]
+    params = [_normal(rng, s, 0.02) for s in shapes]
+    pair = Pair(oracle_mod, True, [(params, {})], lr=1e-3, delta=4.0, kappa=kappa, clipsnr=None,
+                weight_decay=0.1, wd_decaying=True, wd_ts=5.0)
+    for k in range(12):
+        gl = [[_normal(rng, x.shape, 1e-3) for x in params]]
+        pair.step(gl)
+        pair.compare(where=f"kappa={kappa} k={k}")
+    taus = np.concatenate([pair.opt.state[p]["tau"].cpu().numpy().ravel() for p in pair.gpu_params[0]])
+    assert (taus * 12 > 1).mean() > 0.3                      # the pow saw arguments above 1
+
+
 def test_many_tiny_tensors(oracle_mod):
     """C5-shaped list (fewer tensors): log-uniform sizes incl. non-multiples of
     4 and 1-element tensors, 5% all-zero grads, chunks spanning many tensors."""
