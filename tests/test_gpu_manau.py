@@ -211,3 +211,49 @@ def test_manau_weight_time_many_classes(oracle_mod):
             _check_star_p(gp, host[i], prev[i], tag)
             host[i][...] = gp
             assert st["current_alpha"] == ost["current_alpha"], tag
+
+
+@pytest.mark.parametrize("kappa,mk4", [(1.0, None), (2.0, None), (0.0, None), (0.3, None), (1.0, (0.2, 0.5))])
+def test_manau_pow_kinds(oracle_mod, kappa, mk4):
+    """Manau's branch instances the golden runs leave out: kappa 1 (no pow),
+    special exponents -1 and 1, a general one, and the mk4 powers with
+    kappa 1.  Against the oracle as above, 10 steps."""
+    import contextlib
+
+    import adana_amd
+
+    O = oracle_mod
+    print("case: Manau pow kind kappa", kappa, "mk4", mk4, flush=True)
+    rng = np.random.default_rng(int(31 + 7 * kappa))
+    shapes = [(97, 24), (24,), (1000,), (5,), (4096 + 3,)]
+    names = ["transformer.wte.weight"] + [f"h.{i}.ln.weight" for i in range(len(shapes) - 1)]
+    p0 = [rng.normal(0, 0.02, s).astype(np.float32) for s in shapes]
+    params = [torch.nn.Parameter(torch.from_numpy(x.copy()).to(DEV)) for x in p0]
+    mk4A, mk4B = mk4 if mk4 else (0.0, 0.0)
+    kw = dict(lr=1e-2, weight_decay=0.1, kappa=kappa, clipsnr=2.0, delta=4.0, mk4A=mk4A, mk4B=mk4B,
+              wd_decaying=True, wd_ts=3.0)
+    with contextlib.redirect_stdout(io.StringIO()):
+        opt = adana_amd.Manau([{"params": params, "param_names": names}], **kw)
+    host = [x.copy() for x in p0]
+    orc = O.OracleManau(groups=[O.OracleManauGroup(
+        params=host, use_muon=[False] * len(host), lr=kw["lr"], weight_decay=kw["weight_decay"], delta=4.0,
+        kappa=kappa, mk4A=mk4A, mk4B=mk4B, clipsnr=2.0, wd_decaying=True, wd_ts=3.0)], peak_lr=kw["lr"])
+    for k in range(1, 11):
+        gs = [rng.normal(0, 1e-3, s).astype(np.float32) for s in shapes]
+        for p, g in zip(params, gs):
+            p.grad = torch.from_numpy(g.copy()).to(DEV)
+        prev = [x.copy() for x in host]
+        opt.step()
+        orc.step([gs])
+        torch.cuda.synchronize()
+        for i, p in enumerate(params):
+            st, ost = opt.state[p], orc.state[id(host[i])]
+            tag = f"kappa={kappa} mk4={mk4} t={k} tensor {i}"
+            for key in ("dana_m", "dana_v", "dana_tau"):
+                assert ulp_diff(st[key].cpu().numpy(), ost[key]).max() == 0, f"{tag} {key}"
+            gp = p.detach().cpu().numpy()
+            _check_star_p(gp, host[i], prev[i], tag)
+            host[i][...] = gp
+            got = [float(st[key]) for key in ("current_alpha_factor", "gradient_norm", "auto_factor_mean", "m_norm")]
+            ref = [ost[key] for key in ("current_alpha_factor", "gradient_norm", "auto_factor_mean", "m_norm")]
+            np.testing.assert_allclose(got, ref, rtol=1e-5, atol=1e-30, err_msg=tag)
