@@ -26,6 +26,7 @@ namespace {
 
 PyObject *g_grad_name = nullptr;
 PyObject *g_step_name = nullptr;
+PyObject *g_params_name = nullptr;
 PyObject *g_one = nullptr;
 
 // True when params[i].grad is the gradient cached[i] (None: no gradient).
@@ -131,12 +132,50 @@ PyObject *bump_versions(PyObject *, PyObject *args) {
     Py_RETURN_NONE;
 }
 
+/* same_params(param_groups, flat) -> bool
+ *
+ * True when the concatenation of every group's "params" is, object for
+ * object, the list ``flat`` (the optimizer's cached parameter list). */
+PyObject *same_params(PyObject *, PyObject *args) {
+    PyObject *groups, *flat;
+    if (!PyArg_ParseTuple(args, "OO!", &groups, &PyList_Type, &flat)) return nullptr;
+    PyObject *gs = PySequence_Fast(groups, "same_params: param_groups must be a sequence");
+    if (!gs) return nullptr;
+    const Py_ssize_t ng = PySequence_Fast_GET_SIZE(gs), nf = PyList_GET_SIZE(flat);
+    Py_ssize_t k = 0;
+    bool same = true;
+    for (Py_ssize_t g = 0; g < ng && same; ++g) {
+        PyObject *grp = PySequence_Fast_GET_ITEM(gs, g);
+        PyObject *ps = PyDict_Check(grp) ? PyDict_GetItemWithError(grp, g_params_name) : nullptr; /* borrowed */
+        if (!ps) {
+            if (!PyErr_Occurred()) PyErr_SetString(PyExc_KeyError, "params");
+            Py_DECREF(gs);
+            return nullptr;
+        }
+        PyObject *pf = PySequence_Fast(ps, "same_params: a group's params must be a sequence");
+        if (!pf) {
+            Py_DECREF(gs);
+            return nullptr;
+        }
+        const Py_ssize_t np_ = PySequence_Fast_GET_SIZE(pf);
+        if (k + np_ > nf) same = false;
+        for (Py_ssize_t i = 0; i < np_ && same; ++i, ++k)
+            same = PySequence_Fast_GET_ITEM(pf, i) == PyList_GET_ITEM(flat, k);
+        Py_DECREF(pf);
+    }
+    Py_DECREF(gs);
+    if (same && k == nf) Py_RETURN_TRUE;
+    Py_RETURN_FALSE;
+}
+
 PyMethodDef methods[] = {
     {"advance_if_same", advance_if_same, METH_VARARGS,
      "advance_if_same(params, grads, states) -> bool: if params[i].grad is grads[i] for all i, "
      "increment every states[j]['step'] and return True; otherwise change nothing and return False."},
     {"bump_versions", bump_versions, METH_VARARGS,
      "bump_versions(tensors) -> None: increment each tensor's autograd version counter."},
+    {"same_params", same_params, METH_VARARGS,
+     "same_params(param_groups, flat) -> bool: the groups' params, concatenated, are the objects of flat."},
     {nullptr, nullptr, 0, nullptr},
 };
 
@@ -151,6 +190,7 @@ PyMODINIT_FUNC PyInit__hoststep(void) {
     }
     if (!(g_grad_name = PyUnicode_InternFromString("grad"))) return nullptr;
     if (!(g_step_name = PyUnicode_InternFromString("step"))) return nullptr;
+    if (!(g_params_name = PyUnicode_InternFromString("params"))) return nullptr;
     if (!(g_one = PyLong_FromLong(1))) return nullptr;
     return PyModule_Create(&module);
 }

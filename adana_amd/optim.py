@@ -428,9 +428,12 @@ class _DanaFamily(Optimizer):
         return hp
 
     def _flat_params(self):
-        """All parameters in group order, with their group index (cached)."""
+        """All parameters in group order, with their group index (cached; the
+        cache is checked object for object against the groups every call, so
+        added groups and parameters replaced in place are picked up)."""
         sig = tuple((id(g["params"]), len(g["params"])) for g in self.param_groups)
-        if self._flat is None or self._flat[0] != sig:
+        if (self._flat is None or self._flat[0] != sig
+                or not _hoststep.same_params(self.param_groups, self._flat[1])):
             params, gidx = [], []
             for gi, group in enumerate(self.param_groups):
                 params.extend(group["params"])

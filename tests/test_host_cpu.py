@@ -356,3 +356,30 @@ def test_stream_probe_library_rejects_bad_arguments():
     assert cp(0x1000, 0x2000, 1000, part, 0, None) == -1  # not a multiple of 1024
     assert cp(0, 0x2000, 1024, part, 0, None) == -1       # null
     assert cp(0x1000, 0x2000, 1024, None, 0, None) == -1  # no partials
+
+
+def test_flat_params_follow_the_groups():
+    """The cached parameter list is checked object for object against the
+    groups: a parameter replaced inside a group's list (same list, same
+    length) and an added group are both picked up, as the reference's step,
+    which re-reads group['params'] every time, would see them."""
+    import adana_amd
+    from adana_amd import _hoststep
+
+    a, b, c = (torch.nn.Parameter(torch.zeros(3)) for _ in range(3))
+    opt = adana_amd.ADana([a, b], lr=1e-3)
+    flat, gidx = opt._flat_params()
+    assert flat == [a, b] and gidx == [0, 0]
+    assert _hoststep.same_params(opt.param_groups, flat)
+    opt.param_groups[0]["params"][1] = c                     # in place
+    assert not _hoststep.same_params(opt.param_groups, flat)
+    flat, _ = opt._flat_params()
+    assert flat[1] is c
+    d = torch.nn.Parameter(torch.zeros(2))
+    opt.add_param_group({"params": [d], "weight_decay": 0.1})
+    flat, gidx = opt._flat_params()
+    assert flat == [a, c, d] and gidx == [0, 0, 1]
+    assert not _hoststep.same_params(opt.param_groups, [a, c])            # shorter cache
+    assert not _hoststep.same_params(opt.param_groups, [a, c, d, d])      # longer cache
+    with pytest.raises(KeyError):
+        _hoststep.same_params([{"lr": 1.0}], [])
