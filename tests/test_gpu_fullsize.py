@@ -130,3 +130,69 @@ def test_full_size_sampled_parity(oracle_mod, name):
             assert st["step"] == t
     del opt, params, groups
     torch.cuda.empty_cache()
+
+
+def _norm64(t: torch.Tensor, block: int = 1 << 28) -> float:
+    """Binary64 2-norm of a large tensor, block by block (no full-size copy)."""
+    f = t.detach().reshape(-1)
+    s = 0.0
+    for a in range(0, f.numel(), block):
+        s += float(torch.sum(f[a:a + block].double() ** 2))
+    return s ** 0.5
+
+
+def test_single_tensor_beyond_2_31_elements(oracle_mod):
+    """One Dana-Star-MK4 tensor of 2^31 + 1027 elements (per-tensor offsets,
+    chunk indices and fold ranges past 2^31; a ragged last chunk), 2 steps.
+    Sampled oracle replay as above, with the elements around index 2^31 and
+    the last ones always in the sample; gradient_norm and m_norm against
+    binary64 reductions of the whole tensor."""
+    import adana_amd
+
+    O = oracle_mod
+    n = (1 << 31) + 1027
+    print(f"case: one tensor of {n} elements, 2 steps", flush=True)
+    hp = dict(lr=1e-3, delta=8.0, kappa=0.85, epsilon=1e-8, weight_decay=0.4, clipsnr=2.0, wd_decaying=True,
+              wd_ts=10.0)
+    gen = torch.Generator(device=DEV)
+    gen.manual_seed(3)
+    p = torch.nn.Parameter(torch.empty(n, device=DEV).normal_(0, 0.02, generator=gen))
+    opt = adana_amd.DANA_STAR_MK4([p], **hp)
+    rng = np.random.default_rng(11)
+    edge = [0, 1, (1 << 31) - 4, (1 << 31) - 1, 1 << 31, (1 << 31) + 1, n - 1027, n - 3, n - 2, n - 1]
+    pick = np.unique(np.concatenate([edge, rng.integers(0, n, size=SAMPLES)]))
+    ix = torch.from_numpy(pick).to(DEV)
+
+    def gather(t):
+        return t.detach().reshape(-1).index_select(0, ix).float().cpu().numpy()
+
+    hp_, hg = gather(p), None
+    hm, hv, ht = (np.zeros_like(hp_) for _ in range(3))
+    for t in (1, 2):
+        gen.manual_seed(2000 + t)
+        p.grad = torch.empty(n, device=DEV).normal_(0, 1e-3, generator=gen)
+        hg = gather(p.grad)
+        gnorm = _norm64(p.grad)
+        before = hp_.copy()
+        opt.step()
+        torch.cuda.synchronize()
+        st = opt.state[p]
+        osc = O.step_scalars(lr=hp["lr"], peak_lr=hp["lr"], delta=hp["delta"], kappa=hp["kappa"],
+                             epsilon=hp["epsilon"], weight_decay=hp["weight_decay"], clipsnr=hp["clipsnr"],
+                             wd_decaying=True, wd_ts=hp["wd_ts"], gamma_3_factor=1.0, t=t)
+        O.element_step(True, hp_, hg, hm, hv, ht, osc)
+        for key, want in (("m", hm), ("v", hv), ("tau", ht)):
+            assert ulp_diff(gather(st[key]), want).max() == 0, (t, key)
+        got = gather(p)
+        d = ulp_diff(got, hp_)
+        bad = np.nonzero(d)[0]
+        assert bad.size <= STAR_HARD_CASES, (t, bad.size)
+        for j in bad:
+            scale = max(abs(float(before[j])), abs(float(hp_[j])))
+            assert abs(float(got[j]) - float(hp_[j])) <= STAR_P_ULPS * np.spacing(np.float32(scale)), t
+        hp_[...] = got
+        np.testing.assert_allclose(float(st["gradient_norm"]), gnorm, rtol=1e-5)
+        np.testing.assert_allclose(float(st["m_norm"]), _norm64(st["m"]), rtol=1e-5)
+        assert st["step"] == t
+    del opt, p
+    torch.cuda.empty_cache()

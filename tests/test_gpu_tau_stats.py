@@ -118,3 +118,37 @@ def test_large_tensor_timing(oracle_mod):
     t2 = time.perf_counter()
     assert _same(gl, wl) and _same(gs, ws)
     print(f"64M elements: GPU select {1e3 * (t1 - t0):.1f} ms, copy + np.sort {1e3 * (t2 - t1):.1f} ms", flush=True)
+
+
+def test_order_stats_beyond_2_31_elements():
+    """A tensor of 2^31 + 1027 values x[i] = i mod 2^24 (exact in float32):
+    value v occurs 129 times for v < 1027 and 128 times otherwise, so the
+    value at every rank, including ranks past 2^31, has a closed form.  The
+    reference's index set is int32 and cannot address this tensor (its
+    formula raises there, see test_tau_stats_cpu.py), so the ranks are the
+    same positions 1.1^k - 1 from both ends, computed in int64, through
+    order_values."""
+    from adana_amd.tau_stats import order_values
+
+    n, M, extra = (1 << 31) + 1027, 1 << 24, 1027
+    print(f"case: order statistics of {n} values", flush=True)
+    x = torch.empty(n, dtype=torch.float32, device=DEV)
+    block = 1 << 27
+    for a in range(0, n, block):
+        b = min(n, a + block)
+        x[a:b] = (torch.arange(a, b, dtype=torch.int64, device=DEV) % M).to(torch.float32)
+
+    def value_at(r):
+        r = np.asarray(r, dtype=np.int64)
+        head = extra * 129
+        return np.where(r < head, r // 129, extra + (r - head) // 128).astype(np.float32)
+
+    max_k = int(np.ceil(np.log(n) / np.log(1.1)))
+    idx = np.minimum(np.unique((1.1 ** np.arange(max_k + 1)).astype(np.int64) - 1), n - 1)
+    ranks = np.unique(np.concatenate([idx, (n - 1) - idx]))
+    assert ranks.max() > (1 << 31) and ranks.min() == 0
+    (vals,) = order_values([x], [ranks])
+    assert np.array_equal(vals, value_at(ranks))
+    assert vals[-1] == M - 1
+    del x
+    torch.cuda.empty_cache()

@@ -101,3 +101,20 @@ def test_order_stats_library_validates_before_device_work():
     assert call(1 << 32, [0]) == -3 and "2^32" in _lib.last_error()          # ADANA_E_UNSUPPORTED
     assert call(10, [3]) == -1 and "workspace" in _lib.last_error()
     assert L.adana_order_stats_workspace(1, 2) > L.adana_order_stats_workspace(1, 1) > 0
+
+
+def test_index_formula_fails_past_2_31_elements_as_the_reference():
+    """src/optim/tau_stats_collector.py:360-366 casts 1.1^k to int32 and
+    clamps with n - 1; for a tensor of more than 2^31 elements numpy 2
+    refuses that clamp.  The restatement keeps the reference's behaviour
+    (the GPU select itself handles such tensors: order_values with int64
+    ranks, tests/test_gpu_tau_stats.py)."""
+    import warnings
+
+    from adana_amd.tau_stats import order_stat_indices
+
+    with warnings.catch_warnings():
+        warnings.simplefilter("ignore", RuntimeWarning)   # the int32 cast's "invalid value"
+        with pytest.raises(OverflowError):
+            order_stat_indices((1 << 31) + 1027)
+        assert order_stat_indices((1 << 31) - 1)[-1] == (1 << 31) - 2   # still fine below
