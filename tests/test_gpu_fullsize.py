@@ -196,3 +196,33 @@ def test_single_tensor_beyond_2_31_elements(oracle_mod):
         assert st["step"] == t
     del opt, p
     torch.cuda.empty_cache()
+
+
+def test_clip_single_tensor_beyond_2_31_elements(oracle_mod):
+    """clip_grad_norm_ over one gradient of 2^31 + 1027 elements: the total
+    within 2e-6 of the binary64 norm of the whole tensor, and the sampled
+    clipped gradients (around index 2^31 and at the end included) equal to
+    torch's binary32 product with the coefficient of that total."""
+    import adana_amd
+
+    O = oracle_mod
+    n = (1 << 31) + 1027
+    print(f"case: clip_grad_norm_ over one gradient of {n} elements", flush=True)
+    gen = torch.Generator(device=DEV)
+    gen.manual_seed(5)
+    p = torch.nn.Parameter(torch.zeros(1, device=DEV).expand(n))     # no storage needed for p
+    p.grad = torch.empty(n, device=DEV).normal_(0, 1e-3, generator=gen)
+    rng = np.random.default_rng(13)
+    edge = [0, (1 << 31) - 1, 1 << 31, (1 << 31) + 1, n - 1]
+    ix = torch.from_numpy(np.unique(np.concatenate([edge, rng.integers(0, n, size=SAMPLES)]))).to(DEV)
+    g0 = p.grad.index_select(0, ix).cpu().numpy()
+    want = _norm64(p.grad)
+    total = adana_amd.clip_grad_norm_([p], 0.5)
+    torch.cuda.synchronize()
+    assert abs(float(total) - want) <= 2e-6 * want
+    coef = O.clip_coef(np.float32(float(total)), 0.5)
+    assert coef < 1.0                                              # the norm (~46) is above max_norm
+    got = p.grad.index_select(0, ix).cpu().numpy()
+    assert np.array_equal(got.view(np.uint32), O.clip_scale(g0, coef).view(np.uint32))
+    del p
+    torch.cuda.empty_cache()
