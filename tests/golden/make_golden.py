@@ -23,7 +23,13 @@ schema of keys, Python types, dtypes and shapes): the checkpoint interchange
 tests load it into this build's optimizers and compare schemas
 (src/optim/utils.py:283-310 saves exactly this dict).
 
-Usage:  python tests/golden/make_golden.py [--ref /root/reference] [--compiled] [--state-only]
+A fourth output (--nonfinite) repeats the eager runs of four cases with a few
+NaN / +inf / -inf gradient entries (NONFINITE) and stores them as
+``nonfinite.inputs.npz`` and ``<case>.nonfinite.npz``: how the reference's
+ops carry non-finite values (lerp, addcmul, sqrt, clamp, sign of NaN, the
+diagnostics' sums) is pinned by its own run.
+
+Usage:  python tests/golden/make_golden.py [--ref /root/reference] [--compiled] [--state-only] [--nonfinite]
 """
 from __future__ import annotations
 
@@ -101,6 +107,22 @@ def make_inputs(seed: int = 1234):
     has_grad = np.ones((N_STEPS, len(SHAPES)), dtype=bool)
     has_grad[0::2, NONE_ON_ODD] = False          # steps 1, 3, 5, ... have grad None
     return p0, grads, has_grad
+
+
+# Non-finite gradient entries for the --nonfinite fixtures: (step, tensor,
+# flat index, value).  Steps 3 and 6; tensor NONE_ON_ODD only on even steps.
+NONFINITE = [(3, 0, 2, float("nan")), (3, 0, 5, float("inf")), (3, 0, 9, float("-inf")),
+             (3, 1, 7, float("inf")), (3, 3, 4, float("nan")),
+             (6, 2, 3, float("nan")), (6, 4, 0, float("-inf")), (6, NONE_ON_ODD, 1, float("inf"))]
+NONFINITE_CASES = ("adana", "dana_mk4", "dana_star", "dana_star_mk4")
+
+
+def inject_nonfinite(grads):
+    """Copies of the step gradients with the NONFINITE entries written in."""
+    out = [[g.copy() for g in gs] for gs in grads]
+    for k, i, j, val in NONFINITE:
+        out[k - 1][i].reshape(-1)[j] = np.float32(val)
+    return out
 
 
 def load_module(ref: str, name: str):
@@ -181,6 +203,8 @@ def main():
     ap.add_argument("--compiled", action="store_true")
     ap.add_argument("--state-only", action="store_true",
                     help="only (re)write the <case>.state8.npz checkpoint fixtures")
+    ap.add_argument("--nonfinite", action="store_true",
+                    help="only write nonfinite.inputs.npz and <case>.nonfinite.npz (NaN/inf gradient entries)")
     args = ap.parse_args()
     import torch
 
@@ -198,6 +222,22 @@ def main():
                       for c, (m, cl, kw) in CASES.items()},
             "torch": torch.__version__, "cpu_capability": torch.backends.cpu.get_cpu_capability()}
     inputs["meta"] = np.array(json.dumps(meta))
+    if args.nonfinite:
+        grads_nf = inject_nonfinite(grads)
+        assert all(has_grad[k - 1, i] for k, i, _, _ in NONFINITE)
+        nf = dict(inputs)
+        for k in range(N_STEPS):
+            for i in range(len(SHAPES)):
+                nf[f"g_{k + 1}_{i}"] = grads_nf[k][i]
+        meta_nf = dict(meta, cases={c: meta["cases"][c] for c in NONFINITE_CASES},
+                       nonfinite=[[k, i, j, repr(v)] for k, i, j, v in NONFINITE])
+        nf["meta"] = np.array(json.dumps(meta_nf))
+        np.savez_compressed(os.path.join(HERE, "nonfinite.inputs.npz"), **nf)
+        for case in NONFINITE_CASES:
+            out = run_case(args.ref, case, False, p0, grads_nf, has_grad)
+            np.savez_compressed(os.path.join(HERE, f"{case}.nonfinite.npz"), **out)
+            print(f"wrote {case}.nonfinite.npz", flush=True)
+        return 0
     if args.state_only:
         for case in CASES:
             st = {}

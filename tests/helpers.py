@@ -38,8 +38,10 @@ def bf16_ulp_diff(a16: np.ndarray, b16: np.ndarray) -> np.ndarray:
     return np.abs(ordered(a16) - ordered(b16))
 
 
-def load_golden_inputs():
-    z = np.load(os.path.join(GOLDEN, "inputs.npz"))
+def load_golden_inputs(name: str = "inputs"):
+    """Inputs of the golden runs: ``inputs`` (finite gradients) or
+    ``nonfinite.inputs`` (the same with NaN / inf entries)."""
+    z = np.load(os.path.join(GOLDEN, f"{name}.npz"))
     meta = json.loads(str(z["meta"]))
     shapes = [tuple(s) for s in meta["shapes"]]
     p0 = [z[f"p0_{i}"] for i in range(len(shapes))]

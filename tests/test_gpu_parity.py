@@ -177,7 +177,22 @@ def test_golden_cases_on_gpu(oracle_mod, case):
     """The golden-vector scenarios (two groups, grad None every other step,
     all-zero and row-sparse grads, warm-up/cosine lr) on the GPU vs the oracle."""
     print("case: golden", case, flush=True)
-    meta, p0, grads, has_grad = load_golden_inputs()
+    _golden_on_gpu(oracle_mod, case, "inputs")
+
+
+@pytest.mark.parametrize("case", ["adana", "dana_mk4", "dana_star", "dana_star_mk4"])
+def test_nonfinite_gradients_on_gpu(oracle_mod, case):
+    """The same scenarios with NaN, +inf and -inf gradient entries at steps 3
+    and 6 (tests/golden/nonfinite.inputs.npz; the oracle follows the
+    reference's own run there): the elements they reach turn NaN (v: inf)
+    exactly where the oracle's do, the other elements keep the usual bars,
+    and the tensors' diagnostics are NaN."""
+    print("case: non-finite gradients", case, flush=True)
+    _golden_on_gpu(oracle_mod, case, "nonfinite.inputs")
+
+
+def _golden_on_gpu(oracle_mod, case, inputs):
+    meta, p0, grads, has_grad = load_golden_inputs(inputs)
     c = meta["cases"][case]
     kw = dict(c["kwargs"])
     star = c["class"] == "DANA_STAR_MK4"

@@ -87,6 +87,49 @@ def test_golden_trajectory(oracle_mod, case):
             assert _scaled_err(p, gold[f"p{i}_t{k}"], scale).max() <= 2 * k
 
 
+@pytest.mark.parametrize("case", ["adana", "dana_mk4", "dana_star", "dana_star_mk4"])
+def test_nonfinite_trajectory(oracle_mod, case):
+    """NaN, +inf and -inf gradient entries (tests/golden/make_golden.py
+    --nonfinite: the reference's own run).  Every element the reference turns
+    NaN or inf is NaN or the same inf here, in p, m, v and tau; the finite
+    elements meet the golden bars; diagnostics NaN where the reference's are."""
+    O = oracle_mod
+    meta, p0, grads, has_grad = load_golden_inputs("nonfinite.inputs")
+    gold = load_golden_case(case, "nonfinite")
+    params = [x.copy() for x in p0]
+    opt, kw, star = _make_oracle(O, meta, case, params)
+    for k in range(1, meta["n_steps"] + 1):
+        for g in opt.groups:
+            g.lr = kw["lr"] * meta["lr_multiplier"][k - 1]
+        opt.step(_grads_for_step(meta, grads, has_grad, k))
+        for i, p in enumerate(params):
+            st = opt.state.get(id(p))
+            if st is None:
+                continue
+            got = np.array([st[key] for key in O.DIAG_KEYS])
+            np.testing.assert_allclose(got, gold["diag"][k - 1, i], rtol=2e-5, atol=1e-12, equal_nan=True,
+                                       err_msg=f"{case} diag t={k} tensor {i}")
+        if k not in meta["checkpoints"]:
+            continue
+        for i, p in enumerate(params):
+            st = opt.state.get(id(p), {})
+            if "m" not in st:
+                continue
+            for key in ("m", "v") + (("tau",) if star else ()):
+                ref = gold[f"{key}{i}_t{k}"]
+                assert np.array_equal(np.isnan(st[key]), np.isnan(ref)), (case, key, k, i)
+                bound = 2 if key == "tau" else 0
+                assert ulp_diff(st[key], ref).max() <= bound, (case, key, k, i)
+            ref = gold[f"p{i}_t{k}"]
+            assert np.array_equal(np.isnan(p), np.isnan(ref)) and np.array_equal(np.isinf(p), np.isinf(ref))
+            fin = np.isfinite(ref)
+            assert np.array_equal(p[~fin & ~np.isnan(ref)], ref[~fin & ~np.isnan(ref)])
+            if np.isnan(ref).any():
+                assert (~fin).sum() < ref.size            # the other elements stay finite
+            scale = np.full(fin.sum(), np.abs(ref[fin]).max(), np.float32)
+            assert _scaled_err(p[fin], ref[fin], scale).max() <= 2 * k, (case, k, i)
+
+
 @pytest.mark.parametrize("case", golden_cases("eager"))
 @pytest.mark.parametrize("t0", [0, 7, 8])
 def test_golden_single_step(oracle_mod, case, t0):
