@@ -18,7 +18,11 @@ Muon buffers at CHECKPOINTS, every step's Dana diagnostics, the groups'
 weighted_step_count, the state_dict schema at STATE_AT and the constructor's
 printed parameter-assignment summary.
 
-Usage:  python tests/golden/make_golden_manau.py [--ref /root/reference]
+--nonfinite repeats two cases with NaN / +inf / -inf gradient entries in
+Dana-branch tensors (NONFINITE) and writes ``manau.nonfinite.inputs.npz`` and
+``manau.<case>.nonfinite.npz``.
+
+Usage:  python tests/golden/make_golden_manau.py [--ref /root/reference] [--nonfinite]
 """
 from __future__ import annotations
 
@@ -77,6 +81,20 @@ def make_inputs(seed: int = 4321):
             gs.append(g)
         grads.append(gs)
     return p0, grads
+
+
+# Non-finite gradient entries for --nonfinite: (step, tensor, flat index,
+# value), in Dana-branch tensors (the embedding, a LayerNorm vector, the head).
+NONFINITE = [(3, 0, 5, float("nan")), (3, 0, 30, float("inf")), (3, 5, 2, float("-inf")),
+             (6, 8, 11, float("nan")), (6, 7, 0, float("inf"))]
+NONFINITE_CASES = ("manau", "manau_mk4")
+
+
+def inject_nonfinite(grads):
+    out = [[g.copy() for g in gs] for gs in grads]
+    for k, i, j, val in NONFINITE:
+        out[k - 1][i].reshape(-1)[j] = np.float32(val)
+    return out
 
 
 def load_module(ref: str, name: str):
@@ -154,6 +172,8 @@ def run_case(ref: str, case: str, p0, grads):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--ref", default="/root/reference")
+    ap.add_argument("--nonfinite", action="store_true",
+                    help="only write manau.nonfinite.inputs.npz and manau.<case>.nonfinite.npz")
     args = ap.parse_args()
     import torch
 
@@ -167,6 +187,20 @@ def main():
             "state_at": STATE_AT, "lr_multiplier": [lr_multiplier(k) for k in range(1, N_STEPS + 1)],
             "cases": CASES, "torch": torch.__version__}
     inputs["meta"] = np.array(json.dumps(meta))
+    if args.nonfinite:
+        grads = inject_nonfinite(grads)
+        for k in range(N_STEPS):
+            for i in range(len(PARAMS)):
+                inputs[f"g_{k + 1}_{i}"] = grads[k][i]
+        meta_nf = dict(meta, cases={c: CASES[c] for c in NONFINITE_CASES},
+                       nonfinite=[[k, i, j, repr(v)] for k, i, j, v in NONFINITE])
+        inputs["meta"] = np.array(json.dumps(meta_nf))
+        np.savez_compressed(os.path.join(HERE, "manau.nonfinite.inputs.npz"), **inputs)
+        for case in NONFINITE_CASES:
+            out = run_case(args.ref, case, p0, grads)
+            np.savez_compressed(os.path.join(HERE, f"manau.{case}.nonfinite.npz"), **out)
+            print("wrote", case, "nonfinite")
+        return
     np.savez_compressed(os.path.join(HERE, "manau.inputs.npz"), **inputs)
     for case in CASES:
         out = run_case(args.ref, case, p0, grads)

@@ -34,13 +34,17 @@ GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
 CASES = ("manau", "manau_wt", "manau_mk4")
 
 
-def _load(case):
-    z = np.load(os.path.join(GOLDEN, "manau.inputs.npz"))
+def _load(case, nonfinite=False):
+    """Inputs and the reference's recorded run; ``nonfinite``: the inputs with
+    NaN / inf gradient entries in Dana-branch tensors (make_golden_manau.py
+    --nonfinite)."""
+    tag = ".nonfinite" if nonfinite else ""
+    z = np.load(os.path.join(GOLDEN, f"manau{tag}.inputs.npz"))
     meta = json.loads(str(z["meta"]))
     n = len(meta["params"])
     p0 = [z[f"p0_{i}"] for i in range(n)]
     grads = [[z[f"g_{k}_{i}"] for i in range(n)] for k in range(1, meta["n_steps"] + 1)]
-    return meta, p0, grads, np.load(os.path.join(GOLDEN, f"manau.{case}.npz"))
+    return meta, p0, grads, np.load(os.path.join(GOLDEN, f"manau.{case}{tag}.npz"))
 
 
 def _build(meta, case, p0):
@@ -67,11 +71,11 @@ def _set_step_inputs(opt, params, meta, kw, grads, k):
         p.grad = torch.from_numpy(grads[k - 1][i].copy()).to(DEV)
 
 
-@pytest.mark.parametrize("case", CASES)
-def test_manau_matches_oracle_and_reference(oracle_mod, case):
+@pytest.mark.parametrize("case,nonfinite", [(c, False) for c in CASES] + [("manau", True), ("manau_mk4", True)])
+def test_manau_matches_oracle_and_reference(oracle_mod, case, nonfinite):
     O = oracle_mod
-    print("case: Manau", case, flush=True)
-    meta, p0, grads, gold = _load(case)
+    print("case: Manau", case, "non-finite gradients" if nonfinite else "", flush=True)
+    meta, p0, grads, gold = _load(case, nonfinite)
     opt, params, kw = _build(meta, case, p0)
     use_muon = [bool(opt.state[p]["use_muon"]) for p in params]
     assert use_muon == [bool(u) for u in gold["use_muon"]]
@@ -119,7 +123,7 @@ def test_manau_matches_oracle_and_reference(oracle_mod, case):
             assert st["current_alpha"] == ost["current_alpha"] == gold["diag"][k - 1, i, 0], tag
             got = [float(st[key]) for key in ("current_alpha_factor", "gradient_norm", "auto_factor_mean", "m_norm")]
             ref = [ost[key] for key in ("current_alpha_factor", "gradient_norm", "auto_factor_mean", "m_norm")]
-            np.testing.assert_allclose(got, ref, rtol=1e-5, atol=1e-30, err_msg=tag)
+            np.testing.assert_allclose(got, ref, rtol=1e-5, atol=1e-30, equal_nan=True, err_msg=tag)
     # Muon parameters after 12 steps of bfloat16 Newton-Schulz updates (each
     # about 0.2 * lr per entry) on the GPU vs the reference's CPU run
     print(f"max |p_muon - reference| / lr over the checkpoints: {worst_muon:.3g}", flush=True)

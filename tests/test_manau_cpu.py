@@ -26,8 +26,8 @@ CASES = ("manau", "manau_wt", "manau_mk4")
 DIAG = ("current_alpha", "current_alpha_factor", "gradient_norm", "auto_factor_mean", "m_norm")
 
 
-def _inputs():
-    z = np.load(os.path.join(GOLDEN, "manau.inputs.npz"))
+def _inputs(name="manau.inputs"):
+    z = np.load(os.path.join(GOLDEN, f"{name}.npz"))
     meta = json.loads(str(z["meta"]))
     n = len(meta["params"])
     p0 = [z[f"p0_{i}"] for i in range(n)]
@@ -99,6 +99,50 @@ def test_oracle_manau_follows_reference_trajectory(oracle_mod, case):
             assert ulp_diff(st["dana_tau"], gold[f"dana_tau{i}_t{k}"]).max() <= max(2, k // 2), (case, k, names[i])
             scale = np.full(p.shape, np.abs(gold[f"p{i}_t{k}"]).max(), np.float32)
             assert _scaled_err(p, gold[f"p{i}_t{k}"], scale).max() <= 2 * k, (case, k, names[i])
+
+
+@pytest.mark.parametrize("case", ["manau", "manau_mk4"])
+def test_oracle_manau_nonfinite_gradients(oracle_mod, case):
+    """NaN, +inf and -inf gradient entries in Dana-branch tensors
+    (make_golden_manau.py --nonfinite, the reference's own run): the oracle
+    puts NaN and inf where the reference does in dana_m, dana_v, dana_tau and
+    p; the other elements meet the trajectory bars; diagnostics NaN alike."""
+    O = oracle_mod
+    meta, p0, grads = _inputs("manau.nonfinite.inputs")
+    gold = np.load(os.path.join(GOLDEN, f"manau.{case}.nonfinite.npz"))
+    use_muon = gold["use_muon"]
+    params = [x.copy() for x in p0]
+    opt, kw, order = _oracle(O, meta, case, params, use_muon)
+    hit = set()
+    for k in range(1, meta["n_steps"] + 1):
+        for g in opt.groups:
+            g.lr = kw["lr"] * meta["lr_multiplier"][k - 1]
+        opt.step([[grads[k - 1][i] for i in idx] for idx in order])
+        for i, p in enumerate(params):
+            if use_muon[i]:
+                continue
+            st = opt.state[id(p)]
+            got = np.array([st[key] for key in DIAG[1:]])
+            np.testing.assert_allclose(got, gold["diag"][k - 1, i][1:], rtol=2e-5, atol=1e-12, equal_nan=True,
+                                       err_msg=f"{case} t={k} tensor {i}")
+        if k not in meta["checkpoints"]:
+            continue
+        for i, p in enumerate(params):
+            if use_muon[i]:
+                continue
+            st = opt.state[id(p)]
+            for key, bound in (("dana_m", 0), ("dana_v", 0), ("dana_tau", max(2, k // 2))):
+                ref = gold[f"{key}{i}_t{k}"]
+                assert np.array_equal(np.isnan(st[key]), np.isnan(ref)), (case, key, k, i)
+                assert ulp_diff(st[key], ref).max() <= bound, (case, key, k, i)
+            ref = gold[f"p{i}_t{k}"]
+            assert np.array_equal(np.isnan(p), np.isnan(ref)) and np.array_equal(np.isinf(p), np.isinf(ref))
+            if not np.isfinite(ref).all():
+                hit.add(i)
+            fin = np.isfinite(ref)
+            scale = np.full(fin.sum(), np.abs(ref[fin]).max(), np.float32)
+            assert _scaled_err(p[fin], ref[fin], scale).max() <= 2 * k, (case, k, i)
+    assert hit == {0, 5, 7, 8}                                  # every injected tensor went non-finite
 
 
 @pytest.mark.parametrize("case", CASES)
