@@ -452,34 +452,49 @@ def test_run_twice_is_deterministic():
 
 @pytest.mark.parametrize("star", [False, True])
 def test_drift_over_1000_steps(oracle_mod, star):
-    """1,000 steps without re-synchronising the oracle: m, v, tau stay
-    bit-exact (they never read p); ADana p stays bit-exact; Dana-Star p drifts
-    by at most a few ulp of the tensor's scale."""
-    print("case: 1000-step drift star", star, flush=True)
+    """1,000 steps at config C1's shape (1024 x 4096) without re-synchronising
+    the oracle: m, v, tau stay bit-exact (they never read p); ADana p stays
+    bit-exact; Dana-Star p differs only where a pow hard case (rate ~4e-9 per
+    element and step) left a trace, by at most a few ulp of the tensor's
+    scale.  Reports max / median ulp and the max relative difference."""
+    print("case: 1000-step drift at 1024x4096, star", star, flush=True)
     rng = np.random.default_rng(23)
-    shape = (257, 255)
+    shape = (1024, 4096)
+    n = shape[0] * shape[1]
     pair = Pair(oracle_mod, star, [([_normal(rng, shape, 0.02)], {})], lr=1e-3, delta=8.0,
                 kappa=0.85, clipsnr=2.0 if star else None, weight_decay=0.4, wd_decaying=True,
                 wd_ts=100.0)
-    worst = 0.0
+    gen = torch.Generator(device=DEV)
+    gpu_p = pair.gpu_params[0][0]
+    c = pair.cpu_params[0][0]
+    worst, worst_rel, med = 0.0, 0.0, 0.0
     for t in range(1, 1001):
-        pair.step([[_normal(rng, shape, 1e-3)]])
+        gen.manual_seed(5000 + t)
+        g = torch.empty(shape, device=DEV).normal_(0.0, 1e-3, generator=gen)
+        gpu_p.grad = g
+        pair.opt.step()
+        pair.oracle.step([[g.cpu().numpy()]])
         if t % 100 == 0 or t in (1, 8, 9):
-            p = pair.gpu_params[0][0].detach().cpu().numpy()
-            c = pair.cpu_params[0][0]
-            st, ost = pair.opt.state[pair.gpu_params[0][0]], pair.oracle.state[id(c)]
+            torch.cuda.synchronize()
+            p = gpu_p.detach().cpu().numpy()
+            st, ost = pair.opt.state[gpu_p], pair.oracle.state[id(c)]
             for key in ("m", "v") + (("tau",) if star else ()):
                 assert ulp_diff(st[key].cpu().numpy(), ost[key]).max() == 0, (t, key)
+            d = ulp_diff(p, c)
+            nz = d[d > 0]
             scale = np.full(p.shape, np.abs(c).max(), np.float32)
             err = np.abs(p.astype(np.float64) - c) / np.spacing(scale).astype(np.float64)
-            worst = max(worst, float(err.max()))
-            n_diff = int(np.count_nonzero(ulp_diff(p, c)))
+            rel = np.abs(p.astype(np.float64) - c) / np.maximum(np.abs(c.astype(np.float64)), 1e-30)
+            worst, worst_rel = max(worst, float(err.max())), max(worst_rel, float(rel.max()))
+            med = float(np.median(nz)) if nz.size else 0.0
+            print(f"t={t}: {nz.size} elements differ, max {int(d.max())} ulp, median {med:.1f} ulp of the "
+                  f"differing ones, max rel {float(rel.max()):.2e}", flush=True)
             if not star:
-                assert err.max() == 0, t
+                assert d.max() == 0, t
             else:
                 # a pow hard case leaves a <=1-ulp trace in p that later steps carry
-                assert n_diff <= 8, (t, n_diff)
-    print(f"max drift of p over 1000 steps: {worst:.2f} ulp of max|p|", flush=True)
+                assert nz.size <= 8 + math.ceil(2e-8 * n * t), (t, nz.size)
+    print(f"max drift of p over 1000 steps: {worst:.2f} ulp of max|p|, max rel {worst_rel:.2e}", flush=True)
     assert worst <= 4
 
 
