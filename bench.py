@@ -112,6 +112,21 @@ def bytes_per_elem(w):
     return b
 
 
+def cpu_model() -> str:
+    """The host CPU's model name (first 'model name' of /proc/cpuinfo), and
+    the cores this process may use."""
+    name = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    name = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return f"{name}; {len(os.sched_getaffinity(0))} cores available"
+
+
 def cos_inf(k, n=200, warmup=4, final_div=0.1):
     if k < warmup:
         return (k + 1) / warmup
@@ -194,7 +209,7 @@ def cpu_baseline(w, target_s=10.0, max_elems=1 << 26):
             break
     per_step = el / reps
     gbs = total * bytes_per_elem(w) / per_step / 1e9
-    return {"value": round(gbs, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+    return {"value": round(gbs, 3), "unit": "GB/s", "cores": threads, "kind": "port", "cpu_model": cpu_model(),
             "sample": f"{total} elements (first {len(arrays)} tensors of the list), "
                       f"{reps} timed steps after 1 warm-up, {per_step * 1e3:.1f} ms/step, "
                       f"oracle/adana_oracle.c with {threads} OpenMP threads",
@@ -341,9 +356,9 @@ def consumer_bench(args):
             _ = srt[idx], srt[(x.size - 1) - idx]
         cpu_ms = (time.perf_counter() - c0) * 1e3
         cpu = {"value": round(ns / (cpu_ms * 1e-3) / 1e9, 4), "unit": "Gelem/s", "cores": 1,
-               "kind": "port", "sample": f"first 4 tau tensors ({ns} elements): tau.cpu(), np.sort, "
-                                         f"order-statistic picks as src/optim/tau_stats_collector.py:131-160, "
-                                         f"{cpu_ms:.0f} ms"}
+               "kind": "port", "cpu_model": cpu_model(),
+               "sample": f"first 4 tau tensors ({ns} elements): tau.cpu(), np.sort, order-statistic picks as "
+                         f"src/optim/tau_stats_collector.py:131-160, {cpu_ms:.0f} ms"}
         value = n_elems / (ms * 1e-3) / 1e9
         metric, unit = "tau order statistics over the north-star state (elements/s)", "Gelem/s"
     else:
@@ -356,8 +371,9 @@ def consumer_bench(args):
                     vals.append(st[k].item())
         cpu_ms = (time.perf_counter() - c0) * 1e3
         cpu = {"value": round(n_elems / (cpu_ms * 1e-3), 1), "unit": "tensors/s", "cores": 1,
-               "kind": "port", "sample": f"all {n_elems} tensors, value by value (.item() per "
-                                         f"diagnostic) as src/optim/utils.py:572-596, {cpu_ms:.1f} ms"}
+               "kind": "port", "cpu_model": cpu_model(),
+               "sample": f"all {n_elems} tensors, value by value (.item() per diagnostic) as "
+                         f"src/optim/utils.py:572-596, {cpu_ms:.1f} ms"}
         value = n_elems / (ms * 1e-3)
         metric, unit = "log_optimizer_schedules over 10,000 tensors (tensors/s)", "tensors/s"
     print(json.dumps({"metric": metric, "value": round(value, 4), "unit": unit, "n_gpus": 1,
@@ -461,7 +477,7 @@ def manau_bench(args):
             reps += 1
         per = (time.perf_counter() - t0) / reps
         result["cpu_baseline"] = {"value": round(36 * n / per / 1e9, 3), "unit": "GB/s", "cores": threads,
-                                  "kind": "port",
+                                  "kind": "port", "cpu_model": cpu_model(),
                                   "sample": f"{n} elements, {reps} steps of oracle/adana_oracle.c's Manau branch "
                                             f"with {threads} OpenMP threads, {per * 1e3:.1f} ms/step"}
     print(json.dumps(result), flush=True)
