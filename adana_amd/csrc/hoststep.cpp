@@ -20,6 +20,7 @@
 
 #include <Python.h>
 
+#include <cstdint>
 #include <exception>
 
 namespace {
@@ -47,36 +48,34 @@ int same_grad(PyObject *p, PyObject *cached) {
     return same;
 }
 
-/* advance_if_same(params, grads, states) -> bool
- *
- * True when params[i].grad is grads[i] for every i (None included); then every
- * dict in ``states`` has its "step" entry incremented by one.  False (and
- * nothing modified) as soon as one gradient differs. */
-PyObject *advance_if_same(PyObject *, PyObject *args) {
-    PyObject *params, *grads, *states;
-    if (!PyArg_ParseTuple(args, "O!O!O!", &PyList_Type, &params, &PyList_Type, &grads, &PyList_Type, &states))
-        return nullptr;
-    const Py_ssize_t n = PyList_GET_SIZE(params);
-    if (PyList_GET_SIZE(grads) != n) Py_RETURN_FALSE;
-    try {
-        for (Py_ssize_t i = 0; i < n; ++i) {
-            const int same = same_grad(PyList_GET_ITEM(params, i), PyList_GET_ITEM(grads, i));
-            if (same < 0) return nullptr;
-            if (!same) Py_RETURN_FALSE;
-        }
-    } catch (const std::exception &e) {
-        PyErr_SetString(PyExc_RuntimeError, e.what());
-        return nullptr;
+// The data pointer of tensor `t` (0 for None), or -1 with a Python error set.
+int data_ptr_of(PyObject *t, uint64_t *out) {
+    if (t == Py_None) {
+        *out = 0;
+        return 0;
     }
-    // Tensors stepped together hold equal counts: the new int of the previous
-    // entry is reused (ints are immutable) when this entry's old int is equal.
+    if (THPVariable_CheckExact(t)) {
+        *out = reinterpret_cast<uint64_t>(THPVariable_Unpack(t).data_ptr());
+        return 0;
+    }
+    PyObject *r = PyObject_CallMethod(t, "data_ptr", nullptr);
+    if (!r) return -1;
+    *out = static_cast<uint64_t>(PyLong_AsUnsignedLongLong(r));
+    Py_DECREF(r);
+    return PyErr_Occurred() ? -1 : 0;
+}
+
+// states[i]["step"] += 1 for every dict; tensors stepped together hold equal
+// counts, so the new int of the previous entry is reused (ints are immutable)
+// when this entry's old int is equal.  0, or -1 with a Python error set.
+int advance_states(PyObject *states) {
     const Py_ssize_t m = PyList_GET_SIZE(states);
     PyObject *prev_v = nullptr, *prev_w = nullptr;
     int rc = 0;
     for (Py_ssize_t i = 0; i < m && !rc; ++i) {
         PyObject *st = PyList_GET_ITEM(states, i);
         if (!PyDict_Check(st)) {
-            PyErr_SetString(PyExc_TypeError, "advance_if_same: state entries must be dicts");
+            PyErr_SetString(PyExc_TypeError, "step counters: state entries must be dicts");
             rc = -1;
             break;
         }
@@ -104,8 +103,124 @@ PyObject *advance_if_same(PyObject *, PyObject *args) {
     }
     Py_XDECREF(prev_v);
     Py_XDECREF(prev_w);
-    if (rc) return nullptr;
+    return rc;
+}
+
+/* advance_if_same(params, grads, states[, param_ptrs]) -> bool
+ *
+ * True when params[i].grad is grads[i] for every i (None included); then every
+ * dict in ``states`` has its "step" entry incremented by one.  False (and
+ * nothing modified) as soon as one gradient differs. */
+PyObject *advance_if_same(PyObject *, PyObject *args) {
+    PyObject *params, *grads, *states, *pptrs = Py_None;
+    if (!PyArg_ParseTuple(args, "O!O!O!|O", &PyList_Type, &params, &PyList_Type, &grads, &PyList_Type, &states,
+                          &pptrs))
+        return nullptr;
+    const Py_ssize_t n = PyList_GET_SIZE(params);
+    if (PyList_GET_SIZE(grads) != n) Py_RETURN_FALSE;
+    const uint64_t *want = nullptr;
+    if (pptrs != Py_None) {
+        if (!PyBytes_Check(pptrs) || PyBytes_GET_SIZE(pptrs) != 8 * n) Py_RETURN_FALSE;
+        want = reinterpret_cast<const uint64_t *>(PyBytes_AS_STRING(pptrs));
+    }
+    try {
+        for (Py_ssize_t i = 0; i < n; ++i) {
+            PyObject *p = PyList_GET_ITEM(params, i);
+            const int same = same_grad(p, PyList_GET_ITEM(grads, i));
+            if (same < 0) return nullptr;
+            if (!same) Py_RETURN_FALSE;
+            if (want) {
+                uint64_t ptr;
+                if (data_ptr_of(p, &ptr)) return nullptr;
+                if (ptr != want[i]) Py_RETURN_FALSE;
+            }
+        }
+    } catch (const std::exception &e) {
+        PyErr_SetString(PyExc_RuntimeError, e.what());
+        return nullptr;
+    }
+    if (advance_states(states)) return nullptr;
     Py_RETURN_TRUE;
+}
+
+/* advance_steps(states) -> None: every dict's "step" entry + 1. */
+PyObject *advance_steps(PyObject *, PyObject *args) {
+    PyObject *states;
+    if (!PyArg_ParseTuple(args, "O!", &PyList_Type, &states)) return nullptr;
+    if (advance_states(states)) return nullptr;
+    Py_RETURN_NONE;
+}
+
+/* grads_of(params) -> (grads, absent)
+ *
+ * ``[p.grad for p in params]`` and a bytes object whose byte i is 1 where
+ * params[i].grad is None. */
+PyObject *grads_of(PyObject *, PyObject *args) {
+    PyObject *params;
+    if (!PyArg_ParseTuple(args, "O!", &PyList_Type, &params)) return nullptr;
+    const Py_ssize_t n = PyList_GET_SIZE(params);
+    PyObject *out = PyList_New(n);
+    if (!out) return nullptr;
+    PyObject *absent = PyBytes_FromStringAndSize(nullptr, n);
+    if (!absent) {
+        Py_DECREF(out);
+        return nullptr;
+    }
+    char *ab = PyBytes_AS_STRING(absent);
+    try {
+        for (Py_ssize_t i = 0; i < n; ++i) {
+            PyObject *p = PyList_GET_ITEM(params, i);
+            PyObject *g;
+            if (THPVariable_CheckExact(p)) {
+                const at::Tensor &t = THPVariable_Unpack(p).unsafeGetTensorImpl()->grad();
+                if (t.defined()) {
+                    g = THPVariable_Wrap(t);
+                } else {
+                    Py_INCREF(Py_None);
+                    g = Py_None;
+                }
+            } else {
+                g = PyObject_GetAttr(p, g_grad_name);
+            }
+            if (!g) {
+                Py_DECREF(out);
+                Py_DECREF(absent);
+                return nullptr;
+            }
+            ab[i] = g == Py_None ? 1 : 0;
+            PyList_SET_ITEM(out, i, g);                      /* steals the reference */
+        }
+    } catch (const std::exception &e) {
+        Py_DECREF(out);
+        Py_DECREF(absent);
+        PyErr_SetString(PyExc_RuntimeError, e.what());
+        return nullptr;
+    }
+    return Py_BuildValue("NN", out, absent);
+}
+
+/* data_ptrs(tensors) -> bytes: each tensor's data_ptr() (0 for None) as
+ * native uint64 values. */
+PyObject *data_ptrs(PyObject *, PyObject *args) {
+    PyObject *ts;
+    if (!PyArg_ParseTuple(args, "O!", &PyList_Type, &ts)) return nullptr;
+    const Py_ssize_t n = PyList_GET_SIZE(ts);
+    PyObject *out = PyBytes_FromStringAndSize(nullptr, 8 * n);
+    if (!out) return nullptr;
+    uint64_t *w = reinterpret_cast<uint64_t *>(PyBytes_AS_STRING(out));
+    try {
+        for (Py_ssize_t i = 0; i < n; ++i) {
+            if (data_ptr_of(PyList_GET_ITEM(ts, i), &w[i])) {
+                Py_DECREF(out);
+                return nullptr;
+            }
+        }
+    } catch (const std::exception &e) {
+        Py_DECREF(out);
+        PyErr_SetString(PyExc_RuntimeError, e.what());
+        return nullptr;
+    }
+    return out;
 }
 
 /* bump_versions(tensors) -> None
@@ -170,8 +285,15 @@ PyObject *same_params(PyObject *, PyObject *args) {
 
 PyMethodDef methods[] = {
     {"advance_if_same", advance_if_same, METH_VARARGS,
-     "advance_if_same(params, grads, states) -> bool: if params[i].grad is grads[i] for all i, "
-     "increment every states[j]['step'] and return True; otherwise change nothing and return False."},
+     "advance_if_same(params, grads, states[, param_ptrs]) -> bool: if params[i].grad is grads[i] for all i "
+     "(and params[i].data_ptr() is param_ptrs[i], native uint64 bytes), increment every states[j]['step'] "
+     "and return True; otherwise change nothing and return False."},
+    {"advance_steps", advance_steps, METH_VARARGS,
+     "advance_steps(states) -> None: increment every states[j]['step']."},
+    {"grads_of", grads_of, METH_VARARGS,
+     "grads_of(params) -> (grads, absent): [p.grad for p in params] and a bytes of 1 where grad is None."},
+    {"data_ptrs", data_ptrs, METH_VARARGS,
+     "data_ptrs(tensors) -> bytes: each tensor's data_ptr() (0 for None) as native uint64."},
     {"bump_versions", bump_versions, METH_VARARGS,
      "bump_versions(tensors) -> None: increment each tensor's autograd version counter."},
     {"same_params", same_params, METH_VARARGS,

@@ -262,5 +262,5 @@ class Manau(_DanaFamily):
         else:
             for ls in self._sets:
                 ls.grads = grads if len(self._sets) == 1 else [grads[i] for i in ls.index]
-                self._refresh_grads(ls)
+                self._refresh_ptrs(ls)
         self._launch(params, grads, classes, None)

@@ -32,7 +32,6 @@ written as RNE(master) in the same pass.
 from __future__ import annotations
 
 import ctypes
-import itertools
 import operator
 from typing import Iterable, List, Optional
 
@@ -93,7 +92,7 @@ class _LaunchSet:
         self.workspace = None
         self.plan = None
         self.diag = None
-        self.ptr_key = None
+        self.ptr_key = None         # the gradients' and parameters' data pointers the tables hold
 
 
 class _DanaFamily(Optimizer):
@@ -169,9 +168,9 @@ class _DanaFamily(Optimizer):
                     st[fam] = t
 
     def invalidate_plan(self) -> None:
-        """Forget cached device tables and tensor lists (call after swapping
-        state tensors or parameter storage, or editing a group's parameter
-        list in place)."""
+        """Forget cached device tables and tensor lists (call after swapping a
+        state tensor by hand; new gradients, rebound parameter storage and
+        parameters replaced in a group's list are followed by step())."""
         self._sets = None
         self._structure = None
         self._flat = None
@@ -337,7 +336,7 @@ class _DanaFamily(Optimizer):
             numels = np.fromiter((p.numel() for p in ls.params), dtype=np.int64, count=len(ls.params))
             ls.vstart, ls.fold_first, ls.n_chunks, ls.n_folds = _lib.plan_layout(numels)
             ls.host_desc = self._desc_rows(ls)
-            ls.ptr_key = ls.host_desc["grad"].copy()
+            ls.ptr_key = (_hoststep.data_ptrs(ls.grads), _hoststep.data_ptrs(ls.params))
             with torch.cuda.device(ls.device):
                 self._upload(ls)
                 n = len(ls.params)
@@ -464,33 +463,33 @@ class _DanaFamily(Optimizer):
         all_params, gidx = self._flat_params()
         act = self._active
         if (self._sets is not None and act is not None
-                and _hoststep.advance_if_same(all_params, act["all_grads"], act["states"])):
+                and _hoststep.advance_if_same(all_params, act["all_grads"], act["states"], act["pptrs"])):
             # Persistent gradients: every p.grad is the same tensor object as at
-            # the last step (grad None where it was None), so the active set,
-            # device tables and scalar classes carry over; advance_if_same has
-            # already done the per-tensor ``state['step'] += 1`` (adana.py:197).
+            # the last step (grad None where it was None) and every parameter
+            # keeps its storage, so the active set, device tables and scalar
+            # classes carry over; advance_if_same has already done the
+            # per-tensor ``state['step'] += 1`` (adana.py:197).
             grads = act["grads"]
             classes = act["classes"] = [(gi, t + 1) for gi, t in act["classes"]]
             params = act["params"]
             return self._launch(params, grads, classes, loss)
-        all_grads = list(map(_GRAD, all_params))
-        absent = tuple(map(operator.is_, all_grads, itertools.repeat(None)))   # adana.py:186
+        all_grads, absent = _hoststep.grads_of(all_params)                   # adana.py:186
 
         if self._sets is not None and act is not None and act["absent"] == absent:
-            # Steady state: the same tensors have gradients as at the last step, so
-            # every active tensor advances by one and the scalar classes carry over.
+            # Steady state: the same tensors have gradients as at the last step
+            # (new gradient tensors, as after zero_grad(set_to_none=True)), so
+            # every active tensor advances by one and the scalar classes carry
+            # over; the device tables are re-pointed where an address moved.
             grads = all_grads if act["all"] else [all_grads[i] for i in act["index"]]
-            for st in act["states"]:
-                st["step"] += 1                                              # adana.py:197
+            _hoststep.advance_steps(act["states"])                             # adana.py:197
             classes = act["classes"] = [(gi, t + 1) for gi, t in act["classes"]]
             params = act["params"]
             for ls in self._sets:
-                new = grads if len(self._sets) == 1 else [grads[i] for i in ls.index]
-                if not all(map(operator.is_, new, ls.grads)):
-                    ls.grads = new
-                    self._refresh_grads(ls)
+                ls.grads = grads if len(self._sets) == 1 else [grads[i] for i in ls.index]
+                self._refresh_ptrs(ls)
             act["all_grads"] = all_grads
             act["grads"] = grads
+            act["pptrs"] = _hoststep.data_ptrs(all_params)
         else:
             params, grads, states, keys, index, fresh = [], [], [], [], [], []
             for i, (p, g) in enumerate(zip(all_params, all_grads)):
@@ -528,10 +527,11 @@ class _DanaFamily(Optimizer):
             else:
                 for ls in self._sets:
                     ls.grads = grads if len(self._sets) == 1 else [grads[i] for i in ls.index]
-                    self._refresh_grads(ls)
+                    self._refresh_ptrs(ls)
             self._active = {"absent": absent, "all": len(index) == len(all_params),
                             "index": index, "states": states, "params": params,
-                            "classes": classes, "all_grads": all_grads, "grads": grads}
+                            "classes": classes, "all_grads": all_grads, "grads": grads,
+                            "pptrs": _hoststep.data_ptrs(all_params)}
         return self._launch(params, grads, classes, loss)
 
     def _launch(self, params, grads, classes, loss):
@@ -574,17 +574,18 @@ class _DanaFamily(Optimizer):
             _hoststep.bump_versions(grads)
         return loss
 
-    def _refresh_grads(self, ls: _LaunchSet) -> None:
-        """Re-point the launch set's descriptors at this step's gradients (only
-        re-uploaded when an address moved)."""
-        gptr = np.fromiter(map(_DATA_PTR, ls.grads), dtype=np.uint64, count=len(ls.grads))
-        if np.array_equal(gptr, ls.ptr_key):
+    def _refresh_ptrs(self, ls: _LaunchSet) -> None:
+        """Re-point the launch set's descriptors at this step's gradients and
+        the parameters' current storage (re-uploaded only when an address
+        moved: a new gradient allocation, or ``p.data`` rebound)."""
+        key = (_hoststep.data_ptrs(ls.grads), _hoststep.data_ptrs(ls.params))
+        if key == ls.ptr_key:
             return
         for p, g in zip(ls.params, ls.grads):
             if self._validate(p, g) != ls.flags:
                 raise RuntimeError(f"{type(self).__name__}: gradient dtype changed")
         ls.host_desc = self._desc_rows(ls)
-        ls.ptr_key = ls.host_desc["grad"].copy()
+        ls.ptr_key = key
         with torch.cuda.device(ls.device):
             self._upload(ls)
 

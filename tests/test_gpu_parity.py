@@ -519,3 +519,34 @@ def test_large_tensor_fold_path(oracle_mod, star):
     total = adana_amd.clip_grad_norm_(pair.gpu_params[0], 1e9)
     want = float(np.sqrt(sum(float(np.sum(np.square(g.cpu().numpy().astype(np.float64)))) for g in grads)))
     assert abs(float(total) - want) <= 2e-6 * want
+
+
+@pytest.mark.parametrize("fresh_grads", [False, True])
+def test_parameter_storage_rebound_is_followed(oracle_mod, fresh_grads):
+    """``p.data = other`` between steps (a new storage for the parameter) is
+    picked up without invalidate_plan(): the step updates the new storage and
+    leaves the old one alone, with gradients that persist between steps and
+    with new gradient tensors every step (zero_grad(set_to_none=True))."""
+    print("case: parameter storage rebound, fresh grads", fresh_grads, flush=True)
+    rng = np.random.default_rng(41)
+    shapes = [(300,), (64, 33), (7,)]
+    params = [_normal(rng, s, 0.02) for s in shapes]
+    pair = Pair(oracle_mod, True, [(params, {})], lr=1e-3, delta=8.0, kappa=0.85, clipsnr=2.0,
+                weight_decay=0.1)
+    gl = [[_normal(rng, x.shape, 1e-3) for x in params]]
+    gpu_grads = [torch.from_numpy(g.copy()).to(DEV) for g in gl[0]]
+    for k in range(6):
+        if k == 3:
+            p = pair.gpu_params[0][1]
+            old = p.data
+            p.data = old.clone()                                   # same values, new storage
+            snapshot = old.clone()
+        for p, g in zip(pair.gpu_params[0], gpu_grads):
+            p.grad = g.clone() if fresh_grads else g
+        pair.prev = [[x.copy() for x in cp] for cp in pair.cpu_params]
+        pair.opt.step()
+        pair.oracle.step(gl)
+        torch.cuda.synchronize()
+        pair.compare(where=f"k={k}")
+        if k >= 3:
+            assert torch.equal(old, snapshot)                      # the old storage is not written

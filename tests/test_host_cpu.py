@@ -383,3 +383,37 @@ def test_flat_params_follow_the_groups():
     assert not _hoststep.same_params(opt.param_groups, [a, c, d, d])      # longer cache
     with pytest.raises(KeyError):
         _hoststep.same_params([{"lr": 1.0}], [])
+
+
+def test_hoststep_grads_ptrs_and_steps():
+    """grads_of is [p.grad for p in params] plus the None pattern; data_ptrs
+    gives each data_ptr() (0 for None); advance_steps increments every
+    counter; advance_if_same with parameter pointers refuses a parameter
+    whose storage was rebound (p.data = ...)."""
+    from adana_amd import _hoststep
+
+    class Sub(torch.Tensor):
+        pass
+
+    ps = [torch.nn.Parameter(torch.zeros(3)), torch.nn.Parameter(torch.zeros(2)),
+          torch.zeros(4).as_subclass(Sub).requires_grad_()]
+    ps[0].grad = torch.ones(3)
+    ps[2].grad = torch.ones(4).as_subclass(Sub)
+    grads, absent = _hoststep.grads_of(ps)
+    assert grads[0] is ps[0].grad and grads[1] is None and grads[2] is ps[2].grad
+    assert absent == bytes([0, 1, 0])
+    ptrs = np.frombuffer(_hoststep.data_ptrs([ps[0], None, ps[2].grad]), dtype=np.uint64)
+    assert ptrs.tolist() == [ps[0].data_ptr(), 0, ps[2].grad.data_ptr()]
+    with pytest.raises(AttributeError):                       # not a tensor: no data_ptr()
+        _hoststep.data_ptrs(["x"])
+    states = [{"step": 1}, {"step": 1}]
+    _hoststep.advance_steps(states)
+    assert [s["step"] for s in states] == [2, 2]
+    pp = _hoststep.data_ptrs(ps)
+    assert _hoststep.advance_if_same(ps, grads, states, pp) is True
+    assert [s["step"] for s in states] == [3, 3]
+    ps[1].data = torch.zeros(2)                                 # storage rebound
+    assert _hoststep.advance_if_same(ps, grads, states, pp) is False
+    assert [s["step"] for s in states] == [3, 3]
+    assert _hoststep.advance_if_same(ps, grads, states, _hoststep.data_ptrs(ps)) is True
+    assert _hoststep.advance_if_same(ps, grads, states, b"short") is False
