@@ -283,6 +283,36 @@ PyObject *same_params(PyObject *, PyObject *args) {
     Py_RETURN_FALSE;
 }
 
+/* grads_match(params, grads, bf16) -> bool
+ *
+ * True when every grads[i] can stand in for the gradient the launch tables
+ * were built with: a dense, contiguous tensor on params[i]'s device, of
+ * params[i]'s shape, float32 (bfloat16 when ``bf16``).  False for anything
+ * else, including objects that are not exactly torch tensors: the caller
+ * then checks them one by one (and raises the precise error). */
+PyObject *grads_match(PyObject *, PyObject *args) {
+    PyObject *params, *grads;
+    int bf16 = 0;
+    if (!PyArg_ParseTuple(args, "O!O!p", &PyList_Type, &params, &PyList_Type, &grads, &bf16)) return nullptr;
+    const Py_ssize_t n = PyList_GET_SIZE(params);
+    if (PyList_GET_SIZE(grads) != n) Py_RETURN_FALSE;
+    const c10::ScalarType want = bf16 ? c10::ScalarType::BFloat16 : c10::ScalarType::Float;
+    try {
+        for (Py_ssize_t i = 0; i < n; ++i) {
+            PyObject *p = PyList_GET_ITEM(params, i), *g = PyList_GET_ITEM(grads, i);
+            if (!THPVariable_CheckExact(p) || !THPVariable_CheckExact(g)) Py_RETURN_FALSE;
+            const at::Tensor &pt = THPVariable_Unpack(p), &gt = THPVariable_Unpack(g);
+            if (!gt.defined() || gt.is_sparse() || gt.scalar_type() != want || gt.device() != pt.device() ||
+                !gt.sizes().equals(pt.sizes()) || !gt.is_contiguous())
+                Py_RETURN_FALSE;
+        }
+    } catch (const std::exception &e) {
+        PyErr_SetString(PyExc_RuntimeError, e.what());
+        return nullptr;
+    }
+    Py_RETURN_TRUE;
+}
+
 PyMethodDef methods[] = {
     {"advance_if_same", advance_if_same, METH_VARARGS,
      "advance_if_same(params, grads, states[, param_ptrs]) -> bool: if params[i].grad is grads[i] for all i "
@@ -292,6 +322,9 @@ PyMethodDef methods[] = {
      "advance_steps(states) -> None: increment every states[j]['step']."},
     {"grads_of", grads_of, METH_VARARGS,
      "grads_of(params) -> (grads, absent): [p.grad for p in params] and a bytes of 1 where grad is None."},
+    {"grads_match", grads_match, METH_VARARGS,
+     "grads_match(params, grads, bf16) -> bool: every grad is a dense contiguous tensor of its param's "
+     "device and shape, float32 (bfloat16 when bf16)."},
     {"data_ptrs", data_ptrs, METH_VARARGS,
      "data_ptrs(tensors) -> bytes: each tensor's data_ptr() (0 for None) as native uint64."},
     {"bump_versions", bump_versions, METH_VARARGS,

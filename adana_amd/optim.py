@@ -93,6 +93,7 @@ class _LaunchSet:
         self.plan = None
         self.diag = None
         self.ptr_key = None         # the gradients' and parameters' data pointers the tables hold
+        self.rest_ok = None         # per row: the non-gradient pointers allow the vector path
 
 
 class _DanaFamily(Optimizer):
@@ -283,8 +284,12 @@ class _DanaFamily(Optimizer):
         return flags
 
     def _desc_rows(self, ls: _LaunchSet) -> np.ndarray:
+        """Descriptor rows of the launch set; also records in ``ls.rest_ok``
+        whether each row's pointers other than the gradient's are 16-byte
+        aligned (the vector path needs them and the gradient aligned)."""
         n = len(ls.params)
         d = np.zeros(n, dtype=_lib.DESC_DTYPE)
+        rest = np.zeros(n, dtype=bool)
         for j, (p, g, st) in enumerate(zip(ls.params, ls.grads, ls.states)):
             master = st.get("master")
             param_ptr = master.data_ptr() if master is not None else p.data_ptr()
@@ -293,11 +298,12 @@ class _DanaFamily(Optimizer):
             tau_ptr = st[kt].data_ptr() if self._STAR else 0
             gp = g.data_ptr()
             m_ptr, v_ptr = st[km].data_ptr(), st[kv].data_ptr()
-            ok = (param_ptr % 16 == 0 and m_ptr % 16 == 0 and v_ptr % 16 == 0
-                  and tau_ptr % 16 == 0 and gp % (8 if g.dtype == torch.bfloat16 else 16) == 0
-                  and lp_ptr % 8 == 0)
+            rest[j] = (param_ptr % 16 == 0 and m_ptr % 16 == 0 and v_ptr % 16 == 0
+                       and tau_ptr % 16 == 0 and lp_ptr % 8 == 0)
+            ok = rest[j] and gp % (8 if g.dtype == torch.bfloat16 else 16) == 0
             d[j] = (param_ptr, gp, m_ptr, v_ptr, tau_ptr, lp_ptr, p.numel(), ls.sclass[j],
                     _lib.DESC_VEC_OK if ok else 0)
+        ls.rest_ok = rest
         return d
 
     def _upload(self, ls: _LaunchSet) -> None:
@@ -581,10 +587,19 @@ class _DanaFamily(Optimizer):
         key = (_hoststep.data_ptrs(ls.grads), _hoststep.data_ptrs(ls.params))
         if key == ls.ptr_key:
             return
-        for p, g in zip(ls.params, ls.grads):
-            if self._validate(p, g) != ls.flags:
-                raise RuntimeError(f"{type(self).__name__}: gradient dtype changed")
-        ls.host_desc = self._desc_rows(ls)
+        bf16 = bool(ls.flags & _lib.GRAD_BF16)
+        if key[1] == ls.ptr_key[1] and _hoststep.grads_match(ls.params, ls.grads, bf16):
+            # only gradients moved, and each is a dense contiguous tensor of its
+            # parameter's shape and the set's dtype: re-point the grad column
+            g = np.frombuffer(key[0], dtype=np.uint64)
+            ls.host_desc["grad"] = g
+            ok = ls.rest_ok & (g % (8 if bf16 else 16) == 0)
+            ls.host_desc["flags"] = np.where(ok, _lib.DESC_VEC_OK, 0).astype(ls.host_desc["flags"].dtype)
+        else:
+            for p, g in zip(ls.params, ls.grads):
+                if self._validate(p, g) != ls.flags:
+                    raise RuntimeError(f"{type(self).__name__}: gradient dtype changed")
+            ls.host_desc = self._desc_rows(ls)
         ls.ptr_key = key
         with torch.cuda.device(ls.device):
             self._upload(ls)

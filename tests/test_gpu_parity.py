@@ -550,3 +550,40 @@ def test_parameter_storage_rebound_is_followed(oracle_mod, fresh_grads):
         pair.compare(where=f"k={k}")
         if k >= 3:
             assert torch.equal(old, snapshot)                      # the old storage is not written
+
+
+@pytest.mark.parametrize("star", [False, True])
+def test_new_gradient_buffers_every_step(oracle_mod, star):
+    """New gradient tensors at new addresses every step, alternating between
+    16-byte-aligned buffers and views 4 bytes into a flat buffer (so the
+    descriptors' vector-path flag flips each step): the re-pointed tables
+    give the oracle's results every step."""
+    print("case: new gradient buffers every step, star", star, flush=True)
+    rng = np.random.default_rng(43)
+    shapes = [(1000,), (64, 33), (5,), (4096 + 8,)]
+    params = [_normal(rng, s, 0.02) for s in shapes]
+    pair = Pair(oracle_mod, star, [(params, {})], lr=1e-3, delta=8.0, kappa=0.85,
+                clipsnr=2.0 if star else None, weight_decay=0.1)
+    total = sum(int(np.prod(s)) for s in shapes)
+    for k in range(8):
+        gl = [[_normal(rng, x.shape, 1e-3) for x in params]]
+        if k % 2:
+            flat = torch.empty(total + 1, device=DEV)
+            off = 1                                             # 4 bytes in: not 16-byte aligned
+            views = []
+            for g in gl[0]:
+                v = flat[off:off + g.size].view(g.shape)
+                v.copy_(torch.from_numpy(g))
+                views.append(v)
+                off += g.size
+        else:
+            views = [torch.from_numpy(g.copy()).to(DEV) for g in gl[0]]
+        for p, v in zip(pair.gpu_params[0], views):
+            p.grad = v
+        pair.prev = [[x.copy() for x in cp] for cp in pair.cpu_params]
+        pair.opt.step()
+        pair.oracle.step(gl)
+        torch.cuda.synchronize()
+        pair.compare(where=f"k={k}")
+        flags = pair.opt._sets[0].host_desc["flags"]
+        assert (flags != 0).all() == (k % 2 == 0), (k, flags)

@@ -417,3 +417,23 @@ def test_hoststep_grads_ptrs_and_steps():
     assert [s["step"] for s in states] == [3, 3]
     assert _hoststep.advance_if_same(ps, grads, states, _hoststep.data_ptrs(ps)) is True
     assert _hoststep.advance_if_same(ps, grads, states, b"short") is False
+
+
+def test_hoststep_grads_match():
+    """grads_match accepts dense contiguous gradients of each parameter's
+    shape and the expected dtype, and refuses anything else (the optimizer
+    then checks pair by pair and raises the precise error)."""
+    from adana_amd import _hoststep
+
+    ps = [torch.nn.Parameter(torch.zeros(4, 3)), torch.nn.Parameter(torch.zeros(5))]
+    good = [torch.zeros(4, 3), torch.zeros(5)]
+    assert _hoststep.grads_match(ps, good, False) is True
+    assert _hoststep.grads_match(ps, good, True) is False                       # dtype
+    assert _hoststep.grads_match(ps, [torch.zeros(3, 4), good[1]], False) is False   # shape
+    assert _hoststep.grads_match(ps, [torch.zeros(3, 4).t(), good[1]], False) is False  # not contiguous
+    assert _hoststep.grads_match(ps, [good[0], torch.zeros(5, dtype=torch.float64)], False) is False
+    assert _hoststep.grads_match(ps, [good[0], torch.zeros(5).to_sparse()], False) is False
+    assert _hoststep.grads_match(ps, [good[0], None], False) is False
+    assert _hoststep.grads_match(ps, good[:1], False) is False                   # length
+    b = [torch.nn.Parameter(torch.zeros(4, dtype=torch.bfloat16))]
+    assert _hoststep.grads_match(b, [torch.zeros(4, dtype=torch.bfloat16)], True) is True
