@@ -550,6 +550,36 @@ def main():
     achieved = algo_bytes / (kern_ms * 1e-3) / 1e9
     value = algo_bytes / (ms_per_step * 1e-3) / 1e9
 
+    host = None
+    if not w.get("clip"):
+        # Host time of opt.step() alone: with the same gradient tensors every step, and with a
+        # different gradient tensor, at a different address, for every parameter every step
+        # (the reference's loop runs zero_grad(set_to_none=True) before each backward, so
+        # its gradients are new tensors; the caching allocator may or may not reuse addresses).
+        cur = [p.grad for p in params]
+        alt = [g.clone() for g in cur]
+
+        def host_ms(fresh, k0):
+            t = []
+            for k in range(args.steps):
+                if fresh:
+                    for p, g in zip(params, alt if k % 2 == 0 else cur):
+                        p.grad = g
+                h0 = time.perf_counter()
+                one_step(k0 + k)
+                t.append((time.perf_counter() - h0) * 1e3)
+            torch.cuda.synchronize()
+            return round(float(np.median(t)), 4)
+
+        k0 = args.warmup + args.steps
+        host = {"same_grads": host_ms(False, k0), "new_grads_every_step": host_ms(True, k0 + args.steps),
+                "note": "median host time of opt.step() alone (launches are asynchronous); "
+                        "new_grads_every_step: every p.grad replaced by a tensor at another address "
+                        "before each step, outside the timed call"}
+        for p, g in zip(params, cur):
+            p.grad = g
+        del alt, cur
+
     cold = None
     if algo_bytes < MALL_BYTES:
         # the step's working set fits in the 256 MB MALL (Infinity Cache) and stays there between
@@ -560,7 +590,7 @@ def main():
             flush.fill_(float(k))
             e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
             e0.record(stream)
-            one_step(args.warmup + args.steps + k)
+            one_step(args.warmup + 3 * args.steps + k)
             e1.record(stream)
             torch.cuda.synchronize()
             cold_ms.append(e0.elapsed_time(e1))
@@ -588,6 +618,7 @@ def main():
                    "parallelism": "single GPU",
                    **({"grad_clip": w["clip"], "first_grad_norm": grad_norms[0]} if w.get("clip") else {})},
         "kernel_ms_per_step": round(kern_ms, 4),
+        **({"host_step_ms": host} if host else {}),
         **({"mall_cold": cold} if cold else {}),
         "kernel_ms_p90": round(float(np.percentile(dev_ms, 90)), 4),
         "params_per_s": round(n_elems / (ms_per_step * 1e-3), 1),
