@@ -14,7 +14,6 @@ Bars (stated per assertion):
   * diagnostics: rtol 1e-5 against the oracle's binary64 sums.
 """
 import math
-import os
 
 import numpy as np
 import pytest
