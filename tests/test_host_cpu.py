@@ -437,3 +437,18 @@ def test_hoststep_grads_match():
     assert _hoststep.grads_match(ps, good[:1], False) is False                   # length
     b = [torch.nn.Parameter(torch.zeros(4, dtype=torch.bfloat16))]
     assert _hoststep.grads_match(b, [torch.zeros(4, dtype=torch.bfloat16)], True) is True
+
+
+def test_missing_library_fails_loudly(monkeypatch):
+    """Without the built HIP library there is no step at all: loading it, and
+    constructing an optimizer, raise AdanaLibraryError naming the build
+    command (no CPU or eager fallback exists)."""
+    import adana_amd
+    from adana_amd import _lib
+
+    monkeypatch.setattr(_lib, "LIB_PATH", "/nonexistent/libadana_mta.so")
+    monkeypatch.setattr(_lib, "_lib", None)
+    with pytest.raises(_lib.AdanaLibraryError, match="is not built"):
+        _lib.lib()
+    with pytest.raises(_lib.AdanaLibraryError, match="no non-HIP path"):
+        adana_amd.DANA_STAR_MK4([torch.nn.Parameter(torch.zeros(3))], lr=1e-3)
