@@ -502,8 +502,10 @@ def main():
               f"(--gpus {args.gpus} requested); see DESIGN.md for how it shards", file=sys.stderr)
         return 2
 
+    import __graft_entry__
     import torch
 
+    __graft_entry__.ensure_built()      # a fresh checkout has no built libraries
     if args.workload == "copy_probe":
         return copy_probe(args.steps)
     if args.workload in ("tau_stats", "diag_readout"):

@@ -16,22 +16,12 @@ def pytest_configure(config):
     config.addinivalue_line("markers", "slow: long CPU test")
 
 
-def _built() -> bool:
-    import glob
-
-    return (os.path.exists(os.path.join(ROOT, "adana_amd", "libadana_mta.so"))
-            and bool(glob.glob(os.path.join(ROOT, "adana_amd", "_hoststep*.so")))
-            and os.path.exists(os.path.join(ROOT, "oracle", "liboracle.so"))
-            and os.path.exists(os.path.join(TESTS, "libadana_mathcheck.so")))
-
-
 def pytest_sessionstart(session):
     """A tree without the native libraries (built artefacts are not in git)
     builds them once first; a built tree is used as it is."""
-    if not _built():
-        import __graft_entry__
+    import __graft_entry__
 
-        __graft_entry__.build()
+    __graft_entry__.ensure_built()
 
 
 @pytest.fixture(scope="session")
