@@ -586,3 +586,43 @@ def test_new_gradient_buffers_every_step(oracle_mod, star):
         pair.compare(where=f"k={k}")
         flags = pair.opt._sets[0].host_desc["flags"]
         assert (flags != 0).all() == (k % 2 == 0), (k, flags)
+
+
+@pytest.mark.parametrize("star", [False, True])
+def test_closure_and_group_added_mid_run(oracle_mod, star):
+    """step(closure): the closure runs with gradients enabled, its loss is
+    returned, and the gradients it leaves are the ones stepped
+    (src/optim/adana.py:155-160).  add_param_group after 3 steps: the new
+    group joins with fresh state and both groups match the oracle."""
+    O = oracle_mod
+    print("case: closure and add_param_group, star", star, flush=True)
+    rng = np.random.default_rng(47)
+    a = [_normal(rng, (300,), 0.02), _normal(rng, (17, 9), 0.02)]
+    pair = Pair(O, star, [(a, {"weight_decay": 0.1})], lr=1e-3, delta=8.0, kappa=0.85,
+                clipsnr=2.0 if star else None, weight_decay=0.1)
+    for k in range(6):
+        if k == 3:
+            b = [_normal(rng, (1000,), 0.02), _normal(rng, (5,), 0.02)]
+            tb = [torch.nn.Parameter(torch.from_numpy(x.copy()).to(DEV)) for x in b]
+            pair.opt.add_param_group({"params": tb, "weight_decay": 0.0})
+            cb = [x.copy() for x in b]
+            pair.gpu_params.append(tb)
+            pair.cpu_params.append(cb)
+            pair.oracle.groups.append(O.OracleGroup(params=cb, lr=1e-3, weight_decay=0.0))
+        gl = [[_normal(rng, x.shape, 1e-3) for x in cp] for cp in pair.cpu_params]
+        seen = {}
+
+        def closure():
+            seen["grad_enabled"] = torch.is_grad_enabled()
+            for tp, gs in zip(pair.gpu_params, gl):
+                for p, g in zip(tp, gs):
+                    p.grad = torch.from_numpy(g.copy()).to(DEV)
+            return torch.tensor(float(k) + 0.5)
+
+        pair.prev = [[x.copy() for x in cp] for cp in pair.cpu_params]
+        loss = pair.opt.step(closure)
+        pair.oracle.step(gl)
+        torch.cuda.synchronize()
+        assert seen["grad_enabled"] and float(loss) == k + 0.5
+        pair.compare(where=f"k={k}")
+    assert [g["weighted_step_count"] for g in pair.opt.param_groups] == [6.0, 3.0]
