@@ -13,6 +13,9 @@
 // store are part of the pattern: without them the same stream measured about
 // 5% slower on MI355X.)
 //
+// A second kernel does the same for the bf16-master ADana step (fp32 master,
+// m, v and bf16 gradient in; fp32 master, m, v and bf16 parameter out).
+//
 // Not part of the optimizer's interface: built as a separate library
 // (libadana_probe.so) and loaded only by bench.py.
 #include <hip/hip_runtime.h>
@@ -82,6 +85,37 @@ __global__ __launch_bounds__(kThreads) void stream_5r4w_kernel(float *a0, float 
     chunk_partial(s, partials);
 }
 
+// The bf16-master ADana step's pattern (config C4): fp32 master, m, v and the
+// bf16 gradient read; fp32 master, m, v written back in place and the bf16
+// parameter written, with the step's policies (8-byte non-temporal loads and
+// stores for the bf16 arrays, as the step's vector path) and end of chunk.
+typedef unsigned int U2 __attribute__((ext_vector_type(2)));
+typedef __attribute__((address_space(1))) U2 GU2;
+
+__global__ __launch_bounds__(kThreads) void stream_master_kernel(float *master, const unsigned short *g, float *m,
+                                                                float *v, unsigned short *p16, float4 *partials) {
+    const int64_t lo = static_cast<int64_t>(blockIdx.x) * kChunk;
+    const int64_t i = lo + 4 * threadIdx.x;
+    const F4 a = __builtin_nontemporal_load((const GF4 *)(master + i));
+    const F4 b = __builtin_nontemporal_load((const GF4 *)(m + i));
+    const F4 c = __builtin_nontemporal_load((const GF4 *)(v + i));
+    const U2 h = __builtin_nontemporal_load((const GU2 *)(g + i));
+    F4 s = a + b + c;
+    s.x += __uint_as_float(h.x << 16);
+    s.y += __uint_as_float(h.y << 16);
+    store_stream(master + lo, 16 * threadIdx.x, s);
+    F4 o = s;
+    o.x += 1.0f;
+    store_stream(m + lo, 16 * threadIdx.x, o);
+    o.x += 1.0f;
+    store_stream(v + lo, 16 * threadIdx.x, o);
+    U2 q;
+    q.x = __float_as_uint(s.z) >> 16;
+    q.y = __float_as_uint(s.w) >> 16;
+    __builtin_nontemporal_store(q, (GU2 *)(p16 + i));
+    chunk_partial(s, partials);
+}
+
 // STREAM copy in the same style: dst[i] = src[i], with the same end of chunk
 __global__ __launch_bounds__(kThreads) void stream_copy_kernel(float *dst, const float *src, float4 *partials) {
     const int64_t lo = static_cast<int64_t>(blockIdx.x) * kChunk;
@@ -120,6 +154,25 @@ extern "C" int adana_probe_stream_5r4w(float *const *arrays, int64_t n, float4 *
     hipLaunchKernelGGL(stream_5r4w_kernel, dim3(static_cast<unsigned>(n / kChunk)), dim3(kThreads),
                        static_cast<unsigned>(lds), stream, arrays[0], arrays[1], arrays[2], arrays[3], arrays[4],
                        partials);
+    return static_cast<int>(hipGetLastError());
+}
+
+// The bf16-master pattern over n elements: master, m, v fp32 (16-byte aligned),
+// g and p16 bfloat16 (8-byte aligned), all distinct, n a positive multiple of
+// 1024; `partials` room for n / 1024 float4.
+extern "C" int adana_probe_stream_master(float *master, const void *g, float *m, float *v, void *p16, int64_t n,
+                                         float4 *partials, int wgs_per_cu, hipStream_t stream) {
+    if (!master || !g || !m || !v || !p16 || !partials || n <= 0 || n % kChunk != 0 || n / kChunk > 0x7fffffff ||
+        wgs_per_cu < 0)
+        return -1;
+    for (const void *q : {static_cast<const void *>(master), static_cast<const void *>(m), static_cast<const void *>(v)})
+        if (reinterpret_cast<uintptr_t>(q) % 16 != 0) return -1;
+    if (reinterpret_cast<uintptr_t>(g) % 8 != 0 || reinterpret_cast<uintptr_t>(p16) % 8 != 0) return -1;
+    const int64_t lds = cap_lds(wgs_per_cu);
+    if (lds < 0) return -1;
+    hipLaunchKernelGGL(stream_master_kernel, dim3(static_cast<unsigned>(n / kChunk)), dim3(kThreads),
+                       static_cast<unsigned>(lds), stream, master, static_cast<const unsigned short *>(g), m, v,
+                       static_cast<unsigned short *>(p16), partials);
     return static_cast<int>(hipGetLastError());
 }
 

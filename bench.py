@@ -239,6 +239,55 @@ def copy_probe(steps):
     return 0
 
 
+def master_ceiling(n_elems, reps=5):
+    """The HBM rate of the bf16-master ADana step's access pattern without its
+    arithmetic (stream_probe.hip's stream_master_kernel: fp32 master, m, v and
+    bf16 gradient read; fp32 master, m, v and bf16 parameter written; 28 bytes
+    per element), the better of 4 and 5 resident workgroups per CU."""
+    import ctypes
+
+    import torch
+
+    lib = ctypes.CDLL(os.path.join(ROOT, "adana_amd", "libadana_probe.so"))
+    fn = lib.adana_probe_stream_master
+    fn.argtypes = [ctypes.c_void_p] * 5 + [ctypes.c_int64, ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p]
+    fn.restype = ctypes.c_int
+    n = n_elems // 1024 * 1024
+    f32 = [torch.zeros(n, device="cuda:0") for _ in range(3)]
+    b16 = [torch.zeros(n, dtype=torch.bfloat16, device="cuda:0") for _ in range(2)]
+    partials = torch.empty(n // 1024 * 4, device="cuda:0")
+    stream = torch.cuda.current_stream()
+    best = None
+    for cap in (4, 5):
+        def run():
+            rc = fn(ctypes.c_void_p(f32[0].data_ptr()), ctypes.c_void_p(b16[0].data_ptr()),
+                    ctypes.c_void_p(f32[1].data_ptr()), ctypes.c_void_p(f32[2].data_ptr()),
+                    ctypes.c_void_p(b16[1].data_ptr()), n, ctypes.c_void_p(partials.data_ptr()), cap,
+                    ctypes.c_void_p(stream.cuda_stream))
+            if rc != 0:
+                raise RuntimeError(f"adana_probe_stream_master failed ({rc})")
+        run()
+        torch.cuda.synchronize()
+        ev = [torch.cuda.Event(enable_timing=True) for _ in range(reps + 1)]
+        for k in range(reps):
+            ev[k].record(stream)
+            run()
+        ev[-1].record(stream)
+        torch.cuda.synchronize()
+        ms = float(np.median([ev[k].elapsed_time(ev[k + 1]) for k in range(reps)]))
+        gbs = 28 * n / (ms * 1e-3) / 1e9
+        if best is None or gbs > best[0]:
+            best = (gbs, cap, ms)
+    del f32, b16, partials
+    torch.cuda.empty_cache()
+    return {"achieved": round(best[0], 2), "frac": round(best[0] / HBM_PEAK_GBS, 4), "wgs_per_cu": best[1],
+            "ms": round(best[2], 4),
+            "probe": f"fp32 master, m, v and bf16 gradient of {n} elements read, master, m, v written back "
+                     f"in place and the bf16 parameter written, one 16-byte partial per 1024-element chunk: "
+                     f"the bf16-master step's access pattern without its arithmetic (stream_probe.hip), "
+                     f"median of {reps} launches"}
+
+
 def stream_ceiling(n_elems, reps=5):
     """The HBM rate of the Dana-Star step's access pattern without its
     arithmetic: 5 fp32 arrays read and 4 written back in place, with the step
@@ -642,6 +691,11 @@ def main():
         result["roofline"]["frac_of_mix_ceiling"] = round(achieved / ceiling["achieved"], 4)
         result["roofline"]["stream_copy"] = copy
         result["roofline"]["frac_of_stream_copy"] = round(achieved / copy["achieved"], 4)
+    if bpe == 28 and w["master"] and not w.get("clip") and not args.no_ceiling_probe:
+        print("[bench] timing the bf16-master stream probe", file=sys.stderr, flush=True)
+        ceiling = master_ceiling(n_elems)
+        result["roofline"]["mix_ceiling"] = ceiling
+        result["roofline"]["frac_of_mix_ceiling"] = round(achieved / ceiling["achieved"], 4)
     if not args.no_cpu_baseline:
         print("[bench] timing the CPU oracle baseline", file=sys.stderr, flush=True)
         result["cpu_baseline"] = cpu_baseline(w, target_s=args.cpu_seconds)

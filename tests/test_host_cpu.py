@@ -356,6 +356,16 @@ def test_stream_probe_library_rejects_bad_arguments():
     assert cp(0x1000, 0x2000, 1000, part, 0, None) == -1  # not a multiple of 1024
     assert cp(0, 0x2000, 1024, part, 0, None) == -1       # null
     assert cp(0x1000, 0x2000, 1024, None, 0, None) == -1  # no partials
+    ms = lib.adana_probe_stream_master
+    ms.argtypes = [ctypes.c_void_p] * 5 + [ctypes.c_int64, ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p]
+    ms.restype = ctypes.c_int
+    a, g, mm, v, p16 = 0x1000, 0x2000, 0x3000, 0x4000, 0x5000
+    assert ms(a, g, mm, v, p16, 1000, part, 4, None) == -1     # not a multiple of 1024
+    assert ms(a, None, mm, v, p16, 1024, part, 4, None) == -1   # null gradient
+    assert ms(a + 8, g, mm, v, p16, 1024, part, 4, None) == -1  # fp32 array not 16-byte aligned
+    assert ms(a, g + 4, mm, v, p16, 1024, part, 4, None) == -1  # bf16 array not 8-byte aligned
+    assert ms(a, g, mm, v, p16, 1024, None, 4, None) == -1      # no partials
+    assert ms(a, g, mm, v, p16, 1024, part, -1, None) == -1     # negative cap
 
 
 def test_flat_params_follow_the_groups():
