@@ -67,17 +67,20 @@ __device__ __forceinline__ void chunk_partial(F4 s, float4 *partials) {
     }
 }
 
-// arrays a[0..4] are read; a[0..3] are written back (in place)
-__global__ __launch_bounds__(kThreads) void stream_5r4w_kernel(float *a0, float *a1, float *a2, float *a3,
-                                                              float *a4, float4 *partials) {
+// arrays a[0..R-1] are read; a[0..W-1] are written back (in place).
+// R = 5, W = 4: the Dana-Star step (p, g, m, v, tau in; p, m, v, tau out);
+// R = 4, W = 3: the fp32 ADana step (p, g, m, v in; p, m, v out).
+template <int R, int W>
+__global__ __launch_bounds__(kThreads) void stream_rw_kernel(float *a0, float *a1, float *a2, float *a3,
+                                                            float *a4, float4 *partials) {
     float *const a[5] = {a0, a1, a2, a3, a4};
     const int64_t lo = static_cast<int64_t>(blockIdx.x) * kChunk;
     const int64_t i = lo + 4 * threadIdx.x;
     F4 s = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-    for (int k = 0; k < 5; ++k) s += __builtin_nontemporal_load((const GF4 *)(a[k] + i));
+    for (int k = 0; k < R; ++k) s += __builtin_nontemporal_load((const GF4 *)(a[k] + i));
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {
+    for (int k = 0; k < W; ++k) {
         F4 o = s;
         o.x += static_cast<float>(k);
         store_stream(a[k] + lo, 16 * threadIdx.x, o);
@@ -137,6 +140,19 @@ int64_t cap_lds(int wgs) {
     return (l > 0 && l <= per_block) ? l : -1;
 }
 
+template <int R, int W>
+int launch_rw(float *const *arrays, int64_t n, float4 *partials, int wgs_per_cu, hipStream_t stream) {
+    if (!arrays || !partials || n <= 0 || n % kChunk != 0 || n / kChunk > 0x7fffffff || wgs_per_cu < 0)
+        return -1;
+    for (int k = 0; k < R; ++k)
+        if (!arrays[k] || reinterpret_cast<uintptr_t>(arrays[k]) % 16 != 0) return -1;
+    const int64_t lds = cap_lds(wgs_per_cu);
+    if (lds < 0) return -1;
+    hipLaunchKernelGGL((stream_rw_kernel<R, W>), dim3(static_cast<unsigned>(n / kChunk)), dim3(kThreads),
+                       static_cast<unsigned>(lds), stream, arrays[0], arrays[1], arrays[2], arrays[3],
+                       R > 4 ? arrays[4] : nullptr, partials);
+    return static_cast<int>(hipGetLastError());
+}
 }  // namespace
 
 // One launch over n elements of each array (n a positive multiple of 1024;
@@ -145,16 +161,14 @@ int64_t cap_lds(int wgs) {
 // cap).  Returns 0 or a HIP error code; -1 for bad arguments.
 extern "C" int adana_probe_stream_5r4w(float *const *arrays, int64_t n, float4 *partials, int wgs_per_cu,
                                        hipStream_t stream) {
-    if (!arrays || !partials || n <= 0 || n % kChunk != 0 || n / kChunk > 0x7fffffff || wgs_per_cu < 0)
-        return -1;
-    for (int k = 0; k < 5; ++k)
-        if (!arrays[k] || reinterpret_cast<uintptr_t>(arrays[k]) % 16 != 0) return -1;
-    const int64_t lds = cap_lds(wgs_per_cu);
-    if (lds < 0) return -1;
-    hipLaunchKernelGGL(stream_5r4w_kernel, dim3(static_cast<unsigned>(n / kChunk)), dim3(kThreads),
-                       static_cast<unsigned>(lds), stream, arrays[0], arrays[1], arrays[2], arrays[3], arrays[4],
-                       partials);
-    return static_cast<int>(hipGetLastError());
+    return launch_rw<5, 4>(arrays, n, partials, wgs_per_cu, stream);
+}
+
+// The fp32 ADana pattern: arrays[0..3] read, arrays[0..2] written back (same
+// conditions as above for those 4 arrays).
+extern "C" int adana_probe_stream_4r3w(float *const *arrays, int64_t n, float4 *partials, int wgs_per_cu,
+                                       hipStream_t stream) {
+    return launch_rw<4, 3>(arrays, n, partials, wgs_per_cu, stream);
 }
 
 // The bf16-master pattern over n elements: master, m, v fp32 (16-byte aligned),

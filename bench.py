@@ -288,9 +288,10 @@ def master_ceiling(n_elems, reps=5):
                      f"median of {reps} launches"}
 
 
-def stream_ceiling(n_elems, reps=5):
-    """The HBM rate of the Dana-Star step's access pattern without its
-    arithmetic: 5 fp32 arrays read and 4 written back in place, with the step
+def stream_ceiling(n_elems, reps=5, star=True):
+    """The HBM rate of the step's access pattern without its arithmetic:
+    5 fp32 arrays read and 4 written back in place (Dana-Star: p, g, m, v,
+    tau), or 4 read and 3 written back (fp32 ADana: p, g, m, v), with the step
     kernel's tiles, load/store policies and residency cap
     (adana_amd/csrc/stream_probe.hip), at the workload's element count; the
     better of 3 and 4 resident workgroups per CU.  Also a STREAM copy of the
@@ -300,9 +301,11 @@ def stream_ceiling(n_elems, reps=5):
     import torch
 
     lib = ctypes.CDLL(os.path.join(ROOT, "adana_amd", "libadana_probe.so"))
-    fn = lib.adana_probe_stream_5r4w
+    fn = lib.adana_probe_stream_5r4w if star else lib.adana_probe_stream_4r3w
     fn.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p]
     fn.restype = ctypes.c_int
+    n_read, n_write = (5, 4) if star else (4, 3)
+    bpe = 4 * (n_read + n_write)
     n = n_elems // 1024 * 1024
     arrays = [torch.zeros(n, device="cuda:0") for _ in range(5)]
     partials = torch.empty(n // 1024 * 4, device="cuda:0")
@@ -323,13 +326,13 @@ def stream_ceiling(n_elems, reps=5):
         ev[-1].record(stream)
         torch.cuda.synchronize()
         ms = float(np.median([ev[k].elapsed_time(ev[k + 1]) for k in range(reps)]))
-        gbs = 36 * n / (ms * 1e-3) / 1e9
+        gbs = bpe * n / (ms * 1e-3) / 1e9
         if best is None or gbs > best[0]:
             best = (gbs, cap, ms)
     mix = {"achieved": round(best[0], 2), "frac": round(best[0] / HBM_PEAK_GBS, 4), "wgs_per_cu": best[1],
            "ms": round(best[2], 4),
-           "probe": f"5 fp32 arrays of {n} elements read, 4 written back in place, one 16-byte partial "
-                    f"per 1024-element chunk: the step kernel's access pattern without its arithmetic "
+           "probe": f"{n_read} fp32 arrays of {n} elements read, {n_write} written back in place, one 16-byte "
+                    f"partial per 1024-element chunk: the step kernel's access pattern without its arithmetic "
                     f"(stream_probe.hip), median of {reps} launches"}
     # STREAM copy (arrays[1] -> arrays[0]) in the same style, the better of uncapped and 6 per CU
     cp = lib.adana_probe_copy
@@ -683,10 +686,10 @@ def main():
     }
     del opt, params
     torch.cuda.empty_cache()
-    if bpe == 36 and not w["master"] and not args.no_ceiling_probe:
+    if bpe in (28, 36) and not w["master"] and not args.no_ceiling_probe:
         # the same access pattern without the arithmetic: what the memory system allows this mix
-        print("[bench] timing the 5-read/4-write stream probe", file=sys.stderr, flush=True)
-        ceiling, copy = stream_ceiling(n_elems)
+        print("[bench] timing the stream probe of the step's access pattern", file=sys.stderr, flush=True)
+        ceiling, copy = stream_ceiling(n_elems, star=bpe == 36)
         result["roofline"]["mix_ceiling"] = ceiling
         result["roofline"]["frac_of_mix_ceiling"] = round(achieved / ceiling["achieved"], 4)
         result["roofline"]["stream_copy"] = copy

@@ -348,6 +348,12 @@ def test_stream_probe_library_rejects_bad_arguments():
     assert fn(holes, 1024, part, 4, None) == -1           # null array
     odd = (ctypes.c_void_p * 5)(0x1000, 0x1004, 0x1000, 0x1000, 0x1000)
     assert fn(odd, 1024, part, 4, None) == -1             # misaligned array
+    f4 = lib.adana_probe_stream_4r3w
+    f4.argtypes = fn.argtypes
+    f4.restype = ctypes.c_int
+    assert f4(odd, 1024, part, 4, None) == -1             # misaligned array
+    assert f4(five, 1000, part, 4, None) == -1            # not a multiple of 1024
+    assert f4(None, 1024, part, 4, None) == -1            # no array table
     cp = lib.adana_probe_copy
     cp.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p, ctypes.c_int,
                    ctypes.c_void_p]
