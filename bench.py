@@ -551,7 +551,8 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build's step is single-GPU "
-              f"(--gpus {args.gpus} requested); see DESIGN.md for how it shards", file=sys.stderr)
+              f"(--gpus {args.gpus} requested); the update is element-wise, so each rank would run it on "
+              f"its own shard", file=sys.stderr)
         return 2
 
     import __graft_entry__

@@ -1,5 +1,5 @@
-"""The C ABI driven directly, as a non-Python caller (or INTEGRATION.md's
-ctypes example) would: plan layout, device table, chunk index, workspace,
+"""The C ABI driven directly, as a non-Python caller (or a plain ctypes
+binding) would: plan layout, device table, chunk index, workspace,
 one adana_mta_step per step -- against the oracle, bit-exact for m, v and
 tau and under the Dana-Star pow bar for p; diagnostics rtol 1e-5."""
 import ctypes
