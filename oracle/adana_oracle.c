@@ -41,39 +41,8 @@
 #include <stdint.h>
 #include <string.h>
 
-typedef struct {
-    float a;        /* alpha = fp32(delta / (delta + t)), double divide      */
-    float oma;      /* fp32(1 - a)                                           */
-    float s;        /* fp32(t)                                               */
-    float eps;      /* fp32(epsilon)                                         */
-    float pw;       /* ADana: fp32((1 + s) ** (1 - kappa)), binary64 pow     */
-    float min_p;    /* Star: fp32(1 / (1 + s))                               */
-    float clip;     /* fp32(clipsnr)                                         */
-    int32_t has_clip;
-    float c3;       /* fp32(-lr) * fp32(gamma_3_factor)                      */
-    float cg2;      /* fp32(-lr)                                             */
-    float opw;      /* fp32(1 + wd_factor)                                   */
-    float star_exp; /* fp32(1 - kappa): exponent of the per-element pow      */
-    int32_t pow_mode; /* ATen's pow(Tensor, Scalar) specialisation, below     */
-} adana_oracle_scalars;
+#include "adana_oracle.h"
 
-/* Manau's Dana-Star-MK4 branch (src/optim/manau.py:556-613): its scalars
- * are the branch's Python floats rounded to binary32 where they meet float32
- * tensors (tensor-scalar operands, full_like). */
-typedef struct {
-    float a;        /* fp32(alpha)                                        */
-    float oma;      /* fp32(1 - alpha), binary64 difference               */
-    float s;        /* fp32(step)                                         */
-    float eps;      /* fp32(epsilon)                                      */
-    float min_p;    /* fp32(1 / (1 + step)), binary64 quotient            */
-    float clip;     /* fp32(clipsnr)                                      */
-    float lr;       /* fp32(lr)                                           */
-    float wdf;      /* fp32(1 - wd/(1+step/wd_ts)*lr) or fp32(1 - wd*lr)  */
-    float e[3];     /* fp32 exponents: 1-kappa, 2 mk4B + 1, 2 (-mk4A - mk4B) */
-    int32_t mode[3];/* their ATen specialisations                         */
-    int32_t has_wd; /* weight_decay != 0                                  */
-    int32_t reserved;
-} adana_oracle_manau_scalars;
 
 /* pow(Tensor, Scalar) specialisations in ATen, chosen on the binary64
  * exponent: 0 -> ones, 0.5 -> sqrt, -0.5 -> 1/sqrt, -1 -> 1/x, 2 -> x*x,

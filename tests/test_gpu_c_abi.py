@@ -3,6 +3,7 @@ binding) would: plan layout, device table, chunk index, workspace,
 one adana_mta_step per step -- against the oracle, bit-exact for m, v and
 tau and under the Dana-Star pow bar for p; diagnostics rtol 1e-5."""
 import ctypes
+import os
 
 import numpy as np
 import pytest
@@ -75,3 +76,19 @@ def test_integration_example_through_the_c_abi(oracle_mod):
             cpu["p"][i][...] = p[i].cpu().numpy()
             ref = O.finalize_diag(sums[i], sizes[i])
             np.testing.assert_allclose(d[i], [ref[k] for k in O.DIAG_KEYS], rtol=1e-5, atol=1e-30, equal_nan=True)
+
+
+def test_cpp_host_drives_the_c_abi():
+    """tests/c_abi_driver (C++, built by tests/Makefile): its own HIP
+    allocations, adana_plan_layout / adana_plan_index / adana_workspace_bytes,
+    then adana_mta_step for 6 Dana-Star-MK4 steps over 5 tensors, each step
+    checked against the C oracle (m, v, tau bit-exact, p under the pow bar,
+    diagnostics 1e-5).  Runs as a child process, with no Python in the step."""
+    import subprocess
+
+    exe = os.path.join(os.path.dirname(os.path.abspath(__file__)), "c_abi_driver")
+    print("case: C++ host program over the C ABI", flush=True)
+    r = subprocess.run([exe], capture_output=True, text=True, timeout=120)
+    print(r.stdout[-2000:], flush=True)
+    assert r.returncode == 0, r.stdout[-2000:] + r.stderr[-2000:]
+    assert r.stdout.strip().splitlines()[-1] == "c_abi_driver: ok"
