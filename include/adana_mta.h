@@ -48,7 +48,8 @@
  * Ownership: the library allocates nothing; every device buffer is owned by
  * the caller (PyTorch's caching allocator in the Python binding) and only
  * borrowed for the call.  Launches are asynchronous on the caller's HIP
- * stream; nothing synchronises the host.  Errors: functions return 0 on
+ * stream; nothing synchronises the host, except adana_order_stats (host-driven
+ * between its passes).  Errors: functions return 0 on
  * success or a negative code; adana_last_error() returns the message of the
  * calling thread's last failure.
  */
