@@ -5,7 +5,11 @@ workloads' own lists and hyper-parameters (bench.workload):
     embedding gradients;
   * c4: ADana on the same list with bf16 parameters, fp32 master/m/v and
     bf16 gradients;
-  * c3: Dana-Star-MK4, 1,311,082,496 parameters (d_model 2048, 24 layers).
+  * c3: Dana-Star-MK4, 1,311,082,496 parameters (d_model 2048, 24 layers);
+  * c2: Dana-MK4, 50,938,880 parameters in 67 tensors, 1-D gradients x 0.1;
+  * c5: Dana-Star-MK4 over 10,000 log-uniform tensors (94,406,322
+    parameters), 5% of them with all-zero gradients (64 sampled elements per
+    tensor).
 Two weight-decay groups as src/models/base.py:503-561; launcher
 hyper-parameters as scripts/launch.sh:36-40,188-223.
 
@@ -40,10 +44,11 @@ pytestmark = [pytest.mark.gpu,
 DEV = "cuda:0"
 SAMPLES = 1024          # per tensor, plus its first and last element
 STEPS = 3
-ELEMENTS = {"north_star": 2_645_527_040, "c4": 2_645_527_040, "c3": 1_311_082_496}
+ELEMENTS = {"north_star": 2_645_527_040, "c4": 2_645_527_040, "c3": 1_311_082_496, "c2": 50_938_880,
+            "c5": 94_406_322}
 
 
-@pytest.mark.parametrize("name", ["north_star", "c4", "c3"])
+@pytest.mark.parametrize("name", ["north_star", "c4", "c3", "c2", "c5"])
 def test_full_size_sampled_parity(oracle_mod, name):
     import adana_amd
     from bench import workload
@@ -68,12 +73,14 @@ def test_full_size_sampled_parity(oracle_mod, name):
     cls = adana_amd.DANA_STAR_MK4 if star else adana_amd.ADana
     opt = cls(groups, master_weights=master, **hp)
     sparse_emb = name in ("north_star", "c3")
+    zero = np.random.default_rng(1).random(len(params)) < 0.05
     emb = len(w["groups"][0])                            # the tied embedding opens the no-decay group
     rng = np.random.default_rng(7)
     idx = []
     for p in params:
         n = p.numel()
-        pick = np.unique(np.concatenate([[0, n - 1], rng.integers(0, n, size=min(n, SAMPLES))]))
+        per = SAMPLES if len(params) < 1000 else 64              # C5: 10,000 tensors
+        pick = np.unique(np.concatenate([[0, n - 1], rng.integers(0, n, size=min(n, per))]))
         idx.append(torch.from_numpy(pick).to(DEV))
 
     def gather(ts):
@@ -85,8 +92,12 @@ def test_full_size_sampled_parity(oracle_mod, name):
     host_tau = [np.zeros_like(x) for x in host_p] if star else [None] * len(params)
     for t in range(1, STEPS + 1):
         gen.manual_seed(1000 + t)
-        for p in params:
+        for i, p in enumerate(params):
             p.grad = torch.empty(p.shape, device=DEV).normal_(0, 1e-3, generator=gen).to(pdtype)
+            if name == "c2" and p.dim() == 1:
+                p.grad.mul_(0.1)                         # the bench's C2: 1-D gradients x 0.1
+            if name == "c5" and zero[i]:
+                p.grad.zero_()                           # the bench's C5: 5% all-zero gradients
         if sparse_emb:
             rows = (torch.rand((params[emb].shape[0], 1), device=DEV, generator=gen) < 0.1).to(pdtype)
             params[emb].grad.mul_(rows)                  # row-sparse embedding gradient
