@@ -438,6 +438,49 @@ def consumer_bench(args):
     return 0
 
 
+def manau_model(seed=0, grad_seed=None):
+    """The north-star model's parameter list as Manau takes it (named groups:
+    the 2-D Linear weights with weight decay 0.1; the tied embedding and the
+    LayerNorm weights without), on cuda:0, with N(0, 1e-3) gradients
+    (embedding rows nonzero w.p. 0.1), and Manau's hyper-parameters."""
+    import torch
+
+    d, layers, vocab = 2560, 32, 50304
+    dev = torch.device("cuda:0")
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(seed)
+    decay, nodecay = [], [("transformer.wte.weight", (vocab, d))]
+    for l in range(layers):
+        decay += [(f"transformer.h.{l}.attn.c_attn.weight", (3 * d, d)),
+                  (f"transformer.h.{l}.attn.c_proj.weight", (d, d)),
+                  (f"transformer.h.{l}.mlp.c_fc.weight", (4 * d, d)),
+                  (f"transformer.h.{l}.mlp.c_proj.weight", (d, 4 * d))]
+        nodecay += [(f"transformer.h.{l}.ln_1.weight", (d,)), (f"transformer.h.{l}.ln_2.weight", (d,))]
+    nodecay += [("transformer.ln_f.weight", (d,))]
+    groups, params = [], []
+    for named, wd in ((decay, 0.1), (nodecay, 0.0)):
+        ps = [torch.nn.Parameter(torch.empty(s, device=dev).normal_(0, 0.02, generator=gen)) for _, s in named]
+        groups.append({"params": ps, "param_names": [n for n, _ in named], "weight_decay": wd})
+        params += ps
+    manau_grads(params, groups[1]["params"][0], gen if grad_seed is None else grad_seed)
+    hp = dict(lr=2e-2, kappa=0.85, clipsnr=2.0, delta=8.0, wd_decaying=True, wd_ts=10.0)
+    return groups, params, hp
+
+
+def manau_grads(params, emb, gen):
+    """N(0, 1e-3) gradients for every parameter, the embedding's rows nonzero
+    with probability 0.1 (``gen``: a cuda generator or an integer seed)."""
+    import torch
+
+    if isinstance(gen, int):
+        seed, gen = gen, torch.Generator(device="cuda:0")
+        gen.manual_seed(seed)
+    for p in params:
+        p.grad = torch.empty_like(p).normal_(0, 1e-3, generator=gen)
+    rows = (torch.rand((emb.shape[0], 1), device=emb.device, generator=gen) < 0.1).float()
+    emb.grad.mul_(rows)                                          # row-sparse embedding gradient
+
+
 def manau_bench(args):
     """Manau (src/optim/manau.py) on the north-star model: Muon for the 2-D
     Linear weights, the HIP Dana-Star-MK4 branch for the tied embedding and
@@ -451,26 +494,7 @@ def manau_bench(args):
 
     import adana_amd
 
-    d, layers, vocab = 2560, 32, 50304
-    dev = torch.device("cuda:0")
-    gen = torch.Generator(device=dev)
-    gen.manual_seed(0)
-    decay, nodecay = [], [("transformer.wte.weight", (vocab, d))]
-    for l in range(layers):
-        decay += [(f"transformer.h.{l}.attn.c_attn.weight", (3 * d, d)), (f"transformer.h.{l}.attn.c_proj.weight", (d, d)),
-                  (f"transformer.h.{l}.mlp.c_fc.weight", (4 * d, d)), (f"transformer.h.{l}.mlp.c_proj.weight", (d, 4 * d))]
-        nodecay += [(f"transformer.h.{l}.ln_1.weight", (d,)), (f"transformer.h.{l}.ln_2.weight", (d,))]
-    nodecay += [("transformer.ln_f.weight", (d,))]
-    groups, params = [], []
-    for named, wd in ((decay, 0.1), (nodecay, 0.0)):
-        ps = [torch.nn.Parameter(torch.empty(s, device=dev).normal_(0, 0.02, generator=gen)) for _, s in named]
-        groups.append({"params": ps, "param_names": [n for n, _ in named], "weight_decay": wd})
-        params += ps
-    for p in params:
-        p.grad = torch.empty_like(p).normal_(0, 1e-3, generator=gen)
-    rows = (torch.rand((vocab, 1), device=dev, generator=gen) < 0.1).float()
-    groups[1]["params"][0].grad.mul_(rows)                      # row-sparse embedding gradient
-    hp = dict(lr=2e-2, kappa=0.85, clipsnr=2.0, delta=8.0, wd_decaying=True, wd_ts=10.0)
+    groups, params, hp = manau_model()
     with contextlib.redirect_stdout(io.StringIO()):
         opt = adana_amd.Manau(groups, **hp)
     dana = [p for p in params if not opt.state[p]["use_muon"]]

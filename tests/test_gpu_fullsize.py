@@ -237,3 +237,80 @@ def test_clip_single_tensor_beyond_2_31_elements(oracle_mod):
     assert np.array_equal(got.view(np.uint32), O.clip_scale(g0, coef).view(np.uint32))
     del p
     torch.cuda.empty_cache()
+
+
+def test_manau_dana_branch_full_size(oracle_mod):
+    """Manau on the north-star model (bench.manau_model: 2,516,582,400 Muon and
+    128,944,640 Dana-Star-MK4 parameters), 2 steps with new gradients each:
+    the Dana branch's sampled m, v, tau bit-exact against the oracle's Manau
+    restatement replayed on the same elements, p under the pow bar, and
+    gradient_norm / m_norm of every branch tensor against binary64
+    reductions of the whole tensor."""
+    import contextlib
+    import io
+
+    import adana_amd
+    from bench import manau_grads, manau_model
+
+    O = oracle_mod
+    print("case: Manau's Dana branch on the north-star model, 2 steps", flush=True)
+    groups, params, hp = manau_model(seed=0)
+    with contextlib.redirect_stdout(io.StringIO()):
+        opt = adana_amd.Manau(groups, **hp)
+    rng = np.random.default_rng(17)
+    dana, picks, ogroups, host = [], [], [], []
+    for g in groups:
+        mine = [p for p in g["params"] if not opt.state[p]["use_muon"]]
+        if not mine:
+            continue
+        hs = []
+        for p in mine:
+            n = p.numel()
+            ix = torch.from_numpy(np.unique(np.concatenate([[0, n - 1], rng.integers(0, n, size=SAMPLES)]))).to(DEV)
+            dana.append(p)
+            picks.append(ix)
+            hs.append(p.detach().reshape(-1).index_select(0, ix).cpu().numpy())
+        host.append(hs)
+        ogroups.append(O.OracleManauGroup(params=hs, use_muon=[False] * len(hs), lr=hp["lr"],
+                                          weight_decay=g["weight_decay"], delta=hp["delta"], kappa=hp["kappa"],
+                                          clipsnr=hp["clipsnr"], wd_decaying=hp["wd_decaying"], wd_ts=hp["wd_ts"]))
+    orc = O.OracleManau(groups=ogroups, peak_lr=hp["lr"])
+    flat_host = [h for hs in host for h in hs]
+    assert sum(p.numel() for p in dana) == 128_944_640
+
+    def gather(ts):
+        return [t.detach().reshape(-1).index_select(0, ix).float().cpu().numpy() for t, ix in zip(ts, picks)]
+
+    for t in (1, 2):
+        if t > 1:
+            manau_grads(params, groups[1]["params"][0], 100 + t)
+        gs = gather([p.grad for p in dana])
+        gnorm = [_norm64(p.grad) for p in dana]
+        before = [x.copy() for x in flat_host]
+        opt.step()
+        torch.cuda.synchronize()
+        k = 0
+        og = []
+        for hs in host:
+            og.append(gs[k:k + len(hs)])
+            k += len(hs)
+        orc.step(og)
+        got = {key: gather([opt.state[p][key] for p in dana]) for key in ("dana_m", "dana_v", "dana_tau")}
+        got_p = gather(dana)
+        for i, p in enumerate(dana):
+            ost = orc.state[id(flat_host[i])]
+            where = (t, i, tuple(p.shape))
+            for key in ("dana_m", "dana_v", "dana_tau"):
+                assert ulp_diff(got[key][i], ost[key]).max() == 0, (where, key)
+            d = ulp_diff(got_p[i], flat_host[i])
+            bad = np.nonzero(d)[0]
+            assert bad.size <= STAR_HARD_CASES, (where, bad.size)
+            for j in bad:
+                scale = max(abs(float(before[i][j])), abs(float(flat_host[i][j])))
+                assert abs(float(got_p[i][j]) - float(flat_host[i][j])) <= STAR_P_ULPS * np.spacing(np.float32(scale))
+            flat_host[i][...] = got_p[i]                     # continue from the GPU's p
+            st = opt.state[p]
+            np.testing.assert_allclose(float(st["gradient_norm"]), gnorm[i], rtol=1e-5, err_msg=str(where))
+            np.testing.assert_allclose(float(st["m_norm"]), _norm64(st["dana_m"]), rtol=1e-5, err_msg=str(where))
+    del opt, params, groups
+    torch.cuda.empty_cache()
