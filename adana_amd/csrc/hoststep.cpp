@@ -106,33 +106,41 @@ int advance_states(PyObject *states) {
     return rc;
 }
 
-/* advance_if_same(params, grads, states[, param_ptrs]) -> bool
+/* advance_if_same(params, grads, states[, param_ptrs[, grad_ptrs]]) -> bool
  *
  * True when params[i].grad is grads[i] for every i (None included); then every
  * dict in ``states`` has its "step" entry incremented by one.  False (and
  * nothing modified) as soon as one gradient differs. */
 PyObject *advance_if_same(PyObject *, PyObject *args) {
-    PyObject *params, *grads, *states, *pptrs = Py_None;
-    if (!PyArg_ParseTuple(args, "O!O!O!|O", &PyList_Type, &params, &PyList_Type, &grads, &PyList_Type, &states,
-                          &pptrs))
+    PyObject *params, *grads, *states, *pptrs = Py_None, *gptrs = Py_None;
+    if (!PyArg_ParseTuple(args, "O!O!O!|OO", &PyList_Type, &params, &PyList_Type, &grads, &PyList_Type, &states,
+                          &pptrs, &gptrs))
         return nullptr;
     const Py_ssize_t n = PyList_GET_SIZE(params);
     if (PyList_GET_SIZE(grads) != n) Py_RETURN_FALSE;
-    const uint64_t *want = nullptr;
+    const uint64_t *want_p = nullptr, *want_g = nullptr;
     if (pptrs != Py_None) {
         if (!PyBytes_Check(pptrs) || PyBytes_GET_SIZE(pptrs) != 8 * n) Py_RETURN_FALSE;
-        want = reinterpret_cast<const uint64_t *>(PyBytes_AS_STRING(pptrs));
+        want_p = reinterpret_cast<const uint64_t *>(PyBytes_AS_STRING(pptrs));
+    }
+    if (gptrs != Py_None) {
+        if (!PyBytes_Check(gptrs) || PyBytes_GET_SIZE(gptrs) != 8 * n) Py_RETURN_FALSE;
+        want_g = reinterpret_cast<const uint64_t *>(PyBytes_AS_STRING(gptrs));
     }
     try {
         for (Py_ssize_t i = 0; i < n; ++i) {
-            PyObject *p = PyList_GET_ITEM(params, i);
-            const int same = same_grad(p, PyList_GET_ITEM(grads, i));
+            PyObject *p = PyList_GET_ITEM(params, i), *g = PyList_GET_ITEM(grads, i);
+            const int same = same_grad(p, g);
             if (same < 0) return nullptr;
             if (!same) Py_RETURN_FALSE;
-            if (want) {
-                uint64_t ptr;
+            uint64_t ptr;
+            if (want_p) {
                 if (data_ptr_of(p, &ptr)) return nullptr;
-                if (ptr != want[i]) Py_RETURN_FALSE;
+                if (ptr != want_p[i]) Py_RETURN_FALSE;
+            }
+            if (want_g) {                          // the same gradient object may have new storage (set_)
+                if (data_ptr_of(g, &ptr)) return nullptr;
+                if (ptr != want_g[i]) Py_RETURN_FALSE;
             }
         }
     } catch (const std::exception &e) {
@@ -315,9 +323,9 @@ PyObject *grads_match(PyObject *, PyObject *args) {
 
 PyMethodDef methods[] = {
     {"advance_if_same", advance_if_same, METH_VARARGS,
-     "advance_if_same(params, grads, states[, param_ptrs]) -> bool: if params[i].grad is grads[i] for all i "
-     "(and params[i].data_ptr() is param_ptrs[i], native uint64 bytes), increment every states[j]['step'] "
-     "and return True; otherwise change nothing and return False."},
+     "advance_if_same(params, grads, states[, param_ptrs[, grad_ptrs]]) -> bool: if params[i].grad is "
+     "grads[i] for all i (and params[i] / grads[i] still have the data pointers given as native uint64 bytes), "
+     "increment every states[j]['step'] and return True; otherwise change nothing and return False."},
     {"advance_steps", advance_steps, METH_VARARGS,
      "advance_steps(states) -> None: increment every states[j]['step']."},
     {"grads_of", grads_of, METH_VARARGS,

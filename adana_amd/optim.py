@@ -469,10 +469,11 @@ class _DanaFamily(Optimizer):
         all_params, gidx = self._flat_params()
         act = self._active
         if (self._sets is not None and act is not None
-                and _hoststep.advance_if_same(all_params, act["all_grads"], act["states"], act["pptrs"])):
+                and _hoststep.advance_if_same(all_params, act["all_grads"], act["states"], act["pptrs"],
+                                              act["gptrs"])):
             # Persistent gradients: every p.grad is the same tensor object as at
-            # the last step (grad None where it was None) and every parameter
-            # keeps its storage, so the active set, device tables and scalar
+            # the last step (grad None where it was None), and every parameter
+            # and gradient keeps its storage, so the active set, device tables and scalar
             # classes carry over; advance_if_same has already done the
             # per-tensor ``state['step'] += 1`` (adana.py:197).
             grads = act["grads"]
@@ -496,6 +497,7 @@ class _DanaFamily(Optimizer):
             act["all_grads"] = all_grads
             act["grads"] = grads
             act["pptrs"] = _hoststep.data_ptrs(all_params)
+            act["gptrs"] = _hoststep.data_ptrs(all_grads)
         else:
             params, grads, states, keys, index, fresh = [], [], [], [], [], []
             for i, (p, g) in enumerate(zip(all_params, all_grads)):
@@ -537,7 +539,7 @@ class _DanaFamily(Optimizer):
             self._active = {"absent": absent, "all": len(index) == len(all_params),
                             "index": index, "states": states, "params": params,
                             "classes": classes, "all_grads": all_grads, "grads": grads,
-                            "pptrs": _hoststep.data_ptrs(all_params)}
+                            "pptrs": _hoststep.data_ptrs(all_params), "gptrs": _hoststep.data_ptrs(all_grads)}
         return self._launch(params, grads, classes, loss)
 
     def _launch(self, params, grads, classes, loss):

@@ -588,6 +588,33 @@ def test_new_gradient_buffers_every_step(oracle_mod, star):
         assert (flags != 0).all() == (k % 2 == 0), (k, flags)
 
 
+def test_gradient_storage_swapped_in_place(oracle_mod):
+    """The same gradient objects every step, but ``g.set_(other)`` moves their
+    storage between steps: the step reads the new storage (the object-identity
+    fast path also compares data pointers)."""
+    print("case: gradient storage swapped under the same objects", flush=True)
+    rng = np.random.default_rng(45)
+    shapes = [(1000,), (64, 33), (5,)]
+    params = [_normal(rng, s, 0.02) for s in shapes]
+    pair = Pair(oracle_mod, True, [(params, {})], lr=1e-3, delta=8.0, kappa=0.85, clipsnr=2.0,
+                weight_decay=0.1)
+    grads = [torch.zeros(s, device=DEV) for s in shapes]
+    for p, g in zip(pair.gpu_params[0], grads):
+        p.grad = g
+    for k in range(6):
+        gl = [[_normal(rng, x.shape, 1e-3) for x in params]]
+        for g, new in zip(grads, gl[0]):
+            if k % 2:
+                g.set_(torch.from_numpy(new.copy()).to(DEV))       # same object, new storage
+            else:
+                g.copy_(torch.from_numpy(new))
+        pair.prev = [[x.copy() for x in cp] for cp in pair.cpu_params]
+        pair.opt.step()
+        pair.oracle.step(gl)
+        torch.cuda.synchronize()
+        pair.compare(where=f"k={k}")
+
+
 @pytest.mark.parametrize("star", [False, True])
 def test_closure_and_group_added_mid_run(oracle_mod, star):
     """step(closure): the closure runs with gradients enabled, its loss is

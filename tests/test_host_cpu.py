@@ -433,6 +433,11 @@ def test_hoststep_grads_ptrs_and_steps():
     assert [s["step"] for s in states] == [3, 3]
     assert _hoststep.advance_if_same(ps, grads, states, _hoststep.data_ptrs(ps)) is True
     assert _hoststep.advance_if_same(ps, grads, states, b"short") is False
+    pp, gp = _hoststep.data_ptrs(ps), _hoststep.data_ptrs(grads)
+    assert _hoststep.advance_if_same(ps, grads, states, pp, gp) is True
+    grads[0].set_(torch.ones(3))                                # same object, new storage
+    assert _hoststep.advance_if_same(ps, grads, states, pp, gp) is False
+    assert _hoststep.advance_if_same(ps, grads, states, pp, _hoststep.data_ptrs(grads)) is True
 
 
 def test_hoststep_grads_match():
