@@ -12,7 +12,12 @@
 //     order (NaN last; -0 and +0 adjacent, equal as values);
 //   * a pass resolves the next w key bits (w <= 8) of every wanted rank: one
 //     read of the tensors, a histogram per (tensor, active prefix) of the next
-//     digit, kept in LDS by each workgroup and flushed with global atomics;
+//     digit, kept in LDS by each workgroup and flushed with global atomics.
+//     A value finds its prefix's histogram through a two-table cuckoo hash
+//     of the tensor's active prefixes (built on the host, copied to LDS): two
+//     independent LDS reads per value, however many prefixes are active.
+//     Tensors with fewer than 4 active prefixes, or whose table did not build,
+//     use a binary search over the sorted prefixes instead;
 //   * a walk kernel (one wavefront per rank) takes each rank's histogram to
 //     its next digit and residual rank on the device; the host reads back the
 //     new prefixes and the next pass narrows to them.  w is 8 while few
@@ -20,6 +25,11 @@
 //     always fit in LDS.
 // Exact (integer counting), deterministic results; no sort scratch.  Traffic:
 // 4 bytes per element per pass, 4 to 8 passes.
+//
+// The cuckoo hash: table k (k = 0, 1) holds 2^b entries {prefix, slot} and a
+// prefix p lives at (p * mul_k) >> (32 - b) in one of the two tables; an
+// empty entry holds 0xffffffff, which no prefix equals (a prefix has fewer
+// than 32 bits).
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -35,7 +45,9 @@ namespace {
 
 constexpr int kThreads = 256;
 constexpr int kTileElems = 65536;                 // elements per workgroup (64 loads of 4 per thread)
-constexpr int kLdsBudget = 40 * 1024;             // histogram + prefix table bytes per workgroup
+constexpr int kLdsBudget = 40 * 1024;             // histogram + prefix tables bytes per workgroup
+constexpr int kHashMinSlots = 4;                  // fewer active prefixes: binary search
+constexpr uint32_t kEmpty = 0xffffffffu;
 
 typedef float F4 __attribute__((ext_vector_type(4)));
 #define GLOBAL_AS __attribute__((address_space(1)))
@@ -47,12 +59,20 @@ __device__ __forceinline__ uint32_t order_key(float x) {
     return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
 }
 
+struct HashInfo {               // per tensor: its cuckoo tables in PassArgs::table
+    int32_t first;                // first entry
+    int32_t bits;                 // b: 2^b entries per table; 0 = binary search
+    uint32_t mul[2];              // odd multipliers of the two hash functions
+};
+
 struct PassArgs {
     const float *const *tensor;   // device array of tensor base pointers
     const int64_t *numel;         // device, per tensor
     const int64_t *tile_first;    // device, n + 1: first workgroup of each tensor
     const int32_t *slot_first;    // device, n + 1: first prefix slot of each tensor
     const uint32_t *prefix;       // device, sorted prefixes of each tensor's slots
+    const HashInfo *hinfo;        // device, per tensor
+    const uint2 *table;           // device, the tensors' cuckoo tables ({prefix, slot} entries)
     uint32_t *hist;               // device, [slot][bin] counts
     int32_t n;
     int32_t known_bits;           // key bits already resolved (prefix width)
@@ -74,9 +94,20 @@ __global__ __launch_bounds__(kThreads) void select_hist_kernel(PassArgs a) {
     const int bins = 1 << a.width;
     uint32_t *h = lds;                                   // [ns][bins]
     uint32_t *pre = lds + ns * bins;                     // [ns]
+    uint2 *tab = reinterpret_cast<uint2 *>(lds + ((ns * bins + ns + 1) & ~1));   // [2][2^hb], 8-byte aligned
+    const HashInfo hi = a.hinfo[t];
+    const int hb = a.known_bits > 0 ? hi.bits : 0;
     for (int i = threadIdx.x; i < ns * bins; i += kThreads) h[i] = 0;
     for (int i = threadIdx.x; i < ns; i += kThreads) pre[i] = a.prefix[s0 + i];
+    if (hb > 0)
+        for (int i = threadIdx.x; i < (2 << hb); i += kThreads) tab[i] = a.table[hi.first + i];
     __syncthreads();
+    // slot of prefix p in the cuckoo tables, or -1 when p is not active
+    auto hashed_slot = [&](uint32_t p) -> int {
+        const uint2 u = tab[(p * hi.mul[0]) >> (32 - hb)];
+        const uint2 w = tab[(1 << hb) + ((p * hi.mul[1]) >> (32 - hb))];
+        return u.x == p ? static_cast<int>(u.y) : (w.x == p ? static_cast<int>(w.y) : -1);
+    };
 
     const float *x = a.tensor[t];
     const int64_t n = a.numel[t];
@@ -125,6 +156,13 @@ __global__ __launch_bounds__(kThreads) void select_hist_kernel(PassArgs a) {
             if (a.known_bits == 0) {
 #pragma unroll
                 for (int e = 0; e < kVals; ++e) add(static_cast<int>((key[e] >> shift) & mask));
+            } else if (hb > 0) {
+                int sl[kVals];
+#pragma unroll
+                for (int e = 0; e < kVals; ++e) sl[e] = hashed_slot(key[e] >> (32 - a.known_bits));
+#pragma unroll
+                for (int e = 0; e < kVals; ++e)
+                    if (sl[e] >= 0) add(sl[e] * bins + static_cast<int>((key[e] >> shift) & mask));
             } else {
                 uint32_t p[kVals];
                 int lo[kVals];
@@ -153,7 +191,10 @@ __global__ __launch_bounds__(kThreads) void select_hist_kernel(PassArgs a) {
             for (int k = 0; k < cnt; ++k) {
                 const uint32_t key = order_key(x[e0 + k]);
                 int sl = 0;
-                if (a.known_bits > 0) {
+                if (hb > 0) {
+                    sl = hashed_slot(key >> (32 - a.known_bits));
+                    if (sl < 0) continue;
+                } else if (a.known_bits > 0) {
                     const uint32_t pk = key >> (32 - a.known_bits);
                     for (int step = top; step > 0; step >>= 1) {
                         const int c = sl + step;
@@ -220,6 +261,49 @@ __global__ __launch_bounds__(kThreads) void select_walk_kernel(const uint32_t *_
     }
 }
 
+// Odd multiplier number `seed` (the 32-bit finaliser of MurmurHash3 over
+// the seed, low bit set).
+uint32_t hash_multiplier(uint32_t seed) {
+    uint32_t x = seed * 0x9e3779b9u + 0x7f4a7c15u;
+    x ^= x >> 16;
+    x *= 0x85ebca6bu;
+    x ^= x >> 13;
+    x *= 0xc2b2ae35u;
+    x ^= x >> 16;
+    return x | 1u;
+}
+
+// Places keys[k] (with slot k) in two tables of 2^b entries (tab[0, 2^b) and
+// tab[2^b, 2^(b+1))), each key at (key * mul[side]) >> (32 - b) of one side.
+// False when an eviction chain exceeds its bound; the caller then retries
+// with other multipliers or larger tables.
+bool cuckoo_build(const uint32_t *keys, int ns, int b, const uint32_t mul[2], uint2 *tab) {
+    const uint32_t T = 1u << b;
+    for (uint32_t i = 0; i < 2 * T; ++i) tab[i] = make_uint2(kEmpty, 0u);
+    for (int k = 0; k < ns; ++k) {
+        uint2 cur = make_uint2(keys[k], static_cast<uint32_t>(k));
+        int side = 0;
+        bool placed = false;
+        for (int it = 0; it < 4 * ns + 32 && !placed; ++it) {
+            uint2 &e = tab[side * T + ((cur.x * mul[side]) >> (32 - b))];
+            std::swap(e, cur);
+            placed = cur.x == kEmpty;
+            side ^= 1;                   // the evicted key's other place is in the other table
+        }
+        if (!placed) return false;
+    }
+    return true;
+}
+
+constexpr int kHashMaxBits = 10;                  // tables of at most 2 x 1024 entries (16 KB of LDS)
+constexpr int kHashGrow = 2;                      // table doublings tried before the binary search
+
+inline int ceil_log2(int x) {
+    int b = 0;
+    while ((1 << b) < x) ++b;
+    return b;
+}
+
 inline uint32_t key_to_bits(uint32_t key) {
     return (key & 0x80000000u) ? (key & 0x7fffffffu) : ~key;
 }
@@ -230,7 +314,8 @@ int check(hipError_t e, const char *what) {
 }
 
 struct Layout {                 // device workspace carving
-    size_t ptrs, numel, tile_first, slot_first, prefix, hist, rank_slot, residual, rank_prefix, err, total;
+    size_t ptrs, numel, tile_first, slot_first, prefix, hinfo, table, hist, rank_slot, residual, rank_prefix, err,
+        total;
 };
 
 Layout layout(int32_t n, int64_t total_ranks) {
@@ -242,6 +327,10 @@ Layout layout(int32_t n, int64_t total_ranks) {
     L.tile_first = off; off += up(8 * static_cast<size_t>(n + 1));
     L.slot_first = off; off += up(4 * static_cast<size_t>(n + 1));
     L.prefix = off; off += up(4 * static_cast<size_t>(total_ranks > 0 ? total_ranks : 1));
+    L.hinfo = off; off += up(sizeof(HashInfo) * static_cast<size_t>(n));
+    // a tensor with s active prefixes has tables of 2 x 2^b entries, 2^b < 2 s
+    // grown at most kHashGrow times: under 2^(kHashGrow + 2) s entries of 8 bytes
+    L.table = off; off += up((8u << (kHashGrow + 2)) * static_cast<size_t>(total_ranks > 0 ? total_ranks : 1));
     L.hist = off; off += up(4 * 256 * static_cast<size_t>(total_ranks > 0 ? total_ranks : 1));
     const size_t nr = static_cast<size_t>(total_ranks > 0 ? total_ranks : 1);
     L.rank_slot = off; off += up(4 * nr);
@@ -317,6 +406,8 @@ int adana_order_stats(const float *const *h_tensor, const int64_t *h_numel, int3
     std::vector<uint32_t> prefix;
     std::vector<int32_t> rank_slot(static_cast<size_t>(total));
     std::vector<uint32_t> p;
+    std::vector<HashInfo> hinfo(static_cast<size_t>(n));
+    std::vector<uint2> table;
     int known = 0;
     while (known < 32) {
         // slots: each tensor's distinct prefixes among its wanted ranks, sorted;
@@ -336,18 +427,47 @@ int adana_order_stats(const float *const *h_tensor, const int64_t *h_numel, int3
             max_slots = std::max(max_slots, static_cast<int>(p.size()));
         }
         slot_first[n] = static_cast<int32_t>(prefix.size());
-        // digit width: the widest whose histograms (and prefix table) fit the LDS budget
+        // digit width: the widest whose histograms (and sorted prefixes) fit the LDS budget
         int width = 8;
         while (width > 1 && static_cast<size_t>(max_slots) * ((1u << width) + 1) * 4 > kLdsBudget) --width;
         if (static_cast<size_t>(max_slots) * ((1u << width) + 1) * 4 > kLdsBudget)
             return adana_set_error(ADANA_E_UNSUPPORTED, "adana_order_stats: %d ranks in one tensor is too many", max_slots);
         width = std::min(width, 32 - known);
         const int bins = 1 << width;
+        // cuckoo tables of each tensor's active prefixes (LDS on top of the
+        // histograms: at most 16 KB more)
+        table.clear();
+        size_t lds = 0;
+        for (int32_t i = 0; i < n; ++i) {
+            HashInfo &hi = hinfo[i];
+            hi = HashInfo{static_cast<int32_t>(table.size()), 0, {0u, 0u}};
+            const int ns = slot_first[i + 1] - slot_first[i];
+            if (known > 0 && ns >= kHashMinSlots) {
+                const uint32_t *keys = prefix.data() + slot_first[i];
+                for (int b = ceil_log2(ns); b <= std::min(ceil_log2(ns) + kHashGrow, kHashMaxBits) && !hi.bits; ++b) {
+                    table.resize(static_cast<size_t>(hi.first) + (2u << b));
+                    for (uint32_t seed = 0; seed < 8 && !hi.bits; ++seed) {
+                        const uint32_t mul[2] = {hash_multiplier(2 * seed), hash_multiplier(2 * seed + 1)};
+                        if (cuckoo_build(keys, ns, b, mul, table.data() + hi.first))
+                            hi = HashInfo{hi.first, b, {mul[0], mul[1]}};
+                    }
+                }
+                if (!hi.bits) table.resize(static_cast<size_t>(hi.first));   // binary search for this tensor
+            }
+            const size_t need = ((static_cast<size_t>(ns) * (bins + 1) + 1) & ~static_cast<size_t>(1)) * 4 +
+                                (hi.bits ? static_cast<size_t>(16) << hi.bits : 0);
+            lds = std::max(lds, need);
+        }
         const size_t hist_n = prefix.size() * static_cast<size_t>(bins);
         if ((rc = check(hipMemcpyAsync(ws + L.slot_first, slot_first.data(), 4 * static_cast<size_t>(n + 1),
                                        hipMemcpyHostToDevice, st), "copy")) ||
             (rc = check(hipMemcpyAsync(ws + L.prefix, prefix.data(), 4 * prefix.size(), hipMemcpyHostToDevice, st),
                         "copy")) ||
+            (rc = check(hipMemcpyAsync(ws + L.hinfo, hinfo.data(), sizeof(HashInfo) * static_cast<size_t>(n),
+                                       hipMemcpyHostToDevice, st), "copy")) ||
+            (rc = table.empty() ? ADANA_OK
+                                : check(hipMemcpyAsync(ws + L.table, table.data(), sizeof(uint2) * table.size(),
+                                                       hipMemcpyHostToDevice, st), "copy")) ||
             (rc = check(hipMemcpyAsync(ws + L.rank_slot, rank_slot.data(), 4 * static_cast<size_t>(total),
                                        hipMemcpyHostToDevice, st), "copy")) ||
             (rc = check(hipMemsetAsync(ws + L.hist, 0, 4 * hist_n, st), "clear")))
@@ -358,11 +478,12 @@ int adana_order_stats(const float *const *h_tensor, const int64_t *h_numel, int3
         pa.tile_first = reinterpret_cast<const int64_t *>(ws + L.tile_first);
         pa.slot_first = reinterpret_cast<const int32_t *>(ws + L.slot_first);
         pa.prefix = reinterpret_cast<const uint32_t *>(ws + L.prefix);
+        pa.hinfo = reinterpret_cast<const HashInfo *>(ws + L.hinfo);
+        pa.table = reinterpret_cast<const uint2 *>(ws + L.table);
         pa.hist = reinterpret_cast<uint32_t *>(ws + L.hist);
         pa.n = n;
         pa.known_bits = known;
         pa.width = width;
-        const size_t lds = static_cast<size_t>(max_slots) * (bins + 1) * 4;
         hipLaunchKernelGGL(select_hist_kernel, dim3(static_cast<unsigned>(n_tiles)), dim3(kThreads),
                            static_cast<unsigned>(lds), st, pa);
         if ((rc = check(hipGetLastError(), "histogram launch"))) return rc;
