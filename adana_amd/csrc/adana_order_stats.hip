@@ -417,6 +417,20 @@ int adana_order_stats(const float *const *h_tensor, const int64_t *h_numel, int3
         for (int32_t i = 0; i < n; ++i) {
             slot_first[i] = static_cast<int32_t>(prefix.size());
             const int64_t a = h_rank_first[i], b = h_rank_first[i + 1];
+            if (std::is_sorted(rank_prefix.begin() + a, rank_prefix.begin() + b)) {
+                // ascending ranks (the usual request) have non-decreasing
+                // prefixes: distinct prefixes and slots in one scan
+                int32_t s = -1;
+                for (int64_t j = a; j < b; ++j) {
+                    if (j == a || rank_prefix[j] != rank_prefix[j - 1]) {
+                        prefix.push_back(rank_prefix[j]);
+                        ++s;
+                    }
+                    rank_slot[j] = slot_first[i] + s;
+                }
+                max_slots = std::max(max_slots, s + 1);
+                continue;
+            }
             p.assign(rank_prefix.begin() + a, rank_prefix.begin() + b);
             std::sort(p.begin(), p.end());
             p.erase(std::unique(p.begin(), p.end()), p.end());

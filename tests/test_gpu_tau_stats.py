@@ -56,6 +56,29 @@ def test_order_statistics_match_oracle(oracle_mod):
         assert gl.dtype == np.float32
 
 
+def test_ranks_in_any_order():
+    """order_values takes each tensor's ranks in any order, repeats included:
+    the values equal np.sort(x)[ranks] position by position (shuffled ranks
+    take the library's sorting path, ascending ones its linear scan)."""
+    from adana_amd.tau_stats import order_values
+
+    rng = np.random.default_rng(11)
+    print("case: order_values with shuffled and repeated ranks", flush=True)
+    xs = [rng.normal(0, 1, 300_001).astype(np.float32), np.clip(rng.beta(2, 5, 70_000), 0, 1).astype(np.float32),
+          (rng.integers(0, 5, 40_000) / 4).astype(np.float32)]
+    ranks = []
+    for x in xs:
+        r = np.unique(np.concatenate([np.int64(1.1 ** np.arange(120)) - 1, rng.integers(0, x.size, 300)]))
+        r = r[r < x.size]
+        ranks.append(r)
+    shuffled = [rng.permutation(np.concatenate([r, r[:17]])) for r in ranks]
+    tensors = [torch.from_numpy(x).to(DEV) for x in xs]
+    for rs in (ranks, shuffled):
+        got = order_values(tensors, rs)
+        for x, r, g in zip(xs, rs, got):
+            assert _same(g, np.sort(x)[r])
+
+
 def test_unaligned_and_empty_tensors(oracle_mod):
     import adana_amd
 
