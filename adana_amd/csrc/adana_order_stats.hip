@@ -313,7 +313,9 @@ int check(hipError_t e, const char *what) {
     return ADANA_OK;
 }
 
-struct Layout {                 // device workspace carving
+// Device workspace carving.  slot_first .. table are one block, uploaded
+// with one copy per pass; rank_prefix and err are read back with one copy.
+struct Layout {
     size_t ptrs, numel, tile_first, slot_first, prefix, hinfo, table, hist, rank_slot, residual, rank_prefix, err,
         total;
 };
@@ -328,12 +330,12 @@ Layout layout(int32_t n, int64_t total_ranks) {
     L.slot_first = off; off += up(4 * static_cast<size_t>(n + 1));
     L.prefix = off; off += up(4 * static_cast<size_t>(total_ranks > 0 ? total_ranks : 1));
     L.hinfo = off; off += up(sizeof(HashInfo) * static_cast<size_t>(n));
-    // a tensor with s active prefixes has tables of 2 x 2^b entries, 2^b < 2 s
-    // grown at most kHashGrow times: under 2^(kHashGrow + 2) s entries of 8 bytes
-    L.table = off; off += up((8u << (kHashGrow + 2)) * static_cast<size_t>(total_ranks > 0 ? total_ranks : 1));
-    L.hist = off; off += up(4 * 256 * static_cast<size_t>(total_ranks > 0 ? total_ranks : 1));
     const size_t nr = static_cast<size_t>(total_ranks > 0 ? total_ranks : 1);
     L.rank_slot = off; off += up(4 * nr);
+    // a tensor with s active prefixes has tables of 2 x 2^b entries, 2^b < 2 s
+    // grown at most kHashGrow times: under 2^(kHashGrow + 2) s entries of 8 bytes
+    L.table = off; off += up((8u << (kHashGrow + 2)) * nr);
+    L.hist = off; off += up(4 * 256 * nr);
     L.residual = off; off += up(8 * nr);
     L.rank_prefix = off; off += up(4 * nr);
     L.err = off; off += up(4);
@@ -381,7 +383,8 @@ int adana_order_stats(const float *const *h_tensor, const int64_t *h_numel, int3
 
     // per-rank search state: the rank's prefix (host copy, read back after
     // each pass) and, on the device, its residual rank within that prefix
-    std::vector<uint32_t> rank_prefix(static_cast<size_t>(total), 0u);
+    // (read back with err, which is its last element)
+    std::vector<uint32_t> rank_prefix((L.err + 4 - L.rank_prefix) / 4, 0u);
     std::vector<int64_t> tile_first(static_cast<size_t>(n) + 1, 0);
     for (int32_t i = 0; i < n; ++i) {
         const bool wanted = h_rank_first[i + 1] > h_rank_first[i];
@@ -398,8 +401,7 @@ int adana_order_stats(const float *const *h_tensor, const int64_t *h_numel, int3
                                    hipMemcpyHostToDevice, st), "copy")) ||
         (rc = check(hipMemcpyAsync(ws + L.residual, h_ranks, 8 * static_cast<size_t>(total), hipMemcpyHostToDevice,
                                    st), "copy")) ||
-        (rc = check(hipMemsetAsync(ws + L.rank_prefix, 0, 4 * static_cast<size_t>(total), st), "clear")) ||
-        (rc = check(hipMemsetAsync(d_err, 0, 4, st), "clear")))
+        (rc = check(hipMemsetAsync(ws + L.rank_prefix, 0, L.err + 4 - L.rank_prefix, st), "clear")))
         return rc;
 
     std::vector<int32_t> slot_first(static_cast<size_t>(n) + 1);
@@ -408,6 +410,7 @@ int adana_order_stats(const float *const *h_tensor, const int64_t *h_numel, int3
     std::vector<uint32_t> p;
     std::vector<HashInfo> hinfo(static_cast<size_t>(n));
     std::vector<uint2> table;
+    std::vector<char> stage;                       // the slot_first .. table block, as uploaded
     int known = 0;
     while (known < 32) {
         // slots: each tensor's distinct prefixes among its wanted ranks, sorted;
@@ -473,17 +476,15 @@ int adana_order_stats(const float *const *h_tensor, const int64_t *h_numel, int3
             lds = std::max(lds, need);
         }
         const size_t hist_n = prefix.size() * static_cast<size_t>(bins);
-        if ((rc = check(hipMemcpyAsync(ws + L.slot_first, slot_first.data(), 4 * static_cast<size_t>(n + 1),
-                                       hipMemcpyHostToDevice, st), "copy")) ||
-            (rc = check(hipMemcpyAsync(ws + L.prefix, prefix.data(), 4 * prefix.size(), hipMemcpyHostToDevice, st),
+        stage.resize(L.table - L.slot_first + sizeof(uint2) * table.size());
+        memcpy(stage.data(), slot_first.data(), 4 * static_cast<size_t>(n + 1));
+        memcpy(stage.data() + (L.prefix - L.slot_first), prefix.data(), 4 * prefix.size());
+        memcpy(stage.data() + (L.hinfo - L.slot_first), hinfo.data(), sizeof(HashInfo) * static_cast<size_t>(n));
+        memcpy(stage.data() + (L.rank_slot - L.slot_first), rank_slot.data(), 4 * static_cast<size_t>(total));
+        if (!table.empty())
+            memcpy(stage.data() + (L.table - L.slot_first), table.data(), sizeof(uint2) * table.size());
+        if ((rc = check(hipMemcpyAsync(ws + L.slot_first, stage.data(), stage.size(), hipMemcpyHostToDevice, st),
                         "copy")) ||
-            (rc = check(hipMemcpyAsync(ws + L.hinfo, hinfo.data(), sizeof(HashInfo) * static_cast<size_t>(n),
-                                       hipMemcpyHostToDevice, st), "copy")) ||
-            (rc = table.empty() ? ADANA_OK
-                                : check(hipMemcpyAsync(ws + L.table, table.data(), sizeof(uint2) * table.size(),
-                                                       hipMemcpyHostToDevice, st), "copy")) ||
-            (rc = check(hipMemcpyAsync(ws + L.rank_slot, rank_slot.data(), 4 * static_cast<size_t>(total),
-                                       hipMemcpyHostToDevice, st), "copy")) ||
             (rc = check(hipMemsetAsync(ws + L.hist, 0, 4 * hist_n, st), "clear")))
             return rc;
         PassArgs pa;
@@ -507,13 +508,11 @@ int adana_order_stats(const float *const *h_tensor, const int64_t *h_numel, int3
                            reinterpret_cast<int64_t *>(ws + L.residual), reinterpret_cast<uint32_t *>(ws + L.rank_prefix),
                            total, width, d_err);
         if ((rc = check(hipGetLastError(), "walk launch"))) return rc;
-        int32_t err = 0;
-        if ((rc = check(hipMemcpyAsync(rank_prefix.data(), ws + L.rank_prefix, 4 * static_cast<size_t>(total),
+        if ((rc = check(hipMemcpyAsync(rank_prefix.data(), ws + L.rank_prefix, 4 * rank_prefix.size(),
                                        hipMemcpyDeviceToHost, st), "copy")) ||
-            (rc = check(hipMemcpyAsync(&err, d_err, 4, hipMemcpyDeviceToHost, st), "copy")) ||
             (rc = check(hipStreamSynchronize(st), "synchronize")))
             return rc;
-        if (err) return adana_set_error(ADANA_E_HIP, "adana_order_stats: a histogram does not cover its rank");
+        if (rank_prefix.back() != 0) return adana_set_error(ADANA_E_HIP, "adana_order_stats: a histogram does not cover its rank");
         known += width;
     }
     for (int64_t j = 0; j < total; ++j) {

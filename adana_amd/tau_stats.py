@@ -23,7 +23,7 @@ from typing import Dict, List, Sequence, Tuple
 import numpy as np
 import torch
 
-from . import _lib
+from . import _hoststep, _lib
 
 __all__ = ["order_stat_indices", "order_values", "compute_tau_order_statistics",
            "extract_tau_statistics"]
@@ -38,45 +38,52 @@ def order_stat_indices(n: int) -> np.ndarray:
     return np.minimum(indices, n - 1)
 
 
+def _select(flat: Sequence[torch.Tensor], numel: np.ndarray, ranks: np.ndarray,
+            rank_first: np.ndarray) -> np.ndarray:
+    """One adana_order_stats call: the values at ``ranks[rank_first[i]:
+    rank_first[i + 1]]`` of each contiguous float32 tensor ``flat[i]``,
+    concatenated."""
+    dev = flat[0].device
+    for f in flat:
+        if f.device.type != "cuda" or f.dtype != torch.float32:
+            raise RuntimeError(f"order_values: float32 ROCm tensors only (got {f.dtype} on {f.device})")
+        if f.device != dev:
+            raise NotImplementedError("order_values: tensors on more than one device")
+    n = len(flat)
+    total = int(rank_first[-1])
+    ptrs = np.frombuffer(_hoststep.data_ptrs(list(flat)), dtype=np.uint64)
+    values = np.empty(max(total, 1), dtype=np.float32)
+    ranks = ranks if total else np.zeros(1, np.int64)
+    L = _lib.lib()
+    ws = torch.empty(max(int(L.adana_order_stats_workspace(n, total)), 1), dtype=torch.uint8, device=dev)
+    with torch.cuda.device(dev):
+        stream = torch.cuda.current_stream(dev).cuda_stream
+        _lib.check(L.adana_order_stats(ctypes.c_void_p(ptrs.ctypes.data), ctypes.c_void_p(numel.ctypes.data),
+                                       n, ctypes.c_void_p(ranks.ctypes.data),
+                                       ctypes.c_void_p(rank_first.ctypes.data),
+                                       ctypes.c_void_p(values.ctypes.data), ctypes.c_void_p(ws.data_ptr()),
+                                       ws.numel(), ctypes.c_void_p(stream)), "adana_order_stats")
+    return values
+
+
+def _contiguous(t: torch.Tensor) -> torch.Tensor:
+    t = t.detach()
+    return t if t.is_contiguous() else t.contiguous()
+
+
 def order_values(tensors: Sequence[torch.Tensor], ranks: Sequence[np.ndarray]) -> List[np.ndarray]:
     """Values at ``ranks[i]`` (ascending order, np.sort's) of each float32
     CUDA tensor, exactly, in one batched device selection."""
     if len(tensors) != len(ranks):
         raise ValueError("order_values: one rank array per tensor")
-    flat, numel, rank_first, all_ranks = [], [], [0], []
-    for t, r in zip(tensors, ranks):
-        if t.device.type != "cuda" or t.dtype != torch.float32:
-            raise RuntimeError(f"order_values: float32 ROCm tensors only (got {t.dtype} on {t.device})")
-        f = t.detach().reshape(-1)
-        if not f.is_contiguous():
-            f = f.contiguous()
-        flat.append(f)
-        numel.append(f.numel())
-        r = np.ascontiguousarray(r, dtype=np.int64)
-        all_ranks.append(r)
-        rank_first.append(rank_first[-1] + r.size)
-    n = len(flat)
-    if n == 0:
+    if not tensors:
         return []
-    ptrs = np.array([f.data_ptr() for f in flat], dtype=np.uint64)
-    numel_a = np.array(numel, dtype=np.int64)
-    rank_first_a = np.array(rank_first, dtype=np.int64)
-    ranks_a = np.concatenate(all_ranks) if rank_first[-1] else np.zeros(1, np.int64)
-    values = np.empty(max(rank_first[-1], 1), dtype=np.float32)
-    L = _lib.lib()
-    dev = flat[0].device
-    for f in flat:
-        if f.device != dev:
-            raise NotImplementedError("order_values: tensors on more than one device")
-    ws = torch.empty(max(int(L.adana_order_stats_workspace(n, rank_first[-1])), 1), dtype=torch.uint8,
-                     device=dev)
-    with torch.cuda.device(dev):
-        stream = torch.cuda.current_stream(dev).cuda_stream
-        _lib.check(L.adana_order_stats(ctypes.c_void_p(ptrs.ctypes.data), ctypes.c_void_p(numel_a.ctypes.data),
-                                       n, ctypes.c_void_p(ranks_a.ctypes.data),
-                                       ctypes.c_void_p(rank_first_a.ctypes.data),
-                                       ctypes.c_void_p(values.ctypes.data), ctypes.c_void_p(ws.data_ptr()),
-                                       ws.numel(), ctypes.c_void_p(stream)), "adana_order_stats")
+    flat = [_contiguous(t) for t in tensors]
+    all_ranks = [np.ascontiguousarray(r, dtype=np.int64).ravel() for r in ranks]
+    rank_first = np.zeros(len(flat) + 1, dtype=np.int64)
+    np.cumsum([r.size for r in all_ranks], out=rank_first[1:])
+    numel = np.array([f.numel() for f in flat], dtype=np.int64)
+    values = _select(flat, numel, np.concatenate(all_ranks), rank_first)
     return [values[a:b].copy() for a, b in zip(rank_first[:-1], rank_first[1:])]
 
 
@@ -95,25 +102,47 @@ def _rank_plan(n: int) -> Tuple[np.ndarray, np.ndarray, np.ndarray]:
     return wanted, pos_small, pos_large
 
 
+@functools.lru_cache(maxsize=16)
+def _batch_plan(sizes: Tuple[int, ...]):
+    """For a list of tensor sizes: the sizes, the concatenated ranks and their
+    offsets for one _select call, and the positions of every tensor's largest
+    and smallest order statistics in its result (global indices, with the
+    offsets where each tensor's share starts).  Depends on the sizes only, so
+    repeated collections over one model reuse it; arrays are read-only."""
+    plans = [_rank_plan(n) if n else None for n in sizes]
+    counts = [p[0].size if p else 0 for p in plans]
+    rank_first = np.zeros(len(sizes) + 1, dtype=np.int64)
+    np.cumsum(counts, out=rank_first[1:])
+    ranks = (np.concatenate([p[0] for p in plans if p]) if rank_first[-1]
+             else np.zeros(0, np.int64))
+    large, small, out_first = [], [], [0]
+    for p, base in zip(plans, rank_first[:-1]):
+        if p is not None:
+            large.append(p[2] + base)
+            small.append(p[1] + base)
+        out_first.append(out_first[-1] + (p[1].size if p else 0))
+    large = np.concatenate(large) if large else np.zeros(0, np.int64)
+    small = np.concatenate(small) if small else np.zeros(0, np.int64)
+    numel = np.array(sizes, dtype=np.int64)
+    for a in (numel, ranks, rank_first, large, small):
+        a.flags.writeable = False
+    return numel, ranks, rank_first, large, small, out_first
+
+
 def _stats_for(tensors: Sequence[torch.Tensor]) -> List[Tuple[np.ndarray, np.ndarray]]:
-    plans, ranks = [], []
-    for t in tensors:
-        n = t.numel()
-        if n == 0:
-            plans.append(None)
-            ranks.append(np.zeros(0, np.int64))
-            continue
-        plan = _rank_plan(n)
-        plans.append(plan)
-        ranks.append(plan[0])
-    vals = order_values(tensors, ranks)
+    """(largest, smallest) order statistics of each tensor, from one selection."""
+    if not tensors:
+        return []
+    flat = [_contiguous(t) for t in tensors]
+    numel, ranks, rank_first, large, small, out_first = _batch_plan(tuple(f.numel() for f in flat))
+    values = _select(flat, numel, ranks, rank_first)
+    vl, vs = values[large], values[small]
     out = []
-    for plan, v in zip(plans, vals):
-        if plan is None:
+    for n, a, b in zip(numel, out_first[:-1], out_first[1:]):
+        if n == 0:
             out.append((np.array([]), np.array([])))          # the reference's empty result
-            continue
-        _, pos_small, pos_large = plan
-        out.append((v[pos_large], v[pos_small]))
+        else:
+            out.append((vl[a:b], vs[a:b]))
     return out
 
 

@@ -69,6 +69,25 @@ def test_product_indices_match_oracle_formula(n):
     assert idx.dtype.kind == "i" and idx.max() <= n - 1 and idx.min() >= 0
 
 
+def test_batch_plan_places_every_statistic(oracle_mod):
+    """The cached batch plan of a mixed list (empty and one-element tensors
+    among others): selecting its ranks from each tensor's np.sort and reading
+    its large / small positions gives the oracle's statistics per tensor."""
+    from adana_amd.tau_stats import _batch_plan
+
+    rng = np.random.default_rng(5)
+    sizes = (5, 0, 1000, 1, 77, 1000, 65537)
+    xs = [rng.normal(0, 1, n).astype(np.float32) for n in sizes]
+    numel, ranks, rank_first, large, small, out_first = _batch_plan(sizes)
+    assert _batch_plan(sizes)[1] is ranks                      # cached per size list
+    assert list(numel) == list(sizes) and rank_first[0] == 0 and rank_first[-1] == ranks.size
+    values = np.concatenate([np.sort(x)[ranks[a:b]] for x, a, b in zip(xs, rank_first[:-1], rank_first[1:])])
+    vl, vs = values[large], values[small]
+    for x, a, b in zip(xs, out_first[:-1], out_first[1:]):
+        wl, ws = oracle_mod.tau_order_statistics(x)
+        assert np.array_equal(vl[a:b], wl) and np.array_equal(vs[a:b], ws)
+
+
 def test_order_values_rejects_cpu_tensors():
     from adana_amd.tau_stats import order_values
 
