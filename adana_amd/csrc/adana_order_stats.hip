@@ -45,7 +45,13 @@ namespace {
 
 constexpr int kThreads = 256;
 constexpr int kTileElems = 65536;                 // elements per workgroup (64 loads of 4 per thread)
-constexpr int kLdsBudget = 40 * 1024;             // histogram + prefix tables bytes per workgroup
+// Histogram + sorted-prefix bytes per workgroup (the cuckoo tables come on
+// top).  Smaller budgets mean narrower digits but more resident workgroups;
+// on a north-star tau state 28 KB measured best (16-56 KB swept).
+constexpr int kLdsBudget = 28 * 1024;
+// Width-1 histograms of a tensor with very many active prefixes may use up to
+// this much (with at most 16 KB of tables: 64 KB in all).
+constexpr int kLdsMaxHist = 48 * 1024;
 constexpr int kHashMinSlots = 4;                  // fewer active prefixes: binary search
 constexpr uint32_t kEmpty = 0xffffffffu;
 
@@ -447,7 +453,7 @@ int adana_order_stats(const float *const *h_tensor, const int64_t *h_numel, int3
         // digit width: the widest whose histograms (and sorted prefixes) fit the LDS budget
         int width = 8;
         while (width > 1 && static_cast<size_t>(max_slots) * ((1u << width) + 1) * 4 > kLdsBudget) --width;
-        if (static_cast<size_t>(max_slots) * ((1u << width) + 1) * 4 > kLdsBudget)
+        if (static_cast<size_t>(max_slots) * ((1u << width) + 1) * 4 > kLdsMaxHist)
             return adana_set_error(ADANA_E_UNSUPPORTED, "adana_order_stats: %d ranks in one tensor is too many", max_slots);
         width = std::min(width, 32 - known);
         const int bins = 1 << width;
@@ -471,9 +477,12 @@ int adana_order_stats(const float *const *h_tensor, const int64_t *h_numel, int3
                 }
                 if (!hi.bits) table.resize(static_cast<size_t>(hi.first));   // binary search for this tensor
             }
-            const size_t need = ((static_cast<size_t>(ns) * (bins + 1) + 1) & ~static_cast<size_t>(1)) * 4 +
-                                (hi.bits ? static_cast<size_t>(16) << hi.bits : 0);
-            lds = std::max(lds, need);
+            const size_t hist_bytes = ((static_cast<size_t>(ns) * (bins + 1) + 1) & ~static_cast<size_t>(1)) * 4;
+            if (hi.bits && hist_bytes + (static_cast<size_t>(16) << hi.bits) > 64 * 1024) {
+                table.resize(static_cast<size_t>(hi.first));             // no room: binary search
+                hi.bits = 0;
+            }
+            lds = std::max(lds, hist_bytes + (hi.bits ? static_cast<size_t>(16) << hi.bits : 0));
         }
         const size_t hist_n = prefix.size() * static_cast<size_t>(bins);
         stage.resize(L.table - L.slot_first + sizeof(uint2) * table.size());

@@ -79,6 +79,23 @@ def test_ranks_in_any_order():
             assert _same(g, np.sort(x)[r])
 
 
+def test_many_ranks_in_one_tensor():
+    """3,000 ranks of one tensor of distinct values: the late passes hold
+    3,000 active prefixes, so the digits narrow to 1 bit past the LDS budget
+    and the prefix lookup falls back to the binary search (tables too large);
+    a second tensor with 600 ranks uses the cuckoo tables in the same passes."""
+    from adana_amd.tau_stats import order_values
+
+    rng = np.random.default_rng(13)
+    print("case: 3000 and 600 ranks per tensor", flush=True)
+    xs = [rng.permutation(np.arange(200_000, dtype=np.float32) * np.float32(0.5) - 7),
+          rng.normal(0, 1, 150_000).astype(np.float32)]
+    ranks = [np.sort(rng.choice(x.size, k, replace=False)) for x, k in zip(xs, (3000, 600))]
+    got = order_values([torch.from_numpy(x).to(DEV) for x in xs], ranks)
+    for x, r, g in zip(xs, ranks, got):
+        assert _same(g, np.sort(x)[r])
+
+
 def test_unaligned_and_empty_tensors(oracle_mod):
     import adana_amd
 
