@@ -307,7 +307,11 @@ size_t adana_order_stats_workspace(int32_t n_tensors, int64_t total_ranks);
  * digit per wanted prefix in LDS; after each pass every rank is narrowed to
  * its next digit on the device, and the host reads back the new prefixes to
  * set up the next pass.  Synchronises ``stream``.  d_workspace: at least
- * adana_order_stats_workspace(n_tensors, h_rank_first[n_tensors]) bytes. */
+ * adana_order_stats_workspace(n_tensors, h_rank_first[n_tensors]) bytes.
+ * Ranks may come in any order and repeat; ascending ranks save a host sort
+ * per pass.  Returns ADANA_E_UNSUPPORTED for a tensor of 2^32 elements or
+ * more, or one whose ranks hold more than 4,096 distinct values at some
+ * pass (its histograms would not fit in LDS). */
 int adana_order_stats(const float *const *h_tensors, const int64_t *h_numel, int32_t n_tensors,
                       const int64_t *h_ranks, const int64_t *h_rank_first, float *h_values,
                       void *d_workspace, size_t workspace_bytes, void *stream);
