@@ -339,6 +339,7 @@ class _DanaFamily(Optimizer):
             ls.sclass.append(c - ls.class_base)
         out = list(sets.values())
         for ls in out:
+            self._check_state_shapes(ls)
             numels = np.fromiter((p.numel() for p in ls.params), dtype=np.int64, count=len(ls.params))
             ls.vstart, ls.fold_first, ls.n_chunks, ls.n_folds = _lib.plan_layout(numels)
             ls.host_desc = self._desc_rows(ls)
@@ -582,6 +583,20 @@ class _DanaFamily(Optimizer):
             _hoststep.bump_versions(grads)
         return loss
 
+    def _check_state_shapes(self, ls: _LaunchSet) -> None:
+        """A parameter whose storage was rebound (``p.data = x``) must keep the
+        shape of its state: the laid-out plan, the workspace and the state
+        slabs are sized by it.  The reference fails the same way, in
+        ``m.lerp_(grad, alpha)`` (src/optim/adana.py:101)."""
+        km = self._KEYS[0]
+        for p, st in zip(ls.params, ls.states):
+            m = st[km]
+            if p.shape != m.shape:
+                a, b = tuple(m.shape), tuple(p.shape)
+                raise RuntimeError(f"{type(self).__name__}: parameter of shape {b} has optimizer state "
+                                   f"of shape {a}: the size of tensor a ({a}) must match the size of "
+                                   f"tensor b ({b})")
+
     def _refresh_ptrs(self, ls: _LaunchSet) -> None:
         """Re-point the launch set's descriptors at this step's gradients and
         the parameters' current storage (re-uploaded only when an address
@@ -589,6 +604,8 @@ class _DanaFamily(Optimizer):
         key = (_hoststep.data_ptrs(ls.grads), _hoststep.data_ptrs(ls.params))
         if key == ls.ptr_key:
             return
+        if key[1] != ls.ptr_key[1]:
+            self._check_state_shapes(ls)
         bf16 = bool(ls.flags & _lib.GRAD_BF16)
         if key[1] == ls.ptr_key[1] and _hoststep.grads_match(ls.params, ls.grads, bf16):
             # only gradients moved, and each is a dense contiguous tensor of its

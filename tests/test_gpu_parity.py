@@ -551,6 +551,33 @@ def test_parameter_storage_rebound_is_followed(oracle_mod, fresh_grads):
             assert torch.equal(old, snapshot)                      # the old storage is not written
 
 
+@pytest.mark.parametrize("drop_other_grad", [False, True])
+def test_parameter_rebound_to_another_shape_raises(drop_other_grad):
+    """``p.data = x`` with x of another shape (and a gradient of that shape)
+    raises at the next step, before any launch, whether the plan is reused
+    (same tensors have gradients) or rebuilt (another tensor's gradient is
+    None); the other tensors' state is left as it was."""
+    import adana_amd
+
+    print("case: parameter rebound to another shape, drop other grad", drop_other_grad, flush=True)
+    ps = [torch.nn.Parameter(torch.full((300,), 0.5, device=DEV)),
+          torch.nn.Parameter(torch.full((64, 33), 0.5, device=DEV))]
+    opt = adana_amd.DANA_STAR_MK4(ps, lr=1e-3, kappa=0.85)
+    for _ in range(2):
+        for p in ps:
+            p.grad = torch.full_like(p, 1e-3)
+        opt.step()
+    torch.cuda.synchronize()
+    m_before = opt.state[ps[0]]["m"].clone()
+    ps[1].data = torch.zeros(65, 33, device=DEV)
+    ps[1].grad = torch.full_like(ps[1], 1e-3)
+    ps[0].grad = None if drop_other_grad else torch.full_like(ps[0], 1e-3)
+    with pytest.raises(RuntimeError, match="must match the size"):
+        opt.step()
+    torch.cuda.synchronize()
+    assert torch.equal(opt.state[ps[0]]["m"], m_before)
+
+
 @pytest.mark.parametrize("star", [False, True])
 def test_new_gradient_buffers_every_step(oracle_mod, star):
     """New gradient tensors at new addresses every step, alternating between

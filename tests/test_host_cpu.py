@@ -473,3 +473,24 @@ def test_missing_library_fails_loudly(monkeypatch):
         _lib.lib()
     with pytest.raises(_lib.AdanaLibraryError, match="no non-HIP path"):
         adana_amd.DANA_STAR_MK4([torch.nn.Parameter(torch.zeros(3))], lr=1e-3)
+
+
+def test_rebound_parameter_of_another_shape_raises():
+    """A parameter whose storage is rebound to another shape (``p.data = x``)
+    no longer fits its laid-out state: the plan check raises before any
+    launch, as the reference's ``m.lerp_(grad, alpha)`` would
+    (src/optim/adana.py:101).  The check runs on host tensors only."""
+    import adana_amd
+    from adana_amd.optim import _LaunchSet
+
+    for cls in (adana_amd.ADana, adana_amd.DANA_STAR_MK4):
+        ps = [torch.nn.Parameter(torch.zeros(6)), torch.nn.Parameter(torch.zeros(2, 3))]
+        opt = cls(ps, lr=1e-3)
+        ls = _LaunchSet(torch.device("cpu"), 0, 0)
+        ls.params = ps
+        ls.states = [{"m": torch.zeros(6), "v": torch.zeros(6), "tau": torch.zeros(6)},
+                     {"m": torch.zeros(2, 3), "v": torch.zeros(2, 3), "tau": torch.zeros(2, 3)}]
+        opt._check_state_shapes(ls)                       # shapes agree: no error
+        ps[1].data = torch.zeros(3, 3)
+        with pytest.raises(RuntimeError, match="must match the size"):
+            opt._check_state_shapes(ls)

@@ -2,9 +2,12 @@
 
 1. Golden vectors written by the reference's own step() (tests/golden/):
    m and v bit-exact along the whole trajectory; tau within 2 ulp; p within
-   2 ulp (ADana) / 4 ulp (Dana-Star) per step from identical state, in ulps
-   of max(|p_before|, |p_after|, |update|) (the reference's CPU sqrt and pow are Sleef
-   approximations, the oracle's are correctly rounded).
+   2 ulp (ADana) / 3 ulp (Dana-Star) per step from identical state, in ulps
+   of max(|p_before|, |p_after|, |update|).  The whole gap is torch's CPU
+   sqrt and pow (SIMD approximations; the oracle's are correctly rounded):
+   tests/test_torch_restatement.py reproduces the reference's bits at 0 ulp
+   with torch ops in the reference's order, and the oracle's bits at 0 ulp
+   with only those two functions made correctly rounded.
 2. Closed forms for a constant gradient from zero state (float64 maths).
 3. Invariants and special cases the reference's formulas imply.
 """
@@ -166,10 +169,10 @@ def test_golden_single_step(oracle_mod, case, t0):
         ref = gold[f"p{i}_t{k}"]
         scale = np.maximum(np.maximum(np.abs(prev[i]), np.abs(ref)), np.abs(ref - prev[i]))
         err = _scaled_err(p, ref, scale)
-        # Dana-Star's update passes through three of the reference's Sleef
+        # Dana-Star's update passes through three of torch's CPU
         # approximations (sqrt(v), sqrt(tau_reg), pow), each <=1 ulp off the
-        # correctly rounded value the oracle takes, so its bound is 4 ulp.
-        bound = 4 if star else 2
+        # correctly rounded value the oracle takes: measured worst 3 ulp.
+        bound = 3 if star else 2
         assert err.max() <= bound, f"{case} t0={t0} tensor {i}: {err.max()} ulp"
 
 
