@@ -16,7 +16,7 @@ import numpy as np
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libadana_mta.so")
 
-ABI_VERSION = 3
+ABI_VERSION = 4
 CHUNK_ELEMS = 1024
 ALIGN_ELEMS = 4
 MAX_CLASSES = 8
@@ -106,8 +106,9 @@ EXPORTS = (
     "adana_abi_version", "adana_last_error", "adana_step_scalars_init", "adana_manau_scalars_init",
     "adana_plan_layout", "adana_plan_index", "adana_workspace_bytes", "adana_mta_step",
     "adana_mta_step_scaled", "adana_grad_clip_norm", "adana_grad_scale",
-    "adana_order_stats_workspace", "adana_order_stats",
+    "adana_order_stats_workspace", "adana_order_stats", "adana_mta_step_noalloc",
 )
+NOALLOC_SCRATCH_BYTES = 64 << 20
 
 _lib = None
 
@@ -137,6 +138,8 @@ def _declare(L) -> None:
     L.adana_workspace_bytes.restype = ctypes.c_size_t
     L.adana_mta_step.argtypes = [ctypes.POINTER(Plan), P, i32, u32, P, ctypes.c_size_t, P, P]
     L.adana_mta_step.restype = ctypes.c_int
+    L.adana_mta_step_noalloc.argtypes = [ctypes.POINTER(Plan), P, i32, u32, P, P]
+    L.adana_mta_step_noalloc.restype = ctypes.c_int
     L.adana_mta_step_scaled.argtypes = [ctypes.POINTER(Plan), P, i32, u32, P, P, ctypes.c_size_t, P, P]
     L.adana_mta_step_scaled.restype = ctypes.c_int
     L.adana_grad_clip_norm.argtypes = [ctypes.POINTER(Plan), u32, ctypes.c_double, P, ctypes.c_size_t,

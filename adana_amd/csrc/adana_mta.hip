@@ -23,10 +23,12 @@
 // only fused multiply-adds are the ones ATen's lerp_ and addcmul_ perform.
 #include <hip/hip_runtime.h>
 
+#include <atomic>
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <mutex>
 
 #include "adana_mta.h"
 #include "adana_internal.h"
@@ -1341,6 +1343,71 @@ int adana_mta_step_scaled(const adana_plan *plan, const adana_step_scalars *h_sc
     if (!d_grad_scale) return adana_set_error(ADANA_E_INVALID, "adana_mta_step_scaled: null gradient scale");
     return step_impl("adana_mta_step_scaled", plan, h_scalars, n_classes, variant_flags, d_grad_scale,
                      d_workspace, ws_bytes, d_diag, stream);
+}
+
+}  // extern "C"
+
+// ---------------------------------------------------------------------------
+// Allocation-free step: the chunk partials and folds live in a file-scope
+// device array (each GPU the library runs on holds its own copy until the
+// process ends) instead of a caller workspace.  Host code never uses the
+// array's name as an address: the per-device address comes from
+// hipGetSymbolAddress, once per device, on the entry point's first call on
+// that device.  Every call on one GPU shares that GPU's array; the step
+// writes every slot it reads, so nothing needs clearing, but calls that
+// overlap on one GPU (two streams, two threads) race on it.
+// ---------------------------------------------------------------------------
+static __device__ __align__(256) unsigned char scratch[ADANA_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::atomic<void *> g_scratch[kMaxDevices];
+std::mutex g_scratch_mu;
+
+// Device address of the current device's copy of `scratch`.
+int scratch_address(void **out, const char *fn) {
+    int dev = -1;
+    hipError_t err = hipGetDevice(&dev);
+    if (err != hipSuccess) return adana_set_error(ADANA_E_HIP, "%s: hipGetDevice: %s", fn, hipGetErrorString(err));
+    if (dev < 0 || dev >= kMaxDevices) return adana_set_error(ADANA_E_UNSUPPORTED, "%s: device %d", fn, dev);
+    void *p = g_scratch[dev].load(std::memory_order_acquire);
+    if (!p) {
+        std::lock_guard<std::mutex> lock(g_scratch_mu);
+        p = g_scratch[dev].load(std::memory_order_relaxed);
+        if (!p) {
+            err = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+            if (err != hipSuccess || !p)
+                return adana_set_error(ADANA_E_HIP, "%s: hipGetSymbolAddress(scratch) on device %d: %s", fn, dev,
+                                       hipGetErrorString(err));
+            g_scratch[dev].store(p, std::memory_order_release);
+        }
+    }
+    *out = p;
+    return ADANA_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int adana_mta_step_noalloc(const adana_plan *plan, const adana_step_scalars *h_scalars, int32_t n_classes,
+                           uint32_t variant_flags, float *d_diag, void *stream) {
+    const char *fn = "adana_mta_step_noalloc";
+    if (int rc = check_plan(plan, fn)) return rc;
+    const size_t need = workspace_bytes(*plan);
+    if (need > static_cast<size_t>(ADANA_NOALLOC_SCRATCH_BYTES))
+        return adana_set_error(ADANA_E_UNSUPPORTED,
+                               "%s: the list needs %zu bytes of scratch (16 per chunk and tensor, 32 per fold), "
+                               "more than the library's static %zu bytes; call adana_mta_step with a workspace",
+                               fn, need, static_cast<size_t>(ADANA_NOALLOC_SCRATCH_BYTES));
+    if (int rc = check_plan_arrays(*plan, fn)) return rc;
+    if (plan->n_tensors == 0) return ADANA_OK;
+    if (!d_diag || !h_scalars) return adana_set_error(ADANA_E_INVALID, "%s: null pointer argument", fn);
+    void *ws = nullptr;
+    if (int rc = scratch_address(&ws, fn)) return rc;
+    return step_impl(fn, plan, h_scalars, n_classes, variant_flags, nullptr, ws,
+                     static_cast<size_t>(ADANA_NOALLOC_SCRATCH_BYTES), d_diag, stream);
 }
 
 int adana_grad_clip_norm(const adana_plan *plan, uint32_t grad_flags, double max_norm, void *d_workspace,

@@ -42,10 +42,14 @@
  *        tensor to the host and calls compute_tau_order_statistics, :336-376:
  *        np.sort, then the sorted values at ranks floor(1.1^k) - 1 from both
  *        ends): exact values at given ranks, selected on the GPU.
+ *   adana_mta_step_noalloc   <- adana_mta_step with its scratch in a static
+ *        device array (no reference counterpart: for callers that cannot
+ *        allocate).
  *   adana_last_error, adana_abi_version, adana_workspace_bytes,
  *        adana_order_stats_workspace: plumbing (no reference counterpart).
  *
- * Ownership: the library allocates nothing; every device buffer is owned by
+ * Ownership: the library allocates nothing (adana_mta_step_noalloc's static
+ * scratch is part of the loaded code object); every device buffer is owned by
  * the caller (PyTorch's caching allocator in the Python binding) and only
  * borrowed for the call.  Launches are asynchronous on the caller's HIP
  * stream; nothing synchronises the host, except adana_order_stats (host-driven
@@ -63,7 +67,7 @@
 extern "C" {
 #endif
 
-#define ADANA_ABI_VERSION 3
+#define ADANA_ABI_VERSION 4
 
 /* Elements per work chunk (one 256-thread workgroup, one 16-byte vector per
  * thread per array).  Tensors start at multiples of ADANA_ALIGN_ELEMS in the
@@ -271,6 +275,26 @@ int adana_mta_step_scaled(const adana_plan *plan, const adana_step_scalars *h_sc
                           int32_t n_classes, uint32_t variant_flags,
                           const float *d_grad_scale, void *d_workspace,
                           size_t workspace_bytes, float *d_diag, void *stream);
+
+/* Bytes of the library's static device scratch behind adana_mta_step_noalloc
+ * (per GPU, held until the process ends): room for lists of up to about
+ * 4.1 million work chunks (4.2e9 elements), since the step needs 16 bytes per
+ * (chunk, tensor) slot and 32 per fold. */
+#define ADANA_NOALLOC_SCRATCH_BYTES (64u << 20)
+
+/* Device.  adana_mta_step without a workspace argument: the chunk partials
+ * and folds go to a static device array of ADANA_NOALLOC_SCRATCH_BYTES, so
+ * the call allocates nothing (no hipMalloc, no allocating library call).  No
+ * counterpart in the reference: it is for callers that cannot allocate (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  Returns ADANA_E_UNSUPPORTED, with a message, for a list whose
+ * adana_workspace_bytes exceeds ADANA_NOALLOC_SCRATCH_BYTES.  Every call on
+ * one GPU shares that GPU's array: calls that overlap on one GPU (several
+ * streams or threads) race and must be serialised by the caller.  The
+ * array's address on each device is looked up on the first call with that
+ * device current. */
+int adana_mta_step_noalloc(const adana_plan *plan, const adana_step_scalars *h_scalars,
+                           int32_t n_classes, uint32_t variant_flags, float *d_diag, void *stream);
 
 /* Device.  The norm half of torch.nn.utils.clip_grad_norm_(params, max_norm)
  * with norm_type 2 (src/optim/base.py:250-257, src/distributed/backend.py:

@@ -181,6 +181,26 @@ def test_mta_step_rejects_bad_arguments():
     assert L.adana_plan_index(None, 3, 5, None, None) == -1
 
 
+def test_mta_step_noalloc_rejects_bad_arguments():
+    """The allocation-free step checks its arguments, and refuses a list
+    whose scratch would not fit the static array, before any device call."""
+    from adana_amd import _lib
+
+    L = _lib.lib()
+    sc = (_lib.StepScalars * 1)()
+    scp = ctypes.cast(sc, ctypes.c_void_p)
+    assert L.adana_mta_step_noalloc(None, scp, 1, 0, None, None) == -1
+    assert "null plan" in _lib.last_error()
+    pl = _lib.Plan(n_tensors=3, n_chunks=1, n_folds=3)
+    assert L.adana_mta_step_noalloc(ctypes.byref(pl), scp, 1, 0, None, None) == -1
+    assert "null pointer" in _lib.last_error()
+    pl = _lib.Plan(desc=0x1000, vstart=0x1000, chunk_first=0x1000, fold_first=0x1000, n_tensors=3,
+                   n_chunks=_lib.NOALLOC_SCRATCH_BYTES // 16, n_folds=0)
+    assert L.adana_mta_step_noalloc(ctypes.byref(pl), scp, 1, 0, ctypes.c_void_p(0x1000), None) == -3
+    assert "static" in _lib.last_error()
+    assert L.adana_mta_step_noalloc(ctypes.byref(_lib.Plan()), None, 0, 0, None, None) == 0
+
+
 # --------------------------------------------------------------------------
 # Python interface parity with the reference classes
 # --------------------------------------------------------------------------

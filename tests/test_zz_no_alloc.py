@@ -1,0 +1,119 @@
+"""adana_mta_step_noalloc (scratch in the library's static device array)
+against adana_mta_step (scratch in a caller workspace), through the C ABI:
+two calls in a row on the same device, the second over a smaller list, each
+bit for bit equal to the workspace entry point (p, m, v, tau and the five
+diagnostics); and a list too large for the static scratch is refused before
+any launch."""
+import ctypes
+
+import numpy as np
+import pytest
+import torch
+
+pytestmark = [pytest.mark.gpu,
+              pytest.mark.skipif(not torch.cuda.is_available(), reason="needs a ROCm GPU")]
+
+
+class _List:
+    """One tensor list with its device tables, in two identical copies of
+    p / m / v / tau (one per entry point) and shared gradients."""
+
+    def __init__(self, sizes, star, seed):
+        from adana_amd import _lib
+
+        rng = np.random.default_rng(seed)
+        self.sizes = sizes
+        self.star = star
+        p0 = [torch.from_numpy(rng.normal(0, 0.02, n).astype(np.float32)).cuda() for n in sizes]
+        self.copies = []
+        for _ in range(2):
+            c = {"p": [x.clone() for x in p0], "m": [torch.zeros_like(x) for x in p0],
+                 "v": [torch.zeros_like(x) for x in p0], "tau": [torch.zeros_like(x) for x in p0]}
+            self.copies.append(c)
+        self.g = [torch.empty_like(x) for x in p0]
+        self.rng = rng
+        n = len(sizes)
+        vstart, fold_first, self.n_chunks, n_folds = _lib.plan_layout(np.array(sizes, np.int64))
+        self.plans, self.tables, self.chunk_first = [], [], []
+        L = _lib.lib()
+        stream = torch.cuda.current_stream().cuda_stream
+        for c in self.copies:
+            desc = np.zeros(n, _lib.DESC_DTYPE)
+            for i in range(n):
+                desc[i] = (c["p"][i].data_ptr(), self.g[i].data_ptr(), c["m"][i].data_ptr(), c["v"][i].data_ptr(),
+                           c["tau"][i].data_ptr() if star else 0, 0, sizes[i], 0, _lib.DESC_VEC_OK)
+            table = torch.from_numpy(np.concatenate([desc.view(np.uint8), vstart.view(np.uint8),
+                                                     fold_first.view(np.uint8)])).cuda()
+            plan = _lib.Plan(desc=table.data_ptr(), vstart=table.data_ptr() + 64 * n,
+                             fold_first=table.data_ptr() + 64 * n + 8 * (n + 1), n_tensors=n,
+                             n_chunks=self.n_chunks, n_folds=n_folds)
+            cf = torch.empty(max(self.n_chunks, 1), dtype=torch.int32, device="cuda")
+            _lib.check(L.adana_plan_index(ctypes.c_void_p(plan.vstart), n, self.n_chunks,
+                                          ctypes.c_void_p(cf.data_ptr()), ctypes.c_void_p(stream)), "plan_index")
+            plan.chunk_first = cf.data_ptr()
+            self.plans.append(plan)
+            self.tables.append(table)
+            self.chunk_first.append(cf)
+        self.diag = [torch.full((5 * n,), float("nan"), device="cuda") for _ in range(2)]
+        self.ws = torch.empty(_lib.workspace_bytes(self.plans[0]), dtype=torch.uint8, device="cuda")
+        assert _lib.workspace_bytes(self.plans[0]) <= _lib.NOALLOC_SCRATCH_BYTES
+
+    def step(self, t):
+        from adana_amd import _lib
+
+        L = _lib.lib()
+        for gi, n in zip(self.g, self.sizes):
+            gi.copy_(torch.from_numpy(self.rng.normal(0, 1e-3, n).astype(np.float32)))
+        hp = _lib.HParams(peak_lr=1e-3, delta=8.0, kappa=0.85, epsilon=1e-8, weight_decay=0.4, clipsnr=2.0,
+                          wd_ts=10.0, gamma_3_factor=1.0, has_clip=1, wd_decaying=1)
+        sc = (_lib.StepScalars * 1)(_lib.step_scalars(hp, 1e-3, t))
+        flags = _lib.VARIANT_STAR if self.star else 0
+        stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+        _lib.check(L.adana_mta_step(ctypes.byref(self.plans[0]), ctypes.cast(sc, ctypes.c_void_p), 1, flags,
+                                    ctypes.c_void_p(self.ws.data_ptr()), self.ws.numel(),
+                                    ctypes.c_void_p(self.diag[0].data_ptr()), stream), "adana_mta_step")
+        _lib.check(L.adana_mta_step_noalloc(ctypes.byref(self.plans[1]), ctypes.cast(sc, ctypes.c_void_p), 1,
+                                            flags, ctypes.c_void_p(self.diag[1].data_ptr()), stream),
+                   "adana_mta_step_noalloc")
+        torch.cuda.synchronize()
+
+    def assert_equal(self, where):
+        a, b = self.copies
+        keys = ("p", "m", "v") + (("tau",) if self.star else ())
+        for key in keys:
+            for i in range(len(self.sizes)):
+                x, y = a[key][i].cpu().numpy(), b[key][i].cpu().numpy()
+                assert np.array_equal(x.view(np.int32), y.view(np.int32)), (where, key, i)
+        d0, d1 = self.diag[0].cpu().numpy(), self.diag[1].cpu().numpy()
+        assert np.array_equal(d0.view(np.int32), d1.view(np.int32)), (where, d0, d1)
+
+
+def test_noalloc_matches_workspace_entry_point():
+    print("case: adana_mta_step_noalloc vs adana_mta_step, Dana-Star list of 10.1M elements", flush=True)
+    big = _List([1 << 20, 3, 70_000, 9_000_000, 5], star=True, seed=11)
+    for t in (1, 2):
+        big.step(t)
+        big.assert_equal(f"big t={t}")
+    print("case: adana_mta_step_noalloc second call, smaller ADana list", flush=True)
+    small = _List([5000, 17, 1024], star=False, seed=12)
+    for t in (1, 2):
+        small.step(t)
+        small.assert_equal(f"small t={t}")
+
+
+def test_noalloc_rejects_lists_beyond_its_scratch():
+    """A list needing more scratch than the static array gets
+    ADANA_E_UNSUPPORTED and a message, before any device work (the plan's
+    device pointers are never read)."""
+    from adana_amd import _lib
+
+    L = _lib.lib()
+    print("case: adana_mta_step_noalloc refuses an oversized list", flush=True)
+    chunks = _lib.NOALLOC_SCRATCH_BYTES // 16 + 1
+    plan = _lib.Plan(desc=16, vstart=16, fold_first=16, chunk_first=16, n_tensors=1, n_chunks=chunks, n_folds=0)
+    hp = _lib.HParams(peak_lr=1e-3, delta=8.0, kappa=1.0, epsilon=1e-8)
+    sc = (_lib.StepScalars * 1)(_lib.step_scalars(hp, 1e-3, 1))
+    rc = L.adana_mta_step_noalloc(ctypes.byref(plan), ctypes.cast(sc, ctypes.c_void_p), 1, 0,
+                                  ctypes.c_void_p(16), ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+    assert rc == -3
+    assert "static" in _lib.last_error()
