@@ -482,27 +482,128 @@ __device__ __forceinline__ void store_grad1(const void *g, int64_t off, float x)
 // waves would wait on their own stores, which the gfx9 vmcnt counter orders
 // with later loads).  All variants run VEC = 4 (256 threads); VEC = 2 (512
 // threads) is kept compilable for tuning.
+//
+// A chunk inside one tensor (every chunk of a large tensor but its ends) is
+// one uniform segment.  A chunk shared by several tensors (small tensors
+// packed together, or a tensor's tail and the next one's head) is still one
+// pass: each thread finds its own tensor by a binary search over the chunk's
+// tensors, all threads load and store at once, and only the per-tensor
+// partial sums are then reduced segment by segment.
 // ---------------------------------------------------------------------------
+
+// One thread's elements of tensor d from element `off` on (`left` of them
+// remain in the tensor; VEC at most are processed), with their diagnostics
+// terms added to acc.  UNIFORM: every thread of the workgroup works on this
+// tensor and the chunk's part of it starts at element seg0, so the fp32
+// stores go out as buffer stores from that uniform base.
+template <bool STAR, bool GBF16, bool PBF16, int POWK, int VEC, bool UNIFORM>
+__device__ __forceinline__ void thread_elems(const adana_tensor_desc &d, int64_t off, int64_t left, int64_t seg0,
+                                             const ScalarPack &pack, float gs, const PowTab &tab,
+                                             float (&acc)[4]) {
+    const adana_step_scalars &sc = pack.c[d.sclass];
+    const bool scaled = pack.gscale != nullptr;                    // uniform
+    float *pp = static_cast<float *>(d.param) + off;
+    float *mp = d.m + off;
+    float *vp = d.v + off;
+    float *tp = STAR ? d.tau + off : nullptr;
+    const int cnt = left < VEC ? static_cast<int>(left) : VEC;
+    if (cnt == VEC && (d.flags & ADANA_DESC_VEC_OK)) {
+        float P[VEC], G[VEC], M[VEC], V[VEC], T[VEC];
+        ld_n<VEC>(pp, P);
+        load_grad_n<GBF16, VEC>(d.grad, off, G);
+        ld_n<VEC>(mp, M);
+        ld_n<VEC>(vp, V);
+        if constexpr (STAR) {
+            ld_n<VEC>(tp, T);
+        } else {
+#pragma unroll
+            for (int k = 0; k < VEC; ++k) T[k] = 0.0f;
+        }
+        if (scaled) {
+#pragma unroll
+            for (int k = 0; k < VEC; ++k) G[k] = scale_grad<GBF16>(G[k], gs);
+            if (pack.write_grad) store_grad_n<GBF16, VEC>(d.grad, off, G);
+        }
+        update_n<STAR, POWK, VEC>(P, G, M, V, T, sc, tab, acc);
+        if constexpr (UNIFORM && VEC == 4) {
+            const int byte_off = static_cast<int>((off - seg0) * 4);
+            st4_stream(static_cast<float *>(d.param) + seg0, byte_off, P);
+            st4_stream(d.m + seg0, byte_off, M);
+            st4_stream(d.v + seg0, byte_off, V);
+            if constexpr (STAR) st4_stream(d.tau + seg0, byte_off, T);
+        } else {
+            st_n<VEC>(pp, P);
+            st_n<VEC>(mp, M);
+            st_n<VEC>(vp, V);
+            if constexpr (STAR) st_n<VEC>(tp, T);
+        }
+        if constexpr (PBF16) st_bf16_n<VEC>(static_cast<unsigned short *>(d.param_lp) + off, P);
+    } else {
+        // unaligned tensor, or the last (< VEC) elements of a tensor
+        for (int e = 0; e < cnt; ++e) {
+            float mm = mp[e], vv = vp[e], tt = STAR ? tp[e] : 0.0f;
+            float g = load_grad1<GBF16>(d.grad, off + e);
+            if (scaled) {
+                g = scale_grad<GBF16>(g, gs);
+                if (pack.write_grad) store_grad1<GBF16>(d.grad, off + e, g);
+            }
+            const float o = update_elem<STAR, POWK>(pp[e], g, mm, vv, tt, sc, tab, acc);
+            pp[e] = o;
+            mp[e] = mm;
+            vp[e] = vv;
+            if constexpr (STAR) tp[e] = tt;
+            if constexpr (PBF16) static_cast<unsigned short *>(d.param_lp)[off + e] = f32_to_bf16(o);
+        }
+    }
+}
+
+// The workgroup's sums of acc, stored by thread 0 as one float4: a wave
+// reduction, then a fixed-order combine of the waves in LDS.  The LDS slot
+// alternates between calls (par), so no barrier is needed after thread 0 has
+// read it.
+template <int kW>
+__device__ __forceinline__ void block_partial(float (&acc)[4], float (*red)[kW][4], int &par, float4 *dst) {
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    wave_sum4_to_lane63(acc);
+    if (lane == 63) {
+#pragma unroll
+        for (int k = 0; k < 4; ++k) red[par][wave][k] = acc[k];
+    }
+    __syncthreads();
+    if (tid == 0) {
+        float4 q = make_float4(red[par][0][0], red[par][0][1], red[par][0][2], red[par][0][3]);
+#pragma unroll
+        for (int w = 1; w < kW; ++w) {
+            q.x += red[par][w][0];
+            q.y += red[par][w][1];
+            q.z += red[par][w][2];
+            q.w += red[par][w][3];
+        }
+        *dst = q;
+    }
+    par ^= 1;
+}
 
 template <bool STAR, bool GBF16, bool PBF16, int POWK, int VEC>
 __global__ __launch_bounds__(kChunk / VEC) void mta_step_kernel(const adana_tensor_desc *__restrict__ desc,
                                                                 const int64_t *__restrict__ vstart,
                                                                 const int32_t *__restrict__ chunk_first,
                                                                 int32_t n, ScalarPack pack,
-                                                                float *__restrict__ partials) {
+                                                                float *__restrict__ partials,
+                                                                int32_t *__restrict__ counters) {
     constexpr int kThreads = kChunk / VEC;
     constexpr int kW = kThreads / 64;
     __shared__ float red[2][kW][4];
     int par = 0;
     const int tid = threadIdx.x;
-    const int lane = tid & 63;
-    const int wave = tid >> 6;
     const int64_t chunk = blockIdx.x;
     const int64_t lo = chunk * kChunk;
     const int64_t hi = lo + kChunk;
     const int64_t mine = lo + VEC * tid;   // virtual index of this thread's VEC elements
-    const bool scaled = pack.gscale != nullptr;                    // uniform
-    const float gs = scaled ? *pack.gscale : 1.0f;
+    float4 *part4 = reinterpret_cast<float4 *>(partials);
+    // the combine kernel's per-tensor arrival counters start at zero
+    for (int64_t k = chunk * kThreads + tid; k < n; k += static_cast<int64_t>(gridDim.x) * kThreads) counters[k] = 0;
+    const float gs = pack.gscale != nullptr ? *pack.gscale : 1.0f;
     PowTab tab{adana::kLog, adana::kExp2J};
     if constexpr (STAR && pow_tables(POWK)) {
         static_assert(kThreads >= 256, "one thread per table entry");
@@ -517,92 +618,41 @@ __global__ __launch_bounds__(kChunk / VEC) void mta_step_kernel(const adana_tens
         tab = PowTab{s_log, s_exp2j};
     }
 
-    for (int i = chunk_first[chunk]; i < n; ++i) {
-        const int64_t vs = vstart[i];
+    const int i0 = chunk_first[chunk];
+    const int64_t vs0 = vstart[i0];
+    const adana_tensor_desc d0 = desc[i0];
+    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    if (vs0 <= lo && vs0 + d0.numel >= hi) {
+        // the whole chunk lies in tensor i0
+        thread_elems<STAR, GBF16, PBF16, POWK, VEC, true>(d0, mine - vs0, vs0 + d0.numel - mine, lo - vs0, pack, gs,
+                                                          tab, acc);
+        block_partial<kW>(acc, red, par, part4 + chunk + i0);
+        return;
+    }
+    // Shared chunk: its tensors are i0 .. i1 (chunk_first of the next chunk is
+    // the first tensor reaching it, which may also reach into this one).
+    const int i1 = (chunk + 1 < static_cast<int64_t>(gridDim.x)) ? chunk_first[chunk + 1] : n - 1;
+    int l = i0, r = i1;                      // this thread's tensor: the last i with vstart[i] <= mine
+    while (l < r) {
+        const int mid = (l + r + 1) >> 1;
+        if (vstart[mid] <= mine) l = mid; else r = mid - 1;
+    }
+    {
+        const adana_tensor_desc d = desc[l];
+        const int64_t vs = vstart[l];
+        if (mine >= vs && mine < vs + d.numel)
+            thread_elems<STAR, GBF16, PBF16, POWK, VEC, false>(d, mine - vs, vs + d.numel - mine, 0, pack, gs, tab,
+                                                               acc);
+    }
+    // one (chunk, tensor) partial per tensor overlapping the chunk, in order
+    for (int j = i0; j <= i1; ++j) {
+        const int64_t vs = vstart[j];
         if (vs >= hi) break;
-        const adana_tensor_desc d = desc[i];
-        const int64_t ve = vs + d.numel;
-        if (ve <= lo) continue;                                    // uniform across the block
-        const adana_step_scalars &sc = pack.c[d.sclass];
-        float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-        if (mine >= vs && mine < ve) {
-            const int64_t off = mine - vs;                         // multiple of VEC
-            float *pp = static_cast<float *>(d.param) + off;
-            float *mp = d.m + off;
-            float *vp = d.v + off;
-            float *tp = STAR ? d.tau + off : nullptr;
-            const int cnt = (ve - mine) < VEC ? static_cast<int>(ve - mine) : VEC;
-            if (cnt == VEC && (d.flags & ADANA_DESC_VEC_OK)) {
-                float P[VEC], G[VEC], M[VEC], V[VEC], T[VEC];
-                ld_n<VEC>(pp, P);
-                load_grad_n<GBF16, VEC>(d.grad, off, G);
-                ld_n<VEC>(mp, M);
-                ld_n<VEC>(vp, V);
-                if constexpr (STAR) {
-                    ld_n<VEC>(tp, T);
-                } else {
+        if (vs + desc[j].numel <= lo) continue;                    // uniform across the block
+        float a[4];
 #pragma unroll
-                    for (int k = 0; k < VEC; ++k) T[k] = 0.0f;
-                }
-                if (scaled) {
-#pragma unroll
-                    for (int k = 0; k < VEC; ++k) G[k] = scale_grad<GBF16>(G[k], gs);
-                    if (pack.write_grad) store_grad_n<GBF16, VEC>(d.grad, off, G);
-                }
-                update_n<STAR, POWK, VEC>(P, G, M, V, T, sc, tab, acc);
-                if constexpr (VEC == 4) {
-                    const int64_t seg0 = (lo > vs ? lo : vs) - vs;      // uniform
-                    const int byte_off = static_cast<int>((off - seg0) * 4);
-                    st4_stream(static_cast<float *>(d.param) + seg0, byte_off, P);
-                    st4_stream(d.m + seg0, byte_off, M);
-                    st4_stream(d.v + seg0, byte_off, V);
-                    if constexpr (STAR) st4_stream(d.tau + seg0, byte_off, T);
-                } else {
-                    st_n<VEC>(pp, P);
-                    st_n<VEC>(mp, M);
-                    st_n<VEC>(vp, V);
-                    if constexpr (STAR) st_n<VEC>(tp, T);
-                }
-                if constexpr (PBF16) st_bf16_n<VEC>(static_cast<unsigned short *>(d.param_lp) + off, P);
-            } else {
-                // unaligned tensor, or the last (< VEC) elements of a tensor
-                for (int e = 0; e < cnt; ++e) {
-                    float mm = mp[e], vv = vp[e], tt = STAR ? tp[e] : 0.0f;
-                    float g = load_grad1<GBF16>(d.grad, off + e);
-                    if (scaled) {
-                        g = scale_grad<GBF16>(g, gs);
-                        if (pack.write_grad) store_grad1<GBF16>(d.grad, off + e, g);
-                    }
-                    const float o = update_elem<STAR, POWK>(pp[e], g, mm, vv, tt, sc, tab, acc);
-                    pp[e] = o;
-                    mp[e] = mm;
-                    vp[e] = vv;
-                    if constexpr (STAR) tp[e] = tt;
-                    if constexpr (PBF16) static_cast<unsigned short *>(d.param_lp)[off + e] = f32_to_bf16(o);
-                }
-            }
-        }
-        // (chunk, tensor) segment sums: wave reduction, then a fixed-order
-        // combine of the waves in LDS.  The LDS slot alternates between
-        // segments, so no barrier is needed after thread 0 has read it.
-        wave_sum4_to_lane63(acc);
-        if (lane == 63) {
-#pragma unroll
-            for (int k = 0; k < 4; ++k) red[par][wave][k] = acc[k];
-        }
-        __syncthreads();
-        if (tid == 0) {
-            float4 q = make_float4(red[par][0][0], red[par][0][1], red[par][0][2], red[par][0][3]);
-#pragma unroll
-            for (int w = 1; w < kW; ++w) {
-                q.x += red[par][w][0];
-                q.y += red[par][w][1];
-                q.z += red[par][w][2];
-                q.w += red[par][w][3];
-            }
-            reinterpret_cast<float4 *>(partials)[chunk + i] = q;
-        }
-        par ^= 1;
+        for (int k = 0; k < 4; ++k) a[k] = (l == j) ? acc[k] : 0.0f;
+        block_partial<kW>(a, red, par, part4 + chunk + j);
     }
 }
 
@@ -648,65 +698,99 @@ __device__ __forceinline__ void block_sum4(double &s0, double &s1, double &s2, d
     s3 = ((red[0][3] + red[1][3]) + red[2][3]) + red[3][3];
 }
 
-__global__ __launch_bounds__(kBlock) void fold_kernel(const adana_tensor_desc *__restrict__ desc,
-                                                      const int64_t *__restrict__ vstart,
-                                                      const int32_t *__restrict__ fold_first, int32_t n,
-                                                      const float *__restrict__ partials,
-                                                      double4 *__restrict__ folds) {
-    __shared__ double red[kWaves][4];
-    const int64_t j = blockIdx.x;
-    int l = 0, r = n - 1;                       // last tensor with fold_first[i] <= j
-    while (l < r) {
-        const int mid = (l + r + 1) >> 1;
-        if (fold_first[mid] <= j) l = mid; else r = mid - 1;
-    }
-    const int i = l;
-    const int64_t vs = vstart[i], numel = desc[i].numel;
-    const int64_t b0 = vs / kChunk, b1 = (vs + numel - 1) / kChunk;
-    const int64_t lo = b0 + (j - fold_first[i]) * kFold;
-    const int64_t hi = (lo + kFold - 1 < b1) ? lo + kFold - 1 : b1;
-    const float4 *p4 = reinterpret_cast<const float4 *>(partials);
-    float4 q[kFoldPerThread];
-#pragma unroll
-    for (int u = 0; u < kFoldPerThread; ++u) {
-        const int64_t b = lo + u * kBlock + threadIdx.x;
-        q[u] = (b <= hi) ? p4[b + i] : make_float4(0.f, 0.f, 0.f, 0.f);
-    }
-    double s0 = 0.0, s1 = 0.0, s2 = 0.0, s3 = 0.0;
-#pragma unroll
-    for (int u = 0; u < kFoldPerThread; ++u) {
-        s0 += q[u].x; s1 += q[u].y; s2 += q[u].z; s3 += q[u].w;
-    }
-    block_sum4(s0, s1, s2, s3, red);
-    if (threadIdx.x == 0) folds[j] = make_double4(s0, s1, s2, s3);
+// The five diagnostics of tensor i from its four binary64 sums
+// (src/optim/adana.py:146-151, :221-225).
+__device__ __forceinline__ void write_diag(float *diag, int i, double n, double s0, double s1, double s2, double s3) {
+    const float ca = static_cast<float>(s0 / n);         // alpha_factor.mean()
+    const float afm = static_cast<float>(s2 / n);        // mfac.mean()
+    float *o = diag + 5 * static_cast<int64_t>(i);
+    o[0] = ca;
+    o[1] = static_cast<float>(sqrt(s1));                 // grad.norm()
+    o[2] = afm;
+    o[3] = ca / afm;                                     // current_alpha / auto_factor_mean
+    o[4] = static_cast<float>(sqrt(s3));                 // m.norm()
 }
 
-// Stage 2: one wave per tensor sums its folds -- or, for a tensor of at most
-// ADANA_DIRECT_CHUNKS chunks (no folds), its chunk partials directly, in
-// binary64 -- and writes the five diagnostics (src/optim/adana.py:146-151,
-// :221-225).
-__global__ __launch_bounds__(kBlock) void finalize_kernel(const adana_tensor_desc *__restrict__ desc,
-                                                          const int64_t *__restrict__ vstart,
-                                                          const int32_t *__restrict__ fold_first,
-                                                          int32_t n, const float *__restrict__ partials,
-                                                          const double4 *__restrict__ folds,
-                                                          float *__restrict__ diag) {
-    const int lane = threadIdx.x & 63;
-    const int i = blockIdx.x * kWaves + (threadIdx.x >> 6);
-    if (i >= n) return;                                   // whole wave
+// Diagnostics combine: one launch after the main kernel.
+//  * Workgroups [0, n_folds) are fold workgroups: fold j reduces up to
+//    ADANA_FOLD_CHUNKS consecutive chunk partials of one tensor of more than
+//    ADANA_DIRECT_CHUNKS chunks, in binary64 and a fixed order, to folds[j].
+//    The last of a tensor's folds to finish (an arrival counter per tensor,
+//    zeroed by the main kernel; agent-scope acquire/release, so the folds
+//    written on other XCDs are visible) sums the tensor's folds in index
+//    order and writes its diagnostics.
+//  * The workgroups after them take four tensors each, one wave per tensor
+//    of at most ADANA_DIRECT_CHUNKS chunks, summing its chunk partials
+//    directly in binary64.
+// Every sum has a fixed order whichever workgroup finishes last, so the
+// diagnostics are deterministic.
+__global__ __launch_bounds__(kBlock) void combine_kernel(const adana_tensor_desc *__restrict__ desc,
+                                                         const int64_t *__restrict__ vstart,
+                                                         const int32_t *__restrict__ fold_first, int32_t n,
+                                                         int32_t n_folds, const float *__restrict__ partials,
+                                                         double4 *__restrict__ folds, int32_t *__restrict__ counters,
+                                                         float *__restrict__ diag) {
+    __shared__ double red[kWaves][4];
+    __shared__ int is_last;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int64_t b = blockIdx.x;
+    const float4 *p4 = reinterpret_cast<const float4 *>(partials);
+    if (b < n_folds) {
+        const int64_t j = b;
+        int l = 0, r = n - 1;                   // last tensor with fold_first[i] <= j
+        while (l < r) {
+            const int mid = (l + r + 1) >> 1;
+            if (fold_first[mid] <= j) l = mid; else r = mid - 1;
+        }
+        const int i = l;
+        const int64_t vs = vstart[i], numel = desc[i].numel;
+        const int64_t b0 = vs / kChunk, b1 = (vs + numel - 1) / kChunk;
+        const int64_t lo = b0 + (j - fold_first[i]) * kFold;
+        const int64_t hi = (lo + kFold - 1 < b1) ? lo + kFold - 1 : b1;
+        float4 q[kFoldPerThread];
+#pragma unroll
+        for (int u = 0; u < kFoldPerThread; ++u) {
+            const int64_t c = lo + u * kBlock + threadIdx.x;
+            q[u] = (c <= hi) ? p4[c + i] : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+        double s0 = 0.0, s1 = 0.0, s2 = 0.0, s3 = 0.0;
+#pragma unroll
+        for (int u = 0; u < kFoldPerThread; ++u) {
+            s0 += q[u].x; s1 += q[u].y; s2 += q[u].z; s3 += q[u].w;
+        }
+        block_sum4(s0, s1, s2, s3, red);
+        const int f0 = fold_first[i], f1 = fold_first[i + 1];
+        if (threadIdx.x == 0) {
+            folds[j] = make_double4(s0, s1, s2, s3);
+            const int prev = __hip_atomic_fetch_add(&counters[i], 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+            is_last = (prev == f1 - f0 - 1);
+        }
+        __syncthreads();
+        if (!is_last || wave != 0) return;
+        s0 = s1 = s2 = s3 = 0.0;
+        for (int f = f0 + lane; f < f1; f += 64) {
+            const double4 t = folds[f];
+            s0 += t.x; s1 += t.y; s2 += t.z; s3 += t.w;
+        }
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) {
+            s0 += __shfl_xor(s0, o, 64);
+            s1 += __shfl_xor(s1, o, 64);
+            s2 += __shfl_xor(s2, o, 64);
+            s3 += __shfl_xor(s3, o, 64);
+        }
+        if (lane == 0) write_diag(diag, i, static_cast<double>(numel), s0, s1, s2, s3);
+        return;
+    }
+    const int i = static_cast<int>((b - n_folds) * kWaves + wave);
+    if (i >= n || fold_first[i + 1] > fold_first[i]) return;           // whole wave
     double s0 = 0.0, s1 = 0.0, s2 = 0.0, s3 = 0.0;
     const int64_t numel = desc[i].numel;
-    if (fold_first[i + 1] > fold_first[i]) {
-        for (int f = fold_first[i] + lane; f < fold_first[i + 1]; f += 64) {
-            const double4 q = folds[f];
-            s0 += q.x; s1 += q.y; s2 += q.z; s3 += q.w;
-        }
-    } else if (numel > 0) {
-        const float4 *p4 = reinterpret_cast<const float4 *>(partials);
+    if (numel > 0) {
         const int64_t b0 = vstart[i] / kChunk, b1 = (vstart[i] + numel - 1) / kChunk;
 #pragma unroll 8
-        for (int64_t b = b0 + lane; b <= b1; b += 64) {
-            const float4 q = p4[b + i];
+        for (int64_t c = b0 + lane; c <= b1; c += 64) {
+            const float4 q = p4[c + i];
             s0 += q.x; s1 += q.y; s2 += q.z; s3 += q.w;
         }
     }
@@ -717,17 +801,7 @@ __global__ __launch_bounds__(kBlock) void finalize_kernel(const adana_tensor_des
         s2 += __shfl_xor(s2, o, 64);
         s3 += __shfl_xor(s3, o, 64);
     }
-    if (lane == 0) {
-        const double nd = static_cast<double>(desc[i].numel);
-        const float ca = static_cast<float>(s0 / nd);     // alpha_factor.mean()
-        const float afm = static_cast<float>(s2 / nd);    // mfac.mean()
-        float *o = diag + 5 * static_cast<int64_t>(i);
-        o[0] = ca;
-        o[1] = static_cast<float>(sqrt(s1));              // grad.norm()
-        o[2] = afm;
-        o[3] = ca / afm;                                  // current_alpha / auto_factor_mean
-        o[4] = static_cast<float>(sqrt(s3));              // m.norm()
-    }
+    if (lane == 0) write_diag(diag, i, static_cast<double>(numel), s0, s1, s2, s3);
 }
 
 // ---------------------------------------------------------------------------
@@ -833,7 +907,8 @@ __global__ __launch_bounds__(kBlock) void grad_sumsq_kernel(const adana_tensor_d
     for (int c = 0; c < nc; ++c) sumsq_chunk<GBF16>(desc, vstart, chunk_first[c0 + c], n, c0 + c, partials, red);
 }
 
-// Stage 1 of the norm combine: like fold_kernel, for one binary64 sum.
+// Stage 1 of the norm combine: like the fold workgroups of combine_kernel, for one
+// binary64 sum.
 __global__ __launch_bounds__(kBlock) void sumsq_fold_kernel(const adana_tensor_desc *__restrict__ desc,
                                                             const int64_t *__restrict__ vstart,
                                                             const int32_t *__restrict__ fold_first, int32_t n,
@@ -959,13 +1034,17 @@ __global__ __launch_bounds__(kBlock) void grad_scale_kernel(const adana_tensor_d
 }
 
 // Workspace layout: chunk partials (float4 per (chunk, tensor) slot), then the
-// folds (double4 each), 256-byte aligned.
+// folds (double4 each), then the combine's arrival counters (int32 per
+// tensor), each part 256-byte aligned.
 size_t partials_bytes(const adana_plan &pl) {
     return static_cast<size_t>(pl.n_chunks + pl.n_tensors) * 16;
 }
 size_t folds_offset(const adana_plan &pl) { return (partials_bytes(pl) + 255) / 256 * 256; }
+size_t counters_offset(const adana_plan &pl) {
+    return (folds_offset(pl) + static_cast<size_t>(pl.n_folds) * 32 + 255) / 256 * 256;
+}
 size_t workspace_bytes(const adana_plan &pl) {
-    return folds_offset(pl) + static_cast<size_t>(pl.n_folds) * 32;
+    return counters_offset(pl) + static_cast<size_t>(pl.n_tensors) * 4;
 }
 
 // Residency cap.  The step reaches the highest HBM throughput with 4 (fp32
@@ -1021,36 +1100,37 @@ size_t lds_for_cap(int wgs, int64_t n_chunks) {
 
 template <bool STAR, bool GBF16, bool PBF16, int POWK>
 void launch_main(int64_t n_chunks, hipStream_t st, const adana_tensor_desc *d, const int64_t *vs,
-                 const int32_t *cf, int32_t n, const ScalarPack &pack, float *partials) {
+                 const int32_t *cf, int32_t n, const ScalarPack &pack, float *partials, int32_t *counters) {
     constexpr int kVec = 4;
     const bool small_tensors = n_chunks < 64 * static_cast<int64_t>(n);
     const size_t lds = lds_for_cap(residency_cap<STAR, PBF16, POWK>(small_tensors), n_chunks);
     hipLaunchKernelGGL((mta_step_kernel<STAR, GBF16, PBF16, POWK, kVec>), dim3(static_cast<unsigned>(n_chunks)),
-                       dim3(kChunk / kVec), static_cast<unsigned>(lds), st, d, vs, cf, n, pack, partials);
+                       dim3(kChunk / kVec), static_cast<unsigned>(lds), st, d, vs, cf, n, pack, partials,
+                       counters);
 }
 
 template <bool STAR, bool GBF16, bool PBF16>
 void launch_pow(int powk, int64_t n_chunks, hipStream_t st, const adana_tensor_desc *d,
                 const int64_t *vs, const int32_t *cf, int32_t n, const ScalarPack &pack,
-                float *partials) {
+                float *partials, int32_t *counters) {
     if constexpr (!STAR) {
         // ADana's (1 + t) ** (1 - kappa) is a host scalar: no per-element pow
-        launch_main<false, GBF16, PBF16, POW_ONE>(n_chunks, st, d, vs, cf, n, pack, partials);
+        launch_main<false, GBF16, PBF16, POW_ONE>(n_chunks, st, d, vs, cf, n, pack, partials, counters);
     } else if (powk == POW_GENERAL) {
-        launch_main<true, GBF16, PBF16, POW_GENERAL>(n_chunks, st, d, vs, cf, n, pack, partials);
+        launch_main<true, GBF16, PBF16, POW_GENERAL>(n_chunks, st, d, vs, cf, n, pack, partials, counters);
     } else if (powk == POW_ONE) {
-        launch_main<true, GBF16, PBF16, POW_ONE>(n_chunks, st, d, vs, cf, n, pack, partials);
+        launch_main<true, GBF16, PBF16, POW_ONE>(n_chunks, st, d, vs, cf, n, pack, partials, counters);
     } else if (powk == POW_SPECIAL) {
-        launch_main<true, GBF16, PBF16, POW_SPECIAL>(n_chunks, st, d, vs, cf, n, pack, partials);
+        launch_main<true, GBF16, PBF16, POW_SPECIAL>(n_chunks, st, d, vs, cf, n, pack, partials, counters);
     } else if constexpr (!GBF16 && !PBF16) {        // Manau's branch: float32 only
         if (powk == POW_MANAU_GENERAL) {
-            launch_main<true, false, false, POW_MANAU_GENERAL>(n_chunks, st, d, vs, cf, n, pack, partials);
+            launch_main<true, false, false, POW_MANAU_GENERAL>(n_chunks, st, d, vs, cf, n, pack, partials, counters);
         } else if (powk == POW_MANAU_ONE) {
-            launch_main<true, false, false, POW_MANAU_ONE>(n_chunks, st, d, vs, cf, n, pack, partials);
+            launch_main<true, false, false, POW_MANAU_ONE>(n_chunks, st, d, vs, cf, n, pack, partials, counters);
         } else if (powk == POW_MANAU_SPECIAL) {
-            launch_main<true, false, false, POW_MANAU_SPECIAL>(n_chunks, st, d, vs, cf, n, pack, partials);
+            launch_main<true, false, false, POW_MANAU_SPECIAL>(n_chunks, st, d, vs, cf, n, pack, partials, counters);
         } else {
-            launch_main<true, false, false, POW_MANAU_MK4>(n_chunks, st, d, vs, cf, n, pack, partials);
+            launch_main<true, false, false, POW_MANAU_MK4>(n_chunks, st, d, vs, cf, n, pack, partials, counters);
         }
     }
 }
@@ -1279,6 +1359,7 @@ int step_impl(const char *fn, const adana_plan *plan, const adana_step_scalars *
     hipStream_t st = static_cast<hipStream_t>(stream);
     float *partials = static_cast<float *>(d_workspace);
     double4 *folds = reinterpret_cast<double4 *>(static_cast<char *>(d_workspace) + folds_offset(pl));
+    int32_t *counters = reinterpret_cast<int32_t *>(static_cast<char *>(d_workspace) + counters_offset(pl));
     const bool star = variant_flags & ADANA_VARIANT_STAR;
     const bool gb = variant_flags & ADANA_GRAD_BF16;
     const bool pb = variant_flags & ADANA_PARAM_BF16;
@@ -1305,7 +1386,8 @@ int step_impl(const char *fn, const adana_plan *plan, const adana_step_scalars *
         int powk = all_general ? POW_GENERAL : (all_one ? POW_ONE : POW_SPECIAL);
         if (manau) powk = mk4_trivial ? powk + POW_MANAU_GENERAL : POW_MANAU_MK4;
 #define ADANA_LAUNCH(S, G, P) \
-        launch_pow<S, G, P>(powk, pl.n_chunks, st, pl.desc, pl.vstart, pl.chunk_first, n, pack, partials)
+        launch_pow<S, G, P>(powk, pl.n_chunks, st, pl.desc, pl.vstart, pl.chunk_first, n, pack, partials, \
+                            counters)
         if (star || manau) {
             if (gb) { if (pb) ADANA_LAUNCH(true, true, true); else ADANA_LAUNCH(true, true, false); }
             else    { if (pb) ADANA_LAUNCH(true, false, true); else ADANA_LAUNCH(true, false, false); }
@@ -1316,14 +1398,11 @@ int step_impl(const char *fn, const adana_plan *plan, const adana_step_scalars *
 #undef ADANA_LAUNCH
         if (int rc = launch_status(fn, "main")) return rc;
     }
-    if (pl.n_folds > 0) {
-        hipLaunchKernelGGL(fold_kernel, dim3(static_cast<unsigned>(pl.n_folds)), dim3(kBlock), 0, st,
-                           pl.desc, pl.vstart, pl.fold_first, n, partials, folds);
-        if (int rc = launch_status(fn, "fold")) return rc;
-    }
-    hipLaunchKernelGGL(finalize_kernel, dim3(static_cast<unsigned>((n + kWaves - 1) / kWaves)), dim3(kBlock),
-                       0, st, pl.desc, pl.vstart, pl.fold_first, n, partials, folds, d_diag);
-    return launch_status(fn, "finalize");
+    const int64_t combine_wgs = pl.n_folds + (n + kWaves - 1) / kWaves;
+    hipLaunchKernelGGL(combine_kernel, dim3(static_cast<unsigned>(combine_wgs)), dim3(kBlock), 0, st, pl.desc,
+                       pl.vstart, pl.fold_first, n, static_cast<int32_t>(pl.n_folds), partials, folds, counters,
+                       d_diag);
+    return launch_status(fn, "combine");
 }
 
 }  // namespace

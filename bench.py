@@ -532,7 +532,7 @@ def manau_bench(args):
         "full_manau_step_ms": round(full_wall, 3),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": "mta_step_kernel (Manau variant) + fold_kernel + finalize_kernel"},
+                     "kernel": "mta_step_kernel (Manau variant) + combine_kernel"},
     }
     del opt, params, groups
     torch.cuda.empty_cache()
@@ -705,9 +705,9 @@ def main():
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": traffic,
                      "kernel": ("grad_sumsq_kernel + sumsq_fold_kernel + clip_finalize_kernel + "
-                                "mta_step_kernel + fold_kernel + finalize_kernel (events bracket one step)"
+                                "mta_step_kernel + combine_kernel (events bracket one step)"
                                 if w.get("clip") else
-                                "mta_step_kernel + fold_kernel + finalize_kernel (events bracket one step)")},
+                                "mta_step_kernel + combine_kernel (events bracket one step)")},
     }
     del opt, params
     torch.cuda.empty_cache()

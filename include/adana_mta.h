@@ -251,8 +251,8 @@ size_t adana_workspace_bytes(const adana_plan *plan);
  *   h_scalars   host array of n_classes scalar classes (passed by value to
  *               the kernel; no host-to-device copy)
  *   d_workspace device scratch of at least adana_workspace_bytes(plan) bytes
- *               (per-chunk partial sums and their folds; contents on entry
- *               are ignored)
+ *               (per-chunk partial sums, their folds and one arrival counter
+ *               per tensor; contents on entry are ignored)
  *   d_diag      device float[5 * n_tensors]: per tensor current_alpha,
  *               gradient_norm, auto_factor_mean, current_kappa_factor,
  *               m_norm (src/optim/adana.py:221-225)
@@ -279,7 +279,7 @@ int adana_mta_step_scaled(const adana_plan *plan, const adana_step_scalars *h_sc
 /* Bytes of the library's static device scratch behind adana_mta_step_noalloc
  * (per GPU, held until the process ends): room for lists of up to about
  * 4.1 million work chunks (4.2e9 elements), since the step needs 16 bytes per
- * (chunk, tensor) slot and 32 per fold. */
+ * (chunk, tensor) slot, 32 per fold and 4 per tensor. */
 #define ADANA_NOALLOC_SCRATCH_BYTES (64u << 20)
 
 /* Device.  adana_mta_step without a workspace argument: the chunk partials

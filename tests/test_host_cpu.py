@@ -150,7 +150,10 @@ def test_workspace_bytes():
     from adana_amd import _lib
 
     pl = _lib.Plan(n_tensors=10, n_chunks=100, n_folds=12)
-    assert _lib.workspace_bytes(pl) == (110 * 16 + 255) // 256 * 256 + 12 * 32
+    # chunk partials, then folds, then one arrival counter per tensor, each 256-byte aligned
+    folds_at = (110 * 16 + 255) // 256 * 256
+    counters_at = (folds_at + 12 * 32 + 255) // 256 * 256
+    assert _lib.workspace_bytes(pl) == counters_at + 10 * 4
 
 
 def test_mta_step_rejects_bad_arguments():
