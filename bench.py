@@ -248,7 +248,7 @@ def master_ceiling(n_elems, reps=5):
 
     import torch
 
-    lib = ctypes.CDLL(os.path.join(ROOT, "adana_amd", "libadana_probe.so"))
+    lib = ctypes.CDLL(os.path.join(ROOT, "probes", "libadana_probe.so"))
     fn = lib.adana_probe_stream_master
     fn.argtypes = [ctypes.c_void_p] * 5 + [ctypes.c_int64, ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p]
     fn.restype = ctypes.c_int
@@ -293,14 +293,14 @@ def stream_ceiling(n_elems, reps=5, star=True):
     5 fp32 arrays read and 4 written back in place (Dana-Star: p, g, m, v,
     tau), or 4 read and 3 written back (fp32 ADana: p, g, m, v), with the step
     kernel's tiles, load/store policies and residency cap
-    (adana_amd/csrc/stream_probe.hip), at the workload's element count; the
+    (probes/stream_probe.hip), at the workload's element count; the
     better of 3 and 4 resident workgroups per CU.  Also a STREAM copy of the
     same element count in the same style (the better of uncapped and 6)."""
     import ctypes
 
     import torch
 
-    lib = ctypes.CDLL(os.path.join(ROOT, "adana_amd", "libadana_probe.so"))
+    lib = ctypes.CDLL(os.path.join(ROOT, "probes", "libadana_probe.so"))
     fn = lib.adana_probe_stream_5r4w if star else lib.adana_probe_stream_4r3w
     fn.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p]
     fn.restype = ctypes.c_int
@@ -363,6 +363,89 @@ def stream_ceiling(n_elems, reps=5, star=True):
     copy = {"achieved": round(best_copy[0], 2), "frac": round(best_copy[0] / HBM_PEAK_GBS, 4),
             "wgs_per_cu": best_copy[1], "probe": f"STREAM copy of {n} fp32 elements, same access style"}
     return mix, copy
+
+
+def stream_sweep(args):
+    """The memory system's ceiling for the north-star step's access pattern.
+
+    The step streams 5 fp32 arrays in and 4 back out (36 B per element) over
+    2.65e9 elements.  This workload times that pattern without arithmetic
+    (probes/stream_probe.hip) in every launch shape tried, on arrays of the
+    north-star size, in a fixed launch order so that a ``rocprofv3 --pmc``
+    run over the same command can attribute every dispatch:
+      * one-shot workgroups (the step's shape) at 1..8 resident workgroups per
+        CU and uncapped;
+      * the wave-specialised persistent kernel (loader wave + direct-to-LDS
+        ring; stages, compute waves, workgroups per CU);
+      * the same five arrays read only and four written only, and a copy.
+    Each configuration is launched 1 + reps times (one warm-up), in two
+    rounds; the JSON line lists the launch order and each configuration's
+    best median."""
+    import ctypes
+
+    import torch
+
+    lib = ctypes.CDLL(os.path.join(ROOT, "probes", "libadana_probe.so"))
+    P, I64, INT = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int
+    for name in ("adana_probe_stream_5r4w", "adana_probe_stream_5r0w", "adana_probe_stream_0r4w"):
+        getattr(lib, name).argtypes = [P, I64, P, INT, P]
+        getattr(lib, name).restype = INT
+    lib.adana_probe_stream_5r4w_ws.argtypes = [P, I64, P, INT, INT, INT, P]
+    lib.adana_probe_stream_5r4w_ws.restype = INT
+    lib.adana_probe_copy.argtypes = [P, P, I64, P, INT, P]
+    lib.adana_probe_copy.restype = INT
+    n = 2645527040 // 1024 * 1024
+    arrays = [torch.zeros(n, device="cuda:0") for _ in range(5)]
+    partials = torch.empty(n // 1024 * 4, device="cuda:0")
+    ptrs = (ctypes.c_void_p * 5)(*[a.data_ptr() for a in arrays])
+    st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    part = ctypes.c_void_p(partials.data_ptr())
+    a0, a1 = ctypes.c_void_p(arrays[0].data_ptr()), ctypes.c_void_p(arrays[1].data_ptr())
+    cfgs = []                                   # (name, bytes per launch, launch)
+    for cap in (1, 2, 3, 4, 5, 6, 7, 8, 0):
+        cfgs.append((f"5r4w one-shot cap {cap or 'none'}", 36 * n,
+                     lambda cap=cap: lib.adana_probe_stream_5r4w(ptrs, n, part, cap, st)))
+    for stages, cw, g in ((3, 4, 1), (3, 4, 2), (4, 4, 1), (3, 8, 1)):
+        cfgs.append((f"5r4w wave-specialised stages {stages} compute waves {cw} wgs/CU {g}", 36 * n,
+                     lambda a=(stages, cw, g): lib.adana_probe_stream_5r4w_ws(ptrs, n, part, a[0], a[1], a[2], st)))
+    for cap in (3, 4, 0):
+        cfgs.append((f"5r0w read-only cap {cap or 'none'}", 20 * n,
+                     lambda cap=cap: lib.adana_probe_stream_5r0w(ptrs, n, part, cap, st)))
+    for cap in (3, 4, 0):
+        cfgs.append((f"0r4w write-only cap {cap or 'none'}", 16 * n,
+                     lambda cap=cap: lib.adana_probe_stream_0r4w(ptrs, n, part, cap, st)))
+    for cap in (4, 0):
+        cfgs.append((f"1r1w copy cap {cap or 'none'}", 8 * n,
+                     lambda cap=cap: lib.adana_probe_copy(a0, a1, n, part, cap, st)))
+    reps = max(2, args.steps)
+    best = {}
+    order = []
+    for rnd in range(2):
+        for name, nbytes, fn in cfgs:
+            print(f"[bench] stream_sweep round {rnd}: {name}", file=sys.stderr, flush=True)
+            ev = [torch.cuda.Event(enable_timing=True) for _ in range(reps + 1)]
+            if fn() != 0:
+                raise RuntimeError(f"probe launch failed: {name}")
+            stream = torch.cuda.current_stream()
+            for k in range(reps):
+                ev[k].record(stream)
+                if fn() != 0:
+                    raise RuntimeError(f"probe launch failed: {name}")
+            ev[-1].record(stream)
+            torch.cuda.synchronize()
+            order.append([name, 1 + reps])
+            ms = float(np.median([ev[k].elapsed_time(ev[k + 1]) for k in range(reps)]))
+            tbs = nbytes / (ms * 1e-3) / 1e12
+            if name not in best or tbs > best[name]["TB/s"]:
+                best[name] = {"TB/s": round(tbs, 3), "ms": round(ms, 3), "frac": round(tbs * 1e3 / HBM_PEAK_GBS, 4)}
+    top = max((v["TB/s"], k) for k, v in best.items() if k.startswith("5r4w"))
+    print(json.dumps({"metric": "5-read/4-write stream ceiling at the north-star size (TB/s)", "value": top[0],
+                      "unit": "TB/s", "n_gpus": 1, "steps": reps, "warmup": 1, "ms_per_step": best[top[1]]["ms"],
+                      "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+                      "data": "synthetic (zeros)",
+                      "config": {"workload": "stream_sweep", "elements": n, "best": top[1]},
+                      "configs": best, "launch_order": order}), flush=True)
+    return 0
 
 
 def consumer_bench(args):
@@ -567,7 +650,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--workload", default="north_star",
                     choices=["north_star", "north_star_clip", "c1", "c2", "c3", "c4", "c5",
-                             "copy_probe", "tau_stats", "diag_readout", "manau"])
+                             "copy_probe", "tau_stats", "diag_readout", "manau", "stream_sweep"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-ceiling-probe", action="store_true",
                     help="skip the 5-read/4-write stream probe reported as roofline.mix_ceiling")
@@ -589,6 +672,8 @@ def main():
         return consumer_bench(args)
     if args.workload == "manau":
         return manau_bench(args)
+    if args.workload == "stream_sweep":
+        return stream_sweep(args)
     w = workload(args.workload)
     print(f"[bench] workload {w['name']} ({w['optimizer']}): building on cuda:0", file=sys.stderr,
           flush=True)
