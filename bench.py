@@ -20,9 +20,10 @@ Prints ONE JSON line.  ``value`` is the whole-step throughput in algorithmic
 HBM GB/s (bytes the update must move per element x elements / wall-clock ms
 per step, host work included).  ``roofline.achieved`` uses the device time of
 the step's kernels, measured with HIP events recorded on the stream they are
-launched on.  ``cpu_baseline`` times the CPU oracle (a C restatement of the
-reference step, OpenMP over the host cores) on a bounded sample of the same
-workload.
+launched on.  ``cpu_baseline`` times the reference's step restated as torch eager ops over
+CPU tensors (oracle/torch_ref.py, the reference's per-tensor loop) on the
+host's cores on a bounded sample of the same workload, with the C oracle
+(OpenMP) beside it.
 """
 from __future__ import annotations
 
@@ -168,52 +169,92 @@ def build_gpu(w, seed=0):
     return opt, params
 
 
-def cpu_baseline(w, target_s=10.0, max_elems=1 << 26):
-    """Time the CPU oracle on the first tensors of the workload (up to
-    max_elems elements), one step per repetition, for about target_s seconds."""
-    from oracle import oracle as O
-
-    cores = len(os.sched_getaffinity(0))
-    cores = min(cores, int(os.environ.get("OMP_NUM_THREADS", cores)), 16)
-    threads = O.set_threads(cores)
-    rng = np.random.default_rng(3)
-    shapes = [s for shapes in w["groups"] for s in shapes]
-    arrays, total = [], 0
-    for s in shapes:
-        n = int(np.prod(s))
-        if total + n > max_elems:
-            n = max_elems - total
+def _sample_shapes(w, max_elems):
+    """The workload's first tensors (flattened), up to max_elems elements in
+    all, the last one cut short if needed."""
+    out, total = [], 0
+    for s in (s for shapes in w["groups"] for s in shapes):
+        n = min(int(np.prod(s)), max_elems - total)
         if n <= 0:
             break
-        arrays.append(n)
+        out.append(n)
         total += n
-    ps = [rng.normal(0, 0.02, n).astype(np.float32) for n in arrays]
-    gs = [rng.normal(0, 1e-3, n).astype(np.float32) for n in arrays]
-    if w["master"]:
-        ps = [O.f32_to_bf16(x) for x in ps]
-        gs = [O.f32_to_bf16(x) for x in gs]
+    return out, total
+
+
+def cpu_threads() -> int:
+    """Host threads for the CPU baselines: the process's CPU affinity, capped
+    by OMP_NUM_THREADS when it is set (the GPU box sets it to its CPU share)."""
+    cores = len(os.sched_getaffinity(0))
+    if os.environ.get("OMP_NUM_THREADS", "").isdigit():
+        cores = min(cores, int(os.environ["OMP_NUM_THREADS"]))
+    return max(cores, 1)
+
+
+def cpu_baseline(w, target_s=10.0, max_elems=1 << 25):
+    """The reference's CPU step, timed on the host's cores on a bounded sample
+    of the workload (its first tensors, up to max_elems elements): the step
+    restated as torch eager ops over CPU tensors with the reference's
+    per-tensor loop (oracle/torch_ref.py: src/optim/adana.py:162-225,
+    src/optim/dana_star_mk4.py:215-294; bit-identical to the reference's own
+    eager run, tests/test_torch_restatement.py), torch.set_num_threads over
+    the cores.  Beside it, the C oracle (oracle/adana_oracle.c, OpenMP) on the
+    same sample.  bf16-master workloads time the float32 master update."""
+    import torch
+
+    from oracle import oracle as O
+    from oracle.torch_ref import TorchRefGroup, TorchRefOptimizer
+
+    cores = cpu_threads()
+    sizes, total = _sample_shapes(w, max_elems)
+    all_elems = sum(int(np.prod(s)) for shapes in w["groups"] for s in shapes)
     hp = w["hp"]
-    opt = O.OracleOptimizer(groups=[O.OracleGroup(params=ps, lr=hp["lr"], delta=hp["delta"],
-                                                  epsilon=hp["epsilon"],
+    rng = np.random.default_rng(3)
+    ps = [rng.normal(0, 0.02, n).astype(np.float32) for n in sizes]
+    gs = [rng.normal(0, 1e-3, n).astype(np.float32) for n in sizes]
+    frac = total / all_elems
+    bpe = bytes_per_elem(w)
+
+    def timed(step):
+        step()                                    # warm-up: first touch of the state
+        reps, t0 = 0, time.perf_counter()
+        while True:
+            step()
+            reps += 1
+            el = time.perf_counter() - t0
+            if el >= target_s or reps >= 50:
+                return el / reps, reps
+
+    prev = torch.get_num_threads()
+    torch.set_num_threads(cores)
+    tp = [torch.from_numpy(x.copy()) for x in ps]
+    tg = [[torch.from_numpy(x) for x in gs]]
+    ref = TorchRefOptimizer(groups=[TorchRefGroup(params=tp, lr=hp["lr"], delta=hp["delta"], epsilon=hp["epsilon"],
                                                   weight_decay=hp["weight_decay"])],
-                            star=w["star"], peak_lr=hp["lr"], kappa=hp["kappa"],
-                            clipsnr=hp["clipsnr"], wd_decaying=hp["wd_decaying"],
-                            wd_ts=hp["wd_ts"], master=w["master"])
-    opt.step([gs])                       # warm-up: first touch of the state
-    reps, t0 = 0, time.perf_counter()
-    while True:
-        opt.step([gs])
-        reps += 1
-        el = time.perf_counter() - t0
-        if el >= target_s or reps >= 50:
-            break
-    per_step = el / reps
-    gbs = total * bytes_per_elem(w) / per_step / 1e9
-    return {"value": round(gbs, 3), "unit": "GB/s", "cores": threads, "kind": "port", "cpu_model": cpu_model(),
-            "sample": f"{total} elements (first {len(arrays)} tensors of the list), "
-                      f"{reps} timed steps after 1 warm-up, {per_step * 1e3:.1f} ms/step, "
-                      f"oracle/adana_oracle.c with {threads} OpenMP threads",
-            "ms_per_step_sample": round(per_step * 1e3, 3)}
+                            star=w["star"], peak_lr=hp["lr"], kappa=hp["kappa"], clipsnr=hp["clipsnr"],
+                            wd_decaying=hp["wd_decaying"], wd_ts=hp["wd_ts"])
+    per_t, reps_t = timed(lambda: ref.step(tg))
+    torch.set_num_threads(prev)
+    del tp, tg, ref
+
+    threads = O.set_threads(cores)
+    opt = O.OracleOptimizer(groups=[O.OracleGroup(params=[x.copy() for x in ps], lr=hp["lr"], delta=hp["delta"],
+                                                  epsilon=hp["epsilon"], weight_decay=hp["weight_decay"])],
+                            star=w["star"], peak_lr=hp["lr"], kappa=hp["kappa"], clipsnr=hp["clipsnr"],
+                            wd_decaying=hp["wd_decaying"], wd_ts=hp["wd_ts"])
+    per_c, reps_c = timed(lambda: opt.step([gs]))
+    sample = (f"{total} of the workload's {all_elems} elements ({100 * frac:.2f}%): its first {len(sizes)} tensors, "
+              f"fp32")
+    return {"value": round(total * bpe / per_t / 1e9, 3), "unit": "GB/s", "cores": cores, "kind": "port",
+            "cpu_model": cpu_model(),
+            "sample": f"{sample}; oracle/torch_ref.py (the reference's step() as torch eager ops, per-tensor "
+                      f"loop) with torch.set_num_threads({cores}) (the process's CPU affinity, capped by "
+                      f"OMP_NUM_THREADS); {reps_t} timed steps after 1 warm-up, {per_t * 1e3:.1f} ms/step",
+            "sample_fraction": round(frac, 5), "ms_per_step_sample": round(per_t * 1e3, 3),
+            "c_oracle": {"value": round(total * bpe / per_c / 1e9, 3), "unit": "GB/s", "cores": threads,
+                         "ms_per_step_sample": round(per_c * 1e3, 3),
+                         "sample": f"same sample, oracle/adana_oracle.c with {threads} OpenMP threads, "
+                                   f"{reps_c} timed steps"}}
 
 
 def copy_probe(steps):
@@ -622,7 +663,7 @@ def manau_bench(args):
     if not args.no_cpu_baseline:
         from oracle import oracle as O
 
-        threads = O.set_threads(min(len(os.sched_getaffinity(0)), int(os.environ.get("OMP_NUM_THREADS", 16)), 16))
+        threads = O.set_threads(cpu_threads())
         rng = np.random.default_rng(3)
         n = 1 << 25
         arrs = [rng.normal(0, 0.02, n).astype(np.float32), rng.normal(0, 1e-3, n).astype(np.float32)]

@@ -6,10 +6,13 @@ workloads' own lists and hyper-parameters (bench.workload):
   * c4: ADana on the same list with bf16 parameters, fp32 master/m/v and
     bf16 gradients;
   * c3: Dana-Star-MK4, 1,311,082,496 parameters (d_model 2048, 24 layers);
-  * c2: Dana-MK4, 50,938,880 parameters in 67 tensors, 1-D gradients x 0.1;
+  * c2: Dana-MK4, 50,938,880 parameters in 67 tensors, 1-D gradients x 0.1,
+    under the bench's warm-up/cosine lr schedule (a new group lr every step);
   * c5: Dana-Star-MK4 over 10,000 log-uniform tensors (94,406,322
-    parameters), 5% of them with all-zero gradients (64 sampled elements per
-    tensor).
+    parameters), 5% of them with all-zero gradients (256 sampled elements
+    per tensor).
+Ten steps each, so every run crosses t = delta = 8, where alpha = 0.5 and
+ATen's lerp takes its second branch.
 Two weight-decay groups as src/models/base.py:503-561; launcher
 hyper-parameters as scripts/launch.sh:36-40,188-223.
 
@@ -21,8 +24,13 @@ their inputs exactly.  Bars:
   * sampled Dana-Star p: bit-exact except the pow's rare rounding-boundary
     cases (at most STAR_HARD_CASES per tensor per step, each within
     STAR_P_ULPS ulps of max(|p_before|, |p_after|));
-  * gradient_norm and m_norm of every tensor (reductions over all of its
-    elements): rtol 1e-5 against binary64 reductions of the full tensors.
+  * all five diagnostics of every tensor, reductions over all of its
+    elements, rtol 1e-5: gradient_norm and m_norm against binary64 norms of
+    the full gradient and m; current_alpha and auto_factor_mean against
+    binary64 means of alpha_factor and mfac recomputed from the full
+    post-step m, v (and tau) by torch ops on the device (each element's m,
+    v, tau is the oracle's, as the samples show); current_kappa_factor
+    against their ratio (NaN for all-zero gradients).
 """
 import os
 import sys
@@ -43,7 +51,7 @@ pytestmark = [pytest.mark.gpu,
 
 DEV = "cuda:0"
 SAMPLES = 1024          # per tensor, plus its first and last element
-STEPS = 3
+STEPS = 10
 ELEMENTS = {"north_star": 2_645_527_040, "c4": 2_645_527_040, "c3": 1_311_082_496, "c2": 50_938_880,
             "c5": 94_406_322}
 
@@ -79,7 +87,7 @@ def test_full_size_sampled_parity(oracle_mod, name):
     idx = []
     for p in params:
         n = p.numel()
-        per = SAMPLES if len(params) < 1000 else 64              # C5: 10,000 tensors
+        per = SAMPLES if len(params) < 1000 else 256             # C5: 10,000 tensors
         pick = np.unique(np.concatenate([[0, n - 1], rng.integers(0, n, size=min(n, per))]))
         idx.append(torch.from_numpy(pick).to(DEV))
 
@@ -90,7 +98,12 @@ def test_full_size_sampled_parity(oracle_mod, name):
     host_m = [np.zeros_like(x) for x in host_p]
     host_v = [np.zeros_like(x) for x in host_p]
     host_tau = [np.zeros_like(x) for x in host_p] if star else [None] * len(params)
+    from bench import cos_inf
+
     for t in range(1, STEPS + 1):
+        lr = hp["lr"] * cos_inf(t - 1) if w["schedule"] == "cos_inf" else hp["lr"]
+        for g in opt.param_groups:
+            g["lr"] = lr                                 # the bench's one_step(k) for k = t - 1
         gen.manual_seed(1000 + t)
         for i, p in enumerate(params):
             p.grad = torch.empty(p.shape, device=DEV).normal_(0, 1e-3, generator=gen).to(pdtype)
@@ -112,7 +125,7 @@ def test_full_size_sampled_parity(oracle_mod, name):
         got_v = gather([opt.state[p]["v"] for p in params])
         got_tau = gather([opt.state[p]["tau"] for p in params]) if star else None
         for i in range(len(params)):
-            osc = O.step_scalars(lr=hp["lr"], peak_lr=hp["lr"], delta=hp["delta"], kappa=hp["kappa"],
+            osc = O.step_scalars(lr=lr, peak_lr=hp["lr"], delta=hp["delta"], kappa=hp["kappa"],
                                  epsilon=hp["epsilon"], weight_decay=wd_of[i], clipsnr=hp["clipsnr"],
                                  wd_decaying=hp["wd_decaying"], wd_ts=hp["wd_ts"], gamma_3_factor=1.0, t=t)
             O.element_step(star, host_p[i], host_g[i], host_m[i], host_v[i], host_tau[i], osc)
@@ -138,9 +151,42 @@ def test_full_size_sampled_parity(oracle_mod, name):
             np.testing.assert_allclose(float(st["gradient_norm"]), gnorm[i], rtol=1e-5, err_msg=str(where))
             mnorm = float(torch.linalg.vector_norm(st["m"].double()))
             np.testing.assert_allclose(float(st["m_norm"]), mnorm, rtol=1e-5, err_msg=str(where))
+            ca, afm = _alpha_mfac_means(star, st["m"], st["v"], st.get("tau"), t, hp)
+            got = [float(st[k]) for k in ("current_alpha", "auto_factor_mean", "current_kappa_factor")]
+            np.testing.assert_allclose(got, [ca, afm, ca / afm if afm else float("nan")], rtol=1e-5,
+                                       atol=0, equal_nan=True, err_msg=str(where))
             assert st["step"] == t
     del opt, params, groups
     torch.cuda.empty_cache()
+
+
+def _alpha_mfac_means(star, m, v, tau, t, hp, block=1 << 26):
+    """Binary64 means of alpha_factor and mfac over a whole tensor, from its
+    post-step m, v (and tau) at step t (src/optim/adana.py:107-123;
+    src/optim/dana_star_mk4.py:143-174), block by block on the device."""
+    mf, vf = m.detach().reshape(-1), v.detach().reshape(-1)
+    tf = tau.detach().reshape(-1) if star else None
+    e = 1.0 - hp["kappa"]
+    clip = hp["clipsnr"]
+    s_af = s_mf = 0.0
+    for a in range(0, mf.numel(), block):
+        mm, vv = mf[a:a + block].double(), vf[a:a + block].double()
+        se = torch.sqrt(vv) + hp["epsilon"]
+        if star:
+            ta = tf[a:a + block].double()
+            ct = torch.clamp(ta, max=0.5)
+            treg = torch.clamp(ct / (1.0 - ct), min=1.0 / (1.0 + t))
+            mfac = torch.abs(mm) * torch.sqrt(treg) / se / treg
+            af = torch.clamp(ta * t, min=1.0) ** e * mfac
+        else:
+            mfac = torch.abs(mm) / se
+            af = (1.0 + t) ** e * mfac
+        if clip is not None:
+            af = torch.clamp(af, max=clip)
+        s_af += float(af.sum())
+        s_mf += float(mfac.sum())
+    n = mf.numel()
+    return s_af / n, s_mf / n
 
 
 def _norm64(t: torch.Tensor, block: int = 1 << 28) -> float:

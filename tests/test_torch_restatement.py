@@ -6,8 +6,8 @@ reference's own ``step()`` on this container's CPU) differ by a few ulp in p
 and tau.  This file shows that the whole difference comes from two
 functions and nothing else:
 
-1. ``_torch_step`` restates the two updates as torch CPU tensor ops, one op
-   for each tensor op of src/optim/adana.py:101-151 and
+1. ``oracle.torch_ref`` restates the two updates as torch CPU tensor ops,
+   one op for each tensor op of src/optim/adana.py:101-151 and
    src/optim/dana_star_mk4.py:137-203, in that order, with the six 0-d
    float32 scalars the reference's ``step()`` builds (adana.py:199-208).  Run
    with torch's own ``sqrt`` and ``**`` it reproduces the golden p, m, v, tau
@@ -49,91 +49,34 @@ def _cr_pow(x: torch.Tensor, e: float) -> torch.Tensor:
     return torch.tensor(flat, dtype=torch.float64).reshape(x.shape).float()
 
 
-def _torch_step(star, p, g, m, v, tau, sc, hp, sqrt=torch.sqrt, epow=None, slip=None):
-    """One tensor's update in place; returns the five diagnostics.  ``sc`` =
-    (step, alpha, g2, g3, schedule_factor, wd) as 0-d float32 tensors.
-    ``slip`` plants one plausible mistake (tests of the pin only)."""
-    step_t, a_t, g2_t, g3_t, sf_t, wd_t = sc
-    kappa, clip = hp["kappa"], hp["clipsnr"]
-    if slip == "wd_first":
-        p.mul_(1 + (-wd_t * sf_t))
-    if slip == "lerp_one_branch":
-        m.add_(a_t * (g - m))
-    else:
-        m.lerp_(g, a_t)                                       # adana.py:101
-    if slip == "addcmul_unfused":
-        v.mul_(1 - a_t).add_(a_t * (g * g))
-    else:
-        v.mul_(1 - a_t).addcmul_(g, g, value=a_t)             # :104
-    se = sqrt(v).add_(hp["epsilon"])                          # :107
-    if star:
-        ag = torch.abs(g)                                     # dana_star_mk4.py:147
-        tau.lerp_(ag / (ag + se), a_t)                        # :148-149
-        ct = torch.clamp(tau, max=0.5)                        # :152
-        pe = ct / (1.0 - ct)                                  # :153
-        min_p = 1.0 / (1.0 + step_t)                          # :154
-        treg = min_p + torch.relu(pe - min_p)                 # :156
-        et = torch.clamp(tau * (step_t + (1 if slip == "time_plus_one" else 0)), min=1.0)   # :159
-        nt = sqrt(treg) / se                                  # :163-164
-        mnt = torch.abs(m) * nt                               # :165
-        mfac = mnt / treg                                     # :167
-        pw = et ** (1 - kappa) if epow is None else epow(et, 1 - kappa)
-        af = pw * mfac                                        # :170 / :174
-        if clip is not None:
-            af = torch.clamp(af, max=clip)
-        g3t = (-g3_t) * hp["gamma_3_factor"] * (torch.sign(m) * (treg * af + mnt))   # :177
-    else:
-        nt = 1.0 / se                                         # adana.py:110
-        mfac = torch.abs(m) * nt                              # :111, :115
-        af = ((1.0 + step_t) ** (1 - kappa)) * mfac           # :114, :119 / :123
-        if clip is not None:
-            af = torch.clamp(af, max=clip)
-        g3t = (-g3_t) * hp["gamma_3_factor"] * (torch.sign(m) * af + m * nt)         # :126
-    g2t = (-g2_t) * (g * nt) if slip == "g2_assoc" else (-g2_t) * g * nt   # :129 / :180
-    p.add_(g2t + g3t)                                         # :132-135
-    if slip == "wd_first":
-        pass
-    elif hp["wd_decaying"]:                                   # :139-142
-        wdf = -wd_t / (1 + step_t / hp["wd_ts"]) * sf_t
-        p.mul_(1 + wdf)                                       # :143
-    else:
-        p.mul_(1 + (-wd_t * sf_t))
-    ca = af.mean()                                            # :146-151
-    return [ca, g.norm(), mfac.mean(), ca / mfac.mean(), m.norm()]
-
-
 def _run(case, *, sqrt=torch.sqrt, epow=None, on_step=None, slip=None):
-    """The reference's step() loop over the golden inputs with _torch_step:
-    two groups (weight decay on group 0 only), per-tensor step counters,
-    grad None skipped, lr = peak * multiplier(k)."""
+    """oracle.torch_ref's restatement of the reference's step() over the
+    golden inputs: two groups (weight decay on group 0 only), per-tensor step
+    counters, grad None skipped, lr = peak * multiplier(k).  ``on_step(k,
+    params, state, diags)`` sees the state after each step; ``diags[i]`` are
+    the five diagnostics of the tensors stepped at k."""
+    from oracle.torch_ref import DIAG_KEYS, TorchRefGroup, TorchRefOptimizer
+
     meta, p0, grads, has_grad = load_golden_inputs()
-    ent = meta["cases"][case]
-    kw = ent["kwargs"]
-    star = ent["class"] == "DANA_STAR_MK4"
+    kw = meta["cases"][case]["kwargs"]
+    star = meta["cases"][case]["class"] == "DANA_STAR_MK4"
     params = [torch.from_numpy(x.copy()) for x in p0]
-    state = {}
+    idx = [[i for i in range(len(params)) if meta["group_of"][i] == gi] for gi in range(2)]
+    groups = [TorchRefGroup(params=[params[i] for i in idx[gi]], lr=kw["lr"], delta=kw["delta"], epsilon=1e-8,
+                            weight_decay=kw["weight_decay"] * meta["group_wd_scale"][gi]) for gi in range(2)]
+    opt = TorchRefOptimizer(groups=groups, star=star, peak_lr=kw["lr"], kappa=kw["kappa"], clipsnr=kw["clipsnr"],
+                            wd_decaying=kw["wd_decaying"], wd_ts=kw["wd_ts"], gamma_3_factor=kw["gamma_3_factor"])
     for k in range(1, meta["n_steps"] + 1):
-        lr = kw["lr"] * meta["lr_multiplier"][k - 1]
-        diags = {}
-        for i, p in enumerate(params):
-            if not has_grad[k - 1, i]:
-                continue
-            g = torch.from_numpy(grads[k - 1][i].copy())
-            st = state.setdefault(i, {"step": 0, "m": torch.zeros_like(p), "v": torch.zeros_like(p),
-                                      "tau": torch.zeros_like(p)})
-            st["step"] += 1
-            t = st["step"]
-            wd = kw["weight_decay"] * meta["group_wd_scale"][meta["group_of"][i]]
-            f32 = dict(dtype=torch.float32)
-            sc = (torch.tensor(t, **f32), torch.tensor(kw["delta"] / (kw["delta"] + t), **f32),
-                  torch.tensor(lr, **f32), torch.tensor(lr, **f32), torch.tensor(lr / kw["lr"], **f32),
-                  torch.tensor(wd, **f32))
-            hp = dict(kw, epsilon=1e-8)
-            d = _torch_step(star, p, g, st["m"], st["v"], st["tau"], sc, hp, sqrt=sqrt, epow=epow, slip=slip)
-            diags[i] = [float(x) for x in d]
+        for g in groups:
+            g.lr = kw["lr"] * meta["lr_multiplier"][k - 1]
+        gl = [[torch.from_numpy(grads[k - 1][i].copy()) if has_grad[k - 1, i] else None for i in idx[gi]]
+              for gi in range(2)]
+        opt.step(gl, sqrt=sqrt, epow=epow, slip=slip)
+        state = {i: opt.state[id(p)] for i, p in enumerate(params) if id(p) in opt.state}
+        diags = {i: [float(state[i][key]) for key in DIAG_KEYS] for i in range(len(params)) if has_grad[k - 1, i]}
         if on_step is not None:
             on_step(k, params, state, diags)
-    return meta, star, params, state
+    return meta, star, params, opt.state
 
 
 @pytest.mark.skipif(torch.backends.cpu.get_cpu_capability() != load_golden_inputs()[0].get("cpu_capability"),
