@@ -20,7 +20,7 @@ group) is not part of this single-GPU build and raises.
 from __future__ import annotations
 
 import math
-from typing import Dict, Tuple
+from typing import Dict, List, Tuple
 
 import torch
 from torch.optim import Optimizer
@@ -28,32 +28,58 @@ from torch.optim import Optimizer
 from . import _lib
 from .optim import _DanaFamily
 
-
-def zeropower_via_newtonschulz5(G: torch.Tensor, steps: int) -> torch.Tensor:
-    """Newton-Schulz orthogonalisation of a 2-D matrix (manau.py:18-40), in
-    G's dtype.  Transposed operands are made contiguous before each product
-    (same values; the batched-product path has faulted on transposed bfloat16
-    operands on this platform)."""
-    assert len(G.shape) == 2
-    a, b, c = (3.4445, -4.7750, 2.0315)
-    X = G
-    if G.size(0) > G.size(1):
-        X = X.T.contiguous()
-    X = X / (X.norm() + 1e-7)
-    for _ in range(steps):
-        A = X @ X.T.contiguous()
-        B = b * A + c * A @ A
-        X = a * X + B @ X
-    if G.size(0) > G.size(1):
-        X = X.T
-    return X
+# Parameter names whose tensors stay on the Dana branch even when 2-D: token
+# and position embeddings and the output head (src/optim/manau.py:186-189).
+_DANA_NAME_MARKERS = ("wte.weight", "wpe.weight", "lm_head.weight")
+# The quintic Newton-Schulz coefficients of Muon (K. Jordan's published
+# orthogonalisation; src/optim/manau.py:23).
+_NS_A, _NS_B, _NS_C = 3.4445, -4.7750, 2.0315
 
 
-def adjust_lr_wd_for_muon(lr, matched_adamw_rms, param_shape):
-    """manau.py:81-86."""
-    A, B = param_shape[:2]
-    adjusted_ratio = math.sqrt(max(A, B)) * matched_adamw_rms
-    return lr * adjusted_ratio
+def _newton_schulz(m: torch.Tensor, iters: int) -> torch.Tensor:
+    """Approximately orthogonalise a 2-D matrix (its U V^T) in its own dtype:
+    normalise by the Frobenius norm, then ``iters`` rounds of
+    X <- a X + (b A + (c A) A) X with A = X X^T, on the wide orientation of
+    the matrix (rows <= columns), transposed back at the end.  This is the
+    products' order of src/optim/manau.py:18-40, so bfloat16 results agree
+    with the reference's.  Every product takes contiguous operands: torch's
+    bfloat16 batched-product path is documented on this platform to fault
+    the GPU with a transposed right operand, so none is ever passed."""
+    if m.dim() != 2:
+        raise ValueError(f"Newton-Schulz needs a matrix, got shape {tuple(m.shape)}")
+    tall = m.shape[0] > m.shape[1]
+    x = m.transpose(0, 1).contiguous() if tall else m
+    x = x / (x.norm() + 1e-7)
+    for _ in range(iters):
+        gram = x @ x.transpose(0, 1).contiguous()
+        poly = _NS_B * gram + _NS_C * gram @ gram
+        x = _NS_A * x + poly @ x
+    return x.transpose(0, 1) if tall else x
+
+
+def _muon_lr(lr: float, matched_adamw_rms: float, shape) -> float:
+    """Muon's step size for a matrix of ``shape``: lr scaled by
+    sqrt(max(rows, cols)) * matched_adamw_rms, so the update's RMS matches an
+    AdamW update's (src/optim/manau.py:81-86)."""
+    return lr * (math.sqrt(max(shape[0], shape[1])) * matched_adamw_rms)
+
+
+def _assignment_report(muon: List[Tuple[str, torch.Size, int]], dana: List[Tuple[str, torch.Size, int]]) -> str:
+    """The parameter-assignment summary the reference's constructor prints
+    (src/optim/manau.py:198-223), character for character."""
+    rule, thin = "=" * 80, "-" * 80
+    n_muon = sum(n for _, _, n in muon)
+    n_dana = sum(n for _, _, n in dana)
+    total = n_muon + n_dana
+    out = ["", rule, "Manau Optimizer Parameter Assignment", rule]
+    for tag, title, label, rows, count in (("Muon", "Muon (Newton-Schulz)", "Muon", muon, n_muon),
+                                            ("DANA", "DANA-STAR-MK4", "DANA", dana, n_dana)):
+        out += ["", f"{title} parameters: {len(rows)}", f"Total {label} params: {count:,} ({count / 1e6:.2f}M)",
+                thin]
+        out += [f"  [{tag}] {name:50s} {str(shape):20s} {numel:>12,} params" for name, shape, numel in rows]
+    out += ["", rule, f"Total parameters: {total:,} ({total / 1e6:.2f}M)",
+            f"Muon ratio: {100 * n_muon / total:.1f}%", f"DANA ratio: {100 * n_dana / total:.1f}%", rule, "", ""]
+    return "\n".join(out)
 
 
 class Manau(_DanaFamily):
@@ -79,50 +105,30 @@ class Manau(_DanaFamily):
         self.distributed_mode = False
         self.lr = lr
         self._engine_init(master_weights=False)
+        rows = {True: [], False: []}
+        for group in self.param_groups:
+            for name, p, to_muon in self._routes(group):
+                self.state[p]["use_muon"] = to_muon
+                rows[to_muon].append((name, p.shape, p.numel()))
+        print(_assignment_report(rows[True], rows[False]), end="")
 
-        muon_params, dana_params = [], []
-        muon_total_params = dana_total_params = 0
-        for group in self.param_groups:                                # manau.py:176-196
-            param_names = group.get("param_names", None)
-            if param_names is None:
-                raise ValueError(
-                    "Manau optimizer requires 'param_names' to be provided in param_groups. "
-                    "This is needed to correctly identify embeddings and head layers."
-                )
-            for idx, p in enumerate(group["params"]):
-                is_embedding_or_head = False
-                if idx < len(param_names):
-                    pname = param_names[idx]
-                    if any(identifier in pname for identifier in ["wte.weight", "wpe.weight", "lm_head.weight"]):
-                        is_embedding_or_head = True
-                if not is_embedding_or_head and p.ndim >= 2:
-                    self.state[p]["use_muon"] = True
-                    muon_params.append((pname, p.shape, p.numel()))
-                    muon_total_params += p.numel()
-                else:
-                    self.state[p]["use_muon"] = False
-                    dana_params.append((pname, p.shape, p.numel()))
-                    dana_total_params += p.numel()
-
-        print("\n" + "=" * 80)                                          # manau.py:198-223
-        print("Manau Optimizer Parameter Assignment")
-        print("=" * 80)
-        print(f"\nMuon (Newton-Schulz) parameters: {len(muon_params)}")
-        print(f"Total Muon params: {muon_total_params:,} ({muon_total_params/1e6:.2f}M)")
-        print("-" * 80)
-        for pname, shape, numel in muon_params:
-            print(f"  [Muon] {pname:50s} {str(shape):20s} {numel:>12,} params")
-        print(f"\nDANA-STAR-MK4 parameters: {len(dana_params)}")
-        print(f"Total DANA params: {dana_total_params:,} ({dana_total_params/1e6:.2f}M)")
-        print("-" * 80)
-        for pname, shape, numel in dana_params:
-            print(f"  [DANA] {pname:50s} {str(shape):20s} {numel:>12,} params")
-        print("\n" + "=" * 80)
-        print(f"Total parameters: {muon_total_params + dana_total_params:,} "
-              f"({(muon_total_params + dana_total_params)/1e6:.2f}M)")
-        print(f"Muon ratio: {100*muon_total_params/(muon_total_params + dana_total_params):.1f}%")
-        print(f"DANA ratio: {100*dana_total_params/(muon_total_params + dana_total_params):.1f}%")
-        print("=" * 80 + "\n")
+    @staticmethod
+    def _routes(group):
+        """(name, parameter, goes to Muon) for every parameter of a group:
+        matrices go to Muon unless their name marks an embedding or the head
+        (src/optim/manau.py:176-196).  A parameter past the end of the group's
+        name list keeps the previous name, as in the reference."""
+        names = group.get("param_names")
+        if names is None:
+            raise ValueError("Manau: every parameter group needs a 'param_names' list (one name per "
+                             "parameter) to tell embeddings and the output head from the other matrices")
+        name = ""
+        out = []
+        for i, p in enumerate(group["params"]):
+            name = names[i] if i < len(names) else name
+            dana_by_name = any(marker in name for marker in _DANA_NAME_MARKERS)
+            out.append((name, p, p.ndim >= 2 and not dana_by_name))
+        return out
 
     def enable_distributed_mode(self, global_buffer_sizes, dist_group, tp_group,
                                 dist_metas: Dict[torch.nn.Parameter, object]):
@@ -148,64 +154,64 @@ class Manau(_DanaFamily):
             out.append(_lib.manau_scalars(hp, lr, step, alpha))
         return out
 
+    def _ema_alpha(self, group, own_step: int):
+        """The EMA coefficient of one parameter's update and the step it was
+        taken at: delta / (delta + t) with t the parameter's own step, or,
+        with weight_time, the group's weighted step count (advanced here by
+        lr / peak lr, once per parameter) and the coefficient scaled by that
+        time factor (src/optim/manau.py:345-355, :541-555)."""
+        weight_time = group["weight_time"]
+        tf = group["lr"] / self.lr if weight_time else 1.0
+        group["weighted_step_count"] += tf
+        delta = group["delta"]
+        if weight_time:
+            t = group["weighted_step_count"]
+            return t, delta / (delta + t) * tf
+        return own_step, delta / (delta + own_step)
+
+    def _muon_input(self, group, p) -> torch.Tensor:
+        """Advance one Muon parameter's momentum buffer and return its
+        Newton-Schulz input in bfloat16 (src/optim/manau.py:320-371):
+        heavy-ball momentum, Nesterov by default, or with dana_momentum the
+        Dana EMA of the gradient added to it with weight step^(1 - kappa)."""
+        g = p.grad
+        if g is None:
+            raise AssertionError("Manau: a Muon parameter has no gradient")
+        st = self.state[p]
+        buf = st.get("muon_buffer")
+        if buf is None:
+            buf = st["muon_buffer"] = torch.zeros_like(g)
+            st["step"] = 0
+        st["step"] += 1
+        if group["dana_momentum"]:
+            _, a = self._ema_alpha(group, st["step"])
+            buf.mul_(1 - a).add_(g, alpha=a)
+            direction = g + buf * (st["step"] ** (1 - group["kappa"]))
+        else:
+            mu = group["momentum"]
+            buf.mul_(mu).add_(g)
+            direction = g.add(buf, alpha=mu) if group["nesterov"] else buf
+        return direction.bfloat16()
+
     @torch.no_grad()
     def step(self):
+        muon = [(group, p) for group in self.param_groups for p in group["params"]
+                if self.state[p].get("use_muon", False)]
         for group in self.param_groups:             # the Dana branch has no CPU path: refuse first
             for p in group["params"]:
                 if not self.state[p].get("use_muon", False) and p.device.type != "cuda":
                     raise RuntimeError(f"Manau: parameters must live on a ROCm GPU (got {p.device}); "
                                        "the Dana-Star-MK4 step has no CPU path")
-        ns_inputs = {}
-        for group in self.param_groups:                                 # manau.py:320-371
-            momentum = group["momentum"]
-            dana_momentum = group["dana_momentum"]
-            delta = group["delta"]
-            kappa = group["kappa"]
-            weight_time = group["weight_time"]
-            for p in group["params"]:
-                if not self.state[p].get("use_muon", False):
-                    continue
-                g = p.grad
-                assert g is not None
-                assert self.distributed_mode or g.dim() == 2
-                state = self.state[p]
-                if "muon_buffer" not in state:
-                    state["muon_buffer"] = torch.zeros_like(g)
-                    state["step"] = 0
-                buf = state["muon_buffer"]
-                state["step"] += 1
-                if dana_momentum:
-                    step = state["step"]
-                    time_factor = group["lr"] / self.lr if weight_time else 1.0
-                    group["weighted_step_count"] += time_factor
-                    if weight_time:
-                        step = group["weighted_step_count"]
-                        alpha = delta / (delta + step) * time_factor
-                    else:
-                        alpha = delta / (delta + step)
-                    buf.mul_(1 - alpha).add_(g, alpha=alpha)
-                else:
-                    buf.mul_(momentum).add_(g)
-                if dana_momentum:
-                    step = state["step"]
-                    time_scaling = step ** (1 - kappa)
-                    g = g + buf * time_scaling
-                else:
-                    g = g.add(buf, alpha=momentum) if group["nesterov"] else buf
-                ns_inputs[p] = g.bfloat16()
-
-        for group in self.param_groups:                                 # manau.py:456-502
+        # every momentum first (they advance the weighted step counts the
+        # Dana branch reads), then every orthogonalised update, then the
+        # Dana branch (src/optim/manau.py:320-613)
+        inputs = [self._muon_input(group, p) for group, p in muon]
+        for (group, p), x in zip(muon, inputs):
+            update = _newton_schulz(x, group["ns_steps"])
             lr = group["lr"]
-            for p in group["params"]:
-                if not self.state[p].get("use_muon", False):
-                    continue
-                ns_input = ns_inputs[p]
-                update = zeropower_via_newtonschulz5(ns_input, steps=group["ns_steps"])
-                p.data.mul_(1 - lr * group["weight_decay"])
-                adjusted_lr = adjust_lr_wd_for_muon(lr, group["matched_adamw_rms"], ns_input.shape)
-                p.data.add_(update, alpha=-adjusted_lr)
-
-        self._dana_step()                                               # manau.py:504-613
+            p.data.mul_(1 - lr * group["weight_decay"])
+            p.data.add_(update, alpha=-_muon_lr(lr, group["matched_adamw_rms"], x.shape))
+        self._dana_step()
 
     def _dana_step(self) -> None:
         """The Dana-Star-MK4 branch: the host bookkeeping of manau.py:520-578
@@ -214,26 +220,18 @@ class Manau(_DanaFamily):
         params, grads, states, keys = [], [], [], []
         fresh = []
         for gi, group in enumerate(self.param_groups):
-            delta = group["delta"]
-            weight_time = group["weight_time"]
             for p in group["params"]:
                 st = self.state[p]
                 if st.get("use_muon", False):
                     continue
                 g = p.grad
-                assert g is not None
+                if g is None:
+                    raise AssertionError("Manau: a Dana-branch parameter has no gradient")
                 if "dana_m" not in st:                                  # :533-537
                     fresh.append((p, st))
                     st["step"] = 0
                 st["step"] += 1
-                time_factor = group["lr"] / self.lr if weight_time else 1.0
-                group["weighted_step_count"] += time_factor
-                if weight_time:
-                    step = group["weighted_step_count"]
-                    alpha = delta / (delta + step) * time_factor
-                else:
-                    step = st["step"]
-                    alpha = delta / (delta + step)
+                step, alpha = self._ema_alpha(group, st["step"])
                 st["current_alpha"] = alpha                             # :578
                 params.append(p)
                 grads.append(g)
