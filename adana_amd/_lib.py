@@ -16,7 +16,7 @@ import numpy as np
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libadana_mta.so")
 
-ABI_VERSION = 4
+ABI_VERSION = 5
 CHUNK_ELEMS = 1024
 ALIGN_ELEMS = 4
 MAX_CLASSES = 8
@@ -28,6 +28,7 @@ GRAD_BF16 = 0x2
 PARAM_BF16 = 0x4
 WRITE_GRAD = 0x8
 VARIANT_MANAU = 0x10
+STATE_BF16 = 0x20
 DESC_VEC_OK = 0x1
 
 # adana_tensor_desc as a numpy record (64 bytes, same field order).

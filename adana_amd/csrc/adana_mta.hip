@@ -217,6 +217,150 @@ __device__ __forceinline__ float star_phase_b(float p, float g, const StarMid &a
 }
 
 // ---------------------------------------------------------------------------
+// The reference's own bfloat16 path (ADANA_STATE_BF16): bfloat16 parameters
+// make m, v and tau bfloat16 too (zeros_like(p), src/optim/adana.py:191-195;
+// src/optim/dana_star_mk4.py:251-255) and every tensor op rounds its binary32
+// result to bfloat16, as ATen's kernels do on bfloat16 tensors.  How each op
+// meets its float32 0-d and Python-scalar operands (probed op by op against
+// torch 2.10 and pinned by the reference's own bfloat16 run):
+//   * lerp_'s float32 0-d weight is rounded to bfloat16 first;
+//   * mul / div with the 0-d tensor second (v.mul_(1 - a), tau * step,
+//     p.mul_(1 + wd)) use its binary32 value; with the 0-d tensor first
+//     ((-g2) * grad, (-g3)*gf * x, pow * mfac, min_p + x) or in add / sub
+//     (add_(epsilon), pe - min_p) it is rounded to bfloat16;
+//   * addcmul_(g, g, value=a) = fma(a * g, g, v), a unrounded;
+//   * Dana-Star's pow(et, 1 - kappa) takes the exponent rounded to bfloat16;
+//   * clamp(x, max=c) compares with c rounded to bfloat16.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float rb(float x) { return bf16_round(x); }
+
+// The launch's binary32 scalars as the bfloat16 ops see them.
+struct Scalars16 {
+    float a16, lerp_coef16, eps16, pw16, min_p16, clip16, c3_16, cg2_16, e16;
+    bool lerp_small16;
+};
+__device__ __forceinline__ Scalars16 scalars16(const adana_step_scalars &sc) {
+    Scalars16 q;
+    q.a16 = rb(sc.a);
+    q.lerp_small16 = fabsf(q.a16) < 0.5f;
+    q.lerp_coef16 = q.lerp_small16 ? q.a16 : q.a16 - 1.0f;
+    q.eps16 = rb(sc.eps);
+    q.pw16 = rb(sc.pw);
+    q.min_p16 = rb(sc.min_p);
+    q.clip16 = rb(sc.clip);
+    q.c3_16 = rb(sc.c3);
+    q.cg2_16 = rb(sc.cg2);
+    q.e16 = rb(sc.star_exp);
+    return q;
+}
+
+// src/optim/adana.py:101-143 on bfloat16 tensors
+__device__ __forceinline__ float adana_elem16(float p, float g, float &m, float &v, const adana_step_scalars &sc,
+                                              const Scalars16 &q, float (&acc)[4]) {
+    const float mn = rb(__builtin_fmaf(q.lerp_coef16, g - m, q.lerp_small16 ? m : g));   // :101
+    float vn = rb(v * sc.oma);                                                          // :104 mul_
+    vn = rb(__builtin_fmaf(sc.a * g, g, vn));                                           //      addcmul_
+    const float se = rb(rb(sqrtf(vn)) + q.eps16);                                       // :107
+    const float nt = rb(1.0f / se);                                                     // :110
+    const float mfac = rb(fabsf(mn) * nt);                                              // :111, :115
+    float af = rb(q.pw16 * mfac);                                                       // :119 / :123
+    if (sc.has_clip) af = clamp_max(af, q.clip16);
+    const float inner = rb(sign_f(mn) * af + rb(mn * nt));                              // :126
+    const float g3t = rb(q.c3_16 * inner);
+    const float g2t = rb(rb(q.cg2_16 * g) * nt);                                        // :129
+    float pn = rb(p + rb(g2t + g3t));                                                   // :132-135
+    pn = rb(pn * sc.opw);                                                               // :143
+    m = mn;
+    v = vn;
+    accumulate(acc, af, g, mfac, mn);
+    return pn;
+}
+
+// src/optim/dana_star_mk4.py:137-159 on bfloat16 tensors
+__device__ __forceinline__ StarMid star16_phase_a(float g, float m, float v, float tau, const adana_step_scalars &sc,
+                                                  const Scalars16 &q) {
+    StarMid o;
+    o.m = rb(__builtin_fmaf(q.lerp_coef16, g - m, q.lerp_small16 ? m : g));            // :137
+    o.v = rb(v * sc.oma);                                                               // :140
+    o.v = rb(__builtin_fmaf(sc.a * g, g, o.v));
+    o.se = rb(rb(sqrtf(o.v)) + q.eps16);                                                // :143
+    const float ag = fabsf(g);                                                          // :147
+    const float tu = rb(ag / rb(ag + o.se));                                            // :148
+    o.tau = rb(__builtin_fmaf(q.lerp_coef16, tu - tau, q.lerp_small16 ? tau : tu));     // :149
+    const float ct = clamp_max(o.tau, 0.5f);                                            // :152
+    const float pe = rb(ct / rb(1.0f - ct));                                            // :153
+    o.tr = rb(q.min_p16 + relu_f(rb(pe - q.min_p16)));                                  // :154-156
+    o.et = clamp_min(rb(o.tau * sc.s), 1.0f);                                           // :159
+    return o;
+}
+
+// src/optim/dana_star_mk4.py:163-195 on bfloat16 tensors, given pw = et ** e16
+__device__ __forceinline__ float star16_phase_b(float p, float g, const StarMid &a, float pw,
+                                                const adana_step_scalars &sc, const Scalars16 &q, float (&acc)[4]) {
+    const float nt = rb(rb(sqrtf(a.tr)) / a.se);                                        // :163-164
+    const float mnt = rb(fabsf(a.m) * nt);                                              // :165
+    const float mfac = rb(mnt / a.tr);                                                  // :167
+    float af = rb(pw * mfac);                                                           // :170 / :174
+    if (sc.has_clip) af = clamp_max(af, q.clip16);
+    const float inner = sign_f(a.m) * rb(rb(a.tr * af) + mnt);                          // :177
+    const float g3t = rb(q.c3_16 * inner);
+    const float g2t = rb(rb(q.cg2_16 * g) * nt);                                        // :180
+    float pn = rb(p + rb(g2t + g3t));                                                   // :183-186
+    pn = rb(pn * sc.opw);                                                               // :195
+    accumulate(acc, af, g, mfac, a.m);
+    return pn;
+}
+
+// et ** e16 rounded to bfloat16 (ATen's pow(Tensor, Scalar) on bfloat16:
+// exponent rounded to bfloat16, specialisations chosen on the binary64
+// exponent, the result rounded to binary32 and then to bfloat16).
+template <int POWK>
+__device__ __forceinline__ float pow16(float x, const adana_step_scalars &sc, const Scalars16 &q, const PowTab &tab) {
+    if constexpr (POWK == POW_GENERAL) {
+        return rb(adana::pow_f32_unit_exp_tab(x, q.e16, tab.log, tab.exp2j));
+    } else if constexpr (POWK == POW_ONE) {
+        return 1.0f;
+    } else {
+        switch (sc.pow_mode) {
+        case ADANA_POW_ONE: return 1.0f;
+        case ADANA_POW_IDENTITY: return x;
+        case ADANA_POW_SQRT: return rb(sqrtf(x));
+        case ADANA_POW_RSQRT: return rb(1.0f / sqrtf(x));
+        case ADANA_POW_RECIP: return rb(1.0f / x);
+        case ADANA_POW_SQUARE: return rb(x * x);
+        case ADANA_POW_CUBE: return rb((x * x) * x);
+        case ADANA_POW_INVSQ: return rb(1.0f / (x * x));
+        default: return rb(adana::pow_f32_via_f64(x, q.e16));
+        }
+    }
+}
+
+template <bool STAR, int POWK, int N>
+__device__ __forceinline__ void update_n16(float (&P)[N], const float (&G)[N], float (&M)[N], float (&V)[N],
+                                           float (&T)[N], const adana_step_scalars &sc, const PowTab &tab,
+                                           float (&acc)[4]) {
+    const Scalars16 q = scalars16(sc);
+    if constexpr (!STAR) {
+#pragma unroll
+        for (int k = 0; k < N; ++k) P[k] = adana_elem16(P[k], G[k], M[k], V[k], sc, q, acc);
+    } else {
+        StarMid a[N];
+#pragma unroll
+        for (int k = 0; k < N; ++k) a[k] = star16_phase_a(G[k], M[k], V[k], T[k], sc, q);
+        float pw[N];
+#pragma unroll
+        for (int k = 0; k < N; ++k) pw[k] = pow16<POWK>(a[k].et, sc, q, tab);
+#pragma unroll
+        for (int k = 0; k < N; ++k) {
+            P[k] = star16_phase_b(P[k], G[k], a[k], pw[k], sc, q, acc);
+            M[k] = a[k].m;
+            V[k] = a[k].v;
+            T[k] = a[k].tau;
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
 // Manau's eager Dana-Star-MK4 branch (src/optim/manau.py:556-613).  Same state
 // as Dana-Star, different op order: multiply-then-add moments (ATen's
 // add_(x, alpha=a) is one fused multiply-add), (|g| + sqrt v) + eps in the
@@ -491,22 +635,74 @@ __device__ __forceinline__ void store_grad1(const void *g, int64_t off, float x)
 // partial sums are then reduced segment by segment.
 // ---------------------------------------------------------------------------
 
+// Parameter modes of the step (ADANA_PARAM_BF16 / ADANA_STATE_BF16):
+//   PM_F32    float32 parameter and state;
+//   PM_MASTER float32 master copy and state, bfloat16 parameter = RNE(master);
+//   PM_BF16   the reference's bfloat16 path: parameter, m, v, tau bfloat16,
+//             every op rounded to bfloat16 (update_n16).
+enum ParamMode { PM_F32 = 0, PM_MASTER = 1, PM_BF16 = 2 };
+
 // One thread's elements of tensor d from element `off` on (`left` of them
 // remain in the tensor; VEC at most are processed), with their diagnostics
 // terms added to acc.  UNIFORM: every thread of the workgroup works on this
 // tensor and the chunk's part of it starts at element seg0, so the fp32
 // stores go out as buffer stores from that uniform base.
-template <bool STAR, bool GBF16, bool PBF16, int POWK, int VEC, bool UNIFORM>
+template <bool STAR, bool GBF16, int PM, int POWK, int VEC, bool UNIFORM>
 __device__ __forceinline__ void thread_elems(const adana_tensor_desc &d, int64_t off, int64_t left, int64_t seg0,
                                              const ScalarPack &pack, float gs, const PowTab &tab,
                                              float (&acc)[4]) {
     const adana_step_scalars &sc = pack.c[d.sclass];
     const bool scaled = pack.gscale != nullptr;                    // uniform
+    const int cnt = left < VEC ? static_cast<int>(left) : VEC;
+    if constexpr (PM == PM_BF16) {
+        unsigned short *pp = static_cast<unsigned short *>(d.param) + off;
+        unsigned short *mp = reinterpret_cast<unsigned short *>(d.m) + off;
+        unsigned short *vp = reinterpret_cast<unsigned short *>(d.v) + off;
+        unsigned short *tp = STAR ? reinterpret_cast<unsigned short *>(d.tau) + off : nullptr;
+        if (cnt == VEC && (d.flags & ADANA_DESC_VEC_OK)) {
+            float P[VEC], G[VEC], M[VEC], V[VEC], T[VEC];
+            ld_bf16_n<VEC>(pp, P);
+            load_grad_n<true, VEC>(d.grad, off, G);
+            ld_bf16_n<VEC>(mp, M);
+            ld_bf16_n<VEC>(vp, V);
+            if constexpr (STAR) {
+                ld_bf16_n<VEC>(tp, T);
+            } else {
+#pragma unroll
+                for (int k = 0; k < VEC; ++k) T[k] = 0.0f;
+            }
+            if (scaled) {
+#pragma unroll
+                for (int k = 0; k < VEC; ++k) G[k] = scale_grad<true>(G[k], gs);
+                if (pack.write_grad) store_grad_n<true, VEC>(d.grad, off, G);
+            }
+            update_n16<STAR, POWK, VEC>(P, G, M, V, T, sc, tab, acc);
+            st_bf16_n<VEC>(pp, P);
+            st_bf16_n<VEC>(mp, M);
+            st_bf16_n<VEC>(vp, V);
+            if constexpr (STAR) st_bf16_n<VEC>(tp, T);
+        } else {
+            for (int e = 0; e < cnt; ++e) {
+                float P[1] = {bf16_to_f32(pp[e])}, M[1] = {bf16_to_f32(mp[e])}, V[1] = {bf16_to_f32(vp[e])};
+                float T[1] = {STAR ? bf16_to_f32(tp[e]) : 0.0f};
+                float G[1] = {load_grad1<true>(d.grad, off + e)};
+                if (scaled) {
+                    G[0] = scale_grad<true>(G[0], gs);
+                    if (pack.write_grad) store_grad1<true>(d.grad, off + e, G[0]);
+                }
+                update_n16<STAR, POWK, 1>(P, G, M, V, T, sc, tab, acc);
+                pp[e] = f32_to_bf16(P[0]);
+                mp[e] = f32_to_bf16(M[0]);
+                vp[e] = f32_to_bf16(V[0]);
+                if constexpr (STAR) tp[e] = f32_to_bf16(T[0]);
+            }
+        }
+        return;
+    }
     float *pp = static_cast<float *>(d.param) + off;
     float *mp = d.m + off;
     float *vp = d.v + off;
     float *tp = STAR ? d.tau + off : nullptr;
-    const int cnt = left < VEC ? static_cast<int>(left) : VEC;
     if (cnt == VEC && (d.flags & ADANA_DESC_VEC_OK)) {
         float P[VEC], G[VEC], M[VEC], V[VEC], T[VEC];
         ld_n<VEC>(pp, P);
@@ -537,7 +733,7 @@ __device__ __forceinline__ void thread_elems(const adana_tensor_desc &d, int64_t
             st_n<VEC>(vp, V);
             if constexpr (STAR) st_n<VEC>(tp, T);
         }
-        if constexpr (PBF16) st_bf16_n<VEC>(static_cast<unsigned short *>(d.param_lp) + off, P);
+        if constexpr (PM == PM_MASTER) st_bf16_n<VEC>(static_cast<unsigned short *>(d.param_lp) + off, P);
     } else {
         // unaligned tensor, or the last (< VEC) elements of a tensor
         for (int e = 0; e < cnt; ++e) {
@@ -552,7 +748,7 @@ __device__ __forceinline__ void thread_elems(const adana_tensor_desc &d, int64_t
             mp[e] = mm;
             vp[e] = vv;
             if constexpr (STAR) tp[e] = tt;
-            if constexpr (PBF16) static_cast<unsigned short *>(d.param_lp)[off + e] = f32_to_bf16(o);
+            if constexpr (PM == PM_MASTER) static_cast<unsigned short *>(d.param_lp)[off + e] = f32_to_bf16(o);
         }
     }
 }
@@ -584,7 +780,7 @@ __device__ __forceinline__ void block_partial(float (&acc)[4], float (*red)[kW][
     par ^= 1;
 }
 
-template <bool STAR, bool GBF16, bool PBF16, int POWK, int VEC>
+template <bool STAR, bool GBF16, int PM, int POWK, int VEC>
 __global__ __launch_bounds__(kChunk / VEC) void mta_step_kernel(const adana_tensor_desc *__restrict__ desc,
                                                                 const int64_t *__restrict__ vstart,
                                                                 const int32_t *__restrict__ chunk_first,
@@ -624,7 +820,7 @@ __global__ __launch_bounds__(kChunk / VEC) void mta_step_kernel(const adana_tens
     float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
     if (vs0 <= lo && vs0 + d0.numel >= hi) {
         // the whole chunk lies in tensor i0
-        thread_elems<STAR, GBF16, PBF16, POWK, VEC, true>(d0, mine - vs0, vs0 + d0.numel - mine, lo - vs0, pack, gs,
+        thread_elems<STAR, GBF16, PM, POWK, VEC, true>(d0, mine - vs0, vs0 + d0.numel - mine, lo - vs0, pack, gs,
                                                           tab, acc);
         block_partial<kW>(acc, red, par, part4 + chunk + i0);
         return;
@@ -641,7 +837,7 @@ __global__ __launch_bounds__(kChunk / VEC) void mta_step_kernel(const adana_tens
         const adana_tensor_desc d = desc[l];
         const int64_t vs = vstart[l];
         if (mine >= vs && mine < vs + d.numel)
-            thread_elems<STAR, GBF16, PBF16, POWK, VEC, false>(d, mine - vs, vs + d.numel - mine, 0, pack, gs, tab,
+            thread_elems<STAR, GBF16, PM, POWK, VEC, false>(d, mine - vs, vs + d.numel - mine, 0, pack, gs, tab,
                                                                acc);
     }
     // one (chunk, tensor) partial per tensor overlapping the chunk, in order
@@ -699,16 +895,27 @@ __device__ __forceinline__ void block_sum4(double &s0, double &s1, double &s2, d
 }
 
 // The five diagnostics of tensor i from its four binary64 sums
-// (src/optim/adana.py:146-151, :221-225).
-__device__ __forceinline__ void write_diag(float *diag, int i, double n, double s0, double s1, double s2, double s3) {
-    const float ca = static_cast<float>(s0 / n);         // alpha_factor.mean()
-    const float afm = static_cast<float>(s2 / n);        // mfac.mean()
-    float *o = diag + 5 * static_cast<int64_t>(i);
-    o[0] = ca;
+// (src/optim/adana.py:146-151, :221-225): float32, or with bf16 (the
+// reference's bfloat16 path, whose diagnostics are bfloat16 0-d tensors)
+// each value rounded to bfloat16 and the kappa factor the rounded quotient
+// of the two rounded means, stored as bfloat16.
+__device__ __forceinline__ void write_diag(void *diag, int bf16, int i, double n, double s0, double s1, double s2,
+                                           double s3) {
+    float o[5];
+    o[0] = static_cast<float>(s0 / n);                   // alpha_factor.mean()
     o[1] = static_cast<float>(sqrt(s1));                 // grad.norm()
-    o[2] = afm;
-    o[3] = ca / afm;                                     // current_alpha / auto_factor_mean
+    o[2] = static_cast<float>(s2 / n);                   // mfac.mean()
     o[4] = static_cast<float>(sqrt(s3));                 // m.norm()
+    if (bf16) {
+        unsigned short *h = static_cast<unsigned short *>(diag) + 5 * static_cast<int64_t>(i);
+        for (int k = 0; k < 5; ++k) o[k] = bf16_round(o[k]);
+        o[3] = bf16_round(o[0] / o[2]);                  // current_alpha / auto_factor_mean
+        for (int k = 0; k < 5; ++k) h[k] = f32_to_bf16(o[k]);
+        return;
+    }
+    o[3] = o[0] / o[2];
+    float *f = static_cast<float *>(diag) + 5 * static_cast<int64_t>(i);
+    for (int k = 0; k < 5; ++k) f[k] = o[k];
 }
 
 // Diagnostics combine: one launch after the main kernel.
@@ -729,7 +936,7 @@ __global__ __launch_bounds__(kBlock) void combine_kernel(const adana_tensor_desc
                                                          const int32_t *__restrict__ fold_first, int32_t n,
                                                          int32_t n_folds, const float *__restrict__ partials,
                                                          double4 *__restrict__ folds, int32_t *__restrict__ counters,
-                                                         float *__restrict__ diag) {
+                                                         void *__restrict__ diag, int diag_bf16) {
     __shared__ double red[kWaves][4];
     __shared__ int is_last;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -779,7 +986,7 @@ __global__ __launch_bounds__(kBlock) void combine_kernel(const adana_tensor_desc
             s2 += __shfl_xor(s2, o, 64);
             s3 += __shfl_xor(s3, o, 64);
         }
-        if (lane == 0) write_diag(diag, i, static_cast<double>(numel), s0, s1, s2, s3);
+        if (lane == 0) write_diag(diag, diag_bf16, i, static_cast<double>(numel), s0, s1, s2, s3);
         return;
     }
     const int i = static_cast<int>((b - n_folds) * kWaves + wave);
@@ -801,7 +1008,7 @@ __global__ __launch_bounds__(kBlock) void combine_kernel(const adana_tensor_desc
         s2 += __shfl_xor(s2, o, 64);
         s3 += __shfl_xor(s3, o, 64);
     }
-    if (lane == 0) write_diag(diag, i, static_cast<double>(numel), s0, s1, s2, s3);
+    if (lane == 0) write_diag(diag, diag_bf16, i, static_cast<double>(numel), s0, s1, s2, s3);
 }
 
 // ---------------------------------------------------------------------------
@@ -1060,9 +1267,9 @@ size_t workspace_bytes(const adana_plan &pl) {
 // tensors of 64-65536 elements: 0.715 ms capped, 0.666 ms uncapped; the same
 // list at kappa = 1 prefers the cap, 0.658 against 0.748 ms).  The cap is
 // imposed with dynamic LDS the kernel does not touch.
-template <bool STAR, bool PBF16, int POWK>
+template <bool STAR, int PM, int POWK>
 constexpr int residency_cap(bool small_tensors) {
-    return (STAR && pow_tables(POWK) && small_tensors) ? 0 : (PBF16 ? 5 : 4);
+    return (STAR && pow_tables(POWK) && small_tensors) ? 0 : (PM == PM_MASTER ? 5 : 4);
 }
 
 // Upper bound on the kernel's static LDS (the reduction slots and, for the
@@ -1098,39 +1305,39 @@ size_t lds_for_cap(int wgs, int64_t n_chunks) {
     return l <= static_cast<size_t>(lds_per_block[dev]) ? l : 0;
 }
 
-template <bool STAR, bool GBF16, bool PBF16, int POWK>
+template <bool STAR, bool GBF16, int PM, int POWK>
 void launch_main(int64_t n_chunks, hipStream_t st, const adana_tensor_desc *d, const int64_t *vs,
                  const int32_t *cf, int32_t n, const ScalarPack &pack, float *partials, int32_t *counters) {
     constexpr int kVec = 4;
     const bool small_tensors = n_chunks < 64 * static_cast<int64_t>(n);
-    const size_t lds = lds_for_cap(residency_cap<STAR, PBF16, POWK>(small_tensors), n_chunks);
-    hipLaunchKernelGGL((mta_step_kernel<STAR, GBF16, PBF16, POWK, kVec>), dim3(static_cast<unsigned>(n_chunks)),
+    const size_t lds = lds_for_cap(residency_cap<STAR, PM, POWK>(small_tensors), n_chunks);
+    hipLaunchKernelGGL((mta_step_kernel<STAR, GBF16, PM, POWK, kVec>), dim3(static_cast<unsigned>(n_chunks)),
                        dim3(kChunk / kVec), static_cast<unsigned>(lds), st, d, vs, cf, n, pack, partials,
                        counters);
 }
 
-template <bool STAR, bool GBF16, bool PBF16>
+template <bool STAR, bool GBF16, int PM>
 void launch_pow(int powk, int64_t n_chunks, hipStream_t st, const adana_tensor_desc *d,
                 const int64_t *vs, const int32_t *cf, int32_t n, const ScalarPack &pack,
                 float *partials, int32_t *counters) {
     if constexpr (!STAR) {
         // ADana's (1 + t) ** (1 - kappa) is a host scalar: no per-element pow
-        launch_main<false, GBF16, PBF16, POW_ONE>(n_chunks, st, d, vs, cf, n, pack, partials, counters);
+        launch_main<false, GBF16, PM, POW_ONE>(n_chunks, st, d, vs, cf, n, pack, partials, counters);
     } else if (powk == POW_GENERAL) {
-        launch_main<true, GBF16, PBF16, POW_GENERAL>(n_chunks, st, d, vs, cf, n, pack, partials, counters);
+        launch_main<true, GBF16, PM, POW_GENERAL>(n_chunks, st, d, vs, cf, n, pack, partials, counters);
     } else if (powk == POW_ONE) {
-        launch_main<true, GBF16, PBF16, POW_ONE>(n_chunks, st, d, vs, cf, n, pack, partials, counters);
+        launch_main<true, GBF16, PM, POW_ONE>(n_chunks, st, d, vs, cf, n, pack, partials, counters);
     } else if (powk == POW_SPECIAL) {
-        launch_main<true, GBF16, PBF16, POW_SPECIAL>(n_chunks, st, d, vs, cf, n, pack, partials, counters);
-    } else if constexpr (!GBF16 && !PBF16) {        // Manau's branch: float32 only
+        launch_main<true, GBF16, PM, POW_SPECIAL>(n_chunks, st, d, vs, cf, n, pack, partials, counters);
+    } else if constexpr (!GBF16 && PM == PM_F32) {  // Manau's branch: float32 only
         if (powk == POW_MANAU_GENERAL) {
-            launch_main<true, false, false, POW_MANAU_GENERAL>(n_chunks, st, d, vs, cf, n, pack, partials, counters);
+            launch_main<true, false, PM_F32, POW_MANAU_GENERAL>(n_chunks, st, d, vs, cf, n, pack, partials, counters);
         } else if (powk == POW_MANAU_ONE) {
-            launch_main<true, false, false, POW_MANAU_ONE>(n_chunks, st, d, vs, cf, n, pack, partials, counters);
+            launch_main<true, false, PM_F32, POW_MANAU_ONE>(n_chunks, st, d, vs, cf, n, pack, partials, counters);
         } else if (powk == POW_MANAU_SPECIAL) {
-            launch_main<true, false, false, POW_MANAU_SPECIAL>(n_chunks, st, d, vs, cf, n, pack, partials, counters);
+            launch_main<true, false, PM_F32, POW_MANAU_SPECIAL>(n_chunks, st, d, vs, cf, n, pack, partials, counters);
         } else {
-            launch_main<true, false, false, POW_MANAU_MK4>(n_chunks, st, d, vs, cf, n, pack, partials, counters);
+            launch_main<true, false, PM_F32, POW_MANAU_MK4>(n_chunks, st, d, vs, cf, n, pack, partials, counters);
         }
     }
 }
@@ -1336,12 +1543,16 @@ int step_impl(const char *fn, const adana_plan *plan, const adana_step_scalars *
     if (int rc = check_plan(plan, fn)) return rc;
     const adana_plan &pl = *plan;
     const uint32_t allowed = ADANA_VARIANT_STAR | ADANA_GRAD_BF16 | ADANA_PARAM_BF16 | ADANA_VARIANT_MANAU |
-                             (d_grad_scale ? ADANA_WRITE_GRAD : 0u);
+                             ADANA_STATE_BF16 | (d_grad_scale ? ADANA_WRITE_GRAD : 0u);
     if (variant_flags & ~allowed)
         return adana_set_error(ADANA_E_INVALID, "%s: unknown variant flags 0x%x", fn, variant_flags);
     const bool manau = variant_flags & ADANA_VARIANT_MANAU;
-    if (manau && (variant_flags & (ADANA_GRAD_BF16 | ADANA_PARAM_BF16)))
+    if (manau && (variant_flags & (ADANA_GRAD_BF16 | ADANA_PARAM_BF16 | ADANA_STATE_BF16)))
         return adana_set_error(ADANA_E_INVALID, "%s: ADANA_VARIANT_MANAU is float32 only", fn);
+    const bool s16 = variant_flags & ADANA_STATE_BF16;
+    if (s16 && (!(variant_flags & ADANA_GRAD_BF16) || (variant_flags & ADANA_PARAM_BF16)))
+        return adana_set_error(ADANA_E_INVALID, "%s: ADANA_STATE_BF16 needs ADANA_GRAD_BF16 and excludes "
+                               "ADANA_PARAM_BF16", fn);
     if (int rc = check_plan_arrays(pl, fn)) return rc;
     if (pl.n_tensors == 0) return ADANA_OK;
     if (!d_workspace || !d_diag || !h_scalars)
@@ -1389,11 +1600,13 @@ int step_impl(const char *fn, const adana_plan *plan, const adana_step_scalars *
         launch_pow<S, G, P>(powk, pl.n_chunks, st, pl.desc, pl.vstart, pl.chunk_first, n, pack, partials, \
                             counters)
         if (star || manau) {
-            if (gb) { if (pb) ADANA_LAUNCH(true, true, true); else ADANA_LAUNCH(true, true, false); }
-            else    { if (pb) ADANA_LAUNCH(true, false, true); else ADANA_LAUNCH(true, false, false); }
+            if (s16) ADANA_LAUNCH(true, true, PM_BF16);
+            else if (gb) { if (pb) ADANA_LAUNCH(true, true, PM_MASTER); else ADANA_LAUNCH(true, true, PM_F32); }
+            else         { if (pb) ADANA_LAUNCH(true, false, PM_MASTER); else ADANA_LAUNCH(true, false, PM_F32); }
         } else {
-            if (gb) { if (pb) ADANA_LAUNCH(false, true, true); else ADANA_LAUNCH(false, true, false); }
-            else    { if (pb) ADANA_LAUNCH(false, false, true); else ADANA_LAUNCH(false, false, false); }
+            if (s16) ADANA_LAUNCH(false, true, PM_BF16);
+            else if (gb) { if (pb) ADANA_LAUNCH(false, true, PM_MASTER); else ADANA_LAUNCH(false, true, PM_F32); }
+            else         { if (pb) ADANA_LAUNCH(false, false, PM_MASTER); else ADANA_LAUNCH(false, false, PM_F32); }
         }
 #undef ADANA_LAUNCH
         if (int rc = launch_status(fn, "main")) return rc;
@@ -1401,7 +1614,7 @@ int step_impl(const char *fn, const adana_plan *plan, const adana_step_scalars *
     const int64_t combine_wgs = pl.n_folds + (n + kWaves - 1) / kWaves;
     hipLaunchKernelGGL(combine_kernel, dim3(static_cast<unsigned>(combine_wgs)), dim3(kBlock), 0, st, pl.desc,
                        pl.vstart, pl.fold_first, n, static_cast<int32_t>(pl.n_folds), partials, folds, counters,
-                       d_diag);
+                       static_cast<void *>(d_diag), s16 ? 1 : 0);
     return launch_status(fn, "combine");
 }
 

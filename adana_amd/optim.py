@@ -7,7 +7,12 @@ instance attributes and per-parameter state keys are the reference's:
 
     state[p] = {'step': int, 'm': T, 'v': T, ['tau': T,]
                 'current_alpha', 'gradient_norm', 'auto_factor_mean',
-                'current_kappa_factor', 'm_norm'}            (0-d fp32 tensors)
+                'current_kappa_factor', 'm_norm'}        (0-d tensors of p's dtype)
+
+T has p's shape and dtype (zeros_like(p)).  bfloat16 parameters therefore
+run the reference's own bfloat16 path: bfloat16 m, v, tau and diagnostics,
+every op of the update rounded to bfloat16 as ATen's ops round it
+(ADANA_STATE_BF16).
 
 What differs is how a step executes.  The reference loops over tensors in
 Python, makes six 0-d device tensors per tensor and calls a torch.compile'd
@@ -26,8 +31,8 @@ into the next ``step()`` (adana_amd/clip.py).
 
 Extension (no reference counterpart): ``master_weights=True`` lets bfloat16
 parameters keep a float32 master copy (state key ``'master'``) with float32
-m/v[/tau]; the update runs in float32 on the master and the bf16 parameter is
-written as RNE(master) in the same pass.
+m/v[/tau] instead; the update runs in float32 on the master and the bf16
+parameter is written as RNE(master) in the same pass.
 """
 from __future__ import annotations
 
@@ -58,15 +63,19 @@ _SLAB_ALIGN = 1024      # elements (4 KB): every state tensor starts a fresh wor
 
 
 def _carve(buf: torch.Tensor, off: int, shape) -> torch.Tensor:
-    """A float32 tensor of ``shape`` over ``buf[off:]`` with a storage of its
-    own (not a view: deepcopy, torch.save and the like see only its bytes);
-    the slab lives as long as any tensor carved from it."""
+    """A tensor of ``shape`` and ``buf``'s dtype (float32 or bfloat16) over
+    ``buf[off:]`` with a storage of its own (deepcopy, torch.save and the
+    like see only its bytes); the slab lives as long as any tensor carved
+    from it.  bfloat16 has no array-interface type code: it is carved as
+    int16 and viewed as bfloat16 (a view of that private storage)."""
     ref = _SlabRef()
     ref.buf = buf
-    ref.__cuda_array_interface__ = {"shape": tuple(shape), "typestr": "<f4",
-                                    "data": (buf.data_ptr() + 4 * off, False),
+    bf16 = buf.dtype == torch.bfloat16
+    ref.__cuda_array_interface__ = {"shape": tuple(shape), "typestr": "<i2" if bf16 else "<f4",
+                                    "data": (buf.data_ptr() + buf.element_size() * off, False),
                                     "version": 3, "strides": None}
-    return torch.as_tensor(ref, device=buf.device)
+    t = torch.as_tensor(ref, device=buf.device)
+    return t.view(torch.bfloat16) if bf16 else t
 
 
 class _LaunchSet:
@@ -124,6 +133,11 @@ class _DanaFamily(Optimizer):
             fams.append("master")
         return fams
 
+    def _state_dtype(self, p: torch.Tensor) -> torch.dtype:
+        """dtype of p's m, v, tau: p's own, as zeros_like(p) gives it
+        (src/optim/adana.py:193-194), except float32 in master-weights mode."""
+        return torch.float32 if (p.dtype == torch.bfloat16 and self.master_weights) else p.dtype
+
     def _pack_states(self, items, source) -> None:
         """Allocate the state tensors of the (param, state) pairs ``items``:
         zero m, v[, tau] shaped like p (src/optim/adana.py:191-195;
@@ -144,22 +158,23 @@ class _DanaFamily(Optimizer):
                     elif fam == "master":
                         st[fam] = p.detach().to(torch.float32)
                     else:
-                        st[fam] = torch.zeros_like(p, dtype=torch.float32 if p.dtype == torch.bfloat16 else p.dtype)
+                        st[fam] = torch.zeros_like(p, dtype=self._state_dtype(p))
                 continue
             by_dev.setdefault(p.device, []).append((p, st))
         for dev, group in by_dev.items():
             fams = {}
             for p, st in group:
                 for fam in self._state_families(p):
-                    fams.setdefault(fam, []).append((p, st))
-            for fam, members in fams.items():
+                    dt = torch.float32 if fam == "master" else self._state_dtype(p)
+                    fams.setdefault((fam, dt), []).append((p, st))
+            for (fam, dt), members in fams.items():
                 offs, total = [], 0
                 for p, _ in members:
                     offs.append(total)
                     total += (p.numel() + _SLAB_ALIGN - 1) // _SLAB_ALIGN * _SLAB_ALIGN
-                # 4 KB of headroom so that the first tensor starts on a 4 KB boundary
-                slab = torch.zeros(total + _SLAB_ALIGN, dtype=torch.float32, device=dev)
-                base = (-(slab.data_ptr() // 4)) % _SLAB_ALIGN
+                # headroom so that the first tensor starts on a _SLAB_ALIGN-element boundary
+                slab = torch.zeros(total + _SLAB_ALIGN, dtype=dt, device=dev)
+                base = (-(slab.data_ptr() // slab.element_size())) % _SLAB_ALIGN
                 for (p, st), off in zip(members, offs):
                     t = _carve(slab, base + off, p.shape)
                     if source is not None:
@@ -271,14 +286,12 @@ class _DanaFamily(Optimizer):
                 raise RuntimeError(f"{type(self).__name__}: float32 parameter with {g.dtype} "
                                    "gradient (expected float32)")
         elif p.dtype == torch.bfloat16:
-            if not self.master_weights:
-                raise NotImplementedError(
-                    f"{type(self).__name__}: bfloat16 parameters need master_weights=True "
-                    "(float32 master copy and moments)")
             if g.dtype != torch.bfloat16:
                 raise RuntimeError(f"{type(self).__name__}: bfloat16 parameter with {g.dtype} "
                                    "gradient (expected bfloat16)")
-            flags |= _lib.PARAM_BF16 | _lib.GRAD_BF16
+            # master_weights: float32 master and moments (extension); otherwise the
+            # reference's own bfloat16 path, m, v, tau bfloat16 and every op rounded
+            flags |= _lib.GRAD_BF16 | (_lib.PARAM_BF16 if self.master_weights else _lib.STATE_BF16)
         else:
             raise NotImplementedError(f"{type(self).__name__}: parameter dtype {p.dtype}")
         return flags
@@ -298,8 +311,9 @@ class _DanaFamily(Optimizer):
             tau_ptr = st[kt].data_ptr() if self._STAR else 0
             gp = g.data_ptr()
             m_ptr, v_ptr = st[km].data_ptr(), st[kv].data_ptr()
-            rest[j] = (param_ptr % 16 == 0 and m_ptr % 16 == 0 and v_ptr % 16 == 0
-                       and tau_ptr % 16 == 0 and lp_ptr % 8 == 0)
+            vec = 8 if ls.flags & _lib.STATE_BF16 else 16       # 4 elements of the state dtype
+            rest[j] = (param_ptr % vec == 0 and m_ptr % vec == 0 and v_ptr % vec == 0
+                       and tau_ptr % vec == 0 and lp_ptr % 8 == 0)
             ok = rest[j] and gp % (8 if g.dtype == torch.bfloat16 else 16) == 0
             d[j] = (param_ptr, gp, m_ptr, v_ptr, tau_ptr, lp_ptr, p.numel(), ls.sclass[j],
                     _lib.DESC_VEC_OK if ok else 0)
@@ -356,8 +370,9 @@ class _DanaFamily(Optimizer):
                 ls.plan.chunk_first = ls.chunk_first.data_ptr()
                 ls.workspace = torch.empty(max(_lib.workspace_bytes(ls.plan), 1), dtype=torch.uint8,
                                            device=ls.device)
-                ls.diag = torch.full((len(ls.params), 5), float("nan"), dtype=torch.float32,
-                                     device=ls.device)
+                # the reference's bfloat16 path keeps bfloat16 diagnostics
+                ls.diag = torch.full((len(ls.params), 5), float("nan"), device=ls.device,
+                                     dtype=torch.bfloat16 if ls.flags & _lib.STATE_BF16 else torch.float32)
             for j, (p, st) in enumerate(zip(ls.params, ls.states)):
                 # 0-d tensors over the kernel's output rows, each with a storage
                 # of its own: a deepcopy of one parameter's state (DynamicsLogger,
@@ -389,7 +404,8 @@ class _DanaFamily(Optimizer):
                 if not st or mark not in st:
                     continue
                 loc = self._diag_loc.get(p)
-                if loc is not None and st[mark].data_ptr() != loc[0].data_ptr() + 4 * (5 * loc[1] + col0):
+                if loc is not None and st[mark].data_ptr() != (loc[0].data_ptr()
+                                                               + loc[0].element_size() * (5 * loc[1] + col0)):
                     loc = None                     # state tensors replaced (e.g. load_state_dict)
                 if loc is None:
                     loose.append((len(params), st))
@@ -411,7 +427,7 @@ class _DanaFamily(Optimizer):
             torch.cuda.current_stream(dev).synchronize()
         out = np.empty((len(params), 5), dtype=np.float32)
         for (buf, rows, pos), h in zip(bufs, host):
-            out[pos] = h.numpy()[rows]
+            out[pos] = (h.float() if h.dtype == torch.bfloat16 else h).numpy()[rows]
         for pos, st in loose:                      # loaded, not yet stepped: read one by one
             out[pos] = np.nan
             for col, k in self._DIAG_COLUMNS:

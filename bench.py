@@ -85,6 +85,12 @@ def workload(name):
         w = workload("north_star")
         w.update(name=name, clip=0.5, grad_note=w["grad_note"] + "; clip_grad_norm_(0.5) each step")
         return w
+    if name == "north_star_bf16":
+        # the reference's own bfloat16 path: bfloat16 parameters and gradients make m, v, tau
+        # bfloat16 (zeros_like(p)) and every op rounds to bfloat16
+        w = workload("north_star")
+        w.update(name=name, state_bf16=True, grad_note="bf16 N(0,1e-3); embedding rows nonzero w.p. 0.1")
+        return w
     if name in ("c4", "north_star"):
         decay, nodecay = gpt_shapes(50304, 2560, 32)
         if name == "c4":
@@ -104,6 +110,8 @@ def workload(name):
 
 
 def bytes_per_elem(w):
+    if w.get("state_bf16"):
+        return 18 if w["star"] else 14        # p, g, m, v (+tau) read, p, m, v (+tau) written, 2 B each
     if w["master"]:
         b = 28 + (8 if w["star"] else 0)      # master 4+4, g 2, m/v 16, p_bf16 2 (+tau 8)
     else:
@@ -141,7 +149,7 @@ def build_gpu(w, seed=0):
     dev = torch.device("cuda:0")
     gen = torch.Generator(device=dev)
     gen.manual_seed(seed)
-    pdtype = torch.bfloat16 if w["master"] else torch.float32
+    pdtype = torch.bfloat16 if (w["master"] or w.get("state_bf16")) else torch.float32
     groups, params = [], []
     zero_rng = np.random.default_rng(seed + 1)
     # Every parameter first, then every gradient: the order in which a model's
@@ -158,7 +166,7 @@ def build_gpu(w, seed=0):
             g = torch.empty(s, dtype=torch.float32, device=dev).normal_(0.0, 1e-3, generator=gen)
             if w["name"] == "c2" and len(s) == 1:
                 g.mul_(0.1)
-            if w["name"] in ("c3", "north_star", "north_star_clip") and gi == 1 and ti == 0:
+            if w["name"] in ("c3", "north_star", "north_star_clip", "north_star_bf16") and gi == 1 and ti == 0:
                 rows = torch.rand(s[0], device=dev, generator=gen) < 0.1     # row-sparse embedding grad
                 g.mul_(rows[:, None].to(g.dtype))
             if w["name"] == "c5" and zero_rng.random() < 0.05:
@@ -199,7 +207,9 @@ def cpu_baseline(w, target_s=10.0, max_elems=1 << 25):
     src/optim/dana_star_mk4.py:215-294; bit-identical to the reference's own
     eager run, tests/test_torch_restatement.py), torch.set_num_threads over
     the cores.  Beside it, the C oracle (oracle/adana_oracle.c, OpenMP) on the
-    same sample.  bf16-master workloads time the float32 master update."""
+    same sample.  bf16-master workloads time the float32 master update; the
+    bf16-state workload (the reference's own bfloat16 path) runs both on
+    bfloat16 tensors."""
     import torch
 
     from oracle import oracle as O
@@ -225,10 +235,12 @@ def cpu_baseline(w, target_s=10.0, max_elems=1 << 25):
             if el >= target_s or reps >= 50:
                 return el / reps, reps
 
+    s16 = bool(w.get("state_bf16"))
+    tdt = torch.bfloat16 if s16 else torch.float32
     prev = torch.get_num_threads()
     torch.set_num_threads(cores)
-    tp = [torch.from_numpy(x.copy()) for x in ps]
-    tg = [[torch.from_numpy(x) for x in gs]]
+    tp = [torch.from_numpy(x.copy()).to(tdt) for x in ps]
+    tg = [[torch.from_numpy(x).to(tdt) for x in gs]]
     ref = TorchRefOptimizer(groups=[TorchRefGroup(params=tp, lr=hp["lr"], delta=hp["delta"], epsilon=hp["epsilon"],
                                                   weight_decay=hp["weight_decay"])],
                             star=w["star"], peak_lr=hp["lr"], kappa=hp["kappa"], clipsnr=hp["clipsnr"],
@@ -238,13 +250,15 @@ def cpu_baseline(w, target_s=10.0, max_elems=1 << 25):
     del tp, tg, ref
 
     threads = O.set_threads(cores)
-    opt = O.OracleOptimizer(groups=[O.OracleGroup(params=[x.copy() for x in ps], lr=hp["lr"], delta=hp["delta"],
+    cps = [O.f32_to_bf16(x) for x in ps] if s16 else [x.copy() for x in ps]
+    cgs = [O.f32_to_bf16(x) for x in gs] if s16 else gs
+    opt = O.OracleOptimizer(groups=[O.OracleGroup(params=cps, lr=hp["lr"], delta=hp["delta"],
                                                   epsilon=hp["epsilon"], weight_decay=hp["weight_decay"])],
                             star=w["star"], peak_lr=hp["lr"], kappa=hp["kappa"], clipsnr=hp["clipsnr"],
-                            wd_decaying=hp["wd_decaying"], wd_ts=hp["wd_ts"])
-    per_c, reps_c = timed(lambda: opt.step([gs]))
+                            wd_decaying=hp["wd_decaying"], wd_ts=hp["wd_ts"], bf16=s16)
+    per_c, reps_c = timed(lambda: opt.step([cgs]))
     sample = (f"{total} of the workload's {all_elems} elements ({100 * frac:.2f}%): its first {len(sizes)} tensors, "
-              f"fp32")
+              f"{'bf16 parameters and state' if s16 else 'fp32'}")
     return {"value": round(total * bpe / per_t / 1e9, 3), "unit": "GB/s", "cores": cores, "kind": "port",
             "cpu_model": cpu_model(),
             "sample": f"{sample}; oracle/torch_ref.py (the reference's step() as torch eager ops, per-tensor "
@@ -690,7 +704,7 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--workload", default="north_star",
-                    choices=["north_star", "north_star_clip", "c1", "c2", "c3", "c4", "c5",
+                    choices=["north_star", "north_star_clip", "north_star_bf16", "c1", "c2", "c3", "c4", "c5",
                              "copy_probe", "tau_stats", "diag_readout", "manau", "stream_sweep"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-ceiling-probe", action="store_true",
@@ -815,7 +829,7 @@ def main():
         "metric": METRIC, "value": round(value, 2), "unit": "GB/s", "n_gpus": 1,
         "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms_per_step, 4),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
-        "dtype": "bf16+f32" if w["master"] else "f32", "data": "synthetic",
+        "dtype": "bf16+f32" if w["master"] else ("bf16" if w.get("state_bf16") else "f32"), "data": "synthetic",
         "config": {"workload": w["name"], "optimizer": w["optimizer"], "params": n_elems,
                    "tensors": len(params), "bytes_per_elem": bpe,
                    "algorithmic_bytes_per_step": algo_bytes, "grads": w["grad_note"],

@@ -67,7 +67,7 @@
 extern "C" {
 #endif
 
-#define ADANA_ABI_VERSION 4
+#define ADANA_ABI_VERSION 5
 
 /* Elements per work chunk (one 256-thread workgroup, one 16-byte vector per
  * thread per array).  Tensors start at multiples of ADANA_ALIGN_ELEMS in the
@@ -93,9 +93,17 @@ extern "C" {
 #define ADANA_VARIANT_MANAU 0x10u /* Manau's Dana-Star-MK4 branch: tau state,
                                     Manau's op order; float32 only; scalars
                                     from adana_manau_scalars_init            */
+#define ADANA_STATE_BF16   0x20u /* the reference's own bfloat16 path: param,
+                                    m, v, tau (and, with ADANA_GRAD_BF16,
+                                    which it requires, grad) are bfloat16 and
+                                    every op rounds to bfloat16 as ATen's do;
+                                    d_diag holds 5 bfloat16 per tensor;
+                                    excludes ADANA_PARAM_BF16                */
 
 /* adana_tensor_desc.flags */
-#define ADANA_DESC_VEC_OK  0x1u  /* all pointers aligned for 16-byte access   */
+#define ADANA_DESC_VEC_OK  0x1u  /* all pointers aligned for the vector path:
+                                    16 bytes for float32 arrays, 8 for
+                                    bfloat16 ones                            */
 
 /* Error codes */
 #define ADANA_OK              0
@@ -107,9 +115,10 @@ extern "C" {
 typedef struct adana_tensor_desc {
     void       *param;     /* float32 param, or the float32 master copy      */
     const void *grad;      /* float32 or bfloat16 gradient (same numel)      */
-    float      *m;         /* first moment, float32                          */
-    float      *v;         /* second moment, float32                         */
-    float      *tau;       /* Dana-Star tau, float32 (NULL otherwise)        */
+    float      *m;         /* first moment, float32 (bfloat16 with
+                              ADANA_STATE_BF16, as are v and tau)            */
+    float      *v;         /* second moment                                  */
+    float      *tau;       /* Dana-Star tau (NULL otherwise)                 */
     void       *param_lp;  /* bfloat16 param written as RNE(master), or NULL */
     int64_t     numel;
     int32_t     sclass;    /* index into the launch's scalar classes         */
@@ -255,7 +264,8 @@ size_t adana_workspace_bytes(const adana_plan *plan);
  *               per tensor; contents on entry are ignored)
  *   d_diag      device float[5 * n_tensors]: per tensor current_alpha,
  *               gradient_norm, auto_factor_mean, current_kappa_factor,
- *               m_norm (src/optim/adana.py:221-225)
+ *               m_norm (src/optim/adana.py:221-225); with ADANA_STATE_BF16
+ *               5 * n_tensors bfloat16 values instead
  *   stream      hipStream_t (NULL = default stream)
  * All tensors of one call share variant_flags. */
 int adana_mta_step(const adana_plan *plan, const adana_step_scalars *h_scalars,

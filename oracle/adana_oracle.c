@@ -12,6 +12,9 @@
  *                               src/optim/dana_star_mk4.py:136-203
  *   adana_oracle_manau_step  <- Manau.step's Dana-Star-MK4 branch
  *                               src/optim/manau.py:556-613
+ *   adana_oracle_step_bf16   <- both updates on bfloat16 parameters (the
+ *                               reference's own bfloat16 path, every op
+ *                               rounded to bfloat16; rules below)
  *
  * Arithmetic contract (the oracle of record):
  *   - every tensor op of the reference is one IEEE-754 binary32 operation,
@@ -208,6 +211,89 @@ static inline float manau_elem(float p, float g, float *mp, float *vp, float *tp
     return p;
 }
 
+/* ---------------------------------------------------------------------------
+ * The reference's own bfloat16 path: bfloat16 parameters make m, v and tau
+ * bfloat16 too (zeros_like(p), src/optim/adana.py:191-195;
+ * src/optim/dana_star_mk4.py:251-255), and every tensor op of the update
+ * rounds its result to bfloat16 after computing in binary32, as ATen's CPU
+ * kernels do.  How each op meets its binary32 0-d and Python-scalar
+ * operands was probed op by op against torch 2.10's CPU kernels and is
+ * pinned by the reference's own bfloat16 run (tests/golden/, the bf16_eager fixtures):
+ *   - lerp_(end, w), w a float32 0-d tensor: w is rounded to bfloat16 first;
+ *   - mul / div with the 0-d tensor as the second operand (v.mul_(1 - a),
+ *     tau * step, p.mul_(1 + wd)): binary32 value as it is;
+ *   - the 0-d tensor as the first operand ((-g2) * grad, (-g3)*gf * ...,
+ *     pow * mfac in ADana, min_p + relu(...)), or any add / sub with a
+ *     scalar (add_(epsilon), pe - min_p): the scalar rounded to bfloat16;
+ *   - addcmul_(g, g, value=a): (a * g) * g + v in binary32, a unrounded;
+ *   - Dana-Star's pow(et, 1 - kappa): the exponent rounded to bfloat16;
+ *   - clamp(x, max=c): c rounded to bfloat16.
+ * ------------------------------------------------------------------------- */
+static inline float rb(float x) { return bf16_to_f32(f32_to_bf16(x)); }
+
+/* x ** e16 (e16 already bfloat16) by ATen's specialisation, rounded once to
+ * binary32 and then to bfloat16. */
+static inline float o_pow16(float x, float e16, int32_t mode) { return rb(o_pow_mode(x, e16, mode)); }
+
+static inline float adana_elem16(float p, float g, float *mp, float *vp, const adana_oracle_scalars *sc,
+                                 double acc[4]) {
+    const float a16 = rb(sc->a);
+    float m = rb(o_lerp(*mp, g, a16));                       /* :101 */
+    float v = rb(*vp * sc->oma);                             /* :104 mul_ */
+    v = rb(fmaf(sc->a * g, g, v));                           /* :104 addcmul_ */
+    float se = rb(rb(sqrtf(v)) + rb(sc->eps));               /* :107 */
+    float nt = rb(1.0f / se);                                /* :110 */
+    float mn = rb(fabsf(m) * nt);                            /* :111, :115 */
+    float af = rb(rb(sc->pw) * mn);                          /* :119/:123 */
+    if (sc->has_clip) af = o_clamp_max(af, rb(sc->clip));
+    float inner = rb(o_sign(m) * af + rb(m * nt));           /* :126 */
+    float g3t = rb(rb(sc->c3) * inner);
+    float g2t = rb(rb(rb(sc->cg2) * g) * nt);                /* :129 */
+    p = rb(p + rb(g2t + g3t));                               /* :132-135 */
+    p = rb(p * sc->opw);                                     /* :143 */
+    *mp = m;
+    *vp = v;
+    acc[0] += (double)af;
+    acc[1] += (double)g * (double)g;
+    acc[2] += (double)mn;
+    acc[3] += (double)m * (double)m;
+    return p;
+}
+
+static inline float star_elem16(float p, float g, float *mp, float *vp, float *tp,
+                                const adana_oracle_scalars *sc, double acc[4]) {
+    const float a16 = rb(sc->a), minp16 = rb(sc->min_p);
+    float m = rb(o_lerp(*mp, g, a16));                       /* :137 */
+    float v = rb(*vp * sc->oma);                             /* :140 */
+    v = rb(fmaf(sc->a * g, g, v));
+    float se = rb(rb(sqrtf(v)) + rb(sc->eps));               /* :143 */
+    float ag = fabsf(g);                                     /* :147 */
+    float tu = rb(ag / rb(ag + se));                         /* :148 */
+    float tau = rb(o_lerp(*tp, tu, a16));                    /* :149 */
+    float ct = o_clamp_max(tau, 0.5f);                       /* :152 */
+    float pe = rb(ct / rb(1.0f - ct));                       /* :153 */
+    float tr = rb(minp16 + o_relu(rb(pe - minp16)));         /* :154-156 */
+    float et = o_clamp_min(rb(tau * sc->s), 1.0f);           /* :159 */
+    float nt = rb(rb(sqrtf(tr)) / se);                       /* :163-164 */
+    float mnt = rb(fabsf(m) * nt);                           /* :165 */
+    float mf = rb(mnt / tr);                                 /* :167 */
+    float af = rb(o_pow16(et, rb(sc->star_exp), sc->pow_mode) * mf);   /* :170 / :174 */
+    if (sc->has_clip) af = o_clamp_max(af, rb(sc->clip));
+    float inner = o_sign(m) * rb(rb(tr * af) + mnt);         /* :177 */
+    float g3t = rb(rb(sc->c3) * inner);
+    float g2t = rb(rb(rb(sc->cg2) * g) * nt);                /* :180 */
+    p = rb(p + rb(g2t + g3t));                               /* :183-186 */
+    p = rb(p * sc->opw);                                     /* :195 */
+    *mp = m;
+    *vp = v;
+    *tp = tau;
+    acc[0] += (double)af;
+    acc[1] += (double)g * (double)g;
+    acc[2] += (double)mf;
+    acc[3] += (double)m * (double)m;
+    return p;
+}
+
 /* Parallel element loops.  Element results do not depend on the thread
  * count; the binary64 diagnostic sums may differ in the last bits. */
 #define DIAG_LOOP(BODY)                                                        \
@@ -259,6 +345,21 @@ void adana_oracle_step_g16(int64_t n, int32_t star, float *p, const uint16_t *g1
         DIAG_LOOP(p[i] = star_elem(p[i], bf16_to_f32(g16[i]), &m[i], &v[i], &tau[i], sc, acc))
     } else {
         DIAG_LOOP(p[i] = adana_elem(p[i], bf16_to_f32(g16[i]), &m[i], &v[i], sc, acc))
+    }
+}
+
+/* The reference's bfloat16 path: p, g, m, v and tau all bfloat16 (tau may
+ * be NULL for the ADana variants). */
+void adana_oracle_step_bf16(int64_t n, int32_t star, uint16_t *p, const uint16_t *g, uint16_t *m,
+                            uint16_t *v, uint16_t *tau, const adana_oracle_scalars *sc, double diag[4]) {
+    if (star) {
+        DIAG_LOOP(float mm = bf16_to_f32(m[i]); float vv = bf16_to_f32(v[i]); float tt = bf16_to_f32(tau[i]);
+                  p[i] = f32_to_bf16(star_elem16(bf16_to_f32(p[i]), bf16_to_f32(g[i]), &mm, &vv, &tt, sc, acc));
+                  m[i] = f32_to_bf16(mm); v[i] = f32_to_bf16(vv); tau[i] = f32_to_bf16(tt))
+    } else {
+        DIAG_LOOP(float mm = bf16_to_f32(m[i]); float vv = bf16_to_f32(v[i]);
+                  p[i] = f32_to_bf16(adana_elem16(bf16_to_f32(p[i]), bf16_to_f32(g[i]), &mm, &vv, sc, acc));
+                  m[i] = f32_to_bf16(mm); v[i] = f32_to_bf16(vv))
     }
 }
 

@@ -60,6 +60,8 @@ void adana_oracle_master_step(int64_t n, int32_t star, float *master, uint16_t *
                               const adana_oracle_scalars *sc, double diag[4]);
 void adana_oracle_step_g16(int64_t n, int32_t star, float *p, const uint16_t *g16, float *m,
                            float *v, float *tau, const adana_oracle_scalars *sc, double diag[4]);
+void adana_oracle_step_bf16(int64_t n, int32_t star, uint16_t *p, const uint16_t *g, uint16_t *m,
+                            uint16_t *v, uint16_t *tau, const adana_oracle_scalars *sc, double diag[4]);
 void adana_oracle_f32_to_bf16(int64_t n, const float *x, uint16_t *y);
 int adana_oracle_abi_version(void);
 void adana_oracle_set_threads(int n);

@@ -82,6 +82,7 @@ def lib():
         L.adana_oracle_manau_step.argtypes = [i64, P, P, P, P, P, ctypes.POINTER(OracleManauScalars), P]
         L.adana_oracle_master_step.argtypes = [i64, i32, P, P, P, P, P, P, SP, P]
         L.adana_oracle_step_g16.argtypes = [i64, i32, P, P, P, P, P, SP, P]
+        L.adana_oracle_step_bf16.argtypes = [i64, i32, P, P, P, P, P, SP, P]
         L.adana_oracle_f32_to_bf16.argtypes = [i64, P, P]
         L.adana_oracle_set_threads.argtypes = [ctypes.c_int]
         L.adana_oracle_set_threads.restype = None
@@ -89,7 +90,7 @@ def lib():
         L.adana_oracle_get_threads.restype = ctypes.c_int
         for fn in (L.adana_oracle_adana_step, L.adana_oracle_star_step,
                    L.adana_oracle_master_step, L.adana_oracle_step_g16,
-                   L.adana_oracle_f32_to_bf16):
+                   L.adana_oracle_step_bf16, L.adana_oracle_f32_to_bf16):
             fn.restype = None
         _lib = L
     return _lib
@@ -216,6 +217,10 @@ def element_step(star: bool, p: np.ndarray, g: np.ndarray, m: np.ndarray, v: np.
     elif g.dtype == np.uint16 and p.dtype == np.float32:
         L.adana_oracle_step_g16(n, int(star), _ptr(p), _ptr(g), _ptr(m), _ptr(v),
                                 _ptr(tau) if star else None, ctypes.byref(sc), _ptr(diag))
+    elif g.dtype == np.uint16 and p.dtype == np.uint16 and m.dtype == np.uint16:
+        # the reference's own bfloat16 path: p, g, m, v, tau all bfloat16 bits
+        L.adana_oracle_step_bf16(n, int(star), _ptr(p), _ptr(g), _ptr(m), _ptr(v),
+                                 _ptr(tau) if star else None, ctypes.byref(sc), _ptr(diag))
     else:
         raise TypeError(f"oracle: unsupported dtypes p={p.dtype} g={g.dtype}")
     return diag
@@ -295,15 +300,24 @@ DIAG_KEYS = ("current_alpha", "gradient_norm", "auto_factor_mean",
              "current_kappa_factor", "m_norm")
 
 
-def finalize_diag(sums: np.ndarray, n: int) -> Dict[str, float]:
-    """Per-tensor diagnostics from binary64 sums (src/optim/adana.py:146-151,221-225)."""
+def finalize_diag(sums: np.ndarray, n: int, bf16: bool = False) -> Dict[str, float]:
+    """Per-tensor diagnostics from binary64 sums (src/optim/adana.py:146-151,221-225).
+    bf16: the reference's bfloat16 path, where each diagnostic is a bfloat16
+    0-d tensor (binary32 reduction rounded to bfloat16) and the kappa factor
+    is the quotient of the two rounded values, itself rounded."""
     with np.errstate(invalid="ignore", divide="ignore"):
         ca = sums[0] / n if n else float("nan")
         afm = sums[2] / n if n else float("nan")
-        kf = np.float64(ca) / np.float64(afm)
-    return {"current_alpha": float(ca), "gradient_norm": math.sqrt(sums[1]),
+        gn, mn = math.sqrt(sums[1]), math.sqrt(sums[3])
+        if bf16:
+            r = lambda x: float(bf16_to_f32(f32_to_bf16(np.array([x], np.float32)))[0])  # noqa: E731
+            ca, afm, gn, mn = r(ca), r(afm), r(gn), r(mn)
+            kf = r(np.float32(ca) / np.float32(afm))
+        else:
+            kf = np.float64(ca) / np.float64(afm)
+    return {"current_alpha": float(ca), "gradient_norm": gn,
             "auto_factor_mean": float(afm), "current_kappa_factor": float(kf),
-            "m_norm": math.sqrt(sums[3])}
+            "m_norm": mn}
 
 
 @dataclass
@@ -323,7 +337,9 @@ class OracleOptimizer:
     ``star`` selects Dana-Star(-MK4); ``clipsnr=None`` disables SNR clipping.
     ``peak_lr`` plays the part of the constructor's ``lr`` (``self.lr``).
     Params are float32 arrays (or, with ``master=True``, uint16 bf16 arrays
-    with an fp32 master copy kept in the state).
+    with an fp32 master copy kept in the state; or, with ``bf16=True``, uint16
+    bf16 arrays whose m, v, tau are bf16 too: the reference's own bfloat16
+    path).
     """
 
     groups: List[OracleGroup]
@@ -335,6 +351,7 @@ class OracleOptimizer:
     wd_ts: float = 1.0
     gamma_3_factor: float = 1.0
     master: bool = False
+    bf16: bool = False
     state: Dict[int, dict] = field(default_factory=dict)
 
     def step(self, grads: Sequence[Sequence[Optional[np.ndarray]]]) -> None:
@@ -349,11 +366,12 @@ class OracleOptimizer:
                 key = id(p)
                 st = self.state.get(key)
                 if st is None:                                 # adana.py:191-195
+                    sdt = np.uint16 if self.bf16 else np.float32     # zeros_like(p)
                     st = {"step": 0,
-                          "m": np.zeros(p.shape, np.float32),
-                          "v": np.zeros(p.shape, np.float32)}
+                          "m": np.zeros(p.shape, sdt),
+                          "v": np.zeros(p.shape, sdt)}
                     if self.star:
-                        st["tau"] = np.zeros(p.shape, np.float32)
+                        st["tau"] = np.zeros(p.shape, sdt)
                     if self.master:
                         st["master"] = bf16_to_f32(p).reshape(p.shape).copy()
                     self.state[key] = st
@@ -368,7 +386,7 @@ class OracleOptimizer:
                                        st.get("tau"), sc)
                 else:
                     sums = element_step(self.star, p, g, st["m"], st["v"], st.get("tau"), sc)
-                st.update(finalize_diag(sums, p.size))
+                st.update(finalize_diag(sums, p.size, bf16=self.bf16))
 
 
 # --------------------------------------------------------------------------

@@ -23,6 +23,14 @@ schema of keys, Python types, dtypes and shapes): the checkpoint interchange
 tests load it into this build's optimizers and compare schemas
 (src/optim/utils.py:283-310 saves exactly this dict).
 
+A fifth output (--bf16) runs every case with the reference's own bfloat16
+path: bfloat16 parameters and gradients (the float32 inputs rounded to
+nearest even), so ``zeros_like(p)`` makes m, v and tau bfloat16 as well and
+every tensor op rounds to bfloat16 (src/optim/adana.py:191-195;
+src/optim/dana_star_mk4.py:251-255).  Both modes are recorded, eager and
+``torch.compile``: ``<case>.bf16_eager.npz`` / ``<case>.bf16_compiled.npz``,
+tensors stored as their 16-bit patterns (uint16), diagnostics as float32.
+
 A fourth output (--nonfinite) repeats the eager runs of four cases with a few
 NaN / +inf / -inf gradient entries (NONFINITE) and stores them as
 ``nonfinite.inputs.npz`` and ``<case>.nonfinite.npz``: how the reference's
@@ -154,12 +162,21 @@ def state_dict_fixture(sd) -> dict:
     return out
 
 
-def run_case(ref: str, case: str, compiled: bool, p0, grads, has_grad, state_out=None):
+def _bits(t) -> np.ndarray:
+    """A tensor as numpy: float32 values, or the 16-bit patterns of bfloat16."""
+    import torch
+
+    t = t.detach().cpu()
+    return t.view(torch.int16).numpy().view(np.uint16).copy() if t.dtype == torch.bfloat16 else t.numpy().copy()
+
+
+def run_case(ref: str, case: str, compiled: bool, p0, grads, has_grad, state_out=None, bf16: bool = False):
     import torch
 
     modname, clsname, kw = CASES[case]
     cls = getattr(load_module(ref, modname), clsname)
-    params = [torch.nn.Parameter(torch.from_numpy(x.copy())) for x in p0]
+    dt = torch.bfloat16 if bf16 else torch.float32
+    params = [torch.nn.Parameter(torch.from_numpy(x.copy()).to(dt)) for x in p0]
     groups = []
     for gi, scale in enumerate(GROUP_WD_SCALE):
         groups.append({"params": [p for i, p in enumerate(params) if GROUP_OF[i] == gi],
@@ -176,7 +193,7 @@ def run_case(ref: str, case: str, compiled: bool, p0, grads, has_grad, state_out
         for g in opt.param_groups:
             g["lr"] = peak * lr_multiplier(k)
         for i, p in enumerate(params):
-            p.grad = torch.from_numpy(grads[k - 1][i].copy()) if has_grad[k - 1, i] else None
+            p.grad = torch.from_numpy(grads[k - 1][i].copy()).to(dt) if has_grad[k - 1, i] else None
         opt.step()
         for i, p in enumerate(params):
             st = opt.state[p]
@@ -187,10 +204,10 @@ def run_case(ref: str, case: str, compiled: bool, p0, grads, has_grad, state_out
         if k in CHECKPOINTS:
             for i, p in enumerate(params):
                 st = opt.state[p]
-                out[f"p{i}_t{k}"] = p.detach().numpy().copy()
+                out[f"p{i}_t{k}"] = _bits(p)
                 for name in ("m", "v", "tau"):
                     if name in st:
-                        out[f"{name}{i}_t{k}"] = st[name].numpy().copy()
+                        out[f"{name}{i}_t{k}"] = _bits(st[name])
                 out[f"step{i}_t{k}"] = np.int64(st.get("step", 0))
     out["diag"] = diags
     out["weighted_step_count"] = np.array([g["weighted_step_count"] for g in opt.param_groups])
@@ -203,6 +220,8 @@ def main():
     ap.add_argument("--compiled", action="store_true")
     ap.add_argument("--state-only", action="store_true",
                     help="only (re)write the <case>.state8.npz checkpoint fixtures")
+    ap.add_argument("--bf16", action="store_true",
+                    help="only write <case>.bf16_eager.npz and <case>.bf16_compiled.npz (bfloat16 parameters)")
     ap.add_argument("--nonfinite", action="store_true",
                     help="only write nonfinite.inputs.npz and <case>.nonfinite.npz (NaN/inf gradient entries)")
     args = ap.parse_args()
@@ -237,6 +256,13 @@ def main():
             out = run_case(args.ref, case, False, p0, grads_nf, has_grad)
             np.savez_compressed(os.path.join(HERE, f"{case}.nonfinite.npz"), **out)
             print(f"wrote {case}.nonfinite.npz", flush=True)
+        return 0
+    if args.bf16:
+        for mode in ("eager", "compiled"):
+            for case in CASES:
+                out = run_case(args.ref, case, mode == "compiled", p0, grads, has_grad, bf16=True)
+                np.savez_compressed(os.path.join(HERE, f"{case}.bf16_{mode}.npz"), **out)
+                print(f"wrote {case}.bf16_{mode}.npz", flush=True)
         return 0
     if args.state_only:
         for case in CASES:

@@ -361,3 +361,61 @@ def test_gamma3_zero_is_rmsprop_like(oracle_mod):
     v = (8.0 / 9.0) * g.astype(np.float64) ** 2
     pd = pd - 1e-2 * g / (np.sqrt(v) + 1e-8)
     np.testing.assert_allclose(p, pd, rtol=1e-6, atol=3e-9)
+
+
+# --------------------------------------------------------------------------
+# The reference's own bfloat16 path (bfloat16 parameters, m, v, tau)
+# --------------------------------------------------------------------------
+
+@pytest.mark.parametrize("case", golden_cases("bf16_eager"))
+def test_bf16_golden_trajectory(oracle_mod, case):
+    """The oracle's bfloat16 restatement (adana_oracle_step_bf16) follows the
+    reference's own bfloat16 eager run (tests/golden/<case>.bf16_eager.npz)
+    bit for bit: p, m, v, tau at every checkpoint and all five bfloat16
+    diagnostics at every step."""
+    from helpers import bf16_ulp_diff
+
+    O = oracle_mod
+    meta, p0, grads, has_grad = load_golden_inputs()
+    gold = load_golden_case(case, "bf16_eager")
+    params = [O.f32_to_bf16(x) for x in p0]
+    opt, kw, star = _make_oracle(O, meta, case, params)
+    opt.bf16 = True
+    for k in range(1, meta["n_steps"] + 1):
+        for g in opt.groups:
+            g.lr = kw["lr"] * meta["lr_multiplier"][k - 1]
+        gl = _grads_for_step(meta, [[O.f32_to_bf16(x) for x in gs] for gs in grads], has_grad, k)
+        opt.step(gl)
+        for i, p in enumerate(params):
+            st = opt.state.get(id(p))
+            if st is None or not has_grad[k - 1, i]:
+                continue
+            got = np.array([st[key] for key in O.DIAG_KEYS], np.float32)
+            ref = gold["diag"][k - 1, i]
+            assert np.array_equal(np.isnan(got), np.isnan(ref)) and np.array_equal(got[~np.isnan(got)],
+                                                                                ref[~np.isnan(ref)]), (case, k, i)
+        if k not in meta["checkpoints"]:
+            continue
+        for i, p in enumerate(params):
+            assert bf16_ulp_diff(p, gold[f"p{i}_t{k}"]).max() == 0, (case, "p", k, i)
+            st = opt.state.get(id(p))
+            if st is None:
+                continue
+            for key in ("m", "v", "tau") if star else ("m", "v"):
+                assert st[key].dtype == np.uint16
+                assert bf16_ulp_diff(st[key], gold[f"{key}{i}_t{k}"]).max() == 0, (case, key, k, i)
+
+
+@pytest.mark.parametrize("case", ["adana", "dana_star_mk4"])
+def test_bf16_reference_modes_differ(case):
+    """The reference's torch.compile path does not round its intermediates to
+    bfloat16 (Inductor keeps them in binary32), so its bfloat16 run differs
+    from its eager run; the oracle follows the eager one.  Recorded so that
+    the choice stays visible."""
+    from helpers import bf16_ulp_diff
+
+    meta = load_golden_inputs()[0]
+    e, c = load_golden_case(case, "bf16_eager"), load_golden_case(case, "bf16_compiled")
+    k = meta["checkpoints"][0]
+    assert any(bf16_ulp_diff(e[f"m{i}_t{k}"], c[f"m{i}_t{k}"]).max() > 0 for i in range(len(meta["shapes"]))
+               if f"m{i}_t{k}" in e)

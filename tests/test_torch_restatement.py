@@ -209,3 +209,36 @@ def test_planted_slips_are_caught(slip):
         moved = moved or any(not np.array_equal(p.numpy().view(np.int32), gold[case][f"p{i}_t{k}"].view(np.int32))
                              for i, p in enumerate(params))
     assert moved, slip
+
+
+@pytest.mark.skipif(torch.backends.cpu.get_cpu_capability() != load_golden_inputs()[0].get("cpu_capability"),
+                    reason="torch's CPU sqrt/pow bits depend on the SIMD level the fixtures were written with")
+@pytest.mark.parametrize("case", golden_cases("bf16_eager"))
+def test_torch_restatement_reproduces_reference_bf16_bits(case):
+    """The same torch restatement on bfloat16 parameters (m, v, tau bfloat16
+    by zeros_like) gives the reference's own bfloat16 eager bits."""
+    from oracle.torch_ref import TorchRefGroup, TorchRefOptimizer
+
+    meta, p0, grads, has_grad = load_golden_inputs()
+    gold = load_golden_case(case, "bf16_eager")
+    kw = meta["cases"][case]["kwargs"]
+    star = meta["cases"][case]["class"] == "DANA_STAR_MK4"
+    params = [torch.from_numpy(x.copy()).to(torch.bfloat16) for x in p0]
+    idx = [[i for i in range(len(params)) if meta["group_of"][i] == gi] for gi in range(2)]
+    groups = [TorchRefGroup(params=[params[i] for i in idx[gi]], lr=kw["lr"], delta=kw["delta"], epsilon=1e-8,
+                            weight_decay=kw["weight_decay"] * meta["group_wd_scale"][gi]) for gi in range(2)]
+    opt = TorchRefOptimizer(groups=groups, star=star, peak_lr=kw["lr"], kappa=kw["kappa"], clipsnr=kw["clipsnr"],
+                            wd_decaying=kw["wd_decaying"], wd_ts=kw["wd_ts"], gamma_3_factor=kw["gamma_3_factor"])
+    bits = lambda t: t.view(torch.int16).numpy().view(np.uint16)          # noqa: E731
+    for k in range(1, meta["n_steps"] + 1):
+        for g in groups:
+            g.lr = kw["lr"] * meta["lr_multiplier"][k - 1]
+        opt.step([[torch.from_numpy(grads[k - 1][i].copy()).to(torch.bfloat16) if has_grad[k - 1, i] else None
+                   for i in idx[gi]] for gi in range(2)])
+        if k not in meta["checkpoints"]:
+            continue
+        for i, p in enumerate(params):
+            assert np.array_equal(bits(p), gold[f"p{i}_t{k}"]), (case, k, i)
+            st = opt.state.get(id(p))
+            for key in (("m", "v", "tau") if star else ("m", "v")) if st else ():
+                assert np.array_equal(bits(st[key]), gold[f"{key}{i}_t{k}"]), (case, key, k, i)
