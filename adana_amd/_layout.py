@@ -1,0 +1,27 @@
+"""Memory layouts the element-wise step can run over in storage order."""
+from __future__ import annotations
+
+import torch
+
+
+def dense_layout(t: torch.Tensor) -> bool:
+    """Whether t's elements fill one gap-free, non-overlapping block of
+    memory in some order (contiguous, or a permutation of it such as a
+    transposed matrix): then an element-wise update can run over its
+    numel() elements from data_ptr() on.  Dimensions of size 1 are ignored,
+    and an empty tensor (whatever its strides) has nothing to lay out."""
+    if t.numel() == 0:
+        return True
+    dims = sorted((st, n) for n, st in zip(t.shape, t.stride()) if n != 1)
+    expect = 1
+    for st, n in dims:
+        if st != expect:
+            return False
+        expect *= n
+    return True
+
+
+def same_layout(a: torch.Tensor, b: torch.Tensor) -> bool:
+    """Same shape and the same strides on every dimension of size > 1 (any
+    strides, for empty tensors)."""
+    return a.shape == b.shape and (a.numel() == 0 or all(n == 1 or sa == sb for n, sa, sb in zip(a.shape, a.stride(), b.stride())))

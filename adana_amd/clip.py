@@ -35,6 +35,7 @@ import numpy as np
 import torch
 
 from . import _hoststep, _lib
+from ._layout import dense_layout
 
 __all__ = ["clip_grad_norm_", "GradPlan"]
 
@@ -149,8 +150,9 @@ def _validate(grads: List[torch.Tensor]):
         if g.device != g0.device or g.dtype != g0.dtype:
             raise NotImplementedError("clip_grad_norm_: all gradients must share one device and dtype "
                                       f"({g0.device}/{g0.dtype} vs {g.device}/{g.dtype})")
-        if g.is_sparse or not g.is_contiguous():
-            raise NotImplementedError("clip_grad_norm_: sparse or non-contiguous gradients are not supported")
+        if g.is_sparse or not dense_layout(g):
+            raise NotImplementedError("clip_grad_norm_: sparse gradients, or gradients whose elements overlap "
+                                      "or leave gaps in memory, are not supported")
     return g0.device, g0.dtype == torch.bfloat16
 
 

@@ -291,11 +291,24 @@ PyObject *same_params(PyObject *, PyObject *args) {
     Py_RETURN_FALSE;
 }
 
+/* Same sizes, and the same strides on every dimension of size > 1 (any
+ * strides for empty tensors). */
+bool same_layout(const at::Tensor &a, const at::Tensor &b) {
+    if (!a.sizes().equals(b.sizes())) return false;
+    if (a.numel() == 0) return true;
+    const auto n = a.sizes();
+    const auto sa = a.strides(), sb = b.strides();
+    for (size_t d = 0; d < n.size(); ++d)
+        if (n[d] != 1 && sa[d] != sb[d]) return false;
+    return true;
+}
+
 /* grads_match(params, grads, bf16) -> bool
  *
  * True when every grads[i] can stand in for the gradient the launch tables
- * were built with: a dense, contiguous tensor on params[i]'s device, of
- * params[i]'s shape, float32 (bfloat16 when ``bf16``).  False for anything
+ * were built with: a dense tensor on params[i]'s device with params[i]'s
+ * shape and strides (the parameters' own layouts were checked when the
+ * tables were built), float32 (bfloat16 when ``bf16``).  False for anything
  * else, including objects that are not exactly torch tensors: the caller
  * then checks them one by one (and raises the precise error). */
 PyObject *grads_match(PyObject *, PyObject *args) {
@@ -311,7 +324,7 @@ PyObject *grads_match(PyObject *, PyObject *args) {
             if (!THPVariable_CheckExact(p) || !THPVariable_CheckExact(g)) Py_RETURN_FALSE;
             const at::Tensor &pt = THPVariable_Unpack(p), &gt = THPVariable_Unpack(g);
             if (!gt.defined() || gt.is_sparse() || gt.scalar_type() != want || gt.device() != pt.device() ||
-                !gt.sizes().equals(pt.sizes()) || !gt.is_contiguous())
+                !same_layout(gt, pt))
                 Py_RETURN_FALSE;
         }
     } catch (const std::exception &e) {
@@ -331,8 +344,8 @@ PyMethodDef methods[] = {
     {"grads_of", grads_of, METH_VARARGS,
      "grads_of(params) -> (grads, absent): [p.grad for p in params] and a bytes of 1 where grad is None."},
     {"grads_match", grads_match, METH_VARARGS,
-     "grads_match(params, grads, bf16) -> bool: every grad is a dense contiguous tensor of its param's "
-     "device and shape, float32 (bfloat16 when bf16)."},
+     "grads_match(params, grads, bf16) -> bool: every grad is a dense tensor of its param's "
+     "device, shape and strides, float32 (bfloat16 when bf16)."},
     {"data_ptrs", data_ptrs, METH_VARARGS,
      "data_ptrs(tensors) -> bytes: each tensor's data_ptr() (0 for None) as native uint64."},
     {"bump_versions", bump_versions, METH_VARARGS,

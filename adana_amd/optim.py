@@ -45,6 +45,7 @@ import torch
 from torch.optim import Optimizer
 
 from . import _hoststep, _lib
+from ._layout import dense_layout, same_layout
 from .clip import GradPlan, clip_grad_norm_ as _clip_grad_norm
 
 DIAG_KEYS = ("current_alpha", "gradient_norm", "auto_factor_mean",
@@ -62,18 +63,20 @@ class _SlabRef:
 _SLAB_ALIGN = 1024      # elements (4 KB): every state tensor starts a fresh work chunk
 
 
-def _carve(buf: torch.Tensor, off: int, shape) -> torch.Tensor:
-    """A tensor of ``shape`` and ``buf``'s dtype (float32 or bfloat16) over
-    ``buf[off:]`` with a storage of its own (deepcopy, torch.save and the
-    like see only its bytes); the slab lives as long as any tensor carved
-    from it.  bfloat16 has no array-interface type code: it is carved as
-    int16 and viewed as bfloat16 (a view of that private storage)."""
+def _carve(buf: torch.Tensor, off: int, shape, strides=None) -> torch.Tensor:
+    """A tensor of ``shape`` (and element ``strides``; None: contiguous) and
+    ``buf``'s dtype (float32 or bfloat16) over ``buf[off:]`` with a storage of
+    its own (deepcopy, torch.save and the like see only its bytes); the slab
+    lives as long as any tensor carved from it.  bfloat16 has no
+    array-interface type code: it is carved as int16 and viewed as bfloat16
+    (a view of that private storage)."""
     ref = _SlabRef()
     ref.buf = buf
     bf16 = buf.dtype == torch.bfloat16
+    es = buf.element_size()
     ref.__cuda_array_interface__ = {"shape": tuple(shape), "typestr": "<i2" if bf16 else "<f4",
-                                    "data": (buf.data_ptr() + buf.element_size() * off, False),
-                                    "version": 3, "strides": None}
+                                    "data": (buf.data_ptr() + es * off, False), "version": 3,
+                                    "strides": None if strides is None else tuple(es * x for x in strides)}
     t = torch.as_tensor(ref, device=buf.device)
     return t.view(torch.bfloat16) if bf16 else t
 
@@ -149,7 +152,7 @@ class _DanaFamily(Optimizer):
         than one allocation per tensor, interleaved m, v, tau)."""
         by_dev = {}
         for p, st in items:
-            dense = (p.device.type == "cuda" and p.is_contiguous() and p.dtype in (torch.float32, torch.bfloat16))
+            dense = (p.device.type == "cuda" and dense_layout(p) and p.dtype in (torch.float32, torch.bfloat16))
             if not dense:   # not steppable here anyway (step() raises): plain per-tensor state
                 for fam in self._state_families(p):
                     old = source[p][fam] if source is not None else None
@@ -176,7 +179,8 @@ class _DanaFamily(Optimizer):
                 slab = torch.zeros(total + _SLAB_ALIGN, dtype=dt, device=dev)
                 base = (-(slab.data_ptr() // slab.element_size())) % _SLAB_ALIGN
                 for (p, st), off in zip(members, offs):
-                    t = _carve(slab, base + off, p.shape)
+                    # zeros_like(p): p's shape and, for a transposed or permuted p, its strides
+                    t = _carve(slab, base + off, p.shape, None if p.is_contiguous() else p.stride())
                     if source is not None:
                         t.copy_(source[p][fam])
                     elif fam == "master":
@@ -277,9 +281,12 @@ class _DanaFamily(Optimizer):
             raise RuntimeError(f"{type(self).__name__}: grad must match its parameter's "
                                f"device and shape ({g.device}/{tuple(g.shape)} vs "
                                f"{p.device}/{tuple(p.shape)})")
-        if not (p.is_contiguous() and g.is_contiguous()):
-            raise NotImplementedError(f"{type(self).__name__}: non-contiguous parameters or "
-                                      "gradients are not supported")
+        if not dense_layout(p):
+            raise NotImplementedError(f"{type(self).__name__}: parameters whose elements overlap or leave "
+                                      "gaps in memory are not supported (contiguous or permuted layouts are)")
+        if not same_layout(p, g):
+            raise NotImplementedError(f"{type(self).__name__}: the gradient's strides {tuple(g.stride())} differ "
+                                      f"from its parameter's {tuple(p.stride())}")
         flags = self._VARIANT
         if p.dtype == torch.float32:
             if g.dtype != torch.float32:
@@ -607,8 +614,12 @@ class _DanaFamily(Optimizer):
         km = self._KEYS[0]
         for p, st in zip(ls.params, ls.states):
             m = st[km]
-            if p.shape != m.shape:
+            if not same_layout(p, m):
                 a, b = tuple(m.shape), tuple(p.shape)
+                if a == b:
+                    raise RuntimeError(f"{type(self).__name__}: parameter of strides {tuple(p.stride())} has "
+                                       f"optimizer state of strides {tuple(m.stride())}; rebind it with the "
+                                       "layout it had")
                 raise RuntimeError(f"{type(self).__name__}: parameter of shape {b} has optimizer state "
                                    f"of shape {a}: the size of tensor a ({a}) must match the size of "
                                    f"tensor b ({b})")

@@ -680,3 +680,60 @@ def test_closure_and_group_added_mid_run(oracle_mod, star):
         assert seen["grad_enabled"] and float(loss) == k + 0.5
         pair.compare(where=f"k={k}")
     assert [g["weighted_step_count"] for g in pair.opt.param_groups] == [6.0, 3.0]
+
+
+@pytest.mark.parametrize("star", [False, True])
+def test_permuted_parameters(oracle_mod, star):
+    """Parameters with dense non-contiguous layouts (a transposed matrix, a
+    permuted 3-D tensor) and gradients of the same strides, as autograd
+    produces them: the state is zeros_like(p) with p's strides, the step runs
+    in storage order, and every element matches the oracle's (run on the
+    logical arrays); 8 steps crossing t = delta.  A gradient of other strides,
+    or a parameter with gaps, is refused."""
+    import adana_amd
+
+    O = oracle_mod
+    print("case: permuted parameter layouts, star", star, flush=True)
+    rng = np.random.default_rng(77)
+    base = [torch.from_numpy(_normal(rng, (64, 33), 0.02)).to(DEV).t(),
+            torch.from_numpy(_normal(rng, (4, 5, 6), 0.02)).to(DEV).permute(2, 0, 1),
+            torch.from_numpy(_normal(rng, (1000,), 0.02)).to(DEV)]
+    ps = [torch.nn.Parameter(b) for b in base]
+    assert not ps[0].is_contiguous() and not ps[1].is_contiguous()
+    host = [p.detach().cpu().numpy().copy() for p in ps]                   # logical order
+    hp = dict(lr=1e-3, delta=8.0, kappa=0.85, clipsnr=2.0, weight_decay=0.1, wd_decaying=True, wd_ts=10.0)
+    opt = (adana_amd.DANA_STAR_MK4 if star else adana_amd.ADana)(ps, **hp)
+    orc = O.OracleOptimizer(groups=[O.OracleGroup(params=host, lr=1e-3, weight_decay=0.1)], star=star,
+                            peak_lr=1e-3, kappa=0.85, clipsnr=2.0, wd_decaying=True, wd_ts=10.0)
+    for t in range(1, 9):
+        gl = [_normal(rng, h.shape, 1e-3) for h in host]
+        for p, g in zip(ps, gl):
+            gt = torch.empty_strided(p.shape, p.stride(), device=DEV)
+            gt.copy_(torch.from_numpy(g))
+            p.grad = gt
+        prev = [h.copy() for h in host]
+        opt.step()
+        orc.step([gl])
+        torch.cuda.synchronize()
+        for i, p in enumerate(ps):
+            st, ost = opt.state[p], orc.state[id(host[i])]
+            tag = f"t={t} tensor {i} shape {tuple(p.shape)} strides {p.stride()}"
+            for key in ("m", "v") + (("tau",) if star else ()):
+                assert st[key].stride() == p.stride(), tag
+                assert ulp_diff(st[key].cpu().numpy(), ost[key]).max() == 0, f"{tag} {key}"
+            gp = p.detach().cpu().numpy()
+            if star:
+                _check_star_p(gp, host[i], prev[i], tag)
+            else:
+                assert ulp_diff(gp, host[i]).max() == 0, tag
+            host[i][...] = gp
+            got = np.array([float(st[k]) for k in O.DIAG_KEYS])
+            np.testing.assert_allclose(got, [ost[k] for k in O.DIAG_KEYS], rtol=1e-5, atol=1e-30, err_msg=tag)
+    ps[0].grad = torch.zeros(ps[0].shape, device=DEV)                      # contiguous: other strides
+    with pytest.raises(NotImplementedError, match="strides"):
+        opt.step()
+    gapped = torch.nn.Parameter(torch.zeros(10, 8, device=DEV)[:, :4])
+    gapped.grad = torch.zeros_like(gapped)
+    opt2 = (adana_amd.DANA_STAR_MK4 if star else adana_amd.ADana)([gapped], **hp)
+    with pytest.raises(NotImplementedError, match="gaps"):
+        opt2.step()

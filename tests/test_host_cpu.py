@@ -531,3 +531,19 @@ def test_rebound_parameter_of_another_shape_raises():
         ps[1].data = torch.zeros(3, 3)
         with pytest.raises(RuntimeError, match="must match the size"):
             opt._check_state_shapes(ls)
+
+
+def test_dense_layouts():
+    """The layouts the element-wise step runs over in storage order:
+    contiguous and permuted tensors, empty tensors of any strides; not
+    gapped or overlapping ones."""
+    from adana_amd._layout import dense_layout, same_layout
+
+    a = torch.zeros(3, 4)
+    assert dense_layout(a) and dense_layout(a.t()) and dense_layout(torch.zeros(2, 3, 4).permute(2, 0, 1))
+    assert dense_layout(torch.from_numpy(np.zeros((0,), np.float32)))          # stride 0, no elements
+    assert dense_layout(torch.zeros(5, 1, 3)[:, :, :])
+    assert not dense_layout(a[:, :2]) and not dense_layout(a.expand(2, 3, 4)) and not dense_layout(a[::2])
+    assert same_layout(a.t(), torch.ones(3, 4).t())
+    assert not same_layout(a.t(), a.t().contiguous())
+    assert same_layout(torch.zeros(3, 1), torch.zeros(1, 3).t())               # size-1 dims' strides ignored
