@@ -1,8 +1,11 @@
 // adana_fastmath.h -- correctly rounded binary32 division and square root for
 // operand ranges on which the full IEEE sequences' range scaling and
-// special-case fixups are identities.  Same results, fewer instructions.
-// tests/gpu_mathcheck.hip checks both exhaustively over the ranges the
-// optimizer kernel uses them on.
+// special-case fixups are identities, and the bfloat16 path's rounding,
+// division and square root.  Same results, fewer instructions.
+// tests/gpu_mathcheck.hip checks each exhaustively: the binary32 ones over the
+// ranges the optimizer kernel uses them on, the bfloat16 ones over every
+// bfloat16 input (every pair for the division) and the rounding over every
+// binary32 input.
 #ifndef ADANA_FASTMATH_H
 #define ADANA_FASTMATH_H
 
@@ -38,6 +41,64 @@ __device__ __forceinline__ float sqrt_normal(float x) {
     float o = rm <= 0.0f ? sm : s;
     o = rp > 0.0f ? sp : o;
     return o;
+}
+
+// ---------------------------------------------------------------------------
+// bfloat16 rounding and the bfloat16 path's division and square root.
+// ---------------------------------------------------------------------------
+
+// Round to nearest even; a NaN stays a quiet NaN ((bits >> 16) | 0x40): gfx950's
+// v_cvt_pk_bf16_f32, which rounds two binary32 values into the two halves of
+// one register.  bf16_round converts the pair (0, f): the low half is then
+// zero and the high half bf16(f), so the register is already the rounded
+// value as a binary32 -- one instruction, no shift.
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ unsigned short bf16_bits(float f) {
+    return __builtin_bit_cast(unsigned short, static_cast<__bf16>(f));
+}
+__device__ __forceinline__ float bf16_round(float f) {
+    const f32x2_t v = {0.0f, f};
+    return __builtin_bit_cast(float, __builtin_convertvector(v, bf16x2_t));
+}
+// bf16(lo) | bf16(hi) << 16: two values' bits in one 32-bit word.
+__device__ __forceinline__ unsigned int bf16_pack2(float lo, float hi) {
+    const f32x2_t v = {lo, hi};
+    return __builtin_bit_cast(unsigned int, __builtin_convertvector(v, bf16x2_t));
+}
+
+// a / b for bfloat16 values a and b: a binary32 value that rounds to the same
+// bfloat16 as the correctly rounded binary32 quotient.  Why the hardware
+// reciprocal is enough: with a = A 2^i and b = B 2^j (A, B at most 8
+// significant bits), a quotient equal to a bfloat16 midpoint M 2^k (M odd, 9
+// bits) would need A = M B, more than 8 bits; so a normal quotient lies at
+// least 2^k / 255 > 2^7 binary32 ulps from every midpoint, and a * rcp(b)
+// (within 2 ulps) rounds like it.  Denominators outside the normal range,
+// quotients below 2^-125 (bfloat16's subnormal grid) and NaNs take the IEEE
+// sequence; a zero numerator's fast result is the IEEE one.
+__device__ __forceinline__ float div_bf16(float a, float b) {
+    float q = a * __builtin_amdgcn_rcpf(b);
+    const bool fast = (fabsf(q) >= 0x1p-125f || a == 0.0f) && fabsf(b) >= 0x1p-126f;
+    if (__builtin_expect(!fast, 0)) {
+        asm volatile("" : "+v"(a), "+v"(b));   // a real branch: the compiler may not run the IEEE
+        q = a / b;                             // sequence for every element and select
+    }
+    return q;
+}
+
+// sqrt(x) for a bfloat16 value x: a binary32 value that rounds to the same
+// bfloat16 as the correctly rounded square root.  sqrt(x) = M 2^k (M odd, 9
+// bits) would need x = M^2 2^2k, 17 significant bits; so sqrt(x) lies at least
+// 2^5 binary32 ulps from every bfloat16 midpoint and the hardware square root
+// (within 1 ulp) rounds like the exact one.  Zeros give themselves; other
+// inputs below 2^-126 (subnormals, negatives) and NaNs take the IEEE sequence.
+__device__ __forceinline__ float sqrt_bf16(float x) {
+    float s = __builtin_amdgcn_sqrtf(x);
+    if (__builtin_expect(!(x >= 0x1p-126f || x == 0.0f), 0)) {
+        asm volatile("" : "+v"(x));
+        s = __builtin_sqrtf(x);
+    }
+    return s;
 }
 
 }  // namespace adana

@@ -79,14 +79,9 @@ __device__ __forceinline__ float relu_f(float x) { return x < 0.0f ? 0.0f : x; }
 __device__ __forceinline__ float bf16_to_f32(unsigned short h) {
     return __uint_as_float(static_cast<unsigned int>(h) << 16);
 }
-// Round to nearest even; NaN stays a quiet NaN.
-__device__ __forceinline__ unsigned short f32_to_bf16(float f) {
-    unsigned int u = __float_as_uint(f);
-    if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<unsigned short>((u >> 16) | 0x40u);
-    u += 0x7fffu + ((u >> 16) & 1u);
-    return static_cast<unsigned short>(u >> 16);
-}
-__device__ __forceinline__ float bf16_round(float f) { return bf16_to_f32(f32_to_bf16(f)); }
+// Round to nearest even (NaN stays a quiet NaN): gfx950's conversion instruction.
+__device__ __forceinline__ unsigned short f32_to_bf16(float f) { return adana::bf16_bits(f); }
+__device__ __forceinline__ float bf16_round(float f) { return adana::bf16_round(f); }
 
 // clip_grad_norm_'s in-place product (torch/nn/utils/clip_grad.py,
 // _clip_grads_with_norm_: torch._foreach_mul_(grads, clip_coef_clamped)):
@@ -231,6 +226,8 @@ __device__ __forceinline__ float star_phase_b(float p, float g, const StarMid &a
 //   * addcmul_(g, g, value=a) = fma(a * g, g, v), a unrounded;
 //   * Dana-Star's pow(et, 1 - kappa) takes the exponent rounded to bfloat16;
 //   * clamp(x, max=c) compares with c rounded to bfloat16.
+// Divisions and square roots of bfloat16 values use adana::div_bf16 and
+// adana::sqrt_bf16, whose results round to the same bfloat16 as the IEEE ones.
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ float rb(float x) { return bf16_round(x); }
 
@@ -260,8 +257,8 @@ __device__ __forceinline__ float adana_elem16(float p, float g, float &m, float 
     const float mn = rb(__builtin_fmaf(q.lerp_coef16, g - m, q.lerp_small16 ? m : g));   // :101
     float vn = rb(v * sc.oma);                                                          // :104 mul_
     vn = rb(__builtin_fmaf(sc.a * g, g, vn));                                           //      addcmul_
-    const float se = rb(rb(sqrtf(vn)) + q.eps16);                                       // :107
-    const float nt = rb(1.0f / se);                                                     // :110
+    const float se = rb(rb(adana::sqrt_bf16(vn)) + q.eps16);                            // :107
+    const float nt = rb(adana::div_bf16(1.0f, se));                                     // :110
     const float mfac = rb(fabsf(mn) * nt);                                              // :111, :115
     float af = rb(q.pw16 * mfac);                                                       // :119 / :123
     if (sc.has_clip) af = clamp_max(af, q.clip16);
@@ -283,12 +280,12 @@ __device__ __forceinline__ StarMid star16_phase_a(float g, float m, float v, flo
     o.m = rb(__builtin_fmaf(q.lerp_coef16, g - m, q.lerp_small16 ? m : g));            // :137
     o.v = rb(v * sc.oma);                                                               // :140
     o.v = rb(__builtin_fmaf(sc.a * g, g, o.v));
-    o.se = rb(rb(sqrtf(o.v)) + q.eps16);                                                // :143
+    o.se = rb(rb(adana::sqrt_bf16(o.v)) + q.eps16);                                     // :143
     const float ag = fabsf(g);                                                          // :147
-    const float tu = rb(ag / rb(ag + o.se));                                            // :148
+    const float tu = rb(adana::div_bf16(ag, rb(ag + o.se)));                            // :148
     o.tau = rb(__builtin_fmaf(q.lerp_coef16, tu - tau, q.lerp_small16 ? tau : tu));     // :149
     const float ct = clamp_max(o.tau, 0.5f);                                            // :152
-    const float pe = rb(ct / rb(1.0f - ct));                                            // :153
+    const float pe = rb(adana::div_bf16(ct, rb(1.0f - ct)));                            // :153
     o.tr = rb(q.min_p16 + relu_f(rb(pe - q.min_p16)));                                  // :154-156
     o.et = clamp_min(rb(o.tau * sc.s), 1.0f);                                           // :159
     return o;
@@ -297,9 +294,9 @@ __device__ __forceinline__ StarMid star16_phase_a(float g, float m, float v, flo
 // src/optim/dana_star_mk4.py:163-195 on bfloat16 tensors, given pw = et ** e16
 __device__ __forceinline__ float star16_phase_b(float p, float g, const StarMid &a, float pw,
                                                 const adana_step_scalars &sc, const Scalars16 &q, float (&acc)[4]) {
-    const float nt = rb(rb(sqrtf(a.tr)) / a.se);                                        // :163-164
+    const float nt = rb(adana::div_bf16(rb(adana::sqrt_bf16(a.tr)), a.se));             // :163-164
     const float mnt = rb(fabsf(a.m) * nt);                                              // :165
-    const float mfac = rb(mnt / a.tr);                                                  // :167
+    const float mfac = rb(adana::div_bf16(mnt, a.tr));                                  // :167
     float af = rb(pw * mfac);                                                           // :170 / :174
     if (sc.has_clip) af = clamp_max(af, q.clip16);
     const float inner = sign_f(a.m) * rb(rb(a.tr * af) + mnt);                          // :177
@@ -324,9 +321,9 @@ __device__ __forceinline__ float pow16(float x, const adana_step_scalars &sc, co
         switch (sc.pow_mode) {
         case ADANA_POW_ONE: return 1.0f;
         case ADANA_POW_IDENTITY: return x;
-        case ADANA_POW_SQRT: return rb(sqrtf(x));
+        case ADANA_POW_SQRT: return rb(adana::sqrt_bf16(x));
         case ADANA_POW_RSQRT: return rb(1.0f / sqrtf(x));
-        case ADANA_POW_RECIP: return rb(1.0f / x);
+        case ADANA_POW_RECIP: return rb(adana::div_bf16(1.0f, x));
         case ADANA_POW_SQUARE: return rb(x * x);
         case ADANA_POW_CUBE: return rb((x * x) * x);
         case ADANA_POW_INVSQ: return rb(1.0f / (x * x));
@@ -568,12 +565,10 @@ template <int N>
 __device__ __forceinline__ void st_bf16_n(void *p, const float (&x)[N]) {
     typename VecT<N>::H h;
     if constexpr (N == 2) {
-        h = static_cast<unsigned int>(f32_to_bf16(x[0])) | (static_cast<unsigned int>(f32_to_bf16(x[1])) << 16);
+        h = adana::bf16_pack2(x[0], x[1]);
     } else {
 #pragma unroll
-        for (int k = 0; k < N / 2; ++k)
-            h[k] = static_cast<unsigned int>(f32_to_bf16(x[2 * k])) |
-                   (static_cast<unsigned int>(f32_to_bf16(x[2 * k + 1])) << 16);
+        for (int k = 0; k < N / 2; ++k) h[k] = adana::bf16_pack2(x[2 * k], x[2 * k + 1]);
     }
     __builtin_nontemporal_store(h, (GLOBAL_AS typename VecT<N>::H *)(p));
 }
@@ -1265,11 +1260,15 @@ size_t workspace_bytes(const adana_plan &pl) {
 // their time in per-segment work (tensor lookup, reductions, partial stores)
 // and in the pow: it runs best at its register limit (Dana-Star over 10,000
 // tensors of 64-65536 elements: 0.715 ms capped, 0.666 ms uncapped; the same
-// list at kappa = 1 prefers the cap, 0.658 against 0.748 ms).  The cap is
-// imposed with dynamic LDS the kernel does not touch.
+// list at kappa = 1 prefers the cap, 0.658 against 0.748 ms).  bfloat16
+// state (PM_BF16) moves half the bytes per workgroup and runs best uncapped:
+// Dana-Star with the pow at 2.65B params, 14.25 ms at 4, 12.84-12.86 ms at 5,
+// 6, 8 and uncapped (its registers allow 5).  The cap is imposed with dynamic
+// LDS the kernel does not touch.
 template <bool STAR, int PM, int POWK>
 constexpr int residency_cap(bool small_tensors) {
-    return (STAR && pow_tables(POWK) && small_tensors) ? 0 : (PM == PM_MASTER ? 5 : 4);
+    if (PM == PM_BF16 || (STAR && pow_tables(POWK) && small_tensors)) return 0;
+    return PM == PM_MASTER ? 5 : 4;
 }
 
 // Upper bound on the kernel's static LDS (the reduction slots and, for the

@@ -222,3 +222,4 @@ def test_bf16_state_dict_matches_reference_schema():
 
 def _bits_t(t):
     return t.detach().view(torch.int16)
+

@@ -1,6 +1,8 @@
 """Exhaustive checks, on the GPU, that the shortened division and square root
 of adana_amd/csrc/adana_fastmath.h return exactly what the IEEE sequences do
-over the input ranges the Dana-Star kernel feeds them."""
+over the input ranges the Dana-Star kernel feeds them, and that the bfloat16
+path's rounding, division and square root agree with round-to-nearest-even
+of the IEEE results on every input."""
 import ctypes
 import os
 import struct
@@ -45,4 +47,27 @@ def test_sqrt_normal_exhaustive():
     """sqrt for every binary32 in [2^-96, 2^64] (tau_reg lies in [2^-24, 1])."""
     print("case: sqrt_normal exhaustive [2^-96, 2^64]", flush=True)
     bad, first = _run(1, _bits(2.0 ** -96), _bits(2.0 ** 64))
+    assert bad == 0, f"{bad} mismatches, first pattern {first:#010x}"
+
+
+def test_bf16_conversion_is_rne_on_every_binary32():
+    """gfx950's conversion instruction (v_cvt_pk_bf16_f32) over all 2^32
+    binary32 patterns: round-to-nearest-even, NaN -> (bits >> 16) | 0x40."""
+    print("case: bf16 conversion exhaustive", flush=True)
+    bad, first = _run(2, 0, 0xFFFFFFFF)
+    assert bad == 0, f"{bad} mismatches, first pattern {first:#010x}"
+
+
+def test_div_bf16_exhaustive_over_all_pairs():
+    """bf16(div_bf16(a, b)) == bf16(a / b) for all 2^32 pairs of bfloat16 a, b
+    (zeros, subnormals, infinities and NaNs included)."""
+    print("case: div_bf16 exhaustive", flush=True)
+    bad, first = _run(3, 0, 0xFFFFFFFF)
+    assert bad == 0, f"{bad} mismatches, first pair {first:#010x}"
+
+
+def test_sqrt_bf16_exhaustive():
+    """bf16(sqrt_bf16(x)) == bf16(sqrtf(x)) for all 65,536 bfloat16 x."""
+    print("case: sqrt_bf16 exhaustive", flush=True)
+    bad, first = _run(4, 0, 0xFFFF)
     assert bad == 0, f"{bad} mismatches, first pattern {first:#010x}"
