@@ -43,6 +43,18 @@ __device__ __forceinline__ float sqrt_normal(float x) {
     return o;
 }
 
+// Correctly rounded sqrt for every binary32 x: sqrt_normal on [2^-96, +inf]
+// (about 8 instructions against the IEEE sequence's 20), the IEEE sequence for
+// zeros, small and negative inputs and NaNs, behind a real branch.
+__device__ __forceinline__ float sqrt_f32(float x) {
+    float s = sqrt_normal(x);
+    if (__builtin_expect(!(x >= 0x1p-96f), 0)) {
+        asm volatile("" : "+v"(x));   // keeps the IEEE sequence out of the common path
+        s = __builtin_sqrtf(x);
+    }
+    return s;
+}
+
 // ---------------------------------------------------------------------------
 // bfloat16 rounding and the bfloat16 path's division and square root.
 // ---------------------------------------------------------------------------

@@ -124,8 +124,8 @@ __device__ __forceinline__ float pow_aten(float x, const adana_step_scalars &sc,
         switch (sc.pow_mode) {
         case ADANA_POW_ONE: return 1.0f;
         case ADANA_POW_IDENTITY: return x;
-        case ADANA_POW_SQRT: return sqrtf(x);
-        case ADANA_POW_RSQRT: return 1.0f / sqrtf(x);
+        case ADANA_POW_SQRT: return adana::sqrt_f32(x);
+        case ADANA_POW_RSQRT: return 1.0f / adana::sqrt_f32(x);
         case ADANA_POW_RECIP: return 1.0f / x;
         case ADANA_POW_SQUARE: return x * x;
         case ADANA_POW_CUBE: return (x * x) * x;
@@ -153,7 +153,7 @@ __device__ __forceinline__ float adana_elem(float p, float g, float &m, float &v
                                             const adana_step_scalars &sc, float (&acc)[4]) {
     const float mn = lerp_aten(m, g, sc);                        // :101
     const float vn = __builtin_fmaf(sc.a * g, g, v * sc.oma);    // :104 mul_, addcmul_
-    const float se = sqrtf(vn) + sc.eps;                         // :107
+    const float se = adana::sqrt_f32(vn) + sc.eps;               // :107
     const float nt = 1.0f / se;                                  // :110
     const float mfac = fabsf(mn) * nt;                           // :111, :115
     float af = sc.pw * mfac;                                     // :119 / :123
@@ -181,7 +181,7 @@ __device__ __forceinline__ StarMid star_phase_a(float g, float m, float v, float
     StarMid o;
     o.m = lerp_aten(m, g, sc);                                   // :137
     o.v = __builtin_fmaf(sc.a * g, g, v * sc.oma);               // :140
-    o.se = sqrtf(o.v) + sc.eps;                                  // :143
+    o.se = adana::sqrt_f32(o.v) + sc.eps;                        // :143
     const float ag = fabsf(g);                                   // :147
     const float tu = ag / (ag + o.se);                           // :148
     o.tau = lerp_aten(tau, tu, sc);                              // :149
@@ -322,7 +322,7 @@ __device__ __forceinline__ float pow16(float x, const adana_step_scalars &sc, co
         case ADANA_POW_ONE: return 1.0f;
         case ADANA_POW_IDENTITY: return x;
         case ADANA_POW_SQRT: return rb(adana::sqrt_bf16(x));
-        case ADANA_POW_RSQRT: return rb(1.0f / sqrtf(x));
+        case ADANA_POW_RSQRT: return rb(1.0f / adana::sqrt_f32(x));
         case ADANA_POW_RECIP: return rb(adana::div_bf16(1.0f, x));
         case ADANA_POW_SQUARE: return rb(x * x);
         case ADANA_POW_CUBE: return rb((x * x) * x);
@@ -385,8 +385,8 @@ __device__ __forceinline__ float pow_by_mode(float x, float e, int mode) {
     switch (mode) {
     case ADANA_POW_ONE: return 1.0f;
     case ADANA_POW_IDENTITY: return x;
-    case ADANA_POW_SQRT: return sqrtf(x);
-    case ADANA_POW_RSQRT: return 1.0f / sqrtf(x);
+    case ADANA_POW_SQRT: return adana::sqrt_f32(x);
+    case ADANA_POW_RSQRT: return 1.0f / adana::sqrt_f32(x);
     case ADANA_POW_RECIP: return 1.0f / x;
     case ADANA_POW_SQUARE: return x * x;
     case ADANA_POW_CUBE: return (x * x) * x;
@@ -401,14 +401,14 @@ __device__ __forceinline__ float manau_elem(float p, float g, float &m, float &v
     const float mn = __builtin_fmaf(g, sc.a, m * sc.oma);            // :567 mul_(1-a).add_(g, alpha=a)
     const float vn = __builtin_fmaf(sc.a * g, g, v * sc.oma);        // :569 mul_(1-a).addcmul_(g, g, value=a)
     const float ag = fabsf(g);
-    const float sv = sqrtf(vn);
+    const float sv = adana::sqrt_f32(vn);
     const float tu = ag / ((ag + sv) + sc.eps);                      // :572, _tau_updater :292-299
     const float tn = __builtin_fmaf(tu, sc.a, tau * sc.oma);         // :573
     const float ct = clamp_max(tn, 0.5f);                            // _tau_reg :277-282
     const float pe = ct / (1.0f - ct);
     const float tr = maximum_f(pe, sc.min_p);
     const float et = maximum_f(tn * sc.s, 1.0f);                     // _effective_time :288-290
-    const float nt = sqrtf(tr) / (sv + sc.eps);                      // _norm_term :301-310
+    const float nt = adana::sqrt_f32(tr) / (sv + sc.eps);            // _norm_term :301-310
     const float mfac = (nt * fabsf(mn)) / tr;                        // :583
     float af;                                                        // :584-589
     if constexpr (POWK == POW_MANAU_MK4) {

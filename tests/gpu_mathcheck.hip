@@ -12,6 +12,7 @@
 //              pattern = (a's bfloat16 bits << 16) | b's bits in [lo, hi]
 //   which = 4: bf16_round(sqrt_bf16(x)) vs bf16_round(sqrtf(x)) for the
 //              bfloat16 patterns [lo, hi] (hi <= 0xffff)
+//   which = 5: sqrt_f32(x) vs sqrtf(x) for the binary32 patterns [lo, hi]
 // out[0] counts mismatching patterns, out[1] holds the smallest one.
 #include <hip/hip_runtime.h>
 
@@ -52,10 +53,13 @@ __global__ void check_kernel(int which, uint32_t lo, uint64_t count, unsigned lo
             const float a = __uint_as_float(bits & 0xffff0000u), b = __uint_as_float(bits << 16);
             got = adana::bf16_round(adana::div_bf16(a, b));
             ref = adana::bf16_round(a / b);
-        } else {
+        } else if (which == 4) {
             const float v = __uint_as_float(bits << 16);
             got = adana::bf16_round(adana::sqrt_bf16(v));
             ref = adana::bf16_round(sqrtf(v));
+        } else {
+            got = adana::sqrt_f32(x);
+            ref = sqrtf(x);
         }
         const bool same = __float_as_uint(got) == __float_as_uint(ref) ||
                           (which != 2 && got != got && ref != ref);
@@ -68,7 +72,7 @@ __global__ void check_kernel(int which, uint32_t lo, uint64_t count, unsigned lo
 
 extern "C" int adana_mathcheck(int which, uint32_t lo, uint32_t hi, unsigned long long *d_out,
                                void *stream) {
-    if (hi < lo || which < 0 || which > 4 || (which == 4 && hi > 0xffffu) || !d_out) return -1;
+    if (hi < lo || which < 0 || which > 5 || (which == 4 && hi > 0xffffu) || !d_out) return -1;
     const uint64_t count = static_cast<uint64_t>(hi) - lo + 1;
     hipLaunchKernelGGL(check_kernel, dim3(8192), dim3(256), 0, static_cast<hipStream_t>(stream), which, lo,
                        count, d_out);

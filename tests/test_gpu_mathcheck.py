@@ -44,9 +44,10 @@ def test_div_core_exhaustive_on_tau_range():
 
 
 def test_sqrt_normal_exhaustive():
-    """sqrt for every binary32 in [2^-96, 2^64] (tau_reg lies in [2^-24, 1])."""
-    print("case: sqrt_normal exhaustive [2^-96, 2^64]", flush=True)
-    bad, first = _run(1, _bits(2.0 ** -96), _bits(2.0 ** 64))
+    """sqrt for every binary32 in [2^-96, +inf] (tau_reg lies in [2^-24, 1];
+    sqrt_f32 sends the second moment there when it is at least 2^-96)."""
+    print("case: sqrt_normal exhaustive [2^-96, inf]", flush=True)
+    bad, first = _run(1, _bits(2.0 ** -96), 0x7F800000)
     assert bad == 0, f"{bad} mismatches, first pattern {first:#010x}"
 
 
@@ -70,4 +71,11 @@ def test_sqrt_bf16_exhaustive():
     """bf16(sqrt_bf16(x)) == bf16(sqrtf(x)) for all 65,536 bfloat16 x."""
     print("case: sqrt_bf16 exhaustive", flush=True)
     bad, first = _run(4, 0, 0xFFFF)
+    assert bad == 0, f"{bad} mismatches, first pattern {first:#010x}"
+
+
+def test_sqrt_f32_exhaustive():
+    """sqrt_f32(x) == sqrtf(x) bit for bit on all 2^32 binary32 patterns."""
+    print("case: sqrt_f32 exhaustive", flush=True)
+    bad, first = _run(5, 0, 0xFFFFFFFF)
     assert bad == 0, f"{bad} mismatches, first pattern {first:#010x}"
