@@ -72,9 +72,15 @@ struct ScalarPack {
 __device__ __forceinline__ float sign_f(float x) {  // torch.sign: 0 for +-0, NaN
     return x > 0.0f ? 1.0f : (x < 0.0f ? -1.0f : 0.0f);
 }
-__device__ __forceinline__ float clamp_max(float x, float c) { return x > c ? c : x; }
-__device__ __forceinline__ float clamp_min(float x, float c) { return x < c ? c : x; }
-__device__ __forceinline__ float relu_f(float x) { return x < 0.0f ? 0.0f : x; }
+// torch.clamp(x, max=c), torch.clamp(x, min=c), torch.relu: NaN propagates.
+// gfx950's IEEE 754-2019 minimum / maximum (v_minimum3_f32, v_maximum3_f32),
+// one instruction each.  They order -0 below +0, where the compare-and-select
+// forms return x; that differs only for zeros of opposite sign, which the step
+// never meets with a visible effect: the bounds are 0.5, 1 and the SNR clip
+// applied to a non-negative factor, and relu's result is added to min_p > 0.
+__device__ __forceinline__ float clamp_max(float x, float c) { return __builtin_elementwise_minimum(x, c); }
+__device__ __forceinline__ float clamp_min(float x, float c) { return __builtin_elementwise_maximum(x, c); }
+__device__ __forceinline__ float relu_f(float x) { return __builtin_elementwise_maximum(x, 0.0f); }
 
 __device__ __forceinline__ float bf16_to_f32(unsigned short h) {
     return __uint_as_float(static_cast<unsigned int>(h) << 16);
