@@ -1471,11 +1471,12 @@ int64_t adana_plan_layout(const int64_t *numel, int32_t n, int64_t *vstart,
     for (int32_t i = 0; i < n; ++i) {
         if (numel[i] < 0) return adana_set_error(ADANA_E_INVALID, "adana_plan_layout: numel[%d] < 0", i);
         // A tensor that would cross a chunk boundary from inside a chunk
-        // starts at the next boundary instead: a workgroup walks its chunk's
-        // tensors one after another, each with its own load round trip, so
-        // chunks shared by a large tensor's head or tail cost time (C5's
-        // 10,000-tensor list: -14% with this rule).  Small tensors still
-        // pack together inside one chunk.
+        // starts at the next boundary instead, so that a large tensor's head
+        // or tail does not share a chunk: a shared chunk costs a tensor lookup
+        // per thread and one partial reduction per tensor (C5's 10,000-tensor
+        // list: -14% with this rule, measured when a chunk's tensors were
+        // still walked one after another).  Small tensors still pack
+        // together inside one chunk.
         const int64_t r = off % kChunk;
         if (r != 0 && r + numel[i] > kChunk) off += kChunk - r;
         vstart[i] = off;

@@ -225,12 +225,13 @@ def test_clip_twice_then_step(oracle_mod):
         np.testing.assert_allclose(p.grad.cpu().numpy(), c.grad.cpu().numpy(), rtol=1e-6, atol=0)
 
 
-def test_clip_not_owned_falls_back_to_eager(oracle_mod):
+def test_clip_not_owned_scales_in_place_at_once(oracle_mod):
     """Parameters the optimizer does not step (or a subset) are scaled at
-    once instead of deferred; zero_grad drops a pending scale."""
+    once, by the HIP grad_scale_kernel, instead of deferred into the step;
+    zero_grad drops a pending scale."""
     import adana_amd
 
-    print("case: clip fallback", flush=True)
+    print("case: clip of parameters the optimizer does not own", flush=True)
     rng = np.random.default_rng(41)
     ps = [torch.nn.Parameter(torch.from_numpy(_normal(rng, (128,), 0.02)).to(DEV)) for _ in range(3)]
     opt = adana_amd.ADana(ps[:2], lr=1e-3)
