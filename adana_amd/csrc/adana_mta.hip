@@ -919,25 +919,51 @@ __device__ __forceinline__ void write_diag(void *diag, int bf16, int i, double n
     for (int k = 0; k < 5; ++k) f[k] = o[k];
 }
 
-// Diagnostics combine: one launch after the main kernel.
+// Diagnostics combine, after the main kernel.
 //  * Workgroups [0, n_folds) are fold workgroups: fold j reduces up to
 //    ADANA_FOLD_CHUNKS consecutive chunk partials of one tensor of more than
 //    ADANA_DIRECT_CHUNKS chunks, in binary64 and a fixed order, to folds[j].
-//    The last of a tensor's folds to finish (an arrival counter per tensor,
-//    zeroed by the main kernel; agent-scope acquire/release, so the folds
-//    written on other XCDs are visible) sums the tensor's folds in index
-//    order and writes its diagnostics.
-//  * The workgroups after them take four tensors each, one wave per tensor
-//    of at most ADANA_DIRECT_CHUNKS chunks, summing its chunk partials
-//    directly in binary64.
+//    With kCombineFenced, the last of a tensor's folds to finish (an arrival
+//    counter per tensor, zeroed by the main kernel; agent-scope release and
+//    acquire, so the folds written on other XCDs are visible) sums the
+//    tensor's folds in index order and writes its diagnostics: one launch.
+//    With kCombineFoldOnly the fold workgroups only store their folds, and a
+//    second launch (kCombineFinalizeFolded) sums them.
+//  * The workgroups after them take four tensors each, one wave per tensor:
+//    in the first launch the tensors of at most ADANA_DIRECT_CHUNKS chunks,
+//    summing their chunk partials directly in binary64; in the
+//    kCombineFinalizeFolded launch (no fold workgroups) the folded tensors.
 // Every sum has a fixed order whichever workgroup finishes last, so the
-// diagnostics are deterministic.
+// diagnostics are deterministic.  The fenced single launch suits lists with
+// few folds; each fold workgroup's release is an L2 write-back of its XCD on
+// gfx950, so lists with many folds take the second launch instead
+// (kFencedFoldsMax).
+enum CombineMode { kCombineFenced = 0, kCombineFoldOnly = 1, kCombineFinalizeFolded = 2 };
+constexpr int64_t kFencedFoldsMax = 256;
+
+// One wave: tensor i's diagnostics from its folds, summed in index order.
+__device__ __forceinline__ void finalize_folds(const double4 *__restrict__ folds, int f0, int f1, int lane,
+                                               void *diag, int diag_bf16, int i, int64_t numel) {
+    double s0 = 0.0, s1 = 0.0, s2 = 0.0, s3 = 0.0;
+    for (int f = f0 + lane; f < f1; f += 64) {
+        const double4 t = folds[f];
+        s0 += t.x; s1 += t.y; s2 += t.z; s3 += t.w;
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        s0 += __shfl_xor(s0, o, 64);
+        s1 += __shfl_xor(s1, o, 64);
+        s2 += __shfl_xor(s2, o, 64);
+        s3 += __shfl_xor(s3, o, 64);
+    }
+    if (lane == 0) write_diag(diag, diag_bf16, i, static_cast<double>(numel), s0, s1, s2, s3);
+}
 __global__ __launch_bounds__(kBlock) void combine_kernel(const adana_tensor_desc *__restrict__ desc,
                                                          const int64_t *__restrict__ vstart,
                                                          const int32_t *__restrict__ fold_first, int32_t n,
                                                          int32_t n_folds, const float *__restrict__ partials,
                                                          double4 *__restrict__ folds, int32_t *__restrict__ counters,
-                                                         void *__restrict__ diag, int diag_bf16) {
+                                                         void *__restrict__ diag, int diag_bf16, int mode) {
     __shared__ double red[kWaves][4];
     __shared__ int is_last;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -968,30 +994,34 @@ __global__ __launch_bounds__(kBlock) void combine_kernel(const adana_tensor_desc
         }
         block_sum4(s0, s1, s2, s3, red);
         const int f0 = fold_first[i], f1 = fold_first[i + 1];
+        if (mode != kCombineFenced) {
+            if (threadIdx.x == 0) folds[j] = make_double4(s0, s1, s2, s3);
+            return;
+        }
         if (threadIdx.x == 0) {
             folds[j] = make_double4(s0, s1, s2, s3);
-            const int prev = __hip_atomic_fetch_add(&counters[i], 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+            // Every arrival releases its fold; only the last one acquires (the
+            // increments form one release sequence, so the acquire fence after
+            // reading the final count sees every fold).  On gfx950 an
+            // agent-scope acquire invalidates the XCD's L2: paid once per
+            // tensor, not once per fold workgroup.
+            const int prev = __hip_atomic_fetch_add(&counters[i], 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
             is_last = (prev == f1 - f0 - 1);
+            if (is_last) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
         }
         __syncthreads();
         if (!is_last || wave != 0) return;
-        s0 = s1 = s2 = s3 = 0.0;
-        for (int f = f0 + lane; f < f1; f += 64) {
-            const double4 t = folds[f];
-            s0 += t.x; s1 += t.y; s2 += t.z; s3 += t.w;
-        }
-#pragma unroll
-        for (int o = 32; o > 0; o >>= 1) {
-            s0 += __shfl_xor(s0, o, 64);
-            s1 += __shfl_xor(s1, o, 64);
-            s2 += __shfl_xor(s2, o, 64);
-            s3 += __shfl_xor(s3, o, 64);
-        }
-        if (lane == 0) write_diag(diag, diag_bf16, i, static_cast<double>(numel), s0, s1, s2, s3);
+        finalize_folds(folds, f0, f1, lane, diag, diag_bf16, i, numel);
         return;
     }
     const int i = static_cast<int>((b - n_folds) * kWaves + wave);
-    if (i >= n || fold_first[i + 1] > fold_first[i]) return;           // whole wave
+    if (i >= n) return;                                                   // whole wave
+    const bool folded = fold_first[i + 1] > fold_first[i];
+    if (mode == kCombineFinalizeFolded) {
+        if (folded) finalize_folds(folds, fold_first[i], fold_first[i + 1], lane, diag, diag_bf16, i, desc[i].numel);
+        return;
+    }
+    if (folded) return;
     double s0 = 0.0, s1 = 0.0, s2 = 0.0, s3 = 0.0;
     const int64_t numel = desc[i].numel;
     if (numel > 0) {
@@ -1617,11 +1647,18 @@ int step_impl(const char *fn, const adana_plan *plan, const adana_step_scalars *
 #undef ADANA_LAUNCH
         if (int rc = launch_status(fn, "main")) return rc;
     }
-    const int64_t combine_wgs = pl.n_folds + (n + kWaves - 1) / kWaves;
-    hipLaunchKernelGGL(combine_kernel, dim3(static_cast<unsigned>(combine_wgs)), dim3(kBlock), 0, st, pl.desc,
-                       pl.vstart, pl.fold_first, n, static_cast<int32_t>(pl.n_folds), partials, folds, counters,
-                       static_cast<void *>(d_diag), s16 ? 1 : 0);
-    return launch_status(fn, "combine");
+    const int64_t tensor_wgs = (n + kWaves - 1) / kWaves;
+    const bool fenced = pl.n_folds <= kFencedFoldsMax;
+    hipLaunchKernelGGL(combine_kernel, dim3(static_cast<unsigned>(pl.n_folds + tensor_wgs)), dim3(kBlock), 0, st,
+                       pl.desc, pl.vstart, pl.fold_first, n, static_cast<int32_t>(pl.n_folds), partials, folds,
+                       counters, static_cast<void *>(d_diag), s16 ? 1 : 0,
+                       fenced ? kCombineFenced : kCombineFoldOnly);
+    if (int rc = launch_status(fn, "combine")) return rc;
+    if (fenced) return ADANA_OK;
+    hipLaunchKernelGGL(combine_kernel, dim3(static_cast<unsigned>(tensor_wgs)), dim3(kBlock), 0, st, pl.desc,
+                       pl.vstart, pl.fold_first, n, 0, partials, folds, counters, static_cast<void *>(d_diag),
+                       s16 ? 1 : 0, static_cast<int>(kCombineFinalizeFolded));
+    return launch_status(fn, "combine (finalize)");
 }
 
 }  // namespace
