@@ -1285,12 +1285,14 @@ size_t workspace_bytes(const adana_plan &pl) {
     return counters_offset(pl) + static_cast<size_t>(pl.n_tensors) * 4;
 }
 
-// Residency cap.  The step reaches the highest HBM throughput with 4 (fp32
-// params) or 5 (bf16 params with fp32 master) workgroups per CU rather than
-// the 7-8 its registers allow: fewer concurrent streams contend less in the
-// memory system (measured on MI355X: ADana fp32 13.1 -> 12.1 ms, Dana-Star
-// kappa=1 17.1 -> 16.1 ms, bf16 master 13.0 -> 12.1 ms at 2.65B params;
-// Dana-Star with the pow, tables in LDS, 16.6 -> 16.3 ms).  The exception is
+// Residency cap.  The step reaches the highest HBM throughput with 4
+// workgroups per CU rather than the 7-8 its registers allow: fewer concurrent
+// streams contend less in the memory system (measured on MI355X at 2.65B
+// params, uncapped -> capped: ADana fp32 13.1 -> 12.1 ms, Dana-Star kappa=1
+// 17.1 -> 16.1 ms, Dana-Star with the pow, tables in LDS, 16.6 -> 16.3 ms;
+// same-process sweep of caps 3/4/5/6: bf16 params with fp32 master 11.78 /
+// 11.84 / 12.20 / 12.66 ms, north-star 16.19 / 15.57 / 15.86 / 16.17 ms, C3
+// 8.19 / 8.07 / 8.14 / 8.32 ms, C2 0.245 / 0.239 / 0.244 / 0.245 ms).  The exception is
 // the pow instance on lists of small tensors (`small_tensors`: fewer than 64
 // chunks per tensor on average), whose workgroups spend a larger share of
 // their time in per-segment work (tensor lookup, reductions, partial stores)
@@ -1304,7 +1306,7 @@ size_t workspace_bytes(const adana_plan &pl) {
 template <bool STAR, int PM, int POWK>
 constexpr int residency_cap(bool small_tensors) {
     if (PM == PM_BF16 || (STAR && pow_tables(POWK) && small_tensors)) return 0;
-    return PM == PM_MASTER ? 5 : 4;
+    return 4;
 }
 
 // Upper bound on the kernel's static LDS (the reduction slots and, for the
