@@ -60,9 +60,10 @@ static_assert(sizeof(adana_manau_scalars) == sizeof(adana_step_scalars), "Manau 
 
 struct ScalarPack {
     adana_step_scalars c[ADANA_MAX_CLASSES];
-    const float *gscale;  // device pointer to the clip coefficient, or NULL
-    int32_t write_grad;   // store the scaled gradient back (ADANA_WRITE_GRAD)
+    const float *gscale;          // device pointer to the clip coefficient, or NULL
+    int32_t write_grad;           // store the scaled gradient back (ADANA_WRITE_GRAD)
     int32_t reserved;
+    const unsigned short *pow16;  // POW_TABLE16: the launch's pow table in the workspace
 };
 
 // ---------------------------------------------------------------------------
@@ -107,8 +108,11 @@ enum PowKind { POW_GENERAL = 0, POW_ONE = 1, POW_SPECIAL = 2,
                // Manau's Dana-Star-MK4 branch with mk4A = mk4B = 0 (its other two
                // powers are then a copy and a one), by the kind of its 1 - kappa
                // exponent; POW_MANAU_MK4: any exponents, chosen per class at run time
-               POW_MANAU_GENERAL = 3, POW_MANAU_ONE = 4, POW_MANAU_SPECIAL = 5, POW_MANAU_MK4 = 6 };
-constexpr bool is_manau(int powk) { return powk >= POW_MANAU_GENERAL; }
+               POW_MANAU_GENERAL = 3, POW_MANAU_ONE = 4, POW_MANAU_SPECIAL = 5, POW_MANAU_MK4 = 6,
+               // bfloat16 state with one general exponent for the launch: the pow of
+               // every possible input read from a table the launch fills first
+               POW_TABLE16 = 7 };
+constexpr bool is_manau(int powk) { return powk >= POW_MANAU_GENERAL && powk <= POW_MANAU_MK4; }
 constexpr bool pow_tables(int powk) { return powk == POW_GENERAL || powk == POW_MANAU_GENERAL; }
 
 // The pow's tables as the kernel reads them: POW_GENERAL instances copy them
@@ -118,6 +122,7 @@ constexpr bool pow_tables(int powk) { return powk == POW_GENERAL || powk == POW_
 struct PowTab {
     const adana::LogPair *log;
     const double *exp2j;
+    const unsigned short *pow16;   // POW_TABLE16 only
 };
 
 template <int POWK>
@@ -237,6 +242,9 @@ __device__ __forceinline__ float star_phase_b(float p, float g, const StarMid &a
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ float rb(float x) { return bf16_round(x); }
 
+// POW_TABLE16: one entry per bfloat16 value in [1, +inf] (bits 0x3F80 .. 0x7F80).
+constexpr unsigned int kPow16Entries = 0x7F80u - 0x3F80u + 1u;
+
 // The launch's binary32 scalars as the bfloat16 ops see them.
 struct Scalars16 {
     float a16, lerp_coef16, eps16, pw16, min_p16, clip16, c3_16, cg2_16, e16;
@@ -319,7 +327,14 @@ __device__ __forceinline__ float star16_phase_b(float p, float g, const StarMid 
 // exponent, the result rounded to binary32 and then to bfloat16).
 template <int POWK>
 __device__ __forceinline__ float pow16(float x, const adana_step_scalars &sc, const Scalars16 &q, const PowTab &tab) {
-    if constexpr (POWK == POW_GENERAL) {
+    if constexpr (POWK == POW_TABLE16) {
+        // x = max(bf16(tau * t), 1) is a bfloat16 value in [1, +inf] or a NaN:
+        // entry (bits >> 16) - 0x3F80 of the table pow16_fill_kernel wrote
+        // with the POW_GENERAL code below, so the same bits.  A NaN gives
+        // itself, quieted, as that code does.
+        const unsigned int idx = (__float_as_uint(x) >> 16) - 0x3F80u;
+        return idx < kPow16Entries ? bf16_to_f32(tab.pow16[idx]) : rb(x);
+    } else if constexpr (POWK == POW_GENERAL) {
         return rb(adana::pow_f32_unit_exp_tab(x, q.e16, tab.log, tab.exp2j));
     } else if constexpr (POWK == POW_ONE) {
         return 1.0f;
@@ -336,6 +351,17 @@ __device__ __forceinline__ float pow16(float x, const adana_step_scalars &sc, co
         default: return rb(adana::pow_f32_via_f64(x, q.e16));
         }
     }
+}
+
+// The POW_TABLE16 table of a launch whose classes share one general exponent
+// (sc: any of them): entry k = pow16 of the bfloat16 value with bits
+// 0x3F80 + k, by the POW_GENERAL code, stored as bfloat16 bits.
+__global__ __launch_bounds__(256) void pow16_fill_kernel(unsigned short *__restrict__ tab, adana_step_scalars sc) {
+    const unsigned int k = blockIdx.x * 256u + threadIdx.x;
+    if (k >= kPow16Entries) return;
+    const Scalars16 q = scalars16(sc);
+    const float x = bf16_to_f32(static_cast<unsigned short>(0x3F80u + k));
+    tab[k] = f32_to_bf16(pow16<POW_GENERAL>(x, sc, q, PowTab{adana::kLog, adana::kExp2J, nullptr}));
 }
 
 template <bool STAR, int POWK, int N>
@@ -801,7 +827,7 @@ __global__ __launch_bounds__(kChunk / VEC) void mta_step_kernel(const adana_tens
     // the combine kernel's per-tensor arrival counters start at zero
     for (int64_t k = chunk * kThreads + tid; k < n; k += static_cast<int64_t>(gridDim.x) * kThreads) counters[k] = 0;
     const float gs = pack.gscale != nullptr ? *pack.gscale : 1.0f;
-    PowTab tab{adana::kLog, adana::kExp2J};
+    PowTab tab{adana::kLog, adana::kExp2J, pack.pow16};
     if constexpr (STAR && pow_tables(POWK)) {
         static_assert(kThreads >= 256, "one thread per table entry");
         __shared__ adana::LogPair s_log[128];
@@ -812,7 +838,7 @@ __global__ __launch_bounds__(kChunk / VEC) void mta_step_kernel(const adana_tens
             s_exp2j[tid - 128] = adana::kExp2J[tid - 128];
         }
         __syncthreads();
-        tab = PowTab{s_log, s_exp2j};
+        tab = PowTab{s_log, s_exp2j, nullptr};
     }
 
     const int i0 = chunk_first[chunk];
@@ -1273,7 +1299,8 @@ __global__ __launch_bounds__(kBlock) void grad_scale_kernel(const adana_tensor_d
 
 // Workspace layout: chunk partials (float4 per (chunk, tensor) slot), then the
 // folds (double4 each), then the combine's arrival counters (int32 per
-// tensor), each part 256-byte aligned.
+// tensor), then the bfloat16 pow table (POW_TABLE16 launches), each part
+// 256-byte aligned.
 size_t partials_bytes(const adana_plan &pl) {
     return static_cast<size_t>(pl.n_chunks + pl.n_tensors) * 16;
 }
@@ -1281,8 +1308,11 @@ size_t folds_offset(const adana_plan &pl) { return (partials_bytes(pl) + 255) / 
 size_t counters_offset(const adana_plan &pl) {
     return (folds_offset(pl) + static_cast<size_t>(pl.n_folds) * 32 + 255) / 256 * 256;
 }
+size_t pow16_offset(const adana_plan &pl) {
+    return (counters_offset(pl) + static_cast<size_t>(pl.n_tensors) * 4 + 255) / 256 * 256;
+}
 size_t workspace_bytes(const adana_plan &pl) {
-    return counters_offset(pl) + static_cast<size_t>(pl.n_tensors) * 4;
+    return pow16_offset(pl) + static_cast<size_t>(kPow16Entries) * 2;
 }
 
 // Residency cap.  The step reaches the highest HBM throughput with 4
@@ -1366,6 +1396,9 @@ void launch_pow(int powk, int64_t n_chunks, hipStream_t st, const adana_tensor_d
         launch_main<true, GBF16, PM, POW_ONE>(n_chunks, st, d, vs, cf, n, pack, partials, counters);
     } else if (powk == POW_SPECIAL) {
         launch_main<true, GBF16, PM, POW_SPECIAL>(n_chunks, st, d, vs, cf, n, pack, partials, counters);
+    } else if constexpr (PM == PM_BF16) {
+        if (powk == POW_TABLE16)
+            launch_main<true, GBF16, PM, POW_TABLE16>(n_chunks, st, d, vs, cf, n, pack, partials, counters);
     } else if constexpr (!GBF16 && PM == PM_F32) {  // Manau's branch: float32 only
         if (powk == POW_MANAU_GENERAL) {
             launch_main<true, false, PM_F32, POW_MANAU_GENERAL>(n_chunks, st, d, vs, cf, n, pack, partials, counters);
@@ -1634,6 +1667,21 @@ int step_impl(const char *fn, const adana_plan *plan, const adana_step_scalars *
         }
         int powk = all_general ? POW_GENERAL : (all_one ? POW_ONE : POW_SPECIAL);
         if (manau) powk = mk4_trivial ? powk + POW_MANAU_GENERAL : POW_MANAU_MK4;
+        if (s16 && star && powk == POW_GENERAL) {
+            // bfloat16 state: one exponent for every class -> fill the launch's
+            // pow table first (16,385 entries, stream-ordered before the step)
+            bool same_exp = true;
+            for (int c = 1; c < n_classes; ++c) same_exp = same_exp && h_scalars[c].star_exp == h_scalars[0].star_exp;
+            if (same_exp) {
+                unsigned short *tab = reinterpret_cast<unsigned short *>(static_cast<char *>(d_workspace) +
+                                                                          pow16_offset(pl));
+                hipLaunchKernelGGL(pow16_fill_kernel, dim3((kPow16Entries + 255) / 256), dim3(256), 0, st, tab,
+                                   h_scalars[0]);
+                if (int rc = launch_status(fn, "pow table")) return rc;
+                pack.pow16 = tab;
+                powk = POW_TABLE16;
+            }
+        }
 #define ADANA_LAUNCH(S, G, P) \
         launch_pow<S, G, P>(powk, pl.n_chunks, st, pl.desc, pl.vstart, pl.chunk_first, n, pack, partials, \
                             counters)

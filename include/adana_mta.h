@@ -260,8 +260,9 @@ size_t adana_workspace_bytes(const adana_plan *plan);
  *   h_scalars   host array of n_classes scalar classes (passed by value to
  *               the kernel; no host-to-device copy)
  *   d_workspace device scratch of at least adana_workspace_bytes(plan) bytes
- *               (per-chunk partial sums, their folds and one arrival counter
- *               per tensor; contents on entry are ignored)
+ *               (per-chunk partial sums, their folds, one arrival counter
+ *               per tensor, and 32 KB for the pow table a bfloat16-state
+ *               Dana-Star launch fills first; contents on entry are ignored)
  *   d_diag      device float[5 * n_tensors]: per tensor current_alpha,
  *               gradient_norm, auto_factor_mean, current_kappa_factor,
  *               m_norm (src/optim/adana.py:221-225); with ADANA_STATE_BF16

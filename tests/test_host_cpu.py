@@ -150,10 +150,12 @@ def test_workspace_bytes():
     from adana_amd import _lib
 
     pl = _lib.Plan(n_tensors=10, n_chunks=100, n_folds=12)
-    # chunk partials, then folds, then one arrival counter per tensor, each 256-byte aligned
+    # chunk partials, then folds, then one arrival counter per tensor, then the
+    # bfloat16 pow table (one entry per bf16 value in [1, +inf]), each 256-byte aligned
     folds_at = (110 * 16 + 255) // 256 * 256
     counters_at = (folds_at + 12 * 32 + 255) // 256 * 256
-    assert _lib.workspace_bytes(pl) == counters_at + 10 * 4
+    table_at = (counters_at + 10 * 4 + 255) // 256 * 256
+    assert _lib.workspace_bytes(pl) == table_at + (0x7F80 - 0x3F80 + 1) * 2
 
 
 def test_mta_step_rejects_bad_arguments():
