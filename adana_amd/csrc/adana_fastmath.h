@@ -13,6 +13,20 @@
 
 namespace adana {
 
+// v_cmp_class_f32 masks.
+constexpr int kClassZero = (1 << 5) | (1 << 6);
+constexpr int kClassNormal = (1 << 3) | (1 << 8);
+constexpr int kClassPosNormal = 1 << 8;
+
+// x, as a new value the compiler cannot compute before the branch that holds
+// this (one v_mov in that branch): keeps an IEEE sequence in its rare arm
+// instead of being run for every element and selected.
+__device__ __forceinline__ float opaque(float x) {
+    float y;
+    asm volatile("v_mov_b32 %0, %1" : "=v"(y) : "v"(x));
+    return y;
+}
+
 // Correctly rounded a / b for operands on which the IEEE division sequence's
 // range scaling (v_div_scale) and special-case fixup (v_div_fixup) are
 // identities: b normal in [0.5, 1], and a either normal or b == 1.  This is the
@@ -48,10 +62,7 @@ __device__ __forceinline__ float sqrt_normal(float x) {
 // zeros, small and negative inputs and NaNs, behind a real branch.
 __device__ __forceinline__ float sqrt_f32(float x) {
     float s = sqrt_normal(x);
-    if (__builtin_expect(!(x >= 0x1p-96f), 0)) {
-        asm volatile("" : "+v"(x));   // keeps the IEEE sequence out of the common path
-        s = __builtin_sqrtf(x);
-    }
+    if (__builtin_expect(!(x >= 0x1p-96f), 0)) s = __builtin_sqrtf(opaque(x));
     return s;
 }
 
@@ -85,16 +96,15 @@ __device__ __forceinline__ unsigned int bf16_pack2(float lo, float hi) {
 // significant bits), a quotient equal to a bfloat16 midpoint M 2^k (M odd, 9
 // bits) would need A = M B, more than 8 bits; so a normal quotient lies at
 // least 2^k / 255 > 2^7 binary32 ulps from every midpoint, and a * rcp(b)
-// (within 2 ulps) rounds like it.  Denominators outside the normal range,
-// quotients below 2^-125 (bfloat16's subnormal grid) and NaNs take the IEEE
-// sequence; a zero numerator's fast result is the IEEE one.
+// (within 2 ulps) rounds like it.  A zero product with a normal reciprocal is
+// a zero numerator or a quotient below 2^-149, which the IEEE quotient rounds
+// to a bfloat16 zero of the same sign.  Anything else (a subnormal, infinite
+// or NaN quotient or reciprocal) takes the IEEE sequence.
 __device__ __forceinline__ float div_bf16(float a, float b) {
-    float q = a * __builtin_amdgcn_rcpf(b);
-    const bool fast = (fabsf(q) >= 0x1p-125f || a == 0.0f) && fabsf(b) >= 0x1p-126f;
-    if (__builtin_expect(!fast, 0)) {
-        asm volatile("" : "+v"(a), "+v"(b));   // a real branch: the compiler may not run the IEEE
-        q = a / b;                             // sequence for every element and select
-    }
+    const float y = __builtin_amdgcn_rcpf(b);
+    float q = a * y;
+    const bool fast = __builtin_amdgcn_classf(q, kClassNormal | kClassZero) && __builtin_amdgcn_classf(y, kClassNormal);
+    if (__builtin_expect(!fast, 0)) q = opaque(a) / b;
     return q;
 }
 
@@ -103,13 +113,10 @@ __device__ __forceinline__ float div_bf16(float a, float b) {
 // bits) would need x = M^2 2^2k, 17 significant bits; so sqrt(x) lies at least
 // 2^5 binary32 ulps from every bfloat16 midpoint and the hardware square root
 // (within 1 ulp) rounds like the exact one.  Zeros give themselves; other
-// inputs below 2^-126 (subnormals, negatives) and NaNs take the IEEE sequence.
+// inputs (subnormals, negatives, infinities) and NaNs take the IEEE sequence.
 __device__ __forceinline__ float sqrt_bf16(float x) {
     float s = __builtin_amdgcn_sqrtf(x);
-    if (__builtin_expect(!(x >= 0x1p-126f || x == 0.0f), 0)) {
-        asm volatile("" : "+v"(x));
-        s = __builtin_sqrtf(x);
-    }
+    if (__builtin_expect(!__builtin_amdgcn_classf(x, kClassPosNormal | kClassZero), 0)) s = __builtin_sqrtf(opaque(x));
     return s;
 }
 
