@@ -9,7 +9,7 @@ import numpy as np
 import pytest
 import torch
 
-from helpers import ulp_diff
+from helpers import bf16_ulp_diff, ulp_diff
 from test_gpu_parity import STAR_HARD_CASES
 
 pytestmark = [pytest.mark.gpu,
@@ -92,3 +92,77 @@ def test_cpp_host_drives_the_c_abi():
     print(r.stdout[-2000:], flush=True)
     assert r.returncode == 0, r.stdout[-2000:] + r.stderr[-2000:]
     assert r.stdout.strip().splitlines()[-1] == "c_abi_driver: ok"
+
+
+@pytest.mark.parametrize("kappas", [(0.85, 0.85), (0.85, 0.6)], ids=["one_exponent_table", "two_exponents_general"])
+def test_bf16_state_classes_through_the_c_abi(oracle_mod, kappas):
+    """bfloat16 state (ADANA_STATE_BF16) through the raw C ABI with two scalar
+    classes.  One shared exponent takes the launch's pow table; two
+    exponents (reachable only through the C ABI: the Python classes share
+    one kappa) take the binary64 pow per element.  Both bit-exact against
+    the oracle's bfloat16 restatement (Dana-Star p: the pow allowance),
+    12 steps so that tau * t passes 1 and alpha passes 0.5."""
+    from adana_amd import _lib
+
+    print("case: raw C ABI, bf16 state, kappas", kappas, flush=True)
+    O = oracle_mod
+    L = _lib.lib()
+    rng = np.random.default_rng(11)
+    sizes = [70_000, 4099, 1 << 16]
+    cls = [0, 1, 0]
+    p_h = [O.f32_to_bf16(rng.normal(0, 0.02, n).astype(np.float32)) for n in sizes]
+
+    def dev(h):
+        return torch.from_numpy(h.view(np.int16).copy()).view(torch.bfloat16).cuda()
+
+    p = [dev(h) for h in p_h]
+    m = [torch.zeros_like(x) for x in p]
+    v = [torch.zeros_like(x) for x in p]
+    tau = [torch.zeros_like(x) for x in p]
+    g = [torch.empty_like(x) for x in p]
+    n = len(sizes)
+    vstart, fold_first, n_chunks, n_folds = _lib.plan_layout(np.array(sizes, dtype=np.int64))
+    desc = np.zeros(n, _lib.DESC_DTYPE)
+    for i in range(n):
+        desc[i] = (p[i].data_ptr(), g[i].data_ptr(), m[i].data_ptr(), v[i].data_ptr(), tau[i].data_ptr(), 0,
+                   sizes[i], cls[i], _lib.DESC_VEC_OK)
+    table = torch.from_numpy(np.concatenate([desc.view(np.uint8), vstart.view(np.uint8),
+                                             fold_first.view(np.uint8)])).cuda()
+    plan = _lib.Plan(desc=table.data_ptr(), vstart=table.data_ptr() + 64 * n,
+                     fold_first=table.data_ptr() + 64 * n + 8 * (n + 1), n_tensors=n,
+                     n_chunks=n_chunks, n_folds=n_folds)
+    chunk_first = torch.empty(n_chunks, dtype=torch.int32, device="cuda")
+    stream = torch.cuda.current_stream().cuda_stream
+    _lib.check(L.adana_plan_index(ctypes.c_void_p(plan.vstart), n, n_chunks,
+                                  ctypes.c_void_p(chunk_first.data_ptr()), ctypes.c_void_p(stream)), "plan_index")
+    plan.chunk_first = chunk_first.data_ptr()
+    ws = torch.empty(_lib.workspace_bytes(plan), dtype=torch.uint8, device="cuda")
+    diag = torch.empty(5 * n, dtype=torch.bfloat16, device="cuda")
+    kw = dict(peak_lr=1e-3, delta=8.0, epsilon=1e-8, weight_decay=0.4, clipsnr=2.0, wd_ts=10.0,
+              gamma_3_factor=1.0)
+    hps = [_lib.HParams(kappa=k, has_clip=1, wd_decaying=1, **kw) for k in kappas]
+    cpu = {"p": [h.copy() for h in p_h]}
+    for key in ("m", "v", "tau"):
+        cpu[key] = [np.zeros(nn, np.uint16) for nn in sizes]
+    flags = _lib.VARIANT_STAR | _lib.GRAD_BF16 | _lib.STATE_BF16
+    for t in range(1, 13):
+        g_h = [O.f32_to_bf16(rng.normal(0, 1e-3, nn).astype(np.float32)) for nn in sizes]
+        for gi, h in zip(g, g_h):
+            gi.copy_(dev(h))
+        sc = (_lib.StepScalars * 2)(*[_lib.step_scalars(hp, 1e-3, t) for hp in hps])
+        _lib.check(L.adana_mta_step(ctypes.byref(plan), ctypes.cast(sc, ctypes.c_void_p), 2, flags,
+                                    ctypes.c_void_p(ws.data_ptr()), ws.numel(), ctypes.c_void_p(diag.data_ptr()),
+                                    ctypes.c_void_p(stream)), "mta_step")
+        for i in range(n):
+            osc = O.step_scalars(lr=1e-3, kappa=kappas[cls[i]], wd_decaying=True, t=t, **kw)
+            O.element_step(True, cpu["p"][i], g_h[i], cpu["m"][i], cpu["v"][i], cpu["tau"][i], osc)
+        torch.cuda.synchronize()
+        for i in range(n):
+            for key, arr in (("m", m), ("v", v), ("tau", tau)):
+                got = arr[i].cpu().view(torch.int16).numpy().view(np.uint16)
+                assert np.array_equal(got, cpu[key][i]), (t, i, key)
+            got = p[i].cpu().view(torch.int16).numpy().view(np.uint16)
+            d = bf16_ulp_diff(got, cpu["p"][i])
+            bad = int(np.count_nonzero(d))
+            assert bad <= STAR_HARD_CASES and (bad == 0 or d.max() <= 1), (t, i, bad, d.max())
+            cpu["p"][i][...] = got
