@@ -1312,6 +1312,7 @@ size_t pow16_offset(const adana_plan &pl) {
     return (counters_offset(pl) + static_cast<size_t>(pl.n_tensors) * 4 + 255) / 256 * 256;
 }
 size_t workspace_bytes(const adana_plan &pl) {
+    if (pl.n_chunks == 0) return counters_offset(pl) + static_cast<size_t>(pl.n_tensors) * 4;   // no launch needs the table
     return pow16_offset(pl) + static_cast<size_t>(kPow16Entries) * 2;
 }
 

@@ -156,6 +156,9 @@ def test_workspace_bytes():
     counters_at = (folds_at + 12 * 32 + 255) // 256 * 256
     table_at = (counters_at + 10 * 4 + 255) // 256 * 256
     assert _lib.workspace_bytes(pl) == table_at + (0x7F80 - 0x3F80 + 1) * 2
+    # a list without elements launches no step kernel: no table, and nothing at all when empty
+    assert _lib.workspace_bytes(_lib.Plan(n_tensors=3, n_chunks=0, n_folds=0)) == 256 + 3 * 4
+    assert _lib.workspace_bytes(_lib.Plan(n_tensors=0, n_chunks=0, n_folds=0)) == 0
 
 
 def test_mta_step_rejects_bad_arguments():
