@@ -334,7 +334,85 @@ PyObject *grads_match(PyObject *, PyObject *args) {
     Py_RETURN_TRUE;
 }
 
+/* grads_scan(params, bf16) -> (grads, absent, grad_ptrs, param_ptrs, match)
+ *
+ * One pass doing what grads_of(params), data_ptrs(grads), data_ptrs(params)
+ * and grads_match(params, grads, bf16) do together: the gradients and their
+ * None pattern, both pointer tables (0 for None), and True when every
+ * parameter has a gradient that matches it as grads_match requires. */
+PyObject *grads_scan(PyObject *, PyObject *args) {
+    PyObject *params;
+    int bf16 = 0;
+    if (!PyArg_ParseTuple(args, "O!p", &PyList_Type, &params, &bf16)) return nullptr;
+    const Py_ssize_t n = PyList_GET_SIZE(params);
+    const c10::ScalarType want = bf16 ? c10::ScalarType::BFloat16 : c10::ScalarType::Float;
+    PyObject *out = PyList_New(n);
+    PyObject *absent = PyBytes_FromStringAndSize(nullptr, n);
+    PyObject *gp = PyBytes_FromStringAndSize(nullptr, 8 * n);
+    PyObject *pp = PyBytes_FromStringAndSize(nullptr, 8 * n);
+    if (!out || !absent || !gp || !pp) {
+        Py_XDECREF(out);
+        Py_XDECREF(absent);
+        Py_XDECREF(gp);
+        Py_XDECREF(pp);
+        return nullptr;
+    }
+    char *ab = PyBytes_AS_STRING(absent);
+    uint64_t *gw = reinterpret_cast<uint64_t *>(PyBytes_AS_STRING(gp));
+    uint64_t *pw = reinterpret_cast<uint64_t *>(PyBytes_AS_STRING(pp));
+    bool match = true;
+    try {
+        for (Py_ssize_t i = 0; i < n; ++i) {
+            PyObject *p = PyList_GET_ITEM(params, i);
+            PyObject *g;
+            if (THPVariable_CheckExact(p)) {
+                const at::Tensor &pt = THPVariable_Unpack(p);
+                const at::Tensor &t = pt.unsafeGetTensorImpl()->grad();
+                pw[i] = reinterpret_cast<uint64_t>(pt.data_ptr());
+                if (t.defined()) {
+                    g = THPVariable_Wrap(t);
+                    gw[i] = reinterpret_cast<uint64_t>(t.data_ptr());
+                    match = match && !t.is_sparse() && t.scalar_type() == want && t.device() == pt.device() &&
+                            same_layout(t, pt);
+                } else {
+                    Py_INCREF(Py_None);
+                    g = Py_None;
+                    gw[i] = 0;
+                    match = false;
+                }
+            } else {
+                g = PyObject_GetAttr(p, g_grad_name);
+                match = false;
+                if (g && (data_ptr_of(g, &gw[i]) || data_ptr_of(p, &pw[i]))) {
+                    Py_DECREF(g);
+                    g = nullptr;
+                }
+            }
+            if (!g) {
+                Py_DECREF(out);
+                Py_DECREF(absent);
+                Py_DECREF(gp);
+                Py_DECREF(pp);
+                return nullptr;
+            }
+            ab[i] = g == Py_None ? 1 : 0;
+            PyList_SET_ITEM(out, i, g);                      /* steals the reference */
+        }
+    } catch (const std::exception &e) {
+        Py_DECREF(out);
+        Py_DECREF(absent);
+        Py_DECREF(gp);
+        Py_DECREF(pp);
+        PyErr_SetString(PyExc_RuntimeError, e.what());
+        return nullptr;
+    }
+    return Py_BuildValue("NNNNO", out, absent, gp, pp, match ? Py_True : Py_False);
+}
+
 PyMethodDef methods[] = {
+    {"grads_scan", grads_scan, METH_VARARGS,
+     "grads_scan(params, bf16) -> (grads, absent, grad_ptrs, param_ptrs, match): grads_of, data_ptrs of the "
+     "gradients and of the parameters, and grads_match, in one pass"},
     {"advance_if_same", advance_if_same, METH_VARARGS,
      "advance_if_same(params, grads, states[, param_ptrs[, grad_ptrs]]) -> bool: if params[i].grad is "
      "grads[i] for all i (and params[i] / grads[i] still have the data pointers given as native uint64 bytes), "

@@ -504,7 +504,14 @@ class _DanaFamily(Optimizer):
             classes = act["classes"] = [(gi, t + 1) for gi, t in act["classes"]]
             params = act["params"]
             return self._launch(params, grads, classes, loss)
-        all_grads, absent = _hoststep.grads_of(all_params)                   # adana.py:186
+        scan = None
+        if self._sets is not None and act is not None and act["all"] and len(self._sets) == 1:
+            # one launch set over every parameter: the gradients, their None
+            # pattern, both pointer tables and the layout check in one pass
+            scan = _hoststep.grads_scan(all_params, bool(self._sets[0].flags & _lib.GRAD_BF16))
+            all_grads, absent = scan[0], scan[1]                             # adana.py:186
+        else:
+            all_grads, absent = _hoststep.grads_of(all_params)               # adana.py:186
 
         if self._sets is not None and act is not None and act["absent"] == absent:
             # Steady state: the same tensors have gradients as at the last step
@@ -515,13 +522,19 @@ class _DanaFamily(Optimizer):
             _hoststep.advance_steps(act["states"])                             # adana.py:197
             classes = act["classes"] = [(gi, t + 1) for gi, t in act["classes"]]
             params = act["params"]
-            for ls in self._sets:
-                ls.grads = grads if len(self._sets) == 1 else [grads[i] for i in ls.index]
-                self._refresh_ptrs(ls)
+            if scan is not None:
+                ls = self._sets[0]
+                ls.grads = grads
+                self._refresh_ptrs(ls, key=(scan[2], scan[3]), grads_ok=scan[4])
+                act["pptrs"], act["gptrs"] = scan[3], scan[2]
+            else:
+                for ls in self._sets:
+                    ls.grads = grads if len(self._sets) == 1 else [grads[i] for i in ls.index]
+                    self._refresh_ptrs(ls)
+                act["pptrs"] = _hoststep.data_ptrs(all_params)
+                act["gptrs"] = _hoststep.data_ptrs(all_grads)
             act["all_grads"] = all_grads
             act["grads"] = grads
-            act["pptrs"] = _hoststep.data_ptrs(all_params)
-            act["gptrs"] = _hoststep.data_ptrs(all_grads)
         else:
             params, grads, states, keys, index, fresh = [], [], [], [], [], []
             for i, (p, g) in enumerate(zip(all_params, all_grads)):
@@ -624,17 +637,22 @@ class _DanaFamily(Optimizer):
                                    f"of shape {a}: the size of tensor a ({a}) must match the size of "
                                    f"tensor b ({b})")
 
-    def _refresh_ptrs(self, ls: _LaunchSet) -> None:
+    def _refresh_ptrs(self, ls: _LaunchSet, key=None, grads_ok=None) -> None:
         """Re-point the launch set's descriptors at this step's gradients and
         the parameters' current storage (re-uploaded only when an address
-        moved: a new gradient allocation, or ``p.data`` rebound)."""
-        key = (_hoststep.data_ptrs(ls.grads), _hoststep.data_ptrs(ls.params))
+        moved: a new gradient allocation, or ``p.data`` rebound).  ``key``:
+        the gradients' and parameters' pointer tables, and ``grads_ok`` the
+        grads_match result, when the caller has them already."""
+        if key is None:
+            key = (_hoststep.data_ptrs(ls.grads), _hoststep.data_ptrs(ls.params))
         if key == ls.ptr_key:
             return
         if key[1] != ls.ptr_key[1]:
             self._check_state_shapes(ls)
         bf16 = bool(ls.flags & _lib.GRAD_BF16)
-        if key[1] == ls.ptr_key[1] and _hoststep.grads_match(ls.params, ls.grads, bf16):
+        if grads_ok is None and key[1] == ls.ptr_key[1]:
+            grads_ok = _hoststep.grads_match(ls.params, ls.grads, bf16)
+        if key[1] == ls.ptr_key[1] and grads_ok:
             # only gradients moved, and each is a dense contiguous tensor of its
             # parameter's shape and the set's dtype: re-point the grad column
             g = np.frombuffer(key[0], dtype=np.uint64)
