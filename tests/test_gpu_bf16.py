@@ -223,3 +223,50 @@ def test_bf16_state_dict_matches_reference_schema():
 def _bits_t(t):
     return t.detach().view(torch.int16)
 
+
+
+@pytest.mark.parametrize("star", [False, True])
+def test_bf16_nonfinite_gradients(oracle_mod, star):
+    """NaN, +inf and -inf gradient entries (and huge and subnormal ones) on the
+    bfloat16 path: p, m, v, tau bit-exact against the oracle's bfloat16
+    restatement wherever it is finite, and NaN where it is NaN (the IEEE arms
+    of the bf16 division and square root, and the pow table's NaN entry)."""
+    import adana_amd
+
+    O = oracle_mod
+    print("case: bf16 state, non-finite gradients, star", star, flush=True)
+    rng = np.random.default_rng(5)
+    sizes = [4096, 777]
+    host = [O.f32_to_bf16(rng.normal(0, 0.02, n).astype(np.float32)) for n in sizes]
+    gpu = [torch.nn.Parameter(_to_gpu16(h)) for h in host]
+    hp = dict(lr=1e-3, delta=8.0, kappa=0.85, weight_decay=0.1, clipsnr=2.0)
+    cls = adana_amd.DANA_STAR_MK4 if star else adana_amd.ADana
+    opt = cls(gpu, **hp)
+    orc = O.OracleOptimizer(groups=[O.OracleGroup(params=host, lr=hp["lr"], weight_decay=0.1)],
+                            star=star, peak_lr=hp["lr"], kappa=0.85, clipsnr=2.0, bf16=True)
+    specials = np.array([np.nan, np.inf, -np.inf, 3e38, -3e38, 1e-40, -1e-40, 0.0], np.float32)
+    for t in range(1, 11):
+        gf = [rng.normal(0, 1e-3, n).astype(np.float32) for n in sizes]
+        if t in (2, 5, 9):
+            for g in gf:
+                idx = rng.choice(g.size, 40, replace=False)
+                g[idx] = rng.choice(specials, 40)
+        g16 = [O.f32_to_bf16(g) for g in gf]
+        for p, g in zip(gpu, g16):
+            p.grad = _to_gpu16(g)
+        opt.step()
+        orc.step([g16])
+        torch.cuda.synchronize()
+        for i, p in enumerate(gpu):
+            st, ost = opt.state[p], orc.state[id(host[i])]
+            tag = f"star {star} t={t} tensor {i}"
+            for key in ("m", "v", "tau") if star else ("m", "v"):
+                got, want = _bits(st[key]), ost[key]
+                gn, wn = np.isnan(O.bf16_to_f32(got)), np.isnan(O.bf16_to_f32(want))
+                assert np.array_equal(gn, wn), f"{tag} {key}: NaN in different places"
+                _check(got[~gn], want[~wn], f"{tag} {key}")
+            got, want = _bits(p), host[i]
+            gn, wn = np.isnan(O.bf16_to_f32(got)), np.isnan(O.bf16_to_f32(want))
+            assert np.array_equal(gn, wn), f"{tag} p: NaN in different places"
+            _check(got[~gn], want[~wn], f"{tag} p", STAR_HARD_CASES if star else 0)
+            host[i][...] = got
