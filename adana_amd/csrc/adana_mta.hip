@@ -903,6 +903,12 @@ constexpr int kFold = ADANA_FOLD_CHUNKS;
 constexpr int kFoldPerThread = kFold / kBlock;
 static_assert(kFold % kBlock == 0, "fold workgroups cover whole thread rows");
 
+// Chunk range [lo, hi] of fold j, tensor i's (fold_first[i] <= j < fold_first[i + 1]).
+__device__ __forceinline__ void fold_range(int64_t j, int f0, int64_t b0, int64_t b1, int64_t &lo, int64_t &hi) {
+    lo = b0 + (j - f0) * kFold;
+    hi = (lo + kFold - 1 < b1) ? lo + kFold - 1 : b1;
+}
+
 __device__ __forceinline__ void block_sum4(double &s0, double &s1, double &s2, double &s3,
                                            double (*red)[4]) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -949,7 +955,9 @@ __device__ __forceinline__ void write_diag(void *diag, int bf16, int i, double n
 //  * Workgroups [0, n_folds) are fold workgroups: fold j reduces up to
 //    ADANA_FOLD_CHUNKS consecutive chunk partials of one tensor of more than
 //    ADANA_DIRECT_CHUNKS chunks, in binary64 and a fixed order, to folds[j].
-//    With kCombineFenced, the last of a tensor's folds to finish (an arrival
+//    A tensor with a single fold (at most ADANA_FOLD_CHUNKS chunks) is
+//    finalized by that workgroup.  For more, with kCombineFenced, the last
+//    of a tensor's folds to finish (an arrival
 //    counter per tensor, zeroed by the main kernel; agent-scope release and
 //    acquire, so the folds written on other XCDs are visible) sums the
 //    tensor's folds in index order and writes its diagnostics: one launch.
@@ -1005,8 +1013,9 @@ __global__ __launch_bounds__(kBlock) void combine_kernel(const adana_tensor_desc
         const int i = l;
         const int64_t vs = vstart[i], numel = desc[i].numel;
         const int64_t b0 = vs / kChunk, b1 = (vs + numel - 1) / kChunk;
-        const int64_t lo = b0 + (j - fold_first[i]) * kFold;
-        const int64_t hi = (lo + kFold - 1 < b1) ? lo + kFold - 1 : b1;
+        const int f0 = fold_first[i], f1 = fold_first[i + 1];
+        int64_t lo, hi;
+        fold_range(j, f0, b0, b1, lo, hi);
         float4 q[kFoldPerThread];
 #pragma unroll
         for (int u = 0; u < kFoldPerThread; ++u) {
@@ -1019,7 +1028,10 @@ __global__ __launch_bounds__(kBlock) void combine_kernel(const adana_tensor_desc
             s0 += q[u].x; s1 += q[u].y; s2 += q[u].z; s3 += q[u].w;
         }
         block_sum4(s0, s1, s2, s3, red);
-        const int f0 = fold_first[i], f1 = fold_first[i + 1];
+        if (f1 - f0 == 1) {               // the tensor's only fold: its diagnostics, no handoff
+            if (threadIdx.x == 0) write_diag(diag, diag_bf16, i, static_cast<double>(numel), s0, s1, s2, s3);
+            return;
+        }
         if (mode != kCombineFenced) {
             if (threadIdx.x == 0) folds[j] = make_double4(s0, s1, s2, s3);
             return;
@@ -1042,12 +1054,12 @@ __global__ __launch_bounds__(kBlock) void combine_kernel(const adana_tensor_desc
     }
     const int i = static_cast<int>((b - n_folds) * kWaves + wave);
     if (i >= n) return;                                                   // whole wave
-    const bool folded = fold_first[i + 1] > fold_first[i];
+    const int nf = fold_first[i + 1] - fold_first[i];
     if (mode == kCombineFinalizeFolded) {
-        if (folded) finalize_folds(folds, fold_first[i], fold_first[i + 1], lane, diag, diag_bf16, i, desc[i].numel);
+        if (nf > 1) finalize_folds(folds, fold_first[i], fold_first[i + 1], lane, diag, diag_bf16, i, desc[i].numel);
         return;
     }
-    if (folded) return;
+    if (nf > 0) return;
     double s0 = 0.0, s1 = 0.0, s2 = 0.0, s3 = 0.0;
     const int64_t numel = desc[i].numel;
     if (numel > 0) {
@@ -1188,8 +1200,8 @@ __global__ __launch_bounds__(kBlock) void sumsq_fold_kernel(const adana_tensor_d
     const int i = l;
     const int64_t vs = vstart[i], numel = desc[i].numel;
     const int64_t b0 = vs / kChunk, b1 = (vs + numel - 1) / kChunk;
-    const int64_t lo = b0 + (j - fold_first[i]) * kFold;
-    const int64_t hi = (lo + kFold - 1 < b1) ? lo + kFold - 1 : b1;
+    int64_t lo, hi;
+    fold_range(j, fold_first[i], b0, b1, lo, hi);
     double s = 0.0;
 #pragma unroll
     for (int u = 0; u < kFoldPerThread; ++u) {

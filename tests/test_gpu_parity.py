@@ -500,13 +500,15 @@ def test_drift_over_1000_steps(oracle_mod, star):
 @pytest.mark.parametrize("star", [False, True])
 def test_large_tensor_fold_path(oracle_mod, star):
     """Tensors of more than ADANA_DIRECT_CHUNKS chunks go through the fold
-    workgroups; smaller ones are summed directly by the finalize step: both
-    in one list, diagnostics against the oracle (and the clip norm path)."""
+    workgroups (a tensor with a single fold finalizes itself, one with
+    several hands off to its last fold); smaller ones are summed directly:
+    all kinds in one list, diagnostics against the oracle (and the clip norm
+    path)."""
     import adana_amd
 
     print("case: large tensor fold path star", star, flush=True)
     rng = np.random.default_rng(9)
-    sizes = [9_000_000, 5, 512 * 1024, 512 * 1024 + 1, 70_000]
+    sizes = [9_000_000, 5, 512 * 1024, 512 * 1024 + 1, 70_000, 4096 * 1024, 4096 * 1024 + 1, 3000 * 1024 + 7]
     params = [_normal(rng, (n,), 0.02) for n in sizes]
     pair = Pair(oracle_mod, star, [(params, {})], lr=1e-3, delta=8.0, kappa=0.85, clipsnr=2.0,
                 weight_decay=0.1, wd_decaying=True, wd_ts=10.0)
