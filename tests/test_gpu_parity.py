@@ -739,3 +739,49 @@ def test_permuted_parameters(oracle_mod, star):
     opt2 = (adana_amd.DANA_STAR_MK4 if star else adana_amd.ADana)([gapped], **hp)
     with pytest.raises(NotImplementedError, match="gaps"):
         opt2.step()
+
+
+def test_step_hooks_profiler_and_scheduler():
+    """step() keeps torch.optim.Optimizer's behaviour: per-optimizer and global
+    pre/post hooks run (a pre-hook may replace the arguments), the profiler
+    records the ``Optimizer.step#ADana.step`` range, an LR scheduler sees the
+    steps, and the update is the same as without any of them."""
+    import adana_amd
+    from torch.optim.optimizer import register_optimizer_step_post_hook, register_optimizer_step_pre_hook
+
+    print("case: step hooks, profiler, scheduler", flush=True)
+    torch.manual_seed(3)
+    ref = torch.nn.Parameter(torch.randn(5000, device=DEV) * 0.02)
+    hooked = torch.nn.Parameter(ref.detach().clone())
+    opt_ref = adana_amd.ADana([ref], lr=1e-3, kappa=0.85)
+    opt = adana_amd.ADana([hooked], lr=1e-3, kappa=0.85)
+    g = torch.randn(5000, device=DEV) * 1e-3
+    ref.grad, hooked.grad = g.clone(), g.clone()
+    opt_ref.step()                                                  # before any hook is registered
+    calls = []
+    h1 = opt.register_step_pre_hook(lambda o, a, k: calls.append(("pre", o is opt)))
+    h2 = opt.register_step_post_hook(lambda o, a, k: calls.append(("post", o is opt)))
+    h3 = register_optimizer_step_pre_hook(lambda o, a, k: calls.append(("gpre", o is opt)))
+    h4 = register_optimizer_step_post_hook(lambda o, a, k: calls.append(("gpost", o is opt)))
+    swapped = lambda: torch.tensor(7.0)                              # noqa: E731
+    h5 = opt.register_step_pre_hook(lambda o, a, k: ((o,), {"closure": swapped}))
+    loss = opt.step(closure=lambda: torch.tensor(1.0))
+    assert float(loss) == 7.0                                       # the pre-hook's closure ran
+    assert calls == [("gpre", True), ("pre", True), ("post", True), ("gpost", True)]
+    for h in (h1, h2, h3, h4, h5):
+        h.remove()
+    sched = torch.optim.lr_scheduler.LambdaLR(opt, lambda k: 1.0)
+    with torch.profiler.profile(activities=[torch.profiler.ProfilerActivity.CPU]) as prof:
+        ref.grad, hooked.grad = g.clone(), g.clone()
+        opt_ref.step()
+        opt.step()
+        sched.step()
+    assert any(e.name == "Optimizer.step#ADana.step" for e in prof.events())
+    assert sched.last_epoch == 1
+    for _ in range(2):
+        ref.grad, hooked.grad = g.clone(), g.clone()
+        opt_ref.step()
+        opt.step()
+    torch.cuda.synchronize()
+    assert torch.equal(ref, hooked)
+    assert opt.state[hooked]["step"] == opt_ref.state[ref]["step"] == 4
