@@ -58,11 +58,13 @@ __device__ __forceinline__ float sqrt_normal(float x) {
 }
 
 // Correctly rounded sqrt for every binary32 x: sqrt_normal on [2^-96, +inf]
-// (about 8 instructions against the IEEE sequence's 20), the IEEE sequence for
-// zeros, small and negative inputs and NaNs, behind a real branch.
+// and for +-0 (about 8 instructions against the IEEE sequence's 20), the IEEE
+// sequence for small nonzero and negative inputs and NaNs, behind a real
+// branch.  Zeros stay on the fast path: a second moment that never saw a
+// nonzero gradient (zero rows of an embedding) is 0 for whole waves.
 __device__ __forceinline__ float sqrt_f32(float x) {
     float s = sqrt_normal(x);
-    if (__builtin_expect(!(x >= 0x1p-96f), 0)) s = __builtin_sqrtf(opaque(x));
+    if (__builtin_expect(!(x >= 0x1p-96f || x == 0.0f), 0)) s = __builtin_sqrtf(opaque(x));
     return s;
 }
 
