@@ -1343,8 +1343,10 @@ size_t workspace_bytes(const adana_plan &pl) {
 // tensors of 64-65536 elements: 0.715 ms capped, 0.666 ms uncapped; the same
 // list at kappa = 1 prefers the cap, 0.658 against 0.748 ms).  bfloat16
 // state (PM_BF16) moves half the bytes per workgroup and runs best uncapped:
-// Dana-Star with the pow at 2.65B params, 14.25 ms at 4, 12.84-12.86 ms at 5,
-// 6, 8 and uncapped (its registers allow 5).  The cap is imposed with dynamic
+// Dana-Star at 2.65B params with the per-element pow, 14.25 ms at 4,
+// 12.84-12.86 ms at 5, 6, 8 and uncapped (its registers allow 5); with the
+// pow table (59 VGPRs), 12.25 / 10.82 / 10.29 / 10.04 ms at 4 / 5 / 6 / 7 and
+// 10.00 ms uncapped.  The cap is imposed with dynamic
 // LDS the kernel does not touch.
 template <bool STAR, int PM, int POWK>
 constexpr int residency_cap(bool small_tensors) {
