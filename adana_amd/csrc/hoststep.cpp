@@ -17,6 +17,7 @@
  */
 #include <torch/csrc/autograd/python_variable.h>
 #include <torch/csrc/autograd/variable.h>
+#include <ATen/ops/from_blob.h>
 
 #include <Python.h>
 
@@ -409,7 +410,61 @@ PyObject *grads_scan(PyObject *, PyObject *args) {
     return Py_BuildValue("NNNNO", out, absent, gp, pp, match ? Py_True : Py_False);
 }
 
+/* bind_diag(buf, states, columns) -> None
+ *
+ * For every state dict states[j] and (col, key) in ``columns``: states[j][key]
+ * = a new 0-d tensor over buf's element 5 * j + col, with a storage of its
+ * own that keeps buf's storage alive.  A diagnostic kept from one step is
+ * then not rewritten by the next (which writes a new buffer), and a deepcopy
+ * of one parameter's state copies only its own elements. */
+PyObject *bind_diag(PyObject *, PyObject *args) {
+    PyObject *bufobj, *states, *columns;
+    if (!PyArg_ParseTuple(args, "OO!O!", &bufobj, &PyList_Type, &states, &PyList_Type, &columns)) return nullptr;
+    if (!THPVariable_Check(bufobj)) {
+        PyErr_SetString(PyExc_TypeError, "bind_diag: buf must be a tensor");
+        return nullptr;
+    }
+    const Py_ssize_t n = PyList_GET_SIZE(states), nc = PyList_GET_SIZE(columns);
+    try {
+        const at::Tensor &buf = THPVariable_Unpack(bufobj);
+        if (!buf.is_contiguous() || buf.numel() < 5 * n) {
+            PyErr_SetString(PyExc_ValueError, "bind_diag: buffer too small or not contiguous");
+            return nullptr;
+        }
+        const c10::Storage keep = buf.storage();
+        const auto es = buf.element_size();
+        char *base = static_cast<char *>(buf.data_ptr());
+        const auto opts = buf.options();
+        for (Py_ssize_t j = 0; j < n; ++j) {
+            PyObject *st = PyList_GET_ITEM(states, j);
+            if (!PyDict_Check(st)) {
+                PyErr_SetString(PyExc_TypeError, "bind_diag: state entries must be dicts");
+                return nullptr;
+            }
+            for (Py_ssize_t c = 0; c < nc; ++c) {
+                PyObject *ck = PyList_GET_ITEM(columns, c);
+                long col;
+                PyObject *key;
+                if (!PyArg_ParseTuple(ck, "lO", &col, &key)) return nullptr;
+                at::Tensor t = at::from_blob(base + es * (5 * j + col), at::IntArrayRef{}, [keep](void *) {}, opts);
+                PyObject *w = THPVariable_Wrap(std::move(t));
+                if (!w) return nullptr;
+                const int rc = PyDict_SetItem(st, key, w);
+                Py_DECREF(w);
+                if (rc) return nullptr;
+            }
+        }
+    } catch (const std::exception &e) {
+        PyErr_SetString(PyExc_RuntimeError, e.what());
+        return nullptr;
+    }
+    Py_RETURN_NONE;
+}
+
 PyMethodDef methods[] = {
+    {"bind_diag", bind_diag, METH_VARARGS,
+     "bind_diag(buf, states, columns): states[j][key] = own-storage 0-d tensor over buf[5 * j + col] "
+     "for (col, key) in columns"},
     {"grads_scan", grads_scan, METH_VARARGS,
      "grads_scan(params, bf16) -> (grads, absent, grad_ptrs, param_ptrs, match): grads_of, data_ptrs of the "
      "gradients and of the parameters, and grads_match, in one pass"},

@@ -19,10 +19,14 @@ Python, makes six 0-d device tensors per tensor and calls a torch.compile'd
 update per tensor (src/optim/adana.py:184-225).  Here the host computes the
 per-step scalars once per (group, step) class in C, and a single
 multi-tensor HIP kernel (adana_amd/csrc/adana_mta.hip) updates every tensor
-and writes all diagnostics into one device buffer.  The diagnostic entries of
-the state are 0-d views of that buffer: they hold the latest step's values
-(the reference rebinds new tensors each step; here the same tensors are
-refreshed in place).
+and writes all diagnostics into one device buffer.  As in the reference
+(which binds new 0-d tensors each step), every step binds new diagnostic
+tensors, each with a storage of its own over a new buffer, so a diagnostic
+kept from one step keeps its value.  That costs about 2 us of host time per
+parameter, so for lists of more than 512 stepped tensors (10,000 small
+tensors, say, where it would exceed the device's step) the entries are
+instead bound once and refreshed in place; ``fresh_diagnostics`` (keyword-
+only, an extension) forces either.
 
 Gradient clipping (src/optim/base.py:250-257): ``opt.clip_grad_norm_(max_norm)``
 (or ``adana_amd.clip_grad_norm_(params, max_norm, optimizer=opt)``) returns
@@ -116,16 +120,19 @@ class _DanaFamily(Optimizer):
     _VARIANT = 0                                   # adana_mta_step variant flags
     _KEYS = ("m", "v", "tau")                      # state keys of the moments and tau
     _DIAG_COLUMNS = tuple(enumerate(DIAG_KEYS))    # (kernel output column, state key)
+    _FRESH_DIAG_MAX_TENSORS = 512                  # default limit of fresh diagnostics per step
 
-    def _engine_init(self, master_weights: bool) -> None:
+    def _engine_init(self, master_weights: bool, fresh_diagnostics: Optional[bool] = None) -> None:
         self.master_weights = bool(master_weights)
+        self.fresh_diagnostics = fresh_diagnostics
+        self._diag_cols = [tuple(c) for c in self._DIAG_COLUMNS]
         self._sets: Optional[List[_LaunchSet]] = None
         self._structure = None
         self._flat = None
         self._active = None
         self._pending_clip = None
         self._clip_plan_obj = None
-        self._diag_loc = {}        # param -> (diagnostics buffer, row) of its latest plan
+        self._diag_loc = {}        # param -> (launch set, row) of its latest plan
         self._diag_epoch = 0       # bumped whenever a plan or the state tensors change
         self._diag_cache = None
         _lib.lib()  # fail at construction, not at the first step, without the kernel library
@@ -381,14 +388,13 @@ class _DanaFamily(Optimizer):
                 # the reference's bfloat16 path keeps bfloat16 diagnostics
                 ls.diag = torch.full((len(ls.params), 5), float("nan"), device=ls.device,
                                      dtype=torch.bfloat16 if ls.flags & _lib.STATE_BF16 else torch.float32)
-            for j, (p, st) in enumerate(zip(ls.params, ls.states)):
-                # 0-d tensors over the kernel's output rows, each with a storage
-                # of its own: a deepcopy of one parameter's state (DynamicsLogger,
-                # src/logger/logger.py:93) then copies 4 bytes per diagnostic,
-                # not the whole list's buffer
-                for col, key in self._DIAG_COLUMNS:
-                    st[key] = _carve(ls.diag, 5 * j + col, ())
-                self._diag_loc[p] = (ls.diag, j)
+            # 0-d tensors over the kernel's output rows, each with a storage of
+            # its own: a deepcopy of one parameter's state (DynamicsLogger,
+            # src/logger/logger.py:93) then copies 4 bytes per diagnostic, not
+            # the whole list's buffer
+            _hoststep.bind_diag(ls.diag, ls.states, self._diag_cols)
+            for j, p in enumerate(ls.params):
+                self._diag_loc[p] = (ls, j)
         self._diag_epoch += 1
         return out
 
@@ -412,8 +418,8 @@ class _DanaFamily(Optimizer):
                 if not st or mark not in st:
                     continue
                 loc = self._diag_loc.get(p)
-                if loc is not None and st[mark].data_ptr() != (loc[0].data_ptr()
-                                                               + loc[0].element_size() * (5 * loc[1] + col0)):
+                if loc is not None and st[mark].data_ptr() != (loc[0].diag.data_ptr()
+                                                               + loc[0].diag.element_size() * (5 * loc[1] + col0)):
                     loc = None                     # state tensors replaced (e.g. load_state_dict)
                 if loc is None:
                     loose.append((len(params), st))
@@ -422,19 +428,19 @@ class _DanaFamily(Optimizer):
                     ent[1].append(loc[1])
                     ent[2].append(len(params))
                 params.append(p)
-            bufs = [(buf, np.asarray(rows, np.int64), np.asarray(pos, np.int64))
-                    for buf, rows, pos in by_buf.values()]
+            bufs = [(ls, np.asarray(rows, np.int64), np.asarray(pos, np.int64))
+                    for ls, rows, pos in by_buf.values()]
             cache = self._diag_cache = (key, params, bufs, loose)
         _, params, bufs, loose = cache
         host = []
-        for buf, _, _ in bufs:
-            h = torch.empty(buf.shape, dtype=buf.dtype, pin_memory=True)
-            h.copy_(buf, non_blocking=True)
+        for ls, _, _ in bufs:                      # each launch set's latest buffer
+            h = torch.empty(ls.diag.shape, dtype=ls.diag.dtype, pin_memory=True)
+            h.copy_(ls.diag, non_blocking=True)
             host.append(h)
-        for dev in {buf.device for buf, _, _ in bufs}:
+        for dev in {ls.diag.device for ls, _, _ in bufs}:
             torch.cuda.current_stream(dev).synchronize()
         out = np.empty((len(params), 5), dtype=np.float32)
-        for (buf, rows, pos), h in zip(bufs, host):
+        for (ls, rows, pos), h in zip(bufs, host):
             out[pos] = (h.float() if h.dtype == torch.bfloat16 else h).numpy()[rows]
         for pos, st in loose:                      # loaded, not yet stepped: read one by one
             out[pos] = np.nan
@@ -624,7 +630,14 @@ class _DanaFamily(Optimizer):
 
         scalars = self._scalars(classes)
         L = _lib.lib()
+        fresh = self.fresh_diagnostics
+        if fresh is None:
+            fresh = sum(len(ls.params) for ls in self._sets) <= self._FRESH_DIAG_MAX_TENSORS
         for ls in self._sets:
+            if fresh:
+                # a new buffer for this step's diagnostics (stream-ordered
+                # reuse by the caching allocator once nothing refers to it)
+                ls.diag = torch.empty_like(ls.diag)
             n_cls = min(_lib.MAX_CLASSES, len(classes) - ls.class_base)
             sc_arr = (type(scalars[0]) * n_cls)(*scalars[ls.class_base:ls.class_base + n_cls])
             with torch.cuda.device(ls.device):
@@ -641,6 +654,9 @@ class _DanaFamily(Optimizer):
                         ctypes.c_void_p(ls.workspace.data_ptr()), ls.workspace.numel(),
                         ctypes.c_void_p(ls.diag.data_ptr()), ctypes.c_void_p(stream)),
                         "adana_mta_step_scaled")
+        if fresh:
+            for ls in self._sets:                          # adana.py:221-225: new 0-d tensors
+                _hoststep.bind_diag(ls.diag, ls.states, self._diag_cols)
         _hoststep.bump_versions(params)                    # p was updated in place
         if wflag:
             _hoststep.bump_versions(grads)
@@ -702,7 +718,8 @@ class ADana(_DanaFamily):
     Same constructor, defaults, group keys and state keys as
     src/optim/adana.py:32-70; ``use_foreach`` is accepted and has no effect
     (there is one code path).  ``master_weights`` is an extension for
-    bfloat16 parameters (keyword-only).
+    bfloat16 parameters and ``fresh_diagnostics`` one for the diagnostics'
+    binding (both keyword-only; see the module docstring).
     """
 
     _STAR = False
@@ -711,7 +728,7 @@ class ADana(_DanaFamily):
                  kappa: float = 1.0, epsilon: float = 1e-8, weight_decay: float = 0.0,
                  clipsnr: float = None, wd_decaying: bool = False, wd_ts: float = 1.0,
                  gamma_3_factor: float = 1.0, use_foreach: bool = False, *,
-                 master_weights: bool = False):
+                 master_weights: bool = False, fresh_diagnostics: Optional[bool] = None):
         defaults = dict(lr=lr, delta=delta, epsilon=epsilon, weight_decay=weight_decay,
                         weighted_step_count=0)
         self.lr = lr
@@ -725,7 +742,7 @@ class ADana(_DanaFamily):
         self.gamma_3_factor = gamma_3_factor
         self.use_foreach = use_foreach
         super().__init__(params, defaults)
-        self._engine_init(master_weights)
+        self._engine_init(master_weights, fresh_diagnostics)
 
 
 class DANA_STAR_MK4(_DanaFamily):
@@ -743,7 +760,7 @@ class DANA_STAR_MK4(_DanaFamily):
                  epsilon: float = 1e-8, weight_decay: float = 0.0, clipsnr: float = 1.0,
                  weight_time: bool = False, wd_decaying: bool = False, wd_ts: float = 1.0,
                  gamma_3_factor: float = 1.0, use_foreach: bool = False, *,
-                 master_weights: bool = False):
+                 master_weights: bool = False, fresh_diagnostics: Optional[bool] = None):
         assert mk4A == 0.0, f"mk4A must be 0.0, got {mk4A}"
         assert mk4B == 0.0, f"mk4B must be 0.0, got {mk4B}"
         assert weight_time == False, f"weight_time must be False, got {weight_time}"  # noqa: E712
@@ -763,4 +780,4 @@ class DANA_STAR_MK4(_DanaFamily):
         self.gamma_3_factor = gamma_3_factor
         self.use_foreach = use_foreach
         super().__init__(params, defaults)
-        self._engine_init(master_weights)
+        self._engine_init(master_weights, fresh_diagnostics)

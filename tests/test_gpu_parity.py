@@ -785,3 +785,42 @@ def test_step_hooks_profiler_and_scheduler():
     torch.cuda.synchronize()
     assert torch.equal(ref, hooked)
     assert opt.state[hooked]["step"] == opt_ref.state[ref]["step"] == 4
+
+
+@pytest.mark.parametrize("fresh", [None, False])
+def test_diagnostics_fresh_each_step(fresh):
+    """As the reference binds new 0-d tensors each step (src/optim/adana.py:
+    221-225), a diagnostic kept from one step keeps its value after the next
+    (the default for lists of up to 512 tensors); each has a storage of its
+    own (a deepcopy copies 4 bytes); the packed read-out and .item() agree.
+    With fresh_diagnostics=False the entries are bound once and refreshed in
+    place."""
+    import copy
+
+    import adana_amd
+
+    print("case: fresh diagnostics", fresh, flush=True)
+    torch.manual_seed(8)
+    ps = [torch.nn.Parameter(torch.randn(n, device=DEV) * 0.02) for n in (3000, 70_000)]
+    opt = adana_amd.DANA_STAR_MK4(ps, lr=1e-3, kappa=0.85, clipsnr=2.0, fresh_diagnostics=fresh)
+    for p in ps:
+        p.grad = torch.randn_like(p) * 1e-3
+    opt.step()
+    kept = opt.state[ps[1]]["gradient_norm"]
+    first = float(kept)
+    assert kept.untyped_storage().nbytes() == 4
+    assert copy.deepcopy(opt.state[ps[1]])["m_norm"].untyped_storage().nbytes() == 4
+    for p in ps:
+        p.grad = torch.randn_like(p) * 5e-3
+    opt.step()
+    now = opt.state[ps[1]]["gradient_norm"]
+    want = float(torch.linalg.vector_norm(ps[1].grad.double()))
+    assert float(now) == pytest.approx(want, rel=1e-5)
+    if fresh is None:
+        assert now is not kept and float(kept) == first             # the kept tensor holds step 1's value
+    else:
+        assert now is kept and float(kept) == float(now)            # one tensor, refreshed in place
+    params, vals = opt.diagnostics_host()
+    for p, row in zip(params, vals):
+        st = opt.state[p]
+        assert list(row) == pytest.approx([float(st[k]) for k in adana_amd.optim.DIAG_KEYS], rel=0, nan_ok=True)
