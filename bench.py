@@ -432,10 +432,16 @@ def stream_sweep(args):
         CU and uncapped;
       * the wave-specialised persistent kernel (loader wave + direct-to-LDS
         ring; stages, compute waves, workgroups per CU);
-      * the same five arrays read only and four written only, and a copy.
+      * the same five arrays read only and four written only, and a copy;
+      * then (after the separate arrays are freed) the one-shot shape at the
+        step's cap of 4 with the five arrays placed in one allocation,
+        ``k * (n + 4 Mi)`` floats plus ``k * skew`` bytes from its start
+        (array k = 0..4): the rate's dependence on the arrays' relative
+        placement, which the caller's allocator decides for p and g.
     Each configuration is launched 1 + reps times (one warm-up), in two
     rounds; the JSON line lists the launch order and each configuration's
-    best median."""
+    best median.  ``value`` is the best 5-read/4-write rate over separately
+    allocated arrays (the placement leg is reported beside it)."""
     import ctypes
 
     import torch
@@ -475,24 +481,43 @@ def stream_sweep(args):
     reps = max(2, args.steps)
     best = {}
     order = []
-    for rnd in range(2):
-        for name, nbytes, fn in cfgs:
-            print(f"[bench] stream_sweep round {rnd}: {name}", file=sys.stderr, flush=True)
-            ev = [torch.cuda.Event(enable_timing=True) for _ in range(reps + 1)]
+
+    def one(rnd, name, nbytes, fn):
+        print(f"[bench] stream_sweep round {rnd}: {name}", file=sys.stderr, flush=True)
+        ev = [torch.cuda.Event(enable_timing=True) for _ in range(reps + 1)]
+        if fn() != 0:
+            raise RuntimeError(f"probe launch failed: {name}")
+        stream = torch.cuda.current_stream()
+        for k in range(reps):
+            ev[k].record(stream)
             if fn() != 0:
                 raise RuntimeError(f"probe launch failed: {name}")
-            stream = torch.cuda.current_stream()
-            for k in range(reps):
-                ev[k].record(stream)
-                if fn() != 0:
-                    raise RuntimeError(f"probe launch failed: {name}")
-            ev[-1].record(stream)
-            torch.cuda.synchronize()
-            order.append([name, 1 + reps])
-            ms = float(np.median([ev[k].elapsed_time(ev[k + 1]) for k in range(reps)]))
-            tbs = nbytes / (ms * 1e-3) / 1e12
-            if name not in best or tbs > best[name]["TB/s"]:
-                best[name] = {"TB/s": round(tbs, 3), "ms": round(ms, 3), "frac": round(tbs * 1e3 / HBM_PEAK_GBS, 4)}
+        ev[-1].record(stream)
+        torch.cuda.synchronize()
+        order.append([name, 1 + reps])
+        ms = float(np.median([ev[k].elapsed_time(ev[k + 1]) for k in range(reps)]))
+        tbs = nbytes / (ms * 1e-3) / 1e12
+        if name not in best or tbs > best[name]["TB/s"]:
+            best[name] = {"TB/s": round(tbs, 3), "ms": round(ms, 3), "frac": round(tbs * 1e3 / HBM_PEAK_GBS, 4)}
+
+    def sweep(cfgs):
+        for rnd in range(2):
+            for name, nbytes, fn in cfgs:
+                one(rnd, name, nbytes, fn)
+
+    sweep(cfgs)
+    # placement leg: one allocation, array k at k * (n + 4 Mi) floats + k * skew bytes
+    del arrays, ptrs, a0, a1, cfgs
+    torch.cuda.empty_cache()
+    slot = n + (4 << 20)
+    buf = torch.zeros(5 * slot, device="cuda:0")
+    place = []
+    for skew in (0, 4096, 8192, 1 << 20, (2 << 20) + 8192):
+        pp = (ctypes.c_void_p * 5)(*[buf.data_ptr() + 4 * k * slot + k * skew for k in range(5)])
+        place.append((f"placement: one allocation, skew {skew} B per array, cap 4", 36 * n,
+                      lambda pp=pp: lib.adana_probe_stream_5r4w(pp, n, part, 4, st)))
+    sweep(place)
+    del buf
     top = max((v["TB/s"], k) for k, v in best.items() if k.startswith("5r4w"))
     print(json.dumps({"metric": "5-read/4-write stream ceiling at the north-star size (TB/s)", "value": top[0],
                       "unit": "TB/s", "n_gpus": 1, "steps": reps, "warmup": 1, "ms_per_step": best[top[1]]["ms"],
