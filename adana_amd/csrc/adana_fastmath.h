@@ -27,6 +27,17 @@ __device__ __forceinline__ float opaque(float x) {
     return y;
 }
 
+// A class mask for v_cmp_class_f32, held in an SGPR.  With a constant mask the
+// compiler picks the VOPC form, whose mask operand must be a VGPR, and writes
+// the literal into a VGPR before every test (gfx9's VOP3 encodings take no
+// literal); from an SGPR the VOP3 form reads it directly, one VALU instruction
+// per test instead of two.
+__device__ __forceinline__ int class_mask(int m) {
+    int r;
+    asm("s_mov_b32 %0, %1" : "=s"(r) : "i"(m));
+    return r;
+}
+
 // Correctly rounded a / b for operands on which the IEEE division sequence's
 // range scaling (v_div_scale) and special-case fixup (v_div_fixup) are
 // identities: b normal in [0.5, 1], and a either normal or b == 1.  This is the
@@ -86,6 +97,14 @@ __device__ __forceinline__ float bf16_round(float f) {
     const f32x2_t v = {0.0f, f};
     return __builtin_bit_cast(float, __builtin_convertvector(v, bf16x2_t));
 }
+// The same rounding in integer arithmetic, for host code and for values
+// that are the same for every lane (the launch's scalars, rounded once on
+// the host): round to nearest even, a NaN quieted as above.
+__host__ __device__ inline float bf16_round_int(float f) {
+    const unsigned int u = __builtin_bit_cast(unsigned int, f);
+    const unsigned int r = (u & 0x7fffffffu) > 0x7f800000u ? (u | 0x00400000u) : u + 0x7fffu + ((u >> 16) & 1u);
+    return __builtin_bit_cast(float, r & 0xffff0000u);
+}
 // bf16(lo) | bf16(hi) << 16: two values' bits in one 32-bit word.
 __device__ __forceinline__ unsigned int bf16_pack2(float lo, float hi) {
     const f32x2_t v = {lo, hi};
@@ -105,7 +124,8 @@ __device__ __forceinline__ unsigned int bf16_pack2(float lo, float hi) {
 __device__ __forceinline__ float div_bf16(float a, float b) {
     const float y = __builtin_amdgcn_rcpf(b);
     float q = a * y;
-    const bool fast = __builtin_amdgcn_classf(q, kClassNormal | kClassZero) && __builtin_amdgcn_classf(y, kClassNormal);
+    const bool fast = __builtin_amdgcn_classf(q, class_mask(kClassNormal | kClassZero)) &&
+                      __builtin_amdgcn_classf(y, class_mask(kClassNormal));
     if (__builtin_expect(!fast, 0)) q = opaque(a) / b;
     return q;
 }
@@ -118,7 +138,8 @@ __device__ __forceinline__ float div_bf16(float a, float b) {
 // inputs (subnormals, negatives, infinities) and NaNs take the IEEE sequence.
 __device__ __forceinline__ float sqrt_bf16(float x) {
     float s = __builtin_amdgcn_sqrtf(x);
-    if (__builtin_expect(!__builtin_amdgcn_classf(x, kClassPosNormal | kClassZero), 0)) s = __builtin_sqrtf(opaque(x));
+    if (__builtin_expect(!__builtin_amdgcn_classf(x, class_mask(kClassPosNormal | kClassZero)), 0))
+        s = __builtin_sqrtf(opaque(x));
     return s;
 }
 

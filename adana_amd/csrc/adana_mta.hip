@@ -58,12 +58,36 @@ static_assert(sizeof(adana_tensor_desc) == 64, "descriptor layout");
 static_assert(sizeof(adana_step_scalars) == 64, "scalar layout");
 static_assert(sizeof(adana_manau_scalars) == sizeof(adana_step_scalars), "Manau scalars share the slot");
 
+// A class's binary32 scalars as the bfloat16 ops see them (the reference's
+// bfloat16 path, ADANA_STATE_BF16).  Computed once per launch on the host
+// (ScalarPack::c16) and by pow16_fill_kernel; bf16_round_int is the
+// conversion instruction's rounding in integer arithmetic.
+struct Scalars16 {
+    float a16, lerp_coef16, eps16, pw16, min_p16, clip16, c3_16, cg2_16, e16;
+    int32_t lerp_small16;
+};
+__host__ __device__ inline Scalars16 scalars16(const adana_step_scalars &sc) {
+    Scalars16 q;
+    q.a16 = adana::bf16_round_int(sc.a);
+    q.lerp_small16 = fabsf(q.a16) < 0.5f;
+    q.lerp_coef16 = q.lerp_small16 ? q.a16 : q.a16 - 1.0f;
+    q.eps16 = adana::bf16_round_int(sc.eps);
+    q.pw16 = adana::bf16_round_int(sc.pw);
+    q.min_p16 = adana::bf16_round_int(sc.min_p);
+    q.clip16 = adana::bf16_round_int(sc.clip);
+    q.c3_16 = adana::bf16_round_int(sc.c3);
+    q.cg2_16 = adana::bf16_round_int(sc.cg2);
+    q.e16 = adana::bf16_round_int(sc.star_exp);
+    return q;
+}
+
 struct ScalarPack {
     adana_step_scalars c[ADANA_MAX_CLASSES];
     const float *gscale;          // device pointer to the clip coefficient, or NULL
     int32_t write_grad;           // store the scaled gradient back (ADANA_WRITE_GRAD)
     int32_t reserved;
     const unsigned short *pow16;  // POW_TABLE16: the launch's pow table in the workspace
+    Scalars16 c16[ADANA_MAX_CLASSES];   // ADANA_STATE_BF16: scalars16(c[k])
 };
 
 // ---------------------------------------------------------------------------
@@ -245,25 +269,6 @@ __device__ __forceinline__ float rb(float x) { return bf16_round(x); }
 // POW_TABLE16: one entry per bfloat16 value in [1, +inf] (bits 0x3F80 .. 0x7F80).
 constexpr unsigned int kPow16Entries = 0x7F80u - 0x3F80u + 1u;
 
-// The launch's binary32 scalars as the bfloat16 ops see them.
-struct Scalars16 {
-    float a16, lerp_coef16, eps16, pw16, min_p16, clip16, c3_16, cg2_16, e16;
-    bool lerp_small16;
-};
-__device__ __forceinline__ Scalars16 scalars16(const adana_step_scalars &sc) {
-    Scalars16 q;
-    q.a16 = rb(sc.a);
-    q.lerp_small16 = fabsf(q.a16) < 0.5f;
-    q.lerp_coef16 = q.lerp_small16 ? q.a16 : q.a16 - 1.0f;
-    q.eps16 = rb(sc.eps);
-    q.pw16 = rb(sc.pw);
-    q.min_p16 = rb(sc.min_p);
-    q.clip16 = rb(sc.clip);
-    q.c3_16 = rb(sc.c3);
-    q.cg2_16 = rb(sc.cg2);
-    q.e16 = rb(sc.star_exp);
-    return q;
-}
 
 // src/optim/adana.py:101-143 on bfloat16 tensors
 __device__ __forceinline__ float adana_elem16(float p, float g, float &m, float &v, const adana_step_scalars &sc,
@@ -280,7 +285,7 @@ __device__ __forceinline__ float adana_elem16(float p, float g, float &m, float 
     const float g3t = rb(q.c3_16 * inner);
     const float g2t = rb(rb(q.cg2_16 * g) * nt);                                        // :129
     float pn = rb(p + rb(g2t + g3t));                                                   // :132-135
-    pn = rb(pn * sc.opw);                                                               // :143
+    pn = pn * sc.opw;           // :143, rounded to bfloat16 by the store (the same RNE)
     m = mn;
     v = vn;
     accumulate(acc, af, g, mfac, mn);
@@ -317,7 +322,7 @@ __device__ __forceinline__ float star16_phase_b(float p, float g, const StarMid 
     const float g3t = rb(q.c3_16 * inner);
     const float g2t = rb(rb(q.cg2_16 * g) * nt);                                        // :180
     float pn = rb(p + rb(g2t + g3t));                                                   // :183-186
-    pn = rb(pn * sc.opw);                                                               // :195
+    pn = pn * sc.opw;           // :195, rounded to bfloat16 by the store (the same RNE)
     accumulate(acc, af, g, mfac, a.m);
     return pn;
 }
@@ -332,8 +337,12 @@ __device__ __forceinline__ float pow16(float x, const adana_step_scalars &sc, co
         // entry (bits >> 16) - 0x3F80 of the table pow16_fill_kernel wrote
         // with the POW_GENERAL code below, so the same bits.  A NaN gives
         // itself, quieted, as that code does.
+        // Branch-free (the load reads entry 0 for a NaN), so a thread's
+        // lookups are in flight together.
         const unsigned int idx = (__float_as_uint(x) >> 16) - 0x3F80u;
-        return idx < kPow16Entries ? bf16_to_f32(tab.pow16[idx]) : rb(x);
+        const bool in = idx < kPow16Entries;
+        const float t = bf16_to_f32(tab.pow16[in ? idx : 0u]);
+        return in ? t : rb(x);
     } else if constexpr (POWK == POW_GENERAL) {
         return rb(adana::pow_f32_unit_exp_tab(x, q.e16, tab.log, tab.exp2j));
     } else if constexpr (POWK == POW_ONE) {
@@ -366,9 +375,8 @@ __global__ __launch_bounds__(256) void pow16_fill_kernel(unsigned short *__restr
 
 template <bool STAR, int POWK, int N>
 __device__ __forceinline__ void update_n16(float (&P)[N], const float (&G)[N], float (&M)[N], float (&V)[N],
-                                           float (&T)[N], const adana_step_scalars &sc, const PowTab &tab,
-                                           float (&acc)[4]) {
-    const Scalars16 q = scalars16(sc);
+                                           float (&T)[N], const adana_step_scalars &sc, const Scalars16 &q,
+                                           const PowTab &tab, float (&acc)[4]) {
     if constexpr (!STAR) {
 #pragma unroll
         for (int k = 0; k < N; ++k) P[k] = adana_elem16(P[k], G[k], M[k], V[k], sc, q, acc);
@@ -682,6 +690,7 @@ __device__ __forceinline__ void thread_elems(const adana_tensor_desc &d, int64_t
     const bool scaled = pack.gscale != nullptr;                    // uniform
     const int cnt = left < VEC ? static_cast<int>(left) : VEC;
     if constexpr (PM == PM_BF16) {
+        const Scalars16 &q = pack.c16[d.sclass];
         unsigned short *pp = static_cast<unsigned short *>(d.param) + off;
         unsigned short *mp = reinterpret_cast<unsigned short *>(d.m) + off;
         unsigned short *vp = reinterpret_cast<unsigned short *>(d.v) + off;
@@ -703,7 +712,7 @@ __device__ __forceinline__ void thread_elems(const adana_tensor_desc &d, int64_t
                 for (int k = 0; k < VEC; ++k) G[k] = scale_grad<true>(G[k], gs);
                 if (pack.write_grad) store_grad_n<true, VEC>(d.grad, off, G);
             }
-            update_n16<STAR, POWK, VEC>(P, G, M, V, T, sc, tab, acc);
+            update_n16<STAR, POWK, VEC>(P, G, M, V, T, sc, q, tab, acc);
             st_bf16_n<VEC>(pp, P);
             st_bf16_n<VEC>(mp, M);
             st_bf16_n<VEC>(vp, V);
@@ -717,7 +726,7 @@ __device__ __forceinline__ void thread_elems(const adana_tensor_desc &d, int64_t
                     G[0] = scale_grad<true>(G[0], gs);
                     if (pack.write_grad) store_grad1<true>(d.grad, off + e, G[0]);
                 }
-                update_n16<STAR, POWK, 1>(P, G, M, V, T, sc, tab, acc);
+                update_n16<STAR, POWK, 1>(P, G, M, V, T, sc, q, tab, acc);
                 pp[e] = f32_to_bf16(P[0]);
                 mp[e] = f32_to_bf16(M[0]);
                 vp[e] = f32_to_bf16(V[0]);
@@ -1652,6 +1661,8 @@ int step_impl(const char *fn, const adana_plan *plan, const adana_step_scalars *
     memcpy(pack.c, h_scalars, sizeof(adana_step_scalars) * static_cast<size_t>(n_classes));
     pack.gscale = d_grad_scale;
     pack.write_grad = (variant_flags & ADANA_WRITE_GRAD) ? 1 : 0;
+    if (variant_flags & ADANA_STATE_BF16)
+        for (int k = 0; k < n_classes; ++k) pack.c16[k] = scalars16(pack.c[k]);
     hipStream_t st = static_cast<hipStream_t>(stream);
     float *partials = static_cast<float *>(d_workspace);
     double4 *folds = reinterpret_cast<double4 *>(static_cast<char *>(d_workspace) + folds_offset(pl));

@@ -6,8 +6,8 @@
 //   which = 1: sqrt_normal(x) vs sqrtf(x) for the patterns [lo, hi]
 //   which = 2: bf16_bits(x) (the conversion instruction) vs round-to-nearest-
 //              even in integer arithmetic, NaN -> (bits >> 16) | 0x40, for the
-//              binary32 patterns [lo, hi]; bf16_round(x) and bf16_pack2(x, x)
-//              hold the same bits
+//              binary32 patterns [lo, hi]; bf16_round(x), bf16_pack2(x, x)
+//              and bf16_round_int(x) hold the same bits
 //   which = 3: bf16_round(div_bf16(a, b)) vs bf16_round(a / b) for the pairs
 //              pattern = (a's bfloat16 bits << 16) | b's bits in [lo, hi]
 //   which = 4: bf16_round(sqrt_bf16(x)) vs bf16_round(sqrtf(x)) for the
@@ -36,7 +36,8 @@ __global__ void check_kernel(int which, uint32_t lo, uint64_t count, unsigned lo
             const uint32_t h = adana::bf16_bits(x);
             const uint32_t hr = __float_as_uint(adana::bf16_round(x));          // (0, x) pair form
             const uint32_t hp = adana::bf16_pack2(x, x);                        // packed pair form
-            if (hr != (h << 16) || hp != (h | (h << 16))) {
+            const uint32_t hi = __float_as_uint(adana::bf16_round_int(x));      // integer form
+            if (hr != (h << 16) || hp != (h | (h << 16)) || hi != hr) {
                 atomicAdd(&out[0], 1ull);
                 atomicMin(&out[1], static_cast<unsigned long long>(bits));
                 continue;

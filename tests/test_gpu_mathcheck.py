@@ -53,7 +53,8 @@ def test_sqrt_normal_exhaustive():
 
 def test_bf16_conversion_is_rne_on_every_binary32():
     """gfx950's conversion instruction (v_cvt_pk_bf16_f32) over all 2^32
-    binary32 patterns: round-to-nearest-even, NaN -> (bits >> 16) | 0x40."""
+    binary32 patterns: round-to-nearest-even, NaN -> (bits >> 16) | 0x40; the
+    integer form bf16_round_int (the launch's bf16 scalars) gives the same bits."""
     print("case: bf16 conversion exhaustive", flush=True)
     bad, first = _run(2, 0, 0xFFFFFFFF)
     assert bad == 0, f"{bad} mismatches, first pattern {first:#010x}"
