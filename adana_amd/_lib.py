@@ -16,11 +16,11 @@ import numpy as np
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libadana_mta.so")
 
-ABI_VERSION = 5
+ABI_VERSION = 6
 CHUNK_ELEMS = 1024
 ALIGN_ELEMS = 4
 MAX_CLASSES = 8
-FOLD_CHUNKS = 2048
+FOLD_CHUNKS = 512
 DIRECT_CHUNKS = 512
 
 VARIANT_STAR = 0x1

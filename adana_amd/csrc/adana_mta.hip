@@ -911,6 +911,7 @@ __global__ __launch_bounds__(kBlock) void chunk_index_kernel(const int64_t *__re
 constexpr int kFold = ADANA_FOLD_CHUNKS;
 constexpr int kFoldPerThread = kFold / kBlock;
 static_assert(kFold % kBlock == 0, "fold workgroups cover whole thread rows");
+static_assert(kFold <= ADANA_DIRECT_CHUNKS, "a folded tensor (more than ADANA_DIRECT_CHUNKS chunks) has two folds or more");
 
 // Chunk range [lo, hi] of fold j, tensor i's (fold_first[i] <= j < fold_first[i + 1]).
 __device__ __forceinline__ void fold_range(int64_t j, int f0, int64_t b0, int64_t b1, int64_t &lo, int64_t &hi) {
@@ -1037,10 +1038,6 @@ __global__ __launch_bounds__(kBlock) void combine_kernel(const adana_tensor_desc
             s0 += q[u].x; s1 += q[u].y; s2 += q[u].z; s3 += q[u].w;
         }
         block_sum4(s0, s1, s2, s3, red);
-        if (f1 - f0 == 1) {               // the tensor's only fold: its diagnostics, no handoff
-            if (threadIdx.x == 0) write_diag(diag, diag_bf16, i, static_cast<double>(numel), s0, s1, s2, s3);
-            return;
-        }
         if (mode != kCombineFenced) {
             if (threadIdx.x == 0) folds[j] = make_double4(s0, s1, s2, s3);
             return;
@@ -1065,7 +1062,7 @@ __global__ __launch_bounds__(kBlock) void combine_kernel(const adana_tensor_desc
     if (i >= n) return;                                                   // whole wave
     const int nf = fold_first[i + 1] - fold_first[i];
     if (mode == kCombineFinalizeFolded) {
-        if (nf > 1) finalize_folds(folds, fold_first[i], fold_first[i + 1], lane, diag, diag_bf16, i, desc[i].numel);
+        if (nf > 0) finalize_folds(folds, fold_first[i], fold_first[i + 1], lane, diag, diag_bf16, i, desc[i].numel);
         return;
     }
     if (nf > 0) return;

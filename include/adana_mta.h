@@ -67,7 +67,7 @@
 extern "C" {
 #endif
 
-#define ADANA_ABI_VERSION 5
+#define ADANA_ABI_VERSION 6
 
 /* Elements per work chunk (one 256-thread workgroup, one 16-byte vector per
  * thread per array).  Tensors start at multiples of ADANA_ALIGN_ELEMS in the
@@ -80,8 +80,9 @@ extern "C" {
 #define ADANA_MAX_CLASSES 8
 /* Chunk partials one fold workgroup of the diagnostics combine reduces.
  * Tensors of at most ADANA_DIRECT_CHUNKS chunks get no fold workgroups: the
- * finalize step sums their chunk partials directly. */
-#define ADANA_FOLD_CHUNKS 2048
+ * finalize step sums their chunk partials directly; a larger tensor has two
+ * folds or more. */
+#define ADANA_FOLD_CHUNKS 512
 #define ADANA_DIRECT_CHUNKS 512
 
 /* variant_flags of adana_mta_step */

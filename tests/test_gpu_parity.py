@@ -500,10 +500,10 @@ def test_drift_over_1000_steps(oracle_mod, star):
 @pytest.mark.parametrize("star", [False, True])
 def test_large_tensor_fold_path(oracle_mod, star):
     """Tensors of more than ADANA_DIRECT_CHUNKS chunks go through the fold
-    workgroups (a tensor with a single fold finalizes itself, one with
-    several hands off to its last fold); smaller ones are summed directly:
-    all kinds in one list, diagnostics against the oracle (and the clip norm
-    path)."""
+    workgroups (two folds or more; the last to finish finalizes the tensor,
+    and 512 * 1024 + 1 elements leave a fold of one chunk); smaller ones are
+    summed directly: all kinds in one list, diagnostics against the oracle
+    (and the clip norm path)."""
     import adana_amd
 
     print("case: large tensor fold path star", star, flush=True)
