@@ -107,7 +107,8 @@ EXPORTS = (
     "adana_abi_version", "adana_last_error", "adana_step_scalars_init", "adana_manau_scalars_init",
     "adana_plan_layout", "adana_plan_index", "adana_workspace_bytes", "adana_mta_step",
     "adana_mta_step_scaled", "adana_grad_clip_norm", "adana_grad_scale",
-    "adana_order_stats_workspace", "adana_order_stats", "adana_mta_step_noalloc",
+    "adana_order_stats_workspace", "adana_order_stats_workspace_compact", "adana_order_stats",
+    "adana_mta_step_noalloc",
 )
 NOALLOC_SCRATCH_BYTES = 64 << 20
 
@@ -150,6 +151,8 @@ def _declare(L) -> None:
     L.adana_grad_scale.restype = ctypes.c_int
     L.adana_order_stats_workspace.argtypes = [i32, i64]
     L.adana_order_stats_workspace.restype = ctypes.c_size_t
+    L.adana_order_stats_workspace_compact.argtypes = [P, P, i32]
+    L.adana_order_stats_workspace_compact.restype = ctypes.c_size_t
     L.adana_order_stats.argtypes = [P, P, i32, P, P, P, P, ctypes.c_size_t, P]
     L.adana_order_stats.restype = ctypes.c_int
 

@@ -24,7 +24,11 @@
 //     prefixes are active and smaller when many are, so that the histograms
 //     always fit in LDS.
 // Exact (integer counting), deterministic results; no sort scratch.  Traffic:
-// 4 bytes per element per pass, 4 to 8 passes.
+// 4 bytes per element per pass, 4 to 8 passes -- except that once few of a
+// tensor's values still match its active prefixes (the last walk's counts
+// tell the host how many), one pass also copies the matching values into a
+// per-tile region and the later passes read only those (compaction; needs
+// the larger workspace of adana_order_stats_workspace_compact).
 //
 // The cuckoo hash: table k (k = 0, 1) holds 2^b entries {prefix, slot} and a
 // prefix p lives at (p * mul_k) >> (32 - b) in one of the two tables; an
@@ -52,8 +56,21 @@ constexpr int kLdsBudget = 28 * 1024;
 // Width-1 histograms of a tensor with very many active prefixes may use up to
 // this much (with at most 16 KB of tables: 64 KB in all).
 constexpr int kLdsMaxHist = 48 * 1024;
+// Dynamic LDS of one workgroup at most: 64 KB less room for the kernel's own
+// static words (the compaction's row count and overflow flag).
+constexpr int kLdsMaxDynamic = 64 * 1024 - 256;
 constexpr int kHashMinSlots = 4;                  // fewer active prefixes: binary search
 constexpr uint32_t kEmpty = 0xffffffffu;
+// Compaction: each thread of a tile may keep up to kCompactRows of its 256
+// values (row r of the tile's region holds every thread's r-th value, so the
+// rows read back coalesced); a tensor is compacted in the first pass whose
+// matching values are at most 1 / kCompactDen of its elements, half of the
+// region's capacity, so that few threads overflow.  A tile with an overflowing
+// thread is read whole in the later passes.
+constexpr int kCompactRows = 32;
+constexpr int64_t kCompactDen = 16;
+constexpr uint32_t kTileOverflow = 0x80000000u;
+enum TensorMode : int32_t { kReadTensor = 0, kReadAndCompact = 1, kReadCompact = 2 };
 
 typedef float F4 __attribute__((ext_vector_type(4)));
 #define GLOBAL_AS __attribute__((address_space(1)))
@@ -80,6 +97,10 @@ struct PassArgs {
     const HashInfo *hinfo;        // device, per tensor
     const uint2 *table;           // device, the tensors' cuckoo tables ({prefix, slot} entries)
     uint32_t *hist;               // device, [slot][bin] counts
+    const int32_t *tmode;         // device, per tensor: TensorMode of this pass
+    uint32_t *region;             // device, per tile: kCompactRows rows of kThreads values (compaction)
+    uint8_t *rcount;              // device, per tile: each thread's values in the region
+    uint32_t *tmeta;              // device, per tile: rows used, or kTileOverflow
     int32_t n;
     int32_t known_bits;           // key bits already resolved (prefix width)
     int32_t width;                // bits resolved by this pass
@@ -87,6 +108,7 @@ struct PassArgs {
 
 __global__ __launch_bounds__(kThreads) void select_hist_kernel(PassArgs a) {
     extern __shared__ uint32_t lds[];
+    __shared__ uint32_t s_rows, s_overflow;             // compaction: the tile's rows used, any overflow
     const int64_t wg = blockIdx.x;
     int l = 0, r = a.n - 1;                             // last tensor with tile_first <= wg
     while (l < r) {
@@ -103,16 +125,37 @@ __global__ __launch_bounds__(kThreads) void select_hist_kernel(PassArgs a) {
     uint2 *tab = reinterpret_cast<uint2 *>(lds + ((ns * bins + ns + 1) & ~1));   // [2][2^hb], 8-byte aligned
     const HashInfo hi = a.hinfo[t];
     const int hb = a.known_bits > 0 ? hi.bits : 0;
+    const int mode = a.tmode[t];                         // uniform: TensorMode
     for (int i = threadIdx.x; i < ns * bins; i += kThreads) h[i] = 0;
     for (int i = threadIdx.x; i < ns; i += kThreads) pre[i] = a.prefix[s0 + i];
     if (hb > 0)
         for (int i = threadIdx.x; i < (2 << hb); i += kThreads) tab[i] = a.table[hi.first + i];
+    if (threadIdx.x == 0) {
+        s_rows = 0;
+        s_overflow = 0;
+    }
     __syncthreads();
     // slot of prefix p in the cuckoo tables, or -1 when p is not active
     auto hashed_slot = [&](uint32_t p) -> int {
         const uint2 u = tab[(p * hi.mul[0]) >> (32 - hb)];
         const uint2 w = tab[(1 << hb) + ((p * hi.mul[1]) >> (32 - hb))];
         return u.x == p ? static_cast<int>(u.y) : (w.x == p ? static_cast<int>(w.y) : -1);
+    };
+    // Slot search: the last slot whose prefix is <= p (power-of-two steps
+    // from the largest below ns); the value counts if that slot's prefix is p.
+    int top = 1;
+    while (top * 2 < ns) top *= 2;
+    // slot of a key's prefix among the active ones, or -1 (one value at a time)
+    auto slot_of = [&](uint32_t key) -> int {
+        if (a.known_bits == 0) return 0;
+        const uint32_t pk = key >> (32 - a.known_bits);
+        if (hb > 0) return hashed_slot(pk);
+        int sl = 0;
+        for (int step = top; step > 0; step >>= 1) {
+            const int c = sl + step;
+            if (c < ns && pre[c] <= pk) sl = c;
+        }
+        return pre[sl] == pk ? sl : -1;
     };
 
     const float *x = a.tensor[t];
@@ -135,18 +178,40 @@ __global__ __launch_bounds__(kThreads) void select_hist_kernel(PassArgs a) {
             run_len = 1;
         }
     };
-    // Slot search: the last slot whose prefix is <= p (power-of-two steps
-    // from the largest below ns), run for a batch of values in lock-step so
-    // that their LDS reads overlap; a value counts if that slot's prefix is p.
-    int top = 1;
-    while (top * 2 < ns) top *= 2;
+    // Compaction: in a kReadAndCompact pass every value that matches an
+    // active prefix is also kept in the tile's region (row = the thread's
+    // count so far), up to kCompactRows per thread.
+    const bool compact = mode == kReadAndCompact;
+    uint32_t *reg = a.region ? a.region + wg * static_cast<int64_t>(kCompactRows * kThreads) : nullptr;
+    int kept = 0;
+    auto keep = [&](float v) {
+        if (kept < kCompactRows) reg[kept * kThreads + threadIdx.x] = __float_as_uint(v);
+        ++kept;
+    };
+    bool from_region = false;
+    uint32_t rows = 0;
+    if (mode == kReadCompact) {
+        const uint32_t meta = a.tmeta[wg];
+        from_region = (meta & kTileOverflow) == 0;
+        rows = meta;
+    }
     constexpr int kIters = kTileElems / (4 * kThreads);
     // Whole aligned tiles: kBatch 16-byte loads in flight per thread (the LDS
     // histograms cap residency at a few workgroups per CU, so each thread must
     // keep several loads outstanding); 8 measured slower (registers).
     constexpr int kBatch = 4;
     constexpr int kVals = 4 * kBatch;
-    if (aligned && base + kTileElems <= n) {
+    if (from_region) {
+        // the values an earlier pass kept for this tile (every value of the
+        // tile that can still match is among them)
+        const int mine = a.rcount[wg * kThreads + threadIdx.x];
+        for (int row = 0; row < static_cast<int>(rows); ++row) {
+            if (row >= mine) break;
+            const uint32_t key = order_key(__uint_as_float(reg[row * kThreads + threadIdx.x]));
+            const int sl = slot_of(key);
+            if (sl >= 0) add(sl * bins + static_cast<int>((key >> shift) & mask));
+        }
+    } else if (aligned && base + kTileElems <= n) {
         for (int it = 0; it < kIters; it += kBatch) {
             F4 q[kBatch];
 #pragma unroll
@@ -167,8 +232,12 @@ __global__ __launch_bounds__(kThreads) void select_hist_kernel(PassArgs a) {
 #pragma unroll
                 for (int e = 0; e < kVals; ++e) sl[e] = hashed_slot(key[e] >> (32 - a.known_bits));
 #pragma unroll
-                for (int e = 0; e < kVals; ++e)
-                    if (sl[e] >= 0) add(sl[e] * bins + static_cast<int>((key[e] >> shift) & mask));
+                for (int e = 0; e < kVals; ++e) {
+                    if (sl[e] >= 0) {
+                        add(sl[e] * bins + static_cast<int>((key[e] >> shift) & mask));
+                        if (compact) keep(q[e >> 2][e & 3]);
+                    }
+                }
             } else {
                 uint32_t p[kVals];
                 int lo[kVals];
@@ -185,8 +254,12 @@ __global__ __launch_bounds__(kThreads) void select_hist_kernel(PassArgs a) {
                     }
                 }
 #pragma unroll
-                for (int e = 0; e < kVals; ++e)
-                    if (pre[lo[e]] == p[e]) add(lo[e] * bins + static_cast<int>((key[e] >> shift) & mask));
+                for (int e = 0; e < kVals; ++e) {
+                    if (pre[lo[e]] == p[e]) {
+                        add(lo[e] * bins + static_cast<int>((key[e] >> shift) & mask));
+                        if (compact) keep(q[e >> 2][e & 3]);
+                    }
+                }
             }
         }
     } else {
@@ -195,25 +268,23 @@ __global__ __launch_bounds__(kThreads) void select_hist_kernel(PassArgs a) {
             if (e0 >= n) break;
             const int cnt = static_cast<int>((n - e0) < 4 ? n - e0 : 4);
             for (int k = 0; k < cnt; ++k) {
-                const uint32_t key = order_key(x[e0 + k]);
-                int sl = 0;
-                if (hb > 0) {
-                    sl = hashed_slot(key >> (32 - a.known_bits));
-                    if (sl < 0) continue;
-                } else if (a.known_bits > 0) {
-                    const uint32_t pk = key >> (32 - a.known_bits);
-                    for (int step = top; step > 0; step >>= 1) {
-                        const int c = sl + step;
-                        if (c < ns && pre[c] <= pk) sl = c;
-                    }
-                    if (pre[sl] != pk) continue;
-                }
+                const float v = x[e0 + k];
+                const uint32_t key = order_key(v);
+                const int sl = slot_of(key);
+                if (sl < 0) continue;
                 add(sl * bins + static_cast<int>((key >> shift) & mask));
+                if (compact) keep(v);
             }
         }
     }
     if (run_len) atomicAdd(&h[run_bin], run_len);
+    if (compact) {
+        a.rcount[wg * kThreads + threadIdx.x] = static_cast<uint8_t>(kept < kCompactRows ? kept : kCompactRows);
+        atomicMax(&s_rows, static_cast<uint32_t>(kept < kCompactRows ? kept : kCompactRows));
+        if (kept > kCompactRows) atomicOr(&s_overflow, 1u);
+    }
     __syncthreads();
+    if (compact && threadIdx.x == 0) a.tmeta[wg] = s_overflow ? kTileOverflow : s_rows;
     uint32_t *g = a.hist + static_cast<int64_t>(s0) * bins;
     for (int i = threadIdx.x; i < ns * bins; i += kThreads)
         if (h[i]) atomicAdd(&g[i], h[i]);
@@ -222,14 +293,16 @@ __global__ __launch_bounds__(kThreads) void select_hist_kernel(PassArgs a) {
 // One wavefront per wanted rank: the first digit of the rank's slot
 // histogram whose cumulative count exceeds the rank's residual rank becomes
 // the rank's next prefix digit, and the residual drops by the counts below
-// it.  A rank that no digit covers sets *err (the histograms disagree with
-// the tensor sizes).
+// it; that digit's count (the values sharing the rank's new prefix) goes to
+// rank_count.  A rank that no digit covers sets *err (the histograms disagree
+// with the tensor sizes).
 constexpr int kWalkWaves = kThreads / 64;
 
 __global__ __launch_bounds__(kThreads) void select_walk_kernel(const uint32_t *__restrict__ hist,
                                                                 const int32_t *__restrict__ rank_slot,
                                                                 int64_t *__restrict__ residual,
-                                                                uint32_t *__restrict__ rank_prefix, int64_t total,
+                                                                uint32_t *__restrict__ rank_prefix,
+                                                                uint32_t *__restrict__ rank_count, int64_t total,
                                                                 int width, int32_t *__restrict__ err) {
     const int lane = threadIdx.x & 63;
     const int64_t j = static_cast<int64_t>(blockIdx.x) * kWalkWaves + (threadIdx.x >> 6);
@@ -264,6 +337,7 @@ __global__ __launch_bounds__(kThreads) void select_walk_kernel(const uint32_t *_
         while (d < per - 1 && below + c[d] <= rr) below += c[d++];
         residual[j] = static_cast<int64_t>(rr - below);
         rank_prefix[j] = (rank_prefix[j] << width) | static_cast<uint32_t>(lane * per + d);
+        rank_count[j] = static_cast<uint32_t>(c[d]);
     }
 }
 
@@ -320,13 +394,16 @@ int check(hipError_t e, const char *what) {
 }
 
 // Device workspace carving.  slot_first .. table are one block, uploaded
-// with one copy per pass; rank_prefix and err are read back with one copy.
+// with one copy per pass; rank_prefix, rank_count and err are read back with
+// one copy.  The compaction regions (per tile: kCompactRows rows of values,
+// each thread's count, the tile's rows or overflow) come last and only in the
+// larger workspace.
 struct Layout {
-    size_t ptrs, numel, tile_first, slot_first, prefix, hinfo, table, hist, rank_slot, residual, rank_prefix, err,
-        total;
+    size_t ptrs, numel, tile_first, slot_first, prefix, hinfo, tmode, rank_slot, table, hist, residual, rank_prefix,
+        rank_count, err, total, region, rcount, tmeta, total_compact;
 };
 
-Layout layout(int32_t n, int64_t total_ranks) {
+Layout layout(int32_t n, int64_t total_ranks, int64_t n_tiles) {
     auto up = [](size_t b) { return (b + 255) / 256 * 256; };
     Layout L{};
     size_t off = 0;
@@ -336,6 +413,7 @@ Layout layout(int32_t n, int64_t total_ranks) {
     L.slot_first = off; off += up(4 * static_cast<size_t>(n + 1));
     L.prefix = off; off += up(4 * static_cast<size_t>(total_ranks > 0 ? total_ranks : 1));
     L.hinfo = off; off += up(sizeof(HashInfo) * static_cast<size_t>(n));
+    L.tmode = off; off += up(4 * static_cast<size_t>(n));
     const size_t nr = static_cast<size_t>(total_ranks > 0 ? total_ranks : 1);
     L.rank_slot = off; off += up(4 * nr);
     // a tensor with s active prefixes has tables of 2 x 2^b entries, 2^b < 2 s
@@ -343,10 +421,27 @@ Layout layout(int32_t n, int64_t total_ranks) {
     L.table = off; off += up((8u << (kHashGrow + 2)) * nr);
     L.hist = off; off += up(4 * 256 * nr);
     L.residual = off; off += up(8 * nr);
-    L.rank_prefix = off; off += up(4 * nr);
+    L.rank_prefix = off; off += 4 * nr;
+    L.rank_count = off; off += 4 * nr;
     L.err = off; off += up(4);
     L.total = off;
+    const size_t tiles = static_cast<size_t>(n_tiles > 0 ? n_tiles : 0);
+    L.region = off; off += up(4 * static_cast<size_t>(kCompactRows) * kThreads * tiles);
+    L.rcount = off; off += up(static_cast<size_t>(kThreads) * tiles);
+    L.tmeta = off; off += up(4 * tiles);
+    L.total_compact = off;
     return L;
+}
+
+// Workgroups of each tensor's pass (tiles of kTileElems; none for a tensor
+// with no wanted rank): tile_first[0..n].
+void tile_layout(const int64_t *numel, const int64_t *rank_first, int32_t n, std::vector<int64_t> &tile_first) {
+    tile_first.assign(static_cast<size_t>(n) + 1, 0);
+    for (int32_t i = 0; i < n; ++i) {
+        const bool wanted = rank_first[i + 1] > rank_first[i];
+        const int64_t tiles = wanted ? (numel[i] + kTileElems - 1) / kTileElems : 0;
+        tile_first[i + 1] = tile_first[i] + tiles;
+    }
 }
 
 }  // namespace
@@ -355,7 +450,17 @@ extern "C" {
 
 size_t adana_order_stats_workspace(int32_t n_tensors, int64_t total_ranks) {
     if (n_tensors < 0 || total_ranks < 0) return 0;
-    return layout(n_tensors, total_ranks).total;
+    return layout(n_tensors, total_ranks, 0).total;
+}
+
+size_t adana_order_stats_workspace_compact(const int64_t *h_numel, const int64_t *h_rank_first, int32_t n_tensors) {
+    if (n_tensors < 0 || (n_tensors > 0 && (!h_numel || !h_rank_first))) return 0;
+    if (n_tensors == 0) return layout(0, 0, 0).total_compact;
+    for (int32_t i = 0; i < n_tensors; ++i)
+        if (h_numel[i] < 0 || h_rank_first[i] < 0 || h_rank_first[i] > h_rank_first[i + 1]) return 0;
+    std::vector<int64_t> tile_first;
+    tile_layout(h_numel, h_rank_first, n_tensors, tile_first);
+    return layout(n_tensors, h_rank_first[n_tensors], tile_first[n_tensors]).total_compact;
 }
 
 int adana_order_stats(const float *const *h_tensor, const int64_t *h_numel, int32_t n,
@@ -381,23 +486,22 @@ int adana_order_stats(const float *const *h_tensor, const int64_t *h_numel, int3
                             static_cast<long long>(h_ranks[j]), i, static_cast<long long>(h_numel[i]));
     }
     if (total == 0) return ADANA_OK;
-    const Layout L = layout(n, total);
+    std::vector<int64_t> tile_first;
+    tile_layout(h_numel, h_rank_first, n, tile_first);
+    const int64_t n_tiles = tile_first[n];
+    const Layout L = layout(n, total, n_tiles);
     if (!d_workspace || ws_bytes < L.total)
         return adana_set_error(ADANA_E_INVALID, "adana_order_stats: workspace of %zu bytes < %zu needed", ws_bytes, L.total);
+    const bool compaction = ws_bytes >= L.total_compact;
     hipStream_t st = static_cast<hipStream_t>(stream);
     char *ws = static_cast<char *>(d_workspace);
 
-    // per-rank search state: the rank's prefix (host copy, read back after
-    // each pass) and, on the device, its residual rank within that prefix
-    // (read back with err, which is its last element)
+    // per-rank search state read back after each pass: the rank's prefix
+    // (rank_prefix[0, total)), the count of values that share it
+    // (rank_prefix[count_at + j]) and err (the last element); on the device
+    // only, its residual rank within that prefix
     std::vector<uint32_t> rank_prefix((L.err + 4 - L.rank_prefix) / 4, 0u);
-    std::vector<int64_t> tile_first(static_cast<size_t>(n) + 1, 0);
-    for (int32_t i = 0; i < n; ++i) {
-        const bool wanted = h_rank_first[i + 1] > h_rank_first[i];
-        const int64_t tiles = wanted ? (h_numel[i] + kTileElems - 1) / kTileElems : 0;
-        tile_first[i + 1] = tile_first[i] + tiles;
-    }
-    const int64_t n_tiles = tile_first[n];
+    const size_t count_at = (L.rank_count - L.rank_prefix) / 4;
     if (n_tiles > 0x7fffffffLL) return adana_set_error(ADANA_E_UNSUPPORTED, "adana_order_stats: too many elements");
     int32_t *d_err = reinterpret_cast<int32_t *>(ws + L.err);
     int rc;
@@ -415,6 +519,8 @@ int adana_order_stats(const float *const *h_tensor, const int64_t *h_numel, int3
     std::vector<int32_t> rank_slot(static_cast<size_t>(total));
     std::vector<uint32_t> p;
     std::vector<HashInfo> hinfo(static_cast<size_t>(n));
+    std::vector<int32_t> tmode(static_cast<size_t>(n), kReadTensor);
+    std::vector<char> slot_seen;
     std::vector<uint2> table;
     std::vector<char> stage;                       // the slot_first .. table block, as uploaded
     int known = 0;
@@ -450,6 +556,24 @@ int adana_order_stats(const float *const *h_tensor, const int64_t *h_numel, int3
             max_slots = std::max(max_slots, static_cast<int>(p.size()));
         }
         slot_first[n] = static_cast<int32_t>(prefix.size());
+        // compaction: a tensor whose active prefixes hold at most 1 / kCompactDen
+        // of its values (the last walk's counts) keeps them in this pass and
+        // reads only them afterwards
+        for (int32_t i = 0; i < n; ++i)
+            if (tmode[i] == kReadAndCompact) tmode[i] = kReadCompact;
+        if (compaction && known > 0) {
+            slot_seen.assign(prefix.size(), 0);
+            for (int32_t i = 0; i < n; ++i) {
+                if (tmode[i] != kReadTensor || h_rank_first[i + 1] == h_rank_first[i]) continue;
+                int64_t matching = 0;
+                for (int64_t j = h_rank_first[i]; j < h_rank_first[i + 1]; ++j) {
+                    if (slot_seen[rank_slot[j]]) continue;
+                    slot_seen[rank_slot[j]] = 1;
+                    matching += rank_prefix[count_at + j];
+                }
+                if (matching * kCompactDen <= h_numel[i]) tmode[i] = kReadAndCompact;
+            }
+        }
         // digit width: the widest whose histograms (and sorted prefixes) fit the LDS budget
         int width = 8;
         while (width > 1 && static_cast<size_t>(max_slots) * ((1u << width) + 1) * 4 > kLdsBudget) --width;
@@ -478,7 +602,7 @@ int adana_order_stats(const float *const *h_tensor, const int64_t *h_numel, int3
                 if (!hi.bits) table.resize(static_cast<size_t>(hi.first));   // binary search for this tensor
             }
             const size_t hist_bytes = ((static_cast<size_t>(ns) * (bins + 1) + 1) & ~static_cast<size_t>(1)) * 4;
-            if (hi.bits && hist_bytes + (static_cast<size_t>(16) << hi.bits) > 64 * 1024) {
+            if (hi.bits && hist_bytes + (static_cast<size_t>(16) << hi.bits) > kLdsMaxDynamic) {
                 table.resize(static_cast<size_t>(hi.first));             // no room: binary search
                 hi.bits = 0;
             }
@@ -489,6 +613,7 @@ int adana_order_stats(const float *const *h_tensor, const int64_t *h_numel, int3
         memcpy(stage.data(), slot_first.data(), 4 * static_cast<size_t>(n + 1));
         memcpy(stage.data() + (L.prefix - L.slot_first), prefix.data(), 4 * prefix.size());
         memcpy(stage.data() + (L.hinfo - L.slot_first), hinfo.data(), sizeof(HashInfo) * static_cast<size_t>(n));
+        memcpy(stage.data() + (L.tmode - L.slot_first), tmode.data(), 4 * static_cast<size_t>(n));
         memcpy(stage.data() + (L.rank_slot - L.slot_first), rank_slot.data(), 4 * static_cast<size_t>(total));
         if (!table.empty())
             memcpy(stage.data() + (L.table - L.slot_first), table.data(), sizeof(uint2) * table.size());
@@ -505,6 +630,10 @@ int adana_order_stats(const float *const *h_tensor, const int64_t *h_numel, int3
         pa.hinfo = reinterpret_cast<const HashInfo *>(ws + L.hinfo);
         pa.table = reinterpret_cast<const uint2 *>(ws + L.table);
         pa.hist = reinterpret_cast<uint32_t *>(ws + L.hist);
+        pa.tmode = reinterpret_cast<const int32_t *>(ws + L.tmode);
+        pa.region = compaction ? reinterpret_cast<uint32_t *>(ws + L.region) : nullptr;
+        pa.rcount = compaction ? reinterpret_cast<uint8_t *>(ws + L.rcount) : nullptr;
+        pa.tmeta = compaction ? reinterpret_cast<uint32_t *>(ws + L.tmeta) : nullptr;
         pa.n = n;
         pa.known_bits = known;
         pa.width = width;
@@ -515,7 +644,7 @@ int adana_order_stats(const float *const *h_tensor, const int64_t *h_numel, int3
         hipLaunchKernelGGL(select_walk_kernel, dim3(static_cast<unsigned>(walk_blocks)), dim3(kThreads), 0, st,
                            pa.hist, reinterpret_cast<const int32_t *>(ws + L.rank_slot),
                            reinterpret_cast<int64_t *>(ws + L.residual), reinterpret_cast<uint32_t *>(ws + L.rank_prefix),
-                           total, width, d_err);
+                           reinterpret_cast<uint32_t *>(ws + L.rank_count), total, width, d_err);
         if ((rc = check(hipGetLastError(), "walk launch"))) return rc;
         if ((rc = check(hipMemcpyAsync(rank_prefix.data(), ws + L.rank_prefix, 4 * rank_prefix.size(),
                                        hipMemcpyDeviceToHost, st), "copy")) ||

@@ -39,10 +39,12 @@ def order_stat_indices(n: int) -> np.ndarray:
 
 
 def _select(flat: Sequence[torch.Tensor], numel: np.ndarray, ranks: np.ndarray,
-            rank_first: np.ndarray) -> np.ndarray:
+            rank_first: np.ndarray, compact: bool = True) -> np.ndarray:
     """One adana_order_stats call: the values at ``ranks[rank_first[i]:
     rank_first[i + 1]]`` of each contiguous float32 tensor ``flat[i]``,
-    concatenated."""
+    concatenated.  ``compact``: give it the workspace with which its late
+    passes read only the values that can still match (about 1/8 of the
+    tensors' bytes more; same results)."""
     dev = flat[0].device
     for f in flat:
         if f.device.type != "cuda" or f.dtype != torch.float32:
@@ -55,7 +57,12 @@ def _select(flat: Sequence[torch.Tensor], numel: np.ndarray, ranks: np.ndarray,
     values = np.empty(max(total, 1), dtype=np.float32)
     ranks = ranks if total else np.zeros(1, np.int64)
     L = _lib.lib()
-    ws = torch.empty(max(int(L.adana_order_stats_workspace(n, total)), 1), dtype=torch.uint8, device=dev)
+    if compact:
+        nbytes = int(L.adana_order_stats_workspace_compact(ctypes.c_void_p(numel.ctypes.data),
+                                                             ctypes.c_void_p(rank_first.ctypes.data), n))
+    else:
+        nbytes = int(L.adana_order_stats_workspace(n, total))
+    ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=dev)
     with torch.cuda.device(dev):
         stream = torch.cuda.current_stream(dev).cuda_stream
         _lib.check(L.adana_order_stats(ctypes.c_void_p(ptrs.ctypes.data), ctypes.c_void_p(numel.ctypes.data),
@@ -71,9 +78,11 @@ def _contiguous(t: torch.Tensor) -> torch.Tensor:
     return t if t.is_contiguous() else t.contiguous()
 
 
-def order_values(tensors: Sequence[torch.Tensor], ranks: Sequence[np.ndarray]) -> List[np.ndarray]:
+def order_values(tensors: Sequence[torch.Tensor], ranks: Sequence[np.ndarray],
+                 compact: bool = True) -> List[np.ndarray]:
     """Values at ``ranks[i]`` (ascending order, np.sort's) of each float32
-    CUDA tensor, exactly, in one batched device selection."""
+    CUDA tensor, exactly, in one batched device selection (``compact``: see
+    _select)."""
     if len(tensors) != len(ranks):
         raise ValueError("order_values: one rank array per tensor")
     if not tensors:
@@ -83,7 +92,7 @@ def order_values(tensors: Sequence[torch.Tensor], ranks: Sequence[np.ndarray]) -
     rank_first = np.zeros(len(flat) + 1, dtype=np.int64)
     np.cumsum([r.size for r in all_ranks], out=rank_first[1:])
     numel = np.array([f.numel() for f in flat], dtype=np.int64)
-    values = _select(flat, numel, np.concatenate(all_ranks), rank_first)
+    values = _select(flat, numel, np.concatenate(all_ranks), rank_first, compact)
     return [values[a:b].copy() for a, b in zip(rank_first[:-1], rank_first[1:])]
 
 

@@ -46,7 +46,8 @@
  *        device array (no reference counterpart: for callers that cannot
  *        allocate).
  *   adana_last_error, adana_abi_version, adana_workspace_bytes,
- *        adana_order_stats_workspace: plumbing (no reference counterpart).
+ *        adana_order_stats_workspace, adana_order_stats_workspace_compact:
+ *        plumbing (no reference counterpart).
  *
  * Ownership: the library allocates nothing (adana_mta_step_noalloc's static
  * scratch is part of the loaded code object); every device buffer is owned by
@@ -333,6 +334,16 @@ int adana_grad_scale(const adana_plan *plan, uint32_t grad_flags, const float *d
 /* Bytes of device workspace adana_order_stats needs. */
 size_t adana_order_stats_workspace(int32_t n_tensors, int64_t total_ranks);
 
+/* Bytes of device workspace with which adana_order_stats also compacts: once
+ * at most 1/16 of a tensor's values still share a prefix with its wanted
+ * ranks, one pass keeps those values (per 65,536-element tile, up to 32 of
+ * each thread's 256) and the later passes read only them.  About 1/8 of the
+ * wanted tensors' bytes more than adana_order_stats_workspace.  Same
+ * arguments as adana_order_stats (h_numel[n_tensors], h_rank_first[n_tensors
+ * + 1]); 0 for invalid ones. */
+size_t adana_order_stats_workspace_compact(const int64_t *h_numel, const int64_t *h_rank_first,
+                                           int32_t n_tensors);
+
 /* Host-driven, synchronous.  Exact order statistics of float32 tensors: for
  * each tensor i (h_tensors[i]: device pointer, h_numel[i] elements, any
  * alignment), the values at ranks h_ranks[h_rank_first[i] ..
@@ -343,7 +354,9 @@ size_t adana_order_stats_workspace(int32_t n_tensors, int64_t total_ranks);
  * digit per wanted prefix in LDS; after each pass every rank is narrowed to
  * its next digit on the device, and the host reads back the new prefixes to
  * set up the next pass.  Synchronises ``stream``.  d_workspace: at least
- * adana_order_stats_workspace(n_tensors, h_rank_first[n_tensors]) bytes.
+ * adana_order_stats_workspace(n_tensors, h_rank_first[n_tensors]) bytes;
+ * with adana_order_stats_workspace_compact(...) bytes or more, the late passes
+ * read only the values that can still match (same results).
  * Ranks may come in any order and repeat; ascending ranks save a host sort
  * per pass.  Returns ADANA_E_UNSUPPORTED for a tensor of 2^32 elements or
  * more, or one whose ranks hold more than 4,096 distinct values at some

@@ -192,3 +192,68 @@ def test_order_stats_beyond_2_31_elements():
     assert vals[-1] == M - 1
     del x
     torch.cuda.empty_cache()
+
+
+def _select_raw(xs, ranks, compact):
+    """adana_order_stats through ctypes with a zeroed workspace (of the
+    compacting size when ``compact``): the values, and the per-tile words
+    the compaction wrote (the last block of that workspace: one word per
+    65,536-element tile, rows kept or 0x80000000 for a tile read whole)."""
+    import ctypes
+
+    from adana_amd import _hoststep, _lib
+
+    L = _lib.lib()
+    flat = [torch.from_numpy(x).to(DEV) if isinstance(x, np.ndarray) else x for x in xs]
+    numel = np.array([f.numel() for f in flat], np.int64)
+    rank_first = np.zeros(len(flat) + 1, np.int64)
+    np.cumsum([r.size for r in ranks], out=rank_first[1:])
+    rk = np.concatenate(ranks).astype(np.int64)
+    ptrs = np.frombuffer(_hoststep.data_ptrs(flat), dtype=np.uint64)
+    P = ctypes.c_void_p
+    if compact:
+        nbytes = L.adana_order_stats_workspace_compact(P(numel.ctypes.data), P(rank_first.ctypes.data), len(flat))
+    else:
+        nbytes = L.adana_order_stats_workspace(len(flat), int(rank_first[-1]))
+    ws = torch.zeros(nbytes, dtype=torch.uint8, device=DEV)
+    vals = np.empty(rk.size, np.float32)
+    rc = L.adana_order_stats(P(ptrs.ctypes.data), P(numel.ctypes.data), len(flat), P(rk.ctypes.data),
+                             P(rank_first.ctypes.data), P(vals.ctypes.data), P(ws.data_ptr()), nbytes,
+                             P(torch.cuda.current_stream().cuda_stream))
+    _lib.check(rc, "adana_order_stats")
+    tiles = int(sum((n + 65535) // 65536 for n, a, b in zip(numel, rank_first[:-1], rank_first[1:]) if b > a))
+    meta_bytes = (4 * tiles + 255) // 256 * 256
+    meta = ws[nbytes - meta_bytes:nbytes - meta_bytes + 4 * tiles].cpu().numpy().view(np.uint32) if compact else None
+    return [vals[a:b] for a, b in zip(rank_first[:-1], rank_first[1:])], meta
+
+
+def test_compaction_gives_the_same_values():
+    """Late passes over compacted values (the larger workspace) against the
+    plain passes and np.sort: a uniform tensor, whose active prefixes soon
+    hold few values (every tile compacted, none overflowing); a sorted one,
+    whose matching values crowd into a few tiles (threads there overflow their
+    32 rows, so those tiles are read whole); an unaligned view; a tensor of
+    mostly equal values (never compacted); and a tiny one, in one batch."""
+    from adana_amd.tau_stats import _rank_plan
+
+    rng = np.random.default_rng(17)
+    print("case: order statistics with and without compaction", flush=True)
+    base = rng.random(3_000_001).astype(np.float32)
+    mostly_equal = np.zeros(400_000, np.float32)
+    mostly_equal[::50] = rng.random(8_000).astype(np.float32)
+    xs = [rng.random(2_500_000).astype(np.float32), np.sort(rng.random(2_000_000).astype(np.float32)),
+          torch.from_numpy(base).to(DEV)[1:], mostly_equal, rng.random(100).astype(np.float32)]
+    hosts = [x if isinstance(x, np.ndarray) else base[1:] for x in xs]
+    ranks = [_rank_plan(h.size)[0] for h in hosts]
+    got_c, meta = _select_raw(xs, ranks, True)
+    got_p, _ = _select_raw(xs, ranks, False)
+    for h, r, gc, gp in zip(hosts, ranks, got_c, got_p):
+        want = np.sort(h)[r]
+        assert _same(gc, want) and _same(gp, want)
+    tiles = [(h.size + 65535) // 65536 for h in hosts]
+    first = np.concatenate([[0], np.cumsum(tiles)])
+    m = [meta[a:b] for a, b in zip(first[:-1], first[1:])]
+    assert np.all((m[0] > 0) & (m[0] < 0x80000000)), "uniform: every tile compacted, none overflowing"
+    assert np.any(m[1] == 0x80000000) and np.any((m[1] > 0) & (m[1] < 0x80000000)), "sorted: both kinds of tile"
+    assert np.all(m[2] != 0), "unaligned view compacted"
+    assert np.all(m[3] == 0), "mostly equal values: never compacted"

@@ -120,6 +120,14 @@ def test_order_stats_library_validates_before_device_work():
     assert call(1 << 32, [0]) == -3 and "2^32" in _lib.last_error()          # ADANA_E_UNSUPPORTED
     assert call(10, [3]) == -1 and "workspace" in _lib.last_error()
     assert L.adana_order_stats_workspace(1, 2) > L.adana_order_stats_workspace(1, 1) > 0
+    # the compacting workspace: the plain one plus 32 rows of 256 values, 256
+    # counts and a word per 65,536-element tile of every tensor with ranks
+    nm = (ctypes.c_int64 * 2)(1 << 20, 5)
+    rf = (ctypes.c_int64 * 3)(0, 2, 2)
+    plain = L.adana_order_stats_workspace(2, 2)
+    assert L.adana_order_stats_workspace_compact(nm, rf, 2) >= plain + 16 * (32 * 256 * 4 + 256 + 4)
+    bad = (ctypes.c_int64 * 3)(0, 2, 1)
+    assert L.adana_order_stats_workspace_compact(nm, bad, 2) == 0
 
 
 def test_index_formula_fails_past_2_31_elements_as_the_reference():
