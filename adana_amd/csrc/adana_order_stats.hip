@@ -106,6 +106,10 @@ struct PassArgs {
     int32_t width;                // bits resolved by this pass
 };
 
+// KEEP: the instance for a pass in which some tensor is compacted (the
+// value-keeping code costs the hot loop registers, so passes without it run
+// the instance without it).
+template <bool KEEP>
 __global__ __launch_bounds__(kThreads) void select_hist_kernel(PassArgs a) {
     extern __shared__ uint32_t lds[];
     __shared__ uint32_t s_rows, s_overflow;             // compaction: the tile's rows used, any overflow
@@ -181,7 +185,7 @@ __global__ __launch_bounds__(kThreads) void select_hist_kernel(PassArgs a) {
     // Compaction: in a kReadAndCompact pass every value that matches an
     // active prefix is also kept in the tile's region (row = the thread's
     // count so far), up to kCompactRows per thread.
-    const bool compact = mode == kReadAndCompact;
+    const bool compact = KEEP && mode == kReadAndCompact;
     uint32_t *reg = a.region ? a.region + wg * static_cast<int64_t>(kCompactRows * kThreads) : nullptr;
     int kept = 0;
     auto keep = [&](float v) {
@@ -527,9 +531,16 @@ int adana_order_stats(const float *const *h_tensor, const int64_t *h_numel, int3
     while (known < 32) {
         // slots: each tensor's distinct prefixes among its wanted ranks, sorted;
         // rank_slot: each rank's slot (absolute index)
+        // and, for compaction, the values of each tensor that share a prefix
+        // with its ranks (the last walk's counts, one per distinct prefix): a
+        // tensor where they are at most 1 / kCompactDen of its values keeps
+        // them in this pass and reads only them afterwards
         prefix.clear();
         int max_slots = 0;
         for (int32_t i = 0; i < n; ++i) {
+            if (tmode[i] == kReadAndCompact) tmode[i] = kReadCompact;
+            const bool judge = compaction && known > 0 && tmode[i] == kReadTensor;
+            int64_t matching = 0;
             slot_first[i] = static_cast<int32_t>(prefix.size());
             const int64_t a = h_rank_first[i], b = h_rank_first[i + 1];
             if (std::is_sorted(rank_prefix.begin() + a, rank_prefix.begin() + b)) {
@@ -540,40 +551,30 @@ int adana_order_stats(const float *const *h_tensor, const int64_t *h_numel, int3
                     if (j == a || rank_prefix[j] != rank_prefix[j - 1]) {
                         prefix.push_back(rank_prefix[j]);
                         ++s;
+                        matching += rank_prefix[count_at + j];
                     }
                     rank_slot[j] = slot_first[i] + s;
                 }
                 max_slots = std::max(max_slots, s + 1);
-                continue;
+            } else {
+                p.assign(rank_prefix.begin() + a, rank_prefix.begin() + b);
+                std::sort(p.begin(), p.end());
+                p.erase(std::unique(p.begin(), p.end()), p.end());
+                slot_seen.assign(p.size(), 0);
+                for (int64_t j = a; j < b; ++j) {
+                    const int32_t k = static_cast<int32_t>(std::lower_bound(p.begin(), p.end(), rank_prefix[j]) - p.begin());
+                    rank_slot[j] = slot_first[i] + k;
+                    if (!slot_seen[k]) {
+                        slot_seen[k] = 1;
+                        matching += rank_prefix[count_at + j];
+                    }
+                }
+                prefix.insert(prefix.end(), p.begin(), p.end());
+                max_slots = std::max(max_slots, static_cast<int>(p.size()));
             }
-            p.assign(rank_prefix.begin() + a, rank_prefix.begin() + b);
-            std::sort(p.begin(), p.end());
-            p.erase(std::unique(p.begin(), p.end()), p.end());
-            for (int64_t j = a; j < b; ++j)
-                rank_slot[j] = slot_first[i] +
-                               static_cast<int32_t>(std::lower_bound(p.begin(), p.end(), rank_prefix[j]) - p.begin());
-            prefix.insert(prefix.end(), p.begin(), p.end());
-            max_slots = std::max(max_slots, static_cast<int>(p.size()));
+            if (judge && b > a && matching * kCompactDen <= h_numel[i]) tmode[i] = kReadAndCompact;
         }
         slot_first[n] = static_cast<int32_t>(prefix.size());
-        // compaction: a tensor whose active prefixes hold at most 1 / kCompactDen
-        // of its values (the last walk's counts) keeps them in this pass and
-        // reads only them afterwards
-        for (int32_t i = 0; i < n; ++i)
-            if (tmode[i] == kReadAndCompact) tmode[i] = kReadCompact;
-        if (compaction && known > 0) {
-            slot_seen.assign(prefix.size(), 0);
-            for (int32_t i = 0; i < n; ++i) {
-                if (tmode[i] != kReadTensor || h_rank_first[i + 1] == h_rank_first[i]) continue;
-                int64_t matching = 0;
-                for (int64_t j = h_rank_first[i]; j < h_rank_first[i + 1]; ++j) {
-                    if (slot_seen[rank_slot[j]]) continue;
-                    slot_seen[rank_slot[j]] = 1;
-                    matching += rank_prefix[count_at + j];
-                }
-                if (matching * kCompactDen <= h_numel[i]) tmode[i] = kReadAndCompact;
-            }
-        }
         // digit width: the widest whose histograms (and sorted prefixes) fit the LDS budget
         int width = 8;
         while (width > 1 && static_cast<size_t>(max_slots) * ((1u << width) + 1) * 4 > kLdsBudget) --width;
@@ -637,8 +638,13 @@ int adana_order_stats(const float *const *h_tensor, const int64_t *h_numel, int3
         pa.n = n;
         pa.known_bits = known;
         pa.width = width;
-        hipLaunchKernelGGL(select_hist_kernel, dim3(static_cast<unsigned>(n_tiles)), dim3(kThreads),
-                           static_cast<unsigned>(lds), st, pa);
+        const bool keep = std::find(tmode.begin(), tmode.end(), kReadAndCompact) != tmode.end();
+        if (keep)
+            hipLaunchKernelGGL(select_hist_kernel<true>, dim3(static_cast<unsigned>(n_tiles)), dim3(kThreads),
+                               static_cast<unsigned>(lds), st, pa);
+        else
+            hipLaunchKernelGGL(select_hist_kernel<false>, dim3(static_cast<unsigned>(n_tiles)), dim3(kThreads),
+                               static_cast<unsigned>(lds), st, pa);
         if ((rc = check(hipGetLastError(), "histogram launch"))) return rc;
         const int64_t walk_blocks = (total + kWalkWaves - 1) / kWalkWaves;
         hipLaunchKernelGGL(select_walk_kernel, dim3(static_cast<unsigned>(walk_blocks)), dim3(kThreads), 0, st,

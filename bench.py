@@ -545,17 +545,37 @@ def consumer_bench(args):
     import adana_amd
     from adana_amd.tau_stats import order_stat_indices
 
-    w = workload("north_star" if args.workload == "tau_stats" else "c5")
+    tau = args.workload in ("tau_stats", "tau_stats_spread")
+    w = workload("north_star" if tau else "c5")
     print(f"[bench] {args.workload}: building {w['name']} state on cuda:0", file=sys.stderr, flush=True)
     opt, params = build_gpu(w)
     for _ in range(3):
         opt.step()
     torch.cuda.synchronize()
-    if args.workload == "tau_stats":
+    plain = None
+    if tau:
         taus = [opt.state[p]["tau"] for p in params]
         n_elems = sum(t.numel() for t in taus)
+        if args.workload == "tau_stats_spread":
+            # After 3 steps with the same gradients nearly every tau sits in one narrow
+            # cluster.  A run's tau is spread over (0, 1): Beta(2, 5) draws here
+            # (X / (X + Y), X ~ Gamma(2), Y ~ Gamma(5), each -log of a product of uniforms).
+            gen = torch.Generator(device="cuda:0")
+            gen.manual_seed(7)
+            for t in taus:
+                u = lambda: torch.rand(t.shape, device="cuda:0", generator=gen)  # noqa: E731
+                x = -torch.log(u() * u())
+                y = -torch.log(u() * u() * u() * u() * u())
+                t.copy_(x / (x + y))
+            torch.cuda.synchronize()
         run = lambda: adana_amd.extract_tau_statistics(opt)       # noqa: E731
         unit_bytes = 4 * n_elems                                  # tau scanned once per pass
+        from adana_amd import tau_stats as T
+        flat = [T._contiguous(t) for t in taus]
+        plan = T._batch_plan(tuple(f.numel() for f in flat))[:3]
+
+        def plain(compact):                                       # the selection alone, either way
+            T._select(flat, *plan, compact=compact)
     else:
         name = "dana-star-mk4"
         run = lambda: adana_amd.log_optimizer_schedules(opt, name)  # noqa: E731
@@ -569,8 +589,25 @@ def consumer_bench(args):
         run()
     torch.cuda.synchronize()
     ms = (time.perf_counter() - t0) * 1e3 / args.steps
+    select_ms = None
+    if plain is not None:
+        # the device selection alone (no result dictionaries), with and without
+        # compaction, interleaved call by call
+        t = {True: [], False: []}
+        for rep in range(args.steps + 1):
+            for c in (True, False):
+                torch.cuda.synchronize()
+                t0 = time.perf_counter()
+                plain(c)
+                torch.cuda.synchronize()
+                if rep:
+                    t[c].append((time.perf_counter() - t0) * 1e3)
+        select_ms = {"compaction": round(float(np.median(t[True])), 4),
+                     "no_compaction": round(float(np.median(t[False])), 4),
+                     "note": "median over the steps of the device selection alone (adana_order_stats), "
+                             "interleaved; compaction is the default"}
     # the reference's host path, timed on a bounded sample
-    if args.workload == "tau_stats":
+    if tau:
         sample = [t for t in taus][:4]                            # first four tensors of the list
         ns = sum(t.numel() for t in sample)
         c0 = time.perf_counter()
@@ -585,7 +622,9 @@ def consumer_bench(args):
                "sample": f"first 4 tau tensors ({ns} elements): tau.cpu(), np.sort, order-statistic picks as "
                          f"src/optim/tau_stats_collector.py:131-160, {cpu_ms:.0f} ms"}
         value = n_elems / (ms * 1e-3) / 1e9
-        metric, unit = "tau order statistics over the north-star state (elements/s)", "Gelem/s"
+        metric = ("tau order statistics over the north-star state (elements/s)" if args.workload == "tau_stats"
+                  else "tau order statistics over north-star-sized tau, Beta(2, 5) values (elements/s)")
+        unit = "Gelem/s"
     else:
         c0 = time.perf_counter()
         vals = []
@@ -606,7 +645,10 @@ def consumer_bench(args):
                       "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
                       "data": "synthetic",
                       "config": {"workload": args.workload, "state_of": w["name"], "elements": n_elems,
-                                 "bytes_read_once": unit_bytes},
+                                 "bytes_read_once": unit_bytes,
+                                 **({"tau": "Beta(2, 5) draws over the state's tau tensors"}
+                                    if args.workload == "tau_stats_spread" else {})},
+                      **({"select_ms": select_ms} if select_ms is not None else {}),
                       "cpu_baseline": cpu}), flush=True)
     return 0
 
@@ -741,7 +783,8 @@ def main():
                     help="untimed warm-up steps (default 3; 40 for c5)")
     ap.add_argument("--workload", default="north_star",
                     choices=["north_star", "north_star_clip", "north_star_bf16", "c1", "c2", "c3", "c4", "c5",
-                             "copy_probe", "tau_stats", "diag_readout", "manau", "stream_sweep"])
+                             "copy_probe", "tau_stats", "tau_stats_spread", "diag_readout", "manau",
+                             "stream_sweep"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-ceiling-probe", action="store_true",
                     help="skip the 5-read/4-write stream probe reported as roofline.mix_ceiling")
@@ -761,7 +804,7 @@ def main():
     __graft_entry__.ensure_built()      # a fresh checkout has no built libraries
     if args.workload == "copy_probe":
         return copy_probe(args.steps)
-    if args.workload in ("tau_stats", "diag_readout"):
+    if args.workload in ("tau_stats", "tau_stats_spread", "diag_readout"):
         return consumer_bench(args)
     if args.workload == "manau":
         return manau_bench(args)
