@@ -9,19 +9,20 @@ workloads' own lists and hyper-parameters (bench.workload):
   * c2: Dana-MK4, 50,938,880 parameters in 67 tensors, 1-D gradients x 0.1,
     under the bench's warm-up/cosine lr schedule (a new group lr every step);
   * c5: Dana-Star-MK4 over 10,000 log-uniform tensors (94,406,322
-    parameters), 5% of them with all-zero gradients (256 sampled elements
-    per tensor).
+    parameters), 5% of them with all-zero gradients.
 Ten steps each, so every run crosses t = delta = 8, where alpha = 0.5 and
 ATen's lerp takes its second branch.
 Two weight-decay groups as src/models/base.py:503-561; launcher
 hyper-parameters as scripts/launch.sh:36-40,188-223.
 
 The oracle cannot run billions of elements in seconds, but the update is
-element-wise, so it replays a random sample of every tensor's elements from
-their inputs exactly.  Bars:
-  * sampled m, v, tau, ADana's master: bit-exact; bf16 params: equal to
+element-wise, so for north_star, c4 and c3 it replays a random sample of
+every tensor's elements (1,024 and the first and last) from their inputs
+exactly; c2 and c5 (at most FULL_REPLAY elements) are replayed whole, every
+element of every tensor at every step.  Bars:
+  * replayed m, v, tau, ADana's master: bit-exact; bf16 params: equal to
     RNE(master) (ADana);
-  * sampled Dana-Star p: bit-exact except the pow's rare rounding-boundary
+  * replayed Dana-Star p: bit-exact except the pow's rare rounding-boundary
     cases (at most STAR_HARD_CASES per tensor per step, each within
     STAR_P_ULPS ulps of max(|p_before|, |p_after|));
   * all five diagnostics of every tensor, reductions over all of its
@@ -51,13 +52,14 @@ pytestmark = [pytest.mark.gpu,
 
 DEV = "cuda:0"
 SAMPLES = 1024          # per tensor, plus its first and last element
+FULL_REPLAY = 100_000_000   # configurations of at most this many elements: every element replayed
 STEPS = 10
 ELEMENTS = {"north_star": 2_645_527_040, "c4": 2_645_527_040, "c3": 1_311_082_496, "c2": 50_938_880,
             "c5": 94_406_322}
 
 
 @pytest.mark.parametrize("name", ["north_star", "c4", "c3", "c2", "c5"])
-def test_full_size_sampled_parity(oracle_mod, name):
+def test_full_size_parity(oracle_mod, name):
     import adana_amd
     from bench import workload
 
@@ -66,7 +68,9 @@ def test_full_size_sampled_parity(oracle_mod, name):
     star, master, hp = w["star"], w["master"], w["hp"]
     shapes = [s for g in w["groups"] for s in g]
     assert sum(int(np.prod(s)) for s in shapes) == ELEMENTS[name]
-    print(f"case: {name} at full size ({ELEMENTS[name]} params), {STEPS} steps, sampled oracle replay", flush=True)
+    full = ELEMENTS[name] <= FULL_REPLAY
+    print(f"case: {name} at full size ({ELEMENTS[name]} params), {STEPS} steps, "
+          f"{'full' if full else 'sampled'} oracle replay", flush=True)
     pdtype = torch.bfloat16 if master else torch.float32
     gen = torch.Generator(device=DEV)
     gen.manual_seed(0)
@@ -87,11 +91,12 @@ def test_full_size_sampled_parity(oracle_mod, name):
     idx = []
     for p in params:
         n = p.numel()
-        per = SAMPLES if len(params) < 1000 else 256             # C5: 10,000 tensors
-        pick = np.unique(np.concatenate([[0, n - 1], rng.integers(0, n, size=min(n, per))]))
-        idx.append(torch.from_numpy(pick).to(DEV))
+        pick = np.unique(np.concatenate([[0, n - 1], rng.integers(0, n, size=min(n, SAMPLES))]))
+        idx.append(None if full else torch.from_numpy(pick).to(DEV))
 
     def gather(ts):
+        if full:
+            return [t.detach().reshape(-1).float().cpu().numpy() for t in ts]
         return [t.detach().reshape(-1).index_select(0, ix).float().cpu().numpy() for t, ix in zip(ts, idx)]
 
     host_p = gather(params)                              # master mode: the master starts as float(p_bf16)
