@@ -443,6 +443,9 @@ def stream_sweep(args):
       * the wave-specialised persistent kernel (loader wave + direct-to-LDS
         ring; stages, compute waves, workgroups per CU);
       * the same five arrays read only and four written only, and a copy;
+      * persistent workgroups (1, 2 or 4 per CU) dealt tiles grid-stride, with
+        a plain loop and a double-buffered one that issues the next tile's
+        loads before the current tile's stores;
       * then (after the separate arrays are freed) the one-shot shape at the
         step's cap of 4 with the five arrays placed in one allocation,
         ``k * (n + 4 Mi)`` floats plus ``k * skew`` bytes from its start
@@ -465,6 +468,8 @@ def stream_sweep(args):
     lib.adana_probe_stream_5r4w_ws.restype = INT
     lib.adana_probe_copy.argtypes = [P, P, I64, P, INT, P]
     lib.adana_probe_copy.restype = INT
+    lib.adana_probe_stream_5r4w_persistent.argtypes = [P, I64, P, INT, INT, P]
+    lib.adana_probe_stream_5r4w_persistent.restype = INT
     n = 2645527040 // 1024 * 1024
     arrays = [torch.zeros(n, device="cuda:0") for _ in range(5)]
     partials = torch.empty(n // 1024 * 4, device="cuda:0")
@@ -488,6 +493,10 @@ def stream_sweep(args):
     for cap in (4, 0):
         cfgs.append((f"1r1w copy cap {cap or 'none'}", 8 * n,
                      lambda cap=cap: lib.adana_probe_copy(a0, a1, n, part, cap, st)))
+    for db in (0, 1):
+        for g in (1, 2, 4):
+            cfgs.append((f"5r4w persistent {'double-buffered' if db else 'plain'} wgs/CU {g}", 36 * n,
+                         lambda a=(g, db): lib.adana_probe_stream_5r4w_persistent(ptrs, n, part, a[0], a[1], st)))
     reps = max(2, args.steps)
     best = {}
     order = []

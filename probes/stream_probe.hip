@@ -23,12 +23,14 @@
 // (global_load_lds_dwordx4) and compute waves read the tile from LDS and
 // store the results.  No wave's vmcnt wait then covers its own stores (the
 // loader only loads, the compute waves only store), which is what slows a
-// plain persistent loop on gfx9.
+// plain persistent loop on gfx9.  A fourth, persistent workgroups with a
+// plain and a double-buffered loop, completes the comparison.
 //
 // Not part of the optimizer's interface: built as a separate library
 // (probes/libadana_probe.so) and loaded only by bench.py.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cstdint>
 
 namespace {
@@ -285,6 +287,116 @@ extern "C" int adana_probe_stream_5r4w_ws(float *const *arrays, int64_t n, float
     if (stages == 4 && compute_waves == 4) return launch_ws<4, 4>(arrays, n, partials, wgs_per_cu, stream);
     if (stages == 3 && compute_waves == 8) return launch_ws<3, 8>(arrays, n, partials, wgs_per_cu, stream);
     return -1;
+}
+
+// ---------------------------------------------------------------------------
+// Persistent workgroups over the same one-chunk tiles, dealt grid-stride: a
+// plain loop (load, add, store, partial) and a double-buffered one that
+// issues the next tile's loads before the current tile's stores (vector
+// memory operations complete in order on gfx9, so waiting for those loads
+// does not wait for the stores), unrolled by two over fixed register
+// buffers so that the compiler's waits count only the older loads.  The next
+// tile index is clamped to the last tile so that every load is in bounds and
+// unconditional.
+namespace {
+
+// The chunk's sum over the workgroup into partials[c]: as chunk_partial, with
+// the LDS slots alternating between consecutive chunks of one workgroup.
+__device__ __forceinline__ void chunk_partial_at(F4 s, float4 *partials, int64_t c) {
+    __shared__ float red[2][kThreads / 64][4];
+    float t[4] = {s.x, s.y, s.z, s.w};
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+#pragma unroll
+        for (int k = 0; k < 4; ++k) t[k] += __shfl_xor(t[k], o, 64);
+    }
+    const int par = static_cast<int>(c & 1);
+    if ((threadIdx.x & 63) == 0) {
+#pragma unroll
+        for (int k = 0; k < 4; ++k) red[par][threadIdx.x >> 6][k] = t[k];
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        float4 q = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        for (int w = 0; w < kThreads / 64; ++w) {
+            q.x += red[par][w][0];
+            q.y += red[par][w][1];
+            q.z += red[par][w][2];
+            q.w += red[par][w][3];
+        }
+        partials[c] = q;
+    }
+}
+
+__device__ __forceinline__ void tile_load5(float *const (&a)[5], int64_t c, F4 (&x)[5]) {
+#pragma unroll
+    for (int k = 0; k < 5; ++k)
+        x[k] = __builtin_nontemporal_load((const GF4 *)(a[k] + c * kChunk + 4 * threadIdx.x));
+}
+__device__ __forceinline__ void tile_use5(float *const (&a)[5], int64_t c, const F4 (&x)[5], float4 *partials) {
+    const F4 s = x[0] + x[1] + x[2] + x[3] + x[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        F4 o = s;
+        o.x += static_cast<float>(k);
+        store_stream(a[k] + c * kChunk, 16 * threadIdx.x, o);
+    }
+    chunk_partial_at(s, partials, c);
+}
+
+template <bool DOUBLE>
+__global__ __launch_bounds__(kThreads) void stream_persistent_kernel(float *a0, float *a1, float *a2, float *a3,
+                                                                     float *a4, float4 *partials,
+                                                                     int64_t n_chunks) {
+    float *const a[5] = {a0, a1, a2, a3, a4};
+    const int64_t g = gridDim.x, last = n_chunks - 1;
+    int64_t c = blockIdx.x;
+    if (c >= n_chunks) return;                      // whole workgroup
+    F4 A[5], B[5];
+    if constexpr (!DOUBLE) {
+        for (; c < n_chunks; c += g) {
+            tile_load5(a, c, A);
+            tile_use5(a, c, A, partials);
+        }
+    } else {
+        tile_load5(a, c, A);
+        for (;;) {
+            const int64_t cb = c + g;
+            tile_load5(a, cb < last ? cb : last, B);
+            tile_use5(a, c, A, partials);
+            if (cb >= n_chunks) break;
+            const int64_t ca = cb + g;
+            tile_load5(a, ca < last ? ca : last, A);
+            tile_use5(a, cb, B, partials);
+            if (ca >= n_chunks) break;
+            c = ca;
+        }
+    }
+}
+
+}  // namespace
+
+// The 5-read/4-write pattern through persistent workgroups: `wgs_per_cu`
+// (1..8) per CU, plain (double_buffer 0) or double-buffered (1).  Same array
+// conditions as adana_probe_stream_5r4w; partials: n / 1024 float4.
+extern "C" int adana_probe_stream_5r4w_persistent(float *const *arrays, int64_t n, float4 *partials, int wgs_per_cu,
+                                                  int double_buffer, hipStream_t stream) {
+    if (!arrays || !partials || n <= 0 || n % kChunk != 0 || wgs_per_cu < 1 || wgs_per_cu > 8) return -1;
+    for (int k = 0; k < 5; ++k)
+        if (!arrays[k] || reinterpret_cast<uintptr_t>(arrays[k]) % 16 != 0) return -1;
+    int dev = 0, cus = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+        return -1;
+    const int64_t n_chunks = n / kChunk;
+    const int64_t grid = std::min<int64_t>(static_cast<int64_t>(cus) * wgs_per_cu, n_chunks);
+    if (double_buffer)
+        hipLaunchKernelGGL(stream_persistent_kernel<true>, dim3(static_cast<unsigned>(grid)), dim3(kThreads), 0,
+                           stream, arrays[0], arrays[1], arrays[2], arrays[3], arrays[4], partials, n_chunks);
+    else
+        hipLaunchKernelGGL(stream_persistent_kernel<false>, dim3(static_cast<unsigned>(grid)), dim3(kThreads), 0,
+                           stream, arrays[0], arrays[1], arrays[2], arrays[3], arrays[4], partials, n_chunks);
+    return static_cast<int>(hipGetLastError());
 }
 
 // The 5 arrays read only (no stores) and 4 written only (no loads), in the
