@@ -257,3 +257,33 @@ def test_compaction_gives_the_same_values():
     assert np.any(m[1] == 0x80000000) and np.any((m[1] > 0) & (m[1] < 0x80000000)), "sorted: both kinds of tile"
     assert np.all(m[2] != 0), "unaligned view compacted"
     assert np.all(m[3] == 0), "mostly equal values: never compacted"
+
+
+def test_compaction_with_special_values_and_shuffled_ranks():
+    """Compaction on values with NaN, +-0, +-inf and denormals mixed in, and
+    with ranks given out of order and repeated (the host's other slot path):
+    the same values as np.sort and as the uncompacted passes, with every tile
+    of both tensors compacted."""
+    from adana_amd.tau_stats import _rank_plan
+
+    rng = np.random.default_rng(19)
+    print("case: compaction with special values and shuffled ranks", flush=True)
+    x = rng.normal(0, 1, 2_000_000).astype(np.float32)
+    x[::97] = np.nan
+    x[1::101] = 0.0
+    x[2::103] = -0.0
+    x[3::107] = np.inf
+    x[4::109] = -np.inf
+    x[5::113] = 1e-42
+    y = rng.random(1_500_000).astype(np.float32)
+    ry = _rank_plan(y.size)[0]
+    ry = rng.permutation(np.concatenate([ry, ry[:40]]))          # out of order, with repeats
+    ranks = [_rank_plan(x.size)[0], ry]
+    got_c, meta = _select_raw([x, y], ranks, True)
+    got_p, _ = _select_raw([x, y], ranks, False)
+    for h, r, gc, gp in zip((x, y), ranks, got_c, got_p):
+        want = np.sort(h)[r]
+        assert _same(gc, want) and _same(gp, want)
+    tx = (x.size + 65535) // 65536
+    assert np.all(meta[:tx] != 0), "special values: every tile compacted"
+    assert np.all(meta[tx:] != 0), "shuffled ranks: every tile compacted"
