@@ -413,6 +413,18 @@ def stream_ceiling(n_elems, reps=5, star=True):
     return mix, copy
 
 
+def settle_gc():
+    """Run Python's cyclic garbage collector once and freeze what survives,
+    before a workload's warm-up steps.  A full collection over the setup's
+    objects (~270K after importing torch and building the north-star state)
+    takes ~70 ms; one that came due inside a timed loop would measure the
+    bench's setup, not the step.  Collecting before the warm-up rather than
+    right before the timed loop leaves the warm-up steps to bring the GPU's
+    clock back up after the pause."""
+    gc.collect()
+    gc.freeze()
+
+
 def launch_ms(run, reps, stream):
     """Mean device time of ``reps`` back-to-back calls of ``run`` (after one
     untimed call), from events at the two ends only: an event between two
@@ -591,10 +603,9 @@ def consumer_bench(args):
         run = lambda: adana_amd.log_optimizer_schedules(opt, name)  # noqa: E731
         n_elems = len(params)
         unit_bytes = 20 * n_elems                                 # five fp32 diagnostics each
+    settle_gc()
     for _ in range(args.warmup):
         run()
-    gc.collect()                                                  # as in the step bench: no setup garbage
-    gc.freeze()
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for _ in range(args.steps):
@@ -728,6 +739,7 @@ def manau_bench(args):
     n_dana = sum(p.numel() for p in dana)
     n_muon = sum(p.numel() for p in params) - n_dana
     print(f"[bench] manau: {n_muon} Muon + {n_dana} Dana params", file=sys.stderr, flush=True)
+    settle_gc()
     for _ in range(args.warmup):
         opt.step()
     torch.cuda.synchronize()
@@ -735,8 +747,6 @@ def manau_bench(args):
 
     def timed(fn, k):                                            # events at the loop's two ends only
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        gc.collect()                                             # as in the step bench: no setup garbage
-        gc.freeze()
         torch.cuda.synchronize()
         t0 = time.perf_counter()
         e0.record(stream)
@@ -816,6 +826,7 @@ def main():
     import torch
 
     __graft_entry__.ensure_built()      # a fresh checkout has no built libraries
+    gc.freeze()                         # the imports' objects: later collections skip them
     if args.workload == "copy_probe":
         return copy_probe(args.steps)
     if args.workload in ("tau_stats", "tau_stats_spread", "diag_readout"):
@@ -842,6 +853,7 @@ def main():
             grad_norms.append(opt.clip_grad_norm_(w["clip"]).item())   # src/optim/base.py:250-257
         opt.step()
 
+    settle_gc()
     torch.cuda.synchronize()
     for k in range(args.warmup):
         one_step(k)
@@ -853,12 +865,6 @@ def main():
     # steps leaves the GPU idle for ~3 us (C1 0.0282 -> 0.0249 ms per step without
     # them), which is the harness's cost, not the step's.
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    # A full collection of Python's cyclic garbage collector over the setup's objects
-    # (~270K after the north-star build) takes ~70 ms; one that comes due inside the
-    # timed loop measures the bench's setup, not the step. Collect now, and freeze
-    # what survives so that later collections skip it.
-    gc.collect()
-    gc.freeze()
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     e0.record(stream)
@@ -953,8 +959,8 @@ def main():
         **({"mall_cold": cold} if cold else {}),
         "kernel_ms_p90": round(float(np.percentile(dev_ms, 90)), 4),
         "timing_note": "value and ms_per_step: wall time of the timed loop (Python's garbage collector run and "
-                       "the setup's objects frozen just before it); kernel_ms_per_step: events at the loop's two "
-                       "ends only; kernel_ms_p90: the next steps with an event between every two",
+                       "the setup's objects frozen before the warm-up); kernel_ms_per_step: events at the loop's "
+                       "two ends only; kernel_ms_p90: the next steps with an event between every two",
         "params_per_s": round(n_elems / (ms_per_step * 1e-3), 1),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
