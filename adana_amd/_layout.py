@@ -21,6 +21,22 @@ def dense_layout(t: torch.Tensor) -> bool:
     return True
 
 
+def no_overlap(t: torch.Tensor) -> bool:
+    """Whether t's elements are known to sit at distinct addresses: ordered by
+    stride, each dimension of size > 1 steps past the whole extent of the
+    smaller ones (contiguous, permuted and sliced layouts such as
+    ``x[:, :k]`` or ``x[::2]``).  An expanded tensor (stride 0) fails, as
+    does any layout this rule cannot clear."""
+    if t.numel() == 0:
+        return True
+    extent = 0
+    for st, n in sorted((st, n) for n, st in zip(t.shape, t.stride()) if n != 1):
+        if st <= extent:
+            return False
+        extent += st * (n - 1)
+    return True
+
+
 def same_layout(a: torch.Tensor, b: torch.Tensor) -> bool:
     """Same shape and the same strides on every dimension of size > 1 (any
     strides, for empty tensors)."""

@@ -9,10 +9,14 @@ instance attributes and per-parameter state keys are the reference's:
                 'current_alpha', 'gradient_norm', 'auto_factor_mean',
                 'current_kappa_factor', 'm_norm'}        (0-d tensors of p's dtype)
 
-T has p's shape and dtype (zeros_like(p)).  bfloat16 parameters therefore
-run the reference's own bfloat16 path: bfloat16 m, v, tau and diagnostics,
-every op of the update rounded to bfloat16 as ATen's ops round it
-(ADANA_STATE_BF16).
+T has p's shape, dtype and, as zeros_like gives them, strides: p's own for a
+contiguous or permuted p, contiguous for a p with gaps (a slice such as
+``w[:, :k]``).  The kernel pairs elements by their offset in the state's
+layout; a parameter or gradient of another layout is copied into a staging
+buffer of that layout before the launch and (the parameter) back after it,
+on the same stream.  Since T has p's dtype, bfloat16 parameters run the
+reference's own bfloat16 path: bfloat16 m, v, tau and diagnostics, every op
+of the update rounded to bfloat16 as ATen's ops round it (ADANA_STATE_BF16).
 
 What differs is how a step executes.  The reference loops over tensors in
 Python, makes six 0-d device tensors per tensor and calls a torch.compile'd
@@ -50,7 +54,7 @@ from torch.optim import Optimizer
 from torch.optim import optimizer as _torch_optimizer
 
 from . import _hoststep, _lib
-from ._layout import dense_layout, same_layout
+from ._layout import dense_layout, no_overlap, same_layout
 from .clip import GradPlan, clip_grad_norm_ as _clip_grad_norm
 
 DIAG_KEYS = ("current_alpha", "gradient_norm", "auto_factor_mean",
@@ -111,6 +115,8 @@ class _LaunchSet:
         self.diag = None
         self.ptr_key = None         # the gradients' and parameters' data pointers the tables hold
         self.rest_ok = None         # per row: the non-gradient pointers allow the vector path
+        self.stage = []             # (row, param staging or None, grad staging or None)
+        self.stage_bufs = {}        # (row, "p" | "g") -> staging tensor, kept while it fits
 
 
 class _DanaFamily(Optimizer):
@@ -161,7 +167,7 @@ class _DanaFamily(Optimizer):
         by_dev = {}
         for p, st in items:
             dense = (p.device.type == "cuda" and dense_layout(p) and p.dtype in (torch.float32, torch.bfloat16))
-            if not dense:   # not steppable here anyway (step() raises): plain per-tensor state
+            if not dense:   # a layout with gaps (zeros_like(p) is contiguous), or not steppable here
                 for fam in self._state_families(p):
                     old = source[p][fam] if source is not None else None
                     if old is not None:
@@ -289,12 +295,11 @@ class _DanaFamily(Optimizer):
             raise RuntimeError(f"{type(self).__name__}: grad must match its parameter's "
                                f"device and shape ({g.device}/{tuple(g.shape)} vs "
                                f"{p.device}/{tuple(p.shape)})")
-        if not dense_layout(p):
-            raise NotImplementedError(f"{type(self).__name__}: parameters whose elements overlap or leave "
-                                      "gaps in memory are not supported (contiguous or permuted layouts are)")
-        if not same_layout(p, g):
-            raise NotImplementedError(f"{type(self).__name__}: the gradient's strides {tuple(g.stride())} differ "
-                                      f"from its parameter's {tuple(p.stride())}")
+        if not no_overlap(p):
+            # the reference's in-place ops on such a parameter raise (an
+            # expanded one) or race; the update is written back element by element
+            raise NotImplementedError(f"{type(self).__name__}: parameters whose elements may share memory "
+                                      f"(strides {tuple(p.stride())}) are not supported")
         flags = self._VARIANT
         if p.dtype == torch.float32:
             if g.dtype != torch.float32:
@@ -318,13 +323,24 @@ class _DanaFamily(Optimizer):
         n = len(ls.params)
         d = np.zeros(n, dtype=_lib.DESC_DTYPE)
         rest = np.zeros(n, dtype=bool)
+        km, kv, kt = self._KEYS
+        stage = []
         for j, (p, g, st) in enumerate(zip(ls.params, ls.grads, ls.states)):
+            # The kernel pairs elements by storage offset, in the layout of the
+            # state (zeros_like(p): p's strides for a contiguous or permuted p,
+            # contiguous for one with gaps).  A parameter or gradient of
+            # another layout is staged through a buffer of the state's layout.
+            m = st[km]
+            ps = None if same_layout(p, m) else self._staging(ls, j, "p", p, m)
+            gs = None if same_layout(g, m) else self._staging(ls, j, "g", g, m)
+            if ps is not None or gs is not None:
+                stage.append((j, ps, gs))
+            pt = p if ps is None else ps
             master = st.get("master")
-            param_ptr = master.data_ptr() if master is not None else p.data_ptr()
-            lp_ptr = p.data_ptr() if master is not None else 0
-            km, kv, kt = self._KEYS
+            param_ptr = master.data_ptr() if master is not None else pt.data_ptr()
+            lp_ptr = pt.data_ptr() if master is not None else 0
             tau_ptr = st[kt].data_ptr() if self._STAR else 0
-            gp = g.data_ptr()
+            gp = (g if gs is None else gs).data_ptr()
             m_ptr, v_ptr = st[km].data_ptr(), st[kv].data_ptr()
             vec = 8 if ls.flags & _lib.STATE_BF16 else 16       # 4 elements of the state dtype
             rest[j] = (param_ptr % vec == 0 and m_ptr % vec == 0 and v_ptr % vec == 0
@@ -333,7 +349,20 @@ class _DanaFamily(Optimizer):
             d[j] = (param_ptr, gp, m_ptr, v_ptr, tau_ptr, lp_ptr, p.numel(), ls.sclass[j],
                     _lib.DESC_VEC_OK if ok else 0)
         ls.rest_ok = rest
+        ls.stage = stage
         return d
+
+    @staticmethod
+    def _staging(ls: _LaunchSet, j: int, kind: str, x: torch.Tensor, like: torch.Tensor) -> torch.Tensor:
+        """The staging buffer of row j's parameter or gradient: x's dtype in
+        ``like``'s shape and layout, kept across steps (its address is in the
+        device descriptors) while that still fits."""
+        key = (j, kind)
+        buf = ls.stage_bufs.get(key)
+        if buf is None or buf.dtype != x.dtype or not same_layout(buf, like) or buf.device != like.device:
+            buf = ls.stage_bufs[key] = torch.empty_strided(like.shape, like.stride(), dtype=x.dtype,
+                                                           device=like.device)
+        return buf
 
     def _upload(self, ls: _LaunchSet) -> None:
         """Copy [descriptors | vstart | fold_first] to the device (async, pinned)."""
@@ -642,6 +671,11 @@ class _DanaFamily(Optimizer):
             sc_arr = (type(scalars[0]) * n_cls)(*scalars[ls.class_base:ls.class_base + n_cls])
             with torch.cuda.device(ls.device):
                 stream = torch.cuda.current_stream(ls.device).cuda_stream
+                for j, ps, gs in ls.stage:       # into the state's layout (same stream)
+                    if ps is not None and not ls.flags & _lib.PARAM_BF16:   # the master is read instead
+                        ps.copy_(ls.params[j])
+                    if gs is not None:
+                        gs.copy_(ls.grads[j])
                 if gscale is None:
                     _lib.check(L.adana_mta_step(
                         ctypes.byref(ls.plan), ctypes.cast(sc_arr, ctypes.c_void_p), n_cls, ls.flags,
@@ -654,6 +688,11 @@ class _DanaFamily(Optimizer):
                         ctypes.c_void_p(ls.workspace.data_ptr()), ls.workspace.numel(),
                         ctypes.c_void_p(ls.diag.data_ptr()), ctypes.c_void_p(stream)),
                         "adana_mta_step_scaled")
+                for j, ps, gs in ls.stage:       # and back
+                    if ps is not None:
+                        ls.params[j].copy_(ps)
+                    if gs is not None and wflag:
+                        ls.grads[j].copy_(gs)
         if fresh:
             for ls in self._sets:                          # adana.py:221-225: new 0-d tensors
                 _hoststep.bind_diag(ls.diag, ls.states, self._diag_cols)
@@ -666,19 +705,19 @@ class _DanaFamily(Optimizer):
         """A parameter whose storage was rebound (``p.data = x``) must keep the
         shape of its state: the laid-out plan, the workspace and the state
         slabs are sized by it.  The reference fails the same way, in
-        ``m.lerp_(grad, alpha)`` (src/optim/adana.py:101)."""
+        ``m.lerp_(grad, alpha)`` (src/optim/adana.py:101).  (A new layout of
+        the same shape is staged like any other.)"""
         km = self._KEYS[0]
         for p, st in zip(ls.params, ls.states):
             m = st[km]
-            if not same_layout(p, m):
+            if p.shape != m.shape:
                 a, b = tuple(m.shape), tuple(p.shape)
-                if a == b:
-                    raise RuntimeError(f"{type(self).__name__}: parameter of strides {tuple(p.stride())} has "
-                                       f"optimizer state of strides {tuple(m.stride())}; rebind it with the "
-                                       "layout it had")
                 raise RuntimeError(f"{type(self).__name__}: parameter of shape {b} has optimizer state "
                                    f"of shape {a}: the size of tensor a ({a}) must match the size of "
                                    f"tensor b ({b})")
+            if not no_overlap(p):
+                raise NotImplementedError(f"{type(self).__name__}: parameters whose elements may share memory "
+                                          f"(strides {tuple(p.stride())}) are not supported")
 
     def _refresh_ptrs(self, ls: _LaunchSet, key=None, grads_ok=None) -> None:
         """Re-point the launch set's descriptors at this step's gradients and
@@ -695,7 +734,7 @@ class _DanaFamily(Optimizer):
         bf16 = bool(ls.flags & _lib.GRAD_BF16)
         if grads_ok is None and key[1] == ls.ptr_key[1]:
             grads_ok = _hoststep.grads_match(ls.params, ls.grads, bf16)
-        if key[1] == ls.ptr_key[1] and grads_ok:
+        if key[1] == ls.ptr_key[1] and grads_ok and not ls.stage:
             # only gradients moved, and each is a dense contiguous tensor of its
             # parameter's shape and the set's dtype: re-point the grad column
             g = np.frombuffer(key[0], dtype=np.uint64)

@@ -690,8 +690,8 @@ def test_permuted_parameters(oracle_mod, star):
     permuted 3-D tensor) and gradients of the same strides, as autograd
     produces them: the state is zeros_like(p) with p's strides, the step runs
     in storage order, and every element matches the oracle's (run on the
-    logical arrays); 8 steps crossing t = delta.  A gradient of other strides,
-    or a parameter with gaps, is refused."""
+    logical arrays); 8 steps crossing t = delta.  (Gradients of other strides
+    and parameters with gaps: test_staged_layouts.)"""
     import adana_amd
 
     O = oracle_mod
@@ -731,14 +731,97 @@ def test_permuted_parameters(oracle_mod, star):
             host[i][...] = gp
             got = np.array([float(st[k]) for k in O.DIAG_KEYS])
             np.testing.assert_allclose(got, [ost[k] for k in O.DIAG_KEYS], rtol=1e-5, atol=1e-30, err_msg=tag)
-    ps[0].grad = torch.zeros(ps[0].shape, device=DEV)                      # contiguous: other strides
-    with pytest.raises(NotImplementedError, match="strides"):
+
+
+def _bits(t: torch.Tensor) -> torch.Tensor:
+    t = t.detach().contiguous()
+    return t.view(torch.int16 if t.dtype == torch.bfloat16 else torch.int32)
+
+
+@pytest.mark.parametrize("mode", ["f32", "master", "bf16"])
+@pytest.mark.parametrize("star", [False, True])
+def test_staged_layouts(star, mode):
+    """Parameters with gaps in memory (slices of larger tensors, whose state
+    zeros_like makes contiguous) and gradients whose strides differ from
+    their state's are staged through buffers of the state's layout.  Every
+    step equals, bit for bit (p, m, v, tau, the five diagnostics), the same
+    optimizer's step on twins of the state's layout with gradients of that
+    layout (nothing staged; their parity with the oracle the other tests
+    pin).  The memory between a gapped parameter's elements is untouched; a
+    gradient's layout changes between steps; 10 steps cross t = delta.  On
+    clip_grad_norm_ steps the coefficient is fused into the staged load and
+    written back through the staging buffer: every gradient then equals
+    RN(g * coef), and the twins step on those products.  A parameter whose
+    elements share memory (expanded) is refused."""
+    import adana_amd
+
+    print("case: staged layouts, star", star, "mode", mode, flush=True)
+    dt = torch.float32 if mode == "f32" else torch.bfloat16
+    gen = torch.Generator().manual_seed(91)
+
+    def rnd(*shape, std=0.02):
+        return (torch.randn(*shape, generator=gen) * std).to(dt).to(DEV)
+
+    def transposed(g):          # g's values in the reverse-strided dense layout
+        return torch.empty(g.shape[::-1], dtype=dt, device=DEV).t().copy_(g)
+
+    big0, big1 = rnd(12, 40), rnd(3001)
+    keep0, keep1 = big0.clone(), big1.clone()
+    views = [big0[:, 5:21],                       # gapped rows: contiguous state
+             big1[::3],                           # stride 3: contiguous state
+             rnd(64, 33).t(),                     # permuted: state of its strides
+             rnd(30, 20).t()[2:17],               # permuted and gapped: contiguous state
+             rnd(5000)]                           # contiguous, never staged
+    ps = [torch.nn.Parameter(v) for v in views]
+    twins = [torch.nn.Parameter(v.detach().clone()) for v in views]   # clone: the state's layout
+    assert not any(p.is_contiguous() for p in ps[:4])
+    cls = adana_amd.DANA_STAR_MK4 if star else adana_amd.ADana
+    hp = dict(lr=1e-3, delta=8.0, kappa=0.85, clipsnr=2.0, weight_decay=0.1, wd_decaying=True, wd_ts=10.0,
+              master_weights=mode == "master")
+    opt, ref = cls(ps, **hp), cls(twins, **hp)
+    keys = ("m", "v") + (("tau",) if star else ()) + (("master",) if mode == "master" else ())
+    for t in range(1, 11):
+        gl = [rnd(*p.shape, std=1e-3) for p in ps]                    # contiguous values
+        ps[0].grad = transposed(gl[0])                                # staged
+        ps[1].grad = gl[1].clone()                                    # p staged, g not
+        ps[2].grad = gl[2].clone() if t % 2 else torch.empty_like(ps[2]).copy_(gl[2])   # staged on odd t
+        ps[3].grad = transposed(gl[3])                                # both staged
+        ps[4].grad = gl[4].clone()
+        clip = t in (5, 7, 9)
+        if clip:
+            opt.clip_grad_norm_(1e-3)
+            coef = opt._pending_clip[2][1]
+            assert float(coef) < 1.0
+            gl = [(g.float() * coef).to(dt) for g in gl]              # _foreach_mul_(grads, coef)
+        for q, g in zip(twins, gl):
+            q.grad = torch.empty_like(q).copy_(g)
         opt.step()
-    gapped = torch.nn.Parameter(torch.zeros(10, 8, device=DEV)[:, :4])
-    gapped.grad = torch.zeros_like(gapped)
-    opt2 = (adana_amd.DANA_STAR_MK4 if star else adana_amd.ADana)([gapped], **hp)
-    with pytest.raises(NotImplementedError, match="gaps"):
-        opt2.step()
+        ref.step()
+        torch.cuda.synchronize()
+        for i, (p, q) in enumerate(zip(ps, twins)):
+            tag = f"t={t} tensor {i} shape {tuple(p.shape)} strides {p.stride()}"
+            assert torch.equal(_bits(p), _bits(q)), tag
+            for k in keys:
+                assert same_layout_as(opt.state[p][k], ref.state[q][k]), f"{tag} {k}"
+                assert torch.equal(_bits(opt.state[p][k]), _bits(ref.state[q][k])), f"{tag} {k}"
+            for k in adana_amd.optim.DIAG_KEYS:
+                assert torch.equal(_bits(opt.state[p][k]), _bits(ref.state[q][k])), f"{tag} {k}"
+            if clip:
+                assert torch.equal(_bits(p.grad), _bits(gl[i])), f"{tag} clipped grad"
+    gap0 = torch.ones_like(big0, dtype=torch.bool)
+    gap0[:, 5:21] = False
+    gap1 = torch.ones_like(big1, dtype=torch.bool)
+    gap1[::3] = False
+    assert torch.equal(big0[gap0], keep0[gap0]) and torch.equal(big1[gap1], keep1[gap1])
+    assert not torch.equal(big0[~gap0], keep0[~gap0])                # the slice itself was stepped
+    shared = torch.nn.Parameter(torch.zeros(1, 8, dtype=dt, device=DEV).expand(4, 8))
+    shared.grad = torch.zeros(4, 8, dtype=dt, device=DEV)
+    with pytest.raises(NotImplementedError, match="share memory"):
+        cls([shared], **hp).step()
+
+
+def same_layout_as(a: torch.Tensor, b: torch.Tensor) -> bool:
+    return a.shape == b.shape and a.stride() == b.stride()
 
 
 def test_step_hooks_profiler_and_scheduler():

@@ -533,9 +533,47 @@ def test_rebound_parameter_of_another_shape_raises():
         ls.states = [{"m": torch.zeros(6), "v": torch.zeros(6), "tau": torch.zeros(6)},
                      {"m": torch.zeros(2, 3), "v": torch.zeros(2, 3), "tau": torch.zeros(2, 3)}]
         opt._check_state_shapes(ls)                       # shapes agree: no error
+        ps[1].data = torch.zeros(3, 2).t()
+        opt._check_state_shapes(ls)                       # another layout of the shape: staged
+        ps[1].data = torch.zeros(1, 3).expand(2, 3)
+        with pytest.raises(NotImplementedError, match="share memory"):
+            opt._check_state_shapes(ls)
         ps[1].data = torch.zeros(3, 3)
         with pytest.raises(RuntimeError, match="must match the size"):
             opt._check_state_shapes(ls)
+
+
+def test_staging_decisions():
+    """The descriptor rows of a launch set point at the state's layout: a
+    parameter or gradient whose strides differ from its state's is given a
+    staging buffer of the state's shape, strides and its own dtype, kept
+    (same address) while it still fits; tensors of the state's layout are
+    used in place.  Host tensors only (no launch)."""
+    import adana_amd
+    from adana_amd.optim import _LaunchSet
+
+    big = torch.zeros(12, 40)
+    ps = [torch.nn.Parameter(big[:, 5:21]), torch.nn.Parameter(torch.zeros(9, 7).t()),
+          torch.nn.Parameter(torch.zeros(50))]
+    opt = adana_amd.ADana(ps, lr=1e-3)
+    ls = _LaunchSet(torch.device("cpu"), 0, 0)
+    ls.params = ps
+    ls.states = [{"m": torch.zeros_like(p), "v": torch.zeros_like(p)} for p in ps]
+    ls.sclass = [0, 0, 0]
+    assert ls.states[0]["m"].is_contiguous() and ls.states[1]["m"].stride() == ps[1].stride()
+    ls.grads = [torch.zeros(16, 12).t(), torch.zeros(7, 9), torch.zeros(50)]
+    d = opt._desc_rows(ls)
+    assert [j for j, _, _ in ls.stage] == [0, 1]
+    (_, p0, g0), (_, p1, g1) = ls.stage
+    assert p0.is_contiguous() and p0.shape == ps[0].shape and g0.is_contiguous()   # gapped p, transposed g
+    assert p1 is None and g1.stride() == ps[1].stride()                            # contiguous g of a permuted p
+    assert int(d["param"][0]) == p0.data_ptr() and int(d["grad"][0]) == g0.data_ptr()
+    assert int(d["param"][1]) == ps[1].data_ptr() and int(d["grad"][1]) == g1.data_ptr()
+    assert int(d["param"][2]) == ps[2].data_ptr() and int(d["grad"][2]) == ls.grads[2].data_ptr()
+    ls.grads = [torch.zeros(12, 16), torch.zeros(9, 7).t(), torch.zeros(50)]
+    opt._desc_rows(ls)
+    assert [(j, ps_ is not None, gs is not None) for j, ps_, gs in ls.stage] == [(0, True, False)]
+    assert ls.stage[0][1] is p0                                                    # the same buffer
 
 
 def test_dense_layouts():
@@ -549,6 +587,10 @@ def test_dense_layouts():
     assert dense_layout(torch.from_numpy(np.zeros((0,), np.float32)))          # stride 0, no elements
     assert dense_layout(torch.zeros(5, 1, 3)[:, :, :])
     assert not dense_layout(a[:, :2]) and not dense_layout(a.expand(2, 3, 4)) and not dense_layout(a[::2])
+    from adana_amd._layout import no_overlap
+    assert no_overlap(a) and no_overlap(a.t()) and no_overlap(a[:, :2]) and no_overlap(a[::2])
+    assert no_overlap(torch.zeros(20, 30).t()[2:17]) and no_overlap(torch.zeros(3, 1, 4)[:, :, ::3])
+    assert not no_overlap(a.expand(2, 3, 4)) and not no_overlap(torch.zeros(4).as_strided((3, 2), (1, 1)))
     assert same_layout(a.t(), torch.ones(3, 4).t())
     assert not same_layout(a.t(), a.t().contiguous())
     assert same_layout(torch.zeros(3, 1), torch.zeros(1, 3).t())               # size-1 dims' strides ignored
