@@ -143,6 +143,24 @@ class _DanaFamily(Optimizer):
         self._diag_cache = None
         _lib.lib()  # fail at construction, not at the first step, without the kernel library
 
+    # -- pickling and deepcopy --------------------------------------------
+    # torch.optim.Optimizer pickles only defaults, state and param_groups, so
+    # the constructor's instance attributes (self.lr, self.kappa, ...) would
+    # be lost and the copy's first step() would fail.  They travel with the
+    # rest; the device tables, launch sets and caches are rebuilt by the
+    # copy's first step() (its state tensors are its own, not slab views).
+    def __getstate__(self):
+        state = super().__getstate__()
+        state["_config"] = {k: v for k, v in vars(self).items() if not k.startswith("_") and k not in state}
+        return state
+
+    def __setstate__(self, state):
+        config = state.pop("_config", None)
+        super().__setstate__(state)
+        if config is not None:
+            self.__dict__.update(config)
+            self._engine_init(self.master_weights, self.fresh_diagnostics)
+
     # -- state ------------------------------------------------------------
     def _state_families(self, p: torch.Tensor):
         fams = list(self._KEYS[:3 if self._STAR else 2])

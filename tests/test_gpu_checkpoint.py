@@ -12,7 +12,9 @@ restores ``opt.state_dict()``):
     bit-identically;
   * a reference checkpoint (fp32 moments, no master copy) loads into the bf16
     master-weights extension and continues as the oracle does from the same
-    state.
+    state;
+  * a deepcopy of a stepped optimizer keeps its configuration and steps on
+    its own tensors, bit-identically to the original.
 """
 import io
 import math
@@ -219,6 +221,49 @@ def test_state_tensors_have_own_storages_in_family_slabs():
     buf = io.BytesIO()
     torch.save(opt.state_dict(), buf)
     assert len(buf.getvalue()) < 3 * 4 * sum(p.numel() for p in params) + 200_000
+
+
+@pytest.mark.parametrize("star", [False, True])
+def test_deepcopy_of_a_stepped_optimizer_steps_on_its_own(star):
+    """copy.deepcopy of an optimizer after 3 steps copies its parameters and
+    state and keeps its configuration (torch.optim.Optimizer alone would drop
+    self.lr and the rest, and the copy's step() would fail); the copy then
+    steps on its own tensors, bit-identically to the original fed the same
+    gradients, and leaves the original's tensors untouched."""
+    import copy
+    import adana_amd
+
+    print("case: deepcopy of a stepped optimizer, star", star, flush=True)
+    torch.manual_seed(5)
+    params = [torch.nn.Parameter(torch.randn(s, device=DEV) * 0.02) for s in [(300, 7), (5,), (70000,)]]
+    cls = adana_amd.DANA_STAR_MK4 if star else adana_amd.ADana
+    opt = cls(params, lr=1e-3, kappa=0.85, clipsnr=2.0, weight_decay=0.1)
+    for _ in range(3):
+        for p in params:
+            p.grad = torch.randn_like(p) * 1e-3
+        opt.step()
+    twin = copy.deepcopy(opt)
+    tparams = twin.param_groups[0]["params"]
+    assert all(a is not b and torch.equal(a, b) for a, b in zip(params, tparams))
+    keys = ("m", "v") + (("tau",) if star else ())
+    for _ in range(6):
+        grads = [torch.randn_like(p) * 1e-3 for p in params]
+        for p, q, g in zip(params, tparams, grads):
+            p.grad, q.grad = g.clone(), g.clone()
+        opt.step()
+        before = [p.detach().clone() for p in params]
+        twin.step()
+        torch.cuda.synchronize()
+        for p, q, b in zip(params, tparams, before):
+            assert torch.equal(p, b)                               # the original is not touched
+            assert torch.equal(p, q)
+            for k in keys:
+                assert opt.state[p][k].data_ptr() != twin.state[q][k].data_ptr()
+                assert torch.equal(opt.state[p][k], twin.state[q][k])
+            assert opt.state[p]["step"] == twin.state[q]["step"]
+            for k in adana_amd.optim.DIAG_KEYS:
+                assert torch.equal(opt.state[p][k], twin.state[q][k]) or (
+                    opt.state[p][k].isnan() and twin.state[q][k].isnan())
 
 
 def test_diagnostics_have_own_storages_and_stay_live():

@@ -594,3 +594,26 @@ def test_dense_layouts():
     assert same_layout(a.t(), torch.ones(3, 4).t())
     assert not same_layout(a.t(), a.t().contiguous())
     assert same_layout(torch.zeros(3, 1), torch.zeros(1, 3).t())               # size-1 dims' strides ignored
+
+
+def test_deepcopy_and_pickle_keep_the_configuration():
+    """torch.optim.Optimizer pickles only defaults, state and param_groups;
+    the constructor's instance attributes (self.lr, self.kappa, ...)
+    travel too, so a deepcopy or an unpickled optimizer can step, and its
+    engine caches start empty.  Host tensors only (no step)."""
+    import copy
+    import pickle
+
+    import adana_amd
+
+    for cls, kw in ((adana_amd.ADana, dict(kappa=0.7, clipsnr=2.0)),
+                    (adana_amd.DANA_STAR_MK4, dict(kappa=0.6, clipsnr=3.0, wd_ts=5.0))):
+        opt = cls([torch.nn.Parameter(torch.zeros(3))], lr=2e-3, fresh_diagnostics=False, **kw)
+        for other in (copy.deepcopy(opt), pickle.loads(pickle.dumps(opt))):
+            for k, v in vars(opt).items():
+                if not k.startswith("_"):
+                    assert k in vars(other), (cls.__name__, k)
+                    if k not in ("state", "param_groups", "defaults"):   # torch's __setstate__ adds to defaults
+                        assert getattr(other, k) == v, (cls.__name__, k)
+            assert other._sets is None and other._active is None and other._diag_loc == {}
+            assert other.param_groups[0]["params"][0] is not opt.param_groups[0]["params"][0]
