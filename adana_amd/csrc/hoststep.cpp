@@ -446,6 +446,10 @@ PyObject *bind_diag(PyObject *, PyObject *args) {
                 long col;
                 PyObject *key;
                 if (!PyArg_ParseTuple(ck, "lO", &col, &key)) return nullptr;
+                if (col < 0 || col >= 5) {
+                    PyErr_SetString(PyExc_ValueError, "bind_diag: column out of range [0, 5)");
+                    return nullptr;
+                }
                 at::Tensor t = at::from_blob(base + es * (5 * j + col), at::IntArrayRef{}, [keep](void *) {}, opts);
                 PyObject *w = THPVariable_Wrap(std::move(t));
                 if (!w) return nullptr;

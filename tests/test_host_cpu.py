@@ -617,3 +617,27 @@ def test_deepcopy_and_pickle_keep_the_configuration():
                         assert getattr(other, k) == v, (cls.__name__, k)
             assert other._sets is None and other._active is None and other._diag_loc == {}
             assert other.param_groups[0]["params"][0] is not opt.param_groups[0]["params"][0]
+
+
+def test_bind_diag_entries():
+    """_hoststep.bind_diag binds states[j][key] to a 0-d tensor over element
+    5 * j + col of the buffer, each with a 4-byte storage of its own that
+    keeps the buffer alive; a column outside [0, 5), a buffer shorter than 5
+    per state, and non-dict states are refused."""
+    from adana_amd import _hoststep
+
+    buf = torch.arange(10, dtype=torch.float32)
+    states = [{}, {}]
+    _hoststep.bind_diag(buf, states, [(0, "a"), (4, "e")])
+    assert [float(s[k]) for s in states for k in ("a", "e")] == [0.0, 4.0, 5.0, 9.0]
+    t = states[1]["e"]
+    assert t.dim() == 0 and t.untyped_storage().nbytes() == 4 and t.data_ptr() == buf.data_ptr() + 4 * 9
+    buf[9] = 42.0
+    del buf
+    assert float(t) == 42.0
+    with pytest.raises(ValueError, match="column"):
+        _hoststep.bind_diag(torch.zeros(10), [{}, {}], [(5, "x")])
+    with pytest.raises(ValueError, match="too small"):
+        _hoststep.bind_diag(torch.zeros(9), [{}, {}], [(0, "x")])
+    with pytest.raises(TypeError, match="dicts"):
+        _hoststep.bind_diag(torch.zeros(10), [{}, 3], [(0, "x")])
