@@ -835,26 +835,48 @@ __global__ __launch_bounds__(kChunk / VEC) void mta_step_kernel(const adana_tens
     float4 *part4 = reinterpret_cast<float4 *>(partials);
     // the combine kernel's per-tensor arrival counters start at zero
     for (int64_t k = chunk * kThreads + tid; k < n; k += static_cast<int64_t>(gridDim.x) * kThreads) counters[k] = 0;
+    // A compiler-only barrier (no instruction).  Measured, not derived: with
+    // it the compiler loads the gradient scale with a vector load and orders
+    // the ADana instances' arithmetic differently, and in a same-process A/B
+    // the 51M-param Dana-MK4 list stepped 3.5-4% faster and the bf16-master
+    // ADana list 1.3% faster; the Dana-Star lists did not move.
+    asm volatile("" ::: "memory");
     const float gs = pack.gscale != nullptr ? *pack.gscale : 1.0f;
     PowTab tab{adana::kLog, adana::kExp2J, pack.pow16};
-    if constexpr (STAR && pow_tables(POWK)) {
-        static_assert(kThreads >= 256, "one thread per table entry");
-        __shared__ adana::LogPair s_log[128];
-        __shared__ double s_exp2j[128];
-        if (tid < 128) {
-            s_log[tid] = adana::kLog[tid];
-        } else if (tid < 256) {
-            s_exp2j[tid - 128] = adana::kExp2J[tid - 128];
-        }
-        __syncthreads();
-        tab = PowTab{s_log, s_exp2j, nullptr};
+    // Dana-Star's binary64 pow reads its tables from LDS.  The 3 KB are 192
+    // 16-byte words (kLog, then kExp2J), one per thread of the first 192; the
+    // loads are issued here and the words written to LDS only after the
+    // chunk's descriptor loads below are issued, so the two round trips
+    // overlap.  (Writing them after the streaming loads instead, with the
+    // barrier between those loads and the arithmetic, cost the 10,000-tensor
+    // list 8%.)
+    constexpr bool kTab = STAR && pow_tables(POWK);
+    constexpr int kTabWords = 192;
+    static_assert(!kTab || kThreads >= kTabWords, "one thread per table word");
+    static_assert(sizeof(adana::kLog) == 128 * 16 && sizeof(adana::kExp2J) == 64 * 16, "table layout");
+    __shared__ uint4 s_tab[kTab ? kTabWords : 1];
+    uint4 tab_word{};
+    if constexpr (kTab) {
+        if (tid < 128)
+            tab_word = reinterpret_cast<const uint4 *>(adana::kLog)[tid];
+        else if (tid < kTabWords)
+            tab_word = reinterpret_cast<const uint4 *>(adana::kExp2J)[tid - 128];
+        tab = PowTab{reinterpret_cast<const adana::LogPair *>(s_tab), reinterpret_cast<const double *>(s_tab + 128),
+                     nullptr};
     }
 
     const int i0 = chunk_first[chunk];
     const int64_t vs0 = vstart[i0];
     const adana_tensor_desc d0 = desc[i0];
     float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-    if (vs0 <= lo && vs0 + d0.numel >= hi) {
+    // both bounds at once (no short circuit), so that the descriptor's numel
+    // is fetched with the rest of it rather than after a branch
+    const bool inside = (vs0 <= lo) & (vs0 + d0.numel >= hi);
+    if constexpr (kTab) {
+        if (tid < kTabWords) s_tab[tid] = tab_word;
+        __syncthreads();
+    }
+    if (inside) {
         // the whole chunk lies in tensor i0
         thread_elems<STAR, GBF16, PM, POWK, VEC, true>(d0, mine - vs0, vs0 + d0.numel - mine, lo - vs0, pack, gs,
                                                           tab, acc);
