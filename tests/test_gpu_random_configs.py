@@ -12,7 +12,8 @@ gradients None (that tensor skips the step and keeps its state), and checks
 every step against the oracle (src/optim/adana.py:101-153,
 src/optim/dana_star_mk4.py:137-203) to the bars of test_gpu_parity.py: m, v
 and tau bit-exact, p bit-exact (Dana-Star: at most 2 hard-case elements per
-tensor, within 2 scaled ulp), diagnostics rtol 1e-5.
+tensor, within 2 scaled ulp), diagnostics rtol 1e-5.  A second sweep runs
+the same draws on the reference's own bfloat16 path.
 """
 import numpy as np
 import pytest
@@ -86,3 +87,65 @@ def test_random_configuration(oracle_mod, seed):
             grads.append(gs)
         pair.step(grads)
         pair.compare(where=f"seed {seed} k={k}")
+
+
+@pytest.mark.parametrize("seed", range(24))
+def test_random_configuration_bf16_state(oracle_mod, seed):
+    """The same draws on the reference's own bfloat16 path (bfloat16
+    parameters, m, v, tau; every op rounded to bfloat16), against the
+    oracle's bfloat16 restatement to the bars of test_gpu_bf16.py: m, v, tau
+    bit-exact, p bit-exact (Dana-Star: at most 2 elements per tensor within 1
+    bfloat16 ulp), diagnostics within 1 bfloat16 ulp."""
+    import adana_amd
+    from test_gpu_bf16 import _bits, _check, _diag_close, _to_gpu16
+    from test_gpu_parity import STAR_HARD_CASES
+
+    O = oracle_mod
+    rng, star, _, groups, hp = _draw(100 + seed)
+    shapes = [s for ss, _ in groups for s in ss]
+    print(f"case: random bf16-state configuration seed {seed}: star {star} groups {len(groups)} "
+          f"tensors {len(shapes)} elements {sum(int(np.prod(s)) for s in shapes)} {hp}", flush=True)
+    host = [[O.f32_to_bf16(_normal(rng, s, 0.02)) for s in ss] for ss, _ in groups]
+    gpu = [[torch.nn.Parameter(_to_gpu16(h)) for h in hs] for hs in host]
+    cls = adana_amd.DANA_STAR_MK4 if star else adana_amd.ADana
+    opt = cls([dict(params=ps, **gkw) for ps, (_, gkw) in zip(gpu, groups)], **hp)
+    orc = O.OracleOptimizer(
+        groups=[O.OracleGroup(params=hs, lr=gkw["lr"], delta=gkw["delta"], epsilon=gkw["epsilon"],
+                              weight_decay=gkw["weight_decay"]) for hs, (_, gkw) in zip(host, groups)],
+        star=star, peak_lr=hp["lr"], kappa=hp["kappa"], clipsnr=hp["clipsnr"], wd_decaying=hp["wd_decaying"],
+        wd_ts=hp["wd_ts"], gamma_3_factor=hp["gamma_3_factor"], bf16=True)
+    keys = ("m", "v", "tau") if star else ("m", "v")
+    for k in range(7):
+        for g, og, (_, gkw) in zip(opt.param_groups, orc.groups, groups):
+            g["lr"] = og.lr = gkw["lr"] * float(rng.uniform(0.5, 1.5))
+        grads = []
+        for ps, ss in zip(gpu, (ss for ss, _ in groups)):
+            gs = []
+            for p, s in zip(ps, ss):
+                u = rng.random()
+                if u < 0.12:
+                    p.grad = None
+                    gs.append(None)
+                    continue
+                g = _normal(rng, s, float(10 ** rng.uniform(-5, -1)))
+                g16 = O.f32_to_bf16(np.zeros_like(g) if u < 0.18 else g)
+                p.grad = _to_gpu16(g16)
+                gs.append(g16)
+            grads.append(gs)
+        opt.step()
+        orc.step(grads)
+        torch.cuda.synchronize()
+        for gi, (ps, hs) in enumerate(zip(gpu, host)):
+            for pi, (p, h) in enumerate(zip(ps, hs)):
+                st, ost = opt.state[p], orc.state.get(id(h))
+                tag = f"seed {seed} k={k} group {gi} tensor {pi} shape {h.shape}"
+                if ost is None:
+                    assert len(st) == 0, tag
+                    continue
+                assert st["step"] == ost["step"], tag
+                for key in keys:
+                    _check(_bits(st[key]), ost[key], f"{tag} {key}")
+                got = _bits(p)
+                _check(got, h, f"{tag} p", STAR_HARD_CASES if star else 0)
+                h[...] = got.reshape(h.shape)
+                _diag_close([float(st[key]) for key in O.DIAG_KEYS], [float(ost[key]) for key in O.DIAG_KEYS], tag)
