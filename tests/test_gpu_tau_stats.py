@@ -287,3 +287,59 @@ def test_compaction_with_special_values_and_shuffled_ranks():
     tx = (x.size + 65535) // 65536
     assert np.all(meta[:tx] != 0), "special values: every tile compacted"
     assert np.all(meta[tx:] != 0), "shuffled ranks: every tile compacted"
+
+
+def _random_values(rng, n):
+    kind = int(rng.integers(7))
+    if kind == 0:
+        x = rng.random(n)
+    elif kind == 1:
+        x = rng.normal(0, float(10 ** rng.uniform(-3, 3)), n)
+    elif kind == 2:
+        x = 1.0 + rng.normal(0, 1e-6, n)                          # one narrow cluster
+    elif kind == 3:
+        x = rng.integers(0, int(rng.integers(1, 20)), n) / 7.0    # few distinct values
+    elif kind == 4:
+        x = rng.beta(2, 5, n)
+    elif kind == 5:
+        x = 10.0 ** rng.uniform(-40, 38, n) * rng.choice([-1.0, 1.0], n)
+    else:
+        x = np.sort(rng.random(n))                                 # sorted: values crowd into few tiles
+    x = x.astype(np.float32)
+    if n and rng.random() < 0.4:                                   # sprinkle special values
+        for v in (np.nan, np.inf, -np.inf, 0.0, -0.0, 1e-42, -1e-42):
+            x[rng.integers(0, n, int(rng.integers(0, 4)))] = v
+    return x
+
+
+@pytest.mark.parametrize("seed", range(24))
+def test_random_lists_and_ranks(seed):
+    """Seeded random tensor lists (0 to 400,000 elements; uniform, normal,
+    one narrow cluster, few distinct values, beta, 78 decades of both signs,
+    sorted; NaN, infinities, signed zeros and denormals sprinkled in) and rank
+    sets (sorted and distinct, or shuffled with repeats; up to 600 per
+    tensor), with and without compaction: every value equals
+    np.sort(x)[rank]."""
+    from adana_amd import tau_stats
+
+    rng = np.random.default_rng(5000 + seed)
+    xs, ranks = [], []
+    for _ in range(int(rng.integers(1, 11))):
+        u = rng.random()
+        n = 0 if u < 0.08 else int(rng.integers(1, 50)) if u < 0.3 else int(np.exp(rng.uniform(np.log(50), np.log(400_000))))
+        xs.append(_random_values(rng, n))
+        if n == 0:
+            ranks.append(np.zeros(0, np.int64))
+            continue
+        k = int(rng.integers(1, min(n, 600) + 1))
+        if rng.random() < 0.5:
+            r = np.sort(rng.choice(n, k, replace=False))
+        else:
+            r = rng.integers(0, n, k)
+        ranks.append(r.astype(np.int64))
+    compact = bool(rng.integers(2))
+    print(f"case: random order statistics seed {seed}: {len(xs)} tensors, sizes {[x.size for x in xs]}, "
+          f"compact {compact}", flush=True)
+    got = tau_stats.order_values([torch.from_numpy(x).to(DEV) for x in xs], ranks, compact=compact)
+    for i, (x, r, g) in enumerate(zip(xs, ranks, got)):
+        assert _same(g, np.sort(x)[r]), f"seed {seed} tensor {i} (n={x.size}, {r.size} ranks)"
