@@ -13,7 +13,8 @@ every step against the oracle (src/optim/adana.py:101-153,
 src/optim/dana_star_mk4.py:137-203) to the bars of test_gpu_parity.py: m, v
 and tau bit-exact, p bit-exact (Dana-Star: at most 2 hard-case elements per
 tensor, within 2 scaled ulp), diagnostics rtol 1e-5.  A second sweep runs
-the same draws on the reference's own bfloat16 path.
+the same draws on the reference's own bfloat16 path, a third with
+clip_grad_norm_ fused into every step.
 """
 import numpy as np
 import pytest
@@ -149,3 +150,36 @@ def test_random_configuration_bf16_state(oracle_mod, seed):
                 _check(got, h, f"{tag} p", STAR_HARD_CASES if star else 0)
                 h[...] = got.reshape(h.shape)
                 _diag_close([float(st[key]) for key in O.DIAG_KEYS], [float(ost[key]) for key in O.DIAG_KEYS], tag)
+
+
+@pytest.mark.parametrize("seed", range(16))
+def test_random_configuration_with_clipping(oracle_mod, seed):
+    """The same draws (fp32 or bf16 master) with clip_grad_norm_ through the
+    optimizer before every step, its scaling fused into the step: max_norm
+    drawn around the gradients' norm (clipping or not), the clipped gradient
+    written back or not; the total norm, the written-back gradients and the
+    step checked against the oracle's clip (torch's formula) and step."""
+    from test_gpu_clip import _clipped_pair_step
+
+    O = oracle_mod
+    rng, star, master, groups, hp = _draw(200 + seed)
+    if sum(int(np.prod(s)) for ss, _ in groups for s in ss) == 0:
+        groups[0][0].append((100,))                      # something to clip
+    write_back = bool(rng.integers(2))
+    print(f"case: random clipped configuration seed {seed}: star {star} master {master} "
+          f"write_back {write_back} {hp}", flush=True)
+
+    def param(s):
+        x = _normal(rng, s, 0.02)
+        return O.f32_to_bf16(x) if master else x
+
+    pair = Pair(O, star, [([param(s) for s in ss], gkw) for ss, gkw in groups], master=master, **hp)
+    for k in range(5):
+        std = float(10 ** rng.uniform(-4, -1))
+        grads = [[_normal(rng, s, std) for s in ss] for ss, _ in groups]
+        norm = float(np.sqrt(sum(float(np.sum(np.square(g, dtype=np.float64))) for gs in grads for g in gs)))
+        max_norm = max(norm, 1e-12) * float(10 ** rng.uniform(-1, 0.5))
+        if master:
+            grads = [[O.f32_to_bf16(g).reshape(g.shape) for g in gs] for gs in grads]
+        _clipped_pair_step(pair, O, grads, max_norm, write_back, bf16=master)
+        pair.compare(where=f"seed {seed} k={k}")
