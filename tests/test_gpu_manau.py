@@ -261,3 +261,57 @@ def test_manau_pow_kinds(oracle_mod, kappa, mk4):
             got = [float(st[key]) for key in ("current_alpha_factor", "gradient_norm", "auto_factor_mean", "m_norm")]
             ref = [ost[key] for key in ("current_alpha_factor", "gradient_norm", "auto_factor_mean", "m_norm")]
             np.testing.assert_allclose(got, ref, rtol=1e-5, atol=1e-30, err_msg=tag)
+
+
+@pytest.mark.parametrize("seed", range(12))
+def test_manau_random_configuration(oracle_mod, seed):
+    """Seeded random Dana-branch configurations: an embedding matrix and 1-6
+    vectors (1 to 70,000 elements), kappa from every pow kind's values, mk4A,
+    mk4B, clipsnr, delta, weight_time, dana_momentum, decaying weight decay,
+    a new lr every step and some all-zero gradients; 8 steps against the
+    oracle as above."""
+    import contextlib
+
+    import adana_amd
+
+    O = oracle_mod
+    rng = np.random.default_rng(7000 + seed)
+    shapes = [(int(rng.integers(1, 200)), int(rng.integers(1, 64)))]
+    shapes += [(int(np.exp(rng.uniform(0, np.log(70000)))),) for _ in range(int(rng.integers(1, 7)))]
+    names = ["transformer.wte.weight"] + [f"h.{i}.ln.weight" for i in range(len(shapes) - 1)]
+    kw = dict(lr=float(10 ** rng.uniform(-3, -1.5)), weight_decay=float(rng.choice([0.0, 0.1])),
+              kappa=float(rng.choice([0.0, 0.5, 0.85, 1.0, 2.0])), clipsnr=float(rng.choice([0.5, 1.0, 2.0])),
+              delta=float(rng.choice([2.0, 4.0, 8.0])), mk4A=float(rng.choice([0.0, 0.1])),
+              mk4B=float(rng.choice([0.0, 0.2])), weight_time=bool(rng.integers(2)),
+              dana_momentum=bool(rng.integers(2)), wd_decaying=bool(rng.integers(2)),
+              wd_ts=float(rng.choice([1.0, 3.0])))
+    print(f"case: Manau random configuration seed {seed}: shapes {shapes} {kw}", flush=True)
+    p0 = [rng.normal(0, 0.02, s).astype(np.float32) for s in shapes]
+    params = [torch.nn.Parameter(torch.from_numpy(x.copy()).to(DEV)) for x in p0]
+    with contextlib.redirect_stdout(io.StringIO()):
+        opt = adana_amd.Manau([{"params": params, "param_names": names}], **kw)
+    host = [x.copy() for x in p0]
+    okw = {k: v for k, v in kw.items() if k != "lr"}
+    orc = O.OracleManau(groups=[O.OracleManauGroup(params=host, use_muon=[False] * len(host), lr=kw["lr"],
+                                                   **okw)], peak_lr=kw["lr"])
+    for k in range(1, 9):
+        opt.param_groups[0]["lr"] = orc.groups[0].lr = kw["lr"] * float(rng.uniform(0.5, 1.5))
+        gs = [(np.zeros(s, np.float32) if rng.random() < 0.1 else
+               rng.normal(0, float(10 ** rng.uniform(-5, -2)), s).astype(np.float32)) for s in shapes]
+        for p, g in zip(params, gs):
+            p.grad = torch.from_numpy(g.copy()).to(DEV)
+        prev = [x.copy() for x in host]
+        opt.step()
+        orc.step([gs])
+        torch.cuda.synchronize()
+        for i, p in enumerate(params):
+            st, ost = opt.state[p], orc.state[id(host[i])]
+            tag = f"seed {seed} t={k} tensor {i}"
+            for key in ("dana_m", "dana_v", "dana_tau"):
+                assert ulp_diff(st[key].cpu().numpy(), ost[key]).max() == 0, f"{tag} {key}"
+            gp = p.detach().cpu().numpy()
+            _check_star_p(gp, host[i], prev[i], tag)
+            host[i][...] = gp
+            got = [float(st[key]) for key in ("current_alpha_factor", "gradient_norm", "auto_factor_mean", "m_norm")]
+            ref = [ost[key] for key in ("current_alpha_factor", "gradient_norm", "auto_factor_mean", "m_norm")]
+            np.testing.assert_allclose(got, ref, rtol=1e-5, atol=1e-30, equal_nan=True, err_msg=tag)
