@@ -150,6 +150,10 @@ class _DanaFamily(Optimizer):
     # rest; the device tables, launch sets and caches are rebuilt by the
     # copy's first step() (its state tensors are its own, not slab views).
     def __getstate__(self):
+        # a clip deferred to the next step() is applied to the gradients now,
+        # as torch's in-place clipping would have left them, so that a copy
+        # (whose engine starts empty) steps on the clipped gradients too
+        self.flush_clip()
         state = super().__getstate__()
         state["_config"] = {k: v for k, v in vars(self).items() if not k.startswith("_") and k not in state}
         return state

@@ -227,9 +227,11 @@ def test_state_tensors_have_own_storages_in_family_slabs():
 def test_deepcopy_of_a_stepped_optimizer_steps_on_its_own(star):
     """copy.deepcopy of an optimizer after 3 steps copies its parameters and
     state and keeps its configuration (torch.optim.Optimizer alone would drop
-    self.lr and the rest, and the copy's step() would fail); the copy then
-    steps on its own tensors, bit-identically to the original fed the same
-    gradients, and leaves the original's tensors untouched."""
+    self.lr and the rest, and the copy's step() would fail); a clip pending
+    at the copy is applied to the original's gradients first (a Parameter's
+    copy has no gradient); the copy then steps on its own tensors,
+    bit-identically to the original fed the same gradients, and leaves the
+    original's tensors untouched."""
     import copy
     import adana_amd
 
@@ -242,9 +244,19 @@ def test_deepcopy_of_a_stepped_optimizer_steps_on_its_own(star):
         for p in params:
             p.grad = torch.randn_like(p) * 1e-3
         opt.step()
+    for p in params:                                   # a clip pending when the copy is taken
+        p.grad = torch.randn_like(p) * 1e-1
+    opt.clip_grad_norm_(1e-3)
     twin = copy.deepcopy(opt)
     tparams = twin.param_groups[0]["params"]
     assert all(a is not b and torch.equal(a, b) for a, b in zip(params, tparams))
+    assert opt._pending_clip is None and all(q.grad is None for q in tparams)  # Parameter copies drop grads
+    for p, q in zip(params, tparams):
+        q.grad = p.grad.clone()                           # the clipped gradients
+    opt.step()
+    twin.step()
+    torch.cuda.synchronize()
+    assert all(torch.equal(p, q) for p, q in zip(params, tparams))
     keys = ("m", "v") + (("tau",) if star else ())
     for _ in range(6):
         grads = [torch.randn_like(p) * 1e-3 for p in params]
