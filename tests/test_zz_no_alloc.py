@@ -99,6 +99,13 @@ def test_noalloc_matches_workspace_entry_point():
     for t in (1, 2):
         small.step(t)
         small.assert_equal(f"small t={t}")
+    print("case: adana_mta_step_noalloc, 2,000 small Dana-Star tensors (shared chunks, direct combine)",
+          flush=True)
+    sizes = np.exp(np.random.default_rng(13).uniform(0, np.log(5000), 2000)).astype(np.int64).tolist()
+    many = _List(sizes, star=True, seed=13)
+    for t in (1, 2):
+        many.step(t)
+        many.assert_equal(f"many t={t}")
 
 
 def test_noalloc_rejects_lists_beyond_its_scratch():
