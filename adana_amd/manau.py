@@ -116,8 +116,10 @@ class Manau(_DanaFamily):
     def _routes(group):
         """(name, parameter, goes to Muon) for every parameter of a group:
         matrices go to Muon unless their name marks an embedding or the head
-        (src/optim/manau.py:176-196).  A parameter past the end of the group's
-        name list keeps the previous name, as in the reference."""
+        (src/optim/manau.py:176-196).  Only a parameter with a name of its own
+        can be marked by it: one past the end of the group's name list goes to
+        Muon if it is a matrix (manau.py:185-190), and the printed report shows
+        it under the previous name, as the reference's does."""
         names = group.get("param_names")
         if names is None:
             raise ValueError("Manau: every parameter group needs a 'param_names' list (one name per "
@@ -125,8 +127,9 @@ class Manau(_DanaFamily):
         name = ""
         out = []
         for i, p in enumerate(group["params"]):
-            name = names[i] if i < len(names) else name
-            dana_by_name = any(marker in name for marker in _DANA_NAME_MARKERS)
+            named = i < len(names)
+            name = names[i] if named else name
+            dana_by_name = named and any(marker in name for marker in _DANA_NAME_MARKERS)
             out.append((name, p, p.ndim >= 2 and not dana_by_name))
         return out
 

@@ -150,20 +150,35 @@ class _DanaFamily(Optimizer):
     # rest; the device tables, launch sets and caches are rebuilt by the
     # copy's first step() (its state tensors are its own, not slab views).
     def __getstate__(self):
-        # a clip deferred to the next step() is applied to the gradients now,
-        # as torch's in-place clipping would have left them, so that a copy
-        # (whose engine starts empty) steps on the clipped gradients too
-        self.flush_clip()
+        # A clip deferred to the next step() must reach the copy too.  With
+        # write_back it is applied to the gradients now, as torch's in-place
+        # clipping would have left them.  Without write_back the caller's
+        # gradients stay unscaled: the coefficient travels with the state and
+        # the copy defers the same scaling on its own gradients.
+        pend = self._pending_clip
+        if pend is not None and pend[3]:
+            self.flush_clip()
+            pend = None
         state = super().__getstate__()
         state["_config"] = {k: v for k, v in vars(self).items() if not k.startswith("_") and k not in state}
+        if pend is not None:
+            state["_pending_clip_coef"] = pend[2]
         return state
 
     def __setstate__(self, state):
         config = state.pop("_config", None)
+        coef = state.pop("_pending_clip_coef", None)
         super().__setstate__(state)
         if config is not None:
             self.__dict__.update(config)
             self._engine_init(self.master_weights, self.fresh_diagnostics)
+        if coef is not None:
+            params, _ = self._flat_params()
+            own = [g for g in map(_GRAD, params) if g is not None]
+            if own:                  # (nn.Parameter's deepcopy drops .grad: nothing to scale then)
+                plan = self._clip_plan(own[0].device, own[0].dtype == torch.bfloat16)
+                plan.prepare(own)
+                self._pending_clip = (own, plan, coef, False)
 
     # -- state ------------------------------------------------------------
     def _state_families(self, p: torch.Tensor):

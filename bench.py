@@ -147,10 +147,30 @@ def cpu_model() -> str:
     return f"{name}; {len(os.sched_getaffinity(0))} cores available"
 
 
-def cos_inf(k, n=200, warmup=4, final_div=0.1):
-    if k < warmup:
-        return (k + 1) / warmup
-    return final_div + (1 - final_div) * 0.5 * (1 + math.cos(math.pi * min(k - warmup, n - warmup) / (n - warmup)))
+def cos_inf_schedule(n_iterations, n_warmup, div_factor, final_div_factor, n_inf):
+    """The lr factor of the reference's ``cos_inf`` scheduler
+    (src/optim/schedule.py:70-98), restated: a linear warm-up from
+    1/div_factor to 1 over n_warmup steps, a cosine down to
+    1/(div_factor * final_div_factor) at n_iterations - n_inf, constant after.
+    src/main.py:411-423 applies it through torch.optim.lr_scheduler.LambdaLR,
+    so optimizer step k (0-based) runs at peak * factor(k)."""
+    final = 1.0 / div_factor / final_div_factor
+    n_anneal = n_iterations - n_inf
+
+    def factor(step):
+        if step < n_warmup:
+            return step / n_warmup + (1 - step / n_warmup) / div_factor
+        if step < n_anneal:
+            t = (step - n_warmup) / (n_anneal - n_warmup)
+            return final + 0.5 * (1.0 - final) * (1 + np.cos(np.pi * t))
+        return final
+
+    return factor
+
+
+# C2's scheduler: --scheduler cos_inf with 200 iterations, warm-up 200 / 50 = 4 steps,
+# div_factor 1e2, final_div_factor 1e-1 and no constant tail (scripts/launch.sh:176,311)
+C2_SCHEDULE = dict(n_iterations=200, n_warmup=4, div_factor=1e2, final_div_factor=1e-1, n_inf=0)
 
 
 def build_gpu(w, seed=0):
@@ -453,12 +473,7 @@ def stream_sweep(args):
     run over the same command can attribute every dispatch:
       * one-shot workgroups (the step's shape) at 1..8 resident workgroups per
         CU and uncapped;
-      * the wave-specialised persistent kernel (loader wave + direct-to-LDS
-        ring; stages, compute waves, workgroups per CU);
       * the same five arrays read only and four written only, and a copy;
-      * persistent workgroups (1, 2 or 4 per CU) dealt tiles grid-stride, with
-        a plain loop and a double-buffered one that issues the next tile's
-        loads before the current tile's stores;
       * then (after the separate arrays are freed) the one-shot shape at the
         step's cap of 4 with the five arrays placed in one allocation,
         ``k * (n + 4 Mi)`` floats plus ``k * skew`` bytes from its start
@@ -477,12 +492,8 @@ def stream_sweep(args):
     for name in ("adana_probe_stream_5r4w", "adana_probe_stream_5r0w", "adana_probe_stream_0r4w"):
         getattr(lib, name).argtypes = [P, I64, P, INT, P]
         getattr(lib, name).restype = INT
-    lib.adana_probe_stream_5r4w_ws.argtypes = [P, I64, P, INT, INT, INT, P]
-    lib.adana_probe_stream_5r4w_ws.restype = INT
     lib.adana_probe_copy.argtypes = [P, P, I64, P, INT, P]
     lib.adana_probe_copy.restype = INT
-    lib.adana_probe_stream_5r4w_persistent.argtypes = [P, I64, P, INT, INT, P]
-    lib.adana_probe_stream_5r4w_persistent.restype = INT
     n = 2645527040 // 1024 * 1024
     arrays = [torch.zeros(n, device="cuda:0") for _ in range(5)]
     partials = torch.empty(n // 1024 * 4, device="cuda:0")
@@ -494,9 +505,6 @@ def stream_sweep(args):
     for cap in (1, 2, 3, 4, 5, 6, 7, 8, 0):
         cfgs.append((f"5r4w one-shot cap {cap or 'none'}", 36 * n,
                      lambda cap=cap: lib.adana_probe_stream_5r4w(ptrs, n, part, cap, st)))
-    for stages, cw, g in ((3, 4, 1), (3, 4, 2), (4, 4, 1), (3, 8, 1)):
-        cfgs.append((f"5r4w wave-specialised stages {stages} compute waves {cw} wgs/CU {g}", 36 * n,
-                     lambda a=(stages, cw, g): lib.adana_probe_stream_5r4w_ws(ptrs, n, part, a[0], a[1], a[2], st)))
     for cap in (3, 4, 0):
         cfgs.append((f"5r0w read-only cap {cap or 'none'}", 20 * n,
                      lambda cap=cap: lib.adana_probe_stream_5r0w(ptrs, n, part, cap, st)))
@@ -506,10 +514,6 @@ def stream_sweep(args):
     for cap in (4, 0):
         cfgs.append((f"1r1w copy cap {cap or 'none'}", 8 * n,
                      lambda cap=cap: lib.adana_probe_copy(a0, a1, n, part, cap, st)))
-    for db in (0, 1):
-        for g in (1, 2, 4):
-            cfgs.append((f"5r4w persistent {'double-buffered' if db else 'plain'} wgs/CU {g}", 36 * n,
-                         lambda a=(g, db): lib.adana_probe_stream_5r4w_persistent(ptrs, n, part, a[0], a[1], st)))
     reps = max(2, args.steps)
     best = {}
     order = []
@@ -842,16 +846,18 @@ def main():
     n_elems = sum(p.numel() for p in params)
     bpe = bytes_per_elem(w)
     algo_bytes = n_elems * bpe
-    peak = w["hp"]["lr"]
     grad_norms = []
+    sched = None
+    if w["schedule"] == "cos_inf":
+        # src/main.py:411-423: LambdaLR sets group['lr'] = peak * factor(k) after step k
+        sched = torch.optim.lr_scheduler.LambdaLR(opt, cos_inf_schedule(**C2_SCHEDULE))
 
-    def one_step(k):
-        if w["schedule"] == "cos_inf":
-            for g in opt.param_groups:
-                g["lr"] = peak * cos_inf(k)
+    def one_step(_k):
         if w.get("clip"):
             grad_norms.append(opt.clip_grad_norm_(w["clip"]).item())   # src/optim/base.py:250-257
         opt.step()
+        if sched is not None:
+            sched.step()
 
     settle_gc()
     torch.cuda.synchronize()
@@ -953,6 +959,8 @@ def main():
                    "hyperparams": w["hp"], "master_weights": w["master"],
                    "parallelism": "single GPU",
                    **({"warmup_note": w["warmup_note"]} if "warmup_note" in w else {}),
+                   **({"lr_schedule": dict(C2_SCHEDULE, kind="cos_inf (src/optim/schedule.py:70-98)",
+                                           via="torch.optim.lr_scheduler.LambdaLR")} if sched else {}),
                    **({"grad_clip": w["clip"], "first_grad_norm": grad_norms[0]} if w.get("clip") else {})},
         "kernel_ms_per_step": round(kern_ms, 4),
         **({"host_step_ms": host} if host else {}),

@@ -16,16 +16,6 @@
 // A second kernel does the same for the bf16-master ADana step (fp32 master,
 // m, v and bf16 gradient in; fp32 master, m, v and bf16 parameter out).
 //
-// A third kernel family answers whether a different schedule of the same
-// stream could beat the one-shot workgroups: a persistent, wave-specialised
-// workgroup (stream_ws_kernel) in which one loader wave pulls each tile of
-// all five arrays straight into an LDS ring with 16-byte direct-to-LDS loads
-// (global_load_lds_dwordx4) and compute waves read the tile from LDS and
-// store the results.  No wave's vmcnt wait then covers its own stores (the
-// loader only loads, the compute waves only store), which is what slows a
-// plain persistent loop on gfx9.  A fourth, persistent workgroups with a
-// plain and a double-buffered loop, completes the comparison.
-//
 // Not part of the optimizer's interface: built as a separate library
 // (probes/libadana_probe.so) and loaded only by bench.py.
 #include <hip/hip_runtime.h>
@@ -166,100 +156,6 @@ int launch_rw(float *const *arrays, int64_t n, float4 *partials, int wgs_per_cu,
     return static_cast<int>(hipGetLastError());
 }
 
-// ---------------------------------------------------------------------------
-// Wave-specialised persistent stream.  Workgroup = CW compute waves + one
-// loader wave (the last); one tile = 1024 elements of each of the R arrays
-// (R x 4 KB), S tiles in an LDS ring.  Tiles are dealt grid-stride.  Per
-// tile j the loader issues tile j + S - 1 into the slot tile j - 1 freed and
-// waits (vmcnt) until tile j + 1 has landed; the compute waves read tile j
-// from LDS, add, and store W arrays with the step's sc1|nt buffer stores;
-// one s_barrier per tile hands the slots over.  The barrier is the bare
-// s_barrier (no fences): LDS visibility comes from the loader's vmcnt wait,
-// and nothing global is shared between the waves.
-// ---------------------------------------------------------------------------
-#define LDS_AS __attribute__((address_space(3)))
-#define GLB_AS __attribute__((address_space(1)))
-
-// s_waitcnt vmcnt(N), other counters not waited on (gfx9 encoding).
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-    static_assert(N >= 0 && N < 64, "vmcnt range");
-    __builtin_amdgcn_s_waitcnt((((N >> 4) & 3) << 14) | (0xF << 8) | (0x7 << 4) | (N & 0xF));
-}
-
-constexpr int kDmaPerArray = kChunk * 4 / 1024;   // 1 KB per LDS-DMA instruction (64 lanes x 16 B)
-
-template <int R, int W, int S, int CW>
-__global__ __launch_bounds__((CW + 1) * 64) void stream_ws_kernel(float *a0, float *a1, float *a2, float *a3,
-                                                                 float *a4, int64_t n_tiles, float4 *partials) {
-    __shared__ F4 ring[S][R][kChunk / 4];
-    float *const a[5] = {a0, a1, a2, a3, a4};
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);   // wave-uniform branch below
-    const int lane = threadIdx.x & 63;
-    const int64_t first = blockIdx.x, stride = gridDim.x;
-    const int64_t J = first < n_tiles ? (n_tiles - first + stride - 1) / stride : 0;
-    constexpr int kPerTile = R * kDmaPerArray;
-    static_assert((S - 2) * kPerTile < 64, "the loader's wait must fit vmcnt");
-    if (wave == CW) {
-        auto issue = [&](int64_t j) {
-            const int slot = static_cast<int>(j % S);
-            const int64_t base = (first + j * stride) * kChunk;
-#pragma unroll
-            for (int r = 0; r < R; ++r) {
-#pragma unroll
-                for (int i = 0; i < kDmaPerArray; ++i)
-                    __builtin_amdgcn_global_load_lds((const GLB_AS void *)(a[r] + base + i * 256 + 4 * lane),
-                                                     (LDS_AS void *)&ring[slot][r][i * 64], 16, 0, 2 /* nt */);
-            }
-        };
-        const int64_t pro = J < S - 1 ? J : S - 1;
-        for (int64_t j = 0; j < pro; ++j) issue(j);
-        if (pro == S - 1) wait_vmcnt<(S - 2) * kPerTile>(); else wait_vmcnt<0>();
-        __builtin_amdgcn_s_barrier();
-        for (int64_t j = 0; j < J; ++j) {
-            if (j + S - 1 < J) {
-                issue(j + S - 1);
-                wait_vmcnt<(S - 2) * kPerTile>();        // tile j + 1 has landed
-            } else {
-                wait_vmcnt<0>();
-            }
-            __builtin_amdgcn_s_barrier();
-        }
-        return;
-    }
-    __builtin_amdgcn_s_barrier();
-    F4 acc = {0.f, 0.f, 0.f, 0.f};
-    for (int64_t j = 0; j < J; ++j) {
-        const int slot = static_cast<int>(j % S);
-        const int64_t tile = first + j * stride;
-        for (int q = threadIdx.x; q < kChunk / 4; q += CW * 64) {
-            F4 x = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-            for (int r = 0; r < R; ++r) x += ring[slot][r][q];
-#pragma unroll
-            for (int r = 0; r < W; ++r) {
-                F4 o = x;
-                o.x += static_cast<float>(r);
-                store_stream(a[r] + tile * kChunk, 16 * q, o);
-            }
-            acc += x;
-        }
-        __builtin_amdgcn_s_barrier();
-    }
-    if (lane == 0) partials[blockIdx.x * CW + wave] = make_float4(acc.x, acc.y, acc.z, acc.w);
-}
-
-template <int S, int CW>
-int launch_ws(float *const *arrays, int64_t n, float4 *partials, int wgs_per_cu, hipStream_t stream) {
-    int dev = 0, cus = 0;
-    if (hipGetDevice(&dev) != hipSuccess ||
-        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
-        return -1;
-    const int64_t grid = static_cast<int64_t>(cus) * wgs_per_cu;
-    hipLaunchKernelGGL((stream_ws_kernel<5, 4, S, CW>), dim3(static_cast<unsigned>(grid)), dim3((CW + 1) * 64), 0,
-                       stream, arrays[0], arrays[1], arrays[2], arrays[3], arrays[4], n / kChunk, partials);
-    return static_cast<int>(hipGetLastError());
-}
 }  // namespace
 
 // One launch over n elements of each array (n a positive multiple of 1024;
@@ -269,134 +165,6 @@ int launch_ws(float *const *arrays, int64_t n, float4 *partials, int wgs_per_cu,
 extern "C" int adana_probe_stream_5r4w(float *const *arrays, int64_t n, float4 *partials, int wgs_per_cu,
                                        hipStream_t stream) {
     return launch_rw<5, 4>(arrays, n, partials, wgs_per_cu, stream);
-}
-
-// The 5-read/4-write pattern through the wave-specialised persistent kernel:
-// `stages` tiles in the LDS ring (3 or 4), `compute_waves` (4 or 8) beside
-// the loader wave, `wgs_per_cu` (1 or 2) workgroups per CU, tiles dealt
-// grid-stride.  Same array conditions as above; `partials` room for
-// wgs_per_cu * CUs * compute_waves float4.
-extern "C" int adana_probe_stream_5r4w_ws(float *const *arrays, int64_t n, float4 *partials, int stages,
-                                          int compute_waves, int wgs_per_cu, hipStream_t stream) {
-    if (!arrays || !partials || n <= 0 || n % kChunk != 0 || n / kChunk > 0x7fffffff || wgs_per_cu < 1 ||
-        wgs_per_cu > 2)
-        return -1;
-    for (int k = 0; k < 5; ++k)
-        if (!arrays[k] || reinterpret_cast<uintptr_t>(arrays[k]) % 16 != 0) return -1;
-    if (stages == 3 && compute_waves == 4) return launch_ws<3, 4>(arrays, n, partials, wgs_per_cu, stream);
-    if (stages == 4 && compute_waves == 4) return launch_ws<4, 4>(arrays, n, partials, wgs_per_cu, stream);
-    if (stages == 3 && compute_waves == 8) return launch_ws<3, 8>(arrays, n, partials, wgs_per_cu, stream);
-    return -1;
-}
-
-// ---------------------------------------------------------------------------
-// Persistent workgroups over the same one-chunk tiles, dealt grid-stride: a
-// plain loop (load, add, store, partial) and a double-buffered one that
-// issues the next tile's loads before the current tile's stores (vector
-// memory operations complete in order on gfx9, so waiting for those loads
-// does not wait for the stores), unrolled by two over fixed register
-// buffers so that the compiler's waits count only the older loads.  The next
-// tile index is clamped to the last tile so that every load is in bounds and
-// unconditional.
-namespace {
-
-// The chunk's sum over the workgroup into partials[c]: as chunk_partial, with
-// the LDS slots alternating between consecutive chunks of one workgroup.
-__device__ __forceinline__ void chunk_partial_at(F4 s, float4 *partials, int64_t c) {
-    __shared__ float red[2][kThreads / 64][4];
-    float t[4] = {s.x, s.y, s.z, s.w};
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-#pragma unroll
-        for (int k = 0; k < 4; ++k) t[k] += __shfl_xor(t[k], o, 64);
-    }
-    const int par = static_cast<int>(c & 1);
-    if ((threadIdx.x & 63) == 0) {
-#pragma unroll
-        for (int k = 0; k < 4; ++k) red[par][threadIdx.x >> 6][k] = t[k];
-    }
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        float4 q = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-        for (int w = 0; w < kThreads / 64; ++w) {
-            q.x += red[par][w][0];
-            q.y += red[par][w][1];
-            q.z += red[par][w][2];
-            q.w += red[par][w][3];
-        }
-        partials[c] = q;
-    }
-}
-
-__device__ __forceinline__ void tile_load5(float *const (&a)[5], int64_t c, F4 (&x)[5]) {
-#pragma unroll
-    for (int k = 0; k < 5; ++k)
-        x[k] = __builtin_nontemporal_load((const GF4 *)(a[k] + c * kChunk + 4 * threadIdx.x));
-}
-__device__ __forceinline__ void tile_use5(float *const (&a)[5], int64_t c, const F4 (&x)[5], float4 *partials) {
-    const F4 s = x[0] + x[1] + x[2] + x[3] + x[4];
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-        F4 o = s;
-        o.x += static_cast<float>(k);
-        store_stream(a[k] + c * kChunk, 16 * threadIdx.x, o);
-    }
-    chunk_partial_at(s, partials, c);
-}
-
-template <bool DOUBLE>
-__global__ __launch_bounds__(kThreads) void stream_persistent_kernel(float *a0, float *a1, float *a2, float *a3,
-                                                                     float *a4, float4 *partials,
-                                                                     int64_t n_chunks) {
-    float *const a[5] = {a0, a1, a2, a3, a4};
-    const int64_t g = gridDim.x, last = n_chunks - 1;
-    int64_t c = blockIdx.x;
-    if (c >= n_chunks) return;                      // whole workgroup
-    F4 A[5], B[5];
-    if constexpr (!DOUBLE) {
-        for (; c < n_chunks; c += g) {
-            tile_load5(a, c, A);
-            tile_use5(a, c, A, partials);
-        }
-    } else {
-        tile_load5(a, c, A);
-        for (;;) {
-            const int64_t cb = c + g;
-            tile_load5(a, cb < last ? cb : last, B);
-            tile_use5(a, c, A, partials);
-            if (cb >= n_chunks) break;
-            const int64_t ca = cb + g;
-            tile_load5(a, ca < last ? ca : last, A);
-            tile_use5(a, cb, B, partials);
-            if (ca >= n_chunks) break;
-            c = ca;
-        }
-    }
-}
-
-}  // namespace
-
-// The 5-read/4-write pattern through persistent workgroups: `wgs_per_cu`
-// (1..8) per CU, plain (double_buffer 0) or double-buffered (1).  Same array
-// conditions as adana_probe_stream_5r4w; partials: n / 1024 float4.
-extern "C" int adana_probe_stream_5r4w_persistent(float *const *arrays, int64_t n, float4 *partials, int wgs_per_cu,
-                                                  int double_buffer, hipStream_t stream) {
-    if (!arrays || !partials || n <= 0 || n % kChunk != 0 || wgs_per_cu < 1 || wgs_per_cu > 8) return -1;
-    for (int k = 0; k < 5; ++k)
-        if (!arrays[k] || reinterpret_cast<uintptr_t>(arrays[k]) % 16 != 0) return -1;
-    int dev = 0, cus = 0;
-    if (hipGetDevice(&dev) != hipSuccess ||
-        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
-        return -1;
-    const int64_t n_chunks = n / kChunk;
-    const int64_t grid = std::min<int64_t>(static_cast<int64_t>(cus) * wgs_per_cu, n_chunks);
-    if (double_buffer)
-        hipLaunchKernelGGL(stream_persistent_kernel<true>, dim3(static_cast<unsigned>(grid)), dim3(kThreads), 0,
-                           stream, arrays[0], arrays[1], arrays[2], arrays[3], arrays[4], partials, n_chunks);
-    else
-        hipLaunchKernelGGL(stream_persistent_kernel<false>, dim3(static_cast<unsigned>(grid)), dim3(kThreads), 0,
-                           stream, arrays[0], arrays[1], arrays[2], arrays[3], arrays[4], partials, n_chunks);
-    return static_cast<int>(hipGetLastError());
 }
 
 // The 5 arrays read only (no stores) and 4 written only (no loads), in the

@@ -72,14 +72,40 @@ def test_default_warmups():
 
 
 def test_cos_inf_schedule():
-    """Linear warm-up over 4 steps, then a cosine down to a tenth of the peak
-    at step 200 (the C2 configuration's warmup-cosine lr)."""
-    assert bench.cos_inf(0) == pytest.approx(0.25)
-    assert bench.cos_inf(3) == pytest.approx(1.0)
-    assert bench.cos_inf(4) == pytest.approx(1.0)
-    assert bench.cos_inf(102) == pytest.approx(0.1 + 0.9 * 0.5, rel=1e-12)
-    assert bench.cos_inf(200) == pytest.approx(0.1)
-    assert all(bench.cos_inf(k) >= bench.cos_inf(k + 1) for k in range(4, 200))
+    """C2's lr factor is the reference's cos_inf (src/optim/schedule.py:88-96:
+    step/n_warmup + (1 - step/n_warmup)/div_factor while warming up, then
+    final + (1 - final)(1 + cos(pi t))/2 with final = 1/div/final_div = 0.1),
+    pinned here by values worked out from that formula by hand."""
+    f = bench.cos_inf_schedule(**bench.C2_SCHEDULE)
+    assert bench.C2_SCHEDULE == dict(n_iterations=200, n_warmup=4, div_factor=1e2, final_div_factor=1e-1,
+                                     n_inf=0)
+    assert f(0) == pytest.approx(0.01, rel=1e-15)            # 0 + 1/100
+    assert f(1) == pytest.approx(0.2575, rel=1e-15)          # 1/4 + (3/4)/100
+    assert f(2) == pytest.approx(0.505, rel=1e-15)
+    assert f(3) == pytest.approx(0.7525, rel=1e-15)
+    assert f(4) == pytest.approx(1.0, rel=1e-15)             # t = 0: 0.1 + 0.9
+    assert f(102) == pytest.approx(0.55, rel=1e-12)          # t = 1/2: 0.1 + 0.45
+    assert f(199) == pytest.approx(0.1 + 0.45 * (1 - math.cos(math.pi / 196)), rel=1e-12)
+    assert f(200) == pytest.approx(0.1, rel=1e-15) and f(500) == f(200)
+    assert all(f(k) < f(k + 1) for k in range(4)) and all(f(k) > f(k + 1) for k in range(4, 200))
+
+
+def test_c2_lr_through_lambdalr():
+    """The bench drives C2's lr through torch.optim.lr_scheduler.LambdaLR as
+    src/main.py:411-423 does: step k runs at peak * factor(k), group['lr']
+    set at construction (k = 0) and after every step."""
+    import torch
+
+    p = torch.nn.Parameter(torch.zeros(1))
+    opt = torch.optim.SGD([p], lr=3e-3)
+    f = bench.cos_inf_schedule(**bench.C2_SCHEDULE)
+    sched = torch.optim.lr_scheduler.LambdaLR(opt, f)
+    seen = []
+    for _ in range(8):
+        seen.append(opt.param_groups[0]["lr"])
+        opt.step()
+        sched.step()
+    assert seen == [3e-3 * f(k) for k in range(8)]
 
 
 def test_more_than_one_gpu_is_refused(capsys, monkeypatch):

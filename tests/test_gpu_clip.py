@@ -263,3 +263,47 @@ def test_c_abi_clip_empty_list():
                "adana_grad_clip_norm")
     torch.cuda.synchronize()
     assert out.tolist() == [0.0, 1.0]
+
+
+@pytest.mark.parametrize("write_back", [True, False])
+def test_deepcopy_with_pending_clip(write_back):
+    """copy.deepcopy of an optimizer with a clip deferred to its next step():
+    with write_back the original's gradients are scaled then (what torch's
+    in-place clipping leaves); without it the original's gradients stay
+    unscaled and the copy defers the same scaling.  Either way the original
+    and the copy then take bit-identical steps on the clipped gradients.
+    (Plain tensors as parameters: nn.Parameter's deepcopy drops .grad.)"""
+    import copy
+
+    import adana_amd
+
+    print("case: deepcopy with a pending clip, write_back", write_back, flush=True)
+    rng = np.random.default_rng(51)
+    ps = [torch.from_numpy(_normal(rng, s, 0.02)).to(DEV).requires_grad_() for s in ((96, 64), (64,), (5,))]
+    for p in ps:
+        p.grad = torch.from_numpy(_normal(rng, p.shape, 1.0)).to(DEV)
+    opt = adana_amd.DANA_STAR_MK4(ps, lr=1e-3, kappa=0.85, clipsnr=2.0)
+    twin = [p.detach().clone().requires_grad_() for p in ps]
+    for t, p in zip(twin, ps):
+        t.grad = p.grad.clone()
+    ref = adana_amd.DANA_STAR_MK4(twin, lr=1e-3, kappa=0.85, clipsnr=2.0)
+    ref.clip_grad_norm_(0.5, write_back=write_back)
+    ref.step()                                   # the fused path, on a twin that is never copied
+    unscaled = [p.grad.clone() for p in ps]
+    opt.clip_grad_norm_(0.5, write_back=write_back)
+    cp = copy.deepcopy(opt)
+    assert (opt._pending_clip is None) == write_back
+    for p, g in zip(ps, unscaled):
+        assert torch.equal(p.grad, g) != write_back      # scaled now only with write_back
+    opt.step()
+    cp.step()
+    torch.cuda.synchronize()
+    cps = [p for g in cp.param_groups for p in g["params"]]
+    for a, b, c in zip(ps, cps, twin):
+        assert torch.equal(a.detach(), c.detach()), "original vs never-copied twin"
+        assert torch.equal(b.detach(), c.detach()), "copy vs never-copied twin"
+    for a, c in zip(ps, twin):
+        assert torch.equal(a.grad, c.grad)
+    if not write_back:
+        for b, g in zip(cps, unscaled):
+            assert torch.equal(b.grad, g), "the copy's gradients stay unscaled too"

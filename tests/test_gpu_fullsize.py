@@ -7,7 +7,7 @@ workloads' own lists and hyper-parameters (bench.workload):
     bf16 gradients;
   * c3: Dana-Star-MK4, 1,311,082,496 parameters (d_model 2048, 24 layers);
   * c2: Dana-MK4, 50,938,880 parameters in 67 tensors, 1-D gradients x 0.1,
-    under the bench's warm-up/cosine lr schedule (a new group lr every step);
+    under the bench's lr schedule, the reference's cos_inf through LambdaLR (a new group lr every step);
   * c5: Dana-Star-MK4 over 10,000 log-uniform tensors (94,406,322
     parameters), 5% of them with all-zero gradients.
 Ten steps each, so every run crosses t = delta = 8, where alpha = 0.5 and
@@ -103,12 +103,17 @@ def test_full_size_parity(oracle_mod, name):
     host_m = [np.zeros_like(x) for x in host_p]
     host_v = [np.zeros_like(x) for x in host_p]
     host_tau = [np.zeros_like(x) for x in host_p] if star else [None] * len(params)
-    from bench import cos_inf
+    from bench import C2_SCHEDULE, cos_inf_schedule
 
+    sched, factor = None, None
+    if w["schedule"] == "cos_inf":
+        # as the bench and src/main.py:411-423: LambdaLR over the reference's cos_inf factor
+        factor = cos_inf_schedule(**C2_SCHEDULE)
+        sched = torch.optim.lr_scheduler.LambdaLR(opt, factor)
     for t in range(1, STEPS + 1):
-        lr = hp["lr"] * cos_inf(t - 1) if w["schedule"] == "cos_inf" else hp["lr"]
-        for g in opt.param_groups:
-            g["lr"] = lr                                 # the bench's one_step(k) for k = t - 1
+        lr = opt.param_groups[0]["lr"]
+        assert all(g["lr"] == lr for g in opt.param_groups)
+        assert lr == (hp["lr"] * factor(t - 1) if sched is not None else hp["lr"])
         gen.manual_seed(1000 + t)
         for i, p in enumerate(params):
             p.grad = torch.empty(p.shape, device=DEV).normal_(0, 1e-3, generator=gen).to(pdtype)
@@ -123,6 +128,8 @@ def test_full_size_parity(oracle_mod, name):
         gnorm = [float(torch.linalg.vector_norm(p.grad.double())) for p in params]
         p_before = [x.copy() for x in host_p]
         opt.step()
+        if sched is not None:
+            sched.step()
         torch.cuda.synchronize()
         got_p = gather([opt.state[p]["master"] for p in params] if master else params)
         got_lp = gather(params) if master else None

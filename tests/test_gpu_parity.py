@@ -235,10 +235,12 @@ def _gpt_list(rng, vocab, d, layers, mlp=4):
     return decay, nodecay
 
 
-def _cos_inf(k, warmup=4, n=40, div=1e2, final_div=1e-1):
-    if k < warmup:
-        return (k + 1) / warmup
-    return final_div + (1 - final_div) * 0.5 * (1 + math.cos(math.pi * (k - warmup) / (n - warmup)))
+def _cos_inf(k):
+    """The reference's cos_inf lr factor (src/optim/schedule.py:70-98, restated
+    in bench.py) over a 40-iteration run with a 4-step warm-up."""
+    from bench import cos_inf_schedule
+
+    return cos_inf_schedule(n_iterations=40, n_warmup=4, div_factor=1e2, final_div_factor=1e-1, n_inf=0)(k)
 
 
 @pytest.mark.parametrize("star", [False, True])

@@ -376,14 +376,6 @@ def test_stream_probe_library_rejects_bad_arguments():
     assert fn(holes, 1024, part, 4, None) == -1           # null array
     odd = (ctypes.c_void_p * 5)(0x1000, 0x1004, 0x1000, 0x1000, 0x1000)
     assert fn(odd, 1024, part, 4, None) == -1             # misaligned array
-    ws = lib.adana_probe_stream_5r4w_ws
-    ws.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_int,
-                   ctypes.c_void_p]
-    ws.restype = ctypes.c_int
-    assert ws(five, 1000, part, 3, 4, 1, None) == -1        # not a multiple of 1024
-    assert ws(odd, 1024, part, 3, 4, 1, None) == -1         # misaligned array
-    assert ws(five, 1024, part, 3, 4, 3, None) == -1        # more workgroups per CU than the LDS ring allows
-    assert ws(five, 1024, part, 5, 4, 1, None) == -1        # no such instance
     for name in ("adana_probe_stream_5r0w", "adana_probe_stream_0r4w"):
         f = getattr(lib, name)
         f.argtypes = fn.argtypes

@@ -282,3 +282,27 @@ def test_manau_host_errors():
     with pytest.raises(RuntimeError, match="ROCm GPU"):
         opt.step()
     assert all(torch.equal(a, q) for a, q in zip(before, params))       # refused before any update
+
+
+def test_manau_names_shorter_than_params():
+    """A parameter past the end of its group's name list has no name of its
+    own (manau.py:183-190 marks only ``idx < len(param_names)``): a matrix
+    there goes to Muon even when the last listed name is the head's, and a
+    vector to the Dana branch; the report lists it under that last name."""
+    import contextlib
+    import io
+
+    import torch
+
+    import adana_amd
+
+    head = torch.nn.Parameter(torch.zeros(8, 4))
+    extra_mat = torch.nn.Parameter(torch.zeros(4, 4))
+    extra_vec = torch.nn.Parameter(torch.zeros(4))
+    printed = io.StringIO()
+    with contextlib.redirect_stdout(printed):
+        opt = adana_amd.Manau([{"params": [head, extra_mat, extra_vec], "param_names": ["lm_head.weight"]}])
+    assert opt.state[head]["use_muon"] is False
+    assert opt.state[extra_mat]["use_muon"] is True
+    assert opt.state[extra_vec]["use_muon"] is False
+    assert printed.getvalue().count("lm_head.weight") == 3
