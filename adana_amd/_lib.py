@@ -16,7 +16,7 @@ import numpy as np
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libadana_mta.so")
 
-ABI_VERSION = 6
+ABI_VERSION = 7
 CHUNK_ELEMS = 1024
 ALIGN_ELEMS = 4
 MAX_CLASSES = 8
@@ -29,11 +29,13 @@ PARAM_BF16 = 0x4
 WRITE_GRAD = 0x8
 VARIANT_MANAU = 0x10
 STATE_BF16 = 0x20
+NUMERICS_EAGER = 0x40
 DESC_VEC_OK = 0x1
 
-# adana_tensor_desc as a numpy record (64 bytes, same field order).
+# adana_tensor_desc as a numpy record (64 bytes, same field order; the
+# gradient pointers are a separate array, adana_plan.grad).
 DESC_DTYPE = np.dtype([
-    ("param", np.uint64), ("grad", np.uint64), ("m", np.uint64), ("v", np.uint64),
+    ("param", np.uint64), ("reserved0", np.uint64), ("m", np.uint64), ("v", np.uint64),
     ("tau", np.uint64), ("param_lp", np.uint64), ("numel", np.int64),
     ("sclass", np.int32), ("flags", np.uint32),
 ])
@@ -48,7 +50,7 @@ class HParams(ctypes.Structure):
         ("epsilon", ctypes.c_double), ("weight_decay", ctypes.c_double),
         ("clipsnr", ctypes.c_double), ("wd_ts", ctypes.c_double),
         ("gamma_3_factor", ctypes.c_double), ("has_clip", ctypes.c_int32),
-        ("wd_decaying", ctypes.c_int32),
+        ("wd_decaying", ctypes.c_int32), ("eager", ctypes.c_int32), ("reserved", ctypes.c_int32),
     ]
 
 
@@ -61,7 +63,7 @@ class StepScalars(ctypes.Structure):
         ("min_p", ctypes.c_float), ("clip", ctypes.c_float), ("c3", ctypes.c_float),
         ("cg2", ctypes.c_float), ("opw", ctypes.c_float), ("star_exp", ctypes.c_float),
         ("pow_mode", ctypes.c_int32), ("has_clip", ctypes.c_int32),
-        ("lerp_small", ctypes.c_int32), ("reserved", ctypes.c_int32),
+        ("lerp_small", ctypes.c_int32), ("pow_int", ctypes.c_int32),
     ]
 
 
@@ -97,7 +99,8 @@ class Plan(ctypes.Structure):
     """adana_plan: host struct of device pointers."""
 
     _fields_ = [
-        ("desc", ctypes.c_void_p), ("vstart", ctypes.c_void_p), ("chunk_first", ctypes.c_void_p),
+        ("desc", ctypes.c_void_p), ("grad", ctypes.c_void_p), ("vstart", ctypes.c_void_p),
+        ("chunk_first", ctypes.c_void_p),
         ("fold_first", ctypes.c_void_p), ("n_tensors", ctypes.c_int32),
         ("reserved", ctypes.c_int32), ("n_chunks", ctypes.c_int64), ("n_folds", ctypes.c_int64),
     ]

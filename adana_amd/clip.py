@@ -41,10 +41,10 @@ __all__ = ["clip_grad_norm_", "GradPlan"]
 
 
 class GradPlan:
-    """A laid-out gradient list on one device (descriptors carry only the
-    gradient pointer, numel and alignment flag).  The layout is rebuilt when
-    the tensor sizes change; the descriptor table is re-uploaded only when a
-    gradient address moved."""
+    """A laid-out gradient list on one device (the descriptors carry only the
+    numel; the gradient pointers are the plan's separate array).  The layout
+    is rebuilt when the tensor sizes change; the gradient pointers are
+    re-uploaded only when an address moved."""
 
     def __init__(self, device: torch.device, bf16: bool):
         self.device = device
@@ -55,42 +55,36 @@ class GradPlan:
         self.grads: List[torch.Tensor] = []
         self.plan = _lib.Plan()
         self.dev_table = None
+        self.dev_grad = None
         self.chunk_first = None
         self.workspace = None
 
     def prepare(self, grads: List[torch.Tensor]) -> None:
         n = len(grads)
         numels = np.fromiter((g.numel() for g in grads), dtype=np.int64, count=n)
-        ptrs = np.fromiter((g.data_ptr() for g in grads), dtype=np.uint64, count=n)
+        ptrs = np.frombuffer(_hoststep.data_ptrs(grads), dtype=np.uint64)
         relayout = self.numels is None or not np.array_equal(numels, self.numels)
-        if relayout:
-            self.vstart, self.fold_first, self.n_chunks, self.n_folds = _lib.plan_layout(numels)
-            self.numels = numels
-            self.ptrs = None
         self.grads = grads
-        if self.ptrs is not None and np.array_equal(ptrs, self.ptrs):
-            return
-        desc = np.zeros(n, dtype=_lib.DESC_DTYPE)
-        desc["grad"] = ptrs
-        desc["numel"] = numels
-        align = 8 if self.bf16 else 16
-        desc["flags"] = np.where(ptrs % align == 0, _lib.DESC_VEC_OK, 0).astype(np.uint32)
-        table = np.concatenate([desc.view(np.uint8), self.vstart.view(np.uint8),
-                                self.fold_first.view(np.uint8)])
-        host = torch.from_numpy(table).pin_memory()
         with torch.cuda.device(self.device):
-            if self.dev_table is None or self.dev_table.numel() != host.numel():
-                self.dev_table = torch.empty(host.numel(), dtype=torch.uint8, device=self.device)
-            self.dev_table.copy_(host, non_blocking=True)
-            base = self.dev_table.data_ptr()
-            pl = self.plan
-            pl.desc = base
-            pl.vstart = base + 64 * n
-            pl.fold_first = base + 64 * n + 8 * (n + 1)
-            pl.n_tensors = n
-            pl.n_chunks = self.n_chunks
-            pl.n_folds = self.n_folds
-            if relayout or self.chunk_first is None:
+            if relayout:
+                self.vstart, self.fold_first, self.n_chunks, self.n_folds = _lib.plan_layout(numels)
+                self.numels = numels
+                desc = np.zeros(n, dtype=_lib.DESC_DTYPE)
+                desc["numel"] = numels
+                table = np.concatenate([desc.view(np.uint8), self.vstart.view(np.uint8),
+                                        self.fold_first.view(np.uint8)])
+                self.dev_table = torch.from_numpy(table).pin_memory().to(self.device, non_blocking=True)
+                self.dev_grad = torch.empty(max(n, 1), dtype=torch.int64, device=self.device)
+                self.ptrs = None
+                base = self.dev_table.data_ptr()
+                pl = self.plan
+                pl.desc = base
+                pl.grad = self.dev_grad.data_ptr()
+                pl.vstart = base + 64 * n
+                pl.fold_first = base + 64 * n + 8 * (n + 1)
+                pl.n_tensors = n
+                pl.n_chunks = self.n_chunks
+                pl.n_folds = self.n_folds
                 self.chunk_first = torch.empty(max(self.n_chunks, 1), dtype=torch.int32, device=self.device)
                 stream = torch.cuda.current_stream(self.device).cuda_stream
                 _lib.check(_lib.lib().adana_plan_index(
@@ -100,7 +94,10 @@ class GradPlan:
                 pl.chunk_first = self.chunk_first.data_ptr()
                 self.workspace = torch.empty(max(_lib.workspace_bytes(pl), 1), dtype=torch.uint8,
                                              device=self.device)
-        self.ptrs = ptrs
+            if n and (self.ptrs is None or not np.array_equal(ptrs, self.ptrs)):
+                self.dev_grad[:n].copy_(torch.from_numpy(ptrs.view(np.int64).copy()).pin_memory(),
+                                        non_blocking=True)
+                self.ptrs = ptrs.copy()
 
     def clip_norm(self, max_norm: float) -> torch.Tensor:
         """Launch the norm pass; returns a new device float32[2] = (total, coef)."""

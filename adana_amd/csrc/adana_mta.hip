@@ -19,8 +19,12 @@
 //     (deterministic, no atomics).
 //
 // Element arithmetic follows the reference's op order with every op one
-// correctly rounded binary32 operation (built with -ffp-contract=off); the
-// only fused multiply-adds are the ones ATen's lerp_ and addcmul_ perform.
+// correctly rounded binary32 operation (built with -ffp-contract=off), in one
+// of the reference's two numerics: its default torch.compile path (Inductor's
+// decompositions of lerp_ and addcmul_, products and sums rounded one by one,
+// bfloat16 state rounded only where it is stored), or, with
+// ADANA_NUMERICS_EAGER, its ATen ops (lerp_ and addcmul_ as single-rounded
+// FMAs; bfloat16 state rounded after every op).
 #include <hip/hip_runtime.h>
 
 #include <atomic>
@@ -114,6 +118,26 @@ __device__ __forceinline__ float bf16_to_f32(unsigned short h) {
 __device__ __forceinline__ unsigned short f32_to_bf16(float f) { return adana::bf16_bits(f); }
 __device__ __forceinline__ float bf16_round(float f) { return adana::bf16_round(f); }
 
+// x ** k for an integer k (|k| < 32), as Inductor's pow lowering expands it
+// (torch/_inductor/lowering.py, pow_recursive): for k < 0 the powers of
+// 1 / x; x ** 2j = (x ** j) ** 2 and x ** (2j + 1) = (x ** j) ** 2 * x, i.e.
+// left-to-right binary powering, every product rounded.  k == 0 gives 1.
+__host__ __device__ inline float pow_int_f32(float x, int k) {
+    if (k < 0) {
+        x = 1.0f / x;
+        k = -k;
+    }
+    if (k == 0) return 1.0f;
+    int top = 0;
+    while ((k >> (top + 1)) != 0) ++top;
+    float r = x;
+    for (int b = top - 1; b >= 0; --b) {
+        r = r * r;
+        if ((k >> b) & 1) r = r * x;
+    }
+    return r;
+}
+
 // clip_grad_norm_'s in-place product (torch/nn/utils/clip_grad.py,
 // _clip_grads_with_norm_: torch._foreach_mul_(grads, clip_coef_clamped)):
 // g * coef in binary32, rounded to bfloat16 for bfloat16 gradients.
@@ -165,15 +189,29 @@ __device__ __forceinline__ float pow_aten(float x, const adana_step_scalars &sc,
         case ADANA_POW_SQUARE: return x * x;
         case ADANA_POW_CUBE: return (x * x) * x;
         case ADANA_POW_INVSQ: return 1.0f / (x * x);
+        case ADANA_POW_INT: return pow_int_f32(x, sc.pow_int);
         default: return adana::pow_f32_via_f64(x, sc.star_exp);
         }
     }
 }
 
-// m.lerp_(grad, alpha): ATen computes fma(w, end - self, self) for |w| < 0.5
-// and fma(w - 1, end - self, end) otherwise (w - 1 is precomputed, exact).
-__device__ __forceinline__ float lerp_aten(float self, float end, const adana_step_scalars &sc) {
-    return __builtin_fmaf(sc.lerp_coef, end - self, sc.lerp_small ? self : end);
+// m.lerp_(grad, alpha) with w = alpha, c = (|w| < 0.5 ? w : w - 1) (w - 1 is
+// precomputed, exact) and b = (|w| < 0.5 ? self : end).  ATen (eager)
+// computes fma(c, end - self, b); Inductor's decomposition (torch._refs.lerp,
+// the compiled path) computes c * (end - self) + b, product and sum rounded
+// separately.
+template <bool EAGER>
+__device__ __forceinline__ float lerp_op(float self, float end, const adana_step_scalars &sc) {
+    if constexpr (EAGER) return __builtin_fmaf(sc.lerp_coef, end - self, sc.lerp_small ? self : end);
+    else return sc.lerp_coef * (end - self) + (sc.lerp_small ? self : end);
+}
+// v.mul_(1 - alpha).addcmul_(grad, grad, value=alpha): ATen's addcmul_ is
+// fma(alpha * g, g, v * (1 - alpha)); Inductor computes v * (1 - alpha) +
+// (g * g) * alpha.
+template <bool EAGER>
+__device__ __forceinline__ float ema2_op(float v, float g, const adana_step_scalars &sc) {
+    if constexpr (EAGER) return __builtin_fmaf(sc.a * g, g, v * sc.oma);
+    else return v * sc.oma + (g * g) * sc.a;
 }
 
 __device__ __forceinline__ void accumulate(float (&acc)[4], float af, float g, float mfac, float m) {
@@ -184,10 +222,11 @@ __device__ __forceinline__ void accumulate(float (&acc)[4], float af, float g, f
 }
 
 // ADana / Dana-MK4, one element: src/optim/adana.py:101-143.
+template <bool EAGER>
 __device__ __forceinline__ float adana_elem(float p, float g, float &m, float &v,
                                             const adana_step_scalars &sc, float (&acc)[4]) {
-    const float mn = lerp_aten(m, g, sc);                        // :101
-    const float vn = __builtin_fmaf(sc.a * g, g, v * sc.oma);    // :104 mul_, addcmul_
+    const float mn = lerp_op<EAGER>(m, g, sc);                   // :101
+    const float vn = ema2_op<EAGER>(v, g, sc);                   // :104 mul_, addcmul_
     const float se = adana::sqrt_f32(vn) + sc.eps;               // :107
     const float nt = 1.0f / se;                                  // :110
     const float mfac = fabsf(mn) * nt;                           // :111, :115
@@ -211,15 +250,16 @@ struct StarMid {
 };
 
 // src/optim/dana_star_mk4.py:137-159
+template <bool EAGER>
 __device__ __forceinline__ StarMid star_phase_a(float g, float m, float v, float tau,
                                                 const adana_step_scalars &sc) {
     StarMid o;
-    o.m = lerp_aten(m, g, sc);                                   // :137
-    o.v = __builtin_fmaf(sc.a * g, g, v * sc.oma);               // :140
+    o.m = lerp_op<EAGER>(m, g, sc);                              // :137
+    o.v = ema2_op<EAGER>(v, g, sc);                              // :140
     o.se = adana::sqrt_f32(o.v) + sc.eps;                        // :143
     const float ag = fabsf(g);                                   // :147
     const float tu = ag / (ag + o.se);                           // :148
-    o.tau = lerp_aten(tau, tu, sc);                              // :149
+    o.tau = lerp_op<EAGER>(tau, tu, sc);                         // :149
     const float ct = clamp_max(o.tau, 0.5f);                     // :152
     // ct in [0, 0.5]: 1 - ct is in [0.5, 1], and exactly 1 when ct < 2^-25
     const float pe = adana::div_core(ct, 1.0f - ct);                    // :153
@@ -249,8 +289,11 @@ __device__ __forceinline__ float star_phase_b(float p, float g, const StarMid &a
 // ---------------------------------------------------------------------------
 // The reference's own bfloat16 path (ADANA_STATE_BF16): bfloat16 parameters
 // make m, v and tau bfloat16 too (zeros_like(p), src/optim/adana.py:191-195;
-// src/optim/dana_star_mk4.py:251-255) and every tensor op rounds its binary32
-// result to bfloat16, as ATen's kernels do on bfloat16 tensors.  How each op
+// src/optim/dana_star_mk4.py:251-255).  Compiled (the default), Inductor
+// loads them as binary32, runs the binary32 update above and rounds the four
+// stored results to bfloat16: thread_elems does exactly that.  Eager
+// (ADANA_NUMERICS_EAGER), every tensor op rounds its binary32 result to
+// bfloat16, as ATen's kernels do on bfloat16 tensors (below).  How each op
 // meets its float32 0-d and Python-scalar operands (probed op by op against
 // torch 2.10 and pinned by the reference's own bfloat16 run):
 //   * lerp_'s float32 0-d weight is rounded to bfloat16 first;
@@ -480,15 +523,15 @@ __device__ __forceinline__ float manau_elem(float p, float g, float &m, float &v
 }
 
 // One element of either variant (the element-wise tail path).
-template <bool STAR, int POWK>
+template <bool STAR, int POWK, bool EAGER>
 __device__ __forceinline__ float update_elem(float p, float g, float &m, float &v, float &tau,
                                              const adana_step_scalars &sc, const PowTab &tab, float (&acc)[4]) {
     if constexpr (is_manau(POWK)) {
         return manau_elem<POWK>(p, g, m, v, tau, as_manau(sc), tab, acc);
     } else if constexpr (!STAR) {
-        return adana_elem(p, g, m, v, sc, acc);
+        return adana_elem<EAGER>(p, g, m, v, sc, acc);
     } else {
-        const StarMid a = star_phase_a(g, m, v, tau, sc);
+        const StarMid a = star_phase_a<EAGER>(g, m, v, tau, sc);
         const float pn = star_phase_b(p, g, a, pow_aten<POWK>(a.et, sc, tab), sc, acc);
         m = a.m;
         v = a.v;
@@ -499,7 +542,7 @@ __device__ __forceinline__ float update_elem(float p, float g, float &m, float &
 
 // N consecutive elements of one thread (the vector path).  Dana-Star runs
 // phase A for all N, then the N pows, then phase B.
-template <bool STAR, int POWK, int N>
+template <bool STAR, int POWK, bool EAGER, int N>
 __device__ __forceinline__ void update_n(float (&P)[N], const float (&G)[N], float (&M)[N], float (&V)[N],
                                          float (&T)[N], const adana_step_scalars &sc, const PowTab &tab,
                                          float (&acc)[4]) {
@@ -509,11 +552,11 @@ __device__ __forceinline__ void update_n(float (&P)[N], const float (&G)[N], flo
         for (int k = 0; k < N; ++k) P[k] = manau_elem<POWK>(P[k], G[k], M[k], V[k], T[k], ms, tab, acc);
     } else if constexpr (!STAR) {
 #pragma unroll
-        for (int k = 0; k < N; ++k) P[k] = adana_elem(P[k], G[k], M[k], V[k], sc, acc);
+        for (int k = 0; k < N; ++k) P[k] = adana_elem<EAGER>(P[k], G[k], M[k], V[k], sc, acc);
     } else {
         StarMid a[N];
 #pragma unroll
-        for (int k = 0; k < N; ++k) a[k] = star_phase_a(G[k], M[k], V[k], T[k], sc);
+        for (int k = 0; k < N; ++k) a[k] = star_phase_a<EAGER>(G[k], M[k], V[k], T[k], sc);
         float pw[N];
 #pragma unroll
         for (int k = 0; k < N; ++k) pw[k] = pow_aten<POWK>(a[k].et, sc, tab);
@@ -636,6 +679,11 @@ __device__ __forceinline__ void load_grad_n(const void *g, int64_t off, float (&
     if constexpr (GBF16) ld_bf16_n<N>(static_cast<const unsigned short *>(g) + off, o);
     else ld_n<N>(static_cast<const float *>(g) + off, o);
 }
+// The vector path's alignment of a gradient: 16 bytes for float32, 8 for bfloat16.
+template <bool GBF16>
+__device__ __forceinline__ bool grad_vec_aligned(const void *g) {
+    return (reinterpret_cast<uintptr_t>(g) & (GBF16 ? 7u : 15u)) == 0;
+}
 template <bool GBF16>
 __device__ __forceinline__ float load_grad1(const void *g, int64_t off) {
     if constexpr (GBF16) return bf16_to_f32(static_cast<const unsigned short *>(g)[off]);
@@ -682,23 +730,26 @@ enum ParamMode { PM_F32 = 0, PM_MASTER = 1, PM_BF16 = 2 };
 // terms added to acc.  UNIFORM: every thread of the workgroup works on this
 // tensor and the chunk's part of it starts at element seg0, so the fp32
 // stores go out as buffer stores from that uniform base.
-template <bool STAR, bool GBF16, int PM, int POWK, int VEC, bool UNIFORM>
-__device__ __forceinline__ void thread_elems(const adana_tensor_desc &d, int64_t off, int64_t left, int64_t seg0,
-                                             const ScalarPack &pack, float gs, const PowTab &tab,
+template <bool STAR, bool GBF16, int PM, int POWK, bool EAGER, int VEC, bool UNIFORM>
+__device__ __forceinline__ void thread_elems(const adana_tensor_desc &d, const void *grad, int64_t off, int64_t left,
+                                             int64_t seg0, const ScalarPack &pack, float gs, const PowTab &tab,
                                              float (&acc)[4]) {
     const adana_step_scalars &sc = pack.c[d.sclass];
     const bool scaled = pack.gscale != nullptr;                    // uniform
     const int cnt = left < VEC ? static_cast<int>(left) : VEC;
-    if constexpr (PM == PM_BF16) {
-        const Scalars16 &q = pack.c16[d.sclass];
+    // the descriptor's flag covers every pointer but the gradient's
+    const bool vec_ok = (d.flags & ADANA_DESC_VEC_OK) && grad_vec_aligned<GBF16>(grad);
+    if constexpr (PM == PM_BF16 && !EAGER) {
+        // the compiled path on bfloat16 state: binary32 throughout, the four
+        // stored results rounded to bfloat16 (round to nearest even)
         unsigned short *pp = static_cast<unsigned short *>(d.param) + off;
         unsigned short *mp = reinterpret_cast<unsigned short *>(d.m) + off;
         unsigned short *vp = reinterpret_cast<unsigned short *>(d.v) + off;
         unsigned short *tp = STAR ? reinterpret_cast<unsigned short *>(d.tau) + off : nullptr;
-        if (cnt == VEC && (d.flags & ADANA_DESC_VEC_OK)) {
+        if (cnt == VEC && vec_ok) {
             float P[VEC], G[VEC], M[VEC], V[VEC], T[VEC];
             ld_bf16_n<VEC>(pp, P);
-            load_grad_n<true, VEC>(d.grad, off, G);
+            load_grad_n<true, VEC>(grad, off, G);
             ld_bf16_n<VEC>(mp, M);
             ld_bf16_n<VEC>(vp, V);
             if constexpr (STAR) {
@@ -710,7 +761,52 @@ __device__ __forceinline__ void thread_elems(const adana_tensor_desc &d, int64_t
             if (scaled) {
 #pragma unroll
                 for (int k = 0; k < VEC; ++k) G[k] = scale_grad<true>(G[k], gs);
-                if (pack.write_grad) store_grad_n<true, VEC>(d.grad, off, G);
+                if (pack.write_grad) store_grad_n<true, VEC>(grad, off, G);
+            }
+            update_n<STAR, POWK, false, VEC>(P, G, M, V, T, sc, tab, acc);
+            st_bf16_n<VEC>(pp, P);
+            st_bf16_n<VEC>(mp, M);
+            st_bf16_n<VEC>(vp, V);
+            if constexpr (STAR) st_bf16_n<VEC>(tp, T);
+        } else {
+            for (int e = 0; e < cnt; ++e) {
+                float mm = bf16_to_f32(mp[e]), vv = bf16_to_f32(vp[e]), tt = STAR ? bf16_to_f32(tp[e]) : 0.0f;
+                float g = load_grad1<true>(grad, off + e);
+                if (scaled) {
+                    g = scale_grad<true>(g, gs);
+                    if (pack.write_grad) store_grad1<true>(grad, off + e, g);
+                }
+                const float o = update_elem<STAR, POWK, false>(bf16_to_f32(pp[e]), g, mm, vv, tt, sc, tab, acc);
+                pp[e] = f32_to_bf16(o);
+                mp[e] = f32_to_bf16(mm);
+                vp[e] = f32_to_bf16(vv);
+                if constexpr (STAR) tp[e] = f32_to_bf16(tt);
+            }
+        }
+        return;
+    }
+    if constexpr (PM == PM_BF16) {
+        const Scalars16 &q = pack.c16[d.sclass];
+        unsigned short *pp = static_cast<unsigned short *>(d.param) + off;
+        unsigned short *mp = reinterpret_cast<unsigned short *>(d.m) + off;
+        unsigned short *vp = reinterpret_cast<unsigned short *>(d.v) + off;
+        unsigned short *tp = STAR ? reinterpret_cast<unsigned short *>(d.tau) + off : nullptr;
+        if (cnt == VEC && vec_ok) {
+            float P[VEC], G[VEC], M[VEC], V[VEC], T[VEC];
+            ld_bf16_n<VEC>(pp, P);
+            load_grad_n<true, VEC>(grad, off, G);
+            ld_bf16_n<VEC>(mp, M);
+            ld_bf16_n<VEC>(vp, V);
+            if constexpr (STAR) {
+                ld_bf16_n<VEC>(tp, T);
+            } else {
+#pragma unroll
+                for (int k = 0; k < VEC; ++k) T[k] = 0.0f;
+            }
+            if (scaled) {
+#pragma unroll
+                for (int k = 0; k < VEC; ++k) G[k] = scale_grad<true>(G[k], gs);
+                if (pack.write_grad) store_grad_n<true, VEC>(grad, off, G);
             }
             update_n16<STAR, POWK, VEC>(P, G, M, V, T, sc, q, tab, acc);
             st_bf16_n<VEC>(pp, P);
@@ -721,10 +817,10 @@ __device__ __forceinline__ void thread_elems(const adana_tensor_desc &d, int64_t
             for (int e = 0; e < cnt; ++e) {
                 float P[1] = {bf16_to_f32(pp[e])}, M[1] = {bf16_to_f32(mp[e])}, V[1] = {bf16_to_f32(vp[e])};
                 float T[1] = {STAR ? bf16_to_f32(tp[e]) : 0.0f};
-                float G[1] = {load_grad1<true>(d.grad, off + e)};
+                float G[1] = {load_grad1<true>(grad, off + e)};
                 if (scaled) {
                     G[0] = scale_grad<true>(G[0], gs);
-                    if (pack.write_grad) store_grad1<true>(d.grad, off + e, G[0]);
+                    if (pack.write_grad) store_grad1<true>(grad, off + e, G[0]);
                 }
                 update_n16<STAR, POWK, 1>(P, G, M, V, T, sc, q, tab, acc);
                 pp[e] = f32_to_bf16(P[0]);
@@ -739,10 +835,10 @@ __device__ __forceinline__ void thread_elems(const adana_tensor_desc &d, int64_t
     float *mp = d.m + off;
     float *vp = d.v + off;
     float *tp = STAR ? d.tau + off : nullptr;
-    if (cnt == VEC && (d.flags & ADANA_DESC_VEC_OK)) {
+    if (cnt == VEC && vec_ok) {
         float P[VEC], G[VEC], M[VEC], V[VEC], T[VEC];
         ld_n<VEC>(pp, P);
-        load_grad_n<GBF16, VEC>(d.grad, off, G);
+        load_grad_n<GBF16, VEC>(grad, off, G);
         ld_n<VEC>(mp, M);
         ld_n<VEC>(vp, V);
         if constexpr (STAR) {
@@ -754,9 +850,9 @@ __device__ __forceinline__ void thread_elems(const adana_tensor_desc &d, int64_t
         if (scaled) {
 #pragma unroll
             for (int k = 0; k < VEC; ++k) G[k] = scale_grad<GBF16>(G[k], gs);
-            if (pack.write_grad) store_grad_n<GBF16, VEC>(d.grad, off, G);
+            if (pack.write_grad) store_grad_n<GBF16, VEC>(grad, off, G);
         }
-        update_n<STAR, POWK, VEC>(P, G, M, V, T, sc, tab, acc);
+        update_n<STAR, POWK, EAGER, VEC>(P, G, M, V, T, sc, tab, acc);
         if constexpr (UNIFORM && VEC == 4) {
             const int byte_off = static_cast<int>((off - seg0) * 4);
             st4_stream(static_cast<float *>(d.param) + seg0, byte_off, P);
@@ -774,12 +870,12 @@ __device__ __forceinline__ void thread_elems(const adana_tensor_desc &d, int64_t
         // unaligned tensor, or the last (< VEC) elements of a tensor
         for (int e = 0; e < cnt; ++e) {
             float mm = mp[e], vv = vp[e], tt = STAR ? tp[e] : 0.0f;
-            float g = load_grad1<GBF16>(d.grad, off + e);
+            float g = load_grad1<GBF16>(grad, off + e);
             if (scaled) {
                 g = scale_grad<GBF16>(g, gs);
-                if (pack.write_grad) store_grad1<GBF16>(d.grad, off + e, g);
+                if (pack.write_grad) store_grad1<GBF16>(grad, off + e, g);
             }
-            const float o = update_elem<STAR, POWK>(pp[e], g, mm, vv, tt, sc, tab, acc);
+            const float o = update_elem<STAR, POWK, EAGER>(pp[e], g, mm, vv, tt, sc, tab, acc);
             pp[e] = o;
             mp[e] = mm;
             vp[e] = vv;
@@ -816,8 +912,9 @@ __device__ __forceinline__ void block_partial(float (&acc)[4], float (*red)[kW][
     par ^= 1;
 }
 
-template <bool STAR, bool GBF16, int PM, int POWK, int VEC>
+template <bool STAR, bool GBF16, int PM, int POWK, bool EAGER, int VEC>
 __global__ __launch_bounds__(kChunk / VEC) void mta_step_kernel(const adana_tensor_desc *__restrict__ desc,
+                                                                const void *const *__restrict__ gradp,
                                                                 const int64_t *__restrict__ vstart,
                                                                 const int32_t *__restrict__ chunk_first,
                                                                 int32_t n, ScalarPack pack,
@@ -868,6 +965,7 @@ __global__ __launch_bounds__(kChunk / VEC) void mta_step_kernel(const adana_tens
     const int i0 = chunk_first[chunk];
     const int64_t vs0 = vstart[i0];
     const adana_tensor_desc d0 = desc[i0];
+    const void *g0 = gradp[i0];
     float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
     // both bounds at once (no short circuit), so that the descriptor's numel
     // is fetched with the rest of it rather than after a branch
@@ -878,8 +976,8 @@ __global__ __launch_bounds__(kChunk / VEC) void mta_step_kernel(const adana_tens
     }
     if (inside) {
         // the whole chunk lies in tensor i0
-        thread_elems<STAR, GBF16, PM, POWK, VEC, true>(d0, mine - vs0, vs0 + d0.numel - mine, lo - vs0, pack, gs,
-                                                          tab, acc);
+        thread_elems<STAR, GBF16, PM, POWK, EAGER, VEC, true>(d0, g0, mine - vs0, vs0 + d0.numel - mine, lo - vs0,
+                                                                 pack, gs, tab, acc);
         block_partial<kW>(acc, red, par, part4 + chunk + i0);
         return;
     }
@@ -895,8 +993,8 @@ __global__ __launch_bounds__(kChunk / VEC) void mta_step_kernel(const adana_tens
         const adana_tensor_desc d = desc[l];
         const int64_t vs = vstart[l];
         if (mine >= vs && mine < vs + d.numel)
-            thread_elems<STAR, GBF16, PM, POWK, VEC, false>(d, mine - vs, vs + d.numel - mine, 0, pack, gs, tab,
-                                                               acc);
+            thread_elems<STAR, GBF16, PM, POWK, EAGER, VEC, false>(d, gradp[l], mine - vs, vs + d.numel - mine, 0,
+                                                                      pack, gs, tab, acc);
     }
     // one (chunk, tensor) partial per tensor overlapping the chunk, in order
     for (int j = i0; j <= i1; ++j) {
@@ -1132,6 +1230,7 @@ constexpr int kSumsqChunks = 4;
 
 template <bool GBF16>
 __device__ __forceinline__ void sumsq_chunk(const adana_tensor_desc *__restrict__ desc,
+                                              const void *const *__restrict__ gradp,
                                               const int64_t *__restrict__ vstart, int first, int32_t n,
                                               int64_t chunk, double2 *__restrict__ partials, double (*red)[kWaves]) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -1140,21 +1239,21 @@ __device__ __forceinline__ void sumsq_chunk(const adana_tensor_desc *__restrict_
     for (int i = first; i < n; ++i) {
         const int64_t vs = vstart[i];
         if (vs >= hi) break;
-        const adana_tensor_desc d = desc[i];
-        const int64_t ve = vs + d.numel;
+        const int64_t ve = vs + desc[i].numel;
         if (ve <= lo) continue;
+        const void *grad = gradp[i];
         double acc = 0.0;
         if (mine >= vs && mine < ve) {
             const int64_t off = mine - vs;
             const int cnt = (ve - mine) < 4 ? static_cast<int>(ve - mine) : 4;
-            if (cnt == 4 && (d.flags & ADANA_DESC_VEC_OK)) {
+            if (cnt == 4 && grad_vec_aligned<GBF16>(grad)) {
                 float G[4];
-                load_grad_n<GBF16, 4>(d.grad, off, G);
+                load_grad_n<GBF16, 4>(grad, off, G);
 #pragma unroll
                 for (int k = 0; k < 4; ++k) acc += static_cast<double>(G[k]) * static_cast<double>(G[k]);
             } else {
                 for (int e = 0; e < cnt; ++e) {
-                    const double g = load_grad1<GBF16>(d.grad, off + e);
+                    const double g = load_grad1<GBF16>(grad, off + e);
                     acc += g * g;
                 }
             }
@@ -1170,6 +1269,7 @@ __device__ __forceinline__ void sumsq_chunk(const adana_tensor_desc *__restrict_
 
 template <bool GBF16>
 __global__ __launch_bounds__(kBlock) void grad_sumsq_kernel(const adana_tensor_desc *__restrict__ desc,
+                                                            const void *const *__restrict__ gradp,
                                                             const int64_t *__restrict__ vstart,
                                                             const int32_t *__restrict__ chunk_first,
                                                             int32_t n, int64_t n_chunks,
@@ -1181,12 +1281,13 @@ __global__ __launch_bounds__(kBlock) void grad_sumsq_kernel(const adana_tensor_d
     const int64_t nc = (n_chunks - c0) < K ? n_chunks - c0 : K;
     const int i0 = chunk_first[c0];
     const int64_t vs = vstart[i0];
-    const adana_tensor_desc d = desc[i0];
-    if (nc == K && vs <= c0 * kChunk && vs + d.numel >= (c0 + K) * kChunk && (d.flags & ADANA_DESC_VEC_OK)) {
+    const int64_t numel0 = desc[i0].numel;
+    const void *g0 = gradp[i0];
+    if (nc == K && vs <= c0 * kChunk && vs + numel0 >= (c0 + K) * kChunk && grad_vec_aligned<GBF16>(g0)) {
         const int64_t off0 = c0 * kChunk + 4 * tid - vs;
         float G[K][4];
 #pragma unroll
-        for (int c = 0; c < K; ++c) load_grad_n<GBF16, 4>(d.grad, off0 + c * kChunk, G[c]);
+        for (int c = 0; c < K; ++c) load_grad_n<GBF16, 4>(g0, off0 + c * kChunk, G[c]);
         double acc[K];
 #pragma unroll
         for (int c = 0; c < K; ++c) {
@@ -1208,7 +1309,7 @@ __global__ __launch_bounds__(kBlock) void grad_sumsq_kernel(const adana_tensor_d
             partials[c0 + tid + i0] = make_double2(((red[tid][0] + red[tid][1]) + red[tid][2]) + red[tid][3], 0.0);
         return;
     }
-    for (int c = 0; c < nc; ++c) sumsq_chunk<GBF16>(desc, vstart, chunk_first[c0 + c], n, c0 + c, partials, red);
+    for (int c = 0; c < nc; ++c) sumsq_chunk<GBF16>(desc, gradp, vstart, chunk_first[c0 + c], n, c0 + c, partials, red);
 }
 
 // Stage 1 of the norm combine: like the fold workgroups of combine_kernel, for one
@@ -1309,6 +1410,7 @@ __global__ __launch_bounds__(kClipThreads) void clip_finalize_kernel(const adana
 // optimizer step).
 template <bool GBF16>
 __global__ __launch_bounds__(kBlock) void grad_scale_kernel(const adana_tensor_desc *__restrict__ desc,
+                                                            const void *const *__restrict__ gradp,
                                                             const int64_t *__restrict__ vstart,
                                                             const int32_t *__restrict__ chunk_first,
                                                             int32_t n, const float *__restrict__ scale) {
@@ -1319,20 +1421,20 @@ __global__ __launch_bounds__(kBlock) void grad_scale_kernel(const adana_tensor_d
     for (int i = chunk_first[chunk]; i < n; ++i) {
         const int64_t vs = vstart[i];
         if (vs >= hi) break;
-        const adana_tensor_desc d = desc[i];
-        const int64_t ve = vs + d.numel;
+        const int64_t ve = vs + desc[i].numel;
         if (ve <= lo || mine < vs || mine >= ve) continue;
+        const void *grad = gradp[i];
         const int64_t off = mine - vs;
         const int cnt = (ve - mine) < 4 ? static_cast<int>(ve - mine) : 4;
-        if (cnt == 4 && (d.flags & ADANA_DESC_VEC_OK)) {
+        if (cnt == 4 && grad_vec_aligned<GBF16>(grad)) {
             float G[4];
-            load_grad_n<GBF16, 4>(d.grad, off, G);
+            load_grad_n<GBF16, 4>(grad, off, G);
 #pragma unroll
             for (int k = 0; k < 4; ++k) G[k] = scale_grad<GBF16>(G[k], s);
-            store_grad_n<GBF16, 4>(d.grad, off, G);
+            store_grad_n<GBF16, 4>(grad, off, G);
         } else {
             for (int e = 0; e < cnt; ++e)
-                store_grad1<GBF16>(d.grad, off + e, scale_grad<GBF16>(load_grad1<GBF16>(d.grad, off + e), s));
+                store_grad1<GBF16>(grad, off + e, scale_grad<GBF16>(load_grad1<GBF16>(grad, off + e), s));
         }
     }
 }
@@ -1415,42 +1517,51 @@ size_t lds_for_cap(int wgs, int64_t n_chunks) {
     return l <= static_cast<size_t>(lds_per_block[dev]) ? l : 0;
 }
 
-template <bool STAR, bool GBF16, int PM, int POWK>
-void launch_main(int64_t n_chunks, hipStream_t st, const adana_tensor_desc *d, const int64_t *vs,
-                 const int32_t *cf, int32_t n, const ScalarPack &pack, float *partials, int32_t *counters) {
+// The launch's device arrays and workspace pointers.
+struct LaunchArgs {
+    int64_t n_chunks;
+    hipStream_t st;
+    const adana_tensor_desc *desc;
+    const void *const *grad;
+    const int64_t *vstart;
+    const int32_t *chunk_first;
+    int32_t n;
+    float *partials;
+    int32_t *counters;
+};
+
+template <bool STAR, bool GBF16, int PM, int POWK, bool EAGER>
+void launch_main(const LaunchArgs &a, const ScalarPack &pack) {
     constexpr int kVec = 4;
-    const bool small_tensors = n_chunks < 64 * static_cast<int64_t>(n);
-    const size_t lds = lds_for_cap(residency_cap<STAR, PM, POWK>(small_tensors), n_chunks);
-    hipLaunchKernelGGL((mta_step_kernel<STAR, GBF16, PM, POWK, kVec>), dim3(static_cast<unsigned>(n_chunks)),
-                       dim3(kChunk / kVec), static_cast<unsigned>(lds), st, d, vs, cf, n, pack, partials,
-                       counters);
+    const bool small_tensors = a.n_chunks < 64 * static_cast<int64_t>(a.n);
+    const size_t lds = lds_for_cap(residency_cap<STAR, PM, POWK>(small_tensors), a.n_chunks);
+    hipLaunchKernelGGL((mta_step_kernel<STAR, GBF16, PM, POWK, EAGER, kVec>), dim3(static_cast<unsigned>(a.n_chunks)),
+                       dim3(kChunk / kVec), static_cast<unsigned>(lds), a.st, a.desc, a.grad, a.vstart,
+                       a.chunk_first, a.n, pack, a.partials, a.counters);
 }
 
-template <bool STAR, bool GBF16, int PM>
-void launch_pow(int powk, int64_t n_chunks, hipStream_t st, const adana_tensor_desc *d,
-                const int64_t *vs, const int32_t *cf, int32_t n, const ScalarPack &pack,
-                float *partials, int32_t *counters) {
+template <bool STAR, bool GBF16, int PM, bool EAGER>
+void launch_pow(int powk, const LaunchArgs &a, const ScalarPack &pack) {
     if constexpr (!STAR) {
         // ADana's (1 + t) ** (1 - kappa) is a host scalar: no per-element pow
-        launch_main<false, GBF16, PM, POW_ONE>(n_chunks, st, d, vs, cf, n, pack, partials, counters);
+        launch_main<false, GBF16, PM, POW_ONE, EAGER>(a, pack);
     } else if (powk == POW_GENERAL) {
-        launch_main<true, GBF16, PM, POW_GENERAL>(n_chunks, st, d, vs, cf, n, pack, partials, counters);
+        launch_main<true, GBF16, PM, POW_GENERAL, EAGER>(a, pack);
     } else if (powk == POW_ONE) {
-        launch_main<true, GBF16, PM, POW_ONE>(n_chunks, st, d, vs, cf, n, pack, partials, counters);
+        launch_main<true, GBF16, PM, POW_ONE, EAGER>(a, pack);
     } else if (powk == POW_SPECIAL) {
-        launch_main<true, GBF16, PM, POW_SPECIAL>(n_chunks, st, d, vs, cf, n, pack, partials, counters);
-    } else if constexpr (PM == PM_BF16) {
-        if (powk == POW_TABLE16)
-            launch_main<true, GBF16, PM, POW_TABLE16>(n_chunks, st, d, vs, cf, n, pack, partials, counters);
-    } else if constexpr (!GBF16 && PM == PM_F32) {  // Manau's branch: float32 only
+        launch_main<true, GBF16, PM, POW_SPECIAL, EAGER>(a, pack);
+    } else if constexpr (PM == PM_BF16 && EAGER) {
+        if (powk == POW_TABLE16) launch_main<true, GBF16, PM, POW_TABLE16, true>(a, pack);
+    } else if constexpr (!GBF16 && PM == PM_F32 && EAGER) {  // Manau's branch: float32, its own op order
         if (powk == POW_MANAU_GENERAL) {
-            launch_main<true, false, PM_F32, POW_MANAU_GENERAL>(n_chunks, st, d, vs, cf, n, pack, partials, counters);
+            launch_main<true, false, PM_F32, POW_MANAU_GENERAL, true>(a, pack);
         } else if (powk == POW_MANAU_ONE) {
-            launch_main<true, false, PM_F32, POW_MANAU_ONE>(n_chunks, st, d, vs, cf, n, pack, partials, counters);
+            launch_main<true, false, PM_F32, POW_MANAU_ONE, true>(a, pack);
         } else if (powk == POW_MANAU_SPECIAL) {
-            launch_main<true, false, PM_F32, POW_MANAU_SPECIAL>(n_chunks, st, d, vs, cf, n, pack, partials, counters);
+            launch_main<true, false, PM_F32, POW_MANAU_SPECIAL, true>(a, pack);
         } else {
-            launch_main<true, false, PM_F32, POW_MANAU_MK4>(n_chunks, st, d, vs, cf, n, pack, partials, counters);
+            launch_main<true, false, PM_F32, POW_MANAU_MK4, true>(a, pack);
         }
     }
 }
@@ -1469,6 +1580,37 @@ int pow_mode_of(double e) {
     if (e == 3.0) return ADANA_POW_CUBE;
     if (e == -2.0) return ADANA_POW_INVSQ;
     return ADANA_POW_GENERAL;
+}
+
+// Inductor's pow lowering (torch/_inductor/lowering.py, pow): an exponent
+// equal to an integer k becomes pow(x, k) -- 1 for k == 0, a copy for k == 1,
+// and for any other |k| < 32 the products of pow_recursive (pow_int_f32);
+// 0.5 becomes sqrt; anything else stays a pow with the exponent rounded to
+// binary32 (-0.5 included).  *k receives the integer exponent.
+int pow_mode_compiled(double e, int32_t *k) {
+    *k = 0;
+    if (e == 0.0) return ADANA_POW_ONE;
+    if (e == 1.0) return ADANA_POW_IDENTITY;
+    if (e == 0.5) return ADANA_POW_SQRT;
+    if (e == std::floor(e) && std::fabs(e) < 32.0) {
+        *k = static_cast<int32_t>(e);
+        return ADANA_POW_INT;
+    }
+    return ADANA_POW_GENERAL;
+}
+
+// ADana's (1 + step) ** (1 - kappa) on a 0-d float32 tensor under
+// torch.compile: Inductor's CPU code evaluates a general exponent as
+// std::pow(float, float), the exponent rounded to binary32.
+float pow0d_compiled(float x, double e) {
+    int32_t k;
+    switch (pow_mode_compiled(e, &k)) {
+    case ADANA_POW_ONE: return 1.0f;
+    case ADANA_POW_IDENTITY: return x;
+    case ADANA_POW_SQRT: return std::sqrt(x);
+    case ADANA_POW_INT: return pow_int_f32(x, k);
+    default: return std::pow(x, static_cast<float>(e));
+    }
 }
 
 // ATen pow(Tensor, Scalar) on a 0-d float tensor: specialisations as above,
@@ -1525,7 +1667,7 @@ int adana_step_scalars_init(adana_step_scalars *out, const adana_hparams *hp, do
     out->lerp_coef = out->lerp_small ? a : a - 1.0f;
     out->s = s;
     out->eps = static_cast<float>(hp->epsilon);
-    out->pw = pow0d(one_p_s, 1.0 - hp->kappa);
+    out->pw = hp->eager ? pow0d(one_p_s, 1.0 - hp->kappa) : pow0d_compiled(one_p_s, 1.0 - hp->kappa);
     out->min_p = 1.0f / one_p_s;
     out->has_clip = hp->has_clip ? 1 : 0;
     out->clip = hp->has_clip ? static_cast<float>(hp->clipsnr) : INFINITY;
@@ -1540,7 +1682,13 @@ int adana_step_scalars_init(adana_step_scalars *out, const adana_hparams *hp, do
     }
     out->opw = 1.0f + wdf;
     out->star_exp = static_cast<float>(1.0 - hp->kappa);
-    out->pow_mode = pow_mode_of(1.0 - hp->kappa);
+    if (hp->eager) {
+        out->pow_mode = pow_mode_of(1.0 - hp->kappa);
+    } else {
+        int32_t k;
+        out->pow_mode = pow_mode_compiled(1.0 - hp->kappa, &k);
+        out->pow_int = k;
+    }
     return ADANA_OK;
 }
 
@@ -1638,7 +1786,8 @@ int check_plan(const adana_plan *plan, const char *fn) {
     return ADANA_OK;
 }
 int check_plan_arrays(const adana_plan &pl, const char *fn) {
-    if (pl.n_tensors > 0 && (!pl.desc || !pl.vstart || !pl.fold_first || (pl.n_chunks > 0 && !pl.chunk_first)))
+    if (pl.n_tensors > 0 &&
+        (!pl.desc || !pl.grad || !pl.vstart || !pl.fold_first || (pl.n_chunks > 0 && !pl.chunk_first)))
         return adana_set_error(ADANA_E_INVALID, "%s: null pointer in the plan arrays", fn);
     return ADANA_OK;
 }
@@ -1656,7 +1805,7 @@ int step_impl(const char *fn, const adana_plan *plan, const adana_step_scalars *
     if (int rc = check_plan(plan, fn)) return rc;
     const adana_plan &pl = *plan;
     const uint32_t allowed = ADANA_VARIANT_STAR | ADANA_GRAD_BF16 | ADANA_PARAM_BF16 | ADANA_VARIANT_MANAU |
-                             ADANA_STATE_BF16 | (d_grad_scale ? ADANA_WRITE_GRAD : 0u);
+                             ADANA_STATE_BF16 | ADANA_NUMERICS_EAGER | (d_grad_scale ? ADANA_WRITE_GRAD : 0u);
     if (variant_flags & ~allowed)
         return adana_set_error(ADANA_E_INVALID, "%s: unknown variant flags 0x%x", fn, variant_flags);
     const bool manau = variant_flags & ADANA_VARIANT_MANAU;
@@ -1680,7 +1829,8 @@ int step_impl(const char *fn, const adana_plan *plan, const adana_step_scalars *
     memcpy(pack.c, h_scalars, sizeof(adana_step_scalars) * static_cast<size_t>(n_classes));
     pack.gscale = d_grad_scale;
     pack.write_grad = (variant_flags & ADANA_WRITE_GRAD) ? 1 : 0;
-    if (variant_flags & ADANA_STATE_BF16)
+    const bool eager = variant_flags & ADANA_NUMERICS_EAGER;
+    if (s16 && eager)
         for (int k = 0; k < n_classes; ++k) pack.c16[k] = scalars16(pack.c[k]);
     hipStream_t st = static_cast<hipStream_t>(stream);
     float *partials = static_cast<float *>(d_workspace);
@@ -1711,9 +1861,10 @@ int step_impl(const char *fn, const adana_plan *plan, const adana_step_scalars *
         }
         int powk = all_general ? POW_GENERAL : (all_one ? POW_ONE : POW_SPECIAL);
         if (manau) powk = mk4_trivial ? powk + POW_MANAU_GENERAL : POW_MANAU_MK4;
-        if (s16 && star && powk == POW_GENERAL) {
-            // bfloat16 state: one exponent for every class -> fill the launch's
-            // pow table first (16,385 entries, stream-ordered before the step)
+        if (s16 && eager && star && powk == POW_GENERAL) {
+            // bfloat16 state, every op rounded: the pow's input is a bfloat16
+            // value; with one exponent for every class, fill the launch's pow
+            // table first (16,385 entries, stream-ordered before the step)
             bool same_exp = true;
             for (int c = 1; c < n_classes; ++c) same_exp = same_exp && h_scalars[c].star_exp == h_scalars[0].star_exp;
             if (same_exp) {
@@ -1726,9 +1877,9 @@ int step_impl(const char *fn, const adana_plan *plan, const adana_step_scalars *
                 powk = POW_TABLE16;
             }
         }
+        const LaunchArgs la{pl.n_chunks, st, pl.desc, pl.grad, pl.vstart, pl.chunk_first, n, partials, counters};
 #define ADANA_LAUNCH(S, G, P) \
-        launch_pow<S, G, P>(powk, pl.n_chunks, st, pl.desc, pl.vstart, pl.chunk_first, n, pack, partials, \
-                            counters)
+        ((eager || manau) ? launch_pow<S, G, P, true>(powk, la, pack) : launch_pow<S, G, P, false>(powk, la, pack))
         if (star || manau) {
             if (s16) ADANA_LAUNCH(true, true, PM_BF16);
             else if (gb) { if (pb) ADANA_LAUNCH(true, true, PM_MASTER); else ADANA_LAUNCH(true, true, PM_F32); }
@@ -1858,10 +2009,10 @@ int adana_grad_clip_norm(const adana_plan *plan, uint32_t grad_flags, double max
     const int32_t n = pl.n_tensors;
     if (pl.n_chunks > 0) {
         const dim3 grid(static_cast<unsigned>((pl.n_chunks + kSumsqChunks - 1) / kSumsqChunks));
-        if (gb) hipLaunchKernelGGL(grad_sumsq_kernel<true>, grid, dim3(kBlock), 0, st, pl.desc, pl.vstart,
-                                   pl.chunk_first, n, pl.n_chunks, partials);
-        else hipLaunchKernelGGL(grad_sumsq_kernel<false>, grid, dim3(kBlock), 0, st, pl.desc, pl.vstart,
-                                pl.chunk_first, n, pl.n_chunks, partials);
+        if (gb) hipLaunchKernelGGL(grad_sumsq_kernel<true>, grid, dim3(kBlock), 0, st, pl.desc, pl.grad,
+                                   pl.vstart, pl.chunk_first, n, pl.n_chunks, partials);
+        else hipLaunchKernelGGL(grad_sumsq_kernel<false>, grid, dim3(kBlock), 0, st, pl.desc, pl.grad,
+                                pl.vstart, pl.chunk_first, n, pl.n_chunks, partials);
         if (int rc = launch_status(fn, "sum of squares")) return rc;
     }
     if (pl.n_folds > 0) {
@@ -1889,11 +2040,11 @@ int adana_grad_scale(const adana_plan *plan, uint32_t grad_flags, const float *d
     hipStream_t st = static_cast<hipStream_t>(stream);
     const dim3 grid(static_cast<unsigned>(pl.n_chunks));
     if (grad_flags & ADANA_GRAD_BF16)
-        hipLaunchKernelGGL(grad_scale_kernel<true>, grid, dim3(kBlock), 0, st, pl.desc, pl.vstart, pl.chunk_first,
-                           pl.n_tensors, d_scale);
+        hipLaunchKernelGGL(grad_scale_kernel<true>, grid, dim3(kBlock), 0, st, pl.desc, pl.grad, pl.vstart,
+                           pl.chunk_first, pl.n_tensors, d_scale);
     else
-        hipLaunchKernelGGL(grad_scale_kernel<false>, grid, dim3(kBlock), 0, st, pl.desc, pl.vstart, pl.chunk_first,
-                           pl.n_tensors, d_scale);
+        hipLaunchKernelGGL(grad_scale_kernel<false>, grid, dim3(kBlock), 0, st, pl.desc, pl.grad, pl.vstart,
+                           pl.chunk_first, pl.n_tensors, d_scale);
     return launch_status(fn, "scale");
 }
 

@@ -14,6 +14,13 @@
  * version counters are bumped directly.  Objects that are not exactly a
  * torch.Tensor or torch.nn.Parameter (subclasses may override attribute access)
  * take the generic Python path.
+ *
+ * StepTable holds one laid-out plan's rows and does a step's host work in one
+ * pass whether or not the gradients are new tensors: every gradient is checked
+ * against its parameter and its pointer gathered, the step counters advance
+ * and the parameters' version counters are bumped.  It also keeps the
+ * diagnostics bound in the state dicts, refreshed in place by each step, with
+ * any the caller still refers to moved aside first.
  */
 #include <torch/csrc/autograd/python_variable.h>
 #include <torch/csrc/autograd/variable.h>
@@ -23,6 +30,9 @@
 
 #include <cstdint>
 #include <exception>
+#include <new>
+#include <utility>
+#include <vector>
 
 namespace {
 
@@ -66,15 +76,16 @@ int data_ptr_of(PyObject *t, uint64_t *out) {
     return PyErr_Occurred() ? -1 : 0;
 }
 
-// states[i]["step"] += 1 for every dict; tensors stepped together hold equal
-// counts, so the new int of the previous entry is reused (ints are immutable)
-// when this entry's old int is equal.  0, or -1 with a Python error set.
-int advance_states(PyObject *states) {
-    const Py_ssize_t m = PyList_GET_SIZE(states);
+// states[i]["step"] += 1 for every dict (i < n; state(i) returns it, borrowed);
+// tensors stepped together hold equal counts, so the new int of the previous
+// entry is reused (ints are immutable) when this entry's old int is equal.
+// 0, or -1 with a Python error set.
+template <class State>
+int advance_states_impl(size_t n, State state) {
     PyObject *prev_v = nullptr, *prev_w = nullptr;
     int rc = 0;
-    for (Py_ssize_t i = 0; i < m && !rc; ++i) {
-        PyObject *st = PyList_GET_ITEM(states, i);
+    for (size_t i = 0; i < n && !rc; ++i) {
+        PyObject *st = state(i);
         if (!PyDict_Check(st)) {
             PyErr_SetString(PyExc_TypeError, "step counters: state entries must be dicts");
             rc = -1;
@@ -105,6 +116,13 @@ int advance_states(PyObject *states) {
     Py_XDECREF(prev_v);
     Py_XDECREF(prev_w);
     return rc;
+}
+int advance_states(PyObject *states) {
+    return advance_states_impl(static_cast<size_t>(PyList_GET_SIZE(states)),
+                               [states](size_t i) { return PyList_GET_ITEM(states, static_cast<Py_ssize_t>(i)); });
+}
+int advance_states_vec(const std::vector<PyObject *> &states) {
+    return advance_states_impl(states.size(), [&states](size_t i) { return states[i]; });
 }
 
 /* advance_if_same(params, grads, states[, param_ptrs[, grad_ptrs]]) -> bool
@@ -465,7 +483,374 @@ PyObject *bind_diag(PyObject *, PyObject *args) {
     Py_RETURN_NONE;
 }
 
+/* ---------------------------------------------------------------------------
+ * StepTable: one plan's rows (the stepped parameters, in launch order), their
+ * state dicts, the parameters that had no gradient when the plan was built,
+ * and the diagnostics bound into the state dicts.
+ * ------------------------------------------------------------------------- */
+struct TableData {
+    std::vector<PyObject *> params, states, inactive;   // strong references
+    std::vector<uint64_t> pptr;                          // parameter data pointers the plan holds
+    std::vector<uint64_t> last;                          // gradient pointers of the last accepted scan
+    std::vector<uint64_t> tmp;                           // this scan's pointers until it is accepted
+    std::vector<PyObject *> diag;                        // bound diagnostics, ncols per row (strong)
+    std::vector<std::pair<long, PyObject *>> cols;       // (kernel output column, state key), keys strong
+    c10::ScalarType want = c10::ScalarType::Float;
+};
+
+struct StepTable {
+    PyObject_HEAD
+    TableData *d;
+};
+
+void release_all(std::vector<PyObject *> &v) {
+    for (PyObject *o : v) Py_XDECREF(o);
+    v.clear();
+}
+
+void table_dealloc(PyObject *self) {
+    TableData *d = reinterpret_cast<StepTable *>(self)->d;
+    if (d) {
+        release_all(d->params);
+        release_all(d->states);
+        release_all(d->inactive);
+        release_all(d->diag);
+        for (auto &c : d->cols) Py_XDECREF(c.second);
+        delete d;
+    }
+    Py_TYPE(self)->tp_free(self);
+}
+
+PyTypeObject StepTableType = {PyVarObject_HEAD_INIT(nullptr, 0)};
+
+int copy_list(PyObject *lst, std::vector<PyObject *> &out) {
+    if (!PyList_Check(lst)) {
+        PyErr_SetString(PyExc_TypeError, "step_table: lists expected");
+        return -1;
+    }
+    const Py_ssize_t n = PyList_GET_SIZE(lst);
+    out.reserve(static_cast<size_t>(n));
+    for (Py_ssize_t i = 0; i < n; ++i) {
+        PyObject *o = PyList_GET_ITEM(lst, i);
+        Py_INCREF(o);
+        out.push_back(o);
+    }
+    return 0;
+}
+
+/* step_table(params, states, inactive, bf16) -> StepTable
+ *
+ * params: the plan's rows (exact torch.Tensor / nn.Parameter objects whose
+ * gradients the plan expects at their own layout); states: their state dicts;
+ * inactive: every other parameter of the optimizer (no gradient at plan
+ * time); bf16: the gradients are bfloat16 (else float32). */
+PyObject *step_table(PyObject *, PyObject *args) {
+    PyObject *params, *states, *inactive;
+    int bf16 = 0;
+    if (!PyArg_ParseTuple(args, "O!O!O!p", &PyList_Type, &params, &PyList_Type, &states, &PyList_Type, &inactive,
+                          &bf16))
+        return nullptr;
+    if (PyList_GET_SIZE(params) != PyList_GET_SIZE(states)) {
+        PyErr_SetString(PyExc_ValueError, "step_table: one state dict per parameter");
+        return nullptr;
+    }
+    StepTable *t = PyObject_New(StepTable, &StepTableType);
+    if (!t) return nullptr;
+    t->d = new (std::nothrow) TableData();
+    if (!t->d) {
+        Py_DECREF(t);
+        return PyErr_NoMemory();
+    }
+    TableData &d = *t->d;
+    d.want = bf16 ? c10::ScalarType::BFloat16 : c10::ScalarType::Float;
+    if (copy_list(params, d.params) || copy_list(states, d.states) || copy_list(inactive, d.inactive)) {
+        Py_DECREF(t);
+        return nullptr;
+    }
+    try {
+        d.pptr.resize(d.params.size());
+        d.last.assign(d.params.size(), 0);
+        d.tmp.assign(d.params.size(), 0);
+        for (size_t i = 0; i < d.params.size(); ++i) {
+            PyObject *p = d.params[i];
+            if (!THPVariable_CheckExact(p) || !PyDict_Check(d.states[i])) {
+                PyErr_SetString(PyExc_TypeError, "step_table: rows must be exact tensors with dict states");
+                Py_DECREF(t);
+                return nullptr;
+            }
+            d.pptr[i] = reinterpret_cast<uint64_t>(THPVariable_Unpack(p).const_data_ptr());
+        }
+        for (PyObject *p : d.inactive)
+            if (!THPVariable_CheckExact(p)) {
+                PyErr_SetString(PyExc_TypeError, "step_table: parameters must be exact tensors");
+                Py_DECREF(t);
+                return nullptr;
+            }
+    } catch (const std::exception &e) {
+        Py_DECREF(t);
+        PyErr_SetString(PyExc_RuntimeError, e.what());
+        return nullptr;
+    }
+    return reinterpret_cast<PyObject *>(t);
+}
+
+/* StepTable.scan(out_address) -> (lo, hi) or None
+ *
+ * One step's host bookkeeping for the plan (src/optim/adana.py:184-197,
+ * src/optim/dana_star_mk4.py:243-262) when the plan still fits: every row has
+ * a gradient that is a dense tensor of its parameter's device, shape, strides
+ * and the plan's dtype, every parameter keeps the storage the plan holds, and
+ * no inactive parameter has gained a gradient.  Then the gradients' data
+ * pointers are written to the uint64 array at out_address (one per row),
+ * every state's "step" goes up by one, every parameter's version counter is
+ * bumped (the launch that follows updates them in place), and the rows
+ * [lo, hi) whose gradient pointer differs from the last accepted scan are
+ * returned (lo == hi: none moved).  None, with nothing modified, when the
+ * plan does not fit: the caller takes its general path (which also raises
+ * the precise error for a bad gradient). */
+PyObject *table_scan(PyObject *self, PyObject *arg) {
+    TableData &d = *reinterpret_cast<StepTable *>(self)->d;
+    const unsigned long long addr = PyLong_AsUnsignedLongLong(arg);
+    if (PyErr_Occurred()) return nullptr;
+    uint64_t *out = reinterpret_cast<uint64_t *>(static_cast<uintptr_t>(addr));
+    const size_t n = d.params.size();
+    if (n && !out) {
+        PyErr_SetString(PyExc_ValueError, "StepTable.scan: null output array");
+        return nullptr;
+    }
+    try {
+        for (PyObject *p : d.inactive)
+            if (THPVariable_Unpack(p).unsafeGetTensorImpl()->grad().defined()) Py_RETURN_NONE;
+        size_t lo = n, hi = 0;
+        for (size_t i = 0; i < n; ++i) {
+            const at::Tensor &pt = THPVariable_Unpack(d.params[i]);
+            if (reinterpret_cast<uint64_t>(pt.const_data_ptr()) != d.pptr[i]) Py_RETURN_NONE;
+            const at::Tensor &g = pt.unsafeGetTensorImpl()->grad();
+            if (!g.defined() || g.is_sparse() || g.scalar_type() != d.want || g.device() != pt.device() ||
+                !same_layout(g, pt))
+                Py_RETURN_NONE;
+            const uint64_t gp = reinterpret_cast<uint64_t>(g.const_data_ptr());
+            d.tmp[i] = gp;
+            if (gp != d.last[i]) {
+                if (i < lo) lo = i;
+                hi = i + 1;
+            }
+        }
+        if (advance_states_vec(d.states)) return nullptr;
+        for (size_t i = 0; i < n; ++i) out[i] = d.tmp[i];
+        for (size_t i = lo; i < hi; ++i) d.last[i] = d.tmp[i];
+        for (PyObject *p : d.params) torch::autograd::impl::bump_version(THPVariable_Unpack(p));
+        if (lo > hi) lo = hi = 0;
+        return Py_BuildValue("nn", static_cast<Py_ssize_t>(lo), static_cast<Py_ssize_t>(hi));
+    } catch (const std::exception &e) {
+        PyErr_SetString(PyExc_RuntimeError, e.what());
+        return nullptr;
+    }
+}
+
+/* StepTable.forget() -> None: the next scan reports every row as moved (the
+ * device copy of the gradient pointers must be written in full again). */
+PyObject *table_forget(PyObject *self, PyObject *) {
+    TableData &d = *reinterpret_cast<StepTable *>(self)->d;
+    d.last.assign(d.last.size(), 0);
+    Py_RETURN_NONE;
+}
+
+/* StepTable.grads_are(grads) -> bool: row i's current gradient is grads[i]
+ * (the same tensor) for every row. */
+PyObject *table_grads_are(PyObject *self, PyObject *arg) {
+    TableData &d = *reinterpret_cast<StepTable *>(self)->d;
+    if (!PyList_Check(arg) || static_cast<size_t>(PyList_GET_SIZE(arg)) != d.params.size()) Py_RETURN_FALSE;
+    for (size_t i = 0; i < d.params.size(); ++i) {
+        PyObject *g = PyList_GET_ITEM(arg, static_cast<Py_ssize_t>(i));
+        if (!THPVariable_Check(g)) Py_RETURN_FALSE;
+        const at::Tensor &cur = THPVariable_Unpack(d.params[i]).unsafeGetTensorImpl()->grad();
+        if (!cur.defined() || cur.unsafeGetTensorImpl() != THPVariable_Unpack(g).unsafeGetTensorImpl())
+            Py_RETURN_FALSE;
+    }
+    Py_RETURN_TRUE;
+}
+
+/* A new 0-d tensor over element k of buf with a storage of its own that keeps
+ * buf's storage alive (a deepcopy of it copies only its own bytes). */
+PyObject *diag_tensor(const at::Tensor &buf, int64_t k) {
+    const c10::Storage keep = buf.storage();
+    char *base = static_cast<char *>(buf.data_ptr());
+    at::Tensor t = at::from_blob(base + buf.element_size() * k, at::IntArrayRef{}, [keep](void *) {}, buf.options());
+    return THPVariable_Wrap(std::move(t));
+}
+
+/* StepTable.diag_bind(buf, columns) -> None
+ *
+ * Row j's state[key] = a new 0-d tensor over buf[len(columns)_all * j + col]
+ * for every (col, key) in columns (buf holds 5 values per row, the kernel's
+ * output), kept by the table for diag_check / diag_rehome. */
+PyObject *table_diag_bind(PyObject *self, PyObject *args) {
+    TableData &d = *reinterpret_cast<StepTable *>(self)->d;
+    PyObject *bufobj, *columns;
+    if (!PyArg_ParseTuple(args, "OO!", &bufobj, &PyList_Type, &columns)) return nullptr;
+    if (!THPVariable_Check(bufobj)) {
+        PyErr_SetString(PyExc_TypeError, "StepTable.diag_bind: buf must be a tensor");
+        return nullptr;
+    }
+    try {
+        const at::Tensor &buf = THPVariable_Unpack(bufobj);
+        const size_t n = d.params.size();
+        if (!buf.is_contiguous() || buf.numel() < static_cast<int64_t>(5 * n)) {
+            PyErr_SetString(PyExc_ValueError, "StepTable.diag_bind: buffer too small or not contiguous");
+            return nullptr;
+        }
+        for (auto &c : d.cols) Py_XDECREF(c.second);
+        d.cols.clear();
+        release_all(d.diag);
+        const Py_ssize_t nc = PyList_GET_SIZE(columns);
+        for (Py_ssize_t c = 0; c < nc; ++c) {
+            long col;
+            PyObject *key;
+            if (!PyArg_ParseTuple(PyList_GET_ITEM(columns, c), "lO", &col, &key)) return nullptr;
+            if (col < 0 || col >= 5) {
+                PyErr_SetString(PyExc_ValueError, "StepTable.diag_bind: column out of range [0, 5)");
+                return nullptr;
+            }
+            Py_INCREF(key);
+            d.cols.emplace_back(col, key);
+        }
+        d.diag.assign(n * d.cols.size(), nullptr);
+        for (size_t j = 0; j < n; ++j)
+            for (size_t c = 0; c < d.cols.size(); ++c) {
+                PyObject *w = diag_tensor(buf, static_cast<int64_t>(5 * j) + d.cols[c].first);
+                if (!w) return nullptr;
+                if (PyDict_SetItem(d.states[j], d.cols[c].second, w)) {
+                    Py_DECREF(w);
+                    return nullptr;
+                }
+                d.diag[j * d.cols.size() + c] = w;                   // the table's reference
+            }
+    } catch (const std::exception &e) {
+        PyErr_SetString(PyExc_RuntimeError, e.what());
+        return nullptr;
+    }
+    Py_RETURN_NONE;
+}
+
+/* StepTable.diag_check() -> (held, lost)
+ *
+ * Before a step rewrites the diagnostics buffer in place: the bound
+ * diagnostics that something besides the state dict and the table still
+ * refers to (a Python reference, or another tensor over its storage, as a
+ * view or detach() gives) -- `held`, flat indices j * ncols + c -- and those
+ * whose state entry no longer is the bound tensor (replaced or deleted) --
+ * `lost`. */
+PyObject *table_diag_check(PyObject *self, PyObject *) {
+    TableData &d = *reinterpret_cast<StepTable *>(self)->d;
+    PyObject *held = PyList_New(0), *lost = PyList_New(0);
+    if (!held || !lost) {
+        Py_XDECREF(held);
+        Py_XDECREF(lost);
+        return nullptr;
+    }
+    for (size_t k = 0; k < d.diag.size(); ++k) {
+        PyObject *o = d.diag[k];
+        const Py_ssize_t rc = Py_REFCNT(o);
+        c10::StorageImpl *si = THPVariable_Unpack(o).unsafeGetTensorImpl()->unsafe_storage().unsafeGetStorageImpl();
+        PyObject *dst = nullptr;
+        if (rc > 2 || c10::raw::intrusive_ptr::use_count(si) > 1) dst = held;
+        else if (rc < 2) dst = lost;
+        if (dst) {
+            PyObject *ix = PyLong_FromSize_t(k);
+            if (!ix || PyList_Append(dst, ix)) {
+                Py_XDECREF(ix);
+                Py_DECREF(held);
+                Py_DECREF(lost);
+                return nullptr;
+            }
+            Py_DECREF(ix);
+        }
+    }
+    return Py_BuildValue("NN", held, lost);
+}
+
+void drop_storage(void *ctx) { delete static_cast<c10::Storage *>(ctx); }
+
+/* StepTable.diag_rehome(held, copy, lost, buf) -> None
+ *
+ * held[i] (a flat index from diag_check) keeps its value: its storage (and so
+ * every tensor sharing it) now reads element i of `copy`, which the caller
+ * has filled with the current values on the launch's stream.  Then every
+ * held and lost entry gets a new 0-d tensor over its element of `buf`, bound
+ * in its state dict and kept by the table. */
+PyObject *table_diag_rehome(PyObject *self, PyObject *args) {
+    TableData &d = *reinterpret_cast<StepTable *>(self)->d;
+    PyObject *held, *copyobj, *lost, *bufobj;
+    if (!PyArg_ParseTuple(args, "O!OO!O", &PyList_Type, &held, &copyobj, &PyList_Type, &lost, &bufobj)) return nullptr;
+    if (!THPVariable_Check(copyobj) || !THPVariable_Check(bufobj)) {
+        PyErr_SetString(PyExc_TypeError, "StepTable.diag_rehome: tensors expected");
+        return nullptr;
+    }
+    const size_t nc = d.cols.size();
+    try {
+        const at::Tensor &copy = THPVariable_Unpack(copyobj);
+        const at::Tensor &buf = THPVariable_Unpack(bufobj);
+        const Py_ssize_t nh = PyList_GET_SIZE(held);
+        if (!copy.is_contiguous() || copy.numel() < nh || copy.scalar_type() != buf.scalar_type()) {
+            PyErr_SetString(PyExc_ValueError, "StepTable.diag_rehome: copy does not match the held entries");
+            return nullptr;
+        }
+        char *cbase = static_cast<char *>(copy.data_ptr());
+        const int64_t es = copy.element_size();
+        for (int pass = 0; pass < 2; ++pass) {
+            PyObject *lst = pass == 0 ? held : lost;
+            for (Py_ssize_t i = 0; i < PyList_GET_SIZE(lst); ++i) {
+                const size_t k = PyLong_AsSize_t(PyList_GET_ITEM(lst, i));
+                if (PyErr_Occurred()) return nullptr;
+                if (k >= d.diag.size()) {
+                    PyErr_SetString(PyExc_IndexError, "StepTable.diag_rehome: index out of range");
+                    return nullptr;
+                }
+                if (pass == 0) {
+                    c10::StorageImpl *si =
+                        THPVariable_Unpack(d.diag[k]).unsafeGetTensorImpl()->unsafe_storage().unsafeGetStorageImpl();
+                    si->set_data_ptr_noswap(c10::DataPtr(cbase + es * i, new c10::Storage(copy.storage()),
+                                                         &drop_storage, copy.device()));
+                }
+                const size_t j = k / nc, c = k % nc;
+                PyObject *w = diag_tensor(buf, static_cast<int64_t>(5 * j) + d.cols[c].first);
+                if (!w) return nullptr;
+                if (PyDict_SetItem(d.states[j], d.cols[c].second, w)) {
+                    Py_DECREF(w);
+                    return nullptr;
+                }
+                Py_DECREF(d.diag[k]);
+                d.diag[k] = w;
+            }
+        }
+    } catch (const std::exception &e) {
+        PyErr_SetString(PyExc_RuntimeError, e.what());
+        return nullptr;
+    }
+    Py_RETURN_NONE;
+}
+
+PyMethodDef table_methods[] = {
+    {"scan", table_scan, METH_O,
+     "scan(out_address) -> (lo, hi) or None: check every row's gradient, write the gradient pointers, advance the "
+     "step counters and bump the parameters' versions; the rows whose pointer moved, or None (nothing done)"},
+    {"forget", table_forget, METH_NOARGS, "forget() -> None: the next scan reports every row as moved"},
+    {"grads_are", table_grads_are, METH_O, "grads_are(grads) -> bool: row i's gradient is grads[i] for every row"},
+    {"diag_bind", table_diag_bind, METH_VARARGS,
+     "diag_bind(buf, columns) -> None: bind a new 0-d tensor over buf[5 * j + col] as state[key] of every row"},
+    {"diag_check", table_diag_check, METH_NOARGS,
+     "diag_check() -> (held, lost): bound diagnostics still referred to elsewhere, and those no longer bound"},
+    {"diag_rehome", table_diag_rehome, METH_VARARGS,
+     "diag_rehome(held, copy, lost, buf) -> None: held entries read copy[i] from now on; held and lost entries "
+     "are bound anew over buf"},
+    {nullptr, nullptr, 0, nullptr},
+};
+
 PyMethodDef methods[] = {
+    {"step_table", step_table, METH_VARARGS,
+     "step_table(params, states, inactive, bf16) -> StepTable: the plan's rows, their state dicts, the other "
+     "parameters (no gradient at plan time) and the gradients' dtype"},
     {"bind_diag", bind_diag, METH_VARARGS,
      "bind_diag(buf, states, columns): states[j][key] = own-storage 0-d tensor over buf[5 * j + col] "
      "for (col, key) in columns"},
@@ -505,5 +890,20 @@ PyMODINIT_FUNC PyInit__hoststep(void) {
     if (!(g_step_name = PyUnicode_InternFromString("step"))) return nullptr;
     if (!(g_params_name = PyUnicode_InternFromString("params"))) return nullptr;
     if (!(g_one = PyLong_FromLong(1))) return nullptr;
-    return PyModule_Create(&module);
+    StepTableType.tp_name = "adana_amd._hoststep.StepTable";
+    StepTableType.tp_basicsize = sizeof(StepTable);
+    StepTableType.tp_dealloc = table_dealloc;
+    StepTableType.tp_flags = Py_TPFLAGS_DEFAULT;
+    StepTableType.tp_doc = "One laid-out plan's rows: the step's per-tensor host work in one pass";
+    StepTableType.tp_methods = table_methods;
+    if (PyType_Ready(&StepTableType) < 0) return nullptr;
+    PyObject *m = PyModule_Create(&module);
+    if (!m) return nullptr;
+    Py_INCREF(&StepTableType);
+    if (PyModule_AddObject(m, "StepTable", reinterpret_cast<PyObject *>(&StepTableType)) < 0) {
+        Py_DECREF(&StepTableType);
+        Py_DECREF(m);
+        return nullptr;
+    }
+    return m;
 }

@@ -104,7 +104,7 @@ class Manau(_DanaFamily):
         Optimizer.__init__(self, param_groups, defaults)
         self.distributed_mode = False
         self.lr = lr
-        self._engine_init(master_weights=False)
+        self._engine_init(master_weights=False, numerics="eager")   # the branch is eager ATen ops
         rows = {True: [], False: []}
         for group in self.param_groups:
             for name, p, to_muon in self._routes(group):

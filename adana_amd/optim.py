@@ -14,23 +14,38 @@ contiguous or permuted p, contiguous for a p with gaps (a slice such as
 ``w[:, :k]``).  The kernel pairs elements by their offset in the state's
 layout; a parameter or gradient of another layout is copied into a staging
 buffer of that layout before the launch and (the parameter) back after it,
-on the same stream.  Since T has p's dtype, bfloat16 parameters run the
-reference's own bfloat16 path: bfloat16 m, v, tau and diagnostics, every op
-of the update rounded to bfloat16 as ATen's ops round it (ADANA_STATE_BF16).
+on the same stream.  Since T has p's dtype, bfloat16 parameters keep
+bfloat16 m, v and tau, as in the reference.
+
+Numerics.  The reference always steps through torch.compile
+(src/optim/adana.py:72-79, 210-216; src/optim/dana_star_mk4.py:88-96, 275),
+and that is what the kernel reproduces by default (``numerics="compiled"``):
+Inductor's forms of lerp_ and addcmul_ (every product and sum rounded on its
+own), binary32 arithmetic throughout, and for bfloat16 state a rounding to
+bfloat16 only where m, v, tau and p are stored.  ``numerics="eager"``
+(keyword-only, an extension) reproduces the same update run as ATen eager
+ops instead: lerp_ and addcmul_ as single-rounded fused multiply-adds and, on
+bfloat16 state, every op rounded to bfloat16.
 
 What differs is how a step executes.  The reference loops over tensors in
 Python, makes six 0-d device tensors per tensor and calls a torch.compile'd
 update per tensor (src/optim/adana.py:184-225).  Here the host computes the
 per-step scalars once per (group, step) class in C, and a single
 multi-tensor HIP kernel (adana_amd/csrc/adana_mta.hip) updates every tensor
-and writes all diagnostics into one device buffer.  As in the reference
-(which binds new 0-d tensors each step), every step binds new diagnostic
-tensors, each with a storage of its own over a new buffer, so a diagnostic
-kept from one step keeps its value.  That costs about 2 us of host time per
-parameter, so for lists of more than 512 stepped tensors (10,000 small
-tensors, say, where it would exceed the device's step) the entries are
-instead bound once and refreshed in place; ``fresh_diagnostics`` (keyword-
-only, an extension) forces either.
+and writes all diagnostics into one device buffer.  The per-tensor host work
+(gradient checks and pointers, step counters, version counters) is one C++
+pass (adana_amd/_hoststep.StepTable); only gradient pointers that moved since
+the last step are uploaded.
+
+Diagnostics.  The reference binds five new 0-d tensors per parameter every
+step (adana.py:221-225), so a diagnostic kept from one step keeps its value.
+Here every step writes into the same buffer, over which the state entries
+are bound; before a step rewrites it, any entry something else still refers
+to (a Python reference, a view, a detach()) is moved to a copy of its own
+and the state gets a new tensor.  That check costs a few ns per entry; for
+lists of more than 2,048 stepped tensors it is skipped (a warning says so
+once), and a kept diagnostic then follows the buffer.  ``fresh_diagnostics``
+(keyword-only, an extension) forces the check on (True) or off (False).
 
 Gradient clipping (src/optim/base.py:250-257): ``opt.clip_grad_norm_(max_norm)``
 (or ``adana_amd.clip_grad_norm_(params, max_norm, optimizer=opt)``) returns
@@ -46,6 +61,7 @@ from __future__ import annotations
 
 import ctypes
 import operator
+import warnings
 from typing import Iterable, List, Optional
 
 import numpy as np
@@ -104,17 +120,19 @@ class _LaunchSet:
         self.states: List[dict] = []
         self.sclass: List[int] = []
         self.host_desc = None
+        self.host_grad = None       # numpy uint64: the gradient pointers the device array holds
         self.vstart = None
         self.fold_first = None
         self.n_chunks = 0
         self.n_folds = 0
-        self.dev_table = None
+        self.dev_table = None       # [descriptors | vstart | fold_first]
+        self.dev_grad = None        # int64 device array: adana_plan.grad
         self.chunk_first = None
         self.workspace = None
         self.plan = None
         self.diag = None
-        self.ptr_key = None         # the gradients' and parameters' data pointers the tables hold
-        self.rest_ok = None         # per row: the non-gradient pointers allow the vector path
+        self.table = None           # _hoststep.StepTable over the rows (diagnostics; the fast scan)
+        self.ptr_key = None         # the parameters' data pointers the tables hold
         self.stage = []             # (row, param staging or None, grad staging or None)
         self.stage_bufs = {}        # (row, "p" | "g") -> staging tensor, kept while it fits
 
@@ -126,16 +144,22 @@ class _DanaFamily(Optimizer):
     _VARIANT = 0                                   # adana_mta_step variant flags
     _KEYS = ("m", "v", "tau")                      # state keys of the moments and tau
     _DIAG_COLUMNS = tuple(enumerate(DIAG_KEYS))    # (kernel output column, state key)
-    _FRESH_DIAG_MAX_TENSORS = 512                  # default limit of fresh diagnostics per step
+    _DIAG_CHECK_MAX_TENSORS = 2048                 # default limit of the kept-diagnostics check
 
-    def _engine_init(self, master_weights: bool, fresh_diagnostics: Optional[bool] = None) -> None:
+    def _engine_init(self, master_weights: bool, fresh_diagnostics: Optional[bool] = None,
+                     numerics: str = "compiled") -> None:
+        if numerics not in ("compiled", "eager"):
+            raise ValueError(f"numerics must be 'compiled' or 'eager', got {numerics!r}")
         self.master_weights = bool(master_weights)
         self.fresh_diagnostics = fresh_diagnostics
+        self.numerics = numerics
         self._diag_cols = [tuple(c) for c in self._DIAG_COLUMNS]
         self._sets: Optional[List[_LaunchSet]] = None
         self._structure = None
         self._flat = None
-        self._active = None
+        self._fast = False          # one launch set, no staging: step() may take StepTable.scan
+        self._classes = None
+        self._diag_warned = False
         self._pending_clip = None
         self._clip_plan_obj = None
         self._diag_loc = {}        # param -> (launch set, row) of its latest plan
@@ -171,7 +195,7 @@ class _DanaFamily(Optimizer):
         super().__setstate__(state)
         if config is not None:
             self.__dict__.update(config)
-            self._engine_init(self.master_weights, self.fresh_diagnostics)
+            self._engine_init(self.master_weights, self.fresh_diagnostics, getattr(self, "numerics", "compiled"))
         if coef is not None:
             params, _ = self._flat_params()
             own = [g for g in map(_GRAD, params) if g is not None]
@@ -245,7 +269,7 @@ class _DanaFamily(Optimizer):
         self._sets = None
         self._structure = None
         self._flat = None
-        self._active = None
+        self._fast = False
         self._diag_epoch += 1
 
     def load_state_dict(self, state_dict) -> None:
@@ -337,7 +361,7 @@ class _DanaFamily(Optimizer):
             # expanded one) or race; the update is written back element by element
             raise NotImplementedError(f"{type(self).__name__}: parameters whose elements may share memory "
                                       f"(strides {tuple(p.stride())}) are not supported")
-        flags = self._VARIANT
+        flags = self._VARIANT | (_lib.NUMERICS_EAGER if self.numerics == "eager" else 0)
         if p.dtype == torch.float32:
             if g.dtype != torch.float32:
                 raise RuntimeError(f"{type(self).__name__}: float32 parameter with {g.dtype} "
@@ -347,21 +371,23 @@ class _DanaFamily(Optimizer):
                 raise RuntimeError(f"{type(self).__name__}: bfloat16 parameter with {g.dtype} "
                                    "gradient (expected bfloat16)")
             # master_weights: float32 master and moments (extension); otherwise the
-            # reference's own bfloat16 path, m, v, tau bfloat16 and every op rounded
+            # reference's own bfloat16 path, m, v, tau bfloat16 as zeros_like(p) makes them
             flags |= _lib.GRAD_BF16 | (_lib.PARAM_BF16 if self.master_weights else _lib.STATE_BF16)
         else:
             raise NotImplementedError(f"{type(self).__name__}: parameter dtype {p.dtype}")
         return flags
 
     def _desc_rows(self, ls: _LaunchSet) -> np.ndarray:
-        """Descriptor rows of the launch set; also records in ``ls.rest_ok``
-        whether each row's pointers other than the gradient's are 16-byte
-        aligned (the vector path needs them and the gradient aligned)."""
+        """Descriptor rows of the launch set, and its gradient pointers in
+        ``ls.host_grad`` (the gradient's staging buffer where it has one).
+        The descriptor's vector-path flag covers the pointers other than the
+        gradient's, whose alignment the kernel checks itself."""
         n = len(ls.params)
         d = np.zeros(n, dtype=_lib.DESC_DTYPE)
-        rest = np.zeros(n, dtype=bool)
+        gptr = np.zeros(n, dtype=np.uint64)
         km, kv, kt = self._KEYS
         stage = []
+        vec = 8 if ls.flags & _lib.STATE_BF16 else 16       # 4 elements of the state dtype
         for j, (p, g, st) in enumerate(zip(ls.params, ls.grads, ls.states)):
             # The kernel pairs elements by storage offset, in the layout of the
             # state (zeros_like(p): p's strides for a contiguous or permuted p,
@@ -377,15 +403,13 @@ class _DanaFamily(Optimizer):
             param_ptr = master.data_ptr() if master is not None else pt.data_ptr()
             lp_ptr = pt.data_ptr() if master is not None else 0
             tau_ptr = st[kt].data_ptr() if self._STAR else 0
-            gp = (g if gs is None else gs).data_ptr()
+            gptr[j] = (g if gs is None else gs).data_ptr()
             m_ptr, v_ptr = st[km].data_ptr(), st[kv].data_ptr()
-            vec = 8 if ls.flags & _lib.STATE_BF16 else 16       # 4 elements of the state dtype
-            rest[j] = (param_ptr % vec == 0 and m_ptr % vec == 0 and v_ptr % vec == 0
-                       and tau_ptr % vec == 0 and lp_ptr % 8 == 0)
-            ok = rest[j] and gp % (8 if g.dtype == torch.bfloat16 else 16) == 0
-            d[j] = (param_ptr, gp, m_ptr, v_ptr, tau_ptr, lp_ptr, p.numel(), ls.sclass[j],
+            ok = (param_ptr % vec == 0 and m_ptr % vec == 0 and v_ptr % vec == 0
+                  and tau_ptr % vec == 0 and lp_ptr % 8 == 0)
+            d[j] = (param_ptr, 0, m_ptr, v_ptr, tau_ptr, lp_ptr, p.numel(), ls.sclass[j],
                     _lib.DESC_VEC_OK if ok else 0)
-        ls.rest_ok = rest
+        ls.host_grad = gptr
         ls.stage = stage
         return d
 
@@ -402,25 +426,42 @@ class _DanaFamily(Optimizer):
         return buf
 
     def _upload(self, ls: _LaunchSet) -> None:
-        """Copy [descriptors | vstart | fold_first] to the device (async, pinned)."""
+        """Copy [descriptors | vstart | fold_first] and the gradient pointers
+        to the device (async, pinned) and point the plan at them."""
         table = np.concatenate([ls.host_desc.view(np.uint8), ls.vstart.view(np.uint8),
                                 ls.fold_first.view(np.uint8)])
         host = torch.from_numpy(table).pin_memory()
+        n = len(ls.params)
         if ls.dev_table is None or ls.dev_table.numel() != host.numel():
             ls.dev_table = torch.empty(host.numel(), dtype=torch.uint8, device=ls.device)
+        if ls.dev_grad is None or ls.dev_grad.numel() != max(n, 1):
+            ls.dev_grad = torch.zeros(max(n, 1), dtype=torch.int64, device=ls.device)
         ls.dev_table.copy_(host, non_blocking=True)
-        n = len(ls.params)
+        if n:
+            ls.dev_grad.copy_(torch.from_numpy(ls.host_grad.view(np.int64)).pin_memory(), non_blocking=True)
         base = ls.dev_table.data_ptr()
         if ls.plan is None:
             ls.plan = _lib.Plan()
         ls.plan.desc = base
+        ls.plan.grad = ls.dev_grad.data_ptr()
         ls.plan.vstart = base + 64 * n
         ls.plan.fold_first = base + 64 * n + 8 * (n + 1)
         ls.plan.n_tensors = n
         ls.plan.n_chunks = ls.n_chunks
         ls.plan.n_folds = ls.n_folds
 
-    def _build(self, params, grads, states, sclass, flags_list) -> List[_LaunchSet]:
+    @staticmethod
+    def _upload_grads(ls: _LaunchSet, lo: int, hi: int) -> None:
+        """Copy gradient pointers [lo, hi) of ls.host_grad to the device (async,
+        pinned; stream-ordered before the launch that reads them)."""
+        host = torch.from_numpy(ls.host_grad[lo:hi].view(np.int64)).pin_memory()
+        ls.dev_grad[lo:hi].copy_(host, non_blocking=True)
+
+    def _build(self, params, grads, states, sclass, flags_list, inactive=None) -> List[_LaunchSet]:
+        """Lay out the launch sets of this step's (param, grad, state) rows.
+        ``inactive``: the optimizer's other parameters (no gradient now);
+        given, and with a single launch set that stages nothing, step() may
+        take the one-pass StepTable.scan from the next step on."""
         sets = {}
         for i, (p, g, st, c, fl) in enumerate(zip(params, grads, states, sclass, flags_list)):
             key = (p.device, fl, c // _lib.MAX_CLASSES)
@@ -433,12 +474,16 @@ class _DanaFamily(Optimizer):
             ls.states.append(st)
             ls.sclass.append(c - ls.class_base)
         out = list(sets.values())
+        fast = (inactive is not None and len(out) == 1
+                and all(type(t) in (torch.Tensor, torch.nn.Parameter) for t in params)
+                and all(type(t) in (torch.Tensor, torch.nn.Parameter) for t in inactive))
         for ls in out:
             self._check_state_shapes(ls)
             numels = np.fromiter((p.numel() for p in ls.params), dtype=np.int64, count=len(ls.params))
             ls.vstart, ls.fold_first, ls.n_chunks, ls.n_folds = _lib.plan_layout(numels)
             ls.host_desc = self._desc_rows(ls)
-            ls.ptr_key = (_hoststep.data_ptrs(ls.grads), _hoststep.data_ptrs(ls.params))
+            ls.ptr_key = _hoststep.data_ptrs(ls.params)
+            fast = fast and not ls.stage
             with torch.cuda.device(ls.device):
                 self._upload(ls)
                 n = len(ls.params)
@@ -454,13 +499,17 @@ class _DanaFamily(Optimizer):
                 # the reference's bfloat16 path keeps bfloat16 diagnostics
                 ls.diag = torch.full((len(ls.params), 5), float("nan"), device=ls.device,
                                      dtype=torch.bfloat16 if ls.flags & _lib.STATE_BF16 else torch.float32)
+            # The rows' table: its scan is the fast path of the next steps (a
+            # single launch set only), and it keeps the diagnostics bound as
             # 0-d tensors over the kernel's output rows, each with a storage of
-            # its own: a deepcopy of one parameter's state (DynamicsLogger,
-            # src/logger/logger.py:93) then copies 4 bytes per diagnostic, not
-            # the whole list's buffer
-            _hoststep.bind_diag(ls.diag, ls.states, self._diag_cols)
+            # its own (a deepcopy of one parameter's state, as DynamicsLogger
+            # takes, src/logger/logger.py:93, copies its own bytes only).
+            ls.table = _hoststep.step_table(ls.params, ls.states, list(inactive) if fast else [],
+                                            bool(ls.flags & _lib.GRAD_BF16))
+            ls.table.diag_bind(ls.diag, self._diag_cols)
             for j, p in enumerate(ls.params):
                 self._diag_loc[p] = (ls, j)
+        self._fast = fast
         self._diag_epoch += 1
         return out
 
@@ -527,6 +576,7 @@ class _DanaFamily(Optimizer):
         hp.wd_ts = self.wd_ts
         hp.gamma_3_factor = self.gamma_3_factor
         hp.wd_decaying = 1 if self.wd_decaying else 0
+        hp.eager = 1 if self.numerics == "eager" else 0
         return hp
 
     def _flat_params(self):
@@ -541,7 +591,7 @@ class _DanaFamily(Optimizer):
                 params.extend(group["params"])
                 gidx.extend([gi] * len(group["params"]))
             self._flat = (sig, params, gidx)
-            self._active = None
+            self._fast = False
         return self._flat[1], self._flat[2]
 
     def _scalars(self, classes):
@@ -588,106 +638,113 @@ class _DanaFamily(Optimizer):
             # src/optim/adana.py:163-167: g2 = g3 = lr, sf = lr / self.lr
             group["weighted_step_count"] += group["lr"] / self.lr
         all_params, gidx = self._flat_params()
-        act = self._active
-        if (self._sets is not None and act is not None
-                and _hoststep.advance_if_same(all_params, act["all_grads"], act["states"], act["pptrs"],
-                                              act["gptrs"])):
-            # Persistent gradients: every p.grad is the same tensor object as at
-            # the last step (grad None where it was None), and every parameter
-            # and gradient keeps its storage, so the active set, device tables and scalar
-            # classes carry over; advance_if_same has already done the
-            # per-tensor ``state['step'] += 1`` (adana.py:197).
-            grads = act["grads"]
-            classes = act["classes"] = [(gi, t + 1) for gi, t in act["classes"]]
-            params = act["params"]
-            return self._launch(params, grads, classes, loss)
-        scan = None
-        if self._sets is not None and act is not None and act["all"] and len(self._sets) == 1:
-            # one launch set over every parameter: the gradients, their None
-            # pattern, both pointer tables and the layout check in one pass
-            scan = _hoststep.grads_scan(all_params, bool(self._sets[0].flags & _lib.GRAD_BF16))
-            all_grads, absent = scan[0], scan[1]                             # adana.py:186
+        if self._fast:
+            # One launch set that stages nothing: one C++ pass checks that every
+            # row still has a gradient of its parameter's layout and that no
+            # other parameter gained one, gathers the gradient pointers, does
+            # every ``state['step'] += 1`` (adana.py:197) and bumps the
+            # parameters' versions; only pointers that moved are uploaded.
+            ls = self._sets[0]
+            span = ls.table.scan(ls.host_grad.ctypes.data)
+            if span is not None:
+                self._classes = [(gi, t + 1) for gi, t in self._classes]
+                if span[1] > span[0]:
+                    self._upload_grads(ls, span[0], span[1])
+                return self._launch(None, None, self._classes, loss)
+        # The general path: the reference's walk (adana.py:184-197) in Python.
+        params, grads, states, keys, inactive = [], [], [], [], []
+        fresh = []
+        for p, gi in zip(all_params, gidx):
+            g = p.grad
+            if g is None:                                                    # adana.py:186
+                inactive.append(p)
+                continue
+            st = self.state[p]
+            if len(st) == 0:                                                 # adana.py:191-195
+                fresh.append((p, st))
+                st["step"] = 0
+            st["step"] += 1                                                  # adana.py:197
+            params.append(p)
+            grads.append(g)
+            states.append(st)
+            keys.append((gi, st["step"]))
+        if fresh:
+            self._pack_states(fresh, None)
+        if not params:
+            self._fast = False
+            return loss
+        # (group, step) scalar classes
+        cls_index = {}
+        sclass = []
+        for k in keys:
+            c = cls_index.get(k)
+            if c is None:
+                c = cls_index[k] = len(cls_index)
+            sclass.append(c)
+        classes = list(cls_index)
+        structure = (tuple(map(id, params)), tuple(sclass), tuple(map(id, inactive)))
+        if self._sets is None or structure != self._structure:
+            flags = [self._validate(p, g) for p, g in zip(params, grads)]
+            self._sets = self._build(params, grads, states, sclass, flags, inactive)
+            self._structure = structure
         else:
-            all_grads, absent = _hoststep.grads_of(all_params)               # adana.py:186
-
-        if self._sets is not None and act is not None and act["absent"] == absent:
-            # Steady state: the same tensors have gradients as at the last step
-            # (new gradient tensors, as after zero_grad(set_to_none=True)), so
-            # every active tensor advances by one and the scalar classes carry
-            # over; the device tables are re-pointed where an address moved.
-            grads = all_grads if act["all"] else [all_grads[i] for i in act["index"]]
-            _hoststep.advance_steps(act["states"])                             # adana.py:197
-            classes = act["classes"] = [(gi, t + 1) for gi, t in act["classes"]]
-            params = act["params"]
-            if scan is not None:
-                ls = self._sets[0]
-                ls.grads = grads
-                self._refresh_ptrs(ls, key=(scan[2], scan[3]), grads_ok=scan[4])
-                act["pptrs"], act["gptrs"] = scan[3], scan[2]
-            else:
-                for ls in self._sets:
-                    ls.grads = grads if len(self._sets) == 1 else [grads[i] for i in ls.index]
-                    self._refresh_ptrs(ls)
-                act["pptrs"] = _hoststep.data_ptrs(all_params)
-                act["gptrs"] = _hoststep.data_ptrs(all_grads)
-            act["all_grads"] = all_grads
-            act["grads"] = grads
-        else:
-            params, grads, states, keys, index, fresh = [], [], [], [], [], []
-            for i, (p, g) in enumerate(zip(all_params, all_grads)):
-                if g is None:                                                # adana.py:186
-                    continue
-                st = self.state[p]
-                if len(st) == 0:                                             # adana.py:191-195
-                    fresh.append((p, st))
-                    st["step"] = 0
-                st["step"] += 1                                              # adana.py:197
-                params.append(p)
-                grads.append(g)
-                states.append(st)
-                keys.append((gidx[i], st["step"]))
-                index.append(i)
-            if fresh:
-                self._pack_states(fresh, None)
-            if not params:
-                self._active = None
-                return loss
-            # (group, step) scalar classes
-            cls_index = {}
-            sclass = []
-            for k in keys:
-                c = cls_index.get(k)
-                if c is None:
-                    c = cls_index[k] = len(cls_index)
-                sclass.append(c)
-            classes = list(cls_index)
-            structure = (tuple(map(id, params)), tuple(sclass))
-            if self._sets is None or structure != self._structure:
-                flags = [self._validate(p, g) for p, g in zip(params, grads)]
-                self._sets = self._build(params, grads, states, sclass, flags)
-                self._structure = structure
-            else:
-                for ls in self._sets:
-                    ls.grads = grads if len(self._sets) == 1 else [grads[i] for i in ls.index]
-                    self._refresh_ptrs(ls)
-            self._active = {"absent": absent, "all": len(index) == len(all_params),
-                            "index": index, "states": states, "params": params,
-                            "classes": classes, "all_grads": all_grads, "grads": grads,
-                            "pptrs": _hoststep.data_ptrs(all_params), "gptrs": _hoststep.data_ptrs(all_grads)}
+            for ls in self._sets:
+                ls.grads = grads if len(self._sets) == 1 else [grads[i] for i in ls.index]
+                self._refresh_ptrs(ls)
+        self._classes = classes
         return self._launch(params, grads, classes, loss)
 
     _step_hooked = Optimizer.profile_hook_step(torch.no_grad()(_step))
 
+    def _diag_checked(self) -> bool:
+        """Whether this step checks the bound diagnostics before rewriting them
+        (fresh_diagnostics: True / False forces it; None: lists of at most
+        _DIAG_CHECK_MAX_TENSORS stepped tensors)."""
+        if self.fresh_diagnostics is not None:
+            return bool(self.fresh_diagnostics)
+        if sum(len(ls.params) for ls in self._sets) <= self._DIAG_CHECK_MAX_TENSORS:
+            return True
+        if not self._diag_warned:
+            self._diag_warned = True
+            warnings.warn(f"{type(self).__name__}: more than {self._DIAG_CHECK_MAX_TENSORS} stepped tensors, so "
+                          "each step refreshes the diagnostics in state in place without checking whether one "
+                          "is still held elsewhere (a diagnostic kept from an earlier step then shows the latest "
+                          "value); pass fresh_diagnostics=True to keep the reference's new tensors per step",
+                          RuntimeWarning, stacklevel=4)
+        return False
+
+    def _diag_guard(self, ls: _LaunchSet) -> None:
+        """Before a step rewrites ls.diag in place: every bound diagnostic that
+        something else still refers to keeps its value in a copy of its own
+        (taken on the launch's stream, ahead of the launch), and the state
+        gets a new 0-d tensor over the buffer, as the reference binds new
+        tensors every step (src/optim/adana.py:221-225)."""
+        held, lost = ls.table.diag_check()
+        if not held and not lost:
+            return
+        copy = ls.diag.new_empty(0)
+        if held:
+            nc = len(self._diag_cols)
+            flat = [(k // nc) * 5 + self._diag_cols[k % nc][0] for k in held]
+            copy = ls.diag.view(-1).index_select(0, torch.tensor(flat, dtype=torch.int64, device=ls.device))
+        ls.table.diag_rehome(held, copy, lost, ls.diag)
+
     def _launch(self, params, grads, classes, loss):
-        """One adana_mta_step (or adana_mta_step_scaled) per launch set."""
+        """One adana_mta_step (or adana_mta_step_scaled) per launch set.
+        ``params``/``grads``: the step's rows from the general path (their
+        versions are bumped here), or None after StepTable.scan (which bumped
+        them)."""
         # a clip armed by clip_grad_norm_(..., optimizer=self) on exactly these
         # gradients is applied inside the kernel; otherwise it is applied now
         gscale, wflag = None, 0
         pend = self._pending_clip
         if pend is not None:
             own, _, clip, write_back = pend
-            if (len(own) == len(grads) and all(map(operator.is_, grads, own))
-                    and all(ls.device == clip.device for ls in self._sets)):
+            if grads is None:
+                same = self._sets[0].table.grads_are(own)
+            else:
+                same = len(own) == len(grads) and all(map(operator.is_, grads, own))
+            if same and all(ls.device == clip.device for ls in self._sets):
                 self._pending_clip = None
                 gscale = clip.data_ptr() + 4
                 wflag = _lib.WRITE_GRAD if write_back else 0
@@ -696,47 +753,50 @@ class _DanaFamily(Optimizer):
 
         scalars = self._scalars(classes)
         L = _lib.lib()
-        fresh = self.fresh_diagnostics
-        if fresh is None:
-            fresh = sum(len(ls.params) for ls in self._sets) <= self._FRESH_DIAG_MAX_TENSORS
+        checked = self._diag_checked()
+        cur = torch.cuda.current_device()
         for ls in self._sets:
-            if fresh:
-                # a new buffer for this step's diagnostics (stream-ordered
-                # reuse by the caching allocator once nothing refers to it)
-                ls.diag = torch.empty_like(ls.diag)
             n_cls = min(_lib.MAX_CLASSES, len(classes) - ls.class_base)
             sc_arr = (type(scalars[0]) * n_cls)(*scalars[ls.class_base:ls.class_base + n_cls])
-            with torch.cuda.device(ls.device):
-                stream = torch.cuda.current_stream(ls.device).cuda_stream
-                for j, ps, gs in ls.stage:       # into the state's layout (same stream)
-                    if ps is not None and not ls.flags & _lib.PARAM_BF16:   # the master is read instead
-                        ps.copy_(ls.params[j])
-                    if gs is not None:
-                        gs.copy_(ls.grads[j])
-                if gscale is None:
-                    _lib.check(L.adana_mta_step(
-                        ctypes.byref(ls.plan), ctypes.cast(sc_arr, ctypes.c_void_p), n_cls, ls.flags,
-                        ctypes.c_void_p(ls.workspace.data_ptr()), ls.workspace.numel(),
-                        ctypes.c_void_p(ls.diag.data_ptr()), ctypes.c_void_p(stream)), "adana_mta_step")
-                else:
-                    _lib.check(L.adana_mta_step_scaled(
-                        ctypes.byref(ls.plan), ctypes.cast(sc_arr, ctypes.c_void_p), n_cls,
-                        ls.flags | wflag, ctypes.c_void_p(gscale),
-                        ctypes.c_void_p(ls.workspace.data_ptr()), ls.workspace.numel(),
-                        ctypes.c_void_p(ls.diag.data_ptr()), ctypes.c_void_p(stream)),
-                        "adana_mta_step_scaled")
-                for j, ps, gs in ls.stage:       # and back
-                    if ps is not None:
-                        ls.params[j].copy_(ps)
-                    if gs is not None and wflag:
-                        ls.grads[j].copy_(gs)
-        if fresh:
-            for ls in self._sets:                          # adana.py:221-225: new 0-d tensors
-                _hoststep.bind_diag(ls.diag, ls.states, self._diag_cols)
-        _hoststep.bump_versions(params)                    # p was updated in place
+            if ls.device.index == cur:
+                self._launch_set(L, ls, sc_arr, n_cls, gscale, wflag, checked)
+            else:
+                with torch.cuda.device(ls.device):
+                    self._launch_set(L, ls, sc_arr, n_cls, gscale, wflag, checked)
+        if params is not None:
+            _hoststep.bump_versions(params)                # p was updated in place
         if wflag:
-            _hoststep.bump_versions(grads)
+            _hoststep.bump_versions(pend[0])
         return loss
+
+    def _launch_set(self, L, ls: _LaunchSet, sc_arr, n_cls: int, gscale, wflag: int, checked: bool) -> None:
+        """One launch set's staging copies, diagnostics guard and step launch,
+        with ls.device current."""
+        stream = torch.cuda.current_stream(ls.device).cuda_stream
+        if checked:
+            self._diag_guard(ls)
+        for j, ps, gs in ls.stage:       # into the state's layout (same stream)
+            if ps is not None and not ls.flags & _lib.PARAM_BF16:   # the master is read instead
+                ps.copy_(ls.params[j])
+            if gs is not None:
+                gs.copy_(ls.grads[j])
+        if gscale is None:
+            _lib.check(L.adana_mta_step(
+                ctypes.byref(ls.plan), ctypes.cast(sc_arr, ctypes.c_void_p), n_cls, ls.flags,
+                ctypes.c_void_p(ls.workspace.data_ptr()), ls.workspace.numel(),
+                ctypes.c_void_p(ls.diag.data_ptr()), ctypes.c_void_p(stream)), "adana_mta_step")
+        else:
+            _lib.check(L.adana_mta_step_scaled(
+                ctypes.byref(ls.plan), ctypes.cast(sc_arr, ctypes.c_void_p), n_cls,
+                ls.flags | wflag, ctypes.c_void_p(gscale),
+                ctypes.c_void_p(ls.workspace.data_ptr()), ls.workspace.numel(),
+                ctypes.c_void_p(ls.diag.data_ptr()), ctypes.c_void_p(stream)),
+                "adana_mta_step_scaled")
+        for j, ps, gs in ls.stage:       # and back
+            if ps is not None:
+                ls.params[j].copy_(ps)
+            if gs is not None and wflag:
+                ls.grads[j].copy_(gs)
 
     def _check_state_shapes(self, ls: _LaunchSet) -> None:
         """A parameter whose storage was rebound (``p.data = x``) must keep the
@@ -756,36 +816,38 @@ class _DanaFamily(Optimizer):
                 raise NotImplementedError(f"{type(self).__name__}: parameters whose elements may share memory "
                                           f"(strides {tuple(p.stride())}) are not supported")
 
-    def _refresh_ptrs(self, ls: _LaunchSet, key=None, grads_ok=None) -> None:
-        """Re-point the launch set's descriptors at this step's gradients and
-        the parameters' current storage (re-uploaded only when an address
-        moved: a new gradient allocation, or ``p.data`` rebound).  ``key``:
-        the gradients' and parameters' pointer tables, and ``grads_ok`` the
-        grads_match result, when the caller has them already."""
-        if key is None:
-            key = (_hoststep.data_ptrs(ls.grads), _hoststep.data_ptrs(ls.params))
-        if key == ls.ptr_key:
-            return
-        if key[1] != ls.ptr_key[1]:
-            self._check_state_shapes(ls)
+    def _refresh_ptrs(self, ls: _LaunchSet) -> None:
+        """Re-point the launch set's tables at this step's gradients and the
+        parameters' current storage (the general path; re-uploaded only where
+        an address moved: new gradient tensors, or ``p.data`` rebound)."""
+        pkey = _hoststep.data_ptrs(ls.params)
+        gptr = np.frombuffer(_hoststep.data_ptrs(ls.grads), dtype=np.uint64)
         bf16 = bool(ls.flags & _lib.GRAD_BF16)
-        if grads_ok is None and key[1] == ls.ptr_key[1]:
-            grads_ok = _hoststep.grads_match(ls.params, ls.grads, bf16)
-        if key[1] == ls.ptr_key[1] and grads_ok and not ls.stage:
-            # only gradients moved, and each is a dense contiguous tensor of its
-            # parameter's shape and the set's dtype: re-point the grad column
-            g = np.frombuffer(key[0], dtype=np.uint64)
-            ls.host_desc["grad"] = g
-            ok = ls.rest_ok & (g % (8 if bf16 else 16) == 0)
-            ls.host_desc["flags"] = np.where(ok, _lib.DESC_VEC_OK, 0).astype(ls.host_desc["flags"].dtype)
-        else:
-            for p, g in zip(ls.params, ls.grads):
-                if self._validate(p, g) != ls.flags:
-                    raise RuntimeError(f"{type(self).__name__}: gradient dtype changed")
-            ls.host_desc = self._desc_rows(ls)
-        ls.ptr_key = key
+        if pkey == ls.ptr_key and not ls.stage and _hoststep.grads_match(ls.params, ls.grads, bf16):
+            # only gradients may have moved, each a dense tensor of its
+            # parameter's layout and the set's dtype: re-point those
+            moved = np.flatnonzero(gptr != ls.host_grad)
+            if moved.size:
+                ls.host_grad = gptr.copy()
+                with torch.cuda.device(ls.device):
+                    self._upload_grads(ls, int(moved[0]), int(moved[-1]) + 1)
+                ls.table.forget()
+            return
+        if pkey != ls.ptr_key:
+            self._check_state_shapes(ls)
+        for p, g in zip(ls.params, ls.grads):
+            if self._validate(p, g) != ls.flags:
+                raise RuntimeError(f"{type(self).__name__}: gradient dtype changed")
+        ls.host_desc = self._desc_rows(ls)
         with torch.cuda.device(ls.device):
             self._upload(ls)
+        if pkey != ls.ptr_key or ls.stage:
+            # the rows' storage moved (or is staged): the fast scan's table is
+            # rebuilt from the next general step's plan
+            self._structure = None
+            self._fast = False
+        ls.ptr_key = pkey
+        ls.table.forget()
 
 
 class ADana(_DanaFamily):
@@ -793,9 +855,10 @@ class ADana(_DanaFamily):
 
     Same constructor, defaults, group keys and state keys as
     src/optim/adana.py:32-70; ``use_foreach`` is accepted and has no effect
-    (there is one code path).  ``master_weights`` is an extension for
-    bfloat16 parameters and ``fresh_diagnostics`` one for the diagnostics'
-    binding (both keyword-only; see the module docstring).
+    (there is one code path).  Keyword-only extensions (see the module
+    docstring): ``numerics`` ("compiled", the reference's default
+    torch.compile path, or "eager"), ``master_weights`` for bfloat16
+    parameters and ``fresh_diagnostics`` for the diagnostics' check.
     """
 
     _STAR = False
@@ -804,7 +867,8 @@ class ADana(_DanaFamily):
                  kappa: float = 1.0, epsilon: float = 1e-8, weight_decay: float = 0.0,
                  clipsnr: float = None, wd_decaying: bool = False, wd_ts: float = 1.0,
                  gamma_3_factor: float = 1.0, use_foreach: bool = False, *,
-                 master_weights: bool = False, fresh_diagnostics: Optional[bool] = None):
+                 master_weights: bool = False, fresh_diagnostics: Optional[bool] = None,
+                 numerics: str = "compiled"):
         defaults = dict(lr=lr, delta=delta, epsilon=epsilon, weight_decay=weight_decay,
                         weighted_step_count=0)
         self.lr = lr
@@ -818,14 +882,15 @@ class ADana(_DanaFamily):
         self.gamma_3_factor = gamma_3_factor
         self.use_foreach = use_foreach
         super().__init__(params, defaults)
-        self._engine_init(master_weights, fresh_diagnostics)
+        self._engine_init(master_weights, fresh_diagnostics, numerics)
 
 
 class DANA_STAR_MK4(_DanaFamily):
     """Dana-Star (``clipsnr=None``) and Dana-Star-MK4 (``clipsnr=float``).
 
     Same constructor (including the mk4A / mk4B / weight_time assertions),
-    defaults, group keys and state keys as src/optim/dana_star_mk4.py:10-86.
+    defaults, group keys and state keys as src/optim/dana_star_mk4.py:10-86;
+    the same keyword-only extensions as ADana.
     """
 
     _STAR = True
@@ -836,7 +901,8 @@ class DANA_STAR_MK4(_DanaFamily):
                  epsilon: float = 1e-8, weight_decay: float = 0.0, clipsnr: float = 1.0,
                  weight_time: bool = False, wd_decaying: bool = False, wd_ts: float = 1.0,
                  gamma_3_factor: float = 1.0, use_foreach: bool = False, *,
-                 master_weights: bool = False, fresh_diagnostics: Optional[bool] = None):
+                 master_weights: bool = False, fresh_diagnostics: Optional[bool] = None,
+                 numerics: str = "compiled"):
         assert mk4A == 0.0, f"mk4A must be 0.0, got {mk4A}"
         assert mk4B == 0.0, f"mk4B must be 0.0, got {mk4B}"
         assert weight_time == False, f"weight_time must be False, got {weight_time}"  # noqa: E712
@@ -856,4 +922,4 @@ class DANA_STAR_MK4(_DanaFamily):
         self.gamma_3_factor = gamma_3_factor
         self.use_foreach = use_foreach
         super().__init__(params, defaults)
-        self._engine_init(master_weights, fresh_diagnostics)
+        self._engine_init(master_weights, fresh_diagnostics, numerics)

@@ -68,7 +68,7 @@
 extern "C" {
 #endif
 
-#define ADANA_ABI_VERSION 6
+#define ADANA_ABI_VERSION 7
 
 /* Elements per work chunk (one 256-thread workgroup, one 16-byte vector per
  * thread per array).  Tensors start at multiples of ADANA_ALIGN_ELEMS in the
@@ -97,15 +97,27 @@ extern "C" {
                                     from adana_manau_scalars_init            */
 #define ADANA_STATE_BF16   0x20u /* the reference's own bfloat16 path: param,
                                     m, v, tau (and, with ADANA_GRAD_BF16,
-                                    which it requires, grad) are bfloat16 and
-                                    every op rounds to bfloat16 as ATen's do;
+                                    which it requires, grad) are bfloat16;
                                     d_diag holds 5 bfloat16 per tensor;
                                     excludes ADANA_PARAM_BF16                */
+#define ADANA_NUMERICS_EAGER 0x40u /* the update as the reference's ATen ops
+                                    run it with torch.compile disabled (lerp_
+                                    and addcmul_ as single-rounded FMAs; with
+                                    ADANA_STATE_BF16 every op rounded to
+                                    bfloat16).  Without it: the reference's
+                                    default torch.compile path (Inductor's
+                                    forms: products and sums rounded one by
+                                    one, binary32 throughout, bfloat16 state
+                                    rounded only where it is stored).  The
+                                    scalars must come from hparams with the
+                                    same choice (adana_hparams.eager).        */
 
 /* adana_tensor_desc.flags */
-#define ADANA_DESC_VEC_OK  0x1u  /* all pointers aligned for the vector path:
-                                    16 bytes for float32 arrays, 8 for
-                                    bfloat16 ones                            */
+#define ADANA_DESC_VEC_OK  0x1u  /* param, m, v, tau and param_lp aligned for
+                                    the vector path: 16 bytes for float32
+                                    arrays, 8 for bfloat16 ones (the gradient,
+                                    in adana_plan.grad, is checked by the
+                                    kernel itself)                            */
 
 /* Error codes */
 #define ADANA_OK              0
@@ -113,10 +125,14 @@ extern "C" {
 #define ADANA_E_HIP         (-2)
 #define ADANA_E_UNSUPPORTED (-3)
 
-/* One tensor of the list.  64 bytes; the array lives in device memory. */
+/* One tensor of the list.  64 bytes; the array lives in device memory.  Its
+ * gradient pointer is not here but in adana_plan.grad, a separate array: a
+ * training loop brings new gradient tensors every step
+ * (zero_grad(set_to_none=True), src/optim/base.py:269-289), and re-pointing
+ * them rewrites 8 bytes per tensor instead of a descriptor. */
 typedef struct adana_tensor_desc {
     void       *param;     /* float32 param, or the float32 master copy      */
-    const void *grad;      /* float32 or bfloat16 gradient (same numel)      */
+    const void *reserved0; /* unused (0)                                     */
     float      *m;         /* first moment, float32 (bfloat16 with
                               ADANA_STATE_BF16, as are v and tau)            */
     float      *v;         /* second moment                                  */
@@ -132,6 +148,9 @@ typedef struct adana_tensor_desc {
  * and adana_plan_index (chunk_first). */
 typedef struct adana_plan {
     const adana_tensor_desc *desc;   /* device, n_tensors entries              */
+    const void *const *grad;         /* device, n_tensors gradient pointers:
+                                        float32 or bfloat16, numel elements
+                                        each, any 2- or 4-byte alignment     */
     const int64_t *vstart;           /* device, n_tensors + 1 (layout output)  */
     const int32_t *chunk_first;      /* device, n_chunks (adana_plan_index)    */
     const int32_t *fold_first;       /* device, n_tensors + 1 (layout output)  */
@@ -154,6 +173,8 @@ typedef struct adana_hparams {
     double  gamma_3_factor; /* self.gamma_3_factor                           */
     int32_t has_clip;       /* self.clipsnr is not None                      */
     int32_t wd_decaying;    /* self.wd_decaying                              */
+    int32_t eager;          /* 1: scalars for ADANA_NUMERICS_EAGER launches  */
+    int32_t reserved;
 } adana_hparams;
 
 /* Per-step binary32 scalars of one (group, step) class, each computed on the
@@ -164,25 +185,33 @@ typedef struct adana_step_scalars {
     float   lerp_coef;  /* alpha if |alpha| < 0.5 else alpha - 1 (ATen lerp) */
     float   s;          /* fp32(t)                                           */
     float   eps;        /* fp32(epsilon)                                     */
-    float   pw;         /* ADana: (1 + s) ** (1 - kappa)                     */
+    float   pw;         /* ADana: (1 + s) ** (1 - kappa), by pow_mode        */
     float   min_p;      /* Dana-Star: 1 / (1 + s)                            */
     float   clip;       /* fp32(clipsnr)                                     */
     float   c3;         /* (-lr) * gamma_3_factor                            */
     float   cg2;        /* -lr                                               */
     float   opw;        /* 1 + weight-decay factor                           */
     float   star_exp;   /* fp32(1 - kappa), exponent of Dana-Star's pow      */
-    int32_t pow_mode;   /* ATen pow specialisation (ADANA_POW_*)             */
+    int32_t pow_mode;   /* pow specialisation of 1 - kappa (ADANA_POW_*)     */
     int32_t has_clip;
     int32_t lerp_small; /* |alpha| < 0.5                                     */
-    int32_t reserved;
+    int32_t pow_int;    /* ADANA_POW_INT: the integer exponent               */
 } adana_step_scalars;
 
-/* pow(Tensor, Scalar) specialisations ATen selects on the binary64 exponent
- * (ONE: exponent 0, the result is 1; IDENTITY: exponent 1, a copy) */
+/* Specialisations of x ** e chosen on the binary64 exponent e.
+ * Eager (ATen's pow(Tensor, Scalar)): ONE (e = 0: 1), IDENTITY (e = 1: a
+ * copy), SQRT (0.5), RSQRT (-0.5: 1 / sqrt), RECIP (-1), SQUARE (2), CUBE
+ * (3), INVSQ (-2: 1 / (x * x)); any other e GENERAL.
+ * Compiled (Inductor's pow lowering): ONE (e = 0), IDENTITY (e = 1), SQRT
+ * (0.5), INT (any other integer e with |e| < 32: left-to-right binary
+ * powering of x, or of 1 / x for e < 0, exponent in pow_int); any other e,
+ * -0.5 included, GENERAL.  GENERAL is pow with the exponent rounded to
+ * binary32 (ADana's eager scalar: pow in binary64 with the binary64
+ * exponent). */
 enum {
     ADANA_POW_GENERAL = 0, ADANA_POW_ONE, ADANA_POW_SQRT, ADANA_POW_RSQRT,
     ADANA_POW_RECIP, ADANA_POW_SQUARE, ADANA_POW_CUBE, ADANA_POW_INVSQ,
-    ADANA_POW_IDENTITY
+    ADANA_POW_IDENTITY, ADANA_POW_INT
 };
 
 /* Hyper-parameters of one Manau parameter group that its Dana-Star-MK4

@@ -20,10 +20,19 @@
  *   - every tensor op of the reference is one IEEE-754 binary32 operation,
  *     correctly rounded, in the reference's op order; no contraction
  *     (built with -ffp-contract=off);
- *   - the two composite ATen ops the reference uses are single-rounded FMAs,
- *     as torch 2.10's CPU kernels compute them (probed bitwise):
- *       lerp(a, b, w)          = |w| < 0.5 ? fma(w, b-a, a) : fma(w-1, b-a, b)
- *       addcmul(s, t, t, val)  = fma(val*t, t, s)
+ *   - the two composite ops the reference uses have two forms, chosen by
+ *     adana_oracle_scalars.compiled:
+ *       eager (the update run as ATen ops, torch.compile disabled): single-
+ *       rounded FMAs, as torch 2.10's CPU kernels compute them (probed bitwise)
+ *         lerp(a, b, w)          = |w| < 0.5 ? fma(w, b-a, a) : fma(w-1, b-a, b)
+ *         addcmul(s, t, t, val)  = fma(val*t, t, s)
+ *       compiled (the reference's default path, torch.compile, adana.py:72-79,
+ *       dana_star_mk4.py:88-96): Inductor's decompositions, every product and
+ *       sum rounded on its own (its C++ is built with -ffp-contract=off)
+ *         lerp(a, b, w)          = (|w| < 0.5 ? w : w-1) * (b-a) + (|w| < 0.5 ? a : b)
+ *         v*(1-val) + addcmul    = v*(1-val) + (t*t)*val
+ *     (read from Inductor's generated code for a restatement of the update
+ *     as the same torch ops, and pinned by the reference's compiled runs);
  *   - Dana-Star's per-element pow(et, 1-kappa) takes the exponent rounded to
  *     binary32 (the vectorised ATen path does) and is evaluated in binary64,
  *     then rounded once to binary32;
@@ -47,10 +56,28 @@
 #include "adana_oracle.h"
 
 
-/* pow(Tensor, Scalar) specialisations in ATen, chosen on the binary64
- * exponent: 0 -> ones, 0.5 -> sqrt, -0.5 -> 1/sqrt, -1 -> 1/x, 2 -> x*x,
- * 3 -> x*x*x, -2 -> 1/(x*x); anything else is a general pow. */
-enum { POW_GENERAL = 0, POW_ONE, POW_SQRT, POW_RSQRT, POW_RECIP, POW_SQUARE, POW_CUBE, POW_INVSQ, POW_IDENTITY };
+/* pow(Tensor, Scalar) specialisations, chosen on the binary64 exponent.
+ * ATen (eager): 0 -> ones, 1 -> copy, 0.5 -> sqrt, -0.5 -> 1/sqrt, -1 -> 1/x,
+ * 2 -> x*x, 3 -> x*x*x, -2 -> 1/(x*x); anything else a general pow.
+ * Inductor (compiled): 0 -> ones, 1 -> copy, 0.5 -> sqrt, another integer k
+ * with |k| < 32 -> POW_INT (products, below); anything else a general pow. */
+enum { POW_GENERAL = 0, POW_ONE, POW_SQRT, POW_RSQRT, POW_RECIP, POW_SQUARE, POW_CUBE, POW_INVSQ, POW_IDENTITY,
+       POW_INT };
+
+/* x ** k as Inductor's pow_recursive expands it (torch/_inductor/
+ * lowering.py): for k < 0 the powers of 1/x; x**(2j) = x**j * x**j and
+ * x**(2j+1) = (x**j * x**j) * x, each product rounded to binary32. */
+static float o_pow_int(float x, int32_t k) {
+    if (k < 0) {
+        x = 1.0f / x;
+        k = -k;
+    }
+    if (k == 0) return 1.0f;
+    if (k == 1) return x;
+    float r = o_pow_int(x, k / 2);
+    r = r * r;
+    return (k % 2) ? r * x : r;
+}
 
 /* x ** e by ATen's specialisation `mode` (chosen on the binary64 exponent);
  * any other exponent: binary64 pow of the binary32 exponent, rounded once. */
@@ -70,6 +97,7 @@ static inline float o_pow_mode(float x, float e, int32_t mode) {
 
 static inline float o_pow(float x, const adana_oracle_scalars *sc) {
     switch (sc->pow_mode) {
+    case POW_INT: return o_pow_int(x, sc->pow_int);
     case POW_ONE: return 1.0f;
     case POW_IDENTITY: return x;
     case POW_SQRT: return sqrtf(x);
@@ -82,9 +110,18 @@ static inline float o_pow(float x, const adana_oracle_scalars *sc) {
     }
 }
 
-static inline float o_lerp(float self, float end, float w) {
+static inline float o_lerp(float self, float end, float w, int32_t compiled) {
     float d = end - self;
+    if (compiled) {
+        const int small = fabsf(w) < 0.5f;
+        return (small ? w : w - 1.0f) * d + (small ? self : end);
+    }
     return (fabsf(w) < 0.5f) ? fmaf(w, d, self) : fmaf(w - 1.0f, d, end);
+}
+/* v.mul_(1 - alpha).addcmul_(g, g, value=alpha) (adana.py:104) */
+static inline float o_ema2(float v, float g, const adana_oracle_scalars *sc) {
+    if (sc->compiled) return v * sc->oma + (g * g) * sc->a;
+    return fmaf(sc->a * g, g, v * sc->oma);
 }
 static inline float o_sign(float x) { return x > 0.0f ? 1.0f : (x < 0.0f ? -1.0f : 0.0f); }
 static inline float o_clamp_max(float x, float c) { return x > c ? c : x; }
@@ -109,9 +146,8 @@ static inline uint16_t f32_to_bf16(float f) {
 /* One ADana / Dana-MK4 element (src/optim/adana.py:101-143). */
 static inline float adana_elem(float p, float g, float *mp, float *vp,
                                const adana_oracle_scalars *sc, double acc[4]) {
-    float m = o_lerp(*mp, g, sc->a);                         /* :101 */
-    float v = *vp * sc->oma;                                 /* :104 mul_ */
-    v = fmaf(sc->a * g, g, v);                               /* :104 addcmul_ */
+    float m = o_lerp(*mp, g, sc->a, sc->compiled);           /* :101 */
+    float v = o_ema2(*vp, g, sc);                            /* :104 mul_, addcmul_ */
     float se = sqrtf(v) + sc->eps;                           /* :107 */
     float nt = 1.0f / se;                                    /* :110 */
     float mn = fabsf(m) * nt;                                /* :111, :115 */
@@ -135,13 +171,12 @@ static inline float adana_elem(float p, float g, float *mp, float *vp,
 /* One Dana-Star / Dana-Star-MK4 element (src/optim/dana_star_mk4.py:137-195). */
 static inline float star_elem(float p, float g, float *mp, float *vp, float *tp,
                               const adana_oracle_scalars *sc, double acc[4]) {
-    float m = o_lerp(*mp, g, sc->a);                         /* :137 */
-    float v = *vp * sc->oma;                                 /* :140 */
-    v = fmaf(sc->a * g, g, v);
+    float m = o_lerp(*mp, g, sc->a, sc->compiled);           /* :137 */
+    float v = o_ema2(*vp, g, sc);                            /* :140 */
     float se = sqrtf(v) + sc->eps;                           /* :143 */
     float ag = fabsf(g);                                     /* :147 */
     float tu = ag / (ag + se);                               /* :148 */
-    float tau = o_lerp(*tp, tu, sc->a);                      /* :149 */
+    float tau = o_lerp(*tp, tu, sc->a, sc->compiled);        /* :149 */
     float ct = o_clamp_max(tau, 0.5f);                       /* :152 */
     float pe = ct / (1.0f - ct);                             /* :153 */
     float tr = sc->min_p + o_relu(pe - sc->min_p);           /* :154-156 */
@@ -238,7 +273,7 @@ static inline float o_pow16(float x, float e16, int32_t mode) { return rb(o_pow_
 static inline float adana_elem16(float p, float g, float *mp, float *vp, const adana_oracle_scalars *sc,
                                  double acc[4]) {
     const float a16 = rb(sc->a);
-    float m = rb(o_lerp(*mp, g, a16));                       /* :101 */
+    float m = rb(o_lerp(*mp, g, a16, 0));                    /* :101 */
     float v = rb(*vp * sc->oma);                             /* :104 mul_ */
     v = rb(fmaf(sc->a * g, g, v));                           /* :104 addcmul_ */
     float se = rb(rb(sqrtf(v)) + rb(sc->eps));               /* :107 */
@@ -263,13 +298,13 @@ static inline float adana_elem16(float p, float g, float *mp, float *vp, const a
 static inline float star_elem16(float p, float g, float *mp, float *vp, float *tp,
                                 const adana_oracle_scalars *sc, double acc[4]) {
     const float a16 = rb(sc->a), minp16 = rb(sc->min_p);
-    float m = rb(o_lerp(*mp, g, a16));                       /* :137 */
+    float m = rb(o_lerp(*mp, g, a16, 0));                    /* :137 */
     float v = rb(*vp * sc->oma);                             /* :140 */
     v = rb(fmaf(sc->a * g, g, v));
     float se = rb(rb(sqrtf(v)) + rb(sc->eps));               /* :143 */
     float ag = fabsf(g);                                     /* :147 */
     float tu = rb(ag / rb(ag + se));                         /* :148 */
-    float tau = rb(o_lerp(*tp, tu, a16));                    /* :149 */
+    float tau = rb(o_lerp(*tp, tu, a16, 0));                 /* :149 */
     float ct = o_clamp_max(tau, 0.5f);                       /* :152 */
     float pe = rb(ct / rb(1.0f - ct));                       /* :153 */
     float tr = rb(minp16 + o_relu(rb(pe - minp16)));         /* :154-156 */
@@ -349,10 +384,22 @@ void adana_oracle_step_g16(int64_t n, int32_t star, float *p, const uint16_t *g1
 }
 
 /* The reference's bfloat16 path: p, g, m, v and tau all bfloat16 (tau may
- * be NULL for the ADana variants). */
+ * be NULL for the ADana variants).  Compiled (sc->compiled): Inductor loads
+ * the bfloat16 tensors as binary32, runs the whole update in binary32 (the
+ * compiled forms above, scalars unrounded) and rounds only the four stored
+ * results to bfloat16 (round to nearest even).  Eager: every op rounded to
+ * bfloat16 as ATen's bfloat16 kernels do (adana_elem16, star_elem16). */
 void adana_oracle_step_bf16(int64_t n, int32_t star, uint16_t *p, const uint16_t *g, uint16_t *m,
                             uint16_t *v, uint16_t *tau, const adana_oracle_scalars *sc, double diag[4]) {
-    if (star) {
+    if (sc->compiled && star) {
+        DIAG_LOOP(float mm = bf16_to_f32(m[i]); float vv = bf16_to_f32(v[i]); float tt = bf16_to_f32(tau[i]);
+                  p[i] = f32_to_bf16(star_elem(bf16_to_f32(p[i]), bf16_to_f32(g[i]), &mm, &vv, &tt, sc, acc));
+                  m[i] = f32_to_bf16(mm); v[i] = f32_to_bf16(vv); tau[i] = f32_to_bf16(tt))
+    } else if (sc->compiled) {
+        DIAG_LOOP(float mm = bf16_to_f32(m[i]); float vv = bf16_to_f32(v[i]);
+                  p[i] = f32_to_bf16(adana_elem(bf16_to_f32(p[i]), bf16_to_f32(g[i]), &mm, &vv, sc, acc));
+                  m[i] = f32_to_bf16(mm); v[i] = f32_to_bf16(vv))
+    } else if (star) {
         DIAG_LOOP(float mm = bf16_to_f32(m[i]); float vv = bf16_to_f32(v[i]); float tt = bf16_to_f32(tau[i]);
                   p[i] = f32_to_bf16(star_elem16(bf16_to_f32(p[i]), bf16_to_f32(g[i]), &mm, &vv, &tt, sc, acc));
                   m[i] = f32_to_bf16(mm); v[i] = f32_to_bf16(vv); tau[i] = f32_to_bf16(tt))
@@ -367,7 +414,7 @@ void adana_oracle_f32_to_bf16(int64_t n, const float *x, uint16_t *y) {
     for (int64_t i = 0; i < n; ++i) y[i] = f32_to_bf16(x[i]);
 }
 
-int adana_oracle_abi_version(void) { return 1; }
+int adana_oracle_abi_version(void) { return 2; }
 
 /* Thread count of the parallel loops (the CPU baseline reports it). */
 #include <omp.h>

@@ -27,6 +27,10 @@ typedef struct {
     float opw;      /* fp32(1 + wd_factor)                                   */
     float star_exp; /* fp32(1 - kappa): exponent of the per-element pow      */
     int32_t pow_mode; /* ATen's pow(Tensor, Scalar) specialisation, below     */
+    int32_t compiled; /* 1: torch.compile's (Inductor's) forms of lerp and the
+                         second-moment update, bfloat16 rounding only where a
+                         tensor is stored; 0: the ATen eager ops              */
+    int32_t pow_int;  /* POW_INT: the integer exponent                         */
 } adana_oracle_scalars;
 
 /* Manau's Dana-Star-MK4 branch (src/optim/manau.py:556-613): its scalars

@@ -49,6 +49,8 @@ class OracleScalars(ctypes.Structure):
         ("opw", ctypes.c_float),
         ("star_exp", ctypes.c_float),
         ("pow_mode", ctypes.c_int32),
+        ("compiled", ctypes.c_int32),
+        ("pow_int", ctypes.c_int32),
     ]
 
 
@@ -143,7 +145,7 @@ def _pow0d(x: np.float32, e: float) -> np.float32:
     return f32(math.pow(float(x), e))
 
 
-POW_GENERAL, POW_ONE, POW_SQRT, POW_RSQRT, POW_RECIP, POW_SQUARE, POW_CUBE, POW_INVSQ, POW_IDENTITY = range(9)
+POW_GENERAL, POW_ONE, POW_SQRT, POW_RSQRT, POW_RECIP, POW_SQUARE, POW_CUBE, POW_INVSQ, POW_IDENTITY, POW_INT = range(10)
 
 
 def pow_mode(e: float) -> int:
@@ -154,14 +156,81 @@ def pow_mode(e: float) -> int:
             2.0: POW_SQUARE, 3.0: POW_CUBE, -2.0: POW_INVSQ}.get(e, POW_GENERAL)
 
 
+def pow_mode_compiled(e: float):
+    """(mode, integer exponent) of x ** e under torch.compile: Inductor's pow
+    lowering (torch/_inductor/lowering.py) turns an exponent equal to an
+    integer k into pow(x, k) -- ones for 0, a copy for 1, products for any
+    other |k| < 32 -- and 0.5 into sqrt; every other exponent, -0.5 included,
+    stays a pow with the exponent rounded to binary32."""
+    if e == 0.0:
+        return POW_ONE, 0
+    if e == 1.0:
+        return POW_IDENTITY, 0
+    if e == 0.5:
+        return POW_SQRT, 0
+    if e == math.floor(e) and abs(e) < 32:
+        return POW_INT, int(e)
+    return POW_GENERAL, 0
+
+
+def pow_int(x: np.float32, k: int) -> np.float32:
+    """x ** k for an integer k as Inductor's pow_recursive expands it: for
+    k < 0 the powers of 1 / x; x ** 2j = (x ** j)(x ** j) and
+    x ** (2j + 1) = (x ** j)(x ** j) x, every product one binary32 rounding."""
+    x = f32(x)
+    if k < 0:
+        x, k = f32(1.0) / x, -k
+    if k == 0:
+        return f32(1.0)
+    if k == 1:
+        return x
+    r = pow_int(x, k // 2)
+    r = r * r
+    return r * x if k % 2 else r
+
+
+_libm = None
+
+
+def _powf(x: np.float32, e: np.float32) -> np.float32:
+    """The C library's binary32 pow (what Inductor's CPU code calls as
+    std::pow(float, float) for a 0-d tensor)."""
+    global _libm
+    if _libm is None:
+        _libm = ctypes.CDLL("libm.so.6")
+        _libm.powf.restype = ctypes.c_float
+        _libm.powf.argtypes = [ctypes.c_float, ctypes.c_float]
+    return f32(_libm.powf(float(x), float(e)))
+
+
+def _pow0d_compiled(x: np.float32, e: float) -> np.float32:
+    """``x ** e`` for a 0-d binary32 tensor under torch.compile
+    (src/optim/adana.py:119,123): Inductor's lowering, a general exponent
+    evaluated by the C library's powf with the exponent rounded to binary32."""
+    mode, k = pow_mode_compiled(e)
+    x = f32(x)
+    if mode == POW_ONE:
+        return f32(1.0)
+    if mode == POW_IDENTITY:
+        return x
+    if mode == POW_SQRT:
+        return f32(np.sqrt(x))
+    if mode == POW_INT:
+        return pow_int(x, k)
+    return _powf(x, f32(e))
+
+
 def step_scalars(*, lr: float, peak_lr: float, delta: float, kappa: float, epsilon: float,
                  weight_decay: float, clipsnr: Optional[float], wd_decaying: bool,
-                 wd_ts: float, gamma_3_factor: float, t: int) -> OracleScalars:
+                 wd_ts: float, gamma_3_factor: float, t: int, compiled: bool = True) -> OracleScalars:
     """Scalars of one tensor's update at per-tensor step ``t`` (already incremented).
 
     Follows src/optim/adana.py:163-208 (host) and :104-143 (0-d tensor ops
     inside the compiled update); Dana-Star uses the same host code
-    (src/optim/dana_star_mk4.py:217-272) plus min_p (:154).
+    (src/optim/dana_star_mk4.py:217-272) plus min_p (:154).  The scalars are
+    the same binary32 values under torch.compile (Inductor computes these
+    0-d ops in binary32 in the same order); ``compiled`` selects Inductor's
+    forms of the element ops (adana_oracle.c).
     """
     sf = f32(lr / peak_lr)                       # :165 double divide, :207 fp32
     g2 = f32(lr)                                 # :205
@@ -175,7 +244,7 @@ def step_scalars(*, lr: float, peak_lr: float, delta: float, kappa: float, epsil
     sc.oma = f32(1.0) - a                        # :104 ``1 - alpha``
     sc.s = s
     sc.eps = f32(epsilon)                        # :107 add_(epsilon)
-    sc.pw = _pow0d(one_p_s, 1.0 - kappa)         # :119 / :123
+    sc.pw = (_pow0d_compiled if compiled else _pow0d)(one_p_s, 1.0 - kappa)   # :119 / :123
     sc.min_p = f32(1.0) / one_p_s                # dana_star_mk4.py:154
     sc.has_clip = 0 if clipsnr is None else 1
     sc.clip = f32(clipsnr) if clipsnr is not None else f32(np.inf)
@@ -187,7 +256,11 @@ def step_scalars(*, lr: float, peak_lr: float, delta: float, kappa: float, epsil
         wdf = (-wd) * sf
     sc.opw = f32(1.0) + wdf                      # :143 ``1 + wd_factor``
     sc.star_exp = f32(1.0 - kappa)               # dana_star_mk4.py:170 (vectorised pow)
-    sc.pow_mode = pow_mode(1.0 - kappa)
+    if compiled:
+        sc.pow_mode, sc.pow_int = pow_mode_compiled(1.0 - kappa)
+    else:
+        sc.pow_mode = pow_mode(1.0 - kappa)
+    sc.compiled = 1 if compiled else 0
     return sc
 
 
@@ -339,7 +412,9 @@ class OracleOptimizer:
     Params are float32 arrays (or, with ``master=True``, uint16 bf16 arrays
     with an fp32 master copy kept in the state; or, with ``bf16=True``, uint16
     bf16 arrays whose m, v, tau are bf16 too: the reference's own bfloat16
-    path).
+    path).  ``numerics`` is "compiled" (the reference's default torch.compile
+    path, src/optim/adana.py:72-79, 210-216) or "eager" (its update run as
+    ATen ops).
     """
 
     groups: List[OracleGroup]
@@ -352,6 +427,7 @@ class OracleOptimizer:
     gamma_3_factor: float = 1.0
     master: bool = False
     bf16: bool = False
+    numerics: str = "compiled"
     state: Dict[int, dict] = field(default_factory=dict)
 
     def step(self, grads: Sequence[Sequence[Optional[np.ndarray]]]) -> None:
@@ -380,7 +456,8 @@ class OracleOptimizer:
                                   kappa=self.kappa, epsilon=group.epsilon,
                                   weight_decay=group.weight_decay, clipsnr=self.clipsnr,
                                   wd_decaying=self.wd_decaying, wd_ts=self.wd_ts,
-                                  gamma_3_factor=self.gamma_3_factor, t=st["step"])
+                                  gamma_3_factor=self.gamma_3_factor, t=st["step"],
+                                  compiled=self.numerics == "compiled")
                 if self.master:
                     sums = master_step(self.star, st["master"], p, g, st["m"], st["v"],
                                        st.get("tau"), sc)

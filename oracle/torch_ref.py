@@ -19,6 +19,17 @@ for the tests that pin the CPU oracle: ``sqrt`` and ``epow`` replace torch's
 square root and Dana-Star's element-wise power (to show that they alone
 separate the oracle from the reference), and ``slip`` plants one plausible
 op-order mistake (to show that the golden vectors catch it).
+
+``update_compiled`` restates the same update the way the reference's
+default torch.compile path computes it (Inductor's generated CPU code for
+these ops): lerp_ as ``c * (end - self) + base`` and the second moment as
+``v * (1 - alpha) + (g * g) * alpha`` (no fused multiply-adds), every
+intermediate in binary32, bfloat16 tensors read as binary32 and rounded only
+when m, v, tau and p are stored, ADana's 0-d pow evaluated by the C
+library's powf with the exponent rounded to binary32.  It runs as eager
+torch ops, so the caller passes the square root and element-wise power that
+Inductor's code uses (the tests pin those against the reference's compiled
+fixtures).
 """
 from __future__ import annotations
 
@@ -84,6 +95,65 @@ def update(star: bool, p, g, m, v, tau, sc, hp: dict, sqrt=torch.sqrt, epow=None
     return af.mean(), g.norm(), mfac.mean(), m.norm()         # :146-151
 
 
+def update_compiled(star: bool, p, g, m, v, tau, sc, hp: dict, sqrt, epow, powf):
+    """``update``'s ops as the compiled path computes them (module docstring):
+    p, m, v[, tau] are updated in place from binary32 copies; returns the
+    diagnostics (binary32 sums, rounded to p's dtype) as ``update`` does.
+    ``sqrt(x)``, ``epow(x, e)`` (Dana-Star's element-wise power) and
+    ``powf(x, e)`` (ADana's 0-d power, Python floats) are the functions
+    Inductor's code calls."""
+    step_t, a_t, g2_t, g3_t, sf_t, wd_t = sc
+    kappa, clip = hp["kappa"], hp["clipsnr"]
+    f32 = torch.float32
+    P, G, M, V = p.to(f32), g.to(f32), m.to(f32), v.to(f32)
+    small = bool(torch.abs(a_t) < 0.5)
+    coef = a_t if small else a_t - 1.0                        # torch._refs.lerp
+
+    def lerp(x, y):
+        return coef * (y - x) + (x if small else y)
+
+    M1 = lerp(M, G)                                           # adana.py:101
+    V1 = V * (1 - a_t) + (G * G) * a_t                        # :104
+    se = sqrt(V1) + hp["epsilon"]                             # :107
+    if star:
+        T = tau.to(f32)
+        ag = torch.abs(G)                                     # dana_star_mk4.py:147
+        T1 = lerp(T, ag / (ag + se))                          # :148-149
+        ct = torch.clamp(T1, max=0.5)                         # :152
+        pe = ct / (1.0 - ct)                                  # :153
+        min_p = 1.0 / (1.0 + step_t)                          # :154
+        treg = min_p + torch.relu(pe - min_p)                 # :156
+        et = torch.clamp(T1 * step_t, min=1.0)                # :159
+        nt = sqrt(treg) / se                                  # :163-164
+        mnt = torch.abs(M1) * nt                              # :165
+        mfac = mnt / treg                                     # :167
+        af = epow(et, 1 - kappa) * mfac                       # :170 / :174
+        if clip is not None:
+            af = torch.clamp(af, max=clip)
+        g3t = (-g3_t) * hp["gamma_3_factor"] * (torch.sign(M1) * (treg * af + mnt))   # :177
+    else:
+        nt = 1.0 / se                                         # adana.py:110
+        mfac = torch.abs(M1) * nt                             # :111, :115
+        pw = torch.tensor(powf(float(1.0 + step_t), 1 - kappa), dtype=f32)             # :114, :119
+        af = pw * mfac
+        if clip is not None:
+            af = torch.clamp(af, max=clip)
+        g3t = (-g3_t) * hp["gamma_3_factor"] * (torch.sign(M1) * af + M1 * nt)         # :126
+    g2t = (-g2_t) * G * nt                                    # :129 / :180
+    if hp["wd_decaying"]:                                     # :139-142
+        wdf = -wd_t / (1 + step_t / hp["wd_ts"]) * sf_t
+    else:
+        wdf = -wd_t * sf_t
+    P1 = (P + (g2t + g3t)) * (1 + wdf)                        # :132-143
+    p.copy_(P1)
+    m.copy_(M1)
+    v.copy_(V1)
+    if star:
+        tau.copy_(T1)
+    dt = p.dtype
+    return (af.mean().to(dt), G.norm().to(dt), mfac.mean().to(dt), M1.norm().to(dt))   # :146-151
+
+
 @dataclass
 class TorchRefGroup:
     params: List[torch.Tensor]
@@ -112,7 +182,9 @@ class TorchRefOptimizer:
 
     @torch.no_grad()
     def step(self, grads: Sequence[Sequence[Optional[torch.Tensor]]], sqrt=torch.sqrt, epow=None,
-             slip: Optional[str] = None) -> None:
+             slip: Optional[str] = None, compiled=None) -> None:
+        """One step of the reference's loop.  ``compiled``: None for the eager
+        ops (``update``), or (sqrt, epow, powf) for ``update_compiled``."""
         f32 = dict(dtype=torch.float32)
         for gi, group in enumerate(self.groups):
             lr = group.lr
@@ -134,8 +206,12 @@ class TorchRefOptimizer:
                 sc = (torch.tensor(t, **f32), torch.tensor(group.delta / (group.delta + t), **f32),
                       torch.tensor(lr, **f32), torch.tensor(lr, **f32), torch.tensor(sf, **f32),
                       torch.tensor(group.weight_decay, **f32))                       # :199-208
-                ca, gn, afm, mn = update(self.star, p, g, st["m"], st["v"], st.get("tau"), sc, hp,
-                                         sqrt=sqrt, epow=epow, slip=slip)
+                if compiled is None:
+                    ca, gn, afm, mn = update(self.star, p, g, st["m"], st["v"], st.get("tau"), sc, hp,
+                                             sqrt=sqrt, epow=epow, slip=slip)
+                else:
+                    ca, gn, afm, mn = update_compiled(self.star, p, g, st["m"], st["v"], st.get("tau"), sc, hp,
+                                                      *compiled)
                 st["current_alpha"] = ca                      # :221-225
                 st["gradient_norm"] = gn
                 st["auto_factor_mean"] = afm

@@ -86,6 +86,8 @@ adana_oracle_scalars to_oracle(const adana_step_scalars &s) {
     o.opw = s.opw;
     o.star_exp = s.star_exp;
     o.pow_mode = s.pow_mode;
+    o.pow_int = s.pow_int;
+    o.compiled = 1;          // the library's default numerics (no ADANA_NUMERICS_EAGER)
     return o;
 }
 
@@ -130,11 +132,15 @@ int main() {
     if (n_chunks < 0) LIB_OK(static_cast<int>(n_chunks));
     std::vector<adana_tensor_desc> desc(n);
     for (int i = 0; i < n; ++i)
-        desc[i] = adana_tensor_desc{dp[i], dg[i], dm[i], dv[i], dtau[i], nullptr, numel[i], 0, ADANA_DESC_VEC_OK};
+        desc[i] = adana_tensor_desc{dp[i], nullptr, dm[i], dv[i], dtau[i], nullptr, numel[i], 0, ADANA_DESC_VEC_OK};
+    std::vector<const void *> gptr(dg.begin(), dg.end());
     adana_tensor_desc *d_desc;
+    const void **d_grad;
     int64_t *d_vstart;
     int32_t *d_fold_first, *d_chunk_first;
     HIP_OK(hipMalloc(&d_desc, sizeof(adana_tensor_desc) * n));
+    HIP_OK(hipMalloc(&d_grad, sizeof(void *) * n));
+    HIP_OK(hipMemcpy(d_grad, gptr.data(), sizeof(void *) * n, hipMemcpyHostToDevice));
     HIP_OK(hipMalloc(&d_vstart, 8 * (n + 1)));
     HIP_OK(hipMalloc(&d_fold_first, 4 * (n + 1)));
     HIP_OK(hipMalloc(&d_chunk_first, 4 * n_chunks));
@@ -146,6 +152,7 @@ int main() {
     LIB_OK(adana_plan_index(d_vstart, n, n_chunks, d_chunk_first, stream));
     adana_plan plan{};
     plan.desc = d_desc;
+    plan.grad = d_grad;
     plan.vstart = d_vstart;
     plan.chunk_first = d_chunk_first;
     plan.fold_first = d_fold_first;
@@ -236,6 +243,7 @@ int main() {
         HIP_OK(hipFree(dtau[i]));
     }
     HIP_OK(hipFree(d_desc));
+    HIP_OK(hipFree(d_grad));
     HIP_OK(hipFree(d_vstart));
     HIP_OK(hipFree(d_fold_first));
     HIP_OK(hipFree(d_chunk_first));

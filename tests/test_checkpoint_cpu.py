@@ -121,7 +121,7 @@ def test_oracle_resumes_reference_checkpoint(oracle_mod, case):
                                     weighted_step_count=schema["param_groups"][gi]["weighted_step_count"]))
     opt = O.OracleOptimizer(groups=groups, star=star, peak_lr=kw["lr"], kappa=kw["kappa"],
                             clipsnr=kw["clipsnr"], wd_decaying=kw["wd_decaying"], wd_ts=kw["wd_ts"],
-                            gamma_3_factor=kw["gamma_3_factor"])
+                            gamma_3_factor=kw["gamma_3_factor"], numerics="eager")   # the eager run's checkpoint
     for i, p in enumerate(params):
         st = ref["state"][i]
         opt.state[id(p)] = {"step": st["step"], "m": st["m"].numpy().copy(), "v": st["v"].numpy().copy(),

@@ -1,17 +1,21 @@
 """GPU parity of the reference's own bfloat16 path (ADANA_STATE_BF16):
 bfloat16 parameters without ``master_weights`` keep bfloat16 m, v, tau (the
 reference's ``zeros_like(p)``, src/optim/adana.py:191-195;
-src/optim/dana_star_mk4.py:251-255) and every op rounds to bfloat16.
+src/optim/dana_star_mk4.py:251-255), in both of the reference's numerics:
+its default torch.compile path (binary32 arithmetic, each tensor rounded to
+bfloat16 where it is stored) and its eager ops (every op rounded to
+bfloat16).
 
 Bars:
-  * p, m, v, tau bit-exact against the C oracle's bfloat16 restatement
-    (oracle/adana_oracle.c, adana_oracle_step_bf16), which reproduces the
-    reference's own bfloat16 eager run bit for bit (tests/test_oracle.py);
-    Dana-Star's p additionally allows STAR_HARD_CASES elements per tensor per
-    step within 1 bfloat16 ulp (a pow result within ~2^-52 of a binary32
-    rounding boundary may round either way);
-  * against the reference's bfloat16 eager fixtures directly: every checkpoint
-    of every golden case bit for bit (same allowance);
+  * p, m, v, tau bit-exact against the C oracle's bfloat16 modes
+    (oracle/adana_oracle.c, adana_oracle_step_bf16), which reproduce the
+    reference's own bfloat16 compiled and eager runs bit for bit
+    (tests/test_oracle.py); Dana-Star's p additionally allows
+    STAR_HARD_CASES elements per tensor per step within 1 bfloat16 ulp (a
+    pow result within ~2^-52 of a binary32 rounding boundary may round
+    either way);
+  * against the reference's bfloat16 fixtures directly: every checkpoint of
+    every golden case bit for bit (same allowance), compiled and eager;
   * diagnostics: bfloat16 0-d tensors as the reference's, within 1 bfloat16
     ulp of the oracle's (the reductions' order differs before the rounding).
 """
@@ -53,7 +57,7 @@ def _diag_close(got, want, tag):
         assert abs(g - w) <= tol, (tag, key, g, w)
 
 
-def _golden_run(case, O):
+def _golden_run(case, O, numerics):
     """The golden scenario on bfloat16 parameters: the HIP step and the
     oracle in lock step; yields after every step."""
     import adana_amd
@@ -67,13 +71,13 @@ def _golden_run(case, O):
     groups = [{"params": [gpu[i] for i in idx[gi]], "weight_decay": kw["weight_decay"] * meta["group_wd_scale"][gi]}
               for gi in range(2)]
     cls = adana_amd.DANA_STAR_MK4 if star else adana_amd.ADana
-    opt = cls(groups, **kw)
+    opt = cls(groups, numerics=numerics, **kw)
     orc = O.OracleOptimizer(groups=[O.OracleGroup(params=[host[i] for i in idx[gi]], lr=kw["lr"], delta=kw["delta"],
                                                   epsilon=1e-8, weight_decay=groups[gi]["weight_decay"])
                                     for gi in range(2)],
                             star=star, peak_lr=kw["lr"], kappa=kw["kappa"], clipsnr=kw["clipsnr"],
                             wd_decaying=kw["wd_decaying"], wd_ts=kw["wd_ts"], gamma_3_factor=kw["gamma_3_factor"],
-                            bf16=True)
+                            bf16=True, numerics=numerics)
     for k in range(1, meta["n_steps"] + 1):
         lr = kw["lr"] * meta["lr_multiplier"][k - 1]
         for g in opt.param_groups:
@@ -89,11 +93,12 @@ def _golden_run(case, O):
         yield k, meta, star, opt, orc, gpu, host, has_grad
 
 
+@pytest.mark.parametrize("numerics", ["compiled", "eager"])
 @pytest.mark.parametrize("case", golden_cases("eager"))
-def test_bf16_golden_against_oracle_and_reference(oracle_mod, case):
-    print("case: bf16 state golden scenario", case, flush=True)
-    gold = load_golden_case(case, "bf16_eager")
-    for k, meta, star, opt, orc, gpu, host, has_grad in _golden_run(case, oracle_mod):
+def test_bf16_golden_against_oracle_and_reference(oracle_mod, case, numerics):
+    print("case: bf16 state golden scenario", case, numerics, flush=True)
+    gold = load_golden_case(case, "bf16_compiled" if numerics == "compiled" else "bf16_eager")
+    for k, meta, star, opt, orc, gpu, host, has_grad in _golden_run(case, oracle_mod, numerics):
         for i, p in enumerate(gpu):
             st = opt.state[p]
             ost = orc.state.get(id(host[i]))
@@ -114,14 +119,15 @@ def test_bf16_golden_against_oracle_and_reference(oracle_mod, case):
                 _diag_close([float(st[key]) for key in oracle_mod.DIAG_KEYS],
                             [ost[key] for key in oracle_mod.DIAG_KEYS], tag)
             if k in meta["checkpoints"]:
-                # the reference's own bfloat16 eager run
+                # the reference's own bfloat16 run in the same numerics
                 _check(got, gold[f"p{i}_t{k}"], f"{tag} p vs reference", STAR_HARD_CASES if star else 0)
                 for key in keys:
                     _check(_bits(st[key]), gold[f"{key}{i}_t{k}"], f"{tag} {key} vs reference")
 
 
+@pytest.mark.parametrize("numerics", ["compiled", "eager"])
 @pytest.mark.parametrize("star", [False, True])
-def test_bf16_mixed_list_views_and_clip(oracle_mod, star):
+def test_bf16_mixed_list_views_and_clip(oracle_mod, star, numerics):
     """Tensors of 1 to 70,000 elements, one 2-byte-offset view (scalar path),
     two groups, 12 steps crossing t = delta, a fused clip every third step:
     bit-exact against the oracle (the clip coefficient applied to the bf16
@@ -129,7 +135,7 @@ def test_bf16_mixed_list_views_and_clip(oracle_mod, star):
     import adana_amd
 
     O = oracle_mod
-    print("case: bf16 state mixed list, star", star, flush=True)
+    print("case: bf16 state mixed list, star", star, numerics, flush=True)
     rng = np.random.default_rng(21)
     sizes = [70_000, 1, 3, 1024, 4099, 33 * 65]
     host = [O.f32_to_bf16(rng.normal(0, 0.02, n).astype(np.float32)) for n in sizes]
@@ -145,11 +151,11 @@ def test_bf16_mixed_list_views_and_clip(oracle_mod, star):
     hp = dict(lr=2e-3, delta=8.0, kappa=0.85, weight_decay=0.2, clipsnr=2.0, wd_decaying=True, wd_ts=5.0)
     groups = [{"params": gpu[:3]}, {"params": gpu[3:], "weight_decay": 0.0}]
     cls = adana_amd.DANA_STAR_MK4 if star else adana_amd.ADana
-    opt = cls(groups, **hp)
+    opt = cls(groups, numerics=numerics, **hp)
     orc = O.OracleOptimizer(groups=[O.OracleGroup(params=host[:3], lr=hp["lr"], weight_decay=0.2),
                                     O.OracleGroup(params=host[3:], lr=hp["lr"], weight_decay=0.0)],
                             star=star, peak_lr=hp["lr"], kappa=0.85, clipsnr=2.0, wd_decaying=True, wd_ts=5.0,
-                            bf16=True)
+                            bf16=True, numerics=numerics)
     for t in range(1, 13):
         g16 = [O.f32_to_bf16(rng.normal(0, 1e-3 * (30 if t % 3 == 0 else 1), n).astype(np.float32)) for n in sizes]
         for p, g in zip(gpu, g16):
@@ -225,8 +231,9 @@ def _bits_t(t):
 
 
 
+@pytest.mark.parametrize("numerics", ["compiled", "eager"])
 @pytest.mark.parametrize("star", [False, True])
-def test_bf16_nonfinite_gradients(oracle_mod, star):
+def test_bf16_nonfinite_gradients(oracle_mod, star, numerics):
     """NaN, +inf and -inf gradient entries (and huge and subnormal ones) on the
     bfloat16 path: p, m, v, tau bit-exact against the oracle's bfloat16
     restatement wherever it is finite, and NaN where it is NaN (the IEEE arms
@@ -234,16 +241,16 @@ def test_bf16_nonfinite_gradients(oracle_mod, star):
     import adana_amd
 
     O = oracle_mod
-    print("case: bf16 state, non-finite gradients, star", star, flush=True)
+    print("case: bf16 state, non-finite gradients, star", star, numerics, flush=True)
     rng = np.random.default_rng(5)
     sizes = [4096, 777]
     host = [O.f32_to_bf16(rng.normal(0, 0.02, n).astype(np.float32)) for n in sizes]
     gpu = [torch.nn.Parameter(_to_gpu16(h)) for h in host]
     hp = dict(lr=1e-3, delta=8.0, kappa=0.85, weight_decay=0.1, clipsnr=2.0)
     cls = adana_amd.DANA_STAR_MK4 if star else adana_amd.ADana
-    opt = cls(gpu, **hp)
+    opt = cls(gpu, numerics=numerics, **hp)
     orc = O.OracleOptimizer(groups=[O.OracleGroup(params=host, lr=hp["lr"], weight_decay=0.1)],
-                            star=star, peak_lr=hp["lr"], kappa=0.85, clipsnr=2.0, bf16=True)
+                            star=star, peak_lr=hp["lr"], kappa=0.85, clipsnr=2.0, bf16=True, numerics=numerics)
     specials = np.array([np.nan, np.inf, -np.inf, 3e38, -3e38, 1e-40, -1e-40, 0.0], np.float32)
     for t in range(1, 11):
         gf = [rng.normal(0, 1e-3, n).astype(np.float32) for n in sizes]

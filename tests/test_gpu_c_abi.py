@@ -35,12 +35,13 @@ def test_integration_example_through_the_c_abi(oracle_mod):
     vstart, fold_first, n_chunks, n_folds = _lib.plan_layout(numel)
     desc = np.zeros(len(sizes), _lib.DESC_DTYPE)
     for i in range(len(sizes)):
-        desc[i] = (p[i].data_ptr(), g[i].data_ptr(), m[i].data_ptr(), v[i].data_ptr(), tau[i].data_ptr(), 0,
+        desc[i] = (p[i].data_ptr(), 0, m[i].data_ptr(), v[i].data_ptr(), tau[i].data_ptr(), 0,
                    sizes[i], 0, _lib.DESC_VEC_OK)
     table = torch.from_numpy(np.concatenate([desc.view(np.uint8), vstart.view(np.uint8),
                                              fold_first.view(np.uint8)])).cuda()
+    gtab = torch.tensor([x.data_ptr() for x in g], dtype=torch.int64, device="cuda")
     n = len(sizes)
-    plan = _lib.Plan(desc=table.data_ptr(), vstart=table.data_ptr() + 64 * n,
+    plan = _lib.Plan(desc=table.data_ptr(), grad=gtab.data_ptr(), vstart=table.data_ptr() + 64 * n,
                      fold_first=table.data_ptr() + 64 * n + 8 * (n + 1), n_tensors=n,
                      n_chunks=n_chunks, n_folds=n_folds)
     chunk_first = torch.empty(n_chunks, dtype=torch.int32, device="cuda")
@@ -94,17 +95,19 @@ def test_cpp_host_drives_the_c_abi():
     assert r.stdout.strip().splitlines()[-1] == "c_abi_driver: ok"
 
 
-@pytest.mark.parametrize("kappas", [(0.85, 0.85), (0.85, 0.6)], ids=["one_exponent_table", "two_exponents_general"])
-def test_bf16_state_classes_through_the_c_abi(oracle_mod, kappas):
+@pytest.mark.parametrize("numerics", ["compiled", "eager"])
+@pytest.mark.parametrize("kappas", [(0.85, 0.85), (0.85, 0.6)], ids=["one_exponent", "two_exponents"])
+def test_bf16_state_classes_through_the_c_abi(oracle_mod, kappas, numerics):
     """bfloat16 state (ADANA_STATE_BF16) through the raw C ABI with two scalar
-    classes.  One shared exponent takes the launch's pow table; two
-    exponents (reachable only through the C ABI: the Python classes share
-    one kappa) take the binary64 pow per element.  Both bit-exact against
-    the oracle's bfloat16 restatement (Dana-Star p: the pow allowance),
-    12 steps so that tau * t passes 1 and alpha passes 0.5."""
+    classes, in both numerics.  Eager: one shared exponent takes the
+    launch's pow table; two exponents (reachable only through the C ABI: the
+    Python classes share one kappa) take the binary64 pow per element.
+    Compiled: the binary32 update with the binary64 pow either way.  All
+    bit-exact against the oracle's bfloat16 modes (Dana-Star p: the pow
+    allowance), 12 steps so that tau * t passes 1 and alpha passes 0.5."""
     from adana_amd import _lib
 
-    print("case: raw C ABI, bf16 state, kappas", kappas, flush=True)
+    print("case: raw C ABI, bf16 state, kappas", kappas, numerics, flush=True)
     O = oracle_mod
     L = _lib.lib()
     rng = np.random.default_rng(11)
@@ -124,11 +127,12 @@ def test_bf16_state_classes_through_the_c_abi(oracle_mod, kappas):
     vstart, fold_first, n_chunks, n_folds = _lib.plan_layout(np.array(sizes, dtype=np.int64))
     desc = np.zeros(n, _lib.DESC_DTYPE)
     for i in range(n):
-        desc[i] = (p[i].data_ptr(), g[i].data_ptr(), m[i].data_ptr(), v[i].data_ptr(), tau[i].data_ptr(), 0,
+        desc[i] = (p[i].data_ptr(), 0, m[i].data_ptr(), v[i].data_ptr(), tau[i].data_ptr(), 0,
                    sizes[i], cls[i], _lib.DESC_VEC_OK)
     table = torch.from_numpy(np.concatenate([desc.view(np.uint8), vstart.view(np.uint8),
                                              fold_first.view(np.uint8)])).cuda()
-    plan = _lib.Plan(desc=table.data_ptr(), vstart=table.data_ptr() + 64 * n,
+    gtab = torch.tensor([x.data_ptr() for x in g], dtype=torch.int64, device="cuda")
+    plan = _lib.Plan(desc=table.data_ptr(), grad=gtab.data_ptr(), vstart=table.data_ptr() + 64 * n,
                      fold_first=table.data_ptr() + 64 * n + 8 * (n + 1), n_tensors=n,
                      n_chunks=n_chunks, n_folds=n_folds)
     chunk_first = torch.empty(n_chunks, dtype=torch.int32, device="cuda")
@@ -140,11 +144,12 @@ def test_bf16_state_classes_through_the_c_abi(oracle_mod, kappas):
     diag = torch.empty(5 * n, dtype=torch.bfloat16, device="cuda")
     kw = dict(peak_lr=1e-3, delta=8.0, epsilon=1e-8, weight_decay=0.4, clipsnr=2.0, wd_ts=10.0,
               gamma_3_factor=1.0)
-    hps = [_lib.HParams(kappa=k, has_clip=1, wd_decaying=1, **kw) for k in kappas]
+    eager = numerics == "eager"
+    hps = [_lib.HParams(kappa=k, has_clip=1, wd_decaying=1, eager=int(eager), **kw) for k in kappas]
     cpu = {"p": [h.copy() for h in p_h]}
     for key in ("m", "v", "tau"):
         cpu[key] = [np.zeros(nn, np.uint16) for nn in sizes]
-    flags = _lib.VARIANT_STAR | _lib.GRAD_BF16 | _lib.STATE_BF16
+    flags = _lib.VARIANT_STAR | _lib.GRAD_BF16 | _lib.STATE_BF16 | (_lib.NUMERICS_EAGER if eager else 0)
     for t in range(1, 13):
         g_h = [O.f32_to_bf16(rng.normal(0, 1e-3, nn).astype(np.float32)) for nn in sizes]
         for gi, h in zip(g, g_h):
@@ -154,7 +159,7 @@ def test_bf16_state_classes_through_the_c_abi(oracle_mod, kappas):
                                     ctypes.c_void_p(ws.data_ptr()), ws.numel(), ctypes.c_void_p(diag.data_ptr()),
                                     ctypes.c_void_p(stream)), "mta_step")
         for i in range(n):
-            osc = O.step_scalars(lr=1e-3, kappa=kappas[cls[i]], wd_decaying=True, t=t, **kw)
+            osc = O.step_scalars(lr=1e-3, kappa=kappas[cls[i]], wd_decaying=True, t=t, compiled=not eager, **kw)
             O.element_step(True, cpu["p"][i], g_h[i], cpu["m"][i], cpu["v"][i], cpu["tau"][i], osc)
         torch.cuda.synchronize()
         for i in range(n):

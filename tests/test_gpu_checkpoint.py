@@ -45,7 +45,8 @@ def _build(case, p_init, dtype=torch.float32, **extra):
     for gi in range(2):
         groups.append({"params": [p for i, p in enumerate(params) if meta["group_of"][i] == gi],
                        "weight_decay": kw["weight_decay"] * meta["group_wd_scale"][gi]})
-    return cls(groups, **kw, **extra), params, meta, kw, c["class"] == "DANA_STAR_MK4"
+    # the checkpoints are the reference's eager run's: step in the same numerics
+    return cls(groups, **kw, **{"numerics": "eager", **extra}), params, meta, kw, c["class"] == "DANA_STAR_MK4"
 
 
 def _run(opt, params, meta, kw, grads, has_grad, k0, k1, dtype=torch.float32, on_step=None):
@@ -161,7 +162,7 @@ def test_reference_checkpoint_into_bf16_master_mode(oracle_mod):
                                     weighted_step_count=schema["param_groups"][gi]["weighted_step_count"]))
     orc = O.OracleOptimizer(groups=groups, star=False, peak_lr=kw["lr"], kappa=kw["kappa"],
                             clipsnr=kw["clipsnr"], wd_decaying=kw["wd_decaying"], wd_ts=kw["wd_ts"],
-                            gamma_3_factor=kw["gamma_3_factor"], master=True)
+                            gamma_3_factor=kw["gamma_3_factor"], master=True, numerics="eager")
     for i, p in enumerate(p16):
         st = ref["state"][i]
         orc.state[id(p)] = {"step": st["step"], "m": st["m"].cpu().numpy().copy(),

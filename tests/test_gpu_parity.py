@@ -52,7 +52,7 @@ def _scaled_ulps(x, ref, prev):
 class Pair:
     """The GPU optimizer and the oracle driven in lock step on equal inputs."""
 
-    def __init__(self, O, star, groups_np, master=False, **hp):
+    def __init__(self, O, star, groups_np, master=False, numerics="compiled", **hp):
         import adana_amd
 
         self.O = O
@@ -73,7 +73,7 @@ class Pair:
             self.gpu_params.append(tp)
             torch_groups.append(dict(params=tp, **gkw))
         cls = adana_amd.DANA_STAR_MK4 if star else adana_amd.ADana
-        self.opt = cls(torch_groups, master_weights=master, **hp)
+        self.opt = cls(torch_groups, master_weights=master, numerics=numerics, **hp)
         self.oracle = O.OracleOptimizer(
             groups=[O.OracleGroup(params=cp, lr=gkw.get("lr", hp["lr"]),
                                   delta=gkw.get("delta", hp.get("delta", 8.0)),
@@ -83,7 +83,7 @@ class Pair:
             star=star, peak_lr=hp["lr"], kappa=hp.get("kappa", 1.0),
             clipsnr=hp.get("clipsnr", 1.0 if star else None),
             wd_decaying=hp.get("wd_decaying", False), wd_ts=hp.get("wd_ts", 1.0),
-            gamma_3_factor=hp.get("gamma_3_factor", 1.0), master=master)
+            gamma_3_factor=hp.get("gamma_3_factor", 1.0), master=master, numerics=numerics)
 
     def set_lr(self, lrs):
         for g, og, lr in zip(self.opt.param_groups, self.oracle.groups, lrs):
@@ -164,41 +164,53 @@ def _normal(rng, shape, std):
 
 # --------------------------------------------------------------------------
 
+@pytest.mark.parametrize("numerics", ["compiled", "eager"])
 @pytest.mark.parametrize("clipsnr", [None, 2.0])
-def test_c1_adana_single_tensor(oracle_mod, clipsnr):
+def test_c1_adana_single_tensor(oracle_mod, clipsnr, numerics):
     """Config C1 (1024x4096 fp32, delta 8, omega 4, kappa 0.85, lr 1e-3,
-    wd_ts 10): bit-exact p, m, v for 12 steps (t crosses delta)."""
-    print("case: C1 ADana 1024x4096 clipsnr", clipsnr, flush=True)
+    wd_ts 10): bit-exact p, m, v for 12 steps (t crosses delta), in both of
+    the reference's numerics."""
+    print("case: C1 ADana 1024x4096 clipsnr", clipsnr, numerics, flush=True)
     rng = np.random.default_rng(0)
     pair = Pair(oracle_mod, False, [([_normal(rng, (1024, 4096), 0.02)], {})], lr=1e-3,
                 delta=8.0, kappa=0.85, epsilon=1e-8, weight_decay=4.0 / 10.0, clipsnr=clipsnr,
-                wd_decaying=True, wd_ts=10.0)
+                wd_decaying=True, wd_ts=10.0, numerics=numerics)
     for t in range(1, 13):
         g = np.random.default_rng(1000 + t).normal(0, 1e-3, (1024, 4096)).astype(np.float32)
         pair.step([[g]])
         pair.compare(resync=False, where=f"t={t}")
 
 
+@pytest.mark.parametrize("numerics", ["compiled", "eager"])
 @pytest.mark.parametrize("case", golden_cases("eager"))
-def test_golden_cases_on_gpu(oracle_mod, case):
+def test_golden_cases_on_gpu(oracle_mod, case, numerics):
     """The golden-vector scenarios (two groups, grad None every other step,
-    all-zero and row-sparse grads, warm-up/cosine lr) on the GPU vs the oracle."""
-    print("case: golden", case, flush=True)
-    _golden_on_gpu(oracle_mod, case, "inputs")
+    all-zero and row-sparse grads, warm-up/cosine lr) on the GPU vs the
+    oracle, in both numerics; and, for the compiled numerics, every
+    checkpoint against the reference's own torch.compile run
+    (tests/golden/<case>.compiled.npz): m, v, tau bit-exact, ADana's p
+    bit-exact, Dana-Star's p within 1 ulp of the tensor's largest value (the
+    reference's SIMD pow is not correctly rounded)."""
+    print("case: golden", case, numerics, flush=True)
+    _golden_on_gpu(oracle_mod, case, "inputs", numerics)
 
 
+@pytest.mark.parametrize("numerics", ["compiled", "eager"])
 @pytest.mark.parametrize("case", ["adana", "dana_mk4", "dana_star", "dana_star_mk4"])
-def test_nonfinite_gradients_on_gpu(oracle_mod, case):
+def test_nonfinite_gradients_on_gpu(oracle_mod, case, numerics):
     """The same scenarios with NaN, +inf and -inf gradient entries at steps 3
     and 6 (tests/golden/nonfinite.inputs.npz; the oracle follows the
     reference's own run there): the elements they reach turn NaN (v: inf)
     exactly where the oracle's do, the other elements keep the usual bars,
     and the tensors' diagnostics are NaN."""
-    print("case: non-finite gradients", case, flush=True)
-    _golden_on_gpu(oracle_mod, case, "nonfinite.inputs")
+    print("case: non-finite gradients", case, numerics, flush=True)
+    _golden_on_gpu(oracle_mod, case, "nonfinite.inputs", numerics)
 
 
-def _golden_on_gpu(oracle_mod, case, inputs):
+def _golden_on_gpu(oracle_mod, case, inputs, numerics):
+    from helpers import load_golden_case
+
+    gold = load_golden_case(case, "compiled") if (inputs == "inputs" and numerics == "compiled") else None
     meta, p0, grads, has_grad = load_golden_inputs(inputs)
     c = meta["cases"][case]
     kw = dict(c["kwargs"])
@@ -208,7 +220,7 @@ def _golden_on_gpu(oracle_mod, case, inputs):
         idx = [i for i in range(len(p0)) if meta["group_of"][i] == gi]
         groups.append(([p0[i] for i in idx],
                        {"weight_decay": kw["weight_decay"] * meta["group_wd_scale"][gi]}))
-    pair = Pair(oracle_mod, star, groups, **kw)
+    pair = Pair(oracle_mod, star, groups, numerics=numerics, **kw)
     for k in range(1, meta["n_steps"] + 1):
         lr = kw["lr"] * meta["lr_multiplier"][k - 1]
         pair.set_lr([lr, lr])
@@ -217,6 +229,17 @@ def _golden_on_gpu(oracle_mod, case, inputs):
             idx = [i for i in range(len(p0)) if meta["group_of"][i] == gi]
             gl.append([grads[k - 1][i] if has_grad[k - 1, i] else None for i in idx])
         pair.step(gl)
+        if gold is not None and k in meta["checkpoints"]:
+            flat = [p for tp in pair.gpu_params for p in tp]
+            order = [i for gi in range(2) for i in range(len(p0)) if meta["group_of"][i] == gi]
+            for p, i in zip(flat, order):
+                st = pair.opt.state[p]
+                for key in ("m", "v", "tau") if star else ("m", "v"):
+                    if key in st:
+                        assert ulp_diff(st[key].cpu().numpy(), gold[f"{key}{i}_t{k}"]).max() == 0, (case, k, i, key)
+                ref = gold[f"p{i}_t{k}"]
+                err = _scaled_ulps(p.detach().cpu().numpy(), ref, np.full(ref.shape, np.abs(ref).max(), np.float32))
+                assert err.max() <= (1 if star else 0), (case, k, i, err.max())
         pair.compare(where=f"{case} t={k}")
         for g, og in zip(pair.opt.param_groups, pair.oracle.groups):
             assert g["weighted_step_count"] == og.weighted_step_count
@@ -261,20 +284,23 @@ def test_gpt_list_two_groups(oracle_mod, star):
         pair.compare(where=f"k={k}")
 
 
-@pytest.mark.parametrize("kappa", [1.0, 0.0, 1.5, 2.0, -1.0, -2.0, 3.0, 0.3])
-def test_star_pow_modes(oracle_mod, kappa):
+@pytest.mark.parametrize("numerics", ["compiled", "eager"])
+@pytest.mark.parametrize("kappa", [1.0, 0.0, 1.5, 2.0, -1.0, -2.0, 3.0, 0.3, -3.0])
+def test_star_pow_modes(oracle_mod, kappa, numerics):
     """Every kind of the per-element pow eff_time ** (1 - kappa)
-    (src/optim/dana_star_mk4.py:168-170) through the kernel: exponent 0
-    (kappa 1: no pow), 1 (kappa 0: identity), ATen's special exponents
-    -0.5, -1, 2, 3, -2, and a general one (0.5 and 0.15 run in the golden
-    cases).  No SNR clip, so the pow reaches p unclamped; 12 steps, so that
-    tau * t passes 1 and the pow sees arguments above 1."""
-    print("case: Dana-Star pow mode kappa", kappa, flush=True)
+    (src/optim/dana_star_mk4.py:168-170) through the kernel, in both
+    numerics: exponent 0 (kappa 1: no pow), 1 (kappa 0: identity), -0.5
+    (eager: 1/sqrt; compiled: a general pow), -1, 2, 3, 4 and -2 (eager:
+    ATen's specialisations or a general pow; compiled: Inductor's integer
+    powering by products), and a general one (0.5 and 0.15 run in the
+    golden cases).  No SNR clip, so the pow reaches p unclamped; 12 steps,
+    so that tau * t passes 1 and the pow sees arguments above 1."""
+    print("case: Dana-Star pow mode kappa", kappa, numerics, flush=True)
     rng = np.random.default_rng(int(100 + 10 * kappa))
     shapes = [(37, 19), (1024,), (5,), (4096 + 3,)]
     params = [_normal(rng, s, 0.02) for s in shapes]
     pair = Pair(oracle_mod, True, [(params, {})], lr=1e-3, delta=4.0, kappa=kappa, clipsnr=None,
-                weight_decay=0.1, wd_decaying=True, wd_ts=5.0)
+                weight_decay=0.1, wd_decaying=True, wd_ts=5.0, numerics=numerics)
     for k in range(12):
         gl = [[_normal(rng, x.shape, 1e-3) for x in params]]
         pair.step(gl)
@@ -594,8 +620,10 @@ def test_parameter_rebound_to_another_shape_raises(drop_other_grad):
 def test_new_gradient_buffers_every_step(oracle_mod, star):
     """New gradient tensors at new addresses every step, alternating between
     16-byte-aligned buffers and views 4 bytes into a flat buffer (so the
-    descriptors' vector-path flag flips each step): the re-pointed tables
-    give the oracle's results every step."""
+    kernel's gradient alignment test flips each step between the vector and
+    the element-wise path): the re-pointed gradient array gives the oracle's
+    results every step, and every step after the first takes the one-pass
+    host scan."""
     print("case: new gradient buffers every step, star", star, flush=True)
     rng = np.random.default_rng(43)
     shapes = [(1000,), (64, 33), (5,), (4096 + 8,)]
@@ -623,8 +651,10 @@ def test_new_gradient_buffers_every_step(oracle_mod, star):
         pair.oracle.step(gl)
         torch.cuda.synchronize()
         pair.compare(where=f"k={k}")
-        flags = pair.opt._sets[0].host_desc["flags"]
-        assert (flags != 0).all() == (k % 2 == 0), (k, flags)
+        ls = pair.opt._sets[0]
+        assert (ls.host_desc["flags"] != 0).all()               # the other pointers stay aligned
+        assert (ls.host_grad % 16 == 0).all() == (k % 2 == 0), (k, ls.host_grad % 16)
+        assert pair.opt._fast
 
 
 def test_gradient_storage_swapped_in_place(oracle_mod):
@@ -881,18 +911,20 @@ def test_step_hooks_profiler_and_scheduler():
 
 
 @pytest.mark.parametrize("fresh", [None, False])
-def test_diagnostics_fresh_each_step(fresh):
+def test_diagnostics_kept_from_a_step_keep_their_value(fresh):
     """As the reference binds new 0-d tensors each step (src/optim/adana.py:
-    221-225), a diagnostic kept from one step keeps its value after the next
-    (the default for lists of up to 512 tensors); each has a storage of its
-    own (a deepcopy copies 4 bytes); the packed read-out and .item() agree.
-    With fresh_diagnostics=False the entries are bound once and refreshed in
-    place."""
+    221-225), a diagnostic kept from one step -- a reference to it, or a
+    tensor sharing its storage (detach(), a view) -- keeps its value after
+    the next step, and the state holds a new tensor (the default for lists
+    of up to 2,048 tensors); entries nothing else refers to are refreshed in
+    place.  Each has a storage of its own (a deepcopy copies 4 bytes); the
+    packed read-out and .item() agree.  With fresh_diagnostics=False every
+    entry is refreshed in place."""
     import copy
 
     import adana_amd
 
-    print("case: fresh diagnostics", fresh, flush=True)
+    print("case: kept diagnostics", fresh, flush=True)
     torch.manual_seed(8)
     ps = [torch.nn.Parameter(torch.randn(n, device=DEV) * 0.02) for n in (3000, 70_000)]
     opt = adana_amd.DANA_STAR_MK4(ps, lr=1e-3, kappa=0.85, clipsnr=2.0, fresh_diagnostics=fresh)
@@ -901,6 +933,11 @@ def test_diagnostics_fresh_each_step(fresh):
     opt.step()
     kept = opt.state[ps[1]]["gradient_norm"]
     first = float(kept)
+    detached = opt.state[ps[0]]["m_norm"].detach()               # shares the entry's storage
+    first_d = float(detached)
+    untouched = opt.state[ps[0]]["current_alpha"]
+    untouched_id = id(untouched)
+    del untouched
     assert kept.untyped_storage().nbytes() == 4
     assert copy.deepcopy(opt.state[ps[1]])["m_norm"].untyped_storage().nbytes() == 4
     for p in ps:
@@ -911,9 +948,42 @@ def test_diagnostics_fresh_each_step(fresh):
     assert float(now) == pytest.approx(want, rel=1e-5)
     if fresh is None:
         assert now is not kept and float(kept) == first             # the kept tensor holds step 1's value
+        assert float(detached) == first_d                            # and so does a tensor over its storage
+        assert float(opt.state[ps[0]]["m_norm"]) != first_d
+        assert id(opt.state[ps[0]]["current_alpha"]) == untouched_id  # refreshed in place
     else:
         assert now is kept and float(kept) == float(now)            # one tensor, refreshed in place
     params, vals = opt.diagnostics_host()
     for p, row in zip(params, vals):
         st = opt.state[p]
         assert list(row) == pytest.approx([float(st[k]) for k in adana_amd.optim.DIAG_KEYS], rel=0, nan_ok=True)
+
+
+def test_diagnostics_check_skipped_above_the_limit_warns_once():
+    """Lists of more than 2,048 stepped tensors skip the check (its cost
+    grows with the list): a RuntimeWarning says so once, and a kept entry
+    then follows the buffer; fresh_diagnostics=True keeps the check."""
+    import warnings
+
+    import adana_amd
+
+    print("case: kept-diagnostics check above the limit", flush=True)
+    for fresh in (None, True):
+        ps = [torch.nn.Parameter(torch.full((4,), 0.01 * (i % 7 + 1), device=DEV)) for i in range(2049)]
+        opt = adana_amd.ADana(ps, lr=1e-3, fresh_diagnostics=fresh)
+        for p in ps:
+            p.grad = torch.full_like(p, 1e-3)
+        with warnings.catch_warnings(record=True) as w:
+            warnings.simplefilter("always")
+            opt.step()
+            kept = opt.state[ps[5]]["gradient_norm"]
+            first = float(kept)
+            for p in ps:
+                p.grad = torch.full_like(p, 2e-3)
+            opt.step()
+        msgs = [x for x in w if issubclass(x.category, RuntimeWarning) and "2048" in str(x.message)]
+        assert len(msgs) == (1 if fresh is None else 0)
+        if fresh is None:
+            assert opt.state[ps[5]]["gradient_norm"] is kept and float(kept) == pytest.approx(2 * first)
+        else:
+            assert opt.state[ps[5]]["gradient_norm"] is not kept and float(kept) == first

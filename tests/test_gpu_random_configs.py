@@ -5,7 +5,8 @@ Dana-Star-MK4), fp32 parameters or the bf16-master extension, 1-3 parameter
 groups with their own lr, delta, epsilon and weight decay, 1-10 tensors per
 group (empty, tiny, ragged and up to 70,000-element sizes, 1-D and 2-D), kappa
 from the values that select each pow kind (0, 0.5, 0.85, 1, 1.5, 2, 3),
-clipsnr, decaying weight decay, wd_ts and gamma_3_factor.  It then takes 7
+clipsnr, decaying weight decay, wd_ts, gamma_3_factor and the numerics
+(the reference's compiled path or its eager ops).  It then takes 7
 steps (crossing t = delta for the smallest deltas) with a new lr per group
 each step, gradients of random scale with some all-zero tensors, and some
 gradients None (that tensor skips the step and keeps its state), and checks
@@ -54,6 +55,7 @@ def _draw(seed):
         hp["clipsnr"] = float(rng.choice([0.5, 1.0, 2.0]))
     else:
         hp["clipsnr"] = None if rng.random() < 0.5 else float(rng.choice([0.5, 2.0]))
+    hp["numerics"] = "eager" if rng.random() < 0.4 else "compiled"
     return rng, star, master, groups, hp
 
 
@@ -114,7 +116,7 @@ def test_random_configuration_bf16_state(oracle_mod, seed):
         groups=[O.OracleGroup(params=hs, lr=gkw["lr"], delta=gkw["delta"], epsilon=gkw["epsilon"],
                               weight_decay=gkw["weight_decay"]) for hs, (_, gkw) in zip(host, groups)],
         star=star, peak_lr=hp["lr"], kappa=hp["kappa"], clipsnr=hp["clipsnr"], wd_decaying=hp["wd_decaying"],
-        wd_ts=hp["wd_ts"], gamma_3_factor=hp["gamma_3_factor"], bf16=True)
+        wd_ts=hp["wd_ts"], gamma_3_factor=hp["gamma_3_factor"], bf16=True, numerics=hp["numerics"])
     keys = ("m", "v", "tau") if star else ("m", "v")
     for k in range(7):
         for g, og, (_, gkw) in zip(opt.param_groups, orc.groups, groups):

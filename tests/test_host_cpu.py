@@ -180,6 +180,9 @@ def test_mta_step_rejects_bad_arguments():
     fake = ctypes.c_void_p(0x1000)
     pl = _lib.Plan(desc=0x1000, vstart=0x1000, chunk_first=0x1000, fold_first=0x1000,
                    n_tensors=3, n_chunks=1, n_folds=3)
+    assert L.adana_mta_step(ctypes.byref(pl), scp, 1, 0, fake, 1 << 20, fake, None) == -1
+    assert "null pointer" in _lib.last_error()                   # no gradient pointer array
+    pl.grad = 0x1000
     assert L.adana_mta_step(ctypes.byref(pl), scp, 0, 0, fake, 1 << 20, fake, None) == -1
     assert "n_classes" in _lib.last_error()
     assert L.adana_mta_step(ctypes.byref(pl), scp, 1, 0, fake, 16, fake, None) == -1
@@ -559,9 +562,11 @@ def test_staging_decisions():
     (_, p0, g0), (_, p1, g1) = ls.stage
     assert p0.is_contiguous() and p0.shape == ps[0].shape and g0.is_contiguous()   # gapped p, transposed g
     assert p1 is None and g1.stride() == ps[1].stride()                            # contiguous g of a permuted p
-    assert int(d["param"][0]) == p0.data_ptr() and int(d["grad"][0]) == g0.data_ptr()
-    assert int(d["param"][1]) == ps[1].data_ptr() and int(d["grad"][1]) == g1.data_ptr()
-    assert int(d["param"][2]) == ps[2].data_ptr() and int(d["grad"][2]) == ls.grads[2].data_ptr()
+    g = ls.host_grad                                                               # adana_plan.grad
+    assert int(d["param"][0]) == p0.data_ptr() and int(g[0]) == g0.data_ptr()
+    assert int(d["param"][1]) == ps[1].data_ptr() and int(g[1]) == g1.data_ptr()
+    assert int(d["param"][2]) == ps[2].data_ptr() and int(g[2]) == ls.grads[2].data_ptr()
+    assert int(d["reserved0"].max()) == 0
     ls.grads = [torch.zeros(12, 16), torch.zeros(9, 7).t(), torch.zeros(50)]
     opt._desc_rows(ls)
     assert [(j, ps_ is not None, gs is not None) for j, ps_, gs in ls.stage] == [(0, True, False)]
@@ -607,7 +612,7 @@ def test_deepcopy_and_pickle_keep_the_configuration():
                     assert k in vars(other), (cls.__name__, k)
                     if k not in ("state", "param_groups", "defaults"):   # torch's __setstate__ adds to defaults
                         assert getattr(other, k) == v, (cls.__name__, k)
-            assert other._sets is None and other._active is None and other._diag_loc == {}
+            assert other._sets is None and other._fast is False and other._diag_loc == {}
             assert other.param_groups[0]["params"][0] is not opt.param_groups[0]["params"][0]
 
 

@@ -23,7 +23,19 @@ So the oracle differs from the reference only where torch's CPU sqrt and pow
 (SIMD approximations, not correctly rounded) differ from correctly rounded
 results.  ``test_oracle_gap_is_sqrt_and_pow_only`` records the size of that
 gap per step.
+
+The same two steps pin the oracle's compiled numerics (the reference's
+default torch.compile path, tests/golden/*.compiled.npz and
+*.bf16_compiled.npz): ``oracle.torch_ref.update_compiled`` -- Inductor's
+forms of the update, run as eager ops with the square root and power
+Inductor's CPU code calls (a correctly rounded sqrt, at::vec's SIMD pow on
+every element, the C library's powf for ADana's 0-d power) -- reproduces the
+compiled fixtures at 0 ulp; with the element-wise power made correctly
+rounded it reproduces the oracle's compiled mode at 0 ulp.  So in compiled
+mode the oracle differs from the reference only where the SIMD pow of
+Dana-Star's effective time is not correctly rounded.
 """
+import ctypes
 import math
 
 import numpy as np
@@ -49,18 +61,51 @@ def _cr_pow(x: torch.Tensor, e: float) -> torch.Tensor:
     return torch.tensor(flat, dtype=torch.float64).reshape(x.shape).float()
 
 
-def _run(case, *, sqrt=torch.sqrt, epow=None, on_step=None, slip=None):
+def _simd_pow(x: torch.Tensor, e: float) -> torch.Tensor:
+    """The element-wise power of Inductor's CPU code for exponent e: its pow
+    lowering (torch/_inductor/lowering.py) makes 0.5 a square root (correctly
+    rounded, as its SIMD sqrt is) and any other exponent at::vec's SIMD pow
+    with e rounded to binary32, on every element (the generated loop loads a
+    tensor's tail as a masked vector).  Eager torch.pow runs the same SIMD
+    function on whole 32-element blocks, so it is run here on a copy padded
+    to a multiple of 64.  (The fixtures' exponents are 0, 0.15 and 0.5.)"""
+    if e == 0.0:
+        return torch.ones_like(x)
+    if e == 0.5:
+        return _cr_sqrt(x)
+    flat = x.reshape(-1)
+    pad = (-flat.numel()) % 64
+    y = torch.pow(torch.cat([flat, torch.ones(pad, dtype=x.dtype)]), e)
+    return y[:flat.numel()].reshape(x.shape)
+
+
+_LIBM = ctypes.CDLL("libm.so.6")
+_LIBM.powf.restype = ctypes.c_float
+_LIBM.powf.argtypes = [ctypes.c_float, ctypes.c_float]
+
+
+def _powf(x: float, e: float) -> float:
+    """std::pow(float, float), what Inductor's CPU code calls for ADana's 0-d
+    (1 + step) ** (1 - kappa): the C library's powf, exponent rounded to
+    binary32 (the lowering's integer and 0.5 cases do not occur here)."""
+    return _LIBM.powf(x, float(np.float32(e)))
+
+
+def _run(case, *, sqrt=torch.sqrt, epow=None, on_step=None, slip=None, compiled=None, bf16=False):
     """oracle.torch_ref's restatement of the reference's step() over the
     golden inputs: two groups (weight decay on group 0 only), per-tensor step
     counters, grad None skipped, lr = peak * multiplier(k).  ``on_step(k,
     params, state, diags)`` sees the state after each step; ``diags[i]`` are
-    the five diagnostics of the tensors stepped at k."""
+    the five diagnostics of the tensors stepped at k.  ``compiled``: the
+    (sqrt, epow, powf) of torch_ref.update_compiled, or None for the eager
+    ops.  ``bf16``: bfloat16 parameters and gradients."""
     from oracle.torch_ref import DIAG_KEYS, TorchRefGroup, TorchRefOptimizer
 
     meta, p0, grads, has_grad = load_golden_inputs()
     kw = meta["cases"][case]["kwargs"]
     star = meta["cases"][case]["class"] == "DANA_STAR_MK4"
-    params = [torch.from_numpy(x.copy()) for x in p0]
+    dt = torch.bfloat16 if bf16 else torch.float32
+    params = [torch.from_numpy(x.copy()).to(dt) for x in p0]
     idx = [[i for i in range(len(params)) if meta["group_of"][i] == gi] for gi in range(2)]
     groups = [TorchRefGroup(params=[params[i] for i in idx[gi]], lr=kw["lr"], delta=kw["delta"], epsilon=1e-8,
                             weight_decay=kw["weight_decay"] * meta["group_wd_scale"][gi]) for gi in range(2)]
@@ -69,9 +114,9 @@ def _run(case, *, sqrt=torch.sqrt, epow=None, on_step=None, slip=None):
     for k in range(1, meta["n_steps"] + 1):
         for g in groups:
             g.lr = kw["lr"] * meta["lr_multiplier"][k - 1]
-        gl = [[torch.from_numpy(grads[k - 1][i].copy()) if has_grad[k - 1, i] else None for i in idx[gi]]
+        gl = [[torch.from_numpy(grads[k - 1][i].copy()).to(dt) if has_grad[k - 1, i] else None for i in idx[gi]]
               for gi in range(2)]
-        opt.step(gl, sqrt=sqrt, epow=epow, slip=slip)
+        opt.step(gl, sqrt=sqrt, epow=epow, slip=slip, compiled=compiled)
         state = {i: opt.state[id(p)] for i, p in enumerate(params) if id(p) in opt.state}
         diags = {i: [float(state[i][key]) for key in DIAG_KEYS] for i in range(len(params)) if has_grad[k - 1, i]}
         if on_step is not None:
@@ -242,3 +287,73 @@ def test_torch_restatement_reproduces_reference_bf16_bits(case):
             st = opt.state.get(id(p))
             for key in (("m", "v", "tau") if star else ("m", "v")) if st else ():
                 assert np.array_equal(bits(st[key]), gold[f"{key}{i}_t{k}"]), (case, key, k, i)
+
+
+def _bits(t: torch.Tensor) -> np.ndarray:
+    return t.view(torch.int16).numpy().view(np.uint16) if t.dtype == torch.bfloat16 else t.numpy().view(np.uint32)
+
+
+@pytest.mark.skipif(torch.backends.cpu.get_cpu_capability() != load_golden_inputs()[0].get("cpu_capability"),
+                    reason="torch's CPU SIMD pow bits depend on the SIMD level the fixtures were written with")
+@pytest.mark.parametrize("mode", ["compiled", "bf16_compiled"])
+@pytest.mark.parametrize("case", golden_cases("compiled"))
+def test_compiled_restatement_reproduces_reference_bits(case, mode):
+    """Inductor's forms of the update (torch_ref.update_compiled) with the
+    square root and powers Inductor's CPU code calls give the reference's
+    torch.compile bits (0 ulp) for p, m, v, tau at every checkpoint, on
+    float32 and on bfloat16 parameters; diagnostics within 1e-5 (Inductor
+    sums in another order)."""
+    gold = load_golden_case(case, mode)
+    meta = load_golden_inputs()[0]
+    bf16 = mode.startswith("bf16")
+    star = meta["cases"][case]["class"] == "DANA_STAR_MK4"
+
+    def check(k, params, state, diags):
+        for i, d in diags.items():
+            np.testing.assert_allclose(d, gold["diag"][k - 1, i], rtol=8e-3 if bf16 else 1e-5, atol=0,
+                                       equal_nan=True)
+        if k not in meta["checkpoints"]:
+            return
+        for i, p in enumerate(params):
+            assert np.array_equal(_bits(p), gold[f"p{i}_t{k}"].view(_bits(p).dtype)), (case, mode, k, i)
+            for key in (("m", "v", "tau") if star else ("m", "v")) if i in state else ():
+                got = _bits(state[i][key])
+                assert np.array_equal(got, gold[f"{key}{i}_t{k}"].view(got.dtype)), (case, mode, key, k, i)
+
+    _run(case, on_step=check, compiled=(_cr_sqrt, _simd_pow, _powf), bf16=bf16)
+
+
+@pytest.mark.parametrize("mode", ["compiled", "bf16_compiled"])
+@pytest.mark.parametrize("case", golden_cases("compiled"))
+def test_oracle_equals_compiled_restatement_with_correct_rounding(oracle_mod, case, mode):
+    """The same compiled-form restatement with Dana-Star's element-wise power
+    correctly rounded gives the oracle's compiled mode bit for bit (p, m, v,
+    tau, float32 and bfloat16) along the whole 20-step trajectory: the
+    oracle's compiled numerics differ from the reference's only in that
+    power."""
+    from test_oracle import _grads_for_step, _make_oracle
+
+    O = oracle_mod
+    bf16 = mode.startswith("bf16")
+    meta, p0, grads, has_grad = load_golden_inputs()
+    o_params = [(O.f32_to_bf16(x) if bf16 else x).copy() for x in p0]
+    opt, kw, star = _make_oracle(O, meta, case, o_params, "compiled", bf16=bf16)
+    o_grads = [[O.f32_to_bf16(g) for g in gs] for gs in grads] if bf16 else grads
+
+    def cr_pow(x, e):
+        return _cr_sqrt(x) if e == 0.5 else (torch.ones_like(x) if e == 0.0 else _cr_pow(x, e))
+
+    def check(k, params, state, diags):
+        for g in opt.groups:
+            g.lr = kw["lr"] * meta["lr_multiplier"][k - 1]
+        opt.step(_grads_for_step(meta, o_grads, has_grad, k))
+        for i, p in enumerate(params):
+            assert np.array_equal(_bits(p), o_params[i].view(_bits(p).dtype)), (case, mode, k, i)
+            if i not in state:
+                continue
+            ost = opt.state[id(o_params[i])]
+            for key in ("m", "v") + (("tau",) if star else ()):
+                got = _bits(state[i][key])
+                assert np.array_equal(got, ost[key].view(got.dtype)), (case, mode, key, k, i)
+
+    _run(case, on_step=check, compiled=(_cr_sqrt, cr_pow, _powf), bf16=bf16)
