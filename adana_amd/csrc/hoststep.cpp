@@ -18,9 +18,13 @@
  * StepTable holds one laid-out plan's rows and does a step's host work in one
  * pass whether or not the gradients are new tensors: every gradient is checked
  * against its parameter and its pointer gathered, the step counters advance
- * and the parameters' version counters are bumped.  It also keeps the
- * diagnostics bound in the state dicts, refreshed in place by each step, with
- * any the caller still refers to moved aside first.
+ * and the parameters' version counters are bumped.  For plans of thousands of
+ * rows, a few helper threads check and bump contiguous ranges of rows while
+ * the calling thread advances the step counters, so the cache misses of a
+ * cold walk (right after a backward pass) overlap.  A scan either does all of
+ * this or changes nothing.  StepTable also keeps the diagnostics bound in the
+ * state dicts, refreshed in place by each step, with any the caller still
+ * refers to moved aside first.
  */
 #include <torch/csrc/autograd/python_variable.h>
 #include <torch/csrc/autograd/variable.h>
@@ -28,9 +32,17 @@
 
 #include <Python.h>
 
+#include <c10/core/InferenceMode.h>
+#include <pthread.h>
+
+#include <algorithm>
+#include <atomic>
+#include <condition_variable>
 #include <cstdint>
 #include <exception>
+#include <mutex>
 #include <new>
+#include <thread>
 #include <utility>
 #include <vector>
 
@@ -76,15 +88,40 @@ int data_ptr_of(PyObject *t, uint64_t *out) {
     return PyErr_Occurred() ? -1 : 0;
 }
 
+// Puts states[i]["step"] back to saved[i] for i < saved.size() and releases
+// saved (a Python error already set is kept).
+template <class State>
+void restore_steps(State state, std::vector<PyObject *> &saved) {
+    PyObject *et, *ev, *tb;
+    PyErr_Fetch(&et, &ev, &tb);
+    for (size_t i = 0; i < saved.size(); ++i) {
+        if (PyDict_SetItem(state(i), g_step_name, saved[i])) PyErr_Clear();
+        Py_DECREF(saved[i]);
+    }
+    saved.clear();
+    PyErr_Restore(et, ev, tb);
+}
+
 // states[i]["step"] += 1 for every dict (i < n; state(i) returns it, borrowed);
 // tensors stepped together hold equal counts, so the new int of the previous
 // entry is reused (ints are immutable) when this entry's old int is equal.
-// 0, or -1 with a Python error set.
+// Returns 0 with the old values in ``saved`` (new references, for a later
+// restore_steps); -1 with a Python error set and every dict as it was; or,
+// with ints_only, 1 (every dict as it was, no error) as soon as a count is not
+// an exact int -- adding to anything else may run Python code.
 template <class State>
-int advance_states_impl(size_t n, State state) {
+int advance_states_impl(size_t n, State state, std::vector<PyObject *> &saved, bool ints_only = false) {
     PyObject *prev_v = nullptr, *prev_w = nullptr;
     int rc = 0;
+    saved.clear();
+    saved.reserve(n);
     for (size_t i = 0; i < n && !rc; ++i) {
+        if (i + 16 < n) __builtin_prefetch(state(i + 16), 0, 3);
+        if (i + 8 < n && PyDict_Check(state(i + 8))) {
+            const char *keys = reinterpret_cast<const char *>(reinterpret_cast<PyDictObject *>(state(i + 8))->ma_keys);
+            __builtin_prefetch(keys, 1, 3);
+            __builtin_prefetch(keys + 64, 1, 3);
+        }
         PyObject *st = state(i);
         if (!PyDict_Check(st)) {
             PyErr_SetString(PyExc_TypeError, "step counters: state entries must be dicts");
@@ -95,6 +132,10 @@ int advance_states_impl(size_t n, State state) {
         if (!v) {
             if (!PyErr_Occurred()) PyErr_SetString(PyExc_KeyError, "step");
             rc = -1;
+            break;
+        }
+        if (ints_only && !PyLong_CheckExact(v)) {
+            rc = 1;
             break;
         }
         const bool reuse = prev_v && (v == prev_v || (PyLong_CheckExact(v) && PyLong_CheckExact(prev_v) &&
@@ -111,18 +152,25 @@ int advance_states_impl(size_t n, State state) {
             prev_v = v;
             prev_w = w;
         }
-        rc = PyDict_SetItem(st, g_step_name, prev_w);
+        Py_INCREF(v);
+        if (PyDict_SetItem(st, g_step_name, prev_w)) {
+            Py_DECREF(v);
+            rc = -1;
+            break;
+        }
+        saved.push_back(v);
     }
     Py_XDECREF(prev_v);
     Py_XDECREF(prev_w);
+    if (rc) restore_steps(state, saved);
     return rc;
 }
 int advance_states(PyObject *states) {
-    return advance_states_impl(static_cast<size_t>(PyList_GET_SIZE(states)),
-                               [states](size_t i) { return PyList_GET_ITEM(states, static_cast<Py_ssize_t>(i)); });
-}
-int advance_states_vec(const std::vector<PyObject *> &states) {
-    return advance_states_impl(states.size(), [&states](size_t i) { return states[i]; });
+    std::vector<PyObject *> saved;
+    auto state = [states](size_t i) { return PyList_GET_ITEM(states, static_cast<Py_ssize_t>(i)); };
+    const int rc = advance_states_impl(static_cast<size_t>(PyList_GET_SIZE(states)), state, saved);
+    for (PyObject *o : saved) Py_DECREF(o);
+    return rc;
 }
 
 /* advance_if_same(params, grads, states[, param_ptrs[, grad_ptrs]]) -> bool
@@ -322,6 +370,53 @@ bool same_layout(const at::Tensor &a, const at::Tensor &b) {
     return true;
 }
 
+/* Prefetch hints for a scan over thousands of tensors.  Each row's check
+ * chases PyObject -> TensorImpl -> AutogradMeta -> gradient TensorImpl ->
+ * StorageImpl, and its bookkeeping touches the state dict and the version
+ * counter: a dozen cache lines per row, scattered over the heap and mostly
+ * cold right after a backward pass.  Issued a few rows ahead, in the order
+ * the chain resolves, they overlap those misses instead of taking them one
+ * after another.  A prefetch never faults, so a stale address costs nothing
+ * but the hint. */
+inline void prefetch_lines(const void *p, int lines) {
+    for (int k = 0; k < lines; ++k) __builtin_prefetch(static_cast<const char *>(p) + 64 * k, 0, 3);
+}
+static_assert(sizeof(c10::VariableVersion) == sizeof(void *),
+              "c10::VariableVersion is expected to hold one pointer (its VersionCounter)");
+// The VersionCounter object behind a tensor's version counter (for a hint only).
+inline const void *version_counter_object(const at::TensorImpl *t) {
+    return *reinterpret_cast<const void *const *>(&t->version_counter());
+}
+inline at::TensorImpl *impl_of(PyObject *exact_tensor) {
+    return THPVariable_Unpack(exact_tensor).unsafeGetTensorImpl();
+}
+struct ScanPrefetch {
+    PyObject *const *params;   // the rows [0, n) of one scan range
+    size_t n;
+    const at::TensorImpl *grad_ring[8] = {};
+    // hints for the rows the scan reaches 16, 12, 8, 4 and 2 rows after row i
+    void ahead(size_t i) {
+        if (i + 16 < n) __builtin_prefetch(params[i + 16], 0, 3);
+        if (i + 12 < n) prefetch_lines(impl_of(params[i + 12]), 3);
+        if (i + 8 < n) {
+            const at::TensorImpl *t = impl_of(params[i + 8]);
+            if (t->autograd_meta()) prefetch_lines(t->autograd_meta(), 2);
+            __builtin_prefetch(t->unsafe_storage().unsafeGetStorageImpl(), 0, 3);
+            __builtin_prefetch(version_counter_object(t), 1, 3);
+        }
+        if (i + 4 < n) {
+            const at::Tensor &g = impl_of(params[i + 4])->grad();
+            const at::TensorImpl *gi = g.defined() ? g.unsafeGetTensorImpl() : nullptr;
+            grad_ring[(i + 4) & 7] = gi;
+            if (gi) prefetch_lines(gi, 3);
+        }
+        if (i + 2 < n && i >= 2) {
+            const at::TensorImpl *gi = grad_ring[(i + 2) & 7];
+            if (gi) __builtin_prefetch(gi->unsafe_storage().unsafeGetStorageImpl(), 0, 3);
+        }
+    }
+};
+
 /* grads_match(params, grads, bf16) -> bool
  *
  * True when every grads[i] can stand in for the gradient the launch tables
@@ -493,6 +588,7 @@ struct TableData {
     std::vector<uint64_t> pptr;                          // parameter data pointers the plan holds
     std::vector<uint64_t> last;                          // gradient pointers of the last accepted scan
     std::vector<uint64_t> tmp;                           // this scan's pointers until it is accepted
+    std::vector<PyObject *> saved;                       // a scan's old step counts until it is accepted
     std::vector<PyObject *> diag;                        // bound diagnostics, ncols per row (strong)
     std::vector<std::pair<long, PyObject *>> cols;       // (kernel output column, state key), keys strong
     c10::ScalarType want = c10::ScalarType::Float;
@@ -594,6 +690,165 @@ PyObject *step_table(PyObject *, PyObject *args) {
     return reinterpret_cast<PyObject *>(t);
 }
 
+/* One scan range's checks, rows [lo, hi) of the plan: every row has a dense
+ * gradient of the plan's dtype on its parameter's device with its parameter's
+ * shape and strides, the parameter keeps the storage the plan holds, and its
+ * version counter can be bumped (inference tensors only in inference mode,
+ * where the bump is a no-op).  The gradient pointers go to d.tmp; rows whose
+ * pointer moved since the last accepted scan widen [*clo, *chi).  false as
+ * soon as a row does not fit.  It reads tensors only (no Python API, no
+ * reference counts), so helper threads run it while the caller holds the GIL. */
+bool check_rows(TableData &d, size_t lo, size_t hi, bool inference, size_t *clo, size_t *chi) {
+    ScanPrefetch ahead{d.params.data() + lo, hi - lo};
+    for (size_t i = lo; i < hi; ++i) {
+        ahead.ahead(i - lo);
+        const at::Tensor &pt = THPVariable_Unpack(d.params[i]);
+        if (reinterpret_cast<uint64_t>(pt.const_data_ptr()) != d.pptr[i]) return false;
+        if (!inference && !pt.unsafeGetTensorImpl()->version_counter().enabled()) return false;
+        const at::Tensor &g = pt.unsafeGetTensorImpl()->grad();
+        if (!g.defined() || g.is_sparse() || g.scalar_type() != d.want || g.device() != pt.device() ||
+            !same_layout(g, pt))
+            return false;
+        const uint64_t gp = reinterpret_cast<uint64_t>(g.const_data_ptr());
+        d.tmp[i] = gp;
+        if (gp != d.last[i]) {
+            if (i < *clo) *clo = i;
+            *chi = i + 1;
+        }
+    }
+    return true;
+}
+
+// Bumps the version counters of rows [lo, hi), whose parameters the launch
+// that follows updates in place (check_rows has passed them).
+void bump_rows(TableData &d, size_t lo, size_t hi) {
+    for (size_t i = lo; i < hi; ++i) {
+        if (i + 8 < hi) __builtin_prefetch(version_counter_object(impl_of(d.params[i + 8])), 1, 3);
+        at::TensorImpl *t = impl_of(d.params[i]);
+        if (t->version_counter().enabled()) t->bump_version();
+    }
+}
+
+/* Helper threads for the scans of long plans (thousands of rows).  Each
+ * helper checks and then bumps one contiguous range of rows, so the cache
+ * misses of the ranges overlap, while the calling thread, which holds the
+ * GIL, advances the step counters.  Helpers never call into Python or touch
+ * reference counts, and a scan waits for every helper it started before it
+ * returns.  After fork() the child starts a pool of its own. */
+constexpr int kMaxHelpers = 8;
+constexpr size_t kParallelRows = 2048;   // shorter plans are scanned by the calling thread
+constexpr size_t kMinRowsPerHelper = 1024;
+
+struct ScanPool {
+    std::mutex mu;
+    std::condition_variable cv;
+    uint64_t gen = 0;                     // moved (under mu) to start a job
+    int started = 0;                      // helper threads running
+    // the job, written before gen moves
+    TableData *d = nullptr;
+    int parts = 0;
+    bool inference = false;
+    struct Part {
+        size_t lo, hi, clo, chi;
+        bool ok;
+    } part[kMaxHelpers];
+    std::atomic<int> checked{0}, finished{0};
+    std::atomic<int> decision{0};         // 0 pending, 1 bump the versions, 2 stop
+};
+ScanPool *g_pool = nullptr;
+int g_helpers = 3;
+
+inline void cpu_relax() { __builtin_ia32_pause(); }
+
+void helper_main(ScanPool *P, int id) {
+    uint64_t seen = 0;
+    for (;;) {
+        {
+            std::unique_lock<std::mutex> lk(P->mu);
+            P->cv.wait(lk, [&] { return P->gen != seen; });
+            seen = P->gen;
+            if (id >= P->parts) continue;
+        }
+        ScanPool::Part &r = P->part[id];
+        bool ok;
+        try {
+            ok = check_rows(*P->d, r.lo, r.hi, P->inference, &r.clo, &r.chi);
+        } catch (...) {
+            ok = false;   // the caller's general path raises the precise error
+        }
+        r.ok = ok;
+        P->checked.fetch_add(1, std::memory_order_acq_rel);
+        int dec;
+        while ((dec = P->decision.load(std::memory_order_acquire)) == 0) cpu_relax();
+        if (dec == 1) bump_rows(*P->d, r.lo, r.hi);
+        P->finished.fetch_add(1, std::memory_order_acq_rel);
+    }
+}
+
+void pool_after_fork_child() { g_pool = nullptr; }
+
+// The pool with at least `want` helpers running (fewer if threads cannot be started).
+ScanPool *scan_pool(int want) {
+    if (!g_pool) {
+        static bool registered = false;
+        if (!registered) {
+            pthread_atfork(nullptr, nullptr, pool_after_fork_child);
+            registered = true;
+        }
+        g_pool = new ScanPool();   // lives until the process ends, like its threads
+    }
+    ScanPool *P = g_pool;
+    while (P->started < want) {
+        try {
+            std::thread(helper_main, P, P->started).detach();
+        } catch (const std::exception &) {
+            break;
+        }
+        ++P->started;
+    }
+    return P;
+}
+
+/* The scan's checks and version bumps on `parts` helpers while this thread
+ * advances the step counters.  1: done; 0: a row does not fit (nothing
+ * modified); -1: error, with a Python error set (nothing modified). */
+int scan_parallel(TableData &d, ScanPool &P, int parts, size_t *lo, size_t *hi) {
+    const size_t n = d.params.size();
+    P.d = &d;
+    P.parts = parts;
+    P.inference = c10::InferenceMode::is_enabled();
+    for (int k = 0; k < parts; ++k) P.part[k] = {n * k / parts, n * (k + 1) / parts, n, 0, false};
+    P.checked.store(0);
+    P.finished.store(0);
+    P.decision.store(0);
+    {
+        std::lock_guard<std::mutex> lk(P.mu);
+        ++P.gen;
+    }
+    P.cv.notify_all();
+    // Exact-int counters advance now and are put back if a row does not fit;
+    // any other kind of counter waits for the checks (adding to it may run
+    // Python code, which must not run while the helpers read the tensors).
+    auto state = [&d](size_t i) { return d.states[i]; };
+    int arc = advance_states_impl(n, state, d.saved, true);
+    while (P.checked.load(std::memory_order_acquire) < parts) cpu_relax();
+    bool fits = true;
+    for (int k = 0; k < parts; ++k) fits = fits && P.part[k].ok;
+    if (fits && arc == 1) arc = advance_states_impl(n, state, d.saved);
+    const bool go = fits && arc == 0;
+    P.decision.store(go ? 1 : 2, std::memory_order_release);
+    while (P.finished.load(std::memory_order_acquire) < parts) cpu_relax();
+    if (!go) {
+        if (arc == 0) restore_steps(state, d.saved);
+        return arc < 0 ? -1 : 0;
+    }
+    for (int k = 0; k < parts; ++k) {
+        if (P.part[k].clo < *lo) *lo = P.part[k].clo;
+        if (P.part[k].chi > *hi) *hi = P.part[k].chi;
+    }
+    return 1;
+}
+
 /* StepTable.scan(out_address) -> (lo, hi) or None
  *
  * One step's host bookkeeping for the plan (src/optim/adana.py:184-197,
@@ -607,7 +862,8 @@ PyObject *step_table(PyObject *, PyObject *args) {
  * [lo, hi) whose gradient pointer differs from the last accepted scan are
  * returned (lo == hi: none moved).  None, with nothing modified, when the
  * plan does not fit: the caller takes its general path (which also raises
- * the precise error for a bad gradient). */
+ * the precise error for a bad gradient).  Plans of thousands of rows are
+ * checked by helper threads (scan_threads). */
 PyObject *table_scan(PyObject *self, PyObject *arg) {
     TableData &d = *reinterpret_cast<StepTable *>(self)->d;
     const unsigned long long addr = PyLong_AsUnsignedLongLong(arg);
@@ -622,30 +878,50 @@ PyObject *table_scan(PyObject *self, PyObject *arg) {
         for (PyObject *p : d.inactive)
             if (THPVariable_Unpack(p).unsafeGetTensorImpl()->grad().defined()) Py_RETURN_NONE;
         size_t lo = n, hi = 0;
-        for (size_t i = 0; i < n; ++i) {
-            const at::Tensor &pt = THPVariable_Unpack(d.params[i]);
-            if (reinterpret_cast<uint64_t>(pt.const_data_ptr()) != d.pptr[i]) Py_RETURN_NONE;
-            const at::Tensor &g = pt.unsafeGetTensorImpl()->grad();
-            if (!g.defined() || g.is_sparse() || g.scalar_type() != d.want || g.device() != pt.device() ||
-                !same_layout(g, pt))
-                Py_RETURN_NONE;
-            const uint64_t gp = reinterpret_cast<uint64_t>(g.const_data_ptr());
-            d.tmp[i] = gp;
-            if (gp != d.last[i]) {
-                if (i < lo) lo = i;
-                hi = i + 1;
-            }
+        int parts = 0;
+        if (n >= kParallelRows && g_helpers > 0)
+            parts = static_cast<int>(std::min<size_t>(static_cast<size_t>(g_helpers), n / kMinRowsPerHelper));
+        ScanPool *pool = parts >= 2 ? scan_pool(parts) : nullptr;
+        if (pool) parts = std::min(parts, pool->started);
+        if (pool && parts >= 2) {
+            const int rc = scan_parallel(d, *pool, parts, &lo, &hi);
+            if (rc < 0) return nullptr;
+            if (rc == 0) Py_RETURN_NONE;
+        } else {
+            if (!check_rows(d, 0, n, c10::InferenceMode::is_enabled(), &lo, &hi)) Py_RETURN_NONE;
+            if (advance_states_impl(n, [&d](size_t i) { return d.states[i]; }, d.saved)) return nullptr;
+            bump_rows(d, 0, n);
         }
-        if (advance_states_vec(d.states)) return nullptr;
+        for (PyObject *o : d.saved) Py_DECREF(o);
+        d.saved.clear();
         for (size_t i = 0; i < n; ++i) out[i] = d.tmp[i];
         for (size_t i = lo; i < hi; ++i) d.last[i] = d.tmp[i];
-        for (PyObject *p : d.params) torch::autograd::impl::bump_version(THPVariable_Unpack(p));
         if (lo > hi) lo = hi = 0;
         return Py_BuildValue("nn", static_cast<Py_ssize_t>(lo), static_cast<Py_ssize_t>(hi));
     } catch (const std::exception &e) {
         PyErr_SetString(PyExc_RuntimeError, e.what());
         return nullptr;
     }
+}
+
+/* scan_threads([k]) -> int: how many helper threads a scan of a plan of
+ * thousands of rows uses (k given: set it, 0 to 8; 0 scans on the calling
+ * thread alone).  Returns the value before the call. */
+PyObject *scan_threads(PyObject *, PyObject *args) {
+    int k = -1;
+    if (!PyArg_ParseTuple(args, "|i", &k)) return nullptr;
+    const int before = g_helpers;
+    if (k >= 0) {
+        if (k > kMaxHelpers) {
+            PyErr_Format(PyExc_ValueError, "scan_threads: at most %d helper threads", kMaxHelpers);
+            return nullptr;
+        }
+        g_helpers = k;
+    } else if (PyTuple_GET_SIZE(args)) {
+        PyErr_SetString(PyExc_ValueError, "scan_threads: k must be >= 0");
+        return nullptr;
+    }
+    return PyLong_FromLong(before);
 }
 
 /* StepTable.forget() -> None: the next scan reports every row as moved (the
@@ -861,6 +1137,9 @@ PyMethodDef methods[] = {
      "advance_if_same(params, grads, states[, param_ptrs[, grad_ptrs]]) -> bool: if params[i].grad is "
      "grads[i] for all i (and params[i] / grads[i] still have the data pointers given as native uint64 bytes), "
      "increment every states[j]['step'] and return True; otherwise change nothing and return False."},
+    {"scan_threads", scan_threads, METH_VARARGS,
+     "scan_threads([k]) -> int: helper threads for the scans of plans of thousands of rows (k given: set it, "
+     "0 to 8; 0 = the calling thread alone); returns the previous value."},
     {"advance_steps", advance_steps, METH_VARARGS,
      "advance_steps(states) -> None: increment every states[j]['step']."},
     {"grads_of", grads_of, METH_VARARGS,

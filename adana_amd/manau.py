@@ -19,6 +19,7 @@ group) is not part of this single-GPU build and raises.
 """
 from __future__ import annotations
 
+import ctypes
 import math
 from typing import Dict, List, Tuple
 
@@ -143,6 +144,14 @@ class Manau(_DanaFamily):
     # The fused clip path would scale only the Dana branch's gradients.
     def _arm_clip(self, grads, plan, clip, write_back: bool) -> bool:
         return False
+
+    def _fill_scalars(self, ls, classes) -> int:
+        """The launch set's scalar classes of the branch (adana_manau_scalars,
+        the same 64-byte slots) written into ls.sc_arr; their count."""
+        n_cls = min(_lib.MAX_CLASSES, len(classes) - ls.class_base)
+        for k, sc in enumerate(self._scalars(classes[ls.class_base:ls.class_base + n_cls])):
+            ctypes.memmove(ctypes.byref(ls.sc_arr[k]), ctypes.byref(sc), 64)
+        return n_cls
 
     def _scalars(self, classes):
         hps, out = {}, []

@@ -132,6 +132,9 @@ class _LaunchSet:
         self.plan = None
         self.diag = None
         self.table = None           # _hoststep.StepTable over the rows (diagnostics; the fast scan)
+        self.grad_addr = 0          # host_grad's address (StepTable.scan writes there)
+        self.sc_arr = None          # the launch's scalar classes, filled in place every step
+        self.args = None            # the launch's constant ctypes arguments
         self.ptr_key = None         # the parameters' data pointers the tables hold
         self.stage = []             # (row, param staging or None, grad staging or None)
         self.stage_bufs = {}        # (row, "p" | "g") -> staging tensor, kept while it fits
@@ -160,6 +163,7 @@ class _DanaFamily(Optimizer):
         self._fast = False          # one launch set, no staging: step() may take StepTable.scan
         self._classes = None
         self._diag_warned = False
+        self._hp_cache = {}
         self._pending_clip = None
         self._clip_plan_obj = None
         self._diag_loc = {}        # param -> (launch set, row) of its latest plan
@@ -410,6 +414,7 @@ class _DanaFamily(Optimizer):
             d[j] = (param_ptr, 0, m_ptr, v_ptr, tau_ptr, lp_ptr, p.numel(), ls.sclass[j],
                     _lib.DESC_VEC_OK if ok else 0)
         ls.host_grad = gptr
+        ls.grad_addr = gptr.ctypes.data
         ls.stage = stage
         return d
 
@@ -499,6 +504,10 @@ class _DanaFamily(Optimizer):
                 # the reference's bfloat16 path keeps bfloat16 diagnostics
                 ls.diag = torch.full((len(ls.params), 5), float("nan"), device=ls.device,
                                      dtype=torch.bfloat16 if ls.flags & _lib.STATE_BF16 else torch.float32)
+            ls.sc_arr = (_lib.StepScalars * _lib.MAX_CLASSES)()
+            ls.args = (ctypes.byref(ls.plan), ctypes.cast(ls.sc_arr, ctypes.c_void_p),
+                       ctypes.c_void_p(ls.workspace.data_ptr()), ls.workspace.numel(),
+                       ctypes.c_void_p(ls.diag.data_ptr()))
             # The rows' table: its scan is the fast path of the next steps (a
             # single launch set only), and it keeps the diagnostics bound as
             # 0-d tensors over the kernel's output rows, each with a storage of
@@ -594,14 +603,30 @@ class _DanaFamily(Optimizer):
             self._fast = False
         return self._flat[1], self._flat[2]
 
-    def _scalars(self, classes):
-        hps, out = {}, []
-        for gi, t in classes:
-            hp = hps.get(gi)
-            if hp is None:
-                hp = hps[gi] = self._hparams(self.param_groups[gi])
-            out.append(_lib.step_scalars(hp, self.param_groups[gi]["lr"], t))
-        return out
+    def _group_hparams(self, gi: int) -> "_lib.HParams":
+        """Group gi's hyper-parameters for the scalar code, rebuilt only when a
+        value they are made of changed."""
+        g = self.param_groups[gi]
+        key = (g["delta"], g["epsilon"], g["weight_decay"], self.lr, self.kappa, self.clipsnr, self.wd_ts,
+               self.gamma_3_factor, self.wd_decaying, self.numerics)
+        ent = self._hp_cache.get(gi)
+        if ent is None or ent[0] != key:
+            ent = self._hp_cache[gi] = (key, self._hparams(g))
+        return ent[1]
+
+    def _fill_scalars(self, ls: _LaunchSet, classes) -> int:
+        """Write the launch set's scalar classes (adana_step_scalars_init, per
+        (group, step) class, at the group's current lr) into ls.sc_arr;
+        return their count."""
+        L = _lib.lib()
+        n_cls = min(_lib.MAX_CLASSES, len(classes) - ls.class_base)
+        for k in range(n_cls):
+            gi, t = classes[ls.class_base + k]
+            _lib.check(L.adana_step_scalars_init(ctypes.byref(ls.sc_arr[k]),
+                                                 ctypes.byref(self._group_hparams(gi)),
+                                                 float(self.param_groups[gi]["lr"]), int(t)),
+                       "adana_step_scalars_init")
+        return n_cls
 
     def step(self, closure=None):
         """One optimizer step (src/optim/adana.py:155-227); returns the
@@ -645,7 +670,7 @@ class _DanaFamily(Optimizer):
             # every ``state['step'] += 1`` (adana.py:197) and bumps the
             # parameters' versions; only pointers that moved are uploaded.
             ls = self._sets[0]
-            span = ls.table.scan(ls.host_grad.ctypes.data)
+            span = ls.table.scan(ls.grad_addr)
             if span is not None:
                 self._classes = [(gi, t + 1) for gi, t in self._classes]
                 if span[1] > span[0]:
@@ -751,28 +776,27 @@ class _DanaFamily(Optimizer):
             else:
                 self.flush_clip()
 
-        scalars = self._scalars(classes)
         L = _lib.lib()
         checked = self._diag_checked()
         cur = torch.cuda.current_device()
         for ls in self._sets:
-            n_cls = min(_lib.MAX_CLASSES, len(classes) - ls.class_base)
-            sc_arr = (type(scalars[0]) * n_cls)(*scalars[ls.class_base:ls.class_base + n_cls])
+            n_cls = self._fill_scalars(ls, classes)
             if ls.device.index == cur:
-                self._launch_set(L, ls, sc_arr, n_cls, gscale, wflag, checked)
+                self._launch_set(L, ls, n_cls, gscale, wflag, checked)
             else:
                 with torch.cuda.device(ls.device):
-                    self._launch_set(L, ls, sc_arr, n_cls, gscale, wflag, checked)
+                    self._launch_set(L, ls, n_cls, gscale, wflag, checked)
         if params is not None:
             _hoststep.bump_versions(params)                # p was updated in place
         if wflag:
             _hoststep.bump_versions(pend[0])
         return loss
 
-    def _launch_set(self, L, ls: _LaunchSet, sc_arr, n_cls: int, gscale, wflag: int, checked: bool) -> None:
+    def _launch_set(self, L, ls: _LaunchSet, n_cls: int, gscale, wflag: int, checked: bool) -> None:
         """One launch set's staging copies, diagnostics guard and step launch,
-        with ls.device current."""
-        stream = torch.cuda.current_stream(ls.device).cuda_stream
+        with ls.device current, on torch's current stream."""
+        stream = ctypes.c_void_p(torch._C._cuda_getCurrentRawStream(ls.device.index))
+        plan, sc, ws, ws_bytes, diag = ls.args
         if checked:
             self._diag_guard(ls)
         for j, ps, gs in ls.stage:       # into the state's layout (same stream)
@@ -781,17 +805,12 @@ class _DanaFamily(Optimizer):
             if gs is not None:
                 gs.copy_(ls.grads[j])
         if gscale is None:
-            _lib.check(L.adana_mta_step(
-                ctypes.byref(ls.plan), ctypes.cast(sc_arr, ctypes.c_void_p), n_cls, ls.flags,
-                ctypes.c_void_p(ls.workspace.data_ptr()), ls.workspace.numel(),
-                ctypes.c_void_p(ls.diag.data_ptr()), ctypes.c_void_p(stream)), "adana_mta_step")
+            rc = L.adana_mta_step(plan, sc, n_cls, ls.flags, ws, ws_bytes, diag, stream)
+            if rc:
+                _lib.check(rc, "adana_mta_step")
         else:
-            _lib.check(L.adana_mta_step_scaled(
-                ctypes.byref(ls.plan), ctypes.cast(sc_arr, ctypes.c_void_p), n_cls,
-                ls.flags | wflag, ctypes.c_void_p(gscale),
-                ctypes.c_void_p(ls.workspace.data_ptr()), ls.workspace.numel(),
-                ctypes.c_void_p(ls.diag.data_ptr()), ctypes.c_void_p(stream)),
-                "adana_mta_step_scaled")
+            _lib.check(L.adana_mta_step_scaled(plan, sc, n_cls, ls.flags | wflag, ctypes.c_void_p(gscale),
+                                               ws, ws_bytes, diag, stream), "adana_mta_step_scaled")
         for j, ps, gs in ls.stage:       # and back
             if ps is not None:
                 ls.params[j].copy_(ps)
@@ -828,7 +847,7 @@ class _DanaFamily(Optimizer):
             # parameter's layout and the set's dtype: re-point those
             moved = np.flatnonzero(gptr != ls.host_grad)
             if moved.size:
-                ls.host_grad = gptr.copy()
+                ls.host_grad[:] = gptr
                 with torch.cuda.device(ls.device):
                     self._upload_grads(ls, int(moved[0]), int(moved[-1]) + 1)
                 ls.table.forget()

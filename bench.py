@@ -463,6 +463,75 @@ def launch_ms(run, reps, stream):
     return e0.elapsed_time(e1) / reps
 
 
+def same_cap_probe(run_step, w, n_elems, n_tensors, reps=5, rounds=3):
+    """The step and its access pattern without the arithmetic at the step's
+    own residency cap, timed alternately in one process (``rounds`` rounds of
+    ``reps`` back-to-back steps, then ``reps`` back-to-back probe launches):
+    the probe is probes/stream_probe.hip's 5-in/4-out (Dana-Star), 4-in/3-out
+    (ADana) or bf16-master kernel, and the cap is the one the step's launch
+    takes (4 resident workgroups per CU on grids of at least 64 chunks per
+    CU, none on smaller grids or for Dana-Star's pow instance on lists of
+    small tensors).  Returns None for workloads without a probe (bfloat16
+    state)."""
+    import ctypes
+
+    import torch
+
+    if w.get("state_bf16"):
+        return None
+    n = n_elems // 1024 * 1024
+    n_chunks = n // 1024
+    small = n_chunks < 64 * n_tensors
+    general_pow = w["star"] and 0.0 < 1.0 - w["hp"]["kappa"] < 1.0
+    cap = 0 if (n_chunks < 64 * 256 or (general_pow and small)) else 4
+    lib = ctypes.CDLL(os.path.join(ROOT, "probes", "libadana_probe.so"))
+    stream = torch.cuda.current_stream()
+    partials = torch.empty(n_chunks * 4, device="cuda:0")
+    if w["master"]:
+        fn = lib.adana_probe_stream_master
+        fn.argtypes = [ctypes.c_void_p] * 5 + [ctypes.c_int64, ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p]
+        fn.restype = ctypes.c_int
+        f32 = [torch.zeros(n, device="cuda:0") for _ in range(3)]
+        b16 = [torch.zeros(n, dtype=torch.bfloat16, device="cuda:0") for _ in range(2)]
+        bpe = 28
+        args = [ctypes.c_void_p(f32[0].data_ptr()), ctypes.c_void_p(b16[0].data_ptr()),
+                ctypes.c_void_p(f32[1].data_ptr()), ctypes.c_void_p(f32[2].data_ptr()),
+                ctypes.c_void_p(b16[1].data_ptr()), n, ctypes.c_void_p(partials.data_ptr()), cap,
+                ctypes.c_void_p(stream.cuda_stream)]
+        keep = (f32, b16)
+        what = "bf16-master pattern (28 B/element)"
+    else:
+        fn = lib.adana_probe_stream_5r4w if w["star"] else lib.adana_probe_stream_4r3w
+        fn.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p]
+        fn.restype = ctypes.c_int
+        arrays = [torch.zeros(n, device="cuda:0") for _ in range(5 if w["star"] else 4)]
+        ptrs = (ctypes.c_void_p * 5)(*([a.data_ptr() for a in arrays] + [0] * (5 - len(arrays))))
+        bpe = 36 if w["star"] else 28
+        args = [ptrs, n, ctypes.c_void_p(partials.data_ptr()), cap, ctypes.c_void_p(stream.cuda_stream)]
+        keep = (arrays, ptrs)
+        what = ("5 fp32 arrays read, 4 written back" if w["star"] else "4 fp32 arrays read, 3 written back")
+
+    def run_probe():
+        if fn(*args) != 0:
+            raise RuntimeError("stream probe launch failed")
+
+    steps, probes = [], []
+    for _ in range(rounds):
+        steps.append(launch_ms(run_step, reps, stream))
+        probes.append(launch_ms(run_probe, reps, stream))
+    del keep, partials
+    torch.cuda.empty_cache()
+    step_ms, probe_ms = float(np.median(steps)), float(np.median(probes))
+    probe_gbs = bpe * n / (probe_ms * 1e-3) / 1e9
+    return {"wgs_per_cu": cap, "probe_ms": round(probe_ms, 4), "probe_achieved": round(probe_gbs, 2),
+            "probe_frac": round(probe_gbs / HBM_PEAK_GBS, 4), "step_ms": round(step_ms, 4),
+            "step_over_probe": round(probe_ms / step_ms, 4),
+            "note": f"the step's access pattern without its arithmetic ({what}, stream_probe.hip) at the "
+                    f"step's own residency cap ({cap or 'none'} workgroups per CU), timed alternately with the "
+                    f"step in this process: {rounds} rounds of {reps} back-to-back launches each, medians; "
+                    f"step_over_probe = probe ms / step ms (the step's rate as a fraction of the probe's)"}
+
+
 def stream_sweep(args):
     """The memory system's ceiling for the north-star step's access pattern.
 
@@ -894,19 +963,33 @@ def main():
 
     host = None
     if not w.get("clip"):
-        # Host time of opt.step() alone: with the same gradient tensors every step, and with a
-        # different gradient tensor, at a different address, for every parameter every step
-        # (the reference's loop runs zero_grad(set_to_none=True) before each backward, so
-        # its gradients are new tensors; the caching allocator may or may not reuse addresses).
+        # Host time of opt.step() alone (its launches are asynchronous), three ways:
+        #  * same_grads: the same gradient tensors every step;
+        #  * reference_loop: the reference's training loop (src/optim/base.py:250-289):
+        #    zero_grad(set_to_none=True), a backward pass that gives every parameter a
+        #    new gradient tensor (autograd allocates it from the caching allocator; the
+        #    loss sum((p * w).sum()) makes that gradient w, the workload's gradient),
+        #    then a host synchronisation (the loop's grad_norm.item()) before step();
+        #  * moved_every_step: every gradient replaced by a tensor at another address
+        #    before each step (the worst case for re-pointing).
         cur = [p.grad for p in params]
         alt = [g.clone() for g in cur]
 
-        def host_ms(fresh, k0):
+        def backward():
+            with torch.enable_grad():
+                loss = torch.stack([(p * g).sum() for p, g in zip(params, cur)]).sum()
+            loss.backward()
+
+        def host_ms(mode, k0):
             t = []
             for k in range(args.steps):
-                if fresh:
+                if mode == "moved_every_step":
                     for p, g in zip(params, alt if k % 2 == 0 else cur):
                         p.grad = g
+                elif mode == "reference_loop":
+                    opt.zero_grad(set_to_none=True)
+                    backward()
+                    torch.cuda.synchronize()
                 h0 = time.perf_counter()
                 one_step(k0 + k)
                 t.append((time.perf_counter() - h0) * 1e3)
@@ -914,13 +997,28 @@ def main():
             return round(float(np.median(t)), 4)
 
         k0 = args.warmup + 2 * args.steps
-        host = {"same_grads": host_ms(False, k0), "new_grads_every_step": host_ms(True, k0 + args.steps),
-                "note": "median host time of opt.step() alone (launches are asynchronous); "
-                        "new_grads_every_step: every p.grad replaced by a tensor at another address "
-                        "before each step, outside the timed call"}
+        host = {mode: host_ms(mode, k0 + i * args.steps)
+                for i, mode in enumerate(("same_grads", "reference_loop", "moved_every_step"))}
+        host["note"] = ("median host time of opt.step() alone (launches are asynchronous): same_grads, the same "
+                        "gradient tensors every step; reference_loop, zero_grad(set_to_none=True), a backward pass "
+                        "that gives every parameter a new gradient tensor, and a host synchronisation before each "
+                        "step, as src/optim/base.py:250-289 runs it; moved_every_step, every p.grad replaced "
+                        "by a tensor at another address before each step")
         for p, g in zip(params, cur):
             p.grad = g
         del alt, cur
+
+    same_cap = None
+    if not args.no_ceiling_probe and not w.get("clip"):
+        print("[bench] timing the step and its access pattern at the step's residency cap, alternately",
+              file=sys.stderr, flush=True)
+        k_sc = [args.warmup + 5 * args.steps]
+
+        def run_step():
+            one_step(k_sc[0])
+            k_sc[0] += 1
+
+        same_cap = same_cap_probe(run_step, w, n_elems, len(params))
 
     cold = None
     if algo_bytes < MALL_BYTES:
@@ -957,6 +1055,7 @@ def main():
                    "tensors": len(params), "bytes_per_elem": bpe,
                    "algorithmic_bytes_per_step": algo_bytes, "grads": w["grad_note"],
                    "hyperparams": w["hp"], "master_weights": w["master"],
+                   "numerics": "compiled (the reference's default torch.compile path)",
                    "parallelism": "single GPU",
                    **({"warmup_note": w["warmup_note"]} if "warmup_note" in w else {}),
                    **({"lr_schedule": dict(C2_SCHEDULE, kind="cos_inf (src/optim/schedule.py:70-98)",
@@ -980,6 +1079,8 @@ def main():
     }
     del opt, params
     torch.cuda.empty_cache()
+    if same_cap is not None:
+        result["roofline"]["same_cap_probe"] = same_cap
     if bpe in (28, 36) and not w["master"] and not args.no_ceiling_probe:
         # the same access pattern without the arithmetic: what the memory system allows this mix
         print("[bench] timing the stream probe of the step's access pattern", file=sys.stderr, flush=True)

@@ -638,3 +638,27 @@ def test_bind_diag_entries():
         _hoststep.bind_diag(torch.zeros(9), [{}, {}], [(0, "x")])
     with pytest.raises(TypeError, match="dicts"):
         _hoststep.bind_diag(torch.zeros(10), [{}, 3], [(0, "x")])
+
+
+@pytest.mark.parametrize("numerics", ["compiled", "eager"])
+def test_scalar_fill_in_place(numerics):
+    """The launch fills its scalar classes in place (adana_step_scalars_init
+    into the set's array, hyper-parameters cached per group and rebuilt when
+    one changes): the same bits as the one-off scalars, per class, for the
+    group's current lr and the class's step.  Host only (no launch)."""
+    import adana_amd
+    from adana_amd import _lib
+    from adana_amd.optim import _LaunchSet
+
+    ps = [torch.nn.Parameter(torch.zeros(4)) for _ in range(3)]
+    opt = adana_amd.DANA_STAR_MK4([{"params": ps[:2]}, {"params": ps[2:], "weight_decay": 0.3, "lr": 2e-3}],
+                                  lr=1e-3, kappa=0.85, wd_decaying=True, wd_ts=7.0, numerics=numerics)
+    ls = _LaunchSet(torch.device("cpu"), 0, 0)
+    ls.sc_arr = (_lib.StepScalars * _lib.MAX_CLASSES)()
+    classes = [(0, 3), (1, 3), (0, 5)]
+    for wd in (0.3, 0.5):                       # a changed group value reaches the scalars
+        opt.param_groups[1]["weight_decay"] = wd
+        assert opt._fill_scalars(ls, classes) == 3
+        for k, (gi, t) in enumerate(classes):
+            want = _lib.step_scalars(opt._hparams(opt.param_groups[gi]), opt.param_groups[gi]["lr"], t)
+            assert bytes(ls.sc_arr[k]) == bytes(want), (wd, k)
