@@ -62,6 +62,7 @@ from __future__ import annotations
 import ctypes
 import operator
 import warnings
+import weakref
 from typing import Iterable, List, Optional
 
 import numpy as np
@@ -86,6 +87,8 @@ class _SlabRef:
 
 
 _SLAB_ALIGN = 1024      # elements (4 KB): every state tensor starts a fresh work chunk
+_CANARY32 = 0x7FA5A5A5  # a float32 NaN bit pattern around each state slab's tensors
+_CANARY16 = 0x7FA5      # the bfloat16 one
 
 
 def _carve(buf: torch.Tensor, off: int, shape, strides=None) -> torch.Tensor:
@@ -169,6 +172,7 @@ class _DanaFamily(Optimizer):
         self._diag_loc = {}        # param -> (launch set, row) of its latest plan
         self._diag_epoch = 0       # bumped whenever a plan or the state tensors change
         self._diag_cache = None
+        self._slab_guards = []     # (weakref to a state slab, family, base, total, [(offset, numel)])
         _lib.lib()  # fail at construction, not at the first step, without the kernel library
 
     # -- pickling and deepcopy --------------------------------------------
@@ -257,6 +261,13 @@ class _DanaFamily(Optimizer):
                 # headroom so that the first tensor starts on a _SLAB_ALIGN-element boundary
                 slab = torch.zeros(total + _SLAB_ALIGN, dtype=dt, device=dev)
                 base = (-(slab.data_ptr() // slab.element_size())) % _SLAB_ALIGN
+                # canaries before the first tensor and after the last (no kernel writes there)
+                bits = slab.view(torch.int16 if dt == torch.bfloat16 else torch.int32)
+                canary = _CANARY16 if dt == torch.bfloat16 else _CANARY32
+                bits[:base].fill_(canary)
+                bits[base + total:].fill_(canary)
+                self._slab_guards.append((weakref.ref(slab), fam, base, total,
+                                          [(off, p.numel()) for (p, _), off in zip(members, offs)]))
                 for (p, st), off in zip(members, offs):
                     # zeros_like(p): p's shape and, for a transposed or permuted p, its strides
                     t = _carve(slab, base + off, p.shape, None if p.is_contiguous() else p.stride())
@@ -265,6 +276,32 @@ class _DanaFamily(Optimizer):
                     elif fam == "master":
                         t.copy_(p.detach())
                     st[fam] = t
+
+    def _check_slab_guards(self) -> int:
+        """Check the elements of every live state slab that belong to no state
+        tensor: the canaries before the first tensor and after the last still
+        hold their bit pattern, and the padding between tensors is still zero.
+        Returns the number of slabs checked; raises RuntimeError naming the
+        first element that changed (a kernel wrote outside its tensors)."""
+        checked = 0
+        for ref, fam, base, total, members in self._slab_guards:
+            slab = ref()
+            if slab is None:
+                continue
+            bits = slab.view(torch.int16 if slab.dtype == torch.bfloat16 else torch.int32)
+            canary = _CANARY16 if slab.dtype == torch.bfloat16 else _CANARY32
+            spans = [(0, base, canary), (base + total, bits.numel(), canary)]
+            ends = [off + n for off, n in members]
+            starts = [off for off, _ in members[1:]] + [total]
+            spans += [(base + e, base + s, 0) for e, s in zip(ends, starts) if s > e]
+            for lo, hi, want in spans:
+                if hi > lo:
+                    bad = (bits[lo:hi] != want).nonzero()
+                    if bad.numel():
+                        raise RuntimeError(f"{type(self).__name__}: state slab {fam!r} element "
+                                           f"{lo + int(bad[0])} outside every tensor was overwritten")
+            checked += 1
+        return checked
 
     def invalidate_plan(self) -> None:
         """Forget cached device tables and tensor lists (call after swapping a

@@ -369,8 +369,12 @@ def test_unaligned_views(oracle_mod, star):
             else:
                 assert ulp_diff(gp, c).max() == 0
             c[...] = gp
-    # the untouched guard elements around the views stay untouched
-    assert flat[0].item() == float(_normal(np.random.default_rng(7), (sum(sizes) + 3,), 0.02)[0])
+    # the guard elements around the views (one before the first, two after the
+    # last) and the gradient buffer's leading guard stay untouched
+    start = _normal(np.random.default_rng(7), (sum(sizes) + 3,), 0.02)
+    for i in (0, sum(sizes) + 1, sum(sizes) + 2):
+        assert flat[i].item() == float(start[i]), i
+    assert gflat[0].item() == 0.0
 
 
 @pytest.mark.parametrize("star", [False, True])
@@ -987,3 +991,34 @@ def test_diagnostics_check_skipped_above_the_limit_warns_once():
             assert opt.state[ps[5]]["gradient_norm"] is kept and float(kept) == pytest.approx(2 * first)
         else:
             assert opt.state[ps[5]]["gradient_norm"] is not kept and float(kept) == first
+
+
+@pytest.mark.parametrize("master", [False, True])
+@pytest.mark.parametrize("star", [False, True])
+def test_state_slab_guards(star, master):
+    """The state slabs' elements outside every state tensor -- a canary bit
+    pattern before the first tensor and after the last, zero padding between
+    tensors -- are untouched after steps over tensors that end on, before and
+    after chunk boundaries; and the check sees a changed canary."""
+    import adana_amd
+
+    print("case: state slab guards star", star, "master", master, flush=True)
+    rng = np.random.default_rng(11)
+    sizes = [1, 1023, 1024, 1025, 5000, 3]
+    dt = torch.bfloat16 if master else torch.float32
+    params = [torch.nn.Parameter(torch.from_numpy(_normal(rng, (n,), 0.02)).to(DEV).to(dt)) for n in sizes]
+    cls = adana_amd.DANA_STAR_MK4 if star else adana_amd.ADana
+    opt = cls(params, lr=1e-3, kappa=0.85, weight_decay=0.1, master_weights=master)
+    for _ in range(3):
+        for p, n in zip(params, sizes):
+            p.grad = torch.from_numpy(_normal(rng, (n,), 1e-3)).to(DEV).to(dt)
+        opt.step()
+    torch.cuda.synchronize()
+    families = (3 if star else 2) + (1 if master else 0)
+    assert opt._check_slab_guards() == families
+    ref, fam, base, total, _ = opt._slab_guards[0]
+    slab = ref()
+    bits = slab.view(torch.int16 if slab.dtype == torch.bfloat16 else torch.int32)
+    bits[base + total] = 0
+    with pytest.raises(RuntimeError, match="overwritten"):
+        opt._check_slab_guards()

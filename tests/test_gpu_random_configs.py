@@ -90,6 +90,7 @@ def test_random_configuration(oracle_mod, seed):
             grads.append(gs)
         pair.step(grads)
         pair.compare(where=f"seed {seed} k={k}")
+    pair.opt._check_slab_guards()     # nothing written outside the state tensors
 
 
 @pytest.mark.parametrize("seed", range(24))
@@ -152,6 +153,7 @@ def test_random_configuration_bf16_state(oracle_mod, seed):
                 _check(got, h, f"{tag} p", STAR_HARD_CASES if star else 0)
                 h[...] = got.reshape(h.shape)
                 _diag_close([float(st[key]) for key in O.DIAG_KEYS], [float(ost[key]) for key in O.DIAG_KEYS], tag)
+    opt._check_slab_guards()          # nothing written outside the state tensors
 
 
 @pytest.mark.parametrize("seed", range(16))

@@ -136,7 +136,8 @@ def test_nonfinite_trajectory(oracle_mod, case):
             if np.isnan(ref).any():
                 assert (~fin).sum() < ref.size            # the other elements stay finite
             scale = np.full(fin.sum(), np.abs(ref[fin]).max(), np.float32)
-            assert _scaled_err(p[fin], ref[fin], scale).max() <= 2 * k, (case, k, i)
+            # measured worst 2 ulps of the tensor's largest |p| (dana_star, t = 7 .. 20), bar 3
+            assert _scaled_err(p[fin], ref[fin], scale).max() <= 3, (case, k, i)
 
 
 @pytest.mark.parametrize("case", golden_cases("eager"))
