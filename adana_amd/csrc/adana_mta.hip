@@ -703,12 +703,11 @@ __device__ __forceinline__ void store_grad1(const void *g, int64_t off, float x)
 }
 
 // ---------------------------------------------------------------------------
-// Main multi-tensor kernel: one 1024-element chunk per workgroup, VEC
-// consecutive elements (one 4*VEC-byte vector per array) per thread, a single
-// load -> update -> store pass (waves exit right after their stores; looping
-// waves would wait on their own stores, which the gfx9 vmcnt counter orders
-// with later loads).  All variants run VEC = 4 (256 threads); VEC = 2 (512
-// threads) is kept compilable for tuning.
+// Main multi-tensor kernel: one 1024-element chunk per workgroup, GROUPS
+// groups of VEC = 4 consecutive elements (one 16-byte vector per array) per
+// thread: 256 threads with one group, 128 with two (launch_main picks).  Each
+// group is one load -> update -> store pass; waves exit right after their
+// last stores.
 //
 // A chunk inside one tensor (every chunk of a large tensor but its ends) is
 // one uniform segment.  A chunk shared by several tensors (small tensors
@@ -885,6 +884,78 @@ __device__ __forceinline__ void thread_elems(const adana_tensor_desc &d, const v
     }
 }
 
+// The GROUPS groups of one thread in a chunk that lies inside tensor d, group
+// k at element off + k * span, when every group is a whole aligned vector:
+// all groups' loads are issued before the first group's arithmetic, so a
+// wave's second group is in flight while it computes the first.  Returns
+// false (nothing done) otherwise; the caller then runs thread_elems per group,
+// each group's loads after the previous group's stores.  Only the compiled
+// bfloat16-state instances take it: they are bound by arithmetic and gain
+// from the overlap (Dana-Star at 2.65B params: 11.16 -> 10.78 ms), while the
+// float32 ones, bound by HBM, lose to the extra loads in flight (north-star
+// 15.02 -> 16.37 ms, C2 0.239 -> 0.266 ms; same-box A/B).
+template <bool STAR, bool GBF16, int PM, int POWK, bool EAGER, int VEC, int GROUPS>
+__device__ __forceinline__ bool thread_groups_uniform(const adana_tensor_desc &d, const void *grad, int64_t off,
+                                                      int64_t left, int64_t seg0, int span, const ScalarPack &pack,
+                                                      float gs, const PowTab &tab, float (&acc)[4]) {
+    static_assert(VEC == 4, "grouped path: 16-byte vectors");
+    if constexpr (PM != PM_BF16 || EAGER || GROUPS == 1) {
+        return false;
+    } else {
+        const bool vec_ok = (d.flags & ADANA_DESC_VEC_OK) && grad_vec_aligned<GBF16>(grad);
+        if (!vec_ok || left < static_cast<int64_t>(GROUPS - 1) * span + VEC) return false;
+        const adana_step_scalars &sc = pack.c[d.sclass];
+        float P[GROUPS][VEC], G[GROUPS][VEC], M[GROUPS][VEC], V[GROUPS][VEC], T[GROUPS][VEC];
+#pragma unroll
+        for (int k = 0; k < GROUPS; ++k) {
+            const int64_t o = off + static_cast<int64_t>(k) * span;
+            if constexpr (PM == PM_BF16) {
+                ld_bf16_n<VEC>(static_cast<unsigned short *>(d.param) + o, P[k]);
+                ld_bf16_n<VEC>(reinterpret_cast<unsigned short *>(d.m) + o, M[k]);
+                ld_bf16_n<VEC>(reinterpret_cast<unsigned short *>(d.v) + o, V[k]);
+                if constexpr (STAR) ld_bf16_n<VEC>(reinterpret_cast<unsigned short *>(d.tau) + o, T[k]);
+            } else {
+                ld_n<VEC>(static_cast<float *>(d.param) + o, P[k]);
+                ld_n<VEC>(d.m + o, M[k]);
+                ld_n<VEC>(d.v + o, V[k]);
+                if constexpr (STAR) ld_n<VEC>(d.tau + o, T[k]);
+            }
+            load_grad_n<GBF16, VEC>(grad, o, G[k]);
+            if constexpr (!STAR) {
+#pragma unroll
+                for (int e = 0; e < VEC; ++e) T[k][e] = 0.0f;
+            }
+        }
+        if (pack.gscale != nullptr) {
+#pragma unroll
+            for (int k = 0; k < GROUPS; ++k) {
+#pragma unroll
+                for (int e = 0; e < VEC; ++e) G[k][e] = scale_grad<GBF16>(G[k][e], gs);
+                if (pack.write_grad) store_grad_n<GBF16, VEC>(grad, off + static_cast<int64_t>(k) * span, G[k]);
+            }
+        }
+#pragma unroll
+        for (int k = 0; k < GROUPS; ++k) {
+            const int64_t o = off + static_cast<int64_t>(k) * span;
+            update_n<STAR, POWK, EAGER, VEC>(P[k], G[k], M[k], V[k], T[k], sc, tab, acc);
+            if constexpr (PM == PM_BF16) {
+                st_bf16_n<VEC>(static_cast<unsigned short *>(d.param) + o, P[k]);
+                st_bf16_n<VEC>(reinterpret_cast<unsigned short *>(d.m) + o, M[k]);
+                st_bf16_n<VEC>(reinterpret_cast<unsigned short *>(d.v) + o, V[k]);
+                if constexpr (STAR) st_bf16_n<VEC>(reinterpret_cast<unsigned short *>(d.tau) + o, T[k]);
+            } else {
+                const int byte_off = static_cast<int>((o - seg0) * 4);
+                st4_stream(static_cast<float *>(d.param) + seg0, byte_off, P[k]);
+                st4_stream(d.m + seg0, byte_off, M[k]);
+                st4_stream(d.v + seg0, byte_off, V[k]);
+                if constexpr (STAR) st4_stream(d.tau + seg0, byte_off, T[k]);
+                if constexpr (PM == PM_MASTER) st_bf16_n<VEC>(static_cast<unsigned short *>(d.param_lp) + o, P[k]);
+            }
+        }
+        return true;
+    }
+}
+
 // The workgroup's sums of acc, stored by thread 0 as one float4: a wave
 // reduction, then a fixed-order combine of the waves in LDS.  The LDS slot
 // alternates between calls (par), so no barrier is needed after thread 0 has
@@ -912,15 +983,17 @@ __device__ __forceinline__ void block_partial(float (&acc)[4], float (*red)[kW][
     par ^= 1;
 }
 
-template <bool STAR, bool GBF16, int PM, int POWK, bool EAGER, int VEC>
-__global__ __launch_bounds__(kChunk / VEC) void mta_step_kernel(const adana_tensor_desc *__restrict__ desc,
-                                                                const void *const *__restrict__ gradp,
-                                                                const int64_t *__restrict__ vstart,
-                                                                const int32_t *__restrict__ chunk_first,
-                                                                int32_t n, ScalarPack pack,
-                                                                float *__restrict__ partials,
-                                                                int32_t *__restrict__ counters) {
-    constexpr int kThreads = kChunk / VEC;
+template <bool STAR, bool GBF16, int PM, int POWK, bool EAGER, int VEC, int GROUPS>
+__global__ __launch_bounds__(kChunk / (VEC * GROUPS)) void mta_step_kernel(
+        const adana_tensor_desc *__restrict__ desc, const void *const *__restrict__ gradp,
+        const int64_t *__restrict__ vstart, const int32_t *__restrict__ chunk_first, int32_t n, ScalarPack pack,
+        float *__restrict__ partials, int32_t *__restrict__ counters) {
+    // GROUPS groups of VEC consecutive elements per thread, group k at element
+    // k * kSpan of the chunk: each group's loads and stores stay coalesced,
+    // and the per-chunk work (descriptor loads, table copy, reduction) is
+    // shared by GROUPS * VEC elements per thread.
+    constexpr int kThreads = kChunk / (VEC * GROUPS);
+    constexpr int kSpan = kThreads * VEC;
     constexpr int kW = kThreads / 64;
     __shared__ float red[2][kW][4];
     int par = 0;
@@ -928,7 +1001,7 @@ __global__ __launch_bounds__(kChunk / VEC) void mta_step_kernel(const adana_tens
     const int64_t chunk = blockIdx.x;
     const int64_t lo = chunk * kChunk;
     const int64_t hi = lo + kChunk;
-    const int64_t mine = lo + VEC * tid;   // virtual index of this thread's VEC elements
+    const int64_t mine = lo + VEC * tid;   // virtual index of this thread's first group
     float4 *part4 = reinterpret_cast<float4 *>(partials);
     // the combine kernel's per-tensor arrival counters start at zero
     for (int64_t k = chunk * kThreads + tid; k < n; k += static_cast<int64_t>(gridDim.x) * kThreads) counters[k] = 0;
@@ -941,23 +1014,28 @@ __global__ __launch_bounds__(kChunk / VEC) void mta_step_kernel(const adana_tens
     const float gs = pack.gscale != nullptr ? *pack.gscale : 1.0f;
     PowTab tab{adana::kLog, adana::kExp2J, pack.pow16};
     // Dana-Star's binary64 pow reads its tables from LDS.  The 3 KB are 192
-    // 16-byte words (kLog, then kExp2J), one per thread of the first 192; the
-    // loads are issued here and the words written to LDS only after the
-    // chunk's descriptor loads below are issued, so the two round trips
-    // overlap.  (Writing them after the streaming loads instead, with the
-    // barrier between those loads and the arithmetic, cost the 10,000-tensor
-    // list 8%.)
+    // 16-byte words (kLog, then kExp2J), kTabPer per thread; the loads are
+    // issued here and the words written to LDS only after the chunk's
+    // descriptor loads below are issued, so the two round trips overlap.
+    // (Writing them after the streaming loads instead, with the barrier
+    // between those loads and the arithmetic, cost the 10,000-tensor list 8%.)
     constexpr bool kTab = STAR && pow_tables(POWK);
     constexpr int kTabWords = 192;
-    static_assert(!kTab || kThreads >= kTabWords, "one thread per table word");
+    constexpr int kTabPer = (kTabWords + kThreads - 1) / kThreads;
     static_assert(sizeof(adana::kLog) == 128 * 16 && sizeof(adana::kExp2J) == 64 * 16, "table layout");
+    static_assert(kTabPer <= 2, "at most two table words per thread");
     __shared__ uint4 s_tab[kTab ? kTabWords : 1];
-    uint4 tab_word{};
+    // two named words, not an array: a private array here is placed in LDS
+    uint4 tab_w0{}, tab_w1{};
+    auto table_word = [](int w) {
+        return w < 128 ? reinterpret_cast<const uint4 *>(adana::kLog)[w]
+                       : reinterpret_cast<const uint4 *>(adana::kExp2J)[w - 128];
+    };
     if constexpr (kTab) {
-        if (tid < 128)
-            tab_word = reinterpret_cast<const uint4 *>(adana::kLog)[tid];
-        else if (tid < kTabWords)
-            tab_word = reinterpret_cast<const uint4 *>(adana::kExp2J)[tid - 128];
+        if (tid < kTabWords) tab_w0 = table_word(tid);
+        if constexpr (kTabPer > 1) {
+            if (tid + kThreads < kTabWords) tab_w1 = table_word(tid + kThreads);
+        }
         tab = PowTab{reinterpret_cast<const adana::LogPair *>(s_tab), reinterpret_cast<const double *>(s_tab + 128),
                      nullptr};
     }
@@ -966,35 +1044,52 @@ __global__ __launch_bounds__(kChunk / VEC) void mta_step_kernel(const adana_tens
     const int64_t vs0 = vstart[i0];
     const adana_tensor_desc d0 = desc[i0];
     const void *g0 = gradp[i0];
-    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
     // both bounds at once (no short circuit), so that the descriptor's numel
     // is fetched with the rest of it rather than after a branch
     const bool inside = (vs0 <= lo) & (vs0 + d0.numel >= hi);
     if constexpr (kTab) {
-        if (tid < kTabWords) s_tab[tid] = tab_word;
+        if (tid < kTabWords) s_tab[tid] = tab_w0;
+        if constexpr (kTabPer > 1) {
+            if (tid + kThreads < kTabWords) s_tab[tid + kThreads] = tab_w1;
+        }
         __syncthreads();
     }
     if (inside) {
         // the whole chunk lies in tensor i0
-        thread_elems<STAR, GBF16, PM, POWK, EAGER, VEC, true>(d0, g0, mine - vs0, vs0 + d0.numel - mine, lo - vs0,
-                                                                 pack, gs, tab, acc);
+        float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        if (!thread_groups_uniform<STAR, GBF16, PM, POWK, EAGER, VEC, GROUPS>(
+                d0, g0, mine - vs0, vs0 + d0.numel - mine, lo - vs0, kSpan, pack, gs, tab, acc)) {
+#pragma unroll
+            for (int k = 0; k < GROUPS; ++k) {
+                const int64_t m = mine + k * kSpan;
+                thread_elems<STAR, GBF16, PM, POWK, EAGER, VEC, true>(d0, g0, m - vs0, vs0 + d0.numel - m, lo - vs0,
+                                                                         pack, gs, tab, acc);
+            }
+        }
         block_partial<kW>(acc, red, par, part4 + chunk + i0);
         return;
     }
     // Shared chunk: its tensors are i0 .. i1 (chunk_first of the next chunk is
     // the first tensor reaching it, which may also reach into this one).
     const int i1 = (chunk + 1 < static_cast<int64_t>(gridDim.x)) ? chunk_first[chunk + 1] : n - 1;
-    int l = i0, r = i1;                      // this thread's tensor: the last i with vstart[i] <= mine
-    while (l < r) {
-        const int mid = (l + r + 1) >> 1;
-        if (vstart[mid] <= mine) l = mid; else r = mid - 1;
-    }
-    {
+    int own[GROUPS];
+    float acc[GROUPS][4];
+#pragma unroll
+    for (int k = 0; k < GROUPS; ++k) {
+        const int64_t m = mine + k * kSpan;
+        int l = i0, r = i1;                  // this group's tensor: the last i with vstart[i] <= m
+        while (l < r) {
+            const int mid = (l + r + 1) >> 1;
+            if (vstart[mid] <= m) l = mid; else r = mid - 1;
+        }
+        own[k] = l;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) acc[k][c] = 0.0f;
         const adana_tensor_desc d = desc[l];
         const int64_t vs = vstart[l];
-        if (mine >= vs && mine < vs + d.numel)
-            thread_elems<STAR, GBF16, PM, POWK, EAGER, VEC, false>(d, gradp[l], mine - vs, vs + d.numel - mine, 0,
-                                                                      pack, gs, tab, acc);
+        if (m >= vs && m < vs + d.numel)
+            thread_elems<STAR, GBF16, PM, POWK, EAGER, VEC, false>(d, gradp[l], m - vs, vs + d.numel - m, 0, pack,
+                                                                      gs, tab, acc[k]);
     }
     // one (chunk, tensor) partial per tensor overlapping the chunk, in order
     for (int j = i0; j <= i1; ++j) {
@@ -1003,7 +1098,12 @@ __global__ __launch_bounds__(kChunk / VEC) void mta_step_kernel(const adana_tens
         if (vs + desc[j].numel <= lo) continue;                    // uniform across the block
         float a[4];
 #pragma unroll
-        for (int k = 0; k < 4; ++k) a[k] = (l == j) ? acc[k] : 0.0f;
+        for (int c = 0; c < 4; ++c) a[c] = (own[0] == j) ? acc[0][c] : 0.0f;
+#pragma unroll
+        for (int k = 1; k < GROUPS; ++k) {
+#pragma unroll
+            for (int c = 0; c < 4; ++c) a[c] += (own[k] == j) ? acc[k][c] : 0.0f;
+        }
         block_partial<kW>(a, red, par, part4 + chunk + j);
     }
 }
@@ -1484,37 +1584,50 @@ constexpr int residency_cap(bool small_tensors) {
     return 4;
 }
 
-// Upper bound on the kernel's static LDS (the reduction slots and, for the
-// pow instances, the 3 KB table copy), reserved beside the cap's dynamic LDS.
-constexpr size_t kStaticLdsReserve = 4096;
-
-// Dynamic LDS bytes that leave room for exactly `wgs` workgroups per CU on
-// the current device (0: no cap, or the device's LDS size is unavailable).
-// Grids of fewer than 64 chunks per CU stay uncapped: there the cap only adds
-// dispatch rounds.
-size_t lds_for_cap(int wgs, int64_t n_chunks) {
-    if (wgs <= 0) return 0;
-    static int lds_per_cu[64];
-    static int lds_per_block[64];
-    static int cus[64];
+// Dynamic LDS bytes that, beside the kernel's `static_lds` bytes, leave room
+// for exactly `wgs` workgroups per CU on the current device (0: no cap, or
+// the device's LDS size is unavailable): each workgroup then holds 256 bytes
+// less than a 1/wgs share, so `wgs` fit and `wgs + 1` do not.  Grids of fewer
+// than 64 chunks per CU stay uncapped: there the cap only adds dispatch
+// rounds.
+struct DeviceLds {
+    int per_cu = 0, per_block = 0, cus = 0;
+};
+// The current device's LDS sizes and CU count (zeros if unavailable), read once per device.
+DeviceLds device_lds() {
+    static DeviceLds cache[64];
     int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
-    if (lds_per_cu[dev] <= 0) {
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return DeviceLds{};
+    DeviceLds &c = cache[dev];
+    if (c.per_cu <= 0) {
         int cu = 0, blk = 0, n_cu = 0;
         if (hipDeviceGetAttribute(&cu, hipDeviceAttributeMaxSharedMemoryPerMultiprocessor, dev) != hipSuccess ||
             hipDeviceGetAttribute(&blk, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess ||
             hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
-            return 0;
-        lds_per_block[dev] = blk;
-        cus[dev] = n_cu;
-        lds_per_cu[dev] = cu;
+            return DeviceLds{};
+        c.per_block = blk;
+        c.cus = n_cu;
+        c.per_cu = cu;
     }
-    if (n_chunks < 64 * static_cast<int64_t>(cus[dev])) return 0;
-    // wgs * L <= lds < (wgs + 1) * L, with room left for the kernel's static LDS
-    const size_t per_cu = static_cast<size_t>(lds_per_cu[dev]);
+    return c;
+}
+
+// Whether a grid of n_chunks workgroups holds at least `per_cu` of them per CU.
+bool grid_fills(int64_t n_chunks, int per_cu) {
+    const DeviceLds d = device_lds();
+    return d.cus > 0 && n_chunks >= static_cast<int64_t>(per_cu) * d.cus;
+}
+
+size_t lds_for_cap(int wgs, int64_t n_chunks, size_t static_lds) {
+    if (wgs <= 0) return 0;
+    const DeviceLds d = device_lds();
+    if (d.per_cu <= 0 || !grid_fills(n_chunks, 64)) return 0;
+    const size_t per_cu = static_cast<size_t>(d.per_cu);
     if (per_cu < 32 * 1024) return 0;
-    const size_t l = per_cu / static_cast<size_t>(wgs) - kStaticLdsReserve;
-    return l <= static_cast<size_t>(lds_per_block[dev]) ? l : 0;
+    const size_t share = per_cu / static_cast<size_t>(wgs);
+    if (share <= static_lds + 256 || share <= 256 * static_cast<size_t>(wgs + 1)) return 0;
+    const size_t l = share - 256 - static_lds;
+    return l <= static_cast<size_t>(d.per_block) ? l : 0;
 }
 
 // The launch's device arrays and workspace pointers.
@@ -1530,14 +1643,35 @@ struct LaunchArgs {
     int32_t *counters;
 };
 
+template <bool STAR, bool GBF16, int PM, int POWK, bool EAGER, int GROUPS>
+void launch_groups(const LaunchArgs &a, const ScalarPack &pack, bool small_tensors) {
+    constexpr int kVec = 4;
+    constexpr int kThreads = kChunk / (kVec * GROUPS);
+    // the cap counts 256-thread workgroups' worth of waves per CU
+    const int cap = residency_cap<STAR, PM, POWK>(small_tensors) * (256 / kThreads);
+    // the kernel's static LDS: its reduction slots and, for the pow instances, the tables' copy
+    constexpr size_t kStaticLds = 2 * (kThreads / 64) * 4 * sizeof(float) +
+                                  ((STAR && pow_tables(POWK)) ? 192 * 16 : 16);
+    const size_t lds = lds_for_cap(cap, a.n_chunks, kStaticLds);
+    hipLaunchKernelGGL((mta_step_kernel<STAR, GBF16, PM, POWK, EAGER, kVec, GROUPS>),
+                       dim3(static_cast<unsigned>(a.n_chunks)), dim3(kThreads), static_cast<unsigned>(lds), a.st,
+                       a.desc, a.grad, a.vstart, a.chunk_first, a.n, pack, a.partials, a.counters);
+}
+
+// Two groups of four elements per thread (128-thread workgroups, the chunk's
+// fixed work shared by eight elements) on grids of at least 64 chunks per
+// CU; one group (256 threads) on smaller grids, which need the threads, and
+// on the pow instance over lists of small tensors, where the two are even.
+// Same-box A/B, one group -> two: north-star 15.57 -> 15.02 ms, C3 7.80 ->
+// 7.55, C4 11.93 -> 11.59, C2 0.246 -> 0.239, bfloat16-state north-star 11.45
+// -> 10.78 (with the loads first); C1 (4,096 chunks) 0.0259 -> 0.0278 and
+// C5 0.591 -> 0.597 stay on one group.
 template <bool STAR, bool GBF16, int PM, int POWK, bool EAGER>
 void launch_main(const LaunchArgs &a, const ScalarPack &pack) {
-    constexpr int kVec = 4;
     const bool small_tensors = a.n_chunks < 64 * static_cast<int64_t>(a.n);
-    const size_t lds = lds_for_cap(residency_cap<STAR, PM, POWK>(small_tensors), a.n_chunks);
-    hipLaunchKernelGGL((mta_step_kernel<STAR, GBF16, PM, POWK, EAGER, kVec>), dim3(static_cast<unsigned>(a.n_chunks)),
-                       dim3(kChunk / kVec), static_cast<unsigned>(lds), a.st, a.desc, a.grad, a.vstart,
-                       a.chunk_first, a.n, pack, a.partials, a.counters);
+    const bool two = grid_fills(a.n_chunks, 64) && !(STAR && pow_tables(POWK) && small_tensors);
+    if (two) launch_groups<STAR, GBF16, PM, POWK, EAGER, 2>(a, pack, small_tensors);
+    else launch_groups<STAR, GBF16, PM, POWK, EAGER, 1>(a, pack, small_tensors);
 }
 
 template <bool STAR, bool GBF16, int PM, bool EAGER>
