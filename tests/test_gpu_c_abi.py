@@ -171,3 +171,38 @@ def test_bf16_state_classes_through_the_c_abi(oracle_mod, kappas, numerics):
             bad = int(np.count_nonzero(d))
             assert bad <= STAR_HARD_CASES and (bad == 0 or d.max() <= 1), (t, i, bad, d.max())
             cpu["p"][i][...] = got
+
+
+def test_integration_example_runs(oracle_mod):
+    """The ctypes example of INTEGRATION.md section 2 runs as written against the built
+    library (ABI 7 plan with its gradient pointer array) and steps its tensor: the
+    diagnostics are finite and match the oracle's over the same ten steps."""
+    import contextlib
+    import io
+    import os
+    import re
+
+    O = oracle_mod
+    print("case: INTEGRATION.md ctypes example", flush=True)
+    text = open(os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "INTEGRATION.md")).read()
+    section = text[text.index("## 2. C ABI"):]
+    code = re.search(r"```python\n(.*?)```", section, re.S).group(1)
+    ns = {}
+    torch.manual_seed(0)
+    with contextlib.redirect_stdout(io.StringIO()):
+        exec(compile(code, "INTEGRATION.md", "exec"), ns)
+    torch.cuda.synchronize()
+    diag = ns["diag"].cpu().numpy()
+    assert np.isfinite(diag).all(), diag
+    # the same ten steps on the oracle, from the example's own inputs
+    assert ns["p"].shape == (1 << 20,)
+    g = ns["g"].cpu().numpy()
+    torch.manual_seed(0)
+    p0 = torch.randn(1 << 20, device="cuda").cpu().numpy()
+    orc = O.OracleOptimizer(groups=[O.OracleGroup(params=[p0], lr=1e-3, weight_decay=0.4)], star=True, peak_lr=1e-3,
+                            kappa=0.85, clipsnr=2.0, wd_decaying=True, wd_ts=10.0)
+    for _ in range(10):
+        orc.step([[g]])
+    ost = orc.state[id(p0)]
+    np.testing.assert_allclose(diag, [ost[k] for k in O.DIAG_KEYS], rtol=1e-5)
+    np.testing.assert_array_equal(ns["m"].cpu().numpy(), ost["m"])
