@@ -1659,17 +1659,24 @@ void launch_groups(const LaunchArgs &a, const ScalarPack &pack, bool small_tenso
 }
 
 // Two groups of four elements per thread (128-thread workgroups, the chunk's
-// fixed work shared by eight elements) on grids of at least 64 chunks per
-// CU; one group (256 threads) on smaller grids, which need the threads, and
-// on the pow instance over lists of small tensors, where the two are even.
-// Same-box A/B, one group -> two: north-star 15.57 -> 15.02 ms, C3 7.80 ->
-// 7.55, C4 11.93 -> 11.59, C2 0.246 -> 0.239, bfloat16-state north-star 11.45
-// -> 10.78 (with the loads first); C1 (4,096 chunks) 0.0259 -> 0.0278 and
-// C5 0.591 -> 0.597 stay on one group.
+// fixed work shared by eight elements) where that is a steady gain:
+//  * bfloat16 state, bound by arithmetic: north-star list 11.45 -> 10.78 ms
+//    (with the loads first), every box and run;
+//  * grids of 64 chunks per CU up to kTwoGroupMaxChunks: C2 0.246 -> 0.239 ms.
+// One group (256 threads) elsewhere: on smaller grids, which need the threads
+// (C1, 4,096 chunks: 0.0259 -> 0.0278 ms with two); on the pow instance over
+// lists of small tensors (C5 0.591 -> 0.597); and on large float32 lists,
+// where two groups swing with the box's state: 2-3.5% faster on a settled
+// box (north-star 15.57 -> 15.02, C3 7.80 -> 7.55, C4 11.93 -> 11.59 ms),
+// 2-6% slower in its first minutes (north-star 15.54 -> 16.26 ms, in one
+// process on the same tensors; on that box 15.22 -> 14.99 ms ten minutes
+// later), while one group stays within 15.2-15.9 ms throughout.
+constexpr int64_t kTwoGroupMaxChunks = 1 << 18;
 template <bool STAR, bool GBF16, int PM, int POWK, bool EAGER>
 void launch_main(const LaunchArgs &a, const ScalarPack &pack) {
     const bool small_tensors = a.n_chunks < 64 * static_cast<int64_t>(a.n);
-    const bool two = grid_fills(a.n_chunks, 64) && !(STAR && pow_tables(POWK) && small_tensors);
+    const bool two = grid_fills(a.n_chunks, 64) && !(STAR && pow_tables(POWK) && small_tensors) &&
+                     (PM == PM_BF16 || a.n_chunks <= kTwoGroupMaxChunks);
     if (two) launch_groups<STAR, GBF16, PM, POWK, EAGER, 2>(a, pack, small_tensors);
     else launch_groups<STAR, GBF16, PM, POWK, EAGER, 1>(a, pack, small_tensors);
 }
