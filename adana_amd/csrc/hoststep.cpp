@@ -589,6 +589,7 @@ struct TableData {
     std::vector<uint64_t> last;                          // gradient pointers of the last accepted scan
     std::vector<uint64_t> tmp;                           // this scan's pointers until it is accepted
     std::vector<PyObject *> saved;                       // a scan's old step counts until it is accepted
+    bool busy = false;                                   // a scan of this table is running
     std::vector<PyObject *> diag;                        // bound diagnostics, ncols per row (strong)
     std::vector<std::pair<long, PyObject *>> cols;       // (kernel output column, state key), keys strong
     c10::ScalarType want = c10::ScalarType::Float;
@@ -756,6 +757,7 @@ struct ScanPool {
     std::atomic<int> decision{0};         // 0 pending, 1 bump the versions, 2 stop
 };
 ScanPool *g_pool = nullptr;
+bool g_pool_busy = false;   // a scan is using the helpers (the GIL guards this flag)
 int g_helpers = 3;
 
 inline void cpu_relax() { __builtin_ia32_pause(); }
@@ -881,9 +883,22 @@ PyObject *table_scan(PyObject *self, PyObject *arg) {
         int parts = 0;
         if (n >= kParallelRows && g_helpers > 0)
             parts = static_cast<int>(std::min<size_t>(static_cast<size_t>(g_helpers), n / kMinRowsPerHelper));
-        ScanPool *pool = parts >= 2 ? scan_pool(parts) : nullptr;
+        // Python code run by a step counter that is not an int (its __add__) may
+        // re-enter: a scan of this table then takes the general path, and a scan
+        // of another table keeps off the helpers while they serve this one.
+        if (d.busy) Py_RETURN_NONE;
+        ScanPool *pool = (parts >= 2 && !g_pool_busy) ? scan_pool(parts) : nullptr;
         if (pool) parts = std::min(parts, pool->started);
-        if (pool && parts >= 2) {
+        struct Busy {          // set for the scan, cleared on every way out
+            bool &table, *pool;
+            ~Busy() {
+                table = false;
+                if (pool) *pool = false;
+            }
+        } busy{d.busy, (pool && parts >= 2) ? &g_pool_busy : nullptr};
+        d.busy = true;
+        if (busy.pool) {
+            g_pool_busy = true;
             const int rc = scan_parallel(d, *pool, parts, &lo, &hi);
             if (rc < 0) return nullptr;
             if (rc == 0) Py_RETURN_NONE;
@@ -892,6 +907,7 @@ PyObject *table_scan(PyObject *self, PyObject *arg) {
             if (advance_states_impl(n, [&d](size_t i) { return d.states[i]; }, d.saved)) return nullptr;
             bump_rows(d, 0, n);
         }
+
         for (PyObject *o : d.saved) Py_DECREF(o);
         d.saved.clear();
         for (size_t i = 0; i < n; ++i) out[i] = d.tmp[i];

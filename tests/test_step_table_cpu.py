@@ -179,3 +179,29 @@ def test_scan_after_fork():
         assert q.get(timeout=5) == ((0, N), True)
     finally:
         _hoststep.scan_threads(before)
+
+
+def test_scan_reentered_from_a_step_counter(threads):
+    """A step counter whose ``+ 1`` runs Python code that scans again: the same
+    table declines (None, the caller's general path), another table scans on
+    the calling thread (the helpers are serving the outer scan), and the
+    outer scan completes."""
+    params, states = _rows(N)
+    other_params, other_states = _rows(3000, seed=9)
+    table = _hoststep.step_table(params, states, [], False)
+    other = _hoststep.step_table(other_params, other_states, [], False)
+    seen = []
+
+    class Count(int):
+        def __add__(self, k):
+            seen.append(table.scan(np.zeros(N, np.uint64).ctypes.data))
+            seen.append(other.scan(np.zeros(3000, np.uint64).ctypes.data))
+            return Count(int(self) + k)
+
+    states[N // 2]["step"] = Count(7)
+    out = np.zeros(N, np.uint64)
+    assert _scan(table, out) == (0, N)
+    assert seen == [None, (0, 3000)]
+    assert states[N // 2]["step"] == 8 and type(states[N // 2]["step"]) is Count
+    assert all(st["step"] == 8 for st in states) and all(st["step"] == 8 for st in other_states)
+    assert _scan(table, out) == (0, 0)                # and the table scans again afterwards
