@@ -4,7 +4,8 @@ grids of at least 64 chunks per CU: lists of 16,384 chunks and more on a
 256-CU MI355X, up to 2^18 chunks for float32 state, any size for bfloat16
 state), against the oracle on every element: float32 and bf16-master lists of
 ~20M elements in both numerics, and the reference's bfloat16 state, whose
-compiled instance issues both groups' loads first.  Same bars as
+compiled instance issues both groups' loads first (one of its tensors a view
+2 bytes into a buffer, so that its groups take the element-wise path).  Same bars as
 tests/test_gpu_parity.py and tests/test_gpu_bf16.py."""
 import numpy as np
 import pytest
@@ -61,7 +62,15 @@ def test_two_group_grid_bf16_state(oracle_mod, star, numerics):
     print(f"case: two-group grid bf16 state star {star} {numerics} sizes {SIZES}", flush=True)
     rng = np.random.default_rng(32)
     host = [O.f32_to_bf16(rng.normal(0, 0.02, n).astype(np.float32)) for n in SIZES]
-    gpu = [torch.nn.Parameter(_to_gpu16(h)) for h in host]
+    gpu = []
+    flat = torch.empty(SIZES[1] + 1, dtype=torch.bfloat16, device=DEV)
+    for i, h in enumerate(host):
+        if i == 1:                              # 2 bytes in: not 8-byte aligned, the element-wise path
+            v = flat[1:]
+            v.copy_(_to_gpu16(h))
+            gpu.append(torch.nn.Parameter(v))
+        else:
+            gpu.append(torch.nn.Parameter(_to_gpu16(h)))
     cls = adana_amd.DANA_STAR_MK4 if star else adana_amd.ADana
     opt = cls(gpu, numerics=numerics, **HP)
     orc = O.OracleOptimizer(groups=[O.OracleGroup(params=host, lr=HP["lr"], weight_decay=HP["weight_decay"])],
