@@ -22,8 +22,9 @@ per step, host work included).  ``roofline.achieved`` uses the device time of
 the step's kernels, measured with HIP events recorded on the stream they are
 launched on.  ``cpu_baseline`` times the reference's step restated as torch eager ops over
 CPU tensors (oracle/torch_ref.py, the reference's per-tensor loop) on the
-host's cores on a bounded sample of the same workload, with the C oracle
-(OpenMP) beside it.
+host's cores on a bounded sample of the same workload, with the same update
+under torch.compile (the reference's default, Inductor's C++ code) and the C
+oracle (OpenMP) beside it.
 """
 from __future__ import annotations
 
@@ -233,14 +234,17 @@ def cpu_threads() -> int:
 def cpu_baseline(w, target_s=10.0, max_elems=1 << 25):
     """The reference's CPU step, timed on the host's cores on a bounded sample
     of the workload (its first tensors, up to max_elems elements): the step
-    restated as torch eager ops over CPU tensors with the reference's
-    per-tensor loop (oracle/torch_ref.py: src/optim/adana.py:162-225,
+    restated as torch ops over CPU tensors with the reference's per-tensor
+    loop (oracle/torch_ref.py: src/optim/adana.py:162-225,
     src/optim/dana_star_mk4.py:215-294; bit-identical to the reference's own
     eager run, tests/test_torch_restatement.py), torch.set_num_threads over
-    the cores.  Beside it, the C oracle (oracle/adana_oracle.c, OpenMP) on the
-    same sample.  bf16-master workloads time the float32 master update; the
-    bf16-state workload (the reference's own bfloat16 path) runs both on
-    bfloat16 tensors."""
+    the cores, timed twice: as eager ops, and with the update under
+    torch.compile as the reference runs it by default (compiled_leg).
+    ``value`` is the compiled rate, or the eager one where the compiled leg
+    is not timed.  Beside them, the C oracle (oracle/adana_oracle.c, OpenMP)
+    on the same sample.  bf16-master workloads time the float32 master
+    update; the bf16-state workload (the reference's own bfloat16 path) runs
+    all three on bfloat16 tensors."""
     import torch
 
     from oracle import oracle as O
@@ -277,8 +281,10 @@ def cpu_baseline(w, target_s=10.0, max_elems=1 << 25):
                             star=w["star"], peak_lr=hp["lr"], kappa=hp["kappa"], clipsnr=hp["clipsnr"],
                             wd_decaying=hp["wd_decaying"], wd_ts=hp["wd_ts"])
     per_t, reps_t = timed(lambda: ref.step(tg))
+    del tp, ref
+    compiled = compiled_leg(w, ps, tg, total, bpe, timed, cores)
     torch.set_num_threads(prev)
-    del tp, tg, ref
+    del tg
 
     threads = O.set_threads(cores)
     cps = [O.f32_to_bf16(x) for x in ps] if s16 else [x.copy() for x in ps]
@@ -290,16 +296,73 @@ def cpu_baseline(w, target_s=10.0, max_elems=1 << 25):
     per_c, reps_c = timed(lambda: opt.step([cgs]))
     sample = (f"{total} of the workload's {all_elems} elements ({100 * frac:.2f}%): its first {len(sizes)} tensors, "
               f"{'bf16 parameters and state' if s16 else 'fp32'}")
-    return {"value": round(total * bpe / per_t / 1e9, 3), "unit": "GB/s", "cores": cores, "kind": "port",
+    eager = {"value": round(total * bpe / per_t / 1e9, 3), "unit": "GB/s", "cores": cores,
+             "ms_per_step_sample": round(per_t * 1e3, 3),
+             "sample": f"same sample, oracle/torch_ref.py (the reference's step() as torch eager ops, per-tensor "
+                       f"loop) with torch.set_num_threads({cores}); {reps_t} timed steps after 1 warm-up"}
+    c_oracle = {"value": round(total * bpe / per_c / 1e9, 3), "unit": "GB/s", "cores": threads,
+                "ms_per_step_sample": round(per_c * 1e3, 3),
+                "sample": f"same sample, oracle/adana_oracle.c with {threads} OpenMP threads, {reps_c} timed steps"}
+    head = compiled if compiled.get("value") is not None else eager
+    path = "compiled" if head is compiled else "eager"
+    how = ("the reference's update under torch.compile (its default path), one wrapper per shape" if head is compiled
+           else f"the reference's step() as torch eager ops ({compiled['reason']})")
+    return {"value": head["value"], "unit": "GB/s", "cores": cores, "kind": "port", "path": path,
             "cpu_model": cpu_model(),
-            "sample": f"{sample}; oracle/torch_ref.py (the reference's step() as torch eager ops, per-tensor "
-                      f"loop) with torch.set_num_threads({cores}) (the process's CPU affinity, capped by "
-                      f"OMP_NUM_THREADS); {reps_t} timed steps after 1 warm-up, {per_t * 1e3:.1f} ms/step",
-            "sample_fraction": round(frac, 5), "ms_per_step_sample": round(per_t * 1e3, 3),
-            "c_oracle": {"value": round(total * bpe / per_c / 1e9, 3), "unit": "GB/s", "cores": threads,
-                         "ms_per_step_sample": round(per_c * 1e3, 3),
-                         "sample": f"same sample, oracle/adana_oracle.c with {threads} OpenMP threads, "
-                                   f"{reps_c} timed steps"}}
+            "sample": f"{sample}; {how}, oracle/torch_ref.py's per-tensor loop, torch.set_num_threads({cores}) "
+                      f"(the process's CPU affinity, capped by OMP_NUM_THREADS); "
+                      f"{head['ms_per_step_sample']:.1f} ms/step",
+            "sample_fraction": round(frac, 5), "ms_per_step_sample": head["ms_per_step_sample"],
+            "compiled": compiled, "eager": eager, "c_oracle": c_oracle}
+
+
+def compiled_leg(w, ps, tg, total, bpe, timed, cores, max_shapes=8):
+    """The reference's default CPU path on the same sample: the per-tensor
+    update compiled by torch.compile(dynamic=False, fullgraph=False) with one
+    wrapper per tensor shape (src/optim/adana.py:72-79,
+    src/optim/dana_star_mk4.py:88-96), Inductor's C++ code on the host's
+    cores.  Compilation happens in the warm-up step and is reported apart.
+    Samples with more than ``max_shapes`` distinct shapes are not timed:
+    every wrapper recompiles the same function, and past torch._dynamo's
+    recompile limit (8) the reference's loop runs the eager ops, which the
+    eager leg already times."""
+    import torch
+
+    from oracle.torch_ref import TorchRefGroup, TorchRefOptimizer, update
+
+    shapes = sorted({x.shape for x in ps})
+    if len(shapes) > max_shapes:
+        return {"value": None, "reason": f"{len(shapes)} distinct shapes in the sample: past torch._dynamo's "
+                                         f"recompile limit the reference's loop runs its eager ops"}
+    hp = w["hp"]
+    tdt = tg[0][0].dtype
+    print(f"[bench] compiling the reference's update with torch.compile for {len(shapes)} shapes",
+          file=sys.stderr, flush=True)
+    try:
+        wrappers = {}
+
+        def update_fn(p):
+            fn = wrappers.get(p.shape)
+            if fn is None:
+                fn = wrappers[p.shape] = torch.compile(update, dynamic=False, fullgraph=False)
+            return fn
+
+        tp = [torch.from_numpy(x.copy()).to(tdt) for x in ps]
+        ref = TorchRefOptimizer(groups=[TorchRefGroup(params=tp, lr=hp["lr"], delta=hp["delta"],
+                                                      epsilon=hp["epsilon"], weight_decay=hp["weight_decay"])],
+                                star=w["star"], peak_lr=hp["lr"], kappa=hp["kappa"], clipsnr=hp["clipsnr"],
+                                wd_decaying=hp["wd_decaying"], wd_ts=hp["wd_ts"])
+        t0 = time.perf_counter()
+        ref.step(tg, update_fn=update_fn)                  # compiles every shape
+        compile_s = time.perf_counter() - t0
+        per, reps = timed(lambda: ref.step(tg, update_fn=update_fn))
+    except Exception as e:                                 # no host compiler, Inductor error
+        return {"value": None, "reason": f"torch.compile failed: {type(e).__name__}: {str(e)[:200]}"}
+    return {"value": round(total * bpe / per / 1e9, 3), "unit": "GB/s", "cores": cores,
+            "ms_per_step_sample": round(per * 1e3, 3), "compile_s": round(compile_s, 1),
+            "sample": f"same sample, oracle/torch_ref.py's update under torch.compile(dynamic=False, "
+                      f"fullgraph=False), one wrapper per shape (Inductor C++ on {cores} threads); "
+                      f"{reps} timed steps after the compiling step"}
 
 
 def copy_probe(steps):

@@ -182,9 +182,13 @@ class TorchRefOptimizer:
 
     @torch.no_grad()
     def step(self, grads: Sequence[Sequence[Optional[torch.Tensor]]], sqrt=torch.sqrt, epow=None,
-             slip: Optional[str] = None, compiled=None) -> None:
+             slip: Optional[str] = None, compiled=None, update_fn=None) -> None:
         """One step of the reference's loop.  ``compiled``: None for the eager
-        ops (``update``), or (sqrt, epow, powf) for ``update_compiled``."""
+        ops (``update``), or (sqrt, epow, powf) for ``update_compiled``.
+        ``update_fn(p)``, when given, returns the callable that replaces
+        ``update`` for tensor p (bench.py passes ``update`` wrapped in
+        torch.compile, one wrapper per shape, as src/optim/adana.py:72-79
+        and src/optim/dana_star_mk4.py:88-96 do)."""
         f32 = dict(dtype=torch.float32)
         for gi, group in enumerate(self.groups):
             lr = group.lr
@@ -206,7 +210,9 @@ class TorchRefOptimizer:
                 sc = (torch.tensor(t, **f32), torch.tensor(group.delta / (group.delta + t), **f32),
                       torch.tensor(lr, **f32), torch.tensor(lr, **f32), torch.tensor(sf, **f32),
                       torch.tensor(group.weight_decay, **f32))                       # :199-208
-                if compiled is None:
+                if update_fn is not None:
+                    ca, gn, afm, mn = update_fn(p)(self.star, p, g, st["m"], st["v"], st.get("tau"), sc, hp)
+                elif compiled is None:
                     ca, gn, afm, mn = update(self.star, p, g, st["m"], st["v"], st.get("tau"), sc, hp,
                                              sqrt=sqrt, epow=epow, slip=slip)
                 else:
