@@ -154,6 +154,103 @@ def update_compiled(star: bool, p, g, m, v, tau, sc, hp: dict, sqrt, epow, powf)
     return (af.mean().to(dt), G.norm().to(dt), mfac.mean().to(dt), M1.norm().to(dt))   # :146-151
 
 
+def update_foreach(star: bool, p, g, m, v, tau, sc, hp: dict, sqrt, epow, powf, compiled: bool = True):
+    """One tensor's share of the reference's foreach path
+    (``_foreach_compute_kernel_impl``, src/optim/adana.py:310-370 and
+    src/optim/dana_star_mk4.py:395-536), one op per ``torch._foreach_*`` op in
+    that order: p, m, v[, tau] updated in place; returns the diagnostics as
+    ``update`` does, computed as the reference's ``_foreach_step_group`` does
+    after the kernel (.mean() / .norm() of the returned alpha factor and mfac
+    and of grad and m, adana.py:280-285).
+
+    ``sc`` = (step_t, alpha_t, g2, g3, schedule_factor, wd): step_t in p's
+    dtype and alpha_t = delta / (delta + step_t) as 0-d tensors
+    (adana.py:258-262), the rest binary32 0-d tensors.
+
+    ``compiled`` False: the kernel's eager ops, literally, on the tensors'
+    own dtype (ATen's lerp, sqrt and pow; bfloat16 tensors round every op).
+    ``compiled`` True: the constructor's torch.compile of the kernel; every
+    value in binary32 (bfloat16 tensors read as binary32 and rounded where
+    they are stored), ``sqrt``, ``epow`` (Dana-Star's element-wise power) and
+    ``powf`` (ADana's 0-d power of Python floats) as for update_compiled.
+    Either way the foreach path has no addcmul, and its lerps are ATen's
+    kernel on the tensors' own dtype: Inductor keeps a foreach lerp with a
+    list of weight tensors as that kernel, so under torch.compile too m and
+    tau come out of it rounded to their dtype, and tau's lerp reads the tau
+    update stored in tau's dtype (the reference's bfloat16 fixtures fix
+    this)."""
+    step_t, a_t, g2_t, g3_t, sf_t, wd_t = sc
+    kappa, clip, eps = hp["kappa"], hp["clipsnr"], hp["epsilon"]
+    f32 = torch.float32
+    if compiled:
+        P, G, M, V = p.to(f32), g.to(f32), m.to(f32), v.to(f32)
+        st = step_t.to(f32)
+        T = tau.to(f32) if star else None
+    else:
+        P, G, M, V, T, st = p.clone(), g, m.clone(), v.clone(), (tau.clone() if star else None), step_t
+        sqrt, epow = torch.sqrt, torch.pow
+    # _foreach_lerp_(ms, grads, alpha): ATen's kernel in both modes, on m's dtype
+    M = torch.lerp(m, g, a_t).to(f32) if compiled else torch.lerp(M, G, a_t)
+    oma = torch.neg(a_t) + 1.0                                # _foreach_neg, _foreach_add_(., 1.0)
+    V = V * oma                                               # _foreach_mul_(vs, .)
+    V = V + (G * G) * a_t                                     # mul, mul, _foreach_add_
+    sv = sqrt(V)                                              # sqrt_vs
+    if star:
+        ag = torch.abs(G)
+        den = ag + sv                                         # dana_star_mk4.py:429-433
+        if compiled:
+            den = den + eps
+        else:
+            torch._foreach_add_([den], eps)                   # in place: eps in den's dtype
+        tu = ag / den                                         # :436
+        if compiled:                                          # :439, ATen's lerp on tau's dtype
+            T = torch.lerp(tau, tu.to(tau.dtype), a_t).to(f32)
+        else:
+            T = torch.lerp(T, tu, a_t)
+        ct = torch.clamp(T, max=0.5)                          # :444
+        pe = ct / (torch.neg(ct) + 1.0)                       # :447-450
+        min_p = torch.reciprocal(st + 1.0)                    # :455-456
+        treg = torch.maximum(pe, min_p)                       # :457
+        et = T * st                                           # :461
+        et = torch.maximum(et, torch.ones_like(et))           # :462-463
+        nt = sqrt(treg) / (sv + eps)                          # :468-470
+        mfac = nt * (torch.abs(M) / treg)                     # :474-476
+        af = epow(et, 1.0 - kappa) * mfac                     # :480-481
+        if clip is not None:
+            af = torch.clamp(af, max=clip)
+        g3i = (treg * torch.sign(M)) * af + M * nt            # :490-497
+    else:
+        nt = torch.reciprocal(sv + eps)                       # adana.py:327-329
+        mfac = torch.abs(M) * nt                              # :332-333
+        et = st + 1.0                                         # :336
+        ep = torch.tensor(powf(float(et), 1.0 - kappa), dtype=f32) if compiled else torch.pow(et, 1.0 - kappa)
+        af = ep * mfac                                        # :339-340
+        if clip is not None:
+            af = torch.clamp(af, max=clip)
+        g3i = torch.sign(M) * af + M * nt                     # :345-348
+    if compiled:
+        g3i = g3i * hp["gamma_3_factor"]
+    else:
+        torch._foreach_mul_([g3i], hp["gamma_3_factor"])     # in place: the factor in g3i's dtype
+    g3t = g3i * g3_t                                          # _foreach_mul(., g3)
+    g2t = (G * nt) * g2_t                                     # grad_norm, g2_term
+    P = P + torch.neg(g2t + g3t)                              # add, neg_, add_
+    nws = torch.neg(wd_t) * sf_t
+    if hp["wd_decaying"]:                                     # adana.py:357-362
+        wdf = torch.reciprocal(st / hp["wd_ts"] + 1.0) * nws
+    else:
+        wdf = nws if compiled else nws.to(p.dtype)
+    P = P + P * wdf                                           # :367-368
+    p.copy_(P)
+    m.copy_(M)
+    v.copy_(V)
+    if star:
+        tau.copy_(T)
+    dt = p.dtype
+    afd, mfd = af.to(dt), mfac.to(dt)
+    return afd.mean(), g.norm(), mfd.mean(), m.norm()
+
+
 @dataclass
 class TorchRefGroup:
     params: List[torch.Tensor]
@@ -182,13 +279,15 @@ class TorchRefOptimizer:
 
     @torch.no_grad()
     def step(self, grads: Sequence[Sequence[Optional[torch.Tensor]]], sqrt=torch.sqrt, epow=None,
-             slip: Optional[str] = None, compiled=None, update_fn=None) -> None:
+             slip: Optional[str] = None, compiled=None, update_fn=None, foreach=None) -> None:
         """One step of the reference's loop.  ``compiled``: None for the eager
         ops (``update``), or (sqrt, epow, powf) for ``update_compiled``.
         ``update_fn(p)``, when given, returns the callable that replaces
         ``update`` for tensor p (bench.py passes ``update`` wrapped in
         torch.compile, one wrapper per shape, as src/optim/adana.py:72-79
-        and src/optim/dana_star_mk4.py:88-96 do)."""
+        and src/optim/dana_star_mk4.py:88-96 do).  ``foreach``: (sqrt, epow,
+        powf, compiled) runs ``update_foreach`` with the foreach path's
+        scalars (src/optim/adana.py:245-262) instead."""
         f32 = dict(dtype=torch.float32)
         for gi, group in enumerate(self.groups):
             lr = group.lr
@@ -210,7 +309,13 @@ class TorchRefOptimizer:
                 sc = (torch.tensor(t, **f32), torch.tensor(group.delta / (group.delta + t), **f32),
                       torch.tensor(lr, **f32), torch.tensor(lr, **f32), torch.tensor(sf, **f32),
                       torch.tensor(group.weight_decay, **f32))                       # :199-208
-                if update_fn is not None:
+                if foreach is not None:
+                    step_t = torch.tensor(t, dtype=p.dtype)                         # :258
+                    delta_t = torch.tensor(group.delta, **f32)                      # :173
+                    sc = (step_t, delta_t / (delta_t + step_t)) + sc[2:]            # :259
+                    ca, gn, afm, mn = update_foreach(self.star, p, g, st["m"], st["v"], st.get("tau"), sc, hp,
+                                                     *foreach)
+                elif update_fn is not None:
                     ca, gn, afm, mn = update_fn(p)(self.star, p, g, st["m"], st["v"], st.get("tau"), sc, hp)
                 elif compiled is None:
                     ca, gn, afm, mn = update(self.star, p, g, st["m"], st["v"], st.get("tau"), sc, hp,

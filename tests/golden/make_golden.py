@@ -31,6 +31,14 @@ src/optim/dana_star_mk4.py:251-255).  Both modes are recorded, eager and
 ``torch.compile``: ``<case>.bf16_eager.npz`` / ``<case>.bf16_compiled.npz``,
 tensors stored as their 16-bit patterns (uint16), diagnostics as float32.
 
+A sixth output (--foreach) runs every case with ``use_foreach=True``: the
+reference's foreach path (src/optim/adana.py:229-370,
+src/optim/dana_star_mk4.py:298-536), whose ``_foreach_compute_kernel_impl``
+the constructor wraps in ``torch.compile(dynamic=True)``
+(``<case>.foreach.npz``), and the same function as eager ops
+(``<case>.foreach_eager.npz``); float32 and bfloat16 parameters
+(``<case>.bf16_foreach[_eager].npz``).
+
 A fourth output (--nonfinite) repeats the eager runs of four cases with a few
 NaN / +inf / -inf gradient entries (NONFINITE) and stores them as
 ``nonfinite.inputs.npz`` and ``<case>.nonfinite.npz``: how the reference's
@@ -38,6 +46,7 @@ ops carry non-finite values (lerp, addcmul, sqrt, clamp, sign of NaN, the
 diagnostics' sums) is pinned by its own run.
 
 Usage:  python tests/golden/make_golden.py [--ref /root/reference] [--compiled] [--state-only] [--nonfinite]
+                                          [--bf16] [--foreach]
 """
 from __future__ import annotations
 
@@ -170,7 +179,8 @@ def _bits(t) -> np.ndarray:
     return t.view(torch.int16).numpy().view(np.uint16).copy() if t.dtype == torch.bfloat16 else t.numpy().copy()
 
 
-def run_case(ref: str, case: str, compiled: bool, p0, grads, has_grad, state_out=None, bf16: bool = False):
+def run_case(ref: str, case: str, compiled: bool, p0, grads, has_grad, state_out=None, bf16: bool = False,
+             foreach: bool = False):
     import torch
 
     modname, clsname, kw = CASES[case]
@@ -181,9 +191,10 @@ def run_case(ref: str, case: str, compiled: bool, p0, grads, has_grad, state_out
     for gi, scale in enumerate(GROUP_WD_SCALE):
         groups.append({"params": [p for i, p in enumerate(params) if GROUP_OF[i] == gi],
                        "weight_decay": kw["weight_decay"] * scale})
-    opt = cls(groups, **kw)
+    opt = cls(groups, **kw, use_foreach=foreach)
     if not compiled:
         opt._get_compiled_fn = lambda shape: opt._update_param_compiled
+        opt._foreach_compute_kernel = None      # the foreach path then calls its _impl as eager ops
     peak = kw["lr"]
     out = {}
     diags = np.full((N_STEPS, len(SHAPES), 5), np.nan, dtype=np.float32)
@@ -224,6 +235,9 @@ def main():
                     help="only write <case>.bf16_eager.npz and <case>.bf16_compiled.npz (bfloat16 parameters)")
     ap.add_argument("--nonfinite", action="store_true",
                     help="only write nonfinite.inputs.npz and <case>.nonfinite.npz (NaN/inf gradient entries)")
+    ap.add_argument("--foreach", action="store_true",
+                    help="only write the use_foreach=True runs: <case>.foreach[_eager].npz and "
+                         "<case>.bf16_foreach[_eager].npz")
     args = ap.parse_args()
     import torch
 
@@ -256,6 +270,15 @@ def main():
             out = run_case(args.ref, case, False, p0, grads_nf, has_grad)
             np.savez_compressed(os.path.join(HERE, f"{case}.nonfinite.npz"), **out)
             print(f"wrote {case}.nonfinite.npz", flush=True)
+        return 0
+    if args.foreach:
+        for bf16 in (False, True):
+            for mode in ("compiled", "eager"):
+                for case in CASES:
+                    out = run_case(args.ref, case, mode == "compiled", p0, grads, has_grad, bf16=bf16, foreach=True)
+                    name = f"{case}.{'bf16_' if bf16 else ''}foreach{'_eager' if mode == 'eager' else ''}.npz"
+                    np.savez_compressed(os.path.join(HERE, name), **out)
+                    print(f"wrote {name}", flush=True)
         return 0
     if args.bf16:
         for mode in ("eager", "compiled"):

@@ -91,14 +91,16 @@ def _powf(x: float, e: float) -> float:
     return _LIBM.powf(x, float(np.float32(e)))
 
 
-def _run(case, *, sqrt=torch.sqrt, epow=None, on_step=None, slip=None, compiled=None, bf16=False):
+def _run(case, *, sqrt=torch.sqrt, epow=None, on_step=None, slip=None, compiled=None, bf16=False, foreach=None):
     """oracle.torch_ref's restatement of the reference's step() over the
     golden inputs: two groups (weight decay on group 0 only), per-tensor step
     counters, grad None skipped, lr = peak * multiplier(k).  ``on_step(k,
     params, state, diags)`` sees the state after each step; ``diags[i]`` are
     the five diagnostics of the tensors stepped at k.  ``compiled``: the
     (sqrt, epow, powf) of torch_ref.update_compiled, or None for the eager
-    ops.  ``bf16``: bfloat16 parameters and gradients."""
+    ops.  ``bf16``: bfloat16 parameters and gradients.  ``foreach``: the
+    (sqrt, epow, powf, compiled) of torch_ref.update_foreach, the reference's
+    use_foreach=True path."""
     from oracle.torch_ref import DIAG_KEYS, TorchRefGroup, TorchRefOptimizer
 
     meta, p0, grads, has_grad = load_golden_inputs()
@@ -116,7 +118,7 @@ def _run(case, *, sqrt=torch.sqrt, epow=None, on_step=None, slip=None, compiled=
             g.lr = kw["lr"] * meta["lr_multiplier"][k - 1]
         gl = [[torch.from_numpy(grads[k - 1][i].copy()).to(dt) if has_grad[k - 1, i] else None for i in idx[gi]]
               for gi in range(2)]
-        opt.step(gl, sqrt=sqrt, epow=epow, slip=slip, compiled=compiled)
+        opt.step(gl, sqrt=sqrt, epow=epow, slip=slip, compiled=compiled, foreach=foreach)
         state = {i: opt.state[id(p)] for i, p in enumerate(params) if id(p) in opt.state}
         diags = {i: [float(state[i][key]) for key in DIAG_KEYS] for i in range(len(params)) if has_grad[k - 1, i]}
         if on_step is not None:
@@ -357,3 +359,54 @@ def test_oracle_equals_compiled_restatement_with_correct_rounding(oracle_mod, ca
                 assert np.array_equal(got, ost[key].view(got.dtype)), (case, mode, key, k, i)
 
     _run(case, on_step=check, compiled=(_cr_sqrt, cr_pow, _powf), bf16=bf16)
+
+
+FOREACH_MODES = ["foreach", "foreach_eager", "bf16_foreach", "bf16_foreach_eager"]
+
+
+@pytest.mark.skipif(torch.backends.cpu.get_cpu_capability() != load_golden_inputs()[0].get("cpu_capability"),
+                    reason="torch's CPU sqrt/pow bits depend on the SIMD level the fixtures were written with")
+@pytest.mark.parametrize("mode", FOREACH_MODES)
+@pytest.mark.parametrize("case", golden_cases("foreach"))
+def test_foreach_restatement_reproduces_reference_bits(case, mode):
+    """The reference's use_foreach=True path (src/optim/adana.py:229-370,
+    src/optim/dana_star_mk4.py:298-536), restated per tensor by
+    torch_ref.update_foreach, gives its golden bits (0 ulp) for p, m, v, tau
+    at every checkpoint and its diagnostics at every step, in all four of its
+    runs: torch.compile'd (the constructor's default for this path) and eager,
+    float32 and bfloat16 parameters.  Compiled, with a correctly rounded
+    sqrt, Inductor's SIMD pow and powf; eager, ATen's own ops."""
+    gold = load_golden_case(case, mode)
+    meta = load_golden_inputs()[0]
+    bf16 = mode.startswith("bf16")
+    compiled = not mode.endswith("eager")
+    star = meta["cases"][case]["class"] == "DANA_STAR_MK4"
+
+    def check(k, params, state, diags):
+        for i, d in diags.items():
+            ref = gold["diag"][k - 1, i].astype(np.float32)
+            assert ulp_diff(np.array(d, np.float32), ref).max() == 0, (case, mode, k, i, d, ref)
+        if k not in meta["checkpoints"]:
+            return
+        for i, p in enumerate(params):
+            assert np.array_equal(_bits(p), gold[f"p{i}_t{k}"].view(_bits(p).dtype)), (case, mode, k, i)
+            if i not in state:
+                continue
+            assert state[i]["step"] == int(gold[f"step{i}_t{k}"])
+            for key in ("m", "v", "tau") if star else ("m", "v"):
+                got = _bits(state[i][key])
+                assert np.array_equal(got, gold[f"{key}{i}_t{k}"].view(got.dtype)), (case, mode, key, k, i)
+
+    fe = (_cr_sqrt, _simd_pow, _powf, True) if compiled else (None, None, None, False)
+    _run(case, on_step=check, bf16=bf16, foreach=fe)
+
+
+@pytest.mark.parametrize("case", golden_cases("foreach"))
+def test_foreach_runs_differ_from_per_tensor_runs(case):
+    """The foreach path is not the per-tensor path with another loop: its
+    op forms (no addcmul, ATen's lerp under compile, maximum for tau_reg,
+    p + p * wd) give other bits than the default per-tensor compiled run."""
+    meta = load_golden_inputs()[0]
+    a, b = load_golden_case(case, "foreach"), load_golden_case(case, "compiled")
+    k = meta["n_steps"]
+    assert any(not np.array_equal(a[f"p{i}_t{k}"], b[f"p{i}_t{k}"]) for i in range(len(meta["shapes"])))
