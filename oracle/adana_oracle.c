@@ -15,6 +15,10 @@
  *   adana_oracle_step_bf16   <- both updates on bfloat16 parameters (the
  *                               reference's own bfloat16 path, every op
  *                               rounded to bfloat16; rules below)
+ *   adana_oracle_scalars.foreach: the same entry points step the
+ *                               reference's use_foreach=True path instead
+ *                               (src/optim/adana.py:229-370,
+ *                               src/optim/dana_star_mk4.py:298-536)
  *
  * Arithmetic contract (the oracle of record):
  *   - every tensor op of the reference is one IEEE-754 binary32 operation,
@@ -143,6 +147,12 @@ static inline uint16_t f32_to_bf16(float f) {
     return (uint16_t)(u >> 16);
 }
 
+static inline float o_maximum(float a, float b) {   /* torch.maximum: NaN propagates */
+    if (a != a) return a;
+    if (b != b) return b;
+    return a < b ? b : a;
+}
+
 /* One ADana / Dana-MK4 element (src/optim/adana.py:101-143). */
 static inline float adana_elem(float p, float g, float *mp, float *vp,
                                const adana_oracle_scalars *sc, double acc[4]) {
@@ -203,11 +213,6 @@ static inline float star_elem(float p, float g, float *mp, float *vp, float *tp,
     return p;
 }
 
-static inline float o_maximum(float a, float b) {   /* torch.maximum: NaN propagates */
-    if (a != a) return a;
-    if (b != b) return b;
-    return a < b ? b : a;
-}
 
 /* One element of Manau's Dana-Star-MK4 branch (src/optim/manau.py:566-613).
  * ATen's add_(x, alpha=a) and addcmul_(g, g, value=a) are single-rounded
@@ -329,6 +334,81 @@ static inline float star_elem16(float p, float g, float *mp, float *vp, float *t
     return p;
 }
 
+/* ---------------------------------------------------------------------------
+ * The reference's foreach path (use_foreach=True): _foreach_compute_kernel_impl,
+ * src/optim/adana.py:310-370 and src/optim/dana_star_mk4.py:395-536, one
+ * element of one tensor, one binary32 operation per torch._foreach_* op in
+ * that order.  Its forms differ from the per-tensor update's: no addcmul
+ * (v * (1 - a) + (g * g) * a), tau_reg = maximum(p_estimate, min_p),
+ * mfac = nt * (|m| / tau_reg), g3 scaled as (inner * gamma_3_factor) * lr,
+ * g2 = (g * nt) * lr, p - (g2 + g3) and then p + p * wdf.  Its lerps are
+ * ATen's in both of the reference's modes (torch.compile keeps a foreach
+ * lerp with a list of weight tensors as the ATen kernel), so under
+ * torch.compile on bfloat16 tensors (l16) m and tau come out of that kernel
+ * rounded to bfloat16, tau's lerp reads the tau update rounded to bfloat16,
+ * and everything else is binary32 from those values; the alpha factor and
+ * mfac that the diagnostics average are the bfloat16 tensors the kernel
+ * returns.  Scalars: alpha = fp32(delta) / (fp32(delta) + step) and
+ * min_p = 1 / (step + 1) in binary32, step in the parameters' dtype
+ * (adana.py:258-259, dana_star_mk4.py:455-456); wdf from adana.py:357-365.
+ * ------------------------------------------------------------------------- */
+static inline float fe_lerp(float self, float end, const adana_oracle_scalars *sc, int l16) {
+    return l16 ? rb(o_lerp(self, end, rb(sc->a), 0)) : o_lerp(self, end, sc->a, 0);
+}
+
+static inline float adana_elem_fe(float p, float g, float *mp, float *vp, const adana_oracle_scalars *sc,
+                                  int l16, double acc[4]) {
+    float m = fe_lerp(*mp, g, sc, l16);                      /* _foreach_lerp_ */
+    float v = *vp * sc->oma + (g * g) * sc->a;               /* mul_, mul, mul, add_ */
+    float nt = 1.0f / (sqrtf(v) + sc->eps);                  /* sqrt, add, reciprocal */
+    float mf = fabsf(m) * nt;                                /* abs, mul */
+    float af = sc->pw * mf;                                  /* pow (0-d), mul */
+    if (sc->has_clip) af = o_clamp_max(af, sc->clip);
+    float inner = o_sign(m) * af + m * nt;                   /* sign, mul, mul, add */
+    float g3t = (inner * sc->g3f) * sc->lr;                  /* mul_(gamma_3_factor), mul(g3) */
+    float g2t = (g * nt) * sc->lr;                           /* mul, mul(g2) */
+    p = p - (g2t + g3t);                                     /* add, neg_, add_ */
+    p = p + p * sc->wdf;                                     /* mul, add_ */
+    *mp = m;
+    *vp = v;
+    acc[0] += (double)(l16 ? rb(af) : af);
+    acc[1] += (double)g * (double)g;
+    acc[2] += (double)(l16 ? rb(mf) : mf);
+    acc[3] += (double)m * (double)m;
+    return p;
+}
+
+static inline float star_elem_fe(float p, float g, float *mp, float *vp, float *tp,
+                                 const adana_oracle_scalars *sc, int l16, double acc[4]) {
+    float m = fe_lerp(*mp, g, sc, l16);                      /* _foreach_lerp_ */
+    float v = *vp * sc->oma + (g * g) * sc->a;               /* mul_, mul, mul, add_ */
+    float sv = sqrtf(v);                                     /* sqrt_vs */
+    float ag = fabsf(g);
+    float tu = ag / ((ag + sv) + sc->eps);                   /* add, add_(epsilon), div */
+    float tau = fe_lerp(*tp, l16 ? rb(tu) : tu, sc, l16);    /* _foreach_lerp_ */
+    float ct = o_clamp_max(tau, 0.5f);                       /* clamp */
+    float pe = ct / (1.0f - ct);                             /* neg, add_(1.0), div */
+    float tr = o_maximum(pe, sc->min_p);                     /* maximum */
+    float et = o_maximum(tau * sc->s, 1.0f);                 /* mul, maximum(., ones) */
+    float nt = sqrtf(tr) / (sv + sc->eps);                   /* sqrt, add, div */
+    float mf = nt * (fabsf(m) / tr);                         /* abs, div, mul */
+    float af = o_pow(et, sc) * mf;                           /* pow, mul */
+    if (sc->has_clip) af = o_clamp_max(af, sc->clip);
+    float inner = (tr * o_sign(m)) * af + m * nt;            /* sign, mul, mul, mul, add */
+    float g3t = (inner * sc->g3f) * sc->lr;                  /* mul_(gamma_3_factor), mul(g3) */
+    float g2t = (g * nt) * sc->lr;                           /* mul, mul(g2) */
+    p = p - (g2t + g3t);                                     /* add, neg_, add_ */
+    p = p + p * sc->wdf;                                     /* mul, add_ */
+    *mp = m;
+    *vp = v;
+    *tp = tau;
+    acc[0] += (double)(l16 ? rb(af) : af);
+    acc[1] += (double)g * (double)g;
+    acc[2] += (double)(l16 ? rb(mf) : mf);
+    acc[3] += (double)m * (double)m;
+    return p;
+}
+
 /* Parallel element loops.  Element results do not depend on the thread
  * count; the binary64 diagnostic sums may differ in the last bits. */
 #define DIAG_LOOP(BODY)                                                        \
@@ -341,14 +421,22 @@ static inline float star_elem16(float p, float g, float *mp, float *vp, float *t
     }                                                                          \
     diag[0] = s0; diag[1] = s1; diag[2] = s2; diag[3] = s3;
 
+/* The element update of one float32 tensor (per-tensor or foreach forms). */
+static inline float elem32(int32_t star, float p, float g, float *mp, float *vp, float *tp,
+                           const adana_oracle_scalars *sc, double acc[4]) {
+    if (sc->foreach)
+        return star ? star_elem_fe(p, g, mp, vp, tp, sc, 0, acc) : adana_elem_fe(p, g, mp, vp, sc, 0, acc);
+    return star ? star_elem(p, g, mp, vp, tp, sc, acc) : adana_elem(p, g, mp, vp, sc, acc);
+}
+
 void adana_oracle_adana_step(int64_t n, float *p, const float *g, float *m, float *v,
                              const adana_oracle_scalars *sc, double diag[4]) {
-    DIAG_LOOP(p[i] = adana_elem(p[i], g[i], &m[i], &v[i], sc, acc))
+    DIAG_LOOP(p[i] = elem32(0, p[i], g[i], &m[i], &v[i], NULL, sc, acc))
 }
 
 void adana_oracle_star_step(int64_t n, float *p, const float *g, float *m, float *v,
                             float *tau, const adana_oracle_scalars *sc, double diag[4]) {
-    DIAG_LOOP(p[i] = star_elem(p[i], g[i], &m[i], &v[i], &tau[i], sc, acc))
+    DIAG_LOOP(p[i] = elem32(1, p[i], g[i], &m[i], &v[i], &tau[i], sc, acc))
 }
 
 void adana_oracle_manau_step(int64_t n, float *p, const float *g, float *m, float *v, float *tau,
@@ -363,24 +451,16 @@ void adana_oracle_manau_step(int64_t n, float *p, const float *g, float *m, floa
 void adana_oracle_master_step(int64_t n, int32_t star, float *master, uint16_t *p16,
                               const uint16_t *g16, float *m, float *v, float *tau,
                               const adana_oracle_scalars *sc, double diag[4]) {
-    if (star) {
-        DIAG_LOOP(master[i] = star_elem(master[i], bf16_to_f32(g16[i]), &m[i], &v[i], &tau[i], sc, acc);
-                  p16[i] = f32_to_bf16(master[i]))
-    } else {
-        DIAG_LOOP(master[i] = adana_elem(master[i], bf16_to_f32(g16[i]), &m[i], &v[i], sc, acc);
-                  p16[i] = f32_to_bf16(master[i]))
-    }
+    DIAG_LOOP(master[i] = elem32(star, master[i], bf16_to_f32(g16[i]), &m[i], &v[i], star ? &tau[i] : NULL,
+                                 sc, acc);
+              p16[i] = f32_to_bf16(master[i]))
 }
 
 /* fp32 parameters with bf16 gradients (extension, same math). */
 void adana_oracle_step_g16(int64_t n, int32_t star, float *p, const uint16_t *g16, float *m,
                            float *v, float *tau, const adana_oracle_scalars *sc,
                            double diag[4]) {
-    if (star) {
-        DIAG_LOOP(p[i] = star_elem(p[i], bf16_to_f32(g16[i]), &m[i], &v[i], &tau[i], sc, acc))
-    } else {
-        DIAG_LOOP(p[i] = adana_elem(p[i], bf16_to_f32(g16[i]), &m[i], &v[i], sc, acc))
-    }
+    DIAG_LOOP(p[i] = elem32(star, p[i], bf16_to_f32(g16[i]), &m[i], &v[i], star ? &tau[i] : NULL, sc, acc))
 }
 
 /* The reference's bfloat16 path: p, g, m, v and tau all bfloat16 (tau may
@@ -391,7 +471,15 @@ void adana_oracle_step_g16(int64_t n, int32_t star, float *p, const uint16_t *g1
  * bfloat16 as ATen's bfloat16 kernels do (adana_elem16, star_elem16). */
 void adana_oracle_step_bf16(int64_t n, int32_t star, uint16_t *p, const uint16_t *g, uint16_t *m,
                             uint16_t *v, uint16_t *tau, const adana_oracle_scalars *sc, double diag[4]) {
-    if (sc->compiled && star) {
+    if (sc->foreach && star) {             /* the foreach path under torch.compile */
+        DIAG_LOOP(float mm = bf16_to_f32(m[i]); float vv = bf16_to_f32(v[i]); float tt = bf16_to_f32(tau[i]);
+                  p[i] = f32_to_bf16(star_elem_fe(bf16_to_f32(p[i]), bf16_to_f32(g[i]), &mm, &vv, &tt, sc, 1, acc));
+                  m[i] = f32_to_bf16(mm); v[i] = f32_to_bf16(vv); tau[i] = f32_to_bf16(tt))
+    } else if (sc->foreach) {
+        DIAG_LOOP(float mm = bf16_to_f32(m[i]); float vv = bf16_to_f32(v[i]);
+                  p[i] = f32_to_bf16(adana_elem_fe(bf16_to_f32(p[i]), bf16_to_f32(g[i]), &mm, &vv, sc, 1, acc));
+                  m[i] = f32_to_bf16(mm); v[i] = f32_to_bf16(vv))
+    } else if (sc->compiled && star) {
         DIAG_LOOP(float mm = bf16_to_f32(m[i]); float vv = bf16_to_f32(v[i]); float tt = bf16_to_f32(tau[i]);
                   p[i] = f32_to_bf16(star_elem(bf16_to_f32(p[i]), bf16_to_f32(g[i]), &mm, &vv, &tt, sc, acc));
                   m[i] = f32_to_bf16(mm); v[i] = f32_to_bf16(vv); tau[i] = f32_to_bf16(tt))
@@ -414,7 +502,7 @@ void adana_oracle_f32_to_bf16(int64_t n, const float *x, uint16_t *y) {
     for (int64_t i = 0; i < n; ++i) y[i] = f32_to_bf16(x[i]);
 }
 
-int adana_oracle_abi_version(void) { return 2; }
+int adana_oracle_abi_version(void) { return 3; }
 
 /* Thread count of the parallel loops (the CPU baseline reports it). */
 #include <omp.h>

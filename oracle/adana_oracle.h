@@ -31,6 +31,10 @@ typedef struct {
                          second-moment update, bfloat16 rounding only where a
                          tensor is stored; 0: the ATen eager ops              */
     int32_t pow_int;  /* POW_INT: the integer exponent                         */
+    int32_t foreach;  /* 1: the reference's use_foreach=True path (below)       */
+    float g3f;      /* foreach: fp32(gamma_3_factor)                         */
+    float lr;       /* foreach: fp32(lr), both g2 and g3                     */
+    float wdf;      /* foreach: the weight-decay factor (p += p * wdf)       */
 } adana_oracle_scalars;
 
 /* Manau's Dana-Star-MK4 branch (src/optim/manau.py:556-613): its scalars

@@ -51,6 +51,10 @@ class OracleScalars(ctypes.Structure):
         ("pow_mode", ctypes.c_int32),
         ("compiled", ctypes.c_int32),
         ("pow_int", ctypes.c_int32),
+        ("foreach", ctypes.c_int32),
+        ("g3f", ctypes.c_float),
+        ("lr", ctypes.c_float),
+        ("wdf", ctypes.c_float),
     ]
 
 
@@ -66,6 +70,7 @@ class OracleManauScalars(ctypes.Structure):
 
 
 _lib = None
+ORACLE_ABI = 3
 
 
 def lib():
@@ -94,6 +99,9 @@ def lib():
                    L.adana_oracle_master_step, L.adana_oracle_step_g16,
                    L.adana_oracle_step_bf16, L.adana_oracle_f32_to_bf16):
             fn.restype = None
+        if L.adana_oracle_abi_version() != ORACLE_ABI:
+            raise RuntimeError(f"{LIB_PATH}: oracle ABI {L.adana_oracle_abi_version()}, expected {ORACLE_ABI} "
+                               f"(rebuild with oracle.build(force=True))")
         _lib = L
     return _lib
 
@@ -264,6 +272,50 @@ def step_scalars(*, lr: float, peak_lr: float, delta: float, kappa: float, epsil
     return sc
 
 
+def foreach_scalars(*, lr: float, peak_lr: float, delta: float, kappa: float, epsilon: float,
+                    weight_decay: float, clipsnr: Optional[float], wd_decaying: bool,
+                    wd_ts: float, gamma_3_factor: float, t: int, compiled: bool = True,
+                    step_bf16: bool = False) -> OracleScalars:
+    """Scalars of one tensor's update at step ``t`` on the reference's
+    use_foreach=True path: the host code of src/optim/adana.py:171-176,
+    :245-262 (dana_star_mk4.py:229-236, :327-340) and the 0-d tensor ops of
+    ``_foreach_compute_kernel_impl`` (adana.py:316-365; dana_star_mk4.py:
+    455-456, :520-528), all binary32.  step_t has the parameters' dtype
+    (``step_bf16``: bfloat16, so a step above 256 is rounded); alpha is the
+    binary32 quotient of the binary32 delta and that step."""
+    st = f32(t)
+    if step_bf16:
+        st = bf16_to_f32(f32_to_bf16(np.array([st], np.float32)))[0]
+    sf = f32(lr / peak_lr)                       # adana.py:165, :174
+    d = f32(delta)                               # :175
+    a = d / (d + st)                             # :259
+    one_p_s = st + f32(1.0)                      # :336 / dana_star_mk4.py:455
+    sc = OracleScalars()
+    sc.a = a
+    sc.oma = f32(1.0) - a                        # :317-318 neg, add_(1.0)
+    sc.s = st
+    sc.eps = f32(epsilon)
+    sc.pw = (_pow0d_compiled if compiled else _pow0d)(one_p_s, 1.0 - kappa)   # :339
+    sc.min_p = f32(1.0) / one_p_s                # dana_star_mk4.py:456
+    sc.has_clip = 0 if clipsnr is None else 1
+    sc.clip = f32(clipsnr) if clipsnr is not None else f32(np.inf)
+    sc.star_exp = f32(1.0 - kappa)               # dana_star_mk4.py:480
+    if compiled:
+        sc.pow_mode, sc.pow_int = pow_mode_compiled(1.0 - kappa)
+    else:
+        sc.pow_mode = pow_mode(1.0 - kappa)
+    sc.compiled = 1 if compiled else 0
+    sc.foreach = 1
+    sc.g3f = f32(gamma_3_factor)                 # :350
+    sc.lr = f32(lr)                              # :172-173 g2, g3
+    nws = (-f32(weight_decay)) * sf              # :360 / :363
+    if wd_decaying:                              # :357-361
+        sc.wdf = (f32(1.0) / (st / f32(wd_ts) + f32(1.0))) * nws
+    else:
+        sc.wdf = nws
+    return sc
+
+
 # --------------------------------------------------------------------------
 # Element kernels
 # --------------------------------------------------------------------------
@@ -414,7 +466,10 @@ class OracleOptimizer:
     bf16 arrays whose m, v, tau are bf16 too: the reference's own bfloat16
     path).  ``numerics`` is "compiled" (the reference's default torch.compile
     path, src/optim/adana.py:72-79, 210-216) or "eager" (its update run as
-    ATen ops).
+    ATen ops).  ``foreach``: the reference's use_foreach=True path
+    (src/optim/adana.py:229-370, src/optim/dana_star_mk4.py:298-536), whose
+    kernel the reference compiles by default; on the bfloat16 path only that
+    compiled form is restated.
     """
 
     groups: List[OracleGroup]
@@ -428,10 +483,13 @@ class OracleOptimizer:
     master: bool = False
     bf16: bool = False
     numerics: str = "compiled"
+    foreach: bool = False
     state: Dict[int, dict] = field(default_factory=dict)
 
     def step(self, grads: Sequence[Sequence[Optional[np.ndarray]]]) -> None:
         """``grads[gi][pi]`` is the gradient of group gi's param pi, or None."""
+        if self.foreach and self.bf16 and self.numerics != "compiled":
+            raise NotImplementedError("oracle: the foreach path's eager ops on bfloat16 tensors are not restated")
         for gi, group in enumerate(self.groups):
             sf = group.lr / self.peak_lr                       # adana.py:165
             group.weighted_step_count += sf                    # adana.py:167
@@ -452,12 +510,13 @@ class OracleOptimizer:
                         st["master"] = bf16_to_f32(p).reshape(p.shape).copy()
                     self.state[key] = st
                 st["step"] += 1                                # adana.py:197
-                sc = step_scalars(lr=group.lr, peak_lr=self.peak_lr, delta=group.delta,
-                                  kappa=self.kappa, epsilon=group.epsilon,
-                                  weight_decay=group.weight_decay, clipsnr=self.clipsnr,
-                                  wd_decaying=self.wd_decaying, wd_ts=self.wd_ts,
-                                  gamma_3_factor=self.gamma_3_factor, t=st["step"],
-                                  compiled=self.numerics == "compiled")
+                kw = dict(lr=group.lr, peak_lr=self.peak_lr, delta=group.delta,
+                          kappa=self.kappa, epsilon=group.epsilon,
+                          weight_decay=group.weight_decay, clipsnr=self.clipsnr,
+                          wd_decaying=self.wd_decaying, wd_ts=self.wd_ts,
+                          gamma_3_factor=self.gamma_3_factor, t=st["step"],
+                          compiled=self.numerics == "compiled")
+                sc = foreach_scalars(**kw, step_bf16=self.bf16) if self.foreach else step_scalars(**kw)
                 if self.master:
                     sums = master_step(self.star, st["master"], p, g, st["m"], st["v"],
                                        st.get("tau"), sc)
