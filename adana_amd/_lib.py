@@ -16,7 +16,7 @@ import numpy as np
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libadana_mta.so")
 
-ABI_VERSION = 7
+ABI_VERSION = 8
 CHUNK_ELEMS = 1024
 ALIGN_ELEMS = 4
 MAX_CLASSES = 8
@@ -30,6 +30,7 @@ WRITE_GRAD = 0x8
 VARIANT_MANAU = 0x10
 STATE_BF16 = 0x20
 NUMERICS_EAGER = 0x40
+FOREACH = 0x80
 DESC_VEC_OK = 0x1
 
 # adana_tensor_desc as a numpy record (64 bytes, same field order; the
@@ -50,7 +51,7 @@ class HParams(ctypes.Structure):
         ("epsilon", ctypes.c_double), ("weight_decay", ctypes.c_double),
         ("clipsnr", ctypes.c_double), ("wd_ts", ctypes.c_double),
         ("gamma_3_factor", ctypes.c_double), ("has_clip", ctypes.c_int32),
-        ("wd_decaying", ctypes.c_int32), ("eager", ctypes.c_int32), ("reserved", ctypes.c_int32),
+        ("wd_decaying", ctypes.c_int32), ("eager", ctypes.c_int32), ("foreach", ctypes.c_int32),
     ]
 
 

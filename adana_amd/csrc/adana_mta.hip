@@ -195,24 +195,46 @@ __device__ __forceinline__ float pow_aten(float x, const adana_step_scalars &sc,
     }
 }
 
+// Which of the reference's forms of the update an instance computes:
+//  NUM_COMPILED  the per-tensor update under torch.compile (the default);
+//  NUM_EAGER     the same update as ATen's eager ops (ADANA_NUMERICS_EAGER);
+//  NUM_FOREACH   the use_foreach=True path's kernel (ADANA_FOREACH), float32
+//                state, compiled or eager (the two differ only in host
+//                scalars);
+//  NUM_FOREACH16 the same path on bfloat16 state under torch.compile: ATen's
+//                lerp rounds m and tau to bfloat16 (its coefficient comes
+//                from alpha rounded to bfloat16, set by the host), the tau
+//                update is read rounded, the rest is binary32, and the
+//                averaged alpha factor and mfac are the bfloat16 tensors.
+enum Numerics { NUM_COMPILED = 0, NUM_EAGER = 1, NUM_FOREACH = 2, NUM_FOREACH16 = 3 };
+constexpr bool is_foreach(int num) { return num == NUM_FOREACH || num == NUM_FOREACH16; }
+
 // m.lerp_(grad, alpha) with w = alpha, c = (|w| < 0.5 ? w : w - 1) (w - 1 is
-// precomputed, exact) and b = (|w| < 0.5 ? self : end).  ATen (eager)
-// computes fma(c, end - self, b); Inductor's decomposition (torch._refs.lerp,
-// the compiled path) computes c * (end - self) + b, product and sum rounded
-// separately.
-template <bool EAGER>
+// precomputed, exact) and b = (|w| < 0.5 ? self : end).  ATen (eager, and
+// the foreach path's lerp in both modes) computes fma(c, end - self, b);
+// Inductor's decomposition (torch._refs.lerp, the per-tensor compiled path)
+// computes c * (end - self) + b, product and sum rounded separately.
+template <int NUM>
 __device__ __forceinline__ float lerp_op(float self, float end, const adana_step_scalars &sc) {
-    if constexpr (EAGER) return __builtin_fmaf(sc.lerp_coef, end - self, sc.lerp_small ? self : end);
-    else return sc.lerp_coef * (end - self) + (sc.lerp_small ? self : end);
+    if constexpr (NUM == NUM_COMPILED) {
+        return sc.lerp_coef * (end - self) + (sc.lerp_small ? self : end);
+    } else {
+        const float r = __builtin_fmaf(sc.lerp_coef, end - self, sc.lerp_small ? self : end);
+        return NUM == NUM_FOREACH16 ? bf16_round(r) : r;
+    }
 }
 // v.mul_(1 - alpha).addcmul_(grad, grad, value=alpha): ATen's addcmul_ is
 // fma(alpha * g, g, v * (1 - alpha)); Inductor computes v * (1 - alpha) +
-// (g * g) * alpha.
-template <bool EAGER>
+// (g * g) * alpha, and so does the foreach path (mul_, mul, mul, add_).
+template <int NUM>
 __device__ __forceinline__ float ema2_op(float v, float g, const adana_step_scalars &sc) {
-    if constexpr (EAGER) return __builtin_fmaf(sc.a * g, g, v * sc.oma);
+    if constexpr (NUM == NUM_EAGER) return __builtin_fmaf(sc.a * g, g, v * sc.oma);
     else return v * sc.oma + (g * g) * sc.a;
 }
+// The foreach path's alpha factor and mfac as the diagnostics average them:
+// the bfloat16 tensors its kernel returns on bfloat16 state.
+template <int NUM>
+__device__ __forceinline__ float diag_val(float x) { return NUM == NUM_FOREACH16 ? bf16_round(x) : x; }
 
 __device__ __forceinline__ void accumulate(float (&acc)[4], float af, float g, float mfac, float m) {
     acc[0] += af;
@@ -221,25 +243,42 @@ __device__ __forceinline__ void accumulate(float (&acc)[4], float af, float g, f
     acc[3] += m * m;
 }
 
-// ADana / Dana-MK4, one element: src/optim/adana.py:101-143.
-template <bool EAGER>
+// The end of the foreach path's update (src/optim/adana.py:345-368,
+// src/optim/dana_star_mk4.py:497-528): g3 = (inner * gamma_3_factor) * lr,
+// g2 = (g * nt) * lr, p + neg(g2 + g3), then p + p * wdf.  (The per-tensor
+// scalar fields c3, cg2 and opw carry gamma_3_factor, lr and wdf here.)
+__device__ __forceinline__ float foreach_p(float p, float g, float inner, float nt, const adana_step_scalars &sc) {
+    const float g3t = (inner * sc.c3) * sc.cg2;
+    const float g2t = (g * nt) * sc.cg2;
+    const float pn = p - (g2t + g3t);
+    return pn + pn * sc.opw;
+}
+
+// ADana / Dana-MK4, one element: src/optim/adana.py:101-143; foreach path
+// :316-368.
+template <int NUM>
 __device__ __forceinline__ float adana_elem(float p, float g, float &m, float &v,
                                             const adana_step_scalars &sc, float (&acc)[4]) {
-    const float mn = lerp_op<EAGER>(m, g, sc);                   // :101
-    const float vn = ema2_op<EAGER>(v, g, sc);                   // :104 mul_, addcmul_
+    const float mn = lerp_op<NUM>(m, g, sc);                     // :101
+    const float vn = ema2_op<NUM>(v, g, sc);                     // :104 mul_, addcmul_
     const float se = adana::sqrt_f32(vn) + sc.eps;               // :107
     const float nt = 1.0f / se;                                  // :110
     const float mfac = fabsf(mn) * nt;                           // :111, :115
     float af = sc.pw * mfac;                                     // :119 / :123
     if (sc.has_clip) af = clamp_max(af, sc.clip);
     const float inner = sign_f(mn) * af + mn * nt;               // :126
-    const float g3t = sc.c3 * inner;
-    const float g2t = (sc.cg2 * g) * nt;                         // :129
-    float pn = p + (g2t + g3t);                                  // :132-135
-    pn = pn * sc.opw;                                            // :143
+    float pn;
+    if constexpr (is_foreach(NUM)) {
+        pn = foreach_p(p, g, inner, nt, sc);                     // :349-368
+    } else {
+        const float g3t = sc.c3 * inner;
+        const float g2t = (sc.cg2 * g) * nt;                     // :129
+        pn = p + (g2t + g3t);                                    // :132-135
+        pn = pn * sc.opw;                                        // :143
+    }
     m = mn;
     v = vn;
-    accumulate(acc, af, g, mfac, mn);
+    accumulate(acc, diag_val<NUM>(af), g, diag_val<NUM>(mfac), mn);
     return pn;
 }
 
@@ -249,40 +288,62 @@ struct StarMid {
     float m, v, se, tau, tr, et;
 };
 
-// src/optim/dana_star_mk4.py:137-159
-template <bool EAGER>
+// src/optim/dana_star_mk4.py:137-159; foreach path :425-463
+template <int NUM>
 __device__ __forceinline__ StarMid star_phase_a(float g, float m, float v, float tau,
                                                 const adana_step_scalars &sc) {
     StarMid o;
-    o.m = lerp_op<EAGER>(m, g, sc);                              // :137
-    o.v = ema2_op<EAGER>(v, g, sc);                              // :140
-    o.se = adana::sqrt_f32(o.v) + sc.eps;                        // :143
+    o.m = lerp_op<NUM>(m, g, sc);                                // :137
+    o.v = ema2_op<NUM>(v, g, sc);                                // :140
+    const float sv = adana::sqrt_f32(o.v);
+    o.se = sv + sc.eps;                                          // :143
     const float ag = fabsf(g);                                   // :147
-    const float tu = ag / (ag + o.se);                           // :148
-    o.tau = lerp_op<EAGER>(tau, tu, sc);                         // :149
+    float tu;
+    if constexpr (is_foreach(NUM)) {
+        tu = ag / ((ag + sv) + sc.eps);                          // :429-436
+        if constexpr (NUM == NUM_FOREACH16) tu = bf16_round(tu);   // lerp_'s operand, stored
+    } else {
+        tu = ag / (ag + o.se);                                   // :148
+    }
+    o.tau = lerp_op<NUM>(tau, tu, sc);                           // :149
     const float ct = clamp_max(o.tau, 0.5f);                     // :152
     // ct in [0, 0.5]: 1 - ct is in [0.5, 1], and exactly 1 when ct < 2^-25
     const float pe = adana::div_core(ct, 1.0f - ct);                    // :153
-    o.tr = sc.min_p + relu_f(pe - sc.min_p);                     // :154-156
-    o.et = clamp_min(o.tau * sc.s, 1.0f);                        // :159
+    if constexpr (is_foreach(NUM)) {
+        o.tr = clamp_min(pe, sc.min_p);                          // :457 maximum(p_estimate, min_p)
+    } else {
+        o.tr = sc.min_p + relu_f(pe - sc.min_p);                 // :154-156
+    }
+    o.et = clamp_min(o.tau * sc.s, 1.0f);                        // :159 / :461-463
     return o;
 }
 
-// src/optim/dana_star_mk4.py:163-195, given pw = effective_time ** (1 - kappa)
+// src/optim/dana_star_mk4.py:163-195, given pw = effective_time ** (1 - kappa);
+// foreach path :468-528
+template <int NUM>
 __device__ __forceinline__ float star_phase_b(float p, float g, const StarMid &a, float pw,
                                               const adana_step_scalars &sc, float (&acc)[4]) {
     // tau_reg >= 1/(1+t) >= 2^-24 (t < 2^24): far above sqrt's scaling range
     const float nt = adana::sqrt_normal(a.tr) / a.se;                   // :163-164
     const float mnt = fabsf(a.m) * nt;                           // :165
-    const float mfac = mnt / a.tr;                               // :167
+    float mfac;
+    if constexpr (is_foreach(NUM)) mfac = nt * (fabsf(a.m) / a.tr);     // :474-476
+    else mfac = mnt / a.tr;                                      // :167
     float af = pw * mfac;                                        // :170 / :174
     if (sc.has_clip) af = clamp_max(af, sc.clip);
+    // sign(m) * (tau_reg * af + |m| * nt); the foreach path's
+    // (tau_reg * sign(m)) * af + m * nt (:490-497) rounds to the same value
     const float inner = sign_f(a.m) * (a.tr * af + mnt);         // :177
-    const float g3t = sc.c3 * inner;
-    const float g2t = (sc.cg2 * g) * nt;                         // :180
-    float pn = p + (g2t + g3t);                                  // :183-186
-    pn = pn * sc.opw;                                            // :195
-    accumulate(acc, af, g, mfac, a.m);
+    float pn;
+    if constexpr (is_foreach(NUM)) {
+        pn = foreach_p(p, g, inner, nt, sc);                     // :499-528
+    } else {
+        const float g3t = sc.c3 * inner;
+        const float g2t = (sc.cg2 * g) * nt;                     // :180
+        pn = p + (g2t + g3t);                                    // :183-186
+        pn = pn * sc.opw;                                        // :195
+    }
+    accumulate(acc, diag_val<NUM>(af), g, diag_val<NUM>(mfac), a.m);
     return pn;
 }
 
@@ -523,16 +584,16 @@ __device__ __forceinline__ float manau_elem(float p, float g, float &m, float &v
 }
 
 // One element of either variant (the element-wise tail path).
-template <bool STAR, int POWK, bool EAGER>
+template <bool STAR, int POWK, int NUM>
 __device__ __forceinline__ float update_elem(float p, float g, float &m, float &v, float &tau,
                                              const adana_step_scalars &sc, const PowTab &tab, float (&acc)[4]) {
     if constexpr (is_manau(POWK)) {
         return manau_elem<POWK>(p, g, m, v, tau, as_manau(sc), tab, acc);
     } else if constexpr (!STAR) {
-        return adana_elem<EAGER>(p, g, m, v, sc, acc);
+        return adana_elem<NUM>(p, g, m, v, sc, acc);
     } else {
-        const StarMid a = star_phase_a<EAGER>(g, m, v, tau, sc);
-        const float pn = star_phase_b(p, g, a, pow_aten<POWK>(a.et, sc, tab), sc, acc);
+        const StarMid a = star_phase_a<NUM>(g, m, v, tau, sc);
+        const float pn = star_phase_b<NUM>(p, g, a, pow_aten<POWK>(a.et, sc, tab), sc, acc);
         m = a.m;
         v = a.v;
         tau = a.tau;
@@ -542,7 +603,7 @@ __device__ __forceinline__ float update_elem(float p, float g, float &m, float &
 
 // N consecutive elements of one thread (the vector path).  Dana-Star runs
 // phase A for all N, then the N pows, then phase B.
-template <bool STAR, int POWK, bool EAGER, int N>
+template <bool STAR, int POWK, int NUM, int N>
 __device__ __forceinline__ void update_n(float (&P)[N], const float (&G)[N], float (&M)[N], float (&V)[N],
                                          float (&T)[N], const adana_step_scalars &sc, const PowTab &tab,
                                          float (&acc)[4]) {
@@ -552,17 +613,17 @@ __device__ __forceinline__ void update_n(float (&P)[N], const float (&G)[N], flo
         for (int k = 0; k < N; ++k) P[k] = manau_elem<POWK>(P[k], G[k], M[k], V[k], T[k], ms, tab, acc);
     } else if constexpr (!STAR) {
 #pragma unroll
-        for (int k = 0; k < N; ++k) P[k] = adana_elem<EAGER>(P[k], G[k], M[k], V[k], sc, acc);
+        for (int k = 0; k < N; ++k) P[k] = adana_elem<NUM>(P[k], G[k], M[k], V[k], sc, acc);
     } else {
         StarMid a[N];
 #pragma unroll
-        for (int k = 0; k < N; ++k) a[k] = star_phase_a<EAGER>(G[k], M[k], V[k], T[k], sc);
+        for (int k = 0; k < N; ++k) a[k] = star_phase_a<NUM>(G[k], M[k], V[k], T[k], sc);
         float pw[N];
 #pragma unroll
         for (int k = 0; k < N; ++k) pw[k] = pow_aten<POWK>(a[k].et, sc, tab);
 #pragma unroll
         for (int k = 0; k < N; ++k) {
-            P[k] = star_phase_b(P[k], G[k], a[k], pw[k], sc, acc);
+            P[k] = star_phase_b<NUM>(P[k], G[k], a[k], pw[k], sc, acc);
             M[k] = a[k].m;
             V[k] = a[k].v;
             T[k] = a[k].tau;
@@ -729,7 +790,7 @@ enum ParamMode { PM_F32 = 0, PM_MASTER = 1, PM_BF16 = 2 };
 // terms added to acc.  UNIFORM: every thread of the workgroup works on this
 // tensor and the chunk's part of it starts at element seg0, so the fp32
 // stores go out as buffer stores from that uniform base.
-template <bool STAR, bool GBF16, int PM, int POWK, bool EAGER, int VEC, bool UNIFORM>
+template <bool STAR, bool GBF16, int PM, int POWK, int NUM, int VEC, bool UNIFORM>
 __device__ __forceinline__ void thread_elems(const adana_tensor_desc &d, const void *grad, int64_t off, int64_t left,
                                              int64_t seg0, const ScalarPack &pack, float gs, const PowTab &tab,
                                              float (&acc)[4]) {
@@ -738,9 +799,10 @@ __device__ __forceinline__ void thread_elems(const adana_tensor_desc &d, const v
     const int cnt = left < VEC ? static_cast<int>(left) : VEC;
     // the descriptor's flag covers every pointer but the gradient's
     const bool vec_ok = (d.flags & ADANA_DESC_VEC_OK) && grad_vec_aligned<GBF16>(grad);
-    if constexpr (PM == PM_BF16 && !EAGER) {
-        // the compiled path on bfloat16 state: binary32 throughout, the four
-        // stored results rounded to bfloat16 (round to nearest even)
+    if constexpr (PM == PM_BF16 && NUM != NUM_EAGER) {
+        // the compiled paths on bfloat16 state: binary32 throughout (but for
+        // the foreach path's lerps), the four stored results rounded to
+        // bfloat16 (round to nearest even)
         unsigned short *pp = static_cast<unsigned short *>(d.param) + off;
         unsigned short *mp = reinterpret_cast<unsigned short *>(d.m) + off;
         unsigned short *vp = reinterpret_cast<unsigned short *>(d.v) + off;
@@ -762,7 +824,7 @@ __device__ __forceinline__ void thread_elems(const adana_tensor_desc &d, const v
                 for (int k = 0; k < VEC; ++k) G[k] = scale_grad<true>(G[k], gs);
                 if (pack.write_grad) store_grad_n<true, VEC>(grad, off, G);
             }
-            update_n<STAR, POWK, false, VEC>(P, G, M, V, T, sc, tab, acc);
+            update_n<STAR, POWK, NUM, VEC>(P, G, M, V, T, sc, tab, acc);
             st_bf16_n<VEC>(pp, P);
             st_bf16_n<VEC>(mp, M);
             st_bf16_n<VEC>(vp, V);
@@ -775,7 +837,7 @@ __device__ __forceinline__ void thread_elems(const adana_tensor_desc &d, const v
                     g = scale_grad<true>(g, gs);
                     if (pack.write_grad) store_grad1<true>(grad, off + e, g);
                 }
-                const float o = update_elem<STAR, POWK, false>(bf16_to_f32(pp[e]), g, mm, vv, tt, sc, tab, acc);
+                const float o = update_elem<STAR, POWK, NUM>(bf16_to_f32(pp[e]), g, mm, vv, tt, sc, tab, acc);
                 pp[e] = f32_to_bf16(o);
                 mp[e] = f32_to_bf16(mm);
                 vp[e] = f32_to_bf16(vv);
@@ -851,7 +913,7 @@ __device__ __forceinline__ void thread_elems(const adana_tensor_desc &d, const v
             for (int k = 0; k < VEC; ++k) G[k] = scale_grad<GBF16>(G[k], gs);
             if (pack.write_grad) store_grad_n<GBF16, VEC>(grad, off, G);
         }
-        update_n<STAR, POWK, EAGER, VEC>(P, G, M, V, T, sc, tab, acc);
+        update_n<STAR, POWK, NUM, VEC>(P, G, M, V, T, sc, tab, acc);
         if constexpr (UNIFORM && VEC == 4) {
             const int byte_off = static_cast<int>((off - seg0) * 4);
             st4_stream(static_cast<float *>(d.param) + seg0, byte_off, P);
@@ -874,7 +936,7 @@ __device__ __forceinline__ void thread_elems(const adana_tensor_desc &d, const v
                 g = scale_grad<GBF16>(g, gs);
                 if (pack.write_grad) store_grad1<GBF16>(grad, off + e, g);
             }
-            const float o = update_elem<STAR, POWK, EAGER>(pp[e], g, mm, vv, tt, sc, tab, acc);
+            const float o = update_elem<STAR, POWK, NUM>(pp[e], g, mm, vv, tt, sc, tab, acc);
             pp[e] = o;
             mp[e] = mm;
             vp[e] = vv;
@@ -894,12 +956,12 @@ __device__ __forceinline__ void thread_elems(const adana_tensor_desc &d, const v
 // from the overlap (Dana-Star at 2.65B params: 11.16 -> 10.78 ms), while the
 // float32 ones, bound by HBM, lose to the extra loads in flight (north-star
 // 15.02 -> 16.37 ms, C2 0.239 -> 0.266 ms; same-box A/B).
-template <bool STAR, bool GBF16, int PM, int POWK, bool EAGER, int VEC, int GROUPS>
+template <bool STAR, bool GBF16, int PM, int POWK, int NUM, int VEC, int GROUPS>
 __device__ __forceinline__ bool thread_groups_uniform(const adana_tensor_desc &d, const void *grad, int64_t off,
                                                       int64_t left, int64_t seg0, int span, const ScalarPack &pack,
                                                       float gs, const PowTab &tab, float (&acc)[4]) {
     static_assert(VEC == 4, "grouped path: 16-byte vectors");
-    if constexpr (PM != PM_BF16 || EAGER || GROUPS == 1) {
+    if constexpr (PM != PM_BF16 || NUM == NUM_EAGER || GROUPS == 1) {
         return false;
     } else {
         const bool vec_ok = (d.flags & ADANA_DESC_VEC_OK) && grad_vec_aligned<GBF16>(grad);
@@ -937,7 +999,7 @@ __device__ __forceinline__ bool thread_groups_uniform(const adana_tensor_desc &d
 #pragma unroll
         for (int k = 0; k < GROUPS; ++k) {
             const int64_t o = off + static_cast<int64_t>(k) * span;
-            update_n<STAR, POWK, EAGER, VEC>(P[k], G[k], M[k], V[k], T[k], sc, tab, acc);
+            update_n<STAR, POWK, NUM, VEC>(P[k], G[k], M[k], V[k], T[k], sc, tab, acc);
             if constexpr (PM == PM_BF16) {
                 st_bf16_n<VEC>(static_cast<unsigned short *>(d.param) + o, P[k]);
                 st_bf16_n<VEC>(reinterpret_cast<unsigned short *>(d.m) + o, M[k]);
@@ -983,7 +1045,7 @@ __device__ __forceinline__ void block_partial(float (&acc)[4], float (*red)[kW][
     par ^= 1;
 }
 
-template <bool STAR, bool GBF16, int PM, int POWK, bool EAGER, int VEC, int GROUPS>
+template <bool STAR, bool GBF16, int PM, int POWK, int NUM, int VEC, int GROUPS>
 __global__ __launch_bounds__(kChunk / (VEC * GROUPS)) void mta_step_kernel(
         const adana_tensor_desc *__restrict__ desc, const void *const *__restrict__ gradp,
         const int64_t *__restrict__ vstart, const int32_t *__restrict__ chunk_first, int32_t n, ScalarPack pack,
@@ -1057,12 +1119,12 @@ __global__ __launch_bounds__(kChunk / (VEC * GROUPS)) void mta_step_kernel(
     if (inside) {
         // the whole chunk lies in tensor i0
         float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-        if (!thread_groups_uniform<STAR, GBF16, PM, POWK, EAGER, VEC, GROUPS>(
+        if (!thread_groups_uniform<STAR, GBF16, PM, POWK, NUM, VEC, GROUPS>(
                 d0, g0, mine - vs0, vs0 + d0.numel - mine, lo - vs0, kSpan, pack, gs, tab, acc)) {
 #pragma unroll
             for (int k = 0; k < GROUPS; ++k) {
                 const int64_t m = mine + k * kSpan;
-                thread_elems<STAR, GBF16, PM, POWK, EAGER, VEC, true>(d0, g0, m - vs0, vs0 + d0.numel - m, lo - vs0,
+                thread_elems<STAR, GBF16, PM, POWK, NUM, VEC, true>(d0, g0, m - vs0, vs0 + d0.numel - m, lo - vs0,
                                                                          pack, gs, tab, acc);
             }
         }
@@ -1088,7 +1150,7 @@ __global__ __launch_bounds__(kChunk / (VEC * GROUPS)) void mta_step_kernel(
         const adana_tensor_desc d = desc[l];
         const int64_t vs = vstart[l];
         if (m >= vs && m < vs + d.numel)
-            thread_elems<STAR, GBF16, PM, POWK, EAGER, VEC, false>(d, gradp[l], m - vs, vs + d.numel - m, 0, pack,
+            thread_elems<STAR, GBF16, PM, POWK, NUM, VEC, false>(d, gradp[l], m - vs, vs + d.numel - m, 0, pack,
                                                                       gs, tab, acc[k]);
     }
     // one (chunk, tensor) partial per tensor overlapping the chunk, in order
@@ -1643,7 +1705,7 @@ struct LaunchArgs {
     int32_t *counters;
 };
 
-template <bool STAR, bool GBF16, int PM, int POWK, bool EAGER, int GROUPS>
+template <bool STAR, bool GBF16, int PM, int POWK, int NUM, int GROUPS>
 void launch_groups(const LaunchArgs &a, const ScalarPack &pack, bool small_tensors) {
     constexpr int kVec = 4;
     constexpr int kThreads = kChunk / (kVec * GROUPS);
@@ -1653,7 +1715,7 @@ void launch_groups(const LaunchArgs &a, const ScalarPack &pack, bool small_tenso
     constexpr size_t kStaticLds = 2 * (kThreads / 64) * 4 * sizeof(float) +
                                   ((STAR && pow_tables(POWK)) ? 192 * 16 : 16);
     const size_t lds = lds_for_cap(cap, a.n_chunks, kStaticLds);
-    hipLaunchKernelGGL((mta_step_kernel<STAR, GBF16, PM, POWK, EAGER, kVec, GROUPS>),
+    hipLaunchKernelGGL((mta_step_kernel<STAR, GBF16, PM, POWK, NUM, kVec, GROUPS>),
                        dim3(static_cast<unsigned>(a.n_chunks)), dim3(kThreads), static_cast<unsigned>(lds), a.st,
                        a.desc, a.grad, a.vstart, a.chunk_first, a.n, pack, a.partials, a.counters);
 }
@@ -1672,38 +1734,53 @@ void launch_groups(const LaunchArgs &a, const ScalarPack &pack, bool small_tenso
 // process on the same tensors; on that box 15.22 -> 14.99 ms ten minutes
 // later), while one group stays within 15.2-15.9 ms throughout.
 constexpr int64_t kTwoGroupMaxChunks = 1 << 18;
-template <bool STAR, bool GBF16, int PM, int POWK, bool EAGER>
+template <bool STAR, bool GBF16, int PM, int POWK, int NUM>
 void launch_main(const LaunchArgs &a, const ScalarPack &pack) {
     const bool small_tensors = a.n_chunks < 64 * static_cast<int64_t>(a.n);
     const bool two = grid_fills(a.n_chunks, 64) && !(STAR && pow_tables(POWK) && small_tensors) &&
                      (PM == PM_BF16 || a.n_chunks <= kTwoGroupMaxChunks);
-    if (two) launch_groups<STAR, GBF16, PM, POWK, EAGER, 2>(a, pack, small_tensors);
-    else launch_groups<STAR, GBF16, PM, POWK, EAGER, 1>(a, pack, small_tensors);
+    if (two) launch_groups<STAR, GBF16, PM, POWK, NUM, 2>(a, pack, small_tensors);
+    else launch_groups<STAR, GBF16, PM, POWK, NUM, 1>(a, pack, small_tensors);
 }
 
-template <bool STAR, bool GBF16, int PM, bool EAGER>
+template <bool STAR, bool GBF16, int PM, int NUM>
 void launch_pow(int powk, const LaunchArgs &a, const ScalarPack &pack) {
     if constexpr (!STAR) {
         // ADana's (1 + t) ** (1 - kappa) is a host scalar: no per-element pow
-        launch_main<false, GBF16, PM, POW_ONE, EAGER>(a, pack);
+        launch_main<false, GBF16, PM, POW_ONE, NUM>(a, pack);
     } else if (powk == POW_GENERAL) {
-        launch_main<true, GBF16, PM, POW_GENERAL, EAGER>(a, pack);
+        launch_main<true, GBF16, PM, POW_GENERAL, NUM>(a, pack);
     } else if (powk == POW_ONE) {
-        launch_main<true, GBF16, PM, POW_ONE, EAGER>(a, pack);
+        launch_main<true, GBF16, PM, POW_ONE, NUM>(a, pack);
     } else if (powk == POW_SPECIAL) {
-        launch_main<true, GBF16, PM, POW_SPECIAL, EAGER>(a, pack);
-    } else if constexpr (PM == PM_BF16 && EAGER) {
-        if (powk == POW_TABLE16) launch_main<true, GBF16, PM, POW_TABLE16, true>(a, pack);
-    } else if constexpr (!GBF16 && PM == PM_F32 && EAGER) {  // Manau's branch: float32, its own op order
+        launch_main<true, GBF16, PM, POW_SPECIAL, NUM>(a, pack);
+    } else if constexpr (PM == PM_BF16 && NUM == NUM_EAGER) {
+        if (powk == POW_TABLE16) launch_main<true, GBF16, PM, POW_TABLE16, NUM_EAGER>(a, pack);
+    } else if constexpr (!GBF16 && PM == PM_F32 && NUM == NUM_EAGER) {  // Manau's branch: float32, its own op order
         if (powk == POW_MANAU_GENERAL) {
-            launch_main<true, false, PM_F32, POW_MANAU_GENERAL, true>(a, pack);
+            launch_main<true, false, PM_F32, POW_MANAU_GENERAL, NUM_EAGER>(a, pack);
         } else if (powk == POW_MANAU_ONE) {
-            launch_main<true, false, PM_F32, POW_MANAU_ONE, true>(a, pack);
+            launch_main<true, false, PM_F32, POW_MANAU_ONE, NUM_EAGER>(a, pack);
         } else if (powk == POW_MANAU_SPECIAL) {
-            launch_main<true, false, PM_F32, POW_MANAU_SPECIAL, true>(a, pack);
+            launch_main<true, false, PM_F32, POW_MANAU_SPECIAL, NUM_EAGER>(a, pack);
         } else {
-            launch_main<true, false, PM_F32, POW_MANAU_MK4, true>(a, pack);
+            launch_main<true, false, PM_F32, POW_MANAU_MK4, NUM_EAGER>(a, pack);
         }
+    }
+}
+
+// The launch's numerics: the foreach instance of the state's kind (float32
+// state, or bfloat16 state under torch.compile).
+template <bool STAR, bool GBF16, int PM>
+void launch_num(int num, int powk, const LaunchArgs &a, const ScalarPack &pack) {
+    if (num == NUM_EAGER) {
+        launch_pow<STAR, GBF16, PM, NUM_EAGER>(powk, a, pack);
+    } else if (num == NUM_COMPILED) {
+        launch_pow<STAR, GBF16, PM, NUM_COMPILED>(powk, a, pack);
+    } else if constexpr (PM == PM_BF16) {
+        launch_pow<STAR, GBF16, PM, NUM_FOREACH16>(powk, a, pack);
+    } else {
+        launch_pow<STAR, GBF16, PM, NUM_FOREACH>(powk, a, pack);
     }
 }
 
@@ -1770,6 +1847,49 @@ float pow0d(float x, double e) {
     }
 }
 
+// The foreach path's scalars (hp->foreach; src/optim/adana.py:171-176,
+// :245-262 and the 0-d tensor ops of _foreach_compute_kernel_impl, :316-365;
+// src/optim/dana_star_mk4.py:229-236, :327-340, :455-456, :520-528): the
+// step tensor has the parameters' dtype (foreach == 2: bfloat16, rounded to
+// nearest even), alpha is the binary32 quotient of the binary32 delta and
+// that step, and every 0-d op is binary32.  c3, cg2 and opw carry
+// gamma_3_factor, lr and the weight-decay factor wdf.
+int foreach_scalars(adana_step_scalars *out, const adana_hparams *hp, double lr, int64_t step) {
+    float s = static_cast<float>(step);
+    if (hp->foreach == 2) s = adana::bf16_round_int(s);
+    const float sf = static_cast<float>(lr / hp->peak_lr);      // :165, :174
+    const float d = static_cast<float>(hp->delta);               // :175
+    const float a = d / (d + s);                                 // :259
+    const float one_p_s = s + 1.0f;                              // :336 / dana_star_mk4.py:455
+    memset(out, 0, sizeof *out);
+    out->a = a;
+    out->oma = 1.0f - a;                                         // :317-318 neg, add_(1.0)
+    // ATen's lerp on the state's dtype: a bfloat16 lerp takes its weight
+    // rounded to bfloat16
+    const float aw = hp->foreach == 2 ? adana::bf16_round_int(a) : a;
+    out->lerp_small = std::fabs(aw) < 0.5f ? 1 : 0;
+    out->lerp_coef = out->lerp_small ? aw : aw - 1.0f;
+    out->s = s;
+    out->eps = static_cast<float>(hp->epsilon);
+    out->pw = hp->eager ? pow0d(one_p_s, 1.0 - hp->kappa) : pow0d_compiled(one_p_s, 1.0 - hp->kappa);   // :339
+    out->min_p = 1.0f / one_p_s;                                 // dana_star_mk4.py:456
+    out->has_clip = hp->has_clip ? 1 : 0;
+    out->clip = hp->has_clip ? static_cast<float>(hp->clipsnr) : INFINITY;
+    out->c3 = static_cast<float>(hp->gamma_3_factor);            // :350
+    out->cg2 = static_cast<float>(lr);                           // :172-173 g2, g3
+    const float nws = (-static_cast<float>(hp->weight_decay)) * sf;   // :360 / :363
+    out->opw = hp->wd_decaying ? (1.0f / (s / static_cast<float>(hp->wd_ts) + 1.0f)) * nws : nws;  // :357-365
+    out->star_exp = static_cast<float>(1.0 - hp->kappa);         // dana_star_mk4.py:480
+    if (hp->eager) {
+        out->pow_mode = pow_mode_of(1.0 - hp->kappa);
+    } else {
+        int32_t k;
+        out->pow_mode = pow_mode_compiled(1.0 - hp->kappa, &k);
+        out->pow_int = k;
+    }
+    return ADANA_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -1793,6 +1913,9 @@ int adana_step_scalars_init(adana_step_scalars *out, const adana_hparams *hp, do
                                  static_cast<long long>(step));
     if (!(hp->peak_lr != 0.0))
         return adana_set_error(ADANA_E_INVALID, "adana_step_scalars_init: peak lr must be nonzero");
+    if (hp->foreach < 0 || hp->foreach > 2)
+        return adana_set_error(ADANA_E_INVALID, "adana_step_scalars_init: foreach=%d outside [0, 2]", hp->foreach);
+    if (hp->foreach) return foreach_scalars(out, hp, lr, step);
     // Host doubles (src/optim/adana.py:163-165, :200), rounded to binary32 the
     // way torch.tensor(x, dtype=float32) does (:203-208).
     const float sf = static_cast<float>(lr / hp->peak_lr);
@@ -1946,7 +2069,8 @@ int step_impl(const char *fn, const adana_plan *plan, const adana_step_scalars *
     if (int rc = check_plan(plan, fn)) return rc;
     const adana_plan &pl = *plan;
     const uint32_t allowed = ADANA_VARIANT_STAR | ADANA_GRAD_BF16 | ADANA_PARAM_BF16 | ADANA_VARIANT_MANAU |
-                             ADANA_STATE_BF16 | ADANA_NUMERICS_EAGER | (d_grad_scale ? ADANA_WRITE_GRAD : 0u);
+                             ADANA_STATE_BF16 | ADANA_NUMERICS_EAGER | ADANA_FOREACH |
+                             (d_grad_scale ? ADANA_WRITE_GRAD : 0u);
     if (variant_flags & ~allowed)
         return adana_set_error(ADANA_E_INVALID, "%s: unknown variant flags 0x%x", fn, variant_flags);
     const bool manau = variant_flags & ADANA_VARIANT_MANAU;
@@ -1956,6 +2080,12 @@ int step_impl(const char *fn, const adana_plan *plan, const adana_step_scalars *
     if (s16 && (!(variant_flags & ADANA_GRAD_BF16) || (variant_flags & ADANA_PARAM_BF16)))
         return adana_set_error(ADANA_E_INVALID, "%s: ADANA_STATE_BF16 needs ADANA_GRAD_BF16 and excludes "
                                "ADANA_PARAM_BF16", fn);
+    const bool foreach = variant_flags & ADANA_FOREACH;
+    if (foreach && manau)
+        return adana_set_error(ADANA_E_INVALID, "%s: ADANA_FOREACH excludes ADANA_VARIANT_MANAU", fn);
+    if (foreach && s16 && (variant_flags & ADANA_NUMERICS_EAGER))
+        return adana_set_error(ADANA_E_UNSUPPORTED, "%s: the foreach path's eager ops on bfloat16 state "
+                               "(ADANA_FOREACH | ADANA_STATE_BF16 | ADANA_NUMERICS_EAGER) are not implemented", fn);
     if (int rc = check_plan_arrays(pl, fn)) return rc;
     if (pl.n_tensors == 0) return ADANA_OK;
     if (!d_workspace || !d_diag || !h_scalars)
@@ -2019,8 +2149,8 @@ int step_impl(const char *fn, const adana_plan *plan, const adana_step_scalars *
             }
         }
         const LaunchArgs la{pl.n_chunks, st, pl.desc, pl.grad, pl.vstart, pl.chunk_first, n, partials, counters};
-#define ADANA_LAUNCH(S, G, P) \
-        ((eager || manau) ? launch_pow<S, G, P, true>(powk, la, pack) : launch_pow<S, G, P, false>(powk, la, pack))
+        const int num = foreach ? NUM_FOREACH : ((eager || manau) ? NUM_EAGER : NUM_COMPILED);
+#define ADANA_LAUNCH(S, G, P) launch_num<S, G, P>(num, powk, la, pack)
         if (star || manau) {
             if (s16) ADANA_LAUNCH(true, true, PM_BF16);
             else if (gb) { if (pb) ADANA_LAUNCH(true, true, PM_MASTER); else ADANA_LAUNCH(true, true, PM_F32); }

@@ -27,6 +27,17 @@ bfloat16 only where m, v, tau and p are stored.  ``numerics="eager"``
 ops instead: lerp_ and addcmul_ as single-rounded fused multiply-adds and, on
 bfloat16 state, every op rounded to bfloat16.
 
+``use_foreach=True`` (the reference's constructor argument) selects the
+reference's foreach path (src/optim/adana.py:229-370,
+src/optim/dana_star_mk4.py:298-536), whose kernel its constructor compiles:
+the same update in other op forms (no addcmul, ATen's lerp, tau_reg as a
+maximum, mfac = nt * (|m| / tau_reg), g2 and g3 scaled last, weight decay as
+p + p * wdf) with its own scalars (alpha as a binary32 quotient, the step in
+the parameters' dtype).  The step is still one launch.  As in the
+reference, the choice is made at construction; ``numerics="eager"`` with it
+is the same path's kernel run eagerly (float32 and master-weight state; not
+implemented for bfloat16 state).
+
 What differs is how a step executes.  The reference loops over tensors in
 Python, makes six 0-d device tensors per tensor and calls a torch.compile'd
 update per tensor (src/optim/adana.py:184-225).  Here the host computes the
@@ -159,6 +170,14 @@ class _DanaFamily(Optimizer):
         self.master_weights = bool(master_weights)
         self.fresh_diagnostics = fresh_diagnostics
         self.numerics = numerics
+        # the reference picks its foreach kernel in the constructor (adana.py:63-70)
+        self._foreach = bool(getattr(self, "use_foreach", False))
+        if self._foreach and numerics == "eager" and not self.master_weights and any(
+                p.dtype == torch.bfloat16 for g in self.param_groups for p in g["params"]):
+            raise NotImplementedError(f"{type(self).__name__}: use_foreach=True with numerics='eager' on "
+                                      "bfloat16 parameters (the foreach path's eager ops on bfloat16 state) is not "
+                                      "implemented; the default numerics='compiled' is the path the reference "
+                                      "runs with use_foreach=True")
         self._diag_cols = [tuple(c) for c in self._DIAG_COLUMNS]
         self._sets: Optional[List[_LaunchSet]] = None
         self._structure = None
@@ -402,7 +421,8 @@ class _DanaFamily(Optimizer):
             # expanded one) or race; the update is written back element by element
             raise NotImplementedError(f"{type(self).__name__}: parameters whose elements may share memory "
                                       f"(strides {tuple(p.stride())}) are not supported")
-        flags = self._VARIANT | (_lib.NUMERICS_EAGER if self.numerics == "eager" else 0)
+        flags = (self._VARIANT | (_lib.NUMERICS_EAGER if self.numerics == "eager" else 0)
+                 | (_lib.FOREACH if self._foreach else 0))
         if p.dtype == torch.float32:
             if g.dtype != torch.float32:
                 raise RuntimeError(f"{type(self).__name__}: float32 parameter with {g.dtype} "
@@ -414,6 +434,9 @@ class _DanaFamily(Optimizer):
             # master_weights: float32 master and moments (extension); otherwise the
             # reference's own bfloat16 path, m, v, tau bfloat16 as zeros_like(p) makes them
             flags |= _lib.GRAD_BF16 | (_lib.PARAM_BF16 if self.master_weights else _lib.STATE_BF16)
+            if self._foreach and self.numerics == "eager" and not self.master_weights:
+                raise NotImplementedError(f"{type(self).__name__}: use_foreach=True with numerics='eager' on "
+                                          "bfloat16 parameters is not implemented")
         else:
             raise NotImplementedError(f"{type(self).__name__}: parameter dtype {p.dtype}")
         return flags
@@ -610,7 +633,9 @@ class _DanaFamily(Optimizer):
         return params, out
 
     # -- step -------------------------------------------------------------
-    def _hparams(self, group) -> "_lib.HParams":
+    def _hparams(self, group, foreach: int = 0) -> "_lib.HParams":
+        """adana_hparams of a group; ``foreach``: 0, or the foreach path's
+        scalars for float32 (1) or bfloat16 (2) state."""
         hp = _lib.HParams()
         hp.peak_lr = self.lr
         hp.delta = group["delta"]
@@ -623,6 +648,7 @@ class _DanaFamily(Optimizer):
         hp.gamma_3_factor = self.gamma_3_factor
         hp.wd_decaying = 1 if self.wd_decaying else 0
         hp.eager = 1 if self.numerics == "eager" else 0
+        hp.foreach = foreach
         return hp
 
     def _flat_params(self):
@@ -640,15 +666,15 @@ class _DanaFamily(Optimizer):
             self._fast = False
         return self._flat[1], self._flat[2]
 
-    def _group_hparams(self, gi: int) -> "_lib.HParams":
+    def _group_hparams(self, gi: int, foreach: int = 0) -> "_lib.HParams":
         """Group gi's hyper-parameters for the scalar code, rebuilt only when a
         value they are made of changed."""
         g = self.param_groups[gi]
         key = (g["delta"], g["epsilon"], g["weight_decay"], self.lr, self.kappa, self.clipsnr, self.wd_ts,
                self.gamma_3_factor, self.wd_decaying, self.numerics)
-        ent = self._hp_cache.get(gi)
+        ent = self._hp_cache.get((gi, foreach))
         if ent is None or ent[0] != key:
-            ent = self._hp_cache[gi] = (key, self._hparams(g))
+            ent = self._hp_cache[(gi, foreach)] = (key, self._hparams(g, foreach))
         return ent[1]
 
     def _fill_scalars(self, ls: _LaunchSet, classes) -> int:
@@ -657,10 +683,12 @@ class _DanaFamily(Optimizer):
         return their count."""
         L = _lib.lib()
         n_cls = min(_lib.MAX_CLASSES, len(classes) - ls.class_base)
+        # the foreach path's step tensor has the parameters' dtype (adana.py:258)
+        fe = (2 if ls.flags & _lib.STATE_BF16 else 1) if self._foreach else 0
         for k in range(n_cls):
             gi, t = classes[ls.class_base + k]
             _lib.check(L.adana_step_scalars_init(ctypes.byref(ls.sc_arr[k]),
-                                                 ctypes.byref(self._group_hparams(gi)),
+                                                 ctypes.byref(self._group_hparams(gi, fe)),
                                                  float(self.param_groups[gi]["lr"]), int(t)),
                        "adana_step_scalars_init")
         return n_cls
@@ -910,8 +938,9 @@ class ADana(_DanaFamily):
     """ADana (``clipsnr=None``) and Dana-MK4 (``clipsnr=float``).
 
     Same constructor, defaults, group keys and state keys as
-    src/optim/adana.py:32-70; ``use_foreach`` is accepted and has no effect
-    (there is one code path).  Keyword-only extensions (see the module
+    src/optim/adana.py:32-70.  ``use_foreach=True`` gives the reference's
+    foreach path's numerics (see the module docstring).  Keyword-only
+    extensions (see the module
     docstring): ``numerics`` ("compiled", the reference's default
     torch.compile path, or "eager"), ``master_weights`` for bfloat16
     parameters and ``fresh_diagnostics`` for the diagnostics' check.

@@ -12,7 +12,9 @@
  *        0-d device tensors) and the 0-d tensor arithmetic inside the compiled
  *        update (:104 ``1 - alpha``, :114 ``1.0 + step``, :119 pow, :126
  *        ``(-g3) * gamma_3_factor``, :139-143 weight-decay factor) and
- *        DANA_STAR_MK4.step (src/optim/dana_star_mk4.py:217-272, :154 min_p).
+ *        DANA_STAR_MK4.step (src/optim/dana_star_mk4.py:217-272, :154 min_p);
+ *        with adana_hparams.foreach, the foreach path's (adana.py:171-176,
+ *        :245-262, :316-365; dana_star_mk4.py:455-456).
  *   adana_plan_layout        <- the per-tensor Python loop itself
  *        (src/optim/adana.py:184-216; src/optim/dana_star_mk4.py:243-282):
  *        instead of one compiled call per tensor, tensors are laid end to end
@@ -25,7 +27,10 @@
  *        plus the diagnostics stored at src/optim/adana.py:221-225 /
  *        src/optim/dana_star_mk4.py:290-294; with ADANA_VARIANT_MANAU, the
  *        eager Dana-Star-MK4 branch of Manau.step (src/optim/manau.py:504-613)
- *        for the parameters Manau does not give to Muon.
+ *        for the parameters Manau does not give to Muon; with ADANA_FOREACH,
+ *        the use_foreach=True path's _foreach_step_group and
+ *        _foreach_compute_kernel_impl (src/optim/adana.py:229-370;
+ *        src/optim/dana_star_mk4.py:298-536) for all of a group's tensors.
  *   adana_manau_scalars_init <- that branch's host scalars (manau.py:539-555,
  *        :606-610 and the Python-float operands of its tensor ops).
  *   adana_grad_clip_norm     <- the gradient-norm clipping the training loop
@@ -68,7 +73,7 @@
 extern "C" {
 #endif
 
-#define ADANA_ABI_VERSION 7
+#define ADANA_ABI_VERSION 8
 
 /* Elements per work chunk (one 256-thread workgroup, one 16-byte vector per
  * thread per array).  Tensors start at multiples of ADANA_ALIGN_ELEMS in the
@@ -111,6 +116,18 @@ extern "C" {
                                     rounded only where it is stored).  The
                                     scalars must come from hparams with the
                                     same choice (adana_hparams.eager).        */
+#define ADANA_FOREACH      0x80u /* the reference's use_foreach=True path
+                                    (_foreach_compute_kernel_impl,
+                                    src/optim/adana.py:310-370,
+                                    src/optim/dana_star_mk4.py:395-536): its
+                                    op forms (no addcmul, ATen's lerp in both
+                                    modes, tau_reg = maximum(p_est, min_p),
+                                    mfac = nt * (|m| / tau_reg), p += p * wdf)
+                                    and scalars (adana_hparams.foreach).  With
+                                    ADANA_STATE_BF16: the compiled form only
+                                    (m and tau rounded to bfloat16 by ATen's
+                                    lerp, the rest binary32); excludes
+                                    ADANA_VARIANT_MANAU                       */
 
 /* adana_tensor_desc.flags */
 #define ADANA_DESC_VEC_OK  0x1u  /* param, m, v, tau and param_lp aligned for
@@ -174,11 +191,19 @@ typedef struct adana_hparams {
     int32_t has_clip;       /* self.clipsnr is not None                      */
     int32_t wd_decaying;    /* self.wd_decaying                              */
     int32_t eager;          /* 1: scalars for ADANA_NUMERICS_EAGER launches  */
-    int32_t reserved;
+    int32_t foreach;        /* scalars for ADANA_FOREACH launches: 1 with
+                               float32 parameters, 2 with bfloat16 ones (the
+                               path's step tensor has the parameters' dtype);
+                               0: the per-tensor path                        */
 } adana_hparams;
 
 /* Per-step binary32 scalars of one (group, step) class, each computed on the
- * host exactly as the reference's 0-d tensor ops round it.  64 bytes. */
+ * host exactly as the reference's 0-d tensor ops round it.  64 bytes.  The
+ * foreach path (adana_hparams.foreach) computes alpha as the binary32
+ * quotient fp32(delta) / (fp32(delta) + t), t in the parameters' dtype
+ * (src/optim/adana.py:258-259), takes ATen's lerp coefficient from alpha
+ * rounded to bfloat16 when the parameters are bfloat16, and uses the three
+ * fields marked below with their foreach meaning. */
 typedef struct adana_step_scalars {
     float   a;          /* alpha = fp32(delta / (delta + t))                 */
     float   oma;        /* 1 - alpha                                         */
@@ -188,9 +213,10 @@ typedef struct adana_step_scalars {
     float   pw;         /* ADana: (1 + s) ** (1 - kappa), by pow_mode        */
     float   min_p;      /* Dana-Star: 1 / (1 + s)                            */
     float   clip;       /* fp32(clipsnr)                                     */
-    float   c3;         /* (-lr) * gamma_3_factor                            */
-    float   cg2;        /* -lr                                               */
-    float   opw;        /* 1 + weight-decay factor                           */
+    float   c3;         /* (-lr) * gamma_3_factor; foreach: gamma_3_factor   */
+    float   cg2;        /* -lr; foreach: lr                                  */
+    float   opw;        /* 1 + weight-decay factor; foreach: the factor wdf
+                           of p + p * wdf (adana.py:357-368)                 */
     float   star_exp;   /* fp32(1 - kappa), exponent of Dana-Star's pow      */
     int32_t pow_mode;   /* pow specialisation of 1 - kappa (ADANA_POW_*)     */
     int32_t has_clip;

@@ -52,7 +52,7 @@ def _scaled_ulps(x, ref, prev):
 class Pair:
     """The GPU optimizer and the oracle driven in lock step on equal inputs."""
 
-    def __init__(self, O, star, groups_np, master=False, numerics="compiled", **hp):
+    def __init__(self, O, star, groups_np, master=False, numerics="compiled", foreach=False, **hp):
         import adana_amd
 
         self.O = O
@@ -73,7 +73,7 @@ class Pair:
             self.gpu_params.append(tp)
             torch_groups.append(dict(params=tp, **gkw))
         cls = adana_amd.DANA_STAR_MK4 if star else adana_amd.ADana
-        self.opt = cls(torch_groups, master_weights=master, numerics=numerics, **hp)
+        self.opt = cls(torch_groups, master_weights=master, numerics=numerics, use_foreach=foreach, **hp)
         self.oracle = O.OracleOptimizer(
             groups=[O.OracleGroup(params=cp, lr=gkw.get("lr", hp["lr"]),
                                   delta=gkw.get("delta", hp.get("delta", 8.0)),
@@ -83,7 +83,7 @@ class Pair:
             star=star, peak_lr=hp["lr"], kappa=hp.get("kappa", 1.0),
             clipsnr=hp.get("clipsnr", 1.0 if star else None),
             wd_decaying=hp.get("wd_decaying", False), wd_ts=hp.get("wd_ts", 1.0),
-            gamma_3_factor=hp.get("gamma_3_factor", 1.0), master=master, numerics=numerics)
+            gamma_3_factor=hp.get("gamma_3_factor", 1.0), master=master, numerics=numerics, foreach=foreach)
 
     def set_lr(self, lrs):
         for g, og, lr in zip(self.opt.param_groups, self.oracle.groups, lrs):

@@ -87,6 +87,46 @@ def test_host_scalars_match_oracle_bitwise(oracle_mod, kappa):
         assert _f32bits(sc.lerp_coef) == _f32bits(coef)
 
 
+@pytest.mark.parametrize("compiled", [True, False], ids=["compiled", "eager"])
+@pytest.mark.parametrize("foreach", [1, 2], ids=["fp32_step", "bf16_step"])
+@pytest.mark.parametrize("kappa", [0.85, 1.0, 0.5, 1.5])
+def test_host_foreach_scalars_match_oracle_bitwise(oracle_mod, kappa, foreach, compiled):
+    """adana_step_scalars_init with hparams.foreach (the use_foreach=True
+    path) against the oracle's independent restatement (oracle.foreach_scalars),
+    bit for bit; c3, cg2 and opw carry gamma_3_factor, lr and the weight-decay
+    factor; with bfloat16 parameters the step is rounded to bfloat16 and the
+    lerp coefficient comes from alpha rounded to bfloat16."""
+    from adana_amd import _lib
+
+    rng = np.random.default_rng(int(kappa * 100) + 31 * foreach + int(compiled))
+    for trial in range(40):
+        kw = dict(peak_lr=float(10 ** rng.uniform(-4, -1)), delta=float(rng.choice([8.0, 6.0, 7.3, 3.5])),
+                  kappa=kappa, epsilon=float(rng.choice([1e-8, 1e-6])),
+                  weight_decay=float(rng.choice([0.0, 0.4, 0.1])), clipsnr=[None, 1.0, 2.0, 0.37][trial % 4],
+                  wd_decaying=bool(trial % 2), wd_ts=float(rng.choice([1.0, 10.0, 37.5])),
+                  gamma_3_factor=float(rng.choice([1.0, 0.5, 0.7])))
+        lr = kw["peak_lr"] * float(rng.uniform(0.01, 1.0))
+        t = int(rng.choice([1, 2, 7, 8, 9, 100, 257, 12345, 2 ** 20 + 3]))
+        hp = _hp(_lib, **kw)
+        hp.foreach = foreach
+        hp.eager = 0 if compiled else 1
+        sc = _lib.step_scalars(hp, lr, t)
+        ref = oracle_mod.foreach_scalars(lr=lr, t=t, compiled=compiled, step_bf16=foreach == 2, **kw)
+        for name in ("a", "oma", "s", "eps", "pw", "min_p", "star_exp"):
+            assert _f32bits(getattr(sc, name)) == _f32bits(getattr(ref, name)), (name, kw, lr, t)
+        for name, rname in (("c3", "g3f"), ("cg2", "lr"), ("opw", "wdf")):
+            assert _f32bits(getattr(sc, name)) == _f32bits(getattr(ref, rname)), (name, kw, lr, t)
+        assert sc.pow_mode == ref.pow_mode and sc.has_clip == ref.has_clip
+        aw = oracle_mod.bf16_to_f32(oracle_mod.f32_to_bf16(np.array([ref.a], np.float32)))[0] \
+            if foreach == 2 else np.float32(ref.a)
+        assert sc.lerp_small == int(abs(float(aw)) < 0.5)
+        coef = aw if sc.lerp_small else np.float32(aw) - np.float32(1.0)
+        assert _f32bits(sc.lerp_coef) == _f32bits(coef)
+    hp.foreach = 3
+    with pytest.raises(_lib.AdanaLibraryError, match="foreach"):
+        _lib.step_scalars(hp, 1e-3, 1)
+
+
 def test_host_scalars_reject_bad_input():
     from adana_amd import _lib
 
@@ -175,8 +215,13 @@ def test_mta_step_rejects_bad_arguments():
     pl = _lib.Plan(n_tensors=3, n_chunks=1, n_folds=3)
     assert L.adana_mta_step(ctypes.byref(pl), scp, 1, 0, None, 0, None, None) == -1
     assert "null pointer" in _lib.last_error()
-    assert L.adana_mta_step(ctypes.byref(pl), scp, 1, 0x80, None, 0, None, None) == -1
+    assert L.adana_mta_step(ctypes.byref(pl), scp, 1, 0x100, None, 0, None, None) == -1
     assert "variant flags" in _lib.last_error()
+    assert L.adana_mta_step(ctypes.byref(pl), scp, 1, _lib.FOREACH | _lib.VARIANT_MANAU, None, 0, None, None) == -1
+    assert "ADANA_FOREACH excludes" in _lib.last_error()
+    s16 = _lib.FOREACH | _lib.STATE_BF16 | _lib.GRAD_BF16 | _lib.NUMERICS_EAGER
+    assert L.adana_mta_step(ctypes.byref(pl), scp, 1, s16, None, 0, None, None) == -3
+    assert "not implemented" in _lib.last_error()
     fake = ctypes.c_void_p(0x1000)
     pl = _lib.Plan(desc=0x1000, vstart=0x1000, chunk_first=0x1000, fold_first=0x1000,
                    n_tensors=3, n_chunks=1, n_folds=3)
@@ -662,3 +707,19 @@ def test_scalar_fill_in_place(numerics):
         for k, (gi, t) in enumerate(classes):
             want = _lib.step_scalars(opt._hparams(opt.param_groups[gi]), opt.param_groups[gi]["lr"], t)
             assert bytes(ls.sc_arr[k]) == bytes(want), (wd, k)
+
+
+def test_foreach_eager_bf16_state_is_refused():
+    """use_foreach=True with numerics='eager' on bfloat16 parameters (without
+    master weights) is not implemented: the constructor says so, before any
+    step could run other numerics; float32 and master-weight lists build."""
+    import adana_amd
+
+    p = torch.nn.Parameter(torch.zeros(16, dtype=torch.bfloat16))
+    with pytest.raises(NotImplementedError, match="use_foreach"):
+        adana_amd.ADana([p], lr=1e-3, use_foreach=True, numerics="eager")
+    with pytest.raises(NotImplementedError, match="use_foreach"):
+        adana_amd.DANA_STAR_MK4([p], lr=1e-3, use_foreach=True, numerics="eager")
+    adana_amd.ADana([p], lr=1e-3, use_foreach=True)
+    adana_amd.ADana([p], lr=1e-3, use_foreach=True, numerics="eager", master_weights=True)
+    adana_amd.ADana([torch.nn.Parameter(torch.zeros(4))], lr=1e-3, use_foreach=True, numerics="eager")
