@@ -175,7 +175,7 @@ def test_bf16_state_classes_through_the_c_abi(oracle_mod, kappas, numerics):
 
 def test_integration_example_runs(oracle_mod):
     """The ctypes example of INTEGRATION.md section 2 runs as written against the built
-    library (ABI 7 plan with its gradient pointer array) and steps its tensor: the
+    library (a plan with its gradient pointer array) and steps its tensor: the
     diagnostics are finite and match the oracle's over the same ten steps."""
     import contextlib
     import io
