@@ -174,7 +174,7 @@ def cos_inf_schedule(n_iterations, n_warmup, div_factor, final_div_factor, n_inf
 C2_SCHEDULE = dict(n_iterations=200, n_warmup=4, div_factor=1e2, final_div_factor=1e-1, n_inf=0)
 
 
-def build_gpu(w, seed=0):
+def build_gpu(w, seed=0, foreach=False):
     import torch
     import adana_amd
 
@@ -205,7 +205,7 @@ def build_gpu(w, seed=0):
                 g.zero_()
             p.grad = g.to(pdtype)
     cls = adana_amd.DANA_STAR_MK4 if w["star"] else adana_amd.ADana
-    opt = cls(groups, master_weights=w["master"], **w["hp"])
+    opt = cls(groups, master_weights=w["master"], use_foreach=foreach, **w["hp"])
     return opt, params
 
 
@@ -949,6 +949,8 @@ def main():
     ap.add_argument("--no-ceiling-probe", action="store_true",
                     help="skip the 5-read/4-write stream probe reported as roofline.mix_ceiling")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--foreach", action="store_true",
+                    help="step with use_foreach=True (the reference's foreach path's numerics)")
     args = ap.parse_args()
     if args.warmup is None:
         args.warmup = workload(args.workload).get("default_warmup", 3) if args.workload in STEP_WORKLOADS else 3
@@ -974,7 +976,7 @@ def main():
     w = workload(args.workload)
     print(f"[bench] workload {w['name']} ({w['optimizer']}): building on cuda:0", file=sys.stderr,
           flush=True)
-    opt, params = build_gpu(w)
+    opt, params = build_gpu(w, foreach=args.foreach)
     n_elems = sum(p.numel() for p in params)
     bpe = bytes_per_elem(w)
     algo_bytes = n_elems * bpe
@@ -1118,7 +1120,8 @@ def main():
                    "tensors": len(params), "bytes_per_elem": bpe,
                    "algorithmic_bytes_per_step": algo_bytes, "grads": w["grad_note"],
                    "hyperparams": w["hp"], "master_weights": w["master"],
-                   "numerics": "compiled (the reference's default torch.compile path)",
+                   "numerics": ("compiled, use_foreach=True (the reference's foreach kernel under torch.compile)"
+                                if args.foreach else "compiled (the reference's default torch.compile path)"),
                    "parallelism": "single GPU",
                    **({"warmup_note": w["warmup_note"]} if "warmup_note" in w else {}),
                    **({"lr_schedule": dict(C2_SCHEDULE, kind="cos_inf (src/optim/schedule.py:70-98)",
