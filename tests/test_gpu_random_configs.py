@@ -15,7 +15,10 @@ src/optim/dana_star_mk4.py:137-203) to the bars of test_gpu_parity.py: m, v
 and tau bit-exact, p bit-exact (Dana-Star: at most 2 hard-case elements per
 tensor, within 2 scaled ulp), diagnostics rtol 1e-5.  A second sweep runs
 the same draws on the reference's own bfloat16 path, a third with
-clip_grad_norm_ fused into every step.
+clip_grad_norm_ fused into every step, and a fourth with use_foreach=True
+(the reference's foreach path, src/optim/adana.py:229-370,
+src/optim/dana_star_mk4.py:298-536) on float32, bf16-master and bfloat16
+state.
 """
 import numpy as np
 import pytest
@@ -61,8 +64,19 @@ def _draw(seed):
 
 @pytest.mark.parametrize("seed", range(48))
 def test_random_configuration(oracle_mod, seed):
+    _random_configuration(oracle_mod, seed, foreach=False)
+
+
+@pytest.mark.parametrize("seed", range(16))
+def test_random_configuration_foreach(oracle_mod, seed):
+    """Other draws with use_foreach=True, against the oracle's foreach mode."""
+    _random_configuration(oracle_mod, 300 + seed, foreach=True)
+
+
+def _random_configuration(oracle_mod, seed, foreach):
     O = oracle_mod
     rng, star, master, groups, hp = _draw(seed)
+    hp["foreach"] = foreach
     shapes = [s for ss, _ in groups for s in ss]
     print(f"case: random configuration seed {seed}: star {star} master {master} groups {len(groups)} "
           f"tensors {len(shapes)} elements {sum(int(np.prod(s)) for s in shapes)} {hp}", flush=True)
@@ -100,24 +114,38 @@ def test_random_configuration_bf16_state(oracle_mod, seed):
     oracle's bfloat16 restatement to the bars of test_gpu_bf16.py: m, v, tau
     bit-exact, p bit-exact (Dana-Star: at most 2 elements per tensor within 1
     bfloat16 ulp), diagnostics within 1 bfloat16 ulp."""
+    _random_configuration_bf16_state(oracle_mod, 100 + seed, foreach=False)
+
+
+@pytest.mark.parametrize("seed", range(8))
+def test_random_configuration_bf16_state_foreach(oracle_mod, seed):
+    """Other draws on bfloat16 state with use_foreach=True (compiled, the
+    form the reference runs), against the oracle's foreach mode."""
+    _random_configuration_bf16_state(oracle_mod, 400 + seed, foreach=True)
+
+
+def _random_configuration_bf16_state(oracle_mod, seed, foreach):
     import adana_amd
     from test_gpu_bf16 import _bits, _check, _diag_close, _to_gpu16
     from test_gpu_parity import STAR_HARD_CASES
 
     O = oracle_mod
-    rng, star, _, groups, hp = _draw(100 + seed)
+    rng, star, _, groups, hp = _draw(seed)
+    if foreach:
+        hp["numerics"] = "compiled"
     shapes = [s for ss, _ in groups for s in ss]
-    print(f"case: random bf16-state configuration seed {seed}: star {star} groups {len(groups)} "
+    print(f"case: random bf16-state configuration seed {seed} foreach {foreach}: star {star} groups {len(groups)} "
           f"tensors {len(shapes)} elements {sum(int(np.prod(s)) for s in shapes)} {hp}", flush=True)
     host = [[O.f32_to_bf16(_normal(rng, s, 0.02)) for s in ss] for ss, _ in groups]
     gpu = [[torch.nn.Parameter(_to_gpu16(h)) for h in hs] for hs in host]
     cls = adana_amd.DANA_STAR_MK4 if star else adana_amd.ADana
-    opt = cls([dict(params=ps, **gkw) for ps, (_, gkw) in zip(gpu, groups)], **hp)
+    opt = cls([dict(params=ps, **gkw) for ps, (_, gkw) in zip(gpu, groups)], use_foreach=foreach, **hp)
     orc = O.OracleOptimizer(
         groups=[O.OracleGroup(params=hs, lr=gkw["lr"], delta=gkw["delta"], epsilon=gkw["epsilon"],
                               weight_decay=gkw["weight_decay"]) for hs, (_, gkw) in zip(host, groups)],
         star=star, peak_lr=hp["lr"], kappa=hp["kappa"], clipsnr=hp["clipsnr"], wd_decaying=hp["wd_decaying"],
-        wd_ts=hp["wd_ts"], gamma_3_factor=hp["gamma_3_factor"], bf16=True, numerics=hp["numerics"])
+        wd_ts=hp["wd_ts"], gamma_3_factor=hp["gamma_3_factor"], bf16=True, numerics=hp["numerics"],
+        foreach=foreach)
     keys = ("m", "v", "tau") if star else ("m", "v")
     for k in range(7):
         for g, og, (_, gkw) in zip(opt.param_groups, orc.groups, groups):
@@ -162,11 +190,13 @@ def test_random_configuration_with_clipping(oracle_mod, seed):
     optimizer before every step, its scaling fused into the step: max_norm
     drawn around the gradients' norm (clipping or not), the clipped gradient
     written back or not; the total norm, the written-back gradients and the
-    step checked against the oracle's clip (torch's formula) and step."""
+    step checked against the oracle's clip (torch's formula) and step; every
+    fourth seed with use_foreach=True."""
     from test_gpu_clip import _clipped_pair_step
 
     O = oracle_mod
     rng, star, master, groups, hp = _draw(200 + seed)
+    hp["foreach"] = seed % 4 == 3
     if sum(int(np.prod(s)) for ss, _ in groups for s in ss) == 0:
         groups[0][0].append((100,))                      # something to clip
     write_back = bool(rng.integers(2))
