@@ -828,6 +828,18 @@ int scan_parallel(TableData &d, ScanPool &P, int parts, size_t *lo, size_t *hi) 
         ++P.gen;
     }
     P.cv.notify_all();
+    // From here on the helpers wait for a decision: however this function
+    // leaves (an exception included), they get one and finish before it returns.
+    struct Settle {
+        ScanPool &P;
+        int parts;
+        bool done = false;
+        ~Settle() {
+            if (done) return;
+            P.decision.store(2, std::memory_order_release);
+            while (P.finished.load(std::memory_order_acquire) < parts) cpu_relax();
+        }
+    } settle{P, parts};
     // Exact-int counters advance now and are put back if a row does not fit;
     // any other kind of counter waits for the checks (adding to it may run
     // Python code, which must not run while the helpers read the tensors).
@@ -840,6 +852,7 @@ int scan_parallel(TableData &d, ScanPool &P, int parts, size_t *lo, size_t *hi) 
     const bool go = fits && arc == 0;
     P.decision.store(go ? 1 : 2, std::memory_order_release);
     while (P.finished.load(std::memory_order_acquire) < parts) cpu_relax();
+    settle.done = true;
     if (!go) {
         if (arc == 0) restore_steps(state, d.saved);
         return arc < 0 ? -1 : 0;
