@@ -174,7 +174,7 @@ def test_bf16_state_classes_through_the_c_abi(oracle_mod, kappas, numerics):
 
 
 def test_integration_example_runs(oracle_mod):
-    """The ctypes example of INTEGRATION.md section 2 runs as written against the built
+    """The ctypes example of the integration guide's section 2 runs as written against the built
     library (a plan with its gradient pointer array) and steps its tensor: the
     diagnostics are finite and match the oracle's over the same ten steps."""
     import contextlib
@@ -183,7 +183,7 @@ def test_integration_example_runs(oracle_mod):
     import re
 
     O = oracle_mod
-    print("case: INTEGRATION.md ctypes example", flush=True)
+    print("case: integration guide ctypes example", flush=True)
     text = open(os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "INTEGRATION.md")).read()
     section = text[text.index("## 2. C ABI"):]
     code = re.search(r"```python\n(.*?)```", section, re.S).group(1)
