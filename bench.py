@@ -338,6 +338,11 @@ def compiled_leg(w, ps, tg, total, bpe, timed, cores, max_shapes=8):
     tdt = tg[0][0].dtype
     print(f"[bench] compiling the reference's update with torch.compile for {len(shapes)} shapes",
           file=sys.stderr, flush=True)
+    import torch._inductor.config as inductor_config
+
+    # compile in this process: no compile-worker subprocesses started from a
+    # process that holds the GPU
+    inductor_config.compile_threads = 1
     try:
         wrappers = {}
 
