@@ -205,9 +205,13 @@ __device__ __forceinline__ float pow_aten(float x, const adana_step_scalars &sc,
 //                lerp rounds m and tau to bfloat16 (its coefficient comes
 //                from alpha rounded to bfloat16, set by the host), the tau
 //                update is read rounded, the rest is binary32, and the
-//                averaged alpha factor and mfac are the bfloat16 tensors.
-enum Numerics { NUM_COMPILED = 0, NUM_EAGER = 1, NUM_FOREACH = 2, NUM_FOREACH16 = 3 };
-constexpr bool is_foreach(int num) { return num == NUM_FOREACH || num == NUM_FOREACH16; }
+//                averaged alpha factor and mfac are the bfloat16 tensors;
+//  NUM_FOREACH_EAGER16 that path's eager ops on bfloat16 state, every op
+//                rounded to bfloat16 (update_n16).
+enum Numerics { NUM_COMPILED = 0, NUM_EAGER = 1, NUM_FOREACH = 2, NUM_FOREACH16 = 3, NUM_FOREACH_EAGER16 = 4 };
+constexpr bool is_foreach(int num) { return num >= NUM_FOREACH; }
+// bfloat16 state with every op rounded to bfloat16 (the eager ATen forms)
+constexpr bool rounds_every_op(int num) { return num == NUM_EAGER || num == NUM_FOREACH_EAGER16; }
 
 // m.lerp_(grad, alpha) with w = alpha, c = (|w| < 0.5 ? w : w - 1) (w - 1 is
 // precomputed, exact) and b = (|w| < 0.5 ? self : end).  ATen (eager, and
@@ -477,23 +481,86 @@ __global__ __launch_bounds__(256) void pow16_fill_kernel(unsigned short *__restr
     tab[k] = f32_to_bf16(pow16<POW_GENERAL>(x, sc, q, PowTab{adana::kLog, adana::kExp2J, nullptr}));
 }
 
-template <bool STAR, int POWK, int N>
+// The foreach path's eager ops on bfloat16 state (src/optim/adana.py:316-368,
+// src/optim/dana_star_mk4.py:425-528, torch.compile off): every op rounded to
+// bfloat16 with the operand rules above, and two of the foreach ops' own: the
+// in-place _foreach_mul_ by gamma_3_factor takes it rounded to bfloat16
+// (q.c3_16; the out-of-place products do not round their Python scalars),
+// and the epsilon added, in place or not, is rounded too (q.eps16).  The
+// float32 0-d factors second in a product (1 - alpha, alpha, lr, wdf) keep
+// their binary32 values.  The host passes min_p, ADana's power and wdf as the
+// reference's 0-d results (bfloat16 step, foreach_scalars).
+__device__ __forceinline__ float adana_elem16fe(float p, float g, float &m, float &v, const adana_step_scalars &sc,
+                                                const Scalars16 &q, float (&acc)[4]) {
+    const float mn = rb(__builtin_fmaf(q.lerp_coef16, g - m, q.lerp_small16 ? m : g));   // _foreach_lerp_
+    float vn = rb(v * sc.oma);                                                          // _foreach_mul_
+    vn = rb(vn + rb(rb(g * g) * sc.a));                                                 // mul, mul, add_
+    const float nt = rb(adana::div_bf16(1.0f, rb(rb(adana::sqrt_bf16(vn)) + q.eps16)));   // sqrt, add, recip
+    const float mfac = rb(fabsf(mn) * nt);
+    float af = rb(sc.pw * mfac);                                                        // pow (0-d), mul
+    if (sc.has_clip) af = clamp_max(af, q.clip16);
+    const float inner = rb(rb(rb(sign_f(mn) * af) + rb(mn * nt)) * q.c3_16);           // ..., mul_(gamma)
+    const float upd = rb(rb(inner * sc.cg2) + rb(rb(g * nt) * sc.cg2));                // mul(g3), g2, add
+    float pn = rb(p - upd);                                                             // neg_, add_
+    pn = pn + rb(pn * sc.opw);  // mul, add_ (rounded to bfloat16 by the store)
+    m = mn;
+    v = vn;
+    accumulate(acc, af, g, mfac, mn);
+    return pn;
+}
+
+__device__ __forceinline__ StarMid star16fe_phase_a(float g, float m, float v, float tau, const adana_step_scalars &sc,
+                                                    const Scalars16 &q) {
+    StarMid o;
+    o.m = rb(__builtin_fmaf(q.lerp_coef16, g - m, q.lerp_small16 ? m : g));            // _foreach_lerp_
+    o.v = rb(v * sc.oma);                                                               // _foreach_mul_
+    o.v = rb(o.v + rb(rb(g * g) * sc.a));                                               // mul, mul, add_
+    const float sv = rb(adana::sqrt_bf16(o.v));
+    o.se = rb(sv + q.eps16);                                                            // norm_den
+    const float ag = fabsf(g);
+    const float tu = rb(adana::div_bf16(ag, rb(rb(ag + sv) + q.eps16)));                // add, add_, div
+    o.tau = rb(__builtin_fmaf(q.lerp_coef16, tu - tau, q.lerp_small16 ? tau : tu));    // _foreach_lerp_
+    const float ct = clamp_max(o.tau, 0.5f);
+    const float pe = rb(adana::div_bf16(ct, rb(1.0f - ct)));                            // neg, add_, div
+    o.tr = clamp_min(pe, sc.min_p);                                                     // maximum
+    o.et = clamp_min(rb(o.tau * sc.s), 1.0f);                                           // mul, maximum
+    return o;
+}
+
+__device__ __forceinline__ float star16fe_phase_b(float p, float g, const StarMid &a, float pw,
+                                                  const adana_step_scalars &sc, const Scalars16 &q, float (&acc)[4]) {
+    const float nt = rb(adana::div_bf16(rb(adana::sqrt_bf16(a.tr)), a.se));             // sqrt, div
+    const float mfac = rb(nt * rb(adana::div_bf16(fabsf(a.m), a.tr)));                 // abs, div, mul
+    float af = rb(pw * mfac);                                                           // pow, mul
+    if (sc.has_clip) af = clamp_max(af, q.clip16);
+    const float g3i = rb(rb(rb(a.tr * sign_f(a.m)) * af) + rb(a.m * nt));
+    const float upd = rb(rb(rb(g3i * q.c3_16) * sc.cg2) + rb(rb(g * nt) * sc.cg2));    // mul_(gamma), g3, g2
+    float pn = rb(p - upd);                                                             // neg_, add_
+    pn = pn + rb(pn * sc.opw);  // mul, add_ (rounded to bfloat16 by the store)
+    accumulate(acc, af, g, mfac, a.m);
+    return pn;
+}
+
+template <bool STAR, int POWK, int N, bool FE = false>
 __device__ __forceinline__ void update_n16(float (&P)[N], const float (&G)[N], float (&M)[N], float (&V)[N],
                                            float (&T)[N], const adana_step_scalars &sc, const Scalars16 &q,
                                            const PowTab &tab, float (&acc)[4]) {
     if constexpr (!STAR) {
 #pragma unroll
-        for (int k = 0; k < N; ++k) P[k] = adana_elem16(P[k], G[k], M[k], V[k], sc, q, acc);
+        for (int k = 0; k < N; ++k)
+            P[k] = FE ? adana_elem16fe(P[k], G[k], M[k], V[k], sc, q, acc) : adana_elem16(P[k], G[k], M[k], V[k], sc, q, acc);
     } else {
         StarMid a[N];
 #pragma unroll
-        for (int k = 0; k < N; ++k) a[k] = star16_phase_a(G[k], M[k], V[k], T[k], sc, q);
+        for (int k = 0; k < N; ++k)
+            a[k] = FE ? star16fe_phase_a(G[k], M[k], V[k], T[k], sc, q) : star16_phase_a(G[k], M[k], V[k], T[k], sc, q);
         float pw[N];
 #pragma unroll
         for (int k = 0; k < N; ++k) pw[k] = pow16<POWK>(a[k].et, sc, q, tab);
 #pragma unroll
         for (int k = 0; k < N; ++k) {
-            P[k] = star16_phase_b(P[k], G[k], a[k], pw[k], sc, q, acc);
+            P[k] = FE ? star16fe_phase_b(P[k], G[k], a[k], pw[k], sc, q, acc)
+                      : star16_phase_b(P[k], G[k], a[k], pw[k], sc, q, acc);
             M[k] = a[k].m;
             V[k] = a[k].v;
             T[k] = a[k].tau;
@@ -799,7 +866,7 @@ __device__ __forceinline__ void thread_elems(const adana_tensor_desc &d, const v
     const int cnt = left < VEC ? static_cast<int>(left) : VEC;
     // the descriptor's flag covers every pointer but the gradient's
     const bool vec_ok = (d.flags & ADANA_DESC_VEC_OK) && grad_vec_aligned<GBF16>(grad);
-    if constexpr (PM == PM_BF16 && NUM != NUM_EAGER) {
+    if constexpr (PM == PM_BF16 && !rounds_every_op(NUM)) {
         // the compiled paths on bfloat16 state: binary32 throughout (but for
         // the foreach path's lerps), the four stored results rounded to
         // bfloat16 (round to nearest even)
@@ -869,7 +936,7 @@ __device__ __forceinline__ void thread_elems(const adana_tensor_desc &d, const v
                 for (int k = 0; k < VEC; ++k) G[k] = scale_grad<true>(G[k], gs);
                 if (pack.write_grad) store_grad_n<true, VEC>(grad, off, G);
             }
-            update_n16<STAR, POWK, VEC>(P, G, M, V, T, sc, q, tab, acc);
+            update_n16<STAR, POWK, VEC, NUM == NUM_FOREACH_EAGER16>(P, G, M, V, T, sc, q, tab, acc);
             st_bf16_n<VEC>(pp, P);
             st_bf16_n<VEC>(mp, M);
             st_bf16_n<VEC>(vp, V);
@@ -883,7 +950,7 @@ __device__ __forceinline__ void thread_elems(const adana_tensor_desc &d, const v
                     G[0] = scale_grad<true>(G[0], gs);
                     if (pack.write_grad) store_grad1<true>(grad, off + e, G[0]);
                 }
-                update_n16<STAR, POWK, 1>(P, G, M, V, T, sc, q, tab, acc);
+                update_n16<STAR, POWK, 1, NUM == NUM_FOREACH_EAGER16>(P, G, M, V, T, sc, q, tab, acc);
                 pp[e] = f32_to_bf16(P[0]);
                 mp[e] = f32_to_bf16(M[0]);
                 vp[e] = f32_to_bf16(V[0]);
@@ -961,7 +1028,7 @@ __device__ __forceinline__ bool thread_groups_uniform(const adana_tensor_desc &d
                                                       int64_t left, int64_t seg0, int span, const ScalarPack &pack,
                                                       float gs, const PowTab &tab, float (&acc)[4]) {
     static_assert(VEC == 4, "grouped path: 16-byte vectors");
-    if constexpr (PM != PM_BF16 || NUM == NUM_EAGER || GROUPS == 1) {
+    if constexpr (PM != PM_BF16 || rounds_every_op(NUM) || GROUPS == 1) {
         return false;
     } else {
         const bool vec_ok = (d.flags & ADANA_DESC_VEC_OK) && grad_vec_aligned<GBF16>(grad);
@@ -1754,8 +1821,8 @@ void launch_pow(int powk, const LaunchArgs &a, const ScalarPack &pack) {
         launch_main<true, GBF16, PM, POW_ONE, NUM>(a, pack);
     } else if (powk == POW_SPECIAL) {
         launch_main<true, GBF16, PM, POW_SPECIAL, NUM>(a, pack);
-    } else if constexpr (PM == PM_BF16 && NUM == NUM_EAGER) {
-        if (powk == POW_TABLE16) launch_main<true, GBF16, PM, POW_TABLE16, NUM_EAGER>(a, pack);
+    } else if constexpr (PM == PM_BF16 && rounds_every_op(NUM)) {
+        if (powk == POW_TABLE16) launch_main<true, GBF16, PM, POW_TABLE16, NUM>(a, pack);
     } else if constexpr (!GBF16 && PM == PM_F32 && NUM == NUM_EAGER) {  // Manau's branch: float32, its own op order
         if (powk == POW_MANAU_GENERAL) {
             launch_main<true, false, PM_F32, POW_MANAU_GENERAL, NUM_EAGER>(a, pack);
@@ -1769,16 +1836,18 @@ void launch_pow(int powk, const LaunchArgs &a, const ScalarPack &pack) {
     }
 }
 
-// The launch's numerics: the foreach instance of the state's kind (float32
-// state, or bfloat16 state under torch.compile).
+// The launch's numerics (num: NUM_COMPILED, NUM_EAGER, or NUM_FOREACH for
+// the foreach path, whose instance depends on the state's kind: float32
+// state, or bfloat16 state compiled or eager).
 template <bool STAR, bool GBF16, int PM>
-void launch_num(int num, int powk, const LaunchArgs &a, const ScalarPack &pack) {
+void launch_num(int num, bool eager, int powk, const LaunchArgs &a, const ScalarPack &pack) {
     if (num == NUM_EAGER) {
         launch_pow<STAR, GBF16, PM, NUM_EAGER>(powk, a, pack);
     } else if (num == NUM_COMPILED) {
         launch_pow<STAR, GBF16, PM, NUM_COMPILED>(powk, a, pack);
     } else if constexpr (PM == PM_BF16) {
-        launch_pow<STAR, GBF16, PM, NUM_FOREACH16>(powk, a, pack);
+        if (eager) launch_pow<STAR, GBF16, PM, NUM_FOREACH_EAGER16>(powk, a, pack);
+        else launch_pow<STAR, GBF16, PM, NUM_FOREACH16>(powk, a, pack);
     } else {
         launch_pow<STAR, GBF16, PM, NUM_FOREACH>(powk, a, pack);
     }
@@ -1879,6 +1948,17 @@ int foreach_scalars(adana_step_scalars *out, const adana_hparams *hp, double lr,
     out->cg2 = static_cast<float>(lr);                           // :172-173 g2, g3
     const float nws = (-static_cast<float>(hp->weight_decay)) * sf;   // :360 / :363
     out->opw = hp->wd_decaying ? (1.0f / (s / static_cast<float>(hp->wd_ts) + 1.0f)) * nws : nws;  // :357-365
+    if (hp->foreach == 2 && hp->eager) {
+        // eager 0-d ops on the bfloat16 step tensor, each rounded to bfloat16;
+        // the pow's exponent rounded to bfloat16; wdf the float32 product of
+        // the bfloat16 decay and the float32 (-wd) * sf, or without decay
+        // that factor as bfloat16 (.to(p.dtype), :364)
+        const auto rb = [](float x) { return adana::bf16_round_int(x); };
+        const float ops = rb(s + 1.0f);
+        out->min_p = rb(1.0f / ops);
+        out->pw = rb(pow0d(ops, static_cast<double>(rb(static_cast<float>(1.0 - hp->kappa)))));
+        out->opw = hp->wd_decaying ? rb(1.0f / rb(rb(s / static_cast<float>(hp->wd_ts)) + 1.0f)) * nws : rb(nws);
+    }
     out->star_exp = static_cast<float>(1.0 - hp->kappa);         // dana_star_mk4.py:480
     if (hp->eager) {
         out->pow_mode = pow_mode_of(1.0 - hp->kappa);
@@ -2083,9 +2163,6 @@ int step_impl(const char *fn, const adana_plan *plan, const adana_step_scalars *
     const bool foreach = variant_flags & ADANA_FOREACH;
     if (foreach && manau)
         return adana_set_error(ADANA_E_INVALID, "%s: ADANA_FOREACH excludes ADANA_VARIANT_MANAU", fn);
-    if (foreach && s16 && (variant_flags & ADANA_NUMERICS_EAGER))
-        return adana_set_error(ADANA_E_UNSUPPORTED, "%s: the foreach path's eager ops on bfloat16 state "
-                               "(ADANA_FOREACH | ADANA_STATE_BF16 | ADANA_NUMERICS_EAGER) are not implemented", fn);
     if (int rc = check_plan_arrays(pl, fn)) return rc;
     if (pl.n_tensors == 0) return ADANA_OK;
     if (!d_workspace || !d_diag || !h_scalars)
@@ -2150,7 +2227,7 @@ int step_impl(const char *fn, const adana_plan *plan, const adana_step_scalars *
         }
         const LaunchArgs la{pl.n_chunks, st, pl.desc, pl.grad, pl.vstart, pl.chunk_first, n, partials, counters};
         const int num = foreach ? NUM_FOREACH : ((eager || manau) ? NUM_EAGER : NUM_COMPILED);
-#define ADANA_LAUNCH(S, G, P) launch_num<S, G, P>(num, powk, la, pack)
+#define ADANA_LAUNCH(S, G, P) launch_num<S, G, P>(num, eager, powk, la, pack)
         if (star || manau) {
             if (s16) ADANA_LAUNCH(true, true, PM_BF16);
             else if (gb) { if (pb) ADANA_LAUNCH(true, true, PM_MASTER); else ADANA_LAUNCH(true, true, PM_F32); }

@@ -35,8 +35,7 @@ maximum, mfac = nt * (|m| / tau_reg), g2 and g3 scaled last, weight decay as
 p + p * wdf) with its own scalars (alpha as a binary32 quotient, the step in
 the parameters' dtype).  The step is still one launch.  As in the
 reference, the choice is made at construction; ``numerics="eager"`` with it
-is the same path's kernel run eagerly (float32 and master-weight state; not
-implemented for bfloat16 state).
+is the same path's kernel run as eager ops.
 
 What differs is how a step executes.  The reference loops over tensors in
 Python, makes six 0-d device tensors per tensor and calls a torch.compile'd
@@ -172,12 +171,6 @@ class _DanaFamily(Optimizer):
         self.numerics = numerics
         # the reference picks its foreach kernel in the constructor (adana.py:63-70)
         self._foreach = bool(getattr(self, "use_foreach", False))
-        if self._foreach and numerics == "eager" and not self.master_weights and any(
-                p.dtype == torch.bfloat16 for g in self.param_groups for p in g["params"]):
-            raise NotImplementedError(f"{type(self).__name__}: use_foreach=True with numerics='eager' on "
-                                      "bfloat16 parameters (the foreach path's eager ops on bfloat16 state) is not "
-                                      "implemented; the default numerics='compiled' is the path the reference "
-                                      "runs with use_foreach=True")
         self._diag_cols = [tuple(c) for c in self._DIAG_COLUMNS]
         self._sets: Optional[List[_LaunchSet]] = None
         self._structure = None
@@ -434,9 +427,6 @@ class _DanaFamily(Optimizer):
             # master_weights: float32 master and moments (extension); otherwise the
             # reference's own bfloat16 path, m, v, tau bfloat16 as zeros_like(p) makes them
             flags |= _lib.GRAD_BF16 | (_lib.PARAM_BF16 if self.master_weights else _lib.STATE_BF16)
-            if self._foreach and self.numerics == "eager" and not self.master_weights:
-                raise NotImplementedError(f"{type(self).__name__}: use_foreach=True with numerics='eager' on "
-                                          "bfloat16 parameters is not implemented")
         else:
             raise NotImplementedError(f"{type(self).__name__}: parameter dtype {p.dtype}")
         return flags

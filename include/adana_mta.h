@@ -123,10 +123,11 @@ extern "C" {
                                     op forms (no addcmul, ATen's lerp in both
                                     modes, tau_reg = maximum(p_est, min_p),
                                     mfac = nt * (|m| / tau_reg), p += p * wdf)
-                                    and scalars (adana_hparams.foreach).  With
-                                    ADANA_STATE_BF16: the compiled form only
-                                    (m and tau rounded to bfloat16 by ATen's
-                                    lerp, the rest binary32); excludes
+                                    and scalars (adana_hparams.foreach), with
+                                    either numerics (compiled on bfloat16
+                                    state: m and tau rounded to bfloat16 by
+                                    ATen's lerp, the rest binary32; eager:
+                                    every op rounded); excludes
                                     ADANA_VARIANT_MANAU                       */
 
 /* adana_tensor_desc.flags */

@@ -409,6 +409,75 @@ static inline float star_elem_fe(float p, float g, float *mp, float *vp, float *
     return p;
 }
 
+/* The foreach path's eager ops on bfloat16 tensors (torch.compile off):
+ * every op rounded to bfloat16 as ATen's kernels do, with the operand rules
+ * of the per-tensor eager path above, and two of the foreach ops' own: an
+ * in-place _foreach_mul_ by a Python scalar takes the scalar rounded to
+ * bfloat16 (gamma_3_factor), an out-of-place one does not; a Python scalar
+ * added (epsilon) is rounded to bfloat16 in every form.  A 0-d float32
+ * tensor second in a multiplication (1 - alpha, alpha, lr, the weight-decay
+ * factor) keeps its binary32 value.  Scalars (oracle.foreach_scalars with a
+ * bfloat16 step, eager): min_p and ADana's power are the bfloat16 0-d
+ * results, wdf the float32 0-d product (or, without decay, the bfloat16
+ * copy).  (Probed op by op against torch 2.10, pinned by the reference's
+ * own run, tests/golden/<case>.bf16_foreach_eager.npz.) */
+static inline float adana_elem_fe16e(float p, float g, float *mp, float *vp, const adana_oracle_scalars *sc,
+                                     double acc[4]) {
+    const float a16 = rb(sc->a), e16 = rb(sc->eps);
+    float m = rb(o_lerp(*mp, g, a16, 0));                    /* _foreach_lerp_ */
+    float v = rb(*vp * sc->oma);                             /* _foreach_mul_(vs, 1 - alpha) */
+    v = rb(v + rb(rb(g * g) * sc->a));                       /* mul, mul, add_ */
+    float nt = rb(1.0f / rb(rb(sqrtf(v)) + e16));            /* sqrt, add(eps), reciprocal */
+    float mf = rb(fabsf(m) * nt);
+    float af = rb(sc->pw * mf);                              /* pow (0-d, bfloat16), mul */
+    if (sc->has_clip) af = o_clamp_max(af, rb(sc->clip));
+    float g3i = rb(rb(o_sign(m) * af) + rb(m * nt));         /* sign, mul, mul, add */
+    g3i = rb(g3i * rb(sc->g3f));                             /* _foreach_mul_(., gamma_3_factor) */
+    float upd = rb(rb(g3i * sc->lr) + rb(rb(g * nt) * sc->lr));   /* mul(g3), mul, mul(g2), add */
+    p = rb(p - upd);                                         /* neg_, add_ */
+    p = rb(p + rb(p * sc->wdf));                             /* mul, add_ */
+    *mp = m;
+    *vp = v;
+    acc[0] += (double)af;
+    acc[1] += (double)g * (double)g;
+    acc[2] += (double)mf;
+    acc[3] += (double)m * (double)m;
+    return p;
+}
+
+static inline float star_elem_fe16e(float p, float g, float *mp, float *vp, float *tp,
+                                    const adana_oracle_scalars *sc, double acc[4]) {
+    const float a16 = rb(sc->a), e16 = rb(sc->eps);
+    float m = rb(o_lerp(*mp, g, a16, 0));                    /* _foreach_lerp_ */
+    float v = rb(*vp * sc->oma);                             /* _foreach_mul_(vs, 1 - alpha) */
+    v = rb(v + rb(rb(g * g) * sc->a));                       /* mul, mul, add_ */
+    float sv = rb(sqrtf(v));
+    float ag = fabsf(g);
+    float tu = rb(ag / rb(rb(ag + sv) + e16));               /* add, add_(eps), div */
+    float tau = rb(o_lerp(*tp, tu, a16, 0));                 /* _foreach_lerp_ */
+    float ct = o_clamp_max(tau, 0.5f);
+    float pe = rb(ct / rb(1.0f - ct));                       /* neg, add_(1.0), div */
+    float tr = o_maximum(pe, sc->min_p);                     /* maximum */
+    float et = o_maximum(rb(tau * sc->s), 1.0f);             /* mul, maximum(., ones) */
+    float nt = rb(rb(sqrtf(tr)) / rb(sv + e16));             /* sqrt, add(eps), div */
+    float mf = rb(nt * rb(fabsf(m) / tr));                   /* abs, div, mul */
+    float af = rb(o_pow16(et, rb(sc->star_exp), sc->pow_mode) * mf);   /* pow, mul */
+    if (sc->has_clip) af = o_clamp_max(af, rb(sc->clip));
+    float g3i = rb(rb(rb(tr * o_sign(m)) * af) + rb(m * nt)); /* sign, mul, mul, mul, add */
+    g3i = rb(g3i * rb(sc->g3f));                             /* _foreach_mul_(., gamma_3_factor) */
+    float upd = rb(rb(g3i * sc->lr) + rb(rb(g * nt) * sc->lr));   /* mul(g3), mul, mul(g2), add */
+    p = rb(p - upd);                                         /* neg_, add_ */
+    p = rb(p + rb(p * sc->wdf));                             /* mul, add_ */
+    *mp = m;
+    *vp = v;
+    *tp = tau;
+    acc[0] += (double)af;
+    acc[1] += (double)g * (double)g;
+    acc[2] += (double)mf;
+    acc[3] += (double)m * (double)m;
+    return p;
+}
+
 /* Parallel element loops.  Element results do not depend on the thread
  * count; the binary64 diagnostic sums may differ in the last bits. */
 #define DIAG_LOOP(BODY)                                                        \
@@ -471,7 +540,15 @@ void adana_oracle_step_g16(int64_t n, int32_t star, float *p, const uint16_t *g1
  * bfloat16 as ATen's bfloat16 kernels do (adana_elem16, star_elem16). */
 void adana_oracle_step_bf16(int64_t n, int32_t star, uint16_t *p, const uint16_t *g, uint16_t *m,
                             uint16_t *v, uint16_t *tau, const adana_oracle_scalars *sc, double diag[4]) {
-    if (sc->foreach && star) {             /* the foreach path under torch.compile */
+    if (sc->foreach && !sc->compiled && star) {     /* the foreach path's eager ops */
+        DIAG_LOOP(float mm = bf16_to_f32(m[i]); float vv = bf16_to_f32(v[i]); float tt = bf16_to_f32(tau[i]);
+                  p[i] = f32_to_bf16(star_elem_fe16e(bf16_to_f32(p[i]), bf16_to_f32(g[i]), &mm, &vv, &tt, sc, acc));
+                  m[i] = f32_to_bf16(mm); v[i] = f32_to_bf16(vv); tau[i] = f32_to_bf16(tt))
+    } else if (sc->foreach && !sc->compiled) {
+        DIAG_LOOP(float mm = bf16_to_f32(m[i]); float vv = bf16_to_f32(v[i]);
+                  p[i] = f32_to_bf16(adana_elem_fe16e(bf16_to_f32(p[i]), bf16_to_f32(g[i]), &mm, &vv, sc, acc));
+                  m[i] = f32_to_bf16(mm); v[i] = f32_to_bf16(vv))
+    } else if (sc->foreach && star) {      /* the foreach path under torch.compile */
         DIAG_LOOP(float mm = bf16_to_f32(m[i]); float vv = bf16_to_f32(v[i]); float tt = bf16_to_f32(tau[i]);
                   p[i] = f32_to_bf16(star_elem_fe(bf16_to_f32(p[i]), bf16_to_f32(g[i]), &mm, &vv, &tt, sc, 1, acc));
                   m[i] = f32_to_bf16(mm); v[i] = f32_to_bf16(vv); tau[i] = f32_to_bf16(tt))

@@ -309,7 +309,19 @@ def foreach_scalars(*, lr: float, peak_lr: float, delta: float, kappa: float, ep
     sc.g3f = f32(gamma_3_factor)                 # :350
     sc.lr = f32(lr)                              # :172-173 g2, g3
     nws = (-f32(weight_decay)) * sf              # :360 / :363
-    if wd_decaying:                              # :357-361
+    if step_bf16 and not compiled:
+        # eager 0-d ops on the bfloat16 step tensor, each rounded to bfloat16
+        def rb(x):
+            return bf16_to_f32(f32_to_bf16(np.array([x], np.float32)))[0]
+        ops = rb(st + f32(1.0))                  # :336 / dana_star_mk4.py:455
+        sc.min_p = rb(f32(1.0) / ops)            # dana_star_mk4.py:456
+        e16 = float(rb(f32(1.0 - kappa)))        # pow's exponent in bfloat16
+        sc.pw = rb(_pow0d(ops, e16))             # :339
+        if wd_decaying:                          # bfloat16 0-d quotient, float32 0-d product
+            sc.wdf = f32(rb(f32(1.0) / rb(rb(st / f32(wd_ts)) + f32(1.0)))) * nws
+        else:
+            sc.wdf = rb(nws)                     # :364 .to(p.dtype)
+    elif wd_decaying:                            # :357-361
         sc.wdf = (f32(1.0) / (st / f32(wd_ts) + f32(1.0))) * nws
     else:
         sc.wdf = nws
@@ -468,8 +480,8 @@ class OracleOptimizer:
     path, src/optim/adana.py:72-79, 210-216) or "eager" (its update run as
     ATen ops).  ``foreach``: the reference's use_foreach=True path
     (src/optim/adana.py:229-370, src/optim/dana_star_mk4.py:298-536), whose
-    kernel the reference compiles by default; on the bfloat16 path only that
-    compiled form is restated.
+    kernel the reference compiles by default (``numerics`` again selects
+    that compiled form or the kernel's eager ops).
     """
 
     groups: List[OracleGroup]
@@ -488,8 +500,6 @@ class OracleOptimizer:
 
     def step(self, grads: Sequence[Sequence[Optional[np.ndarray]]]) -> None:
         """``grads[gi][pi]`` is the gradient of group gi's param pi, or None."""
-        if self.foreach and self.bf16 and self.numerics != "compiled":
-            raise NotImplementedError("oracle: the foreach path's eager ops on bfloat16 tensors are not restated")
         for gi, group in enumerate(self.groups):
             sf = group.lr / self.peak_lr                       # adana.py:165
             group.weighted_step_count += sf                    # adana.py:167

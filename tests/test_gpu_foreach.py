@@ -5,7 +5,7 @@ tests/test_oracle_foreach.py pins to the reference's own foreach runs: the
 golden scenarios in both of the reference's modes (and, at the checkpoints,
 against the reference's fixtures themselves), C1's size, float32 and
 bf16-master lists that take the two-group launches, and the reference's
-bfloat16 path (compiled), including a tensor on the element-wise path.
+bfloat16 path in both modes, including a tensor on the element-wise path.
 Bars as in tests/test_gpu_parity.py and tests/test_gpu_bf16.py: m, v, tau
 bit-exact; ADana's p bit-exact; Dana-Star's p bit-exact but for the pow's
 hard cases (at most STAR_HARD_CASES elements per tensor per step)."""
@@ -103,18 +103,19 @@ def test_foreach_two_group_grid(oracle_mod, star, master):
 BF16_SIZES = [[37, 3 * 129, 40 * 17, 4099, 70_001], [9_000_000, 6_000_003, 5_000_001, 1027]]
 
 
+@pytest.mark.parametrize("numerics", ["compiled", "eager"])
 @pytest.mark.parametrize("sizes", BF16_SIZES, ids=["small", "grid"])
 @pytest.mark.parametrize("star", [False, True], ids=["adana", "star"])
-def test_foreach_bf16_state(oracle_mod, star, sizes):
-    """The reference's bfloat16 path with use_foreach=True (compiled): m, v,
-    tau bit-exact, p bit-exact but for Dana-Star's pow hard cases, the five
-    bfloat16 diagnostics within 1 bfloat16 ulp; 3 steps with the lr moving,
-    one tensor a view 2 bytes into a buffer (the element-wise path), two
-    groups (weight decay on the first)."""
+def test_foreach_bf16_state(oracle_mod, star, sizes, numerics):
+    """The reference's bfloat16 path with use_foreach=True, compiled and
+    eager: m, v, tau bit-exact, p bit-exact but for Dana-Star's pow hard
+    cases, the five bfloat16 diagnostics within 1 bfloat16 ulp; 3 steps with
+    the lr moving, one tensor a view 2 bytes into a buffer (the element-wise
+    path), two groups (weight decay on the first)."""
     import adana_amd
 
     O = oracle_mod
-    print(f"case: foreach bf16 state star {star} sizes {sizes}", flush=True)
+    print(f"case: foreach bf16 state star {star} sizes {sizes} {numerics}", flush=True)
     rng = np.random.default_rng(34)
     host = [O.f32_to_bf16(rng.normal(0, 0.02, n).astype(np.float32)) for n in sizes]
     gpu = []
@@ -129,11 +130,12 @@ def test_foreach_bf16_state(oracle_mod, star, sizes):
     hp = dict(lr=1e-3, delta=8.0, kappa=0.85, clipsnr=2.0, wd_decaying=True, wd_ts=10.0, gamma_3_factor=0.7)
     cls = adana_amd.DANA_STAR_MK4 if star else adana_amd.ADana
     opt = cls([dict(params=gpu[:3], weight_decay=0.1), dict(params=gpu[3:], weight_decay=0.0)],
-              use_foreach=True, **hp)
+              use_foreach=True, numerics=numerics, **hp)
     orc = O.OracleOptimizer(groups=[O.OracleGroup(params=host[:3], lr=hp["lr"], weight_decay=0.1),
                                     O.OracleGroup(params=host[3:], lr=hp["lr"], weight_decay=0.0)],
                             star=star, peak_lr=hp["lr"], kappa=hp["kappa"], clipsnr=hp["clipsnr"], wd_decaying=True,
-                            wd_ts=hp["wd_ts"], gamma_3_factor=hp["gamma_3_factor"], bf16=True, foreach=True)
+                            wd_ts=hp["wd_ts"], gamma_3_factor=hp["gamma_3_factor"], bf16=True, foreach=True,
+                            numerics=numerics)
     for t in range(1, 4):
         lr = 1e-3 * (1.0 - 0.2 * t)
         for g, og in zip(opt.param_groups, orc.groups):
@@ -146,7 +148,7 @@ def test_foreach_bf16_state(oracle_mod, star, sizes):
         torch.cuda.synchronize()
         for i, p in enumerate(gpu):
             st, ost = opt.state[p], orc.state[id(host[i])]
-            tag = f"foreach bf16 star {star} t={t} tensor {i} (n={sizes[i]})"
+            tag = f"foreach bf16 {numerics} star {star} t={t} tensor {i} (n={sizes[i]})"
             for key in ("m", "v", "tau") if star else ("m", "v"):
                 _check(_bits(st[key]), ost[key], f"{tag} {key}")
             got = _bits(p)
@@ -155,3 +157,40 @@ def test_foreach_bf16_state(oracle_mod, star, sizes):
             _diag_close([float(st[key]) for key in O.DIAG_KEYS], [float(ost[key]) for key in O.DIAG_KEYS], tag)
 
 
+
+
+@pytest.mark.parametrize("case", ["adana", "dana_mk4", "adana_k1_nowd", "dana_star", "dana_star_mk4",
+                                  "dana_star_mk4_k05"])
+def test_foreach_bf16_eager_golden_on_gpu(oracle_mod, case):
+    """The golden scenario on bfloat16 parameters with use_foreach=True and
+    the eager ops: every checkpoint bit-exact against the reference's own run
+    (tests/golden/<case>.bf16_foreach_eager.npz) for m, v and tau, and for p
+    but for Dana-Star's pow hard cases, 20 steps without re-synchronising."""
+    import adana_amd
+
+    O = oracle_mod
+    print("case: foreach bf16 eager golden", case, flush=True)
+    meta, p0, grads, has_grad = load_golden_inputs()
+    gold = load_golden_case(case, "bf16_foreach_eager")
+    kw = dict(meta["cases"][case]["kwargs"])
+    star = meta["cases"][case]["class"] == "DANA_STAR_MK4"
+    gpu = [torch.nn.Parameter(_to_gpu16(O.f32_to_bf16(x))) for x in p0]
+    idx = [[i for i in range(len(p0)) if meta["group_of"][i] == gi] for gi in range(2)]
+    cls = adana_amd.DANA_STAR_MK4 if star else adana_amd.ADana
+    wd = kw.pop("weight_decay")
+    opt = cls([dict(params=[gpu[i] for i in idx[gi]], weight_decay=wd * meta["group_wd_scale"][gi]) for gi in range(2)],
+              use_foreach=True, numerics="eager", **kw)
+    for k in range(1, meta["n_steps"] + 1):
+        for g in opt.param_groups:
+            g["lr"] = kw["lr"] * meta["lr_multiplier"][k - 1]
+        for i, p in enumerate(gpu):
+            p.grad = _to_gpu16(O.f32_to_bf16(grads[k - 1][i])) if has_grad[k - 1, i] else None
+        opt.step()
+        if k not in meta["checkpoints"]:
+            continue
+        torch.cuda.synchronize()
+        for i, p in enumerate(gpu):
+            _check(_bits(p), gold[f"p{i}_t{k}"], f"{case} p t={k} tensor {i}", STAR_HARD_CASES if star else 0)
+            st = opt.state[p]
+            for key in (("m", "v", "tau") if star else ("m", "v")) if st else ():
+                _check(_bits(st[key]), gold[f"{key}{i}_t{k}"], f"{case} {key} t={k} tensor {i}")

@@ -219,9 +219,6 @@ def test_mta_step_rejects_bad_arguments():
     assert "variant flags" in _lib.last_error()
     assert L.adana_mta_step(ctypes.byref(pl), scp, 1, _lib.FOREACH | _lib.VARIANT_MANAU, None, 0, None, None) == -1
     assert "ADANA_FOREACH excludes" in _lib.last_error()
-    s16 = _lib.FOREACH | _lib.STATE_BF16 | _lib.GRAD_BF16 | _lib.NUMERICS_EAGER
-    assert L.adana_mta_step(ctypes.byref(pl), scp, 1, s16, None, 0, None, None) == -3
-    assert "not implemented" in _lib.last_error()
     fake = ctypes.c_void_p(0x1000)
     pl = _lib.Plan(desc=0x1000, vstart=0x1000, chunk_first=0x1000, fold_first=0x1000,
                    n_tensors=3, n_chunks=1, n_folds=3)
@@ -709,17 +706,18 @@ def test_scalar_fill_in_place(numerics):
             assert bytes(ls.sc_arr[k]) == bytes(want), (wd, k)
 
 
-def test_foreach_eager_bf16_state_is_refused():
-    """use_foreach=True with numerics='eager' on bfloat16 parameters (without
-    master weights) is not implemented: the constructor says so, before any
-    step could run other numerics; float32 and master-weight lists build."""
+def test_foreach_builds_on_every_state_kind():
+    """use_foreach=True builds with either numerics on float32, bfloat16 and
+    master-weight parameters, and the choice is the constructor's (it
+    travels with a deep copy)."""
+    import copy
+
     import adana_amd
 
-    p = torch.nn.Parameter(torch.zeros(16, dtype=torch.bfloat16))
-    with pytest.raises(NotImplementedError, match="use_foreach"):
-        adana_amd.ADana([p], lr=1e-3, use_foreach=True, numerics="eager")
-    with pytest.raises(NotImplementedError, match="use_foreach"):
-        adana_amd.DANA_STAR_MK4([p], lr=1e-3, use_foreach=True, numerics="eager")
-    adana_amd.ADana([p], lr=1e-3, use_foreach=True)
-    adana_amd.ADana([p], lr=1e-3, use_foreach=True, numerics="eager", master_weights=True)
-    adana_amd.ADana([torch.nn.Parameter(torch.zeros(4))], lr=1e-3, use_foreach=True, numerics="eager")
+    for dt, master in ((torch.float32, False), (torch.bfloat16, False), (torch.bfloat16, True)):
+        for numerics in ("compiled", "eager"):
+            p = torch.nn.Parameter(torch.zeros(16, dtype=dt))
+            opt = adana_amd.DANA_STAR_MK4([p], lr=1e-3, use_foreach=True, numerics=numerics, master_weights=master)
+            assert opt._foreach and opt.use_foreach
+            assert copy.deepcopy(opt)._foreach
+    assert not adana_amd.ADana([torch.nn.Parameter(torch.zeros(4))], lr=1e-3)._foreach

@@ -37,22 +37,25 @@ def _make(O, meta, case, params, numerics, bf16=False):
     return opt, kw, star
 
 
-@pytest.mark.parametrize("mode", ["foreach", "bf16_foreach"])
+@pytest.mark.parametrize("mode", ["foreach", "bf16_foreach", "bf16_foreach_eager"])
 @pytest.mark.parametrize("case", CASES)
 def test_oracle_equals_foreach_restatement_with_correct_rounding(oracle_mod, case, mode):
     """torch_ref.update_foreach (the reference's bits, test_torch_restatement)
     with Dana-Star's element power correctly rounded gives the oracle's
     foreach mode bit for bit: p, m, v, tau after every one of the 20 steps,
-    float32 and bfloat16."""
+    float32 and bfloat16 compiled; on bfloat16 eager (ATen's own sqrt and
+    pow, which round like the correctly rounded ones at bfloat16 here) the
+    same, diagnostics included."""
     from oracle.torch_ref import DIAG_KEYS, TorchRefGroup, TorchRefOptimizer
     from test_torch_restatement import _cr_pow, _cr_sqrt, _powf
 
     O = oracle_mod
     bf16 = mode.startswith("bf16")
+    eager = mode.endswith("eager")
     meta, p0, grads, has_grad = load_golden_inputs()
     dt = torch.bfloat16 if bf16 else torch.float32
     o_params = [O.f32_to_bf16(x) if bf16 else x.copy() for x in p0]
-    opt, kw, star = _make(O, meta, case, o_params, "compiled", bf16=bf16)
+    opt, kw, star = _make(O, meta, case, o_params, "eager" if eager else "compiled", bf16=bf16)
     t_params = [torch.from_numpy(x.copy()).to(dt) for x in p0]
     idx = [[i for i in range(len(p0)) if meta["group_of"][i] == gi] for gi in range(2)]
     tgroups = [TorchRefGroup(params=[t_params[i] for i in idx[gi]], lr=kw["lr"], delta=kw["delta"], epsilon=1e-8,
@@ -70,7 +73,7 @@ def test_oracle_equals_foreach_restatement_with_correct_rounding(oracle_mod, cas
         og = _grads_for_step(meta, [[O.f32_to_bf16(x) if bf16 else x for x in gs] for gs in grads], has_grad, k)
         opt.step(og)
         tref.step([[torch.from_numpy(grads[k - 1][i].copy()).to(dt) if has_grad[k - 1, i] else None for i in idx[gi]]
-                   for gi in range(2)], foreach=(_cr_sqrt, _cr_pow, _powf, True))
+                   for gi in range(2)], foreach=(None, None, None, False) if eager else (_cr_sqrt, _cr_pow, _powf, True))
         for i in range(len(p0)):
             assert np.array_equal(bits(t_params[i]), o_params[i].view(bits(t_params[i]).dtype)), (case, mode, k, i)
             tst, ost = tref.state.get(id(t_params[i])), opt.state.get(id(o_params[i]))
@@ -126,14 +129,15 @@ def _trajectory(O, case, mode, tau_bar=0):
     return star, worst, dworst
 
 
-@pytest.mark.parametrize("mode", ["foreach", "bf16_foreach"])
+@pytest.mark.parametrize("mode", ["foreach", "bf16_foreach", "bf16_foreach_eager"])
 @pytest.mark.parametrize("case", CASES)
 def test_foreach_golden_trajectory(oracle_mod, case, mode):
     """Compiled, the reference's default for this path: m, v, tau bit-exact
     at every checkpoint, float32 and bfloat16; ADana's p bit-exact;
-    Dana-Star's p within 1 ulp of the tensor's largest |p| (float32; the
-    SIMD pow of the effective time, as on the per-tensor path) and bit-exact
-    on bfloat16; diagnostics within 2e-5 (float32) and 1 bfloat16 ulp."""
+    Dana-Star's p within 2 ulp of the tensor's largest |p| (float32; the
+    SIMD pow of the effective time, as on the per-tensor path; measured 1.5)
+    and bit-exact on bfloat16; diagnostics within 2e-5 (float32) and 1
+    bfloat16 ulp.  The eager ops on bfloat16 state: all bit-exact."""
     star, worst, dworst = _trajectory(oracle_mod, case, mode)
     bf16 = mode.startswith("bf16")
     assert worst <= (2 if star and not bf16 else 0), (case, mode, worst)
