@@ -37,7 +37,9 @@ src/optim/dana_star_mk4.py:298-536), whose ``_foreach_compute_kernel_impl``
 the constructor wraps in ``torch.compile(dynamic=True)``
 (``<case>.foreach.npz``), and the same function as eager ops
 (``<case>.foreach_eager.npz``); float32 and bfloat16 parameters
-(``<case>.bf16_foreach[_eager].npz``).
+(``<case>.bf16_foreach[_eager].npz``); and the compiled float32 run on the
+non-finite gradients of --nonfinite (``<case>.foreach_nonfinite.npz``; the
+inputs are nonfinite.inputs.npz).
 
 A fourth output (--nonfinite) repeats the eager runs of four cases with a few
 NaN / +inf / -inf gradient entries (NONFINITE) and stores them as
@@ -272,6 +274,11 @@ def main():
             print(f"wrote {case}.nonfinite.npz", flush=True)
         return 0
     if args.foreach:
+        grads_nf = inject_nonfinite(grads)
+        for case in NONFINITE_CASES:
+            out = run_case(args.ref, case, True, p0, grads_nf, has_grad, foreach=True)
+            np.savez_compressed(os.path.join(HERE, f"{case}.foreach_nonfinite.npz"), **out)
+            print(f"wrote {case}.foreach_nonfinite.npz", flush=True)
         for bf16 in (False, True):
             for mode in ("compiled", "eager"):
                 for case in CASES:

@@ -194,3 +194,32 @@ def test_foreach_bf16_eager_golden_on_gpu(oracle_mod, case):
             st = opt.state[p]
             for key in (("m", "v", "tau") if star else ("m", "v")) if st else ():
                 _check(_bits(st[key]), gold[f"{key}{i}_t{k}"], f"{case} {key} t={k} tensor {i}")
+
+
+@pytest.mark.parametrize("case", ["adana", "dana_mk4", "dana_star", "dana_star_mk4"])
+def test_foreach_nonfinite_gradients_on_gpu(oracle_mod, case):
+    """The golden scenario's NaN, +inf and -inf gradient entries
+    (nonfinite.inputs.npz) with use_foreach=True: every step against the
+    oracle's foreach mode (NaN where the oracle's NaNs are, the usual bars
+    elsewhere), and every checkpoint's NaN and inf positions against the
+    reference's own foreach run (<case>.foreach_nonfinite.npz)."""
+    print("case: foreach non-finite gradients", case, flush=True)
+    meta, p0, grads, has_grad = load_golden_inputs("nonfinite.inputs")
+    gold = load_golden_case(case, "foreach_nonfinite")
+    kw = dict(meta["cases"][case]["kwargs"])
+    star = meta["cases"][case]["class"] == "DANA_STAR_MK4"
+    idx = [[i for i in range(len(p0)) if meta["group_of"][i] == gi] for gi in range(2)]
+    groups = [([p0[i] for i in idx[gi]], {"weight_decay": kw["weight_decay"] * meta["group_wd_scale"][gi]})
+              for gi in range(2)]
+    pair = Pair(oracle_mod, star, groups, foreach=True, **kw)
+    order = [i for gi in range(2) for i in idx[gi]]
+    for k in range(1, meta["n_steps"] + 1):
+        lr = kw["lr"] * meta["lr_multiplier"][k - 1]
+        pair.set_lr([lr, lr])
+        pair.step([[grads[k - 1][i] if has_grad[k - 1, i] else None for i in idx[gi]] for gi in range(2)])
+        if k in meta["checkpoints"]:
+            for p, i in zip([p for tp in pair.gpu_params for p in tp], order):
+                got, ref = p.detach().cpu().numpy(), gold[f"p{i}_t{k}"]
+                assert np.array_equal(np.isnan(got), np.isnan(ref)) and np.array_equal(np.isinf(got), np.isinf(ref)), \
+                    (case, k, i)
+        pair.compare(where=f"foreach non-finite {case} t={k}")

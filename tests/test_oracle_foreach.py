@@ -203,3 +203,46 @@ def test_foreach_scalars_alpha_and_step_dtype(oracle_mod):
         assert (diff > 0) == expect_diff, (delta, diff)
     sc = O.foreach_scalars(**kw, delta=8.0, t=257, step_bf16=True)
     assert sc.s == 256.0 and O.foreach_scalars(**kw, delta=8.0, t=257).s == 257.0
+
+
+@pytest.mark.parametrize("case", golden_cases("foreach_nonfinite"))
+def test_foreach_nonfinite_trajectory(oracle_mod, case):
+    """The foreach path on NaN, +inf and -inf gradient entries (the
+    reference's own compiled foreach run, make_golden.py --foreach): every
+    element the reference turns NaN or inf is NaN or the same inf here, in p,
+    m, v and tau; the finite elements meet the compiled foreach bars (m, v,
+    tau bit-exact; p within 2 ulp of the tensor's largest finite |p|);
+    diagnostics NaN where the reference's are, else within 2e-5."""
+    O = oracle_mod
+    meta, p0, grads, has_grad = load_golden_inputs("nonfinite.inputs")
+    gold = load_golden_case(case, "foreach_nonfinite")
+    params = [x.copy() for x in p0]
+    opt, kw, star = _make(O, meta, case, params, "compiled")
+    for k in range(1, meta["n_steps"] + 1):
+        for g in opt.groups:
+            g.lr = kw["lr"] * meta["lr_multiplier"][k - 1]
+        opt.step(_grads_for_step(meta, grads, has_grad, k))
+        for i, p in enumerate(params):
+            st = opt.state.get(id(p))
+            if st is None or not has_grad[k - 1, i]:
+                continue
+            got = np.array([st[key] for key in O.DIAG_KEYS])
+            np.testing.assert_allclose(got, gold["diag"][k - 1, i], rtol=2e-5, atol=1e-12, equal_nan=True,
+                                       err_msg=f"{case} diag t={k} tensor {i}")
+        if k not in meta["checkpoints"]:
+            continue
+        for i, p in enumerate(params):
+            st = opt.state.get(id(p), {})
+            if "m" not in st:
+                continue
+            for key in ("m", "v") + (("tau",) if star else ()):
+                ref = gold[f"{key}{i}_t{k}"]
+                assert np.array_equal(np.isnan(st[key]), np.isnan(ref)), (case, key, k, i)
+                assert ulp_diff(st[key], ref).max() == 0, (case, key, k, i)
+            ref = gold[f"p{i}_t{k}"]
+            assert np.array_equal(np.isnan(p), np.isnan(ref)) and np.array_equal(np.isinf(p), np.isinf(ref))
+            fin = np.isfinite(ref)
+            assert np.array_equal(p[~fin & ~np.isnan(ref)], ref[~fin & ~np.isnan(ref)])
+            if fin.any():
+                scale = np.full(fin.sum(), np.abs(ref[fin]).max(), np.float32)
+                assert _scaled_err(p[fin], ref[fin], scale).max() <= 2, (case, k, i)

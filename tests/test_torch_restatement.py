@@ -410,3 +410,44 @@ def test_foreach_runs_differ_from_per_tensor_runs(case):
     a, b = load_golden_case(case, "foreach"), load_golden_case(case, "compiled")
     k = meta["n_steps"]
     assert any(not np.array_equal(a[f"p{i}_t{k}"], b[f"p{i}_t{k}"]) for i in range(len(meta["shapes"])))
+
+
+@pytest.mark.skipif(torch.backends.cpu.get_cpu_capability() != load_golden_inputs()[0].get("cpu_capability"),
+                    reason="torch's CPU SIMD pow bits depend on the SIMD level the fixtures were written with")
+@pytest.mark.parametrize("case", golden_cases("foreach_nonfinite"))
+def test_foreach_restatement_reproduces_nonfinite_run(case):
+    """The foreach restatement on the NaN / +inf / -inf gradients of
+    nonfinite.inputs.npz gives the reference's compiled foreach run bit for
+    bit, NaNs where its NaNs are (of either sign), diagnostics included."""
+    from oracle.torch_ref import DIAG_KEYS, TorchRefGroup, TorchRefOptimizer
+
+    meta, p0, grads, has_grad = load_golden_inputs("nonfinite.inputs")
+    gold = load_golden_case(case, "foreach_nonfinite")
+    kw = meta["cases"][case]["kwargs"]
+    star = meta["cases"][case]["class"] == "DANA_STAR_MK4"
+    params = [torch.from_numpy(x.copy()) for x in p0]
+    idx = [[i for i in range(len(params)) if meta["group_of"][i] == gi] for gi in range(2)]
+    groups = [TorchRefGroup(params=[params[i] for i in idx[gi]], lr=kw["lr"], delta=kw["delta"], epsilon=1e-8,
+                            weight_decay=kw["weight_decay"] * meta["group_wd_scale"][gi]) for gi in range(2)]
+    opt = TorchRefOptimizer(groups=groups, star=star, peak_lr=kw["lr"], kappa=kw["kappa"], clipsnr=kw["clipsnr"],
+                            wd_decaying=kw["wd_decaying"], wd_ts=kw["wd_ts"], gamma_3_factor=kw["gamma_3_factor"])
+    for k in range(1, meta["n_steps"] + 1):
+        for g in groups:
+            g.lr = kw["lr"] * meta["lr_multiplier"][k - 1]
+        opt.step([[torch.from_numpy(grads[k - 1][i].copy()) if has_grad[k - 1, i] else None for i in idx[gi]]
+                  for gi in range(2)], foreach=(_cr_sqrt, _simd_pow, _powf, True))
+        for i, p in enumerate(params):
+            st = opt.state.get(id(p))
+            if st is not None and has_grad[k - 1, i]:
+                got = np.array([float(st[key]) for key in DIAG_KEYS], np.float32)
+                assert ulp_diff(got, gold["diag"][k - 1, i].astype(np.float32)).max() == 0, (case, k, i)
+        if k not in meta["checkpoints"]:
+            continue
+        for i, p in enumerate(params):
+            st = opt.state.get(id(p))
+            for key in ("p",) + ((("m", "v", "tau") if star else ("m", "v")) if st else ()):
+                got, ref = (p if key == "p" else st[key]).numpy(), gold[f"{key}{i}_t{k}"]
+                # NaN where the reference's are NaN (their sign bits are the ops' own), every other bit equal
+                assert np.array_equal(np.isnan(got), np.isnan(ref)), (case, key, k, i)
+                ok = ~np.isnan(ref)
+                assert np.array_equal(got[ok].view(np.int32), ref[ok].view(np.int32)), (case, key, k, i)
