@@ -734,12 +734,24 @@ class _DanaFamily(Optimizer):
         # The general path: the reference's walk (adana.py:184-197) in Python.
         params, grads, states, keys, inactive = [], [], [], [], []
         fresh = []
+        rows = []
+        need = ("m", "v", "tau") if self._STAR else ("m", "v")
         for p, gi in zip(all_params, gidx):
             g = p.grad
             if g is None:                                                    # adana.py:186
                 inactive.append(p)
                 continue
             st = self.state[p]
+            if len(st) != 0:
+                # a state without its moments or step counter fails as the
+                # reference's ``m, v = state['m'], state['v']`` and
+                # ``state['step'] += 1`` do (adana.py:193-197), here before any
+                # counter moves
+                for k in need + ("step",):
+                    if k not in st:
+                        raise KeyError(k)
+            rows.append((p, g, st, gi))
+        for p, g, st, gi in rows:
             if len(st) == 0:                                                 # adana.py:191-195
                 fresh.append((p, st))
                 st["step"] = 0

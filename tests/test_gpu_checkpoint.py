@@ -14,7 +14,9 @@ restores ``opt.state_dict()``):
     master-weights extension and continues as the oracle does from the same
     state;
   * a deepcopy of a stepped optimizer keeps its configuration and steps on
-    its own tensors, bit-identically to the original.
+    its own tensors, bit-identically to the original;
+  * a loaded state missing a moment or its step counter fails with the
+    reference's KeyError before anything changes.
 """
 import io
 import math
@@ -362,3 +364,50 @@ def test_distributed_checkpoint_round_trip(tmp_path):
         assert sa["step"] == sb["step"] == 10
         for key in ("m", "v", "tau"):
             assert torch.equal(sa[key].view(torch.int32), sb[key].view(torch.int32)), key
+
+
+@pytest.mark.parametrize("star", [False, True], ids=["adana", "star"])
+def test_state_missing_a_key_fails_before_any_change(star):
+    """A loaded state without one of its moments (or its step counter) fails
+    with the reference's KeyError (``m, v = state['m'], state['v']``,
+    src/optim/adana.py:193-197) before any step counter, parameter or moment
+    changes; restored, the same optimizer steps as an untouched copy does."""
+    import copy
+
+    import adana_amd
+
+    torch.manual_seed(3)
+    cls = adana_amd.DANA_STAR_MK4 if star else adana_amd.ADana
+    ps = [torch.nn.Parameter(torch.randn(n, device=DEV) * 0.02) for n in (300, 17, 4099)]
+    opt = cls(ps, lr=1e-3, kappa=0.85, weight_decay=0.1)
+    for _ in range(3):
+        for p in ps:
+            p.grad = torch.randn_like(p) * 1e-3
+        opt.step()
+    twin = copy.deepcopy(opt)
+    good = copy.deepcopy(opt.state_dict())
+    keys = ("m", "v", "tau", "step") if star else ("m", "v", "step")
+    for key in keys:
+        sd = copy.deepcopy(good)
+        del sd["state"][1][key]
+        opt.load_state_dict(sd)
+        before = [p.detach().clone() for p in ps]
+        steps = [opt.state[p].get("step") for p in ps]
+        m0 = opt.state[ps[0]]["m"].clone()
+        with pytest.raises(KeyError, match=key):
+            opt.step()
+        torch.cuda.synchronize()
+        assert all(torch.equal(a, p.detach()) for a, p in zip(before, ps)), key
+        assert [opt.state[p].get("step") for p in ps] == steps, key
+        assert torch.equal(opt.state[ps[0]]["m"], m0), key
+    opt.load_state_dict(good)
+    g = [torch.randn_like(p) * 1e-3 for p in ps]
+    for o, params in ((opt, ps), (twin, [p for grp in twin.param_groups for p in grp["params"]])):
+        for p, gg in zip(params, g):
+            p.grad = gg.clone()
+        o.step()
+    torch.cuda.synchronize()
+    for p, q in zip(ps, [p for grp in twin.param_groups for p in grp["params"]]):
+        assert torch.equal(p.detach(), q.detach())
+        for key in keys[:-1]:
+            assert torch.equal(opt.state[p][key], twin.state[q][key])
