@@ -4,8 +4,9 @@ calls in a row on the same device, each later one over a different list,
 each bit for bit equal to the workspace entry point (p, m, v, tau and the
 five diagnostics): float32 lists in both numerics, a list of more than 256
 combine folds (its second combine launch), bfloat16 state with the eager
-path's pow table (placed in the scratch) and in the compiled numerics; and
-a list too large for the static scratch is refused before any launch."""
+path's pow table (placed in the scratch) and in the compiled numerics, the
+foreach path on float32 and bfloat16 state; and a list too large for the
+static scratch is refused before any launch."""
 import ctypes
 
 import numpy as np
@@ -21,13 +22,14 @@ class _List:
     p / m / v / tau (one per entry point) and shared gradients.  ``bf16``:
     bfloat16 parameters, state and gradients (ADANA_STATE_BF16)."""
 
-    def __init__(self, sizes, star, seed, bf16=False, eager=False):
+    def __init__(self, sizes, star, seed, bf16=False, eager=False, foreach=False):
         from adana_amd import _lib
 
         self.sizes = sizes
         self.star = star
         self.bf16 = bf16
         self.eager = eager
+        self.foreach = foreach
         self.dt = torch.bfloat16 if bf16 else torch.float32
         self.gen = torch.Generator(device="cuda")
         self.gen.manual_seed(seed)
@@ -73,9 +75,11 @@ class _List:
         for gi, n in zip(self.g, self.sizes):
             gi.copy_(torch.randn(n, device="cuda", generator=self.gen) * 1e-3)
         hp = _lib.HParams(peak_lr=1e-3, delta=8.0, kappa=0.85, epsilon=1e-8, weight_decay=0.4, clipsnr=2.0,
-                          wd_ts=10.0, gamma_3_factor=1.0, has_clip=1, wd_decaying=1, eager=int(self.eager))
+                          wd_ts=10.0, gamma_3_factor=0.7, has_clip=1, wd_decaying=1, eager=int(self.eager),
+                          foreach=(2 if self.bf16 else 1) if self.foreach else 0)
         sc = (_lib.StepScalars * 1)(_lib.step_scalars(hp, 1e-3, t))
-        flags = (_lib.VARIANT_STAR if self.star else 0) | (_lib.NUMERICS_EAGER if self.eager else 0)
+        flags = ((_lib.VARIANT_STAR if self.star else 0) | (_lib.NUMERICS_EAGER if self.eager else 0)
+                 | (_lib.FOREACH if self.foreach else 0))
         if self.bf16:
             flags |= _lib.GRAD_BF16 | _lib.STATE_BF16
         stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
@@ -140,6 +144,20 @@ def test_noalloc_bf16_state(eager):
     for t in range(1, 13):                      # tau * t passes 1: the pow sees arguments above 1
         lst.step(t)
         lst.assert_equal(f"bf16 t={t}")
+
+
+@pytest.mark.parametrize("kind", ["fp32", "bf16_compiled", "bf16_eager"])
+def test_noalloc_foreach(kind):
+    """The foreach path (ADANA_FOREACH, scalars with hparams.foreach) through
+    both entry points: float32, and bfloat16 state compiled and eager (its
+    pow table in the scratch)."""
+    bf16 = kind != "fp32"
+    print("case: adana_mta_step_noalloc, foreach path,", kind, flush=True)
+    lst = _List([70_000, 3, 1 << 20, 4099], star=True, seed=41, bf16=bf16, eager=kind == "bf16_eager",
+                foreach=True)
+    for t in range(1, 11):
+        lst.step(t)
+        lst.assert_equal(f"foreach {kind} t={t}")
 
 
 def test_noalloc_rejects_lists_beyond_its_scratch():
