@@ -489,20 +489,22 @@ def test_run_twice_is_deterministic():
     assert np.array_equal(np.array(outs[0][1]), np.array(outs[1][1]), equal_nan=True)
 
 
+@pytest.mark.parametrize("foreach", [False, True], ids=["per_tensor", "foreach"])
 @pytest.mark.parametrize("star", [False, True])
-def test_drift_over_1000_steps(oracle_mod, star):
+def test_drift_over_1000_steps(oracle_mod, star, foreach):
     """1,000 steps at config C1's shape (1024 x 4096) without re-synchronising
     the oracle: m, v, tau stay bit-exact (they never read p); ADana p stays
     bit-exact; Dana-Star p differs only where a pow hard case (rate ~4e-9 per
     element and step) left a trace, by at most a few ulp of the tensor's
-    scale.  Reports max / median ulp and the max relative difference."""
-    print("case: 1000-step drift at 1024x4096, star", star, flush=True)
+    scale.  Reports max / median ulp and the max relative difference.  Both
+    of the reference's paths: per tensor and use_foreach=True."""
+    print("case: 1000-step drift at 1024x4096, star", star, "foreach", foreach, flush=True)
     rng = np.random.default_rng(23)
     shape = (1024, 4096)
     n = shape[0] * shape[1]
     pair = Pair(oracle_mod, star, [([_normal(rng, shape, 0.02)], {})], lr=1e-3, delta=8.0,
                 kappa=0.85, clipsnr=2.0 if star else None, weight_decay=0.4, wd_decaying=True,
-                wd_ts=100.0)
+                wd_ts=100.0, foreach=foreach)
     gen = torch.Generator(device=DEV)
     gpu_p = pair.gpu_params[0][0]
     c = pair.cpu_params[0][0]

@@ -6,7 +6,10 @@ with torch's own sqrt and pow: the reference's bits (test_torch_restatement.py
 pins it at 0 ulp against the golden fixtures of both of the reference's modes:
 eager ATen ops, and the default torch.compile path with Inductor's forms).
 The oracle differs from it only where torch's CPU sqrt (eager) and SIMD pow
-(both modes) are not correctly rounded.  Here both run the same 1,000 steps
+(both modes) are not correctly rounded.  The same holds for the
+use_foreach=True path (src/optim/adana.py:229-370,
+src/optim/dana_star_mk4.py:298-536; torch_ref.update_foreach), run here in
+both of its modes too.  Here both run the same 1,000 steps
 on a small list (three tensors, gradients of scales 1e-5 .. 1e-1, a zero
 gradient every 50 steps, an lr that moves), and the tests print the gap:
 
@@ -34,12 +37,19 @@ N_STEPS = 1000
 # Measured on this container's CPU (torch 2.10), max / median over the 1,000 steps:
 #   per step     ADana eager p 3/0; compiled exact; Dana-Star eager p 3/0, tau 2/0; compiled p 2/0
 #   free-running ADana eager p 2/1; compiled exact; Dana-Star eager p 2/1, tau 3/1; compiled p 2/1
+# The foreach path (use_foreach=True), the same 1,000 steps:
+#   per step     ADana compiled exact, eager p 2/0; Dana-Star compiled p 2/0, eager p 3/0, tau 2/0
+#   free-running ADana compiled exact, eager p 2/1; Dana-Star compiled p 2/0.5, eager p 2/1, tau 3/1
 # m and v are exact throughout (their ops have no sqrt or pow).  Bars: those, with headroom.
 BARS = {
     ("eager", False): {"step": dict(p=4, m=0, v=0, tau=0), "free": dict(p=4, m=0, v=0, tau=0)},
     ("eager", True): {"step": dict(p=4, m=0, v=0, tau=3), "free": dict(p=4, m=0, v=0, tau=4)},
     ("compiled", False): {"step": dict(p=0, m=0, v=0, tau=0), "free": dict(p=0, m=0, v=0, tau=0)},
     ("compiled", True): {"step": dict(p=3, m=0, v=0, tau=0), "free": dict(p=4, m=0, v=0, tau=0)},
+    ("foreach", False): {"step": dict(p=0, m=0, v=0, tau=0), "free": dict(p=0, m=0, v=0, tau=0)},
+    ("foreach", True): {"step": dict(p=3, m=0, v=0, tau=0), "free": dict(p=4, m=0, v=0, tau=0)},
+    ("foreach_eager", False): {"step": dict(p=4, m=0, v=0, tau=0), "free": dict(p=4, m=0, v=0, tau=0)},
+    ("foreach_eager", True): {"step": dict(p=4, m=0, v=0, tau=3), "free": dict(p=4, m=0, v=0, tau=4)},
 }
 
 
@@ -82,9 +92,14 @@ def _run(O, star, mode, resync):
     hp = dict(kappa=0.85, clipsnr=2.0, wd_decaying=True, wd_ts=10.0, gamma_3_factor=1.0)
     tref = TorchRefOptimizer(groups=[TorchRefGroup(params=t_params, lr=1e-3, weight_decay=0.1)], star=star,
                              peak_lr=1e-3, **hp)
+    foreach = mode.startswith("foreach")
+    numerics = "eager" if mode.endswith("eager") else "compiled"
     orc = O.OracleOptimizer(groups=[O.OracleGroup(params=o_params, lr=1e-3, weight_decay=0.1)], star=star,
-                            peak_lr=1e-3, numerics=mode, **hp)
+                            peak_lr=1e-3, numerics=numerics, foreach=foreach, **hp)
     compiled = (_cr_sqrt, _simd_pow, _powf) if mode == "compiled" else None
+    fe = None
+    if foreach:
+        fe = (_cr_sqrt, _simd_pow, _powf, True) if numerics == "compiled" else (None, None, None, False)
     per_step = {k: [] for k in ("p", "m", "v", "tau")}
     for k in range(N_STEPS):
         lr = 1e-3 * (0.5 + 0.5 * np.cos(np.pi * k / N_STEPS))
@@ -98,7 +113,7 @@ def _run(O, star, mode, resync):
                 for key in ("m", "v", "tau") if star else ("m", "v"):
                     orc.state[id(o)][key][...] = tref.state[id(t)][key].numpy()
         prev = [t.numpy().copy() for t in t_params]
-        tref.step([[torch.from_numpy(g.copy()) for g in grads]], compiled=compiled)
+        tref.step([[torch.from_numpy(g.copy()) for g in grads]], compiled=compiled, foreach=fe)
         orc.step([grads])
         gap = _gap(tref.state, orc.state, t_params, o_params, prev, star, resync)
         for key, val in gap.items():
@@ -106,7 +121,7 @@ def _run(O, star, mode, resync):
     return {key: (float(np.max(v)), float(np.median(v))) for key, v in per_step.items()}
 
 
-@pytest.mark.parametrize("mode", ["eager", "compiled"])
+@pytest.mark.parametrize("mode", ["eager", "compiled", "foreach", "foreach_eager"])
 @pytest.mark.parametrize("star", [False, True], ids=["adana", "star"])
 @pytest.mark.parametrize("resync", [True, False], ids=["per_step", "free_running"])
 def test_thousand_steps_against_reference_ops(oracle_mod, star, mode, resync):
