@@ -160,6 +160,67 @@ def test_noalloc_foreach(kind):
         lst.assert_equal(f"foreach {kind} t={t}")
 
 
+def test_noalloc_replayed_from_a_captured_graph():
+    """adana_mta_step_noalloc captured once into a HIP graph (torch.cuda.graph),
+    then replayed four times, each replay after the gradients were refilled
+    outside the graph and with eager work and synchronisations between
+    replays: every replay equals an eager adana_mta_step call with the same
+    scalars on the other copy, bit for bit (p, m, v, tau, diagnostics).  The
+    captured launches are the main kernel and the combine; no memset node is
+    recorded (the main kernel clears the arrival counters itself)."""
+    from adana_amd import _lib
+
+    print("case: adana_mta_step_noalloc captured in a HIP graph, 4 replays", flush=True)
+    L = _lib.lib()
+    lst = _List([1 << 20, 3, 70_000, 4099, 5], star=True, seed=51)
+    hp = _lib.HParams(peak_lr=1e-3, delta=8.0, kappa=0.85, epsilon=1e-8, weight_decay=0.4, clipsnr=2.0,
+                      wd_ts=10.0, gamma_3_factor=0.7, has_clip=1, wd_decaying=1)
+    flags = _lib.VARIANT_STAR
+
+    def scalars(t):
+        return (_lib.StepScalars * 1)(_lib.step_scalars(hp, 1e-3, t))
+
+    def call_ws(sc):
+        s = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+        _lib.check(L.adana_mta_step(ctypes.byref(lst.plans[0]), ctypes.cast(sc, ctypes.c_void_p), 1, flags,
+                                    ctypes.c_void_p(lst.ws.data_ptr()), lst.ws.numel(),
+                                    ctypes.c_void_p(lst.diag[0].data_ptr()), s), "adana_mta_step")
+
+    def call_noalloc(sc):
+        s = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+        _lib.check(L.adana_mta_step_noalloc(ctypes.byref(lst.plans[1]), ctypes.cast(sc, ctypes.c_void_p), 1,
+                                            flags, ctypes.c_void_p(lst.diag[1].data_ptr()), s),
+                   "adana_mta_step_noalloc")
+
+    def refill():
+        for gi, n in zip(lst.g, lst.sizes):
+            gi.copy_(torch.randn(n, device="cuda", generator=lst.gen) * 1e-3)
+
+    # an eager step on both copies first (the scratch's device address is looked up there)
+    refill()
+    sc1 = scalars(1)
+    call_ws(sc1)
+    call_noalloc(sc1)
+    torch.cuda.synchronize()
+    lst.assert_equal("eager t=1")
+    sc2 = scalars(2)                 # the graph keeps these scalars: every replay is a step at t = 2
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        call_noalloc(sc2)
+    torch.cuda.synchronize()
+    lst.assert_equal("after capture (nothing ran)")
+    for k in range(4):
+        refill()
+        torch.cuda.synchronize()
+        graph.replay()
+        call_ws(sc2)
+        torch.cuda.synchronize()
+        lst.assert_equal(f"replay {k}")
+        torch.empty(1 << 20, device="cuda").normal_()     # unrelated eager work between replays
+        torch.cuda.synchronize()
+    del graph
+
+
 def test_noalloc_rejects_lists_beyond_its_scratch():
     """A list needing more scratch than the static array gets
     ADANA_E_UNSUPPORTED and a message, before any device work (the plan's
