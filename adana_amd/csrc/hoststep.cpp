@@ -34,6 +34,7 @@
 
 #include <c10/core/InferenceMode.h>
 #include <pthread.h>
+#include <sched.h>
 
 #include <algorithm>
 #include <atomic>
@@ -758,7 +759,21 @@ struct ScanPool {
 };
 ScanPool *g_pool = nullptr;
 bool g_pool_busy = false;   // a scan is using the helpers (the GIL guards this flag)
-int g_helpers = 3;
+int g_helpers = 3;          // set at import by default_helpers()
+
+// Helpers a scan uses by default: the CPUs this process may run on, less two
+// (the calling thread and one to spare), at most kMaxHelpers.  More helpers
+// overlap more of the cold rows' cache misses: on MI355X's host (16 CPUs),
+// 10,000 rows after a backward pass, opt.step()'s host time was 0.69 ms with
+// 3 helpers, 0.60 ms with 6 and 0.57 ms with 8 (medians of 3 x 20 steps).
+int default_helpers() {
+    cpu_set_t set;
+    CPU_ZERO(&set);
+    int cpus = 0;
+    if (sched_getaffinity(0, sizeof set, &set) == 0) cpus = CPU_COUNT(&set);
+    if (cpus <= 0) cpus = static_cast<int>(std::thread::hardware_concurrency());
+    return std::clamp(cpus - 2, 0, kMaxHelpers);
+}
 
 inline void cpu_relax() { __builtin_ia32_pause(); }
 
@@ -1198,6 +1213,7 @@ PyMODINIT_FUNC PyInit__hoststep(void) {
     if (!(g_step_name = PyUnicode_InternFromString("step"))) return nullptr;
     if (!(g_params_name = PyUnicode_InternFromString("params"))) return nullptr;
     if (!(g_one = PyLong_FromLong(1))) return nullptr;
+    g_helpers = default_helpers();
     StepTableType.tp_name = "adana_amd._hoststep.StepTable";
     StepTableType.tp_basicsize = sizeof(StepTable);
     StepTableType.tp_dealloc = table_dealloc;

@@ -33,7 +33,7 @@ def hoststep(ext_dir: str) -> None:
     rng = np.random.default_rng(0)
     cols = [(0, "current_alpha"), (1, "gradient_norm"), (3, "current_kappa_factor")]
     for helpers in (0, 3):
-        assert H.scan_threads(helpers) in (0, 3)
+        assert 0 <= H.scan_threads(helpers) <= 8
         for n in (0, 1, 7, 2600):
             for dtype, bf16 in ((torch.float32, False), (torch.bfloat16, True)):
                 params, states = _rows(rng, torch, n, dtype)

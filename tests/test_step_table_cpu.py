@@ -9,6 +9,8 @@ src/optim/dana_star_mk4.py:243-262): skip parameters without a gradient,
 version counter."""
 import multiprocessing as mp
 import os
+import subprocess
+import sys
 
 import numpy as np
 import pytest
@@ -151,6 +153,19 @@ def test_scan_threads_setting():
         assert _hoststep.scan_threads() == 5
     finally:
         _hoststep.scan_threads(before)
+
+
+def test_scan_threads_default_follows_the_cpus():
+    """At import the helper count is the CPUs the process may run on, less
+    two, within [0, 8] (checked in a fresh interpreter, whose value no other
+    test has changed)."""
+    code = ("import os, torch; from adana_amd import _hoststep; "
+            "print(_hoststep.scan_threads(), min(8, max(0, len(os.sched_getaffinity(0)) - 2)))")
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    out = subprocess.run([sys.executable, "-c", code], cwd=root, capture_output=True, text=True, timeout=300)
+    assert out.returncode == 0, out.stderr
+    got, want = map(int, out.stdout.split())
+    assert got == want
 
 
 def _child_scan(q):
