@@ -721,6 +721,28 @@ bool check_rows(TableData &d, size_t lo, size_t hi, bool inference, size_t *clo,
     return true;
 }
 
+// The bound diagnostics of rows [lo, hi) (flat indices j * ncols + c) that
+// something besides the state dict and the table still refers to -- a Python
+// reference, or another tensor over the same storage, as a view or detach()
+// gives -- go to `held`; those whose state entry no longer is the bound tensor
+// (replaced or deleted) to `lost`.  Reads reference counts only (no Python
+// API), so helper threads run it while the caller holds the GIL: the caller
+// meanwhile rebinds only the step counters of the same dicts, never these
+// objects.
+void diag_rows(const TableData &d, size_t lo, size_t hi, std::vector<size_t> &held, std::vector<size_t> &lost) {
+    const size_t nc = d.cols.size();
+    if (d.diag.empty() || nc == 0) return;
+    const size_t k0 = lo * nc, k1 = hi * nc;
+    for (size_t k = k0; k < k1; ++k) {
+        if (k + 8 < k1) __builtin_prefetch(d.diag[k + 8], 0, 3);
+        PyObject *o = d.diag[k];
+        const Py_ssize_t rc = Py_REFCNT(o);
+        c10::StorageImpl *si = THPVariable_Unpack(o).unsafeGetTensorImpl()->unsafe_storage().unsafeGetStorageImpl();
+        if (rc > 2 || c10::raw::intrusive_ptr::use_count(si) > 1) held.push_back(k);
+        else if (rc < 2) lost.push_back(k);
+    }
+}
+
 // Bumps the version counters of rows [lo, hi), whose parameters the launch
 // that follows updates in place (check_rows has passed them).
 void bump_rows(TableData &d, size_t lo, size_t hi) {
@@ -754,6 +776,9 @@ struct ScanPool {
         size_t lo, hi, clo, chi;
         bool ok;
     } part[kMaxHelpers];
+    bool diag = false;                    // also classify the rows' bound diagnostics (diag_rows)
+    bool diag_only = false;               // a diag_check job: no checks, no decision, no bumps
+    std::vector<size_t> held[kMaxHelpers], lost[kMaxHelpers];
     std::atomic<int> checked{0}, finished{0};
     std::atomic<int> decision{0};         // 0 pending, 1 bump the versions, 2 stop
 };
@@ -787,9 +812,21 @@ void helper_main(ScanPool *P, int id) {
             if (id >= P->parts) continue;
         }
         ScanPool::Part &r = P->part[id];
+        if (P->diag_only) {
+            try {
+                diag_rows(*P->d, r.lo, r.hi, P->held[id], P->lost[id]);
+                r.ok = true;
+            } catch (...) {
+                r.ok = false;
+            }
+            P->finished.fetch_add(1, std::memory_order_acq_rel);
+            continue;
+        }
         bool ok;
         try {
             ok = check_rows(*P->d, r.lo, r.hi, P->inference, &r.clo, &r.chi);
+            // the diagnostics' check overlaps the caller's step counters
+            if (ok && P->diag) diag_rows(*P->d, r.lo, r.hi, P->held[id], P->lost[id]);
         } catch (...) {
             ok = false;   // the caller's general path raises the precise error
         }
@@ -829,12 +866,19 @@ ScanPool *scan_pool(int want) {
 /* The scan's checks and version bumps on `parts` helpers while this thread
  * advances the step counters.  1: done; 0: a row does not fit (nothing
  * modified); -1: error, with a Python error set (nothing modified). */
-int scan_parallel(TableData &d, ScanPool &P, int parts, size_t *lo, size_t *hi) {
+int scan_parallel(TableData &d, ScanPool &P, int parts, size_t *lo, size_t *hi, bool diag, bool *python_ran,
+                  std::vector<size_t> *held, std::vector<size_t> *lost) {
     const size_t n = d.params.size();
     P.d = &d;
     P.parts = parts;
     P.inference = c10::InferenceMode::is_enabled();
-    for (int k = 0; k < parts; ++k) P.part[k] = {n * k / parts, n * (k + 1) / parts, n, 0, false};
+    P.diag = diag;
+    P.diag_only = false;
+    for (int k = 0; k < parts; ++k) {
+        P.part[k] = {n * k / parts, n * (k + 1) / parts, n, 0, false};
+        P.held[k].clear();
+        P.lost[k].clear();
+    }
     P.checked.store(0);
     P.finished.store(0);
     P.decision.store(0);
@@ -863,7 +907,10 @@ int scan_parallel(TableData &d, ScanPool &P, int parts, size_t *lo, size_t *hi) 
     while (P.checked.load(std::memory_order_acquire) < parts) cpu_relax();
     bool fits = true;
     for (int k = 0; k < parts; ++k) fits = fits && P.part[k].ok;
-    if (fits && arc == 1) arc = advance_states_impl(n, state, d.saved);
+    if (fits && arc == 1) {
+        arc = advance_states_impl(n, state, d.saved);
+        *python_ran = true;
+    }
     const bool go = fits && arc == 0;
     P.decision.store(go ? 1 : 2, std::memory_order_release);
     while (P.finished.load(std::memory_order_acquire) < parts) cpu_relax();
@@ -876,10 +923,74 @@ int scan_parallel(TableData &d, ScanPool &P, int parts, size_t *lo, size_t *hi) 
         if (P.part[k].clo < *lo) *lo = P.part[k].clo;
         if (P.part[k].chi > *hi) *hi = P.part[k].chi;
     }
+    if (held && lost) {
+        for (int k = 0; k < parts; ++k) {
+            held->insert(held->end(), P.held[k].begin(), P.held[k].end());
+            lost->insert(lost->end(), P.lost[k].begin(), P.lost[k].end());
+        }
+    }
     return 1;
 }
 
-/* StepTable.scan(out_address) -> (lo, hi) or None
+/* The bound diagnostics' check (diag_rows) of every row, on `parts` helpers:
+ * their held and lost indices, in row order. */
+void diag_parallel(TableData &d, ScanPool &P, int parts, std::vector<size_t> &held, std::vector<size_t> &lost) {
+    const size_t n = d.params.size();
+    P.d = &d;
+    P.parts = parts;
+    P.diag = true;
+    P.diag_only = true;
+    for (int k = 0; k < parts; ++k) {
+        P.part[k] = {n * k / parts, n * (k + 1) / parts, n, 0, false};
+        P.held[k].clear();
+        P.lost[k].clear();
+    }
+    P.checked.store(0);
+    P.finished.store(0);
+    P.decision.store(0);
+    {
+        std::lock_guard<std::mutex> lk(P.mu);
+        ++P.gen;
+    }
+    P.cv.notify_all();
+    while (P.finished.load(std::memory_order_acquire) < parts) cpu_relax();
+    bool ok = true;
+    for (int k = 0; k < parts; ++k) ok = ok && P.part[k].ok;
+    if (!ok) throw std::bad_alloc();
+    for (int k = 0; k < parts; ++k) {
+        held.insert(held.end(), P.held[k].begin(), P.held[k].end());
+        lost.insert(lost.end(), P.lost[k].begin(), P.lost[k].end());
+    }
+}
+
+// The helpers for a pass over the n rows of a plan (parts >= 2), or nullptr
+// (a short plan, no helpers configured, or the helpers already serving a scan
+// further up the stack).
+ScanPool *pool_for(size_t n, int *parts) {
+    *parts = 0;
+    if (n >= kParallelRows && g_helpers > 0)
+        *parts = static_cast<int>(std::min<size_t>(static_cast<size_t>(g_helpers), n / kMinRowsPerHelper));
+    ScanPool *pool = (*parts >= 2 && !g_pool_busy) ? scan_pool(*parts) : nullptr;
+    if (pool) *parts = std::min(*parts, pool->started);
+    return (pool && *parts >= 2) ? pool : nullptr;
+}
+
+// Python list of the size_t values of v (new reference), or nullptr with an error set.
+PyObject *index_list(const std::vector<size_t> &v) {
+    PyObject *l = PyList_New(static_cast<Py_ssize_t>(v.size()));
+    if (!l) return nullptr;
+    for (size_t i = 0; i < v.size(); ++i) {
+        PyObject *ix = PyLong_FromSize_t(v[i]);
+        if (!ix) {
+            Py_DECREF(l);
+            return nullptr;
+        }
+        PyList_SET_ITEM(l, static_cast<Py_ssize_t>(i), ix);
+    }
+    return l;
+}
+
+/* StepTable.scan(out_address[, check_diag]) -> (lo, hi[, held, lost]) or None
  *
  * One step's host bookkeeping for the plan (src/optim/adana.py:184-197,
  * src/optim/dana_star_mk4.py:243-262) when the plan still fits: every row has
@@ -893,10 +1004,15 @@ int scan_parallel(TableData &d, ScanPool &P, int parts, size_t *lo, size_t *hi) 
  * returned (lo == hi: none moved).  None, with nothing modified, when the
  * plan does not fit: the caller takes its general path (which also raises
  * the precise error for a bad gradient).  Plans of thousands of rows are
- * checked by helper threads (scan_threads). */
-PyObject *table_scan(PyObject *self, PyObject *arg) {
+ * checked by helper threads (scan_threads).  With check_diag the same pass
+ * also takes diag_check()'s lists: the helpers classify their rows' bound
+ * diagnostics while the calling thread advances the step counters. */
+PyObject *table_scan(PyObject *self, PyObject *args) {
     TableData &d = *reinterpret_cast<StepTable *>(self)->d;
-    const unsigned long long addr = PyLong_AsUnsignedLongLong(arg);
+    PyObject *addr_obj;
+    int check_diag = 0;
+    if (!PyArg_ParseTuple(args, "O|p", &addr_obj, &check_diag)) return nullptr;
+    const unsigned long long addr = PyLong_AsUnsignedLongLong(addr_obj);
     if (PyErr_Occurred()) return nullptr;
     uint64_t *out = reinterpret_cast<uint64_t *>(static_cast<uintptr_t>(addr));
     const size_t n = d.params.size();
@@ -908,32 +1024,50 @@ PyObject *table_scan(PyObject *self, PyObject *arg) {
         for (PyObject *p : d.inactive)
             if (THPVariable_Unpack(p).unsafeGetTensorImpl()->grad().defined()) Py_RETURN_NONE;
         size_t lo = n, hi = 0;
-        int parts = 0;
-        if (n >= kParallelRows && g_helpers > 0)
-            parts = static_cast<int>(std::min<size_t>(static_cast<size_t>(g_helpers), n / kMinRowsPerHelper));
         // Python code run by a step counter that is not an int (its __add__) may
         // re-enter: a scan of this table then takes the general path, and a scan
         // of another table keeps off the helpers while they serve this one.
         if (d.busy) Py_RETURN_NONE;
-        ScanPool *pool = (parts >= 2 && !g_pool_busy) ? scan_pool(parts) : nullptr;
-        if (pool) parts = std::min(parts, pool->started);
+        int parts = 0;
+        ScanPool *pool = pool_for(n, &parts);
         struct Busy {          // set for the scan, cleared on every way out
             bool &table, *pool;
             ~Busy() {
                 table = false;
                 if (pool) *pool = false;
             }
-        } busy{d.busy, (pool && parts >= 2) ? &g_pool_busy : nullptr};
+        } busy{d.busy, pool ? &g_pool_busy : nullptr};
         d.busy = true;
+        std::vector<size_t> held, lost;
+        bool python_ran = false;
         if (busy.pool) {
             g_pool_busy = true;
-            const int rc = scan_parallel(d, *pool, parts, &lo, &hi);
+            const int rc = scan_parallel(d, *pool, parts, &lo, &hi, check_diag, &python_ran, &held, &lost);
             if (rc < 0) return nullptr;
             if (rc == 0) Py_RETURN_NONE;
         } else {
             if (!check_rows(d, 0, n, c10::InferenceMode::is_enabled(), &lo, &hi)) Py_RETURN_NONE;
-            if (advance_states_impl(n, [&d](size_t i) { return d.states[i]; }, d.saved)) return nullptr;
+            if (check_diag) diag_rows(d, 0, n, held, lost);          // nothing modified yet
+            auto state = [&d](size_t i) { return d.states[i]; };
+            int arc = advance_states_impl(n, state, d.saved, true);
+            if (arc == 1) {
+                arc = advance_states_impl(n, state, d.saved);
+                python_ran = true;
+            }
+            if (arc) return nullptr;
             bump_rows(d, 0, n);
+        }
+        bool diag_known = true;
+        if (check_diag && python_ran) {
+            // a counter's Python code ran after the check and may have touched
+            // the states: check again (None on failure: the caller checks itself)
+            try {
+                held.clear();
+                lost.clear();
+                diag_rows(d, 0, n, held, lost);
+            } catch (const std::exception &) {
+                diag_known = false;
+            }
         }
 
         for (PyObject *o : d.saved) Py_DECREF(o);
@@ -941,7 +1075,17 @@ PyObject *table_scan(PyObject *self, PyObject *arg) {
         for (size_t i = 0; i < n; ++i) out[i] = d.tmp[i];
         for (size_t i = lo; i < hi; ++i) d.last[i] = d.tmp[i];
         if (lo > hi) lo = hi = 0;
-        return Py_BuildValue("nn", static_cast<Py_ssize_t>(lo), static_cast<Py_ssize_t>(hi));
+        if (!check_diag) return Py_BuildValue("nn", static_cast<Py_ssize_t>(lo), static_cast<Py_ssize_t>(hi));
+        if (!diag_known)
+            return Py_BuildValue("nnOO", static_cast<Py_ssize_t>(lo), static_cast<Py_ssize_t>(hi), Py_None, Py_None);
+        PyObject *h = index_list(held);
+        if (!h) return nullptr;
+        PyObject *l = index_list(lost);
+        if (!l) {
+            Py_DECREF(h);
+            return nullptr;
+        }
+        return Py_BuildValue("nnNN", static_cast<Py_ssize_t>(lo), static_cast<Py_ssize_t>(hi), h, l);
     } catch (const std::exception &e) {
         PyErr_SetString(PyExc_RuntimeError, e.what());
         return nullptr;
@@ -1063,31 +1207,31 @@ PyObject *table_diag_bind(PyObject *self, PyObject *args) {
  * `lost`. */
 PyObject *table_diag_check(PyObject *self, PyObject *) {
     TableData &d = *reinterpret_cast<StepTable *>(self)->d;
-    PyObject *held = PyList_New(0), *lost = PyList_New(0);
-    if (!held || !lost) {
-        Py_XDECREF(held);
-        Py_XDECREF(lost);
+    try {
+        std::vector<size_t> held, lost;
+        int parts = 0;
+        ScanPool *pool = d.busy ? nullptr : pool_for(d.params.size(), &parts);
+        if (pool) {
+            g_pool_busy = true;
+            struct Release {
+                ~Release() { g_pool_busy = false; }
+            } release;
+            diag_parallel(d, *pool, parts, held, lost);
+        } else {
+            diag_rows(d, 0, d.params.size(), held, lost);
+        }
+        PyObject *h = index_list(held);
+        if (!h) return nullptr;
+        PyObject *l = index_list(lost);
+        if (!l) {
+            Py_DECREF(h);
+            return nullptr;
+        }
+        return Py_BuildValue("NN", h, l);
+    } catch (const std::exception &e) {
+        PyErr_SetString(PyExc_RuntimeError, e.what());
         return nullptr;
     }
-    for (size_t k = 0; k < d.diag.size(); ++k) {
-        PyObject *o = d.diag[k];
-        const Py_ssize_t rc = Py_REFCNT(o);
-        c10::StorageImpl *si = THPVariable_Unpack(o).unsafeGetTensorImpl()->unsafe_storage().unsafeGetStorageImpl();
-        PyObject *dst = nullptr;
-        if (rc > 2 || c10::raw::intrusive_ptr::use_count(si) > 1) dst = held;
-        else if (rc < 2) dst = lost;
-        if (dst) {
-            PyObject *ix = PyLong_FromSize_t(k);
-            if (!ix || PyList_Append(dst, ix)) {
-                Py_XDECREF(ix);
-                Py_DECREF(held);
-                Py_DECREF(lost);
-                return nullptr;
-            }
-            Py_DECREF(ix);
-        }
-    }
-    return Py_BuildValue("NN", held, lost);
 }
 
 void drop_storage(void *ctx) { delete static_cast<c10::Storage *>(ctx); }
@@ -1152,9 +1296,11 @@ PyObject *table_diag_rehome(PyObject *self, PyObject *args) {
 }
 
 PyMethodDef table_methods[] = {
-    {"scan", table_scan, METH_O,
-     "scan(out_address) -> (lo, hi) or None: check every row's gradient, write the gradient pointers, advance the "
-     "step counters and bump the parameters' versions; the rows whose pointer moved, or None (nothing done)"},
+    {"scan", table_scan, METH_VARARGS,
+     "scan(out_address[, check_diag]) -> (lo, hi) or None: check every row's gradient, write the gradient "
+     "pointers, advance the step counters and bump the parameters' versions; the rows whose pointer moved, or "
+     "None (nothing done).  With check_diag: (lo, hi, held, lost), diag_check()'s lists taken in the same pass "
+     "(None, None if they could not be)"},
     {"forget", table_forget, METH_NOARGS, "forget() -> None: the next scan reports every row as moved"},
     {"grads_are", table_grads_are, METH_O, "grads_are(grads) -> bool: row i's gradient is grads[i] for every row"},
     {"diag_bind", table_diag_bind, METH_VARARGS,

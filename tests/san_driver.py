@@ -81,6 +81,15 @@ def hoststep(ext_dir: str) -> None:
                     assert float(kept) == float(buf[5 * (n - 1) + 1])
                     assert t.diag_check() == ([], [])
                     del kept
+                    # the same lists taken by the scan itself (helpers on long plans)
+                    kept = states[n // 2]["current_alpha"]
+                    view = states[n - 1]["current_kappa_factor"].detach()
+                    states[n // 3]["gradient_norm"] = torch.zeros(())
+                    want = t.diag_check()
+                    got = t.scan(out.ctypes.data, True)
+                    assert got is not None and (got[2], got[3]) == want, (got, want)
+                    assert t.scan(out.ctypes.data, False) == (0, 0)
+                    del view, kept
                 del t
     H.scan_threads(3)
 

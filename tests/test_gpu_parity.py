@@ -921,9 +921,8 @@ def test_diagnostics_kept_from_a_step_keep_their_value(fresh):
     """As the reference binds new 0-d tensors each step (src/optim/adana.py:
     221-225), a diagnostic kept from one step -- a reference to it, or a
     tensor sharing its storage (detach(), a view) -- keeps its value after
-    the next step, and the state holds a new tensor (the default for lists
-    of up to 2,048 tensors); entries nothing else refers to are refreshed in
-    place.  Each has a storage of its own (a deepcopy copies 4 bytes); the
+    the next step, and the state holds a new tensor (the default); entries
+    nothing else refers to are refreshed in place.  Each has a storage of its own (a deepcopy copies 4 bytes); the
     packed read-out and .item() agree.  With fresh_diagnostics=False every
     entry is refreshed in place."""
     import copy
@@ -965,34 +964,46 @@ def test_diagnostics_kept_from_a_step_keep_their_value(fresh):
         assert list(row) == pytest.approx([float(st[k]) for k in adana_amd.optim.DIAG_KEYS], rel=0, nan_ok=True)
 
 
-def test_diagnostics_check_skipped_above_the_limit_warns_once():
-    """Lists of more than 2,048 stepped tensors skip the check (its cost
-    grows with the list): a RuntimeWarning says so once, and a kept entry
-    then follows the buffer; fresh_diagnostics=True keeps the check."""
+@pytest.mark.parametrize("fresh", [None, False])
+def test_diagnostics_kept_on_long_lists(fresh):
+    """A list of 5,000 tensors, long enough for the step table's helper
+    threads: by default a diagnostic kept from the first step (the general
+    path's check) and one kept from the second (the check the fast path's
+    scan takes in the same pass) both keep their values, no warning is
+    raised; with fresh_diagnostics=False the entries are refreshed in place."""
     import warnings
 
     import adana_amd
 
-    print("case: kept-diagnostics check above the limit", flush=True)
-    for fresh in (None, True):
-        ps = [torch.nn.Parameter(torch.full((4,), 0.01 * (i % 7 + 1), device=DEV)) for i in range(2049)]
-        opt = adana_amd.ADana(ps, lr=1e-3, fresh_diagnostics=fresh)
+    print("case: kept diagnostics on 5,000 tensors, fresh", fresh, flush=True)
+    ps = [torch.nn.Parameter(torch.full((4,), 0.01 * (i % 7 + 1), device=DEV)) for i in range(5000)]
+    opt = adana_amd.ADana(ps, lr=1e-3, fresh_diagnostics=fresh)
+    with warnings.catch_warnings():
+        warnings.simplefilter("error")
         for p in ps:
             p.grad = torch.full_like(p, 1e-3)
-        with warnings.catch_warnings(record=True) as w:
-            warnings.simplefilter("always")
-            opt.step()
-            kept = opt.state[ps[5]]["gradient_norm"]
-            first = float(kept)
-            for p in ps:
-                p.grad = torch.full_like(p, 2e-3)
-            opt.step()
-        msgs = [x for x in w if issubclass(x.category, RuntimeWarning) and "2048" in str(x.message)]
-        assert len(msgs) == (1 if fresh is None else 0)
-        if fresh is None:
-            assert opt.state[ps[5]]["gradient_norm"] is kept and float(kept) == pytest.approx(2 * first)
-        else:
-            assert opt.state[ps[5]]["gradient_norm"] is not kept and float(kept) == first
+        opt.step()
+        assert opt._fast                              # the next steps take the table's scan
+        kept1 = opt.state[ps[5]]["gradient_norm"]
+        first = float(kept1)
+        for p in ps:
+            p.grad = torch.full_like(p, 2e-3)
+        opt.step()
+        kept2 = opt.state[ps[4000]]["gradient_norm"]
+        view2 = opt.state[ps[2500]]["m_norm"].detach()
+        second, second_m = float(kept2), float(view2)
+        for p in ps:
+            p.grad = torch.full_like(p, 4e-3)
+        opt.step()
+        torch.cuda.synchronize()
+    now = float(opt.state[ps[4000]]["gradient_norm"])
+    assert now == pytest.approx(2 * second)
+    if fresh is None:
+        assert float(kept1) == first and float(kept2) == second and float(view2) == second_m
+        assert opt.state[ps[5]]["gradient_norm"] is not kept1 and opt.state[ps[4000]]["gradient_norm"] is not kept2
+    else:
+        assert opt.state[ps[4000]]["gradient_norm"] is kept2 and float(kept2) == now
+        assert float(kept1) == pytest.approx(4 * first)
 
 
 @pytest.mark.parametrize("master", [False, True])
