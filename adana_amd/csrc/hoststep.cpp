@@ -733,8 +733,12 @@ void diag_rows(const TableData &d, size_t lo, size_t hi, std::vector<size_t> &he
     const size_t nc = d.cols.size();
     if (d.diag.empty() || nc == 0) return;
     const size_t k0 = lo * nc, k1 = hi * nc;
+    // each entry is a chain of three cold lines (object, TensorImpl, storage):
+    // hints for the entries 16, 8 and 4 ahead, one link further each
     for (size_t k = k0; k < k1; ++k) {
-        if (k + 8 < k1) __builtin_prefetch(d.diag[k + 8], 0, 3);
+        if (k + 16 < k1) __builtin_prefetch(d.diag[k + 16], 0, 3);
+        if (k + 8 < k1) prefetch_lines(impl_of(d.diag[k + 8]), 2);
+        if (k + 4 < k1) __builtin_prefetch(impl_of(d.diag[k + 4])->unsafe_storage().unsafeGetStorageImpl(), 0, 3);
         PyObject *o = d.diag[k];
         const Py_ssize_t rc = Py_REFCNT(o);
         c10::StorageImpl *si = THPVariable_Unpack(o).unsafeGetTensorImpl()->unsafe_storage().unsafeGetStorageImpl();
