@@ -592,6 +592,7 @@ struct TableData {
     std::vector<PyObject *> saved;                       // a scan's old step counts until it is accepted
     bool busy = false;                                   // a scan of this table is running
     std::vector<PyObject *> diag;                        // bound diagnostics, ncols per row (strong)
+    std::vector<c10::Storage> dstore;                    // their storages, one reference each (diag_rows)
     std::vector<std::pair<long, PyObject *>> cols;       // (kernel output column, state key), keys strong
     c10::ScalarType want = c10::ScalarType::Float;
 };
@@ -731,18 +732,19 @@ bool check_rows(TableData &d, size_t lo, size_t hi, bool inference, size_t *clo,
 // objects.
 void diag_rows(const TableData &d, size_t lo, size_t hi, std::vector<size_t> &held, std::vector<size_t> &lost) {
     const size_t nc = d.cols.size();
-    if (d.diag.empty() || nc == 0) return;
+    if (d.diag.empty() || nc == 0 || d.dstore.size() != d.diag.size()) return;
     const size_t k0 = lo * nc, k1 = hi * nc;
-    // each entry is a chain of three cold lines (object, TensorImpl, storage):
-    // hints for the entries 16, 8 and 4 ahead, one link further each
+    // Two cold lines per entry, independent of each other: the object (its
+    // reference count) and the storage the table cached at binding (its use
+    // count: the bound tensor's reference and the table's, more when a view or
+    // detach() shares it).  Hints 16 entries ahead.
     for (size_t k = k0; k < k1; ++k) {
-        if (k + 16 < k1) __builtin_prefetch(d.diag[k + 16], 0, 3);
-        if (k + 8 < k1) prefetch_lines(impl_of(d.diag[k + 8]), 2);
-        if (k + 4 < k1) __builtin_prefetch(impl_of(d.diag[k + 4])->unsafe_storage().unsafeGetStorageImpl(), 0, 3);
-        PyObject *o = d.diag[k];
-        const Py_ssize_t rc = Py_REFCNT(o);
-        c10::StorageImpl *si = THPVariable_Unpack(o).unsafeGetTensorImpl()->unsafe_storage().unsafeGetStorageImpl();
-        if (rc > 2 || c10::raw::intrusive_ptr::use_count(si) > 1) held.push_back(k);
+        if (k + 16 < k1) {
+            __builtin_prefetch(d.diag[k + 16], 0, 3);
+            __builtin_prefetch(d.dstore[k + 16].unsafeGetStorageImpl(), 0, 3);
+        }
+        const Py_ssize_t rc = Py_REFCNT(d.diag[k]);
+        if (rc > 2 || c10::raw::intrusive_ptr::use_count(d.dstore[k].unsafeGetStorageImpl()) > 2) held.push_back(k);
         else if (rc < 2) lost.push_back(k);
     }
 }
@@ -1171,6 +1173,7 @@ PyObject *table_diag_bind(PyObject *self, PyObject *args) {
         for (auto &c : d.cols) Py_XDECREF(c.second);
         d.cols.clear();
         release_all(d.diag);
+        d.dstore.clear();
         const Py_ssize_t nc = PyList_GET_SIZE(columns);
         for (Py_ssize_t c = 0; c < nc; ++c) {
             long col;
@@ -1184,6 +1187,7 @@ PyObject *table_diag_bind(PyObject *self, PyObject *args) {
             d.cols.emplace_back(col, key);
         }
         d.diag.assign(n * d.cols.size(), nullptr);
+        d.dstore.assign(n * d.cols.size(), c10::Storage());
         for (size_t j = 0; j < n; ++j)
             for (size_t c = 0; c < d.cols.size(); ++c) {
                 PyObject *w = diag_tensor(buf, static_cast<int64_t>(5 * j) + d.cols[c].first);
@@ -1193,6 +1197,7 @@ PyObject *table_diag_bind(PyObject *self, PyObject *args) {
                     return nullptr;
                 }
                 d.diag[j * d.cols.size() + c] = w;                   // the table's reference
+                d.dstore[j * d.cols.size() + c] = THPVariable_Unpack(w).storage();
             }
     } catch (const std::exception &e) {
         PyErr_SetString(PyExc_RuntimeError, e.what());
@@ -1290,6 +1295,7 @@ PyObject *table_diag_rehome(PyObject *self, PyObject *args) {
                 }
                 Py_DECREF(d.diag[k]);
                 d.diag[k] = w;
+                if (k < d.dstore.size()) d.dstore[k] = THPVariable_Unpack(w).storage();
             }
         }
     } catch (const std::exception &e) {
